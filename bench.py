@@ -1,0 +1,140 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the MI355X exact-GP engine (one JSON line on stdout).
+
+Metric: fused K.V matvec TFLOP/s at N=250k, d=16 (config 3:
+Matern-5/2 ARD, t=16 right-hand sides).  One "step" is one fused forward
+matvec (K + sigma^2 I) V over the 16 right-hand sides, inputs resident in HBM.
+
+Work model (per (row, column) pair): F = 2d + 2t + c_k flops (c_k = 9 for
+Matern-5/2, 5 for RBF) plus n_tr transcendentals (2 for Matern-5/2).
+value = N^2 F / (host wall time per step); roofline.achieved uses the HIP-event
+duration of the fused tile kernel measured on the provider's stream.
+
+The cpu_baseline leg times the C restatement of the reference matvec
+(oracle/cpu_ref, OpenMP) on a bounded sample of rows of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_FP32_TFLOPS = 157.3       # MI355X dense fp32 (MFMA / packed VALU)
+PEAK_TRANS_PER_S = 9.83e12     # assumed quarter-rate transcendentals (256 CU x 2.4 GHz x 16)
+
+N, D, T = 250_000, 16, 16
+C_K = 9                        # Matern-5/2 epilogue flops per pair
+N_TR = 2                       # sqrt + exp per pair
+FLOPS_PER_PAIR = 2 * D + 2 * T + C_K
+
+
+def _make_inputs():
+    rng = np.random.default_rng(0)
+    X = rng.normal(size=(N, D)).astype(np.float32)
+    V = rng.normal(size=(T, N)).astype(np.float32)
+    V /= np.linalg.norm(V, axis=1, keepdims=True)
+    params = np.concatenate([np.ones(D), [1.0]]).astype(np.float32)
+    return X, V, params, 0.1
+
+
+def _cpu_baseline(X, V, params, noise, target_s: float):
+    from oracle import cpu_ref
+    threads = cpu_ref.num_threads()
+    probe_rows = 32
+    t0 = time.perf_counter()
+    cpu_ref.forward_matvec_rows(1, True, X, params, noise, V, 0, probe_rows)
+    dt = max(time.perf_counter() - t0, 1e-3)
+    rows = int(min(N, max(probe_rows, target_s / dt * probe_rows)))
+    t0 = time.perf_counter()
+    cpu_ref.forward_matvec_rows(1, True, X, params, noise, V, 0, rows)
+    dt = time.perf_counter() - t0
+    flops = rows * N * FLOPS_PER_PAIR
+    return {
+        "value": flops / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"rows [0,{rows}) of the config-3 matvec ({rows}x{N} pairs, t={T}); "
+                  f"{dt:.1f} s on {threads} threads",
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target duration of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU design is described in DESIGN.md and not run here.",
+              file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    from mojogp_amd._provider import NativeProvider, KIND_MATERN52
+
+    X, V, params, noise = _make_inputs()
+    prov = NativeProvider(KIND_MATERN52, True, X, params, noise)
+    try:
+        times_ms, tile_ms, _ = prov.benchmark_forward(V, repeats=args.steps, warmup=args.warmup)
+    finally:
+        prov.close()
+
+    pairs = float(N) * float(N)
+    ms_per_step = float(np.mean(times_ms))
+    value = pairs * FLOPS_PER_PAIR / (ms_per_step * 1e-3) / 1e12
+    achieved = pairs * FLOPS_PER_PAIR / (tile_ms * 1e-3) / 1e12
+    t_roof_ms = pairs * (FLOPS_PER_PAIR / (PEAK_FP32_TFLOPS * 1e12) + N_TR / PEAK_TRANS_PER_S) * 1e3
+
+    result = {
+        "metric": "fused K.V matvec TFLOP/s (N=250k, d=16, t=16, Matern-5/2 ARD)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (X ~ N(0,I), seed 0; 16 unit-norm random right-hand sides)",
+        "config": {"workload": "config 3 forward matvec: (K + 0.1 I) V, N=250000, d=16, t=16, "
+                               "Matern-5/2 ARD, lengthscales 1, outputscale 1",
+                   "N": N, "d": D, "t": T},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+            "traffic": None,
+        },
+        "tile_kernel_ms": round(tile_ms, 4),
+        "issue_slot_roofline_ms": round(t_roof_ms, 3),
+        "issue_slot_roofline_frac": round(t_roof_ms / tile_ms, 4),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = _cpu_baseline(X, V, params, noise, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

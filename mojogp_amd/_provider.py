@@ -1,0 +1,122 @@
+"""Python handle over a native device-resident kernel provider."""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+
+KIND_RBF = 0
+KIND_MATERN52 = 1
+_KIND_NAMES = {"rbf": KIND_RBF, "matern52": KIND_MATERN52}
+
+
+def kind_code(kind) -> int:
+    if isinstance(kind, str):
+        try:
+            return _KIND_NAMES[kind.lower()]
+        except KeyError:
+            raise ValueError(f"unsupported kernel kind {kind!r}") from None
+    return int(kind)
+
+
+def _cols(V: np.ndarray, n: int) -> tuple[np.ndarray, bool]:
+    """Normalise right-hand sides to column-major [ncols][n] float32."""
+    V = _lib.f32(V)
+    if V.ndim == 1:
+        if V.shape[0] != n:
+            raise ValueError(f"vector has length {V.shape[0]}, expected {n}")
+        return V.reshape(1, n), True
+    if V.ndim != 2 or V.shape[1] != n:
+        raise ValueError(f"right-hand sides must have shape (ncols, {n}), got {V.shape}")
+    return V, False
+
+
+class NativeProvider:
+    """Owns one ``mgp_init_provider`` handle (training inputs live in HBM)."""
+
+    def __init__(self, kind, ard: bool, X: np.ndarray, params: np.ndarray, noise: float):
+        X = _lib.f32(X)
+        if X.ndim != 2:
+            raise ValueError("X must be 2-D")
+        params = _lib.f32(params).ravel()
+        self.kind = kind_code(kind)
+        self.ard = bool(ard)
+        self.n, self.d = X.shape
+        self.nparams = params.shape[0]
+        h = C.c_void_p()
+        _lib.call("mgp_init_provider", self.kind, int(self.ard), self.d, self.n,
+                  _lib.fptr(X), _lib.fptr(params), self.nparams, float(noise),
+                  C.byref(h))
+        self._h = h
+        self.params = params.copy()
+        self.noise = float(noise)
+
+    @property
+    def handle(self) -> C.c_void_p:
+        if self._h is None or not self._h.value:
+            raise RuntimeError("provider has been destroyed")
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _lib.call("mgp_destroy_provider", self._h)
+        self._h = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def update_params(self, params) -> None:
+        params = _lib.f32(params).ravel()
+        _lib.call("mgp_update_params", self.handle, _lib.fptr(params), params.shape[0])
+        self.params = params.copy()
+
+    def update_noise(self, noise: float) -> None:
+        _lib.call("mgp_update_noise", self.handle, float(noise))
+        self.noise = float(noise)
+
+    def forward_matvec(self, V) -> np.ndarray:
+        Vc, vec = _cols(V, self.n)
+        out = np.empty_like(Vc)
+        _lib.call("mgp_forward_matvec", self.handle, _lib.fptr(Vc), Vc.shape[0],
+                  _lib.fptr(out))
+        return out[0] if vec else out
+
+    def direct_matvec(self, V) -> np.ndarray:
+        Vc, vec = _cols(V, self.n)
+        out = np.empty_like(Vc)
+        _lib.call("mgp_direct_matvec", self.handle, _lib.fptr(Vc), Vc.shape[0],
+                  _lib.fptr(out))
+        return out[0] if vec else out
+
+    def cross_matvec(self, Xs, V) -> np.ndarray:
+        Xs = _lib.f32(Xs)
+        if Xs.ndim != 2 or Xs.shape[1] != self.d:
+            raise ValueError(f"test inputs must have shape (m, {self.d})")
+        Vc, vec = _cols(V, self.n)
+        m = Xs.shape[0]
+        out = np.empty((Vc.shape[0], m), dtype=np.float32)
+        _lib.call("mgp_cross_matvec", self.handle, _lib.fptr(Xs), m, _lib.fptr(Vc),
+                  Vc.shape[0], _lib.fptr(out))
+        return out[0] if vec else out
+
+    def extract_diagonal(self) -> np.ndarray:
+        out = np.empty(self.n, dtype=np.float32)
+        _lib.call("mgp_extract_diagonal", self.handle, _lib.fptr(out))
+        return out
+
+    def benchmark_forward(self, V, repeats: int, warmup: int):
+        """(per-call wall ms array, mean tile-kernel ms, output)."""
+        Vc, _ = _cols(V, self.n)
+        times = np.zeros(repeats, dtype=np.float64)
+        tile = C.c_double(0.0)
+        out = np.empty_like(Vc)
+        _lib.call("mgp_benchmark_provider_ops", self.handle, _lib.fptr(Vc), Vc.shape[0],
+                  0, int(repeats), int(warmup), _lib.dptr(times), C.byref(tile),
+                  _lib.fptr(out))
+        return times, float(tile.value), out

@@ -1,0 +1,83 @@
+"""Build the gfx950 shared library ``mojogp_amd/lib/libmojogp_amd.so``.
+
+Every ``csrc/*.hip`` translation unit is compiled with hipcc for gfx950 only
+(object files go to ``mojogp_amd/lib/obj``), then linked into one C-ABI
+library that the ctypes loader in ``mojogp_amd._lib`` opens.
+
+Usage: ``python -m mojogp_amd.build`` (or ``build()`` from Python).
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as _cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+LIB_DIR = PKG_DIR / "lib"
+OBJ_DIR = LIB_DIR / "obj"
+LIB_PATH = LIB_DIR / "libmojogp_amd.so"
+ARCH = "gfx950"
+
+# Packed-FP32 VALU forms are disabled for all device code (hipcc's host pass
+# warns that it does not know the feature; that warning is harmless).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; the gfx950 library cannot be built")
+    return path
+
+
+def _compile_one(src: Path) -> Path:
+    obj = OBJ_DIR / (src.stem + ".o")
+    cmd = [_hipcc(), *HIP_FLAGS, "-I", str(CSRC), "-I", str(REPO_DIR / "include"),
+           "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
+    return obj
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile all HIP sources and link the shared library. Returns its path."""
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    jobs = jobs or min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile_one, sources))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+           *map(str, objs)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH} from {len(sources)} sources")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

@@ -1,0 +1,278 @@
+// C ABI: provider lifecycle and kernel products.  Declarations and the
+// reference interface each entry point replaces are in include/mojogp_amd.h.
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "mojogp_amd.h"
+#include "provider.h"
+
+namespace mgp {
+
+thread_local std::string g_last_error;
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+static Provider* as_provider(void* h) {
+  MGP_REQUIRE(h != nullptr, "null provider handle");
+  return static_cast<Provider*>(h);
+}
+
+}  // namespace mgp
+
+using namespace mgp;
+
+extern "C" {
+
+int mgp_last_error(char* buf, size_t len) {
+  const std::string& m = g_last_error;
+  if (buf && len > 0) {
+    const size_t k = std::min(len - 1, m.size());
+    std::memcpy(buf, m.data(), k);
+    buf[k] = '\0';
+  }
+  return (int)m.size();
+}
+
+const char* mgp_version(void) { return "mojogp_amd 0.1.0 gfx950"; }
+
+int mgp_device_count(int* out) {
+  return guarded([&] {
+    int c = 0;
+    MGP_HIP_CHECK(hipGetDeviceCount(&c));
+    *out = c;
+  });
+}
+
+int mgp_init_provider(int kind, int ard, int d, int64_t n, const float* X,
+                      const float* params, int nparams, float noise,
+                      void** out_handle) {
+  return guarded([&] {
+    MGP_REQUIRE(out_handle != nullptr, "out_handle is null");
+    *out_handle = nullptr;
+    MGP_REQUIRE(kind == KIND_RBF || kind == KIND_MATERN52,
+                "kernel kind must be 0 (RBF) or 1 (Matern52)");
+    MGP_REQUIRE(d >= 1 && d <= 32, "input dimension must be in [1, 32]");
+    MGP_REQUIRE(n >= 1, "n must be >= 1");
+    MGP_REQUIRE(X != nullptr && params != nullptr, "null input array");
+    const int expect = ard ? d + 1 : 2;
+    MGP_REQUIRE(nparams == expect,
+                "params has " + std::to_string(nparams) + " values, expected " +
+                    std::to_string(expect));
+    MGP_REQUIRE(std::isfinite(noise) && noise >= 0.f, "noise must be finite and >= 0");
+    for (int p = 0; p < nparams; ++p)
+      MGP_REQUIRE(std::isfinite(params[p]) && params[p] > 0.f,
+                  "kernel parameters must be finite and > 0");
+    auto* pv = new Provider();
+    try {
+      pv->kind = kind;
+      pv->ard = ard != 0;
+      pv->d = d;
+      pv->n = n;
+      pv->nparams = nparams;
+      pv->params.assign(params, params + nparams);
+      pv->noise = noise;
+      pv->center.assign(d, 0.0);
+      for (int64_t i = 0; i < n; ++i)
+        for (int k = 0; k < d; ++k) pv->center[k] += (double)X[i * d + k];
+      for (int k = 0; k < d; ++k) pv->center[k] /= (double)n;
+      MGP_HIP_CHECK(hipStreamCreateWithFlags(&pv->st, hipStreamNonBlocking));
+      pv->X.ensure((size_t)n * d);
+      MGP_HIP_CHECK(hipMemcpyAsync(pv->X.ptr, X, (size_t)n * d * sizeof(float),
+                                   hipMemcpyHostToDevice, pv->st));
+      pv->refresh_coords();
+      MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+    } catch (...) {
+      if (pv->st) (void)hipStreamDestroy(pv->st);
+      delete pv;
+      throw;
+    }
+    *out_handle = pv;
+  });
+}
+
+int mgp_destroy_provider(void* h) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    if (pv->st) (void)hipStreamSynchronize(pv->st);
+    if (pv->ws.ev0) (void)hipEventDestroy(pv->ws.ev0);
+    if (pv->ws.ev1) (void)hipEventDestroy(pv->ws.ev1);
+    hipStream_t st = pv->st;
+    delete pv;  // frees device buffers
+    if (st) (void)hipStreamDestroy(st);
+  });
+}
+
+int mgp_update_params(void* h, const float* params, int nparams) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(nparams == pv->nparams, "wrong number of kernel parameters");
+    for (int p = 0; p < nparams; ++p)
+      MGP_REQUIRE(std::isfinite(params[p]) && params[p] > 0.f,
+                  "kernel parameters must be finite and > 0");
+    pv->params.assign(params, params + nparams);
+    pv->refresh_coords();
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+int mgp_update_noise(void* h, float noise) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(std::isfinite(noise) && noise >= 0.f, "noise must be finite and >= 0");
+    pv->noise = noise;
+  });
+}
+
+int mgp_get_noise(void* h, float* out) {
+  return guarded([&] { *out = as_provider(h)->noise; });
+}
+
+int mgp_get_diagonal_value(void* h, float* out) {
+  return guarded([&] { *out = as_provider(h)->outputscale(); });
+}
+
+int mgp_provider_info(void* h, int64_t* n, int* d, int* nparams, int* kind,
+                      int* ard) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    if (n) *n = pv->n;
+    if (d) *d = pv->d;
+    if (nparams) *nparams = pv->nparams;
+    if (kind) *kind = pv->kind;
+    if (ard) *ard = pv->ard ? 1 : 0;
+  });
+}
+
+int mgp_forward_matvec(void* h, const float* V, int ncols, float* out) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(ncols >= 1, "ncols must be >= 1");
+    MGP_REQUIRE(V && out, "null array");
+    const size_t tot = (size_t)pv->n * ncols;
+    float* dv = pv->io_a.ensure(tot);
+    float* dout = pv->io_b.ensure(tot);
+    MGP_HIP_CHECK(hipMemcpyAsync(dv, V, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    pv->forward(dv, ncols, dout);
+    MGP_HIP_CHECK(hipMemcpyAsync(out, dout, tot * sizeof(float), hipMemcpyDeviceToHost, pv->st));
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+int mgp_forward_matvec_device(void* h, const float* V_dev, int ncols,
+                              float* out_dev) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(ncols >= 1, "ncols must be >= 1");
+    MGP_REQUIRE(V_dev && out_dev, "null device array");
+    pv->forward(V_dev, ncols, out_dev);
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+int mgp_direct_matvec(void* h, const float* V, int ncols, float* out) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(ncols >= 1, "ncols must be >= 1");
+    const size_t tot = (size_t)pv->n * ncols;
+    float* dv = pv->io_a.ensure(tot);
+    float* dout = pv->io_b.ensure(tot);
+    MGP_HIP_CHECK(hipMemcpyAsync(dv, V, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    MatvecArgs a;
+    a.kind = pv->kind;
+    a.outputscale = pv->outputscale();
+    a.noise = pv->noise;
+    a.square = true;
+    a.m = a.n = pv->n;
+    a.ncols = ncols;
+    direct_matvec(a, pv->train, pv->train, pv->d, dv, dout, pv->st);
+    MGP_HIP_CHECK(hipMemcpyAsync(out, dout, tot * sizeof(float), hipMemcpyDeviceToHost, pv->st));
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+int mgp_cross_matvec(void* h, const float* Xs, int64_t m, const float* V,
+                     int ncols, float* out) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(m >= 1 && ncols >= 1, "m and ncols must be >= 1");
+    MGP_REQUIRE(Xs && V && out, "null array");
+    float* dx = pv->Xs.ensure((size_t)m * pv->d);
+    MGP_HIP_CHECK(hipMemcpyAsync(dx, Xs, (size_t)m * pv->d * sizeof(float),
+                                 hipMemcpyHostToDevice, pv->st));
+    pv->pack(dx, m, pv->test);
+    const size_t tv = (size_t)pv->n * ncols, to = (size_t)m * ncols;
+    float* dv = pv->io_a.ensure(tv);
+    float* dout = pv->io_b.ensure(to);
+    MGP_HIP_CHECK(hipMemcpyAsync(dv, V, tv * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    pv->cross(pv->test, dv, ncols, dout);
+    MGP_HIP_CHECK(hipMemcpyAsync(out, dout, to * sizeof(float), hipMemcpyDeviceToHost, pv->st));
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+// k(x, x) of a stationary kernel is the outputscale (r = 1e-10 for Matern
+// rounds to exactly os in fp32).
+int mgp_extract_diagonal(void* h, float* out) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    const float os = pv->outputscale();
+    for (int64_t i = 0; i < pv->n; ++i) out[i] = os;
+  });
+}
+
+int mgp_extract_diagonal_test(void* h, const float* Xs, int64_t m, float* out) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    (void)Xs;
+    const float os = pv->outputscale();
+    for (int64_t i = 0; i < m; ++i) out[i] = os;
+  });
+}
+
+// op 0: forward matvec (the north-star unit).  times_ms[r] is the host wall
+// time of repeat r (launch + device + sync); tile_ms_avg receives the mean
+// HIP-event duration of the fused tile kernel over the repeats.
+int mgp_benchmark_provider_ops(void* h, const float* rhs, int ncols, int op,
+                               int repeats, int warmup, double* times_ms,
+                               double* tile_ms_avg, float* out_or_null) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(ncols >= 1, "num_cols must be positive");
+    MGP_REQUIRE(repeats >= 1, "repeats must be positive");
+    MGP_REQUIRE(warmup >= 0, "warmup must be non-negative");
+    MGP_REQUIRE(op == 0, "op_code must be 0 (forward)");
+    const size_t tot = (size_t)pv->n * ncols;
+    float* dv = pv->io_a.ensure(tot);
+    float* dout = pv->io_b.ensure(tot);
+    MGP_HIP_CHECK(hipMemcpyAsync(dv, rhs, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+    for (int w = 0; w < warmup; ++w) pv->forward(dv, ncols, dout);
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+    if (!pv->ws.ev0) MGP_HIP_CHECK(hipEventCreate(&pv->ws.ev0));
+    if (!pv->ws.ev1) MGP_HIP_CHECK(hipEventCreate(&pv->ws.ev1));
+    pv->ws.time_tile = true;
+    pv->ws.tile_ms = 0.0;
+    pv->ws.tile_calls = 0;
+    try {
+      for (int r = 0; r < repeats; ++r) {
+        auto t0 = std::chrono::steady_clock::now();
+        pv->forward(dv, ncols, dout);
+        MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+        auto t1 = std::chrono::steady_clock::now();
+        if (times_ms)
+          times_ms[r] = std::chrono::duration<double, std::milli>(t1 - t0).count();
+      }
+    } catch (...) {
+      pv->ws.time_tile = false;
+      throw;
+    }
+    pv->ws.time_tile = false;
+    if (tile_ms_avg)
+      *tile_ms_avg = pv->ws.tile_calls ? pv->ws.tile_ms / (double)pv->ws.tile_calls : 0.0;
+    if (out_or_null)
+      MGP_HIP_CHECK(hipMemcpy(out_or_null, dout, tot * sizeof(float), hipMemcpyDeviceToHost));
+  });
+}
+
+}  // extern "C"

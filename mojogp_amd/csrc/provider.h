@@ -1,0 +1,53 @@
+// Device-resident kernel provider: training inputs, hyperparameters, packed
+// tile operands and the stream every call of a handle runs on.
+//
+// Reference counterpart: the generated JITProvider struct and its impl_* entry
+// points (mojogp/codegen_engine/emit/fn_ptr_module.py:159-211, 651-703).
+#pragma once
+
+#include <vector>
+
+#include "matvec.h"
+
+namespace mgp {
+
+struct Provider {
+  int kind = KIND_RBF;
+  bool ard = false;
+  int d = 0;
+  int64_t n = 0;
+  int nparams = 0;             // engine layout: [ls | ls_0..ls_{d-1}], os
+  std::vector<float> params;   // constrained values
+  float noise = 0.f;
+  std::vector<double> center;  // column means of the training inputs
+
+  hipStream_t st = nullptr;
+  DevBuf<float> X;             // raw training inputs [n][d]
+  Coords co;
+  PackedPoints train;
+  MatvecWorkspace ws;
+
+  // Scratch for the host-pointer entry points.
+  DevBuf<float> io_a, io_b, io_c;
+  PackedPoints test;
+  DevBuf<float> Xs;
+
+  // Dense K (materialized route), row-major [n][n].
+  bool materialized = false;
+  DevBuf<float> K;
+
+  float outputscale() const { return params[nparams - 1]; }
+  float lengthscale(int k) const { return ard ? params[k] : params[0]; }
+
+  // Recompute the coordinate map from params and repack the training points.
+  void refresh_coords();
+  // Pack an arbitrary point set with the current coordinate map.
+  void pack(const float* X_dev, int64_t m, PackedPoints& pp);
+
+  // (K + noise I) V  for device arrays V, out ([ncols][n] column-major).
+  void forward(const float* V, int ncols, float* out);
+  // K(Xs, X) V for a packed test set.
+  void cross(const PackedPoints& rows, const float* V, int ncols, float* out);
+};
+
+}  // namespace mgp

@@ -1,0 +1,135 @@
+"""float64 restatement of the reference kernel arithmetic (test infrastructure).
+
+Reference semantics (caspbian/mojogp):
+  * RBF       k = os * exp(max(-0.5 * sum_d (diff_d / l_d)^2, -20))
+  * Matern52  k = os * (1 + sqrt5 r + 5/3 r^2) * exp(max(-sqrt5 r, -20)),
+              r = sqrt(max(sum_d (diff_d / l_d)^2 + 1e-20, 1e-20))
+    (codegen_engine/expressions.py:77-114,197-240: forward expressions;
+     codegen_engine/passes/numerical_stability.py:29-41: exp clamp at -20 for
+     syntactically negative arguments and sqrt(max(x, 1e-20)))
+  * isotropic kernels use a single lengthscale (params [ls, os]); ARD kernels
+    use params [ls_0..ls_{d-1}, os] (kernel.py:324-365, 494-509).
+  * forward product: out[c, i] = sum_j k(x_i, x_j) V[c, j] + noise V[c, i]
+    (codegen_engine/emit/gpu_kernel.py:151-260).
+
+Pinned by tests/test_oracle_kernels.py: scikit-learn RBF / Matern(nu=2.5)
+kernels (unclamped region), the clamp special cases (exact os*e^-20 tails, k(x,
+x) = os), SymPy derivatives and central finite differences of the gradients.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+RBF = 0
+MATERN52 = 1
+
+_SQRT5 = np.sqrt(5.0)
+
+
+def _lengthscales(params: np.ndarray, d: int, ard: bool) -> np.ndarray:
+    params = np.asarray(params, dtype=np.float64)
+    return params[:d] if ard else np.full(d, params[0])
+
+
+def sq_dist(X1: np.ndarray, X2: np.ndarray, ls: np.ndarray) -> np.ndarray:
+    """sum_d ((x1_d - x2_d) / l_d)^2 from per-dimension differences (float64).
+
+    Accumulated one dimension at a time so memory stays at n1*n2 doubles."""
+    A = np.asarray(X1, dtype=np.float64) / ls
+    B = np.asarray(X2, dtype=np.float64) / ls
+    out = np.zeros((A.shape[0], B.shape[0]), dtype=np.float64)
+    for k in range(A.shape[1]):
+        diff = A[:, k, None] - B[None, :, k]
+        out += diff * diff
+    return out
+
+
+def kernel_from_sq(kind: int, r2: np.ndarray, os: float) -> np.ndarray:
+    """Kernel value from the scaled squared distance, with the reference guards."""
+    if kind == RBF:
+        return os * np.exp(np.maximum(-0.5 * r2, -20.0))
+    r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
+    return os * (1.0 + _SQRT5 * r + (5.0 / 3.0) * r * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
+
+
+def kernel_matrix(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
+    """K(X1, X2) in float64."""
+    X1 = np.atleast_2d(np.asarray(X1, dtype=np.float64))
+    X2 = np.atleast_2d(np.asarray(X2, dtype=np.float64))
+    d = X1.shape[1]
+    ls = _lengthscales(params, d, ard)
+    os = float(np.asarray(params, dtype=np.float64)[-1])
+    return kernel_from_sq(kind, sq_dist(X1, X2, ls), os)
+
+
+def forward_matvec(kind: int, X, V, params, noise: float, ard: bool,
+                   rows: np.ndarray | None = None, block: int = 256) -> np.ndarray:
+    """(K + noise I) V for V of shape (ncols, n), optionally only for `rows`.
+
+    Returns shape (ncols, len(rows)) (all rows by default).  Blocked so that
+    n = 250 000 fits in memory.
+    """
+    X = np.asarray(X, dtype=np.float64)
+    V = np.atleast_2d(np.asarray(V, dtype=np.float64))
+    idx = np.arange(X.shape[0]) if rows is None else np.asarray(rows)
+    out = np.empty((V.shape[0], idx.shape[0]), dtype=np.float64)
+    for s in range(0, idx.shape[0], block):
+        r = idx[s:s + block]
+        Kb = kernel_matrix(kind, X[r], X, params, ard)
+        out[:, s:s + block] = V @ Kb.T + noise * V[:, r]
+    return out
+
+
+def cross_matvec(kind: int, Xs, X, V, params, ard: bool, block: int = 256) -> np.ndarray:
+    """K(Xs, X) V for V of shape (ncols, n); returns (ncols, m)."""
+    Xs = np.asarray(Xs, dtype=np.float64)
+    V = np.atleast_2d(np.asarray(V, dtype=np.float64))
+    out = np.empty((V.shape[0], Xs.shape[0]), dtype=np.float64)
+    for s in range(0, Xs.shape[0], block):
+        Kb = kernel_matrix(kind, Xs[s:s + block], X, params, ard)
+        out[:, s:s + block] = V @ Kb.T
+    return out
+
+
+def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
+    """dK/dtheta_p for every engine parameter p, shape (P, n1, n2), float64.
+
+    The reference differentiates the unclamped forward expression with SymPy and
+    then applies the same exp clamp to the result (numerical_stability pass runs
+    on gradients too, passes/numerical_stability.py:92-112); for Matern the r
+    in d/dl cancels analytically (overrides.py:24-41).
+      RBF:      dk/dl_d = k_clamped * diff_d^2 / l_d^3
+      Matern52: dk/dl_d = (5/3) os (1 + sqrt5 r) exp(max(-sqrt5 r, -20)) diff_d^2 / l_d^3
+      both:     dk/dos  = k / os
+    Isotropic: dk/dl = sum_d of the per-dimension terms with l_d = l.
+    """
+    X1 = np.atleast_2d(np.asarray(X1, dtype=np.float64))
+    X2 = np.atleast_2d(np.asarray(X2, dtype=np.float64))
+    d = X1.shape[1]
+    p = np.asarray(params, dtype=np.float64)
+    ls = _lengthscales(p, d, ard)
+    os = p[-1]
+    diff2 = (X1[:, None, :] - X2[None, :, :]) ** 2          # raw differences
+    r2 = np.einsum("ijk,k->ij", diff2, 1.0 / ls**2)
+    k = kernel_from_sq(kind, r2, os)
+    if kind == RBF:
+        h = k
+    else:
+        r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
+        h = (5.0 / 3.0) * os * (1.0 + _SQRT5 * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
+    terms = diff2 / ls**3                                    # (n1, n2, d)
+    if ard:
+        g = [h * terms[:, :, q] for q in range(d)]
+    else:
+        g = [h * terms.sum(axis=2)]
+    g.append(k / os)
+    return np.stack(g, axis=0)
+
+
+def gradient_matvec(kind: int, X, V, params, ard: bool) -> np.ndarray:
+    """out[p, c, i] = sum_j dk_p(x_i, x_j) V[c, j] (reference fused_gradient_matvec
+    layout out[p*n*C + c*n + i], gpu_kernel.py:382-484)."""
+    G = kernel_gradients(kind, X, X, params, ard)
+    V = np.atleast_2d(np.asarray(V, dtype=np.float64))
+    return np.einsum("pij,cj->pci", G, V)

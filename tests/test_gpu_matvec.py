@@ -1,0 +1,124 @@
+"""Parity of the gfx950 kernel products with the float64 oracle.
+
+Bar (north star): norm-wise relative error <= 1e-5 per right-hand side,
+against oracle/kernels.py which restates the reference arithmetic
+(codegen_engine/expressions.py + passes/numerical_stability.py)."""
+
+import numpy as np
+import pytest
+
+from mojogp_amd._provider import NativeProvider
+from oracle import kernels as ok
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _relerr(got, ref):
+    got = np.atleast_2d(np.asarray(got, dtype=np.float64))
+    ref = np.atleast_2d(ref)
+    num = np.linalg.norm(got - ref, axis=1)
+    den = np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
+    return float(np.max(num / den))
+
+
+def _params(rng, d, ard, lo=0.6, hi=1.6, os=1.3):
+    ls = rng.uniform(lo, hi, size=d if ard else 1)
+    return np.concatenate([ls, [os]]).astype(np.float32)
+
+
+CASES = [
+    # kind, ard, d, n, t
+    (ok.RBF, False, 1, 2000, 11),
+    (ok.RBF, True, 8, 3000, 16),
+    (ok.MATERN52, True, 16, 2500, 16),
+    (ok.MATERN52, False, 4, 1000, 1),
+    (ok.RBF, True, 6, 777, 40),
+    (ok.MATERN52, True, 3, 129, 3),
+    (ok.RBF, False, 2, 17, 2),
+    (ok.MATERN52, True, 30, 600, 5),
+    (ok.RBF, True, 5, 1, 1),
+]
+
+
+@pytest.mark.parametrize("kind,ard,d,n,t", CASES)
+def test_forward_matvec_parity(kind, ard, d, n, t):
+    rng = np.random.default_rng(1000 + 7 * d + n)
+    print(f"forward case kind={kind} ard={ard} d={d} n={n} t={t}", flush=True)
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = _params(rng, d, ard)
+    noise = 0.05
+    ref = ok.forward_matvec(kind, X, V, params, noise, ard)
+    with_p = NativeProvider(kind, ard, X, params, noise)
+    try:
+        got = with_p.forward_matvec(V)
+        direct = with_p.direct_matvec(V)
+    finally:
+        with_p.close()
+    assert got.shape == V.shape
+    assert np.all(np.isfinite(got))
+    assert _relerr(got, ref) <= TOL
+    assert _relerr(direct, ref) <= TOL
+
+
+@pytest.mark.parametrize("kind,ard,d", [(ok.RBF, True, 8), (ok.MATERN52, True, 16), (ok.RBF, False, 1)])
+@pytest.mark.parametrize("t", [1, 16, 70])
+def test_cross_matvec_parity(kind, ard, d, t):
+    rng = np.random.default_rng(77 + d + t)
+    n, m = 1500, 333
+    print(f"cross case kind={kind} d={d} t={t}", flush=True)
+    X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
+    Xs = rng.uniform(-2.5, 2.5, size=(m, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = _params(rng, d, ard)
+    ref = ok.cross_matvec(kind, Xs, X, V, params, ard)
+    p = NativeProvider(kind, ard, X, params, 0.1)
+    try:
+        got = p.cross_matvec(Xs, V)
+    finally:
+        p.close()
+    assert got.shape == (t, m) if t > 1 else got.shape == (m,)
+    assert _relerr(got, ref) <= TOL
+
+
+def test_short_lengthscale_and_update_params():
+    """Gram-form cancellation stress: short lengthscales inflate |z|^2."""
+    rng = np.random.default_rng(5)
+    n, d, t = 2048, 16, 16
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    p = NativeProvider(ok.MATERN52, True, X, _params(rng, d, True), 0.01)
+    try:
+        for lo, hi in [(0.25, 0.4), (2.0, 5.0), (0.6, 1.6)]:
+            params = _params(rng, d, True, lo, hi, os=0.8)
+            p.update_params(params)
+            p.update_noise(0.02)
+            ref = ok.forward_matvec(ok.MATERN52, X, V, params, 0.02, True)
+            got = p.forward_matvec(V)
+            print(f"ls range ({lo},{hi}) relerr {_relerr(got, ref):.3e}", flush=True)
+            assert _relerr(got, ref) <= TOL
+    finally:
+        p.close()
+
+
+def test_full_size_c3_sampled_rows():
+    """BASELINE config 3 shape (N=250k, d=16, t=16, Matern-5/2 ARD): rows sampled
+    across the matrix are compared with the float64 oracle."""
+    rng = np.random.default_rng(0)
+    n, d, t = 250_000, 16, 16
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    V /= np.linalg.norm(V, axis=1, keepdims=True)
+    params = np.concatenate([np.full(d, 1.0), [1.0]]).astype(np.float32)
+    p = NativeProvider(ok.MATERN52, True, X, params, 0.1)
+    try:
+        got = p.forward_matvec(V)
+    finally:
+        p.close()
+    rows = np.sort(rng.choice(n, size=192, replace=False))
+    ref = ok.forward_matvec(ok.MATERN52, X, V, params, 0.1, True, rows=rows, block=64)
+    err = _relerr(got[:, rows], ref)
+    print(f"C3 sampled-row relerr {err:.3e}", flush=True)
+    assert err <= TOL
