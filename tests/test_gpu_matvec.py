@@ -79,7 +79,7 @@ def test_cross_matvec_parity(kind, ard, d, t):
         got = p.cross_matvec(Xs, V)
     finally:
         p.close()
-    assert got.shape == (t, m) if t > 1 else got.shape == (m,)
+    assert got.shape == (t, m)
     assert _relerr(got, ref) <= TOL
 
 
