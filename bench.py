@@ -76,7 +76,19 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run the plain copy kernel of BYTES (HBM counter calibration)")
     args = ap.parse_args(argv)
+
+    if args.calibrate_copy:
+        import ctypes
+        from mojogp_amd import _lib
+        ms = ctypes.c_double(0.0)
+        _lib.call("mgp_calibration_copy", int(args.calibrate_copy), 3, ctypes.byref(ms))
+        gbs = 2 * args.calibrate_copy / (ms.value * 1e-3) / 1e9
+        print(json.dumps({"calibration_copy_bytes": args.calibrate_copy,
+                          "ms": ms.value, "GB/s": gbs}), flush=True)
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "

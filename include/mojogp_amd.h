@@ -99,6 +99,12 @@ MGP_API int mgp_benchmark_provider_ops(void* handle, const float* rhs,
                                        int warmup, double* times_ms,
                                        double* tile_ms_avg, float* out_or_null);
 
+/* Streaming device copy of `bytes` repeated `repeats` times; ms_avg gets the
+ * mean duration of one copy.  Used only to calibrate HBM byte counters
+ * (FETCH_SIZE / WRITE_SIZE) against a kernel of known traffic.  No reference
+ * counterpart. */
+MGP_API int mgp_calibration_copy(int64_t bytes, int repeats, double* ms_avg);
+
 #ifdef __cplusplus
 }
 #endif

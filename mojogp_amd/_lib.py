@@ -64,6 +64,7 @@ _SIGNATURES = {
     "mgp_benchmark_provider_ops": (C.c_int, [C.c_void_p, c_float_p, C.c_int, C.c_int,
                                              C.c_int, C.c_int, c_double_p, c_double_p,
                                              c_float_p]),
+    "mgp_calibration_copy": (C.c_int, [C.c_int64, C.c_int, c_double_p]),
 }
 
 _lock = threading.Lock()

@@ -18,6 +18,14 @@ static Provider* as_provider(void* h) {
   return static_cast<Provider*>(h);
 }
 
+// Plain streaming copy used to calibrate HBM byte counters.
+__global__ void k_calibration_copy(const float4* __restrict__ a,
+                                   float4* __restrict__ b, int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+    b[i] = a[i];
+}
+
 }  // namespace mgp
 
 using namespace mgp;
@@ -272,6 +280,35 @@ int mgp_benchmark_provider_ops(void* h, const float* rhs, int ncols, int op,
       *tile_ms_avg = pv->ws.tile_calls ? pv->ws.tile_ms / (double)pv->ws.tile_calls : 0.0;
     if (out_or_null)
       MGP_HIP_CHECK(hipMemcpy(out_or_null, dout, tot * sizeof(float), hipMemcpyDeviceToHost));
+  });
+}
+
+// Copies `bytes` (rounded down to 16) between two fresh device buffers
+// `repeats` times; ms_avg receives the mean HIP-event duration of one copy.
+int mgp_calibration_copy(int64_t bytes, int repeats, double* ms_avg) {
+  return guarded([&] {
+    MGP_REQUIRE(bytes >= 16 && repeats >= 1, "bytes >= 16 and repeats >= 1 required");
+    const int64_t n4 = bytes / 16;
+    DevBuf<float4> a, b;
+    a.ensure((size_t)n4);
+    b.ensure((size_t)n4);
+    MGP_HIP_CHECK(hipMemset(a.ptr, 0, (size_t)n4 * 16));
+    hipEvent_t e0, e1;
+    MGP_HIP_CHECK(hipEventCreate(&e0));
+    MGP_HIP_CHECK(hipEventCreate(&e1));
+    const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(n4, 256), 8192);
+    MGP_HIP_CHECK(hipEventRecord(e0, nullptr));
+    for (int r = 0; r < repeats; ++r)
+      hipLaunchKernelGGL(k_calibration_copy, dim3(blocks), dim3(256), 0, nullptr,
+                         a.ptr, b.ptr, n4);
+    MGP_HIP_CHECK(hipGetLastError());
+    MGP_HIP_CHECK(hipEventRecord(e1, nullptr));
+    MGP_HIP_CHECK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    MGP_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (ms_avg) *ms_avg = ms / repeats;
   });
 }
 
