@@ -99,6 +99,156 @@ MGP_API int mgp_benchmark_provider_ops(void* handle, const float* rhs,
                                        int warmup, double* times_ms,
                                        double* tile_ms_avg, float* out_or_null);
 
+/* ---- Engine: training --------------------------------------------------- */
+
+/* Mirrors the 23 positional arguments of the reference's engine.train()
+ * after the provider/y/params/noise (jit_engine_bindings.mojo:123-250; order
+ * fixed by mojogp/gp.py:1665-1691). */
+typedef struct mgp_train_opts {
+  int max_iterations;
+  float learning_rate;
+  int num_probes;
+  int max_cg_iter;
+  float cg_tol;
+  int precond_rank;
+  int verbose;
+  int use_cosine_lr;
+  int use_preconditioner;
+  int max_tridiag_iter;
+  float precond_rebuild_threshold;
+  int precond_method; /* 0 greedy (1 rpcholesky / 2 nystrom: not implemented) */
+  float init_mean;
+  int enable_early_stopping;
+  int early_stop_patience;
+  float early_stop_tol;
+  int learn_noise;
+  float noise_floor;
+  float noise_regularization;
+  int progress_interval;
+} mgp_train_opts_t;
+
+/* Progress event (the reference's event dict, jit_progress.mojo:22-65). */
+typedef struct mgp_progress {
+  const char* phase; /* "start" "iteration" "nan" "early_stop" "complete" */
+  int current;
+  int total;
+  double nll;
+  double best_nll;
+  int cg_iter;       /* -1: absent */
+  double iter_ms;    /* < 0: absent */
+  double noise;      /* < 0: absent */
+  double mean;
+  int precond_rank;
+  int precond_rebuild_count;
+  int converged;
+} mgp_progress_t;
+typedef void (*mgp_progress_cb)(const mgp_progress_t* event, void* user);
+
+/* Result of mgp_train (the reference's result dict,
+ * jit_engine_bindings.mojo:336-432).  Array members are caller-allocated:
+ * params[nparams], the histories [max_iterations], cached_alpha[n]; any may be
+ * NULL.  The *_len members receive the number of entries written. */
+typedef struct mgp_train_result {
+  float* params;
+  float* nll_history;
+  double* iter_times_ms;
+  int* cg_iterations_history;
+  int* precond_rank_history;
+  int* precond_rebuild_steps;
+  float* cached_alpha;
+  float final_nll;
+  float noise;
+  float mean;
+  int iterations;
+  int converged;
+  int history_len;
+  int cg_history_len;
+  int rank_history_len;
+  int rebuild_steps_len;
+  int precond_build_count;
+  double precond_build_total_ms;
+  int has_alpha;
+} mgp_train_result_t;
+
+/* Adam training of the kernel hyperparameters, noise and constant mean with
+ * preconditioned mBCG / SLQ.  Replaces engine.train() (train_python,
+ * jit_engine_bindings.mojo:123-432 -> train_jit_with_provider,
+ * jit_training.mojo:274-1008).  cb may be NULL. */
+MGP_API int mgp_train(void* handle, const float* y, const float* init_params,
+                      int nparams, float init_noise,
+                      const mgp_train_opts_t* opts, mgp_progress_cb cb,
+                      void* user, mgp_train_result_t* out);
+
+/* One BBMM evaluation at the provider's current hyperparameters: NLL per
+ * sample, y^T K^-1 y, log|K| (SLQ) and gradients[nparams + 1] (kernel
+ * params, then noise) of the reference's bbmm_with_precond
+ * (combined_inv_quad_logdet.mojo:452-1140) with probe seed
+ * iteration*104729+42 and a greedy preconditioner of precond_rank (0: none).
+ * Internal to the reference (no exported counterpart); exposed for
+ * teacher-forced parity tests. */
+MGP_API int mgp_bbmm_eval(void* handle, const float* y, float mean,
+                          int num_probes, int max_cg_iter, int max_tridiag_iter,
+                          float cg_tol, int iteration, int precond_rank,
+                          float* nll, float* inv_quad, float* logdet,
+                          float* grads, int* cg_iterations,
+                          float* precond_logdet);
+/* Counter-hash Gaussian draws of kernel_gpu_gaussian
+ * (pivoted_cholesky.mojo:51-86), computed on the device. */
+MGP_API int mgp_gaussian(int64_t len, uint64_t seed, float* out);
+/* Greedy pivoted Cholesky factor L[rank][n] (column-major, realised rank in
+ * rank_out) and log|L L^T + noise I| of
+ * build_pivoted_cholesky_precond_unified (pivoted_cholesky.mojo:2104-2444). */
+MGP_API int mgp_pivoted_cholesky(void* handle, int rank, float* L_out,
+                                 int* rank_out, float* logdet);
+
+/* ---- Engine: prediction ------------------------------------------------- */
+
+typedef struct mgp_predict_opts {
+  float mean;          /* learned constant mean */
+  int variance_method; /* 0 mean only, 1 LOVE, 2 exact */
+  int max_cg_iter;
+  float cg_tol;
+  int precond_rank;
+  int lanczos_rank;
+  int exact_block_cols;
+} mgp_predict_opts_t;
+
+typedef struct mgp_predict_info {
+  double alpha_time_s;
+  double mean_time_s;
+  double variance_time_s;
+  double total_time_s;
+  double love_root_time_s;
+  int alpha_cache_used;
+  int love_root_cache_used;
+  int alpha_cg_iterations;
+} mgp_predict_info_t;
+
+/* Predictive mean (and variance) at Xs[m][d].  alpha_in / root_in are the
+ * optional cached alpha [n] and LOVE root [lanczos_rank][n]; alpha_out /
+ * root_out (optional) receive what was computed.  The provider must already
+ * hold the trained params/noise.  Replaces engine.predict()
+ * (predict_python, jit_engine_bindings.mojo:944-1235). */
+MGP_API int mgp_predict(void* handle, const float* y, const float* Xs,
+                        int64_t m, const mgp_predict_opts_t* opts,
+                        const float* alpha_in, const float* root_in,
+                        float* mean_out, float* var_out, float* alpha_out,
+                        float* root_out, mgp_predict_info_t* info);
+
+/* Device-resident alpha (+ LOVE root) reused across predictions.  Replace
+ * prepare_prediction_cache / predict_with_cache / destroy_prediction_cache
+ * (jit_engine_bindings.mojo:636-942, PredictionCacheJIT :72-121). */
+MGP_API int mgp_prepare_prediction_cache(void* handle, const float* y,
+                                         const mgp_predict_opts_t* opts,
+                                         const float* alpha_in,
+                                         void** cache_out,
+                                         mgp_predict_info_t* info);
+MGP_API int mgp_predict_with_cache(void* handle, void* cache, const float* Xs,
+                                   int64_t m, int variance_method,
+                                   float* mean_out, float* var_out,
+                                   mgp_predict_info_t* info);
+MGP_API int mgp_destroy_prediction_cache(void* cache);
+
 /* Streaming device copy of `bytes` repeated `repeats` times; ms_avg gets the
  * mean duration of one copy.  Used only to calibrate HBM byte counters
  * (FETCH_SIZE / WRITE_SIZE) against a kernel of known traffic.  No reference

@@ -1,0 +1,344 @@
+"""Python shims with the reference's native-module surface.
+
+``KernelModule`` stands where the reference's generated fn-ptr kernel module
+stands (``init_provider / materialize / destroy_provider``,
+mojogp/codegen_engine/emit/fn_ptr_module.py:998-1211) and ``Engine`` where
+``mojogp_jit_engine`` stands (``train / predict / prepare_prediction_cache /
+predict_with_cache / destroy_prediction_cache / benchmark_provider_ops``,
+mojogp/kernels/jit/jit_engine_bindings.mojo:1750-1775): same positional
+arguments, same return-dict keys.  Every call goes to libmojogp_amd.so; there is
+no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from typing import Any
+
+import numpy as np
+
+from . import _lib
+from ._provider import NativeProvider, kind_code
+
+_DEFAULT_PREDICT_LANCZOS_RANK = 100
+_DEFAULT_ARD_PREDICT_LANCZOS_RANK = 200
+
+
+class KernelModule:
+    """Kernel module for one (kernel family, ARD, input dimension)."""
+
+    def __init__(self, kind, ard: bool, dim: int):
+        self.kind = kind_code(kind)
+        self.ard = bool(ard)
+        self.dim = int(dim)
+
+    def init_provider(self, X, params, noise, observation_noise=None, noise_mode=None,
+                      noise_group_train=None, num_noise_groups=None) -> dict[str, Any]:
+        if observation_noise is not None or noise_mode not in (None, 0):
+            raise NotImplementedError(
+                "heteroskedastic / grouped / learned-vector noise modes are not part of the "
+                "gfx950 hot path; use scalar learned noise")
+        X = _lib.f32(X)
+        if X.ndim != 2 or X.shape[1] != self.dim:
+            raise ValueError(f"X must have shape (n, {self.dim})")
+        prov = NativeProvider(self.kind, self.ard, X, params, noise)
+        return {
+            "provider_ptr": int(prov.handle.value),
+            "n": int(X.shape[0]),
+            "dim": self.dim,
+            "num_gradient_params": prov.nparams,
+            "supports_fused_gradient": True,
+            "supports_fused_ls_os": False,
+            "supports_fused_3param": False,
+            "x_ptr": 0,
+            "is_ard": self.ard,
+            "materialization_mode": 0,
+            "noise_mode": 0,
+            "has_observation_noise_vector": False,
+            "noise_group_ptr": 0,
+            "num_noise_groups": 0,
+            "_provider": prov,
+        }
+
+    def materialize(self, info: dict) -> bool:
+        """Select the materialized route for this provider (dense K on device)."""
+        info["materialization_mode"] = 1
+        return True
+
+    def destroy_provider(self, info: dict) -> bool:
+        prov = info.get("_provider")
+        if prov is not None:
+            prov.close()
+        info["provider_ptr"] = 0
+        info["x_ptr"] = 0
+        info["materialization_mode"] = 0
+        info["_provider"] = None
+        return True
+
+
+def _provider(info: dict) -> NativeProvider:
+    prov = info.get("_provider")
+    if prov is None or not info.get("provider_ptr"):
+        raise RuntimeError("provider_info does not hold a live provider")
+    return prov
+
+
+def _resolve_lanczos_rank(info: dict, requested: int) -> int:
+    """jit_engine_binding_helpers.mojo:23-45 (single-output, non-mixed)."""
+    if requested > 0:
+        return int(requested)
+    rank = _DEFAULT_PREDICT_LANCZOS_RANK
+    if info.get("is_ard"):
+        rank = max(rank, _DEFAULT_ARD_PREDICT_LANCZOS_RANK)
+    return rank
+
+
+def _progress_bridge(callback):
+    if callback is None:
+        null = _lib.PROGRESS_CB()  # NULL function pointer
+        return null, null
+
+    def _cb(ev_ptr, _user):
+        ev = ev_ptr.contents
+        stats = {"nll": float(ev.nll), "best_nll": float(ev.best_nll)}
+        if ev.cg_iter >= 0:
+            stats["cg_iter"] = int(ev.cg_iter)
+        if ev.iter_ms >= 0:
+            stats["iter_ms"] = float(ev.iter_ms)
+        if ev.noise >= 0:
+            stats["noise"] = float(ev.noise)
+        stats["mean"] = float(ev.mean)
+        if ev.precond_rank >= 0:
+            stats["precond_rank"] = int(ev.precond_rank)
+        if ev.precond_rebuild_count >= 0:
+            stats["precond_rebuild_count"] = int(ev.precond_rebuild_count)
+        event = {
+            "operation": "train", "model": "single_output", "route": "unknown",
+            "phase": ev.phase.decode(), "current": int(ev.current), "total": int(ev.total),
+            "converged": bool(ev.converged), "stats": stats,
+        }
+        callback(event)
+
+    cfun = _lib.PROGRESS_CB(_cb)
+    return cfun, cfun
+
+
+class Engine:
+    """Engine module: training and prediction entry points."""
+
+    # ------------------------------------------------------------ train
+    def train(self, *args) -> dict[str, Any]:
+        if len(args) < 17 or len(args) > 25:
+            raise ValueError("train() expects between 17 and 25 positional arguments")
+        info, y, params, init_noise = args[0], args[1], args[2], float(args[3])
+        prov = _provider(info)
+        o = _lib.TrainOpts()
+        o.max_iterations = int(args[4])
+        o.learning_rate = float(args[5])
+        o.num_probes = int(args[6])
+        o.max_cg_iter = int(args[7])
+        o.cg_tol = float(args[8])
+        o.precond_rank = int(args[9])
+        o.verbose = int(bool(args[10]))
+        o.use_cosine_lr = int(bool(args[11]))
+        o.use_preconditioner = int(bool(args[12]))
+        o.max_tridiag_iter = int(args[13])
+        o.precond_rebuild_threshold = float(args[14])
+        o.precond_method = int(args[15])
+        o.init_mean = float(args[16])
+        o.enable_early_stopping = int(bool(args[17])) if len(args) > 17 else 0
+        o.early_stop_patience = int(args[18]) if len(args) > 18 else 10
+        o.early_stop_tol = float(args[19]) if len(args) > 19 else 1e-4
+        o.learn_noise = int(bool(args[20])) if len(args) > 20 else 1
+        o.noise_floor = float(args[21]) if len(args) > 21 else 1e-6
+        o.noise_regularization = float(args[22]) if len(args) > 22 else 0.01
+        callback = args[23] if len(args) > 23 else None
+        o.progress_interval = int(args[24]) if len(args) > 24 else 1
+        if o.max_iterations <= 0:
+            raise ValueError("max_iterations must be > 0")
+
+        y = _lib.f32(y).ravel()
+        params = _lib.f32(params).ravel()
+        n, P, T = prov.n, prov.nparams, o.max_iterations
+        out_params = np.zeros(P, np.float32)
+        nll_h = np.zeros(T, np.float32)
+        times = np.zeros(T, np.float64)
+        cg_h = np.zeros(T, np.int32)
+        rank_h = np.zeros(T, np.int32)
+        rebuild = np.zeros(T, np.int32)
+        alpha = np.zeros(n, np.float32)
+        res = _lib.TrainResult()
+        res.params = _lib.fptr(out_params)
+        res.nll_history = _lib.fptr(nll_h)
+        res.iter_times_ms = _lib.dptr(times)
+        res.cg_iterations_history = cg_h.ctypes.data_as(_lib.c_int_p)
+        res.precond_rank_history = rank_h.ctypes.data_as(_lib.c_int_p)
+        res.precond_rebuild_steps = rebuild.ctypes.data_as(_lib.c_int_p)
+        res.cached_alpha = _lib.fptr(alpha)
+        cfun, _keep = _progress_bridge(callback)
+        _lib.call("mgp_train", prov.handle, _lib.fptr(y), _lib.fptr(params), P, init_noise,
+                  C.byref(o), cfun, None, C.byref(res))
+        # The native loop left the provider at its last evaluated state.
+        hl = res.history_len
+        out = {
+            "final_nll": float(res.final_nll),
+            "noise": float(res.noise),
+            "mean": float(res.mean),
+            "iterations": int(res.iterations),
+            "converged": bool(res.converged),
+            "training_route": "materialized" if info.get("materialization_mode") == 1 else "matrix_free",
+            "materialization_mode": int(info.get("materialization_mode", 0)),
+            "is_ard": bool(info.get("is_ard", False)),
+            "precond_method": int(o.precond_method),
+            "precond_rank": int(o.precond_rank),
+            "max_tridiag_iter": int(o.max_tridiag_iter),
+            "precond_rebuild_threshold": float(o.precond_rebuild_threshold),
+            "use_preconditioner": bool(o.use_preconditioner),
+            "learn_noise": bool(o.learn_noise),
+            "noise_floor": float(o.noise_floor),
+            "noise_regularization": float(o.noise_regularization),
+            "enable_early_stopping": bool(o.enable_early_stopping),
+            "early_stop_patience": int(o.early_stop_patience),
+            "early_stop_tol": float(o.early_stop_tol),
+            "params": [float(v) for v in out_params],
+            "iter_times_ms": [float(v) for v in times[:hl]],
+            "nll_history": [float(v) for v in nll_h[:hl]],
+            "cg_iterations_history": [int(v) for v in cg_h[:res.cg_history_len]],
+            "precond_rank_history": [int(v) for v in rank_h[:res.rank_history_len]],
+            "precond_rebuild_steps": [int(v) for v in rebuild[:res.rebuild_steps_len]],
+            "precond_build_count": int(res.precond_build_count),
+            "precond_rebuild_count": max(0, int(res.precond_build_count) - 1),
+            "precond_build_total_ms": float(res.precond_build_total_ms),
+            "actual_precond_rank": int(rank_h[res.rank_history_len - 1]) if res.rank_history_len else 0,
+        }
+        if res.has_alpha:
+            out["cached_alpha"] = alpha
+        return out
+
+    # ------------------------------------------------------------ predict
+    def predict(self, *args) -> dict[str, Any]:
+        if len(args) < 7 or len(args) > 16:
+            raise ValueError("predict() expects 7 to 16 positional arguments")
+        info, y, Xs, params = args[0], args[1], args[2], args[3]
+        noise, mean, vm = float(args[4]), float(args[5]), int(args[6])
+        max_cg = int(args[7]) if len(args) > 7 else 100
+        tol = float(args[8]) if len(args) > 8 else 1e-2
+        precond_rank = int(args[9]) if len(args) > 9 else 10
+        lanczos_rank = int(args[10]) if len(args) > 10 else 0
+        state_current = bool(args[11]) if len(args) > 11 else False
+        exact_cols = int(args[12]) if len(args) > 12 else 0
+        alpha_in = _lib.f32(args[13]).ravel() if len(args) > 13 and args[13] is not None else None
+        root_in = _lib.f32(args[14]).ravel() if len(args) > 14 and args[14] is not None else None
+        prov = _provider(info)
+        lanczos_rank = _resolve_lanczos_rank(info, lanczos_rank)
+        if not state_current:
+            prov.update_params(params)
+            prov.update_noise(noise)
+        Xs = _lib.f32(Xs)
+        m = Xs.shape[0]
+        y = _lib.f32(y).ravel()
+        if root_in is not None and root_in.size != prov.n * lanczos_rank:
+            root_in = None
+        o = _lib.PredictOpts(mean, vm, max_cg, tol, precond_rank, lanczos_rank, exact_cols)
+        mean_out = np.zeros(m, np.float32)
+        var_out = np.zeros(m, np.float32)
+        alpha_out = np.zeros(prov.n, np.float32)
+        root_out = np.zeros(prov.n * lanczos_rank, np.float32) if vm == 1 and root_in is None else None
+        inf = _lib.PredictInfo()
+        _lib.call("mgp_predict", prov.handle, _lib.fptr(y), _lib.fptr(Xs), m, C.byref(o),
+                  None if alpha_in is None else _lib.fptr(alpha_in),
+                  None if root_in is None else _lib.fptr(root_in),
+                  _lib.fptr(mean_out), _lib.fptr(var_out), _lib.fptr(alpha_out),
+                  None if root_out is None else _lib.fptr(root_out), C.byref(inf))
+        out = {
+            "mean": mean_out,
+            "variance": var_out if vm != 0 else np.zeros(m, np.float32),
+            "std": np.sqrt(var_out) if vm != 0 else np.zeros(m, np.float32),
+            "alpha_time_s": inf.alpha_time_s,
+            "mean_time_s": inf.mean_time_s,
+            "variance_time_s": inf.variance_time_s,
+            "total_time_s": inf.total_time_s,
+            "love_root_time_s": inf.love_root_time_s,
+            "provider_state_update_skipped": state_current,
+            "alpha_cache_used": bool(inf.alpha_cache_used),
+            "love_root_cache_used": bool(inf.love_root_cache_used),
+            "alpha_cg_iterations": int(inf.alpha_cg_iterations),
+        }
+        if alpha_in is None:
+            out["cached_alpha"] = alpha_out
+        if root_out is not None:
+            out["cached_lanczos_root"] = root_out
+        return out
+
+    # ------------------------------------------------------------ cache
+    def prepare_prediction_cache(self, *args) -> dict[str, Any]:
+        if len(args) < 11 or len(args) > 13:
+            raise ValueError("prepare_prediction_cache() expects 11 to 13 positional arguments")
+        info, y, params = args[0], args[1], args[2]
+        noise, mean, vm = float(args[3]), float(args[4]), int(args[5])
+        max_cg, tol, precond_rank = int(args[6]), float(args[7]), int(args[8])
+        lanczos_rank = _resolve_lanczos_rank(info, int(args[9]))
+        state_current = bool(args[10])
+        alpha_in = _lib.f32(args[11]).ravel() if len(args) > 11 and args[11] is not None else None
+        prov = _provider(info)
+        if not state_current:
+            prov.update_params(params)
+            prov.update_noise(noise)
+        y = _lib.f32(y).ravel()
+        o = _lib.PredictOpts(mean, vm, max_cg, tol, precond_rank, lanczos_rank, 0)
+        h = C.c_void_p()
+        inf = _lib.PredictInfo()
+        _lib.call("mgp_prepare_prediction_cache", prov.handle, _lib.fptr(y), C.byref(o),
+                  None if alpha_in is None else _lib.fptr(alpha_in), C.byref(h), C.byref(inf))
+        return {"cache_handle": int(h.value), "variance_method": vm,
+                "lanczos_rank": lanczos_rank, "alpha_time_s": inf.alpha_time_s,
+                "love_root_time_s": inf.love_root_time_s,
+                "alpha_cache_used": bool(inf.alpha_cache_used)}
+
+    def predict_with_cache(self, *args) -> dict[str, Any]:
+        info, handle, Xs = args[0], int(args[1]), _lib.f32(args[2])
+        vm = int(args[6]) if len(args) > 6 else 1
+        prov = _provider(info)
+        m = Xs.shape[0]
+        mean_out = np.zeros(m, np.float32)
+        var_out = np.zeros(m, np.float32)
+        inf = _lib.PredictInfo()
+        _lib.call("mgp_predict_with_cache", prov.handle, C.c_void_p(handle), _lib.fptr(Xs), m, vm,
+                  _lib.fptr(mean_out), _lib.fptr(var_out), C.byref(inf))
+        return {"mean": mean_out,
+                "variance": var_out if vm != 0 else np.zeros(m, np.float32),
+                "std": np.sqrt(var_out) if vm != 0 else np.zeros(m, np.float32),
+                "total_time_s": inf.total_time_s, "alpha_cache_used": True,
+                "love_root_cache_used": bool(inf.love_root_cache_used)}
+
+    def destroy_prediction_cache(self, handle) -> bool:
+        if handle:
+            _lib.call("mgp_destroy_prediction_cache", C.c_void_p(int(handle)))
+        return True
+
+    # ------------------------------------------------------------ bench
+    def benchmark_provider_ops(self, info, rhs, num_cols, op_code, repeats, warmup) -> dict:
+        if int(op_code) != 0:
+            raise ValueError("op_code must be 0 (forward) on this engine")
+        prov = _provider(info)
+        V = _lib.f32(rhs).reshape(int(num_cols), prov.n)
+        times, tile_ms, out = prov.benchmark_forward(V, int(repeats), int(warmup))
+        return {"n": prov.n, "num_cols": int(num_cols), "num_params": prov.nparams,
+                "op_code": 0, "repeats": int(repeats), "warmup": int(warmup),
+                "times_ms": [float(t) for t in times], "tile_kernel_ms": tile_ms,
+                "output_column_major": out.ravel()}
+
+
+_ENGINE = Engine()
+
+
+def load_engine() -> Engine:
+    """Counterpart of mojogp.loader.load_engine (loader.py:239-328)."""
+    _lib.load()
+    return _ENGINE
+
+
+def load_kernel_module(kind, ard: bool, dim: int) -> KernelModule:
+    """Counterpart of mojogp.loader.load_kernel_module_engine (loader.py:331-429)."""
+    _lib.load()
+    return KernelModule(kind, ard, dim)

@@ -25,6 +25,66 @@ c_int_p = C.POINTER(C.c_int)
 c_void_pp = C.POINTER(C.c_void_p)
 
 
+class TrainOpts(C.Structure):
+    """mgp_train_opts_t"""
+    _fields_ = [
+        ("max_iterations", C.c_int), ("learning_rate", C.c_float), ("num_probes", C.c_int),
+        ("max_cg_iter", C.c_int), ("cg_tol", C.c_float), ("precond_rank", C.c_int),
+        ("verbose", C.c_int), ("use_cosine_lr", C.c_int), ("use_preconditioner", C.c_int),
+        ("max_tridiag_iter", C.c_int), ("precond_rebuild_threshold", C.c_float),
+        ("precond_method", C.c_int), ("init_mean", C.c_float),
+        ("enable_early_stopping", C.c_int), ("early_stop_patience", C.c_int),
+        ("early_stop_tol", C.c_float), ("learn_noise", C.c_int), ("noise_floor", C.c_float),
+        ("noise_regularization", C.c_float), ("progress_interval", C.c_int),
+    ]
+
+
+class Progress(C.Structure):
+    """mgp_progress_t"""
+    _fields_ = [
+        ("phase", C.c_char_p), ("current", C.c_int), ("total", C.c_int), ("nll", C.c_double),
+        ("best_nll", C.c_double), ("cg_iter", C.c_int), ("iter_ms", C.c_double),
+        ("noise", C.c_double), ("mean", C.c_double), ("precond_rank", C.c_int),
+        ("precond_rebuild_count", C.c_int), ("converged", C.c_int),
+    ]
+
+
+PROGRESS_CB = C.CFUNCTYPE(None, C.POINTER(Progress), C.c_void_p)
+
+
+class TrainResult(C.Structure):
+    """mgp_train_result_t"""
+    _fields_ = [
+        ("params", c_float_p), ("nll_history", c_float_p), ("iter_times_ms", c_double_p),
+        ("cg_iterations_history", c_int_p), ("precond_rank_history", c_int_p),
+        ("precond_rebuild_steps", c_int_p), ("cached_alpha", c_float_p),
+        ("final_nll", C.c_float), ("noise", C.c_float), ("mean", C.c_float),
+        ("iterations", C.c_int), ("converged", C.c_int), ("history_len", C.c_int),
+        ("cg_history_len", C.c_int), ("rank_history_len", C.c_int),
+        ("rebuild_steps_len", C.c_int), ("precond_build_count", C.c_int),
+        ("precond_build_total_ms", C.c_double), ("has_alpha", C.c_int),
+    ]
+
+
+class PredictOpts(C.Structure):
+    """mgp_predict_opts_t"""
+    _fields_ = [
+        ("mean", C.c_float), ("variance_method", C.c_int), ("max_cg_iter", C.c_int),
+        ("cg_tol", C.c_float), ("precond_rank", C.c_int), ("lanczos_rank", C.c_int),
+        ("exact_block_cols", C.c_int),
+    ]
+
+
+class PredictInfo(C.Structure):
+    """mgp_predict_info_t"""
+    _fields_ = [
+        ("alpha_time_s", C.c_double), ("mean_time_s", C.c_double),
+        ("variance_time_s", C.c_double), ("total_time_s", C.c_double),
+        ("love_root_time_s", C.c_double), ("alpha_cache_used", C.c_int),
+        ("love_root_cache_used", C.c_int), ("alpha_cg_iterations", C.c_int),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The native gfx950 library is missing or failed to load."""
 
@@ -65,6 +125,22 @@ _SIGNATURES = {
                                              C.c_int, C.c_int, c_double_p, c_double_p,
                                              c_float_p]),
     "mgp_calibration_copy": (C.c_int, [C.c_int64, C.c_int, c_double_p]),
+    "mgp_train": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int, C.c_float,
+                            C.POINTER(TrainOpts), PROGRESS_CB, C.c_void_p,
+                            C.POINTER(TrainResult)]),
+    "mgp_predict": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int64,
+                              C.POINTER(PredictOpts), c_float_p, c_float_p, c_float_p,
+                              c_float_p, c_float_p, c_float_p, C.POINTER(PredictInfo)]),
+    "mgp_prepare_prediction_cache": (C.c_int, [C.c_void_p, c_float_p, C.POINTER(PredictOpts),
+                                               c_float_p, c_void_pp, C.POINTER(PredictInfo)]),
+    "mgp_predict_with_cache": (C.c_int, [C.c_void_p, C.c_void_p, c_float_p, C.c_int64, C.c_int,
+                                         c_float_p, c_float_p, C.POINTER(PredictInfo)]),
+    "mgp_destroy_prediction_cache": (C.c_int, [C.c_void_p]),
+    "mgp_bbmm_eval": (C.c_int, [C.c_void_p, c_float_p, C.c_float, C.c_int, C.c_int, C.c_int,
+                                C.c_float, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
+                                c_float_p, c_int_p, c_float_p]),
+    "mgp_gaussian": (C.c_int, [C.c_int64, C.c_uint64, c_float_p]),
+    "mgp_pivoted_cholesky": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_int_p, c_float_p]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,149 @@
+// Host orchestration of the exact-GP algorithms on one provider: batched CG
+// with Lanczos tridiagonals, pivoted-Cholesky preconditioner, one BBMM
+// (NLL + gradients) evaluation, the Adam training loop and prediction.
+//
+// Reference counterparts (caspbian/mojogp):
+//   batched_cg_unified        kernels/combined_inv_quad_logdet.mojo:81-449
+//   bbmm_with_precond         kernels/combined_inv_quad_logdet.mojo:452-1140
+//   build_pivoted_cholesky_precond_unified  kernels/pivoted_cholesky.mojo:2104-2444
+//   train_jit_with_provider   kernels/jit/jit_training.mojo:274-1008
+//   prediction                kernels/jit/jit_prediction.mojo:681-1350
+#pragma once
+
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "solver.h"
+
+namespace mgp {
+
+struct Precond {
+  int rank = 0;        // 0 = no preconditioner
+  float noise = 0.f;   // noise at construction (used by apply, log-det, probes)
+  DevBuf<float> L;     // [rank][n]
+  DevBuf<float> Minv;  // (L^T L + max(noise,1e-6) I)^{-1}, row-major fp32
+  float logdet = 0.f;  // log|L L^T + noise I|
+  WoodburyWork work;
+};
+
+void build_precond(Provider& pv, int rank, int method, Precond& P);
+
+struct CGWork {
+  DevBuf<float> x, r, z, p, Ap;  // [C][n]
+  DevBuf<float> scal;            // rz_old | alpha | beta   (3*C)
+  DevBuf<float> hist_a, hist_b;  // [max_tridiag][C]
+  DevBuf<double> part_a, part_b; // [C][nb]
+  DevBuf<float> resn;            // [1]
+  DevBuf<int> done;
+  CGScalars scalars(int ncols);
+};
+
+struct CGResult {
+  int iterations = 0;
+  bool converged = false;
+  int tridiag_size = 0;
+  std::vector<std::vector<float>> diag, offdiag;  // per column
+};
+
+// Solves (K + noise I) X = rhs for `ncols` columns (device rhs [C][n]);
+// the solution stays in w.x (normalised-RHS scale, as given).
+CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int ncols, int max_iter,
+                    int max_tridiag, float tol, CGWork& w, bool warm_start);
+
+struct BBMMWork {
+  CGWork cg;
+  DevBuf<float> probes, zr, zn, rhs, sol, lf, rf, ycopy;
+  DevBuf<float> probe_norms, rhs_norms;
+  DevBuf<double> part;
+  bool has_x = false;
+};
+
+struct BBMMResult {
+  float nll = 0.f, inv_quad = 0.f, logdet = 0.f;
+  std::vector<float> grads;  // kernel params then noise
+  int cg_iterations = 0;
+  bool converged = false;
+  const float* alpha_dev = nullptr;  // sol column 0 (valid until next call)
+};
+
+BBMMResult bbmm_step(Provider& pv, Precond& P, bool use_precond, const float* y_c,
+                     int num_probes, int max_cg, int max_tridiag, float tol,
+                     int iteration, bool recycle, BBMMWork& w);
+
+struct TrainOptions {
+  int max_iterations = 100;
+  float learning_rate = 0.01f;
+  int num_probes = 10;
+  int max_cg_iter = 100;
+  float cg_tol = 1e-2f;
+  int precond_rank = 10;
+  bool verbose = false;
+  bool use_cosine_lr = false;
+  bool use_preconditioner = true;
+  int max_tridiag_iter = 30;
+  float precond_rebuild_threshold = 0.5f;
+  int precond_method = 0;
+  float init_mean = 0.f;
+  bool enable_early_stopping = false;
+  int early_stop_patience = 10;
+  float early_stop_tol = 1e-4f;
+  bool learn_noise = true;
+  float noise_floor = 1e-6f;
+  float noise_regularization = 0.01f;
+  int progress_interval = 1;
+};
+
+struct ProgressEvent {
+  const char* phase;
+  int current, total;
+  float nll, best_nll;
+  int cg_iter;
+  double iter_ms;
+  float noise, mean;
+  int precond_rank, precond_rebuild_count;
+  bool converged;
+};
+
+struct TrainResult {
+  std::vector<float> params;
+  float noise = 0.f, mean = 0.f, final_nll = 0.f;
+  int iterations = 0;
+  bool converged = false;
+  std::vector<float> nll_history;
+  std::vector<double> iter_times_ms;
+  std::vector<int> cg_iterations_history, precond_rank_history, precond_rebuild_steps;
+  int precond_build_count = 0;
+  double precond_build_total_ms = 0.0;
+  std::vector<float> alpha;  // best-NLL alpha (empty if none)
+};
+
+TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& init_params,
+                  float init_noise, const TrainOptions& o,
+                  const std::function<void(const ProgressEvent&)>& progress);
+
+// ---------------------------------------------------------------- prediction
+struct PredictState {
+  DevBuf<float> alpha;  // [n]
+  DevBuf<float> root;   // [rank][n]
+  int rank = 0;
+  bool has_alpha = false;
+};
+
+// alpha = (K + noise I)^{-1} (y - mean) by unpreconditioned CG with the
+// reference's stop rule (relative residual < tol, pAp guard).
+int solve_alpha(Provider& pv, const float* y_host, float mean, int max_iter, float tol,
+                PredictState& ps);
+// Lanczos inverse root S (S S^T ~ (K + noise I)^{-1}), rank r.
+void lanczos_inv_root(Provider& pv, int r, PredictState& ps);
+
+struct PredictTimes {
+  double alpha_s = 0, love_root_s = 0, mean_s = 0, variance_s = 0, total_s = 0;
+};
+
+// mean[m] (+ var[m] when variance_method == 1, LOVE) for test inputs.
+void predict_from_state(Provider& pv, const PredictState& ps, const float* Xs_host,
+                        int64_t m, float mean, int variance_method, float* mean_out,
+                        float* var_out, PredictTimes& t);
+
+}  // namespace mgp

@@ -1,0 +1,785 @@
+// Host orchestration of training and prediction (see engine.h).
+#include "engine.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+
+#include "host_numerics.h"
+
+namespace mgp {
+
+namespace {
+
+constexpr float kPi = 3.14159265358979323846f;
+
+using Clock = std::chrono::steady_clock;
+double secs_since(Clock::time_point t0) {
+  return std::chrono::duration<double>(Clock::now() - t0).count();
+}
+
+__global__ void k_part_to_float(const double* __restrict__ part, int nb, int ncols,
+                                float* __restrict__ out) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ncols) return;
+  double s = 0.0;
+  for (int b = 0; b < nb; ++b) s += part[(int64_t)c * nb + b];
+  out[c] = (float)s;
+}
+
+void part_to_float(const double* part, int nb, int ncols, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_part_to_float, dim3((unsigned)ceil_div(ncols, 256)), dim3(256), 0, st,
+                     part, nb, ncols, out);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+// --------------------------------------------------- single right-hand-side CG
+// Scalars: s[0] rr_old, s[1] initial residual norm, s[2] alpha, s[3] beta.
+__global__ void k_a1_init(const double* __restrict__ part, int nb, float* s, int* done) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b) acc += part[b];
+  const float rr = (float)acc;
+  float init = sqrtf(rr);
+  if (init < 1e-20f) init = 1.0f;
+  s[0] = rr;
+  s[1] = init;
+  *done = 0;
+}
+
+__global__ void k_a1_alpha(const double* __restrict__ part, int nb, float* s, int* done) {
+  if (threadIdx.x != 0 || blockIdx.x != 0 || *done) return;
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b) acc += part[b];
+  const float pap = (float)acc;
+  if (pap != pap || pap < 1e-10f) {
+    *done = 1;
+    return;
+  }
+  const float a = s[0] / pap;
+  if (a != a) {
+    *done = 1;
+    return;
+  }
+  s[2] = a;
+}
+
+__global__ void k_a1_update(float* __restrict__ x, float* __restrict__ r,
+                            const float* __restrict__ p, const float* __restrict__ Ap,
+                            int64_t n, int nb, const float* __restrict__ s,
+                            const int* __restrict__ done, double* __restrict__ rr_part) {
+  __shared__ double sm[4];
+  if (*done) return;  // uniform
+  const float a = s[2];
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  double acc = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    x[i] += a * p[i];
+    const float ri = r[i] - a * Ap[i];
+    r[i] = ri;
+    acc += (double)ri * (double)ri;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += sm[w];
+    rr_part[blockIdx.x] = t;
+  }
+}
+
+__global__ void k_a1_beta(const double* __restrict__ part, int nb, float tol, float* s,
+                          int* done) {
+  if (threadIdx.x != 0 || blockIdx.x != 0 || *done) return;
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b) acc += part[b];
+  const float rr_new = (float)acc;
+  if (sqrtf(rr_new) / s[1] < tol) {
+    *done = 1;
+    return;
+  }
+  const float rr_old = s[0];
+  float beta = 0.0f;
+  if (rr_old >= 1e-20f) {
+    beta = rr_new / (rr_old + 1e-20f);
+    if (beta < 0.0f || beta != beta) beta = 0.0f;
+  }
+  s[3] = beta;
+  s[0] = rr_new;
+}
+
+__global__ void k_a1_pupdate(float* __restrict__ p, const float* __restrict__ r, int64_t n,
+                             const float* __restrict__ s, const int* __restrict__ done) {
+  if (*done) return;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = r[i] + s[3] * p[i];
+}
+
+// Lanczos three-term recurrence: w -= a v (+ b vprev).
+__global__ void k_three_term(float* __restrict__ w, const float* __restrict__ v,
+                             const float* __restrict__ vprev, float a, float b, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float x = w[i] - a * v[i];
+  if (vprev) x -= b * vprev[i];
+  w[i] = x;
+}
+
+__global__ void k_scale_into(float* __restrict__ dst, const float* __restrict__ src, float inv,
+                             int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i] / inv;
+}
+
+__global__ void k_add_scalar(float* __restrict__ y, float s, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] += s;
+}
+
+inline dim3 g1(int64_t n) { return dim3((unsigned)std::max<int64_t>(1, ceil_div(n, 256))); }
+
+float dot_f(const float* a, const float* b, int64_t n, DevBuf<double>& part, hipStream_t st) {
+  const int nb = reduction_chunks(n);
+  double* pp = part.ensure((size_t)nb + 1);
+  coldot_partial(a, b, n, 1, nb, pp, st);
+  coldot_finalize(pp, nb, 1, pp + nb, st);
+  double h = 0.0;
+  MGP_HIP_CHECK(hipMemcpyAsync(&h, pp + nb, sizeof(double), hipMemcpyDeviceToHost, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  return (float)h;
+}
+
+}  // namespace
+
+CGScalars CGWork::scalars(int ncols) {
+  CGScalars s;
+  s.rz_old = scal.ptr;
+  s.alpha = scal.ptr + ncols;
+  s.beta = scal.ptr + 2 * ncols;
+  s.hist_alpha = hist_a.ptr;
+  s.hist_beta = hist_b.ptr;
+  s.done = done.ptr;
+  return s;
+}
+
+// ------------------------------------------------------------------ precond
+void build_precond(Provider& pv, int rank, int method, Precond& P) {
+  P.noise = pv.noise;
+  if (rank <= 0) {
+    P.rank = 0;
+    P.logdet = 0.f;
+    return;
+  }
+  MGP_REQUIRE(method == 0,
+              "only the greedy pivoted-Cholesky preconditioner (precond_method 0) is "
+              "implemented on gfx950");
+  MGP_REQUIRE(rank <= 1000, "preconditioner rank must be <= 1000");
+  const int64_t n = pv.n;
+  hipStream_t st = pv.st;
+  P.L.ensure((size_t)rank * n);
+  const int k = pivoted_cholesky_greedy(pv, rank, P.L.ptr, st);
+  P.rank = k;
+  DevBuf<double> Md;
+  Md.ensure((size_t)k * k);
+  syrk_ltl(P.L.ptr, n, k, Md.ptr, st);
+  std::vector<double> M((size_t)k * k);
+  MGP_HIP_CHECK(hipMemcpy(M.data(), Md.ptr, M.size() * sizeof(double), hipMemcpyDeviceToHost));
+  const double eff = std::max((double)P.noise, 1e-6);
+  std::vector<double> A(M), inv;
+  for (int i = 0; i < k; ++i) A[(size_t)i * k + i] += eff;
+  if (!spd_inverse(A, k, inv)) throw Error(ST_NUMERIC, "preconditioner core matrix is singular");
+  std::vector<float> invf(inv.begin(), inv.end());
+  P.Minv.ensure(invf.size());
+  MGP_HIP_CHECK(hipMemcpy(P.Minv.ptr, invf.data(), invf.size() * sizeof(float),
+                          hipMemcpyHostToDevice));
+  std::vector<double> B((size_t)k * k);
+  for (size_t q = 0; q < B.size(); ++q) B[q] = M[q] / (double)P.noise;
+  for (int i = 0; i < k; ++i) B[(size_t)i * k + i] += 1.0;
+  P.logdet = (float)n * std::log(P.noise) + (float)logdet_spd(B, k);
+}
+
+// ------------------------------------------------------------------ batched CG
+CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_iter,
+                    int max_tridiag, float tol, CGWork& w, bool warm_start) {
+  const int64_t n = pv.n;
+  hipStream_t st = pv.st;
+  const int nb = reduction_chunks(n);
+  const bool pre = P && P->rank > 0;
+  const size_t nc = (size_t)n * C;
+  float* x = w.x.ptr;  // caller ensured capacity (warm start keeps contents)
+  float* r = w.r.ensure(nc);
+  float* z = pre ? w.z.ensure(nc) : r;
+  float* p = w.p.ensure(nc);
+  float* Ap = w.Ap.ensure(nc);
+  w.scal.ensure((size_t)3 * C);
+  const int mt = std::max(max_tridiag, 1);
+  w.hist_a.ensure((size_t)mt * C);
+  w.hist_b.ensure((size_t)mt * C);
+  double* pa = w.part_a.ensure((size_t)C * nb);
+  double* pb = w.part_b.ensure((size_t)C * nb);
+  w.resn.ensure(1);
+  w.done.ensure(1);
+  CGScalars s = w.scalars(C);
+
+  if (warm_start) {
+    copy(r, rhs, nc, st);
+    pv.forward(x, C, Ap);
+    sub(r, r, Ap, nc, st);
+  } else {
+    fill(x, nc, 0.0f, st);
+    copy(r, rhs, nc, st);
+  }
+  if (pre) {
+    woodbury_apply(P->L.ptr, n, P->rank, P->Minv.ptr, P->noise, r, C, z, P->work, r, nb, pb, st);
+  } else {
+    coldot_partial(r, r, n, C, nb, pb, st);
+  }
+  copy(p, z, nc, st);
+  part_to_float(pb, nb, C, s.rz_old, st);
+
+  CGResult res;
+  int tridiag_size = 0;
+  for (int iter = 0; iter < max_iter; ++iter) {
+    res.iterations = iter + 1;
+    pv.forward(p, C, Ap);
+    coldot_partial(p, Ap, n, C, nb, pa, st);
+    cg_alpha(pa, nb, C, s, st);
+    cg_update(x, r, p, Ap, n, C, nb, s, pa, st);  // pa <- r.r partials
+    if (pre) {
+      woodbury_apply(P->L.ptr, n, P->rank, P->Minv.ptr, P->noise, r, C, z, P->work, r, nb,
+                     pb, st);
+      cg_beta(pb, nb, C, s, iter, max_tridiag, st);
+    } else {
+      cg_beta(pa, nb, C, s, iter, max_tridiag, st);
+    }
+    cg_pupdate(p, z, n, C, s, st);
+    if (iter < max_tridiag) tridiag_size = iter + 1;
+    if (iter >= 10 && (((iter + 1) % 10) == 0 || iter == max_iter - 1)) {
+      cg_mean_resnorm(pa, nb, C, w.resn.ptr, st);
+      float mean_res = 0.f;
+      MGP_HIP_CHECK(hipMemcpyAsync(&mean_res, w.resn.ptr, sizeof(float),
+                                   hipMemcpyDeviceToHost, st));
+      MGP_HIP_CHECK(hipStreamSynchronize(st));
+      if (mean_res < tol && iter >= max_tridiag - 1) {
+        res.converged = true;
+        break;
+      }
+    }
+  }
+  res.tridiag_size = tridiag_size;
+  res.diag.assign(C, {});
+  res.offdiag.assign(C, {});
+  if (tridiag_size > 0) {
+    std::vector<float> ha((size_t)tridiag_size * C), hb((size_t)tridiag_size * C);
+    MGP_HIP_CHECK(hipMemcpyAsync(ha.data(), s.hist_alpha, ha.size() * sizeof(float),
+                                 hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipMemcpyAsync(hb.data(), s.hist_beta, hb.size() * sizeof(float),
+                                 hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    // GPyTorch tridiagonal conventions (combined_inv_quad_logdet.mojo:356-424):
+    // 1/alpha := 1 for alpha < 1e-10; negative beta clamps to 0; building stops
+    // for every column once the largest off-diagonal falls below 1e-6.
+    auto recip = [](float a) { return a < 1e-10f ? 1.0f : 1.0f / a; };
+    for (int k = 0; k < tridiag_size; ++k) {
+      float max_off = 0.0f;
+      for (int c = 0; c < C; ++c) {
+        const float ak = ha[(size_t)k * C + c];
+        float dv = recip(ak);
+        if (k > 0) {
+          const float bk = hb[(size_t)(k - 1) * C + c];
+          const float apr = recip(ha[(size_t)(k - 1) * C + c]);
+          dv = dv + bk * apr;
+          const float bc = bk < 0.0f ? 0.0f : bk;
+          const float off = std::sqrt(bc) * apr;
+          res.offdiag[c].push_back(off);
+          if (off > max_off) max_off = off;
+        }
+        res.diag[c].push_back(dv);
+      }
+      if (k > 0 && max_off < 1e-6f) break;
+    }
+  }
+  return res;
+}
+
+// ------------------------------------------------------------------ BBMM
+BBMMResult bbmm_step(Provider& pv, Precond& P, bool use_precond, const float* y_c, int T,
+                     int max_cg, int max_tridiag, float tol, int iteration, bool recycle,
+                     BBMMWork& w) {
+  const int64_t n = pv.n;
+  hipStream_t st = pv.st;
+  const int C = 1 + T;
+  const size_t nT = (size_t)n * T, nC = (size_t)n * C;
+  const bool pre = use_precond && P.rank > 0;
+  const uint64_t seed = (uint64_t)((int64_t)iteration * 104729 + 42);
+
+  float* probes = w.probes.ensure(std::max<size_t>(nT, 1));
+  float* pn = w.probe_norms.ensure(std::max(T, 1));
+  float* rn = w.rhs_norms.ensure(C);
+  double* part = w.part.ensure((size_t)std::max(C, 1) * reduction_chunks(n) + 64);
+  if (T > 0) {
+    if (pre) {
+      float* zr = w.zr.ensure((size_t)P.rank * T);
+      float* zn = w.zn.ensure(nT);
+      gaussian(zr, (int64_t)P.rank * T, seed, st);
+      gaussian(zn, (int64_t)nT, seed + 1000000ull, st);
+      low_rank_sample(P.L.ptr, n, P.rank, zr, zn, std::sqrt(P.noise), T, probes, st);
+    } else {
+      gaussian(probes, (int64_t)nT, seed, st);
+    }
+    normalize_columns(probes, n, T, pn, part, st);
+  }
+  // RHS [y | Z_norm], every column normalised (GPyTorch linear_cg convention).
+  float* rhs = w.rhs.ensure(nC);
+  copy(rhs, y_c, n, st);
+  if (T > 0) copy(rhs + n, probes, nT, st);
+  normalize_columns(rhs, n, C, rn, part, st);
+
+  const bool warm = recycle && iteration > 0 && w.has_x && w.cg.x.count >= nC;
+  if (!warm) w.cg.x.ensure(nC);
+  if (warm && C > 1) fill(w.cg.x.ptr + n, (int64_t)n * (C - 1), 0.0f, st);
+  CGResult cg = batched_cg(pv, pre ? &P : nullptr, rhs, C, max_cg, max_tridiag, tol, w.cg, warm);
+  w.has_x = true;
+
+  float* sol = w.sol.ensure(nC);
+  copy(sol, w.cg.x.ptr, nC, st);
+  scale_columns(sol, rn, n, C, false, st);
+
+  BBMMResult out;
+  out.cg_iterations = cg.iterations;
+  out.converged = cg.converged;
+  out.alpha_dev = sol;
+  out.inv_quad = dot_f(y_c, sol, n, w.part, st);
+
+  float logdet = 0.0f;
+  if (cg.tridiag_size > 0) {
+    std::vector<std::vector<float>> pd(cg.diag.begin() + 1, cg.diag.end());
+    std::vector<std::vector<float>> po(cg.offdiag.begin() + 1, cg.offdiag.end());
+    logdet = slq_logdet(pd, po, n);
+    if (pre) logdet += P.logdet;
+  }
+  out.logdet = logdet;
+  const float constant = 0.5f * (float)n * std::log(2.0f * kPi);
+  out.nll = (0.5f * out.inv_quad + 0.5f * logdet + constant) / (float)n;
+
+  // Gradient factors: Lf = [-alpha/2 | (0.5/T) U], Rf = [alpha | P^-1 Z].
+  std::vector<float> norms(std::max(T, 1), 1.0f);
+  if (T > 0)
+    MGP_HIP_CHECK(hipMemcpyAsync(norms.data(), pn, T * sizeof(float), hipMemcpyDeviceToHost, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  std::vector<float> lfac(C), rfac(C);
+  lfac[0] = -0.5f;
+  rfac[0] = 1.0f;
+  for (int j = 0; j < T; ++j) {
+    lfac[1 + j] = (0.5f / (float)T) * norms[j];
+    rfac[1 + j] = norms[j];
+  }
+  DevBuf<float> facs;
+  facs.ensure(2 * (size_t)C);
+  MGP_HIP_CHECK(hipMemcpyAsync(facs.ptr, lfac.data(), C * sizeof(float), hipMemcpyHostToDevice, st));
+  MGP_HIP_CHECK(hipMemcpyAsync(facs.ptr + C, rfac.data(), C * sizeof(float), hipMemcpyHostToDevice, st));
+  float* lf = w.lf.ensure(nC);
+  float* rf = w.rf.ensure(nC);
+  copy(lf, sol, nC, st);
+  scale_columns(lf, facs.ptr, n, C, false, st);
+  copy(rf, sol, n, st);
+  if (T > 0) {
+    copy(rf + n, probes, nT, st);
+    scale_columns(rf + n, facs.ptr + C + 1, n, T, false, st);
+    if (pre)
+      woodbury_apply(P.L.ptr, n, P.rank, P.Minv.ptr, P.noise, rf + n, T, rf + n, P.work,
+                     nullptr, reduction_chunks(n), nullptr, st);
+  }
+  const int np = pv.nparams;
+  std::vector<double> g(np, 0.0);
+  gradient_traces(pv, lf, rf, C, g.data(), st);
+  out.grads.resize(np + 1);
+  for (int q = 0; q < np; ++q) {
+    float gq = (float)(g[q] / (double)n);
+    if (!std::isfinite(gq)) gq = 0.0f;
+    out.grads[q] = gq;
+  }
+  // Noise: dK/dsigma^2 = I  ->  sum_c Lf_c . Rf_c / n.
+  const int nb = reduction_chunks(n);
+  coldot_partial(lf, rf, n, C, nb, part, st);
+  coldot_finalize(part, nb, C, part + (size_t)C * nb, st);
+  std::vector<double> dots(C);
+  MGP_HIP_CHECK(hipMemcpyAsync(dots.data(), part + (size_t)C * nb, C * sizeof(double),
+                               hipMemcpyDeviceToHost, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  double tot = 0.0;
+  for (int c = 0; c < C; ++c) tot += dots[c];
+  float gn = (float)(tot / (double)n);
+  if (!std::isfinite(gn)) gn = 0.0f;
+  out.grads[np] = gn;
+  return out;
+}
+
+// ------------------------------------------------------------------ training
+TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& init_params,
+                  float init_noise, const TrainOptions& o,
+                  const std::function<void(const ProgressEvent&)>& progress) {
+  const int64_t n = pv.n;
+  const int P = pv.nparams;
+  hipStream_t st = pv.st;
+  MGP_REQUIRE((int)init_params.size() == P, "initial params size mismatch");
+  MGP_REQUIRE(o.max_iterations >= 1, "max_iterations must be >= 1");
+  MGP_REQUIRE(o.num_probes >= 0, "num_probes must be >= 0");
+
+  DevBuf<float> y, yc;
+  y.ensure(n);
+  yc.ensure(n);
+  MGP_HIP_CHECK(hipMemcpyAsync(y.ptr, y_host, n * sizeof(float), hipMemcpyHostToDevice, st));
+
+  std::vector<float> raw(P + 1);
+  for (int q = 0; q < P; ++q) raw[q] = inv_softplus(init_params[q]);
+  raw[P] = inv_softplus(init_noise);
+  float raw_mean = o.init_mean;
+  std::vector<float> m_(P + 1, 0.f), v_(P + 1, 0.f);
+  float m_mean = 0.f, v_mean = 0.f;
+  int adam_t = 0;
+
+  std::vector<float> best_raw(raw), best_m(P + 1, 0.f), best_v(P + 1, 0.f);
+  float best_raw_mean = raw_mean, best_m_mean = 0.f, best_v_mean = 0.f;
+  int best_t = 0;
+  float best_nll_seen = 1e30f, best_nll = 1e30f;
+  std::vector<float> best_alpha;
+  int no_improve = 0;
+  float lr = o.learning_rate;
+
+  std::vector<float> last_rebuild(init_params);
+  float last_rebuild_noise = init_noise;
+
+  TrainResult res;
+  Precond Pc;
+  BBMMWork work;
+  const int precond_rank = o.use_preconditioner ? o.precond_rank : 0;
+  auto rebuild = [&]() {
+    auto t0 = Clock::now();
+    build_precond(pv, precond_rank, o.precond_method, Pc);
+    res.precond_build_total_ms += secs_since(t0) * 1e3;
+    res.precond_build_count += 1;
+  };
+  rebuild();
+
+  auto emit = [&](const char* phase, int cur, float nll, float bnll, int cgi, double ms,
+                  float noise, float mean, bool conv) {
+    if (!progress) return;
+    ProgressEvent e{phase, cur, o.max_iterations, nll, bnll, cgi, ms, noise, mean,
+                    Pc.rank, std::max(0, res.precond_build_count - 1), conv};
+    progress(e);
+  };
+  emit("start", 0, 0.f, 0.f, -1, -1.0, -1.f, 0.f, false);
+
+  std::vector<float> params(P);
+  int actual = 0;
+  for (int it = 0; it < o.max_iterations; ++it) {
+    auto t_iter = Clock::now();
+    actual = it + 1;
+    for (int q = 0; q < P; ++q) params[q] = softplus(raw[q]);
+    const float noise = o.learn_noise ? softplus(raw[P]) : 0.0f;
+    pv.params = params;
+    pv.refresh_coords();
+    pv.noise = noise;
+
+    if (it > 0) {
+      float max_rel = 0.f;
+      for (int q = 0; q < P; ++q)
+        max_rel = std::max(max_rel, std::fabs(params[q] - last_rebuild[q]) /
+                                        std::max(std::fabs(last_rebuild[q]), 1e-8f));
+      if (o.learn_noise)
+        max_rel = std::max(max_rel, std::fabs(noise - last_rebuild_noise) /
+                                        std::max(std::fabs(last_rebuild_noise), 1e-8f));
+      if (max_rel > o.precond_rebuild_threshold) {
+        rebuild();
+        res.precond_rebuild_steps.push_back(it);
+        last_rebuild = params;
+        last_rebuild_noise = noise;
+      }
+    }
+    res.precond_rank_history.push_back(Pc.rank);
+
+    sub_scalar(yc.ptr, y.ptr, raw_mean, n, st);
+    BBMMResult r = bbmm_step(pv, Pc, o.use_preconditioner, yc.ptr, o.num_probes, o.max_cg_iter,
+                             o.max_tridiag_iter, o.cg_tol, it, it > 0, work);
+    const float nll = r.nll;
+    res.cg_iterations_history.push_back(r.cg_iterations);
+
+    if (nll != nll) {
+      // NaN recovery (jit_training.mojo:605-685): halve LR, restore the best
+      // snapshot, rebuild the preconditioner, skip the update.
+      lr *= 0.5f;
+      raw = best_raw;
+      m_ = best_m;
+      v_ = best_v;
+      m_mean = best_m_mean;
+      v_mean = best_v_mean;
+      adam_t = best_t;
+      raw_mean = best_raw_mean;
+      for (int q = 0; q < P; ++q) params[q] = softplus(raw[q]);
+      last_rebuild = params;
+      const float rn = o.learn_noise ? softplus(raw[P]) : 0.0f;
+      pv.params = params;
+      pv.refresh_coords();
+      pv.noise = rn;
+      last_rebuild_noise = rn;
+      rebuild();
+      res.precond_rebuild_steps.push_back(it);
+      if (o.verbose) std::printf("  NaN NLL detected at iteration %d - halving LR to %g\n", it, lr);
+      emit("nan", actual, nll, best_nll_seen, r.cg_iterations, secs_since(t_iter) * 1e3, rn,
+           raw_mean, false);
+      continue;
+    }
+
+    if (nll < best_nll_seen) {
+      best_nll_seen = nll;
+      best_raw = raw;
+      best_raw_mean = raw_mean;
+      best_m = m_;
+      best_v = v_;
+      best_m_mean = m_mean;
+      best_v_mean = v_mean;
+      best_t = adam_t;
+      best_alpha.resize(n);
+      MGP_HIP_CHECK(hipMemcpyAsync(best_alpha.data(), r.alpha_dev, n * sizeof(float),
+                                   hipMemcpyDeviceToHost, st));
+      MGP_HIP_CHECK(hipStreamSynchronize(st));
+    }
+
+    const float lr_eff = o.use_cosine_lr ? cosine_lr(o.learning_rate, it, o.max_iterations) : lr;
+    std::vector<float> grads(P + 1);
+    for (int q = 0; q < P; ++q) grads[q] = r.grads[q];
+    grads[P] = o.learn_noise ? r.grads[P] : 0.0f;
+
+    // Adam (training_utils.mojo:214-316): moments on raw parameters through the
+    // softplus chain rule, bias correction, raw clamp to [-20, 20].
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    for (int q = 0; q <= P; ++q) {
+      const float gr = clip_gradient(grads[q]) * softplus_derivative(raw[q]);
+      m_[q] = b1 * m_[q] + (1.0f - b1) * gr;
+      v_[q] = b2 * v_[q] + (1.0f - b2) * gr * gr;
+    }
+    adam_t += 1;
+    const float bc1 = 1.0f - pow_float32(b1, adam_t), bc2 = 1.0f - pow_float32(b2, adam_t);
+    for (int q = 0; q <= P; ++q) {
+      const float mh = m_[q] / bc1, vh = v_[q] / bc2;
+      float nr = raw[q] - lr_eff * mh / (std::sqrt(vh) + eps);
+      raw[q] = std::max(-20.0f, std::min(20.0f, nr));
+    }
+    // Constant mean: gradient -sum(alpha)/n, its own Adam moments.
+    {
+      DevBuf<float> ones;
+      ones.ensure(n);
+      fill(ones.ptr, n, 1.0f, st);
+      const float s = dot_f(ones.ptr, r.alpha_dev, n, work.part, st);
+      float mg = clip_gradient(-s / (float)n);
+      m_mean = b1 * m_mean + (1.0f - b1) * mg;
+      v_mean = b2 * v_mean + (1.0f - b2) * mg * mg;
+      const float mh = m_mean / (1.0f - pow_float32(b1, adam_t));
+      const float vh = v_mean / (1.0f - pow_float32(b2, adam_t));
+      raw_mean -= lr_eff * mh / (std::sqrt(vh) + eps);
+    }
+    if (raw_mean != raw_mean || raw_mean > 1000.0f || raw_mean < -1000.0f) raw_mean = o.init_mean;
+    if (o.verbose && (it % 10 == 0 || it == o.max_iterations - 1))
+      std::printf("Iter %d : NLL = %g , noise = %g , mean = %g\n", it, nll, noise, raw_mean);
+
+    const double ms = secs_since(t_iter) * 1e3;
+    res.iter_times_ms.push_back(ms);
+    res.nll_history.push_back(nll);
+    {
+      const int cur = it + 1;
+      const int iv = std::max(1, o.progress_interval);
+      const bool due = cur <= 1 || cur >= o.max_iterations || cur % iv == 0;
+      if (due) emit("iteration", actual, nll, best_nll_seen, r.cg_iterations, ms, noise, raw_mean, false);
+    }
+    if (o.enable_early_stopping) {
+      if (nll < best_nll - o.early_stop_tol) {
+        best_nll = nll;
+        no_improve = 0;
+      } else if (++no_improve >= o.early_stop_patience) {
+        res.converged = true;
+        emit("early_stop", actual, nll, best_nll_seen, r.cg_iterations, ms, noise, raw_mean, true);
+        break;
+      }
+    }
+  }
+
+  raw = best_raw;
+  raw_mean = best_raw_mean;
+  res.params.resize(P);
+  for (int q = 0; q < P; ++q) res.params[q] = softplus(raw[q]);
+  res.noise = o.learn_noise ? softplus(raw[P]) : 0.0f;
+  res.mean = raw_mean;
+  res.final_nll = best_nll_seen;
+  res.iterations = actual;
+  res.alpha = std::move(best_alpha);
+  emit("complete", actual, best_nll_seen, best_nll_seen, -1, -1.0, res.noise, res.mean,
+       res.converged);
+  return res;
+}
+
+// ------------------------------------------------------------------ prediction
+int solve_alpha(Provider& pv, const float* y_host, float mean, int max_iter, float tol,
+                PredictState& ps) {
+  const int64_t n = pv.n;
+  hipStream_t st = pv.st;
+  const int nb = reduction_chunks(n);
+  DevBuf<float> r, p, Ap, s;
+  DevBuf<double> part;
+  DevBuf<int> done;
+  float* x = ps.alpha.ensure(n);
+  r.ensure(n);
+  p.ensure(n);
+  Ap.ensure(n);
+  s.ensure(4);
+  part.ensure((size_t)2 * nb);
+  done.ensure(1);
+  MGP_HIP_CHECK(hipMemcpyAsync(r.ptr, y_host, n * sizeof(float), hipMemcpyHostToDevice, st));
+  sub_scalar(r.ptr, r.ptr, mean, n, st);
+  fill(x, n, 0.0f, st);
+  copy(p.ptr, r.ptr, n, st);
+  coldot_partial(r.ptr, r.ptr, n, 1, nb, part.ptr, st);
+  hipLaunchKernelGGL(k_a1_init, dim3(1), dim3(64), 0, st, part.ptr, nb, s.ptr, done.ptr);
+  int it = 0;
+  for (; it < max_iter; ++it) {
+    pv.forward(p.ptr, 1, Ap.ptr);
+    coldot_partial(p.ptr, Ap.ptr, n, 1, nb, part.ptr, st);
+    hipLaunchKernelGGL(k_a1_alpha, dim3(1), dim3(64), 0, st, part.ptr, nb, s.ptr, done.ptr);
+    hipLaunchKernelGGL(k_a1_update, dim3(nb), dim3(256), 0, st, x, r.ptr, p.ptr, Ap.ptr, n, nb,
+                       s.ptr, done.ptr, part.ptr + nb);
+    hipLaunchKernelGGL(k_a1_beta, dim3(1), dim3(64), 0, st, part.ptr + nb, nb, tol, s.ptr,
+                       done.ptr);
+    hipLaunchKernelGGL(k_a1_pupdate, g1(n), dim3(256), 0, st, p.ptr, r.ptr, n, s.ptr, done.ptr);
+    MGP_HIP_CHECK(hipGetLastError());
+    if ((it & 3) == 3 || it == max_iter - 1) {
+      int dh = 0;
+      MGP_HIP_CHECK(hipMemcpyAsync(&dh, done.ptr, sizeof(int), hipMemcpyDeviceToHost, st));
+      MGP_HIP_CHECK(hipStreamSynchronize(st));
+      if (dh) break;
+    }
+  }
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  ps.has_alpha = true;
+  return it;
+}
+
+void lanczos_inv_root(Provider& pv, int r, PredictState& ps) {
+  const int64_t n = pv.n;
+  hipStream_t st = pv.st;
+  MGP_REQUIRE(r >= 1 && r <= 1000, "Lanczos rank must be in [1, 1000]");
+  const int nb = reduction_chunks(n);
+  DevBuf<float> Q, w;
+  DevBuf<double> part, coef;
+  Q.ensure((size_t)r * n);
+  w.ensure(n);
+  part.ensure((size_t)(r + 1) * nb + 8);
+  coef.ensure((size_t)r + 1);
+  fill(Q.ptr, (int64_t)r * n, 0.0f, st);
+  // Deterministic +-1 start vector (jit_prediction.mojo:999-1015).
+  std::vector<float> z(n);
+  float zsq = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t s = 0xC0FFEE1234567890ull ^ ((uint64_t)i * 0x9E3779B97F4A7C15ull) ^
+                 ((uint64_t)r * 0xBF58476D1CE4E5B9ull);
+    s ^= s >> 12;
+    s ^= s << 25;
+    s ^= s >> 27;
+    s *= 0x2545F4914F6CDD1Dull;
+    z[i] = (s & 0x20000ull) ? 1.0f : -1.0f;
+    zsq += z[i] * z[i];
+  }
+  const float zn = std::sqrt(zsq);
+  for (int64_t i = 0; i < n; ++i) z[i] /= zn;
+  MGP_HIP_CHECK(hipMemcpyAsync(Q.ptr, z.data(), n * sizeof(float), hipMemcpyHostToDevice, st));
+
+  std::vector<double> alpha(r, 0.0), beta(std::max(r - 1, 0), 0.0);
+  std::vector<double> inner(r + 1);
+  float beta_prev = 0.0f;
+  for (int j = 0; j < r; ++j) {
+    const float* v = Q.ptr + (size_t)j * n;
+    pv.forward(v, 1, w.ptr);
+    const float aj = dot_f(v, w.ptr, n, part, st);
+    alpha[j] = aj;
+    hipLaunchKernelGGL(k_three_term, g1(n), dim3(256), 0, st, w.ptr, v,
+                       j > 0 ? Q.ptr + (size_t)(j - 1) * n : nullptr, aj, beta_prev, n);
+    // Full re-orthogonalisation against Q_0..Q_j, at most two passes; the
+    // second pass runs only if the first saw an inner product >= 1e-5.
+    for (int pass = 0; pass < 2; ++pass) {
+      multi_dot(Q.ptr, j + 1, w.ptr, n, part.ptr, nb, coef.ptr, st);
+      MGP_HIP_CHECK(hipMemcpyAsync(inner.data(), coef.ptr, (j + 1) * sizeof(double),
+                                   hipMemcpyDeviceToHost, st));
+      MGP_HIP_CHECK(hipStreamSynchronize(st));
+      double mx = 0.0;
+      for (int k = 0; k <= j; ++k) mx = std::max(mx, std::fabs(inner[k]));
+      multi_axpy(Q.ptr, j + 1, coef.ptr, w.ptr, n, st);
+      if (mx < 1e-5) break;
+    }
+    const float bj = std::sqrt(dot_f(w.ptr, w.ptr, n, part, st));
+    if (j < r - 1) beta[j] = bj;
+    if (bj < 1e-10f) break;  // remaining Q columns stay zero
+    if (j + 1 < r)
+      hipLaunchKernelGGL(k_scale_into, g1(n), dim3(256), 0, st, Q.ptr + (size_t)(j + 1) * n,
+                         w.ptr, bj, n);
+    beta_prev = bj;
+  }
+  std::vector<double> ev, V;
+  if (!tridiag_eigh(alpha, beta, ev, &V))
+    throw Error(ST_NUMERIC, "Lanczos tridiagonal eigendecomposition did not converge");
+  double max_eig = 1e-10;
+  for (double e : ev) max_eig = std::max(max_eig, e);
+  const double clamp = max_eig * 1e-6;
+  std::vector<float> Tinv((size_t)r * r);
+  for (int i = 0; i < r; ++i)
+    for (int c = 0; c < r; ++c) {
+      double s = 0.0;
+      for (int k = 0; k < r; ++k)
+        s += V[(size_t)i * r + k] * V[(size_t)c * r + k] / std::sqrt(std::max(ev[k], clamp));
+      Tinv[(size_t)i * r + c] = (float)s;
+    }
+  DevBuf<float> Td;
+  Td.ensure(Tinv.size());
+  MGP_HIP_CHECK(hipMemcpyAsync(Td.ptr, Tinv.data(), Tinv.size() * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+  ps.root.ensure((size_t)r * n);
+  gemm_nr_rr(Q.ptr, Td.ptr, n, r, ps.root.ptr, st);
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  ps.rank = r;
+}
+
+void predict_from_state(Provider& pv, const PredictState& ps, const float* Xs_host, int64_t m,
+                        float mean, int variance_method, float* mean_out, float* var_out,
+                        PredictTimes& t) {
+  hipStream_t st = pv.st;
+  MGP_REQUIRE(ps.has_alpha, "prediction state has no alpha");
+  float* dx = pv.Xs.ensure((size_t)m * pv.d);
+  MGP_HIP_CHECK(hipMemcpyAsync(dx, Xs_host, (size_t)m * pv.d * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+  pv.pack(dx, m, pv.test);
+  auto t0 = Clock::now();
+  float* dm = pv.io_c.ensure((size_t)m);
+  pv.cross(pv.test, ps.alpha.ptr, 1, dm);
+  hipLaunchKernelGGL(k_add_scalar, g1(m), dim3(256), 0, st, dm, mean, m);
+  MGP_HIP_CHECK(hipMemcpyAsync(mean_out, dm, m * sizeof(float), hipMemcpyDeviceToHost, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  t.mean_s = secs_since(t0);
+  if (variance_method == 1) {
+    MGP_REQUIRE(ps.rank > 0, "LOVE variance needs an inverse root");
+    auto t1 = Clock::now();
+    DevBuf<float> Vs, var;
+    Vs.ensure((size_t)ps.rank * m);
+    var.ensure(m);
+    pv.cross(pv.test, ps.root.ptr, ps.rank, Vs.ptr);
+    love_variance(Vs.ptr, m, ps.rank, pv.outputscale(), var.ptr, st);
+    MGP_HIP_CHECK(hipMemcpyAsync(var_out, var.ptr, m * sizeof(float), hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    t.variance_s = secs_since(t1);
+  } else if (variance_method == 2) {
+    throw Error(ST_INVALID, "exact predictive variance is not implemented on this route yet");
+  }
+}
+
+}  // namespace mgp

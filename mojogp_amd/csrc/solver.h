@@ -1,0 +1,109 @@
+// Device building blocks of the solvers: batched CG vector kernels, probe RNG,
+// pivoted-Cholesky steps, Woodbury apply, gradient traces, Lanczos helpers.
+// All reductions are deterministic (fixed partition, fixed order, fp64).
+#pragma once
+
+#include "provider.h"
+
+namespace mgp {
+
+// Number of row chunks per column used by the two-stage reductions.
+int reduction_chunks(int64_t n);
+
+// part[c*nb + b] = sum_{i in chunk b} a[c*n+i] * b[c*n+i]   (fp64)
+void coldot_partial(const float* a, const float* b, int64_t n, int ncols, int nb,
+                    double* part, hipStream_t st);
+// out[c] = sum_b part[c*nb + b] (fixed order); optionally sqrt.
+void coldot_finalize(const double* part, int nb, int ncols, double* out, hipStream_t st);
+
+// ---------------------------------------------------------------- batched CG
+// Per-column scalars live in one device block (CGScalars).
+struct CGScalars {
+  float* rz_old;   // [C]
+  float* alpha;    // [C]
+  float* beta;     // [C]
+  float* hist_alpha;  // [max_tridiag][C]
+  float* hist_beta;   // [max_tridiag][C]
+  int* done;       // [1] device stop flag (single-rhs solves)
+};
+
+// alpha = safe(rz_old / pAp)   (reference: cg_solver.mojo:181-209)
+void cg_alpha(const double* pap_part, int nb, int ncols, CGScalars s, hipStream_t st);
+// x += alpha p, r -= alpha Ap with the reference skip rules
+// (cg_solver.mojo:138-179); writes rr partials (r.r) for every column.
+void cg_update(float* x, float* r, const float* p, const float* Ap, int64_t n,
+               int ncols, int nb, CGScalars s, double* rr_part, hipStream_t st);
+// beta = safe(rz_new / rz_old), rz_old = rz_new (cg_solver.mojo:211-255);
+// stores alpha/beta into the history slot `iter` when iter < max_tridiag.
+void cg_beta(const double* rz_part, int nb, int ncols, CGScalars s, int iter,
+             int max_tridiag, hipStream_t st);
+// p = z + beta p (cg_solver.mojo:108-136)
+void cg_pupdate(float* p, const float* z, int64_t n, int ncols, CGScalars s,
+                hipStream_t st);
+// mean_c sqrt(rr_c) into *out (cg_solver.mojo:446-543)
+void cg_mean_resnorm(const double* rr_part, int nb, int ncols, float* out,
+                     hipStream_t st);
+
+// ---------------------------------------------------------------- vectors
+void fill(float* x, int64_t count, float v, hipStream_t st);
+void copy(float* dst, const float* src, int64_t count, hipStream_t st);
+// y = a - b
+void sub(float* y, const float* a, const float* b, int64_t count, hipStream_t st);
+// y[i] = x[i] - s
+void sub_scalar(float* y, const float* x, float s, int64_t count, hipStream_t st);
+// columns c: x[c*n+i] *= scale[c] (or /= when divide)
+void scale_columns(float* x, const float* scale, int64_t n, int ncols, bool divide,
+                   hipStream_t st);
+// norms[c] = ||x_c||; x_c /= norms[c]   (pivoted_cholesky.mojo:1818-1907)
+void normalize_columns(float* x, int64_t n, int ncols, float* norms, double* part,
+                       hipStream_t st);
+
+// Counter-hash Gaussian draws: out[i] for i < len with the reference's integer
+// hash and Box-Muller transform (pivoted_cholesky.mojo:51-86).
+void gaussian(float* out, int64_t len, uint64_t seed, hipStream_t st);
+
+// ---------------------------------------------------------------- precond
+struct PivotState;  // device-side pivot bookkeeping
+
+// Greedy pivoted Cholesky of K (pivoted_cholesky.mojo:2104-2444, method 0).
+// L is [rank][n] column-major.  Returns the realized rank.
+int pivoted_cholesky_greedy(Provider& pv, int rank, float* L, hipStream_t st);
+
+// M = L^T L (k x k, fp64) for the first k columns.
+void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st);
+
+// out = (v - L u)/noise with u = Minv (L^T v) for ncols columns (Woodbury,
+// pivoted_cholesky.mojo:1646-1771).  Optionally writes dot partials of
+// dotv . out (for r.z).  out may alias v.
+struct WoodburyWork {
+  DevBuf<float> wpart;   // [nbw][k][C]
+  DevBuf<float> u;       // [C][k]
+};
+void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,
+                    const float* v, int ncols, float* out, WoodburyWork& w,
+                    const float* dotv, int nb, double* dot_part, hipStream_t st);
+// out[c*n + i] = sum_kk L[kk*n+i] * zr[c*k + kk] + s * zn[c*n + i]
+void low_rank_sample(const float* L, int64_t n, int k, const float* zr,
+                     const float* zn, float s, int ncols, float* out, hipStream_t st);
+
+// ---------------------------------------------------------------- gradients
+// g[p] = sum_{a,b} dK_p[a,b] * sum_c Lf[c*n+a] Rf[c*n+b]  for every kernel
+// parameter p (engine layout), fp64 result on the host.
+void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int ncols,
+                     double* g_host, hipStream_t st);
+
+// ---------------------------------------------------------------- Lanczos
+// out[j] = Q_j . w for j < nvec (Q [nvec][n]), fp64 via partials.
+void multi_dot(const float* Q, int nvec, const float* w, int64_t n, double* part,
+               int nb, double* out, hipStream_t st);
+// w -= sum_j coef[j] Q_j
+void multi_axpy(const float* Q, int nvec, const double* coef, float* w, int64_t n,
+                hipStream_t st);
+// S[c*n + i] = sum_k Q[k*n + i] * T[k*r + c]  (n x r times r x r)
+void gemm_nr_rr(const float* Q, const float* T, int64_t n, int r, float* S,
+                hipStream_t st);
+// var[j] = max(diag - sum_k V[k*m + j]^2, 1e-10)  (jit_prediction.mojo:211-233)
+void love_variance(const float* V, int64_t m, int r, float diag, float* var,
+                   hipStream_t st);
+
+}  // namespace mgp

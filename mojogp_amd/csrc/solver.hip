@@ -1,0 +1,922 @@
+// Solver device kernels (see solver.h).  Reference behaviour is cited per
+// kernel; reductions use a fixed chunk partition and fp64 partial sums so every
+// result is bit-reproducible run to run.
+#include "solver.h"
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+namespace mgp {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ double block_sum_d(double v, double* sm) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) sm[w] = v;
+  __syncthreads();
+  double t = 0.0;
+  if (threadIdx.x == 0)
+    for (int k = 0; k < (int)(blockDim.x >> 6); ++k) t += sm[k];
+  return t;  // valid in thread 0
+}
+
+__device__ __forceinline__ bool is_nan(float x) { return x != x; }
+
+inline dim3 grid1(int64_t count) {
+  return dim3((unsigned)std::max<int64_t>(1, ceil_div(count, kBlock)));
+}
+
+// ------------------------------------------------------------- reductions
+__global__ void k_coldot_part(const float* __restrict__ a, const float* __restrict__ b,
+                              int64_t n, int nb, double* __restrict__ part) {
+  __shared__ double sm[4];
+  const int c = blockIdx.y;
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk;
+  const int64_t i1 = min(n, i0 + chunk);
+  const float* ac = a + (int64_t)c * n;
+  const float* bc = b + (int64_t)c * n;
+  double acc = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x)
+    acc += (double)ac[i] * (double)bc[i];
+  const double t = block_sum_d(acc, sm);
+  if (threadIdx.x == 0) part[(int64_t)c * nb + blockIdx.x] = t;
+}
+
+__global__ void k_coldot_final(const double* __restrict__ part, int nb, int ncols,
+                               double* __restrict__ out) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ncols) return;
+  double s = 0.0;
+  for (int b = 0; b < nb; ++b) s += part[(int64_t)c * nb + b];
+  out[c] = s;
+}
+
+__device__ __forceinline__ float part_sum_f(const double* part, int c, int nb) {
+  double s = 0.0;
+  for (int b = 0; b < nb; ++b) s += part[(int64_t)c * nb + b];
+  return (float)s;
+}
+
+// ------------------------------------------------------------- CG scalars
+__global__ void k_cg_alpha(const double* __restrict__ pap_part, int nb, int ncols,
+                           CGScalars s) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ncols) return;
+  const float pap = part_sum_f(pap_part, c, nb);
+  const float rz = s.rz_old[c];
+  float a;
+  if (is_nan(rz) || is_nan(pap) || pap < 1e-10f) a = 0.0f;
+  else a = rz / pap;
+  s.alpha[c] = a;
+}
+
+__global__ void k_cg_update(float* __restrict__ x, float* __restrict__ r,
+                            const float* __restrict__ p, const float* __restrict__ Ap,
+                            int64_t n, int nb, CGScalars s, double* __restrict__ rr_part) {
+  __shared__ double sm[4];
+  const int c = blockIdx.y;
+  const float a = s.alpha[c];
+  const bool active = !(a == 0.0f || is_nan(a));
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk;
+  const int64_t i1 = min(n, i0 + chunk);
+  const int64_t off = (int64_t)c * n;
+  double acc = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    float ri = r[off + i];
+    if (active) {
+      const float pi = p[off + i], api = Ap[off + i];
+      if (!is_nan(pi) && !is_nan(api)) {
+        x[off + i] += a * pi;
+        ri -= a * api;
+        r[off + i] = ri;
+      }
+    }
+    acc += (double)ri * (double)ri;
+  }
+  const double t = block_sum_d(acc, sm);
+  if (threadIdx.x == 0) rr_part[(int64_t)c * nb + blockIdx.x] = t;
+}
+
+__global__ void k_cg_beta(const double* __restrict__ rz_part, int nb, int ncols,
+                          CGScalars s, int iter, int max_tridiag) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ncols) return;
+  const float rz_new = part_sum_f(rz_part, c, nb);
+  const float rz_old = s.rz_old[c];
+  float beta = 0.0f;
+  if (!is_nan(rz_old) && !is_nan(rz_new) && rz_old >= 1e-20f) {
+    beta = rz_new / (rz_old + 1e-20f);
+    if (beta < 0.0f || is_nan(beta)) beta = 0.0f;
+  }
+  s.beta[c] = beta;
+  s.rz_old[c] = is_nan(rz_new) ? 0.0f : rz_new;
+  if (iter < max_tridiag) {
+    s.hist_alpha[(int64_t)iter * ncols + c] = s.alpha[c];
+    s.hist_beta[(int64_t)iter * ncols + c] = beta;
+  }
+}
+
+__global__ void k_cg_pupdate(float* __restrict__ p, const float* __restrict__ z,
+                             int64_t n, int ncols, CGScalars s) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * ncols) return;
+  const int c = (int)(idx / n);
+  const float b = s.beta[c];
+  if (b == 0.0f || is_nan(b)) {
+    p[idx] = z[idx];
+  } else {
+    const float po = p[idx];
+    p[idx] = is_nan(po) ? z[idx] : z[idx] + b * po;
+  }
+}
+
+__global__ void k_mean_resnorm(const double* __restrict__ rr_part, int nb, int ncols,
+                               float* __restrict__ out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  float sum = 0.0f;
+  for (int c = 0; c < ncols; ++c) sum += sqrtf(part_sum_f(rr_part, c, nb));
+  out[0] = ncols > 0 ? sum / (float)ncols : 0.0f;
+}
+
+// ------------------------------------------------------------- vectors
+__global__ void k_fill(float* x, int64_t count, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) x[i] = v;
+}
+__global__ void k_copy(float* __restrict__ d, const float* __restrict__ s, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) d[i] = s[i];
+}
+__global__ void k_sub(float* y, const float* a, const float* b, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) y[i] = a[i] - b[i];
+}
+__global__ void k_sub_scalar(float* y, const float* x, float s, int64_t count) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count) y[i] = x[i] - s;
+}
+__global__ void k_scale_columns(float* x, const float* __restrict__ scale, int64_t n,
+                                int ncols, int divide) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * ncols) return;
+  const float s = scale[idx / n];
+  x[idx] = divide ? x[idx] / s : x[idx] * s;
+}
+__global__ void k_norms_final(const double* __restrict__ part, int nb, int ncols,
+                              float* __restrict__ norms) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < ncols) norms[c] = sqrtf(part_sum_f(part, c, nb));
+}
+
+// ------------------------------------------------------------- RNG
+__global__ void k_gaussian(float* __restrict__ out, int64_t len, uint64_t seed) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= len) return;
+  const uint64_t k = (uint64_t)idx + 1ull;
+  uint64_t s1 = k * 6364136223846793005ull + seed;
+  s1 ^= s1 >> 33;
+  s1 *= 0xff51afd7ed558ccdull;
+  s1 ^= s1 >> 33;
+  uint64_t s2 = k * 1442695040888963407ull + seed + 0xBEEFull;
+  s2 ^= s2 >> 33;
+  s2 *= 0xc4ceb9fe1a85ec53ull;
+  s2 ^= s2 >> 33;
+  const float u1 = ((float)(int64_t)(s1 & 0x7FFFFFull) + 1.0f) / 8388608.0f;
+  const float u2 = (float)(int64_t)(s2 & 0xFFFFFFull) / 16777216.0f;
+  out[idx] = sqrtf(-2.0f * logf(u1)) * cosf(2.0f * 3.14159265f * u2);
+}
+
+// ------------------------------------------------------------- pivoted Cholesky
+// Argmax of the residual diagonal over unmasked rows with the reference's
+// lowest-index tie rule (pivoted_cholesky.mojo:500-610), plus sum |diag|.
+struct ArgmaxAcc {
+  float val;
+  int64_t idx;
+};
+__device__ __forceinline__ ArgmaxAcc amax_merge(ArgmaxAcc a, ArgmaxAcc b) {
+  if (b.val > a.val || (b.val == a.val && b.idx >= 0 && (a.idx < 0 || b.idx < a.idx)))
+    return b;
+  return a;
+}
+
+__device__ void block_argmax_write(ArgmaxAcc loc, double abss, float* pv, int64_t* pi,
+                                   double* pa, int slot) {
+  __shared__ float sv[kBlock];
+  __shared__ int64_t si[kBlock];
+  __shared__ double sm[4];
+  const double tabs = block_sum_d(abss, sm);
+  sv[threadIdx.x] = loc.val;
+  si[threadIdx.x] = loc.idx;
+  __syncthreads();
+  for (int st = kBlock / 2; st > 0; st >>= 1) {
+    if ((int)threadIdx.x < st) {
+      ArgmaxAcc a{sv[threadIdx.x], si[threadIdx.x]};
+      ArgmaxAcc b{sv[threadIdx.x + st], si[threadIdx.x + st]};
+      ArgmaxAcc m = amax_merge(a, b);
+      sv[threadIdx.x] = m.val;
+      si[threadIdx.x] = m.idx;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    pv[slot] = sv[0];
+    pi[slot] = si[0];
+    pa[slot] = tabs;
+  }
+}
+
+__global__ void k_pc_init(float* __restrict__ diag, float* __restrict__ mask, int64_t n,
+                          float os) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    diag[i] = os;
+    mask[i] = 1.0f;
+  }
+}
+
+__global__ void k_pc_argmax_part(const float* __restrict__ diag,
+                                 const float* __restrict__ mask, int64_t n, int nb,
+                                 float* pv, int64_t* pi, double* pa) {
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  ArgmaxAcc loc{-1e30f, -1};
+  double abss = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    if (mask[i] > 0.5f) {
+      const float d = diag[i];
+      loc = amax_merge(loc, ArgmaxAcc{d, i});
+      abss += (double)fabsf(d);
+    }
+  }
+  block_argmax_write(loc, abss, pv, pi, pa, blockIdx.x);
+}
+
+struct PivotDev {
+  int stopped;
+  int rank;
+  int64_t pivot;
+  float maxval;
+  float sumabs;
+};
+
+__global__ void k_pc_select(const float* __restrict__ pv, const int64_t* __restrict__ pi,
+                            const double* __restrict__ pa, int nb, int m,
+                            PivotDev* __restrict__ state, float* __restrict__ mask,
+                            const float* __restrict__ L, int64_t n,
+                            float* __restrict__ coef) {
+  __shared__ int64_t piv_s;
+  __shared__ int stop_s;
+  if (threadIdx.x == 0) {
+    stop_s = state->stopped;
+    if (!stop_s) {
+      ArgmaxAcc best{pv[0], pi[0]};
+      double tot = pa[0];
+      for (int b = 1; b < nb; ++b) {
+        best = amax_merge(best, ArgmaxAcc{pv[b], pi[b]});
+        tot += pa[b];
+      }
+      if (best.val < 1e-10f || best.idx < 0) {
+        state->stopped = 1;
+        state->rank = m > 0 ? m : 1;
+        stop_s = 1;
+      } else {
+        state->pivot = best.idx;
+        state->maxval = best.val;
+        state->sumabs = (float)tot;
+        mask[best.idx] = 0.0f;
+        piv_s = best.idx;
+      }
+    }
+  }
+  __syncthreads();
+  if (stop_s) return;
+  const int64_t p = piv_s;
+  for (int j = threadIdx.x; j < m; j += blockDim.x) coef[j] = L[(int64_t)j * n + p];
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void k_pc_column(
+    const float* __restrict__ Z, int d, int64_t n, float os, int m,
+    float* __restrict__ L, float* __restrict__ diag, const float* __restrict__ mask,
+    const float* __restrict__ coef, const PivotDev* __restrict__ state, int nb,
+    float* pv, int64_t* pi, double* pa) {
+  extern __shared__ float sh[];  // coef[m] then zp[d]
+  if (state->stopped) return;    // uniform across the grid
+  const int64_t p = state->pivot;
+  const float scale = 1.0f / sqrtf(fmaxf(state->maxval, 1e-10f));
+  float* scoef = sh;
+  float* zp = sh + m;
+  for (int j = threadIdx.x; j < m; j += blockDim.x) scoef[j] = coef[j];
+  for (int k = threadIdx.x; k < d; k += blockDim.x) zp[k] = Z[p * d + k];
+  __syncthreads();
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  ArgmaxAcc loc{-1e30f, -1};
+  double abss = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    float r2 = 0.0f;
+    for (int k = 0; k < d; ++k) {
+      const float df = Z[i * d + k] - zp[k];
+      r2 = fmaf(df, df, r2);
+    }
+    float kv;
+    if constexpr (KIND == KIND_RBF) {
+      kv = os * __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
+    } else {
+      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+      const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+      kv = os * fmaf(u, fmaf(u, kLn2 * kLn2 / 3.0f, kLn2), 1.0f) * e;
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < m; ++j) sum += scoef[j] * L[(int64_t)j * n + i];
+    const float v = (kv - sum) * scale;
+    L[(int64_t)m * n + i] = v;
+    if (mask[i] > 0.5f) {
+      const float dn = diag[i] - v * v;
+      diag[i] = dn;
+      loc = amax_merge(loc, ArgmaxAcc{dn, i});
+      abss += (double)fabsf(dn);
+    }
+  }
+  block_argmax_write(loc, abss, pv, pi, pa, blockIdx.x);
+}
+
+// M[a][b] partial over a row split; grid (tiles, tiles, splits), 16x16 threads.
+__global__ void k_syrk_part(const float* __restrict__ L, int64_t n, int k, int splits,
+                            double* __restrict__ part) {
+  __shared__ float ta[16][65];
+  __shared__ float tb[16][65];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int a0 = blockIdx.x * 16, b0 = blockIdx.y * 16;
+  const int64_t chunk = (n + splits - 1) / splits;
+  const int64_t i0 = (int64_t)blockIdx.z * chunk, i1 = min(n, i0 + chunk);
+  double acc = 0.0;
+  for (int64_t s = i0; s < i1; s += 64) {
+    for (int t = threadIdx.x; t < 16 * 64; t += 256) {
+      const int col = t / 64, row = t % 64;
+      const int64_t i = s + row;
+      const bool ok = i < i1;
+      ta[col][row] = (ok && a0 + col < k) ? L[(int64_t)(a0 + col) * n + i] : 0.0f;
+      tb[col][row] = (ok && b0 + col < k) ? L[(int64_t)(b0 + col) * n + i] : 0.0f;
+    }
+    __syncthreads();
+    float f = 0.0f;
+#pragma unroll 8
+    for (int row = 0; row < 64; ++row) f = fmaf(ta[ty][row], tb[tx][row], f);
+    acc += (double)f;
+    __syncthreads();
+  }
+  const int a = a0 + ty, b = b0 + tx;
+  if (a < k && b < k) part[((int64_t)blockIdx.z * k + a) * k + b] = acc;
+}
+
+__global__ void k_syrk_final(const double* __restrict__ part, int k, int splits,
+                             double* __restrict__ M) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)k * k) return;
+  double s = 0.0;
+  for (int z = 0; z < splits; ++z) s += part[(int64_t)z * k * k + idx];
+  M[idx] = s;
+}
+
+// w-part[b][kk][c] = sum_{i in chunk b} L[kk][i] v[c][i]; block = 16 kk x 16 c.
+__global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
+                          const float* __restrict__ v, int ncols, int c0, int nb,
+                          float* __restrict__ wpart) {
+  __shared__ float tl[16][65];
+  __shared__ float tv[16][65];
+  const int tc = threadIdx.x & 15, tk = threadIdx.x >> 4;
+  const int kk0 = blockIdx.y * 16;
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  float acc = 0.0f;
+  for (int64_t s = i0; s < i1; s += 64) {
+    for (int t = threadIdx.x; t < 16 * 64; t += 256) {
+      const int q = t / 64, row = t % 64;
+      const int64_t i = s + row;
+      const bool ok = i < i1;
+      tl[q][row] = (ok && kk0 + q < k) ? L[(int64_t)(kk0 + q) * n + i] : 0.0f;
+      tv[q][row] = (ok && c0 + q < ncols) ? v[(int64_t)(c0 + q) * n + i] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int row = 0; row < 64; ++row) acc = fmaf(tl[tk][row], tv[tc][row], acc);
+    __syncthreads();
+  }
+  const int kk = kk0 + tk, c = c0 + tc;
+  if (kk < k && c < ncols) wpart[((int64_t)blockIdx.x * k + kk) * ncols + c] = acc;
+}
+
+// u[c*k + kk] = sum_q Minv[kk*k + q] * w[q][c],  w = sum over chunks.
+__global__ void k_small_solve(const float* __restrict__ wpart, int nb, int k, int ncols,
+                              const float* __restrict__ Minv, float* __restrict__ u) {
+  extern __shared__ float ws[];  // [k]
+  const int c = blockIdx.x;
+  for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
+    double s = 0.0;
+    for (int b = 0; b < nb; ++b) s += (double)wpart[((int64_t)b * k + kk) * ncols + c];
+    ws[kk] = (float)s;
+  }
+  __syncthreads();
+  for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
+    float s = 0.0f;
+    for (int q = 0; q < k; ++q) s = fmaf(Minv[(int64_t)kk * k + q], ws[q], s);
+    u[(int64_t)c * k + kk] = s;
+  }
+}
+
+// out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * inv_noise for 16 columns
+// starting at c0; optional dot partials of dotv.out per column.
+__global__ __launch_bounds__(256) void k_woodbury_final(
+    const float* __restrict__ L, int64_t n, int k, const float* __restrict__ u,
+    int ncols, int c0, float inv_noise, const float* v, float* out,
+    const float* __restrict__ dotv, int nb, double* __restrict__ dot_part) {
+  extern __shared__ float us[];  // [16][k]
+  __shared__ double sm[4];
+  const int cn = min(16, ncols - c0);
+  for (int t = threadIdx.x; t < 16 * k; t += blockDim.x) {
+    const int c = t / k, kk = t - c * k;
+    us[t] = c < cn ? u[(int64_t)(c0 + c) * k + kk] : 0.0f;
+  }
+  __syncthreads();
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  double dacc[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) dacc[c] = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    float z[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) z[c] = 0.0f;
+    for (int kk = 0; kk < k; ++kk) {
+      const float l = L[(int64_t)kk * n + i];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) z[c] = fmaf(l, us[c * k + kk], z[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      if (c < cn) {
+        const int64_t off = (int64_t)(c0 + c) * n + i;
+        const float o = inv_noise * (v[off] - z[c]);
+        out[off] = o;
+        if (dot_part) dacc[c] += (double)dotv[off] * (double)o;
+      }
+    }
+  }
+  if (dot_part) {
+    for (int c = 0; c < cn; ++c) {
+      const double t = block_sum_d(dacc[c], sm);
+      if (threadIdx.x == 0) dot_part[(int64_t)(c0 + c) * nb + blockIdx.x] = t;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_low_rank_sample(
+    const float* __restrict__ L, int64_t n, int k, const float* __restrict__ zr,
+    const float* __restrict__ zn, float s, int ncols, int c0, float* __restrict__ out) {
+  extern __shared__ float zs[];  // [16][k]
+  const int cn = min(16, ncols - c0);
+  for (int t = threadIdx.x; t < 16 * k; t += blockDim.x) {
+    const int c = t / k, kk = t - c * k;
+    zs[t] = c < cn ? zr[(int64_t)(c0 + c) * k + kk] : 0.0f;
+  }
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float z[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) z[c] = 0.0f;
+  for (int kk = 0; kk < k; ++kk) {
+    const float l = L[(int64_t)kk * n + i];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) z[c] = fmaf(l, zs[c * k + kk], z[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    if (c < cn) {
+      const int64_t off = (int64_t)(c0 + c) * n + i;
+      out[off] = z[c] + s * zn[off];
+    }
+  }
+}
+
+// ------------------------------------------------------------- gradients
+// Block: 256 rows a; LDS tiles of 64 column points b.  Per pair the reference
+// derivatives (see oracle/kernels.py for the closed forms) are weighted by
+// g_ab = sum_c Lf[c][a] Rf[c][b] and accumulated; fp32 within a tile, fp64
+// across tiles.  part[block][p] (p: per-dim lengthscale terms, then os term).
+constexpr int kGradTile = 64;
+
+template <int KIND, int DM, bool ARD>
+__global__ __launch_bounds__(256) void k_grad_trace(
+    const float* __restrict__ Z, int d, int64_t n, const float* __restrict__ Lf,
+    const float* __restrict__ Rf, int ncols, int c0, double* __restrict__ part,
+    int nterms) {
+  __shared__ float zb[kGradTile][DM + 1];
+  __shared__ float rb[kGradTile][17];
+  __shared__ double sm[4];
+  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = a < n;
+  const int cn = min(16, ncols - c0);
+  float za[DM];
+#pragma unroll
+  for (int k = 0; k < DM; ++k) za[k] = (live && k < d) ? Z[a * d + k] : 0.0f;
+  float la[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) la[c] = (live && c < cn) ? Lf[(int64_t)(c0 + c) * n + a] : 0.0f;
+  constexpr int NT = ARD ? DM : 1;
+  double accd[NT + 1];
+#pragma unroll
+  for (int t = 0; t <= NT; ++t) accd[t] = 0.0;
+  for (int64_t b0 = 0; b0 < n; b0 += kGradTile) {
+    __syncthreads();
+    for (int t = threadIdx.x; t < kGradTile * DM; t += blockDim.x) {
+      const int bb = t / DM, k = t - bb * DM;
+      const int64_t b = b0 + bb;
+      zb[bb][k] = (b < n && k < d) ? Z[b * d + k] : 0.0f;
+    }
+    for (int t = threadIdx.x; t < kGradTile * 16; t += blockDim.x) {
+      const int bb = t / 16, c = t - bb * 16;
+      const int64_t b = b0 + bb;
+      rb[bb][c] = (b < n && c < cn) ? Rf[(int64_t)(c0 + c) * n + b] : 0.0f;
+    }
+    __syncthreads();
+    float acc[NT + 1];
+#pragma unroll
+    for (int t = 0; t <= NT; ++t) acc[t] = 0.0f;
+    const int cnt = (int)min((int64_t)kGradTile, n - b0);
+    for (int bb = 0; bb < cnt; ++bb) {
+      float dz2[DM];
+      float r2 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < DM; ++k) {
+        const float df = za[k] - zb[bb][k];
+        dz2[k] = df * df;
+        r2 += dz2[k];
+      }
+      float kv, h;
+      if constexpr (KIND == KIND_RBF) {
+        kv = __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
+        h = kv;
+      } else {
+        const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+        const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+        kv = fmaf(u, fmaf(u, kLn2 * kLn2 / 3.0f, kLn2), 1.0f) * e;
+        h = (5.0f / 3.0f) * fmaf(u, kLn2, 1.0f) * e;
+      }
+      float g = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 16; ++c) g = fmaf(la[c], rb[bb][c], g);
+      const float hg = h * g;
+      acc[NT] = fmaf(kv, g, acc[NT]);
+      if constexpr (ARD) {
+#pragma unroll
+        for (int k = 0; k < DM; ++k) acc[k] = fmaf(hg, dz2[k], acc[k]);
+      } else {
+        acc[0] = fmaf(hg, r2, acc[0]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t <= NT; ++t) accd[t] += (double)acc[t];
+  }
+  // Block reduction of each term.
+  for (int t = 0; t < nterms; ++t) {
+    const int src = (t == nterms - 1) ? NT : t;
+    double v = 0.0;
+#pragma unroll
+    for (int q = 0; q <= NT; ++q)
+      if (q == src) v = accd[q];
+    const double tot = block_sum_d(live ? v : 0.0, sm);
+    if (threadIdx.x == 0) part[(int64_t)blockIdx.x * nterms + t] = tot;
+  }
+}
+
+template <int KIND, bool ARD>
+void launch_grad(int dm, const float* Z, int d, int64_t n, const float* Lf,
+                 const float* Rf, int ncols, int c0, double* part, int nterms,
+                 hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(n, 256));
+  switch (dm) {
+#define MGP_GRAD_CASE(DMV)                                                           \
+  case DMV:                                                                         \
+    hipLaunchKernelGGL((k_grad_trace<KIND, DMV, ARD>), grid, dim3(256), 0, st, Z, d, \
+                       n, Lf, Rf, ncols, c0, part, nterms);                         \
+    break;
+    MGP_GRAD_CASE(1)
+    MGP_GRAD_CASE(2)
+    MGP_GRAD_CASE(4)
+    MGP_GRAD_CASE(8)
+    MGP_GRAD_CASE(16)
+    MGP_GRAD_CASE(32)
+#undef MGP_GRAD_CASE
+    default:
+      throw Error(ST_INVALID, "unsupported gradient dimension bucket");
+  }
+}
+
+// ------------------------------------------------------------- Lanczos
+__global__ void k_multi_dot_part(const float* __restrict__ Q, const float* __restrict__ w,
+                                 int64_t n, int nb, double* __restrict__ part) {
+  __shared__ double sm[4];
+  const int j = blockIdx.y;
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  const float* q = Q + (int64_t)j * n;
+  double acc = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x)
+    acc += (double)q[i] * (double)w[i];
+  const double t = block_sum_d(acc, sm);
+  if (threadIdx.x == 0) part[(int64_t)j * nb + blockIdx.x] = t;
+}
+
+__global__ void k_multi_axpy(const float* __restrict__ Q, int nvec,
+                             const double* __restrict__ coef, float* __restrict__ w,
+                             int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  double s = 0.0;
+  for (int j = 0; j < nvec; ++j) s += coef[j] * (double)Q[(int64_t)j * n + i];
+  w[i] = (float)((double)w[i] - s);
+}
+
+__global__ void k_gemm_nr_rr(const float* __restrict__ Q, const float* __restrict__ T,
+                             int64_t n, int r, int c0, float* __restrict__ S) {
+  extern __shared__ float ts[];  // [r][16]
+  const int cn = min(16, r - c0);
+  for (int t = threadIdx.x; t < r * 16; t += blockDim.x) {
+    const int k = t / 16, c = t - k * 16;
+    ts[t] = c < cn ? T[(int64_t)k * r + c0 + c] : 0.0f;
+  }
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float acc[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) acc[c] = 0.0f;
+  for (int k = 0; k < r; ++k) {
+    const float q = Q[(int64_t)k * n + i];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) acc[c] = fmaf(q, ts[k * 16 + c], acc[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+    if (c < cn) S[(int64_t)(c0 + c) * n + i] = acc[c];
+}
+
+__global__ void k_love_variance(const float* __restrict__ V, int64_t m, int r, float diag,
+                                float* __restrict__ var) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= m) return;
+  float s = 0.0f;
+  for (int k = 0; k < r; ++k) {
+    const float v = V[(int64_t)k * m + j];
+    s = fmaf(v, v, s);
+  }
+  var[j] = fmaxf(diag - s, 1e-10f);
+}
+
+}  // namespace
+
+// ===================================================================== host
+
+int reduction_chunks(int64_t n) {
+  return (int)std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(n, 2048)));
+}
+
+void coldot_partial(const float* a, const float* b, int64_t n, int ncols, int nb,
+                    double* part, hipStream_t st) {
+  hipLaunchKernelGGL(k_coldot_part, dim3(nb, ncols), dim3(kBlock), 0, st, a, b, n, nb, part);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void coldot_finalize(const double* part, int nb, int ncols, double* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_coldot_final, grid1(ncols), dim3(kBlock), 0, st, part, nb, ncols, out);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void cg_alpha(const double* pap_part, int nb, int ncols, CGScalars s, hipStream_t st) {
+  hipLaunchKernelGGL(k_cg_alpha, grid1(ncols), dim3(kBlock), 0, st, pap_part, nb, ncols, s);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void cg_update(float* x, float* r, const float* p, const float* Ap, int64_t n, int ncols,
+               int nb, CGScalars s, double* rr_part, hipStream_t st) {
+  hipLaunchKernelGGL(k_cg_update, dim3(nb, ncols), dim3(kBlock), 0, st, x, r, p, Ap, n, nb,
+                     s, rr_part);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void cg_beta(const double* rz_part, int nb, int ncols, CGScalars s, int iter,
+             int max_tridiag, hipStream_t st) {
+  hipLaunchKernelGGL(k_cg_beta, grid1(ncols), dim3(kBlock), 0, st, rz_part, nb, ncols, s,
+                     iter, max_tridiag);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void cg_pupdate(float* p, const float* z, int64_t n, int ncols, CGScalars s,
+                hipStream_t st) {
+  hipLaunchKernelGGL(k_cg_pupdate, grid1(n * ncols), dim3(kBlock), 0, st, p, z, n, ncols, s);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void cg_mean_resnorm(const double* rr_part, int nb, int ncols, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_mean_resnorm, dim3(1), dim3(64), 0, st, rr_part, nb, ncols, out);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void fill(float* x, int64_t count, float v, hipStream_t st) {
+  if (count <= 0) return;
+  hipLaunchKernelGGL(k_fill, grid1(count), dim3(kBlock), 0, st, x, count, v);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void copy(float* dst, const float* src, int64_t count, hipStream_t st) {
+  if (count <= 0) return;
+  hipLaunchKernelGGL(k_copy, grid1(count), dim3(kBlock), 0, st, dst, src, count);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void sub(float* y, const float* a, const float* b, int64_t count, hipStream_t st) {
+  hipLaunchKernelGGL(k_sub, grid1(count), dim3(kBlock), 0, st, y, a, b, count);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void sub_scalar(float* y, const float* x, float s, int64_t count, hipStream_t st) {
+  hipLaunchKernelGGL(k_sub_scalar, grid1(count), dim3(kBlock), 0, st, y, x, s, count);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void scale_columns(float* x, const float* scale, int64_t n, int ncols, bool divide,
+                   hipStream_t st) {
+  hipLaunchKernelGGL(k_scale_columns, grid1(n * ncols), dim3(kBlock), 0, st, x, scale, n,
+                     ncols, divide ? 1 : 0);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void normalize_columns(float* x, int64_t n, int ncols, float* norms, double* part,
+                       hipStream_t st) {
+  const int nb = reduction_chunks(n);
+  coldot_partial(x, x, n, ncols, nb, part, st);
+  hipLaunchKernelGGL(k_norms_final, grid1(ncols), dim3(kBlock), 0, st, part, nb, ncols, norms);
+  MGP_HIP_CHECK(hipGetLastError());
+  scale_columns(x, norms, n, ncols, true, st);
+}
+
+void gaussian(float* out, int64_t len, uint64_t seed, hipStream_t st) {
+  if (len <= 0) return;
+  hipLaunchKernelGGL(k_gaussian, grid1(len), dim3(kBlock), 0, st, out, len, seed);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+int pivoted_cholesky_greedy(Provider& pv, int rank, float* L, hipStream_t st) {
+  const int64_t n = pv.n;
+  const int nb = reduction_chunks(n);
+  DevBuf<float> diag, mask, coef, pvv;
+  DevBuf<int64_t> piv;
+  DevBuf<double> pa;
+  DevBuf<PivotDev> state;
+  diag.ensure(n);
+  mask.ensure(n);
+  coef.ensure(std::max(rank, 1));
+  pvv.ensure(nb);
+  piv.ensure(nb);
+  pa.ensure(nb);
+  state.ensure(1);
+  PivotDev init{0, rank, 0, 0.f, 0.f};
+  MGP_HIP_CHECK(hipMemcpyAsync(state.ptr, &init, sizeof(init), hipMemcpyHostToDevice, st));
+  fill(L, (int64_t)rank * n, 0.0f, st);
+  hipLaunchKernelGGL(k_pc_init, grid1(n), dim3(kBlock), 0, st, diag.ptr, mask.ptr, n,
+                     pv.outputscale());
+  hipLaunchKernelGGL(k_pc_argmax_part, dim3(nb), dim3(kBlock), 0, st, diag.ptr, mask.ptr,
+                     n, nb, pvv.ptr, piv.ptr, pa.ptr);
+  MGP_HIP_CHECK(hipGetLastError());
+  const float os = pv.outputscale();
+  auto col = pv.kind == KIND_RBF ? k_pc_column<KIND_RBF> : k_pc_column<KIND_MATERN52>;
+  for (int m = 0; m < rank; ++m) {
+    hipLaunchKernelGGL(k_pc_select, dim3(1), dim3(kBlock), 0, st, pvv.ptr, piv.ptr, pa.ptr,
+                       nb, m, state.ptr, mask.ptr, L, n, coef.ptr);
+    const size_t shm = (size_t)(m + pv.d) * sizeof(float);
+    hipLaunchKernelGGL(col, dim3(nb), dim3(kBlock), shm, st, pv.train.z.ptr, pv.d, n, os, m,
+                       L, diag.ptr, mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr,
+                       pa.ptr);
+    MGP_HIP_CHECK(hipGetLastError());
+  }
+  PivotDev fin;
+  MGP_HIP_CHECK(hipMemcpyAsync(&fin, state.ptr, sizeof(fin), hipMemcpyDeviceToHost, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  return fin.stopped ? fin.rank : rank;
+}
+
+void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st) {
+  const int tiles = (int)ceil_div(k, 16);
+  const int splits = (int)std::max<int64_t>(1, std::min<int64_t>(64, ceil_div(n, 4096)));
+  DevBuf<double> part;
+  part.ensure((size_t)splits * k * k);
+  hipLaunchKernelGGL(k_syrk_part, dim3(tiles, tiles, splits), dim3(256), 0, st, L, n, k,
+                     splits, part.ptr);
+  hipLaunchKernelGGL(k_syrk_final, grid1((int64_t)k * k), dim3(kBlock), 0, st, part.ptr, k,
+                     splits, M_dev);
+  MGP_HIP_CHECK(hipGetLastError());
+  MGP_HIP_CHECK(hipStreamSynchronize(st));  // `part` is released on return
+}
+
+void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,
+                    const float* v, int ncols, float* out, WoodburyWork& w,
+                    const float* dotv, int nb, double* dot_part, hipStream_t st) {
+  const int nbw = reduction_chunks(n);
+  float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
+  float* u = w.u.ensure((size_t)ncols * k);
+  for (int c0 = 0; c0 < ncols; c0 += 16) {
+    hipLaunchKernelGGL(k_lt_part, dim3(nbw, (unsigned)ceil_div(k, 16)), dim3(256), 0, st, L,
+                       n, k, v, ncols, c0, nbw, wpart);
+  }
+  hipLaunchKernelGGL(k_small_solve, dim3(ncols), dim3(256), (size_t)k * sizeof(float), st,
+                     wpart, nbw, k, ncols, Minv, u);
+  const float inv_noise = 1.0f / noise;
+  for (int c0 = 0; c0 < ncols; c0 += 16) {
+    hipLaunchKernelGGL(k_woodbury_final, dim3(nb), dim3(256), (size_t)16 * k * sizeof(float),
+                       st, L, n, k, u, ncols, c0, inv_noise, v, out, dotv, nb, dot_part);
+  }
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const float* zn,
+                     float s, int ncols, float* out, hipStream_t st) {
+  for (int c0 = 0; c0 < ncols; c0 += 16) {
+    hipLaunchKernelGGL(k_low_rank_sample, grid1(n), dim3(256), (size_t)16 * k * sizeof(float),
+                       st, L, n, k, zr, zn, s, ncols, c0, out);
+  }
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int ncols,
+                     double* g_host, hipStream_t st) {
+  const int d = pv.d;
+  MGP_REQUIRE(d <= 32, "gradient kernel supports d <= 32");
+  const int dm = d <= 1 ? 1 : d <= 2 ? 2 : d <= 4 ? 4 : d <= 8 ? 8 : d <= 16 ? 16 : 32;
+  const int nterms = pv.ard ? d + 1 : 2;
+  const int64_t nblk = ceil_div(pv.n, 256);
+  DevBuf<double> part;
+  part.ensure((size_t)nblk * nterms);
+  std::vector<double> acc(nterms, 0.0), hpart((size_t)nblk * nterms);
+  for (int c0 = 0; c0 < ncols; c0 += 16) {
+    if (pv.kind == KIND_RBF) {
+      if (pv.ard) launch_grad<KIND_RBF, true>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+      else launch_grad<KIND_RBF, false>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+    } else {
+      if (pv.ard) launch_grad<KIND_MATERN52, true>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+      else launch_grad<KIND_MATERN52, false>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+    }
+    MGP_HIP_CHECK(hipGetLastError());
+    MGP_HIP_CHECK(hipMemcpyAsync(hpart.data(), part.ptr, hpart.size() * sizeof(double),
+                                 hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    for (int64_t b = 0; b < nblk; ++b)
+      for (int t = 0; t < nterms; ++t) acc[t] += hpart[(size_t)b * nterms + t];
+  }
+  // Convert pair sums (scaled coordinates z = (x - c) * kernel_scale / ls) to
+  // parameter derivatives: dk/dl_d = os h (dx_d)^2 / l_d^3 = os h dz_d^2 / (s^2 l_d).
+  const double s = (double)kernel_scale(pv.kind);
+  const double os = (double)pv.outputscale();
+  const int nls = pv.ard ? d : 1;
+  for (int q = 0; q < nls; ++q)
+    g_host[q] = os * acc[q] / (s * s * (double)pv.lengthscale(q));
+  g_host[nls] = acc[nterms - 1];
+}
+
+void multi_dot(const float* Q, int nvec, const float* w, int64_t n, double* part, int nb,
+               double* out, hipStream_t st) {
+  if (nvec <= 0) return;
+  hipLaunchKernelGGL(k_multi_dot_part, dim3(nb, nvec), dim3(kBlock), 0, st, Q, w, n, nb, part);
+  coldot_finalize(part, nb, nvec, out, st);
+}
+
+void multi_axpy(const float* Q, int nvec, const double* coef, float* w, int64_t n,
+                hipStream_t st) {
+  if (nvec <= 0) return;
+  hipLaunchKernelGGL(k_multi_axpy, grid1(n), dim3(kBlock), 0, st, Q, nvec, coef, w, n);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void gemm_nr_rr(const float* Q, const float* T, int64_t n, int r, float* S, hipStream_t st) {
+  for (int c0 = 0; c0 < r; c0 += 16) {
+    hipLaunchKernelGGL(k_gemm_nr_rr, grid1(n), dim3(kBlock), (size_t)r * 16 * sizeof(float),
+                       st, Q, T, n, r, c0, S);
+  }
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void love_variance(const float* V, int64_t m, int r, float diag, float* var, hipStream_t st) {
+  hipLaunchKernelGGL(k_love_variance, grid1(m), dim3(kBlock), 0, st, V, m, r, diag, var);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace mgp

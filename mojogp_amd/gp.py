@@ -1,0 +1,716 @@
+"""SingleOutputGP — the reference's exact-GP surface over the gfx950 engine.
+
+Follows mojogp/gp.py (fit 860-1552, _fit_continuous 1554-1606, _fit_engine
+1608-1883, _predict_engine 1885-2047, predict 2446-2674,
+_predict_continuous 2811-2960): the same argument names and defaults, CG
+presets, route and preconditioner heuristics, initial-lengthscale caps,
+prediction solver budgets and cached-alpha rules.  The hot path runs in
+libmojogp_amd.so through ``mojogp_amd._engine``.
+
+Scope: continuous inputs, RBF / Matern-5/2 kernels (isotropic or ARD), scalar
+learned noise.  Heteroskedastic noise models, categorical/mixed kernels and
+composite kernel trees raise ``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import json
+import warnings
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Any, Optional, Tuple, Union
+
+import numpy as np
+
+from . import _engine
+from .kernel import KernelNode, KernelType, make_ard_kernel
+
+_MODEL_SCHEMA_VERSION = 1
+_DEFAULT_PREDICT_LANCZOS_RANK = 100
+_DEFAULT_ARD_PREDICT_LANCZOS_RANK = 200
+_DEFAULT_EXACT_PREDICT_MAX_CG_ITER = 300
+_DEFAULT_EXACT_PREDICT_CG_TOL = 1e-3
+_DEFAULT_PREDICT_MAX_CG_ITER = _DEFAULT_EXACT_PREDICT_MAX_CG_ITER
+_DEFAULT_PREDICT_CG_TOL = _DEFAULT_EXACT_PREDICT_CG_TOL
+
+_FIT_METHOD_ALIASES = {"mat": "materialized", "mf": "matrix_free"}
+
+
+def normalize_fit_method(method: str, *, allow_auto: bool = False) -> str:
+    """Canonical training route name (mojogp/_routes.py:12-28)."""
+    if not isinstance(method, str):
+        raise ValueError("method must be a string")
+    if method in _FIT_METHOD_ALIASES:
+        return _FIT_METHOD_ALIASES[method]
+    valid = ["materialized", "matrix_free"] + (["auto"] if allow_auto else [])
+    if method in valid:
+        return method
+    aliases = ", ".join(f"'{a}'" for a in sorted(_FIT_METHOD_ALIASES))
+    raise ValueError(f"method must be one of {', '.join(repr(v) for v in valid)}; "
+                     f"accepted aliases: {aliases}")
+
+
+def _prediction_lanczos_rank(rank_hint, training_method, is_ard: bool) -> int:
+    """gp.py:100-125 (single-output, non-mixed)."""
+    rank = int(rank_hint) if rank_hint is not None else 0
+    min_rank = _DEFAULT_PREDICT_LANCZOS_RANK
+    if is_ard:
+        min_rank = max(min_rank, _DEFAULT_ARD_PREDICT_LANCZOS_RANK)
+    return max(rank, min_rank)
+
+
+def _prediction_solver_config(train_info, rank_hint, training_method, *, is_ard,
+                              max_cg_iterations=None, cg_tolerance=None, precond_rank=None,
+                              max_root_decomposition_size=None) -> dict:
+    """gp.py:141-198."""
+    train_info = train_info or {}
+    resolved_precond_rank = int(precond_rank if precond_rank is not None
+                                else train_info.get("precond_rank", 10))
+    predict_rank = _prediction_lanczos_rank(rank_hint, training_method, is_ard)
+    if max_root_decomposition_size is not None:
+        predict_rank = int(max_root_decomposition_size)
+    tmax = int(train_info.get("max_cg_iterations",
+                              train_info.get("max_cg_iter", _DEFAULT_PREDICT_MAX_CG_ITER)))
+    ttol = float(train_info.get("cg_tolerance", train_info.get("cg_tol", _DEFAULT_PREDICT_CG_TOL)))
+    return {
+        "max_cg_iterations": int(max_cg_iterations if max_cg_iterations is not None
+                                 else max(tmax, _DEFAULT_EXACT_PREDICT_MAX_CG_ITER)),
+        "cg_tolerance": float(cg_tolerance if cg_tolerance is not None
+                              else min(ttol, _DEFAULT_EXACT_PREDICT_CG_TOL)),
+        "precond_rank": resolved_precond_rank,
+        "max_root_decomposition_size": predict_rank,
+    }
+
+
+@dataclass
+class TrainingResult:
+    params: np.ndarray
+    noise: float
+    mean: float
+    nll: float
+    iterations: int
+    converged: bool
+    lanczos_root: Optional[np.ndarray]
+    lanczos_rank: int
+    nll_history: Optional[np.ndarray] = None
+    cg_iterations_history: Optional[np.ndarray] = None
+    iter_times_ms: Optional[np.ndarray] = None
+
+
+@dataclass
+class PredictionResult:
+    mean: np.ndarray
+    variance: np.ndarray
+    std: np.ndarray
+
+
+class SingleOutputGP:
+    """Exact Gaussian process regression on one MI355X.
+
+        >>> gp = SingleOutputGP(RBF())
+        >>> gp.fit(X, y, max_iterations=50, method="matrix_free")
+        >>> mean, std = gp.predict(X_test, return_std=True, variance_method="love")
+    """
+
+    _PRECOND_METHOD_MAP = {"greedy": 0, "rpcholesky": 1, "nystrom": 2, "auto": 2}
+    _PRESETS = {
+        "fast": {"max_cg_iter": 50, "cg_tol": 5e-2, "num_probes": 5, "max_tridiag_iter": 15,
+                 "precond_rank": 50, "precond_rebuild_threshold": 0.75, "precond": "greedy"},
+        "balanced": {"max_cg_iter": 100, "cg_tol": 1e-2, "num_probes": 10, "max_tridiag_iter": 30,
+                     "precond_rank": 100, "precond_rebuild_threshold": 0.5, "precond": "greedy"},
+        "accurate": {"max_cg_iter": 200, "cg_tol": 1e-3, "num_probes": 20, "max_tridiag_iter": 60,
+                     "precond_rank": 200, "precond_rebuild_threshold": 0.25, "precond": "greedy"},
+    }
+
+    def __init__(self, kernel: KernelNode, *, init_mean: Optional[float] = None,
+                 verbose: bool = False):
+        if not isinstance(kernel, KernelNode):
+            raise TypeError("kernel must be a KernelNode instance (e.g. RBF(), Matern52()), "
+                            f"got {type(kernel).__name__}")
+        self._original_kernel = kernel
+        self._kernel_pre_ard = kernel
+        self.ard = kernel.has_ard()
+        self.kernel = kernel
+        self.verbose = verbose
+        self._init_mean = init_mean
+        self._X_train: Optional[np.ndarray] = None
+        self._y_train: Optional[np.ndarray] = None
+        self.dim: Optional[int] = None
+        self._is_trained = False
+        self._training_result: Optional[TrainingResult] = None
+        self._training_method: Optional[str] = None
+        self._kernel_module: Optional[_engine.KernelModule] = None
+        self._engine: Optional[_engine.Engine] = None
+        self._provider_info: Optional[dict] = None
+        self._provider_state_current = False
+        self._cached_alpha: Optional[np.ndarray] = None
+        self._cached_alpha_info: Optional[dict] = None
+        self._cached_love_method: Optional[str] = None
+        self._engine_predict_mean: Optional[float] = None
+        self._fitted_mean: Optional[float] = None
+        self._backend_train_info: Optional[dict] = None
+        self._backend_predict_info: Optional[dict] = None
+        self._prediction_cache_handle: Optional[int] = None
+        self._prediction_cache_signature: Optional[tuple] = None
+        self._prediction_cache_info: Optional[dict] = None
+        self._noise_floor = 1e-6
+        self._noise_regularization = 0.0
+
+    # ------------------------------------------------------------ properties
+    @property
+    def num_params(self) -> int:
+        return self.kernel.num_params()
+
+    @property
+    def param_names(self) -> list:
+        return self.kernel.get_param_names()
+
+    @property
+    def is_trained(self) -> bool:
+        return self._is_trained
+
+    @property
+    def training_result(self) -> Optional[TrainingResult]:
+        return self._training_result
+
+    @property
+    def backend_train_info(self) -> Optional[dict]:
+        return self._backend_train_info
+
+    @property
+    def backend_predict_info(self) -> Optional[dict]:
+        return self._backend_predict_info
+
+    def _is_single_kernel_type(self, kt: KernelType) -> bool:
+        return self.kernel.operator is None and self.kernel.kernel_type == kt
+
+    # ------------------------------------------------------------ lifecycle
+    def _ensure_compiled(self) -> None:
+        if self._kernel_module is None or self._engine is None:
+            kind = self.kernel.native_kind()
+            self._kernel_module = _engine.load_kernel_module(kind, self.kernel.ard_dim is not None,
+                                                             self.dim)
+            self._engine = _engine.load_engine()
+
+    def _destroy_prediction_cache(self) -> None:
+        if self._prediction_cache_handle and self._engine is not None:
+            try:
+                self._engine.destroy_prediction_cache(self._prediction_cache_handle)
+            except Exception:
+                pass
+        self._prediction_cache_handle = None
+        self._prediction_cache_signature = None
+        self._prediction_cache_info = None
+
+    def _destroy_provider_info(self) -> None:
+        self._destroy_prediction_cache()
+        if self._provider_info is not None and self._kernel_module is not None:
+            self._kernel_module.destroy_provider(self._provider_info)
+        self._provider_info = None
+        self._provider_state_current = False
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self._destroy_provider_info()
+        except Exception:
+            pass
+
+    def _build_provider_info(self, X, engine_params, noise, method=None) -> dict:
+        self._ensure_compiled()
+        info = self._kernel_module.init_provider(np.ascontiguousarray(X, dtype=np.float32),
+                                                 np.ascontiguousarray(engine_params, np.float32),
+                                                 float(noise))
+        if (method or self._training_method) == "materialized":
+            self._kernel_module.materialize(info)
+        return info
+
+    # ------------------------------------------------------------ CG params
+    @staticmethod
+    def _resolve_cg_params(preset=None, max_cg_iter=None, cg_tol=None, num_probes=None,
+                           max_tridiag_iter=None, precond_rank=None,
+                           precond_rebuild_threshold=None, precond=None) -> dict:
+        """gp.py:821-858."""
+        base = dict(SingleOutputGP._PRESETS[preset or "balanced"])
+        for key, val in (("max_cg_iter", max_cg_iter), ("cg_tol", cg_tol),
+                         ("num_probes", num_probes), ("max_tridiag_iter", max_tridiag_iter),
+                         ("precond_rank", precond_rank),
+                         ("precond_rebuild_threshold", precond_rebuild_threshold),
+                         ("precond", precond)):
+            if val is not None:
+                base[key] = val
+        base.setdefault("precond", "auto")
+        base["precond_method"] = SingleOutputGP._PRECOND_METHOD_MAP.get(base["precond"], 2)
+        return base
+
+    # ------------------------------------------------------------ fit
+    def fit(self, X, y, max_iterations: int = 100, learning_rate: float = 0.01,
+            initial_noise: float = 0.1, initial_params=None, method: str = "auto",
+            enable_early_stopping: bool = False, early_stop_patience: int = 10,
+            early_stop_tol: float = 1e-4, verbose: Optional[bool] = None,
+            preset: Optional[str] = None, max_cg_iterations: Optional[int] = None,
+            cg_tolerance: Optional[float] = None, num_probes: Optional[int] = None,
+            max_tridiag_iterations: Optional[int] = None,
+            preconditioner_rank: Optional[int] = None,
+            precond_rebuild_threshold: Optional[float] = None,
+            use_fused_kernels: bool = True, preconditioner: Optional[str] = None,
+            use_preconditioner: Optional[bool] = None, lr_schedule: str = "constant",
+            prepare_prediction_cache: bool = False,
+            prediction_cache_rank: Optional[int] = None, observation_noise=None,
+            observation_noise_fn=None, noise_function=None, learn_noise: bool = True,
+            noise_floor: float = 1e-6, noise_regularization: float = 0.01,
+            noise_model: str = "scalar", noise_group_train=None, group_noise=None,
+            progress: Any = None, progress_stats: Any = None,
+            progress_interval: int = 1) -> TrainingResult:
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        if X.ndim != 2:
+            raise ValueError(f"X must be 2D, got shape {X.shape}")
+        if y.ndim != 1:
+            raise ValueError(f"y must be 1D, got shape {y.shape}")
+        if X.shape[0] != y.shape[0]:
+            raise ValueError(f"X has {X.shape[0]} samples, y has {y.shape[0]}")
+        if np.any(~np.isfinite(X)):
+            raise ValueError("X contains NaN or Inf values")
+        if np.any(~np.isfinite(y)):
+            raise ValueError("y contains NaN or Inf values")
+        if noise_floor <= 0 or not np.isfinite(noise_floor):
+            raise ValueError("noise_floor must be finite and > 0")
+        if noise_regularization < 0 or not np.isfinite(noise_regularization):
+            raise ValueError("noise_regularization must be finite and >= 0")
+        if (noise_model != "scalar" or observation_noise is not None
+                or observation_noise_fn is not None or noise_function is not None
+                or noise_group_train is not None or group_noise is not None):
+            raise NotImplementedError("only scalar learned noise is served by the gfx950 engine")
+        if not learn_noise:
+            raise NotImplementedError(
+                "Fixed scalar noise is not implemented in the JIT training API yet; use "
+                "learn_noise=True or provide observation_noise")
+        if preset is not None and preset not in self._PRESETS:
+            raise ValueError(f"Unknown preset '{preset}'. Must be one of: {list(self._PRESETS)}")
+        if max_iterations <= 0:
+            raise ValueError(f"max_iterations must be > 0, got {max_iterations}")
+        if int(progress_interval) <= 0:
+            raise ValueError("progress_interval must be a positive integer")
+        if learning_rate <= 0:
+            raise ValueError(f"learning_rate must be > 0, got {learning_rate}")
+        if initial_noise <= 0:
+            raise ValueError(f"initial_noise must be > 0, got {initial_noise}")
+        if early_stop_patience < 0:
+            raise ValueError(f"early_stop_patience must be >= 0, got {early_stop_patience}")
+        if early_stop_tol < 0:
+            raise ValueError(f"early_stop_tol must be >= 0, got {early_stop_tol}")
+        if prediction_cache_rank is not None and prediction_cache_rank <= 0:
+            raise ValueError("prediction_cache_rank must be positive or None")
+        if not enable_early_stopping and (early_stop_patience != 10 or early_stop_tol != 1e-4):
+            warnings.warn("early_stop_patience and early_stop_tol are set but "
+                          "enable_early_stopping=False, so training will run to "
+                          "max_iterations.", UserWarning, stacklevel=2)
+        if not use_fused_kernels:
+            warnings.warn("use_fused_kernels=False has no effect: the JIT engine always uses "
+                          "fused GPU kernels.", UserWarning, stacklevel=2)
+        if lr_schedule not in ("cosine", "constant"):
+            raise ValueError(f"lr_schedule must be 'cosine' or 'constant', got '{lr_schedule}'")
+        if preconditioner is not None and preconditioner not in self._PRECOND_METHOD_MAP:
+            raise ValueError(f"Unknown preconditioner '{preconditioner}'. Must be one of: "
+                             f"{list(self._PRECOND_METHOD_MAP)}")
+        use_cosine_lr = lr_schedule == "cosine"
+
+        self._destroy_provider_info()
+        self._X_train, self._y_train = X, y
+        self.dim = X.shape[1]
+        self._noise_floor = float(noise_floor)
+        self._noise_regularization = float(noise_regularization)
+        self.kernel = make_ard_kernel(self._kernel_pre_ard, self.dim) if self.ard else self._kernel_pre_ard
+        self.kernel.native_kind()  # rejects kernels outside the engine
+        self._kernel_module = None
+        self._engine = None
+
+        default_initial_params = initial_params is None
+        if default_initial_params:
+            initial_params = self.kernel.get_initial_params()
+        else:
+            initial_params = np.asarray(initial_params, dtype=np.float32)
+            if initial_params.shape[0] != self.num_params:
+                raise ValueError(f"initial_params has {initial_params.shape[0]} values, "
+                                 f"expected {self.num_params}")
+        _verbose = verbose if verbose is not None else self.verbose
+
+        method = normalize_fit_method(method, allow_auto=True)
+        resolved = method
+        if method == "auto" and X.shape[0] <= 2000:
+            resolved = "materialized"
+        elif method == "auto":
+            resolved = "matrix_free"
+        self._training_method = resolved
+        self._ensure_compiled()
+
+        # Initial-lengthscale caps (gp.py:1370-1408).
+        if (default_initial_params and resolved == "materialized" and learning_rate <= 0.05
+                and self._is_single_kernel_type(KernelType.RBF) and self.dim == 1
+                and initial_params.shape[0] >= 1):
+            initial_params = initial_params.copy()
+            initial_params[0] = min(float(initial_params[0]), 0.5)
+        if (default_initial_params and resolved == "matrix_free" and learning_rate <= 0.05
+                and self._is_single_kernel_type(KernelType.RBF) and not self.ard
+                and 1 < self.dim <= 8 and X.shape[0] >= 10000 and initial_params.shape[0] >= 1):
+            initial_params = initial_params.copy()
+            initial_params[0] = min(float(initial_params[0]), 0.6)
+
+        # Preconditioner defaults (gp.py:1410-1467).
+        resolved_precond = preconditioner
+        resolved_precond_rank = preconditioner_rank
+        explicit = (preconditioner is not None or preconditioner_rank is not None
+                    or use_preconditioner is not None)
+        if (resolved_precond is None and resolved == "materialized" and learning_rate <= 0.05
+                and self._is_single_kernel_type(KernelType.MATERN32)):
+            resolved_precond = "greedy"
+        if not explicit and resolved == "materialized" and self._is_single_kernel_type(KernelType.LINEAR):
+            resolved_precond_rank = 0
+        if not explicit and resolved == "matrix_free":
+            if (self._is_single_kernel_type(KernelType.RBF) and not self.ard
+                    and 1 < self.dim <= 8 and X.shape[0] >= 5000):
+                resolved_precond = "greedy"
+                resolved_precond_rank = 256
+            else:
+                resolved_precond_rank = 0
+        resolved_threshold = precond_rebuild_threshold
+        if resolved_threshold is None and resolved == "materialized" and self.ard:
+            resolved_threshold = 0.1
+        cg = self._resolve_cg_params(preset=preset, max_cg_iter=max_cg_iterations,
+                                     cg_tol=cg_tolerance, num_probes=num_probes,
+                                     max_tridiag_iter=max_tridiag_iterations,
+                                     precond_rank=resolved_precond_rank,
+                                     precond_rebuild_threshold=resolved_threshold,
+                                     precond=resolved_precond)
+        init_mean = self._init_mean if self._init_mean is not None else float(np.mean(y))
+        result = self._fit_engine(X, y, initial_params, initial_noise, max_iterations,
+                                  learning_rate, resolved, enable_early_stopping, _verbose, cg,
+                                  use_cosine_lr, init_mean, use_preconditioner,
+                                  early_stop_patience, early_stop_tol, learn_noise,
+                                  progress, progress_interval)
+        if prepare_prediction_cache:
+            self.prepare_prediction_cache(variance_method="love",
+                                          max_root_decomposition_size=prediction_cache_rank)
+        return result
+
+    def _fit_engine(self, X, y, initial_params, initial_noise, max_iterations, learning_rate,
+                    route, enable_early_stopping, verbose, cg, use_cosine_lr, init_mean,
+                    use_preconditioner, early_stop_patience, early_stop_tol, learn_noise,
+                    progress, progress_interval) -> TrainingResult:
+        """gp.py:1608-1883."""
+        engine_params = self.kernel.to_engine_params(np.asarray(initial_params, np.float32))
+        self._destroy_provider_info()
+        self._provider_info = self._build_provider_info(X, engine_params, initial_noise, route)
+        self._provider_state_current = True
+        resolved_use_pc = (bool(use_preconditioner) if use_preconditioner is not None
+                           else int(cg["precond_rank"]) > 0)
+        eff_rank = int(cg["precond_rank"]) if resolved_use_pc else 0
+        args = [self._provider_info, y.astype(np.float32), engine_params, float(initial_noise),
+                max_iterations, float(learning_rate), cg["num_probes"], cg["max_cg_iter"],
+                float(cg["cg_tol"]), eff_rank, verbose, use_cosine_lr, resolved_use_pc,
+                cg["max_tridiag_iter"], float(cg["precond_rebuild_threshold"]),
+                cg["precond_method"], float(init_mean), bool(enable_early_stopping),
+                int(early_stop_patience), float(early_stop_tol), bool(learn_noise),
+                float(self._noise_floor), float(self._noise_regularization)]
+        callback = progress if callable(progress) else None
+        if callback is not None:
+            args.extend([callback, int(progress_interval)])
+        result = self._engine.train(*args)
+        self._is_trained = True
+        self._provider_state_current = False
+        self._invalidate_prediction_caches()
+        learned_mean = float(result.get("mean", init_mean))
+        self._engine_predict_mean = learned_mean
+        self._fitted_mean = learned_mean
+        info = {
+            "training_route": route,
+            "materialization_mode": int(self._provider_info.get("materialization_mode", 0)),
+            "is_ard": bool(self._provider_info.get("is_ard", False)),
+            "precond_method": int(result.get("precond_method", cg["precond_method"])),
+            "precond_rank": int(result.get("precond_rank", cg["precond_rank"])),
+            "max_cg_iter": int(cg["max_cg_iter"]),
+            "max_cg_iterations": int(cg["max_cg_iter"]),
+            "cg_tol": float(cg["cg_tol"]),
+            "cg_tolerance": float(cg["cg_tol"]),
+            "max_tridiag_iter": int(cg["max_tridiag_iter"]),
+            "precond_rebuild_threshold": float(cg["precond_rebuild_threshold"]),
+            "enable_early_stopping": bool(enable_early_stopping),
+            "early_stop_patience": int(early_stop_patience),
+            "early_stop_tol": float(early_stop_tol),
+            "use_preconditioner": bool(resolved_use_pc),
+            "noise_mode": "scalar",
+            "learn_noise": bool(learn_noise),
+            "has_observation_noise_vector": False,
+            "noise_regularization": float(self._noise_regularization),
+        }
+        for key in ("actual_precond_rank", "precond_build_count", "precond_rebuild_count",
+                    "precond_build_total_ms", "precond_rank_history", "precond_rebuild_steps"):
+            if key in result:
+                info[key] = result[key]
+        params = self.kernel.from_engine_params(np.array(result["params"], dtype=np.float32))
+        nll_h = np.array(result.get("nll_history", []), dtype=np.float32)
+        times = np.array(result.get("iter_times_ms", []), dtype=np.float32)
+        cg_h = np.array(result.get("cg_iterations_history", []), dtype=np.int32)
+        self._training_result = TrainingResult(
+            params=params, noise=float(result["noise"]), mean=learned_mean,
+            nll=float(result["final_nll"]), iterations=int(result["iterations"]),
+            converged=bool(result["converged"]), lanczos_root=None,
+            lanczos_rank=int(cg["max_tridiag_iter"]), nll_history=nll_h,
+            cg_iterations_history=cg_h, iter_times_ms=times)
+        if result.get("cached_alpha") is not None:
+            self._store_cached_alpha(result["cached_alpha"],
+                                     {"max_cg_iterations": int(cg["max_cg_iter"]),
+                                      "cg_tolerance": float(cg["cg_tol"]),
+                                      "precond_rank": int(cg["precond_rank"])}, "training")
+        if len(times):
+            info["iter_times_ms"] = times.tolist()
+            info["iter_time_median_ms"] = float(np.median(times))
+            info["iter_time_p5_ms"] = float(np.percentile(times, 5))
+            info["iter_time_p95_ms"] = float(np.percentile(times, 95))
+        if len(cg_h):
+            info["cg_iterations_history"] = cg_h.tolist()
+            info["cg_iterations_total"] = int(cg_h.sum())
+            info["cg_iterations_mean"] = float(cg_h.mean())
+            info["cg_iterations_max"] = int(cg_h.max())
+            info["cg_iterations_final_step"] = int(cg_h[-1])
+            info["cg_iterations_measured"] = True
+        self._backend_train_info = info
+        return self._training_result
+
+    # ------------------------------------------------------------ alpha cache
+    def _invalidate_prediction_caches(self) -> None:
+        self._cached_alpha = None
+        self._cached_alpha_info = None
+        self._cached_love_method = None
+        self._destroy_prediction_cache()
+
+    def _store_cached_alpha(self, alpha, solver_config, source) -> None:
+        self._cached_alpha = np.asarray(alpha, dtype=np.float32)
+        self._cached_alpha_info = {"source": source,
+                                   "max_cg_iterations": int(solver_config["max_cg_iterations"]),
+                                   "cg_tolerance": float(solver_config["cg_tolerance"]),
+                                   "precond_rank": int(solver_config["precond_rank"])}
+
+    def _cached_alpha_for_solver(self, solver_config) -> Optional[np.ndarray]:
+        """gp.py:2103-2122: reuse only an alpha solved at least as tightly."""
+        a = self._cached_alpha
+        if a is None or self._y_train is None or len(a) != len(self._y_train):
+            return None
+        info = self._cached_alpha_info or {}
+        if (int(info.get("max_cg_iterations", 0) or 0) < int(solver_config["max_cg_iterations"])
+                or float(info.get("cg_tolerance", float("inf"))) > float(solver_config["cg_tolerance"])):
+            return None
+        return a
+
+    # ------------------------------------------------------------ predict
+    def _solver_config(self, max_cg_iterations=None, cg_tolerance=None, preconditioner_rank=None,
+                       max_root_decomposition_size=None) -> dict:
+        tr = self._training_result
+        return _prediction_solver_config(
+            self._backend_train_info, getattr(tr, "lanczos_rank", 0), self._training_method,
+            is_ard=self.ard, max_cg_iterations=max_cg_iterations, cg_tolerance=cg_tolerance,
+            precond_rank=preconditioner_rank,
+            max_root_decomposition_size=max_root_decomposition_size)
+
+    def _provider_for_prediction(self, params, noise):
+        """Reuse the training provider (its state is re-uploaded unless current)."""
+        if self._provider_info is None:
+            self._provider_info = self._build_provider_info(self._X_train, params, noise)
+            self._provider_state_current = True
+        return self._provider_info
+
+    def predict(self, X, return_var: bool = False, return_std: bool = False,
+                variance_method: str = "love", method: Optional[str] = None,
+                target: str = "latent", observation_noise=None, observation_noise_fn=None,
+                noise_group_test=None, *, max_cg_iterations: Optional[int] = None,
+                cg_tolerance: Optional[float] = None, preconditioner_rank: Optional[int] = None,
+                max_root_decomposition_size: Optional[int] = None,
+                exact_prediction_block_cols: Optional[int] = None, progress: Any = None,
+                progress_stats: Any = None) -> Union[PredictionResult, Tuple[np.ndarray, np.ndarray]]:
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before prediction. Call fit() first.")
+        if return_var and return_std:
+            raise ValueError("Only one of return_var or return_std may be True.")
+        if variance_method not in ("love", "exact", "mean_only"):
+            raise ValueError("variance_method must be one of ('love', 'exact', 'mean_only'), "
+                             f"got '{variance_method}'")
+        if method not in (None, "materialized", "matrix_free"):
+            raise ValueError("method must be one of None, 'materialized', or 'matrix_free', "
+                             f"got '{method}'")
+        if target not in ("latent", "observed"):
+            raise ValueError("target must be 'latent' or 'observed'")
+        if exact_prediction_block_cols is not None and exact_prediction_block_cols <= 0:
+            raise ValueError("exact_prediction_block_cols must be positive or None")
+        X = np.asarray(X, dtype=np.float32)
+        if X.ndim != 2:
+            raise ValueError(f"X must be 2D, got shape {X.shape}")
+        if X.shape[1] != self.dim:
+            raise ValueError(f"X has {X.shape[1]} features, expected {self.dim}")
+        if np.any(~np.isfinite(X)):
+            raise ValueError("X_test contains NaN or Inf values")
+        if target == "observed" and observation_noise is None:
+            raise ValueError("predict_observed()/predict(target='observed') requires "
+                             "observation_noise for test points")
+
+        tr = self._training_result
+        params = self.kernel.to_engine_params(np.array(tr.params, dtype=np.float32))
+        sc = self._solver_config(max_cg_iterations, cg_tolerance, preconditioner_rank,
+                                 max_root_decomposition_size)
+        vm = {"exact": 2, "love": 1, "mean_only": 0}[variance_method]
+        prediction_method = method or self._training_method or "matrix_free"
+        info = self._provider_for_prediction(params, tr.noise)
+        mean_value = float(self._engine_predict_mean if self._engine_predict_mean is not None
+                           else tr.mean)
+        if self._prediction_cache_valid(prediction_method, variance_method, sc, params,
+                                        float(tr.noise), mean_value):
+            res = self._engine.predict_with_cache(info, int(self._prediction_cache_handle),
+                                                  X.astype(np.float32), params, float(tr.noise),
+                                                  mean_value, vm)
+        else:
+            cached_alpha = self._cached_alpha_for_solver(sc)
+            root = None
+            if variance_method == "love" and tr.lanczos_root is not None \
+                    and self._cached_love_method == prediction_method \
+                    and len(tr.lanczos_root) == len(self._y_train) * int(sc["max_root_decomposition_size"]):
+                root = np.ascontiguousarray(tr.lanczos_root, dtype=np.float32)
+            args = [info, self._y_train.astype(np.float32), X.astype(np.float32), params,
+                    float(tr.noise), mean_value, vm, int(sc["max_cg_iterations"]),
+                    float(sc["cg_tolerance"]), int(sc["precond_rank"]),
+                    int(sc["max_root_decomposition_size"]), bool(self._provider_state_current),
+                    int(exact_prediction_block_cols or 0)]
+            if cached_alpha is not None:
+                args.append(np.ascontiguousarray(cached_alpha, dtype=np.float32))
+                if root is not None:
+                    args.append(root)
+            res = self._engine.predict(*args)
+            if res.get("cached_alpha") is not None:
+                self._store_cached_alpha(res["cached_alpha"], sc, "prediction")
+            if res.get("cached_lanczos_root") is not None:
+                tr.lanczos_root = np.asarray(res["cached_lanczos_root"], dtype=np.float32)
+                self._cached_love_method = prediction_method
+        self._provider_state_current = True
+        mean = np.asarray(res["mean"], dtype=np.float32)
+        variance = np.asarray(res.get("variance", np.zeros(len(X))), dtype=np.float32)
+        self._backend_predict_info = {
+            "prediction_method": prediction_method,
+            "variance_method": variance_method,
+            "precond_rank": int(sc["precond_rank"]),
+            "max_cg_iterations": int(sc["max_cg_iterations"]),
+            "cg_tolerance": float(sc["cg_tolerance"]),
+            "max_root_decomposition_size": int(sc["max_root_decomposition_size"]),
+            "prediction_total_time_s": float(res.get("total_time_s", 0.0)),
+            "prediction_alpha_time_s": float(res.get("alpha_time_s", 0.0)),
+            "prediction_mean_time_s": float(res.get("mean_time_s", 0.0)),
+            "prediction_variance_time_s": float(res.get("variance_time_s", 0.0)),
+            "prediction_love_root_time_s": float(res.get("love_root_time_s", 0.0)),
+            "alpha_cache_used": bool(res.get("alpha_cache_used", False)),
+            "love_root_cache_used": bool(res.get("love_root_cache_used", False)),
+        }
+        if target == "observed":
+            obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
+            if obs.shape != (X.shape[0],):
+                raise ValueError(f"observation_noise must have shape ({X.shape[0]},), got {obs.shape}")
+            variance = variance + obs
+        std = np.sqrt(np.maximum(variance, 0))
+        if return_var:
+            return mean, variance
+        if return_std:
+            return mean, std
+        return PredictionResult(mean=mean, variance=variance, std=std)
+
+    def predict_observed(self, X, observation_noise=None, **kwargs):
+        kwargs.pop("target", None)
+        return self.predict(X, target="observed", observation_noise=observation_noise, **kwargs)
+
+    # ------------------------------------------------------------ cache
+    def _cache_signature(self, prediction_method, variance_method, sc, params, noise, mean):
+        return (prediction_method, variance_method, len(self._y_train), int(self.dim or 0),
+                int(sc["max_cg_iterations"]), float(sc["cg_tolerance"]), int(sc["precond_rank"]),
+                int(sc["max_root_decomposition_size"]),
+                tuple(np.asarray(params, np.float32).ravel().tolist()), float(noise), "scalar",
+                None, float(mean))
+
+    def _prediction_cache_valid(self, prediction_method, variance_method, sc, params, noise,
+                                mean) -> bool:
+        if not self._prediction_cache_handle:
+            return False
+        want = self._cache_signature(prediction_method, variance_method, sc, params, noise, mean)
+        return self._prediction_cache_signature == want
+
+    def prepare_prediction_cache(self, variance_method: str = "love", method: Optional[str] = None,
+                                 *, max_cg_iterations: Optional[int] = None,
+                                 cg_tolerance: Optional[float] = None,
+                                 preconditioner_rank: Optional[int] = None,
+                                 max_root_decomposition_size: Optional[int] = None) -> dict:
+        """Device-resident alpha (+ LOVE root) for repeated predictions (gp.py:2134-2279)."""
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before preparing a prediction cache.")
+        if variance_method not in ("love", "mean_only"):
+            raise ValueError("prediction cache supports variance_method 'love' or 'mean_only'")
+        tr = self._training_result
+        params = self.kernel.to_engine_params(np.array(tr.params, dtype=np.float32))
+        sc = self._solver_config(max_cg_iterations, cg_tolerance, preconditioner_rank,
+                                 max_root_decomposition_size)
+        vm = 1 if variance_method == "love" else 0
+        prediction_method = method or self._training_method or "matrix_free"
+        info = self._provider_for_prediction(params, tr.noise)
+        mean_value = float(self._engine_predict_mean if self._engine_predict_mean is not None
+                           else tr.mean)
+        self._destroy_prediction_cache()
+        args = [info, self._y_train.astype(np.float32), params, float(tr.noise), mean_value, vm,
+                int(sc["max_cg_iterations"]), float(sc["cg_tolerance"]), int(sc["precond_rank"]),
+                int(sc["max_root_decomposition_size"]), bool(self._provider_state_current)]
+        cached_alpha = self._cached_alpha_for_solver(sc)
+        if cached_alpha is not None:
+            args.append(cached_alpha)
+        res = self._engine.prepare_prediction_cache(*args)
+        self._provider_state_current = True
+        self._prediction_cache_handle = int(res["cache_handle"])
+        self._prediction_cache_signature = self._cache_signature(
+            prediction_method, variance_method, sc, params, float(tr.noise), mean_value)
+        self._prediction_cache_info = {"prediction_cache_handle": self._prediction_cache_handle,
+                                       "prediction_cache_rank": int(res["lanczos_rank"]) if vm else 0,
+                                       "prediction_cache_has_love_root": bool(vm)}
+        return dict(self._prediction_cache_info)
+
+    # ------------------------------------------------------------ persistence
+    def save(self, path) -> None:
+        """``<path>_config.json`` (schema v1) + ``<path>_arrays.npz`` (gp.py:3648-3733)."""
+        if not self._is_trained:
+            raise RuntimeError("Cannot save an untrained model")
+        path = str(path)
+        tr = self._training_result
+        cfg = {"schema_version": _MODEL_SCHEMA_VERSION,
+               "kernel": self._original_kernel.to_dict(),
+               "training_route": self._training_method,
+               "noise": float(tr.noise), "mean": float(tr.mean), "nll": float(tr.nll),
+               "iterations": int(tr.iterations), "converged": bool(tr.converged),
+               "dim": int(self.dim), "backend_train_info": self._backend_train_info or {}}
+        Path(path + "_config.json").write_text(json.dumps(cfg, indent=2, default=float))
+        np.savez(path + "_arrays.npz", X_train=self._X_train, y_train=self._y_train,
+                 params=np.asarray(tr.params, np.float32))
+
+    @classmethod
+    def load(cls, path) -> "SingleOutputGP":
+        path = str(path)
+        cfg = json.loads(Path(path + "_config.json").read_text())
+        if int(cfg.get("schema_version", 0)) != _MODEL_SCHEMA_VERSION:
+            raise ValueError("unsupported model schema version")
+        arr = np.load(path + "_arrays.npz", allow_pickle=False)
+        gp = cls(KernelNode.from_dict(cfg["kernel"]))
+        gp._X_train = np.ascontiguousarray(arr["X_train"], np.float32)
+        gp._y_train = np.ascontiguousarray(arr["y_train"], np.float32)
+        gp.dim = int(cfg["dim"])
+        gp.kernel = make_ard_kernel(gp._kernel_pre_ard, gp.dim) if gp.ard else gp._kernel_pre_ard
+        gp._training_method = cfg.get("training_route", "matrix_free")
+        gp._backend_train_info = cfg.get("backend_train_info") or {}
+        gp._training_result = TrainingResult(
+            params=np.asarray(arr["params"], np.float32), noise=float(cfg["noise"]),
+            mean=float(cfg["mean"]), nll=float(cfg["nll"]), iterations=int(cfg["iterations"]),
+            converged=bool(cfg["converged"]), lanczos_root=None,
+            lanczos_rank=int(gp._backend_train_info.get("max_tridiag_iter", 30)))
+        gp._engine_predict_mean = float(cfg["mean"])
+        gp._fitted_mean = float(cfg["mean"])
+        gp._is_trained = True
+        gp._ensure_compiled()
+        return gp
