@@ -1,0 +1,450 @@
+"""CPU restatement of the reference's exact-GP engine — TEST INFRASTRUCTURE ONLY.
+
+Restates, in NumPy float64 on dense matrices (small n), the algorithm of
+caspbian/mojogp's engine so the gfx950 product can be checked against it:
+
+  gaussian              kernels/pivoted_cholesky.mojo:51-86 (counter hash +
+                        Box-Muller, bit-identical integer part, float32 math)
+  pivoted_cholesky      kernels/pivoted_cholesky.mojo:2104-2444 (greedy,
+                        lowest-index ties, early stop at max diag < 1e-10)
+  Precond               pivoted_cholesky.mojo:1083-1208 (core inverse with
+                        max(noise,1e-6)), 1411-1518 (log|P| via Sylvester),
+                        1646-1771 (Woodbury), 1909-2011 (N(0,P) probes)
+  batched_cg            kernels/combined_inv_quad_logdet.mojo:81-449 and the
+                        safe alpha/beta rules of kernels/cg_solver.mojo:108-255
+  slq_logdet            kernels/native_numerics.mojo:403-536
+  bbmm_step             kernels/combined_inv_quad_logdet.mojo:452-1140
+  train                 kernels/jit/jit_training.mojo:274-1008 with
+                        kernels/training_utils.mojo:23-320, kernels/utils.mojo:14-90
+  solve_alpha           kernels/jit/jit_prediction.mojo:681-765
+  lanczos_inv_root      kernels/jit/jit_prediction.mojo:974-1177
+  love_variance         kernels/jit/jit_prediction.mojo:211-233
+
+What pins each piece (tests/test_oracle_engine.py): the RNG by moments and a
+Kolmogorov-Smirnov test; pivoted Cholesky by exact reconstruction of low-rank
+matrices and a monotone trace error; Woodbury and log|P| by dense inverse and
+slogdet; CG by np.linalg.solve; SLQ by closed forms (scaled identity) and by
+convergence to slogdet with many probes; BBMM gradients by convergence to the
+exact gradient (dense trace) with many probes; alpha by np.linalg.solve;
+LOVE by the exact posterior variance at full rank.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import kernels as ok
+
+F32 = np.float32
+
+
+# ---------------------------------------------------------------- RNG
+def gaussian(length: int, seed: int) -> np.ndarray:
+    """Counter-hash uniform pair + Box-Muller, float32 (pivoted_cholesky.mojo:51-86)."""
+    k = np.arange(1, length + 1, dtype=np.uint64)
+    seed = np.uint64(seed % (1 << 64))
+    with np.errstate(over="ignore"):
+        s1 = k * np.uint64(6364136223846793005) + seed
+        s1 ^= s1 >> np.uint64(33)
+        s1 *= np.uint64(0xFF51AFD7ED558CCD)
+        s1 ^= s1 >> np.uint64(33)
+        s2 = k * np.uint64(1442695040888963407) + seed + np.uint64(0xBEEF)
+        s2 ^= s2 >> np.uint64(33)
+        s2 *= np.uint64(0xC4CEB9FE1A85EC53)
+        s2 ^= s2 >> np.uint64(33)
+    u1 = ((s1 & np.uint64(0x7FFFFF)).astype(F32) + F32(1.0)) / F32(8388608.0)
+    u2 = (s2 & np.uint64(0xFFFFFF)).astype(F32) / F32(16777216.0)
+    return (np.sqrt(F32(-2.0) * np.log(u1)) * np.cos(F32(2.0) * F32(3.14159265) * u2)).astype(F32)
+
+
+# ---------------------------------------------------------------- precond
+def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32):
+    """Greedy pivoted Cholesky of the kernel matrix K (no noise). Returns (L [n,k], k).
+
+    Runs at the reference's working precision (fp32 by default): the residual
+    diagonal of far-away points rounds to exactly the outputscale, so many
+    entries tie and the lowest index wins; a float64 run breaks those ties
+    differently and picks other pivots."""
+    n = K.shape[0]
+    Kd = np.asarray(K).astype(dtype)
+    diag = np.diag(Kd).copy()
+    mask = np.ones(n, dtype=bool)
+    L = np.zeros((n, rank), dtype=dtype)
+    actual = rank
+    for m in range(rank):
+        cand = np.where(mask, diag, dtype(-np.inf))
+        p = int(np.argmax(cand))           # first maximum = lowest index on ties
+        maxval = cand[p]
+        if not mask.any() or maxval < 1e-10:
+            actual = max(m, 1)
+            break
+        mask[p] = False
+        col = Kd[:, p] - L[:, :m] @ L[p, :m]
+        L[:, m] = col * (dtype(1.0) / np.sqrt(max(maxval, dtype(1e-10))))
+        diag[mask] -= L[mask, m] * L[mask, m]
+    return L[:, :actual].astype(np.float64), actual
+
+
+class Precond:
+    """P = L L^T + noise I with the reference's cached pieces."""
+
+    def __init__(self, L: np.ndarray, noise: float):
+        self.L = L
+        self.noise = float(noise)
+        self.rank = L.shape[1]
+        M = L.T @ L
+        eff = max(self.noise, 1e-6)
+        self.Minv = np.linalg.inv(M + eff * np.eye(self.rank))
+        _, ld = np.linalg.slogdet(np.eye(self.rank) + M / self.noise)
+        self.logdet = L.shape[0] * np.log(self.noise) + ld
+
+    def apply(self, V: np.ndarray) -> np.ndarray:
+        """(V - L Minv L^T V) / noise for V [n, C]."""
+        return (V - self.L @ (self.Minv @ (self.L.T @ V))) / self.noise
+
+    def sample(self, T: int, seed: int) -> np.ndarray:
+        """N(0, P) probes [n, T]: L z_rank + sqrt(noise) z_noise."""
+        n = self.L.shape[0]
+        zr = gaussian(self.rank * T, seed).astype(np.float64).reshape(T, self.rank)
+        zn = gaussian(n * T, seed + 1000000).astype(np.float64).reshape(T, n)
+        return (zr @ self.L.T + np.sqrt(np.float32(self.noise)) * zn).T
+
+
+# ---------------------------------------------------------------- CG
+def _recip(a):
+    return 1.0 if a < 1e-10 else 1.0 / a
+
+
+def batched_cg(A: np.ndarray, rhs: np.ndarray, P: Precond | None, max_iter: int,
+               max_tridiag: int, tol: float, x0: np.ndarray | None = None):
+    """Preconditioned mBCG on columns of rhs [n, C]; returns (x, iters, converged, diags, offs)."""
+    n, C = rhs.shape
+    x = np.zeros_like(rhs) if x0 is None else x0.copy()
+    r = rhs - A @ x if x0 is not None else rhs.copy()
+    z = P.apply(r) if P is not None else r
+    p = z.copy()
+    rz_old = np.sum(r * z, axis=0)
+    ha, hb = [], []
+    iters, converged = 0, False
+    for it in range(max_iter):
+        iters = it + 1
+        Ap = A @ p
+        pAp = np.sum(p * Ap, axis=0)
+        bad = np.isnan(rz_old) | np.isnan(pAp) | (pAp < 1e-10)
+        alpha = np.where(bad, 0.0, rz_old / np.where(bad, 1.0, pAp))
+        active = (alpha != 0.0) & ~np.isnan(alpha)
+        x[:, active] += alpha[active] * p[:, active]
+        r[:, active] -= alpha[active] * Ap[:, active]
+        z = P.apply(r) if P is not None else r
+        rz_new = np.sum(r * z, axis=0)
+        ok_b = ~np.isnan(rz_old) & ~np.isnan(rz_new) & (rz_old >= 1e-20)
+        beta = np.where(ok_b, rz_new / (rz_old + 1e-20), 0.0)
+        beta = np.where((beta < 0) | np.isnan(beta), 0.0, beta)
+        rz_old = np.where(np.isnan(rz_new), 0.0, rz_new)
+        p = np.where(beta == 0.0, z, z + beta * p)
+        if it < max_tridiag:
+            ha.append(alpha.copy())
+            hb.append(beta.copy())
+        if it >= 10 and ((it + 1) % 10 == 0 or it == max_iter - 1):
+            mean_res = np.mean(np.sqrt(np.sum(r * r, axis=0)))
+            if mean_res < tol and it >= max_tridiag - 1:
+                converged = True
+                break
+    diags = [[] for _ in range(C)]
+    offs = [[] for _ in range(C)]
+    for k in range(len(ha)):
+        max_off = 0.0
+        for c in range(C):
+            dv = _recip(ha[k][c])
+            if k > 0:
+                apr = _recip(ha[k - 1][c])
+                dv += hb[k - 1][c] * apr
+                off = np.sqrt(max(hb[k - 1][c], 0.0)) * apr
+                offs[c].append(off)
+                max_off = max(max_off, off)
+            diags[c].append(dv)
+        if k > 0 and max_off < 1e-6:
+            break
+    return x, iters, converged, diags, offs
+
+
+def slq_logdet(diags, offs, n: int) -> float:
+    """n * mean over probes of sum_i V0i^2 log(lambda_i) (native_numerics.mojo:403-536)."""
+    from scipy.linalg import eigh_tridiagonal
+    total, valid = 0.0, 0
+    for d, e in zip(diags, offs):
+        d = np.asarray(d, np.float64)
+        e = np.asarray(e, np.float64)
+        if d.size == 0 or np.any(np.isnan(d)) or np.any(np.isnan(e)):
+            continue
+        if d.size == 1:
+            lam, V = d.copy(), np.ones((1, 1))
+        else:
+            lam, V = eigh_tridiagonal(d, e[: d.size - 1])
+        clamp = max(1e-10, float(lam.max())) * 1e-6
+        keep = (lam >= 0) & (lam >= clamp)
+        total += float(np.sum(V[0, keep] ** 2 * np.log(lam[keep])))
+        valid += 1
+    return 0.0 if valid == 0 else n * total / valid
+
+
+# ---------------------------------------------------------------- BBMM
+def bbmm_step(kind: int, ard: bool, X, y_c, params, noise: float, P: Precond | None,
+              num_probes: int, max_cg: int, max_tridiag: int, tol: float, iteration: int,
+              x_warm: np.ndarray | None = None):
+    """NLL, gradients [P+1] and the CG solution of one BBMM evaluation."""
+    X = np.asarray(X, np.float64)
+    n = X.shape[0]
+    K = ok.kernel_matrix(kind, X, X, params, ard)
+    A = K + noise * np.eye(n)
+    T = num_probes
+    seed = iteration * 104729 + 42
+    if P is not None:
+        Z = P.sample(T, seed)
+    else:
+        Z = gaussian(n * T, seed).astype(np.float64).reshape(T, n).T
+    pnorm = np.linalg.norm(Z, axis=0)
+    Zn = Z / pnorm
+    rhs = np.concatenate([np.asarray(y_c, np.float64)[:, None], Zn], axis=1)
+    rnorm = np.linalg.norm(rhs, axis=0)
+    rhs = rhs / rnorm
+    x, iters, conv, diags, offs = batched_cg(A, rhs, P, max_cg, max_tridiag, tol, x_warm)
+    sol = x * rnorm
+    alpha = sol[:, 0]
+    inv_quad = float(np.dot(y_c, alpha))
+    logdet = 0.0
+    if max_tridiag > 0:
+        logdet = slq_logdet(diags[1:], offs[1:], n)
+        if P is not None:
+            logdet += P.logdet
+    nll = (0.5 * inv_quad + 0.5 * logdet + 0.5 * n * np.log(2 * np.pi)) / n
+    U = sol[:, 1:] * pnorm
+    W = Zn * pnorm
+    if P is not None:
+        W = P.apply(W)
+    G = ok.kernel_gradients(kind, X, X, params, ard)
+    grads = []
+    for g in G:
+        data = alpha @ g @ alpha
+        trace = np.sum(U * (g @ W)) if T > 0 else 0.0
+        grads.append((-0.5 * data + 0.5 * trace / max(T, 1)) / n)
+    noise_g = (-0.5 * alpha @ alpha + 0.5 * np.sum(U * W) / max(T, 1)) / n
+    grads.append(noise_g)
+    return {"nll": nll, "inv_quad": inv_quad, "logdet": logdet, "grads": np.array(grads),
+            "alpha": alpha, "x": x, "cg_iterations": iters, "converged": conv}
+
+
+# ---------------------------------------------------------------- training
+def _softplus(x):
+    x = F32(x)
+    if x > 20:
+        return x
+    if x < -20:
+        return F32(np.exp(x))
+    return F32(np.log(F32(1) + np.exp(x)))
+
+
+def _inv_softplus(y):
+    y = F32(y)
+    if y > 20:
+        return y
+    if y < 1e-6:
+        return F32(np.log(y))
+    return F32(np.log(np.exp(y) - F32(1)))
+
+
+def _softplus_deriv(x):
+    x = F32(x)
+    if x > 20:
+        return F32(1)
+    if x < -20:
+        return F32(np.exp(x))
+    return F32(1) / (F32(1) + np.exp(-x))
+
+
+def _clip(g, m=100.0):
+    g = F32(g)
+    if np.isnan(g) or g > 1e30 or g < -1e30:
+        return F32(0)
+    return F32(min(max(g, -m), m))
+
+
+def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_iterations=50,
+          learning_rate=0.01, num_probes=10, max_cg=100, cg_tol=1e-2, precond_rank=0,
+          max_tridiag=30, rebuild_threshold=0.5, init_mean=None):
+    """Adam over raw (inverse-softplus) hyperparameters and the constant mean,
+    with preconditioner rebuilds, NaN recovery and best-NLL restore."""
+    X = np.asarray(X, np.float64)
+    y = np.asarray(y, np.float64)
+    n = X.shape[0]
+    Pn = len(init_params)
+    init_mean = float(np.mean(y.astype(F32))) if init_mean is None else init_mean
+    raw = np.array([_inv_softplus(v) for v in init_params] + [_inv_softplus(init_noise)], F32)
+    raw_mean = F32(init_mean)
+    m = np.zeros(Pn + 1, F32)
+    v = np.zeros(Pn + 1, F32)
+    mm = vm = F32(0)
+    t = 0
+    best = dict(nll=np.inf, raw=raw.copy(), mean=raw_mean, m=m.copy(), v=v.copy(), mm=mm, vm=vm, t=t,
+                alpha=None)
+    lr = F32(learning_rate)
+
+    def build(params, noise):
+        if precond_rank <= 0:
+            return None
+        K = ok.kernel_matrix(kind, X, X, params, ard)
+        L, _ = pivoted_cholesky(K, precond_rank)
+        return Precond(L, noise)
+
+    P = build(np.asarray(init_params, np.float64), init_noise)
+    last_params, last_noise = np.asarray(init_params, F32).copy(), F32(init_noise)
+    x_prev = None
+    nll_hist, cg_hist = [], []
+    for it in range(max_iterations):
+        params = np.array([_softplus(r) for r in raw[:Pn]], F32)
+        noise = _softplus(raw[Pn])
+        if it > 0:
+            rel = np.abs(params - last_params) / np.maximum(np.abs(last_params), 1e-8)
+            rel = max(float(rel.max()), abs(noise - last_noise) / max(abs(last_noise), 1e-8))
+            if rel > rebuild_threshold:
+                P = build(params, noise)
+                last_params, last_noise = params.copy(), noise
+        y_c = (y.astype(F32) - raw_mean).astype(np.float64)
+        warm = None
+        if it > 0 and x_prev is not None:
+            warm = x_prev.copy()
+            warm[:, 1:] = 0.0
+        res = bbmm_step(kind, ard, X, y_c, params.astype(np.float64), float(noise), P, num_probes,
+                        max_cg, max_tridiag, cg_tol, it, warm)
+        x_prev = res["x"]
+        nll = res["nll"]
+        cg_hist.append(res["cg_iterations"])
+        if np.isnan(nll):
+            lr = lr * F32(0.5)
+            raw, raw_mean = best["raw"].copy(), best["mean"]
+            m, v, mm, vm, t = best["m"].copy(), best["v"].copy(), best["mm"], best["vm"], best["t"]
+            params = np.array([_softplus(r) for r in raw[:Pn]], F32)
+            noise = _softplus(raw[Pn])
+            last_params, last_noise = params.copy(), noise
+            P = build(params, noise)
+            continue
+        if nll < best["nll"]:
+            best.update(nll=nll, raw=raw.copy(), mean=raw_mean, m=m.copy(), v=v.copy(), mm=mm,
+                        vm=vm, t=t, alpha=res["alpha"].copy())
+        g = res["grads"].astype(F32)
+        for q in range(Pn + 1):
+            gr = _clip(g[q]) * _softplus_deriv(raw[q])
+            m[q] = F32(0.9) * m[q] + F32(0.1) * gr
+            v[q] = F32(0.999) * v[q] + F32(0.001) * gr * gr
+        t += 1
+        bc1 = F32(1) - F32(0.9) ** t
+        bc2 = F32(1) - F32(0.999) ** t
+        for q in range(Pn + 1):
+            nr = raw[q] - lr * (m[q] / bc1) / (np.sqrt(v[q] / bc2) + F32(1e-8))
+            raw[q] = F32(min(max(nr, -20.0), 20.0))
+        mg = _clip(-np.sum(res["alpha"]) / n)
+        mm = F32(0.9) * mm + F32(0.1) * mg
+        vm = F32(0.999) * vm + F32(0.001) * mg * mg
+        raw_mean = F32(raw_mean - lr * (mm / bc1) / (np.sqrt(vm / bc2) + F32(1e-8)))
+        if np.isnan(raw_mean) or abs(raw_mean) > 1000:
+            raw_mean = F32(init_mean)
+        nll_hist.append(nll)
+    params = np.array([_softplus(r) for r in best["raw"][:Pn]], F32)
+    return {"params": params, "noise": float(_softplus(best["raw"][Pn])),
+            "mean": float(best["mean"]), "final_nll": float(best["nll"]),
+            "alpha": best["alpha"], "nll_history": np.array(nll_hist),
+            "cg_iterations_history": np.array(cg_hist)}
+
+
+# ---------------------------------------------------------------- prediction
+def solve_alpha(A: np.ndarray, rhs: np.ndarray, max_iter: int, tol: float) -> np.ndarray:
+    """Unpreconditioned CG with relative-residual stop (jit_prediction.mojo:681-765)."""
+    x = np.zeros_like(rhs)
+    r = rhs.copy()
+    p = r.copy()
+    rr_old = float(r @ r)
+    init = np.sqrt(rr_old)
+    if init < 1e-20:
+        init = 1.0
+    for _ in range(max_iter):
+        Ap = A @ p
+        pAp = float(p @ Ap)
+        if np.isnan(pAp) or pAp < 1e-10:
+            break
+        a = rr_old / pAp
+        x += a * p
+        r -= a * Ap
+        rr_new = float(r @ r)
+        if np.sqrt(rr_new) / init < tol:
+            break
+        beta = rr_new / (rr_old + 1e-20) if rr_old >= 1e-20 else 0.0
+        if beta < 0 or np.isnan(beta):
+            beta = 0.0
+        p = r + beta * p
+        rr_old = rr_new
+    return x
+
+
+def lanczos_start(n: int, r: int) -> np.ndarray:
+    """Deterministic +-1 start vector (jit_prediction.mojo:999-1015), normalised."""
+    i = np.arange(n, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        s = (np.uint64(0xC0FFEE1234567890) ^ (i * np.uint64(0x9E3779B97F4A7C15))
+             ^ (np.uint64(r) * np.uint64(0xBF58476D1CE4E5B9)))
+        s ^= s >> np.uint64(12)
+        s ^= s << np.uint64(25)
+        s ^= s >> np.uint64(27)
+        s *= np.uint64(0x2545F4914F6CDD1D)
+    z = np.where((s & np.uint64(0x20000)) != 0, 1.0, -1.0)
+    return z / np.linalg.norm(z)
+
+
+def lanczos_inv_root(A: np.ndarray, r: int) -> np.ndarray:
+    """S [n, r] with S S^T ~ A^{-1}: Lanczos with full re-orthogonalisation."""
+    n = A.shape[0]
+    Q = np.zeros((n, r))
+    alpha = np.zeros(r)
+    beta = np.zeros(max(r - 1, 0))
+    Q[:, 0] = lanczos_start(n, r)
+    b_prev = 0.0
+    for j in range(r):
+        v = Q[:, j]
+        w = A @ v
+        alpha[j] = v @ w
+        w = w - alpha[j] * v
+        if j > 0:
+            w = w - b_prev * Q[:, j - 1]
+        for _ in range(2):
+            inner = Q[:, : j + 1].T @ w
+            w = w - Q[:, : j + 1] @ inner
+            if np.max(np.abs(inner)) < 1e-5:
+                break
+        b = np.linalg.norm(w)
+        if j < r - 1:
+            beta[j] = b
+        if b < 1e-10:
+            break
+        if j + 1 < r:
+            Q[:, j + 1] = w / b
+        b_prev = b
+    from scipy.linalg import eigh_tridiagonal
+    lam, V = eigh_tridiagonal(alpha, beta) if r > 1 else (alpha.copy(), np.ones((1, 1)))
+    clamp = max(1e-10, lam.max()) * 1e-6
+    lam = np.maximum(lam, clamp)
+    Tis = (V / np.sqrt(lam)) @ V.T
+    return Q @ Tis
+
+
+def predict(kind: int, ard: bool, X, y, Xs, params, noise: float, mean: float, *,
+            max_cg=300, tol=1e-3, lanczos_rank=100):
+    """Mean and LOVE variance as the reference computes them."""
+    X = np.asarray(X, np.float64)
+    n = X.shape[0]
+    A = ok.kernel_matrix(kind, X, X, params, ard) + noise * np.eye(n)
+    alpha = solve_alpha(A, np.asarray(y, np.float64) - mean, max_cg, tol)
+    Ks = ok.kernel_matrix(kind, Xs, X, params, ard)
+    mu = Ks @ alpha + mean
+    S = lanczos_inv_root(A, lanczos_rank)
+    V = Ks @ S
+    var = np.maximum(float(np.asarray(params)[-1]) - np.sum(V * V, axis=1), 1e-10)
+    return mu, var, alpha

@@ -1,0 +1,232 @@
+"""Pins the CPU restatement of the engine (oracle/engine.py) against facts that do
+not depend on it: library solvers, closed forms, exact identities and
+statistical properties.  CPU only, small n."""
+
+import numpy as np
+import pytest
+from scipy import stats
+
+from oracle import engine as oe
+from oracle import kernels as ok
+
+
+def _spd(rng, n, d=3, noise=0.1, kind=ok.MATERN52):
+    X = rng.normal(size=(n, d))
+    params = np.concatenate([rng.uniform(0.7, 1.5, d), [1.3]])
+    K = ok.kernel_matrix(kind, X, X, params, True)
+    return X, params, K, K + noise * np.eye(n)
+
+
+# ------------------------------------------------------------------ RNG
+def test_gaussian_moments_and_normality():
+    z = oe.gaussian(200_000, 42).astype(np.float64)
+    assert abs(z.mean()) < 0.01
+    assert abs(z.var() - 1.0) < 0.01
+    assert stats.kstest(z[:20000], "norm").pvalue > 1e-3
+
+
+def test_gaussian_deterministic_and_seed_dependent():
+    a = oe.gaussian(1000, 7)
+    assert np.array_equal(a, oe.gaussian(1000, 7))
+    assert not np.array_equal(a, oe.gaussian(1000, 8))
+    assert np.array_equal(oe.gaussian(1000, 7)[:10], oe.gaussian(10, 7))
+
+
+def test_gaussian_integer_hash_with_python_ints():
+    """Same uniforms from arbitrary-precision integers reduced mod 2^64."""
+    M = (1 << 64) - 1
+    seed = 104729 * 3 + 42
+    out = oe.gaussian(5, seed)
+    for idx in range(5):
+        k = idx + 1
+        s1 = (k * 6364136223846793005 + seed) & M
+        s1 ^= s1 >> 33
+        s1 = (s1 * 0xFF51AFD7ED558CCD) & M
+        s1 ^= s1 >> 33
+        s2 = (k * 1442695040888963407 + seed + 0xBEEF) & M
+        s2 ^= s2 >> 33
+        s2 = (s2 * 0xC4CEB9FE1A85EC53) & M
+        s2 ^= s2 >> 33
+        u1 = ((s1 & 0x7FFFFF) + 1) / 8388608.0
+        u2 = (s2 & 0xFFFFFF) / 16777216.0
+        z = np.sqrt(-2 * np.log(u1)) * np.cos(2 * 3.14159265 * u2)
+        assert out[idx] == pytest.approx(z, rel=2e-6, abs=2e-6)
+
+
+# ------------------------------------------------------------------ preconditioner
+def test_pivoted_cholesky_exact_on_low_rank():
+    rng = np.random.default_rng(1)
+    B = rng.normal(size=(60, 5))
+    K = B @ B.T
+    L, k = oe.pivoted_cholesky(K, 5, dtype=np.float64)
+    assert k == 5
+    np.testing.assert_allclose(L @ L.T, K, atol=1e-9)
+    L2, k2 = oe.pivoted_cholesky(K, 12, dtype=np.float64)  # stops once the residual vanishes
+    assert k2 == 5
+
+
+def test_pivoted_cholesky_full_rank_and_monotone_error():
+    rng = np.random.default_rng(2)
+    _, _, K, _ = _spd(rng, 40)
+    errs = []
+    for r in (1, 5, 10, 20, 40):
+        L, _ = oe.pivoted_cholesky(K, r, dtype=np.float64)
+        errs.append(np.trace(K - L @ L.T))
+    assert all(a >= b - 1e-12 for a, b in zip(errs, errs[1:]))
+    L, _ = oe.pivoted_cholesky(K, 40, dtype=np.float64)
+    np.testing.assert_allclose(L @ L.T, K, atol=1e-8)
+    L32, _ = oe.pivoted_cholesky(K, 40)
+    np.testing.assert_allclose(L32 @ L32.T, K, atol=1e-4)
+
+
+def test_fp32_residual_ties_pick_lowest_index():
+    # Rows 2 and 3 are far from the first pivot (row 0): their fp32 residual
+    # diagonal rounds to exactly 1.0, so the second pivot is row 2 (lowest
+    # index), although row 3 is farther away in exact arithmetic.
+    K = np.eye(4)
+    K[0, 1] = K[1, 0] = 0.5
+    K[0, 2] = K[2, 0] = 1e-5
+    K[0, 3] = K[3, 0] = 1e-9
+    L32, _ = oe.pivoted_cholesky(K, 2)
+    L64, _ = oe.pivoted_cholesky(K, 2, dtype=np.float64)
+    assert np.argmax(np.abs(L32[:, 1])) == 2
+    assert np.argmax(np.abs(L64[:, 1])) == 3
+
+
+def test_pivot_order_is_greedy_lowest_index():
+    K = np.diag([1.0, 3.0, 3.0, 2.0])
+    L, k = oe.pivoted_cholesky(K, 2)
+    assert np.argmax(np.abs(L[:, 0])) == 1     # tie 3.0 at rows 1, 2 -> row 1
+    assert np.argmax(np.abs(L[:, 1])) == 2
+
+
+def test_woodbury_and_logdet_match_dense():
+    rng = np.random.default_rng(3)
+    _, _, K, _ = _spd(rng, 50)
+    L, _ = oe.pivoted_cholesky(K, 15)
+    P = oe.Precond(L, 0.05)
+    Pm = L @ L.T + 0.05 * np.eye(50)
+    V = rng.normal(size=(50, 4))
+    np.testing.assert_allclose(P.apply(V), np.linalg.solve(Pm, V), rtol=1e-8, atol=1e-10)
+    assert P.logdet == pytest.approx(np.linalg.slogdet(Pm)[1], rel=1e-10)
+
+
+def test_precond_samples_have_covariance_P():
+    rng = np.random.default_rng(4)
+    _, _, K, _ = _spd(rng, 12)
+    L, _ = oe.pivoted_cholesky(K, 4)
+    P = oe.Precond(L, 0.2)
+    Z = P.sample(40000, 42)
+    cov = Z @ Z.T / Z.shape[1]
+    Pm = L @ L.T + 0.2 * np.eye(12)
+    assert np.abs(cov - Pm).max() < 0.06 * np.abs(Pm).max()
+
+
+# ------------------------------------------------------------------ CG / SLQ
+@pytest.mark.parametrize("use_pc", [False, True])
+def test_batched_cg_matches_solve(use_pc):
+    rng = np.random.default_rng(5)
+    _, _, K, A = _spd(rng, 80)
+    P = oe.Precond(oe.pivoted_cholesky(K, 10)[0], 0.1) if use_pc else None
+    rhs = rng.normal(size=(80, 3))
+    x, iters, conv, _, _ = oe.batched_cg(A, rhs, P, 1000, 30, 1e-12)
+    np.testing.assert_allclose(x, np.linalg.solve(A, rhs), rtol=1e-6, atol=1e-9)
+    assert iters >= 30
+
+
+def test_cg_stops_only_on_check_iterations():
+    rng = np.random.default_rng(6)
+    _, _, _, A = _spd(rng, 60)
+    rhs = rng.normal(size=(60, 2))
+    rhs /= np.linalg.norm(rhs, axis=0)
+    _, iters, conv, _, _ = oe.batched_cg(A, rhs, None, 100, 5, 1e-2)
+    assert conv and iters % 10 == 0 and iters >= 10
+
+
+def test_slq_full_lanczos_equals_quadratic_form_of_log():
+    """With n CG steps the probe tridiagonal carries the exact spectral measure:
+    sum_i V0i^2 log(lambda_i) = z^T log(A) z for a unit probe z."""
+    rng = np.random.default_rng(7)
+    n = 24
+    _, _, _, A = _spd(rng, n, noise=0.5)
+    z = rng.normal(size=(n, 1))
+    z /= np.linalg.norm(z)
+    _, _, _, diags, offs = oe.batched_cg(A, z, None, n, n, 1e-30)
+    est = oe.slq_logdet(diags, offs, 1)
+    w, U = np.linalg.eigh(A)
+    exact = float((z[:, 0] @ U) ** 2 @ np.log(w))
+    assert est == pytest.approx(exact, rel=1e-6)
+
+
+def test_slq_scaled_identity_closed_form():
+    n, c = 30, 3.5
+    z = np.ones((n, 2)) / np.sqrt(n)
+    _, _, _, diags, offs = oe.batched_cg(c * np.eye(n), z, None, 5, 5, 1e-30)
+    assert oe.slq_logdet(diags, offs, n) == pytest.approx(n * np.log(c), rel=1e-12)
+
+
+# ------------------------------------------------------------------ BBMM
+def test_bbmm_converges_to_exact_nll_and_gradient():
+    rng = np.random.default_rng(8)
+    n, d = 120, 2
+    X = rng.uniform(-2, 2, size=(n, d))
+    params = np.array([0.9, 1.3, 1.1])
+    noise = 0.2
+    y = np.sin(X.sum(1)) + 0.1 * rng.normal(size=n)
+    A = ok.kernel_matrix(ok.RBF, X, X, params, True) + noise * np.eye(n)
+    r = oe.bbmm_step(ok.RBF, True, X, y, params, noise, None, 400, n, n, 1e-10, 0)
+    a = np.linalg.solve(A, y)
+    nll = (0.5 * y @ a + 0.5 * np.linalg.slogdet(A)[1] + 0.5 * n * np.log(2 * np.pi)) / n
+    assert r["nll"] == pytest.approx(nll, rel=2e-2)
+    assert r["inv_quad"] == pytest.approx(y @ a, rel=1e-8)
+    Ainv = np.linalg.inv(A)
+    G = list(ok.kernel_gradients(ok.RBF, X, X, params, True)) + [np.eye(n)]
+    exact = np.array([(-0.5 * a @ g @ a + 0.5 * np.trace(Ainv @ g)) / n for g in G])
+    assert np.linalg.norm(r["grads"] - exact) < 0.1 * np.linalg.norm(exact)
+
+
+# ------------------------------------------------------------------ prediction
+def test_solve_alpha_matches_solve():
+    rng = np.random.default_rng(9)
+    _, _, _, A = _spd(rng, 70)
+    b = rng.normal(size=70)
+    # The absolute pAp < 1e-10 guard ends the solve once p is tiny, so the
+    # achievable accuracy is limited by that guard rather than by tol.
+    np.testing.assert_allclose(oe.solve_alpha(A, b, 500, 1e-12), np.linalg.solve(A, b), rtol=1e-4)
+    np.testing.assert_allclose(oe.solve_alpha(A, 1e4 * b, 500, 1e-12),
+                               np.linalg.solve(A, 1e4 * b), rtol=1e-8)
+
+
+def test_lanczos_full_rank_root_inverts():
+    rng = np.random.default_rng(10)
+    n = 30
+    _, _, _, A = _spd(rng, n, noise=0.3)
+    S = oe.lanczos_inv_root(A, n)
+    np.testing.assert_allclose(S @ S.T, np.linalg.inv(A), rtol=1e-6, atol=1e-8)
+
+
+def test_love_full_rank_equals_exact_variance():
+    rng = np.random.default_rng(11)
+    n, d = 40, 2
+    X = rng.uniform(-1, 1, size=(n, d))
+    Xs = rng.uniform(-1.2, 1.2, size=(9, d))
+    y = np.cos(X).sum(1)
+    params = np.array([0.8, 1.2])
+    mu, var, _ = oe.predict(ok.MATERN52, False, X, y, Xs, params, 0.3, 0.1, max_cg=500,
+                            tol=1e-12, lanczos_rank=n)
+    A = ok.kernel_matrix(ok.MATERN52, X, X, params, False) + 0.3 * np.eye(n)
+    Ks = ok.kernel_matrix(ok.MATERN52, Xs, X, params, False)
+    np.testing.assert_allclose(mu, Ks @ np.linalg.solve(A, y - 0.1) + 0.1, rtol=1e-5)
+    exact = 1.2 - np.sum(Ks * np.linalg.solve(A, Ks.T).T, axis=1)
+    np.testing.assert_allclose(var, exact, rtol=1e-6, atol=1e-9)
+
+
+def test_train_reduces_nll():
+    rng = np.random.default_rng(12)
+    n = 150
+    X = np.linspace(-3, 3, n)[:, None]
+    y = np.sin(2 * X[:, 0]) + 0.05 * rng.normal(size=n)
+    res = oe.train(ok.RBF, False, X, y, [0.5, 1.0], 0.1, max_iterations=15, num_probes=8)
+    h = res["nll_history"]
+    assert np.all(np.isfinite(h)) and h[-1] < h[0]
+    assert np.all(res["params"] > 0) and res["noise"] > 0
