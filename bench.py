@@ -35,6 +35,9 @@ N, D, T = 250_000, 16, 16
 C_K = 9                        # Matern-5/2 epilogue flops per pair
 N_TR = 2                       # sqrt + exp per pair
 FLOPS_PER_PAIR = 2 * D + 2 * T + C_K
+# HBM bytes per launch of the tile kernel at this workload: FETCH_SIZE x 2.000 +
+# WRITE_SIZE x 1.000 (copy-kernel calibration), profiles/fused_tile_c3_matvec.md.
+TILE_TRAFFIC_BYTES = 1.504e9
 
 
 def _make_inputs():
@@ -46,10 +49,49 @@ def _make_inputs():
     return X, V, params, 0.1
 
 
+def _mbcg_iteration_ms(X, params, noise, iterations: int = 20):
+    """One mBCG iteration at config 3: (K + sigma^2 I) P over t=16 columns with a
+    rank-200 greedy pivoted-Cholesky preconditioner, Woodbury apply, fused
+    dots/updates.  Returns (ms per iteration, wall seconds of the eval)."""
+    import ctypes
+    from mojogp_amd import _lib
+    from mojogp_amd._provider import NativeProvider, KIND_MATERN52
+    rng = np.random.default_rng(1)
+    y = rng.normal(size=N).astype(np.float32)
+    prov = NativeProvider(KIND_MATERN52, True, X, params, noise)
+    g = np.zeros(params.size + 1, np.float32)
+    nll, iq, ld, pl = (ctypes.c_float() for _ in range(4))
+    ci, loop_ms = ctypes.c_int(), ctypes.c_double()
+    t0 = time.perf_counter()
+    try:
+        _lib.call("mgp_bbmm_eval", prov.handle, _lib.fptr(y), 0.0, T - 1, iterations,
+                  iterations, 0.0, 0, 200, ctypes.byref(nll), ctypes.byref(iq), ctypes.byref(ld),
+                  _lib.fptr(g), ctypes.byref(ci), ctypes.byref(pl), ctypes.byref(loop_ms))
+    finally:
+        prov.close()
+    return loop_ms.value / max(ci.value, 1), time.perf_counter() - t0
+
+
+def _fit_c2_seconds():
+    """Config 2 end to end: RBF-ARD, N=50k, d=8, 30 Adam steps, 15 probes,
+    rank-100 greedy preconditioner (matrix-free)."""
+    from mojogp_amd import RBF, SingleOutputGP
+    rng = np.random.default_rng(0)
+    X = rng.uniform(size=(50_000, 8)).astype(np.float32)
+    y = (np.sin(3 * X).sum(1) + 0.1 * rng.normal(size=50_000)).astype(np.float32)
+    gp = SingleOutputGP(RBF(ard=True))
+    t0 = time.perf_counter()
+    tr = gp.fit(X, y, max_iterations=30, method="matrix_free", num_probes=15,
+                preconditioner_rank=100, preconditioner="greedy")
+    dt = time.perf_counter() - t0
+    info = gp.backend_train_info or {}
+    return dt, {"final_nll": tr.nll, "cg_iterations_total": info.get("cg_iterations_total")}
+
+
 def _cpu_baseline(X, V, params, noise, target_s: float):
     from oracle import cpu_ref
     threads = cpu_ref.num_threads()
-    probe_rows = 32
+    probe_rows = 256
     t0 = time.perf_counter()
     cpu_ref.forward_matvec_rows(1, True, X, params, noise, V, 0, probe_rows)
     dt = max(time.perf_counter() - t0, 1e-3)
@@ -76,6 +118,8 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the mBCG-iteration and fit() measurements")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel of BYTES (HBM counter calibration)")
     args = ap.parse_args(argv)
@@ -136,12 +180,20 @@ def main(argv=None) -> int:
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-            "traffic": None,
+            "traffic": TILE_TRAFFIC_BYTES,
         },
         "tile_kernel_ms": round(tile_ms, 4),
         "issue_slot_roofline_ms": round(t_roof_ms, 3),
         "issue_slot_roofline_frac": round(t_roof_ms / tile_ms, 4),
     }
+    if not args.no_extras:
+        it_ms, _ = _mbcg_iteration_ms(X, params, noise)
+        result["mbcg_iter_ms"] = round(it_ms, 3)
+        fit_s, fit_info = _fit_c2_seconds()
+        result["fit_seconds"] = round(fit_s, 3)
+        result["fit_config"] = ("config 2: RBF-ARD N=50000 d=8, 30 Adam steps, 15 probes, "
+                                "rank-100 greedy preconditioner")
+        result["fit_info"] = fit_info
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(X, V, params, noise, args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -183,7 +183,8 @@ MGP_API int mgp_train(void* handle, const float* y, const float* init_params,
  * sample, y^T K^-1 y, log|K| (SLQ) and gradients[nparams + 1] (kernel
  * params, then noise) of the reference's bbmm_with_precond
  * (combined_inv_quad_logdet.mojo:452-1140) with probe seed
- * iteration*104729+42 and a greedy preconditioner of precond_rank (0: none).
+ * iteration*104729+42 and a greedy preconditioner of precond_rank (0: none);
+ * cg_loop_ms receives the wall time of the mBCG iteration loop.
  * Internal to the reference (no exported counterpart); exposed for
  * teacher-forced parity tests. */
 MGP_API int mgp_bbmm_eval(void* handle, const float* y, float mean,
@@ -191,7 +192,7 @@ MGP_API int mgp_bbmm_eval(void* handle, const float* y, float mean,
                           float cg_tol, int iteration, int precond_rank,
                           float* nll, float* inv_quad, float* logdet,
                           float* grads, int* cg_iterations,
-                          float* precond_logdet);
+                          float* precond_logdet, double* cg_loop_ms);
 /* Counter-hash Gaussian draws of kernel_gpu_gaussian
  * (pivoted_cholesky.mojo:51-86), computed on the device. */
 MGP_API int mgp_gaussian(int64_t len, uint64_t seed, float* out);

@@ -138,7 +138,7 @@ _SIGNATURES = {
     "mgp_destroy_prediction_cache": (C.c_int, [C.c_void_p]),
     "mgp_bbmm_eval": (C.c_int, [C.c_void_p, c_float_p, C.c_float, C.c_int, C.c_int, C.c_int,
                                 C.c_float, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
-                                c_float_p, c_int_p, c_float_p]),
+                                c_float_p, c_int_p, c_float_p, c_double_p]),
     "mgp_gaussian": (C.c_int, [C.c_int64, C.c_uint64, c_float_p]),
     "mgp_pivoted_cholesky": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_int_p, c_float_p]),
 }

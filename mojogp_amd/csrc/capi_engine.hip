@@ -146,7 +146,7 @@ int mgp_train(void* handle, const float* y, const float* init_params, int nparam
 int mgp_bbmm_eval(void* handle, const float* y, float mean, int num_probes, int max_cg_iter,
                   int max_tridiag_iter, float cg_tol, int iteration, int precond_rank,
                   float* nll, float* inv_quad, float* logdet, float* grads,
-                  int* cg_iterations, float* precond_logdet) {
+                  int* cg_iterations, float* precond_logdet, double* cg_loop_ms) {
   return guarded([&] {
     Provider* pv = as_provider(handle);
     MGP_REQUIRE(y && nll && grads, "null argument");
@@ -165,6 +165,7 @@ int mgp_bbmm_eval(void* handle, const float* y, float mean, int num_probes, int 
     if (logdet) *logdet = r.logdet;
     if (cg_iterations) *cg_iterations = r.cg_iterations;
     if (precond_logdet) *precond_logdet = P.logdet;
+    if (cg_loop_ms) *cg_loop_ms = r.cg_loop_ms;
     std::memcpy(grads, r.grads.data(), r.grads.size() * sizeof(float));
   });
 }

@@ -43,6 +43,7 @@ struct CGResult {
   int iterations = 0;
   bool converged = false;
   int tridiag_size = 0;
+  double loop_ms = 0.0;  // wall time of the iteration loop (device work synced)
   std::vector<std::vector<float>> diag, offdiag;  // per column
 };
 
@@ -64,6 +65,7 @@ struct BBMMResult {
   std::vector<float> grads;  // kernel params then noise
   int cg_iterations = 0;
   bool converged = false;
+  double cg_loop_ms = 0.0;
   const float* alpha_dev = nullptr;  // sol column 0 (valid until next call)
 };
 

@@ -243,6 +243,8 @@ CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_i
 
   CGResult res;
   int tridiag_size = 0;
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  const auto t_loop = Clock::now();
   for (int iter = 0; iter < max_iter; ++iter) {
     res.iterations = iter + 1;
     pv.forward(p, C, Ap);
@@ -270,6 +272,8 @@ CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_i
       }
     }
   }
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  res.loop_ms = secs_since(t_loop) * 1e3;
   res.tridiag_size = tridiag_size;
   res.diag.assign(C, {});
   res.offdiag.assign(C, {});
@@ -352,6 +356,7 @@ BBMMResult bbmm_step(Provider& pv, Precond& P, bool use_precond, const float* y_
   BBMMResult out;
   out.cg_iterations = cg.iterations;
   out.converged = cg.converged;
+  out.cg_loop_ms = cg.loop_ms;
   out.alpha_dev = sol;
   out.inv_quad = dot_f(y_c, sol, n, w.part, st);
 

@@ -73,7 +73,8 @@ def test_bbmm_eval_matches_oracle(kind, ard, d, n, T, rank):
     nll, iq, ld, ci, pl = C.c_float(), C.c_float(), C.c_float(), C.c_int(), C.c_float()
     try:
         _lib.call("mgp_bbmm_eval", p.handle, _lib.fptr(y), mean, T, 100, 30, 1e-2, it, rank,
-                  C.byref(nll), C.byref(iq), C.byref(ld), _lib.fptr(g), C.byref(ci), C.byref(pl))
+                  C.byref(nll), C.byref(iq), C.byref(ld), _lib.fptr(g), C.byref(ci), C.byref(pl),
+                  None)
     finally:
         p.close()
     P = None
