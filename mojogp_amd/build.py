@@ -36,6 +36,10 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA sources/results in ordinary VGPRs: no v_accvgpr_read/write copies
+    # between the matrix accumulators and the VALU kernel-value math.
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result",
 ]
 

@@ -32,17 +32,32 @@ constexpr int kFlushTiles = 16;     // j tiles between fp64 flushes
 constexpr float kM52A = 0.69314718055994530942f;                     // ln 2
 constexpr float kM52B = 0.69314718055994530942f * 0.69314718055994530942f / 3.0f;
 
+// kExp2Clamp held in a VGPR (hoisted out of the hot loop by the caller).
+__device__ __forceinline__ float clamp_reg() {
+  float c = kExp2Clamp;
+  asm volatile("" : "+v"(c));
+  return c;
+}
+
 // Kernel value from the scaled squared distance s (see kernel_scale()).
+// clampv = kExp2Clamp (from clamp_reg() in hot loops).
 template <int KIND>
-__device__ __forceinline__ float kval(float s) {
+__device__ __forceinline__ float kval(float s, float clampv = kExp2Clamp) {
   if constexpr (KIND == KIND_RBF) {
     // os * exp(max(-0.5 r^2, -20)) = os * 2^-clamp(s, 0, 20 log2 e)
     const float t = __builtin_amdgcn_fmed3f(s, 0.0f, kExp2Clamp);
     return __builtin_amdgcn_exp2f(-t);
   } else {
     // os * (1 + sqrt5 r + 5/3 r^2) * exp(max(-sqrt5 r, -20)),  u = sqrt5 r log2 e
-    const float u = __builtin_amdgcn_sqrtf(fmaxf(s, 0.0f));
-    const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+    // max(s, 0) as a signed-integer max of the bit pattern: one VALU op and no
+    // NaN canonicalization of the MFMA result.
+    const float sc = __builtin_bit_cast(float, max(__builtin_bit_cast(int, s), 0));
+    const float u = __builtin_amdgcn_sqrtf(sc);
+    // min(u, C) kept opaque so that the negation is not rewritten into
+    // max(-u, -C) + v_xor but lands on v_exp_f32 as a source modifier.
+    float m = fminf(u, clampv);
+    asm("" : "+v"(m));
+    const float e = __builtin_amdgcn_exp2f(-m);
     const float p = fmaf(u, fmaf(u, kM52B, kM52A), 1.0f);
     return p * e;
   }
@@ -131,7 +146,8 @@ __global__ __launch_bounds__(256) void k_fused_tile(
     const float* __restrict__ Vin, float* __restrict__ out,
     float* __restrict__ partial, int64_t mpad, int cpad) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave index made wave-uniform (SGPR) so the j-loop bounds stay scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t tile0 = ((int64_t)blockIdx.x * kWaves + wave) * R;
   if (tile0 >= row_tiles) return;  // whole wave idle (no barriers used)
 
@@ -159,14 +175,16 @@ __global__ __launch_bounds__(256) void k_fused_tile(
     }
   }
 
-  // Diagonal-tile mask: lane holds S^T[j = 4(lane/16)+q][i = lane%16].
+  const float clampv = clamp_reg();
+
+  // Lane holds S^T[j = 4(lane/16)+q][i = lane%16] of a 16x16 tile.
   const int li = lane & 15;
   const int lj = 4 * (lane >> 4);
 
-  const int64_t jt_begin = (int64_t)blockIdx.y * jt_per_split;
-  const int64_t jt_end = min(col_tiles, jt_begin + jt_per_split);
-  int since_flush = 0;
-  for (int64_t jt = jt_begin; jt < jt_end; ++jt) {
+  // One j tile against the wave's R row tiles.  MASK restores the exact zero
+  // self-distance on diagonal tiles (Gram-form cancellation guard).
+  auto step = [&](int64_t jt, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     float aj[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) aj[kk] = Aj[(jt * KK + kk) * 64 + lane];
@@ -184,15 +202,16 @@ __global__ __launch_bounds__(256) void k_fused_tile(
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
         s = __builtin_amdgcn_mfma_f32_16x16x4f32(aj[kk], bi[r][kk], s, 0, 0, 0);
-      if (jt == tile0 + r + diag_shift) {
-        // exact zero distance on the diagonal (Gram-form cancellation guard)
+      if constexpr (MASK) {
+        if (jt == tile0 + r + diag_shift) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (li == lj + q) s[q] = 0.0f;
+          for (int q = 0; q < 4; ++q)
+            if (li == lj + q) s[q] = 0.0f;
+        }
       }
       float p[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) p[q] = kval<KIND>(s[q]);
+      for (int q = 0; q < 4; ++q) p[q] = kval<KIND>(s[q], clampv);
       if constexpr (NCG > 0) {
 #pragma unroll
         for (int g = 0; g < NCG; ++g)
@@ -207,24 +226,40 @@ __global__ __launch_bounds__(256) void k_fused_tile(
         acc1[r] = a;
       }
     }
-    if (++since_flush == kFlushTiles) {
-      since_flush = 0;
+  };
+  auto flush = [&]() {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if constexpr (NCG > 0) {
+    for (int r = 0; r < R; ++r) {
+      if constexpr (NCG > 0) {
 #pragma unroll
-          for (int g = 0; g < NCG; ++g) {
+        for (int g = 0; g < NCG; ++g) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) accd[r][g][q] += (double)acc[r][g][q];
-            acc[r][g] = f4{0.f, 0.f, 0.f, 0.f};
-          }
-        } else {
-          accd[r][0][0] += (double)acc1[r];
-          acc1[r] = 0.0f;
+          for (int q = 0; q < 4; ++q) accd[r][g][q] += (double)acc[r][g][q];
+          acc[r][g] = f4{0.f, 0.f, 0.f, 0.f};
         }
+      } else {
+        accd[r][0][0] += (double)acc1[r];
+        acc1[r] = 0.0f;
       }
     }
-  }
+  };
+  // Plain tiles in chunks of kFlushTiles (no branch in the hot loop), then the
+  // diagonal tiles with the mask.
+  auto run = [&](int64_t a, int64_t b) {
+    for (int64_t c0 = a; c0 < b; c0 += kFlushTiles) {
+      const int64_t e = min(b, c0 + kFlushTiles);
+      for (int64_t jt = c0; jt < e; ++jt) step(jt, std::false_type{});
+      flush();
+    }
+  };
+
+  const int64_t jt_begin = (int64_t)blockIdx.y * jt_per_split;
+  const int64_t jt_end = min(col_tiles, jt_begin + jt_per_split);
+  const int64_t dlo = tile0 + diag_shift, dhi = dlo + R;
+  run(jt_begin, min(jt_end, dlo));
+  run(max(jt_begin, dhi), jt_end);
+  for (int64_t jt = max(jt_begin, dlo); jt < min(jt_end, dhi); ++jt) step(jt, std::true_type{});
+  flush();
 
   // Epilogue.
 #pragma unroll
