@@ -13,18 +13,29 @@ struct Coords {
   DevBuf<float> coef;  // [2*d]: center[d] then scale[d]
 };
 
-// Points laid out as 16x16x4 fp32 MFMA operands.
-//   A-side (columns j): aug = [z_0..z_{d-1}, |z|^2, 1, 0 ...]
-//   B-side (rows i):    aug = [-2 z_0..-2 z_{d-1}, 1, |z|^2, 0 ...]
-//   pack[tile][kk][lane] = aug[16*tile + lane%16][4*kk + lane/16]
-// so one MFMA over kk-slices of A(j) and B(i) accumulates |z_i - z_j|^2.
+// Points laid out as v_mfma_f32_16x16x32_bf16 operands.
+//   A-side (columns j): aug = [z_0..z_{d-1}, |z|^2, 1]
+//   B-side (rows i):    aug = [-2 z_0..-2 z_{d-1}, 1, |z|^2]
+// Every fp32 aug value is split exactly into three bf16 parts
+// (x = hi + mid + lo, 8 significant bits each).  The dot product of the two
+// augmented vectors is then the sum of six part-products per dimension,
+//   hi.hi + hi.mid + mid.hi + hi.lo + lo.hi + mid.mid
+// (the dropped mid.lo, lo.mid, lo.lo terms are below 2^-23 relative), which
+// yields |z_i - z_j|^2 at fp32 accuracy on the bf16 matrix cores.
+// Slot k (0 <= k < 32*kb) of a point holds product p = k / D, dimension
+// t = k % D (D = d + 2), zero for k >= 6 D; lane (li + 16 g) of MFMA m carries
+// slots 32 m + 8 g + e, e = 0..7:
+//   pack[tile][m][lane][e] (bf16), lane = point%16 + 16 g
 struct PackedPoints {
   int64_t n = 0;       // real points
   int64_t ntiles = 0;  // 16-point tiles (zero padded)
-  int kk = 0;          // number of K=4 slices (augmented dim / 4)
-  DevBuf<float> A, B;
+  int kb = 0;          // K=32 bf16 MFMAs per 16x16 distance tile
+  DevBuf<uint32_t> A, B;  // two bf16 per dword
   DevBuf<float> z;     // scaled coordinates, row-major [n][d] (direct path)
 };
+
+// Number of K=32 MFMAs for input dimension d: ceil(6 (d + 2) / 32).
+inline int split_mfma_count(int d) { return (6 * (d + 2) + 31) / 32; }
 
 // Multiplier applied to (x - center)/lengthscale so that the squared distance
 // of the scaled points feeds exp2 directly:
@@ -53,6 +64,7 @@ struct MatvecArgs {
 // V and out are column-major device arrays.  Work buffers are grown in `ws`.
 struct MatvecWorkspace {
   DevBuf<float> vpack;    // packed right-hand sides
+  DevBuf<uint32_t> colmax;  // per-column max |V| (fp16 scaling of the product)
   DevBuf<float> partial;  // split-K partial sums
   // Optional HIP-event timing of the tile kernel alone (bench hook).
   bool time_tile = false;
@@ -72,7 +84,7 @@ void direct_matvec(const MatvecArgs& a, const PackedPoints& rows,
                    const PackedPoints& cols, int d, const float* V_dev,
                    float* out_dev, hipStream_t st);
 
-// Maximum input dimension served by the MFMA tile path (augmented K <= 32).
+// Maximum input dimension served by the MFMA tile path (six K=32 MFMAs).
 constexpr int kMaxMfmaDim = 30;
 
 }  // namespace mgp

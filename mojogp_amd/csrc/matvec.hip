@@ -8,9 +8,11 @@
 //
 // Design (not a translation): the product out = K V is evaluated like an
 // attention block.  Per 16x16 tile of (row i, column j) pairs:
-//   1. S^T = A_j . B_i   (v_mfma_f32_16x16x4f32 over the augmented coordinates)
-//      yields the scaled squared distance |z_i - z_j|^2 directly (Gram form with
-//      the norms folded into two extra K slots);
+//   1. S^T = A_j . B_i   (v_mfma_f32_16x16x32_bf16 over the three-way bf16
+//      split of the augmented coordinates, see PackedPoints) yields the scaled
+//      squared distance |z_i - z_j|^2 at fp32 accuracy (Gram form, norms in two
+//      extra dimensions); 4 MFMAs at d = 16 instead of 5 fp32 K=4 MFMAs of
+//      twice the cycle count each;
 //   2. the kernel value is formed in registers (RBF: med3 + exp2;
 //      Matern-5/2: sqrt, min, exp2, two FMAs, one multiply);
 //   3. O^T += V^T . P^T  (four more 16x16x4 MFMAs per 16 right-hand sides).
@@ -24,6 +26,9 @@
 namespace mgp {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 namespace {
 
@@ -49,10 +54,10 @@ __device__ __forceinline__ float kval(float s, float clampv = kExp2Clamp) {
     return __builtin_amdgcn_exp2f(-t);
   } else {
     // os * (1 + sqrt5 r + 5/3 r^2) * exp(max(-sqrt5 r, -20)),  u = sqrt5 r log2 e
-    // max(s, 0) as a signed-integer max of the bit pattern: one VALU op and no
-    // NaN canonicalization of the MFMA result.
-    const float sc = __builtin_bit_cast(float, max(__builtin_bit_cast(int, s), 0));
-    const float u = __builtin_amdgcn_sqrtf(sc);
+    // sqrt(|s|): s < 0 only from Gram-form rounding of a near-zero distance,
+    // where |s| and max(s, 0) agree to the rounding error (dk/du = 0 at u = 0);
+    // the abs is a free source modifier of v_sqrt_f32.
+    const float u = __builtin_amdgcn_sqrtf(fabsf(s));
     // min(u, C) kept opaque so that the negation is not rewritten into
     // max(-u, -C) + v_xor but lands on v_exp_f32 as a source modifier.
     float m = fminf(u, clampv);
@@ -66,59 +71,135 @@ __device__ __forceinline__ float kval(float s, float clampv = kExp2Clamp) {
 // ---------------------------------------------------------------------------
 // Packing
 // ---------------------------------------------------------------------------
+// Exact three-way bf16 split of an fp32 value by truncation: x = hi + mid + lo
+// with each remainder exact in fp32.  Returns the requested part's bits.
+__device__ __forceinline__ uint16_t bf16_part(float x, int part) {
+  const uint32_t b0 = __float_as_uint(x) & 0xFFFF0000u;
+  if (part == 0) return (uint16_t)(b0 >> 16);
+  const float r1 = x - __uint_as_float(b0);
+  const uint32_t b1 = __float_as_uint(r1) & 0xFFFF0000u;
+  if (part == 1) return (uint16_t)(b1 >> 16);
+  const float r2 = r1 - __uint_as_float(b1);
+  return (uint16_t)(__float_as_uint(r2) >> 16);
+}
+
+// Part-product table: slot product p multiplies A part kPartA[p] with B part
+// kPartB[p] (hi=0, mid=1, lo=2).
+__constant__ int kPartA[6] = {0, 0, 1, 0, 2, 1};
+__constant__ int kPartB[6] = {0, 1, 0, 2, 0, 1};
+
+// One thread per (padded) point: scaled coordinates, norm, and the 32*kb bf16
+// slots of both operand sides.
 __global__ void k_pack_points(const float* __restrict__ X, int64_t n, int d,
-                              const float* __restrict__ coef, int kk,
-                              int64_t ntiles, float* __restrict__ A,
-                              float* __restrict__ B, float* __restrict__ Z) {
+                              const float* __restrict__ coef, int kb,
+                              int64_t ntiles, uint16_t* __restrict__ A,
+                              uint16_t* __restrict__ B, float* __restrict__ Z) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= ntiles * 16) return;
   const int li = (int)(i & 15);
   const int64_t tile = i >> 4;
-  const int ka = kk * 4;
-  float nrm = 0.0f;
   const bool real = i < n;
-  for (int k = 0; k < ka; ++k) {
-    float a = 0.0f, b = 0.0f;
-    if (k < d) {
-      float z = 0.0f;
-      if (real) {
-        z = (X[i * d + k] - coef[k]) * coef[d + k];
-        Z[i * d + k] = z;
+  auto zval = [&](int k) -> float {
+    return real ? (X[i * d + k] - coef[k]) * coef[d + k] : 0.0f;
+  };
+  float nrm = 0.0f;
+  for (int k = 0; k < d; ++k) {
+    const float z = zval(k);
+    if (real) Z[i * d + k] = z;
+    nrm = fmaf(z, z, nrm);
+  }
+  const int D = d + 2;
+  for (int k = 0; k < 32 * kb; ++k) {
+    uint16_t a = 0, b = 0;
+    if (k < 6 * D) {
+      const int p = k / D, t = k - p * D;
+      float av, bv;
+      if (t < d) {
+        const float z = zval(t);
+        av = z;
+        bv = -2.0f * z;
+      } else if (t == d) {
+        av = nrm;
+        bv = 1.0f;
+      } else {
+        av = 1.0f;
+        bv = nrm;
       }
-      nrm = fmaf(z, z, nrm);
-      a = z;
-      b = -2.0f * z;
-    } else if (k == d) {
-      a = nrm;
-      b = 1.0f;
-    } else if (k == d + 1) {
-      a = 1.0f;
-      b = nrm;
+      a = bf16_part(av, kPartA[p]);
+      b = bf16_part(bv, kPartB[p]);
     }
-    const int64_t off = ((tile * kk + (k >> 2)) * 64) + li + 16 * (k & 3);
+    const int m = k >> 5, g = (k >> 3) & 3, e = k & 7;
+    const int64_t off = ((tile * kb + m) * 64 + li + 16 * g) * 8 + e;
     A[off] = a;
     B[off] = b;
   }
 }
 
-// packV[g][jt][lane][q] = V[c = 16g + lane%16][j = 16 jt + 4 (lane/16) + q]
-__global__ void k_pack_rhs(const float* __restrict__ V, int64_t n, int ncols,
-                           int ncg, int64_t ntiles, float* __restrict__ P) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index
-  const int64_t total = (int64_t)ncg * ntiles * 64;
-  if (idx >= total) return;
-  const int lane = (int)(idx & 63);
-  const int64_t jt = (idx >> 6) % ntiles;
-  const int g = (int)((idx >> 6) / ntiles);
-  const int c = 16 * g + (lane & 15);
-  const int64_t j0 = 16 * jt + 4 * (lane >> 4);
-  f4 v = {0.f, 0.f, 0.f, 0.f};
-  if (c < ncols) {
-    const float* col = V + (int64_t)c * n;
+// ---------------------------------------------------------------------------
+// Right-hand sides for the fp16 product O^T += V^T P^T
+//
+// P is formed as P' = 2^kPScaleLog2 * k / os in [2^-13.9, 2^15] (the reference
+// clamp keeps k/os >= e^-20), so P' is a normal fp16 number and its two-term
+// split P' = Ph + Pl (both round-to-nearest fp16) carries 22+ significant bits.
+// Each column of V is scaled by 2^shift_c so max|V'_c| lies in [2^14, 2^15) and
+// split the same way.  Ph.Vh + Ph.Vl + Pl.Vh then reproduces P.V to ~2^-23
+// relative; the dropped Pl.Vl term is below 2^-24.  The result is unscaled
+// exactly by 2^-(shift_c + kPScaleLog2).
+// ---------------------------------------------------------------------------
+constexpr int kPScaleLog2 = 15;
+
+__device__ __forceinline__ int col_shift(uint32_t maxbits) {
+  const float mx = __uint_as_float(maxbits);
+  if (!(mx > 0.0f) || mx > 3.0e38f) return 0;  // zero or non-finite column
+  int e;
+  (void)frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1)
+  return 15 - e;
+}
+
+__global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// colmax[c] = max_j |V[c*n + j]| as float bits (non-negative floats order as
+// unsigned integers).  grid = (chunks, ncols).
+__global__ __launch_bounds__(256) void k_col_absmax(const float* __restrict__ V, int64_t n,
+                                                    uint32_t* __restrict__ colmax) {
+  const int c = blockIdx.y;
+  const float* col = V + (int64_t)c * n;
+  uint32_t mx = 0;
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n;
+       j += (int64_t)gridDim.x * blockDim.x)
+    mx = max(mx, __float_as_uint(fabsf(col[j])));
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = (j0 + q < n) ? col[j0 + q] : 0.0f;
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  if ((threadIdx.x & 63) == 0) atomicMax(colmax + c, mx);
+}
+
+// Vp[((g*upairs + u)*2 + part)*64 + lane] (8 fp16): element e holds
+// V'[c = 16g + lane%16][j = 16 (2u + e/4) + 4 (lane/16) + e%4], part 0 = hi,
+// part 1 = lo.  One thread per (g, u, lane).
+__global__ void k_pack_rhs16(const float* __restrict__ V, int64_t n, int ncols,
+                             int ncg, int64_t upairs, const uint32_t* __restrict__ colmax,
+                             h8* __restrict__ P) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)ncg * upairs * 64) return;
+  const int lane = (int)(idx & 63);
+  const int64_t u = (idx >> 6) % upairs;
+  const int g = (int)((idx >> 6) / upairs);
+  const int c = 16 * g + (lane & 15);
+  h8 hi, lo;
+  const int shift = c < ncols ? col_shift(colmax[c]) : 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t j = 16 * (2 * u + (e >> 2)) + 4 * (lane >> 4) + (e & 3);
+    const float v = (c < ncols && j < n) ? ldexpf(V[(int64_t)c * n + j], shift) : 0.0f;
+    hi[e] = (_Float16)v;
+    lo[e] = (_Float16)(v - (float)hi[e]);
   }
-  reinterpret_cast<f4*>(P)[idx] = v;
+  const int64_t base = ((int64_t)g * upairs + u) * 2;
+  P[base * 64 + lane] = hi;
+  P[(base + 1) * 64 + lane] = lo;
 }
 
 // Single right-hand side: zero padded copy.
@@ -128,36 +209,81 @@ __global__ void k_pad_vec(const float* __restrict__ V, int64_t n, int64_t npad,
   if (j < npad) P[j] = j < n ? V[j] : 0.0f;
 }
 
+// 2^kPScaleLog2 * k / os from the scaled squared distance s, returned as a
+// product f * g (Matern-5/2: polynomial times exponential; RBF: g = 1) so the
+// fp16 split can round the exact product (see split_pair).
+template <int KIND>
+__device__ __forceinline__ void kval_scaled(float s, float clampv, float one, float& f,
+                                            float& g) {
+  constexpr float P = (float)(1 << kPScaleLog2);
+  if constexpr (KIND == KIND_RBF) {
+    const float t = __builtin_amdgcn_fmed3f(s, 0.0f, clampv);
+    f = __builtin_amdgcn_exp2f((float)kPScaleLog2 - t);
+    g = one;
+  } else {
+    const float u = __builtin_amdgcn_sqrtf(fabsf(s));
+    float mn = fminf(u, clampv);
+    asm("" : "+v"(mn));
+    g = __builtin_amdgcn_exp2f(-mn);
+    f = fmaf(u, fmaf(u, kM52B * P, kM52A * P), P);
+  }
+}
+
+// Two-term fp16 split of x0 = f0 g0 and x1 = f1 g1 into packed pairs:
+// hi = RNE16(fl(f g)) (v_cvt_pk_f16_f32), lo = RNE16(f g - hi) from the exact
+// fma inside v_fma_mix{lo,hi}_f16 reading hi's halves via op_sel.  Plain C so
+// the compiler schedules these and tracks their VALU->MFMA hazards.  For the
+// RBF path g is an opaque register 1.0 (keeps the residual an fma).
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+template <bool UNIT_G>
+__device__ __forceinline__ void split_pair(float f0, float g0, float f1, float g1,
+                                           h2& hi, h2& lo) {
+  if constexpr (UNIT_G)
+    hi = __builtin_convertvector((f2){f0, f1}, h2);
+  else
+    hi = __builtin_convertvector((f2){f0 * g0, f1 * g1}, h2);
+  lo[0] = (_Float16)__builtin_fmaf(f0, g0, -(float)hi[0]);
+  lo[1] = (_Float16)__builtin_fmaf(f1, g1, -(float)hi[1]);
+}
+
 // ---------------------------------------------------------------------------
 // MFMA tile kernel
-//   NCG > 0 : NCG groups of 16 right-hand sides accumulated on MFMA
-//   NCG == 0: one right-hand side accumulated on VALU
-//   R       : 16-row tiles per wave
-// grid = (row blocks, splits); each block covers kWaves*R row tiles and the
-// j-tile range [blockIdx.y*jt_per_split, ...).  If `partial` is set, raw sums
-// are written to partial[(split*cpad + c)*mpad + i]; otherwise the epilogue
-// applies os and the noise diagonal and writes out[c*m + i].
+//   NCG > 0 : NCG groups of 16 right-hand sides, fp16 split products on MFMA
+//   NCG == 0: one right-hand side accumulated on VALU (fp32)
+//   R       : 16-row tiles per wave (even)
+// The j loop walks pairs of column tiles (2u, 2u+1): one K=32 fp16 MFMA covers
+// the 32 columns of a pair.  grid = (row blocks, splits); block y covers pairs
+// [y*pairs_per_split, ...).  If `partial` is set, unscaled-by-os sums are
+// written to partial[(split*cpad + c)*mpad + i]; otherwise the epilogue applies
+// os and the noise diagonal and writes out[c*m + i].
 // ---------------------------------------------------------------------------
-template <int KIND, int KK, int NCG, int R>
+template <int KIND, int KB, int NCG, int R>
 __global__ __launch_bounds__(256) void k_fused_tile(
-    const float* __restrict__ Bi, int64_t row_tiles, const float* __restrict__ Aj,
-    const float* __restrict__ Vp, int64_t col_tiles, int64_t jt_per_split,
+    const bf8* __restrict__ Bi, int64_t row_tiles, const bf8* __restrict__ Aj,
+    const void* __restrict__ Vp, int64_t col_pairs, int64_t pairs_per_split,
     int64_t diag_shift, int64_t m, int ncols, float os, float noise,
-    const float* __restrict__ Vin, float* __restrict__ out,
-    float* __restrict__ partial, int64_t mpad, int cpad) {
+    const uint32_t* __restrict__ colmax, const float* __restrict__ Vin,
+    float* __restrict__ out, float* __restrict__ partial, int64_t mpad, int cpad) {
+  static_assert(R % 2 == 0, "row tiles per wave must be even (pair alignment)");
   const int lane = threadIdx.x & 63;
   // Wave index made wave-uniform (SGPR) so the j-loop bounds stay scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t tile0 = ((int64_t)blockIdx.x * kWaves + wave) * R;
   if (tile0 >= row_tiles) return;  // whole wave idle (no barriers used)
 
-  float bi[R][KK];
+  bf8 bi[R][KB];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t it = tile0 + r;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      bi[r][kk] = (it < row_tiles) ? Bi[(it * KK + kk) * 64 + lane] : 0.0f;
+    for (int kb = 0; kb < KB; ++kb) {
+      if (it < row_tiles) {
+        bi[r][kb] = Bi[(it * KB + kb) * 64 + lane];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bi[r][kb][e] = (__bf16)0.0f;
+      }
+    }
   }
 
   constexpr int G = NCG > 0 ? NCG : 1;
@@ -176,58 +302,90 @@ __global__ __launch_bounds__(256) void k_fused_tile(
   }
 
   const float clampv = clamp_reg();
+  float one = 1.0f;
+  asm volatile("" : "+v"(one));
 
   // Lane holds S^T[j = 4(lane/16)+q][i = lane%16] of a 16x16 tile.
   const int li = lane & 15;
   const int lj = 4 * (lane >> 4);
+  const h8* V16 = reinterpret_cast<const h8*>(Vp);
+  const float* V32 = reinterpret_cast<const float*>(Vp);
 
-  // One j tile against the wave's R row tiles.  MASK restores the exact zero
-  // self-distance on diagonal tiles (Gram-form cancellation guard).
-  auto step = [&](int64_t jt, auto mask_tag) {
+  // One pair of j tiles against the wave's R row tiles.  MASK restores the
+  // exact zero self-distance on diagonal tiles (Gram-form cancellation guard).
+  auto step = [&](int64_t u, auto mask_tag) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
-    float aj[KK];
+    const int64_t jt0 = 2 * u;
+    bf8 a0[KB], a1[KB];
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) aj[kk] = Aj[(jt * KK + kk) * 64 + lane];
-    f4 vj[G];
+    for (int kb = 0; kb < KB; ++kb) {
+      a0[kb] = Aj[(jt0 * KB + kb) * 64 + lane];
+      a1[kb] = Aj[((jt0 + 1) * KB + kb) * 64 + lane];
+    }
+    h8 vh[G], vl[G];
+    f4 v0, v1;
     if constexpr (NCG > 0) {
 #pragma unroll
-      for (int g = 0; g < NCG; ++g)
-        vj[g] = reinterpret_cast<const f4*>(Vp)[(g * col_tiles + jt) * 64 + lane];
+      for (int g = 0; g < NCG; ++g) {
+        const int64_t base = ((int64_t)g * col_pairs + u) * 2;
+        vh[g] = V16[base * 64 + lane];
+        vl[g] = V16[(base + 1) * 64 + lane];
+      }
     } else {
-      vj[0] = *reinterpret_cast<const f4*>(Vp + 16 * jt + lj);
+      v0 = *reinterpret_cast<const f4*>(V32 + 16 * jt0 + lj);
+      v1 = *reinterpret_cast<const f4*>(V32 + 16 * jt0 + 16 + lj);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      f4 s = {0.f, 0.f, 0.f, 0.f};
+      f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        s = __builtin_amdgcn_mfma_f32_16x16x4f32(aj[kk], bi[r][kk], s, 0, 0, 0);
+      for (int kb = 0; kb < KB; ++kb) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[kb], bi[r][kb], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[kb], bi[r][kb], s1, 0, 0, 0);
+      }
       if constexpr (MASK) {
-        if (jt == tile0 + r + diag_shift) {
+        const int64_t dt = tile0 + r + diag_shift;
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (li == lj + q) s[q] = 0.0f;
+        for (int q = 0; q < 4; ++q) {
+          if (jt0 == dt && li == lj + q) s0[q] = 0.0f;
+          if (jt0 + 1 == dt && li == lj + q) s1[q] = 0.0f;
         }
       }
-      float p[4];
+      float f0[4], g0[4], f1[4], g1[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) p[q] = kval<KIND>(s[q], clampv);
+      for (int q = 0; q < 4; ++q) {
+        kval_scaled<KIND>(s0[q], clampv, one, f0[q], g0[q]);
+        kval_scaled<KIND>(s1[q], clampv, one, f1[q], g1[q]);
+      }
       if constexpr (NCG > 0) {
+        // B operand halves e = 0..3 from tile jt0, 4..7 from jt0 + 1.
+        h2 hA, hB, hC, hD, lA, lB, lC, lD;
+        split_pair<KIND == KIND_RBF>(f0[0], g0[0], f0[1], g0[1], hA, lA);
+        split_pair<KIND == KIND_RBF>(f0[2], g0[2], f0[3], g0[3], hB, lB);
+        split_pair<KIND == KIND_RBF>(f1[0], g1[0], f1[1], g1[1], hC, lC);
+        split_pair<KIND == KIND_RBF>(f1[2], g1[2], f1[3], g1[3], hD, lD);
+        const h8 ph = {hA[0], hA[1], hB[0], hB[1], hC[0], hC[1], hD[0], hD[1]};
+        const h8 pl = {lA[0], lA[1], lB[0], lB[1], lC[0], lC[1], lD[0], lD[1]};
 #pragma unroll
-        for (int g = 0; g < NCG; ++g)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            acc[r][g] = __builtin_amdgcn_mfma_f32_16x16x4f32(vj[g][q], p[q],
-                                                             acc[r][g], 0, 0, 0);
+        for (int g = 0; g < NCG; ++g) {
+          f4 a = acc[r][g];
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[g], ph, a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl[g], ph, a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[g], pl, a, 0, 0, 0);
+          acc[r][g] = a;
+        }
       } else {
         float a = acc1[r];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) a = fmaf(p[q], vj[0][q], a);
+        for (int q = 0; q < 4; ++q) {
+          a = fmaf(f0[q] * g0[q], v0[q], a);
+          a = fmaf(f1[q] * g1[q], v1[q], a);
+        }
         acc1[r] = a;
       }
     }
   };
-  auto flush = [&]() {
+  auto flush = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if constexpr (NCG > 0) {
@@ -243,25 +401,26 @@ __global__ __launch_bounds__(256) void k_fused_tile(
       }
     }
   };
-  // Plain tiles in chunks of kFlushTiles (no branch in the hot loop), then the
-  // diagonal tiles with the mask.
-  auto run = [&](int64_t a, int64_t b) {
-    for (int64_t c0 = a; c0 < b; c0 += kFlushTiles) {
-      const int64_t e = min(b, c0 + kFlushTiles);
-      for (int64_t jt = c0; jt < e; ++jt) step(jt, std::false_type{});
+  // Plain pairs in chunks of kFlushTiles tiles (no branch in the hot loop),
+  // then the diagonal pairs with the mask.
+  constexpr int kFlushPairs = kFlushTiles / 2;
+  auto run = [&](int64_t a, int64_t b) __attribute__((always_inline)) {
+    for (int64_t c0 = a; c0 < b; c0 += kFlushPairs) {
+      const int64_t e = min(b, c0 + kFlushPairs);
+      for (int64_t u = c0; u < e; ++u) step(u, std::false_type{});
       flush();
     }
   };
 
-  const int64_t jt_begin = (int64_t)blockIdx.y * jt_per_split;
-  const int64_t jt_end = min(col_tiles, jt_begin + jt_per_split);
-  const int64_t dlo = tile0 + diag_shift, dhi = dlo + R;
-  run(jt_begin, min(jt_end, dlo));
-  run(max(jt_begin, dhi), jt_end);
-  for (int64_t jt = max(jt_begin, dlo); jt < min(jt_end, dhi); ++jt) step(jt, std::true_type{});
+  const int64_t u_begin = (int64_t)blockIdx.y * pairs_per_split;
+  const int64_t u_end = min(col_pairs, u_begin + pairs_per_split);
+  const int64_t dlo = (tile0 + diag_shift) / 2, dhi = dlo + R / 2;
+  run(u_begin, min(u_end, dlo));
+  run(max(u_begin, dhi), u_end);
+  for (int64_t u = max(u_begin, dlo); u < min(u_end, dhi); ++u) step(u, std::true_type{});
   flush();
 
-  // Epilogue.
+  // Epilogue: undo the fp16 scaling exactly (powers of two).
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t it = tile0 + r;
@@ -271,9 +430,10 @@ __global__ __launch_bounds__(256) void k_fused_tile(
       for (int g = 0; g < NCG; ++g) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const double tot = accd[r][g][q] + (double)acc[r][g][q];
           const int c = 16 * g + lj + q;
           const int64_t i = 16 * it + li;
+          const int shift = c < ncols ? col_shift(colmax[c]) : 0;
+          const double tot = ldexp(accd[r][g][q] + (double)acc[r][g][q], -(shift + kPScaleLog2));
           if (partial) {
             partial[((int64_t)blockIdx.y * cpad + c) * mpad + i] = (float)tot;
           } else if (c < ncols && i < m) {
@@ -288,6 +448,7 @@ __global__ __launch_bounds__(256) void k_fused_tile(
       // rows are shared by the four lane groups (lane/16): fold them
       tot += __shfl_xor(tot, 16);
       tot += __shfl_xor(tot, 32);
+      tot = ldexp(tot, -kPScaleLog2);
       const int64_t i = 16 * it + li;
       if (lane < 16) {
         if (partial) {
@@ -372,37 +533,37 @@ __global__ __launch_bounds__(256) void k_direct(
 // ---------------------------------------------------------------------------
 // Dispatch tables
 // ---------------------------------------------------------------------------
-using TileFn = void (*)(const float*, int64_t, const float*, const float*,
-                        int64_t, int64_t, int64_t, int64_t, int, float, float,
-                        const float*, float*, float*, int64_t, int);
+using TileFn = void (*)(const bf8*, int64_t, const bf8*, const void*, int64_t,
+                        int64_t, int64_t, int64_t, int, float, float,
+                        const uint32_t*, const float*, float*, float*, int64_t, int);
 
-template <int KIND, int NCG, int R>
-TileFn pick_kk(int kk) {
-  switch (kk) {
-    case 1: return k_fused_tile<KIND, 1, NCG, R>;
-    case 2: return k_fused_tile<KIND, 2, NCG, R>;
-    case 3: return k_fused_tile<KIND, 3, NCG, R>;
-    case 4: return k_fused_tile<KIND, 4, NCG, R>;
-    case 5: return k_fused_tile<KIND, 5, NCG, R>;
-    case 6: return k_fused_tile<KIND, 6, NCG, R>;
-    case 7: return k_fused_tile<KIND, 7, NCG, R>;
-    case 8: return k_fused_tile<KIND, 8, NCG, R>;
+// Row tiles per wave: 4, or 2 where the register budget needs it (more than 16
+// right-hand sides, or more than four distance MFMAs per tile).
+constexpr int rows_per_wave_tiles(int kb, int ncg) { return (ncg >= 2 || kb > 4) ? 2 : 4; }
+
+template <int KIND, int NCG>
+TileFn pick_kb(int kb) {
+  switch (kb) {
+    case 1: return k_fused_tile<KIND, 1, NCG, rows_per_wave_tiles(1, NCG)>;
+    case 2: return k_fused_tile<KIND, 2, NCG, rows_per_wave_tiles(2, NCG)>;
+    case 3: return k_fused_tile<KIND, 3, NCG, rows_per_wave_tiles(3, NCG)>;
+    case 4: return k_fused_tile<KIND, 4, NCG, rows_per_wave_tiles(4, NCG)>;
+    case 5: return k_fused_tile<KIND, 5, NCG, rows_per_wave_tiles(5, NCG)>;
+    case 6: return k_fused_tile<KIND, 6, NCG, rows_per_wave_tiles(6, NCG)>;
   }
   return nullptr;
 }
 
 template <int KIND>
-TileFn pick_tile(int kk, int ncg) {
+TileFn pick_tile(int kb, int ncg) {
   switch (ncg) {
-    case 0: return pick_kk<KIND, 0, 4>(kk);
-    case 1: return pick_kk<KIND, 1, 4>(kk);
-    case 2: return pick_kk<KIND, 2, 4>(kk);
-    case 4: return pick_kk<KIND, 4, 2>(kk);
+    case 0: return pick_kb<KIND, 0>(kb);
+    case 1: return pick_kb<KIND, 1>(kb);
+    case 2: return pick_kb<KIND, 2>(kb);
+    case 4: return pick_kb<KIND, 4>(kb);
   }
   return nullptr;
 }
-
-int rows_per_wave_tiles(int ncg) { return ncg == 4 ? 2 : 4; }
 
 }  // namespace
 
@@ -411,16 +572,19 @@ void pack_points(const float* X_dev, int64_t n, const Coords& co,
   const int d = co.d;
   MGP_REQUIRE(d >= 1, "dimension must be >= 1");
   pp.n = n;
-  pp.ntiles = ceil_div(std::max<int64_t>(n, 1), 16);
-  pp.kk = (int)ceil_div(d + 2, 4);
-  const size_t sz = (size_t)pp.ntiles * pp.kk * 64;
+  // Even tile count: the tile kernel walks column tiles in pairs.
+  pp.ntiles = 2 * ceil_div(std::max<int64_t>(n, 1), 32);
+  // Beyond kMaxMfmaDim only the scaled coordinates are built (direct path).
+  pp.kb = d <= kMaxMfmaDim ? split_mfma_count(d) : 0;
+  const size_t sz = (size_t)pp.ntiles * std::max(pp.kb, 1) * 64 * 4;  // dwords
   pp.A.ensure(sz);
   pp.B.ensure(sz);
   pp.z.ensure((size_t)std::max<int64_t>(n, 1) * d);
   const int64_t threads = pp.ntiles * 16;
   hipLaunchKernelGGL(k_pack_points, dim3((unsigned)ceil_div(threads, 256)),
-                     dim3(256), 0, st, X_dev, n, d, co.coef.ptr, pp.kk,
-                     pp.ntiles, pp.A.ptr, pp.B.ptr, pp.z.ptr);
+                     dim3(256), 0, st, X_dev, n, d, co.coef.ptr, pp.kb,
+                     pp.ntiles, reinterpret_cast<uint16_t*>(pp.A.ptr),
+                     reinterpret_cast<uint16_t*>(pp.B.ptr), pp.z.ptr);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -428,9 +592,9 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,
                   MatvecWorkspace& ws, hipStream_t st, int force_splits) {
   MGP_REQUIRE(a.ncols >= 1, "ncols must be >= 1");
-  MGP_REQUIRE(rows.kk == cols.kk && rows.kk >= 1 && rows.kk <= 8,
+  MGP_REQUIRE(rows.kb == cols.kb && rows.kb >= 1 && rows.kb <= 6,
               "MFMA tile path supports input dimension <= 30");
-  const int kk = rows.kk;
+  const int kb = rows.kb;
   const int64_t row_tiles = rows.ntiles, col_tiles = cols.ntiles;
   const int64_t mpad = row_tiles * 16;
 
@@ -438,24 +602,32 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
   for (int c0 = 0; c0 < a.ncols; c0 += 64) {
     const int nc = std::min(64, a.ncols - c0);
     const int ncg = nc == 1 ? 0 : (nc <= 16 ? 1 : (nc <= 32 ? 2 : 4));
-    const int R = rows_per_wave_tiles(ncg);
+    const int R = rows_per_wave_tiles(kb, ncg);
     const int cpad = ncg == 0 ? 1 : 16 * ncg;
     const float* Vc = V_dev + (int64_t)c0 * a.n;
     float* outc = out_dev + (int64_t)c0 * a.m;
     const float* Vin = a.square ? V_dev + (int64_t)c0 * a.m : nullptr;
 
     // Pack right-hand sides.
+    const int64_t col_pairs = col_tiles / 2;
     float* vp;
+    uint32_t* colmax = nullptr;
     if (ncg == 0) {
       const int64_t npad = col_tiles * 16;
       vp = ws.vpack.ensure((size_t)npad);
       hipLaunchKernelGGL(k_pad_vec, dim3((unsigned)ceil_div(npad, 256)), dim3(256),
                          0, st, Vc, a.n, npad, vp);
     } else {
-      const int64_t total = (int64_t)ncg * col_tiles * 64;
-      vp = ws.vpack.ensure((size_t)total * 4);
-      hipLaunchKernelGGL(k_pack_rhs, dim3((unsigned)ceil_div(total, 256)), dim3(256),
-                         0, st, Vc, a.n, nc, ncg, col_tiles, vp);
+      colmax = ws.colmax.ensure(64);
+      hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, st, colmax, (int64_t)64, 0u);
+      const unsigned chunks = (unsigned)std::min<int64_t>(ceil_div(std::max<int64_t>(a.n, 1), 256), 64);
+      hipLaunchKernelGGL(k_col_absmax, dim3(chunks, (unsigned)nc), dim3(256), 0, st, Vc,
+                         a.n, colmax);
+      const int64_t total = (int64_t)ncg * col_pairs * 64;  // 8-half vectors per part
+      vp = ws.vpack.ensure((size_t)total * 2 * 4);
+      hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256),
+                         0, st, Vc, a.n, nc, ncg, col_pairs, colmax,
+                         reinterpret_cast<h8*>(vp));
     }
     MGP_HIP_CHECK(hipGetLastError());
 
@@ -464,26 +636,27 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
     const int64_t row_blocks = ceil_div(row_tiles, (int64_t)kWaves * R);
     int64_t splits = force_splits > 0 ? force_splits : 1;
     if (force_splits <= 0) {
-      while (row_blocks * splits < 2048 && col_tiles / (splits * 2) >= 32 &&
+      while (row_blocks * splits < 2048 && col_pairs / (splits * 2) >= 16 &&
              splits < 64)
         splits *= 2;
     }
-    const int64_t jt_per_split = ceil_div(col_tiles, splits);
-    splits = ceil_div(col_tiles, jt_per_split);
+    const int64_t pairs_per_split = ceil_div(col_pairs, splits);
+    splits = ceil_div(col_pairs, pairs_per_split);
 
     float* partial = nullptr;
     if (splits > 1)
       partial = ws.partial.ensure((size_t)splits * cpad * mpad);
 
-    TileFn fn = a.kind == KIND_RBF ? pick_tile<KIND_RBF>(kk, ncg)
-                                   : pick_tile<KIND_MATERN52>(kk, ncg);
+    TileFn fn = a.kind == KIND_RBF ? pick_tile<KIND_RBF>(kb, ncg)
+                                   : pick_tile<KIND_MATERN52>(kb, ncg);
     MGP_REQUIRE(fn != nullptr, "no tile kernel for this shape");
     const int64_t diag_shift = a.square ? 0 : (int64_t)1 << 40;
     if (ws.time_tile) MGP_HIP_CHECK(hipEventRecord(ws.ev0, st));
     hipLaunchKernelGGL(fn, dim3((unsigned)row_blocks, (unsigned)splits), dim3(256), 0,
-                       st, rows.B.ptr, row_tiles, cols.A.ptr, vp, col_tiles,
-                       jt_per_split, diag_shift, a.m, nc, a.outputscale, a.noise,
-                       Vin, outc, partial, mpad, cpad);
+                       st, reinterpret_cast<const bf8*>(rows.B.ptr), row_tiles,
+                       reinterpret_cast<const bf8*>(cols.A.ptr), (const void*)vp, col_pairs,
+                       pairs_per_split, diag_shift, a.m, nc, a.outputscale, a.noise,
+                       colmax, Vin, outc, partial, mpad, cpad);
     MGP_HIP_CHECK(hipGetLastError());
     if (ws.time_tile) {
       MGP_HIP_CHECK(hipEventRecord(ws.ev1, st));
