@@ -8,7 +8,10 @@ matvec (K + sigma^2 I) V over the 16 right-hand sides, inputs resident in HBM.
 Work model (per (row, column) pair): F = 2d + 2t + c_k flops (c_k = 9 for
 Matern-5/2, 5 for RBF) plus n_tr transcendentals (2 for Matern-5/2).
 value = N^2 F / (host wall time per step); roofline.achieved uses the HIP-event
-duration of the fused tile kernel measured on the provider's stream.
+duration of the fused tile kernel measured on the provider's stream.  The
+arithmetic is fp32-accurate (distances from an exact three-way bf16 split, the
+K.V product from a two-term fp16 split), so the roofline peak is MI355X's fp32
+dense matrix peak.
 
 The cpu_baseline leg times the C restatement of the reference matvec
 (oracle/cpu_ref, OpenMP) on a bounded sample of rows of the same workload.
@@ -37,7 +40,17 @@ N_TR = 2                       # sqrt + exp per pair
 FLOPS_PER_PAIR = 2 * D + 2 * T + C_K
 # HBM bytes per launch of the tile kernel at this workload: FETCH_SIZE x 2.000 +
 # WRITE_SIZE x 1.000 (copy-kernel calibration), profiles/fused_tile_c3_matvec.md.
-TILE_TRAFFIC_BYTES = 1.504e9
+TILE_TRAFFIC_BYTES = 3.610e9
+
+# Instruction-cost model of the tile kernel, cycles per 16x16 tile of pairs on
+# one SIMD at 2.4 GHz, with per-instruction costs measured on MI355X (16-bit
+# K=32 MFMA 16 cycles, VALU 4, transcendental 8) and MFMA / VALU issue taken as
+# serialized (co-execution covers ~30% of MFMA time in the profile):
+#   MFMA: kb distance MFMAs + 1.5 fp16 product MFMAs (t = 16), kb = ceil(6(d+2)/32)
+#   VALU: 4 pairs per lane x (2 transcendentals x 8 + 5.5 other ops x 4)
+KB = -(-6 * (D + 2) // 32)
+MODEL_CYCLES_PER_TILE = (KB + 1.5) * 16 + 4 * (2 * 8 + 5.5 * 4)
+SIMDS, CLOCK_HZ = 1024, 2.4e9
 
 
 def _make_inputs():
@@ -157,6 +170,7 @@ def main(argv=None) -> int:
     value = pairs * FLOPS_PER_PAIR / (ms_per_step * 1e-3) / 1e12
     achieved = pairs * FLOPS_PER_PAIR / (tile_ms * 1e-3) / 1e12
     t_roof_ms = pairs * (FLOPS_PER_PAIR / (PEAK_FP32_TFLOPS * 1e12) + N_TR / PEAK_TRANS_PER_S) * 1e3
+    t_model_ms = (N / 16) ** 2 / SIMDS * MODEL_CYCLES_PER_TILE / CLOCK_HZ * 1e3
 
     result = {
         "metric": "fused K.V matvec TFLOP/s (N=250k, d=16, t=16, Matern-5/2 ARD)",
@@ -185,6 +199,8 @@ def main(argv=None) -> int:
         "tile_kernel_ms": round(tile_ms, 4),
         "issue_slot_roofline_ms": round(t_roof_ms, 3),
         "issue_slot_roofline_frac": round(t_roof_ms / tile_ms, 4),
+        "issue_model_ms": round(t_model_ms, 3),
+        "issue_model_frac": round(t_model_ms / tile_ms, 4),
     }
     if not args.no_extras:
         it_ms, _ = _mbcg_iteration_ms(X, params, noise)

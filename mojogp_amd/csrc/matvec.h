@@ -32,7 +32,22 @@ struct PackedPoints {
   int kb = 0;          // K=32 bf16 MFMAs per 16x16 distance tile
   DevBuf<uint32_t> A, B;  // two bf16 per dword
   DevBuf<float> z;     // scaled coordinates, row-major [n][d] (direct path)
+  float max_norm = 0.f;      // max_i |z_i|^2 (Gram-form error scale)
+  DevBuf<uint32_t> max_norm_dev;
 };
+
+// Upper bound on max|z_i|^2 + max|z_j|^2 for the Gram-form tile path.  Its
+// distance error is ~2^-23 (|z_i|^2 + |z_j|^2), so the product error grows with
+// the data spread in lengthscales; beyond these bounds (measured product error
+// about 1e-5 at the bound) the products are evaluated from per-dimension
+// differences (direct_matvec) instead.  RBF is more sensitive (dk/ds = -ln2 k
+// against ~-0.08 near 0 for Matern-5/2, and a 14x smaller coordinate scale).
+constexpr float kGramMaxNormSumRBF = 4096.0f;
+constexpr float kGramMaxNormSumM52 = 32768.0f;
+inline bool gram_form_ok(int kind, const PackedPoints& rows, const PackedPoints& cols) {
+  const float bound = kind == KIND_RBF ? kGramMaxNormSumRBF : kGramMaxNormSumM52;
+  return rows.kb > 0 && rows.max_norm + cols.max_norm <= bound;
+}
 
 // Number of K=32 MFMAs for input dimension d: ceil(6 (d + 2) / 32).
 inline int split_mfma_count(int d) { return (6 * (d + 2) + 31) / 32; }

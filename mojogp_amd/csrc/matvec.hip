@@ -21,6 +21,7 @@
 #include "matvec.h"
 
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 namespace mgp {
@@ -71,6 +72,11 @@ __device__ __forceinline__ float kval(float s, float clampv = kExp2Clamp) {
 // ---------------------------------------------------------------------------
 // Packing
 // ---------------------------------------------------------------------------
+__global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 // Exact three-way bf16 split of an fp32 value by truncation: x = hi + mid + lo
 // with each remainder exact in fp32.  Returns the requested part's bits.
 __device__ __forceinline__ uint16_t bf16_part(float x, int part) {
@@ -93,9 +99,10 @@ __constant__ int kPartB[6] = {0, 1, 0, 2, 0, 1};
 __global__ void k_pack_points(const float* __restrict__ X, int64_t n, int d,
                               const float* __restrict__ coef, int kb,
                               int64_t ntiles, uint16_t* __restrict__ A,
-                              uint16_t* __restrict__ B, float* __restrict__ Z) {
+                              uint16_t* __restrict__ B, float* __restrict__ Z,
+                              uint32_t* __restrict__ max_norm) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= ntiles * 16) return;
+  const bool active = i < ntiles * 16;  // no early return: the wave reduces below
   const int li = (int)(i & 15);
   const int64_t tile = i >> 4;
   const bool real = i < n;
@@ -108,6 +115,12 @@ __global__ void k_pack_points(const float* __restrict__ X, int64_t n, int d,
     if (real) Z[i * d + k] = z;
     nrm = fmaf(z, z, nrm);
   }
+  // Wave max of the norms (non-negative floats order as unsigned integers).
+  uint32_t mx = __float_as_uint(nrm);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  if ((threadIdx.x & 63) == 0) atomicMax(max_norm, mx);
+  if (!active) return;
   const int D = d + 2;
   for (int k = 0; k < 32 * kb; ++k) {
     uint16_t a = 0, b = 0;
@@ -154,11 +167,6 @@ __device__ __forceinline__ int col_shift(uint32_t maxbits) {
   int e;
   (void)frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1)
   return 15 - e;
-}
-
-__global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
 }
 
 // colmax[c] = max_j |V[c*n + j]| as float bits (non-negative floats order as
@@ -581,11 +589,17 @@ void pack_points(const float* X_dev, int64_t n, const Coords& co,
   pp.B.ensure(sz);
   pp.z.ensure((size_t)std::max<int64_t>(n, 1) * d);
   const int64_t threads = pp.ntiles * 16;
+  uint32_t* mx = pp.max_norm_dev.ensure(1);
+  hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, st, mx, (int64_t)1, 0u);
   hipLaunchKernelGGL(k_pack_points, dim3((unsigned)ceil_div(threads, 256)),
                      dim3(256), 0, st, X_dev, n, d, co.coef.ptr, pp.kb,
                      pp.ntiles, reinterpret_cast<uint16_t*>(pp.A.ptr),
-                     reinterpret_cast<uint16_t*>(pp.B.ptr), pp.z.ptr);
+                     reinterpret_cast<uint16_t*>(pp.B.ptr), pp.z.ptr, mx);
   MGP_HIP_CHECK(hipGetLastError());
+  uint32_t bits = 0;
+  MGP_HIP_CHECK(hipMemcpyAsync(&bits, mx, sizeof(bits), hipMemcpyDeviceToHost, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  std::memcpy(&pp.max_norm, &bits, sizeof(bits));
 }
 
 void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,

@@ -35,7 +35,7 @@ void Provider::forward(const float* V, int ncols, float* out) {
   a.m = n;
   a.n = n;
   a.ncols = ncols;
-  if (d > kMaxMfmaDim) {
+  if (!gram_form_ok(kind, train, train)) {
     direct_matvec(a, train, train, d, V, out, st);
     return;
   }
@@ -52,7 +52,7 @@ void Provider::cross(const PackedPoints& rows, const float* V, int ncols,
   a.m = rows.n;
   a.n = n;
   a.ncols = ncols;
-  if (d > kMaxMfmaDim) {
+  if (!gram_form_ok(kind, rows, train)) {
     direct_matvec(a, rows, train, d, V, out, st);
     return;
   }

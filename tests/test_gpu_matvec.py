@@ -103,6 +103,32 @@ def test_short_lengthscale_and_update_params():
         p.close()
 
 
+@pytest.mark.parametrize("kind", [ok.RBF, ok.MATERN52])
+def test_spread_far_beyond_lengthscale(kind):
+    """Data spread of ~40 lengthscales: |z|^2 reaches ~1e5, where the Gram-form
+    distance error (~2^-23 |z|^2) would exceed the bar; the provider must route
+    the product through per-dimension differences and stay within it, for the
+    training product and for the cross product."""
+    rng = np.random.default_rng(11)
+    n, m, d, t = 4000, 300, 2, 16
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    Xs = rng.normal(size=(m, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = np.array([0.05, 0.07, 1.3], dtype=np.float32)
+    ref = ok.forward_matvec(kind, X, V, params, 0.05, True)
+    refx = ok.cross_matvec(kind, Xs, X, V, params, True)
+    p = NativeProvider(kind, True, X, params, 0.05)
+    try:
+        got = p.forward_matvec(V)
+        gotx = p.cross_matvec(Xs, V)
+    finally:
+        p.close()
+    print(f"spread/ls ~40: forward relerr {_relerr(got, ref):.3e}, "
+          f"cross relerr {_relerr(gotx, refx):.3e}", flush=True)
+    assert _relerr(got, ref) <= TOL
+    assert _relerr(gotx, refx) <= TOL
+
+
 def test_full_size_c3_sampled_rows():
     """BASELINE config 3 shape (N=250k, d=16, t=16, Matern-5/2 ARD): rows sampled
     across the matrix are compared with the float64 oracle."""
