@@ -196,10 +196,14 @@ MGP_API int mgp_bbmm_eval(void* handle, const float* y, float mean,
 /* Counter-hash Gaussian draws of kernel_gpu_gaussian
  * (pivoted_cholesky.mojo:51-86), computed on the device. */
 MGP_API int mgp_gaussian(int64_t len, uint64_t seed, float* out);
-/* Greedy pivoted Cholesky factor L[rank][n] (column-major, realised rank in
- * rank_out) and log|L L^T + noise I| of
- * build_pivoted_cholesky_precond_unified (pivoted_cholesky.mojo:2104-2444). */
-MGP_API int mgp_pivoted_cholesky(void* handle, int rank, float* L_out,
+/* Pivoted Cholesky factor L[rank][n] (column-major, realised rank in
+ * rank_out) and log|L L^T + noise I| of build_pivoted_cholesky_precond_unified
+ * (pivoted_cholesky.mojo:2104-2444).  method: 0 greedy, 1 rpcholesky,
+ * 2 nystrom; error_tol / adaptive_tol / seed as the reference's arguments
+ * (training uses error_tol 0 for greedy, 1e-3 otherwise; adaptive_tol 0.01,
+ * seed 42). */
+MGP_API int mgp_pivoted_cholesky(void* handle, int rank, int method, float error_tol,
+                                 float adaptive_tol, uint64_t seed, float* L_out,
                                  int* rank_out, float* logdet);
 
 /* ---- Engine: prediction ------------------------------------------------- */
@@ -223,6 +227,13 @@ typedef struct mgp_predict_info {
   int alpha_cache_used;
   int love_root_cache_used;
   int alpha_cg_iterations;
+  /* exact variance (variance_method 2): block width, CG blocks, CG
+   * iterations (total / max per block), realised preconditioner rank */
+  int exact_block_cols;
+  int exact_cg_block_count;
+  int exact_cg_total_iterations;
+  int exact_cg_max_iterations;
+  int exact_precond_rank;
 } mgp_predict_info_t;
 
 /* Predictive mean (and variance) at Xs[m][d].  alpha_in / root_in are the

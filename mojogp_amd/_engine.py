@@ -24,6 +24,18 @@ _DEFAULT_PREDICT_LANCZOS_RANK = 100
 _DEFAULT_ARD_PREDICT_LANCZOS_RANK = 200
 
 
+def _exact_keys(inf, vm: int) -> dict[str, Any]:
+    """Exact-variance diagnostics with the reference's result keys
+    (jit_engine_bindings.mojo:1187-1196); cross mode 1 = direct fill."""
+    if vm != 2:
+        return {}
+    return {"exact_block_cols": int(inf.exact_block_cols), "exact_cross_mode": 1,
+            "exact_cg_block_count": int(inf.exact_cg_block_count),
+            "exact_cg_total_iterations": int(inf.exact_cg_total_iterations),
+            "exact_cg_max_iterations": int(inf.exact_cg_max_iterations),
+            "exact_precond_rank": int(inf.exact_precond_rank)}
+
+
 class KernelModule:
     """Kernel module for one (kernel family, ARD, input dimension)."""
 
@@ -264,6 +276,7 @@ class Engine:
             "love_root_cache_used": bool(inf.love_root_cache_used),
             "alpha_cg_iterations": int(inf.alpha_cg_iterations),
         }
+        out.update(_exact_keys(inf, vm))
         if alpha_in is None:
             out["cached_alpha"] = alpha_out
         if root_out is not None:
@@ -305,11 +318,13 @@ class Engine:
         inf = _lib.PredictInfo()
         _lib.call("mgp_predict_with_cache", prov.handle, C.c_void_p(handle), _lib.fptr(Xs), m, vm,
                   _lib.fptr(mean_out), _lib.fptr(var_out), C.byref(inf))
-        return {"mean": mean_out,
-                "variance": var_out if vm != 0 else np.zeros(m, np.float32),
-                "std": np.sqrt(var_out) if vm != 0 else np.zeros(m, np.float32),
-                "total_time_s": inf.total_time_s, "alpha_cache_used": True,
-                "love_root_cache_used": bool(inf.love_root_cache_used)}
+        out = {"mean": mean_out,
+               "variance": var_out if vm != 0 else np.zeros(m, np.float32),
+               "std": np.sqrt(var_out) if vm != 0 else np.zeros(m, np.float32),
+               "total_time_s": inf.total_time_s, "alpha_cache_used": True,
+               "love_root_cache_used": bool(inf.love_root_cache_used)}
+        out.update(_exact_keys(inf, vm))
+        return out
 
     def destroy_prediction_cache(self, handle) -> bool:
         if handle:

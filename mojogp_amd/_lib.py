@@ -82,6 +82,9 @@ class PredictInfo(C.Structure):
         ("variance_time_s", C.c_double), ("total_time_s", C.c_double),
         ("love_root_time_s", C.c_double), ("alpha_cache_used", C.c_int),
         ("love_root_cache_used", C.c_int), ("alpha_cg_iterations", C.c_int),
+        ("exact_block_cols", C.c_int), ("exact_cg_block_count", C.c_int),
+        ("exact_cg_total_iterations", C.c_int), ("exact_cg_max_iterations", C.c_int),
+        ("exact_precond_rank", C.c_int),
     ]
 
 
@@ -140,7 +143,8 @@ _SIGNATURES = {
                                 C.c_float, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
                                 c_float_p, c_int_p, c_float_p, c_double_p]),
     "mgp_gaussian": (C.c_int, [C.c_int64, C.c_uint64, c_float_p]),
-    "mgp_pivoted_cholesky": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_int_p, c_float_p]),
+    "mgp_pivoted_cholesky": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_float, C.c_float,
+                                       C.c_uint64, c_float_p, c_int_p, c_float_p]),
 }
 
 _lock = threading.Lock()

@@ -21,7 +21,26 @@ struct PredictionCache {
   PredictState state;
   float mean = 0.f;
   int variance_method = 0;
+  ExactVarianceOptions exact;
 };
+
+ExactVarianceOptions exact_options(const mgp_predict_opts_t& o) {
+  ExactVarianceOptions e;
+  e.max_cg_iter = o.max_cg_iter;
+  e.cg_tol = o.cg_tol;
+  e.precond_rank = o.precond_rank;
+  e.block_cols = o.exact_block_cols;
+  return e;
+}
+
+void fill_exact_info(mgp_predict_info_t* info, const ExactVarianceStats& es) {
+  if (!info) return;
+  info->exact_block_cols = es.block_cols;
+  info->exact_cg_block_count = es.block_count;
+  info->exact_cg_total_iterations = es.cg_total_iterations;
+  info->exact_cg_max_iterations = es.cg_max_iterations;
+  info->exact_precond_rank = es.precond_rank;
+}
 
 TrainOptions to_options(const mgp_train_opts_t* o) {
   MGP_REQUIRE(o != nullptr, "null train options");
@@ -152,7 +171,7 @@ int mgp_bbmm_eval(void* handle, const float* y, float mean, int num_probes, int 
     MGP_REQUIRE(y && nll && grads, "null argument");
     const int64_t n = pv->n;
     Precond P;
-    build_precond(*pv, precond_rank, 0, P);
+    build_precond(*pv, precond_rank, training_pivot_options(0), P);
     DevBuf<float> yc;
     yc.ensure(n);
     MGP_HIP_CHECK(hipMemcpyAsync(yc.ptr, y, n * sizeof(float), hipMemcpyHostToDevice, pv->st));
@@ -180,11 +199,18 @@ int mgp_gaussian(int64_t len, uint64_t seed, float* out) {
   });
 }
 
-int mgp_pivoted_cholesky(void* handle, int rank, float* L_out, int* rank_out, float* logdet) {
+int mgp_pivoted_cholesky(void* handle, int rank, int method, float error_tol,
+                         float adaptive_tol, uint64_t seed, float* L_out, int* rank_out,
+                         float* logdet) {
   return guarded([&] {
     Provider* pv = as_provider(handle);
     Precond P;
-    build_precond(*pv, rank, 0, P);
+    PivotOptions po;
+    po.method = method;
+    po.error_tol = error_tol;
+    po.adaptive_tol = adaptive_tol;
+    po.seed = seed;
+    build_precond(*pv, rank, po, P);
     if (rank_out) *rank_out = P.rank;
     if (logdet) *logdet = P.logdet;
     if (L_out && P.rank > 0)
@@ -209,7 +235,11 @@ int mgp_predict(void* handle, const float* y, const float* Xs, int64_t m,
     PredictState ps;
     prepare_state(*pv, y, *opts, alpha_in, root_in, ps, info);
     PredictTimes t;
-    predict_from_state(*pv, ps, Xs, m, opts->mean, opts->variance_method, mean_out, var_out, t);
+    const ExactVarianceOptions eo = exact_options(*opts);
+    ExactVarianceStats es;
+    predict_from_state(*pv, ps, Xs, m, opts->mean, opts->variance_method, mean_out, var_out, t,
+                       &eo, &es);
+    if (opts->variance_method == 2) fill_exact_info(info, es);
     if (alpha_out && !alpha_in)
       MGP_HIP_CHECK(hipMemcpy(alpha_out, ps.alpha.ptr, pv->n * sizeof(float), hipMemcpyDeviceToHost));
     if (root_out && opts->variance_method == 1 && !root_in)
@@ -236,6 +266,7 @@ int mgp_prepare_prediction_cache(void* handle, const float* y, const mgp_predict
       c->owner = pv;
       c->mean = opts->mean;
       c->variance_method = opts->variance_method;
+      c->exact = exact_options(*opts);
       prepare_state(*pv, y, *opts, alpha_in, nullptr, c->state, info);
     } catch (...) {
       delete c;
@@ -258,7 +289,10 @@ int mgp_predict_with_cache(void* handle, void* cache, const float* Xs, int64_t m
     if (info) std::memset(info, 0, sizeof(*info));
     auto t0 = Clock::now();
     PredictTimes t;
-    predict_from_state(*pv, c->state, Xs, m, c->mean, variance_method, mean_out, var_out, t);
+    ExactVarianceStats es;
+    predict_from_state(*pv, c->state, Xs, m, c->mean, variance_method, mean_out, var_out, t,
+                       &c->exact, &es);
+    if (variance_method == 2) fill_exact_info(info, es);
     if (info) {
       info->alpha_cache_used = 1;
       info->love_root_cache_used = variance_method == 1;

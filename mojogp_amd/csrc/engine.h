@@ -27,7 +27,10 @@ struct Precond {
   WoodburyWork work;
 };
 
-void build_precond(Provider& pv, int rank, int method, Precond& P);
+// Pivot options of the training loop for a precond_method (greedy: no trace
+// stop; rpcholesky / nystrom: error_tol 1e-3; adaptive_tol 0.01; seed 42).
+PivotOptions training_pivot_options(int method);
+void build_precond(Provider& pv, int rank, const PivotOptions& po, Precond& P);
 
 struct CGWork {
   DevBuf<float> x, r, z, p, Ap;  // [C][n]
@@ -143,9 +146,29 @@ struct PredictTimes {
   double alpha_s = 0, love_root_s = 0, mean_s = 0, variance_s = 0, total_s = 0;
 };
 
-// mean[m] (+ var[m] when variance_method == 1, LOVE) for test inputs.
+// Exact predictive variance options and statistics
+// (predict_variance_exact_jit, jit_prediction.mojo:1357-1789).
+struct ExactVarianceOptions {
+  int max_cg_iter = 300;
+  float cg_tol = 1e-3f;
+  int precond_rank = 10;   // Nystrom pivoted-Cholesky preconditioner; 0 = none
+  int block_cols = 0;      // 0: all columns when materialized, else <= 512
+};
+struct ExactVarianceStats {
+  int block_cols = 0, block_count = 0, cg_total_iterations = 0, cg_max_iterations = 0;
+  int precond_rank = 0;
+};
+
+// var[j] = k(x*_j, x*_j) - K(X, x*_j)^T (K + noise I)^{-1} K(X, x*_j), clamped
+// at 1e-10, for the packed test set pv.test (device output var_dev[m]).
+void exact_variance(Provider& pv, int64_t m, const ExactVarianceOptions& o, float* var_dev,
+                    ExactVarianceStats& stats);
+
+// mean[m] (+ var[m]: variance_method 1 LOVE, 2 exact) for test inputs.
 void predict_from_state(Provider& pv, const PredictState& ps, const float* Xs_host,
                         int64_t m, float mean, int variance_method, float* mean_out,
-                        float* var_out, PredictTimes& t);
+                        float* var_out, PredictTimes& t,
+                        const ExactVarianceOptions* exact = nullptr,
+                        ExactVarianceStats* exact_stats = nullptr);
 
 }  // namespace mgp

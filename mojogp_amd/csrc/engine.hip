@@ -167,21 +167,25 @@ CGScalars CGWork::scalars(int ncols) {
 }
 
 // ------------------------------------------------------------------ precond
-void build_precond(Provider& pv, int rank, int method, Precond& P) {
+PivotOptions training_pivot_options(int method) {
+  PivotOptions o;
+  o.method = method;
+  o.error_tol = method == 0 ? 0.0f : 1e-3f;  // jit_training.mojo:476-478
+  return o;
+}
+
+void build_precond(Provider& pv, int rank, const PivotOptions& po, Precond& P) {
   P.noise = pv.noise;
   if (rank <= 0) {
     P.rank = 0;
     P.logdet = 0.f;
     return;
   }
-  MGP_REQUIRE(method == 0,
-              "only the greedy pivoted-Cholesky preconditioner (precond_method 0) is "
-              "implemented on gfx950");
   MGP_REQUIRE(rank <= 1000, "preconditioner rank must be <= 1000");
   const int64_t n = pv.n;
   hipStream_t st = pv.st;
   P.L.ensure((size_t)rank * n);
-  const int k = pivoted_cholesky_greedy(pv, rank, P.L.ptr, st);
+  const int k = pivoted_cholesky(pv, rank, po, P.L.ptr, st);
   P.rank = k;
   DevBuf<double> Md;
   Md.ensure((size_t)k * k);
@@ -465,7 +469,7 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
   const int precond_rank = o.use_preconditioner ? o.precond_rank : 0;
   auto rebuild = [&]() {
     auto t0 = Clock::now();
-    build_precond(pv, precond_rank, o.precond_method, Pc);
+    build_precond(pv, precond_rank, training_pivot_options(o.precond_method), Pc);
     res.precond_build_total_ms += secs_since(t0) * 1e3;
     res.precond_build_count += 1;
   };
@@ -755,9 +759,74 @@ void lanczos_inv_root(Provider& pv, int r, PredictState& ps) {
   ps.rank = r;
 }
 
+namespace {
+__global__ void k_exact_var(const double* __restrict__ dots, int C, float diag,
+                            float* __restrict__ var) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < C) var[c] = fmaxf(diag - (float)dots[c], 1e-10f);
+}
+}  // namespace
+
+// Reference: predict_variance_exact_jit / run_exact_variance_blocks_jit /
+// solve_exact_cross_block_jit (jit_prediction.mojo:1357-1789).
+void exact_variance(Provider& pv, int64_t m, const ExactVarianceOptions& o, float* var_dev,
+                    ExactVarianceStats& stats) {
+  hipStream_t st = pv.st;
+  const int64_t n = pv.n;
+  MGP_REQUIRE(pv.test.n == m, "test set is not packed");
+  // choose_exact_prediction_block_cols (:1357-1386)
+  int64_t block = 0;
+  if (o.block_cols > 0) block = std::min<int64_t>(o.block_cols, m);
+  else if (pv.materialized) block = m;
+  else block = std::min<int64_t>(m, 512);
+  stats = ExactVarianceStats{};
+  stats.block_cols = (int)block;
+  // Nystrom preconditioner (build_pivoted_cholesky_precond_unified defaults:
+  // method 2, error_tol 1e-3, adaptive_tol 0.01, seed 42).
+  Precond P;
+  PivotOptions po;
+  po.method = 2;
+  po.error_tol = 1e-3f;
+  build_precond(pv, o.precond_rank, po, P);
+  stats.precond_rank = P.rank;
+  const int nb = reduction_chunks(n);
+  DevBuf<float> Kc, norms, rhsb;
+  DevBuf<double> part, dots;
+  CGWork w;
+  const float os = pv.outputscale();
+  for (int64_t s0 = 0; s0 < m; s0 += block) {
+    const int C = (int)std::min<int64_t>(block, m - s0);
+    const size_t nc = (size_t)n * C;
+    float* kc = Kc.ensure(nc);
+    fill_cross(pv.kind, os, pv.test, s0, C, pv.train, pv.d, kc, st);
+    // RHS = normalised cross columns; solve; rescale (solve_exact_cross_block_jit)
+    float* rhs = rhsb.ensure(nc);
+    copy(rhs, kc, (int64_t)nc, st);
+    float* rn = norms.ensure(C);
+    double* pt = part.ensure((size_t)C * nb);
+    normalize_columns(rhs, n, C, rn, pt, st);
+    w.x.ensure(nc);
+    const CGResult r = batched_cg(pv, P.rank > 0 ? &P : nullptr, rhs, C, o.max_cg_iter, 0,
+                                  o.cg_tol, w, false);
+    scale_columns(w.x.ptr, rn, n, C, false, st);
+    stats.block_count += 1;
+    stats.cg_total_iterations += r.iterations;
+    stats.cg_max_iterations = std::max(stats.cg_max_iterations, r.iterations);
+    // var = k** - <K_cross, solve>, clamped at 1e-10 (kernel_exact_variance, :235-257)
+    double* dd = dots.ensure(C);
+    coldot_partial(kc, w.x.ptr, n, C, nb, pt, st);
+    coldot_finalize(pt, nb, C, dd, st);
+    hipLaunchKernelGGL(k_exact_var, dim3((unsigned)ceil_div(C, 256)), dim3(256), 0, st, dd, C,
+                       os, var_dev + s0);
+    MGP_HIP_CHECK(hipGetLastError());
+  }
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+}
+
 void predict_from_state(Provider& pv, const PredictState& ps, const float* Xs_host, int64_t m,
                         float mean, int variance_method, float* mean_out, float* var_out,
-                        PredictTimes& t) {
+                        PredictTimes& t, const ExactVarianceOptions* exact,
+                        ExactVarianceStats* exact_stats) {
   hipStream_t st = pv.st;
   MGP_REQUIRE(ps.has_alpha, "prediction state has no alpha");
   float* dx = pv.Xs.ensure((size_t)m * pv.d);
@@ -783,7 +852,16 @@ void predict_from_state(Provider& pv, const PredictState& ps, const float* Xs_ho
     MGP_HIP_CHECK(hipStreamSynchronize(st));
     t.variance_s = secs_since(t1);
   } else if (variance_method == 2) {
-    throw Error(ST_INVALID, "exact predictive variance is not implemented on this route yet");
+    auto t1 = Clock::now();
+    ExactVarianceOptions eo = exact ? *exact : ExactVarianceOptions{};
+    ExactVarianceStats es;
+    DevBuf<float> var;
+    var.ensure(m);
+    exact_variance(pv, m, eo, var.ptr, es);
+    MGP_HIP_CHECK(hipMemcpyAsync(var_out, var.ptr, m * sizeof(float), hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    if (exact_stats) *exact_stats = es;
+    t.variance_s = secs_since(t1);
   }
 }
 

@@ -99,6 +99,12 @@ void direct_matvec(const MatvecArgs& a, const PackedPoints& rows,
                    const PackedPoints& cols, int d, const float* V_dev,
                    float* out_dev, hipStream_t st);
 
+// Dense block of K(rows, cols): out[c*cols.n + i] = os k(row r0 + c, col i),
+// c < nrows, from per-dimension differences of the scaled coordinates
+// (fused_fill_cross_covariance, gpu_kernel.py:762-835).
+void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r0,
+                int64_t nrows, const PackedPoints& cols, int d, float* out, hipStream_t st);
+
 // Maximum input dimension served by the MFMA tile path (six K=32 MFMAs).
 constexpr int kMaxMfmaDim = 30;
 

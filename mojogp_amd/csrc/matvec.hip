@@ -538,6 +538,26 @@ __global__ __launch_bounds__(256) void k_direct(
   }
 }
 
+// Dense cross-covariance block: out[c*n + i] = os * k(zr[r0 + c], zc[i]) for
+// c < rows, i < n, from per-dimension differences (reference arithmetic).
+template <int KIND>
+__global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr, int64_t r0,
+                                                    int64_t rows, const float* __restrict__ Zc,
+                                                    int64_t n, int d, float os,
+                                                    float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * n) return;
+  const int64_t c = idx / n, i = idx - c * n;
+  const float* zr = Zr + (r0 + c) * d;
+  const float* zc = Zc + i * d;
+  float r2 = 0.0f;
+  for (int k = 0; k < d; ++k) {
+    const float df = zr[k] - zc[k];
+    r2 = fmaf(df, df, r2);
+  }
+  out[idx] = os * kval<KIND>(r2);
+}
+
 // ---------------------------------------------------------------------------
 // Dispatch tables
 // ---------------------------------------------------------------------------
@@ -704,6 +724,17 @@ void direct_matvec(const MatvecArgs& a, const PackedPoints& rows,
                        a.noise, a.square ? 1 : 0, out_dev + (int64_t)c0 * a.m);
     MGP_HIP_CHECK(hipGetLastError());
   }
+}
+
+void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r0,
+                int64_t nrows, const PackedPoints& cols, int d, float* out, hipStream_t st) {
+  MGP_REQUIRE(r0 >= 0 && nrows >= 0 && r0 + nrows <= rows.n, "cross block out of range");
+  const int64_t total = nrows * cols.n;
+  if (total == 0) return;
+  auto fn = kind == KIND_RBF ? k_fill_cross<KIND_RBF> : k_fill_cross<KIND_MATERN52>;
+  hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, rows.z.ptr,
+                     r0, nrows, cols.z.ptr, cols.n, d, outputscale, out);
+  MGP_HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace mgp

@@ -65,9 +65,28 @@ void gaussian(float* out, int64_t len, uint64_t seed, hipStream_t st);
 // ---------------------------------------------------------------- precond
 struct PivotState;  // device-side pivot bookkeeping
 
-// Greedy pivoted Cholesky of K (pivoted_cholesky.mojo:2104-2444, method 0).
-// L is [rank][n] column-major.  Returns the realized rank.
-int pivoted_cholesky_greedy(Provider& pv, int rank, float* L, hipStream_t st);
+// Pivot selection and stopping rules of the reference's unified builder
+// (pivoted_cholesky.mojo:2104-2444):
+//   method 0 greedy     pivot = argmax residual diagonal (lowest index on ties);
+//                       stop when sum|diag|/diag_value < error_tol
+//   method 1 rpcholesky pivot sampled proportionally to the positive residual
+//                       diagonal with a host xorshift64 stream; same stop rule
+//   method 2 nystrom    rpcholesky sampling; stop when sum|diag| <
+//                       adaptive_tol * n * noise (after the first pivot)
+// Every method stops when the largest residual falls below 1e-10.
+struct PivotOptions {
+  int method = 0;
+  float error_tol = 0.f;
+  float adaptive_tol = 0.01f;
+  uint64_t seed = 42;
+};
+
+// Pivoted Cholesky of K into L [rank][n] (column-major by pivot); returns the
+// realized rank.  Greedy with error_tol = 0 runs without host round trips;
+// the other cases read the pivot statistics (and, when sampling, the residual
+// diagonal) back to the host once per pivot, as the reference does.
+int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
+                     hipStream_t st);
 
 // M = L^T L (k x k, fp64) for the first k columns.
 void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st);

@@ -302,6 +302,37 @@ __global__ void k_pc_select(const float* __restrict__ pv, const int64_t* __restr
   for (int j = threadIdx.x; j < m; j += blockDim.x) coef[j] = L[(int64_t)j * n + p];
 }
 
+// Host-driven selection: merge the argmax/abs-sum partials into `state`.
+__global__ void k_pc_reduce(const float* __restrict__ pv, const int64_t* __restrict__ pi,
+                            const double* __restrict__ pa, int nb,
+                            PivotDev* __restrict__ state) {
+  if (threadIdx.x != 0) return;
+  ArgmaxAcc best{pv[0], pi[0]};
+  double tot = pa[0];
+  for (int b = 1; b < nb; ++b) {
+    best = amax_merge(best, ArgmaxAcc{pv[b], pi[b]});
+    tot += pa[b];
+  }
+  state->stopped = 0;
+  state->pivot = best.idx;
+  state->maxval = best.val;
+  state->sumabs = (float)tot;
+}
+
+// Host-driven selection: install the chosen pivot, mask it and gather the
+// coefficients L[j][p] of the previous columns.
+__global__ void k_pc_setpivot(PivotDev* __restrict__ state, float* __restrict__ mask,
+                              const float* __restrict__ L, int64_t n, int m,
+                              float* __restrict__ coef, int64_t p, float maxval) {
+  if (threadIdx.x == 0) {
+    state->stopped = 0;
+    state->pivot = p;
+    state->maxval = maxval;
+    mask[p] = 0.0f;
+  }
+  for (int j = threadIdx.x; j < m; j += blockDim.x) coef[j] = L[(int64_t)j * n + p];
+}
+
 template <int KIND>
 __global__ __launch_bounds__(256) void k_pc_column(
     const float* __restrict__ Z, int d, int64_t n, float os, int m,
@@ -776,7 +807,9 @@ void gaussian(float* out, int64_t len, uint64_t seed, hipStream_t st) {
   MGP_HIP_CHECK(hipGetLastError());
 }
 
-int pivoted_cholesky_greedy(Provider& pv, int rank, float* L, hipStream_t st) {
+int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
+                     hipStream_t st) {
+  MGP_REQUIRE(o.method >= 0 && o.method <= 2, "precond_method must be 0, 1 or 2");
   const int64_t n = pv.n;
   const int nb = reduction_chunks(n);
   DevBuf<float> diag, mask, coef, pvv;
@@ -793,26 +826,88 @@ int pivoted_cholesky_greedy(Provider& pv, int rank, float* L, hipStream_t st) {
   PivotDev init{0, rank, 0, 0.f, 0.f};
   MGP_HIP_CHECK(hipMemcpyAsync(state.ptr, &init, sizeof(init), hipMemcpyHostToDevice, st));
   fill(L, (int64_t)rank * n, 0.0f, st);
-  hipLaunchKernelGGL(k_pc_init, grid1(n), dim3(kBlock), 0, st, diag.ptr, mask.ptr, n,
-                     pv.outputscale());
+  const float os = pv.outputscale();
+  hipLaunchKernelGGL(k_pc_init, grid1(n), dim3(kBlock), 0, st, diag.ptr, mask.ptr, n, os);
   hipLaunchKernelGGL(k_pc_argmax_part, dim3(nb), dim3(kBlock), 0, st, diag.ptr, mask.ptr,
                      n, nb, pvv.ptr, piv.ptr, pa.ptr);
   MGP_HIP_CHECK(hipGetLastError());
-  const float os = pv.outputscale();
   auto col = pv.kind == KIND_RBF ? k_pc_column<KIND_RBF> : k_pc_column<KIND_MATERN52>;
-  for (int m = 0; m < rank; ++m) {
-    hipLaunchKernelGGL(k_pc_select, dim3(1), dim3(kBlock), 0, st, pvv.ptr, piv.ptr, pa.ptr,
-                       nb, m, state.ptr, mask.ptr, L, n, coef.ptr);
+  auto launch_column = [&](int m) {
     const size_t shm = (size_t)(m + pv.d) * sizeof(float);
     hipLaunchKernelGGL(col, dim3(nb), dim3(kBlock), shm, st, pv.train.z.ptr, pv.d, n, os, m,
                        L, diag.ptr, mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr,
                        pa.ptr);
     MGP_HIP_CHECK(hipGetLastError());
+  };
+
+  if (o.method == 0 && !(o.error_tol > 0.f)) {
+    // Greedy without a trace stop: selection stays on the device.
+    for (int m = 0; m < rank; ++m) {
+      hipLaunchKernelGGL(k_pc_select, dim3(1), dim3(kBlock), 0, st, pvv.ptr, piv.ptr,
+                         pa.ptr, nb, m, state.ptr, mask.ptr, L, n, coef.ptr);
+      launch_column(m);
+    }
+    PivotDev fin;
+    MGP_HIP_CHECK(hipMemcpyAsync(&fin, state.ptr, sizeof(fin), hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    return fin.stopped ? fin.rank : rank;
   }
-  PivotDev fin;
-  MGP_HIP_CHECK(hipMemcpyAsync(&fin, state.ptr, sizeof(fin), hipMemcpyDeviceToHost, st));
+
+  // Host-driven selection (pivoted_cholesky.mojo:2195-2334).
+  const float diag_value = os;  // provider diagonal value k(x, x)
+  const float noise = pv.noise;
+  std::vector<char> used((size_t)n, 0);
+  std::vector<float> dh;
+  uint64_t rng = o.seed;
+  for (int m = 0; m < rank; ++m) {
+    hipLaunchKernelGGL(k_pc_reduce, dim3(1), dim3(64), 0, st, pvv.ptr, piv.ptr, pa.ptr, nb,
+                       state.ptr);
+    PivotDev cur;
+    MGP_HIP_CHECK(hipMemcpyAsync(&cur, state.ptr, sizeof(cur), hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    int64_t pivot = cur.pivot;
+    float maxval = cur.maxval;
+    if (maxval < 1e-10f || pivot < 0) return std::max(m, 1);
+    if (o.method == 2) {
+      const float threshold = o.adaptive_tol * (float)n * noise;
+      if (cur.sumabs < threshold && m > 0) return m;
+    } else if (cur.sumabs / diag_value < o.error_tol) {
+      return std::max(m, 1);
+    }
+    if (o.method != 0) {
+      dh.resize((size_t)n);
+      MGP_HIP_CHECK(hipMemcpyAsync(dh.data(), diag.ptr, (size_t)n * sizeof(float),
+                                   hipMemcpyDeviceToHost, st));
+      MGP_HIP_CHECK(hipStreamSynchronize(st));
+      float total = 0.0f;
+      for (int64_t i = 0; i < n; ++i)
+        if (!used[(size_t)i] && dh[(size_t)i] > 0.0f) total += dh[(size_t)i];
+      if (total < 1e-10f) return std::max(m, 1);
+      rng ^= rng >> 12;
+      rng ^= rng << 25;
+      rng ^= rng >> 27;
+      rng *= 0x2545F4914F6CDD1DULL;
+      float u = (float)(int64_t)(rng & 0x7FFFFFFFULL) / 2147483648.0f;
+      u = u * total;
+      float cumsum = 0.0f;
+      for (int64_t i = 0; i < n; ++i) {
+        if (used[(size_t)i]) continue;
+        const float d = dh[(size_t)i];
+        if (d > 0.0f) cumsum += d;
+        if (cumsum >= u) {
+          pivot = i;
+          maxval = d;
+          break;
+        }
+      }
+    }
+    used[(size_t)pivot] = 1;
+    hipLaunchKernelGGL(k_pc_setpivot, dim3(1), dim3(kBlock), 0, st, state.ptr, mask.ptr, L,
+                       n, m, coef.ptr, pivot, maxval);
+    launch_column(m);
+  }
   MGP_HIP_CHECK(hipStreamSynchronize(st));
-  return fin.stopped ? fin.rank : rank;
+  return rank;
 }
 
 void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st) {

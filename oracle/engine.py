@@ -58,8 +58,27 @@ def gaussian(length: int, seed: int) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- precond
-def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32):
-    """Greedy pivoted Cholesky of the kernel matrix K (no noise). Returns (L [n,k], k).
+def _xorshift64(state: int) -> int:
+    """One step of the sampler's xorshift64* (pivoted_cholesky.mojo:2308-2312)."""
+    m = (1 << 64) - 1
+    state ^= state >> 12
+    state ^= (state << 25) & m
+    state ^= state >> 27
+    return (state * 0x2545F4914F6CDD1D) & m
+
+
+def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32, method: int = 0,
+                     error_tol: float = 0.0, adaptive_tol: float = 0.01, seed: int = 42,
+                     noise: float = 0.0, diag_value=None):
+    """Pivoted Cholesky of the kernel matrix K (no noise). Returns (L [n,k], k).
+
+    Restates build_pivoted_cholesky_precond_unified
+    (pivoted_cholesky.mojo:2104-2444): method 0 greedy (argmax of the residual
+    diagonal), 1 rpcholesky and 2 nystrom (pivot drawn proportionally to the
+    positive residual diagonal with a host xorshift64 stream, sequential fp32
+    sums, :2287-2334).  Stops: residual max < 1e-10; nystrom when
+    sum|diag| < adaptive_tol*n*noise after the first pivot; otherwise when
+    sum|diag| / diag_value < error_tol.
 
     Runs at the reference's working precision (fp32 by default): the residual
     diagonal of far-away points rounds to exactly the outputscale, so many
@@ -68,9 +87,12 @@ def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32):
     n = K.shape[0]
     Kd = np.asarray(K).astype(dtype)
     diag = np.diag(Kd).copy()
+    dval = dtype(diag_value if diag_value is not None else diag.max())
     mask = np.ones(n, dtype=bool)
     L = np.zeros((n, rank), dtype=dtype)
     actual = rank
+    rng = int(seed)
+    f32 = np.float32
     for m in range(rank):
         cand = np.where(mask, diag, dtype(-np.inf))
         p = int(np.argmax(cand))           # first maximum = lowest index on ties
@@ -78,6 +100,29 @@ def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32):
         if not mask.any() or maxval < 1e-10:
             actual = max(m, 1)
             break
+        sumabs = f32(np.abs(diag[mask].astype(np.float64)).sum())
+        if method == 2:
+            if sumabs < f32(adaptive_tol) * f32(n) * f32(noise) and m > 0:
+                actual = m
+                break
+        elif f32(sumabs / f32(dval)) < f32(error_tol):
+            actual = max(m, 1)
+            break
+        if method != 0:
+            d32 = diag.astype(f32)
+            w = np.where(mask & (d32 > 0), d32, f32(0.0)).astype(f32)
+            csum = np.cumsum(w, dtype=f32)      # sequential fp32 accumulation
+            total = csum[-1]
+            if total < f32(1e-10):
+                actual = max(m, 1)
+                break
+            rng = _xorshift64(rng)
+            u = f32(f32(rng & 0x7FFFFFFF) / f32(2147483648.0))
+            u = f32(u * total)
+            hit = np.nonzero(mask & (csum >= u))[0]
+            if hit.size:
+                p = int(hit[0])
+                maxval = diag[p]
         mask[p] = False
         col = Kd[:, p] - L[:, :m] @ L[p, :m]
         L[:, m] = col * (dtype(1.0) / np.sqrt(max(maxval, dtype(1e-10))))
@@ -448,3 +493,44 @@ def predict(kind: int, ard: bool, X, y, Xs, params, noise: float, mean: float, *
     V = Ks @ S
     var = np.maximum(float(np.asarray(params)[-1]) - np.sum(V * V, axis=1), 1e-10)
     return mu, var, alpha
+
+
+def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=300,
+                   tol=1e-3, precond_rank=10, block_cols=0, materialized=False):
+    """Exact predictive variance as the reference computes it
+    (jit_prediction.mojo:1357-1789): test columns in blocks (512 on the
+    matrix-free route, all when materialized, or block_cols), right-hand sides
+    K(X, x*_block) normalised per column, mBCG without tridiagonal under a
+    Nystrom pivoted-Cholesky preconditioner (method 2, error_tol 1e-3,
+    adaptive_tol 0.01, seed 42), then var = k** - <K_cross, solve> clamped at
+    1e-10.  Returns (var, realised preconditioner rank, CG iterations per block)."""
+    X = np.asarray(X, np.float64)
+    Xs = np.asarray(Xs, np.float64)
+    n, m = X.shape[0], Xs.shape[0]
+    K = ok.kernel_matrix(kind, X, X, params, ard)
+    A = K + noise * np.eye(n)
+    os_ = float(np.asarray(params)[-1])
+    if block_cols > 0:
+        block = min(block_cols, m)
+    elif materialized:
+        block = m
+    else:
+        block = min(m, 512)
+    P = None
+    rank = 0
+    if precond_rank > 0:
+        L, rank = pivoted_cholesky(K, precond_rank, method=2, error_tol=1e-3,
+                                   adaptive_tol=0.01, seed=42, noise=noise, diag_value=os_)
+        P = Precond(L, noise)
+    var = np.empty(m)
+    iters = []
+    for s0 in range(0, m, block):
+        Kc = ok.kernel_matrix(kind, X, Xs[s0:s0 + block], params, ard)   # [n, C]
+        norms = np.linalg.norm(Kc, axis=0)
+        norms = np.where(norms > 0, norms, 1.0)
+        x, it, _, _, _ = batched_cg(A, Kc / norms, P, max_cg, 0, tol)
+        sol = x * norms
+        var[s0:s0 + block] = np.maximum(os_ - np.sum(Kc * sol, axis=0), 1e-10)
+        iters.append(it)
+    return var, rank, iters
+

@@ -32,23 +32,39 @@ def test_gaussian_matches_oracle():
         np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-5)
 
 
-def test_pivoted_cholesky_matches_oracle():
+PIVOT_CASES = [
+    # method, error_tol, adaptive_tol, seed, rank
+    (0, 0.0, 0.01, 42, 30),
+    (1, 1e-3, 0.01, 42, 30),
+    (2, 1e-3, 0.01, 42, 400),   # nystrom: adaptive rank below the cap
+    (2, 1e-3, 0.01, 7, 25),
+]
+
+
+@pytest.mark.parametrize("method,error_tol,adaptive_tol,seed,rank", PIVOT_CASES)
+def test_pivoted_cholesky_matches_oracle(method, error_tol, adaptive_tol, seed, rank):
     rng = np.random.default_rng(3)
-    n, d, rank = 400, 3, 30
+    n, d = 400, 3
     X = rng.normal(size=(n, d)).astype(np.float32)
     params = np.array([0.9, 1.2, 0.7, 1.4], np.float32)
-    p = NativeProvider(ok.MATERN52, True, X, params, 0.05)
+    noise = 0.05
+    print(f"pivoted cholesky method={method} rank={rank} seed={seed}", flush=True)
+    p = NativeProvider(ok.MATERN52, True, X, params, noise)
     try:
         L = np.zeros((rank, n), np.float32)
         rk, ld = C.c_int(), C.c_float()
-        _lib.call("mgp_pivoted_cholesky", p.handle, rank, _lib.fptr(L), C.byref(rk), C.byref(ld))
+        _lib.call("mgp_pivoted_cholesky", p.handle, rank, method, error_tol, adaptive_tol,
+                  seed, _lib.fptr(L), C.byref(rk), C.byref(ld))
     finally:
         p.close()
     K = ok.kernel_matrix(ok.MATERN52, X, X, params, True)
-    Lr, kr = oe.pivoted_cholesky(K, rank)
-    P = oe.Precond(Lr, 0.05)
+    Lr, kr = oe.pivoted_cholesky(K, rank, method=method, error_tol=error_tol,
+                                 adaptive_tol=adaptive_tol, seed=seed, noise=noise,
+                                 diag_value=float(params[-1]))
+    P = oe.Precond(Lr, noise)
     assert rk.value == kr
-    assert np.abs(L.T - Lr).max() <= 1e-4 * np.abs(Lr).max()
+    k = kr
+    assert np.abs(L[:k].T - Lr).max() <= 1e-4 * np.abs(Lr).max()
     assert ld.value == pytest.approx(P.logdet, rel=1e-5)
 
 
@@ -121,6 +137,52 @@ def test_predict_love_matches_oracle(tol, mean_bar):
           f"{_rel(mu, exact):.2e}) std relerr {_rel(res['std'], np.sqrt(var)):.2e}", flush=True)
     assert _rel(res["mean"], mu) <= mean_bar
     assert _rel(res["std"], np.sqrt(var)) <= 1e-4
+
+
+EXACT_CASES = [
+    # kind, ard, d, n, m, tol, precond_rank, block_cols, std bar
+    (ok.RBF, False, 2, 800, 64, 1e-6, 0, 0, 1e-4),
+    (ok.MATERN52, True, 3, 900, 700, 1e-6, 40, 0, 1e-4),   # two blocks of <= 512
+    (ok.RBF, True, 2, 700, 100, 1e-3, 30, 48, 2e-2),      # block override, loose tol
+]
+
+
+@pytest.mark.parametrize("kind,ard,d,n,m,tol,rank,block,bar", EXACT_CASES)
+def test_exact_variance_matches_oracle(kind, ard, d, n, m, tol, rank, block, bar):
+    """Exact predictive variance (block CG on K(X, X*) under the Nystrom
+    preconditioner) against the CPU restatement, and at tight tolerance against
+    the dense float64 formula k** - k*^T (K + s I)^{-1} k*."""
+    rng = np.random.default_rng(31 + d + m)
+    X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
+    Xs = rng.uniform(-2.5, 2.5, size=(m, d)).astype(np.float32)
+    y = (np.cos(X).prod(1) + 0.05 * rng.normal(size=n)).astype(np.float32)
+    params = np.concatenate([rng.uniform(0.7, 1.2, d if ard else 1), [1.3]]).astype(np.float32)
+    noise, mean = 0.03, 0.0
+    print(f"exact variance kind={kind} ard={ard} d={d} n={n} m={m} tol={tol} rank={rank} "
+          f"block={block}", flush=True)
+    from mojogp_amd._engine import KernelModule, load_engine
+    km = KernelModule(kind, ard, d)
+    info = km.init_provider(X, params, noise)
+    try:
+        res = load_engine().predict(info, y, Xs, params, noise, mean, 2, 400, tol, rank, 0,
+                                    True, block)
+    finally:
+        km.destroy_provider(info)
+    var, krank, iters = oe.exact_variance(kind, ard, X, Xs, params.astype(np.float64), noise,
+                                          max_cg=400, tol=tol, precond_rank=rank,
+                                          block_cols=block)
+    A = ok.kernel_matrix(kind, X, X, params, ard) + noise * np.eye(n)
+    Ks = ok.kernel_matrix(kind, X, Xs, params, ard)
+    dense = np.maximum(float(params[-1]) - np.sum(Ks * np.linalg.solve(A, Ks), axis=0), 1e-10)
+    print(f"  std relerr vs oracle {_rel(res['std'], np.sqrt(var)):.2e}, oracle vs dense "
+          f"{_rel(np.sqrt(var), np.sqrt(dense)):.2e}; blocks {res['exact_cg_block_count']} "
+          f"iters gpu {res['exact_cg_total_iterations']} oracle {sum(iters)}; "
+          f"rank gpu {res['exact_precond_rank']} oracle {krank}", flush=True)
+    assert res["exact_precond_rank"] == krank
+    assert res["exact_cg_block_count"] == len(iters)
+    assert _rel(res["std"], np.sqrt(var)) <= bar
+    if tol <= 1e-6:
+        assert _rel(res["std"], np.sqrt(dense)) <= bar
 
 
 def test_fit_then_predict_matches_oracle():

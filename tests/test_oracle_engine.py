@@ -93,6 +93,64 @@ def test_fp32_residual_ties_pick_lowest_index():
     assert np.argmax(np.abs(L64[:, 1])) == 3
 
 
+def test_sampled_pivots_exact_on_low_rank():
+    # rpcholesky / nystrom on a rank-5 K: every draw lands on a point with
+    # positive residual, and the factor is exact once the residual vanishes.
+    rng = np.random.default_rng(4)
+    B = rng.normal(size=(80, 5))
+    K = B @ B.T
+    for method in (1, 2):
+        L, k = oe.pivoted_cholesky(K, 12, dtype=np.float64, method=method, error_tol=0.0,
+                                   adaptive_tol=0.0, noise=0.1, diag_value=1.0)
+        assert k == 5
+        np.testing.assert_allclose(L @ L.T, K, atol=1e-8)
+
+
+def test_sampled_pivot_frequencies_follow_residual_diagonal():
+    # First pivot over a diagonal K: drawn with probability d_i / sum d
+    # (chi-square over 4000 seeds).
+    w = np.array([0.5, 1.0, 2.0, 4.0, 0.0, 2.5])
+    K = np.diag(w)
+    counts = np.zeros(w.size)
+    for seed in range(1, 4001):
+        L, _ = oe.pivoted_cholesky(K, 1, method=1, error_tol=0.0, seed=seed, diag_value=1.0)
+        counts[int(np.argmax(np.abs(L[:, 0])))] += 1
+    assert counts[4] == 0
+    expected = w / w.sum() * counts.sum()
+    keep = expected > 0
+    chi2 = ((counts[keep] - expected[keep]) ** 2 / expected[keep]).sum()
+    assert stats.chi2.sf(chi2, keep.sum() - 1) > 1e-3
+
+
+def test_nystrom_adaptive_rank_stops_at_noise_floor():
+    rng = np.random.default_rng(5)
+    X = rng.normal(size=(300, 3))
+    params = np.array([0.8, 1.3])
+    K = ok.kernel_matrix(ok.RBF, X, X, params, False)
+    n, noise, tol = 300, 0.05, 0.01
+    L, k = oe.pivoted_cholesky(K, 300, method=2, adaptive_tol=tol, noise=noise,
+                               diag_value=1.3)
+    assert 1 < k < 300
+    thr = tol * n * noise
+    # The first k pivots reproduce the run; its residual trace is below the
+    # floor and the (k-1)-pivot residual is not (fp32 run, small margin).
+    tr_k = np.trace(K - L @ L.T)
+    tr_km1 = np.trace(K - L[:, :k - 1] @ L[:, :k - 1].T)
+    assert tr_k < thr * (1 + 1e-4)
+    assert tr_km1 >= thr * (1 - 1e-4)
+
+
+def test_rpcholesky_relative_trace_stop():
+    rng = np.random.default_rng(6)
+    X = rng.normal(size=(200, 2))
+    params = np.array([1.1, 1.0])
+    K = ok.kernel_matrix(ok.MATERN52, X, X, params, False)
+    L, k = oe.pivoted_cholesky(K, 200, method=1, error_tol=1e-2, diag_value=1.0)
+    assert 1 < k < 200
+    assert np.trace(K - L @ L.T) / 1.0 < 1e-2 * (1 + 1e-4)
+    assert np.trace(K - L[:, :k - 1] @ L[:, :k - 1].T) >= 1e-2 * (1 - 1e-4)
+
+
 def test_pivot_order_is_greedy_lowest_index():
     K = np.diag([1.0, 3.0, 3.0, 2.0])
     L, k = oe.pivoted_cholesky(K, 2)
@@ -230,3 +288,26 @@ def test_train_reduces_nll():
     h = res["nll_history"]
     assert np.all(np.isfinite(h)) and h[-1] < h[0]
     assert np.all(res["params"] > 0) and res["noise"] > 0
+
+# ------------------------------------------------------------------ exact variance
+def test_exact_variance_matches_dense_formula():
+    rng = np.random.default_rng(8)
+    X = rng.uniform(-2, 2, size=(150, 2))
+    Xs = rng.uniform(-2.5, 2.5, size=(40, 2))
+    params = np.array([0.9, 1.1, 1.3])
+    noise = 0.04
+    A = ok.kernel_matrix(ok.MATERN52, X, X, params, True) + noise * np.eye(150)
+    Ks = ok.kernel_matrix(ok.MATERN52, X, Xs, params, True)
+    dense = 1.3 - np.sum(Ks * np.linalg.solve(A, Ks), axis=0)
+    for rank, block in ((0, 0), (20, 16)):
+        var, k, iters = oe.exact_variance(ok.MATERN52, True, X, Xs, params, noise, max_cg=400,
+                                          tol=1e-8, precond_rank=rank, block_cols=block)
+        np.testing.assert_allclose(var, dense, rtol=1e-6, atol=1e-7)
+        assert len(iters) == (1 if block == 0 else 3)
+    # The Nystrom preconditioner cuts the iteration count.
+    _, _, it0 = oe.exact_variance(ok.MATERN52, True, X, Xs, params, noise, tol=1e-6,
+                                  precond_rank=0)
+    _, _, it1 = oe.exact_variance(ok.MATERN52, True, X, Xs, params, noise, tol=1e-6,
+                                  precond_rank=60)
+    assert it1[0] < it0[0]
+
