@@ -56,6 +56,13 @@ MGP_API int mgp_init_provider(int kind, int ard, int d, int64_t n,
                               float noise, void** out_handle);
 /* Replaces destroy_provider(info) (fn_ptr_module.py:1183-1195). */
 MGP_API int mgp_destroy_provider(void* handle);
+
+/* Select the materialized route: allocate the dense K [n][n] (fp32, 4 n^2
+ * bytes) on the device, fill it, and refill it on every parameter update;
+ * forward products then run as a fp32 GEMM (rocBLAS) plus the noise term.
+ * Replaces materialize(info) / _do_materialize (fn_ptr_module.py:363-384,
+ * 1168-1181). */
+MGP_API int mgp_materialize(void* handle);
 /* Replace the impl_update_params / impl_update_noise / impl_get_noise /
  * impl_get_diagonal_value fn pointers (fn_ptr_module.py:651-703). */
 MGP_API int mgp_update_params(void* handle, const float* params, int nparams);

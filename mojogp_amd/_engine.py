@@ -73,7 +73,10 @@ class KernelModule:
         }
 
     def materialize(self, info: dict) -> bool:
-        """Select the materialized route for this provider (dense K on device)."""
+        """Select the materialized route: dense K on the device, refilled on
+        every parameter update, products by fp32 GEMM
+        (materialize / _do_materialize, fn_ptr_module.py:363-384, 1168-1181)."""
+        _provider(info).materialize()
         info["materialization_mode"] = 1
         return True
 

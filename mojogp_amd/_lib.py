@@ -109,6 +109,7 @@ _SIGNATURES = {
     "mgp_init_provider": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int64, c_float_p,
                                     c_float_p, C.c_int, C.c_float, c_void_pp]),
     "mgp_destroy_provider": (C.c_int, [C.c_void_p]),
+    "mgp_materialize": (C.c_int, [C.c_void_p]),
     "mgp_update_params": (C.c_int, [C.c_void_p, c_float_p, C.c_int]),
     "mgp_update_noise": (C.c_int, [C.c_void_p, C.c_float]),
     "mgp_get_noise": (C.c_int, [C.c_void_p, c_float_p]),

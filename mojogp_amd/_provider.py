@@ -94,6 +94,10 @@ class NativeProvider:
                   _lib.fptr(out))
         return out[0] if vec else out
 
+    def materialize(self) -> None:
+        """Switch to the dense-K route (K held on the device, 4 n^2 bytes)."""
+        _lib.call("mgp_materialize", self.handle)
+
     def cross_matvec(self, Xs, V) -> np.ndarray:
         Xs = _lib.f32(Xs)
         if Xs.ndim != 2 or Xs.shape[1] != self.d:

@@ -44,6 +44,11 @@ HIP_FLAGS = [
 ]
 
 
+# rocBLAS serves the plain fp32 GEMM of the materialized route (dense K times
+# the right-hand sides).
+LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -72,7 +77,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         objs = list(ex.map(_compile_one, sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objs)]
+           *map(str, objs), *LINK_LIBS]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")

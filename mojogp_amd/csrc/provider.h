@@ -32,9 +32,11 @@ struct Provider {
   PackedPoints test;
   DevBuf<float> Xs;
 
-  // Dense K (materialized route), row-major [n][n].
+  // Dense K (materialized route), row-major [n][n] (symmetric, so also
+  // column-major), refilled on every parameter update.
   bool materialized = false;
   DevBuf<float> K;
+  void* blas = nullptr;  // rocblas_handle bound to `st` (materialized route)
 
   float outputscale() const { return params[nparams - 1]; }
   float lengthscale(int k) const { return ard ? params[k] : params[0]; }
@@ -43,6 +45,11 @@ struct Provider {
   void refresh_coords();
   // Pack an arbitrary point set with the current coordinate map.
   void pack(const float* X_dev, int64_t m, PackedPoints& pp);
+
+  // Allocate and fill the dense K (materialized route, _do_materialize).
+  void materialize();
+  void fill_dense();
+  void release_blas();
 
   // (K + noise I) V  for device arrays V, out ([ncols][n] column-major).
   void forward(const float* V, int ncols, float* out);

@@ -1,6 +1,8 @@
 // Provider state management and the matvec entry points it serves.
 #include "provider.h"
 
+#include <rocblas/rocblas.h>
+
 #include <algorithm>
 #include <cmath>
 
@@ -20,6 +22,49 @@ void Provider::refresh_coords() {
   MGP_HIP_CHECK(hipMemcpyAsync(co.coef.ptr, coef.data(), coef.size() * sizeof(float),
                                hipMemcpyHostToDevice, st));
   pack_points(X.ptr, n, co, train, st);
+  if (materialized) fill_dense();
+}
+
+namespace {
+#define MGP_BLAS_CHECK(expr)                                                        \
+  do {                                                                              \
+    const rocblas_status s_ = (expr);                                               \
+    if (s_ != rocblas_status_success)                                               \
+      throw Error(ST_HIP, std::string("rocBLAS error in " #expr ": ") +             \
+                              rocblas_status_to_string(s_));                        \
+  } while (0)
+
+__global__ void k_scaled_copy(float* __restrict__ y, const float* __restrict__ x, float a,
+                              int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = a * x[i];
+}
+}  // namespace
+
+void Provider::fill_dense() {
+  fill_cross(kind, outputscale(), train, 0, n, train, d, K.ptr, st);
+}
+
+void Provider::materialize() {
+  if (!materialized) {
+    const double bytes = (double)n * (double)n * sizeof(float);
+    MGP_REQUIRE(bytes <= 200e9, "dense K of this size does not fit the device");
+    K.ensure((size_t)n * (size_t)n);
+    if (!blas) {
+      rocblas_handle h = nullptr;
+      MGP_BLAS_CHECK(rocblas_create_handle(&h));
+      blas = h;
+      MGP_BLAS_CHECK(rocblas_set_stream(h, st));
+    }
+    materialized = true;
+  }
+  fill_dense();
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+}
+
+void Provider::release_blas() {
+  if (blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(blas));
+  blas = nullptr;
 }
 
 void Provider::pack(const float* X_dev, int64_t m, PackedPoints& pp) {
@@ -35,6 +80,20 @@ void Provider::forward(const float* V, int ncols, float* out) {
   a.m = n;
   a.n = n;
   a.ncols = ncols;
+  if (materialized) {
+    // out = noise V, then out += K V (rocBLAS sgemm, fp32; K symmetric so its
+    // row-major storage is the column-major operand).
+    const int64_t total = n * (int64_t)ncols;
+    hipLaunchKernelGGL(k_scaled_copy, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                       out, V, noise, total);
+    MGP_HIP_CHECK(hipGetLastError());
+    const float one = 1.0f;
+    MGP_BLAS_CHECK(rocblas_sgemm(static_cast<rocblas_handle>(blas), rocblas_operation_none,
+                                 rocblas_operation_none, (rocblas_int)n, ncols, (rocblas_int)n,
+                                 &one, K.ptr, (rocblas_int)n, V, (rocblas_int)n, &one, out,
+                                 (rocblas_int)n));
+    return;
+  }
   if (!gram_form_ok(kind, train, train)) {
     direct_matvec(a, train, train, d, V, out, st);
     return;

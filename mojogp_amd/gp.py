@@ -606,6 +606,8 @@ class SingleOutputGP:
             "alpha_cache_used": bool(res.get("alpha_cache_used", False)),
             "love_root_cache_used": bool(res.get("love_root_cache_used", False)),
         }
+        self._backend_predict_info.update(
+            {k: v for k, v in res.items() if k.startswith("exact_")})
         if target == "observed":
             obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
             if obs.shape != (X.shape[0],):

@@ -185,6 +185,38 @@ def test_exact_variance_matches_oracle(kind, ard, d, n, m, tol, rank, block, bar
         assert _rel(res["std"], np.sqrt(dense)) <= bar
 
 
+def test_materialized_fit_and_exact_variance():
+    """Materialized route end to end at small n: the fit follows the same Adam
+    trajectory as the CPU restatement, and exact variance solves all test
+    columns as one block."""
+    rng = np.random.default_rng(12)
+    n, d, m = 600, 2, 96
+    X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
+    y = (np.cos(X).prod(1) + 0.05 * rng.normal(size=n)).astype(np.float32)
+    Xs = rng.uniform(-2.5, 2.5, size=(m, d)).astype(np.float32)
+    from mojogp_amd import RBF, SingleOutputGP
+    gp = SingleOutputGP(RBF())
+    tr = gp.fit(X, y, max_iterations=15, method="materialized", initial_params=[0.7, 1.0],
+                preconditioner_rank=0)
+    assert gp.backend_train_info["materialization_mode"] == 1
+    ref = oe.train(ok.RBF, False, X, y, [0.7, 1.0], 0.1, max_iterations=15, num_probes=10,
+                   max_cg=100, cg_tol=1e-2, precond_rank=0, max_tridiag=30)
+    print(f"materialized fit params {tr.params} vs {ref['params']}, noise {tr.noise} vs "
+          f"{ref['noise']}", flush=True)
+    np.testing.assert_allclose(tr.params, ref["params"], rtol=2e-3)
+    assert tr.noise == pytest.approx(ref["noise"], rel=2e-3)
+    res = gp.predict(Xs, return_std=True, variance_method="exact")
+    mean, std = res if isinstance(res, tuple) else (res.mean, res.std)
+    info = gp.backend_predict_info or {}
+    assert info.get("exact_block_cols", m) == m
+    params = np.asarray(tr.params, np.float64)
+    A = ok.kernel_matrix(ok.RBF, X, X, params, False) + tr.noise * np.eye(n)
+    Ks = ok.kernel_matrix(ok.RBF, X, Xs, params, False)
+    dense = np.maximum(params[-1] - np.sum(Ks * np.linalg.solve(A, Ks), axis=0), 1e-10)
+    print(f"  exact std relerr vs dense {_rel(std, np.sqrt(dense)):.2e}", flush=True)
+    assert _rel(std, np.sqrt(dense)) <= 5e-3
+
+
 def test_fit_then_predict_matches_oracle():
     """Hello-world shape at small n: the whole Adam trajectory on the GPU vs the
     CPU restatement (same probes, same stop rules)."""

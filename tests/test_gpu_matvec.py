@@ -129,6 +129,33 @@ def test_spread_far_beyond_lengthscale(kind):
     assert _relerr(gotx, refx) <= TOL
 
 
+@pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, False, 4, 3000, 16),
+                                            (ok.MATERN52, True, 3, 2048, 1),
+                                            (ok.RBF, True, 2, 1500, 40)])
+def test_materialized_route_parity(kind, ard, d, n, t):
+    """Dense K filled on the device, products by fp32 GEMM (+ noise V); refilled
+    after a parameter update."""
+    rng = np.random.default_rng(40 + d + t)
+    X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = _params(rng, d, ard)
+    print(f"materialized case kind={kind} ard={ard} d={d} n={n} t={t}", flush=True)
+    p = NativeProvider(kind, ard, X, params, 0.07)
+    try:
+        p.materialize()
+        got = p.forward_matvec(V)
+        params2 = _params(rng, d, ard, 0.3, 0.9, os=0.6)
+        p.update_params(params2)
+        got2 = p.forward_matvec(V)
+    finally:
+        p.close()
+    ref = ok.forward_matvec(kind, X, V, params, 0.07, ard)
+    ref2 = ok.forward_matvec(kind, X, V, params2, 0.07, ard)
+    print(f"  relerr {_relerr(got, ref):.3e}, after update {_relerr(got2, ref2):.3e}", flush=True)
+    assert _relerr(got, ref) <= TOL
+    assert _relerr(got2, ref2) <= TOL
+
+
 def test_full_size_c3_sampled_rows():
     """BASELINE config 3 shape (N=250k, d=16, t=16, Matern-5/2 ARD): rows sampled
     across the matrix are compared with the float64 oracle."""
