@@ -96,11 +96,19 @@ MGP_API int mgp_extract_diagonal(void* handle, float* out);
 MGP_API int mgp_extract_diagonal_test(void* handle, const float* Xs, int64_t m,
                                       float* out);
 
+/* out[p][c][i] = sum_j dk(x_i, x_j)/dtheta_p V[c][j] for the P engine
+ * parameters [l | l_0..l_{d-1}, os] (out is [P][ncols][n]).  Replaces the
+ * fused_gradient_matvec / gradient_matvec fn pointers (fn_ptr_module.py:
+ * 493-541; kernels gpu_kernel.py:382-484, 878-975). */
+MGP_API int mgp_gradient_matvec(void* handle, const float* V, int ncols, float* out);
+
 /* Isolated timing of provider ops.  Replaces benchmark_provider_ops(info, rhs,
  * num_cols, op_code, repeats, warmup) (jit_engine_bindings.mojo:439-572);
- * op 0 = forward matvec.  times_ms[repeats] gets per-call host wall times,
- * tile_ms_avg the mean HIP-event duration of the fused tile kernel, and
- * out_or_null (if non-null) the last output. */
+ * op 0 forward matvec, 1 fused gradient products, 2 gradient products + the
+ * per-(parameter, column) dots <rhs_c, out_pc>, 3 the dots alone.
+ * times_ms[repeats] gets per-call host wall times, tile_ms_avg the mean
+ * HIP-event duration of the fused tile kernel (op 0), and out_or_null (if
+ * non-null) the last output ([ncols][n] for op 0, [P][ncols][n] otherwise). */
 MGP_API int mgp_benchmark_provider_ops(void* handle, const float* rhs,
                                        int ncols, int op, int repeats,
                                        int warmup, double* times_ms,

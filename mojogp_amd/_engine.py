@@ -336,15 +336,23 @@ class Engine:
 
     # ------------------------------------------------------------ bench
     def benchmark_provider_ops(self, info, rhs, num_cols, op_code, repeats, warmup) -> dict:
-        if int(op_code) != 0:
-            raise ValueError("op_code must be 0 (forward) on this engine")
+        """jit_engine_bindings.mojo:439-572: op 0 forward, 1 fused gradient,
+        2 fused gradient + dots, 3 dots only after one gradient pass."""
+        op = int(op_code)
+        if op < 0 or op > 3:
+            raise ValueError("op_code must be one of 0, 1, 2, 3")
         prov = _provider(info)
-        V = _lib.f32(rhs).reshape(int(num_cols), prov.n)
-        times, tile_ms, out = prov.benchmark_forward(V, int(repeats), int(warmup))
-        return {"n": prov.n, "num_cols": int(num_cols), "num_params": prov.nparams,
-                "op_code": 0, "repeats": int(repeats), "warmup": int(warmup),
-                "times_ms": [float(t) for t in times], "tile_kernel_ms": tile_ms,
-                "output_column_major": out.ravel()}
+        V = _lib.f32(rhs)
+        if V.size != prov.n * int(num_cols):
+            raise ValueError("rhs size does not match n * num_cols")
+        V = V.reshape(int(num_cols), prov.n)
+        times, tile_ms, out = prov.benchmark_op(V, op, int(repeats), int(warmup))
+        res = {"n": prov.n, "num_cols": int(num_cols), "num_params": prov.nparams,
+               "op_code": op, "repeats": int(repeats), "warmup": int(warmup),
+               "times_ms": [float(t) for t in times], "tile_kernel_ms": tile_ms}
+        if op == 0:
+            res["output_column_major"] = out.ravel()
+        return res
 
 
 _ENGINE = Engine()

@@ -116,11 +116,26 @@ class NativeProvider:
 
     def benchmark_forward(self, V, repeats: int, warmup: int):
         """(per-call wall ms array, mean tile-kernel ms, output)."""
+        return self.benchmark_op(V, 0, repeats, warmup)
+
+    def benchmark_op(self, V, op: int, repeats: int, warmup: int):
+        """benchmark_provider_ops: op 0 forward, 1 gradient products, 2 gradient
+        products + dots, 3 dots only.  Returns (wall ms per call, mean tile ms
+        (op 0), last output ([C, n] for op 0, [P, C, n] otherwise))."""
         Vc, _ = _cols(V, self.n)
         times = np.zeros(repeats, dtype=np.float64)
         tile = C.c_double(0.0)
-        out = np.empty_like(Vc)
+        shape = Vc.shape if op == 0 else (self.nparams,) + Vc.shape
+        out = np.empty(shape, dtype=np.float32)
         _lib.call("mgp_benchmark_provider_ops", self.handle, _lib.fptr(Vc), Vc.shape[0],
-                  0, int(repeats), int(warmup), _lib.dptr(times), C.byref(tile),
+                  int(op), int(repeats), int(warmup), _lib.dptr(times), C.byref(tile),
                   _lib.fptr(out))
         return times, float(tile.value), out
+
+    def gradient_matvec(self, V) -> np.ndarray:
+        """out[p, c, i] = sum_j dk_p(x_i, x_j) V[c, j] for the P engine parameters."""
+        Vc, vec = _cols(V, self.n)
+        out = np.empty((self.nparams, Vc.shape[0], self.n), dtype=np.float32)
+        _lib.call("mgp_gradient_matvec", self.handle, _lib.fptr(Vc), Vc.shape[0],
+                  _lib.fptr(out))
+        return out[:, 0, :] if vec else out

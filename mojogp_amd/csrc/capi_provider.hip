@@ -7,6 +7,7 @@
 
 #include "mojogp_amd.h"
 #include "provider.h"
+#include "solver.h"
 
 namespace mgp {
 
@@ -246,6 +247,21 @@ int mgp_extract_diagonal_test(void* h, const float* Xs, int64_t m, float* out) {
 // op 0: forward matvec (the north-star unit).  times_ms[r] is the host wall
 // time of repeat r (launch + device + sync); tile_ms_avg receives the mean
 // HIP-event duration of the fused tile kernel over the repeats.
+int mgp_gradient_matvec(void* h, const float* V, int ncols, float* out) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(V && out && ncols >= 1, "bad arguments");
+    const size_t tot = (size_t)pv->n * ncols;
+    const size_t outn = tot * (size_t)pv->nparams;
+    float* dv = pv->io_a.ensure(tot);
+    float* dout = pv->io_b.ensure(outn);
+    MGP_HIP_CHECK(hipMemcpyAsync(dv, V, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    pv->gradient(dv, ncols, dout);
+    MGP_HIP_CHECK(hipMemcpyAsync(out, dout, outn * sizeof(float), hipMemcpyDeviceToHost, pv->st));
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
 int mgp_benchmark_provider_ops(void* h, const float* rhs, int ncols, int op,
                                int repeats, int warmup, double* times_ms,
                                double* tile_ms_avg, float* out_or_null) {
@@ -254,12 +270,46 @@ int mgp_benchmark_provider_ops(void* h, const float* rhs, int ncols, int op,
     MGP_REQUIRE(ncols >= 1, "num_cols must be positive");
     MGP_REQUIRE(repeats >= 1, "repeats must be positive");
     MGP_REQUIRE(warmup >= 0, "warmup must be non-negative");
-    MGP_REQUIRE(op == 0, "op_code must be 0 (forward)");
+    MGP_REQUIRE(op >= 0 && op <= 3, "op_code must be one of 0, 1, 2, 3");
     const size_t tot = (size_t)pv->n * ncols;
     float* dv = pv->io_a.ensure(tot);
-    float* dout = pv->io_b.ensure(tot);
+    float* dout = pv->io_b.ensure(op == 0 ? tot : tot * (size_t)pv->nparams);
     MGP_HIP_CHECK(hipMemcpyAsync(dv, rhs, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
     MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+    if (op != 0) {
+      // ops 1-3 (jit_engine_bindings.mojo:494-540): fused gradient products,
+      // + the quadratic forms dots[p][c] = <rhs_c, out_pc>, or the dots alone
+      // after one gradient pass.
+      const int P = pv->nparams;
+      const int nb = reduction_chunks(pv->n);
+      DevBuf<double> part, dots;
+      part.ensure((size_t)ncols * nb);
+      dots.ensure((size_t)P * ncols);
+      auto dots_pass = [&]() {
+        for (int p = 0; p < P; ++p) {
+          coldot_partial(dv, dout + (size_t)p * tot, pv->n, ncols, nb, part.ptr, pv->st);
+          coldot_finalize(part.ptr, nb, ncols, dots.ptr + (size_t)p * ncols, pv->st);
+        }
+      };
+      auto run = [&]() {
+        if (op != 3) pv->gradient(dv, ncols, dout);
+        if (op != 1) dots_pass();
+        MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+      };
+      if (op == 3) pv->gradient(dv, ncols, dout);
+      for (int w = 0; w < warmup; ++w) run();
+      for (int r = 0; r < repeats; ++r) {
+        auto t0 = std::chrono::steady_clock::now();
+        run();
+        auto t1 = std::chrono::steady_clock::now();
+        if (times_ms) times_ms[r] = std::chrono::duration<double, std::milli>(t1 - t0).count();
+      }
+      if (tile_ms_avg) *tile_ms_avg = 0.0;
+      if (out_or_null)
+        MGP_HIP_CHECK(hipMemcpy(out_or_null, dout, tot * (size_t)P * sizeof(float),
+                                hipMemcpyDeviceToHost));
+      return;
+    }
     for (int w = 0; w < warmup; ++w) pv->forward(dv, ncols, dout);
     MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
     if (!pv->ws.ev0) MGP_HIP_CHECK(hipEventCreate(&pv->ws.ev0));

@@ -105,6 +105,14 @@ void direct_matvec(const MatvecArgs& a, const PackedPoints& rows,
 void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r0,
                 int64_t nrows, const PackedPoints& cols, int d, float* out, hipStream_t st);
 
+// out[p][c][i] = sum_j dk(x_i, x_j)/dtheta_p V[c][j] for the P engine
+// parameters ([l | l_0..l_{d-1}, os]); pscale_dev[p] converts the per-pair sums
+// (h |dz|^2 terms, k/os terms) into derivatives: 1/(s^2 l_p) for lengthscales
+// (times os), 1 for the outputscale (see the kernel's comment).
+void gradient_matvec(int kind, bool ard, const PackedPoints& pts, int d, float outputscale,
+                     const float* pscale_dev, const float* V_dev, int ncols, float* out_dev,
+                     hipStream_t st);
+
 // Maximum input dimension served by the MFMA tile path (six K=32 MFMAs).
 constexpr int kMaxMfmaDim = 30;
 

@@ -559,6 +559,100 @@ __global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr
 }
 
 // ---------------------------------------------------------------------------
+// Gradient products: out[p][c][i] = sum_j dk(x_i, x_j)/dtheta_p V[c][j] for the
+// engine parameters theta = [l | l_0..l_{d-1}, os] (fused_all_gradients_matvec,
+// gpu_kernel.py:382-484).  Per pair, from per-dimension differences dz of the
+// scaled coordinates (dz = diff * s / l):
+//   RBF       h = k (clamped);  Matern-5/2  h = (5/3) os (1 + sqrt5 r) e^{max(-sqrt5 r, -20)}
+//   dk/dl_q = h dz_q^2 / (s^2 l_q)   (iso: h |dz|^2 / (s^2 l))
+//   dk/dos  = k / os
+// One thread per row, LDS tiles of column points, kGradCols right-hand sides
+// per pass, fp32 sums flushed into fp64 every tile.
+// ---------------------------------------------------------------------------
+constexpr int kGradTile = 64;
+constexpr int kGradCols = 2;
+constexpr int kGradMaxDim = 32;
+
+template <int KIND, bool ARD>
+__global__ __launch_bounds__(256) void k_grad_matvec(
+    const float* __restrict__ Z, int64_t n, int d, const float* __restrict__ V, int ncols,
+    int c0, float os, const float* __restrict__ pscale, float* __restrict__ out) {
+  extern __shared__ float sm[];  // [kGradTile][d + kGradCols]
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int w = d + kGradCols;
+  const int np = ARD ? d + 1 : 2;
+  float zi[kGradMaxDim];
+  for (int k = 0; k < d; ++k) zi[k] = (i < n) ? Z[i * d + k] : 0.0f;
+  double accd[(kGradMaxDim + 1) * kGradCols];
+  float acc[(kGradMaxDim + 1) * kGradCols];
+  for (int q = 0; q < np * kGradCols; ++q) {
+    accd[q] = 0.0;
+    acc[q] = 0.0f;
+  }
+  for (int64_t j0 = 0; j0 < n; j0 += kGradTile) {
+    __syncthreads();
+    for (int t = threadIdx.x; t < kGradTile * w; t += blockDim.x) {
+      const int jj = t / w, k = t - jj * w;
+      const int64_t j = j0 + jj;
+      float val = 0.0f;
+      if (j < n) {
+        if (k < d) {
+          val = Z[j * d + k];
+        } else {
+          const int c = c0 + (k - d);
+          val = c < ncols ? V[(int64_t)c * n + j] : 0.0f;
+        }
+      }
+      sm[t] = val;
+    }
+    __syncthreads();
+    const int cnt = (int)min((int64_t)kGradTile, n - j0);
+    for (int jj = 0; jj < cnt; ++jj) {
+      const float* row = sm + jj * w;
+      float dz2[kGradMaxDim];
+      float S = 0.0f;
+      for (int k = 0; k < d; ++k) {
+        const float df = zi[k] - row[k];
+        dz2[k] = df * df;
+        S += dz2[k];
+      }
+      const float kv = kval<KIND>(S);  // k / os
+      float h;
+      if constexpr (KIND == KIND_RBF) {
+        h = kv;
+      } else {
+        // (5/3)(1 + sqrt5 r) e^{max(-sqrt5 r,-20)} with sqrt5 r = u ln2, u = sqrt(S)
+        const float u = sqrtf(S);
+        const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+        h = (5.0f / 3.0f) * fmaf(u, kLn2, 1.0f) * e;
+      }
+      for (int c = 0; c < kGradCols; ++c) {
+        const float v = row[d + c];
+        const float hv = h * v;
+        if constexpr (ARD) {
+          for (int q = 0; q < d; ++q) acc[q * kGradCols + c] = fmaf(hv, dz2[q], acc[q * kGradCols + c]);
+        } else {
+          acc[c] = fmaf(hv, S, acc[c]);
+        }
+        acc[(np - 1) * kGradCols + c] = fmaf(kv, v, acc[(np - 1) * kGradCols + c]);
+      }
+    }
+    for (int q = 0; q < np * kGradCols; ++q) {
+      accd[q] += (double)acc[q];
+      acc[q] = 0.0f;
+    }
+  }
+  if (i >= n) return;
+  for (int p = 0; p < np; ++p) {
+    for (int c = 0; c < kGradCols; ++c) {
+      const int cc = c0 + c;
+      if (cc >= ncols) continue;
+      out[((int64_t)p * ncols + cc) * n + i] = (float)(accd[p * kGradCols + c] * pscale[p]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Dispatch tables
 // ---------------------------------------------------------------------------
 using TileFn = void (*)(const bf8*, int64_t, const bf8*, const void*, int64_t,
@@ -735,6 +829,26 @@ void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r
   hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, rows.z.ptr,
                      r0, nrows, cols.z.ptr, cols.n, d, outputscale, out);
   MGP_HIP_CHECK(hipGetLastError());
+}
+
+void gradient_matvec(int kind, bool ard, const PackedPoints& pts, int d, float outputscale,
+                     const float* pscale_dev, const float* V_dev, int ncols, float* out_dev,
+                     hipStream_t st) {
+  MGP_REQUIRE(d >= 1 && d <= kGradMaxDim, "gradient products support input dimension <= 32");
+  MGP_REQUIRE(ncols >= 1, "ncols must be >= 1");
+  const int64_t n = pts.n;
+  const size_t shm = (size_t)kGradTile * (d + kGradCols) * sizeof(float);
+  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256));
+  using Fn = void (*)(const float*, int64_t, int, const float*, int, int, float, const float*,
+                      float*);
+  Fn fn;
+  if (kind == KIND_RBF) fn = ard ? k_grad_matvec<KIND_RBF, true> : k_grad_matvec<KIND_RBF, false>;
+  else fn = ard ? k_grad_matvec<KIND_MATERN52, true> : k_grad_matvec<KIND_MATERN52, false>;
+  for (int c0 = 0; c0 < ncols; c0 += kGradCols) {
+    hipLaunchKernelGGL(fn, grid, dim3(256), shm, st, pts.z.ptr, n, d, V_dev, ncols, c0,
+                       outputscale, pscale_dev, out_dev);
+    MGP_HIP_CHECK(hipGetLastError());
+  }
 }
 
 }  // namespace mgp

@@ -53,6 +53,11 @@ struct Provider {
 
   // (K + noise I) V  for device arrays V, out ([ncols][n] column-major).
   void forward(const float* V, int ncols, float* out);
+  // out[p][c][i] = sum_j dk_p(x_i, x_j) V[c][j] for all P parameters (device
+  // arrays; out is [P][ncols][n]).
+  DevBuf<float> gscale;  // per-parameter scale of the gradient sums
+  void gradient(const float* V, int ncols, float* out);
+
   // K(Xs, X) V for a packed test set.
   void cross(const PackedPoints& rows, const float* V, int ncols, float* out);
 };

@@ -23,6 +23,20 @@ void Provider::refresh_coords() {
                                hipMemcpyHostToDevice, st));
   pack_points(X.ptr, n, co, train, st);
   if (materialized) fill_dense();
+  // Gradient scales: dk/dl_q = os h dz_q^2 / (s^2 l_q); dk/dos = k/os.
+  std::vector<float> gs((size_t)nparams);
+  const double s2 = (double)base * (double)base;
+  for (int q = 0; q < nparams - 1; ++q)
+    gs[q] = (float)((double)outputscale() / (s2 * (double)params[q]));
+  gs[nparams - 1] = 1.0f;
+  gscale.ensure(gs.size());
+  MGP_HIP_CHECK(hipMemcpyAsync(gscale.ptr, gs.data(), gs.size() * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));  // gs is released on return
+}
+
+void Provider::gradient(const float* V, int ncols, float* out) {
+  gradient_matvec(kind, ard, train, d, outputscale(), gscale.ptr, V, ncols, out, st);
 }
 
 namespace {

@@ -156,6 +156,29 @@ def test_materialized_route_parity(kind, ard, d, n, t):
     assert _relerr(got2, ref2) <= TOL
 
 
+@pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, True, 3, 700, 5), (ok.MATERN52, True, 4, 900, 2),
+                                            (ok.RBF, False, 2, 500, 3), (ok.MATERN52, False, 1, 600, 1)])
+def test_gradient_matvec_parity(kind, ard, d, n, t):
+    """Fused gradient products against the float64 closed-form derivatives."""
+    rng = np.random.default_rng(60 + d + t)
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = _params(rng, d, ard)
+    print(f"gradient case kind={kind} ard={ard} d={d} n={n} t={t}", flush=True)
+    p = NativeProvider(kind, ard, X, params, 0.05)
+    try:
+        got = p.gradient_matvec(V)
+        times, _, out = p.benchmark_op(V, 2, 2, 1)
+    finally:
+        p.close()
+    ref = ok.gradient_matvec(kind, X, V, params, ard)
+    got = got.reshape(ref.shape)
+    errs = [_relerr(got[q], ref[q]) for q in range(ref.shape[0])]
+    print(f"  per-parameter relerr max {max(errs):.3e}", flush=True)
+    assert max(errs) <= TOL
+    assert np.array_equal(out.reshape(ref.shape), got)
+
+
 def test_full_size_c3_sampled_rows():
     """BASELINE config 3 shape (N=250k, d=16, t=16, Matern-5/2 ARD): rows sampled
     across the matrix are compared with the float64 oracle."""
