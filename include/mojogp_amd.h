@@ -131,7 +131,7 @@ typedef struct mgp_train_opts {
   int use_preconditioner;
   int max_tridiag_iter;
   float precond_rebuild_threshold;
-  int precond_method; /* 0 greedy (1 rpcholesky / 2 nystrom: not implemented) */
+  int precond_method; /* 0 greedy, 1 rpcholesky, 2 nystrom */
   float init_mean;
   int enable_early_stopping;
   int early_stop_patience;
@@ -275,6 +275,149 @@ MGP_API int mgp_predict_with_cache(void* handle, void* cache, const float* Xs,
                                    float* mean_out, float* var_out,
                                    mgp_predict_info_t* info);
 MGP_API int mgp_destroy_prediction_cache(void* cache);
+
+/* ---- Multi-output LMC ---------------------------------------------------- */
+/* An LMC model is R latent providers (mgp_init_provider with noise 0, all
+ * over the same training inputs X[n][d]) with mixing matrices A[R][T][T]
+ * (row-major), per-task noise[T] and optional fixed observation noise
+ * fixed_noise[T][n] (NULL: none).  Task-blocked vectors are [T][n]
+ * (index t*n + i); C of them are [C][T][n]. */
+
+/* out = (sum_s A_s (x) K_s + diag(noise_t) + diag(fixed)) V for C task-blocked
+ * columns.  Replaces JITLMCGradientAdapter.forward_matvec
+ * (kernels/jit/jit_lmc.mojo:275-330) with kernel_lmc_accumulate_batched /
+ * kernel_lmc_add_noise_batched / kernel_lmc_add_fixed_noise_batched
+ * (kernels/lmc_provider.mojo:113-170). */
+MGP_API int mgp_lmc_forward_matvec(void* const* providers, int R, int T,
+                                   const float* A, const float* noise,
+                                   const float* fixed_noise, const float* V,
+                                   int C, float* out);
+
+/* The positional options of the reference's train_lmc()
+ * (jit_engine_lmc_bindings.mojo:365-390). */
+typedef struct mgp_lmc_train_opts {
+  int max_iterations;
+  float learning_rate;
+  int num_probes;
+  int max_cg_iter;
+  float cg_tol;
+  int precond_rank;    /* 0: no preconditioner */
+  int precond_method;  /* 0 greedy, 1 rpcholesky, 2 nystrom */
+  float precond_rebuild_threshold;
+  int max_tridiag_iter;
+  float early_stop_tol;
+  int early_stop_patience;
+} mgp_lmc_train_opts_t;
+
+/* Result of mgp_lmc_train (the reference's result dict,
+ * jit_engine_lmc_bindings.mojo:533-585).  Caller-allocated arrays (any may be
+ * NULL): params[sum_s P_s] (per latent, concatenated), A[R][T][T],
+ * L[R][T][T], var_diag[R][T], noise[T], mean[T], alpha[T][n] (task-blocked),
+ * nll_history / iter_times_ms [max_iterations]. */
+typedef struct mgp_lmc_train_result {
+  float* params;
+  float* A;
+  float* L;
+  float* var_diag;
+  float* noise;
+  float* mean;
+  float* alpha;
+  float* nll_history;
+  double* iter_times_ms;
+  int history_len;
+  float final_nll;
+  int iterations;
+  int converged;
+  int precond_rebuild_count;
+} mgp_lmc_train_result_t;
+
+/* Joint Adam training of the latent kernel parameters, A_s = L_s L_s^T +
+ * diag(var_diag_s), per-task noise and per-task mean by BBMM on the T*n joint
+ * system with the sum-of-Kronecker Woodbury preconditioner.  y_blocked [T][n];
+ * init_params / trainable: per latent, concatenated.  The providers end with
+ * the best parameters.  Replaces train_lmc() (train_lmc_python,
+ * jit_engine_lmc_bindings.mojo:365-597 -> train_lmc_jit,
+ * kernels/jit/jit_lmc.mojo:699-1529; preconditioner
+ * kernels/lmc_preconditioner.mojo:143-589). */
+MGP_API int mgp_lmc_train(void* const* providers, int R, int T,
+                          const float* y_blocked, const float* init_params,
+                          const int* trainable, const float* init_noise,
+                          const float* fixed_noise, const float* init_mean,
+                          const mgp_lmc_train_opts_t* opts,
+                          mgp_lmc_train_result_t* out);
+
+/* One BBMM evaluation of the LMC marginal likelihood at fixed A / noise /
+ * kernel parameters (y_c: task-blocked, mean removed): NLL per joint entry,
+ * y^T K^-1 y, log|K|, kernel gradients [sum_s P_s], dNLL/dA [R][T][T],
+ * dNLL/dnoise [T], alpha [T][n].  The body of one iteration of train_lmc_jit
+ * (jit_lmc.mojo:1132-1212 with _compute_A_and_noise_gradients_jit
+ * :582-696); internal there, exposed for teacher-forced parity tests. */
+MGP_API int mgp_lmc_bbmm_eval(void* const* providers, int R, int T,
+                              const float* A, const float* noise,
+                              const float* fixed_noise, const float* y_c,
+                              int num_probes, int max_cg_iter,
+                              int max_tridiag_iter, float cg_tol, int iteration,
+                              int precond_rank, int precond_method, float* nll,
+                              float* inv_quad, float* logdet,
+                              float* kernel_grads, float* grad_A,
+                              float* noise_grads, float* alpha_out,
+                              int* cg_iterations, float* precond_logdet);
+
+/* Predictive mean [m][T] (and variance [m][T], latent variances [R][m]) at
+ * Xs[m][d] from the task-blocked alpha [T][n].  variance_method 0 mean only,
+ * 1 LOVE (rank lanczos_rank), 2 exact; each latent's variance is computed
+ * with its provider noise set to the average task noise, mixed by
+ * sum_t' A_s[t][t']^2 and the task noise added.  Replaces predict_lmc()
+ * (predict_lmc_python, jit_engine_lmc_bindings.mojo:1102-1394). */
+MGP_API int mgp_lmc_predict(void* const* providers, int R, int T,
+                            const float* A, const float* alpha,
+                            const float* mean, const float* noise,
+                            const float* Xs, int64_t m, int variance_method,
+                            int max_cg_iter, float cg_tol, int precond_rank,
+                            int lanczos_rank, float* mean_out, float* var_out,
+                            float* latent_var_out);
+
+/* Exact joint posterior variance [m][T] of the LMC model (observation noise
+ * included): per test point and output task, one CG solve of K_full against
+ * the joint cross-covariance column (unpreconditioned, per-column stop
+ * ||r|| / ||b|| < cg_tol), var = sum_s A_s[t][t] os_s - r . beta + noise_t,
+ * clamped at 1e-10.  block_points test points (0: 512) share one block solve.
+ * Replaces _predict_lmc_full_exact_variance_backend
+ * (mojogp/multi_output_gp.py:4360-4515), which issues one
+ * sample_lmc_pathwise() solve per (point, task). */
+MGP_API int mgp_lmc_exact_variance(void* const* providers, int R, int T,
+                                   const float* A, const float* noise,
+                                   const float* fixed_noise, const float* Xs,
+                                   int64_t m, int max_cg_iter, float cg_tol,
+                                   int block_points, float* var_out,
+                                   int* cg_iterations);
+
+/* Pathwise correction for S residuals [S][T][n]: beta = K_full^-1 r by
+ * unpreconditioned CG per column (stop: ||r|| / ||b|| < cg_tol, pAp guard),
+ * correction [S][m][T] = sum_s A_s (x) K_s(Xs, X) beta.  Replaces
+ * sample_lmc_pathwise() (sample_lmc_pathwise_python,
+ * jit_engine_lmc_bindings.mojo:599-797), which handles one sample per call;
+ * here all S samples share each structured product.  cg_iterations receives
+ * the number of joint-operator applications. */
+MGP_API int mgp_lmc_pathwise_correction(void* const* providers, int R, int T,
+                                        const float* A, const float* noise,
+                                        const float* fixed_noise,
+                                        const float* residual, int S,
+                                        const float* Xs, int64_t m,
+                                        int max_cg_iter, float cg_tol,
+                                        float* correction_out,
+                                        int* cg_iterations);
+
+/* Prior draws through a stationary random-Fourier-feature map, fp64:
+ * out[k][i] = sqrt(os) sum_f weights[k][f] sqrt(2/F)
+ *             cos(sum_q X[i][q] / lengthscales[q] * W[f][q] + phase[f]).
+ * Replaces sample_prior_values over the RBF / Matern feature map
+ * (mojogp/pathwise_prior.py:37-47, 130-160); W, phase and weights are drawn
+ * by the caller. */
+MGP_API int mgp_rff_prior_values(const float* X, int64_t n, int d,
+                                 const double* lengthscales, const double* W,
+                                 const double* phase, int F, double outputscale,
+                                 const double* weights, int K, float* out);
 
 /* Streaming device copy of `bytes` repeated `repeats` times; ms_avg gets the
  * mean duration of one copy.  Used only to calibrate HBM byte counters

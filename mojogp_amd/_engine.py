@@ -354,6 +354,188 @@ class Engine:
             res["output_column_major"] = out.ravel()
         return res
 
+    # ------------------------------------------------------------ LMC
+    def train_lmc(self, *args) -> dict[str, Any]:
+        """train_lmc(provider_infos, init_params_per_latent, trainable_masks, Y [n, T],
+        num_tasks, max_iters, lr, verbose, num_probes, max_cg_iter, cg_tol,
+        precond_rank, precond_method, precond_rebuild_threshold, max_tridiag_iter,
+        init_noise [T], fixed_noise [n, T], has_fixed_noise, init_mean [T]
+        [, progress_callback, progress_interval])
+        (train_lmc_python, jit_engine_lmc_bindings.mojo:365-597)."""
+        if len(args) < 19 or len(args) > 21:
+            raise ValueError("train_lmc() expects 19 to 21 positional arguments")
+        infos = list(args[0])
+        provs = [_provider(i) for i in infos]
+        R = len(provs)
+        Y = _lib.f32(args[3])
+        T = int(args[4])
+        if Y.ndim != 2 or Y.shape[1] != T:
+            raise ValueError("Y must have shape (n, num_tasks)")
+        n = Y.shape[0]
+        init_params, masks = [], []
+        for s, prov in enumerate(provs):
+            p = _lib.f32(args[1][s]).ravel()
+            m = np.ascontiguousarray(args[2][s], dtype=bool).ravel()
+            if p.shape[0] != prov.nparams:
+                raise ValueError("train_lmc() initial params length does not match provider "
+                                 "gradient params")
+            if m.shape[0] != prov.nparams:
+                raise ValueError("train_lmc() trainable mask length does not match provider "
+                                 "gradient params")
+            init_params.append(p)
+            masks.append(m)
+        o = _lib.LMCTrainOpts()
+        o.max_iterations = int(args[5])
+        o.learning_rate = float(args[6])
+        o.num_probes = int(args[8])
+        o.max_cg_iter = int(args[9])
+        o.cg_tol = float(args[10])
+        o.precond_rank = int(args[11])
+        o.precond_method = int(args[12])
+        o.precond_rebuild_threshold = float(args[13])
+        o.max_tridiag_iter = int(args[14])
+        o.early_stop_tol = 1e-4
+        o.early_stop_patience = 15
+        if o.max_iterations <= 0:
+            raise ValueError("max_iterations must be > 0")
+        noise0 = _lib.f32(args[15]).ravel()
+        fixed = None
+        if bool(args[17]):
+            fn = _lib.f32(args[16])
+            if fn.shape != (n, T):
+                raise ValueError("train_lmc() fixed observation noise must have shape [n, T]")
+            fixed = np.ascontiguousarray(fn.T)
+        mean0 = _lib.f32(args[18]).ravel()
+        y_blocked = np.ascontiguousarray(Y.T)
+        flat_p = np.concatenate(init_params).astype(np.float32)
+        flat_m = np.concatenate(masks).astype(np.int32)
+        it_max = o.max_iterations
+        out_params = np.zeros_like(flat_p)
+        A = np.zeros((R, T, T), np.float32)
+        L = np.zeros((R, T, T), np.float32)
+        vd = np.zeros((R, T), np.float32)
+        noise = np.zeros(T, np.float32)
+        mean = np.zeros(T, np.float32)
+        alpha = np.zeros(n * T, np.float32)
+        hist = np.zeros(it_max, np.float32)
+        times = np.zeros(it_max, np.float64)
+        res = _lib.LMCTrainResult()
+        res.params, res.A, res.L = _lib.fptr(out_params), _lib.fptr(A), _lib.fptr(L)
+        res.var_diag, res.noise, res.mean = _lib.fptr(vd), _lib.fptr(noise), _lib.fptr(mean)
+        res.alpha, res.nll_history = _lib.fptr(alpha), _lib.fptr(hist)
+        res.iter_times_ms = _lib.dptr(times)
+        _lib.call("mgp_lmc_train", _lib.handles(provs), R, T, _lib.fptr(y_blocked),
+                  _lib.fptr(flat_p), flat_m.ctypes.data_as(_lib.c_int_p), _lib.fptr(noise0),
+                  _lib.ofptr(fixed), _lib.fptr(mean0), C.byref(o), C.byref(res))
+        hl = int(res.history_len)
+        per_latent, off = [], 0
+        for prov in provs:
+            per_latent.append([float(v) for v in out_params[off:off + prov.nparams]])
+            prov.params = out_params[off:off + prov.nparams].copy()
+            prov.noise = 0.0
+            off += prov.nparams
+        mode = int(infos[0].get("materialization_mode", 0))
+        return {
+            "status": "trained", "model_type": "lmc", "num_latents": R, "num_tasks": T, "n": n,
+            "final_nll": float(res.final_nll), "iterations": int(res.iterations),
+            "converged": bool(res.converged), "max_tridiag_iter": o.max_tridiag_iter,
+            "precond_rebuild_threshold": o.precond_rebuild_threshold,
+            "precond_rebuild_count": int(res.precond_rebuild_count),
+            "precond_rank": o.precond_rank, "precond_method": o.precond_method,
+            "uses_fixed_observation_noise": fixed is not None,
+            "training_route": "materialized" if mode == 1 else "matrix_free",
+            "materialization_mode": mode,
+            "params_per_latent": per_latent,
+            "noise_per_task": [float(v) for v in noise],
+            "mean_per_task": [float(v) for v in mean],
+            "A_matrices": A, "L_factors": L, "var_diag": vd, "alpha": alpha,
+            "nll_history": [float(v) for v in hist[:hl]],
+            "iter_times_ms": [float(v) for v in times[:hl]],
+        }
+
+    def predict_lmc(self, *args) -> dict[str, Any]:
+        """predict_lmc(provider_infos, alpha [n*T], A [R, T, T], X_test [m, d],
+        params_per_latent, mean_per_task [T], n_train, num_tasks
+        [, noise_per_task [T], variance_method, max_cg_iter, cg_tol, precond_rank,
+        lanczos_rank]) (predict_lmc_python, jit_engine_lmc_bindings.mojo:1102-1394)."""
+        if len(args) < 8:
+            raise ValueError("predict_lmc() expects at least 8 positional arguments")
+        infos = list(args[0])
+        provs = [_provider(i) for i in infos]
+        R = len(provs)
+        T = int(args[7])
+        alpha = _lib.f32(args[1]).ravel()
+        A = _lib.f32(args[2]).reshape(R, T, T)
+        Xs = _lib.f32(args[3])
+        for s, prov in enumerate(provs):
+            prov.update_params(_lib.f32(args[4][s]).ravel())
+        mean = _lib.f32(args[5]).ravel()
+        if alpha.shape[0] != int(args[6]) * T:
+            raise ValueError("alpha must have n_train * num_tasks entries")
+        noise = _lib.f32(args[8]).ravel() if len(args) > 8 else None
+        vm = int(args[9]) if len(args) > 9 else 0
+        max_cg = int(args[10]) if len(args) > 10 else 100
+        tol = float(args[11]) if len(args) > 11 else 1e-2
+        prank = int(args[12]) if len(args) > 12 else 10
+        lrank = int(args[13]) if len(args) > 13 else 0
+        if lrank <= 0:
+            lrank = _DEFAULT_PREDICT_LANCZOS_RANK
+            if any(i.get("is_ard") for i in infos):
+                lrank = max(lrank, _DEFAULT_ARD_PREDICT_LANCZOS_RANK)
+        if noise is None:
+            vm = 0
+        m = Xs.shape[0]
+        mean_out = np.zeros((m, T), np.float32)
+        var = np.zeros((m, T), np.float32) if vm else None
+        lat = np.zeros((R, m), np.float32) if vm else None
+        _lib.call("mgp_lmc_predict", _lib.handles(provs), R, T, _lib.fptr(A), _lib.fptr(alpha),
+                  _lib.fptr(mean), _lib.ofptr(noise), _lib.fptr(Xs), m, vm, max_cg, tol, prank,
+                  lrank, _lib.fptr(mean_out), _lib.ofptr(var), _lib.ofptr(lat))
+        out = {"mean": mean_out, "lanczos_rank_used": lrank}
+        if vm:
+            out["variance"] = var
+            out["std"] = np.sqrt(var)
+            out["latent_variances"] = lat
+        return out
+
+    def sample_lmc_pathwise(self, *args) -> dict[str, Any]:
+        """sample_lmc_pathwise(provider_infos, residual [n, T] (or [S, n, T]), A, X_test,
+        params_per_latent, noise_per_task [, max_cg_iter, cg_tol, fixed_noise [n, T]])
+        (sample_lmc_pathwise_python, jit_engine_lmc_bindings.mojo:599-797).  A 3-D
+        residual stack is corrected in one batched solve; 'correction' then has
+        shape [S, m, T]."""
+        if len(args) < 6 or len(args) > 9:
+            raise ValueError("sample_lmc_pathwise() expects 6-9 positional arguments")
+        infos = list(args[0])
+        provs = [_provider(i) for i in infos]
+        R = len(provs)
+        resid = _lib.f32(args[1])
+        single = resid.ndim == 2
+        if single:
+            resid = resid[None]
+        S, n, T = resid.shape
+        A = _lib.f32(args[2]).reshape(R, T, T)
+        Xs = _lib.f32(args[3])
+        for s, prov in enumerate(provs):
+            prov.update_params(_lib.f32(args[4][s]).ravel())
+            prov.update_noise(0.0)
+        noise = _lib.f32(args[5]).ravel()
+        max_cg = int(args[6]) if len(args) > 6 else 100
+        tol = float(args[7]) if len(args) > 7 else 1e-2
+        fixed = None
+        if len(args) > 8:
+            fn = _lib.f32(args[8])
+            if fn.size == n * T:
+                fixed = np.ascontiguousarray(fn.reshape(n, T).T)
+        blocked = np.ascontiguousarray(resid.transpose(0, 2, 1))
+        m = Xs.shape[0]
+        corr = np.zeros((S, m, T), np.float32)
+        its = C.c_int(0)
+        _lib.call("mgp_lmc_pathwise_correction", _lib.handles(provs), R, T, _lib.fptr(A),
+                  _lib.fptr(noise), _lib.ofptr(fixed), _lib.fptr(blocked), S, _lib.fptr(Xs), m,
+                  max_cg, tol, _lib.fptr(corr), C.byref(its))
+        return {"correction": corr[0] if single else corr, "cg_iterations": int(its.value)}
+
 
 _ENGINE = Engine()
 

@@ -88,6 +88,28 @@ class PredictInfo(C.Structure):
     ]
 
 
+class LMCTrainOpts(C.Structure):
+    """mgp_lmc_train_opts_t"""
+    _fields_ = [
+        ("max_iterations", C.c_int), ("learning_rate", C.c_float), ("num_probes", C.c_int),
+        ("max_cg_iter", C.c_int), ("cg_tol", C.c_float), ("precond_rank", C.c_int),
+        ("precond_method", C.c_int), ("precond_rebuild_threshold", C.c_float),
+        ("max_tridiag_iter", C.c_int), ("early_stop_tol", C.c_float),
+        ("early_stop_patience", C.c_int),
+    ]
+
+
+class LMCTrainResult(C.Structure):
+    """mgp_lmc_train_result_t"""
+    _fields_ = [
+        ("params", c_float_p), ("A", c_float_p), ("L", c_float_p), ("var_diag", c_float_p),
+        ("noise", c_float_p), ("mean", c_float_p), ("alpha", c_float_p),
+        ("nll_history", c_float_p), ("iter_times_ms", c_double_p), ("history_len", C.c_int),
+        ("final_nll", C.c_float), ("iterations", C.c_int), ("converged", C.c_int),
+        ("precond_rebuild_count", C.c_int),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The native gfx950 library is missing or failed to load."""
 
@@ -147,6 +169,29 @@ _SIGNATURES = {
     "mgp_gaussian": (C.c_int, [C.c_int64, C.c_uint64, c_float_p]),
     "mgp_pivoted_cholesky": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_float, C.c_float,
                                        C.c_uint64, c_float_p, c_int_p, c_float_p]),
+    "mgp_lmc_forward_matvec": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p,
+                                         c_float_p, c_float_p, C.c_int, c_float_p]),
+    "mgp_lmc_train": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p, c_int_p,
+                                c_float_p, c_float_p, c_float_p, C.POINTER(LMCTrainOpts),
+                                C.POINTER(LMCTrainResult)]),
+    "mgp_lmc_bbmm_eval": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p,
+                                    c_float_p, c_float_p, C.c_int, C.c_int, C.c_int, C.c_float,
+                                    C.c_int, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
+                                    c_float_p, c_float_p, c_float_p, c_float_p, c_int_p,
+                                    c_float_p]),
+    "mgp_lmc_predict": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
+                                  c_float_p, c_float_p, C.c_int64, C.c_int, C.c_int, C.c_float,
+                                  C.c_int, C.c_int, c_float_p, c_float_p, c_float_p]),
+    "mgp_lmc_exact_variance": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p,
+                                         c_float_p, c_float_p, C.c_int64, C.c_int, C.c_float,
+                                         C.c_int, c_float_p, c_int_p]),
+    "mgp_lmc_pathwise_correction": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p,
+                                              c_float_p, c_float_p, c_float_p, C.c_int,
+                                              c_float_p, C.c_int64, C.c_int, C.c_float,
+                                              c_float_p, c_int_p]),
+    "mgp_rff_prior_values": (C.c_int, [c_float_p, C.c_int64, C.c_int, c_double_p, c_double_p,
+                                       c_double_p, C.c_int, C.c_double, c_double_p, C.c_int,
+                                       c_float_p]),
 }
 
 _lock = threading.Lock()
@@ -205,6 +250,19 @@ def fptr(a: np.ndarray):
     """float32 pointer of a C-contiguous float32 array."""
     assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
     return a.ctypes.data_as(c_float_p)
+
+
+def ofptr(a):
+    """fptr, or NULL for None."""
+    return None if a is None else fptr(a)
+
+
+def handles(providers) -> C.Array:
+    """void*[R] array of provider handles."""
+    arr = (C.c_void_p * len(providers))()
+    for i, p in enumerate(providers):
+        arr[i] = p.handle.value
+    return arr
 
 
 def dptr(a: np.ndarray):

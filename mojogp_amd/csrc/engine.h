@@ -50,8 +50,24 @@ struct CGResult {
   std::vector<std::vector<float>> diag, offdiag;  // per column
 };
 
-// Solves (K + noise I) X = rhs for `ncols` columns (device rhs [C][n]);
-// the solution stays in w.x (normalised-RHS scale, as given).
+// A symmetric positive definite operator on device vectors of length n for
+// mBCG: matvec(V, C, out) = A V for C columns ([C][n]); precond (optional)
+// writes z = P^{-1} r for C columns plus the fixed-chunk partials of the
+// column dots r.z into rz_part[C * reduction_chunks(n)].
+struct CGOperator {
+  int64_t n = 0;
+  hipStream_t st = nullptr;
+  std::function<void(const float*, int, float*)> matvec;
+  std::function<void(const float*, int, float*, double*)> precond;
+};
+
+// Solves A X = rhs for `ncols` columns (device rhs [C][n]) by the reference's
+// preconditioned mBCG (combined_inv_quad_logdet.mojo:81-449); the solution
+// stays in w.x (normalised-RHS scale, as given).
+CGResult batched_cg(const CGOperator& op, const float* rhs, int ncols, int max_iter,
+                    int max_tridiag, float tol, CGWork& w, bool warm_start);
+// The single-output system (K + noise I) with the pivoted-Cholesky Woodbury
+// preconditioner P (null or rank 0: none).
 CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int ncols, int max_iter,
                     int max_tridiag, float tol, CGWork& w, bool warm_start);
 
@@ -139,6 +155,13 @@ struct PredictState {
 // reference's stop rule (relative residual < tol, pAp guard).
 int solve_alpha(Provider& pv, const float* y_host, float mean, int max_iter, float tol,
                 PredictState& ps);
+// X = A^{-1} B for C device columns [C][n], each column an independent
+// unpreconditioned CG from x0 = 0 with the stop rules of solve_alpha
+// (solve_single_rhs_deterministic_host_jit, jit_prediction.mojo:681-765, run
+// once per column there).  Finished columns freeze while the rest go on.
+// Returns the number of operator applications.
+int solve_columns(const CGOperator& op, const float* B, int C, int max_iter, float tol,
+                  float* X);
 // Lanczos inverse root S (S S^T ~ (K + noise I)^{-1}), rank r.
 void lanczos_inv_root(Provider& pv, int r, PredictState& ps);
 

@@ -119,6 +119,107 @@ __global__ void k_a1_pupdate(float* __restrict__ p, const float* __restrict__ r,
   if (i < n) p[i] = r[i] + s[3] * p[i];
 }
 
+// ---------------------------------------- independent single-RHS CG per column
+// Column c keeps s[4c + 0..3] = rr_old, initial norm, alpha, beta and done[c];
+// done[C] = every column finished.  One thread per column for the scalars.
+__global__ void k_mc_init(const double* __restrict__ part, int nb, int C, float* s, int* done) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b) acc += part[(int64_t)c * nb + b];
+  const float rr = (float)acc;
+  float init = sqrtf(rr);
+  if (init < 1e-20f) init = 1.0f;
+  s[4 * c + 0] = rr;
+  s[4 * c + 1] = init;
+  done[c] = 0;
+}
+
+__global__ void k_mc_alpha(const double* __restrict__ part, int nb, int C, float* s, int* done) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C || done[c]) return;
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b) acc += part[(int64_t)c * nb + b];
+  const float pap = (float)acc;
+  if (pap != pap || pap < 1e-10f) {
+    done[c] = 1;
+    return;
+  }
+  const float a = s[4 * c] / pap;
+  if (a != a) {
+    done[c] = 1;
+    return;
+  }
+  s[4 * c + 2] = a;
+}
+
+// grid (nb, C): x += a p, r -= a Ap on chunk b of column c; rr partials.
+__global__ void k_mc_update(float* __restrict__ x, float* __restrict__ r,
+                            const float* __restrict__ p, const float* __restrict__ Ap, int64_t n,
+                            int nb, const float* __restrict__ s, const int* __restrict__ done,
+                            double* __restrict__ rr_part) {
+  __shared__ double sm[4];
+  const int c = blockIdx.y;
+  if (done[c]) return;  // uniform per block
+  const float a = s[4 * c + 2];
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  const int64_t base = (int64_t)c * n;
+  double acc = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    x[base + i] += a * p[base + i];
+    const float ri = r[base + i] - a * Ap[base + i];
+    r[base + i] = ri;
+    acc += (double)ri * (double)ri;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += sm[w];
+    rr_part[(int64_t)c * nb + blockIdx.x] = t;
+  }
+}
+
+__global__ void k_mc_beta(const double* __restrict__ part, int nb, int C, float tol, float* s,
+                          int* done) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C || done[c]) return;
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b) acc += part[(int64_t)c * nb + b];
+  const float rr_new = (float)acc;
+  if (sqrtf(rr_new) / s[4 * c + 1] < tol) {
+    done[c] = 1;
+    return;
+  }
+  const float rr_old = s[4 * c];
+  float beta = 0.0f;
+  if (rr_old >= 1e-20f) {
+    beta = rr_new / (rr_old + 1e-20f);
+    if (beta < 0.0f || beta != beta) beta = 0.0f;
+  }
+  s[4 * c + 3] = beta;
+  s[4 * c] = rr_new;
+}
+
+__global__ void k_mc_pupdate(float* __restrict__ p, const float* __restrict__ r, int64_t n, int C,
+                             const float* __restrict__ s, const int* __restrict__ done) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * C) return;
+  const int c = (int)(idx / n);
+  if (done[c]) return;
+  p[idx] = r[idx] + s[4 * c + 3] * p[idx];
+}
+
+__global__ void k_mc_alldone(int C, int* done) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int all = 1;
+  for (int c = 0; c < C; ++c) all &= done[c] != 0;
+  done[C] = all;
+}
+
 // Lanczos three-term recurrence: w -= a v (+ b vprev).
 __global__ void k_three_term(float* __restrict__ w, const float* __restrict__ v,
                              const float* __restrict__ vprev, float a, float b, int64_t n) {
@@ -209,10 +310,26 @@ void build_precond(Provider& pv, int rank, const PivotOptions& po, Precond& P) {
 // ------------------------------------------------------------------ batched CG
 CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_iter,
                     int max_tridiag, float tol, CGWork& w, bool warm_start) {
-  const int64_t n = pv.n;
-  hipStream_t st = pv.st;
+  CGOperator op;
+  op.n = pv.n;
+  op.st = pv.st;
+  op.matvec = [&pv](const float* V, int ncols, float* out) { pv.forward(V, ncols, out); };
+  if (P && P->rank > 0) {
+    const int nb = reduction_chunks(pv.n);
+    op.precond = [&pv, P, nb](const float* r, int ncols, float* z, double* rz_part) {
+      woodbury_apply(P->L.ptr, pv.n, P->rank, P->Minv.ptr, P->noise, r, ncols, z, P->work, r,
+                     nb, rz_part, pv.st);
+    };
+  }
+  return batched_cg(op, rhs, C, max_iter, max_tridiag, tol, w, warm_start);
+}
+
+CGResult batched_cg(const CGOperator& op, const float* rhs, int C, int max_iter,
+                    int max_tridiag, float tol, CGWork& w, bool warm_start) {
+  const int64_t n = op.n;
+  hipStream_t st = op.st;
   const int nb = reduction_chunks(n);
-  const bool pre = P && P->rank > 0;
+  const bool pre = (bool)op.precond;
   const size_t nc = (size_t)n * C;
   float* x = w.x.ptr;  // caller ensured capacity (warm start keeps contents)
   float* r = w.r.ensure(nc);
@@ -231,14 +348,14 @@ CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_i
 
   if (warm_start) {
     copy(r, rhs, nc, st);
-    pv.forward(x, C, Ap);
+    op.matvec(x, C, Ap);
     sub(r, r, Ap, nc, st);
   } else {
     fill(x, nc, 0.0f, st);
     copy(r, rhs, nc, st);
   }
   if (pre) {
-    woodbury_apply(P->L.ptr, n, P->rank, P->Minv.ptr, P->noise, r, C, z, P->work, r, nb, pb, st);
+    op.precond(r, C, z, pb);
   } else {
     coldot_partial(r, r, n, C, nb, pb, st);
   }
@@ -251,13 +368,12 @@ CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_i
   const auto t_loop = Clock::now();
   for (int iter = 0; iter < max_iter; ++iter) {
     res.iterations = iter + 1;
-    pv.forward(p, C, Ap);
+    op.matvec(p, C, Ap);
     coldot_partial(p, Ap, n, C, nb, pa, st);
     cg_alpha(pa, nb, C, s, st);
     cg_update(x, r, p, Ap, n, C, nb, s, pa, st);  // pa <- r.r partials
     if (pre) {
-      woodbury_apply(P->L.ptr, n, P->rank, P->Minv.ptr, P->noise, r, C, z, P->work, r, nb,
-                     pb, st);
+      op.precond(r, C, z, pb);
       cg_beta(pb, nb, C, s, iter, max_tridiag, st);
     } else {
       cg_beta(pa, nb, C, s, iter, max_tridiag, st);
@@ -673,6 +789,55 @@ int solve_alpha(Provider& pv, const float* y_host, float mean, int max_iter, flo
   }
   MGP_HIP_CHECK(hipStreamSynchronize(st));
   ps.has_alpha = true;
+  return it;
+}
+
+int solve_columns(const CGOperator& op, const float* B, int C, int max_iter, float tol,
+                  float* X) {
+  MGP_REQUIRE(C >= 1 && C <= 65535, "solve_columns needs 1..65535 columns");
+  const int64_t n = op.n;
+  hipStream_t st = op.st;
+  const int nb = reduction_chunks(n);
+  const size_t nc = (size_t)n * C;
+  DevBuf<float> r, p, Ap, s;
+  DevBuf<double> part;
+  DevBuf<int> done;
+  r.ensure(nc);
+  p.ensure(nc);
+  Ap.ensure(nc);
+  s.ensure((size_t)4 * C);
+  part.ensure((size_t)2 * nb * C);
+  done.ensure((size_t)C + 1);
+  const dim3 gc((unsigned)ceil_div(C, 64));
+  copy(r.ptr, B, (int64_t)nc, st);
+  copy(p.ptr, B, (int64_t)nc, st);
+  fill(X, (int64_t)nc, 0.0f, st);
+  coldot_partial(r.ptr, r.ptr, n, C, nb, part.ptr, st);
+  hipLaunchKernelGGL(k_mc_init, gc, dim3(64), 0, st, part.ptr, nb, C, s.ptr, done.ptr);
+  int it = 0;
+  for (; it < max_iter; ++it) {
+    op.matvec(p.ptr, C, Ap.ptr);
+    coldot_partial(p.ptr, Ap.ptr, n, C, nb, part.ptr, st);
+    hipLaunchKernelGGL(k_mc_alpha, gc, dim3(64), 0, st, part.ptr, nb, C, s.ptr, done.ptr);
+    hipLaunchKernelGGL(k_mc_update, dim3(nb, C), dim3(256), 0, st, X, r.ptr, p.ptr, Ap.ptr, n,
+                       nb, s.ptr, done.ptr, part.ptr + (size_t)nb * C);
+    hipLaunchKernelGGL(k_mc_beta, gc, dim3(64), 0, st, part.ptr + (size_t)nb * C, nb, C, tol,
+                       s.ptr, done.ptr);
+    hipLaunchKernelGGL(k_mc_pupdate, g1((int64_t)nc), dim3(256), 0, st, p.ptr, r.ptr, n, C,
+                       s.ptr, done.ptr);
+    MGP_HIP_CHECK(hipGetLastError());
+    if ((it & 3) == 3 || it == max_iter - 1) {
+      hipLaunchKernelGGL(k_mc_alldone, dim3(1), dim3(64), 0, st, C, done.ptr);
+      int dh = 0;
+      MGP_HIP_CHECK(hipMemcpyAsync(&dh, done.ptr + C, sizeof(int), hipMemcpyDeviceToHost, st));
+      MGP_HIP_CHECK(hipStreamSynchronize(st));
+      if (dh) {
+        ++it;
+        break;
+      }
+    }
+  }
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
   return it;
 }
 

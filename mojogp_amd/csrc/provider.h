@@ -50,6 +50,8 @@ struct Provider {
   void materialize();
   void fill_dense();
   void release_blas();
+  // Rebind the provider (and its rocBLAS handle) to another stream.
+  void set_stream(hipStream_t s);
 
   // (K + noise I) V  for device arrays V, out ([ncols][n] column-major).
   void forward(const float* V, int ncols, float* out);

@@ -76,6 +76,11 @@ void Provider::materialize() {
   MGP_HIP_CHECK(hipStreamSynchronize(st));
 }
 
+void Provider::set_stream(hipStream_t s) {
+  st = s;
+  if (blas) MGP_BLAS_CHECK(rocblas_set_stream(static_cast<rocblas_handle>(blas), s));
+}
+
 void Provider::release_blas() {
   if (blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(blas));
   blas = nullptr;

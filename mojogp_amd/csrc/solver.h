@@ -90,6 +90,10 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
 
 // M = L^T L (k x k, fp64) for the first k columns.
 void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st);
+// M[a][b] = La_a . Lb_b (ka x kb, fp64 on the device) for factors [k][n].
+void cross_ltl(const float* La, int ka, const float* Lb, int kb, int64_t n, double* M_dev,
+               hipStream_t st);
+
 
 // out = (v - L u)/noise with u = Minv (L^T v) for ncols columns (Woodbury,
 // pivoted_cholesky.mojo:1646-1771).  Optionally writes dot partials of
@@ -101,9 +105,16 @@ struct WoodburyWork {
 void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,
                     const float* v, int ncols, float* out, WoodburyWork& w,
                     const float* dotv, int nb, double* dot_part, hipStream_t st);
-// out[c*n + i] = sum_kk L[kk*n+i] * zr[c*k + kk] + s * zn[c*n + i]
+// out[c*n + i] = sum_kk L[kk*n+i] * zr[c*k + kk] + s * zn[c*n + i]  (zn may be null)
 void low_rank_sample(const float* L, int64_t n, int k, const float* zr,
                      const float* zn, float s, int ncols, float* out, hipStream_t st);
+
+// out[c][kk] = L_kk . V_c for ncols columns (L [k][n], V [ncols][n]).
+void lt_matmul(const float* L, int64_t n, int k, const float* V, int ncols, float* out,
+               WoodburyWork& w, hipStream_t st);
+// out[c][i] = sum_kk L[kk][i] Z[c][kk] for ncols columns.
+void l_matmul(const float* L, int64_t n, int k, const float* Z, int ncols, float* out,
+              hipStream_t st);
 
 // ---------------------------------------------------------------- gradients
 // g[p] = sum_{a,b} dK_p[a,b] * sum_c Lf[c*n+a] Rf[c*n+b]  for every kernel

@@ -418,6 +418,55 @@ __global__ void k_syrk_final(const double* __restrict__ part, int k, int splits,
   M[idx] = s;
 }
 
+// part[z][a][b] = sum_{i in split z} La[a][i] Lb[b][i]; grid (ka tiles, kb tiles, splits).
+__global__ void k_cross_part(const float* __restrict__ La, int ka, const float* __restrict__ Lb,
+                             int kb, int64_t n, int splits, double* __restrict__ part) {
+  __shared__ float ta[16][65];
+  __shared__ float tb[16][65];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int a0 = blockIdx.x * 16, b0 = blockIdx.y * 16;
+  const int64_t chunk = (n + splits - 1) / splits;
+  const int64_t i0 = (int64_t)blockIdx.z * chunk, i1 = min(n, i0 + chunk);
+  double acc = 0.0;
+  for (int64_t s = i0; s < i1; s += 64) {
+    for (int t = threadIdx.x; t < 16 * 64; t += 256) {
+      const int col = t / 64, row = t % 64;
+      const int64_t i = s + row;
+      const bool ok = i < i1;
+      ta[col][row] = (ok && a0 + col < ka) ? La[(int64_t)(a0 + col) * n + i] : 0.0f;
+      tb[col][row] = (ok && b0 + col < kb) ? Lb[(int64_t)(b0 + col) * n + i] : 0.0f;
+    }
+    __syncthreads();
+    float f = 0.0f;
+#pragma unroll 8
+    for (int row = 0; row < 64; ++row) f = fmaf(ta[ty][row], tb[tx][row], f);
+    acc += (double)f;
+    __syncthreads();
+  }
+  const int a = a0 + ty, b = b0 + tx;
+  if (a < ka && b < kb) part[((int64_t)blockIdx.z * ka + a) * kb + b] = acc;
+}
+
+__global__ void k_cross_final(const double* __restrict__ part, int64_t count, int splits,
+                              double* __restrict__ M) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= count) return;
+  double s = 0.0;
+  for (int z = 0; z < splits; ++z) s += part[(int64_t)z * count + idx];
+  M[idx] = s;
+}
+
+// out[c][kk] = sum over chunks of wpart[b][kk][c] (fp64 sum, fp32 result).
+__global__ void k_lt_reduce(const float* __restrict__ wpart, int nb, int k, int ncols,
+                            float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)k * ncols) return;
+  const int c = (int)(idx / k), kk = (int)(idx - (int64_t)c * k);
+  double s = 0.0;
+  for (int b = 0; b < nb; ++b) s += (double)wpart[((int64_t)b * k + kk) * ncols + c];
+  out[idx] = (float)s;
+}
+
 // w-part[b][kk][c] = sum_{i in chunk b} L[kk][i] v[c][i]; block = 16 kk x 16 c.
 __global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
                           const float* __restrict__ v, int ncols, int c0, int nb,
@@ -534,7 +583,7 @@ __global__ __launch_bounds__(256) void k_low_rank_sample(
   for (int c = 0; c < 16; ++c) {
     if (c < cn) {
       const int64_t off = (int64_t)(c0 + c) * n + i;
-      out[off] = z[c] + s * zn[off];
+      out[off] = zn ? z[c] + s * zn[off] : z[c];
     }
   }
 }
@@ -1012,6 +1061,43 @@ void gemm_nr_rr(const float* Q, const float* T, int64_t n, int r, float* S, hipS
 void love_variance(const float* V, int64_t m, int r, float diag, float* var, hipStream_t st) {
   hipLaunchKernelGGL(k_love_variance, grid1(m), dim3(kBlock), 0, st, V, m, r, diag, var);
   MGP_HIP_CHECK(hipGetLastError());
+}
+
+void cross_ltl(const float* La, int ka, const float* Lb, int kb, int64_t n, double* M_dev,
+               hipStream_t st) {
+  if (ka <= 0 || kb <= 0) return;
+  const int splits = (int)std::max<int64_t>(1, std::min<int64_t>(64, ceil_div(n, 4096)));
+  DevBuf<double> part;
+  part.ensure((size_t)splits * ka * kb);
+  hipLaunchKernelGGL(k_cross_part, dim3((unsigned)ceil_div(ka, 16), (unsigned)ceil_div(kb, 16), splits),
+                     dim3(256), 0, st, La, ka, Lb, kb, n, splits, part.ptr);
+  hipLaunchKernelGGL(k_cross_final, grid1((int64_t)ka * kb), dim3(kBlock), 0, st, part.ptr,
+                     (int64_t)ka * kb, splits, M_dev);
+  MGP_HIP_CHECK(hipGetLastError());
+  MGP_HIP_CHECK(hipStreamSynchronize(st));  // `part` is released on return
+}
+
+void lt_matmul(const float* L, int64_t n, int k, const float* V, int ncols, float* out,
+               WoodburyWork& w, hipStream_t st) {
+  if (k <= 0 || ncols <= 0) return;
+  const int nbw = reduction_chunks(n);
+  float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
+  for (int c0 = 0; c0 < ncols; c0 += 16)
+    hipLaunchKernelGGL(k_lt_part, dim3(nbw, (unsigned)ceil_div(k, 16)), dim3(256), 0, st, L, n,
+                       k, V, ncols, c0, nbw, wpart);
+  hipLaunchKernelGGL(k_lt_reduce, grid1((int64_t)k * ncols), dim3(kBlock), 0, st, wpart, nbw,
+                     k, ncols, out);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void l_matmul(const float* L, int64_t n, int k, const float* Z, int ncols, float* out,
+              hipStream_t st) {
+  if (ncols <= 0) return;
+  if (k <= 0) {
+    fill(out, n * (int64_t)ncols, 0.0f, st);
+    return;
+  }
+  low_rank_sample(L, n, k, Z, nullptr, 0.0f, ncols, out, st);
 }
 
 }  // namespace mgp

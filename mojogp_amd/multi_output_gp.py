@@ -1,0 +1,683 @@
+"""MultiOutputLMCGP — the reference's LMC multi-output surface over the gfx950 engine.
+
+Follows mojogp/multi_output_gp.py: constructor 3534-3660, fit 4561-4820 /
+_fit_composite 4821-5143, predict 5406-5557 / _predict_composite 5611-6172,
+full exact variance 4360-4515, sample_posterior 6173-6598, score 6600-6636 and
+save / load 6638-7013.  Same argument names and defaults; the model is
+
+    K_full = sum_s A_s (x) K_s + diag(noise_t) (+ fixed observation noise),
+
+one RBF / Matern-5/2 latent kernel per s (isotropic or ARD) over shared inputs.
+Training, prediction, exact variance and the pathwise correction run in
+libmojogp_amd.so; the RFF prior draws use the caller's NumPy Generator exactly
+as the reference and are evaluated on the device.
+
+Scope: continuous inputs, RBF / Matern-5/2 latents.  Categorical / mixed
+latents, composite kernel trees and heteroskedastic noise models raise
+``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Any, Optional, Union
+
+import numpy as np
+
+from . import _engine
+from .gp import normalize_fit_method
+from .kernel import KernelNode, Matern52, RBF, make_ard_kernel
+from .pathwise_prior import (build_feature_weights, build_pathwise_feature_map,
+                             sample_prior_values)
+
+_MODEL_SCHEMA_VERSION = 1
+_PRECOND_METHODS = {"greedy": 0, "rpcholesky": 1, "nystrom": 2}
+_KERNEL_STRINGS = {"rbf": RBF, "matern52": Matern52}
+_DEFAULT_PREDICT_LANCZOS_RANK = 100
+_DEFAULT_ARD_PREDICT_LANCZOS_RANK = 200
+
+
+@dataclass
+class MultiOutputPredictionResult:
+    mean: np.ndarray
+    variance: Optional[np.ndarray] = None
+    std: Optional[np.ndarray] = None
+
+
+@dataclass
+class LMCTrainingResult:
+    final_nll: float
+    nll_history: np.ndarray
+    iterations: int
+    converged: bool
+    num_latents: int
+    num_tasks: int
+    noise_per_task: np.ndarray
+    lengthscales: Optional[np.ndarray] = None
+    outputscales: Optional[np.ndarray] = None
+    params_per_latent: Optional[list] = None
+    kernel_types: Optional[np.ndarray] = None
+    A_matrices: Optional[np.ndarray] = None
+    L_factors: Optional[np.ndarray] = None
+    B: Optional[np.ndarray] = None
+    Q: Optional[np.ndarray] = None
+    Lambda: Optional[np.ndarray] = None
+    alpha: Optional[np.ndarray] = None          # task-blocked [T * n]
+    use_ard: bool = False
+    lengthscales_per_dim: Optional[np.ndarray] = None
+    mean_per_task: Optional[np.ndarray] = None
+    var_diag: Optional[np.ndarray] = None
+    iter_times_ms: Optional[np.ndarray] = None
+    fixed_observation_noise: Optional[np.ndarray] = None
+
+
+def _resolve_precond(rank: int, method: str, use_preconditioner: Optional[bool]):
+    """resolve_preconditioner_settings for the LMC constructor: a disabled
+    preconditioner is rank 0; 'auto' means greedy."""
+    method = "greedy" if method == "auto" else method
+    if method not in _PRECOND_METHODS:
+        raise ValueError(f"preconditioner must be one of {sorted(_PRECOND_METHODS)} or 'auto'")
+    rank = int(rank)
+    if rank < 0:
+        raise ValueError("preconditioner_rank must be >= 0")
+    use = rank > 0 if use_preconditioner is None else bool(use_preconditioner)
+    if not use:
+        rank = 0
+    return use, rank, method, _PRECOND_METHODS[method]
+
+
+def _summarize(kernels, params_per_latent, use_ard: bool):
+    """Lengthscale / outputscale summaries by parameter name
+    (_summarize_lmc_kernel_params, multi_output_gp.py:177-228)."""
+    ls_all, os_all, per_dim = [], [], []
+    for k, p in zip(kernels, params_per_latent):
+        lat = []
+        for name, v in zip(k.get_param_names(), np.asarray(p, np.float32)):
+            if name.endswith("_lengthscale") or "_ls_" in name:
+                ls_all.append(float(v))
+                if "_ls_" in name:
+                    lat.append(float(v))
+            if name.endswith("_outputscale"):
+                os_all.append(float(v))
+        if use_ard and lat:
+            per_dim.append(np.asarray(lat, np.float32))
+    lpd = None
+    if use_ard and per_dim and len({len(v) for v in per_dim}) == 1:
+        lpd = np.stack(per_dim).astype(np.float32)
+    return np.asarray(ls_all, np.float32), np.asarray(os_all, np.float32), lpd
+
+
+class MultiOutputLMCGP:
+    """Linear Model of Coregionalization over R latent kernels."""
+
+    def __init__(self, kernels: list, num_probes: int = 10, max_cg_iterations: int = 200,
+                 cg_tolerance: float = 1.0, preconditioner_rank: int = 15,
+                 precond_rebuild_threshold: float = 0.5, preconditioner: str = "greedy",
+                 use_preconditioner: Optional[bool] = None, max_tridiag_iterations: int = 30,
+                 ard: bool = False, init_mean: Optional[Union[float, np.ndarray]] = None):
+        conv = []
+        for k in kernels:
+            if isinstance(k, str):
+                if k.lower() not in _KERNEL_STRINGS:
+                    raise NotImplementedError(
+                        f"latent kernel {k!r} is outside the gfx950 engine "
+                        f"(supported: {sorted(_KERNEL_STRINGS)})")
+                k = _KERNEL_STRINGS[k.lower()]()
+            if not isinstance(k, KernelNode):
+                raise ValueError("All kernels must be KernelNode objects or valid kernel strings.")
+            k.native_kind()  # raises for unsupported trees
+            conv.append(k)
+        if not conv:
+            raise ValueError("MultiOutputLMCGP needs at least one latent kernel")
+        self._original_kernels = [KernelNode.from_dict(k.to_dict()) for k in conv]
+        self.kernels = conv
+        self.num_latents = len(conv)
+        self.num_probes = int(num_probes)
+        self.max_cg_iter = int(max_cg_iterations)
+        self.cg_tol = float(cg_tolerance)
+        (self.use_preconditioner, self.precond_rank, self.precond,
+         self.precond_method) = _resolve_precond(preconditioner_rank, preconditioner,
+                                                 use_preconditioner)
+        self.precond_rebuild_threshold = float(precond_rebuild_threshold)
+        self.max_tridiag_iter = int(max_tridiag_iterations)
+        self.ard = bool(ard)
+        self.method = "materialized"
+        self._init_mean = init_mean
+        self._fitted_mean: Optional[np.ndarray] = None
+        self._engine = None
+        self._modules: Optional[list] = None
+        self._provider_infos: Optional[list] = None
+        self._is_trained = False
+        self._X_train: Optional[np.ndarray] = None
+        self._Y_train: Optional[np.ndarray] = None
+        self._result: Optional[LMCTrainingResult] = None
+        self._raw_result: Optional[dict] = None
+        self._backend_train_info: Optional[dict] = None
+        self._backend_predict_info: Optional[dict] = None
+        self._backend_sample_info: Optional[dict] = None
+        self._fixed_observation_noise: Optional[np.ndarray] = None
+
+    # ------------------------------------------------------------ properties
+    @property
+    def is_trained(self) -> bool:
+        return self._is_trained
+
+    @property
+    def training_result(self) -> Optional[LMCTrainingResult]:
+        return self._result
+
+    @property
+    def backend_train_info(self) -> Optional[dict]:
+        return self._backend_train_info
+
+    @property
+    def backend_predict_info(self) -> Optional[dict]:
+        return self._backend_predict_info
+
+    @property
+    def backend_sample_info(self) -> Optional[dict]:
+        return self._backend_sample_info
+
+    @property
+    def task_covariance(self) -> Optional[np.ndarray]:
+        return None if self._result is None else self._result.B
+
+    @property
+    def num_tasks(self) -> Optional[int]:
+        return None if self._result is None else self._result.num_tasks
+
+    # ------------------------------------------------------------ providers
+    def _destroy_providers(self) -> None:
+        if self._provider_infos is not None and self._modules is not None:
+            for mod, info in zip(self._modules, self._provider_infos):
+                mod.destroy_provider(info)
+        self._provider_infos = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self._destroy_providers()
+        except Exception:
+            pass
+
+    def _build_providers(self, X: np.ndarray, params_per_latent, method: str) -> list:
+        d = X.shape[1]
+        self._modules = [_engine.load_kernel_module(k.native_kind(), self.ard, d)
+                         for k in self.kernels]
+        infos = []
+        for mod, p in zip(self._modules, params_per_latent):
+            info = mod.init_provider(X, np.asarray(p, np.float32), 0.0)
+            if method == "materialized":
+                mod.materialize(info)
+            infos.append(info)
+        return infos
+
+    def _ensure_providers(self) -> list:
+        if self._provider_infos is None:
+            params = [np.asarray(p, np.float32) for p in self._result.params_per_latent]
+            self._provider_infos = self._build_providers(self._X_train, params, self.method)
+        return self._provider_infos
+
+    # ------------------------------------------------------------ fit
+    def fit(self, X, Y, max_iterations: int = 100, learning_rate: float = 0.05,
+            method: str = "materialized", initial_lengthscales: Optional[np.ndarray] = None,
+            initial_params: Optional[np.ndarray] = None, initial_noise: float = 0.1,
+            initial_noise_per_task: Optional[np.ndarray] = None,
+            fixed_observation_noise: Optional[np.ndarray] = None,
+            input_dependent_noise: Optional[Any] = None, grouped_noise: Optional[Any] = None,
+            verbose: bool = False, early_stop_tol: float = 1e-4, early_stop_patience: int = 15,
+            use_fused_kernels: bool = True, observation_noise=None, observation_noise_fn=None,
+            noise_model: str = "scalar", noise_group_train=None, group_noise=None,
+            progress: Any = None, progress_stats: Optional[Any] = None,
+            progress_interval: int = 1) -> LMCTrainingResult:
+        if (observation_noise is not None or observation_noise_fn is not None
+                or noise_model != "scalar" or noise_group_train is not None
+                or group_noise is not None or input_dependent_noise is not None
+                or grouped_noise is not None):
+            raise NotImplementedError(
+                "MultiOutputLMCGP supports scalar or per-task noise (plus fixed observation "
+                "noise) only")
+        method = normalize_fit_method(method)
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        Y = np.ascontiguousarray(Y, dtype=np.float32)
+        if X.ndim != 2:
+            raise ValueError(f"X must be 2D [n, d], got shape {X.shape}")
+        if Y.ndim != 2:
+            raise ValueError(f"Y must be 2D [n, T], got shape {Y.shape}")
+        if X.shape[0] != Y.shape[0]:
+            raise ValueError(f"X has {X.shape[0]} samples, Y has {Y.shape[0]} -- must match")
+        if not np.all(np.isfinite(X)):
+            raise ValueError("X contains NaN or Inf values")
+        if not np.all(np.isfinite(Y)):
+            raise ValueError("Y contains NaN or Inf values")
+        if initial_noise <= 0:
+            raise ValueError(f"initial_noise must be > 0, got {initial_noise}")
+        if learning_rate <= 0:
+            raise ValueError(f"learning_rate must be > 0, got {learning_rate}")
+        if max_iterations <= 0:
+            raise ValueError(f"max_iterations must be > 0, got {max_iterations}")
+        n, d = X.shape
+        T = Y.shape[1]
+        R = self.num_latents
+        if fixed_observation_noise is not None:
+            fixed_observation_noise = np.ascontiguousarray(fixed_observation_noise, np.float32)
+            if fixed_observation_noise.shape != (n, T):
+                raise ValueError(f"fixed_observation_noise must have shape ({n}, {T})")
+            if not np.all(np.isfinite(fixed_observation_noise)) or np.any(
+                    fixed_observation_noise < 0):
+                raise ValueError("fixed_observation_noise must be finite and >= 0")
+        if initial_noise_per_task is not None:
+            noise0 = np.asarray(initial_noise_per_task, np.float32)
+            if noise0.shape != (T,):
+                raise ValueError(f"initial_noise_per_task must have shape ({T},)")
+            if np.any(noise0 <= 0):
+                raise ValueError("all initial_noise_per_task entries must be > 0")
+        else:
+            noise0 = np.full(T, initial_noise, np.float32)
+        self.method = method
+        self.kernels = [make_ard_kernel(k, d) if self.ard else KernelNode.from_dict(k.to_dict())
+                        for k in self._original_kernels]
+        counts = [k.num_params() for k in self.kernels]
+        if initial_params is not None and initial_lengthscales is not None:
+            raise ValueError("Provide either initial_params or initial_lengthscales for "
+                             "MultiOutputLMCGP.fit(), not both.")
+        if initial_params is not None:
+            flat = np.ascontiguousarray(initial_params, np.float32).ravel()
+            if flat.shape != (sum(counts),):
+                raise ValueError(f"init_params must have shape ({sum(counts)},) "
+                                 "[flat concat of per-latent params]")
+        else:
+            flat = np.concatenate([k.get_initial_params() for k in self.kernels]).astype(np.float32)
+            if initial_lengthscales is not None:
+                flat = self._params_from_lengthscales(np.asarray(initial_lengthscales, np.float32))
+        if self._init_mean is None:
+            mean0 = np.mean(Y, axis=0).astype(np.float32)
+        elif isinstance(self._init_mean, (int, float)):
+            mean0 = np.full(T, float(self._init_mean), np.float32)
+        else:
+            mean0 = np.asarray(self._init_mean, np.float32)
+        per_latent, off = [], 0
+        for c, k in zip(counts, self.kernels):
+            per_latent.append(k.to_engine_params(flat[off:off + c]))
+            off += c
+        self._destroy_providers()
+        self._engine = _engine.load_engine()
+        infos = self._build_providers(X, per_latent, method)
+        masks = [np.ones(c, bool) for c in counts]
+        try:
+            raw = self._engine.train_lmc(
+                infos, per_latent, masks, Y, T, int(max_iterations), float(learning_rate),
+                bool(verbose), self.num_probes, self.max_cg_iter, float(self.cg_tol),
+                self.precond_rank, self.precond_method, float(self.precond_rebuild_threshold),
+                self.max_tridiag_iter, noise0,
+                fixed_observation_noise if fixed_observation_noise is not None
+                else np.zeros((n, T), np.float32),
+                fixed_observation_noise is not None, mean0)
+        except Exception:
+            for mod, info in zip(self._modules, infos):
+                mod.destroy_provider(info)
+            raise
+        self._provider_infos = infos
+        params = [k.from_engine_params(np.asarray(p, np.float32))
+                  for k, p in zip(self.kernels, raw["params_per_latent"])]
+        ls, os_, lpd = _summarize(self.kernels, params, self.ard)
+        A = np.asarray(raw["A_matrices"], np.float32)
+        B = A.sum(axis=0).astype(np.float32)
+        lam, Q = np.linalg.eigh(B.astype(np.float64))
+        self._result = LMCTrainingResult(
+            final_nll=float(raw["final_nll"]),
+            nll_history=np.asarray(raw["nll_history"], np.float32),
+            iterations=int(raw["iterations"]), converged=bool(raw["converged"]),
+            num_latents=R, num_tasks=T,
+            noise_per_task=np.asarray(raw["noise_per_task"], np.float32),
+            lengthscales=ls, outputscales=os_, params_per_latent=[p.tolist() for p in params],
+            kernel_types=np.asarray([k.native_kind() for k in self.kernels], np.int32),
+            A_matrices=A, L_factors=np.asarray(raw["L_factors"], np.float32), B=B,
+            Q=Q.astype(np.float32), Lambda=lam.astype(np.float32),
+            alpha=np.asarray(raw["alpha"], np.float32), use_ard=self.ard,
+            lengthscales_per_dim=lpd, mean_per_task=np.asarray(raw["mean_per_task"], np.float32),
+            var_diag=np.asarray(raw["var_diag"], np.float32),
+            iter_times_ms=np.asarray(raw["iter_times_ms"], np.float64),
+            fixed_observation_noise=fixed_observation_noise)
+        self._X_train, self._Y_train = X, Y
+        self._fixed_observation_noise = fixed_observation_noise
+        self._raw_result = raw
+        self._backend_train_info = {
+            k: raw[k] for k in ("training_route", "materialization_mode", "precond_rank",
+                                "precond_method", "precond_rebuild_count",
+                                "precond_rebuild_threshold", "max_tridiag_iter",
+                                "uses_fixed_observation_noise", "iterations", "converged")}
+        self._backend_train_info["use_preconditioner"] = bool(self.use_preconditioner)
+        self._fitted_mean = self._result.mean_per_task
+        self._is_trained = True
+        self._backend_predict_info = None
+        self._backend_sample_info = None
+        return self._result
+
+    def _params_from_lengthscales(self, values: np.ndarray) -> np.ndarray:
+        """_build_lmc_initial_params_from_lengthscales (multi_output_gp.py:231-290)."""
+        idx = [[i for i, nm in enumerate(k.get_param_names())
+                if nm.endswith("_lengthscale") or "_ls_" in nm] for k in self.kernels]
+        counts = [len(i) for i in idx]
+        total = sum(counts)
+        if values.shape == (len(self.kernels),) and all(c == 1 for c in counts):
+            per = [values[s:s + 1] for s in range(len(self.kernels))]
+        elif values.shape == (total,):
+            per, off = [], 0
+            for c in counts:
+                per.append(values[off:off + c])
+                off += c
+        elif len(set(counts)) == 1 and values.shape == (len(self.kernels), counts[0]):
+            per = [values[s] for s in range(len(self.kernels))]
+        else:
+            raise ValueError(f"initial_lengthscales has shape {values.shape}, incompatible "
+                             f"with per-latent lengthscale counts {counts}")
+        out = []
+        for k, ix, v in zip(self.kernels, idx, per):
+            p = k.get_initial_params().copy()
+            p[ix] = v
+            out.append(p)
+        return np.concatenate(out).astype(np.float32)
+
+    # ------------------------------------------------------------ predict
+    def _check_test(self, X_test) -> np.ndarray:
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before prediction. Call fit() first.")
+        X_test = np.ascontiguousarray(X_test, dtype=np.float32)
+        if X_test.ndim != 2:
+            raise ValueError(f"X_test must be 2D [m, d], got shape {X_test.shape}")
+        if X_test.shape[1] != self._X_train.shape[1]:
+            raise ValueError(f"X_test has {X_test.shape[1]} features, expected "
+                             f"{self._X_train.shape[1]}")
+        if not np.all(np.isfinite(X_test)):
+            raise ValueError("X_test contains NaN or Inf values")
+        return X_test
+
+    def _solve_budget(self):
+        """max(max_cg, 100) iterations, tolerance min(cg_tol, 1e-2)
+        (multi_output_gp.py:4420-4423, 6480-6483)."""
+        tol = min(self.cg_tol, 1e-2) if self.cg_tol > 0 else 1e-2
+        return max(self.max_cg_iter, 100), tol
+
+    def predict(self, X_test, return_var: bool = False, return_std: bool = False,
+                variance_method: str = "love", progress: Any = None,
+                progress_stats: Optional[Any] = None):
+        valid = ("love", "exact", "mean_only")
+        if variance_method not in valid:
+            raise ValueError(f"variance_method must be one of {valid}, got '{variance_method}'")
+        if self._fixed_observation_noise is not None and variance_method == "love":
+            raise NotImplementedError(
+                "MultiOutputLMCGP fixed_observation_noise supports exact prediction and "
+                "pathwise sampling; use variance_method='exact' or 'mean_only'.")
+        X_test = self._check_test(X_test)
+        r = self._result
+        R, T = r.num_latents, r.num_tasks
+        infos = self._ensure_providers()
+        params = [np.asarray(p, np.float32) for p in r.params_per_latent]
+        noise = np.asarray(r.noise_per_task, np.float32)
+        vm = {"mean_only": 0, "love": 1, "exact": 2}[variance_method]
+        rank = _DEFAULT_PREDICT_LANCZOS_RANK
+        if self.ard:
+            rank = max(rank, _DEFAULT_ARD_PREDICT_LANCZOS_RANK)
+        rank = max(rank, int(self.num_probes))
+        res = self._engine.predict_lmc(
+            infos, r.alpha, r.A_matrices, X_test, params, self._fitted_mean,
+            self._X_train.shape[0], T, noise, 1 if vm == 1 else 0, self.max_cg_iter,
+            float(self.cg_tol), self.precond_rank, rank)
+        mean = res["mean"]
+        variance = res.get("variance")
+        route = "predict_lmc"
+        var_route = "predict_lmc" if vm == 1 else None
+        if vm == 2:
+            max_cg, tol = self._solve_budget()
+            if self.method == "materialized":
+                # The reference factors the dense joint covariance on the host
+                # here; the device block solve is run to a tight tolerance.
+                max_cg, tol = max(max_cg, 1000), 1e-6
+            variance = self.exact_variance(X_test, max_cg_iter=max_cg, cg_tol=tol)
+            var_route = "predict_lmc_full_exact"
+        if variance is not None:
+            variance = np.maximum(variance, 1e-10).astype(np.float32)
+        self._backend_predict_info = {
+            "requested_method": self.method, "actual_prediction_route": route,
+            "backend_prediction_used": True, "backend_variance_used": variance is not None,
+            "variance_method": variance_method, "fallback_used": False,
+            "actual_variance_route": var_route,
+            "training_route": (self._backend_train_info or {}).get("training_route",
+                                                                  self.method),
+            "lanczos_rank_used": int(res.get("lanczos_rank_used", rank)),
+            "precond_rank": self.precond_rank, "precond_method": self.precond_method}
+        if return_var:
+            return mean, variance
+        if return_std:
+            return mean, (np.sqrt(variance) if variance is not None else None)
+        return MultiOutputPredictionResult(
+            mean=mean, variance=variance,
+            std=np.sqrt(variance) if variance is not None else None)
+
+    def exact_variance(self, X_test, *, max_cg_iter: Optional[int] = None,
+                       cg_tol: Optional[float] = None, block_points: int = 0) -> np.ndarray:
+        """Exact joint posterior variance [m, T] with the task noise
+        (multi_output_gp.py:4360-4515), all (point, task) right-hand sides of a
+        block in one device solve."""
+        import ctypes as C
+
+        from . import _lib
+        X_test = self._check_test(X_test)
+        r = self._result
+        mc, tol = self._solve_budget()
+        mc = int(max_cg_iter) if max_cg_iter is not None else mc
+        tol = float(cg_tol) if cg_tol is not None else tol
+        infos = self._ensure_providers()
+        provs = [_engine._provider(i) for i in infos]
+        for p, prm in zip(provs, r.params_per_latent):
+            p.update_params(np.asarray(prm, np.float32))
+            p.update_noise(0.0)
+        T = r.num_tasks
+        A = np.ascontiguousarray(r.A_matrices, np.float32)
+        noise = np.ascontiguousarray(r.noise_per_task, np.float32)
+        fixed = None
+        if self._fixed_observation_noise is not None:
+            fixed = np.ascontiguousarray(self._fixed_observation_noise.T)
+        m = X_test.shape[0]
+        var = np.zeros((m, T), np.float32)
+        its = C.c_int(0)
+        _lib.call("mgp_lmc_exact_variance", _lib.handles(provs), len(provs), T, _lib.fptr(A),
+                  _lib.fptr(noise), _lib.ofptr(fixed), _lib.fptr(X_test), m, mc, tol,
+                  int(block_points), _lib.fptr(var), C.byref(its))
+        self._last_exact_cg_iterations = int(its.value)
+        return var
+
+    def score(self, X_test, Y_test) -> dict:
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before scoring. Call fit() first.")
+        Y_test = np.ascontiguousarray(Y_test, dtype=np.float32)
+        pred = self.predict(X_test, variance_method="mean_only")
+        mean = pred.mean if isinstance(pred, MultiOutputPredictionResult) else pred
+        resid = Y_test - mean
+        ss_res = np.sum(resid ** 2)
+        ss_tot = np.sum((Y_test - np.mean(Y_test, axis=0)) ** 2)
+        return {"rmse": float(np.sqrt(np.mean(resid ** 2))),
+                "mae": float(np.mean(np.abs(resid))),
+                "r2": float(1.0 - ss_res / (ss_tot + 1e-10)),
+                "rmse_per_task": np.sqrt(np.mean(resid ** 2, axis=0))}
+
+    # ------------------------------------------------------------ sampling
+    def sample_posterior(self, X_test, n_samples: int = 1, method: str = "diagonal",
+                         n_rff_features: int = 1024,
+                         rng: Optional[np.random.Generator] = None) -> np.ndarray:
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before sampling. Call fit() first.")
+        if method not in ("diagonal", "pathwise"):
+            raise ValueError(f"method must be 'diagonal' or 'pathwise', got '{method}'")
+        if rng is None:
+            rng = np.random.default_rng()
+        route = (self._backend_train_info or {}).get("training_route", self.method)
+        if method == "pathwise":
+            samples = self._sample_posterior_pathwise(X_test, int(n_samples),
+                                                      int(n_rff_features), rng)
+            self._backend_sample_info = {
+                "requested_method": method, "actual_sampling_method": "pathwise",
+                "actual_sampling_route": "provider_pathwise", "backend_sampling_used": True,
+                "backend_correction_used": True,
+                "backend_correction_route": "sample_lmc_pathwise", "training_route": route,
+                "prior_sampler_family": "shared_feature_map",
+                "n_rff_features": int(n_rff_features)}
+            return samples
+        mean, std = self.predict(X_test, return_std=True)
+        z = rng.standard_normal((n_samples, mean.shape[0], mean.shape[1]))
+        self._backend_sample_info = {
+            "requested_method": method, "actual_sampling_method": "diagonal",
+            "actual_sampling_route": "diagonal_from_predictive_std",
+            "backend_sampling_used": True, "backend_correction_used": False,
+            "training_route": route}
+        return (mean[None] + std[None] * z).astype(np.float32)
+
+    def _sample_posterior_pathwise(self, X_test, n_samples: int, n_rff_features: int,
+                                   rng: np.random.Generator) -> np.ndarray:
+        """Prior draws through shared RFF maps plus the exact LMC correction
+        (multi_output_gp.py:6276-6598).  The Generator is consumed in the
+        reference's order (feature maps per latent, then per sample: weights
+        per latent, observation noise); all samples share one batched
+        correction solve."""
+        X_test = self._check_test(X_test)
+        r = self._result
+        R, T = r.num_latents, r.num_tasks
+        X = self._X_train
+        n, d = X.shape
+        S = int(n_samples)
+        if S < 1:
+            raise ValueError("n_samples must be >= 1")
+        y_c = (self._Y_train - np.asarray(self._fitted_mean, np.float32)[None, :]).astype(
+            np.float32)
+        noise = np.asarray(r.noise_per_task, np.float32)
+        mean = np.asarray(self._fitted_mean, np.float32)
+        fmaps, mix = [], []
+        for s in range(R):
+            fmaps.append(build_pathwise_feature_map(
+                self.kernels[s].native_kind(), r.params_per_latent[s], input_dim=d,
+                n_features=n_rff_features, rng=rng, ard=self.ard))
+            A_s = np.asarray(r.A_matrices[s], np.float64)
+            jitter = float(np.abs(np.diag(A_s)).mean()) * 1e-6 + 1e-8
+            mix.append(np.linalg.cholesky(A_s + jitter * np.eye(T)))
+        if self._fixed_observation_noise is not None:
+            scale = np.sqrt(np.maximum(noise[None, :] + self._fixed_observation_noise,
+                                       0.0)).astype(np.float32)
+        else:
+            scale = np.sqrt(np.maximum(noise, 0.0)).astype(np.float32)[None, :]
+        weights = [[None] * R for _ in range(S)]
+        eps = np.empty((S, n, T), np.float32)
+        for c in range(S):
+            for s in range(R):
+                weights[c][s] = build_feature_weights(fmaps[s], T, rng)
+            eps[c] = rng.standard_normal((n, T)).astype(np.float32)
+        prior_train = np.zeros((S, n, T), np.float32)
+        prior_test = np.zeros((S, X_test.shape[0], T), np.float32)
+        for s in range(R):
+            W = np.concatenate([weights[c][s] for c in range(S)], axis=0)   # [S*T, F]
+            tr = sample_prior_values(fmaps[s], X, W).reshape(S, T, n)
+            te = sample_prior_values(fmaps[s], X_test, W).reshape(S, T, -1)
+            for c in range(S):
+                prior_train[c] += np.einsum("ln,tl->nt", tr[c].astype(np.float64),
+                                            mix[s]).astype(np.float32)
+                prior_test[c] += np.einsum("ln,tl->nt", te[c].astype(np.float64),
+                                           mix[s]).astype(np.float32)
+        resid = np.ascontiguousarray(y_c[None] - (prior_train + eps * scale), np.float32)
+        max_cg, tol = self._solve_budget()
+        infos = self._ensure_providers()
+        params = [np.asarray(p, np.float32) for p in r.params_per_latent]
+        fixed = (self._fixed_observation_noise if self._fixed_observation_noise is not None
+                 else np.zeros((0,), np.float32))
+        raw = self._engine.sample_lmc_pathwise(infos, resid, r.A_matrices, X_test, params, noise,
+                                               max_cg, tol, fixed)
+        corr = np.asarray(raw["correction"], np.float32).reshape(S, X_test.shape[0], T)
+        return (mean[None, None, :] + prior_test + corr).astype(np.float32)
+
+    # ------------------------------------------------------------ persistence
+    def save(self, path: str) -> None:
+        """``<path>_config.json`` + ``<path>_arrays.npz`` (multi_output_gp.py:6638-6743)."""
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before saving. Call fit() first.")
+        path = str(path)
+        if path.endswith(".json") or path.endswith(".npz"):
+            path = path.rsplit(".", 1)[0]
+        tr = self._result
+        cfg = {"schema_version": _MODEL_SCHEMA_VERSION, "wrapper": "MultiOutputLMCGP",
+               "ard": self.ard, "method": self.method, "num_probes": self.num_probes,
+               "max_cg_iter": self.max_cg_iter, "cg_tol": self.cg_tol,
+               "use_preconditioner": self.use_preconditioner, "precond_rank": self.precond_rank,
+               "precond": self.precond, "precond_rebuild_threshold": self.precond_rebuild_threshold,
+               "max_tridiag_iter": self.max_tridiag_iter,
+               "num_latents": tr.num_latents, "num_tasks": tr.num_tasks,
+               "final_nll": float(tr.final_nll), "iterations": int(tr.iterations),
+               "converged": bool(tr.converged), "use_ard": bool(tr.use_ard),
+               "has_fixed_observation_noise": self._fixed_observation_noise is not None,
+               "kernel_trees": [k.to_dict() for k in self._original_kernels],
+               "backend_train_info": self._backend_train_info or {}}
+        Path(path + "_config.json").write_text(json.dumps(cfg, indent=2, default=float))
+        arrays = {"X_train": self._X_train, "Y_train": self._Y_train,
+                  "lengthscales": tr.lengthscales, "outputscales": tr.outputscales,
+                  "kernel_types": tr.kernel_types, "noise_per_task": tr.noise_per_task,
+                  "A_matrices": tr.A_matrices, "L_factors": tr.L_factors, "B": tr.B, "Q": tr.Q,
+                  "Lambda": tr.Lambda, "alpha": tr.alpha, "nll_history": tr.nll_history,
+                  "mean_per_task": tr.mean_per_task, "fitted_mean": self._fitted_mean,
+                  "var_diag": tr.var_diag, "iter_times_ms": tr.iter_times_ms,
+                  "lengthscales_per_dim": tr.lengthscales_per_dim,
+                  "fixed_observation_noise": self._fixed_observation_noise}
+        for s, p in enumerate(tr.params_per_latent):
+            arrays[f"params_latent_{s}"] = np.asarray(p, np.float32)
+        np.savez(path + "_arrays.npz", **{k: v for k, v in arrays.items() if v is not None})
+
+    @classmethod
+    def load(cls, path: str, kernels: Optional[list] = None) -> "MultiOutputLMCGP":
+        path = str(path)
+        if path.endswith(".json") or path.endswith(".npz"):
+            path = path.rsplit(".", 1)[0]
+        cfg = json.loads(Path(path + "_config.json").read_text())
+        if cfg.get("wrapper") != "MultiOutputLMCGP":
+            raise ValueError("saved model is not a MultiOutputLMCGP")
+        if int(cfg.get("schema_version", 0)) != _MODEL_SCHEMA_VERSION:
+            raise ValueError("unsupported model schema version")
+        arr = np.load(path + "_arrays.npz", allow_pickle=False)
+        if kernels is None:
+            kernels = [KernelNode.from_dict(k) for k in cfg["kernel_trees"]]
+        gp = cls(kernels, num_probes=cfg["num_probes"], max_cg_iterations=cfg["max_cg_iter"],
+                 cg_tolerance=cfg["cg_tol"], preconditioner_rank=cfg["precond_rank"],
+                 precond_rebuild_threshold=cfg["precond_rebuild_threshold"],
+                 preconditioner=cfg["precond"], use_preconditioner=cfg["use_preconditioner"],
+                 max_tridiag_iterations=cfg.get("max_tridiag_iter", 30), ard=cfg["ard"])
+        gp.method = cfg.get("method", "materialized")
+        gp._X_train = np.ascontiguousarray(arr["X_train"], np.float32)
+        gp._Y_train = np.ascontiguousarray(arr["Y_train"], np.float32)
+        d = gp._X_train.shape[1]
+        gp.kernels = [make_ard_kernel(k, d) if gp.ard else k for k in gp._original_kernels]
+        get = lambda k: arr[k] if k in arr else None  # noqa: E731
+        fixed = get("fixed_observation_noise")
+        gp._fixed_observation_noise = (np.ascontiguousarray(fixed, np.float32)
+                                       if fixed is not None else None)
+        R = int(cfg["num_latents"])
+        gp._result = LMCTrainingResult(
+            final_nll=float(cfg["final_nll"]), nll_history=arr["nll_history"],
+            iterations=int(cfg["iterations"]), converged=bool(cfg["converged"]),
+            num_latents=R, num_tasks=int(cfg["num_tasks"]),
+            noise_per_task=arr["noise_per_task"], lengthscales=get("lengthscales"),
+            outputscales=get("outputscales"),
+            params_per_latent=[arr[f"params_latent_{s}"].tolist() for s in range(R)],
+            kernel_types=get("kernel_types"), A_matrices=arr["A_matrices"],
+            L_factors=get("L_factors"), B=get("B"), Q=get("Q"), Lambda=get("Lambda"),
+            alpha=get("alpha"), use_ard=bool(cfg.get("use_ard", False)),
+            lengthscales_per_dim=get("lengthscales_per_dim"),
+            mean_per_task=get("mean_per_task"), var_diag=get("var_diag"),
+            iter_times_ms=get("iter_times_ms"), fixed_observation_noise=gp._fixed_observation_noise)
+        fm = get("fitted_mean")
+        gp._fitted_mean = fm if fm is not None else gp._result.mean_per_task
+        gp._backend_train_info = cfg.get("backend_train_info") or {}
+        gp._engine = _engine.load_engine()
+        gp._is_trained = True
+        return gp
+
+    def __repr__(self) -> str:
+        kinds = ", ".join(k.kernel_type.name.lower() for k in self._original_kernels)
+        return (f"MultiOutputLMCGP(kernels=[{kinds}], num_latents={self.num_latents}, "
+                f"trained={self._is_trained})")

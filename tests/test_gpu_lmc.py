@@ -1,0 +1,404 @@
+"""GPU parity of the LMC multi-output engine against oracle/lmc.py.
+
+Bars: structured matvec 1e-5 relative per column (north star); NLL / inv_quad
+within 1e-4 relative and stochastic-trace gradients within 1e-3 norm-wise for
+one BBMM evaluation on the same probes; predictive mean / std within 1e-4 at
+tight solve tolerance."""
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from mojogp_amd import _lib
+from mojogp_amd._provider import NativeProvider
+from oracle import engine as oe
+from oracle import kernels as ok
+from oracle import lmc as ol
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _problem(seed, n, d, T, kinds, ards):
+    rng = np.random.default_rng(seed)
+    R = len(kinds)
+    X = rng.uniform(0, 1, size=(n, d)).astype(np.float32)
+    params = [np.concatenate([rng.uniform(0.3, 0.8, d if a else 1), [rng.uniform(0.6, 1.4)]])
+              .astype(np.float32) for a in ards]
+    A = []
+    for _ in range(R):
+        L = rng.normal(size=(T, T)) * 0.6
+        A.append(L @ L.T + 0.1 * np.eye(T))
+    A = np.asarray(A, np.float32)
+    noise = rng.uniform(0.03, 0.12, size=T).astype(np.float32)
+    return rng, X, params, A, noise
+
+
+def _providers(kinds, ards, X, params):
+    return [NativeProvider(k, a, X, p, 0.0) for k, a, p in zip(kinds, ards, params)]
+
+
+def _close(provs):
+    for p in provs:
+        p.close()
+
+
+def _forward_ref(kinds, ards, X, params, A, noise, V, fixed=None):
+    """sum_s A_s (x) K_s V + noise / fixed, per latent (float64)."""
+    n = X.shape[0]
+    T = A.shape[1]
+    Vb = np.asarray(V, np.float64).reshape(V.shape[0], T, n)
+    out = np.zeros_like(Vb)
+    for s in range(len(kinds)):
+        K = ok.kernel_matrix(kinds[s], X, X, params[s], ards[s])
+        KV = np.einsum("ij,ctj->cti", K, Vb)
+        out += np.einsum("ab,cbi->cai", A[s].astype(np.float64), KV)
+    out += np.asarray(noise, np.float64)[None, :, None] * Vb
+    if fixed is not None:
+        out += np.asarray(fixed, np.float64)[None] * Vb
+    return out.reshape(V.shape)
+
+
+FORWARD_CASES = [
+    # n, d, T, kinds, ards, C, fixed
+    (700, 3, 3, (ok.RBF, ok.MATERN52), (False, True), 5, True),
+    (1500, 6, 4, (ok.RBF, ok.MATERN52), (False, False), 16, False),
+    (129, 2, 1, (ok.MATERN52,), (True,), 1, False),
+    (333, 4, 2, (ok.RBF, ok.RBF, ok.MATERN52), (True, False, False), 3, True),
+]
+
+
+@pytest.mark.parametrize("n,d,T,kinds,ards,Cc,fixed", FORWARD_CASES)
+def test_lmc_forward_parity(n, d, T, kinds, ards, Cc, fixed):
+    rng, X, params, A, noise = _problem(100 + n, n, d, T, kinds, ards)
+    print(f"lmc forward n={n} d={d} T={T} R={len(kinds)} C={Cc} fixed={fixed}", flush=True)
+    V = rng.normal(size=(Cc, T * n)).astype(np.float32)
+    fx = rng.uniform(0, 0.05, size=(T, n)).astype(np.float32) if fixed else None
+    provs = _providers(kinds, ards, X, params)
+    out = np.zeros_like(V)
+    try:
+        _lib.call("mgp_lmc_forward_matvec", _lib.handles(provs), len(provs), T, _lib.fptr(A),
+                  _lib.fptr(noise), _lib.ofptr(fx), _lib.fptr(V), Cc, _lib.fptr(out))
+    finally:
+        _close(provs)
+    ref = _forward_ref(kinds, ards, X, params, A, noise, V, fx)
+    errs = [_rel(out[c], ref[c]) for c in range(Cc)]
+    print(f"  max column relerr {max(errs):.2e}", flush=True)
+    assert max(errs) <= 1e-5
+
+
+def _nll_bar(ref, N):
+    """1e-4 of the NLL's own scale: (|y'K^-1 y| + |log|K|| + N log 2 pi) / (2N).
+    The per-entry NLL is a difference of O(1) terms and can sit near zero,
+    where a purely relative bar would be meaningless."""
+    return 1e-4 * (abs(ref["inv_quad"]) + abs(ref["logdet"]) + N * np.log(2 * np.pi)) / (2 * N)
+
+
+def _bbmm_native(provs, A, noise, y, probes, max_cg, max_tridiag, tol, it, rank, fixed=None):
+    R, T = A.shape[0], A.shape[1]
+    nk = sum(p.nparams for p in provs)
+    kg = np.zeros(nk, np.float32)
+    GA = np.zeros((R, T, T), np.float32)
+    ng = np.zeros(T, np.float32)
+    al = np.zeros(y.size, np.float32)
+    nll, iq, ld, ci, pl = C.c_float(), C.c_float(), C.c_float(), C.c_int(), C.c_float()
+    _lib.call("mgp_lmc_bbmm_eval", _lib.handles(provs), R, T, _lib.fptr(A), _lib.fptr(noise),
+              _lib.ofptr(fixed), _lib.fptr(y), probes, max_cg, max_tridiag, tol, it, rank, 0,
+              C.byref(nll), C.byref(iq), C.byref(ld), _lib.fptr(kg), _lib.fptr(GA),
+              _lib.fptr(ng), _lib.fptr(al), C.byref(ci), C.byref(pl))
+    return {"nll": nll.value, "inv_quad": iq.value, "logdet": ld.value, "kernel_grads": kg,
+            "G_A": GA, "noise_grads": ng, "alpha": al, "cg_iterations": ci.value,
+            "precond_logdet": pl.value}
+
+
+@pytest.mark.parametrize("rank,fixed,tol", [(0, False, 1e-5), (6, False, 1.0), (5, True, 1.0)])
+def test_lmc_bbmm_eval_matches_oracle(rank, fixed, tol):
+    """tol 1.0 (the LMC default) runs exactly max_tridiag CG iterations on both
+    sides.  Without a preconditioner 30 iterations leave the probe solves far
+    from converged, where fp32 and fp64 Krylov sequences drift apart, so that
+    case solves to 1e-5 instead; its iteration counts are not compared, since
+    fp32 CG needs more iterations than fp64 to reach that residual."""
+    kinds, ards = (ok.RBF, ok.MATERN52), (False, True)
+    n, d, T = 160, 2, 2
+    rng, X, params, A, noise = _problem(7 + rank, n, d, T, kinds, ards)
+    y = (np.sin(4 * X[:, :1]) * np.array([[1.0, -0.5]]) + 0.1 * rng.normal(size=(n, T)))
+    y = np.ascontiguousarray(y.T.reshape(-1), dtype=np.float32)
+    fx = rng.uniform(0, 0.05, size=(T, n)).astype(np.float32) if fixed else None
+    print(f"lmc bbmm rank={rank} fixed={fixed}", flush=True)
+    provs = _providers(kinds, ards, X, params)
+    try:
+        got = _bbmm_native(provs, A, noise, y, 8, 500, 30, tol, 3, rank, fx)
+    finally:
+        _close(provs)
+    ref = ol.bbmm(list(kinds), list(ards), X, [p.astype(np.float64) for p in params],
+                  A.astype(np.float64), noise.astype(np.float64), y.astype(np.float64),
+                  fixed=fx, num_probes=8, max_cg=500, max_tridiag=30, tol=tol, iteration=3,
+                  precond_rank=rank)
+    print(f"  nll {got['nll']:.7f} vs {ref['nll']:.7f}; cg {got['cg_iterations']} vs "
+          f"{ref['cg_iterations']}; kgrad {_rel(got['kernel_grads'], ref['kernel_grads']):.2e} "
+          f"G_A {_rel(got['G_A'], ref['G_A']):.2e} noise {_rel(got['noise_grads'], ref['noise_grads']):.2e}",
+          flush=True)
+    if tol >= 1.0:
+        assert got["cg_iterations"] == ref["cg_iterations"]
+    assert got["inv_quad"] == pytest.approx(ref["inv_quad"], rel=1e-4)
+    assert got["logdet"] == pytest.approx(ref["logdet"], rel=1e-4)
+    assert abs(got["nll"] - ref["nll"]) <= _nll_bar(ref, T * n)
+    if rank > 0:
+        assert got["precond_logdet"] == pytest.approx(ref["precond_logdet"], rel=1e-5)
+    assert _rel(got["kernel_grads"], ref["kernel_grads"]) <= 1e-3
+    assert _rel(got["G_A"], ref["G_A"]) <= 1e-3
+    assert _rel(got["noise_grads"], ref["noise_grads"]) <= 1e-3
+
+
+@pytest.mark.parametrize("rank", [0, 5])
+def test_lmc_train_matches_oracle(rank):
+    """Four joint Adam steps (kernel params, L_s, var_diag, per-task noise and
+    mean) against the CPU restatement of train_lmc_jit on the same probes."""
+    kinds, ards = (ok.RBF, ok.MATERN52), (False, False)
+    n, d, T = 90, 2, 2
+    rng, X, params, A, noise = _problem(21 + rank, n, d, T, kinds, ards)
+    Y = np.stack([np.sin(5 * X[:, 0]), np.cos(3 * X[:, 1])]) + 0.05 * rng.normal(size=(T, n))
+    Yb = np.ascontiguousarray(Y.reshape(-1), dtype=np.float32)
+    init = [np.array([0.5, 1.0], np.float32), np.array([0.7, 1.0], np.float32)]
+    noise0 = np.full(T, 0.1, np.float32)
+    mean0 = Y.mean(axis=1).astype(np.float32)
+    iters = 4
+    print(f"lmc train rank={rank}", flush=True)
+    provs = _providers(kinds, ards, X, init)
+    o = _lib.LMCTrainOpts(iters, 0.05, 6, 200, 1e-3, rank, 0, 0.5, 30, 1e-4, 15)
+    out_p = np.zeros(4, np.float32)
+    outA, outL = np.zeros((2, T, T), np.float32), np.zeros((2, T, T), np.float32)
+    vd, nz, mn = np.zeros((2, T), np.float32), np.zeros(T, np.float32), np.zeros(T, np.float32)
+    alpha = np.zeros(n * T, np.float32)
+    hist, times = np.zeros(iters, np.float32), np.zeros(iters, np.float64)
+    res = _lib.LMCTrainResult()
+    res.params, res.A, res.L, res.var_diag = (_lib.fptr(out_p), _lib.fptr(outA),
+                                              _lib.fptr(outL), _lib.fptr(vd))
+    res.noise, res.mean, res.alpha = _lib.fptr(nz), _lib.fptr(mn), _lib.fptr(alpha)
+    res.nll_history, res.iter_times_ms = _lib.fptr(hist), _lib.dptr(times)
+    mask = np.ones(4, np.int32)
+    try:
+        _lib.call("mgp_lmc_train", _lib.handles(provs), 2, T, _lib.fptr(Yb),
+                  _lib.fptr(np.concatenate(init)), mask.ctypes.data_as(_lib.c_int_p),
+                  _lib.fptr(noise0), None, _lib.fptr(mean0), C.byref(o), C.byref(res))
+    finally:
+        _close(provs)
+    ref = ol.train(list(kinds), list(ards), X, Yb, init, noise0, mean0, max_iterations=iters,
+                   learning_rate=0.05, num_probes=6, max_cg=200, max_tridiag=30, cg_tol=1e-3,
+                   precond_rank=rank)
+    print(f"  nll {hist[:res.history_len]} vs {ref['nll_history']}", flush=True)
+    print(f"  params {out_p} vs {np.concatenate(ref['params'])}; noise {nz} vs {ref['noise']}",
+          flush=True)
+    assert res.history_len == iters
+    # per-entry NLL near zero: compare on its O(1) scale (0.5 log 2 pi + terms)
+    np.testing.assert_allclose(hist, ref["nll_history"], rtol=0, atol=1e-4)
+    assert _rel(out_p, np.concatenate(ref["params"])) <= 1e-3
+    assert _rel(outA, ref["A"]) <= 1e-3
+    assert _rel(nz, ref["noise"]) <= 1e-3
+    assert _rel(mn, ref["mean"]) <= 1e-3
+
+
+def _dense_posterior(kinds, ards, X, Xs, params, A, noise, y):
+    """Exact joint posterior mean (no mean offset) and variance incl. task noise."""
+    Ks = ol.latent_kernels(kinds, ards, X, params)
+    Kf = ol.dense_operator(Ks, A, noise)
+    n, m, T = X.shape[0], Xs.shape[0], A.shape[1]
+    cross = np.zeros((T * n, m * T))
+    prior = np.zeros((m, T))
+    for s in range(len(kinds)):
+        Kx = ok.kernel_matrix(kinds[s], X, Xs, params[s], ards[s])    # [n, m]
+        for t in range(T):
+            for tp in range(T):
+                cross[tp * n:(tp + 1) * n, t::T] += A[s, tp, t] * Kx
+            prior[:, t] += A[s, t, t] * float(params[s][-1])
+    sol = np.linalg.solve(Kf, np.concatenate([y[:, None], cross], axis=1))
+    mean = (cross.T @ sol[:, 0]).reshape(m, T)
+    var = prior - np.sum(cross * sol[:, 1:], axis=0).reshape(m, T) + noise[None, :]
+    return mean, var, sol[:, 0]
+
+
+def test_lmc_predict_mean_love_and_exact():
+    kinds, ards = (ok.RBF, ok.MATERN52), (False, True)
+    n, d, T, m = 300, 2, 3, 40
+    rng, X, params, A, noise = _problem(33, n, d, T, kinds, ards)
+    # noise 0.15-0.3: |K*| |alpha| / |K* alpha| stays O(10), so fp32 products
+    # can meet the 1e-4 bar (at noise 0.03 the cancellation factor reaches ~500)
+    noise = rng.uniform(0.15, 0.3, size=T).astype(np.float32)
+    Xs = rng.uniform(0, 1, size=(m, d)).astype(np.float32)
+    y = rng.normal(size=T * n)
+    mu, var, alpha = _dense_posterior(kinds, ards, X, Xs, [p.astype(np.float64) for p in params],
+                                      A.astype(np.float64), noise.astype(np.float64), y)
+    mean_t = np.array([0.3, -0.1, 0.05], np.float32)
+    al32 = alpha.astype(np.float32)
+    provs = _providers(kinds, ards, X, params)
+    try:
+        mo = np.zeros((m, T), np.float32)
+        vo = np.zeros((m, T), np.float32)
+        lat = np.zeros((2, m), np.float32)
+        _lib.call("mgp_lmc_predict", _lib.handles(provs), 2, T, _lib.fptr(A), _lib.fptr(al32),
+                  _lib.fptr(mean_t), _lib.fptr(noise), _lib.fptr(Xs), m, 1, 100, 1e-2, 10, 150,
+                  _lib.fptr(mo), _lib.fptr(vo), _lib.fptr(lat))
+        ve = np.zeros((m, T), np.float32)
+        its = C.c_int()
+        _lib.call("mgp_lmc_exact_variance", _lib.handles(provs), 2, T, _lib.fptr(A),
+                  _lib.fptr(noise), None, _lib.fptr(Xs), m, 1000, 1e-6, 16, _lib.fptr(ve),
+                  C.byref(its))
+    finally:
+        _close(provs)
+    mu32 = ol.predict_mean(list(kinds), list(ards), X, Xs, [p.astype(np.float64) for p in params],
+                           A, al32.astype(np.float64), mean_t)
+    print(f"lmc predict mean relerr {_rel(mo, mu32):.2e} (vs exact posterior "
+          f"{_rel(mo, mu + mean_t):.2e}); exact std relerr "
+          f"{_rel(np.sqrt(ve), np.sqrt(var)):.2e} ({its.value} operator applications)", flush=True)
+    assert _rel(mo, mu32) <= 1e-4
+    assert _rel(mo, mu + mean_t) <= 1e-4
+    assert _rel(np.sqrt(ve), np.sqrt(var)) <= 1e-4
+    # LOVE route: per-latent variance at the average task noise, mixed by
+    # sum_t' A_s[t][t']^2, plus the task noise (jit_engine_lmc_bindings.mojo:1196-1390)
+    avg = float(np.mean(noise.astype(np.float64)))
+    want = np.zeros((m, T))
+    for s in range(2):
+        K = ok.kernel_matrix(kinds[s], X, X, params[s], ards[s]) + avg * np.eye(n)
+        S = oe.lanczos_inv_root(K, 150)
+        Kx = ok.kernel_matrix(kinds[s], Xs, X, params[s], ards[s])
+        vs = np.maximum(float(params[s][-1]) - np.sum((Kx @ S) ** 2, axis=1), 1e-10)
+        np.testing.assert_allclose(lat[s], vs, rtol=2e-4, atol=1e-6)
+        w = np.sum(A[s].astype(np.float64) ** 2, axis=1)
+        want += vs[:, None] * w[None, :]
+    want += noise[None, :]
+    print(f"lmc LOVE std relerr {_rel(np.sqrt(vo), np.sqrt(want)):.2e}", flush=True)
+    assert _rel(np.sqrt(vo), np.sqrt(want)) <= 1e-4
+
+
+def test_lmc_exact_variance_reference_tolerance():
+    """At the reference's solve budget (tolerance 1e-2 per column) the device
+    block solve follows the per-column CG of the CPU restatement."""
+    kinds, ards = (ok.RBF, ok.MATERN52), (False, False)
+    n, d, T, m = 200, 3, 2, 12
+    rng, X, params, A, noise = _problem(44, n, d, T, kinds, ards)
+    Xs = rng.uniform(0, 1, size=(m, d)).astype(np.float32)
+    provs = _providers(kinds, ards, X, params)
+    try:
+        ve = np.zeros((m, T), np.float32)
+        _lib.call("mgp_lmc_exact_variance", _lib.handles(provs), 2, T, _lib.fptr(A),
+                  _lib.fptr(noise), None, _lib.fptr(Xs), m, 100, 1e-2, 5, _lib.fptr(ve), None)
+    finally:
+        _close(provs)
+    P64 = [p.astype(np.float64) for p in params]
+    Kf = ol.dense_operator(ol.latent_kernels(kinds, ards, X, P64), A.astype(np.float64),
+                           noise.astype(np.float64))
+    want = np.zeros((m, T))
+    for i in range(m):
+        for t in range(T):
+            r = np.zeros((T, n))
+            prior = 0.0
+            for s in range(2):
+                kx = ok.kernel_matrix(kinds[s], X, Xs[i:i + 1], P64[s], ards[s])[:, 0]
+                for tp in range(T):
+                    r[tp] += A[s, tp, t] * kx
+                prior += A[s, t, t] * float(P64[s][-1])
+            beta = oe.solve_alpha(Kf, r.reshape(-1), 100, 1e-2)
+            want[i, t] = max(prior - r.reshape(-1) @ beta + noise[t], 1e-10)
+    mu, var, _ = _dense_posterior(kinds, ards, X, Xs, P64, A.astype(np.float64),
+                                  noise.astype(np.float64), np.zeros(T * n))
+    e_dev, e_ref = _rel(np.sqrt(ve), np.sqrt(var)), _rel(np.sqrt(want), np.sqrt(var))
+    print(f"lmc exact variance (tol 1e-2): std relerr vs CPU restatement "
+          f"{_rel(np.sqrt(ve), np.sqrt(want)):.2e}; vs exact: device {e_dev:.2e}, "
+          f"restatement {e_ref:.2e}", flush=True)
+    # A column stops at the first iteration under the tolerance, so fp32 and
+    # fp64 runs can stop one iteration apart: the device must be as close to
+    # the exact posterior as the reference algorithm at this budget.
+    assert e_dev <= 2.0 * e_ref + 1e-4
+
+
+def test_lmc_pathwise_correction():
+    kinds, ards = (ok.RBF, ok.MATERN52), (True, False)
+    n, d, T, m, S = 250, 2, 2, 30, 6
+    rng, X, params, A, noise = _problem(55, n, d, T, kinds, ards)
+    Xs = rng.uniform(0, 1, size=(m, d)).astype(np.float32)
+    phase = rng.uniform(0, 2 * np.pi, size=(S, T, 1))
+    resid = (np.sin(5 * X[:, 0][None, None, :] + phase)
+             + 0.2 * rng.normal(size=(S, T, n))).astype(np.float32)
+    provs = _providers(kinds, ards, X, params)
+    try:
+        out = {}
+        for tol in (1e-2, 1e-6):
+            corr = np.zeros((S, m, T), np.float32)
+            _lib.call("mgp_lmc_pathwise_correction", _lib.handles(provs), 2, T, _lib.fptr(A),
+                      _lib.fptr(noise), None, _lib.fptr(resid), S, _lib.fptr(Xs), m,
+                      1000 if tol < 1e-3 else 100, tol, _lib.fptr(corr), None)
+            out[tol] = corr
+    finally:
+        _close(provs)
+    P64 = [p.astype(np.float64) for p in params]
+    for c in range(S):
+        ref = ol.pathwise_correction(list(kinds), list(ards), X, Xs, P64, A.astype(np.float64),
+                                     noise.astype(np.float64), resid[c].reshape(-1), max_cg=100,
+                                     tol=1e-2)
+        Kf = ol.dense_operator(ol.latent_kernels(kinds, ards, X, P64), A.astype(np.float64),
+                               noise.astype(np.float64))
+        beta = np.linalg.solve(Kf, resid[c].reshape(-1).astype(np.float64))
+        exact = ol.predict_mean(list(kinds), list(ards), X, Xs, P64, A, beta, np.zeros(T))
+        e_dev, e_ref = _rel(out[1e-2][c], exact), _rel(ref, exact)
+        print(f"  sample {c}: tol 1e-2 vs restatement {_rel(out[1e-2][c], ref):.2e} "
+              f"(vs dense: device {e_dev:.2e}, restatement {e_ref:.2e}); tight vs dense "
+              f"{_rel(out[1e-6][c], exact):.2e}", flush=True)
+        assert e_dev <= 2.0 * e_ref + 1e-4
+        assert _rel(out[1e-6][c], exact) <= 1e-4
+
+
+@pytest.mark.parametrize("kind,d,ard", [(ok.RBF, 3, True), (ok.MATERN52, 6, False)])
+def test_rff_prior_values(kind, d, ard):
+    from mojogp_amd.pathwise_prior import build_pathwise_feature_map, sample_prior_values
+    rng = np.random.default_rng(3 + d)
+    X = rng.uniform(0, 1, size=(40000, d)).astype(np.float32)
+    params = np.concatenate([rng.uniform(0.2, 0.9, d if ard else 1), [1.3]]).astype(np.float32)
+    fmap = build_pathwise_feature_map(kind, params, input_dim=d, n_features=1024,
+                                      rng=np.random.default_rng(0), ard=ard)
+    W = np.random.default_rng(1).standard_normal((12, 1024)).astype(np.float32)
+    got = sample_prior_values(fmap, X, W)
+    rows = slice(0, 40000, 97)
+    ref = ol.rff_prior_values(X[rows], fmap.lengthscales, fmap.W, fmap.phase, fmap.outputscale, W)
+    print(f"rff prior relerr {_rel(got[:, rows], ref):.2e}", flush=True)
+    assert _rel(got[:, rows], ref) <= 1e-6
+
+
+def test_multi_output_lmcgp_surface(tmp_path):
+    """fit (matrix-free), LOVE / exact predict, seeded pathwise sampling and a
+    save / load round trip through the Python surface."""
+    from mojogp_amd import MultiOutputLMCGP
+    rng = np.random.default_rng(0)
+    n, d, T = 400, 3, 3
+    X = rng.uniform(0, 1, size=(n, d)).astype(np.float32)
+    F = np.stack([np.sin(6 * X[:, 0]), np.cos(4 * X[:, 1] + X[:, 2])], axis=1)
+    W = rng.normal(size=(T, 2))
+    Y = (F @ W.T + 0.05 * rng.normal(size=(n, T))).astype(np.float32)
+    Xs = rng.uniform(0, 1, size=(25, d)).astype(np.float32)
+    gp = MultiOutputLMCGP(kernels=["rbf", "matern52"], num_probes=7)
+    res = gp.fit(X, Y, max_iterations=8, method="matrix_free")
+    print(f"lmc fit nll {res.nll_history}", flush=True)
+    assert np.all(np.isfinite(res.nll_history)) and res.iterations == 8
+    assert gp.backend_train_info["training_route"] == "matrix_free"
+    mean, std = gp.predict(Xs, return_std=True)
+    mean_e, var_e = gp.predict(Xs, return_var=True, variance_method="exact")
+    assert mean.shape == (25, T) and np.all(std > 0) and np.all(var_e > 0)
+    np.testing.assert_allclose(mean, mean_e, rtol=1e-5, atol=1e-6)
+    s1 = gp.sample_posterior(Xs, n_samples=64, method="pathwise", rng=np.random.default_rng(5))
+    s2 = gp.sample_posterior(Xs, n_samples=64, method="pathwise", rng=np.random.default_rng(5))
+    assert s1.shape == (64, 25, T)
+    np.testing.assert_array_equal(s1, s2)
+    # sample mean within 5 standard errors of the exact posterior mean
+    se = np.sqrt(var_e / 64.0)
+    z = np.abs(s1.mean(axis=0) - mean_e) / se
+    print(f"pathwise mean z-score max {z.max():.2f}", flush=True)
+    assert np.mean(z < 5.0) > 0.95
+    gp.save(tmp_path / "lmc")
+    gp2 = MultiOutputLMCGP.load(str(tmp_path / "lmc"))
+    np.testing.assert_allclose(gp2.predict(Xs, variance_method="mean_only").mean, mean,
+                               rtol=1e-6, atol=1e-6)
