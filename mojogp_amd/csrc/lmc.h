@@ -55,7 +55,7 @@ struct LMCStreamGuard {
 
 // P = sum_s (A_s (x) L_s L_s^T) + D with A_s = C_s C_s^T and L_s the rank-r_s
 // pivoted-Cholesky factor of K_s; applied by Woodbury with the inner matrix
-// M = I + U^T D^-1 U (U = [C_s (x) L_s]_s) inverted once in fp64.
+// M = I + U^T D^-1 U (U = [C_s (x) L_s]_s) inverted once and applied in fp64.
 struct LMCPrecond {
   int R = 0, T = 0, K = 0;  // K = sum_s r_s T
   int64_t n = 0;
@@ -63,10 +63,12 @@ struct LMCPrecond {
   std::vector<std::unique_ptr<DevBuf<float>>> L;  // per latent [r_s][n]
   std::vector<float> Cs;               // [R][T][T]
   std::vector<float> noise;            // [T]
-  DevBuf<float> Cs_dev, dinv, dsqrt, Minv;  // Minv [K][K] fp32
+  DevBuf<float> Cs_dev, dinv, dsqrt;
+  DevBuf<double> Minv;  // [K][K], fp64
   float logdet = 0.f;
   // work
-  DevBuf<float> w, Y, yk, zk, Z, out_l, res;
+  DevBuf<float> w, Y, zk, Z, out_l, res;
+  DevBuf<double> yk;
   WoodburyWork lt_work;
 
   bool active() const { return K > 0; }

@@ -68,28 +68,31 @@ __global__ void k_add_fixed(float* __restrict__ out, const float* __restrict__ i
   out[idx] = fmaf(fixed[idx % nT], in[idx], out[idx]);
 }
 
-// y[c][off + j*r + k] = sum_t Cs[t][j] Y[(c*T + t)*r + k]   (U^T w mixing)
+// y[c][off + j*r + k] = sum_t Cs[t][j] Y[(c*T + t)*r + k]   (U^T w mixing, fp64
+// as the reference's host mixing, lmc_preconditioner.mojo:470-480)
 __global__ void k_ut_mix(const float* __restrict__ Y, const float* __restrict__ Cs, int T,
-                         int r, int C, int K, int off, float* __restrict__ y) {
+                         int r, int C, int K, int off, double* __restrict__ y) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)C * T * r) return;
   const int c = (int)(idx / ((int64_t)T * r));
   const int rem = (int)(idx - (int64_t)c * T * r);
   const int j = rem / r, k = rem - j * r;
-  float s = 0.0f;
-  for (int t = 0; t < T; ++t) s = fmaf(Cs[t * T + j], Y[((int64_t)c * T + t) * r + k], s);
+  double s = 0.0;
+  for (int t = 0; t < T; ++t) s += (double)Cs[t * T + j] * (double)Y[((int64_t)c * T + t) * r + k];
   y[(int64_t)c * K + off + j * r + k] = s;
 }
 
-// z[c][a] = sum_b Minv[a][b] y[c][b]; one block per column.
-__global__ void k_small_gemv(const float* __restrict__ Minv, const float* __restrict__ y,
+// z[c][a] = sum_b Minv[a][b] y[c][b] in fp64 (M can be conditioned like
+// n / noise, so its inverse is neither stored nor applied in fp32); one block
+// per column, z rounded to fp32 for the U z products.
+__global__ void k_small_gemv(const double* __restrict__ Minv, const double* __restrict__ y,
                              int K, float* __restrict__ z) {
   const int c = blockIdx.x;
+  const double* yc = y + (int64_t)c * K;
   for (int a = threadIdx.x; a < K; a += blockDim.x) {
     double s = 0.0;
-    const float* row = Minv + (int64_t)a * K;
-    const float* yc = y + (int64_t)c * K;
-    for (int b = 0; b < K; ++b) s += (double)row[b] * (double)yc[b];
+    const double* row = Minv + (int64_t)a * K;
+    for (int b = 0; b < K; ++b) s = fma(row[b], yc[b], s);
     z[(int64_t)c * K + a] = (float)s;
   }
 }
@@ -336,9 +339,8 @@ void LMCPrecond::build(LMCModel& m, int precond_rank, const PivotOptions& po) {
   double ld = logdet_m;
   for (int t = 0; t < T; ++t) ld += (double)n * std::log((double)noise[t]);
   logdet = (float)ld;
-  std::vector<float> invf(inv.begin(), inv.end());
-  Minv.ensure(invf.size());
-  MGP_HIP_CHECK(hipMemcpy(Minv.ptr, invf.data(), invf.size() * sizeof(float), hipMemcpyHostToDevice));
+  Minv.ensure(inv.size());
+  MGP_HIP_CHECK(hipMemcpy(Minv.ptr, inv.data(), inv.size() * sizeof(double), hipMemcpyHostToDevice));
   std::vector<float> di(T), ds(T);
   for (int t = 0; t < T; ++t) {
     di[t] = 1.0f / noise[t];
@@ -378,7 +380,7 @@ void LMCPrecond::apply(const float* r, int C, float* z, double* rz_part, hipStre
   float* wv = w.ensure((size_t)total);
   hipLaunchKernelGGL(k_task_scale, g1(total), dim3(256), 0, st, wv, r, dinv.ptr, n, T, C, 0.0f);
   // 2. y = U^T w
-  float* yk_ = yk.ensure((size_t)C * K);
+  double* yk_ = yk.ensure((size_t)C * K);
   for (int s = 0; s < R; ++s) {
     const int rs = rank[s];
     if (rs == 0) continue;

@@ -79,7 +79,8 @@ struct MatvecArgs {
 // V and out are column-major device arrays.  Work buffers are grown in `ws`.
 struct MatvecWorkspace {
   DevBuf<float> vpack;    // packed right-hand sides
-  DevBuf<uint32_t> colmax;  // per-column max |V| (fp16 scaling of the product)
+  DevBuf<uint32_t> colmax;       // per-column max |V| (fp16 scaling of the product)
+  DevBuf<uint32_t> colmax_part;  // [64][chunks] row-chunk maxima
   DevBuf<float> partial;  // split-K partial sums
   // Optional HIP-event timing of the tile kernel alone (bench hook).
   bool time_tile = false;

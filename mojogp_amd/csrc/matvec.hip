@@ -169,19 +169,36 @@ __device__ __forceinline__ int col_shift(uint32_t maxbits) {
   return 15 - e;
 }
 
-// colmax[c] = max_j |V[c*n + j]| as float bits (non-negative floats order as
-// unsigned integers).  grid = (chunks, ncols).
-__global__ __launch_bounds__(256) void k_col_absmax(const float* __restrict__ V, int64_t n,
-                                                    uint32_t* __restrict__ colmax) {
+// part[c*chunks + b] = max |V[c*n + j]| over the contiguous row chunk b, as
+// float bits (non-negative floats order as unsigned integers).  grid =
+// (chunks, ncols); no atomics, so no same-address serialisation.
+__global__ __launch_bounds__(256) void k_col_absmax_part(const float* __restrict__ V, int64_t n,
+                                                         uint32_t* __restrict__ part) {
+  __shared__ uint32_t wm[4];
   const int c = blockIdx.y;
+  const int chunks = gridDim.x;
+  const int64_t len = (n + chunks - 1) / chunks;
+  const int64_t j0 = (int64_t)blockIdx.x * len, j1 = min(n, j0 + len);
   const float* col = V + (int64_t)c * n;
   uint32_t mx = 0;
-  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n;
-       j += (int64_t)gridDim.x * blockDim.x)
+  for (int64_t j = j0 + threadIdx.x; j < j1; j += blockDim.x)
     mx = max(mx, __float_as_uint(fabsf(col[j])));
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
-  if ((threadIdx.x & 63) == 0) atomicMax(colmax + c, mx);
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    part[(int64_t)c * chunks + blockIdx.x] = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
+}
+
+// colmax[c] = max_b part[c*chunks + b] for c < ncols (one thread per column).
+__global__ void k_col_absmax_final(const uint32_t* __restrict__ part, int chunks, int ncols,
+                                   uint32_t* __restrict__ colmax) {
+  const int c = threadIdx.x;
+  if (c >= ncols) return;
+  uint32_t mx = 0;
+  for (int b = 0; b < chunks; ++b) mx = max(mx, part[(int64_t)c * chunks + b]);
+  colmax[c] = mx;
 }
 
 // Vp[((g*upairs + u)*2 + part)*64 + lane] (8 fp16): element e holds
@@ -747,10 +764,12 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                          0, st, Vc, a.n, npad, vp);
     } else {
       colmax = ws.colmax.ensure(64);
-      hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, st, colmax, (int64_t)64, 0u);
-      const unsigned chunks = (unsigned)std::min<int64_t>(ceil_div(std::max<int64_t>(a.n, 1), 256), 64);
-      hipLaunchKernelGGL(k_col_absmax, dim3(chunks, (unsigned)nc), dim3(256), 0, st, Vc,
-                         a.n, colmax);
+      const int chunks = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(a.n, 1), 4096), 64);
+      uint32_t* cpart = ws.colmax_part.ensure((size_t)64 * chunks);
+      hipLaunchKernelGGL(k_col_absmax_part, dim3((unsigned)chunks, (unsigned)nc), dim3(256), 0,
+                         st, Vc, a.n, cpart);
+      hipLaunchKernelGGL(k_col_absmax_final, dim3(1), dim3(64), 0, st, cpart, chunks, nc,
+                         colmax);
       const int64_t total = (int64_t)ncg * col_pairs * 64;  // 8-half vectors per part
       vp = ws.vpack.ensure((size_t)total * 2 * 4);
       hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256),

@@ -467,14 +467,15 @@ __global__ void k_lt_reduce(const float* __restrict__ wpart, int nb, int k, int 
   out[idx] = (float)s;
 }
 
-// w-part[b][kk][c] = sum_{i in chunk b} L[kk][i] v[c][i]; block = 16 kk x 16 c.
+// w-part[b][kk][c] = sum_{i in chunk b} L[kk][i] v[c][i]; block = 16 kk x 16 c,
+// grid = (chunks, kk tiles, column tiles).
 __global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
-                          const float* __restrict__ v, int ncols, int c0, int nb,
+                          const float* __restrict__ v, int ncols, int nb,
                           float* __restrict__ wpart) {
   __shared__ float tl[16][65];
   __shared__ float tv[16][65];
   const int tc = threadIdx.x & 15, tk = threadIdx.x >> 4;
-  const int kk0 = blockIdx.y * 16;
+  const int kk0 = blockIdx.y * 16, c0 = blockIdx.z * 16;
   const int64_t chunk = (n + nb - 1) / nb;
   const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   float acc = 0.0f;
@@ -559,10 +560,12 @@ __global__ __launch_bounds__(256) void k_woodbury_final(
   }
 }
 
+// grid = (row blocks, column tiles of 16)
 __global__ __launch_bounds__(256) void k_low_rank_sample(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ zr,
-    const float* __restrict__ zn, float s, int ncols, int c0, float* __restrict__ out) {
+    const float* __restrict__ zn, float s, int ncols, float* __restrict__ out) {
   extern __shared__ float zs[];  // [16][k]
+  const int c0 = blockIdx.y * 16;
   const int cn = min(16, ncols - c0);
   for (int t = threadIdx.x; t < 16 * k; t += blockDim.x) {
     const int c = t / k, kk = t - c * k;
@@ -606,6 +609,11 @@ __global__ __launch_bounds__(256) void k_grad_trace(
   const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const bool live = a < n;
   const int cn = min(16, ncols - c0);
+  // column range of this split (whole tiles)
+  const int64_t tiles = (n + kGradTile - 1) / kGradTile;
+  const int64_t tps = (tiles + gridDim.y - 1) / gridDim.y;
+  const int64_t jb = min(n, (int64_t)blockIdx.y * tps * kGradTile);
+  const int64_t je = min(n, jb + tps * kGradTile);
   float za[DM];
 #pragma unroll
   for (int k = 0; k < DM; ++k) za[k] = (live && k < d) ? Z[a * d + k] : 0.0f;
@@ -616,23 +624,23 @@ __global__ __launch_bounds__(256) void k_grad_trace(
   double accd[NT + 1];
 #pragma unroll
   for (int t = 0; t <= NT; ++t) accd[t] = 0.0;
-  for (int64_t b0 = 0; b0 < n; b0 += kGradTile) {
+  for (int64_t b0 = jb; b0 < je; b0 += kGradTile) {
     __syncthreads();
     for (int t = threadIdx.x; t < kGradTile * DM; t += blockDim.x) {
       const int bb = t / DM, k = t - bb * DM;
       const int64_t b = b0 + bb;
-      zb[bb][k] = (b < n && k < d) ? Z[b * d + k] : 0.0f;
+      zb[bb][k] = (b < je && k < d) ? Z[b * d + k] : 0.0f;
     }
     for (int t = threadIdx.x; t < kGradTile * 16; t += blockDim.x) {
       const int bb = t / 16, c = t - bb * 16;
       const int64_t b = b0 + bb;
-      rb[bb][c] = (b < n && c < cn) ? Rf[(int64_t)(c0 + c) * n + b] : 0.0f;
+      rb[bb][c] = (b < je && c < cn) ? Rf[(int64_t)(c0 + c) * n + b] : 0.0f;
     }
     __syncthreads();
     float acc[NT + 1];
 #pragma unroll
     for (int t = 0; t <= NT; ++t) acc[t] = 0.0f;
-    const int cnt = (int)min((int64_t)kGradTile, n - b0);
+    const int cnt = (int)min((int64_t)kGradTile, je - b0);
     for (int bb = 0; bb < cnt; ++bb) {
       float dz2[DM];
       float r2 = 0.0f;
@@ -675,15 +683,23 @@ __global__ __launch_bounds__(256) void k_grad_trace(
     for (int q = 0; q <= NT; ++q)
       if (q == src) v = accd[q];
     const double tot = block_sum_d(live ? v : 0.0, sm);
-    if (threadIdx.x == 0) part[(int64_t)blockIdx.x * nterms + t] = tot;
+    if (threadIdx.x == 0)
+      part[((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * nterms + t] = tot;
   }
+}
+
+// Column splits of the gradient pair loop: enough blocks to fill the chip
+// (>= 2048 with the row blocks) while every split keeps >= 1024 columns.
+static int grad_splits(int64_t n) {
+  const int64_t rows = ceil_div(n, 256);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(2048, rows), ceil_div(n, 1024)));
 }
 
 template <int KIND, bool ARD>
 void launch_grad(int dm, const float* Z, int d, int64_t n, const float* Lf,
                  const float* Rf, int ncols, int c0, double* part, int nterms,
                  hipStream_t st) {
-  const dim3 grid((unsigned)ceil_div(n, 256));
+  const dim3 grid((unsigned)ceil_div(n, 256), (unsigned)grad_splits(n));
   switch (dm) {
 #define MGP_GRAD_CASE(DMV)                                                           \
   case DMV:                                                                         \
@@ -972,16 +988,24 @@ void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st) {
   MGP_HIP_CHECK(hipStreamSynchronize(st));  // `part` is released on return
 }
 
+// Row chunks of the L^T V partial products: >= 256 rows each, at most 256.
+static int lt_chunks(int64_t n) {
+  return (int)std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(n, 256)));
+}
+
+static void launch_lt_part(const float* L, int64_t n, int k, const float* v, int ncols, int nbw,
+                           float* wpart, hipStream_t st) {
+  const dim3 grid((unsigned)nbw, (unsigned)ceil_div(k, 16), (unsigned)ceil_div(ncols, 16));
+  hipLaunchKernelGGL(k_lt_part, grid, dim3(256), 0, st, L, n, k, v, ncols, nbw, wpart);
+}
+
 void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,
                     const float* v, int ncols, float* out, WoodburyWork& w,
                     const float* dotv, int nb, double* dot_part, hipStream_t st) {
-  const int nbw = reduction_chunks(n);
+  const int nbw = lt_chunks(n);
   float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
   float* u = w.u.ensure((size_t)ncols * k);
-  for (int c0 = 0; c0 < ncols; c0 += 16) {
-    hipLaunchKernelGGL(k_lt_part, dim3(nbw, (unsigned)ceil_div(k, 16)), dim3(256), 0, st, L,
-                       n, k, v, ncols, c0, nbw, wpart);
-  }
+  launch_lt_part(L, n, k, v, ncols, nbw, wpart, st);
   hipLaunchKernelGGL(k_small_solve, dim3(ncols), dim3(256), (size_t)k * sizeof(float), st,
                      wpart, nbw, k, ncols, Minv, u);
   const float inv_noise = 1.0f / noise;
@@ -994,10 +1018,9 @@ void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float n
 
 void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const float* zn,
                      float s, int ncols, float* out, hipStream_t st) {
-  for (int c0 = 0; c0 < ncols; c0 += 16) {
-    hipLaunchKernelGGL(k_low_rank_sample, grid1(n), dim3(256), (size_t)16 * k * sizeof(float),
-                       st, L, n, k, zr, zn, s, ncols, c0, out);
-  }
+  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256), (unsigned)ceil_div(ncols, 16));
+  hipLaunchKernelGGL(k_low_rank_sample, grid, dim3(256), (size_t)16 * k * sizeof(float), st, L,
+                     n, k, zr, zn, s, ncols, out);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -1007,7 +1030,7 @@ void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int n
   MGP_REQUIRE(d <= 32, "gradient kernel supports d <= 32");
   const int dm = d <= 1 ? 1 : d <= 2 ? 2 : d <= 4 ? 4 : d <= 8 ? 8 : d <= 16 ? 16 : 32;
   const int nterms = pv.ard ? d + 1 : 2;
-  const int64_t nblk = ceil_div(pv.n, 256);
+  const int64_t nblk = ceil_div(pv.n, 256) * grad_splits(pv.n);
   DevBuf<double> part;
   part.ensure((size_t)nblk * nterms);
   std::vector<double> acc(nterms, 0.0), hpart((size_t)nblk * nterms);
@@ -1080,11 +1103,9 @@ void cross_ltl(const float* La, int ka, const float* Lb, int kb, int64_t n, doub
 void lt_matmul(const float* L, int64_t n, int k, const float* V, int ncols, float* out,
                WoodburyWork& w, hipStream_t st) {
   if (k <= 0 || ncols <= 0) return;
-  const int nbw = reduction_chunks(n);
+  const int nbw = lt_chunks(n);
   float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
-  for (int c0 = 0; c0 < ncols; c0 += 16)
-    hipLaunchKernelGGL(k_lt_part, dim3(nbw, (unsigned)ceil_div(k, 16)), dim3(256), 0, st, L, n,
-                       k, V, ncols, c0, nbw, wpart);
+  launch_lt_part(L, n, k, V, ncols, nbw, wpart, st);
   hipLaunchKernelGGL(k_lt_reduce, grid1((int64_t)k * ncols), dim3(kBlock), 0, st, wpart, nbw,
                      k, ncols, out);
   MGP_HIP_CHECK(hipGetLastError());
