@@ -99,7 +99,8 @@ void cross_ltl(const float* La, int ka, const float* Lb, int kb, int64_t n, doub
 // pivoted_cholesky.mojo:1646-1771).  Optionally writes dot partials of
 // dotv . out (for r.z).  out may alias v.
 struct WoodburyWork {
-  DevBuf<float> wpart;   // [nbw][k][C]
+  DevBuf<float> wpart;   // [nbw][C][k] row-chunk partials of L^T v
+  DevBuf<float> wsum;    // [C][k]
   DevBuf<float> u;       // [C][k]
 };
 void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,

@@ -456,19 +456,24 @@ __global__ void k_cross_final(const double* __restrict__ part, int64_t count, in
   M[idx] = s;
 }
 
-// out[c][kk] = sum over chunks of wpart[b][kk][c] (fp64 sum, fp32 result).
-__global__ void k_lt_reduce(const float* __restrict__ wpart, int nb, int k, int ncols,
-                            float* __restrict__ out) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)k * ncols) return;
-  const int c = (int)(idx / k), kk = (int)(idx - (int64_t)c * k);
+// out[c*k + kk] = sum over chunks b of wpart[(b*ncols + c)*k + kk]: one wave
+// per output, lanes stride the chunks, fp64 sum in a fixed order (lane
+// partials, then the shuffle tree), fp32 result.
+__global__ __launch_bounds__(256) void k_lt_reduce(const float* __restrict__ wpart, int nb, int k,
+                                                   int ncols, float* __restrict__ out) {
+  const int64_t o = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t total = (int64_t)k * ncols;
+  if (o >= total) return;  // uniform per wave
   double s = 0.0;
-  for (int b = 0; b < nb; ++b) s += (double)wpart[((int64_t)b * k + kk) * ncols + c];
-  out[idx] = (float)s;
+  for (int b = lane; b < nb; b += 64) s += (double)wpart[(int64_t)b * total + o];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) out[o] = (float)s;
 }
 
-// w-part[b][kk][c] = sum_{i in chunk b} L[kk][i] v[c][i]; block = 16 kk x 16 c,
-// grid = (chunks, kk tiles, column tiles).
+// w-part[(b*ncols + c)*k + kk] = sum_{i in chunk b} L[kk][i] v[c][i]; block =
+// 16 kk x 16 c, grid = (chunks, kk tiles, column tiles).
 __global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
                           const float* __restrict__ v, int ncols, int nb,
                           float* __restrict__ wpart) {
@@ -493,19 +498,15 @@ __global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
     __syncthreads();
   }
   const int kk = kk0 + tk, c = c0 + tc;
-  if (kk < k && c < ncols) wpart[((int64_t)blockIdx.x * k + kk) * ncols + c] = acc;
+  if (kk < k && c < ncols) wpart[((int64_t)blockIdx.x * ncols + c) * k + kk] = acc;
 }
 
 // u[c*k + kk] = sum_q Minv[kk*k + q] * w[q][c],  w = sum over chunks.
-__global__ void k_small_solve(const float* __restrict__ wpart, int nb, int k, int ncols,
-                              const float* __restrict__ Minv, float* __restrict__ u) {
+__global__ void k_small_solve(const float* __restrict__ w, int k, const float* __restrict__ Minv,
+                              float* __restrict__ u) {
   extern __shared__ float ws[];  // [k]
   const int c = blockIdx.x;
-  for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
-    double s = 0.0;
-    for (int b = 0; b < nb; ++b) s += (double)wpart[((int64_t)b * k + kk) * ncols + c];
-    ws[kk] = (float)s;
-  }
+  for (int kk = threadIdx.x; kk < k; kk += blockDim.x) ws[kk] = w[(int64_t)c * k + kk];
   __syncthreads();
   for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
     float s = 0.0f;
@@ -514,48 +515,34 @@ __global__ void k_small_solve(const float* __restrict__ wpart, int nb, int k, in
   }
 }
 
-// out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * inv_noise for 16 columns
-// starting at c0; optional dot partials of dotv.out per column.
+// out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * inv_noise; one thread per
+// row, grid = (row blocks, column tiles of 16).
 __global__ __launch_bounds__(256) void k_woodbury_final(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ u,
-    int ncols, int c0, float inv_noise, const float* v, float* out,
-    const float* __restrict__ dotv, int nb, double* __restrict__ dot_part) {
+    int ncols, float inv_noise, const float* v, float* out) {
   extern __shared__ float us[];  // [16][k]
-  __shared__ double sm[4];
+  const int c0 = blockIdx.y * 16;
   const int cn = min(16, ncols - c0);
   for (int t = threadIdx.x; t < 16 * k; t += blockDim.x) {
     const int c = t / k, kk = t - c * k;
     us[t] = c < cn ? u[(int64_t)(c0 + c) * k + kk] : 0.0f;
   }
   __syncthreads();
-  const int64_t chunk = (n + nb - 1) / nb;
-  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
-  double dacc[16];
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float z[16];
 #pragma unroll
-  for (int c = 0; c < 16; ++c) dacc[c] = 0.0;
-  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
-    float z[16];
+  for (int c = 0; c < 16; ++c) z[c] = 0.0f;
+  for (int kk = 0; kk < k; ++kk) {
+    const float l = L[(int64_t)kk * n + i];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) z[c] = 0.0f;
-    for (int kk = 0; kk < k; ++kk) {
-      const float l = L[(int64_t)kk * n + i];
-#pragma unroll
-      for (int c = 0; c < 16; ++c) z[c] = fmaf(l, us[c * k + kk], z[c]);
-    }
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      if (c < cn) {
-        const int64_t off = (int64_t)(c0 + c) * n + i;
-        const float o = inv_noise * (v[off] - z[c]);
-        out[off] = o;
-        if (dot_part) dacc[c] += (double)dotv[off] * (double)o;
-      }
-    }
+    for (int c = 0; c < 16; ++c) z[c] = fmaf(l, us[c * k + kk], z[c]);
   }
-  if (dot_part) {
-    for (int c = 0; c < cn; ++c) {
-      const double t = block_sum_d(dacc[c], sm);
-      if (threadIdx.x == 0) dot_part[(int64_t)(c0 + c) * nb + blockIdx.x] = t;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    if (c < cn) {
+      const int64_t off = (int64_t)(c0 + c) * n + i;
+      out[off] = inv_noise * (v[off] - z[c]);
     }
   }
 }
@@ -1004,16 +991,18 @@ void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float n
                     const float* dotv, int nb, double* dot_part, hipStream_t st) {
   const int nbw = lt_chunks(n);
   float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
+  float* wsum = w.wsum.ensure((size_t)ncols * k);
   float* u = w.u.ensure((size_t)ncols * k);
   launch_lt_part(L, n, k, v, ncols, nbw, wpart, st);
+  hipLaunchKernelGGL(k_lt_reduce, dim3((unsigned)ceil_div((int64_t)k * ncols * 64, 256)),
+                     dim3(256), 0, st, wpart, nbw, k, ncols, wsum);
   hipLaunchKernelGGL(k_small_solve, dim3(ncols), dim3(256), (size_t)k * sizeof(float), st,
-                     wpart, nbw, k, ncols, Minv, u);
-  const float inv_noise = 1.0f / noise;
-  for (int c0 = 0; c0 < ncols; c0 += 16) {
-    hipLaunchKernelGGL(k_woodbury_final, dim3(nb), dim3(256), (size_t)16 * k * sizeof(float),
-                       st, L, n, k, u, ncols, c0, inv_noise, v, out, dotv, nb, dot_part);
-  }
+                     wsum, k, Minv, u);
+  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256), (unsigned)ceil_div(ncols, 16));
+  hipLaunchKernelGGL(k_woodbury_final, grid, dim3(256), (size_t)16 * k * sizeof(float), st, L,
+                     n, k, u, ncols, 1.0f / noise, v, out);
   MGP_HIP_CHECK(hipGetLastError());
+  if (dot_part) coldot_partial(dotv, out, n, ncols, nb, dot_part, st);
 }
 
 void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const float* zn,
@@ -1106,8 +1095,8 @@ void lt_matmul(const float* L, int64_t n, int k, const float* V, int ncols, floa
   const int nbw = lt_chunks(n);
   float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
   launch_lt_part(L, n, k, V, ncols, nbw, wpart, st);
-  hipLaunchKernelGGL(k_lt_reduce, grid1((int64_t)k * ncols), dim3(kBlock), 0, st, wpart, nbw,
-                     k, ncols, out);
+  hipLaunchKernelGGL(k_lt_reduce, dim3((unsigned)ceil_div((int64_t)k * ncols * 64, 256)),
+                     dim3(256), 0, st, wpart, nbw, k, ncols, out);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
