@@ -101,6 +101,124 @@ def _fit_c2_seconds():
     return dt, {"final_nll": tr.nll, "cg_iterations_total": info.get("cg_iterations_total")}
 
 
+C5_N, C5_D, C5_T, C5_PROBES = 20_000, 6, 4, 15
+C5_C = C5_PROBES + 1                   # columns per task block (t = 16)
+
+
+def _c5_data(seed: int = 0):
+    """Config 5 generator: X ~ U[0,1]^{20000 x 6}; latent f1 = RBF (l = 0.2) and
+    f2 = Matern-5/2 (l = 0.7) random-Fourier-feature draws (1024 features, the
+    Matern frequencies multivariate-t with 5 degrees of freedom); W ~ N(0,1)^{4x2};
+    Y = [f1 f2] W^T + 0.05 N(0,1)."""
+    rng = np.random.default_rng(seed)
+    X = rng.uniform(0, 1, size=(C5_N, C5_D)).astype(np.float32)
+
+    def rff(ls, matern):
+        Wf = rng.standard_normal((1024, C5_D))
+        if matern:
+            Wf = Wf / np.sqrt(rng.chisquare(5, size=(1024, 1)) / 5.0)
+        b = rng.uniform(0, 2 * np.pi, size=1024)
+        w = rng.standard_normal(1024)
+        return lambda Z: np.sqrt(2.0 / 1024) * np.cos(Z / ls @ Wf.T + b) @ w
+
+    f1, f2 = rff(0.2, False), rff(0.7, True)
+    Wm = rng.standard_normal((C5_T, 2))
+    Y = (np.stack([f1(X), f2(X)], 1) @ Wm.T
+         + 0.05 * rng.standard_normal((C5_N, C5_T))).astype(np.float32)
+    Xs = rng.uniform(0, 1, size=(1000, C5_D)).astype(np.float32)
+    return X, Y, Xs, Wm
+
+
+def _c5_flops_per_pair():
+    """Structured product work per (i, j) pair summed over the two latents:
+    per latent 2d + 2 T C + c_k (RBF 5, Matern-5/2 9)."""
+    return (2 * C5_D + 2 * C5_T * C5_C + 5) + (2 * C5_D + 2 * C5_T * C5_C + 9)
+
+
+def _lmc_c5(repeats: int, warmup: int):
+    """Config 5 legs: the structured product (K_full V over 16 task-blocked
+    columns = 64 columns per latent, inputs resident), one LMC mBCG iteration
+    (15 probes, rank-15 greedy preconditioner per latent), and the end-to-end
+    MultiOutputLMCGP fit (matrix-free, 15 probes, reference defaults otherwise)
+    plus 64 pathwise posterior samples at 1000 test points."""
+    import ctypes
+    from mojogp_amd import MultiOutputLMCGP, _lib
+    from mojogp_amd._provider import KIND_MATERN52, KIND_RBF, NativeProvider
+    X, Y, Xs, Wm = _c5_data()
+    A = np.stack([np.outer(Wm[:, s], Wm[:, s]) + 0.1 * np.eye(C5_T)
+                  for s in range(2)]).astype(np.float32)
+    noise = np.full(C5_T, 0.0025, np.float32)
+    provs = [NativeProvider(KIND_RBF, False, X, np.array([0.2, 1.0], np.float32), 0.0),
+             NativeProvider(KIND_MATERN52, False, X, np.array([0.7, 1.0], np.float32), 0.0)]
+    rng = np.random.default_rng(2)
+    V = rng.standard_normal((C5_C, C5_T * C5_N)).astype(np.float32)
+    times = np.zeros(repeats, np.float64)
+    y = np.ascontiguousarray((Y - Y.mean(0)).T.reshape(-1), dtype=np.float32)
+    nll, iq, ld, pl = (ctypes.c_float() for _ in range(4))
+    ci, loop_ms = ctypes.c_int(), ctypes.c_double()
+    try:
+        _lib.call("mgp_lmc_benchmark_forward", _lib.handles(provs), 2, C5_T, _lib.fptr(A),
+                  _lib.fptr(noise), _lib.fptr(V), C5_C, repeats, warmup, _lib.dptr(times), None)
+        _lib.call("mgp_lmc_bbmm_eval", _lib.handles(provs), 2, C5_T, _lib.fptr(A),
+                  _lib.fptr(noise), None, _lib.fptr(y), C5_PROBES, 200, 30, 1.0, 0, 15, 0,
+                  ctypes.byref(nll), ctypes.byref(iq), ctypes.byref(ld), None, None, None, None,
+                  ctypes.byref(ci), ctypes.byref(pl), ctypes.byref(loop_ms))
+    finally:
+        for p in provs:
+            p.close()
+    ms = float(np.median(times))
+    flops = float(C5_N) * C5_N * _c5_flops_per_pair()
+    gp = MultiOutputLMCGP(kernels=["rbf", "matern52"], num_probes=C5_PROBES)
+    t0 = time.perf_counter()
+    res = gp.fit(X, Y, method="matrix_free")
+    fit_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    gp.sample_posterior(Xs, n_samples=64, method="pathwise", rng=np.random.default_rng(1))
+    samp_s = time.perf_counter() - t0
+    return {
+        "workload": "config 5: LMC N=20000 d=6 T=4 Q=2 (RBF l=0.2, Matern-5/2 l=0.7), "
+                    "t=16 task-blocked columns (64 per latent), synthetic RFF data seed 0",
+        "structured_matvec_ms": round(ms, 4),
+        "structured_matvec_tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+        "mbcg_iter_ms": round(loop_ms.value / max(ci.value, 1), 3),
+        "mbcg_iterations": ci.value,
+        "fit_seconds": round(fit_s, 3),
+        "fit_iterations": res.iterations,
+        "pathwise_64_samples_seconds": round(samp_s, 3),
+    }, (X, V[:1])
+
+
+def _cpu_baseline_c5(X, V1, target_s: float):
+    """Reference-order fp32 C restatement of the config-5 structured product on
+    a bounded sample of rows: both latents' (K_s V) rows for the 64 columns
+    (the T x T mixing is negligible next to it)."""
+    from oracle import cpu_ref
+    threads = cpu_ref.num_threads()
+    Vc = np.ascontiguousarray(np.tile(V1.reshape(C5_T, C5_N), (C5_C, 1))[:C5_T * C5_C])
+    lat = [(0, np.array([0.2, 1.0], np.float32)), (1, np.array([0.7, 1.0], np.float32))]
+
+    def run(rows):
+        for kind, p in lat:
+            cpu_ref.forward_matvec_rows(kind, False, X, p, 0.0, Vc, 0, rows)
+
+    probe = 64
+    t0 = time.perf_counter()
+    run(probe)
+    dt = max(time.perf_counter() - t0, 1e-3)
+    rows = int(min(C5_N, max(probe, target_s / dt * probe)))
+    t0 = time.perf_counter()
+    run(rows)
+    dt = time.perf_counter() - t0
+    return {
+        "value": rows * C5_N * _c5_flops_per_pair() / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"rows [0,{rows}) of both latents' products (64 columns each) of the "
+                  f"config-5 structured matvec; {dt:.1f} s on {threads} threads",
+    }
+
+
 def _cpu_baseline(X, V, params, noise, target_s: float):
     from oracle import cpu_ref
     threads = cpu_ref.num_threads()
@@ -210,8 +328,12 @@ def main(argv=None) -> int:
         result["fit_config"] = ("config 2: RBF-ARD N=50000 d=8, 30 Adam steps, 15 probes, "
                                 "rank-100 greedy preconditioner")
         result["fit_info"] = fit_info
+        c5, c5_inputs = _lmc_c5(repeats=10, warmup=2)
+        result["lmc_c5"] = c5
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(X, V, params, noise, args.cpu_seconds)
+        if not args.no_extras:
+            result["lmc_c5"]["cpu_baseline"] = _cpu_baseline_c5(*c5_inputs, args.cpu_seconds / 2)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -351,7 +351,8 @@ MGP_API int mgp_lmc_train(void* const* providers, int R, int T,
  * y^T K^-1 y, log|K|, kernel gradients [sum_s P_s], dNLL/dA [R][T][T],
  * dNLL/dnoise [T], alpha [T][n].  The body of one iteration of train_lmc_jit
  * (jit_lmc.mojo:1132-1212 with _compute_A_and_noise_gradients_jit
- * :582-696); internal there, exposed for teacher-forced parity tests. */
+ * :582-696); internal there, exposed for teacher-forced parity tests.
+ * cg_loop_ms (optional) gets the wall time of the mBCG iteration loop. */
 MGP_API int mgp_lmc_bbmm_eval(void* const* providers, int R, int T,
                               const float* A, const float* noise,
                               const float* fixed_noise, const float* y_c,
@@ -361,7 +362,18 @@ MGP_API int mgp_lmc_bbmm_eval(void* const* providers, int R, int T,
                               float* inv_quad, float* logdet,
                               float* kernel_grads, float* grad_A,
                               float* noise_grads, float* alpha_out,
-                              int* cg_iterations, float* precond_logdet);
+                              int* cg_iterations, float* precond_logdet,
+                              double* cg_loop_ms);
+
+/* Device-resident timing of the structured product (inputs uploaded once):
+ * times_ms[repeats] gets the HIP-event duration of each product on the
+ * models' stream after `warmup` untimed ones; out (optional) the last result.
+ * The LMC counterpart of benchmark_provider_ops op 0
+ * (jit_engine_bindings.mojo:439-572); no reference export of its own. */
+MGP_API int mgp_lmc_benchmark_forward(void* const* providers, int R, int T,
+                                      const float* A, const float* noise,
+                                      const float* V, int C, int repeats,
+                                      int warmup, double* times_ms, float* out);
 
 /* Predictive mean [m][T] (and variance [m][T], latent variances [R][m]) at
  * Xs[m][d] from the task-blocked alpha [T][n].  variance_method 0 mean only,

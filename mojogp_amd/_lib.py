@@ -178,7 +178,10 @@ _SIGNATURES = {
                                     c_float_p, c_float_p, C.c_int, C.c_int, C.c_int, C.c_float,
                                     C.c_int, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
                                     c_float_p, c_float_p, c_float_p, c_float_p, c_int_p,
-                                    c_float_p]),
+                                    c_float_p, c_double_p]),
+    "mgp_lmc_benchmark_forward": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p,
+                                            c_float_p, C.c_int, C.c_int, C.c_int, c_double_p,
+                                            c_float_p]),
     "mgp_lmc_predict": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
                                   c_float_p, c_float_p, C.c_int64, C.c_int, C.c_int, C.c_float,
                                   C.c_int, C.c_int, c_float_p, c_float_p, c_float_p]),

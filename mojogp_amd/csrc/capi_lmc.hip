@@ -218,7 +218,7 @@ int mgp_lmc_bbmm_eval(void* const* providers, int R, int T, const float* A, cons
                       int max_tridiag_iter, float cg_tol, int iteration, int precond_rank,
                       int precond_method, float* nll, float* inv_quad, float* logdet,
                       float* kernel_grads, float* grad_A, float* noise_grads, float* alpha_out,
-                      int* cg_iterations, float* precond_logdet) {
+                      int* cg_iterations, float* precond_logdet, double* cg_loop_ms) {
   return guarded([&] {
     LMCModel m;
     init_model(m, providers, R, T);
@@ -246,6 +246,43 @@ int mgp_lmc_bbmm_eval(void* const* providers, int R, int T, const float* A, cons
     if (alpha_out) std::memcpy(alpha_out, ev.alpha.data(), ev.alpha.size() * sizeof(float));
     if (cg_iterations) *cg_iterations = ev.cg_iterations;
     if (precond_logdet) *precond_logdet = P.active() ? P.logdet : 0.0f;
+    if (cg_loop_ms) *cg_loop_ms = ev.cg_loop_ms;
+  });
+}
+
+int mgp_lmc_benchmark_forward(void* const* providers, int R, int T, const float* A,
+                              const float* noise, const float* V, int C, int repeats, int warmup,
+                              double* times_ms, float* out) {
+  return guarded([&] {
+    LMCModel m;
+    init_model(m, providers, R, T);
+    if (!V || !times_ms || C < 1 || repeats < 1 || warmup < 0) throw Error(ST_INVALID, "bad arguments");
+    set_mixing(m, A, noise);
+    LMCStreamGuard guard(m);
+    m.upload();
+    const size_t tot = (size_t)m.size() * C;
+    DevBuf<float> dv, dout;
+    dv.ensure(tot);
+    dout.ensure(tot);
+    MGP_HIP_CHECK(hipMemcpyAsync(dv.ptr, V, tot * sizeof(float), hipMemcpyHostToDevice, m.st));
+    for (int i = 0; i < warmup; ++i) m.forward(dv.ptr, C, dout.ptr);
+    hipEvent_t e0, e1;
+    MGP_HIP_CHECK(hipEventCreate(&e0));
+    MGP_HIP_CHECK(hipEventCreate(&e1));
+    for (int i = 0; i < repeats; ++i) {
+      MGP_HIP_CHECK(hipEventRecord(e0, m.st));
+      m.forward(dv.ptr, C, dout.ptr);
+      MGP_HIP_CHECK(hipEventRecord(e1, m.st));
+      MGP_HIP_CHECK(hipEventSynchronize(e1));
+      float ms = 0.0f;
+      MGP_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+      times_ms[i] = ms;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (out)
+      MGP_HIP_CHECK(hipMemcpyAsync(out, dout.ptr, tot * sizeof(float), hipMemcpyDeviceToHost, m.st));
+    MGP_HIP_CHECK(hipStreamSynchronize(m.st));
   });
 }
 

@@ -96,6 +96,7 @@ struct LMCEval {
   std::vector<float> alpha;         // [T][n] (host copy of the solution)
   int cg_iterations = 0;
   bool converged = false;
+  double cg_loop_ms = 0.0;  // wall time of the mBCG iteration loop
 };
 
 // One BBMM evaluation of the LMC marginal likelihood at the model's current

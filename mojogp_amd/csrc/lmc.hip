@@ -463,6 +463,7 @@ LMCEval lmc_bbmm(LMCModel& m, LMCPrecond* P, const float* y_c, int num_probes, i
   LMCEval out;
   out.cg_iterations = cg.iterations;
   out.converged = cg.converged;
+  out.cg_loop_ms = cg.loop_ms;
   {
     coldot_partial(y_c, sol, N, 1, nb, part, st);
     coldot_finalize(part, nb, 1, part + nb, st);

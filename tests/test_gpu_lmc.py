@@ -111,7 +111,7 @@ def _bbmm_native(provs, A, noise, y, probes, max_cg, max_tridiag, tol, it, rank,
     _lib.call("mgp_lmc_bbmm_eval", _lib.handles(provs), R, T, _lib.fptr(A), _lib.fptr(noise),
               _lib.ofptr(fixed), _lib.fptr(y), probes, max_cg, max_tridiag, tol, it, rank, 0,
               C.byref(nll), C.byref(iq), C.byref(ld), _lib.fptr(kg), _lib.fptr(GA),
-              _lib.fptr(ng), _lib.fptr(al), C.byref(ci), C.byref(pl))
+              _lib.fptr(ng), _lib.fptr(al), C.byref(ci), C.byref(pl), None)
     return {"nll": nll.value, "inv_quad": iq.value, "logdet": ld.value, "kernel_grads": kg,
             "G_A": GA, "noise_grads": ng, "alpha": al, "cg_iterations": ci.value,
             "precond_logdet": pl.value}
