@@ -213,8 +213,17 @@ void LMCModel::latent_forward(int s, const float* V, int cols, float* out) {
 
 void LMCModel::forward(const float* V, int C, float* out) {
   const int64_t total = n * T * (int64_t)C;
-  float* t = tmp.ensure((size_t)total);
   for (int s = 0; s < R; ++s) {
+    Provider& pv = *prov[s];
+    if (pv.fused_route() && T <= 16) {
+      // A_s mixing folded into the latent product's split-K reduction
+      const float saved = pv.noise;
+      pv.noise = 0.0f;
+      pv.forward_mixed(V, T * C, A_dev.ptr + s * T * T, T, s > 0, out);
+      pv.noise = saved;
+      continue;
+    }
+    float* t = tmp.ensure((size_t)total);
     latent_forward(s, V, T * C, t);
     hipLaunchKernelGGL(k_lmc_mix, g1(total), dim3(256), 0, st, out, t, A_dev.ptr + s * T * T,
                        n, T, C, s > 0 ? 1 : 0);

@@ -73,6 +73,13 @@ struct MatvecArgs {
   int64_t m = 0;         // rows (output length per column)
   int64_t n = 0;         // columns (input length per column)
   int ncols = 0;         // right-hand sides
+  // Optional task mixing in the epilogue (LMC): the columns form blocks of
+  // mix_T (column c = cc*mix_T + t'), and the result is
+  // out[cc][t][i] (+)= sum_t' mix[t*mix_T + t'] ((K + noise I) V)[cc][t'][i]
+  // with mix a device [mix_T][mix_T] array; ncols must be a multiple of mix_T.
+  const float* mix = nullptr;
+  int mix_T = 0;
+  bool mix_accumulate = false;
 };
 
 // out[c*m + i] = os * sum_j k(r_i, c_j) V[c*n + j]  (+ noise*V[c*m+i] if square)

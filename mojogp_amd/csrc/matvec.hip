@@ -505,6 +505,41 @@ __global__ void k_reduce_splits(const float* __restrict__ partial, int splits,
   out[idx] = o;
 }
 
+// Task-mixing reduction: one thread per (column block cc, row i) sums the split
+// partials of the block's T columns once, then writes the T mixed outputs
+// out[(cc*T + t)*m + i] (+)= sum_t' mix[t*T + t'] (os sum_s partial + noise V).
+constexpr int kMaxMixT = 16;
+__global__ void k_reduce_mix(const float* __restrict__ partial, int splits, int cpad,
+                             int64_t mpad, int64_t m, int nblocks, int T, float os, float noise,
+                             int add_noise, const float* __restrict__ Vin,
+                             const float* __restrict__ mix, int accumulate,
+                             float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)nblocks * m) return;
+  const int cc = (int)(idx / m);
+  const int64_t i = idx - (int64_t)cc * m;
+  float v[kMaxMixT];
+#pragma unroll
+  for (int tp = 0; tp < kMaxMixT; ++tp) {
+    if (tp < T) {
+      const int c = cc * T + tp;
+      double tot = 0.0;
+      for (int sp = 0; sp < splits; ++sp) tot += partial[((int64_t)sp * cpad + c) * mpad + i];
+      float o = os * (float)tot;
+      if (add_noise) o = fmaf(noise, Vin[(int64_t)c * m + i], o);
+      v[tp] = o;
+    }
+  }
+  for (int t = 0; t < T; ++t) {
+    float o = 0.0f;
+#pragma unroll
+    for (int tp = 0; tp < kMaxMixT; ++tp)
+      if (tp < T) o = fmaf(mix[t * T + tp], v[tp], o);
+    const int64_t off = (int64_t)(cc * T + t) * m + i;
+    out[off] = accumulate ? out[off] + o : o;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Direct (per-dimension difference) product: one thread per row, LDS tiles of
 // column points.  Arithmetic follows the reference order: r^2 = sum_d diff^2.
@@ -743,9 +778,15 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
   const int64_t row_tiles = rows.ntiles, col_tiles = cols.ntiles;
   const int64_t mpad = row_tiles * 16;
 
-  // Column chunks of at most 64 right-hand sides per launch.
-  for (int c0 = 0; c0 < a.ncols; c0 += 64) {
-    const int nc = std::min(64, a.ncols - c0);
+  const bool mixing = a.mix != nullptr;
+  if (mixing)
+    MGP_REQUIRE(a.mix_T >= 1 && a.mix_T <= kMaxMixT && a.ncols % a.mix_T == 0,
+                "task mixing needs ncols a multiple of T <= 16");
+  // Column chunks of at most 64 right-hand sides per launch (whole task blocks
+  // when mixing).
+  const int chunk = mixing ? (64 / a.mix_T) * a.mix_T : 64;
+  for (int c0 = 0; c0 < a.ncols; c0 += chunk) {
+    const int nc = std::min(chunk, a.ncols - c0);
     const int ncg = nc == 1 ? 0 : (nc <= 16 ? 1 : (nc <= 32 ? 2 : 4));
     const int R = rows_per_wave_tiles(kb, ncg);
     const int cpad = ncg == 0 ? 1 : 16 * ncg;
@@ -778,12 +819,15 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
     }
     MGP_HIP_CHECK(hipGetLastError());
 
-    // Grid: row blocks x j splits.  Aim for >= 2048 workgroups so 256 CUs see
-    // several waves each, while every split keeps >= 32 j tiles of work.
+    // Grid: row blocks x j splits.  Aim for >= 2048 workgroups (1024 with 64
+    // right-hand sides, whose waves carry 4x the work and whose split partials
+    // cost 4x the traffic) so 256 CUs see several waves each, while every split
+    // keeps >= 32 j tiles of work.
     const int64_t row_blocks = ceil_div(row_tiles, (int64_t)kWaves * R);
+    const int64_t target_blocks = ncg >= 4 ? 1024 : 2048;
     int64_t splits = force_splits > 0 ? force_splits : 1;
     if (force_splits <= 0) {
-      while (row_blocks * splits < 2048 && col_pairs / (splits * 2) >= 16 &&
+      while (row_blocks * splits < target_blocks && col_pairs / (splits * 2) >= 16 &&
              splits < 64)
         splits *= 2;
     }
@@ -791,7 +835,7 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
     splits = ceil_div(col_pairs, pairs_per_split);
 
     float* partial = nullptr;
-    if (splits > 1)
+    if (splits > 1 || mixing)
       partial = ws.partial.ensure((size_t)splits * cpad * mpad);
 
     TileFn fn = a.kind == KIND_RBF ? pick_tile<KIND_RBF>(kb, ncg)
@@ -813,7 +857,14 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
       ws.tile_ms += ms;
       ws.tile_calls += 1;
     }
-    if (splits > 1) {
+    if (mixing) {
+      const int nblk = nc / a.mix_T;
+      const int64_t tot = (int64_t)nblk * a.m;
+      hipLaunchKernelGGL(k_reduce_mix, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st,
+                         partial, (int)splits, cpad, mpad, a.m, nblk, a.mix_T, a.outputscale,
+                         a.noise, a.square ? 1 : 0, Vin, a.mix, a.mix_accumulate ? 1 : 0, outc);
+      MGP_HIP_CHECK(hipGetLastError());
+    } else if (splits > 1) {
       const int64_t tot = (int64_t)nc * a.m;
       hipLaunchKernelGGL(k_reduce_splits, dim3((unsigned)ceil_div(tot, 256)), dim3(256),
                          0, st, partial, (int)splits, cpad, mpad, a.m, nc,

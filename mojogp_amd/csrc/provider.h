@@ -55,6 +55,14 @@ struct Provider {
 
   // (K + noise I) V  for device arrays V, out ([ncols][n] column-major).
   void forward(const float* V, int ncols, float* out);
+  // True when forward() runs the fused tile kernel (not materialized, Gram form
+  // accurate for the packed training set).
+  bool fused_route() const;
+  // Fused route only: out[cc][t] (+)= sum_t' mix[t][t'] ((K + noise I) V)[cc][t'] for
+  // task blocks of T columns (mix: device [T][T]), mixing folded into the
+  // split-K reduction.
+  void forward_mixed(const float* V, int ncols, const float* mix, int T, bool accumulate,
+                     float* out);
   // out[p][c][i] = sum_j dk_p(x_i, x_j) V[c][j] for all P parameters (device
   // arrays; out is [P][ncols][n]).
   DevBuf<float> gscale;  // per-parameter scale of the gradient sums

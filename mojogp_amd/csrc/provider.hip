@@ -120,6 +120,25 @@ void Provider::forward(const float* V, int ncols, float* out) {
   fused_matvec(a, train, train, V, out, ws, st);
 }
 
+bool Provider::fused_route() const { return !materialized && gram_form_ok(kind, train, train); }
+
+void Provider::forward_mixed(const float* V, int ncols, const float* mix, int T, bool accumulate,
+                             float* out) {
+  MGP_REQUIRE(fused_route(), "forward_mixed needs the fused tile route");
+  MatvecArgs a;
+  a.kind = kind;
+  a.outputscale = outputscale();
+  a.noise = noise;
+  a.square = true;
+  a.m = n;
+  a.n = n;
+  a.ncols = ncols;
+  a.mix = mix;
+  a.mix_T = T;
+  a.mix_accumulate = accumulate;
+  fused_matvec(a, train, train, V, out, ws, st);
+}
+
 void Provider::cross(const PackedPoints& rows, const float* V, int ncols,
                      float* out) {
   MatvecArgs a;
