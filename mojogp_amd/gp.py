@@ -677,42 +677,85 @@ class SingleOutputGP:
 
     # ------------------------------------------------------------ persistence
     def save(self, path) -> None:
-        """``<path>_config.json`` (schema v1) + ``<path>_arrays.npz`` (gp.py:3648-3733)."""
+        """``<path>_config.json`` + ``<path>_arrays.npz`` in the reference's
+        schema v1 (gp.py:3648-3733): same config keys and array names, so
+        models round-trip with files the reference writes and reads."""
         if not self._is_trained:
-            raise RuntimeError("Cannot save an untrained model")
+            raise RuntimeError("GP must be trained before saving.")
+        from . import __version__
         path = str(path)
+        if path.endswith(".json") or path.endswith(".npz"):
+            path = path.rsplit(".", 1)[0]
         tr = self._training_result
-        cfg = {"schema_version": _MODEL_SCHEMA_VERSION,
-               "kernel": self._original_kernel.to_dict(),
-               "training_route": self._training_method,
-               "noise": float(tr.noise), "mean": float(tr.mean), "nll": float(tr.nll),
-               "iterations": int(tr.iterations), "converged": bool(tr.converged),
-               "dim": int(self.dim), "backend_train_info": self._backend_train_info or {}}
+        cfg = {
+            "schema_version": _MODEL_SCHEMA_VERSION, "mojogp_version": __version__,
+            "wrapper": "SingleOutputGP", "dim": int(self.dim), "ard": bool(self.ard),
+            "verbose": bool(self.verbose), "cat_dims": {}, "cat_kernel": "ehh",
+            "kernel_mojo_type": self.kernel.to_mojo_type(),
+            "kernel_tree": self._original_kernel.to_dict(), "is_mixed": False,
+            "training_method": self._training_method,
+            "engine_mean": self._engine_predict_mean,
+            "backend_train_info": self._backend_train_info,
+            "cached_love_method": self._cached_love_method, "noise_mode": "scalar",
+            "noise_floor": float(self._noise_floor),
+            "noise_regularization": float(self._noise_regularization),
+            "noise_function": None, "provider_noise_mode_int": None,
+            "has_observation_noise_train": False, "has_observation_noise_fn": False,
+            "has_noise_group_train": False, "has_group_noise": False,
+            "result_type": "TrainingResult", "noise": float(tr.noise), "mean": float(tr.mean),
+            "nll": float(tr.nll), "iterations": int(tr.iterations),
+            "converged": bool(tr.converged), "lanczos_rank": int(tr.lanczos_rank),
+        }
         Path(path + "_config.json").write_text(json.dumps(cfg, indent=2, default=float))
         np.savez(path + "_arrays.npz", X_train=self._X_train, y_train=self._y_train,
                  params=np.asarray(tr.params, np.float32))
 
     @classmethod
-    def load(cls, path) -> "SingleOutputGP":
+    def load(cls, path, kernel: Optional[KernelNode] = None) -> "SingleOutputGP":
+        """Load a model saved by :meth:`save` or by the reference's
+        ``SingleOutputGP.save`` (gp.py:3735-3911) for the continuous, scalar-noise
+        models this engine serves."""
         path = str(path)
+        if path.endswith(".json") or path.endswith(".npz"):
+            path = path.rsplit(".", 1)[0]
         cfg = json.loads(Path(path + "_config.json").read_text())
+        if cfg.get("wrapper") != "SingleOutputGP":
+            raise ValueError("Saved model is not a SingleOutputGP artifact. Expected "
+                             f"wrapper='SingleOutputGP', got {cfg.get('wrapper')!r}.")
         if int(cfg.get("schema_version", 0)) != _MODEL_SCHEMA_VERSION:
-            raise ValueError("unsupported model schema version")
+            raise ValueError(f"Unsupported SingleOutputGP schema_version="
+                             f"{cfg.get('schema_version')}; expected {_MODEL_SCHEMA_VERSION}.")
+        if cfg.get("is_mixed") or cfg.get("result_type", "TrainingResult") != "TrainingResult":
+            raise NotImplementedError("mixed continuous/categorical models are outside the "
+                                      "gfx950 engine")
+        if cfg.get("noise_mode", "scalar") != "scalar" or any(
+                cfg.get(k) for k in ("has_observation_noise_train", "has_observation_noise_fn",
+                                     "has_noise_group_train", "has_group_noise")):
+            raise NotImplementedError("only scalar learned noise is served by the gfx950 engine")
         arr = np.load(path + "_arrays.npz", allow_pickle=False)
-        gp = cls(KernelNode.from_dict(cfg["kernel"]))
+        if kernel is None:
+            if "kernel_tree" not in cfg:
+                raise ValueError("SingleOutputGP artifact is missing required kernel_tree.")
+            kernel = KernelNode.from_dict(cfg["kernel_tree"])
+        gp = cls(kernel, init_mean=cfg.get("init_mean"), verbose=cfg.get("verbose", False))
         gp._X_train = np.ascontiguousarray(arr["X_train"], np.float32)
         gp._y_train = np.ascontiguousarray(arr["y_train"], np.float32)
-        gp.dim = int(cfg["dim"])
+        gp.dim = int(gp._X_train.shape[1])
         gp.kernel = make_ard_kernel(gp._kernel_pre_ard, gp.dim) if gp.ard else gp._kernel_pre_ard
-        gp._training_method = cfg.get("training_route", "matrix_free")
+        gp._training_method = cfg.get("training_method") or "matrix_free"
         gp._backend_train_info = cfg.get("backend_train_info") or {}
+        gp._cached_love_method = cfg.get("cached_love_method")
+        gp._noise_floor = float(cfg.get("noise_floor", 1e-6))
+        gp._noise_regularization = float(cfg.get("noise_regularization", 0.0))
         gp._training_result = TrainingResult(
             params=np.asarray(arr["params"], np.float32), noise=float(cfg["noise"]),
-            mean=float(cfg["mean"]), nll=float(cfg["nll"]), iterations=int(cfg["iterations"]),
-            converged=bool(cfg["converged"]), lanczos_root=None,
-            lanczos_rank=int(gp._backend_train_info.get("max_tridiag_iter", 30)))
-        gp._engine_predict_mean = float(cfg["mean"])
-        gp._fitted_mean = float(cfg["mean"])
+            mean=float(cfg.get("mean", 0.0)), nll=float(cfg["nll"]),
+            iterations=int(cfg["iterations"]), converged=bool(cfg["converged"]),
+            lanczos_root=None, lanczos_rank=int(cfg["lanczos_rank"]))
+        engine_mean = cfg.get("engine_mean")
+        gp._engine_predict_mean = float(engine_mean if engine_mean is not None
+                                        else gp._training_result.mean)
+        gp._fitted_mean = gp._training_result.mean
         gp._is_trained = True
         gp._ensure_compiled()
         return gp

@@ -167,6 +167,30 @@ class KernelNode:
         return p.copy()
 
     # ---------------------------------------------------------- serialisation
+    # Type names written into saved model configs ("kernel_mojo_type"); the
+    # strings are the reference's (kernel.py:273-321) so saved files match.
+    _ARD_TYPE_NAMES = {
+        KernelType.RBF: "RBFComposableARD", KernelType.MATERN12: "Matern12ComposableARD",
+        KernelType.MATERN32: "Matern32ComposableARD",
+        KernelType.MATERN52: "Matern52ComposableARD",
+        KernelType.PERIODIC: "PeriodicComposableARD", KernelType.RQ: "RQComposableARD",
+        KernelType.LINEAR: "LinearComposableARD",
+        KernelType.POLYNOMIAL: "PolynomialComposableARD",
+    }
+
+    def to_mojo_type(self) -> str:
+        if self.kernel_type is not None:
+            if self.ard_dim is not None:
+                return f"{self._ARD_TYPE_NAMES[self.kernel_type]}[{self.ard_dim}]"
+            return self.kernel_type.value
+        if self.operator == "sum":
+            return f"SumKernel[{self.left.to_mojo_type()}, {self.right.to_mojo_type()}]"
+        if self.operator == "product":
+            return f"ProductKernel[{self.left.to_mojo_type()}, {self.right.to_mojo_type()}]"
+        if self.operator == "scale":
+            return f"ScaleKernel[{self.left.to_mojo_type()}]"
+        raise ValueError(f"Unknown operator: {self.operator}")
+
     def to_dict(self) -> Dict[str, Any]:
         d: Dict[str, Any] = {}
         if self.kernel_type is not None:

@@ -602,19 +602,21 @@ class MultiOutputLMCGP:
         path = str(path)
         if path.endswith(".json") or path.endswith(".npz"):
             path = path.rsplit(".", 1)[0]
+        from . import __version__
         tr = self._result
-        cfg = {"schema_version": _MODEL_SCHEMA_VERSION, "wrapper": "MultiOutputLMCGP",
-               "ard": self.ard, "method": self.method, "num_probes": self.num_probes,
-               "max_cg_iter": self.max_cg_iter, "cg_tol": self.cg_tol,
-               "use_preconditioner": self.use_preconditioner, "precond_rank": self.precond_rank,
-               "precond": self.precond, "precond_rebuild_threshold": self.precond_rebuild_threshold,
-               "max_tridiag_iter": self.max_tridiag_iter,
+        cfg = {"schema_version": _MODEL_SCHEMA_VERSION, "mojogp_version": __version__,
+               "wrapper": "MultiOutputLMCGP", "is_composite": True,
+               "has_mixed_latents": False, "ard": self.ard, "method": self.method,
+               "num_probes": self.num_probes, "max_cg_iter": self.max_cg_iter,
+               "cg_tol": self.cg_tol, "use_preconditioner": self.use_preconditioner,
+               "precond_rank": self.precond_rank, "precond": self.precond,
+               "precond_rebuild_threshold": self.precond_rebuild_threshold,
                "num_latents": tr.num_latents, "num_tasks": tr.num_tasks,
                "final_nll": float(tr.final_nll), "iterations": int(tr.iterations),
                "converged": bool(tr.converged), "use_ard": bool(tr.use_ard),
                "has_fixed_observation_noise": self._fixed_observation_noise is not None,
                "kernel_trees": [k.to_dict() for k in self._original_kernels],
-               "backend_train_info": self._backend_train_info or {}}
+               "kernel_mojo_type": self._original_kernels[0].to_mojo_type()}
         Path(path + "_config.json").write_text(json.dumps(cfg, indent=2, default=float))
         arrays = {"X_train": self._X_train, "Y_train": self._Y_train,
                   "lengthscales": tr.lengthscales, "outputscales": tr.outputscales,
@@ -639,14 +641,22 @@ class MultiOutputLMCGP:
             raise ValueError("saved model is not a MultiOutputLMCGP")
         if int(cfg.get("schema_version", 0)) != _MODEL_SCHEMA_VERSION:
             raise ValueError("unsupported model schema version")
+        if cfg.get("has_mixed_latents"):
+            raise NotImplementedError("mixed continuous/categorical LMC latents are outside "
+                                      "the gfx950 engine")
         arr = np.load(path + "_arrays.npz", allow_pickle=False)
+        missing = [k for k in ("X_train", "Y_train", "noise_per_task", "A_matrices",
+                               "nll_history") if k not in arr]
+        if missing:
+            raise ValueError("MultiOutputLMCGP artifact is missing required arrays: "
+                             + ", ".join(missing))
         if kernels is None:
             kernels = [KernelNode.from_dict(k) for k in cfg["kernel_trees"]]
         gp = cls(kernels, num_probes=cfg["num_probes"], max_cg_iterations=cfg["max_cg_iter"],
                  cg_tolerance=cfg["cg_tol"], preconditioner_rank=cfg["precond_rank"],
                  precond_rebuild_threshold=cfg["precond_rebuild_threshold"],
                  preconditioner=cfg["precond"], use_preconditioner=cfg["use_preconditioner"],
-                 max_tridiag_iterations=cfg.get("max_tridiag_iter", 30), ard=cfg["ard"])
+                 ard=cfg["ard"])
         gp.method = cfg.get("method", "materialized")
         gp._X_train = np.ascontiguousarray(arr["X_train"], np.float32)
         gp._Y_train = np.ascontiguousarray(arr["Y_train"], np.float32)
@@ -672,7 +682,7 @@ class MultiOutputLMCGP:
             iter_times_ms=get("iter_times_ms"), fixed_observation_noise=gp._fixed_observation_noise)
         fm = get("fitted_mean")
         gp._fitted_mean = fm if fm is not None else gp._result.mean_per_task
-        gp._backend_train_info = cfg.get("backend_train_info") or {}
+        gp._backend_train_info = {"training_route": gp.method}
         gp._engine = _engine.load_engine()
         gp._is_trained = True
         return gp
