@@ -83,7 +83,7 @@ struct LMCPrecond {
 
 struct LMCWork {
   CGWork cg;
-  DevBuf<float> probes, probe_norms, rhs_norms, rhs, sol, lf, rf, rfm, krf, zr, zn;
+  DevBuf<float> probes, probe_norms, rhs_norms, rhs, sol, lf, rf, rfm, krf, zr, zn, facs;
   DevBuf<double> part;
   bool has_x = false;
 };

@@ -504,18 +504,18 @@ LMCEval lmc_bbmm(LMCModel& m, LMCPrecond* P, const float* y_c, int num_probes, i
     lfac[1 + j] = (0.5f / (float)Pn) * norms[j];
     rfac[1 + j] = norms[j];
   }
-  DevBuf<float> facs;
-  facs.ensure(2 * (size_t)C);
-  MGP_HIP_CHECK(hipMemcpyAsync(facs.ptr, lfac.data(), C * sizeof(float), hipMemcpyHostToDevice, st));
-  MGP_HIP_CHECK(hipMemcpyAsync(facs.ptr + C, rfac.data(), C * sizeof(float), hipMemcpyHostToDevice, st));
+  float* facs = w.facs.ensure(2 * (size_t)C);
+  std::vector<float> hfac(lfac);
+  hfac.insert(hfac.end(), rfac.begin(), rfac.end());
+  MGP_HIP_CHECK(hipMemcpyAsync(facs, hfac.data(), 2 * C * sizeof(float), hipMemcpyHostToDevice, st));
   float* lf = w.lf.ensure(nC);
   float* rf = w.rf.ensure(nC);
   copy(lf, sol, nC, st);
-  scale_columns(lf, facs.ptr, N, C, false, st);
+  scale_columns(lf, facs, N, C, false, st);
   copy(rf, sol, N, st);
   if (Pn > 0) {
     copy(rf + N, probes, nP, st);
-    scale_columns(rf + N, facs.ptr + C + 1, N, Pn, false, st);
+    scale_columns(rf + N, facs + C + 1, N, Pn, false, st);
     if (pre) P->apply(rf + N, Pn, rf + N, nullptr, st);
   }
   // Kernel-parameter gradients per latent: tr((A_s (x) dK_s) Rf Lf^T) =
