@@ -420,6 +420,111 @@ MGP_API int mgp_lmc_pathwise_correction(void* const* providers, int R, int T,
                                         float* correction_out,
                                         int* cg_iterations);
 
+/* ------------------------------------------------------------------ ICM
+ * Intrinsic Coregionalization Model: K_full = os (B (x) K_X) + D with
+ * B = W W^T + diag(softplus(raw_v)) over one base-kernel provider (created
+ * with noise 0).  Task-blocked vectors are [T][n]. */
+
+/* Training options of mgp_icm_train (train_multi_output arguments 8-21,
+ * jit_engine_multi_output_bindings.mojo:57-84). */
+typedef struct mgp_icm_train_opts {
+  int max_iterations;
+  float learning_rate;
+  int task_rank;       /* rank R of W; -1: T */
+  int num_probes;
+  int max_cg_iter;
+  float cg_tol;
+  int precond_rank;    /* 0: no preconditioner */
+  int precond_method;  /* 0 greedy, 1 rpcholesky, 2 nystrom */
+  float precond_rebuild_threshold;
+  int max_tridiag_iter;
+  int early_stop_patience;
+  float early_stop_tol; /* 0 disables early stopping */
+  int use_cosine_lr;
+  int progress_interval;
+} mgp_icm_train_opts_t;
+
+/* Result of mgp_icm_train (the reference's result dict,
+ * jit_engine_multi_output_bindings.mojo:241-320).  Caller-allocated arrays
+ * (any may be NULL): params[P], noise[T], mean[T], B[T][T] (without the
+ * outputscale), alpha[T][n], nll_history / cg_iterations_history /
+ * iter_times_ms [max_iterations]. */
+typedef struct mgp_icm_train_result {
+  float* params;
+  float* noise;
+  float* mean;
+  float* B;
+  float* alpha;
+  float* nll_history;
+  int* cg_iterations_history;
+  double* iter_times_ms;
+  int history_len;
+  float outputscale;
+  float final_nll;
+  int iterations;
+  int converged;
+  int task_rank;
+  int precond_rebuild_count;
+} mgp_icm_train_result_t;
+
+/* Adam training of the base-kernel parameters, the ICM outputscale, per-task
+ * noise, W, raw_v and per-task means by BBMM on the T*n joint system with the
+ * Kronecker preconditioner; y_blocked [T][n]; fixed_noise [T][n] (or NULL)
+ * replaces the per-task noise and disables the preconditioner.  The provider
+ * ends with the best parameters.  Replaces train_multi_output()
+ * (train_multi_output_python, jit_engine_multi_output_bindings.mojo:57-326 ->
+ * train_multi_output_jit, kernels/jit/jit_multi_output.mojo:130-817). */
+MGP_API int mgp_icm_train(void* provider, int T, const float* y_blocked,
+                          const float* init_params, const int* trainable,
+                          const float* init_noise, float init_outputscale,
+                          const float* init_mean, const float* fixed_noise,
+                          const mgp_icm_train_opts_t* opts, mgp_progress_cb cb,
+                          void* user, mgp_icm_train_result_t* out);
+
+/* Mean [m][T] (and variance [m][T] for variance_method 1 LOVE / 2 exact)
+ * from the rotated posterior state: alpha_rot [T][n] (eigen-task s's
+ * weights in row s), Q [T][T] row-major and scales[T] the eigenvectors and
+ * eigenvalues of os B; variance of eigen-task s at noise / scales[s].  The
+ * provider's parameters must already be set.  Replaces predict_multi_output()
+ * (predict_multi_output_python, jit_engine_multi_output_bindings.mojo:329-549). */
+MGP_API int mgp_icm_predict(void* provider, int T, const float* alpha_rot,
+                            const float* Q, const float* scales, const float* Xs,
+                            int64_t m, float noise, int variance_method,
+                            int max_cg_iter, float cg_tol, int precond_rank,
+                            int lanczos_rank, float* mean_out, float* var_out);
+
+/* One BBMM evaluation of the ICM marginal likelihood at fixed parameters
+ * (y_c task-blocked, mean removed): NLL per joint entry, y^T K^-1 y, log|K|,
+ * base-kernel gradients [P], dNLL/d(os), dNLL/dB [T][T] (os times the
+ * mixing gradient, before the reference's +-10 clip), dNLL/dnoise [T] and
+ * alpha [T][n], under a Kronecker preconditioner of precond_rank (0: none).
+ * The body of one iteration of train_multi_output_jit
+ * (jit_multi_output.mojo:406-598); internal there, exposed for parity tests. */
+MGP_API int mgp_icm_bbmm_eval(void* provider, int T, float outputscale, const float* B,
+                              const float* noise, const float* fixed_noise,
+                              const float* y_c, int num_probes, int max_cg_iter,
+                              int max_tridiag_iter, float cg_tol, int iteration,
+                              int precond_rank, int precond_method, float* nll,
+                              float* inv_quad, float* logdet, float* kernel_grads,
+                              float* grad_outputscale, float* grad_B,
+                              float* noise_grads, float* alpha_out,
+                              int* cg_iterations, float* precond_logdet);
+
+/* The Kronecker preconditioner on its own: builds it from the base provider,
+ * applies P^-1 to C task-blocked columns rhs [C][T][n] -> solved, draws
+ * num_probes N(0, P) probes with the given seed -> probes [num_probes][T][n],
+ * and returns log|P| and the factor rank.  KroneckerPreconditioner
+ * (kernels/kronecker_preconditioner.mojo:140-730); internal there, exposed
+ * for parity tests. */
+MGP_API int mgp_kron_precond(void* provider, int T, float outputscale, const float* B,
+                             const float* noise, int precond_rank, int precond_method,
+                             const float* rhs, int C, float* solved, int num_probes,
+                             uint64_t seed, float* probes, float* logdet, int* rank_out);
+
+/* Initial W [T][R] of the task covariance (TaskCovariance.__init__,
+ * kernels/task_covariance.mojo:168-210).  Host-only. */
+MGP_API int mgp_icm_task_covariance_init(int T, int R, int seed, float* W);
+
 /* Prior draws through a stationary random-Fourier-feature map, fp64:
  * out[k][i] = sqrt(os) sum_f weights[k][f] sqrt(2/F)
  *             cos(sum_q X[i][q] / lengthscales[q] * W[f][q] + phase[f]).

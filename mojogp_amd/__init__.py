@@ -3,15 +3,17 @@
 Python + NumPy host surface over hand-written HIP kernels reached through the
 C-ABI library libmojogp_amd.so (ctypes).  No torch in the product path.
 
-    from mojogp_amd import SingleOutputGP, MultiOutputLMCGP, RBF, Matern52
+    from mojogp_amd import SingleOutputGP, MultiOutputGP, MultiOutputLMCGP, RBF, Matern52
 """
 
 from .gp import PredictionResult, SingleOutputGP, TrainingResult
 from .kernel import KernelNode, KernelType, Matern12, Matern32, Matern52, RBF, make_ard_kernel
-from .multi_output_gp import LMCTrainingResult, MultiOutputLMCGP, MultiOutputPredictionResult
+from .multi_output_gp import (LMCTrainingResult, MultiOutputGP, MultiOutputLMCGP,
+                              MultiOutputPredictionResult, MultiOutputTrainingResult)
 
 __version__ = "0.1.0"
 
 __all__ = ["SingleOutputGP", "TrainingResult", "PredictionResult", "KernelNode", "KernelType",
            "RBF", "Matern52", "Matern32", "Matern12", "make_ard_kernel", "MultiOutputLMCGP",
-           "LMCTrainingResult", "MultiOutputPredictionResult"]
+           "LMCTrainingResult", "MultiOutputPredictionResult", "MultiOutputGP",
+           "MultiOutputTrainingResult"]

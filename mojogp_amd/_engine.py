@@ -108,7 +108,7 @@ def _resolve_lanczos_rank(info: dict, requested: int) -> int:
     return rank
 
 
-def _progress_bridge(callback):
+def _progress_bridge(callback, model: str = "single_output"):
     if callback is None:
         null = _lib.PROGRESS_CB()  # NULL function pointer
         return null, null
@@ -128,7 +128,7 @@ def _progress_bridge(callback):
         if ev.precond_rebuild_count >= 0:
             stats["precond_rebuild_count"] = int(ev.precond_rebuild_count)
         event = {
-            "operation": "train", "model": "single_output", "route": "unknown",
+            "operation": "train", "model": model, "route": "unknown",
             "phase": ev.phase.decode(), "current": int(ev.current), "total": int(ev.total),
             "converged": bool(ev.converged), "stats": stats,
         }
@@ -534,6 +534,180 @@ class Engine:
         _lib.call("mgp_lmc_pathwise_correction", _lib.handles(provs), R, T, _lib.fptr(A),
                   _lib.fptr(noise), _lib.ofptr(fixed), _lib.fptr(blocked), S, _lib.fptr(Xs), m,
                   max_cg, tol, _lib.fptr(corr), C.byref(its))
+        return {"correction": corr[0] if single else corr, "cg_iterations": int(its.value)}
+
+
+    # ------------------------------------------------------------ ICM
+    def train_multi_output(self, *args) -> dict[str, Any]:
+        """train_multi_output(provider_info, Y [n, T], initial_params, trainable_mask,
+        initial_noise_per_task [T], initial_outputscale, initial_mean_per_task [T],
+        num_tasks, max_iterations, learning_rate, task_rank, verbose, num_probes,
+        max_cg_iter, cg_tol, precond_rank, precond_method, precond_rebuild_threshold,
+        max_tridiag_iter, early_stop_patience, early_stop_tol [, use_cosine_lr,
+        fixed_observation_noise [n, T], progress_callback, progress_interval])
+        (train_multi_output_python, jit_engine_multi_output_bindings.mojo:57-326)."""
+        if len(args) < 21 or len(args) > 25:
+            raise ValueError("train_multi_output() expects 21 to 25 positional arguments")
+        info = args[0]
+        prov = _provider(info)
+        T = int(args[7])
+        Y = _lib.f32(args[1])
+        if Y.ndim != 2 or Y.shape[1] != T:
+            raise ValueError("Y must have shape (n, num_tasks)")
+        n = Y.shape[0]
+        params = _lib.f32(args[2]).ravel()
+        mask = np.ascontiguousarray(args[3], dtype=bool).ravel()
+        if mask.shape[0] != prov.nparams:
+            raise ValueError("train_multi_output() trainable mask length does not match "
+                             "provider gradient params")
+        if params.shape[0] != prov.nparams:
+            raise ValueError("train_multi_output() initial params length does not match "
+                             "provider gradient params")
+        noise0 = (np.full(T, 0.1, np.float32) if args[4] is None
+                  else _lib.f32(args[4]).ravel())
+        os0 = float(args[5])
+        mean0 = _lib.f32(args[6]).ravel()
+        o = _lib.ICMTrainOpts()
+        o.max_iterations = int(args[8])
+        o.learning_rate = float(args[9])
+        o.task_rank = int(args[10])
+        o.num_probes = int(args[12])
+        o.max_cg_iter = int(args[13])
+        o.cg_tol = float(args[14])
+        o.precond_rank = int(args[15])
+        o.precond_method = int(args[16])
+        o.precond_rebuild_threshold = float(args[17])
+        o.max_tridiag_iter = int(args[18])
+        o.early_stop_patience = int(args[19])
+        o.early_stop_tol = float(args[20])
+        o.use_cosine_lr = int(bool(args[21])) if len(args) > 21 else 0
+        fixed = None
+        if len(args) > 22 and args[22] is not None:
+            fn = _lib.f32(args[22])
+            if fn.shape != (n, T):
+                raise ValueError("train_multi_output() fixed observation noise must have "
+                                 "shape [n, T]")
+            fixed = np.ascontiguousarray(fn.T)
+        callback = args[23] if len(args) > 23 else None
+        o.progress_interval = int(args[24]) if len(args) > 24 else 1
+        if o.max_iterations <= 0:
+            raise ValueError("max_iterations must be > 0")
+        it_max = o.max_iterations
+        out_params = np.zeros(prov.nparams, np.float32)
+        noise = np.zeros(T, np.float32)
+        mean = np.zeros(T, np.float32)
+        B = np.zeros(T * T, np.float32)
+        alpha = np.zeros(n * T, np.float32)
+        hist = np.zeros(it_max, np.float32)
+        cg_hist = np.zeros(it_max, np.int32)
+        times = np.zeros(it_max, np.float64)
+        res = _lib.ICMTrainResult()
+        res.params, res.noise, res.mean = _lib.fptr(out_params), _lib.fptr(noise), _lib.fptr(mean)
+        res.B, res.alpha, res.nll_history = _lib.fptr(B), _lib.fptr(alpha), _lib.fptr(hist)
+        res.cg_iterations_history = cg_hist.ctypes.data_as(_lib.c_int_p)
+        res.iter_times_ms = _lib.dptr(times)
+        cfun, keep = _progress_bridge(callback, model="multi_output_icm")
+        mask_i = mask.astype(np.int32)
+        y_blocked = np.ascontiguousarray(Y.T)
+        _lib.call("mgp_icm_train", prov.handle, T, _lib.fptr(y_blocked), _lib.fptr(params),
+                  mask_i.ctypes.data_as(_lib.c_int_p), _lib.fptr(noise0), os0, _lib.fptr(mean0),
+                  _lib.ofptr(fixed), C.byref(o), cfun, None, C.byref(res))
+        del keep
+        hl = int(res.history_len)
+        prov.params = out_params.copy()
+        prov.noise = 0.0
+        mode = int(info.get("materialization_mode", 0))
+        return {
+            "final_nll": float(res.final_nll), "outputscale": float(res.outputscale),
+            "iterations": int(res.iterations), "converged": bool(res.converged),
+            "num_tasks": T, "task_rank": int(res.task_rank),
+            "max_tridiag_iter": o.max_tridiag_iter,
+            "precond_rebuild_threshold": float(o.precond_rebuild_threshold),
+            "precond_rebuild_count": int(res.precond_rebuild_count),
+            "precond_rank": o.precond_rank, "precond_method": o.precond_method,
+            "early_stop_patience": o.early_stop_patience,
+            "early_stop_tol": float(o.early_stop_tol),
+            "use_cosine_lr": bool(o.use_cosine_lr),
+            "training_route": "materialized" if mode == 1 else "matrix_free",
+            "materialization_mode": mode,
+            "noise_mode": "fixed_per_sample_task" if fixed is not None else "per_task",
+            "has_observation_noise_vector": fixed is not None,
+            "cg_iterations_history": [int(v) for v in cg_hist[:hl]],
+            "iter_times_ms": [float(v) for v in times[:hl]],
+            "nll_history": [float(v) for v in hist[:hl]],
+            "params": [float(v) for v in out_params],
+            "noise_per_task": [float(v) for v in noise],
+            "mean_per_task": [float(v) for v in mean],
+            "B_flat": [float(v) for v in B],
+            "alpha": alpha,
+        }
+
+    def predict_multi_output(self, *args) -> dict[str, Any]:
+        """predict_multi_output(provider_info, alpha_rotated [n, T], Q [T, T],
+        effective_scales [T], X_test [m, d], params, noise, variance_method
+        [, max_cg_iter, cg_tol, precond_rank, lanczos_rank])
+        (predict_multi_output_python, jit_engine_multi_output_bindings.mojo:329-549)."""
+        if len(args) < 8 or len(args) > 12:
+            raise ValueError("predict_multi_output() expects 8-12 positional arguments")
+        info = args[0]
+        prov = _provider(info)
+        alpha_rot = _lib.f32(args[1])
+        if alpha_rot.ndim != 2:
+            raise ValueError("alpha_rotated must have shape [n, T]")
+        n, T = alpha_rot.shape
+        Q = _lib.f32(args[2]).reshape(T, T)
+        scales = _lib.f32(args[3]).ravel()
+        Xs = _lib.f32(args[4])
+        prov.update_params(_lib.f32(args[5]).ravel())
+        noise = float(args[6])
+        prov.update_noise(noise)
+        vm = int(args[7])
+        max_cg = int(args[8]) if len(args) > 8 else 100
+        tol = float(args[9]) if len(args) > 9 else 1e-2
+        prank = int(args[10]) if len(args) > 10 else 10
+        lrank = _resolve_lanczos_rank(info, int(args[11]) if len(args) > 11 else 0)
+        m = Xs.shape[0]
+        mean = np.zeros((m, T), np.float32)
+        var = np.zeros((m, T), np.float32) if vm else None
+        _lib.call("mgp_icm_predict", prov.handle, T, _lib.fptr(np.ascontiguousarray(alpha_rot.T)),
+                  _lib.fptr(Q), _lib.fptr(scales), _lib.fptr(Xs), m, noise, vm, max_cg, tol,
+                  prank, lrank, _lib.fptr(mean), _lib.ofptr(var))
+        out = {"mean": mean, "lanczos_rank_used": lrank}
+        if vm:
+            out["variance"] = var
+            out["std"] = np.sqrt(var)
+        return out
+
+    def sample_multi_output_pathwise(self, *args) -> dict[str, Any]:
+        """sample_multi_output_pathwise(provider_info, residual [n, T] (or [S, n, T]),
+        B [T, T] (outputscale included), X_test [m, d], params, noise_per_task [T]
+        [, max_cg_iter, cg_tol]) (sample_multi_output_pathwise_python,
+        jit_engine_multi_output_bindings.mojo:552-712): beta = (B (x) K + D)^-1 r by
+        unpreconditioned CG per column, correction = B (x) K(X*, X) beta.  A 3-D
+        residual stack is corrected in one batched solve."""
+        if len(args) < 6 or len(args) > 8:
+            raise ValueError("sample_multi_output_pathwise() expects 6-8 positional arguments")
+        info = args[0]
+        prov = _provider(info)
+        resid = _lib.f32(args[1])
+        single = resid.ndim == 2
+        if single:
+            resid = resid[None]
+        S, n, T = resid.shape
+        B = _lib.f32(args[2]).reshape(1, T, T)
+        Xs = _lib.f32(args[3])
+        prov.update_params(_lib.f32(args[4]).ravel())
+        prov.update_noise(0.0)
+        noise = _lib.f32(args[5]).ravel()
+        max_cg = int(args[6]) if len(args) > 6 else 100
+        tol = float(args[7]) if len(args) > 7 else 1e-2
+        blocked = np.ascontiguousarray(resid.transpose(0, 2, 1))
+        m = Xs.shape[0]
+        corr = np.zeros((S, m, T), np.float32)
+        its = C.c_int(0)
+        _lib.call("mgp_lmc_pathwise_correction", _lib.handles([prov]), 1, T, _lib.fptr(B),
+                  _lib.fptr(noise), None, _lib.fptr(blocked), S, _lib.fptr(Xs), m, max_cg, tol,
+                  _lib.fptr(corr), C.byref(its))
         return {"correction": corr[0] if single else corr, "cg_iterations": int(its.value)}
 
 

@@ -110,6 +110,29 @@ class LMCTrainResult(C.Structure):
     ]
 
 
+class ICMTrainOpts(C.Structure):
+    """mgp_icm_train_opts_t"""
+    _fields_ = [
+        ("max_iterations", C.c_int), ("learning_rate", C.c_float), ("task_rank", C.c_int),
+        ("num_probes", C.c_int), ("max_cg_iter", C.c_int), ("cg_tol", C.c_float),
+        ("precond_rank", C.c_int), ("precond_method", C.c_int),
+        ("precond_rebuild_threshold", C.c_float), ("max_tridiag_iter", C.c_int),
+        ("early_stop_patience", C.c_int), ("early_stop_tol", C.c_float),
+        ("use_cosine_lr", C.c_int), ("progress_interval", C.c_int),
+    ]
+
+
+class ICMTrainResult(C.Structure):
+    """mgp_icm_train_result_t"""
+    _fields_ = [
+        ("params", c_float_p), ("noise", c_float_p), ("mean", c_float_p), ("B", c_float_p),
+        ("alpha", c_float_p), ("nll_history", c_float_p), ("cg_iterations_history", c_int_p),
+        ("iter_times_ms", c_double_p), ("history_len", C.c_int), ("outputscale", C.c_float),
+        ("final_nll", C.c_float), ("iterations", C.c_int), ("converged", C.c_int),
+        ("task_rank", C.c_int), ("precond_rebuild_count", C.c_int),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The native gfx950 library is missing or failed to load."""
 
@@ -192,6 +215,21 @@ _SIGNATURES = {
                                               c_float_p, c_float_p, c_float_p, C.c_int,
                                               c_float_p, C.c_int64, C.c_int, C.c_float,
                                               c_float_p, c_int_p]),
+    "mgp_icm_train": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_float_p, c_int_p, c_float_p,
+                                C.c_float, c_float_p, c_float_p, C.POINTER(ICMTrainOpts),
+                                PROGRESS_CB, C.c_void_p, C.POINTER(ICMTrainResult)]),
+    "mgp_icm_predict": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_float_p, c_float_p,
+                                  c_float_p, C.c_int64, C.c_float, C.c_int, C.c_int, C.c_float,
+                                  C.c_int, C.c_int, c_float_p, c_float_p]),
+    "mgp_icm_bbmm_eval": (C.c_int, [C.c_void_p, C.c_int, C.c_float, c_float_p, c_float_p,
+                                    c_float_p, c_float_p, C.c_int, C.c_int, C.c_int, C.c_float,
+                                    C.c_int, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,
+                                    c_float_p, c_float_p, c_float_p, c_float_p, c_float_p,
+                                    c_int_p, c_float_p]),
+    "mgp_kron_precond": (C.c_int, [C.c_void_p, C.c_int, C.c_float, c_float_p, c_float_p,
+                                   C.c_int, C.c_int, c_float_p, C.c_int, c_float_p, C.c_int,
+                                   C.c_uint64, c_float_p, c_float_p, c_int_p]),
+    "mgp_icm_task_covariance_init": (C.c_int, [C.c_int, C.c_int, C.c_int, c_float_p]),
     "mgp_rff_prior_values": (C.c_int, [c_float_p, C.c_int64, C.c_int, c_double_p, c_double_p,
                                        c_double_p, C.c_int, C.c_double, c_double_p, C.c_int,
                                        c_float_p]),

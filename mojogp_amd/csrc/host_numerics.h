@@ -36,6 +36,15 @@ bool spd_inverse(const std::vector<double>& A, int k, std::vector<double>& inv);
 // log|det A| via Cholesky, falling back to partial-pivot LU.
 double logdet_spd(const std::vector<double>& A, int k);
 
+// Symmetric eigen-decomposition of a small row-major matrix by the classical
+// (largest off-diagonal pivot) Jacobi method in fp64: rotations until the
+// largest |off-diagonal| < 1e-12 or 100 k^2 rotations, eigenvalues sorted
+// ascending with their eigenvector columns (V row-major, A = V diag(e) V^T).
+// The same convergence rule, rotation and ordering as the reference's
+// _symmetric_eigen_cpu (kernels/kronecker_preconditioner.mojo:736-822), so the
+// eigenvector signs agree with it.
+void jacobi_eigen(const float* A, int k, float* V, float* evals);
+
 // fp32 helpers with the reference's thresholds.
 float softplus(float x);
 float inv_softplus(float y);

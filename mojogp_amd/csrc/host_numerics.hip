@@ -269,4 +269,61 @@ float cosine_lr(float lr_max, int iteration, int total) {
   return lr_min + 0.5f * (lr_max - lr_min) * (1.0f + std::cos(pi * t));
 }
 
+void jacobi_eigen(const float* A, int k, float* V, float* evals) {
+  std::vector<double> a(A, A + (size_t)k * k), v((size_t)k * k, 0.0);
+  for (int i = 0; i < k; ++i) v[(size_t)i * k + i] = 1.0;
+  const long max_rot = 100L * k * k;
+  for (long it = 0; it < max_rot && k > 1; ++it) {
+    double big = 0.0;
+    int p = 0, q = 1;
+    for (int i = 0; i < k; ++i)
+      for (int j = i + 1; j < k; ++j)
+        if (std::fabs(a[(size_t)i * k + j]) > big) {
+          big = std::fabs(a[(size_t)i * k + j]);
+          p = i;
+          q = j;
+        }
+    if (big < 1e-12) break;
+    const double app = a[(size_t)p * k + p], aqq = a[(size_t)q * k + q];
+    const double apq = a[(size_t)p * k + q];
+    // tan of the rotation angle: the smaller root of t^2 + 2 tau t - 1 = 0
+    const double tau = (aqq - app) / (2.0 * apq);
+    const double t = tau >= 0.0 ? 1.0 / (tau + std::sqrt(1.0 + tau * tau))
+                                : -1.0 / (-tau + std::sqrt(1.0 + tau * tau));
+    const double c = 1.0 / std::sqrt(1.0 + t * t), s = t * c;
+    for (int i = 0; i < k; ++i) {  // columns p, q
+      const double ip = a[(size_t)i * k + p], iq = a[(size_t)i * k + q];
+      a[(size_t)i * k + p] = c * ip - s * iq;
+      a[(size_t)i * k + q] = s * ip + c * iq;
+    }
+    for (int j = 0; j < k; ++j) {  // rows p, q
+      const double pj = a[(size_t)p * k + j], qj = a[(size_t)q * k + j];
+      a[(size_t)p * k + j] = c * pj - s * qj;
+      a[(size_t)q * k + j] = s * pj + c * qj;
+    }
+    a[(size_t)p * k + p] = app - t * apq;
+    a[(size_t)q * k + q] = aqq + t * apq;
+    a[(size_t)p * k + q] = 0.0;
+    a[(size_t)q * k + p] = 0.0;
+    for (int i = 0; i < k; ++i) {
+      const double ip = v[(size_t)i * k + p], iq = v[(size_t)i * k + q];
+      v[(size_t)i * k + p] = c * ip - s * iq;
+      v[(size_t)i * k + q] = s * ip + c * iq;
+    }
+  }
+  std::vector<double> e(k);
+  for (int i = 0; i < k; ++i) e[i] = a[(size_t)i * k + i];
+  for (int i = 0; i < k; ++i) {  // selection sort, ascending
+    int mi = i;
+    for (int j = i + 1; j < k; ++j)
+      if (e[j] < e[mi]) mi = j;
+    if (mi != i) {
+      std::swap(e[i], e[mi]);
+      for (int r = 0; r < k; ++r) std::swap(v[(size_t)r * k + i], v[(size_t)r * k + mi]);
+    }
+  }
+  for (int i = 0; i < k; ++i) evals[i] = (float)e[i];
+  for (size_t i = 0; i < (size_t)k * k; ++i) V[i] = (float)v[i];
+}
+
 }  // namespace mgp

@@ -57,6 +57,7 @@ struct LMCStreamGuard {
 // pivoted-Cholesky factor of K_s; applied by Woodbury with the inner matrix
 // M = I + U^T D^-1 U (U = [C_s (x) L_s]_s) inverted once and applied in fp64.
 struct LMCPrecond {
+  virtual ~LMCPrecond() = default;
   int R = 0, T = 0, K = 0;  // K = sum_s r_s T
   int64_t n = 0;
   std::vector<int> rank, off;          // per latent: r_s, offset of (s, 0, 0) in K
@@ -78,7 +79,29 @@ struct LMCPrecond {
   void apply(const float* r, int C, float* z, double* rz_part, hipStream_t st);
   // N(0, P) probes: D^{1/2} eps + U w (counter-hash Gaussians, seeds
   // seed + 1000000 and seed).
-  void sample(float* out, int C, uint64_t seed, hipStream_t st);
+  virtual void sample(float* out, int C, uint64_t seed, hipStream_t st);
+};
+
+// ICM (Kronecker) preconditioner P = os (B' (x) L L^T) + D (x) I_n with
+// B' = B + 1e-6 D (the jitter D^{-1/2} B D^{-1/2} + 1e-6 I of the reference)
+// and L the rank-r pivoted-Cholesky factor of the base kernel at noise 0
+// (kernels/kronecker_preconditioner.mojo:140-400).  It is applied through the
+// LMC Woodbury path with U = D^{1/2} (x) L and the inner matrix replaced by
+// (Q~ (x) V) diag(C^-1) (Q~ (x) V)^T, where L^T L = V Sigma V^T,
+// D^{-1/2} B D^{-1/2} + 1e-6 I = Q~ Lambda~ Q~^T (Jacobi, fp64) and
+// C^-1[j][i] = 1 / (1/(os lambda_j) + sigma_i); log|P| = n sum_t log noise_t +
+// sum_{j,i} log(1 + os lambda_j sigma_i).  Probes are
+// D^{1/2} z_noise + (C_B (x) L) z_rank with C_B = sqrt(os) D^{1/2} Q~ Lambda~^{1/2},
+// z_noise = gaussian(C*n*T, seed + 12345) ([C][T][n]) and
+// z_rank = gaussian(C*r*T, seed) at index (t*C + c)*r + k (:629-730).
+struct KronPrecond : LMCPrecond {
+  std::vector<float> Cb;             // [T][T] probe factor C_B
+  std::vector<float> sigma, lambda;  // eigenvalues of L^T L and of B~ (ascending)
+  DevBuf<float> Cb_dev, zraw;
+  // m: one-latent model over the base kernel (its A and noise are not read).
+  void build_kron(LMCModel& m, int precond_rank, const PivotOptions& po, float os,
+                  const std::vector<float>& B, const std::vector<float>& noise_t);
+  void sample(float* out, int C, uint64_t seed, hipStream_t st) override;
 };
 
 struct LMCWork {

@@ -107,6 +107,18 @@ __global__ void k_gather_z(const float* __restrict__ z, int T, int r, int C, int
   Z[idx] = z[(int64_t)c * K + off + rem];
 }
 
+// w[c][t*r + k] = raw[(t*C + c)*r + k]: the Kronecker preconditioner's rank
+// draws in its probe-major-per-task order, regrouped per probe
+__global__ void k_kron_zrank(const float* __restrict__ raw, int T, int r, int C,
+                             float* __restrict__ w) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t K = (int64_t)T * r;
+  if (idx >= K * C) return;
+  const int64_t c = idx / K, rem = idx - c * K;
+  const int64_t t = rem / r, k = rem - t * r;
+  w[idx] = raw[(t * C + c) * r + k];
+}
+
 // out = w - dinv[t] * res   (Woodbury final step)
 __global__ void k_woodbury_lmc(float* __restrict__ out, const float* __restrict__ w,
                                const float* __restrict__ res, const float* __restrict__ dinv,
@@ -364,7 +376,9 @@ void LMCPrecond::build(LMCModel& m, int precond_rank, const PivotOptions& po) {
 }
 
 // res = U z for C columns:  res[c][t] = sum_s sum_j C_s[t][j] L_s z[c][(s, j, .)]
-static void lmc_u_times(LMCPrecond& P, const float* z, int C, float* res, hipStream_t st) {
+// (cs: another T x T factor per latent in place of C_s)
+static void lmc_u_times(LMCPrecond& P, const float* z, int C, float* res, hipStream_t st,
+                        const float* cs = nullptr) {
   const int64_t total = P.n * P.T * (int64_t)C;
   bool first = true;
   for (int s = 0; s < P.R; ++s) {
@@ -376,7 +390,8 @@ static void lmc_u_times(LMCPrecond& P, const float* z, int C, float* res, hipStr
     float* ol = P.out_l.ensure((size_t)total);
     l_matmul(P.L[s]->ptr, P.n, r, Z, C * P.T, ol, st);
     hipLaunchKernelGGL(k_lmc_mix, g1(total), dim3(256), 0, st, res, ol,
-                       P.Cs_dev.ptr + (size_t)s * P.T * P.T, P.n, P.T, C, first ? 0 : 1);
+                       (cs ? cs : P.Cs_dev.ptr) + (size_t)s * P.T * P.T, P.n, P.T, C,
+                       first ? 0 : 1);
     first = false;
   }
   if (first) fill(res, total, 0.0f, st);
@@ -419,6 +434,131 @@ void LMCPrecond::sample(float* out, int C, uint64_t seed, hipStream_t st) {
   float* rs_ = res.ensure((size_t)total);
   lmc_u_times(*this, wr, C, rs_, st);
   // out = D^{1/2} eps + U w
+  copy(out, rs_, total, st);
+  hipLaunchKernelGGL(k_task_scale, g1(total), dim3(256), 0, st, out, eps, dsqrt.ptr, n, T, C,
+                     1.0f);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------------ Kronecker preconditioner
+void KronPrecond::build_kron(LMCModel& m, int precond_rank, const PivotOptions& po, float os,
+                             const std::vector<float>& B, const std::vector<float>& noise_t) {
+  R = 1;
+  T = m.T;
+  n = m.n;
+  K = 0;
+  check((int)B.size() == T * T && (int)noise_t.size() == T, "Kronecker preconditioner sizes");
+  if (precond_rank <= 0) return;
+  hipStream_t st = m.st;
+  rank.assign(1, 0);
+  off.assign(1, 0);
+  L.clear();
+  L.push_back(std::make_unique<DevBuf<float>>());
+  Provider& pv = *m.prov[0];
+  const float saved = pv.noise;
+  pv.noise = 0.0f;  // factor of the base kernel at noise 0 (jit_multi_output.mojo:287-297)
+  L[0]->ensure((size_t)precond_rank * n);
+  const int r = pivoted_cholesky(pv, precond_rank, po, L[0]->ptr, st);
+  pv.noise = saved;
+  rank[0] = r;
+  if (r == 0) return;
+  K = r * T;
+  // L^T L (fp32 as the reference's GPU matmul) and its eigenpairs
+  DevBuf<double> ltl_dev;
+  ltl_dev.ensure((size_t)r * r);
+  cross_ltl(L[0]->ptr, r, L[0]->ptr, r, n, ltl_dev.ptr, st);
+  std::vector<double> ltl((size_t)r * r);
+  MGP_HIP_CHECK(hipMemcpy(ltl.data(), ltl_dev.ptr, ltl.size() * sizeof(double),
+                          hipMemcpyDeviceToHost));
+  std::vector<float> ltlf(ltl.begin(), ltl.end()), V((size_t)r * r), Qt((size_t)T * T);
+  sigma.assign(r, 0.0f);
+  lambda.assign(T, 0.0f);
+  jacobi_eigen(ltlf.data(), r, V.data(), sigma.data());
+  // B~ = D^-1/2 B D^-1/2 + 1e-6 I and its eigenpairs
+  std::vector<float> dis(T), ds(T), Bt((size_t)T * T);
+  for (int t = 0; t < T; ++t) {
+    check(noise_t[t] > 0.0f, "Kronecker preconditioner needs positive task noise");
+    dis[t] = 1.0f / std::sqrt(noise_t[t]);
+    ds[t] = std::sqrt(noise_t[t]);
+  }
+  for (int a = 0; a < T; ++a)
+    for (int b = 0; b < T; ++b)
+      Bt[(size_t)a * T + b] = dis[a] * B[(size_t)a * T + b] * dis[b] + (a == b ? 1e-6f : 0.0f);
+  jacobi_eigen(Bt.data(), T, Qt.data(), lambda.data());
+  // C^-1 and log|P| with the reference's clamps (fp32)
+  const float clampv = 1e-8f;
+  std::vector<float> cinv((size_t)T * r);
+  float ld = 0.0f;
+  for (int t = 0; t < T; ++t) ld += (float)n * std::log(noise_t[t]);
+  for (int j = 0; j < T; ++j) {
+    const float lj = std::max(lambda[j], clampv);
+    for (int i = 0; i < r; ++i) {
+      const float si = std::max(sigma[i], clampv);
+      cinv[(size_t)j * r + i] = 1.0f / (1.0f / (os * lj) + si);
+      float arg = 1.0f + os * lj * si;
+      if (arg <= 0.0f) arg = 1e-10f;
+      ld += std::log(arg);
+    }
+  }
+  logdet = ld;
+  // Inner matrix (Q~ (x) V) diag(C^-1) (Q~ (x) V)^T, index t*r + k, in fp64:
+  // H_j = V diag(C^-1[j][.]) V^T, then sum_j Q~[t][j] Q~[t'][j] H_j.
+  std::vector<double> inner((size_t)K * K, 0.0), H((size_t)r * r);
+  for (int j = 0; j < T; ++j) {
+    for (int k1 = 0; k1 < r; ++k1)
+      for (int k2 = 0; k2 < r; ++k2) {
+        double h = 0.0;
+        for (int i = 0; i < r; ++i)
+          h += (double)V[(size_t)k1 * r + i] * (double)V[(size_t)k2 * r + i] *
+               (double)cinv[(size_t)j * r + i];
+        H[(size_t)k1 * r + k2] = h;
+      }
+    for (int t1 = 0; t1 < T; ++t1)
+      for (int t2 = 0; t2 < T; ++t2) {
+        const double q = (double)Qt[(size_t)t1 * T + j] * (double)Qt[(size_t)t2 * T + j];
+        if (q == 0.0) continue;
+        for (int k1 = 0; k1 < r; ++k1) {
+          double* row = inner.data() + ((size_t)t1 * r + k1) * K + (size_t)t2 * r;
+          const double* hr = H.data() + (size_t)k1 * r;
+          for (int k2 = 0; k2 < r; ++k2) row[k2] += q * hr[k2];
+        }
+      }
+  }
+  Minv.ensure(inner.size());
+  MGP_HIP_CHECK(hipMemcpy(Minv.ptr, inner.data(), inner.size() * sizeof(double),
+                          hipMemcpyHostToDevice));
+  // U = D^1/2 (x) L for the shared Woodbury apply; C_B for the probes
+  noise = noise_t;
+  Cs.assign((size_t)T * T, 0.0f);
+  for (int t = 0; t < T; ++t) Cs[(size_t)t * T + t] = ds[t];
+  Cb.assign((size_t)T * T, 0.0f);
+  const float sos = std::sqrt(os);
+  for (int a = 0; a < T; ++a)
+    for (int j = 0; j < T; ++j)
+      Cb[(size_t)a * T + j] =
+          sos * ds[a] * Qt[(size_t)a * T + j] * std::sqrt(std::max(lambda[j], clampv));
+  std::vector<float> di(T);
+  for (int t = 0; t < T; ++t) di[t] = 1.0f / noise_t[t];
+  dinv.ensure(T);
+  dsqrt.ensure(T);
+  Cs_dev.ensure(Cs.size());
+  Cb_dev.ensure(Cb.size());
+  MGP_HIP_CHECK(hipMemcpy(dinv.ptr, di.data(), T * sizeof(float), hipMemcpyHostToDevice));
+  MGP_HIP_CHECK(hipMemcpy(dsqrt.ptr, ds.data(), T * sizeof(float), hipMemcpyHostToDevice));
+  MGP_HIP_CHECK(hipMemcpy(Cs_dev.ptr, Cs.data(), Cs.size() * sizeof(float), hipMemcpyHostToDevice));
+  MGP_HIP_CHECK(hipMemcpy(Cb_dev.ptr, Cb.data(), Cb.size() * sizeof(float), hipMemcpyHostToDevice));
+}
+
+void KronPrecond::sample(float* out, int C, uint64_t seed, hipStream_t st) {
+  const int64_t nT = n * T, total = nT * C;
+  float* eps = w.ensure((size_t)total);
+  gaussian(eps, total, seed + 12345ull, st);
+  float* raw = zraw.ensure((size_t)C * K);
+  gaussian(raw, (int64_t)C * K, seed, st);
+  float* wr = zk.ensure((size_t)C * K);
+  hipLaunchKernelGGL(k_kron_zrank, g1((int64_t)C * K), dim3(256), 0, st, raw, T, rank[0], C, wr);
+  float* rs_ = res.ensure((size_t)total);
+  lmc_u_times(*this, wr, C, rs_, st, Cb_dev.ptr);
   copy(out, rs_, total, st);
   hipLaunchKernelGGL(k_task_scale, g1(total), dim3(256), 0, st, out, eps, dsqrt.ptr, n, T, C,
                      1.0f);

@@ -20,7 +20,7 @@ latents, composite kernel trees and heteroskedastic noise models raise
 from __future__ import annotations
 
 import json
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Any, Optional, Union
 
@@ -691,3 +691,751 @@ class MultiOutputLMCGP:
         kinds = ", ".join(k.kernel_type.name.lower() for k in self._original_kernels)
         return (f"MultiOutputLMCGP(kernels=[{kinds}], num_latents={self.num_latents}, "
                 f"trained={self._is_trained})")
+
+
+# =============================================================================
+# ICM multi-output GP
+# =============================================================================
+
+_ICM_PRESETS = {
+    "fast": {"max_cg_iter": 50, "cg_tol": 5e-2, "num_probes": 5, "max_tridiag_iter": 15,
+             "precond_rank": 5, "precond_rebuild_threshold": 0.75, "precond": "greedy"},
+    "balanced": {"max_cg_iter": 200, "cg_tol": 1e-2, "num_probes": 10, "max_tridiag_iter": 30,
+                 "precond_rank": 15, "precond_rebuild_threshold": 0.5, "precond": "greedy"},
+    "accurate": {"max_cg_iter": 400, "cg_tol": 1e-2, "num_probes": 20, "max_tridiag_iter": 60,
+                 "precond_rank": 20, "precond_rebuild_threshold": 0.25, "precond": "greedy"},
+}
+_PATHWISE_TEST_CHUNK = 512
+
+
+@dataclass
+class MultiOutputTrainingResult:
+    """Trained ICM state (multi_output_gp.py:475-542)."""
+
+    params: np.ndarray
+    noise: float
+    noise_per_task: np.ndarray
+    final_nll: float
+    iterations: int
+    converged: bool
+    num_tasks: int
+    task_rank: int
+    num_kernel_params: int
+    B: np.ndarray                 # [T, T] outputscale * task covariance
+    Q: np.ndarray                 # [T, T] eigenvectors of B
+    Lambda: np.ndarray            # [T] eigenvalues of B, floored at 1e-6
+    effective_scales: np.ndarray  # alias of Lambda
+    W: np.ndarray
+    raw_v: np.ndarray
+    alpha_rotated: np.ndarray     # [n, T]
+    mean_per_task: np.ndarray
+    nll_history: np.ndarray
+    param_names: list
+    cat_params: Optional[np.ndarray] = None
+    cat_param_names: list = field(default_factory=list)
+    iter_times_ms: Optional[np.ndarray] = None
+
+    @property
+    def lengthscale(self) -> float:
+        for i, name in enumerate(self.param_names):
+            if "lengthscale" in name and "ls_" not in name:
+                return float(self.params[i])
+        return float(self.params[0])
+
+    @property
+    def outputscale(self) -> float:
+        for i, name in enumerate(self.param_names):
+            if "outputscale" in name:
+                return float(self.params[i])
+        return float(self.params[-1])
+
+    @property
+    def lengthscales(self) -> np.ndarray:
+        idxs = [i for i, nm in enumerate(self.param_names) if "ls_" in nm]
+        if idxs:
+            return self.params[idxs]
+        return np.array([self.lengthscale], dtype=np.float32)
+
+    @property
+    def dim(self) -> int:
+        return len(self.lengthscales)
+
+
+def _resolve_observed_noise(m: int, T: int, observation_noise=None, noise_group_test=None,
+                            group_noise=None) -> np.ndarray:
+    """Explicit test-point noise [m, T] (multi_output_gp.py:553-603)."""
+    if observation_noise is not None and noise_group_test is not None:
+        raise ValueError("Pass either observation_noise or noise_group_test for observed "
+                         "prediction, not both")
+    if observation_noise is not None:
+        noise = np.ascontiguousarray(observation_noise, dtype=np.float32)
+        if noise.shape != (m, T):
+            raise ValueError(f"observation_noise must have shape ({m}, {T}), got {noise.shape}")
+    elif noise_group_test is not None:
+        if group_noise is None:
+            raise ValueError("noise_group_test requires group_noise from fitted grouped noise "
+                             "state")
+        groups = np.ascontiguousarray(noise_group_test, dtype=np.int32)
+        if groups.shape != (m,):
+            raise ValueError(f"noise_group_test must have shape ({m},), got {groups.shape}")
+        if np.any(groups < 0):
+            raise ValueError("noise_group_test must contain non-negative group ids")
+        if int(groups.max(initial=-1)) >= group_noise.shape[0]:
+            raise ValueError("noise_group_test references a group id outside group_noise")
+        noise = np.ascontiguousarray(group_noise[groups], dtype=np.float32)
+    else:
+        raise ValueError("Observed multi-output prediction requires explicit observation_noise "
+                         "or noise_group_test; training noise is not reused for new points")
+    if not np.all(np.isfinite(noise)):
+        raise ValueError("observed prediction noise contains NaN or Inf values")
+    if np.any(noise <= 0):
+        raise ValueError("observed prediction noise values must be > 0")
+    return noise
+
+
+class MultiOutputGP:
+    """ICM multi-output GP: K_full = os (B (x) K_X) + diag(noise_t),
+    B = W W^T + diag(softplus(raw_v)) (mojogp/multi_output_gp.py:859-3402).
+
+    Training runs the Kronecker-preconditioned BBMM loop of libmojogp_amd.so;
+    prediction decomposes os B = Q diag(Lambda) Q^T into T independent
+    single-output problems (mean from the rotated alpha, LOVE or exact
+    variance per eigen-task).  Kernels: RBF / Matern-5/2, isotropic or ARD.
+    """
+
+    _PRESETS = _ICM_PRESETS
+
+    def __init__(self, kernel: Union[str, KernelNode] = "rbf", task_rank: int = -1,
+                 ard: bool = False, num_probes: Optional[int] = None,
+                 max_cg_iterations: Optional[int] = None, cg_tolerance: Optional[float] = None,
+                 preconditioner_rank: Optional[int] = None,
+                 precond_rebuild_threshold: Optional[float] = None,
+                 preconditioner: Optional[str] = None, use_preconditioner: Optional[bool] = None,
+                 init_mean: Optional[Union[float, np.ndarray]] = None,
+                 preset: Optional[str] = None, max_tridiag_iterations: Optional[int] = None):
+        if preset is not None and preset not in self._PRESETS:
+            raise ValueError(f"Unknown preset '{preset}'. Must be one of: "
+                             f"{list(self._PRESETS)}")
+        base = dict(self._PRESETS[preset or "balanced"])
+        if num_probes is not None:
+            base["num_probes"] = num_probes
+        if max_cg_iterations is not None:
+            base["max_cg_iter"] = max_cg_iterations
+        if cg_tolerance is not None:
+            base["cg_tol"] = cg_tolerance
+        if max_tridiag_iterations is not None:
+            base["max_tridiag_iter"] = max_tridiag_iterations
+        rank = base["precond_rank"] if preconditioner_rank is None else preconditioner_rank
+        (self.use_preconditioner, self.precond_rank, self.precond,
+         self.precond_method) = _resolve_precond(rank, preconditioner or base["precond"],
+                                                 use_preconditioner)
+        self._preconditioner_explicitly_configured = (
+            use_preconditioner is not None or preconditioner_rank is not None
+            or preconditioner is not None)
+        if isinstance(kernel, str):
+            if kernel.lower() not in _KERNEL_STRINGS:
+                raise NotImplementedError(
+                    f"kernel {kernel!r} is outside the gfx950 engine "
+                    f"(supported: {sorted(_KERNEL_STRINGS)})")
+            kernel = _KERNEL_STRINGS[kernel.lower()]()
+        if not isinstance(kernel, KernelNode):
+            raise ValueError(f"kernel must be a string or KernelNode, got {type(kernel)}")
+        kernel.native_kind()  # raises for unsupported trees
+        self._is_composite = True
+        self.kernel = kernel
+        self._original_kernel = kernel
+        self._compiled_kernel = kernel
+        if int(task_rank) == 0 or int(task_rank) < -1:
+            raise ValueError("task_rank must be -1 (full rank) or >= 1")
+        self.task_rank = int(task_rank)
+        self.ard = bool(ard)
+        self.method = "materialized"
+        self.num_probes = int(base["num_probes"])
+        self.max_cg_iter = int(base["max_cg_iter"])
+        self.cg_tol = float(base["cg_tol"])
+        self.precond_rebuild_threshold = float(
+            base["precond_rebuild_threshold"] if precond_rebuild_threshold is None
+            else precond_rebuild_threshold)
+        self.max_tridiag_iter = int(base["max_tridiag_iter"])
+        self._init_mean = init_mean
+        self._fitted_mean: Optional[np.ndarray] = None
+        self._engine = None
+        self._kernel_module = None
+        self._dim: Optional[int] = None
+        self._provider_info: Optional[dict] = None
+        self._training_method: Optional[str] = None
+        self._is_trained = False
+        self._X_train: Optional[np.ndarray] = None
+        self._Y_train: Optional[np.ndarray] = None
+        self._observation_noise_train: Optional[np.ndarray] = None
+        self._noise_group_train: Optional[np.ndarray] = None
+        self._noise_group_values: Optional[np.ndarray] = None
+        self._result: Optional[MultiOutputTrainingResult] = None
+        self._raw_result: Optional[dict] = None
+        self._backend_train_info: Optional[dict] = None
+        self._backend_predict_info: Optional[dict] = None
+        self._backend_sample_info: Optional[dict] = None
+
+    # ------------------------------------------------------------ properties
+    @property
+    def is_trained(self) -> bool:
+        return self._is_trained
+
+    @property
+    def training_result(self) -> Optional[MultiOutputTrainingResult]:
+        return self._result
+
+    @property
+    def backend_train_info(self) -> Optional[dict]:
+        return self._backend_train_info
+
+    @property
+    def backend_predict_info(self) -> Optional[dict]:
+        return self._backend_predict_info
+
+    @property
+    def backend_sample_info(self) -> Optional[dict]:
+        return self._backend_sample_info
+
+    @property
+    def task_covariance(self) -> Optional[np.ndarray]:
+        return None if self._result is None else self._result.B
+
+    @property
+    def num_tasks(self) -> Optional[int]:
+        return None if self._result is None else self._result.num_tasks
+
+    # ------------------------------------------------------------ provider
+    def _destroy_persistent_provider(self) -> None:
+        if self._provider_info is not None and self._kernel_module is not None:
+            self._kernel_module.destroy_provider(self._provider_info)
+        self._provider_info = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self._destroy_persistent_provider()
+        except Exception:
+            pass
+
+    def _ensure_compiled(self, dim: int) -> None:
+        self._engine = _engine.load_engine()
+        self._kernel_module = _engine.load_kernel_module(self._compiled_kernel.native_kind(),
+                                                         self.ard, dim)
+        self._dim = dim
+
+    def _build_provider_info(self, X, params, noise) -> dict:
+        info = self._kernel_module.init_provider(np.ascontiguousarray(X, np.float32),
+                                                 np.ascontiguousarray(params, np.float32),
+                                                 float(noise))
+        if self.method == "materialized":
+            self._kernel_module.materialize(info)
+        return info
+
+    def _ensure_provider(self) -> dict:
+        r = self._result
+        if self._provider_info is None:
+            if self._kernel_module is None:
+                self._ensure_compiled(self._X_train.shape[1])
+            self._provider_info = self._build_provider_info(
+                self._X_train, self._compiled_kernel.to_engine_params(r.params),
+                float(np.mean(r.noise_per_task)))
+        return self._provider_info
+
+    # ------------------------------------------------------------ fit
+    def fit(self, X, Y, max_iterations: int = 100, learning_rate: float = 0.05,
+            method: str = "materialized", initial_lengthscale: float = 1.0,
+            initial_lengthscales: Optional[np.ndarray] = None,
+            initial_params: Optional[np.ndarray] = None, initial_noise: float = 0.1,
+            initial_noise_per_task: Optional[np.ndarray] = None,
+            input_dependent_noise: Optional[Any] = None, grouped_noise: Optional[Any] = None,
+            initial_outputscale: float = 1.0, verbose: bool = False,
+            early_stop_tol: float = 1e-4, early_stop_patience: int = 15,
+            use_fused_kernels: bool = True, lr_schedule: str = "constant",
+            observation_noise: Optional[np.ndarray] = None, observation_noise_fn=None,
+            noise_model: str = "scalar", noise_group_train=None, group_noise=None,
+            progress: Any = None, progress_stats: Optional[Any] = None,
+            progress_interval: int = 1) -> MultiOutputTrainingResult:
+        """multi_output_gp.py:1431-1832 and _fit_composite 1834-2034."""
+        if observation_noise_fn is not None or input_dependent_noise is not None:
+            raise NotImplementedError(
+                "MultiOutputGP input-dependent heteroskedastic noise is in development")
+        if grouped_noise is not None:
+            raise NotImplementedError("grouped_noise models are in development; use "
+                                      "noise_model='grouped' with group_noise")
+        if noise_model not in ("scalar", "fixed_vector", "grouped"):
+            raise NotImplementedError(
+                "MultiOutputGP currently supports scalar, per-task, fixed per-sample-task, and "
+                "fixed grouped noise only")
+        if noise_model == "fixed_vector" and observation_noise is None:
+            raise ValueError("noise_model='fixed_vector' requires observation_noise with "
+                             "shape [n, T]")
+        if noise_model == "grouped" and observation_noise is not None:
+            raise ValueError("noise_model='grouped' expands group_noise to observation_noise; "
+                             "do not also pass observation_noise")
+        if noise_model != "grouped" and (noise_group_train is not None
+                                         or group_noise is not None):
+            raise ValueError("noise_group_train and group_noise require noise_model='grouped'")
+        self._destroy_persistent_provider()
+        method = normalize_fit_method(method)
+        self.method = method
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        Y = np.ascontiguousarray(Y, dtype=np.float32)
+        if X.ndim != 2:
+            raise ValueError(f"X must be 2D [n, d], got shape {X.shape}")
+        if Y.ndim != 2:
+            raise ValueError(f"Y must be 2D [n, T], got shape {Y.shape}")
+        if X.shape[0] != Y.shape[0]:
+            raise ValueError(f"X has {X.shape[0]} samples, Y has {Y.shape[0]} -- must match")
+        if not np.all(np.isfinite(X)):
+            raise ValueError("X contains NaN or Inf values")
+        if not np.all(np.isfinite(Y)):
+            raise ValueError("Y contains NaN or Inf values")
+        if initial_noise <= 0:
+            raise ValueError(f"initial_noise must be > 0, got {initial_noise}")
+        n, d = X.shape
+        T = Y.shape[1]
+        groups_arr = gnoise_arr = None
+        if noise_model == "grouped":
+            if noise_group_train is None:
+                raise ValueError("noise_model='grouped' requires noise_group_train")
+            if group_noise is None:
+                raise ValueError("noise_model='grouped' requires group_noise")
+            groups_arr = np.ascontiguousarray(noise_group_train, dtype=np.int32)
+            if groups_arr.shape != (n,):
+                raise ValueError(f"noise_group_train must have shape ({n},), got "
+                                 f"{groups_arr.shape}")
+            if np.any(groups_arr < 0):
+                raise ValueError("noise_group_train must contain non-negative group ids")
+            gnoise_arr = np.ascontiguousarray(group_noise, dtype=np.float32)
+            if gnoise_arr.ndim != 2 or gnoise_arr.shape[1] != T:
+                raise ValueError(f"group_noise must have shape [G, {T}], got "
+                                 f"{gnoise_arr.shape}")
+            if gnoise_arr.shape[0] == 0:
+                raise ValueError("group_noise must contain at least one group")
+            if not np.all(np.isfinite(gnoise_arr)):
+                raise ValueError("group_noise contains NaN or Inf values")
+            if np.any(gnoise_arr <= 0):
+                raise ValueError("group_noise values must be > 0")
+            if int(groups_arr.max(initial=-1)) >= gnoise_arr.shape[0]:
+                raise ValueError("noise_group_train references a group id outside group_noise")
+            observation_noise = gnoise_arr[groups_arr]
+        obs = None
+        if observation_noise is not None:
+            obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
+            if obs.shape != Y.shape:
+                raise ValueError(f"observation_noise must have shape {Y.shape}, got {obs.shape}")
+            if not np.all(np.isfinite(obs)):
+                raise ValueError("observation_noise contains NaN or Inf values")
+            if np.any(obs <= 0):
+                raise ValueError("observation_noise values must be > 0")
+            initial_noise_per_task = np.mean(obs, axis=0).astype(np.float32)
+            self.use_preconditioner = False
+            self.precond_rank = 0
+        if learning_rate <= 0:
+            raise ValueError(f"learning_rate must be > 0, got {learning_rate}")
+        if max_iterations <= 0:
+            raise ValueError(f"max_iterations must be > 0, got {max_iterations}")
+        if int(progress_interval) < 1:
+            raise ValueError("progress_interval must be >= 1")
+        if lr_schedule not in ("constant", "cosine"):
+            raise ValueError(f"lr_schedule must be 'constant' or 'cosine', got '{lr_schedule}'")
+        if initial_noise_per_task is not None:
+            initial_noise_per_task = np.asarray(initial_noise_per_task, dtype=np.float32)
+            if initial_noise_per_task.shape != (T,):
+                raise ValueError(f"initial_noise_per_task must have shape ({T},), got "
+                                 f"{initial_noise_per_task.shape}")
+            if np.any(initial_noise_per_task <= 0):
+                raise ValueError("all initial_noise_per_task entries must be > 0")
+        if self.task_rank > T:
+            raise ValueError(f"task_rank={self.task_rank} exceeds num_tasks={T}")
+        self._observation_noise_train = obs
+        self._noise_group_train = groups_arr
+        self._noise_group_values = gnoise_arr
+        self._compiled_kernel = (make_ard_kernel(self._original_kernel, d) if self.ard
+                                 else KernelNode.from_dict(self._original_kernel.to_dict()))
+        self.kernel = self._compiled_kernel
+        num_params = self._compiled_kernel.num_params()
+        if initial_lengthscales is not None and len(initial_lengthscales) != num_params - 1:
+            raise ValueError(f"initial_lengthscales must have shape ({num_params - 1},), got "
+                             f"({len(initial_lengthscales)},)")
+        if initial_params is None and (initial_lengthscale != 1.0 or initial_outputscale != 1.0
+                                       or initial_lengthscales is not None):
+            initial_params = np.ones(num_params, dtype=np.float32)
+            if initial_lengthscales is not None:
+                initial_params[:num_params - 1] = np.asarray(initial_lengthscales, np.float32)
+            else:
+                initial_params[:num_params - 1] = initial_lengthscale
+            initial_params[-1] = initial_outputscale
+        if initial_params is None:
+            initial_params = np.ones(num_params, dtype=np.float32)
+        initial_params = np.ascontiguousarray(initial_params, dtype=np.float32)
+        if initial_params.shape != (num_params,):
+            raise ValueError(f"init_params must have shape ({num_params},), got "
+                             f"{initial_params.shape}")
+        if self._init_mean is None:
+            mean0 = np.mean(Y, axis=0).astype(np.float32)
+        elif isinstance(self._init_mean, (int, float)):
+            mean0 = np.full(T, float(self._init_mean), np.float32)
+        else:
+            mean0 = np.asarray(self._init_mean, np.float32)
+        noise0 = (np.ascontiguousarray(initial_noise_per_task, np.float32)
+                  if initial_noise_per_task is not None
+                  else np.full(T, initial_noise, np.float32))
+        self._ensure_compiled(d)
+        engine_params = self._compiled_kernel.to_engine_params(initial_params)
+        info = self._build_provider_info(X, engine_params, 0.0)
+        self._provider_info = info
+        self._training_method = method
+        args = [info, Y, engine_params, np.ones(num_params, dtype=bool), noise0, 1.0, mean0,
+                int(T), int(max_iterations), float(learning_rate), int(self.task_rank),
+                bool(verbose), int(self.num_probes), int(self.max_cg_iter), float(self.cg_tol),
+                int(self.precond_rank), int(self.precond_method),
+                float(self.precond_rebuild_threshold), int(self.max_tridiag_iter),
+                int(early_stop_patience), float(early_stop_tol), lr_schedule == "cosine", obs]
+        if callable(progress):
+            args.extend([progress, int(progress_interval)])
+        try:
+            raw = self._engine.train_multi_output(*args)
+        except Exception:
+            self._destroy_persistent_provider()
+            raise
+        noise_pt = np.asarray(raw["noise_per_task"], np.float32)
+        mean_pt = np.asarray(raw["mean_per_task"], np.float32)
+        params = self._compiled_kernel.from_engine_params(np.asarray(raw["params"], np.float32))
+        os_ = float(raw["outputscale"])
+        B_flat = np.asarray(raw["B_flat"], np.float32)
+        B = B_flat.reshape(T, T) if B_flat.size == T * T else np.eye(T, dtype=np.float32)
+        B_scaled = os_ * B
+        eigvals, Q = np.linalg.eigh(B_scaled)
+        Lam = np.maximum(eigvals, 1e-6).astype(np.float32)
+        alpha_blocked = np.asarray(raw["alpha"], np.float32)
+        alpha_rot = (alpha_blocked.reshape(T, n).T.astype(np.float64)
+                     @ Q.astype(np.float64)).astype(np.float32)
+        hist = np.asarray(raw["nll_history"], np.float32)
+        self._result = MultiOutputTrainingResult(
+            params=params, noise=float(np.mean(noise_pt)), noise_per_task=noise_pt,
+            final_nll=float(raw["final_nll"]), iterations=int(raw["iterations"]),
+            converged=bool(raw["converged"]), num_tasks=T, task_rank=int(raw["task_rank"]),
+            num_kernel_params=len(params), B=B_scaled.astype(np.float32),
+            Q=Q.astype(np.float32), Lambda=Lam, effective_scales=Lam,
+            W=np.zeros((T, max(int(raw["task_rank"]), 1)), np.float32),
+            raw_v=np.zeros(T, np.float32), alpha_rotated=alpha_rot, mean_per_task=mean_pt,
+            nll_history=hist if hist.size else np.array([raw["final_nll"]], np.float32),
+            param_names=self._compiled_kernel.get_param_names(),
+            iter_times_ms=np.asarray(raw["iter_times_ms"], np.float64))
+        self._X_train, self._Y_train = X, Y
+        self._raw_result = raw
+        self._backend_train_info = {
+            k: raw[k] for k in ("training_route", "materialization_mode", "max_tridiag_iter",
+                                "precond_rebuild_threshold", "precond_rebuild_count",
+                                "precond_rank", "precond_method", "noise_mode",
+                                "has_observation_noise_vector", "iter_times_ms")}
+        self._backend_train_info["use_preconditioner"] = bool(self.use_preconditioner)
+        self._is_trained = True
+        self._fitted_mean = mean_pt.copy()
+        self._backend_predict_info = None
+        self._backend_sample_info = None
+        return self._result
+
+    # ------------------------------------------------------------ predict
+    def _check_test(self, X_test) -> np.ndarray:
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before prediction. Call fit() first.")
+        X_test = np.ascontiguousarray(X_test, dtype=np.float32)
+        if X_test.ndim != 2:
+            raise ValueError(f"X_test must be 2D [m, d], got shape {X_test.shape}")
+        if X_test.shape[1] != self._X_train.shape[1]:
+            raise ValueError(f"X_test has {X_test.shape[1]} features, expected "
+                             f"{self._X_train.shape[1]}")
+        if not np.all(np.isfinite(X_test)):
+            raise ValueError("X_test contains NaN or Inf values")
+        return X_test
+
+    def _predict_rank(self) -> int:
+        """_prediction_lanczos_rank (multi_output_gp.py:147-164)."""
+        rank = max(int(self.max_tridiag_iter), _DEFAULT_PREDICT_LANCZOS_RANK)
+        if self.ard:
+            rank = max(rank, _DEFAULT_ARD_PREDICT_LANCZOS_RANK)
+        return rank
+
+    def predict(self, X_test, return_var: bool = False, return_std: bool = False,
+                variance_method: str = "love", progress: Any = None,
+                progress_stats: Optional[Any] = None):
+        """multi_output_gp.py:2521-2691 with _predict_composite 2360-2519."""
+        valid = ("love", "exact", "mean_only")
+        if variance_method not in valid:
+            raise ValueError(f"variance_method must be one of {valid}, got '{variance_method}'")
+        X_test = self._check_test(X_test)
+        r = self._result
+        T = r.num_tasks
+        vm = {"mean_only": 0, "love": 1, "exact": 2}[variance_method]
+        info = self._ensure_provider()
+        params = self._compiled_kernel.to_engine_params(np.asarray(r.params, np.float32))
+        noise = float(np.mean(r.noise_per_task))
+        tol = min(float(self.cg_tol), 1e-2) if float(self.cg_tol) > 0.0 else 1e-2
+        rank = self._predict_rank()
+        res = self._engine.predict_multi_output(
+            info, r.alpha_rotated, r.Q, r.effective_scales, X_test, params, noise, vm,
+            self.max_cg_iter, tol, self.precond_rank, rank)
+        mean = np.asarray(res["mean"], np.float32) + self._fitted_mean[None, :]
+        variance = (np.maximum(np.asarray(res["variance"], np.float32), 0)
+                    if vm and "variance" in res else None)
+        self._backend_predict_info = {
+            "requested_method": self.method, "actual_prediction_route": "predict_multi_output",
+            "backend_prediction_used": True, "backend_variance_used": vm != 0,
+            "variance_method": variance_method, "fallback_used": False,
+            "actual_variance_route": "predict_multi_output" if vm else None,
+            "training_route": (self._backend_train_info or {}).get("training_route",
+                                                                  self.method),
+            "precond_rank": self.precond_rank, "precond_method": self.precond_method,
+            "lanczos_rank_used": int(res.get("lanczos_rank_used", rank))}
+        if return_var:
+            return mean, variance
+        if return_std:
+            return mean, (np.sqrt(variance) if variance is not None else None)
+        return MultiOutputPredictionResult(mean=mean, variance=variance,
+                                           std=np.sqrt(variance) if variance is not None
+                                           else None)
+
+    def predict_latent(self, X_test, return_var: bool = False, return_std: bool = False,
+                       variance_method: str = "love", **kwargs):
+        return self.predict(X_test, return_var=return_var, return_std=return_std,
+                            variance_method=variance_method, **kwargs)
+
+    def predict_observed(self, X_test, observation_noise=None, noise_group_test=None,
+                         return_var: bool = False, return_std: bool = False,
+                         variance_method: str = "love", **kwargs):
+        """p(y_test | y_train) with explicit test noise (multi_output_gp.py:2714-2744)."""
+        latent = self.predict(X_test, variance_method=variance_method, **kwargs)
+        noise = _resolve_observed_noise(latent.mean.shape[0], latent.mean.shape[1],
+                                        observation_noise, noise_group_test,
+                                        self._noise_group_values)
+        var = std = None
+        if latent.variance is not None:
+            var = np.ascontiguousarray(latent.variance + noise, dtype=np.float32)
+            std = np.sqrt(var)
+        if return_var:
+            return latent.mean, var
+        if return_std:
+            return latent.mean, std
+        return MultiOutputPredictionResult(mean=latent.mean, variance=var, std=std)
+
+    def score(self, X_test, Y_test) -> dict:
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before scoring. Call fit() first.")
+        Y_test = np.ascontiguousarray(Y_test, dtype=np.float32)
+        pred = self.predict(X_test)
+        resid = Y_test - pred.mean
+        ss_res = np.sum(resid ** 2)
+        ss_tot = np.sum((Y_test - np.mean(Y_test, axis=0)) ** 2)
+        return {"rmse": float(np.sqrt(np.mean(resid ** 2))),
+                "mae": float(np.mean(np.abs(resid))),
+                "r2": float(1.0 - ss_res / (ss_tot + 1e-10)),
+                "rmse_per_task": np.sqrt(np.mean(resid ** 2, axis=0))}
+
+    # ------------------------------------------------------------ sampling
+    def sample_posterior(self, X_test, n_samples: int = 1, method: str = "diagonal",
+                         n_rff_features: int = 1024,
+                         rng: Optional[np.random.Generator] = None) -> np.ndarray:
+        """multi_output_gp.py:2790-2892."""
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before sampling. Call fit() first.")
+        if method not in ("diagonal", "pathwise"):
+            raise ValueError("MultiOutputGP only supports method='diagonal' or 'pathwise', "
+                             f"got '{method}'.")
+        if rng is None:
+            rng = np.random.default_rng()
+        route = (self._backend_train_info or {}).get("training_route",
+                                                    self._training_method or self.method)
+        if method == "pathwise":
+            samples = self._sample_posterior_pathwise(X_test, int(n_samples),
+                                                      int(n_rff_features), rng)
+            self._backend_sample_info = {
+                "requested_method": method, "actual_sampling_method": "pathwise",
+                "actual_sampling_route": "provider_pathwise", "backend_sampling_used": True,
+                "backend_correction_used": True,
+                "backend_correction_route": "sample_multi_output_pathwise",
+                "training_route": route, "prior_sampler_family": "shared_feature_map",
+                "n_rff_features": int(n_rff_features)}
+            return samples
+        mean, std = self.predict(X_test, return_std=True)
+        z = rng.standard_normal((n_samples, mean.shape[0], mean.shape[1]))
+        self._backend_sample_info = {
+            "requested_method": method, "actual_sampling_method": "diagonal",
+            "actual_sampling_route": "diagonal_from_predictive_std",
+            "backend_sampling_used": True, "backend_correction_used": False,
+            "training_route": route}
+        return (mean[None] + std[None] * z).astype(np.float32)
+
+    def _sample_posterior_pathwise(self, X_test, n_samples: int, n_rff_features: int,
+                                   rng: np.random.Generator) -> np.ndarray:
+        """Shared RFF prior through the eigen-tasks of os B plus the exact
+        Kronecker correction (multi_output_gp.py:2894-3102).  The Generator is
+        consumed in the reference's order (feature map, then per sample: task
+        weights, observation noise); all samples share one batched solve."""
+        X_test = self._check_test(X_test)
+        r = self._result
+        T = r.num_tasks
+        X = self._X_train
+        n, d = X.shape
+        m = X_test.shape[0]
+        S = int(n_samples)
+        if S < 1:
+            raise ValueError("n_samples must be >= 1")
+        params = np.asarray(r.params, np.float32)
+        noise = np.ascontiguousarray(r.noise_per_task, np.float32)
+        mean = np.asarray(self._fitted_mean if self._fitted_mean is not None
+                          else r.mean_per_task, np.float32)
+        y_c = (self._Y_train - mean[None, :]).astype(np.float32)
+        fmap = build_pathwise_feature_map(self._compiled_kernel.native_kind(), params,
+                                          input_dim=d, n_features=n_rff_features, rng=rng,
+                                          ard=self.ard)
+        Qd = np.asarray(r.Q, np.float64)
+        sc = np.sqrt(np.maximum(np.asarray(r.Lambda, np.float64), 1e-8))
+        train_noise = np.sqrt(np.maximum(noise, 0.0)).astype(np.float32)
+        Wts, eps = [], np.empty((S, n, T), np.float32)
+        for c in range(S):
+            Wts.append(build_feature_weights(fmap, T, rng))
+            eps[c] = rng.standard_normal((n, T)).astype(np.float32)
+        Wall = np.concatenate(Wts, axis=0)                       # [S*T, F]
+        tr = sample_prior_values(fmap, X, Wall).reshape(S, T, n)
+        resid = np.empty((S, n, T), np.float32)
+        for c in range(S):
+            prior = np.einsum("ln,tl,l->nt", tr[c].astype(np.float64), Qd, sc).astype(np.float32)
+            resid[c] = y_c - (prior + eps[c] * train_noise[None, :])
+        info = self._ensure_provider()
+        eparams = self._compiled_kernel.to_engine_params(params)
+        max_cg = max(int(self.max_cg_iter), 100)
+        tol = min(float(self.cg_tol), 1e-2) if float(self.cg_tol) > 0.0 else 1e-2
+        out = np.empty((S, m, T), np.float32)
+        for start in range(0, m, _PATHWISE_TEST_CHUNK):
+            end = min(start + _PATHWISE_TEST_CHUNK, m)
+            te = sample_prior_values(fmap, X_test[start:end], Wall).reshape(S, T, end - start)
+            raw = self._engine.sample_multi_output_pathwise(
+                info, resid, np.ascontiguousarray(r.B, np.float32), X_test[start:end], eparams,
+                noise, max_cg, tol)
+            corr = np.asarray(raw["correction"], np.float32).reshape(S, end - start, T)
+            for c in range(S):
+                prior = np.einsum("ln,tl,l->nt", te[c].astype(np.float64), Qd,
+                                  sc).astype(np.float32)
+                out[c, start:end] = mean[None, :] + prior + corr[c]
+        return out
+
+    # ------------------------------------------------------------ persistence
+    def save(self, path: str) -> None:
+        """``<path>_config.json`` + ``<path>_arrays.npz`` (multi_output_gp.py:3104-3207)."""
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before saving. Call fit() first.")
+        path = str(path)
+        if path.endswith(".json") or path.endswith(".npz"):
+            path = path.rsplit(".", 1)[0]
+        from . import __version__
+        tr = self._result
+        cfg = {"schema_version": _MODEL_SCHEMA_VERSION, "mojogp_version": __version__,
+               "wrapper": "MultiOutputGP", "kernel": self._original_kernel.to_mojo_type(),
+               "kernel_tree": self._original_kernel.to_dict(), "is_composite": True,
+               "task_rank": self.task_rank, "ard": self.ard, "method": self.method,
+               "num_probes": self.num_probes, "max_cg_iter": self.max_cg_iter,
+               "cg_tol": self.cg_tol, "use_preconditioner": self.use_preconditioner,
+               "precond_rank": self.precond_rank, "precond": self.precond,
+               "precond_rebuild_threshold": self.precond_rebuild_threshold, "dim": self._dim,
+               "noise": float(tr.noise), "final_nll": float(tr.final_nll),
+               "iterations": int(tr.iterations), "converged": bool(tr.converged),
+               "num_tasks": int(tr.num_tasks), "task_rank_result": int(tr.task_rank),
+               "training_method": self._training_method or self.method,
+               "has_observation_noise_vector": self._observation_noise_train is not None,
+               "has_noise_group_train": self._noise_group_train is not None,
+               "has_group_noise": self._noise_group_values is not None,
+               "result_type": "MultiOutputTrainingResult",
+               "num_kernel_params": int(tr.num_kernel_params),
+               "param_names": list(tr.param_names), "cat_param_names": list(tr.cat_param_names)}
+        Path(path + "_config.json").write_text(json.dumps(cfg, indent=2))
+        arrays = {"X_train": self._X_train, "Y_train": self._Y_train, "B": tr.B, "Q": tr.Q,
+                  "Lambda": tr.Lambda, "W": tr.W, "raw_v": tr.raw_v,
+                  "alpha_rotated": tr.alpha_rotated, "effective_scales": tr.effective_scales,
+                  "noise_per_task": tr.noise_per_task, "nll_history": tr.nll_history,
+                  "mean_per_task": tr.mean_per_task, "params": tr.params,
+                  "X_train_cont": self._X_train}
+        if tr.iter_times_ms is not None:
+            arrays["iter_times_ms"] = tr.iter_times_ms
+        if self._observation_noise_train is not None:
+            arrays["observation_noise_train"] = self._observation_noise_train
+        if self._noise_group_train is not None:
+            arrays["noise_group_train"] = self._noise_group_train
+        if self._noise_group_values is not None:
+            arrays["group_noise"] = self._noise_group_values
+        if self._fitted_mean is not None:
+            arrays["fitted_mean"] = self._fitted_mean
+        np.savez(path + "_arrays.npz", **arrays)
+
+    @classmethod
+    def load(cls, path: str, kernel: Optional[Union[str, KernelNode]] = None) -> "MultiOutputGP":
+        """multi_output_gp.py:3210-3386."""
+        path = str(path)
+        if path.endswith(".json") or path.endswith(".npz"):
+            path = path.rsplit(".", 1)[0]
+        cfg = json.loads(Path(path + "_config.json").read_text())
+        if cfg.get("wrapper") != "MultiOutputGP":
+            raise ValueError("Saved model is not a MultiOutputGP artifact. Expected "
+                             f"wrapper='MultiOutputGP', got {cfg.get('wrapper')!r}.")
+        if int(cfg.get("schema_version", 0)) != _MODEL_SCHEMA_VERSION:
+            raise ValueError(f"Unsupported MultiOutputGP schema_version="
+                             f"{cfg.get('schema_version')}; expected {_MODEL_SCHEMA_VERSION}.")
+        if cfg.get("result_type") != "MultiOutputTrainingResult":
+            raise ValueError(f"Unsupported MultiOutputGP result_type={cfg.get('result_type')!r}")
+        arr = np.load(path + "_arrays.npz", allow_pickle=False)
+        if "C_train" in arr or "cat_params" in arr:
+            raise NotImplementedError("mixed continuous/categorical ICM models are outside the "
+                                      "gfx950 engine")
+        if kernel is None:
+            kernel = (KernelNode.from_dict(cfg["kernel_tree"]) if cfg.get("kernel_tree")
+                      else cfg.get("kernel", "rbf"))
+        gp = cls(kernel=kernel, task_rank=cfg["task_rank"], ard=cfg["ard"],
+                 num_probes=cfg["num_probes"], max_cg_iterations=cfg["max_cg_iter"],
+                 cg_tolerance=cfg["cg_tol"], use_preconditioner=cfg["use_preconditioner"],
+                 preconditioner_rank=cfg["precond_rank"], preconditioner=cfg["precond"],
+                 precond_rebuild_threshold=cfg["precond_rebuild_threshold"])
+        gp.method = cfg["method"]
+        gp._X_train = np.ascontiguousarray(arr["X_train"], np.float32)
+        gp._Y_train = np.ascontiguousarray(arr["Y_train"], np.float32)
+        get = lambda k: arr[k] if k in arr else None  # noqa: E731
+        obs = get("observation_noise_train")
+        gp._observation_noise_train = None if obs is None else np.ascontiguousarray(obs,
+                                                                                    np.float32)
+        grp = get("noise_group_train")
+        gp._noise_group_train = None if grp is None else np.ascontiguousarray(grp, np.int32)
+        gv = get("group_noise")
+        gp._noise_group_values = None if gv is None else np.ascontiguousarray(gv, np.float32)
+        gp._dim = cfg.get("dim")
+        gp._training_method = cfg.get("training_method", gp.method)
+        d = gp._X_train.shape[1]
+        gp._compiled_kernel = (make_ard_kernel(gp._original_kernel, d) if gp.ard
+                               else gp._original_kernel)
+        gp.kernel = gp._compiled_kernel
+        gp._result = MultiOutputTrainingResult(
+            params=np.asarray(arr["params"], np.float32), noise=float(cfg["noise"]),
+            noise_per_task=np.asarray(arr["noise_per_task"], np.float32),
+            final_nll=float(cfg["final_nll"]), iterations=int(cfg["iterations"]),
+            converged=bool(cfg["converged"]), num_tasks=int(cfg["num_tasks"]),
+            task_rank=int(cfg["task_rank_result"]),
+            num_kernel_params=int(cfg["num_kernel_params"]),
+            B=np.asarray(arr["B"], np.float32), Q=np.asarray(arr["Q"], np.float32),
+            Lambda=np.asarray(arr["Lambda"], np.float32),
+            effective_scales=np.asarray(arr["effective_scales"], np.float32),
+            W=arr["W"], raw_v=arr["raw_v"],
+            alpha_rotated=np.asarray(arr["alpha_rotated"], np.float32),
+            mean_per_task=np.asarray(arr["mean_per_task"], np.float32),
+            nll_history=arr["nll_history"], param_names=list(cfg["param_names"]),
+            cat_param_names=list(cfg.get("cat_param_names", [])),
+            iter_times_ms=get("iter_times_ms"))
+        fm = get("fitted_mean")
+        gp._fitted_mean = np.asarray(fm if fm is not None else arr["mean_per_task"], np.float32)
+        gp._is_trained = True
+        gp._backend_train_info = None
+        return gp
+
+    def __repr__(self) -> str:
+        status = "trained" if self._is_trained else "untrained"
+        tasks = f", tasks={self.num_tasks}" if self.num_tasks else ""
+        ard = ", ard=True" if self.ard else ""
+        return f"MultiOutputGP(kernel={self._original_kernel.to_mojo_type()}{tasks}{ard}, {status})"
