@@ -16,7 +16,7 @@
  *     reference (fn_ptr_module.py:391-491).  Inputs X are row-major [n][d].
  *   - Every call is synchronous on return.  Each provider owns one HIP stream;
  *     a handle must not be used from two threads at once.
- *   - Kernel kinds: 0 = RBF, 1 = Matern-5/2.  Parameter layout (engine layout,
+ *   - Kernel kinds: 0 = RBF, 1 = Matern-5/2, 2 = Matern-1/2, 3 = Matern-3/2.  Parameter layout (engine layout,
  *     mojogp/kernel.py:494-509): isotropic [lengthscale, outputscale];
  *     ARD [ls_0 .. ls_{d-1}, outputscale].
  */

@@ -10,7 +10,10 @@ from . import _lib
 
 KIND_RBF = 0
 KIND_MATERN52 = 1
-_KIND_NAMES = {"rbf": KIND_RBF, "matern52": KIND_MATERN52}
+KIND_MATERN12 = 2
+KIND_MATERN32 = 3
+_KIND_NAMES = {"rbf": KIND_RBF, "matern52": KIND_MATERN52, "matern12": KIND_MATERN12,
+               "matern32": KIND_MATERN32}
 
 
 def kind_code(kind) -> int:

@@ -59,8 +59,8 @@ int mgp_init_provider(int kind, int ard, int d, int64_t n, const float* X,
   return guarded([&] {
     MGP_REQUIRE(out_handle != nullptr, "out_handle is null");
     *out_handle = nullptr;
-    MGP_REQUIRE(kind == KIND_RBF || kind == KIND_MATERN52,
-                "kernel kind must be 0 (RBF) or 1 (Matern52)");
+    MGP_REQUIRE(valid_kind(kind),
+                "kernel kind must be 0 (RBF), 1 (Matern52), 2 (Matern12) or 3 (Matern32)");
     MGP_REQUIRE(d >= 1 && d <= 32, "input dimension must be in [1, 32]");
     MGP_REQUIRE(n >= 1, "n must be >= 1");
     MGP_REQUIRE(X != nullptr && params != nullptr, "null input array");

@@ -42,10 +42,19 @@ struct PackedPoints {
 // about 1e-5 at the bound) the products are evaluated from per-dimension
 // differences (direct_matvec) instead.  RBF is more sensitive (dk/ds = -ln2 k
 // against ~-0.08 near 0 for Matern-5/2, and a 14x smaller coordinate scale).
+// Matern-3/2 has dk/ds three times Matern-5/2's at s = 0 and a smaller
+// coordinate scale, hence a 4x tighter bound.  Matern-1/2 is never evaluated
+// in Gram form: k = 2^-sqrt(s) has an unbounded slope in s at s = 0, so the
+// absolute distance error e of near-coincident pairs becomes a kernel error
+// of ~ln2 sqrt(e) instead of ~e.
 constexpr float kGramMaxNormSumRBF = 4096.0f;
 constexpr float kGramMaxNormSumM52 = 32768.0f;
+constexpr float kGramMaxNormSumM32 = 8192.0f;
 inline bool gram_form_ok(int kind, const PackedPoints& rows, const PackedPoints& cols) {
-  const float bound = kind == KIND_RBF ? kGramMaxNormSumRBF : kGramMaxNormSumM52;
+  if (kind == KIND_MATERN12) return false;
+  const float bound = kind == KIND_RBF       ? kGramMaxNormSumRBF
+                      : kind == KIND_MATERN32 ? kGramMaxNormSumM32
+                                              : kGramMaxNormSumM52;
   return rows.kb > 0 && rows.max_norm + cols.max_norm <= bound;
 }
 
@@ -56,9 +65,15 @@ inline int split_mfma_count(int d) { return (6 * (d + 2) + 31) / 32; }
 // of the scaled points feeds exp2 directly:
 //   RBF:       s = 0.5*log2(e)*r^2,  k = os*2^-min(s, 20 log2 e)
 //   Matern52:  s = 5*log2(e)^2*r^2,   u = sqrt(s) = sqrt(5) r log2(e)
+//   Matern12:  u = sqrt(s) = r log2(e),  k = os*2^-min(u, 20 log2 e)
+//   Matern32:  u = sqrt(3) r log2(e),   k = os*(1 + u ln2)*2^-min(u, 20 log2 e)
 inline float kernel_scale(int kind) {
-  return kind == KIND_RBF ? 0.84932180028801904272f   // sqrt(0.5*log2 e)
-                          : 3.22596433305849393025f;  // sqrt(5)*log2 e
+  switch (kind) {
+    case KIND_RBF: return 0.84932180028801904272f;       // sqrt(0.5*log2 e)
+    case KIND_MATERN12: return 1.44269504088896340736f;  // log2 e
+    case KIND_MATERN32: return 2.49882111064734320000f;  // sqrt(3)*log2 e
+    default: return 3.22596433305849393025f;             // sqrt(5)*log2 e
+  }
 }
 
 // Builds packed operands (and scaled coordinates) for n points X[n][d].

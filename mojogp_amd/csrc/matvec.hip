@@ -53,6 +53,14 @@ __device__ __forceinline__ float kval(float s, float clampv = kExp2Clamp) {
     // os * exp(max(-0.5 r^2, -20)) = os * 2^-clamp(s, 0, 20 log2 e)
     const float t = __builtin_amdgcn_fmed3f(s, 0.0f, kExp2Clamp);
     return __builtin_amdgcn_exp2f(-t);
+  } else if constexpr (KIND == KIND_MATERN12) {
+    // os * exp(max(-r, -20)),  u = r log2 e
+    const float u = __builtin_amdgcn_sqrtf(fabsf(s));
+    return __builtin_amdgcn_exp2f(-fminf(u, clampv));
+  } else if constexpr (KIND == KIND_MATERN32) {
+    // os * (1 + sqrt3 r) * exp(max(-sqrt3 r, -20)),  u = sqrt3 r log2 e
+    const float u = __builtin_amdgcn_sqrtf(fabsf(s));
+    return fmaf(u, kLn2, 1.0f) * __builtin_amdgcn_exp2f(-fminf(u, clampv));
   } else {
     // os * (1 + sqrt5 r + 5/3 r^2) * exp(max(-sqrt5 r, -20)),  u = sqrt5 r log2 e
     // sqrt(|s|): s < 0 only from Gram-form rounding of a near-zero distance,
@@ -245,6 +253,12 @@ __device__ __forceinline__ void kval_scaled(float s, float clampv, float one, fl
     const float t = __builtin_amdgcn_fmed3f(s, 0.0f, clampv);
     f = __builtin_amdgcn_exp2f((float)kPScaleLog2 - t);
     g = one;
+  } else if constexpr (KIND == KIND_MATERN32) {
+    const float u = __builtin_amdgcn_sqrtf(fabsf(s));
+    float mn = fminf(u, clampv);
+    asm("" : "+v"(mn));
+    g = __builtin_amdgcn_exp2f(-mn);
+    f = fmaf(u, kLn2 * P, P);
   } else {
     const float u = __builtin_amdgcn_sqrtf(fabsf(s));
     float mn = fminf(u, clampv);
@@ -290,6 +304,7 @@ __global__ __launch_bounds__(256) void k_fused_tile(
     const uint32_t* __restrict__ colmax, const float* __restrict__ Vin,
     float* __restrict__ out, float* __restrict__ partial, int64_t mpad, int cpad) {
   static_assert(R % 2 == 0, "row tiles per wave must be even (pair alignment)");
+  static_assert(KIND != KIND_MATERN12, "Matern-1/2 is evaluated from coordinate differences");
   const int lane = threadIdx.x & 63;
   // Wave index made wave-uniform (SGPR) so the j-loop bounds stay scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -385,10 +400,10 @@ __global__ __launch_bounds__(256) void k_fused_tile(
       if constexpr (NCG > 0) {
         // B operand halves e = 0..3 from tile jt0, 4..7 from jt0 + 1.
         h2 hA, hB, hC, hD, lA, lB, lC, lD;
-        split_pair<KIND == KIND_RBF>(f0[0], g0[0], f0[1], g0[1], hA, lA);
-        split_pair<KIND == KIND_RBF>(f0[2], g0[2], f0[3], g0[3], hB, lB);
-        split_pair<KIND == KIND_RBF>(f1[0], g1[0], f1[1], g1[1], hC, lC);
-        split_pair<KIND == KIND_RBF>(f1[2], g1[2], f1[3], g1[3], hD, lD);
+        split_pair<KIND != KIND_MATERN52 && KIND != KIND_MATERN32>(f0[0], g0[0], f0[1], g0[1], hA, lA);
+        split_pair<KIND != KIND_MATERN52 && KIND != KIND_MATERN32>(f0[2], g0[2], f0[3], g0[3], hB, lB);
+        split_pair<KIND != KIND_MATERN52 && KIND != KIND_MATERN32>(f1[0], g1[0], f1[1], g1[1], hC, lC);
+        split_pair<KIND != KIND_MATERN52 && KIND != KIND_MATERN32>(f1[2], g1[2], f1[3], g1[3], hD, lD);
         const h8 ph = {hA[0], hA[1], hB[0], hB[1], hC[0], hC[1], hD[0], hD[1]};
         const h8 pl = {lA[0], lA[1], lB[0], lB[1], lC[0], lC[1], lD[0], lD[1]};
 #pragma unroll
@@ -672,6 +687,12 @@ __global__ __launch_bounds__(256) void k_grad_matvec(
       float h;
       if constexpr (KIND == KIND_RBF) {
         h = kv;
+      } else if constexpr (KIND == KIND_MATERN12) {
+        // log2(e) e^{max(-r,-20)} / r with the reference's r = sqrt(r^2 + 1e-20)
+        h = kLog2e * kv / sqrtf(S + kM12RFloor);
+      } else if constexpr (KIND == KIND_MATERN32) {
+        // 3 e^{max(-sqrt3 r,-20)}
+        h = 3.0f * __builtin_amdgcn_exp2f(-fminf(sqrtf(S), kExp2Clamp));
       } else {
         // (5/3)(1 + sqrt5 r) e^{max(-sqrt5 r,-20)} with sqrt5 r = u ln2, u = sqrt(S)
         const float u = sqrtf(S);
@@ -838,8 +859,10 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
     if (splits > 1 || mixing)
       partial = ws.partial.ensure((size_t)splits * cpad * mpad);
 
-    TileFn fn = a.kind == KIND_RBF ? pick_tile<KIND_RBF>(kb, ncg)
-                                   : pick_tile<KIND_MATERN52>(kb, ncg);
+    MGP_REQUIRE(a.kind != KIND_MATERN12, "Matern-1/2 has no Gram-form tile path");
+    TileFn fn = a.kind == KIND_RBF        ? pick_tile<KIND_RBF>(kb, ncg)
+                : a.kind == KIND_MATERN32 ? pick_tile<KIND_MATERN32>(kb, ncg)
+                                          : pick_tile<KIND_MATERN52>(kb, ncg);
     MGP_REQUIRE(fn != nullptr, "no tile kernel for this shape");
     const int64_t diag_shift = a.square ? 0 : (int64_t)1 << 40;
     if (ws.time_tile) MGP_HIP_CHECK(hipEventRecord(ws.ev0, st));
@@ -882,7 +905,10 @@ void direct_matvec(const MatvecArgs& a, const PackedPoints& rows,
     const int nc = std::min(kDirectMaxCols, a.ncols - c0);
     const size_t shm = (size_t)kDirectTile * (d + nc) * sizeof(float);
     const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.m, 1), 256));
-    auto fn = a.kind == KIND_RBF ? k_direct<KIND_RBF> : k_direct<KIND_MATERN52>;
+    auto fn = a.kind == KIND_RBF        ? k_direct<KIND_RBF>
+              : a.kind == KIND_MATERN12 ? k_direct<KIND_MATERN12>
+              : a.kind == KIND_MATERN32 ? k_direct<KIND_MATERN32>
+                                        : k_direct<KIND_MATERN52>;
     hipLaunchKernelGGL(fn, grid, dim3(256), shm, st, rows.z.ptr, a.m, cols.z.ptr,
                        a.n, d, V_dev + (int64_t)c0 * a.n, nc, a.outputscale,
                        a.noise, a.square ? 1 : 0, out_dev + (int64_t)c0 * a.m);
@@ -895,7 +921,10 @@ void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r
   MGP_REQUIRE(r0 >= 0 && nrows >= 0 && r0 + nrows <= rows.n, "cross block out of range");
   const int64_t total = nrows * cols.n;
   if (total == 0) return;
-  auto fn = kind == KIND_RBF ? k_fill_cross<KIND_RBF> : k_fill_cross<KIND_MATERN52>;
+  auto fn = kind == KIND_RBF        ? k_fill_cross<KIND_RBF>
+            : kind == KIND_MATERN12 ? k_fill_cross<KIND_MATERN12>
+            : kind == KIND_MATERN32 ? k_fill_cross<KIND_MATERN32>
+                                    : k_fill_cross<KIND_MATERN52>;
   hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, rows.z.ptr,
                      r0, nrows, cols.z.ptr, cols.n, d, outputscale, out);
   MGP_HIP_CHECK(hipGetLastError());
@@ -913,6 +942,10 @@ void gradient_matvec(int kind, bool ard, const PackedPoints& pts, int d, float o
                       float*);
   Fn fn;
   if (kind == KIND_RBF) fn = ard ? k_grad_matvec<KIND_RBF, true> : k_grad_matvec<KIND_RBF, false>;
+  else if (kind == KIND_MATERN12)
+    fn = ard ? k_grad_matvec<KIND_MATERN12, true> : k_grad_matvec<KIND_MATERN12, false>;
+  else if (kind == KIND_MATERN32)
+    fn = ard ? k_grad_matvec<KIND_MATERN32, true> : k_grad_matvec<KIND_MATERN32, false>;
   else fn = ard ? k_grad_matvec<KIND_MATERN52, true> : k_grad_matvec<KIND_MATERN52, false>;
   for (int c0 = 0; c0 < ncols; c0 += kGradCols) {
     hipLaunchKernelGGL(fn, grid, dim3(256), shm, st, pts.z.ptr, n, d, V_dev, ncols, c0,

@@ -16,7 +16,8 @@ namespace mgp {
 
 // Kernel families handled by the hand-written kernels.  Values are part of the
 // C ABI (include/mojogp_amd.h).
-enum KernelKind : int { KIND_RBF = 0, KIND_MATERN52 = 1 };
+enum KernelKind : int { KIND_RBF = 0, KIND_MATERN52 = 1, KIND_MATERN12 = 2, KIND_MATERN32 = 3 };
+inline bool valid_kind(int kind) { return kind >= KIND_RBF && kind <= KIND_MATERN32; }
 
 // ln(2) and log2(e) in float.
 constexpr float kLn2 = 0.69314718055994530942f;
@@ -24,6 +25,10 @@ constexpr float kLog2e = 1.44269504088896340736f;
 // exp(max(x, -20)) clamp of the reference's numerical-stability pass, expressed
 // in base 2: 20 * log2(e).
 constexpr float kExp2Clamp = 20.0f * 1.44269504088896340736f;
+// The reference's r = sqrt(r^2 + 1e-20) floor of the Matern-1/2 distance in
+// the base-2 scaled coordinates (log2(e)^2 * 1e-20); only the gradient weight
+// 1/r needs it.
+constexpr float kM12RFloor = 2.0813689810056076e-20f;
 
 // Error carried to the C boundary.
 struct Error : std::runtime_error {

@@ -361,6 +361,12 @@ __global__ __launch_bounds__(256) void k_pc_column(
     float kv;
     if constexpr (KIND == KIND_RBF) {
       kv = os * __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
+    } else if constexpr (KIND == KIND_MATERN12) {
+      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+      kv = os * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+    } else if constexpr (KIND == KIND_MATERN32) {
+      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+      kv = os * fmaf(u, kLn2, 1.0f) * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
     } else {
       const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
       const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
@@ -641,6 +647,16 @@ __global__ __launch_bounds__(256) void k_grad_trace(
       if constexpr (KIND == KIND_RBF) {
         kv = __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
         h = kv;
+      } else if constexpr (KIND == KIND_MATERN12) {
+        // h = log2(e) k / r with the reference's floored r = sqrt(r^2 + 1e-20)
+        const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+        kv = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+        h = kLog2e * kv / __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f) + kM12RFloor);
+      } else if constexpr (KIND == KIND_MATERN32) {
+        const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+        const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+        kv = fmaf(u, kLn2, 1.0f) * e;
+        h = 3.0f * e;
       } else {
         const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
         const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
@@ -883,7 +899,10 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
   hipLaunchKernelGGL(k_pc_argmax_part, dim3(nb), dim3(kBlock), 0, st, diag.ptr, mask.ptr,
                      n, nb, pvv.ptr, piv.ptr, pa.ptr);
   MGP_HIP_CHECK(hipGetLastError());
-  auto col = pv.kind == KIND_RBF ? k_pc_column<KIND_RBF> : k_pc_column<KIND_MATERN52>;
+  auto col = pv.kind == KIND_RBF        ? k_pc_column<KIND_RBF>
+             : pv.kind == KIND_MATERN12 ? k_pc_column<KIND_MATERN12>
+             : pv.kind == KIND_MATERN32 ? k_pc_column<KIND_MATERN32>
+                                        : k_pc_column<KIND_MATERN52>;
   auto launch_column = [&](int m) {
     const size_t shm = (size_t)(m + pv.d) * sizeof(float);
     hipLaunchKernelGGL(col, dim3(nb), dim3(kBlock), shm, st, pv.train.z.ptr, pv.d, n, os, m,
@@ -1027,6 +1046,12 @@ void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int n
     if (pv.kind == KIND_RBF) {
       if (pv.ard) launch_grad<KIND_RBF, true>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
       else launch_grad<KIND_RBF, false>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+    } else if (pv.kind == KIND_MATERN12) {
+      if (pv.ard) launch_grad<KIND_MATERN12, true>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+      else launch_grad<KIND_MATERN12, false>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+    } else if (pv.kind == KIND_MATERN32) {
+      if (pv.ard) launch_grad<KIND_MATERN32, true>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
+      else launch_grad<KIND_MATERN32, false>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
     } else {
       if (pv.ard) launch_grad<KIND_MATERN52, true>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);
       else launch_grad<KIND_MATERN52, false>(dm, pv.train.z.ptr, d, pv.n, Lf, Rf, ncols, c0, part.ptr, nterms, st);

@@ -1,7 +1,8 @@
 """Kernel specification surface (subset served by the gfx950 engine).
 
 Mirrors the reference's kernel DSL for the hot-path kernels
-(mojogp/kernel.py): ``RBF`` and ``Matern52``, isotropic or ARD, with the same
+(mojogp/kernel.py): ``RBF``, ``Matern12``, ``Matern32`` and ``Matern52``,
+isotropic or ARD, with the same
 parameter names, initial values and engine parameter layout
 (``kernel.py:324-509``):
 
@@ -34,7 +35,8 @@ class KernelType(Enum):
 
 
 # Families the native kernels implement (value = native kind code).
-NATIVE_KINDS = {KernelType.RBF: 0, KernelType.MATERN52: 1}
+NATIVE_KINDS = {KernelType.RBF: 0, KernelType.MATERN52: 1, KernelType.MATERN12: 2,
+                KernelType.MATERN32: 3}
 
 
 @dataclass
@@ -73,7 +75,8 @@ class KernelNode:
     def native_kind(self) -> int:
         if not self.is_native_leaf():
             raise NotImplementedError(
-                f"kernel {self!r} is outside the gfx950 engine (supported: RBF, Matern52, "
+                f"kernel {self!r} is outside the gfx950 engine (supported: RBF, Matern12, "
+                "Matern32, Matern52, "
                 "isotropic or ARD, no composition / active_dims)")
         return NATIVE_KINDS[self.kernel_type]
 

@@ -28,13 +28,13 @@ import numpy as np
 
 from . import _engine
 from .gp import normalize_fit_method
-from .kernel import KernelNode, Matern52, RBF, make_ard_kernel
+from .kernel import KernelNode, Matern12, Matern32, Matern52, RBF, make_ard_kernel
 from .pathwise_prior import (build_feature_weights, build_pathwise_feature_map,
                              sample_prior_values)
 
 _MODEL_SCHEMA_VERSION = 1
 _PRECOND_METHODS = {"greedy": 0, "rpcholesky": 1, "nystrom": 2}
-_KERNEL_STRINGS = {"rbf": RBF, "matern52": Matern52}
+_KERNEL_STRINGS = {"rbf": RBF, "matern12": Matern12, "matern32": Matern32, "matern52": Matern52}
 _DEFAULT_PREDICT_LANCZOS_RANK = 100
 _DEFAULT_ARD_PREDICT_LANCZOS_RANK = 200
 

@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._provider import KIND_MATERN52, KIND_RBF
+from ._provider import KIND_MATERN12, KIND_MATERN32, KIND_MATERN52, KIND_RBF
 
 
 @dataclass(frozen=True)
@@ -45,7 +45,9 @@ class PathwiseFeatureMap:
 
 def build_pathwise_feature_map(kind: int, params, *, input_dim: int, n_features: int,
                                rng: np.random.Generator, ard: bool) -> PathwiseFeatureMap:
-    """Feature map of an RBF / Matern-5/2 leaf with public params [ls..., os]."""
+    """Feature map of an RBF / Matern leaf with public params [ls..., os]
+    (pathwise_prior.py:130-160: Gaussian frequencies for RBF, Student-t with
+    2 nu degrees of freedom per dimension for Matern-nu)."""
     p = np.asarray(params, dtype=np.float64).ravel()
     d = int(input_dim)
     if ard:
@@ -59,6 +61,10 @@ def build_pathwise_feature_map(kind: int, params, *, input_dim: int, n_features:
     outputscale = float(p[-1])
     if kind == KIND_RBF:
         W = rng.standard_normal((n_features, d))
+    elif kind == KIND_MATERN12:
+        W = rng.standard_t(df=1, size=(n_features, d))
+    elif kind == KIND_MATERN32:
+        W = rng.standard_t(df=3, size=(n_features, d))
     elif kind == KIND_MATERN52:
         W = rng.standard_t(df=5, size=(n_features, d))
     else:

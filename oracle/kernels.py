@@ -4,7 +4,9 @@ Reference semantics (caspbian/mojogp):
   * RBF       k = os * exp(max(-0.5 * sum_d (diff_d / l_d)^2, -20))
   * Matern52  k = os * (1 + sqrt5 r + 5/3 r^2) * exp(max(-sqrt5 r, -20)),
               r = sqrt(max(sum_d (diff_d / l_d)^2 + 1e-20, 1e-20))
-    (codegen_engine/expressions.py:77-114,197-240: forward expressions;
+  * Matern12  k = os * exp(max(-r, -20))
+  * Matern32  k = os * (1 + sqrt3 r) * exp(max(-sqrt3 r, -20))
+    (codegen_engine/expressions.py:77-240: forward expressions;
      codegen_engine/passes/numerical_stability.py:29-41: exp clamp at -20 for
      syntactically negative arguments and sqrt(max(x, 1e-20)))
   * isotropic kernels use a single lengthscale (params [ls, os]); ARD kernels
@@ -12,8 +14,8 @@ Reference semantics (caspbian/mojogp):
   * forward product: out[c, i] = sum_j k(x_i, x_j) V[c, j] + noise V[c, i]
     (codegen_engine/emit/gpu_kernel.py:151-260).
 
-Pinned by tests/test_oracle_kernels.py: scikit-learn RBF / Matern(nu=2.5)
-kernels (unclamped region), the clamp special cases (exact os*e^-20 tails, k(x,
+Pinned by tests/test_oracle_kernels.py: scikit-learn RBF / Matern(nu=0.5,
+1.5, 2.5) kernels (unclamped region), the clamp special cases (exact os*e^-20 tails, k(x,
 x) = os), SymPy derivatives and central finite differences of the gradients.
 """
 
@@ -23,8 +25,12 @@ import numpy as np
 
 RBF = 0
 MATERN52 = 1
+MATERN12 = 2
+MATERN32 = 3
+KINDS = (RBF, MATERN52, MATERN12, MATERN32)
 
 _SQRT5 = np.sqrt(5.0)
+_SQRT3 = np.sqrt(3.0)
 
 
 def _lengthscales(params: np.ndarray, d: int, ard: bool) -> np.ndarray:
@@ -50,6 +56,10 @@ def kernel_from_sq(kind: int, r2: np.ndarray, os: float) -> np.ndarray:
     if kind == RBF:
         return os * np.exp(np.maximum(-0.5 * r2, -20.0))
     r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
+    if kind == MATERN12:
+        return os * np.exp(np.maximum(-r, -20.0))
+    if kind == MATERN32:
+        return os * (1.0 + _SQRT3 * r) * np.exp(np.maximum(-_SQRT3 * r, -20.0))
     return os * (1.0 + _SQRT5 * r + (5.0 / 3.0) * r * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
 
 
@@ -101,7 +111,9 @@ def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
     in d/dl cancels analytically (overrides.py:24-41).
       RBF:      dk/dl_d = k_clamped * diff_d^2 / l_d^3
       Matern52: dk/dl_d = (5/3) os (1 + sqrt5 r) exp(max(-sqrt5 r, -20)) diff_d^2 / l_d^3
-      both:     dk/dos  = k / os
+      Matern32: dk/dl_d = 3 os exp(max(-sqrt3 r, -20)) diff_d^2 / l_d^3
+      Matern12: dk/dl_d = os exp(max(-r, -20)) / r diff_d^2 / l_d^3 (r floored as above)
+      all:      dk/dos  = k / os
     Isotropic: dk/dl = sum_d of the per-dimension terms with l_d = l.
     """
     X1 = np.atleast_2d(np.asarray(X1, dtype=np.float64))
@@ -113,10 +125,14 @@ def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
     diff2 = (X1[:, None, :] - X2[None, :, :]) ** 2          # raw differences
     r2 = np.einsum("ijk,k->ij", diff2, 1.0 / ls**2)
     k = kernel_from_sq(kind, r2, os)
+    r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
     if kind == RBF:
         h = k
+    elif kind == MATERN12:
+        h = os * np.exp(np.maximum(-r, -20.0)) / r
+    elif kind == MATERN32:
+        h = 3.0 * os * np.exp(np.maximum(-_SQRT3 * r, -20.0))
     else:
-        r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
         h = (5.0 / 3.0) * os * (1.0 + _SQRT5 * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
     terms = diff2 / ls**3                                    # (n1, n2, d)
     if ard:

@@ -20,6 +20,8 @@ CASES = [
     ("rbf_iso_d3", "rbf", False, 3, [0.4, 1.3], 11, 64, 3, 7),
     ("m52_ard_d2", "matern52", True, 2, [0.3, 0.8, 1.7], 12, 96, 2, 9),
     ("m52_iso_d6", "matern52", False, 6, [0.7, 0.9], 13, 128, 4, 5),
+    ("m12_ard_d3", "matern12", True, 3, [0.5, 0.9, 1.4, 0.8], 14, 80, 3, 6),
+    ("m32_iso_d2", "matern32", False, 2, [0.6, 1.2], 15, 72, 2, 8),
 ]
 
 

@@ -10,14 +10,14 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from mojogp_amd._provider import KIND_MATERN52, KIND_RBF
+from mojogp_amd._provider import KIND_MATERN12, KIND_MATERN32, KIND_MATERN52, KIND_RBF
 from mojogp_amd.pathwise_prior import (build_feature_weights, build_pathwise_feature_map,
                                        sample_prior_values)
 from oracle import lmc as ol
 
 FIX = np.load(Path(__file__).parent / "golden" / "pathwise_prior.npz")
 CASES = sorted({k.split("__")[0] for k in FIX.files})
-KINDS = {"rbf": KIND_RBF, "m52": KIND_MATERN52}
+KINDS = {"rbf": KIND_RBF, "m52": KIND_MATERN52, "m12": KIND_MATERN12, "m32": KIND_MATERN32}
 
 
 def _case(name):

@@ -12,10 +12,11 @@ def _sk_kernel(kind, ls):
     from sklearn.gaussian_process.kernels import RBF, Matern
     if kind == ok.RBF:
         return RBF(length_scale=ls)
-    return Matern(length_scale=ls, nu=2.5)
+    nu = {ok.MATERN12: 0.5, ok.MATERN32: 1.5, ok.MATERN52: 2.5}[kind]
+    return Matern(length_scale=ls, nu=nu)
 
 
-@pytest.mark.parametrize("kind", [ok.RBF, ok.MATERN52])
+@pytest.mark.parametrize("kind", ok.KINDS)
 @pytest.mark.parametrize("ard", [False, True])
 def test_matches_sklearn_in_unclamped_region(kind, ard, rng):
     d = 4
@@ -47,14 +48,14 @@ def test_matern_clamp_tail_keeps_polynomial():
     assert K[0, 0] == pytest.approx(expect, rel=1e-12)
 
 
-@pytest.mark.parametrize("kind", [ok.RBF, ok.MATERN52])
+@pytest.mark.parametrize("kind", ok.KINDS)
 def test_diagonal_is_outputscale(kind, rng):
     X = rng.normal(size=(10, 3))
     K = ok.kernel_matrix(kind, X, X, [0.7, 0.3, 1.1, 2.0], True)
     np.testing.assert_allclose(np.diag(K), 2.0, rtol=1e-9)
 
 
-@pytest.mark.parametrize("kind", [ok.RBF, ok.MATERN52])
+@pytest.mark.parametrize("kind", ok.KINDS)
 @pytest.mark.parametrize("ard", [False, True])
 def test_gradients_match_finite_differences(kind, ard, rng):
     d = 3
@@ -83,6 +84,27 @@ def test_matern_gradient_matches_sympy():
     for p, sym in enumerate([l0, l1, os]):
         ref = float(sp.diff(k, sym).subs(vals))
         assert G[p, 0, 0] == pytest.approx(ref, rel=1e-12)
+
+
+@pytest.mark.parametrize("kind,nu_k", [(ok.MATERN12, "exp"), (ok.MATERN32, "m32")])
+def test_low_order_matern_gradient_matches_sympy(kind, nu_k):
+    """Matern-1/2 and 3/2 lengthscale derivatives of the forward expressions
+    with the reference's r = sqrt(sum (a/l)^2 + 1e-20), as SymPy gives them."""
+    sp = pytest.importorskip("sympy")
+    l0, l1, os, a0, a1 = sp.symbols("l0 l1 os a0 a1", positive=True)
+    r = sp.sqrt((a0 / l0) ** 2 + (a1 / l1) ** 2 + sp.Float(1e-20))
+    if nu_k == "exp":
+        k = os * sp.exp(-r)
+    else:
+        k = os * (1 + sp.sqrt(3) * r) * sp.exp(-sp.sqrt(3) * r)
+    vals = {l0: 0.8, l1: 1.3, os: 1.7, a0: 0.4, a1: -0.9}
+    G = ok.kernel_gradients(kind, np.array([[0.4, -0.9]]), np.zeros((1, 2)), [0.8, 1.3, 1.7], True)
+    for p, sym in enumerate([l0, l1, os]):
+        assert G[p, 0, 0] == pytest.approx(float(sp.diff(k, sym).subs(vals)), rel=1e-12)
+    # coincident points: finite (the floored r), zero lengthscale derivative
+    G0 = ok.kernel_gradients(kind, np.zeros((1, 2)), np.zeros((1, 2)), [0.8, 1.3, 1.7], True)
+    assert np.all(np.isfinite(G0)) and G0[0, 0, 0] == 0.0
+    assert G0[2, 0, 0] == pytest.approx(1.0, abs=1e-9)
 
 
 def test_forward_matvec_matches_dense(rng):
