@@ -67,6 +67,14 @@ MGP_API int mgp_materialize(void* handle);
  * impl_get_diagonal_value fn pointers (fn_ptr_module.py:651-703). */
 MGP_API int mgp_update_params(void* handle, const float* params, int nparams);
 MGP_API int mgp_update_noise(void* handle, float noise);
+
+/* Fixed per-point observation-noise variances noise_vec[n] (finite, > 0), or
+ * NULL to return to the scalar noise: the operator becomes K + diag(noise_vec)
+ * (the scalar noise is then ignored) and preconditioners are built for
+ * L L^T + diag(noise_vec).  Replaces init_provider(X, params, noise,
+ * observation_noise, noise_mode=1) (fn_ptr_module.py:998-1168, noise modes
+ * :297-327). */
+MGP_API int mgp_set_noise_vector(void* handle, const float* noise_vec);
 MGP_API int mgp_get_noise(void* handle, float* out);
 MGP_API int mgp_get_diagonal_value(void* handle, float* out);
 /* Shape of a provider (the n / dim / num_gradient_params / is_ard keys of the

@@ -46,14 +46,27 @@ class KernelModule:
 
     def init_provider(self, X, params, noise, observation_noise=None, noise_mode=None,
                       noise_group_train=None, num_noise_groups=None) -> dict[str, Any]:
-        if observation_noise is not None or noise_mode not in (None, 0):
+        """Noise modes (fn_ptr_module.py:297-327): 0 scalar; 1 fixed per-point
+        vector (observation_noise [n]).  The learned vector / grouped / linear
+        modes 2-4 are not served."""
+        mode = 0 if noise_mode is None and observation_noise is None else (
+            1 if noise_mode is None else int(noise_mode))
+        if mode not in (0, 1):
             raise NotImplementedError(
-                "heteroskedastic / grouped / learned-vector noise modes are not part of the "
-                "gfx950 hot path; use scalar learned noise")
+                "learned vector / grouped / input-dependent noise modes (2-4) are not served "
+                "by the gfx950 engine; use scalar learned noise or a fixed noise vector")
+        if mode == 1 and observation_noise is None:
+            raise ValueError("noise mode 1 needs observation_noise")
         X = _lib.f32(X)
         if X.ndim != 2 or X.shape[1] != self.dim:
             raise ValueError(f"X must have shape (n, {self.dim})")
         prov = NativeProvider(self.kind, self.ard, X, params, noise)
+        if mode == 1:
+            try:
+                prov.set_noise_vector(observation_noise)
+            except Exception:
+                prov.close()
+                raise
         return {
             "provider_ptr": int(prov.handle.value),
             "n": int(X.shape[0]),
@@ -65,8 +78,8 @@ class KernelModule:
             "x_ptr": 0,
             "is_ard": self.ard,
             "materialization_mode": 0,
-            "noise_mode": 0,
-            "has_observation_noise_vector": False,
+            "noise_mode": mode,
+            "has_observation_noise_vector": mode == 1,
             "noise_group_ptr": 0,
             "num_noise_groups": 0,
             "_provider": prov,

@@ -157,6 +157,7 @@ _SIGNATURES = {
     "mgp_materialize": (C.c_int, [C.c_void_p]),
     "mgp_update_params": (C.c_int, [C.c_void_p, c_float_p, C.c_int]),
     "mgp_update_noise": (C.c_int, [C.c_void_p, C.c_float]),
+    "mgp_set_noise_vector": (C.c_int, [C.c_void_p, c_float_p]),
     "mgp_get_noise": (C.c_int, [C.c_void_p, c_float_p]),
     "mgp_get_diagonal_value": (C.c_int, [C.c_void_p, c_float_p]),
     "mgp_provider_info": (C.c_int, [C.c_void_p, c_int64_p, c_int_p, c_int_p, c_int_p,

@@ -83,6 +83,18 @@ class NativeProvider:
         _lib.call("mgp_update_noise", self.handle, float(noise))
         self.noise = float(noise)
 
+    def set_noise_vector(self, noise_vec) -> None:
+        """Fixed per-point noise variances [n] (K + diag(noise_vec)), or None."""
+        if noise_vec is None:
+            _lib.call("mgp_set_noise_vector", self.handle, None)
+            self.noise_vec = None
+            return
+        v = _lib.f32(noise_vec).ravel()
+        if v.shape != (self.n,):
+            raise ValueError(f"noise vector must have shape ({self.n},), got {v.shape}")
+        _lib.call("mgp_set_noise_vector", self.handle, _lib.fptr(v))
+        self.noise_vec = v.copy()
+
     def forward_matvec(self, V) -> np.ndarray:
         Vc, vec = _cols(V, self.n)
         out = np.empty_like(Vc)

@@ -138,8 +138,13 @@ int mgp_update_noise(void* h, float noise) {
   });
 }
 
+// Under a noise vector the reference reports a 1e-6 floor (impl_get_noise,
+// fn_ptr_module.py:673-679).
 int mgp_get_noise(void* h, float* out) {
-  return guarded([&] { *out = as_provider(h)->noise; });
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    *out = pv->has_noise_vec ? 1e-6f : pv->noise;
+  });
 }
 
 int mgp_get_diagonal_value(void* h, float* out) {
@@ -222,6 +227,13 @@ int mgp_cross_matvec(void* h, const float* Xs, int64_t m, const float* V,
     pv->cross(pv->test, dv, ncols, dout);
     MGP_HIP_CHECK(hipMemcpyAsync(out, dout, to * sizeof(float), hipMemcpyDeviceToHost, pv->st));
     MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+int mgp_set_noise_vector(void* h, const float* noise_vec) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    pv->set_noise_vector(noise_vec);
   });
 }
 

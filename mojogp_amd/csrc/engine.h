@@ -23,8 +23,15 @@ struct Precond {
   float noise = 0.f;   // noise at construction (used by apply, log-det, probes)
   DevBuf<float> L;     // [rank][n]
   DevBuf<float> Minv;  // (L^T L + max(noise,1e-6) I)^{-1}, row-major fp32
-  float logdet = 0.f;  // log|L L^T + noise I|
+                       // (diagonal noise D: (I + L^T D^-1 L)^-1)
+  float logdet = 0.f;  // log|L L^T + noise I| (or log|L L^T + D|)
   WoodburyWork work;
+  // Diagonal noise D from the provider's noise vector (pivoted_cholesky.mojo:
+  // 1209-1240, 1346-1520, 2060-2095): per-row 1/d_i and sqrt(d_i).
+  bool vec = false;
+  DevBuf<float> dinv, dsqrt;
+  const float* dinv_ptr() const { return vec ? dinv.ptr : nullptr; }
+  const float* dsqrt_ptr() const { return vec ? dsqrt.ptr : nullptr; }
 };
 
 // Pivot options of the training loop for a precond_method (greedy: no trace

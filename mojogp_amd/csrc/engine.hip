@@ -19,6 +19,15 @@ double secs_since(Clock::time_point t0) {
   return std::chrono::duration<double>(Clock::now() - t0).count();
 }
 
+// dinv[i] = 1 / d[i], dsqrt[i] = sqrt(d[i])
+__global__ void k_recip_sqrt(const float* __restrict__ d, int64_t n, float* __restrict__ dinv,
+                             float* __restrict__ dsqrt) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  dinv[i] = 1.0f / d[i];
+  dsqrt[i] = sqrtf(d[i]);
+}
+
 __global__ void k_part_to_float(const double* __restrict__ part, int nb, int ncols,
                                 float* __restrict__ out) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -276,7 +285,8 @@ PivotOptions training_pivot_options(int method) {
 }
 
 void build_precond(Provider& pv, int rank, const PivotOptions& po, Precond& P) {
-  P.noise = pv.noise;
+  P.vec = pv.has_noise_vec;
+  P.noise = P.vec ? 1e-6f : pv.noise;
   if (rank <= 0) {
     P.rank = 0;
     P.logdet = 0.f;
@@ -288,6 +298,32 @@ void build_precond(Provider& pv, int rank, const PivotOptions& po, Precond& P) {
   P.L.ensure((size_t)rank * n);
   const int k = pivoted_cholesky(pv, rank, po, P.L.ptr, st);
   P.rank = k;
+  if (P.vec) {
+    // P = L L^T + D: M = I + L^T D^-1 L, log|P| = sum log d_i + log|M|.
+    hipLaunchKernelGGL(k_recip_sqrt, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st,
+                       pv.noise_vec.ptr, n,
+                       P.dinv.ensure(n), P.dsqrt.ensure(n));
+    MGP_HIP_CHECK(hipGetLastError());
+    DevBuf<double> Md;
+    Md.ensure((size_t)k * k);
+    syrk_ltl(P.L.ptr, n, k, Md.ptr, st, P.dinv.ptr);
+    std::vector<double> M((size_t)k * k);
+    MGP_HIP_CHECK(hipMemcpy(M.data(), Md.ptr, M.size() * sizeof(double), hipMemcpyDeviceToHost));
+    for (int i = 0; i < k; ++i) M[(size_t)i * k + i] += 1.0;
+    std::vector<double> inv;
+    if (!spd_inverse(M, k, inv)) throw Error(ST_NUMERIC, "preconditioner core matrix is singular");
+    std::vector<float> invf(inv.begin(), inv.end());
+    P.Minv.ensure(invf.size());
+    MGP_HIP_CHECK(hipMemcpy(P.Minv.ptr, invf.data(), invf.size() * sizeof(float),
+                            hipMemcpyHostToDevice));
+    std::vector<float> d((size_t)n);
+    MGP_HIP_CHECK(hipMemcpy(d.data(), pv.noise_vec.ptr, (size_t)n * sizeof(float),
+                            hipMemcpyDeviceToHost));
+    double ld = 0.0;
+    for (int64_t i = 0; i < n; ++i) ld += std::log((double)d[(size_t)i]);
+    P.logdet = (float)(ld + logdet_spd(M, k));
+    return;
+  }
   DevBuf<double> Md;
   Md.ensure((size_t)k * k);
   syrk_ltl(P.L.ptr, n, k, Md.ptr, st);
@@ -318,7 +354,7 @@ CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_i
     const int nb = reduction_chunks(pv.n);
     op.precond = [&pv, P, nb](const float* r, int ncols, float* z, double* rz_part) {
       woodbury_apply(P->L.ptr, pv.n, P->rank, P->Minv.ptr, P->noise, r, ncols, z, P->work, r,
-                     nb, rz_part, pv.st);
+                     nb, rz_part, pv.st, P->dinv_ptr());
     };
   }
   return batched_cg(op, rhs, C, max_iter, max_tridiag, tol, w, warm_start);
@@ -451,7 +487,8 @@ BBMMResult bbmm_step(Provider& pv, Precond& P, bool use_precond, const float* y_
       float* zn = w.zn.ensure(nT);
       gaussian(zr, (int64_t)P.rank * T, seed, st);
       gaussian(zn, (int64_t)nT, seed + 1000000ull, st);
-      low_rank_sample(P.L.ptr, n, P.rank, zr, zn, std::sqrt(P.noise), T, probes, st);
+      low_rank_sample(P.L.ptr, n, P.rank, zr, zn, std::sqrt(P.noise), T, probes, st,
+                      P.dsqrt_ptr());
     } else {
       gaussian(probes, (int64_t)nT, seed, st);
     }
@@ -517,7 +554,7 @@ BBMMResult bbmm_step(Provider& pv, Precond& P, bool use_precond, const float* y_
     scale_columns(rf + n, facs.ptr + C + 1, n, T, false, st);
     if (pre)
       woodbury_apply(P.L.ptr, n, P.rank, P.Minv.ptr, P.noise, rf + n, T, rf + n, P.work,
-                     nullptr, reduction_chunks(n), nullptr, st);
+                     nullptr, reduction_chunks(n), nullptr, st, P.dinv_ptr());
   }
   const int np = pv.nparams;
   std::vector<double> g(np, 0.0);

@@ -19,6 +19,11 @@ struct Provider {
   int nparams = 0;             // engine layout: [ls | ls_0..ls_{d-1}], os
   std::vector<float> params;   // constrained values
   float noise = 0.f;
+  // Fixed per-point noise variances (the reference's noise mode 1): when set,
+  // forward() adds diag(noise_vec) and ignores the scalar noise, and the
+  // preconditioner is built for L L^T + diag(noise_vec).
+  DevBuf<float> noise_vec;
+  bool has_noise_vec = false;
   std::vector<double> center;  // column means of the training inputs
 
   hipStream_t st = nullptr;
@@ -53,8 +58,15 @@ struct Provider {
   // Rebind the provider (and its rocBLAS handle) to another stream.
   void set_stream(hipStream_t s);
 
-  // (K + noise I) V  for device arrays V, out ([ncols][n] column-major).
+  // Host [n] noise variances (all finite and > 0), or nullptr to clear.
+  void set_noise_vector(const float* host);
+  // The scalar noise the operator uses: 0 under a noise vector.
+  float scalar_noise() const { return has_noise_vec ? 0.f : noise; }
+
+  // (K + noise I) V (or (K + diag(noise_vec)) V) for device arrays V, out
+  // ([ncols][n] column-major).
   void forward(const float* V, int ncols, float* out);
+  void forward_scalar(const float* V, int ncols, float* out);  // without the noise vector
   // True when forward() runs the fused tile kernel (not materialized, Gram form
   // accurate for the packed training set).
   bool fused_route() const;

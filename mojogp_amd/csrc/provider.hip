@@ -53,7 +53,29 @@ __global__ void k_scaled_copy(float* __restrict__ y, const float* __restrict__ x
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = a * x[i];
 }
+
+// out[c][i] += dvec[i] * V[c][i]
+__global__ void k_add_diag_vec(float* __restrict__ out, const float* __restrict__ V,
+                               const float* __restrict__ dvec, int64_t n, int ncols) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * ncols) return;
+  out[idx] = fmaf(dvec[idx % n], V[idx], out[idx]);
+}
 }  // namespace
+
+void Provider::set_noise_vector(const float* host) {
+  if (!host) {
+    has_noise_vec = false;
+    return;
+  }
+  for (int64_t i = 0; i < n; ++i)
+    MGP_REQUIRE(std::isfinite(host[i]) && host[i] > 0.f, "noise vector entries must be finite and > 0");
+  noise_vec.ensure((size_t)n);
+  MGP_HIP_CHECK(hipMemcpyAsync(noise_vec.ptr, host, (size_t)n * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  has_noise_vec = true;
+}
 
 void Provider::fill_dense() {
   fill_cross(kind, outputscale(), train, 0, n, train, d, K.ptr, st);
@@ -91,6 +113,17 @@ void Provider::pack(const float* X_dev, int64_t m, PackedPoints& pp) {
 }
 
 void Provider::forward(const float* V, int ncols, float* out) {
+  forward_scalar(V, ncols, out);
+  if (has_noise_vec) {
+    const int64_t total = n * (int64_t)ncols;
+    hipLaunchKernelGGL(k_add_diag_vec, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                       out, V, noise_vec.ptr, n, ncols);
+    MGP_HIP_CHECK(hipGetLastError());
+  }
+}
+
+void Provider::forward_scalar(const float* V, int ncols, float* out) {
+  const float noise = scalar_noise();
   MatvecArgs a;
   a.kind = kind;
   a.outputscale = outputscale();

@@ -89,7 +89,9 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
                      hipStream_t st);
 
 // M = L^T L (k x k, fp64) for the first k columns.
-void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st);
+// M = L^T diag(wt) L when wt (device [n]) is given.
+void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st,
+              const float* wt = nullptr);
 // M[a][b] = La_a . Lb_b (ka x kb, fp64 on the device) for factors [k][n].
 void cross_ltl(const float* La, int ka, const float* Lb, int kb, int64_t n, double* M_dev,
                hipStream_t st);
@@ -103,12 +105,17 @@ struct WoodburyWork {
   DevBuf<float> wsum;    // [C][k]
   DevBuf<float> u;       // [C][k]
 };
+// With dinv (device [n], per-row 1/d_i of a diagonal D): u = Minv L^T D^-1 v and
+// out = D^-1 (v - L u), Minv = (I + L^T D^-1 L)^-1.
 void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,
                     const float* v, int ncols, float* out, WoodburyWork& w,
-                    const float* dotv, int nb, double* dot_part, hipStream_t st);
+                    const float* dotv, int nb, double* dot_part, hipStream_t st,
+                    const float* dinv = nullptr);
 // out[c*n + i] = sum_kk L[kk*n+i] * zr[c*k + kk] + s * zn[c*n + i]  (zn may be null)
+// ds (device [n], optional): per-row sqrt(d_i) in place of s.
 void low_rank_sample(const float* L, int64_t n, int k, const float* zr,
-                     const float* zn, float s, int ncols, float* out, hipStream_t st);
+                     const float* zn, float s, int ncols, float* out, hipStream_t st,
+                     const float* ds = nullptr);
 
 // out[c][kk] = L_kk . V_c for ncols columns (L [k][n], V [ncols][n]).
 void lt_matmul(const float* L, int64_t n, int k, const float* V, int ncols, float* out,

@@ -387,8 +387,9 @@ __global__ __launch_bounds__(256) void k_pc_column(
 }
 
 // M[a][b] partial over a row split; grid (tiles, tiles, splits), 16x16 threads.
+// wt (optional): per-row weight applied to the a side, M = L^T diag(wt) L.
 __global__ void k_syrk_part(const float* __restrict__ L, int64_t n, int k, int splits,
-                            double* __restrict__ part) {
+                            double* __restrict__ part, const float* __restrict__ wt) {
   __shared__ float ta[16][65];
   __shared__ float tb[16][65];
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
@@ -401,7 +402,8 @@ __global__ void k_syrk_part(const float* __restrict__ L, int64_t n, int k, int s
       const int col = t / 64, row = t % 64;
       const int64_t i = s + row;
       const bool ok = i < i1;
-      ta[col][row] = (ok && a0 + col < k) ? L[(int64_t)(a0 + col) * n + i] : 0.0f;
+      const float la = (ok && a0 + col < k) ? L[(int64_t)(a0 + col) * n + i] : 0.0f;
+      ta[col][row] = (wt && ok) ? la * wt[i] : la;
       tb[col][row] = (ok && b0 + col < k) ? L[(int64_t)(b0 + col) * n + i] : 0.0f;
     }
     __syncthreads();
@@ -480,9 +482,10 @@ __global__ __launch_bounds__(256) void k_lt_reduce(const float* __restrict__ wpa
 
 // w-part[(b*ncols + c)*k + kk] = sum_{i in chunk b} L[kk][i] v[c][i]; block =
 // 16 kk x 16 c, grid = (chunks, kk tiles, column tiles).
+// rs (optional): per-row scale of v (diag(rs) v).
 __global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
                           const float* __restrict__ v, int ncols, int nb,
-                          float* __restrict__ wpart) {
+                          float* __restrict__ wpart, const float* __restrict__ rs) {
   __shared__ float tl[16][65];
   __shared__ float tv[16][65];
   const int tc = threadIdx.x & 15, tk = threadIdx.x >> 4;
@@ -496,7 +499,8 @@ __global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
       const int64_t i = s + row;
       const bool ok = i < i1;
       tl[q][row] = (ok && kk0 + q < k) ? L[(int64_t)(kk0 + q) * n + i] : 0.0f;
-      tv[q][row] = (ok && c0 + q < ncols) ? v[(int64_t)(c0 + q) * n + i] : 0.0f;
+      const float vv = (ok && c0 + q < ncols) ? v[(int64_t)(c0 + q) * n + i] : 0.0f;
+      tv[q][row] = (rs && ok) ? vv * rs[i] : vv;
     }
     __syncthreads();
 #pragma unroll 8
@@ -521,11 +525,11 @@ __global__ void k_small_solve(const float* __restrict__ w, int k, const float* _
   }
 }
 
-// out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * inv_noise; one thread per
-// row, grid = (row blocks, column tiles of 16).
+// out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * inv_noise (or * dinv[i]);
+// one thread per row, grid = (row blocks, column tiles of 16).
 __global__ __launch_bounds__(256) void k_woodbury_final(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ u,
-    int ncols, float inv_noise, const float* v, float* out) {
+    int ncols, float inv_noise, const float* v, float* out, const float* __restrict__ dinv) {
   extern __shared__ float us[];  // [16][k]
   const int c0 = blockIdx.y * 16;
   const int cn = min(16, ncols - c0);
@@ -544,19 +548,22 @@ __global__ __launch_bounds__(256) void k_woodbury_final(
 #pragma unroll
     for (int c = 0; c < 16; ++c) z[c] = fmaf(l, us[c * k + kk], z[c]);
   }
+  const float sc = dinv ? dinv[i] : inv_noise;
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     if (c < cn) {
       const int64_t off = (int64_t)(c0 + c) * n + i;
-      out[off] = inv_noise * (v[off] - z[c]);
+      out[off] = sc * (v[off] - z[c]);
     }
   }
 }
 
 // grid = (row blocks, column tiles of 16)
+// ds (optional): per-row scale of zn in place of s.
 __global__ __launch_bounds__(256) void k_low_rank_sample(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ zr,
-    const float* __restrict__ zn, float s, int ncols, float* __restrict__ out) {
+    const float* __restrict__ zn, float s, int ncols, float* __restrict__ out,
+    const float* __restrict__ ds) {
   extern __shared__ float zs[];  // [16][k]
   const int c0 = blockIdx.y * 16;
   const int cn = min(16, ncols - c0);
@@ -575,11 +582,12 @@ __global__ __launch_bounds__(256) void k_low_rank_sample(
 #pragma unroll
     for (int c = 0; c < 16; ++c) z[c] = fmaf(l, zs[c * k + kk], z[c]);
   }
+  const float si = ds ? ds[i] : s;
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
     if (c < cn) {
       const int64_t off = (int64_t)(c0 + c) * n + i;
-      out[off] = zn ? z[c] + s * zn[off] : z[c];
+      out[off] = zn ? z[c] + si * zn[off] : z[c];
     }
   }
 }
@@ -926,7 +934,9 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
 
   // Host-driven selection (pivoted_cholesky.mojo:2195-2334).
   const float diag_value = os;  // provider diagonal value k(x, x)
-  const float noise = pv.noise;
+  // vector-noise providers report the 1e-6 floor here (impl_get_noise,
+  // fn_ptr_module.py:673-679)
+  const float noise = pv.has_noise_vec ? 1e-6f : pv.noise;
   std::vector<char> used((size_t)n, 0);
   std::vector<float> dh;
   uint64_t rng = o.seed;
@@ -981,13 +991,14 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
   return rank;
 }
 
-void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st) {
+void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st,
+              const float* wt) {
   const int tiles = (int)ceil_div(k, 16);
   const int splits = (int)std::max<int64_t>(1, std::min<int64_t>(64, ceil_div(n, 4096)));
   DevBuf<double> part;
   part.ensure((size_t)splits * k * k);
   hipLaunchKernelGGL(k_syrk_part, dim3(tiles, tiles, splits), dim3(256), 0, st, L, n, k,
-                     splits, part.ptr);
+                     splits, part.ptr, wt);
   hipLaunchKernelGGL(k_syrk_final, grid1((int64_t)k * k), dim3(kBlock), 0, st, part.ptr, k,
                      splits, M_dev);
   MGP_HIP_CHECK(hipGetLastError());
@@ -1000,35 +1011,36 @@ static int lt_chunks(int64_t n) {
 }
 
 static void launch_lt_part(const float* L, int64_t n, int k, const float* v, int ncols, int nbw,
-                           float* wpart, hipStream_t st) {
+                           float* wpart, hipStream_t st, const float* rs = nullptr) {
   const dim3 grid((unsigned)nbw, (unsigned)ceil_div(k, 16), (unsigned)ceil_div(ncols, 16));
-  hipLaunchKernelGGL(k_lt_part, grid, dim3(256), 0, st, L, n, k, v, ncols, nbw, wpart);
+  hipLaunchKernelGGL(k_lt_part, grid, dim3(256), 0, st, L, n, k, v, ncols, nbw, wpart, rs);
 }
 
 void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,
                     const float* v, int ncols, float* out, WoodburyWork& w,
-                    const float* dotv, int nb, double* dot_part, hipStream_t st) {
+                    const float* dotv, int nb, double* dot_part, hipStream_t st,
+                    const float* dinv) {
   const int nbw = lt_chunks(n);
   float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
   float* wsum = w.wsum.ensure((size_t)ncols * k);
   float* u = w.u.ensure((size_t)ncols * k);
-  launch_lt_part(L, n, k, v, ncols, nbw, wpart, st);
+  launch_lt_part(L, n, k, v, ncols, nbw, wpart, st, dinv);
   hipLaunchKernelGGL(k_lt_reduce, dim3((unsigned)ceil_div((int64_t)k * ncols * 64, 256)),
                      dim3(256), 0, st, wpart, nbw, k, ncols, wsum);
   hipLaunchKernelGGL(k_small_solve, dim3(ncols), dim3(256), (size_t)k * sizeof(float), st,
                      wsum, k, Minv, u);
   const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256), (unsigned)ceil_div(ncols, 16));
   hipLaunchKernelGGL(k_woodbury_final, grid, dim3(256), (size_t)16 * k * sizeof(float), st, L,
-                     n, k, u, ncols, 1.0f / noise, v, out);
+                     n, k, u, ncols, 1.0f / noise, v, out, dinv);
   MGP_HIP_CHECK(hipGetLastError());
   if (dot_part) coldot_partial(dotv, out, n, ncols, nb, dot_part, st);
 }
 
 void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const float* zn,
-                     float s, int ncols, float* out, hipStream_t st) {
+                     float s, int ncols, float* out, hipStream_t st, const float* ds) {
   const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256), (unsigned)ceil_div(ncols, 16));
   hipLaunchKernelGGL(k_low_rank_sample, grid, dim3(256), (size_t)16 * k * sizeof(float), st, L,
-                     n, k, zr, zn, s, ncols, out);
+                     n, k, zr, zn, s, ncols, out, ds);
   MGP_HIP_CHECK(hipGetLastError());
 }
 

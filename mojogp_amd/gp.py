@@ -36,6 +36,24 @@ _DEFAULT_PREDICT_CG_TOL = _DEFAULT_EXACT_PREDICT_CG_TOL
 _FIT_METHOD_ALIASES = {"mat": "materialized", "mf": "matrix_free"}
 
 
+def _evaluate_noise_fn(fn, X, expected_n: int, name: str, floor: float) -> np.ndarray:
+    """observation_noise_fn(X) -> [n] variances, validated (gp.py:2705-2730)."""
+    if not callable(fn):
+        raise ValueError(f"{name} must be callable")
+    try:
+        noise = fn(np.ascontiguousarray(X, dtype=np.float32))
+    except Exception as exc:
+        raise ValueError(f"{name} failed while evaluating observation noise") from exc
+    obs = np.ascontiguousarray(noise, dtype=np.float32)
+    if obs.shape != (expected_n,):
+        raise ValueError(f"{name} must return shape ({expected_n},), got {obs.shape}")
+    if np.any(~np.isfinite(obs)):
+        raise ValueError(f"{name} returned NaN or Inf values")
+    if np.any(obs < floor):
+        raise ValueError(f"{name} values must be >= noise_floor")
+    return obs
+
+
 def normalize_fit_method(method: str, *, allow_auto: bool = False) -> str:
     """Canonical training route name (mojogp/_routes.py:12-28)."""
     if not isinstance(method, str):
@@ -155,6 +173,11 @@ class SingleOutputGP:
         self._prediction_cache_info: Optional[dict] = None
         self._noise_floor = 1e-6
         self._noise_regularization = 0.0
+        self._noise_mode = "scalar"
+        self._observation_noise_train: Optional[np.ndarray] = None
+        self._noise_group_train: Optional[np.ndarray] = None
+        self._noise_group_values: Optional[np.ndarray] = None
+        self._observation_noise_fn = None
 
     # ------------------------------------------------------------ properties
     @property
@@ -217,9 +240,11 @@ class SingleOutputGP:
 
     def _build_provider_info(self, X, engine_params, noise, method=None) -> dict:
         self._ensure_compiled()
+        obs = getattr(self, "_observation_noise_train", None)
         info = self._kernel_module.init_provider(np.ascontiguousarray(X, dtype=np.float32),
                                                  np.ascontiguousarray(engine_params, np.float32),
-                                                 float(noise))
+                                                 float(noise), observation_noise=obs,
+                                                 noise_mode=None if obs is None else 1)
         if (method or self._training_method) == "materialized":
             self._kernel_module.materialize(info)
         return info
@@ -277,14 +302,9 @@ class SingleOutputGP:
             raise ValueError("noise_floor must be finite and > 0")
         if noise_regularization < 0 or not np.isfinite(noise_regularization):
             raise ValueError("noise_regularization must be finite and >= 0")
-        if (noise_model != "scalar" or observation_noise is not None
-                or observation_noise_fn is not None or noise_function is not None
-                or noise_group_train is not None or group_noise is not None):
-            raise NotImplementedError("only scalar learned noise is served by the gfx950 engine")
-        if not learn_noise:
-            raise NotImplementedError(
-                "Fixed scalar noise is not implemented in the JIT training API yet; use "
-                "learn_noise=True or provide observation_noise")
+        obs_train, noise_mode, groups_arr, gnoise_arr = self._resolve_noise_model(
+            X, noise_model, observation_noise, observation_noise_fn, noise_function,
+            learn_noise, noise_floor, initial_noise, noise_group_train, group_noise)
         if preset is not None and preset not in self._PRESETS:
             raise ValueError(f"Unknown preset '{preset}'. Must be one of: {list(self._PRESETS)}")
         if max_iterations <= 0:
@@ -317,6 +337,11 @@ class SingleOutputGP:
 
         self._destroy_provider_info()
         self._X_train, self._y_train = X, y
+        self._observation_noise_train = obs_train
+        self._noise_mode = noise_mode
+        self._noise_group_train = groups_arr
+        self._noise_group_values = gnoise_arr
+        self._observation_noise_fn = observation_noise_fn
         self.dim = X.shape[1]
         self._noise_floor = float(noise_floor)
         self._noise_regularization = float(noise_regularization)
@@ -393,6 +418,132 @@ class SingleOutputGP:
                                           max_root_decomposition_size=prediction_cache_rank)
         return result
 
+    def _resolve_noise_model(self, X, noise_model, observation_noise, observation_noise_fn,
+                             noise_function, learn_noise, noise_floor, initial_noise,
+                             noise_group_train, group_noise):
+        """Noise-model resolution of gp.py:1010-1161.  Served: learned scalar
+        noise, and fixed per-sample variances (observation_noise,
+        observation_noise_fn, fixed grouped variances), trained as
+        K + diag(noise_i) with the noise not learned.  The learned vector,
+        grouped and input-dependent modes raise NotImplementedError."""
+        if noise_model not in ("scalar", "fixed_vector", "input_dependent", "grouped",
+                               "learned_vector", "learned_input_dependent"):
+            raise ValueError("noise_model must be one of 'scalar', 'fixed_vector', "
+                             "'input_dependent', 'grouped', 'learned_vector', or "
+                             "'learned_input_dependent'")
+        if noise_function is not None and noise_function != "linear":
+            raise ValueError("noise_function must be 'linear' for learned input-dependent noise")
+        if noise_function is not None and noise_model != "learned_input_dependent":
+            raise ValueError("noise_function is only supported with "
+                             "noise_model='learned_input_dependent'")
+        if observation_noise_fn is not None and not callable(observation_noise_fn):
+            raise ValueError("observation_noise_fn must be callable")
+        if observation_noise_fn is not None and observation_noise is not None:
+            raise ValueError("Pass either observation_noise or observation_noise_fn, not both")
+        if observation_noise_fn is not None and noise_model == "grouped":
+            raise ValueError("noise_model='grouped' expands group_noise to observation_noise; "
+                             "do not also pass observation_noise_fn")
+        if noise_model == "input_dependent" and observation_noise_fn is None:
+            raise ValueError("noise_model='input_dependent' requires observation_noise_fn")
+        if noise_model in ("learned_vector", "learned_input_dependent"):
+            raise NotImplementedError(f"noise_model={noise_model!r} (learned per-sample noise) "
+                                      "is not served by the gfx950 engine")
+        if observation_noise is not None and noise_model == "grouped":
+            raise ValueError("noise_model='grouped' expands group_noise to observation_noise; "
+                             "do not also pass observation_noise")
+        if observation_noise_fn is not None:
+            if learn_noise:
+                raise ValueError("learn_noise must be False when observation_noise_fn is "
+                                 "supplied")
+            observation_noise = _evaluate_noise_fn(observation_noise_fn, X, X.shape[0],
+                                                   "observation_noise_fn", noise_floor)
+            noise_model = "fixed_input_dependent"
+        if observation_noise is not None and noise_model == "scalar":
+            noise_model = "fixed_vector"
+        groups_arr = gnoise_arr = None
+        if noise_model == "grouped":
+            if noise_group_train is None:
+                raise ValueError("noise_model='grouped' requires noise_group_train")
+            groups_arr = np.ascontiguousarray(noise_group_train, dtype=np.int32)
+            if groups_arr.shape != (X.shape[0],):
+                raise ValueError(f"noise_group_train must have shape ({X.shape[0]},), got "
+                                 f"{groups_arr.shape}")
+            if np.any(groups_arr < 0):
+                raise ValueError("noise_group_train must contain non-negative group ids")
+            if learn_noise:
+                raise NotImplementedError("learned grouped noise (noise_model='grouped' with "
+                                          "learn_noise=True) is not served by the gfx950 "
+                                          "engine; pass learn_noise=False with group_noise")
+            if group_noise is None:
+                raise ValueError("noise_model='grouped' requires group_noise when "
+                                 "learn_noise=False")
+            gnoise_arr = np.ascontiguousarray(group_noise, dtype=np.float32)
+            if gnoise_arr.ndim != 1:
+                raise ValueError("group_noise must be a 1D array")
+            if gnoise_arr.size == 0:
+                raise ValueError("group_noise must contain at least one group variance")
+            if np.any(~np.isfinite(gnoise_arr)):
+                raise ValueError("group_noise contains NaN or Inf values")
+            if np.any(gnoise_arr < noise_floor):
+                raise ValueError("group_noise values must be >= noise_floor")
+            if int(groups_arr.max(initial=-1)) >= gnoise_arr.shape[0]:
+                raise ValueError("noise_group_train references a group id outside group_noise")
+            noise_model = "fixed_grouped"
+            observation_noise = gnoise_arr[groups_arr]
+        elif noise_group_train is not None or group_noise is not None:
+            raise ValueError("noise_group_train and group_noise require noise_model='grouped'")
+        if observation_noise is None and noise_model == "fixed_vector":
+            raise ValueError("noise_model='fixed_vector' requires observation_noise")
+        if observation_noise is None and not learn_noise:
+            raise NotImplementedError(
+                "Fixed scalar noise is not implemented in the JIT training API yet; use "
+                "learn_noise=True or provide observation_noise")
+        obs = None
+        if observation_noise is not None:
+            if learn_noise:
+                raise ValueError("learn_noise must be False when observation_noise is supplied")
+            obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
+            if obs.shape != (X.shape[0],):
+                raise ValueError(f"observation_noise must have shape ({X.shape[0]},), got "
+                                 f"{obs.shape}")
+            if np.any(~np.isfinite(obs)):
+                raise ValueError("observation_noise contains NaN or Inf values")
+            if np.any(obs < noise_floor):
+                raise ValueError("observation_noise values must be >= noise_floor")
+        return obs, noise_model, groups_arr, gnoise_arr
+
+    def _observed_noise(self, X, observation_noise, observation_noise_fn, noise_group_test):
+        """Test-point noise for target='observed' (gp.py:2611-2650): explicit
+        values, a callable, test group ids, or the stored training callable."""
+        m = X.shape[0]
+        if observation_noise_fn is not None:
+            if observation_noise is not None or noise_group_test is not None:
+                raise ValueError("Pass only one of observation_noise, observation_noise_fn, "
+                                 "or noise_group_test")
+            return _evaluate_noise_fn(observation_noise_fn, X, m, "observation_noise_fn",
+                                      self._noise_floor)
+        if noise_group_test is not None:
+            if observation_noise is not None:
+                raise ValueError("Pass either observation_noise or noise_group_test, not both")
+            if self._noise_group_values is None:
+                raise ValueError("noise_group_test requires a model fitted with grouped noise")
+            groups = np.ascontiguousarray(noise_group_test, dtype=np.int32)
+            if groups.shape != (m,):
+                raise ValueError(f"noise_group_test must have shape ({m},), got {groups.shape}")
+            if np.any(groups < 0) or int(groups.max(initial=-1)) >= self._noise_group_values.size:
+                raise ValueError("noise_group_test references a group id outside group_noise")
+            return self._noise_group_values[groups].astype(np.float32)
+        if observation_noise is None and self._observation_noise_fn is not None:
+            return _evaluate_noise_fn(self._observation_noise_fn, X, m,
+                                      "stored observation_noise_fn", self._noise_floor)
+        if observation_noise is None:
+            raise ValueError("predict_observed()/predict(target='observed') requires "
+                             "observation_noise for test points")
+        obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
+        if obs.shape != (m,):
+            raise ValueError(f"observation_noise must have shape ({m},), got {obs.shape}")
+        return obs
+
     def _fit_engine(self, X, y, initial_params, initial_noise, max_iterations, learning_rate,
                     route, enable_early_stopping, verbose, cg, use_cosine_lr, init_mean,
                     use_preconditioner, early_stop_patience, early_stop_tol, learn_noise,
@@ -438,9 +589,9 @@ class SingleOutputGP:
             "early_stop_patience": int(early_stop_patience),
             "early_stop_tol": float(early_stop_tol),
             "use_preconditioner": bool(resolved_use_pc),
-            "noise_mode": "scalar",
+            "noise_mode": self._noise_mode,
             "learn_noise": bool(learn_noise),
-            "has_observation_noise_vector": False,
+            "has_observation_noise_vector": self._observation_noise_train is not None,
             "noise_regularization": float(self._noise_regularization),
         }
         for key in ("actual_precond_rank", "precond_build_count", "precond_rebuild_count",
@@ -548,9 +699,8 @@ class SingleOutputGP:
             raise ValueError(f"X has {X.shape[1]} features, expected {self.dim}")
         if np.any(~np.isfinite(X)):
             raise ValueError("X_test contains NaN or Inf values")
-        if target == "observed" and observation_noise is None:
-            raise ValueError("predict_observed()/predict(target='observed') requires "
-                             "observation_noise for test points")
+        obs_test = (self._observed_noise(X, observation_noise, observation_noise_fn,
+                                         noise_group_test) if target == "observed" else None)
 
         tr = self._training_result
         params = self.kernel.to_engine_params(np.array(tr.params, dtype=np.float32))
@@ -609,10 +759,7 @@ class SingleOutputGP:
         self._backend_predict_info.update(
             {k: v for k, v in res.items() if k.startswith("exact_")})
         if target == "observed":
-            obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
-            if obs.shape != (X.shape[0],):
-                raise ValueError(f"observation_noise must have shape ({X.shape[0]},), got {obs.shape}")
-            variance = variance + obs
+            variance = variance + obs_test
         std = np.sqrt(np.maximum(variance, 0))
         if return_var:
             return mean, variance
@@ -620,9 +767,18 @@ class SingleOutputGP:
             return mean, std
         return PredictionResult(mean=mean, variance=variance, std=std)
 
-    def predict_observed(self, X, observation_noise=None, **kwargs):
+    def predict_observed(self, X, observation_noise=None, *, observation_noise_fn=None,
+                         noise_group_test=None, **kwargs):
+        """p(y_test | y_train): test-time noise is explicit (gp.py:2681-2703)."""
         kwargs.pop("target", None)
-        return self.predict(X, target="observed", observation_noise=observation_noise, **kwargs)
+        return self.predict(X, target="observed", observation_noise=observation_noise,
+                            observation_noise_fn=observation_noise_fn,
+                            noise_group_test=noise_group_test, **kwargs)
+
+    def predict_latent(self, X, **kwargs):
+        """p(f_test | y_train)."""
+        kwargs.pop("target", None)
+        return self.predict(X, target="latent", **kwargs)
 
     # ------------------------------------------------------------ cache
     def _cache_signature(self, prediction_method, variance_method, sc, params, noise, mean):
@@ -696,19 +852,29 @@ class SingleOutputGP:
             "training_method": self._training_method,
             "engine_mean": self._engine_predict_mean,
             "backend_train_info": self._backend_train_info,
-            "cached_love_method": self._cached_love_method, "noise_mode": "scalar",
+            "cached_love_method": self._cached_love_method, "noise_mode": self._noise_mode,
             "noise_floor": float(self._noise_floor),
             "noise_regularization": float(self._noise_regularization),
-            "noise_function": None, "provider_noise_mode_int": None,
-            "has_observation_noise_train": False, "has_observation_noise_fn": False,
-            "has_noise_group_train": False, "has_group_noise": False,
+            "noise_function": None,
+            "provider_noise_mode_int": 1 if self._observation_noise_train is not None else None,
+            "has_observation_noise_train": self._observation_noise_train is not None,
+            "has_observation_noise_fn": self._observation_noise_fn is not None,
+            "has_noise_group_train": self._noise_group_train is not None,
+            "has_group_noise": self._noise_group_values is not None,
             "result_type": "TrainingResult", "noise": float(tr.noise), "mean": float(tr.mean),
             "nll": float(tr.nll), "iterations": int(tr.iterations),
             "converged": bool(tr.converged), "lanczos_rank": int(tr.lanczos_rank),
         }
         Path(path + "_config.json").write_text(json.dumps(cfg, indent=2, default=float))
-        np.savez(path + "_arrays.npz", X_train=self._X_train, y_train=self._y_train,
-                 params=np.asarray(tr.params, np.float32))
+        arrays = {"X_train": self._X_train, "y_train": self._y_train,
+                  "params": np.asarray(tr.params, np.float32)}
+        if self._observation_noise_train is not None:
+            arrays["observation_noise_train"] = self._observation_noise_train
+        if self._noise_group_train is not None:
+            arrays["noise_group_train"] = self._noise_group_train
+        if self._noise_group_values is not None:
+            arrays["group_noise"] = self._noise_group_values
+        np.savez(path + "_arrays.npz", **arrays)
 
     @classmethod
     def load(cls, path, kernel: Optional[KernelNode] = None) -> "SingleOutputGP":
@@ -728,11 +894,13 @@ class SingleOutputGP:
         if cfg.get("is_mixed") or cfg.get("result_type", "TrainingResult") != "TrainingResult":
             raise NotImplementedError("mixed continuous/categorical models are outside the "
                                       "gfx950 engine")
-        if cfg.get("noise_mode", "scalar") != "scalar" or any(
-                cfg.get(k) for k in ("has_observation_noise_train", "has_observation_noise_fn",
-                                     "has_noise_group_train", "has_group_noise")):
-            raise NotImplementedError("only scalar learned noise is served by the gfx950 engine")
+        mode = cfg.get("noise_mode", "scalar")
+        if mode not in ("scalar", "fixed_vector", "fixed_input_dependent", "fixed_grouped"):
+            raise NotImplementedError(f"noise_mode {mode!r} (learned per-sample noise) is not "
+                                      "served by the gfx950 engine")
         arr = np.load(path + "_arrays.npz", allow_pickle=False)
+        if mode != "scalar" and "observation_noise_train" not in arr:
+            raise ValueError("artifact with fixed per-sample noise lacks observation_noise_train")
         if kernel is None:
             if "kernel_tree" not in cfg:
                 raise ValueError("SingleOutputGP artifact is missing required kernel_tree.")
@@ -747,6 +915,14 @@ class SingleOutputGP:
         gp._cached_love_method = cfg.get("cached_love_method")
         gp._noise_floor = float(cfg.get("noise_floor", 1e-6))
         gp._noise_regularization = float(cfg.get("noise_regularization", 0.0))
+        gp._noise_mode = mode
+        if "observation_noise_train" in arr:
+            gp._observation_noise_train = np.ascontiguousarray(arr["observation_noise_train"],
+                                                               np.float32)
+        if "noise_group_train" in arr:
+            gp._noise_group_train = np.ascontiguousarray(arr["noise_group_train"], np.int32)
+        if "group_noise" in arr:
+            gp._noise_group_values = np.ascontiguousarray(arr["group_noise"], np.float32)
         gp._training_result = TrainingResult(
             params=np.asarray(arr["params"], np.float32), noise=float(cfg["noise"]),
             mean=float(cfg.get("mean", 0.0)), nll=float(cfg["nll"]),

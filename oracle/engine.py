@@ -131,20 +131,33 @@ def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32, method: int = 0
 
 
 class Precond:
-    """P = L L^T + noise I with the reference's cached pieces."""
+    """P = L L^T + noise I with the reference's cached pieces; with a noise
+    vector d [n] (noise mode 1), P = L L^T + diag(d), M = I + L^T D^-1 L
+    (pivoted_cholesky.mojo:1209-1240, 1346-1520, 2060-2095)."""
 
-    def __init__(self, L: np.ndarray, noise: float):
+    def __init__(self, L: np.ndarray, noise):
         self.L = L
-        self.noise = float(noise)
         self.rank = L.shape[1]
         M = L.T @ L
+        self.vec = np.ndim(noise) > 0
+        if self.vec:
+            self.d = np.asarray(noise, np.float64)
+            self.noise = 1e-6
+            Mv = np.eye(self.rank) + L.T @ (L / self.d[:, None])
+            self.Minv = np.linalg.inv(Mv)
+            self.logdet = float(np.sum(np.log(self.d)) + np.linalg.slogdet(Mv)[1])
+            return
+        self.noise = float(noise)
         eff = max(self.noise, 1e-6)
         self.Minv = np.linalg.inv(M + eff * np.eye(self.rank))
         _, ld = np.linalg.slogdet(np.eye(self.rank) + M / self.noise)
         self.logdet = L.shape[0] * np.log(self.noise) + ld
 
     def apply(self, V: np.ndarray) -> np.ndarray:
-        """(V - L Minv L^T V) / noise for V [n, C]."""
+        """(V - L Minv L^T V) / noise for V [n, C] (vector: D^-1 (V - L Minv L^T D^-1 V))."""
+        if self.vec:
+            W = V / self.d[:, None]
+            return (V - self.L @ (self.Minv @ (self.L.T @ W))) / self.d[:, None]
         return (V - self.L @ (self.Minv @ (self.L.T @ V))) / self.noise
 
     def sample(self, T: int, seed: int) -> np.ndarray:
@@ -152,7 +165,9 @@ class Precond:
         n = self.L.shape[0]
         zr = gaussian(self.rank * T, seed).astype(np.float64).reshape(T, self.rank)
         zn = gaussian(n * T, seed + 1000000).astype(np.float64).reshape(T, n)
-        return (zr @ self.L.T + np.sqrt(np.float32(self.noise)) * zn).T
+        s = (np.sqrt(self.d.astype(np.float32)).astype(np.float64) if self.vec
+             else np.sqrt(np.float32(self.noise)))
+        return (zr @ self.L.T + s * zn).T
 
 
 # ---------------------------------------------------------------- CG
@@ -236,12 +251,14 @@ def slq_logdet(diags, offs, n: int) -> float:
 # ---------------------------------------------------------------- BBMM
 def bbmm_step(kind: int, ard: bool, X, y_c, params, noise: float, P: Precond | None,
               num_probes: int, max_cg: int, max_tridiag: int, tol: float, iteration: int,
-              x_warm: np.ndarray | None = None):
-    """NLL, gradients [P+1] and the CG solution of one BBMM evaluation."""
+              x_warm: np.ndarray | None = None, noise_vec=None):
+    """NLL, gradients [P+1] and the CG solution of one BBMM evaluation
+    (noise_vec [n]: K + diag(noise_vec), the scalar noise ignored)."""
     X = np.asarray(X, np.float64)
     n = X.shape[0]
     K = ok.kernel_matrix(kind, X, X, params, ard)
-    A = K + noise * np.eye(n)
+    A = K + (np.diag(np.asarray(noise_vec, np.float64)) if noise_vec is not None
+             else noise * np.eye(n))
     T = num_probes
     seed = iteration * 104729 + 42
     if P is not None:
@@ -316,9 +333,12 @@ def _clip(g, m=100.0):
 
 def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_iterations=50,
           learning_rate=0.01, num_probes=10, max_cg=100, cg_tol=1e-2, precond_rank=0,
-          max_tridiag=30, rebuild_threshold=0.5, init_mean=None):
+          max_tridiag=30, rebuild_threshold=0.5, init_mean=None, noise_vec=None):
     """Adam over raw (inverse-softplus) hyperparameters and the constant mean,
-    with preconditioner rebuilds, NaN recovery and best-NLL restore."""
+    with preconditioner rebuilds, NaN recovery and best-NLL restore.  With a
+    fixed noise vector the noise is not learned (jit_training.mojo:524, 717,
+    947: operator noise 0 + the vector, noise slot frozen, reported noise 0)."""
+    fixed = noise_vec is not None
     X = np.asarray(X, np.float64)
     y = np.asarray(y, np.float64)
     n = X.shape[0]
@@ -339,7 +359,7 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             return None
         K = ok.kernel_matrix(kind, X, X, params, ard)
         L, _ = pivoted_cholesky(K, precond_rank)
-        return Precond(L, noise)
+        return Precond(L, np.asarray(noise_vec, np.float64) if fixed else noise)
 
     P = build(np.asarray(init_params, np.float64), init_noise)
     last_params, last_noise = np.asarray(init_params, F32).copy(), F32(init_noise)
@@ -347,10 +367,12 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
     nll_hist, cg_hist = [], []
     for it in range(max_iterations):
         params = np.array([_softplus(r) for r in raw[:Pn]], F32)
-        noise = _softplus(raw[Pn])
+        noise = F32(0.0) if fixed else _softplus(raw[Pn])
         if it > 0:
             rel = np.abs(params - last_params) / np.maximum(np.abs(last_params), 1e-8)
-            rel = max(float(rel.max()), abs(noise - last_noise) / max(abs(last_noise), 1e-8))
+            rel = float(rel.max())
+            if not fixed:
+                rel = max(rel, abs(noise - last_noise) / max(abs(last_noise), 1e-8))
             if rel > rebuild_threshold:
                 P = build(params, noise)
                 last_params, last_noise = params.copy(), noise
@@ -360,7 +382,7 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             warm = x_prev.copy()
             warm[:, 1:] = 0.0
         res = bbmm_step(kind, ard, X, y_c, params.astype(np.float64), float(noise), P, num_probes,
-                        max_cg, max_tridiag, cg_tol, it, warm)
+                        max_cg, max_tridiag, cg_tol, it, warm, noise_vec=noise_vec)
         x_prev = res["x"]
         nll = res["nll"]
         cg_hist.append(res["cg_iterations"])
@@ -377,6 +399,8 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             best.update(nll=nll, raw=raw.copy(), mean=raw_mean, m=m.copy(), v=v.copy(), mm=mm,
                         vm=vm, t=t, alpha=res["alpha"].copy())
         g = res["grads"].astype(F32)
+        if fixed:
+            g[Pn] = F32(0.0)
         for q in range(Pn + 1):
             gr = _clip(g[q]) * _softplus_deriv(raw[q])
             m[q] = F32(0.9) * m[q] + F32(0.1) * gr
@@ -395,7 +419,7 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             raw_mean = F32(init_mean)
         nll_hist.append(nll)
     params = np.array([_softplus(r) for r in best["raw"][:Pn]], F32)
-    return {"params": params, "noise": float(_softplus(best["raw"][Pn])),
+    return {"params": params, "noise": 0.0 if fixed else float(_softplus(best["raw"][Pn])),
             "mean": float(best["mean"]), "final_nll": float(best["nll"]),
             "alpha": best["alpha"], "nll_history": np.array(nll_hist),
             "cg_iterations_history": np.array(cg_hist)}
@@ -481,11 +505,14 @@ def lanczos_inv_root(A: np.ndarray, r: int) -> np.ndarray:
 
 
 def predict(kind: int, ard: bool, X, y, Xs, params, noise: float, mean: float, *,
-            max_cg=300, tol=1e-3, lanczos_rank=100):
-    """Mean and LOVE variance as the reference computes them."""
+            max_cg=300, tol=1e-3, lanczos_rank=100, noise_vec=None):
+    """Mean and LOVE variance as the reference computes them (noise_vec [n]:
+    K + diag(noise_vec) in place of the scalar noise)."""
     X = np.asarray(X, np.float64)
     n = X.shape[0]
-    A = ok.kernel_matrix(kind, X, X, params, ard) + noise * np.eye(n)
+    A = ok.kernel_matrix(kind, X, X, params, ard) + (
+        np.diag(np.asarray(noise_vec, np.float64)) if noise_vec is not None
+        else noise * np.eye(n))
     alpha = solve_alpha(A, np.asarray(y, np.float64) - mean, max_cg, tol)
     Ks = ok.kernel_matrix(kind, Xs, X, params, ard)
     mu = Ks @ alpha + mean
@@ -496,19 +523,22 @@ def predict(kind: int, ard: bool, X, y, Xs, params, noise: float, mean: float, *
 
 
 def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=300,
-                   tol=1e-3, precond_rank=10, block_cols=0, materialized=False):
+                   tol=1e-3, precond_rank=10, block_cols=0, materialized=False, noise_vec=None):
     """Exact predictive variance as the reference computes it
     (jit_prediction.mojo:1357-1789): test columns in blocks (512 on the
     matrix-free route, all when materialized, or block_cols), right-hand sides
     K(X, x*_block) normalised per column, mBCG without tridiagonal under a
     Nystrom pivoted-Cholesky preconditioner (method 2, error_tol 1e-3,
     adaptive_tol 0.01, seed 42), then var = k** - <K_cross, solve> clamped at
-    1e-10.  Returns (var, realised preconditioner rank, CG iterations per block)."""
+    1e-10.  Returns (var, realised preconditioner rank, CG iterations per block).
+    With noise_vec [n] the operator is K + diag(noise_vec) and the Nystrom stop
+    sees the provider's 1e-6 noise floor (fn_ptr_module.py:673-679)."""
     X = np.asarray(X, np.float64)
     Xs = np.asarray(Xs, np.float64)
     n, m = X.shape[0], Xs.shape[0]
     K = ok.kernel_matrix(kind, X, X, params, ard)
-    A = K + noise * np.eye(n)
+    vec = noise_vec is not None
+    A = K + (np.diag(np.asarray(noise_vec, np.float64)) if vec else noise * np.eye(n))
     os_ = float(np.asarray(params)[-1])
     if block_cols > 0:
         block = min(block_cols, m)
@@ -520,8 +550,9 @@ def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=
     rank = 0
     if precond_rank > 0:
         L, rank = pivoted_cholesky(K, precond_rank, method=2, error_tol=1e-3,
-                                   adaptive_tol=0.01, seed=42, noise=noise, diag_value=os_)
-        P = Precond(L, noise)
+                                   adaptive_tol=0.01, seed=42, noise=1e-6 if vec else noise,
+                                   diag_value=os_)
+        P = Precond(L, np.asarray(noise_vec, np.float64) if vec else noise)
     var = np.empty(m)
     iters = []
     for s0 in range(0, m, block):

@@ -311,3 +311,44 @@ def test_exact_variance_matches_dense_formula():
                                   precond_rank=60)
     assert it1[0] < it0[0]
 
+
+
+def test_precond_noise_vector_woodbury_logdet_and_probes():
+    """P = L L^T + diag(d): apply == solve(P, .), log|P| == slogdet(P), and the
+    probes L z_rank + sqrt(d) z_noise have covariance P (noise mode 1)."""
+    rng = np.random.default_rng(21)
+    n, r = 40, 6
+    L = rng.normal(size=(n, r)) * 0.5
+    d = rng.uniform(0.05, 0.4, size=n)
+    P = oe.Precond(L, d)
+    Pd = L @ L.T + np.diag(d)
+    V = rng.normal(size=(n, 3))
+    np.testing.assert_allclose(P.apply(V), np.linalg.solve(Pd, V), rtol=1e-9, atol=1e-12)
+    assert P.logdet == pytest.approx(np.linalg.slogdet(Pd)[1], rel=1e-12)
+    Z = P.sample(40000, 3)
+    cov = Z @ Z.T / Z.shape[1]
+    scale = np.sqrt(np.outer(np.diag(Pd), np.diag(Pd)))
+    assert np.max(np.abs(cov - Pd) / scale) < 0.03
+
+
+def test_bbmm_noise_vector_reaches_exact_nll():
+    """With a fixed noise vector the BBMM NLL and kernel gradients converge to
+    the exact values of K + diag(d) (many probes, tight CG)."""
+    rng = np.random.default_rng(22)
+    n = 30
+    X = rng.uniform(-1, 1, size=(n, 2))
+    y = np.sin(2 * X[:, 0]) + 0.1 * rng.normal(size=n)
+    params = np.array([0.7, 1.2])
+    d = rng.uniform(0.05, 0.3, size=n)
+    r = oe.bbmm_step(ok.MATERN52, False, X, y, params, 123.0, None, 3000, 200, 60, 1e-10, 0,
+                     noise_vec=d)
+    A = ok.kernel_matrix(ok.MATERN52, X, X, params, False) + np.diag(d)
+    al = np.linalg.solve(A, y)
+    exact = (0.5 * y @ al + 0.5 * np.linalg.slogdet(A)[1] + 0.5 * n * np.log(2 * np.pi)) / n
+    assert r["inv_quad"] == pytest.approx(y @ al, rel=1e-8)
+    assert r["nll"] == pytest.approx(exact, rel=0.02)
+    G = ok.kernel_gradients(ok.MATERN52, X, X, params, False)
+    Ainv = np.linalg.inv(A)
+    for q, g in enumerate(G):
+        ex = (-0.5 * al @ g @ al + 0.5 * np.trace(Ainv @ g)) / n
+        assert r["grads"][q] == pytest.approx(ex, abs=0.05 * abs(ex) + 2e-3)
