@@ -54,6 +54,23 @@ MGP_API int mgp_device_count(int* out);
 MGP_API int mgp_init_provider(int kind, int ard, int d, int64_t n,
                               const float* X, const float* params, int nparams,
                               float noise, void** out_handle);
+/* Provider for a composite kernel tree: sums, products and scales of RBF,
+ * Matern-1/2, 3/2, 5/2, RQ and periodic leaves, each leaf on a subset of the
+ * input dimensions.  spec[spec_len] = [d, nparams, nleaves, nnodes,
+ *   per leaf (tree order): code (0 RBF, 1 M52, 2 M12, 3 M32, 4 RQ,
+ *   5 periodic), ard, ndim, p0, dims[ndim],
+ *   per node (children first, root last): code (0 leaf: a = leaf index;
+ *   1 sum / 2 product: a, b = child nodes; 3 scale: a = child node,
+ *   b = index of the scale factor in params), a, b].
+ * Leaf parameters start at p0: [ls | ls_0..ls_{q-1}], (alpha | period), os.
+ * At most 8 leaves, 16 nodes, 48 parameters, d <= 32, 64 leaf dimensions.
+ * Replaces init_provider of a generated composite module (the kernel
+ * expression tree of codegen_engine/expressions.py:474-648 compiled per
+ * tree, parameter layout mojogp/kernel.py:528-568).  The provider reports
+ * kind -1; products are evaluated per pair from raw inputs (VALU). */
+MGP_API int mgp_init_provider_tree(const int* spec, int spec_len, int d, int64_t n,
+                                   const float* X, const float* params, int nparams,
+                                   float noise, void** out_handle);
 /* Replaces destroy_provider(info) (fn_ptr_module.py:1183-1195). */
 MGP_API int mgp_destroy_provider(void* handle);
 

@@ -7,13 +7,15 @@ C-ABI library libmojogp_amd.so (ctypes).  No torch in the product path.
 """
 
 from .gp import PredictionResult, SingleOutputGP, TrainingResult
-from .kernel import KernelNode, KernelType, Matern12, Matern32, Matern52, RBF, make_ard_kernel
+from .kernel import (RQ, KernelNode, KernelType, Linear, Matern12, Matern32, Matern52, Periodic,
+                     Polynomial, RBF, make_ard_kernel)
 from .multi_output_gp import (LMCTrainingResult, MultiOutputGP, MultiOutputLMCGP,
                               MultiOutputPredictionResult, MultiOutputTrainingResult)
 
 __version__ = "0.1.0"
 
 __all__ = ["SingleOutputGP", "TrainingResult", "PredictionResult", "KernelNode", "KernelType",
-           "RBF", "Matern52", "Matern32", "Matern12", "make_ard_kernel", "MultiOutputLMCGP",
+           "RBF", "Matern52", "Matern32", "Matern12", "RQ", "Periodic", "Linear", "Polynomial",
+           "make_ard_kernel", "MultiOutputLMCGP",
            "LMCTrainingResult", "MultiOutputPredictionResult", "MultiOutputGP",
            "MultiOutputTrainingResult"]

@@ -18,7 +18,7 @@ from typing import Any
 import numpy as np
 
 from . import _lib
-from ._provider import NativeProvider, kind_code
+from ._provider import TREE_KIND, NativeProvider, kind_code
 
 _DEFAULT_PREDICT_LANCZOS_RANK = 100
 _DEFAULT_ARD_PREDICT_LANCZOS_RANK = 200
@@ -37,11 +37,13 @@ def _exact_keys(inf, vm: int) -> dict[str, Any]:
 
 
 class KernelModule:
-    """Kernel module for one (kernel family, ARD, input dimension)."""
+    """Kernel module for one (kernel family, ARD, input dimension), or for one
+    composite kernel tree (``tree_spec``, ``KernelNode.to_tree_spec``)."""
 
-    def __init__(self, kind, ard: bool, dim: int):
-        self.kind = kind_code(kind)
-        self.ard = bool(ard)
+    def __init__(self, kind, ard: bool, dim: int, tree_spec=None):
+        self.tree_spec = None if tree_spec is None else [int(v) for v in tree_spec]
+        self.kind = TREE_KIND if tree_spec is not None else kind_code(kind)
+        self.ard = bool(ard) and tree_spec is None
         self.dim = int(dim)
 
     def init_provider(self, X, params, noise, observation_noise=None, noise_mode=None,
@@ -60,7 +62,7 @@ class KernelModule:
         X = _lib.f32(X)
         if X.ndim != 2 or X.shape[1] != self.dim:
             raise ValueError(f"X must have shape (n, {self.dim})")
-        prov = NativeProvider(self.kind, self.ard, X, params, noise)
+        prov = NativeProvider(self.kind, self.ard, X, params, noise, tree_spec=self.tree_spec)
         if mode == 1:
             try:
                 prov.set_noise_vector(observation_noise)
@@ -734,6 +736,14 @@ def load_engine() -> Engine:
 
 
 def load_kernel_module(kind, ard: bool, dim: int) -> KernelModule:
-    """Counterpart of mojogp.loader.load_kernel_module_engine (loader.py:331-429)."""
+    """Counterpart of mojogp.loader.load_kernel_module_engine (loader.py:331-429).
+
+    ``kind``: a kind code / name, or a (resolved) KernelNode; nodes other than a
+    single RBF / Matern leaf on all inputs get the kernel-tree products."""
     _lib.load()
+    from .kernel import KernelNode
+    if isinstance(kind, KernelNode):
+        if kind.is_native_leaf():
+            return KernelModule(kind.native_kind(), kind.ard_dim is not None, dim)
+        return KernelModule(None, False, dim, tree_spec=kind.to_tree_spec(dim))
     return KernelModule(kind, ard, dim)

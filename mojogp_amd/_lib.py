@@ -153,6 +153,8 @@ _SIGNATURES = {
     "mgp_device_count": (C.c_int, [c_int_p]),
     "mgp_init_provider": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int64, c_float_p,
                                     c_float_p, C.c_int, C.c_float, c_void_pp]),
+    "mgp_init_provider_tree": (C.c_int, [C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int64,
+                                         c_float_p, c_float_p, C.c_int, C.c_float, c_void_pp]),
     "mgp_destroy_provider": (C.c_int, [C.c_void_p]),
     "mgp_materialize": (C.c_int, [C.c_void_p]),
     "mgp_update_params": (C.c_int, [C.c_void_p, c_float_p, C.c_int]),

@@ -16,6 +16,10 @@ _KIND_NAMES = {"rbf": KIND_RBF, "matern52": KIND_MATERN52, "matern12": KIND_MATE
                "matern32": KIND_MATERN32}
 
 
+# Provider kind reported for composite kernel trees.
+TREE_KIND = -1
+
+
 def kind_code(kind) -> int:
     if isinstance(kind, str):
         try:
@@ -40,19 +44,30 @@ def _cols(V: np.ndarray, n: int) -> tuple[np.ndarray, bool]:
 class NativeProvider:
     """Owns one ``mgp_init_provider`` handle (training inputs live in HBM)."""
 
-    def __init__(self, kind, ard: bool, X: np.ndarray, params: np.ndarray, noise: float):
+    def __init__(self, kind, ard: bool, X: np.ndarray, params: np.ndarray, noise: float,
+                 tree_spec=None):
+        """``tree_spec``: flat kernel-tree spec (``KernelNode.to_tree_spec``);
+        ``kind`` and ``ard`` are then ignored."""
         X = _lib.f32(X)
         if X.ndim != 2:
             raise ValueError("X must be 2-D")
         params = _lib.f32(params).ravel()
-        self.kind = kind_code(kind)
-        self.ard = bool(ard)
         self.n, self.d = X.shape
         self.nparams = params.shape[0]
         h = C.c_void_p()
-        _lib.call("mgp_init_provider", self.kind, int(self.ard), self.d, self.n,
-                  _lib.fptr(X), _lib.fptr(params), self.nparams, float(noise),
-                  C.byref(h))
+        if tree_spec is not None:
+            spec = np.ascontiguousarray(np.asarray(tree_spec, dtype=np.int32).ravel())
+            self.kind, self.ard, self.tree_spec = TREE_KIND, False, spec
+            _lib.call("mgp_init_provider_tree", spec.ctypes.data_as(C.POINTER(C.c_int)),
+                      int(spec.size), self.d, self.n, _lib.fptr(X), _lib.fptr(params),
+                      self.nparams, float(noise), C.byref(h))
+        else:
+            self.kind = kind_code(kind)
+            self.ard = bool(ard)
+            self.tree_spec = None
+            _lib.call("mgp_init_provider", self.kind, int(self.ard), self.d, self.n,
+                      _lib.fptr(X), _lib.fptr(params), self.nparams, float(noise),
+                      C.byref(h))
         self._h = h
         self.params = params.copy()
         self.noise = float(noise)

@@ -181,7 +181,7 @@ int mgp_lmc_predict(void* const* providers, int R, int T, const float* A, const 
           DevBuf<float> V;
           V.ensure((size_t)ps.rank * mtest);
           pv.cross(pv.test, ps.root.ptr, ps.rank, V.ptr);
-          love_variance(V.ptr, mtest, ps.rank, pv.outputscale(), vs.ptr, m.st);
+          love_variance(V.ptr, mtest, ps.rank, pv.kdiag(), vs.ptr, m.st);
         } else {
           ExactVarianceOptions eo;
           eo.max_cg_iter = max_cg_iter;

@@ -53,6 +53,36 @@ int mgp_device_count(int* out) {
   });
 }
 
+namespace {
+// Shared tail of provider creation: parameters, stream, device inputs and the
+// first packing.  Owns pv (deleted on failure).
+Provider* finish_provider(Provider* pv, int d, int64_t n, const float* X, const float* params,
+                          int nparams, float noise) {
+  try {
+    pv->d = d;
+    pv->n = n;
+    pv->nparams = nparams;
+    pv->params.assign(params, params + nparams);
+    pv->noise = noise;
+    pv->center.assign(d, 0.0);
+    for (int64_t i = 0; i < n; ++i)
+      for (int k = 0; k < d; ++k) pv->center[k] += (double)X[i * d + k];
+    for (int k = 0; k < d; ++k) pv->center[k] /= (double)n;
+    MGP_HIP_CHECK(hipStreamCreateWithFlags(&pv->st, hipStreamNonBlocking));
+    pv->X.ensure((size_t)n * d);
+    MGP_HIP_CHECK(hipMemcpyAsync(pv->X.ptr, X, (size_t)n * d * sizeof(float),
+                                 hipMemcpyHostToDevice, pv->st));
+    pv->refresh_coords();
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  } catch (...) {
+    if (pv->st) (void)hipStreamDestroy(pv->st);
+    delete pv;
+    throw;
+  }
+  return pv;
+}
+}  // namespace
+
 int mgp_init_provider(int kind, int ard, int d, int64_t n, const float* X,
                       const float* params, int nparams, float noise,
                       void** out_handle) {
@@ -73,30 +103,34 @@ int mgp_init_provider(int kind, int ard, int d, int64_t n, const float* X,
       MGP_REQUIRE(std::isfinite(params[p]) && params[p] > 0.f,
                   "kernel parameters must be finite and > 0");
     auto* pv = new Provider();
-    try {
-      pv->kind = kind;
-      pv->ard = ard != 0;
-      pv->d = d;
-      pv->n = n;
-      pv->nparams = nparams;
-      pv->params.assign(params, params + nparams);
-      pv->noise = noise;
-      pv->center.assign(d, 0.0);
-      for (int64_t i = 0; i < n; ++i)
-        for (int k = 0; k < d; ++k) pv->center[k] += (double)X[i * d + k];
-      for (int k = 0; k < d; ++k) pv->center[k] /= (double)n;
-      MGP_HIP_CHECK(hipStreamCreateWithFlags(&pv->st, hipStreamNonBlocking));
-      pv->X.ensure((size_t)n * d);
-      MGP_HIP_CHECK(hipMemcpyAsync(pv->X.ptr, X, (size_t)n * d * sizeof(float),
-                                   hipMemcpyHostToDevice, pv->st));
-      pv->refresh_coords();
-      MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
-    } catch (...) {
-      if (pv->st) (void)hipStreamDestroy(pv->st);
-      delete pv;
-      throw;
-    }
-    *out_handle = pv;
+    pv->kind = kind;
+    pv->ard = ard != 0;
+    *out_handle = finish_provider(pv, d, n, X, params, nparams, noise);
+  });
+}
+
+int mgp_init_provider_tree(const int* spec, int spec_len, int d, int64_t n, const float* X,
+                           const float* params, int nparams, float noise, void** out_handle) {
+  return guarded([&] {
+    MGP_REQUIRE(out_handle != nullptr, "out_handle is null");
+    *out_handle = nullptr;
+    const KernelTree t = parse_kernel_tree(spec, spec_len);
+    MGP_REQUIRE(t.d == d, "kernel tree spec was built for another input dimension");
+    MGP_REQUIRE(t.nparams == nparams,
+                "params has " + std::to_string(nparams) + " values, the kernel tree expects " +
+                    std::to_string(t.nparams));
+    MGP_REQUIRE(n >= 1, "n must be >= 1");
+    MGP_REQUIRE(X != nullptr && params != nullptr, "null input array");
+    MGP_REQUIRE(std::isfinite(noise) && noise >= 0.f, "noise must be finite and >= 0");
+    for (int p = 0; p < nparams; ++p)
+      MGP_REQUIRE(std::isfinite(params[p]) && params[p] > 0.f,
+                  "kernel parameters must be finite and > 0");
+    auto* pv = new Provider();
+    pv->kind = KIND_TREE;
+    pv->ard = false;
+    pv->is_tree = true;
+    pv->tree = t;
+    *out_handle = finish_provider(pv, d, n, X, params, nparams, noise);
   });
 }
 
@@ -148,7 +182,7 @@ int mgp_get_noise(void* h, float* out) {
 }
 
 int mgp_get_diagonal_value(void* h, float* out) {
-  return guarded([&] { *out = as_provider(h)->outputscale(); });
+  return guarded([&] { *out = as_provider(h)->kdiag(); });
 }
 
 int mgp_provider_info(void* h, int64_t* n, int* d, int* nparams, int* kind,
@@ -197,6 +231,7 @@ int mgp_direct_matvec(void* h, const float* V, int ncols, float* out) {
     float* dv = pv->io_a.ensure(tot);
     float* dout = pv->io_b.ensure(tot);
     MGP_HIP_CHECK(hipMemcpyAsync(dv, V, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    MGP_REQUIRE(!pv->is_tree, "the direct radial matvec does not serve kernel trees");
     MatvecArgs a;
     a.kind = pv->kind;
     a.outputscale = pv->outputscale();
@@ -242,7 +277,7 @@ int mgp_set_noise_vector(void* h, const float* noise_vec) {
 int mgp_extract_diagonal(void* h, float* out) {
   return guarded([&] {
     Provider* pv = as_provider(h);
-    const float os = pv->outputscale();
+    const float os = pv->kdiag();
     for (int64_t i = 0; i < pv->n; ++i) out[i] = os;
   });
 }
@@ -251,7 +286,7 @@ int mgp_extract_diagonal_test(void* h, const float* Xs, int64_t m, float* out) {
   return guarded([&] {
     Provider* pv = as_provider(h);
     (void)Xs;
-    const float os = pv->outputscale();
+    const float os = pv->kdiag();
     for (int64_t i = 0; i < m; ++i) out[i] = os;
   });
 }

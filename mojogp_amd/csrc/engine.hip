@@ -995,12 +995,12 @@ void exact_variance(Provider& pv, int64_t m, const ExactVarianceOptions& o, floa
   DevBuf<float> Kc, norms, rhsb;
   DevBuf<double> part, dots;
   CGWork w;
-  const float os = pv.outputscale();
+  const float os = pv.kdiag();
   for (int64_t s0 = 0; s0 < m; s0 += block) {
     const int C = (int)std::min<int64_t>(block, m - s0);
     const size_t nc = (size_t)n * C;
     float* kc = Kc.ensure(nc);
-    fill_cross(pv.kind, os, pv.test, s0, C, pv.train, pv.d, kc, st);
+    pv.fill_block(pv.test, s0, C, kc);
     // RHS = normalised cross columns; solve; rescale (solve_exact_cross_block_jit)
     float* rhs = rhsb.ensure(nc);
     copy(rhs, kc, (int64_t)nc, st);
@@ -1049,7 +1049,7 @@ void predict_from_state(Provider& pv, const PredictState& ps, const float* Xs_ho
     Vs.ensure((size_t)ps.rank * m);
     var.ensure(m);
     pv.cross(pv.test, ps.root.ptr, ps.rank, Vs.ptr);
-    love_variance(Vs.ptr, m, ps.rank, pv.outputscale(), var.ptr, st);
+    love_variance(Vs.ptr, m, ps.rank, pv.kdiag(), var.ptr, st);
     MGP_HIP_CHECK(hipMemcpyAsync(var_out, var.ptr, m * sizeof(float), hipMemcpyDeviceToHost, st));
     MGP_HIP_CHECK(hipStreamSynchronize(st));
     t.variance_s = secs_since(t1);

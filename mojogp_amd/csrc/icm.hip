@@ -365,7 +365,7 @@ void icm_predict(Provider& pv, int T, const float* alpha_rot, const float* Q,
         DevBuf<float> V;
         V.ensure((size_t)ps.rank * m);
         pv.cross(pv.test, ps.root.ptr, ps.rank, V.ptr);
-        love_variance(V.ptr, m, ps.rank, pv.outputscale(), vs.ptr, st);
+        love_variance(V.ptr, m, ps.rank, pv.kdiag(), vs.ptr, st);
       } else {
         ExactVarianceOptions eo;
         eo.max_cg_iter = max_cg_iter;

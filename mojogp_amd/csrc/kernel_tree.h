@@ -1,0 +1,230 @@
+// Composite kernel trees (sums, products and scales of stationary leaves,
+// each leaf on its own subset of the input dimensions) evaluated per pair
+// from raw coordinate differences.
+//
+// Reference semantics (caspbian/mojogp):
+//   leaf expressions      codegen_engine/expressions.py:77-380 (RBF, Matern
+//                         1/2, 3/2, 5/2, periodic, RQ)
+//   guards                codegen_engine/passes/numerical_stability.py:29-70
+//                         (exp(max(x, -20)) for negative arguments,
+//                         sqrt(max(x, 1e-20)))
+//   engine param layout   mojogp/kernel.py:462-640 (leaves in tree order,
+//                         a scale's factor after its subtree)
+//
+// A leaf's parameters start at p0:
+//   RBF / Matern     [ls | ls_0..ls_{q-1}], os
+//   RQ               [ls | ls_0..ls_{q-1}], alpha, os
+//   periodic         [ls | ls_0..ls_{q-1}], period, os
+// Nodes are listed children first; the last node is the root.
+#pragma once
+
+#include "mgp_common.h"
+
+namespace mgp {
+
+constexpr int kTreeMaxLeaves = 8;
+constexpr int kTreeMaxNodes = 16;
+constexpr int kTreeMaxDims = 64;    // sum over leaves of their dimension counts
+constexpr int kTreeMaxParams = 48;
+constexpr int kTreeMaxInputDim = 32;
+
+// Leaf families beyond the radial kinds of mgp_common.h.
+constexpr int KIND_RQ = 4;
+constexpr int KIND_PERIODIC = 5;
+// Provider kind reported for composite kernel trees.
+constexpr int KIND_TREE = -1;
+
+enum TreeCode : int { TN_LEAF = 0, TN_ADD = 1, TN_MUL = 2, TN_SCALE = 3 };
+
+struct TreeLeaf {
+  int kind, ard, ndim, dim_off, p0;
+};
+// LEAF: a = leaf index; ADD / MUL: a, b = child nodes; SCALE: a = child node,
+// b = index of the scale factor in the parameter vector.
+struct TreeNode {
+  int code, a, b;
+};
+
+struct KernelTree {
+  int d = 0, nparams = 0, nleaves = 0, nnodes = 0;
+  TreeLeaf leaf[kTreeMaxLeaves];
+  TreeNode node[kTreeMaxNodes];
+  int dims[kTreeMaxDims];
+};
+
+// Flat spec (the C ABI's form): [d, nparams, nleaves, nnodes,
+//   per leaf: kind, ard, ndim, p0, dims[ndim] ...,
+//   per node: code, a, b ...].  Throws on malformed specs.
+KernelTree parse_kernel_tree(const int* spec, int len);
+// k(x, x) at the given parameters (all leaves are stationary).
+double tree_diag(const KernelTree& t, const float* params);
+
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
+constexpr float kTreePi = 3.14159265358979323846f;
+
+// Leaf value and the pair quantities its gradient needs.
+struct LeafEval {
+  float k;   // leaf value (os included)
+  float r2;  // scaled squared distance (radial / RQ) or the periodic sum
+  float h;   // radial / RQ: dk/dl_q = h dx_q^2 / l_q^3; periodic: k (see below)
+};
+
+__device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
+                                                   const float* __restrict__ p,
+                                                   const float* xi, const float* xj) {
+  const TreeLeaf& lf = t.leaf[l];
+  LeafEval e;
+  if (lf.kind == KIND_PERIODIC) {
+    const float period = p[lf.p0 + (lf.ard ? lf.ndim : 1)];
+    const float os = p[lf.p0 + (lf.ard ? lf.ndim : 1) + 1];
+    float s = 0.0f;
+    for (int q = 0; q < lf.ndim; ++q) {
+      const int dq = t.dims[lf.dim_off + q];
+      const float sn = sinf(kTreePi * (xi[dq] - xj[dq]) / period);
+      s += lf.ard ? sn * sn / p[lf.p0 + q] : sn * sn;
+    }
+    if (!lf.ard) s /= p[lf.p0];
+    e.r2 = s;
+    e.k = os * expf(fmaxf(-2.0f * s, -20.0f));
+    e.h = e.k;
+    return e;
+  }
+  const int nls = lf.ard ? lf.ndim : 1;
+  float r2 = 0.0f;
+  for (int q = 0; q < lf.ndim; ++q) {
+    const int dq = t.dims[lf.dim_off + q];
+    const float u = (xi[dq] - xj[dq]) / p[lf.p0 + (lf.ard ? q : 0)];
+    r2 = fmaf(u, u, r2);
+  }
+  e.r2 = r2;
+  if (lf.kind == KIND_RQ) {
+    const float alpha = p[lf.p0 + nls];
+    const float os = p[lf.p0 + nls + 1];
+    const float B = 1.0f + r2 / (2.0f * alpha);
+    const float Bm = powf(B, -alpha);
+    e.k = os * Bm;
+    e.h = os * Bm / B;
+    return e;
+  }
+  const float os = p[lf.p0 + nls];
+  if (lf.kind == KIND_RBF) {
+    e.k = os * expf(fmaxf(-0.5f * r2, -20.0f));
+    e.h = e.k;
+    return e;
+  }
+  const float r = sqrtf(fmaxf(r2 + 1e-20f, 1e-20f));
+  if (lf.kind == KIND_MATERN12) {
+    const float ex = expf(fmaxf(-r, -20.0f));
+    e.k = os * ex;
+    e.h = os * ex / r;
+  } else if (lf.kind == KIND_MATERN32) {
+    const float s3 = 1.7320508075688772f * r;
+    const float ex = expf(fmaxf(-s3, -20.0f));
+    e.k = os * (1.0f + s3) * ex;
+    e.h = 3.0f * os * ex;
+  } else {  // Matern-5/2
+    const float s5 = 2.2360679774997897f * r;
+    const float ex = expf(fmaxf(-s5, -20.0f));
+    e.k = os * (1.0f + s5 + (5.0f / 3.0f) * r * r) * ex;
+    e.h = (5.0f / 3.0f) * os * (1.0f + s5) * ex;
+  }
+  return e;
+}
+
+// Tree value for one pair; node values (and leaf evaluations) optionally kept.
+__device__ __forceinline__ float tree_value(const KernelTree& t, const float* __restrict__ p,
+                                            const float* xi, const float* xj,
+                                            LeafEval* leaves = nullptr,
+                                            float* vals = nullptr) {
+  float v[kTreeMaxNodes];
+  for (int i = 0; i < t.nnodes; ++i) {
+    const TreeNode& nd = t.node[i];
+    float x;
+    if (nd.code == TN_LEAF) {
+      const LeafEval le = tree_leaf_eval(t, nd.a, p, xi, xj);
+      if (leaves) leaves[nd.a] = le;
+      x = le.k;
+    } else if (nd.code == TN_ADD) {
+      x = v[nd.a] + v[nd.b];
+    } else if (nd.code == TN_MUL) {
+      x = v[nd.a] * v[nd.b];
+    } else {
+      x = p[nd.b] * v[nd.a];
+    }
+    v[i] = x;
+    if (vals) vals[i] = x;
+  }
+  return v[t.nnodes - 1];
+}
+
+// dK/dtheta_p for every parameter at one pair, accumulated as g[p] += w dK/dp.
+__device__ __forceinline__ void tree_grad_accumulate(const KernelTree& t,
+                                                     const float* __restrict__ p,
+                                                     const float* xi, const float* xj, float w,
+                                                     float* g) {
+  LeafEval le[kTreeMaxLeaves];
+  float val[kTreeMaxNodes], adj[kTreeMaxNodes];
+  tree_value(t, p, xi, xj, le, val);
+  for (int i = 0; i < t.nnodes; ++i) adj[i] = 0.0f;
+  adj[t.nnodes - 1] = w;
+  for (int i = t.nnodes - 1; i >= 0; --i) {
+    const TreeNode& nd = t.node[i];
+    const float a = adj[i];
+    if (nd.code == TN_ADD) {
+      adj[nd.a] += a;
+      adj[nd.b] += a;
+    } else if (nd.code == TN_MUL) {
+      adj[nd.a] += a * val[nd.b];
+      adj[nd.b] += a * val[nd.a];
+    } else if (nd.code == TN_SCALE) {
+      adj[nd.a] += a * p[nd.b];
+      g[nd.b] += a * val[nd.a];
+    } else {
+      const int l = nd.a;
+      const TreeLeaf& lf = t.leaf[l];
+      const LeafEval& e = le[l];
+      const int nls = lf.ard ? lf.ndim : 1;
+      if (lf.kind == KIND_PERIODIC) {
+        const float period = p[lf.p0 + nls];
+        const int ios = lf.p0 + nls + 1;
+        // k = os exp(-2 S), S = sum_q sin^2(pi dx_q / period) / l_q
+        float dperiod = 0.0f;
+        for (int q = 0; q < lf.ndim; ++q) {
+          const int dq = t.dims[lf.dim_off + q];
+          const float dx = xi[dq] - xj[dq];
+          const float ang = kTreePi * dx / period;
+          const float sn = sinf(ang), cs = cosf(ang);
+          const float lq = p[lf.p0 + (lf.ard ? q : 0)];
+          if (lf.ard) g[lf.p0 + q] += a * e.k * 2.0f * sn * sn / (lq * lq);
+          dperiod += sn * cs * dx / lq;
+        }
+        if (!lf.ard) g[lf.p0] += a * e.k * 2.0f * e.r2 / p[lf.p0];
+        g[lf.p0 + nls] += a * e.k * 4.0f * kTreePi * dperiod / (period * period);
+        g[ios] += a * e.k / p[ios];
+        continue;
+      }
+      // radial / RQ lengthscales: dk/dl_q = h dx_q^2 / l_q^3
+      float iso = 0.0f;
+      for (int q = 0; q < lf.ndim; ++q) {
+        const int dq = t.dims[lf.dim_off + q];
+        const float dx = xi[dq] - xj[dq];
+        const float lq = p[lf.p0 + (lf.ard ? q : 0)];
+        const float term = dx * dx / (lq * lq * lq);
+        if (lf.ard) g[lf.p0 + q] += a * e.h * term;
+        else iso += term;
+      }
+      if (!lf.ard) g[lf.p0] += a * e.h * iso;
+      int ios = lf.p0 + nls;
+      if (lf.kind == KIND_RQ) {
+        const float alpha = p[lf.p0 + nls];
+        const float B = 1.0f + e.r2 / (2.0f * alpha);
+        g[lf.p0 + nls] += a * e.k * (-logf(B) + e.r2 / (2.0f * alpha * B));
+        ios += 1;
+      }
+      g[ios] += a * e.k / p[ios];
+    }
+  }
+}
+#endif
+
+}  // namespace mgp

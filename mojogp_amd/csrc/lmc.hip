@@ -1049,7 +1049,7 @@ int lmc_exact_variance(LMCModel& m, int64_t mtest, int max_cg, float tol, int bl
   std::vector<double> prior(T, 0.0);
   for (int s = 0; s < R; ++s)
     for (int t = 0; t < T; ++t)
-      prior[t] += (double)m.A[((size_t)s * T + t) * T + t] * (double)m.prov[s]->outputscale();
+      prior[t] += (double)m.A[((size_t)s * T + t) * T + t] * (double)m.prov[s]->kdiag();
   CGOperator op;
   op.n = N;
   op.st = st;
@@ -1063,8 +1063,7 @@ int lmc_exact_variance(LMCModel& m, int64_t mtest, int max_cg, float tol, int bl
     Kc.ensure((size_t)R * bn * n);
     for (int s = 0; s < R; ++s) {
       Provider& pv = *m.prov[s];
-      fill_cross(pv.kind, pv.outputscale(), pv.test, b0, bn, pv.train, pv.d,
-                 Kc.ptr + (size_t)s * bn * n, st);
+      pv.fill_block(pv.test, b0, bn, Kc.ptr + (size_t)s * bn * n);
     }
     rhs.ensure((size_t)C * N);
     beta.ensure((size_t)C * N);

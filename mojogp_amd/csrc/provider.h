@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "matvec.h"
+#include "tree.h"
 
 namespace mgp {
 
@@ -25,6 +26,13 @@ struct Provider {
   DevBuf<float> noise_vec;
   bool has_noise_vec = false;
   std::vector<double> center;  // column means of the training inputs
+  // Composite kernel tree (sums / products / scales of stationary leaves on
+  // dimension subsets): products are evaluated per pair from raw inputs; the
+  // packed point sets then hold raw coordinates in z and params live on the
+  // device in tparams (tree parameter layout, nparams entries).
+  bool is_tree = false;
+  KernelTree tree;
+  DevBuf<float> tparams;
 
   hipStream_t st = nullptr;
   DevBuf<float> X;             // raw training inputs [n][d]
@@ -44,6 +52,9 @@ struct Provider {
   void* blas = nullptr;  // rocblas_handle bound to `st` (materialized route)
 
   float outputscale() const { return params[nparams - 1]; }
+  // k(x, x) (every supported kernel is stationary): the outputscale for a
+  // single leaf, the tree evaluated at zero distance for composite kernels.
+  float kdiag() const { return is_tree ? (float)tree_diag(tree, params.data()) : outputscale(); }
   float lengthscale(int k) const { return ard ? params[k] : params[0]; }
 
   // Recompute the coordinate map from params and repack the training points.
@@ -82,6 +93,8 @@ struct Provider {
 
   // K(Xs, X) V for a packed test set.
   void cross(const PackedPoints& rows, const float* V, int ncols, float* out);
+  // out[c*n + i] = k(rows[r0 + c], x_i) for c < nrows (dense cross block).
+  void fill_block(const PackedPoints& rows, int64_t r0, int64_t nrows, float* out);
 };
 
 }  // namespace mgp

@@ -9,6 +9,18 @@
 namespace mgp {
 
 void Provider::refresh_coords() {
+  if (is_tree) {
+    for (int q = 0; q < nparams; ++q)
+      MGP_REQUIRE(std::isfinite(params[q]) && params[q] > 0.f,
+                  "kernel tree parameters must be finite and > 0");
+    tparams.ensure((size_t)nparams);
+    MGP_HIP_CHECK(hipMemcpyAsync(tparams.ptr, params.data(), (size_t)nparams * sizeof(float),
+                                 hipMemcpyHostToDevice, st));
+    pack(X.ptr, n, train);
+    if (materialized) fill_dense();
+    MGP_HIP_CHECK(hipStreamSynchronize(st));  // params may change after return
+    return;
+  }
   std::vector<float> coef(2 * (size_t)d);
   const float base = kernel_scale(kind);
   for (int k = 0; k < d; ++k) {
@@ -36,6 +48,7 @@ void Provider::refresh_coords() {
 }
 
 void Provider::gradient(const float* V, int ncols, float* out) {
+  MGP_REQUIRE(!is_tree, "per-parameter gradient products are not available for kernel trees");
   gradient_matvec(kind, ard, train, d, outputscale(), gscale.ptr, V, ncols, out, st);
 }
 
@@ -77,8 +90,14 @@ void Provider::set_noise_vector(const float* host) {
   has_noise_vec = true;
 }
 
-void Provider::fill_dense() {
-  fill_cross(kind, outputscale(), train, 0, n, train, d, K.ptr, st);
+void Provider::fill_dense() { fill_block(train, 0, n, K.ptr); }
+
+void Provider::fill_block(const PackedPoints& rows, int64_t r0, int64_t nrows, float* out) {
+  if (is_tree) {
+    tree_fill(tree, tparams.ptr, rows.z.ptr, r0, nrows, train.z.ptr, n, out, st);
+    return;
+  }
+  fill_cross(kind, outputscale(), rows, r0, nrows, train, d, out, st);
 }
 
 void Provider::materialize() {
@@ -109,6 +128,17 @@ void Provider::release_blas() {
 }
 
 void Provider::pack(const float* X_dev, int64_t m, PackedPoints& pp) {
+  if (is_tree) {  // raw coordinates only (tree products read them directly)
+    pp.n = m;
+    pp.ntiles = 0;
+    pp.kb = 0;
+    pp.max_norm = 0.f;
+    pp.z.ensure((size_t)std::max<int64_t>(m, 1) * d);
+    if (m > 0)
+      MGP_HIP_CHECK(hipMemcpyAsync(pp.z.ptr, X_dev, (size_t)m * d * sizeof(float),
+                                   hipMemcpyDeviceToDevice, st));
+    return;
+  }
   pack_points(X_dev, m, co, pp, st);
 }
 
@@ -146,6 +176,11 @@ void Provider::forward_scalar(const float* V, int ncols, float* out) {
                                  (rocblas_int)n));
     return;
   }
+  if (is_tree) {
+    tree_matvec(tree, tparams.ptr, train.z.ptr, n, train.z.ptr, n, V, ncols, noise, true, out,
+                st);
+    return;
+  }
   if (!gram_form_ok(kind, train, train)) {
     direct_matvec(a, train, train, d, V, out, st);
     return;
@@ -153,7 +188,9 @@ void Provider::forward_scalar(const float* V, int ncols, float* out) {
   fused_matvec(a, train, train, V, out, ws, st);
 }
 
-bool Provider::fused_route() const { return !materialized && gram_form_ok(kind, train, train); }
+bool Provider::fused_route() const {
+  return !is_tree && !materialized && gram_form_ok(kind, train, train);
+}
 
 void Provider::forward_mixed(const float* V, int ncols, const float* mix, int T, bool accumulate,
                              float* out) {
@@ -174,6 +211,11 @@ void Provider::forward_mixed(const float* V, int ncols, const float* mix, int T,
 
 void Provider::cross(const PackedPoints& rows, const float* V, int ncols,
                      float* out) {
+  if (is_tree) {
+    tree_matvec(tree, tparams.ptr, rows.z.ptr, rows.n, train.z.ptr, n, V, ncols, 0.f, false,
+                out, st);
+    return;
+  }
   MatvecArgs a;
   a.kind = kind;
   a.outputscale = outputscale();

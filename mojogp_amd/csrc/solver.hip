@@ -333,9 +333,47 @@ __global__ void k_pc_setpivot(PivotDev* __restrict__ state, float* __restrict__ 
   for (int j = threadIdx.x; j < m; j += blockDim.x) coef[j] = L[(int64_t)j * n + p];
 }
 
+// Pivot-column kernel values: radial kinds read scaled coordinates (z rows);
+// kernel trees read raw coordinates.
 template <int KIND>
+struct RadialColumn {
+  float os;
+  int d;
+  __device__ float operator()(const float* __restrict__ zi, const float* zp) const {
+    float r2 = 0.0f;
+    for (int k = 0; k < d; ++k) {
+      const float df = zi[k] - zp[k];
+      r2 = fmaf(df, df, r2);
+    }
+    if constexpr (KIND == KIND_RBF) {
+      return os * __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
+    } else if constexpr (KIND == KIND_MATERN12) {
+      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+      return os * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+    } else if constexpr (KIND == KIND_MATERN32) {
+      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+      return os * fmaf(u, kLn2, 1.0f) * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+    } else {
+      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
+      const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+      return os * fmaf(u, fmaf(u, kLn2 * kLn2 / 3.0f, kLn2), 1.0f) * e;
+    }
+  }
+};
+
+struct TreeColumn {
+  KernelTree t;
+  const float* p;
+  __device__ float operator()(const float* __restrict__ xi_g, const float* xp) const {
+    float xi[kTreeMaxInputDim];
+    for (int k = 0; k < t.d; ++k) xi[k] = xi_g[k];
+    return tree_value(t, p, xi, xp);
+  }
+};
+
+template <class Eval>
 __global__ __launch_bounds__(256) void k_pc_column(
-    const float* __restrict__ Z, int d, int64_t n, float os, int m,
+    Eval ev, const float* __restrict__ Z, int d, int64_t n, int m,
     float* __restrict__ L, float* __restrict__ diag, const float* __restrict__ mask,
     const float* __restrict__ coef, const PivotDev* __restrict__ state, int nb,
     float* pv, int64_t* pi, double* pa) {
@@ -353,25 +391,7 @@ __global__ __launch_bounds__(256) void k_pc_column(
   ArgmaxAcc loc{-1e30f, -1};
   double abss = 0.0;
   for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
-    float r2 = 0.0f;
-    for (int k = 0; k < d; ++k) {
-      const float df = Z[i * d + k] - zp[k];
-      r2 = fmaf(df, df, r2);
-    }
-    float kv;
-    if constexpr (KIND == KIND_RBF) {
-      kv = os * __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
-    } else if constexpr (KIND == KIND_MATERN12) {
-      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
-      kv = os * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
-    } else if constexpr (KIND == KIND_MATERN32) {
-      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
-      kv = os * fmaf(u, kLn2, 1.0f) * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
-    } else {
-      const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
-      const float e = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
-      kv = os * fmaf(u, fmaf(u, kLn2 * kLn2 / 3.0f, kLn2), 1.0f) * e;
-    }
+    const float kv = ev(Z + i * d, zp);
     float sum = 0.0f;
     for (int j = 0; j < m; ++j) sum += scoef[j] * L[(int64_t)j * n + i];
     const float v = (kv - sum) * scale;
@@ -902,20 +922,37 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
   PivotDev init{0, rank, 0, 0.f, 0.f};
   MGP_HIP_CHECK(hipMemcpyAsync(state.ptr, &init, sizeof(init), hipMemcpyHostToDevice, st));
   fill(L, (int64_t)rank * n, 0.0f, st);
-  const float os = pv.outputscale();
+  const float os = pv.kdiag();
   hipLaunchKernelGGL(k_pc_init, grid1(n), dim3(kBlock), 0, st, diag.ptr, mask.ptr, n, os);
   hipLaunchKernelGGL(k_pc_argmax_part, dim3(nb), dim3(kBlock), 0, st, diag.ptr, mask.ptr,
                      n, nb, pvv.ptr, piv.ptr, pa.ptr);
   MGP_HIP_CHECK(hipGetLastError());
-  auto col = pv.kind == KIND_RBF        ? k_pc_column<KIND_RBF>
-             : pv.kind == KIND_MATERN12 ? k_pc_column<KIND_MATERN12>
-             : pv.kind == KIND_MATERN32 ? k_pc_column<KIND_MATERN32>
-                                        : k_pc_column<KIND_MATERN52>;
   auto launch_column = [&](int m) {
     const size_t shm = (size_t)(m + pv.d) * sizeof(float);
-    hipLaunchKernelGGL(col, dim3(nb), dim3(kBlock), shm, st, pv.train.z.ptr, pv.d, n, os, m,
-                       L, diag.ptr, mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr,
-                       pa.ptr);
+    const float* Z = pv.train.z.ptr;
+    const int d = pv.d;
+    const float osk = pv.outputscale();
+    if (pv.is_tree) {
+      hipLaunchKernelGGL(k_pc_column<TreeColumn>, dim3(nb), dim3(kBlock), shm, st,
+                         TreeColumn{pv.tree, pv.tparams.ptr}, Z, d, n, m, L, diag.ptr, mask.ptr,
+                         coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
+    } else if (pv.kind == KIND_RBF) {
+      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_RBF>>, dim3(nb), dim3(kBlock), shm, st,
+                         RadialColumn<KIND_RBF>{osk, d}, Z, d, n, m, L, diag.ptr, mask.ptr,
+                         coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
+    } else if (pv.kind == KIND_MATERN12) {
+      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_MATERN12>>, dim3(nb), dim3(kBlock), shm,
+                         st, RadialColumn<KIND_MATERN12>{osk, d}, Z, d, n, m, L, diag.ptr,
+                         mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
+    } else if (pv.kind == KIND_MATERN32) {
+      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_MATERN32>>, dim3(nb), dim3(kBlock), shm,
+                         st, RadialColumn<KIND_MATERN32>{osk, d}, Z, d, n, m, L, diag.ptr,
+                         mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
+    } else {
+      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_MATERN52>>, dim3(nb), dim3(kBlock), shm,
+                         st, RadialColumn<KIND_MATERN52>{osk, d}, Z, d, n, m, L, diag.ptr,
+                         mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
+    }
     MGP_HIP_CHECK(hipGetLastError());
   };
 
@@ -1046,6 +1083,10 @@ void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const fl
 
 void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int ncols,
                      double* g_host, hipStream_t st) {
+  if (pv.is_tree) {
+    tree_grad_traces(pv.tree, pv.tparams.ptr, pv.train.z.ptr, pv.n, Lf, Rf, ncols, g_host, st);
+    return;
+  }
   const int d = pv.d;
   MGP_REQUIRE(d <= 32, "gradient kernel supports d <= 32");
   const int dm = d <= 1 ? 1 : d <= 2 ? 2 : d <= 4 ? 4 : d <= 8 ? 8 : d <= 16 ? 16 : 32;

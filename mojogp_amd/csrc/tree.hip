@@ -1,0 +1,271 @@
+// Composite kernel trees on gfx950: products, dense blocks, pivot columns and
+// gradient traces evaluated per pair from raw coordinate differences (VALU;
+// the Gram-form tile path serves single radial leaves).  Tree semantics and
+// reference citations are in kernel_tree.h.
+#include "tree.h"
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+#include <vector>
+
+namespace mgp {
+
+namespace {
+
+constexpr int kTile = 128;      // column points per LDS tile
+constexpr int kMaxCols = 16;    // right-hand sides per pass
+constexpr int kGradCols = 16;   // gradient-trace factor columns per pass
+
+void require(bool ok, const std::string& msg) {
+  if (!ok) throw Error(ST_INVALID, msg);
+}
+
+// out[c][i] = sum_j K(r_i, c_j) V[c][j] (+ noise V[c][i] when square); one
+// thread per row, column points and right-hand sides staged in LDS.
+__global__ __launch_bounds__(256) void k_tree_matvec(
+    const float* __restrict__ Xr, int64_t m, const float* __restrict__ Xc, int64_t n,
+    KernelTree t, const float* __restrict__ p, const float* __restrict__ V, int ncols,
+    float noise, int add_noise, float* __restrict__ out) {
+  extern __shared__ float sm[];  // [kTile][d + ncols]
+  const int d = t.d;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int w = d + ncols;
+  float xi[kTreeMaxInputDim];
+  for (int k = 0; k < d; ++k) xi[k] = (i < m) ? Xr[i * d + k] : 0.0f;
+  double acc[kMaxCols];
+  for (int c = 0; c < kMaxCols; ++c) acc[c] = 0.0;
+  for (int64_t j0 = 0; j0 < n; j0 += kTile) {
+    __syncthreads();
+    for (int q = threadIdx.x; q < kTile * w; q += blockDim.x) {
+      const int jj = q / w, k = q - jj * w;
+      const int64_t j = j0 + jj;
+      float val = 0.0f;
+      if (j < n) val = (k < d) ? Xc[j * d + k] : V[(int64_t)(k - d) * n + j];
+      sm[q] = val;
+    }
+    __syncthreads();
+    const int cnt = (int)min((int64_t)kTile, n - j0);
+    float part[kMaxCols];
+    for (int c = 0; c < kMaxCols; ++c) part[c] = 0.0f;
+    for (int jj = 0; jj < cnt; ++jj) {
+      const float* row = sm + jj * w;
+      const float kv = tree_value(t, p, xi, row);
+      for (int c = 0; c < ncols; ++c) part[c] = fmaf(kv, row[d + c], part[c]);
+    }
+    for (int c = 0; c < ncols; ++c) acc[c] += (double)part[c];
+  }
+  if (i < m) {
+    for (int c = 0; c < ncols; ++c) {
+      float o = (float)acc[c];
+      if (add_noise) o = fmaf(noise, V[(int64_t)c * m + i], o);
+      out[(int64_t)c * m + i] = o;
+    }
+  }
+}
+
+// out[c*n + i] = K(rows[r0 + c], cols[i])
+__global__ void k_tree_fill(const float* __restrict__ Xr, int64_t r0, int64_t rows,
+                            const float* __restrict__ Xc, int64_t n, KernelTree t,
+                            const float* __restrict__ p, float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * n) return;
+  const int64_t c = idx / n, i = idx - c * n;
+  const int d = t.d;
+  float xr[kTreeMaxInputDim], xc[kTreeMaxInputDim];
+  for (int k = 0; k < d; ++k) {
+    xr[k] = Xr[(r0 + c) * d + k];
+    xc[k] = Xc[i * d + k];
+  }
+  out[idx] = tree_value(t, p, xr, xc);
+}
+
+// part[(y*gx + x)*P + q] = sum over the block's pairs (a, b) of
+// dK_ab/dtheta_q sum_c Lf[c][a] Rf[c][b]; grid = (row blocks, column splits).
+__global__ __launch_bounds__(256) void k_tree_grad_trace(
+    const float* __restrict__ X, int64_t n, KernelTree t, const float* __restrict__ p,
+    const float* __restrict__ Lf, const float* __restrict__ Rf, int ncols, int c0,
+    double* __restrict__ part) {
+  __shared__ float xb[64][kTreeMaxInputDim];
+  __shared__ float rb[64][kGradCols];
+  __shared__ double red[256];
+  const int d = t.d, P = t.nparams;
+  const int cn = min(kGradCols, ncols - c0);
+  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = a < n;
+  float xa[kTreeMaxInputDim], la[kGradCols];
+  for (int k = 0; k < d; ++k) xa[k] = live ? X[a * d + k] : 0.0f;
+  for (int c = 0; c < kGradCols; ++c) la[c] = (live && c < cn) ? Lf[(int64_t)(c0 + c) * n + a] : 0.0f;
+  const int64_t tiles = (n + 63) / 64;
+  const int64_t tps = (tiles + gridDim.y - 1) / gridDim.y;
+  const int64_t jb = min(n, (int64_t)blockIdx.y * tps * 64);
+  const int64_t je = min(n, jb + tps * 64);
+  double accd[kTreeMaxParams];
+  for (int q = 0; q < kTreeMaxParams; ++q) accd[q] = 0.0;
+  for (int64_t b0 = jb; b0 < je; b0 += 64) {
+    __syncthreads();
+    for (int q = threadIdx.x; q < 64 * kTreeMaxInputDim; q += blockDim.x) {
+      const int bb = q / kTreeMaxInputDim, k = q - bb * kTreeMaxInputDim;
+      const int64_t b = b0 + bb;
+      xb[bb][k] = (b < je && k < d) ? X[b * d + k] : 0.0f;
+    }
+    for (int q = threadIdx.x; q < 64 * kGradCols; q += blockDim.x) {
+      const int bb = q / kGradCols, c = q - bb * kGradCols;
+      const int64_t b = b0 + bb;
+      rb[bb][c] = (b < je && c < cn) ? Rf[(int64_t)(c0 + c) * n + b] : 0.0f;
+    }
+    __syncthreads();
+    float g[kTreeMaxParams];
+    for (int q = 0; q < kTreeMaxParams; ++q) g[q] = 0.0f;
+    const int cnt = (int)min((int64_t)64, je - b0);
+    if (live) {
+      for (int bb = 0; bb < cnt; ++bb) {
+        float w = 0.0f;
+        for (int c = 0; c < kGradCols; ++c) w = fmaf(la[c], rb[bb][c], w);
+        tree_grad_accumulate(t, p, xa, xb[bb], w, g);
+      }
+    }
+    for (int q = 0; q < P; ++q) accd[q] += (double)g[q];
+  }
+  for (int q = 0; q < P; ++q) {
+    red[threadIdx.x] = live ? accd[q] : 0.0;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+      if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) part[((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * P + q] = red[0];
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+KernelTree parse_kernel_tree(const int* spec, int len) {
+  require(spec != nullptr && len >= 4, "kernel tree spec is too short");
+  KernelTree t;
+  int pos = 0;
+  auto next = [&]() {
+    require(pos < len, "kernel tree spec is truncated");
+    return spec[pos++];
+  };
+  t.d = next();
+  t.nparams = next();
+  t.nleaves = next();
+  t.nnodes = next();
+  require(t.d >= 1 && t.d <= kTreeMaxInputDim, "kernel tree input dimension must be in [1, 32]");
+  require(t.nparams >= 1 && t.nparams <= kTreeMaxParams, "kernel tree has too many parameters");
+  require(t.nleaves >= 1 && t.nleaves <= kTreeMaxLeaves, "kernel tree needs 1..8 leaves");
+  require(t.nnodes >= 1 && t.nnodes <= kTreeMaxNodes, "kernel tree needs 1..16 nodes");
+  int doff = 0;
+  for (int l = 0; l < t.nleaves; ++l) {
+    TreeLeaf& lf = t.leaf[l];
+    lf.kind = next();
+    lf.ard = next();
+    lf.ndim = next();
+    lf.p0 = next();
+    lf.dim_off = doff;
+    require(lf.kind >= KIND_RBF && lf.kind <= KIND_PERIODIC, "unknown kernel tree leaf kind");
+    require(lf.ndim >= 1 && doff + lf.ndim <= kTreeMaxDims, "kernel tree leaf dimensions");
+    for (int q = 0; q < lf.ndim; ++q) {
+      const int dq = next();
+      require(dq >= 0 && dq < t.d, "kernel tree leaf dimension out of range");
+      t.dims[doff++] = dq;
+    }
+    const int nls = lf.ard ? lf.ndim : 1;
+    const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1 : 0;
+    require(lf.p0 >= 0 && lf.p0 + nls + extra + 1 <= t.nparams,
+            "kernel tree leaf parameters out of range");
+  }
+  for (int i = 0; i < t.nnodes; ++i) {
+    TreeNode& nd = t.node[i];
+    nd.code = next();
+    nd.a = next();
+    nd.b = next();
+    switch (nd.code) {
+      case TN_LEAF:
+        require(nd.a >= 0 && nd.a < t.nleaves, "kernel tree leaf node index");
+        break;
+      case TN_ADD:
+      case TN_MUL:
+        require(nd.a >= 0 && nd.a < i && nd.b >= 0 && nd.b < i, "kernel tree child order");
+        break;
+      case TN_SCALE:
+        require(nd.a >= 0 && nd.a < i, "kernel tree child order");
+        require(nd.b >= 0 && nd.b < t.nparams, "kernel tree scale parameter index");
+        break;
+      default:
+        require(false, "unknown kernel tree node code");
+    }
+  }
+  require(pos == len, "kernel tree spec has trailing entries");
+  return t;
+}
+
+double tree_diag(const KernelTree& t, const float* params) {
+  std::vector<double> v((size_t)t.nnodes);
+  for (int i = 0; i < t.nnodes; ++i) {
+    const TreeNode& nd = t.node[i];
+    if (nd.code == TN_LEAF) {
+      const TreeLeaf& lf = t.leaf[nd.a];
+      const int nls = lf.ard ? lf.ndim : 1;
+      const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1 : 0;
+      v[i] = (double)params[lf.p0 + nls + extra];  // every leaf is os at zero distance
+    } else if (nd.code == TN_ADD) {
+      v[i] = v[(size_t)nd.a] + v[(size_t)nd.b];
+    } else if (nd.code == TN_MUL) {
+      v[i] = v[(size_t)nd.a] * v[(size_t)nd.b];
+    } else {
+      v[i] = (double)params[nd.b] * v[(size_t)nd.a];
+    }
+  }
+  return v[(size_t)t.nnodes - 1];
+}
+
+void tree_matvec(const KernelTree& t, const float* p_dev, const float* Xr, int64_t m,
+                 const float* Xc, int64_t n, const float* V, int ncols, float noise,
+                 bool square, float* out, hipStream_t st) {
+  for (int c0 = 0; c0 < ncols; c0 += kMaxCols) {
+    const int nc = std::min(kMaxCols, ncols - c0);
+    const size_t shm = (size_t)kTile * (t.d + nc) * sizeof(float);
+    hipLaunchKernelGGL(k_tree_matvec, dim3((unsigned)ceil_div(std::max<int64_t>(m, 1), 256)),
+                       dim3(256), shm, st, Xr, m, Xc, n, t, p_dev, V + (int64_t)c0 * n, nc,
+                       noise, square ? 1 : 0, out + (int64_t)c0 * m);
+    MGP_HIP_CHECK(hipGetLastError());
+  }
+}
+
+void tree_fill(const KernelTree& t, const float* p_dev, const float* Xr, int64_t r0,
+               int64_t rows, const float* Xc, int64_t n, float* out, hipStream_t st) {
+  const int64_t total = rows * n;
+  if (total == 0) return;
+  hipLaunchKernelGGL(k_tree_fill, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, Xr,
+                     r0, rows, Xc, n, t, p_dev, out);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void tree_grad_traces(const KernelTree& t, const float* p_dev, const float* X, int64_t n,
+                      const float* Lf, const float* Rf, int ncols, double* g_host,
+                      hipStream_t st) {
+  const int P = t.nparams;
+  const int64_t rows = ceil_div(n, 256);
+  const int splits = (int)std::max<int64_t>(
+      1, std::min<int64_t>(ceil_div(2048, rows), ceil_div(n, 1024)));
+  const int64_t nblk = rows * splits;
+  DevBuf<double> part;
+  part.ensure((size_t)nblk * P);
+  std::vector<double> acc((size_t)P, 0.0), hp((size_t)nblk * P);
+  for (int c0 = 0; c0 < ncols; c0 += kGradCols) {
+    hipLaunchKernelGGL(k_tree_grad_trace, dim3((unsigned)rows, (unsigned)splits), dim3(256), 0,
+                       st, X, n, t, p_dev, Lf, Rf, ncols, c0, part.ptr);
+    MGP_HIP_CHECK(hipGetLastError());
+    MGP_HIP_CHECK(hipMemcpyAsync(hp.data(), part.ptr, hp.size() * sizeof(double),
+                                 hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    for (int64_t b = 0; b < nblk; ++b)
+      for (int q = 0; q < P; ++q) acc[(size_t)q] += hp[(size_t)b * P + q];
+  }
+  for (int q = 0; q < P; ++q) g_host[q] = acc[(size_t)q];
+}
+
+}  // namespace mgp

@@ -122,6 +122,16 @@ class PredictionResult:
     std: np.ndarray
 
 
+
+def _check_served(kernel: KernelNode, dim: int) -> None:
+    """Raise NotImplementedError for kernels the gfx950 engine does not serve
+    (single RBF / Matern leaves run on the tile path, other stationary trees
+    on the kernel-tree products)."""
+    if kernel.is_native_leaf():
+        kernel.native_kind()
+    else:
+        kernel.to_tree_spec(dim)
+
 class SingleOutputGP:
     """Exact Gaussian process regression on one MI355X.
 
@@ -210,9 +220,7 @@ class SingleOutputGP:
     # ------------------------------------------------------------ lifecycle
     def _ensure_compiled(self) -> None:
         if self._kernel_module is None or self._engine is None:
-            kind = self.kernel.native_kind()
-            self._kernel_module = _engine.load_kernel_module(kind, self.kernel.ard_dim is not None,
-                                                             self.dim)
+            self._kernel_module = _engine.load_kernel_module(self.kernel, False, self.dim)
             self._engine = _engine.load_engine()
 
     def _destroy_prediction_cache(self) -> None:
@@ -346,7 +354,7 @@ class SingleOutputGP:
         self._noise_floor = float(noise_floor)
         self._noise_regularization = float(noise_regularization)
         self.kernel = make_ard_kernel(self._kernel_pre_ard, self.dim) if self.ard else self._kernel_pre_ard
-        self.kernel.native_kind()  # rejects kernels outside the engine
+        _check_served(self.kernel, self.dim)  # rejects kernels outside the engine
         self._kernel_module = None
         self._engine = None
 

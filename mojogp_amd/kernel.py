@@ -1,17 +1,22 @@
-"""Kernel specification surface (subset served by the gfx950 engine).
+"""Kernel specification surface served by the gfx950 engine.
 
-Mirrors the reference's kernel DSL for the hot-path kernels
-(mojogp/kernel.py): ``RBF``, ``Matern12``, ``Matern32`` and ``Matern52``,
-isotropic or ARD, with the same
-parameter names, initial values and engine parameter layout
-(``kernel.py:324-509``):
+Mirrors the reference's kernel DSL (mojogp/kernel.py): ``RBF``, ``Matern12``,
+``Matern32``, ``Matern52``, ``RQ`` and ``Periodic`` leaves, isotropic or ARD,
+optionally restricted to ``active_dims``, composed with ``+`` (sum), ``*``
+(product) and ``c * K`` (scale), with the reference's parameter names, initial
+values and parameter layout (``kernel.py:324-660``):
 
-  isotropic  [lengthscale, outputscale]
-  ARD        [ls_0 .. ls_{d-1}, outputscale]
+  RBF / Matern   [lengthscale | ls_0 .. ls_{q-1}], outputscale
+  RQ             [lengthscale | ls_0 .. ls_{q-1}], alpha, outputscale
+  Periodic       [lengthscale | ls_0 .. ls_{q-1}], period, outputscale
+  sum / product  left params, then right params
+  scale          inner params, then the scale factor
 
-Composite trees (sum / product / scale) and the other kernel families are
-accepted for construction and serialisation but the engine rejects them at
-``fit`` time: they are outside the accelerated path.
+A single RBF / Matern leaf on all input dimensions runs on the fused MFMA
+tile path; every other tree is compiled by ``to_tree_spec`` into the flat
+integer form the native kernel-tree products take.  ``Linear`` and
+``Polynomial`` leaves are accepted for construction and serialisation but
+rejected at ``fit`` time (non-stationary leaves are outside the served path).
 """
 
 from __future__ import annotations
@@ -37,6 +42,9 @@ class KernelType(Enum):
 # Families the native kernels implement (value = native kind code).
 NATIVE_KINDS = {KernelType.RBF: 0, KernelType.MATERN52: 1, KernelType.MATERN12: 2,
                 KernelType.MATERN32: 3}
+# Leaf codes of the kernel-tree spec (radial kinds keep their codes).
+TREE_LEAF_CODES = {**NATIVE_KINDS, KernelType.RQ: 4, KernelType.PERIODIC: 5}
+_TN_LEAF, _TN_ADD, _TN_MUL, _TN_SCALE = 0, 1, 2, 3
 
 
 @dataclass
@@ -55,6 +63,25 @@ class KernelNode:
     def __add__(self, other: "KernelNode") -> "KernelNode":
         return KernelNode(operator="sum", left=self, right=other)
 
+    def __radd__(self, other):
+        if isinstance(other, (int, float)) and other == 0:
+            return self  # sum() starts from 0
+        return KernelNode(operator="sum", left=other, right=self)
+
+    def with_active_dims(self, dims) -> "KernelNode":
+        """Copy of this (possibly composite) kernel restricted to ``dims``
+        (kernel.py:224-242); leaves inside without their own active_dims see
+        exactly these input columns."""
+        import copy
+        node = copy.deepcopy(self)
+        node.active_dims = tuple(sorted(int(x) for x in dims))
+        return node
+
+    def has_active_dims(self) -> bool:
+        return bool(self.active_dims is not None
+                    or (self.left and self.left.has_active_dims())
+                    or (self.right and self.right.has_active_dims()))
+
     def __mul__(self, other):
         if isinstance(other, (int, float)):
             return KernelNode(operator="scale", left=self, scale_factor=float(other))
@@ -71,6 +98,66 @@ class KernelNode:
 
     def is_native_leaf(self) -> bool:
         return self.kernel_type in NATIVE_KINDS and self.operator is None and self.active_dims is None
+
+    def is_tree_servable(self) -> bool:
+        """Every leaf is one of the stationary families the tree products serve."""
+        if self.kernel_type is not None:
+            return self.kernel_type in TREE_LEAF_CODES
+        return bool(self.left.is_tree_servable()
+                    and (self.operator == "scale" or self.right.is_tree_servable()))
+
+    def to_tree_spec(self, dim: int) -> List[int]:
+        """Flat integer spec of the native kernel-tree products.
+
+        Layout: [d, nparams, nleaves, nnodes, per leaf (tree order): code, ard,
+        ndim, p0, dims..., per node (children first, root last): code, a, b].
+        A leaf's dimensions are its own active_dims, else those of its nearest
+        ancestor with active_dims, else all ``dim`` inputs.  ARD leaves must
+        carry one lengthscale per dimension (``make_ard_kernel``)."""
+        if not self.is_tree_servable():
+            raise NotImplementedError(
+                f"kernel {self!r} has leaves outside the gfx950 engine (served: RBF, Matern12, "
+                "Matern32, Matern52, RQ, Periodic under sum / product / scale)")
+        leaves: List[List[int]] = []
+        nodes: List[List[int]] = []
+
+        def walk(node: "KernelNode", dims: tuple, offset: int):
+            dims = node.active_dims if node.active_dims is not None else dims
+            for x in dims:
+                if not 0 <= x < dim:
+                    raise ValueError(f"active_dims index {x} out of range for {dim}-dimensional input")
+            if node.kernel_type is not None:
+                ard = node.ard_dim is not None
+                if ard and node.ard_dim != len(dims):
+                    raise ValueError(f"ARD leaf {node!r} has {node.ard_dim} lengthscales for "
+                                     f"{len(dims)} active dimensions")
+                leaves.append([TREE_LEAF_CODES[node.kernel_type], int(ard), len(dims), offset,
+                               *dims])
+                nodes.append([_TN_LEAF, len(leaves) - 1, 0])
+                return len(nodes) - 1, offset + node.num_params()
+            if node.operator in ("sum", "product"):
+                a, mid = walk(node.left, dims, offset)
+                b, end = walk(node.right, dims, mid)
+                nodes.append([_TN_ADD if node.operator == "sum" else _TN_MUL, a, b])
+                return len(nodes) - 1, end
+            if node.operator == "scale":
+                a, mid = walk(node.left, dims, offset)
+                nodes.append([_TN_SCALE, a, mid])
+                return len(nodes) - 1, mid + 1
+            raise ValueError(f"Unknown operator: {node.operator}")
+
+        _, nparams = walk(self, tuple(range(dim)), 0)
+        if (len(leaves) > 8 or len(nodes) > 16 or nparams > 48 or dim > 32
+                or sum(lf[2] for lf in leaves) > 64):
+            raise NotImplementedError("kernel trees are served up to 8 leaves, 16 nodes, "
+                                      "48 parameters, 32 input dimensions and 64 leaf "
+                                      "dimensions in total")
+        spec = [dim, nparams, len(leaves), len(nodes)]
+        for lf in leaves:
+            spec += lf
+        for nd in nodes:
+            spec += nd
+        return spec
 
     def native_kind(self) -> int:
         if not self.is_native_leaf():
@@ -232,31 +319,31 @@ class KernelNode:
 
     # ---------------------------------------------------------- evaluation
     def evaluate(self, X, X2=None, params=None) -> np.ndarray:
-        """K(X, X2) in float64 arithmetic, returned as float32 (kernel.py:722-923)."""
-        X = np.asarray(X, dtype=np.float64)
-        X2 = X if X2 is None else np.asarray(X2, dtype=np.float64)
+        """K(X, X2) in float64 arithmetic, returned as float32 (kernel.py:722-923).
+
+        Leaves follow the engine's expressions (codegen_engine/expressions.py:
+        77-326): periodic divides the summed sin^2 terms by the lengthscale
+        (not its square) on raw differences, RQ uses (1 + r^2 / (2 alpha))^-alpha."""
+        X = np.atleast_2d(np.asarray(X, dtype=np.float64))
+        X2 = X if X2 is None else np.atleast_2d(np.asarray(X2, dtype=np.float64))
         p = np.ones(self.num_params()) if params is None else np.asarray(params, np.float64)
-        if self.kernel_type not in (KernelType.RBF, KernelType.MATERN12, KernelType.MATERN32,
-                                    KernelType.MATERN52) or self.operator is not None:
-            raise NotImplementedError("evaluate() covers RBF and Matern leaves")
-        if self.ard_dim is not None:
-            ls, extra = p[: self.ard_dim], self.ard_dim
-        else:
-            ls, extra = np.array([p[0]]), 1
-        A, B = X / ls, X2 / ls
-        sq = (np.sum(A * A, 1)[:, None] + np.sum(B * B, 1)[None, :] - 2 * A @ B.T)
-        sq = np.maximum(sq, 0.0)
-        dist = np.sqrt(sq + 1e-20)
-        os = p[extra]
-        if self.kernel_type == KernelType.RBF:
-            K = os * np.exp(-0.5 * sq)
-        elif self.kernel_type == KernelType.MATERN12:
-            K = os * np.exp(-dist)
-        elif self.kernel_type == KernelType.MATERN32:
-            K = os * (1 + np.sqrt(3.0) * dist) * np.exp(-np.sqrt(3.0) * dist)
-        else:
-            K = os * (1 + np.sqrt(5.0) * dist + 5.0 / 3.0 * sq) * np.exp(-np.sqrt(5.0) * dist)
+        K, _ = self._eval(X, X2, p, 0)
         return K.astype(np.float32)
+
+    def _eval(self, X, X2, p, off):
+        if self.active_dims is not None:
+            cols = list(self.active_dims)
+            X, X2 = X[:, cols], X2[:, cols]
+        if self.kernel_type is not None:
+            return _leaf_matrix(self, X, X2, p[off:off + self.num_params()]), off + self.num_params()
+        if self.operator in ("sum", "product"):
+            A, mid = self.left._eval(X, X2, p, off)
+            B, end = self.right._eval(X, X2, p, mid)
+            return (A + B if self.operator == "sum" else A * B), end
+        if self.operator == "scale":
+            A, mid = self.left._eval(X, X2, p, off)
+            return p[mid] * A, mid + 1
+        raise ValueError(f"Unknown operator: {self.operator}")
 
     def __repr__(self) -> str:
         if self.kernel_type is not None:
@@ -268,11 +355,45 @@ class KernelNode:
         return f"({self.left!r} {sym} {self.right!r})"
 
 
+def _leaf_matrix(node: KernelNode, X, X2, p) -> np.ndarray:
+    kt = node.kernel_type
+    if kt in (KernelType.LINEAR, KernelType.POLYNOMIAL):
+        raise NotImplementedError("evaluate() covers the stationary leaves")
+    q = X.shape[1]
+    nls = node.ard_dim if node.ard_dim is not None else 1
+    if node.ard_dim is not None and node.ard_dim != q:
+        raise ValueError(f"ARD leaf has {node.ard_dim} lengthscales for {q} dimensions")
+    ls = p[:nls]
+    diff = X[:, None, :] - X2[None, :, :]
+    if kt == KernelType.PERIODIC:
+        period, os = p[nls], p[nls + 1]
+        s2 = np.sin(np.pi * diff / period) ** 2
+        S = (s2 / ls).sum(-1) if nls > 1 else s2.sum(-1) / ls[0]
+        return os * np.exp(np.maximum(-2.0 * S, -20.0))
+    r2 = ((diff / ls) ** 2).sum(-1)
+    if kt == KernelType.RQ:
+        alpha, os = p[nls], p[nls + 1]
+        return os * (1.0 + r2 / (2.0 * alpha)) ** (-alpha)
+    os = p[nls]
+    if kt == KernelType.RBF:
+        return os * np.exp(np.maximum(-0.5 * r2, -20.0))
+    r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
+    if kt == KernelType.MATERN12:
+        return os * np.exp(np.maximum(-r, -20.0))
+    if kt == KernelType.MATERN32:
+        return os * (1 + np.sqrt(3.0) * r) * np.exp(np.maximum(-np.sqrt(3.0) * r, -20.0))
+    return os * (1 + np.sqrt(5.0) * r + 5.0 / 3.0 * r2) * np.exp(np.maximum(-np.sqrt(5.0) * r, -20.0))
+
+
 def make_ard_kernel(kernel: KernelNode, dim: int) -> KernelNode:
-    """Resolve ARD leaves to ``dim`` per-dimension lengthscales (kernel.py:1520-1583)."""
+    """Resolve ARD leaves to per-dimension lengthscales (kernel.py:1520-1583).
+
+    A leaf gets one lengthscale per dimension it sees: its own active_dims,
+    else those of its nearest ancestor with active_dims, else ``dim``."""
+    if kernel.active_dims is not None:
+        dim = len(kernel.active_dims)
     if kernel.kernel_type is not None:
-        ard_dim = len(kernel.active_dims) if kernel.active_dims is not None else dim
-        return KernelNode(kernel_type=kernel.kernel_type, ard_dim=ard_dim,
+        return KernelNode(kernel_type=kernel.kernel_type, ard_dim=dim,
                           initial_values=kernel.initial_values, ard=kernel.ard,
                           active_dims=kernel.active_dims)
     return KernelNode(operator=kernel.operator,
@@ -306,4 +427,27 @@ def Matern32(lengthscale: float = 1.0, outputscale: float = 1.0, ard: bool = Fal
 def Matern12(lengthscale: float = 1.0, outputscale: float = 1.0, ard: bool = False,
              active_dims: Optional[List[int]] = None) -> KernelNode:
     return _leaf(KernelType.MATERN12, ard, active_dims, lengthscale=lengthscale,
+                 outputscale=outputscale)
+
+
+def RQ(lengthscale: float = 1.0, alpha: float = 1.0, outputscale: float = 1.0,
+       ard: bool = False, active_dims: Optional[List[int]] = None) -> KernelNode:
+    return _leaf(KernelType.RQ, ard, active_dims, lengthscale=lengthscale, alpha=alpha,
+                 outputscale=outputscale)
+
+
+def Periodic(lengthscale: float = 1.0, period: float = 1.0, outputscale: float = 1.0,
+             ard: bool = False, active_dims: Optional[List[int]] = None) -> KernelNode:
+    return _leaf(KernelType.PERIODIC, ard, active_dims, lengthscale=lengthscale, period=period,
+                 outputscale=outputscale)
+
+
+def Linear(variance: float = 1.0, outputscale: float = 1.0, ard: bool = False,
+           active_dims: Optional[List[int]] = None) -> KernelNode:
+    return _leaf(KernelType.LINEAR, ard, active_dims, variance=variance, outputscale=outputscale)
+
+
+def Polynomial(degree: float = 3.0, offset: float = 1.0, outputscale: float = 1.0,
+               ard: bool = False, active_dims: Optional[List[int]] = None) -> KernelNode:
+    return _leaf(KernelType.POLYNOMIAL, ard, active_dims, degree=degree, offset=offset,
                  outputscale=outputscale)

@@ -39,6 +39,13 @@ F32 = np.float32
 
 
 # ---------------------------------------------------------------- RNG
+def _kdiag(kind, params) -> float:
+    """k(x, x) of a stationary kernel: the outputscale, or a tree at zero distance."""
+    if isinstance(kind, ok.TreeKernel):
+        return kind.diag(params)
+    return float(np.asarray(params)[-1])
+
+
 def gaussian(length: int, seed: int) -> np.ndarray:
     """Counter-hash uniform pair + Box-Muller, float32 (pivoted_cholesky.mojo:51-86)."""
     k = np.arange(1, length + 1, dtype=np.uint64)
@@ -518,7 +525,7 @@ def predict(kind: int, ard: bool, X, y, Xs, params, noise: float, mean: float, *
     mu = Ks @ alpha + mean
     S = lanczos_inv_root(A, lanczos_rank)
     V = Ks @ S
-    var = np.maximum(float(np.asarray(params)[-1]) - np.sum(V * V, axis=1), 1e-10)
+    var = np.maximum(_kdiag(kind, params) - np.sum(V * V, axis=1), 1e-10)
     return mu, var, alpha
 
 
@@ -539,7 +546,7 @@ def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=
     K = ok.kernel_matrix(kind, X, X, params, ard)
     vec = noise_vec is not None
     A = K + (np.diag(np.asarray(noise_vec, np.float64)) if vec else noise * np.eye(n))
-    os_ = float(np.asarray(params)[-1])
+    os_ = _kdiag(kind, params)
     if block_cols > 0:
         block = min(block_cols, m)
     elif materialized:

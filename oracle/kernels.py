@@ -64,7 +64,9 @@ def kernel_from_sq(kind: int, r2: np.ndarray, os: float) -> np.ndarray:
 
 
 def kernel_matrix(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
-    """K(X1, X2) in float64."""
+    """K(X1, X2) in float64 (``kind`` may be a TreeKernel; ``ard`` is then unused)."""
+    if isinstance(kind, TreeKernel):
+        return kind.matrix(X1, X2, params)
     X1 = np.atleast_2d(np.asarray(X1, dtype=np.float64))
     X2 = np.atleast_2d(np.asarray(X2, dtype=np.float64))
     d = X1.shape[1]
@@ -116,6 +118,8 @@ def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
       all:      dk/dos  = k / os
     Isotropic: dk/dl = sum_d of the per-dimension terms with l_d = l.
     """
+    if isinstance(kind, TreeKernel):
+        return kind.gradients(X1, X2, params)
     X1 = np.atleast_2d(np.asarray(X1, dtype=np.float64))
     X2 = np.atleast_2d(np.asarray(X2, dtype=np.float64))
     d = X1.shape[1]
@@ -149,3 +153,130 @@ def gradient_matvec(kind: int, X, V, params, ard: bool) -> np.ndarray:
     G = kernel_gradients(kind, X, X, params, ard)
     V = np.atleast_2d(np.asarray(V, dtype=np.float64))
     return np.einsum("pij,cj->pci", G, V)
+
+
+# ---------------------------------------------------------------------------
+# Composite kernel trees
+#
+# Reference semantics: mojogp/kernel.py:722-803 (recursive evaluation, a
+# node's active_dims slice its inputs, a scale factor follows its subtree in
+# the parameter vector, kernel.py:528-568) with the leaf expressions of the
+# engine (codegen_engine/expressions.py:77-326):
+#   RQ        k = os (1 + r^2 / (2 alpha))^-alpha, r^2 = sum_q (dx_q / l_q)^2
+#   Periodic  k = os exp(max(-2 S, -20)), S = sum_q sin^2(pi dx_q / period) / l_q
+#             (isotropic: sum_q sin^2(pi dx_q / period) / l)
+# and the radial leaves as above.  Pinned by tests/test_oracle_tree.py:
+# scikit-learn RBF / Matern / RationalQuadratic / ExpSineSquared leaves,
+# Sum / Product / ConstantKernel compositions, and central finite
+# differences of the gradients.
+# ---------------------------------------------------------------------------
+
+RQ_LEAF = "RQ"
+PERIODIC_LEAF = "PERIODIC"
+_RADIAL_NAMES = {"RBF": RBF, "MATERN52": MATERN52, "MATERN12": MATERN12, "MATERN32": MATERN32}
+
+
+class TreeKernel:
+    """A kernel tree given as nested dicts (``kernel_type`` or ``operator``,
+    ``left`` / ``right``, ``ard_dim``, ``active_dims``) over ``dim`` inputs."""
+
+    def __init__(self, node: dict, dim: int):
+        self.node = node
+        self.dim = dim
+        self.nparams = self._count(node)
+
+    def _count(self, nd) -> int:
+        if "kernel_type" in nd:
+            extra = 1 if nd["kernel_type"] in (RQ_LEAF, PERIODIC_LEAF) else 0
+            return (nd.get("ard_dim") or 1) + extra + 1
+        if nd["operator"] == "scale":
+            return self._count(nd["left"]) + 1
+        return self._count(nd["left"]) + self._count(nd["right"])
+
+    def matrix(self, X1, X2, params) -> np.ndarray:
+        return self._walk(X1, X2, params, False)[0]
+
+    def gradients(self, X1, X2, params) -> np.ndarray:
+        """dK/dtheta_p for every tree parameter, shape (P, n1, n2)."""
+        return np.stack(self._walk(X1, X2, params, True)[1], axis=0)
+
+    def diag(self, params) -> float:
+        z = np.zeros((1, self.dim))
+        return float(self.matrix(z, z, params)[0, 0])
+
+    def _walk(self, X1, X2, params, grads):
+        X1 = np.atleast_2d(np.asarray(X1, dtype=np.float64))
+        X2 = np.atleast_2d(np.asarray(X2, dtype=np.float64))
+        p = np.asarray(params, dtype=np.float64)
+        if p.shape != (self.nparams,):
+            raise ValueError(f"tree expects {self.nparams} parameters, got {p.shape}")
+        K, G, _ = self._node(self.node, X1, X2, p, 0, grads)
+        return K, G
+
+    def _node(self, nd, X1, X2, p, off, grads):
+        if nd.get("active_dims") is not None:
+            cols = list(nd["active_dims"])
+            X1, X2 = X1[:, cols], X2[:, cols]
+        if "kernel_type" in nd:
+            n = self._count(nd)
+            K, G = _tree_leaf(nd, X1, X2, p[off:off + n], grads)
+            return K, G, off + n
+        A, GA, mid = self._node(nd["left"], X1, X2, p, off, grads)
+        if nd["operator"] == "scale":
+            c = p[mid]
+            return c * A, ([c * g for g in GA] + [A] if grads else None), mid + 1
+        B, GB, end = self._node(nd["right"], X1, X2, p, mid, grads)
+        if nd["operator"] == "sum":
+            return A + B, (GA + GB if grads else None), end
+        return A * B, ([g * B for g in GA] + [A * g for g in GB] if grads else None), end
+
+
+def _tree_leaf(nd, X1, X2, p, grads):
+    kt = nd["kernel_type"]
+    q = X1.shape[1]
+    ard = nd.get("ard_dim") is not None
+    if ard and nd["ard_dim"] != q:
+        raise ValueError("ARD leaf lengthscale count differs from its dimension count")
+    nls = q if ard else 1
+    ls = p[:nls] if ard else np.full(q, p[0])
+    diff = X1[:, None, :] - X2[None, :, :]
+    if kt == PERIODIC_LEAF:
+        period, os = p[nls], p[nls + 1]
+        ang = np.pi * diff / period
+        s2 = np.sin(ang) ** 2
+        S = (s2 / ls).sum(-1)
+        k = os * np.exp(np.maximum(-2.0 * S, -20.0))
+        if not grads:
+            return k, None
+        G = ([2.0 * k * s2[:, :, j] / ls[j] ** 2 for j in range(q)] if ard
+             else [2.0 * k * S / p[0]])
+        G.append(4.0 * np.pi * k / period**2 * (np.sin(ang) * np.cos(ang) * diff / ls).sum(-1))
+        G.append(k / os)
+        return k, G
+    d2 = diff**2
+    r2 = (d2 / ls**2).sum(-1)
+    if kt == RQ_LEAF:
+        alpha, os = p[nls], p[nls + 1]
+        B = 1.0 + r2 / (2.0 * alpha)
+        k = os * B ** (-alpha)
+        h = os * B ** (-alpha - 1.0)
+        extra = [k * (-np.log(B) + r2 / (2.0 * alpha * B))]
+    else:
+        kind = _RADIAL_NAMES[kt]
+        os = p[nls]
+        k = kernel_from_sq(kind, r2, os)
+        r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
+        if kind == RBF:
+            h = k
+        elif kind == MATERN12:
+            h = os * np.exp(np.maximum(-r, -20.0)) / r
+        elif kind == MATERN32:
+            h = 3.0 * os * np.exp(np.maximum(-_SQRT3 * r, -20.0))
+        else:
+            h = (5.0 / 3.0) * os * (1.0 + _SQRT5 * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
+        extra = []
+    if not grads:
+        return k, None
+    terms = d2 / ls**3
+    G = [h * terms[:, :, j] for j in range(q)] if ard else [h * terms.sum(-1)]
+    return k, G + extra + [k / os]
