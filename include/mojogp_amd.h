@@ -71,6 +71,17 @@ MGP_API int mgp_init_provider(int kind, int ard, int d, int64_t n,
 MGP_API int mgp_init_provider_tree(const int* spec, int spec_len, int d, int64_t n,
                                    const float* X, const float* params, int nparams,
                                    float noise, void** out_handle);
+/* Learned per-point noise for mgp_train (the provider noise modes 2-4 of
+ * init_provider, fn_ptr_module.py:297-327, trained as
+ * jit_training.mojo:41-228, 352-960): mode 2 one variance per point, 3 one
+ * per group (group_ids[n] in [0, num_groups)), 4 softplus(w0 + w . x) + floor
+ * on the raw inputs; 0 clears.  Needs a noise vector set first
+ * (mgp_set_noise_vector: the initial variances).  Training starts every raw
+ * value at inv_softplus(init_noise - noise_floor) (mode 4: the intercept;
+ * weights 0), learns them with their own Adam moments and leaves the final
+ * vector on the provider. */
+MGP_API int mgp_set_learned_noise(void* handle, int mode, const int* group_ids,
+                                  int num_groups);
 /* Replaces destroy_provider(info) (fn_ptr_module.py:1183-1195). */
 MGP_API int mgp_destroy_provider(void* handle);
 
@@ -208,6 +219,13 @@ typedef struct mgp_train_result {
   int precond_build_count;
   double precond_build_total_ms;
   int has_alpha;
+  /* Learned noise modes (mgp_set_learned_noise): the final per-point
+   * variances [n] and, for mode 4, the raw linear-function weights [1 + d]
+   * (intercept first).  Caller-allocated, may be NULL. */
+  float* learned_noise;
+  float* noise_fn_params;
+  int has_learned_noise;
+  int noise_fn_len;
 } mgp_train_result_t;
 
 /* Adam training of the kernel hyperparameters, noise and constant mean with

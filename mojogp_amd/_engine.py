@@ -49,23 +49,24 @@ class KernelModule:
     def init_provider(self, X, params, noise, observation_noise=None, noise_mode=None,
                       noise_group_train=None, num_noise_groups=None) -> dict[str, Any]:
         """Noise modes (fn_ptr_module.py:297-327): 0 scalar; 1 fixed per-point
-        vector (observation_noise [n]).  The learned vector / grouped / linear
-        modes 2-4 are not served."""
+        vector (observation_noise [n]); 2 learned per-point, 3 learned per
+        group (noise_group_train [n], num_noise_groups), 4 learned linear
+        function of the inputs — observation_noise holds the initial vector."""
         mode = 0 if noise_mode is None and observation_noise is None else (
             1 if noise_mode is None else int(noise_mode))
-        if mode not in (0, 1):
-            raise NotImplementedError(
-                "learned vector / grouped / input-dependent noise modes (2-4) are not served "
-                "by the gfx950 engine; use scalar learned noise or a fixed noise vector")
-        if mode == 1 and observation_noise is None:
-            raise ValueError("noise mode 1 needs observation_noise")
+        if mode not in (0, 1, 2, 3, 4):
+            raise ValueError(f"noise_mode must be 0-4, got {mode}")
+        if mode >= 1 and observation_noise is None:
+            raise ValueError(f"noise mode {mode} needs observation_noise")
         X = _lib.f32(X)
         if X.ndim != 2 or X.shape[1] != self.dim:
             raise ValueError(f"X must have shape (n, {self.dim})")
         prov = NativeProvider(self.kind, self.ard, X, params, noise, tree_spec=self.tree_spec)
-        if mode == 1:
+        if mode >= 1:
             try:
                 prov.set_noise_vector(observation_noise)
+                if mode >= 2:
+                    prov.set_learned_noise(mode, noise_group_train, num_noise_groups)
             except Exception:
                 prov.close()
                 raise
@@ -81,7 +82,7 @@ class KernelModule:
             "is_ard": self.ard,
             "materialization_mode": 0,
             "noise_mode": mode,
-            "has_observation_noise_vector": mode == 1,
+            "has_observation_noise_vector": mode >= 1,
             "noise_group_ptr": 0,
             "num_noise_groups": 0,
             "_provider": prov,
@@ -197,7 +198,11 @@ class Engine:
         rank_h = np.zeros(T, np.int32)
         rebuild = np.zeros(T, np.int32)
         alpha = np.zeros(n, np.float32)
+        learned = np.zeros(n, np.float32)
+        fnp = np.zeros(prov.d + 1, np.float32)
         res = _lib.TrainResult()
+        res.learned_noise = _lib.fptr(learned)
+        res.noise_fn_params = _lib.fptr(fnp)
         res.params = _lib.fptr(out_params)
         res.nll_history = _lib.fptr(nll_h)
         res.iter_times_ms = _lib.dptr(times)
@@ -243,6 +248,10 @@ class Engine:
         }
         if res.has_alpha:
             out["cached_alpha"] = alpha
+        if res.has_learned_noise:
+            out["learned_observation_noise"] = learned
+        if res.noise_fn_len:
+            out["learned_noise_function_params"] = fnp[:res.noise_fn_len].copy()
         return out
 
     # ------------------------------------------------------------ predict

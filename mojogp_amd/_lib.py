@@ -63,6 +63,8 @@ class TrainResult(C.Structure):
         ("cg_history_len", C.c_int), ("rank_history_len", C.c_int),
         ("rebuild_steps_len", C.c_int), ("precond_build_count", C.c_int),
         ("precond_build_total_ms", C.c_double), ("has_alpha", C.c_int),
+        ("learned_noise", c_float_p), ("noise_fn_params", c_float_p),
+        ("has_learned_noise", C.c_int), ("noise_fn_len", C.c_int),
     ]
 
 
@@ -156,6 +158,7 @@ _SIGNATURES = {
     "mgp_init_provider_tree": (C.c_int, [C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int64,
                                          c_float_p, c_float_p, C.c_int, C.c_float, c_void_pp]),
     "mgp_destroy_provider": (C.c_int, [C.c_void_p]),
+    "mgp_set_learned_noise": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int), C.c_int]),
     "mgp_materialize": (C.c_int, [C.c_void_p]),
     "mgp_update_params": (C.c_int, [C.c_void_p, c_float_p, C.c_int]),
     "mgp_update_noise": (C.c_int, [C.c_void_p, C.c_float]),

@@ -110,6 +110,23 @@ class NativeProvider:
         _lib.call("mgp_set_noise_vector", self.handle, _lib.fptr(v))
         self.noise_vec = v.copy()
 
+    def set_learned_noise(self, mode: int, group_ids=None, num_groups=None) -> None:
+        """Learned per-point noise for training (modes 2 per point, 3 per group,
+        4 linear in the inputs; 0 clears).  The current noise vector is the
+        initial state."""
+        gp_ = None
+        ng = 0
+        if int(mode) == 3:
+            if group_ids is None:
+                raise ValueError("grouped noise needs group ids")
+            g = np.ascontiguousarray(np.asarray(group_ids, dtype=np.int32).ravel())
+            if g.shape != (self.n,):
+                raise ValueError(f"group ids must have shape ({self.n},)")
+            ng = int(num_groups) if num_groups is not None else int(g.max()) + 1
+            self._groups = g
+            gp_ = g.ctypes.data_as(C.POINTER(C.c_int))
+        _lib.call("mgp_set_learned_noise", self.handle, int(mode), gp_, ng)
+
     def forward_matvec(self, V) -> np.ndarray:
         Vc, vec = _cols(V, self.n)
         out = np.empty_like(Vc)

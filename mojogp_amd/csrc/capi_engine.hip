@@ -159,6 +159,9 @@ int mgp_train(void* handle, const float* y, const float* init_params, int nparam
     out->precond_build_total_ms = r.precond_build_total_ms;
     out->has_alpha = r.alpha.empty() ? 0 : 1;
     copy_out(out->cached_alpha, r.alpha);
+    out->has_learned_noise = r.learned_noise.empty() ? 0 : 1;
+    copy_out(out->learned_noise, r.learned_noise);
+    out->noise_fn_len = copy_out(out->noise_fn_params, r.noise_fn_params);
   });
 }
 

@@ -265,6 +265,27 @@ int mgp_cross_matvec(void* h, const float* Xs, int64_t m, const float* V,
   });
 }
 
+int mgp_set_learned_noise(void* h, int mode, const int* group_ids, int num_groups) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(mode == 0 || (mode >= 2 && mode <= 4), "learned noise mode must be 0, 2, 3 or 4");
+    if (mode == 0) {
+      pv->learned_noise_mode = 0;
+      return;
+    }
+    MGP_REQUIRE(pv->has_noise_vec, "set the initial noise vector before a learned noise mode");
+    if (mode == 3) {
+      MGP_REQUIRE(group_ids != nullptr && num_groups >= 1, "grouped noise needs group ids");
+      for (int64_t i = 0; i < pv->n; ++i)
+        MGP_REQUIRE(group_ids[i] >= 0 && group_ids[i] < num_groups,
+                    "noise group id outside [0, num_groups)");
+      pv->noise_groups.assign(group_ids, group_ids + pv->n);
+      pv->num_noise_groups = num_groups;
+    }
+    pv->learned_noise_mode = mode;
+  });
+}
+
 int mgp_set_noise_vector(void* h, const float* noise_vec) {
   return guarded([&] {
     Provider* pv = as_provider(h);

@@ -144,6 +144,9 @@ struct TrainResult {
   int precond_build_count = 0;
   double precond_build_total_ms = 0.0;
   std::vector<float> alpha;  // best-NLL alpha (empty if none)
+  // Learned noise modes: the final per-point variances [n] and, for the
+  // linear mode, the raw function weights [1 + d] (intercept first).
+  std::vector<float> learned_noise, noise_fn_params;
 };
 
 TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& init_params,

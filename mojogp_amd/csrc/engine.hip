@@ -581,6 +581,165 @@ BBMMResult bbmm_step(Provider& pv, Precond& P, bool use_precond, const float* y_
   return out;
 }
 
+// ------------------------------------------------------------------ learned noise
+namespace {
+// out[i] = sum_c Lf[c][i] Rf[c][i]: with Lf = [-alpha/2 | (0.5/T) U] and
+// Rf = [alpha | P^-1 Z] this is 0.5 (diag(K^-1) estimate_i - alpha_i^2), the
+// per-point derivative of n * NLL with respect to noise variance i.
+__global__ void k_row_dots(const float* __restrict__ lf, const float* __restrict__ rf, int64_t n,
+                           int C, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  double s = 0.0;
+  for (int c = 0; c < C; ++c) s += (double)lf[(int64_t)c * n + i] * (double)rf[(int64_t)c * n + i];
+  out[i] = (float)s;
+}
+
+// Learned per-point noise state of the reference's noise modes 2-4
+// (jit_training.mojo:41-228, 352-437, 699-812, 919-960): raw values on the
+// host (one per point, one per group, or the 1 + d weights of a linear
+// function of the raw inputs), their own Adam moments, a best-NLL snapshot.
+// The noise vector noise_i = softplus(raw_i) + floor is rebuilt and uploaded
+// from this state; gradients come from the per-point row dots of the BBMM
+// gradient factors.
+struct LearnedNoise {
+  int mode = 0;
+  int64_t n = 0;
+  int d = 0;
+  float floor = 1e-6f, reg = 0.f, target = 0.f;
+  std::vector<float> raw, m, v, best_raw, best_m, best_v, vec, Xh, rd;
+  const std::vector<int>* groups = nullptr;
+  DevBuf<float> rd_dev;
+
+  void init(Provider& pv, float init_noise, const TrainOptions& o) {
+    mode = pv.learned_noise_mode;
+    if (mode == 0) return;
+    MGP_REQUIRE(mode >= 2 && mode <= 4, "learned noise mode must be 2, 3 or 4");
+    MGP_REQUIRE(pv.has_noise_vec, "learned noise needs an initial noise vector");
+    n = pv.n;
+    d = pv.d;
+    floor = o.noise_floor;
+    reg = o.noise_regularization;
+    target = std::max(init_noise, floor);
+    size_t S = (size_t)n;
+    if (mode == 3) {
+      MGP_REQUIRE(pv.num_noise_groups >= 1 && (int64_t)pv.noise_groups.size() == n,
+                  "learned grouped noise needs group ids");
+      S = (size_t)pv.num_noise_groups;
+      groups = &pv.noise_groups;
+    }
+    if (mode == 4) {
+      S = (size_t)d + 1;
+      Xh.resize((size_t)n * d);
+      MGP_HIP_CHECK(hipMemcpyAsync(Xh.data(), pv.X.ptr, Xh.size() * sizeof(float),
+                                   hipMemcpyDeviceToHost, pv.st));
+      MGP_HIP_CHECK(hipStreamSynchronize(pv.st));
+    }
+    const float r0 = inv_softplus(std::max(init_noise - floor, 1e-8f));
+    raw.assign(S, mode == 4 ? 0.0f : r0);
+    raw[0] = r0;
+    m.assign(S, 0.0f);
+    v.assign(S, 0.0f);
+    best_raw = raw;
+    best_m = m;
+    best_v = v;
+    vec.resize((size_t)n);
+    MGP_HIP_CHECK(hipMemcpyAsync(vec.data(), pv.noise_vec.ptr, (size_t)n * sizeof(float),
+                                 hipMemcpyDeviceToHost, pv.st));
+    MGP_HIP_CHECK(hipStreamSynchronize(pv.st));
+  }
+
+  float linear_raw(int64_t i) const {
+    float r = raw[0];
+    for (int j = 0; j < d; ++j) r += raw[(size_t)j + 1] * Xh[(size_t)i * d + j];
+    return r;
+  }
+
+  void apply(Provider& pv) {
+    for (int64_t i = 0; i < n; ++i) {
+      if (mode == 2) {
+        vec[(size_t)i] = softplus(raw[(size_t)i]) + floor;
+      } else if (mode == 3) {
+        const int g = (*groups)[(size_t)i];
+        if (g >= 0 && g < (int)raw.size()) vec[(size_t)i] = softplus(raw[(size_t)g]) + floor;
+      } else {
+        vec[(size_t)i] = softplus(linear_raw(i)) + floor;
+      }
+    }
+    pv.load_noise_vector(vec.data());
+  }
+
+  void snapshot() {
+    best_raw = raw;
+    best_m = m;
+    best_v = v;
+  }
+  void restore() {
+    raw = best_raw;
+    m = best_m;
+    v = best_v;
+  }
+
+  // d/dnoise of the noise regulariser reg * log(noise / target)^2 / (2 count).
+  double reg_grad(float noise, double count) const {
+    if (!(reg > 0.f)) return 0.0;
+    return (double)reg * std::log((double)noise / (double)target) / ((double)noise * count);
+  }
+
+  void step(Provider& pv, const float* lf, const float* rf, int C, float lr, int t) {
+    rd.resize((size_t)n);
+    rd_dev.ensure((size_t)n);
+    hipLaunchKernelGGL(k_row_dots, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, pv.st, lf, rf,
+                       n, C, rd_dev.ptr);
+    MGP_HIP_CHECK(hipGetLastError());
+    MGP_HIP_CHECK(hipMemcpyAsync(rd.data(), rd_dev.ptr, (size_t)n * sizeof(float),
+                                 hipMemcpyDeviceToHost, pv.st));
+    MGP_HIP_CHECK(hipStreamSynchronize(pv.st));
+    const double dn = (double)n;
+    std::vector<double> g(raw.size(), 0.0);
+    if (mode == 2) {
+      for (int64_t i = 0; i < n; ++i) {
+        const float ri = raw[(size_t)i];
+        const float ni = softplus(ri) + floor;
+        g[(size_t)i] = ((double)rd[(size_t)i] / dn + reg_grad(ni, dn)) * softplus_derivative(ri);
+      }
+    } else if (mode == 3) {
+      const int G = (int)raw.size();
+      for (int64_t i = 0; i < n; ++i) {
+        const int gi = (*groups)[(size_t)i];
+        if (gi >= 0 && gi < G) g[(size_t)gi] += (double)rd[(size_t)i] / dn;
+      }
+      for (int k = 0; k < G; ++k) {
+        const float ng = softplus(raw[(size_t)k]) + floor;
+        g[(size_t)k] = (g[(size_t)k] + reg_grad(ng, (double)G)) * softplus_derivative(raw[(size_t)k]);
+      }
+    } else {
+      for (int64_t i = 0; i < n; ++i) {
+        const float ri = linear_raw(i);
+        const float ni = softplus(ri) + floor;
+        const double gr = ((double)rd[(size_t)i] / dn + reg_grad(ni, dn)) * softplus_derivative(ri);
+        g[0] += gr;
+        for (int j = 0; j < d; ++j) g[(size_t)j + 1] += gr * Xh[(size_t)i * d + j];
+      }
+      if (reg > 0.f)
+        for (int j = 1; j <= d; ++j) g[(size_t)j] += (double)reg * raw[(size_t)j] / std::max(d, 1);
+    }
+    // Adam on the raw values (kernel_adam_update_vector): non-finite or
+    // |g| > 1e6 gradients count as 0; no clamp of the raw values.
+    const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    const float bp1 = pow_float32(b1, t), bp2 = pow_float32(b2, t);
+    for (size_t k = 0; k < raw.size(); ++k) {
+      float gk = (float)g[k];
+      if (gk != gk || gk > 1e6f || gk < -1e6f) gk = 0.0f;
+      m[k] = b1 * m[k] + (1.0f - b1) * gk;
+      v[k] = b2 * v[k] + (1.0f - b2) * gk * gk;
+      const float mh = m[k] / (1.0f - bp1), vh = v[k] / (1.0f - bp2);
+      raw[k] -= lr * mh / (std::sqrt(vh) + eps);
+    }
+  }
+};
+}  // namespace
+
 // ------------------------------------------------------------------ training
 TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& init_params,
                   float init_noise, const TrainOptions& o,
@@ -619,6 +778,9 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
   TrainResult res;
   Precond Pc;
   BBMMWork work;
+  LearnedNoise ln;
+  ln.init(pv, init_noise, o);
+  if (ln.mode) ln.apply(pv);
   const int precond_rank = o.use_preconditioner ? o.precond_rank : 0;
   auto rebuild = [&]() {
     auto t0 = Clock::now();
@@ -644,6 +806,7 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
     actual = it + 1;
     for (int q = 0; q < P; ++q) params[q] = softplus(raw[q]);
     const float noise = o.learn_noise ? softplus(raw[P]) : 0.0f;
+    if (ln.mode) ln.apply(pv);
     pv.params = params;
     pv.refresh_coords();
     pv.noise = noise;
@@ -656,6 +819,7 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
       if (o.learn_noise)
         max_rel = std::max(max_rel, std::fabs(noise - last_rebuild_noise) /
                                         std::max(std::fabs(last_rebuild_noise), 1e-8f));
+      if (ln.mode) max_rel = o.precond_rebuild_threshold + 1.0f;  // the vector moves every step
       if (max_rel > o.precond_rebuild_threshold) {
         rebuild();
         res.precond_rebuild_steps.push_back(it);
@@ -689,6 +853,10 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
       pv.refresh_coords();
       pv.noise = rn;
       last_rebuild_noise = rn;
+      if (ln.mode) {
+        ln.restore();
+        ln.apply(pv);
+      }
       rebuild();
       res.precond_rebuild_steps.push_back(it);
       if (o.verbose) std::printf("  NaN NLL detected at iteration %d - halving LR to %g\n", it, lr);
@@ -706,6 +874,7 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
       best_m_mean = m_mean;
       best_v_mean = v_mean;
       best_t = adam_t;
+      if (ln.mode) ln.snapshot();
       best_alpha.resize(n);
       MGP_HIP_CHECK(hipMemcpyAsync(best_alpha.data(), r.alpha_dev, n * sizeof(float),
                                    hipMemcpyDeviceToHost, st));
@@ -732,6 +901,7 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
       float nr = raw[q] - lr_eff * mh / (std::sqrt(vh) + eps);
       raw[q] = std::max(-20.0f, std::min(20.0f, nr));
     }
+    if (ln.mode) ln.step(pv, work.lf.ptr, work.rf.ptr, 1 + o.num_probes, lr_eff, adam_t);
     // Constant mean: gradient -sum(alpha)/n, its own Adam moments.
     {
       DevBuf<float> ones;
@@ -772,6 +942,12 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
 
   raw = best_raw;
   raw_mean = best_raw_mean;
+  if (ln.mode) {
+    ln.raw = ln.best_raw;
+    ln.apply(pv);
+    res.learned_noise = ln.vec;
+    if (ln.mode == 4) res.noise_fn_params = ln.raw;
+  }
   res.params.resize(P);
   for (int q = 0; q < P; ++q) res.params[q] = softplus(raw[q]);
   res.noise = o.learn_noise ? softplus(raw[P]) : 0.0f;

@@ -25,6 +25,13 @@ struct Provider {
   // preconditioner is built for L L^T + diag(noise_vec).
   DevBuf<float> noise_vec;
   bool has_noise_vec = false;
+  // Learned per-point noise (the reference's noise modes 2-4): 2 one variance
+  // per point, 3 one per group (noise_groups[i] in [0, num_noise_groups)),
+  // 4 softplus of a linear function of the raw inputs.  Training recomputes
+  // noise_vec from the learned state every iteration; 0 = not learned.
+  int learned_noise_mode = 0;
+  std::vector<int> noise_groups;
+  int num_noise_groups = 0;
   std::vector<double> center;  // column means of the training inputs
   // Composite kernel tree (sums / products / scales of stationary leaves on
   // dimension subsets): products are evaluated per pair from raw inputs; the
@@ -71,6 +78,9 @@ struct Provider {
 
   // Host [n] noise variances (all finite and > 0), or nullptr to clear.
   void set_noise_vector(const float* host);
+  // Upload n host variances into the active noise vector without validation
+  // (training's learned-noise updates; values are softplus + floor).
+  void load_noise_vector(const float* host);
   // The scalar noise the operator uses: 0 under a noise vector.
   float scalar_noise() const { return has_noise_vec ? 0.f : noise; }
 

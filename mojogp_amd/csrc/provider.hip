@@ -79,10 +79,19 @@ __global__ void k_add_diag_vec(float* __restrict__ out, const float* __restrict_
 void Provider::set_noise_vector(const float* host) {
   if (!host) {
     has_noise_vec = false;
+    learned_noise_mode = 0;
     return;
   }
   for (int64_t i = 0; i < n; ++i)
     MGP_REQUIRE(std::isfinite(host[i]) && host[i] > 0.f, "noise vector entries must be finite and > 0");
+  noise_vec.ensure((size_t)n);
+  MGP_HIP_CHECK(hipMemcpyAsync(noise_vec.ptr, host, (size_t)n * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  has_noise_vec = true;
+}
+
+void Provider::load_noise_vector(const float* host) {
   noise_vec.ensure((size_t)n);
   MGP_HIP_CHECK(hipMemcpyAsync(noise_vec.ptr, host, (size_t)n * sizeof(float),
                                hipMemcpyHostToDevice, st));

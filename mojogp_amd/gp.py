@@ -123,6 +123,9 @@ class PredictionResult:
 
 
 
+# Provider noise modes of the learned per-sample models (fn_ptr_module.py:297-327).
+_LEARNED_NOISE_MODES = {"learned_vector": 2, "learned_grouped": 3, "learned_input_dependent": 4}
+
 def _check_served(kernel: KernelNode, dim: int) -> None:
     """Raise NotImplementedError for kernels the gfx950 engine does not serve
     (single RBF / Matern leaves run on the tile path, other stationary trees
@@ -188,6 +191,7 @@ class SingleOutputGP:
         self._noise_group_train: Optional[np.ndarray] = None
         self._noise_group_values: Optional[np.ndarray] = None
         self._observation_noise_fn = None
+        self._noise_function_params: Optional[np.ndarray] = None
 
     # ------------------------------------------------------------ properties
     @property
@@ -246,13 +250,25 @@ class SingleOutputGP:
         except Exception:
             pass
 
-    def _build_provider_info(self, X, engine_params, noise, method=None) -> dict:
+    def _build_provider_info(self, X, engine_params, noise, method=None,
+                             training: bool = False) -> dict:
+        """Provider for training or prediction.  A learned noise mode trains
+        with its provider mode (2-4); afterwards, and for prediction, the
+        learned training variances are a fixed vector (mode 1)."""
         self._ensure_compiled()
         obs = getattr(self, "_observation_noise_train", None)
+        mode = None if obs is None else 1
+        groups = ngroups = None
+        if training and self._noise_mode in _LEARNED_NOISE_MODES:
+            mode = _LEARNED_NOISE_MODES[self._noise_mode]
+            if mode == 3:
+                groups = self._noise_group_train
+                ngroups = int(self._noise_group_values.size)
         info = self._kernel_module.init_provider(np.ascontiguousarray(X, dtype=np.float32),
                                                  np.ascontiguousarray(engine_params, np.float32),
                                                  float(noise), observation_noise=obs,
-                                                 noise_mode=None if obs is None else 1)
+                                                 noise_mode=mode, noise_group_train=groups,
+                                                 num_noise_groups=ngroups)
         if (method or self._training_method) == "materialized":
             self._kernel_module.materialize(info)
         return info
@@ -350,6 +366,7 @@ class SingleOutputGP:
         self._noise_group_train = groups_arr
         self._noise_group_values = gnoise_arr
         self._observation_noise_fn = observation_noise_fn
+        self._noise_function_params = None
         self.dim = X.shape[1]
         self._noise_floor = float(noise_floor)
         self._noise_regularization = float(noise_regularization)
@@ -429,18 +446,19 @@ class SingleOutputGP:
     def _resolve_noise_model(self, X, noise_model, observation_noise, observation_noise_fn,
                              noise_function, learn_noise, noise_floor, initial_noise,
                              noise_group_train, group_noise):
-        """Noise-model resolution of gp.py:1010-1161.  Served: learned scalar
-        noise, and fixed per-sample variances (observation_noise,
-        observation_noise_fn, fixed grouped variances), trained as
-        K + diag(noise_i) with the noise not learned.  The learned vector,
-        grouped and input-dependent modes raise NotImplementedError."""
+        """Noise-model resolution of gp.py:1010-1161.  Returns (initial
+        per-point vector or None, resolved mode name, group ids, group values).
+
+        Fixed modes (observation_noise, observation_noise_fn, fixed grouped
+        variances) train K + diag(noise_i) with the noise frozen; learned
+        modes ('learned_vector', grouped with learn_noise=True,
+        'learned_input_dependent' with noise_function='linear') learn the
+        per-point variances during fit."""
         if noise_model not in ("scalar", "fixed_vector", "input_dependent", "grouped",
                                "learned_vector", "learned_input_dependent"):
             raise ValueError("noise_model must be one of 'scalar', 'fixed_vector', "
                              "'input_dependent', 'grouped', 'learned_vector', or "
                              "'learned_input_dependent'")
-        if noise_function is not None and noise_function != "linear":
-            raise ValueError("noise_function must be 'linear' for learned input-dependent noise")
         if noise_function is not None and noise_model != "learned_input_dependent":
             raise ValueError("noise_function is only supported with "
                              "noise_model='learned_input_dependent'")
@@ -453,9 +471,25 @@ class SingleOutputGP:
                              "do not also pass observation_noise_fn")
         if noise_model == "input_dependent" and observation_noise_fn is None:
             raise ValueError("noise_model='input_dependent' requires observation_noise_fn")
-        if noise_model in ("learned_vector", "learned_input_dependent"):
-            raise NotImplementedError(f"noise_model={noise_model!r} (learned per-sample noise) "
-                                      "is not served by the gfx950 engine")
+        if noise_model == "learned_input_dependent":
+            if noise_function != "linear":
+                raise ValueError("noise_model='learned_input_dependent' requires "
+                                 "noise_function='linear'")
+            if observation_noise is not None:
+                raise ValueError("noise_model='learned_input_dependent' learns training noise; "
+                                 "do not also pass observation_noise")
+            if observation_noise_fn is not None:
+                raise ValueError("noise_model='learned_input_dependent' learns its own noise "
+                                 "function; do not also pass observation_noise_fn")
+            if noise_group_train is not None or group_noise is not None:
+                raise ValueError("noise_model='learned_input_dependent' does not use grouped "
+                                 "noise inputs")
+            if not learn_noise:
+                raise ValueError("learn_noise must be True for "
+                                 "noise_model='learned_input_dependent'")
+            if initial_noise <= noise_floor:
+                raise ValueError("initial_noise must be greater than noise_floor for learned "
+                                 "input-dependent noise")
         if observation_noise is not None and noise_model == "grouped":
             raise ValueError("noise_model='grouped' expands group_noise to observation_noise; "
                              "do not also pass observation_noise")
@@ -478,14 +512,21 @@ class SingleOutputGP:
                                  f"{groups_arr.shape}")
             if np.any(groups_arr < 0):
                 raise ValueError("noise_group_train must contain non-negative group ids")
+            max_group = int(groups_arr.max(initial=-1))
             if learn_noise:
-                raise NotImplementedError("learned grouped noise (noise_model='grouped' with "
-                                          "learn_noise=True) is not served by the gfx950 "
-                                          "engine; pass learn_noise=False with group_noise")
-            if group_noise is None:
-                raise ValueError("noise_model='grouped' requires group_noise when "
-                                 "learn_noise=False")
-            gnoise_arr = np.ascontiguousarray(group_noise, dtype=np.float32)
+                if initial_noise <= noise_floor:
+                    raise ValueError("initial_noise must be greater than noise_floor for "
+                                     "learned grouped noise")
+                gnoise_arr = (np.full(max_group + 1, float(initial_noise), np.float32)
+                              if group_noise is None
+                              else np.ascontiguousarray(group_noise, dtype=np.float32))
+                noise_model = "learned_grouped"
+            else:
+                if group_noise is None:
+                    raise ValueError("noise_model='grouped' requires group_noise when "
+                                     "learn_noise=False")
+                gnoise_arr = np.ascontiguousarray(group_noise, dtype=np.float32)
+                noise_model = "fixed_grouped"
             if gnoise_arr.ndim != 1:
                 raise ValueError("group_noise must be a 1D array")
             if gnoise_arr.size == 0:
@@ -494,20 +535,33 @@ class SingleOutputGP:
                 raise ValueError("group_noise contains NaN or Inf values")
             if np.any(gnoise_arr < noise_floor):
                 raise ValueError("group_noise values must be >= noise_floor")
-            if int(groups_arr.max(initial=-1)) >= gnoise_arr.shape[0]:
+            if max_group >= gnoise_arr.shape[0]:
                 raise ValueError("noise_group_train references a group id outside group_noise")
-            noise_model = "fixed_grouped"
             observation_noise = gnoise_arr[groups_arr]
         elif noise_group_train is not None or group_noise is not None:
             raise ValueError("noise_group_train and group_noise require noise_model='grouped'")
+        obs = None
+        if noise_model == "learned_vector":
+            if observation_noise is not None:
+                raise ValueError("noise_model='learned_vector' learns training noise; do not "
+                                 "also pass observation_noise")
+            if not learn_noise:
+                raise ValueError("learn_noise must be True for noise_model='learned_vector'")
+            if initial_noise <= noise_floor:
+                raise ValueError("initial_noise must be greater than noise_floor for "
+                                 "learned_vector noise")
+            obs = np.full(X.shape[0], float(initial_noise), np.float32)
+        if noise_model == "learned_grouped":
+            obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
+        if noise_model == "learned_input_dependent":
+            obs = np.full(X.shape[0], float(initial_noise), np.float32)
         if observation_noise is None and noise_model == "fixed_vector":
             raise ValueError("noise_model='fixed_vector' requires observation_noise")
         if observation_noise is None and not learn_noise:
             raise NotImplementedError(
                 "Fixed scalar noise is not implemented in the JIT training API yet; use "
                 "learn_noise=True or provide observation_noise")
-        obs = None
-        if observation_noise is not None:
+        if observation_noise is not None and noise_model != "learned_grouped":
             if learn_noise:
                 raise ValueError("learn_noise must be False when observation_noise is supplied")
             obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
@@ -519,6 +573,23 @@ class SingleOutputGP:
             if np.any(obs < noise_floor):
                 raise ValueError("observation_noise values must be >= noise_floor")
         return obs, noise_model, groups_arr, gnoise_arr
+
+    def _evaluate_learned_noise_function(self, X) -> np.ndarray:
+        """softplus(w0 + X w) + noise_floor of a learned linear noise function
+        (gp.py:2732-2757)."""
+        if self._noise_mode != "learned_input_dependent":
+            raise ValueError("learned noise function is only available for "
+                             "learned_input_dependent models")
+        w = self._noise_function_params
+        if w is None:
+            raise ValueError("learned input-dependent noise parameters are unavailable")
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        w = np.asarray(w, dtype=np.float32)
+        if w.shape != (X.shape[1] + 1,):
+            raise ValueError("learned input-dependent noise parameters do not match the model "
+                             "input dimension")
+        raw = w[0] + X @ w[1:]
+        return (np.logaddexp(0.0, raw.astype(np.float64)) + self._noise_floor).astype(np.float32)
 
     def _observed_noise(self, X, observation_noise, observation_noise_fn, noise_group_test):
         """Test-point noise for target='observed' (gp.py:2611-2650): explicit
@@ -544,6 +615,8 @@ class SingleOutputGP:
         if observation_noise is None and self._observation_noise_fn is not None:
             return _evaluate_noise_fn(self._observation_noise_fn, X, m,
                                       "stored observation_noise_fn", self._noise_floor)
+        if observation_noise is None and self._noise_mode == "learned_input_dependent":
+            return self._evaluate_learned_noise_function(X)
         if observation_noise is None:
             raise ValueError("predict_observed()/predict(target='observed') requires "
                              "observation_noise for test points")
@@ -559,7 +632,8 @@ class SingleOutputGP:
         """gp.py:1608-1883."""
         engine_params = self.kernel.to_engine_params(np.asarray(initial_params, np.float32))
         self._destroy_provider_info()
-        self._provider_info = self._build_provider_info(X, engine_params, initial_noise, route)
+        self._provider_info = self._build_provider_info(X, engine_params, initial_noise, route,
+                                                        training=True)
         self._provider_state_current = True
         resolved_use_pc = (bool(use_preconditioner) if use_preconditioner is not None
                            else int(cg["precond_rank"]) > 0)
@@ -616,7 +690,31 @@ class SingleOutputGP:
             converged=bool(result["converged"]), lanczos_root=None,
             lanczos_rank=int(cg["max_tridiag_iter"]), nll_history=nll_h,
             cg_iterations_history=cg_h, iter_times_ms=times)
-        if result.get("cached_alpha") is not None:
+        learned = result.get("learned_observation_noise")
+        if learned is not None:
+            # gp.py:1809-1838: the learned variances become the training noise
+            # vector; grouped models keep per-group means, linear ones the
+            # function weights.
+            self._observation_noise_train = np.ascontiguousarray(learned, dtype=np.float32)
+            info["has_observation_noise_vector"] = True
+            info["learned_observation_noise_min"] = float(np.min(learned))
+            info["learned_observation_noise_max"] = float(np.max(learned))
+            info["learned_observation_noise_mean"] = float(np.mean(learned))
+            if self._noise_mode == "learned_grouped" and self._noise_group_train is not None:
+                gv = np.zeros(int(np.max(self._noise_group_train)) + 1, dtype=np.float32)
+                for gid in range(gv.size):
+                    mask = self._noise_group_train == gid
+                    if np.any(mask):
+                        gv[gid] = float(np.mean(self._observation_noise_train[mask]))
+                self._noise_group_values = gv
+                info["learned_group_noise"] = gv.tolist()
+        fnp = result.get("learned_noise_function_params")
+        if fnp is not None:
+            self._noise_function_params = np.ascontiguousarray(fnp, dtype=np.float32)
+            info["learned_noise_function"] = "linear"
+            info["learned_noise_function_params"] = self._noise_function_params.tolist()
+        if (result.get("cached_alpha") is not None
+                and self._noise_mode not in _LEARNED_NOISE_MODES):
             self._store_cached_alpha(result["cached_alpha"],
                                      {"max_cg_iterations": int(cg["max_cg_iter"]),
                                       "cg_tolerance": float(cg["cg_tol"]),
@@ -863,8 +961,11 @@ class SingleOutputGP:
             "cached_love_method": self._cached_love_method, "noise_mode": self._noise_mode,
             "noise_floor": float(self._noise_floor),
             "noise_regularization": float(self._noise_regularization),
-            "noise_function": None,
-            "provider_noise_mode_int": 1 if self._observation_noise_train is not None else None,
+            "noise_function": ("linear" if self._noise_mode == "learned_input_dependent"
+                               else None),
+            "provider_noise_mode_int": (
+                _LEARNED_NOISE_MODES.get(self._noise_mode, 1)
+                if self._observation_noise_train is not None else None),
             "has_observation_noise_train": self._observation_noise_train is not None,
             "has_observation_noise_fn": self._observation_noise_fn is not None,
             "has_noise_group_train": self._noise_group_train is not None,
@@ -880,6 +981,8 @@ class SingleOutputGP:
             arrays["observation_noise_train"] = self._observation_noise_train
         if self._noise_group_train is not None:
             arrays["noise_group_train"] = self._noise_group_train
+        if self._noise_function_params is not None:
+            arrays["noise_function_params"] = self._noise_function_params
         if self._noise_group_values is not None:
             arrays["group_noise"] = self._noise_group_values
         np.savez(path + "_arrays.npz", **arrays)
@@ -903,9 +1006,9 @@ class SingleOutputGP:
             raise NotImplementedError("mixed continuous/categorical models are outside the "
                                       "gfx950 engine")
         mode = cfg.get("noise_mode", "scalar")
-        if mode not in ("scalar", "fixed_vector", "fixed_input_dependent", "fixed_grouped"):
-            raise NotImplementedError(f"noise_mode {mode!r} (learned per-sample noise) is not "
-                                      "served by the gfx950 engine")
+        if mode not in ("scalar", "fixed_vector", "fixed_input_dependent", "fixed_grouped",
+                        *_LEARNED_NOISE_MODES):
+            raise ValueError(f"unknown noise_mode {mode!r} in the artifact")
         arr = np.load(path + "_arrays.npz", allow_pickle=False)
         if mode != "scalar" and "observation_noise_train" not in arr:
             raise ValueError("artifact with fixed per-sample noise lacks observation_noise_train")
@@ -924,6 +1027,9 @@ class SingleOutputGP:
         gp._noise_floor = float(cfg.get("noise_floor", 1e-6))
         gp._noise_regularization = float(cfg.get("noise_regularization", 0.0))
         gp._noise_mode = mode
+        if "noise_function_params" in arr:
+            gp._noise_function_params = np.ascontiguousarray(arr["noise_function_params"],
+                                                             np.float32)
         if "observation_noise_train" in arr:
             gp._observation_noise_train = np.ascontiguousarray(arr["observation_noise_train"],
                                                                np.float32)

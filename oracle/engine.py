@@ -299,8 +299,69 @@ def bbmm_step(kind: int, ard: bool, X, y_c, params, noise: float, P: Precond | N
         grads.append((-0.5 * data + 0.5 * trace / max(T, 1)) / n)
     noise_g = (-0.5 * alpha @ alpha + 0.5 * np.sum(U * W) / max(T, 1)) / n
     grads.append(noise_g)
+    # per point: 0.5 (diag(A^-1) estimate - alpha_i^2) (jit_training.mojo:110-145)
+    rowdot = -0.5 * alpha * alpha + (0.5 / max(T, 1)) * np.sum(U * W, axis=1)
     return {"nll": nll, "inv_quad": inv_quad, "logdet": logdet, "grads": np.array(grads),
-            "alpha": alpha, "x": x, "cg_iterations": iters, "converged": conv}
+            "alpha": alpha, "x": x, "cg_iterations": iters, "converged": conv,
+            "rowdot": rowdot}
+
+
+# ---------------------------------------------------------------- learned noise
+def learned_noise_vector(mode: int, raw, floor: float, groups=None, X=None) -> np.ndarray:
+    """Per-point variances from the learned state (jit_training.mojo:41-84):
+    mode 2 softplus(raw_i) + floor, 3 softplus(raw_{group_i}) + floor,
+    4 softplus(raw_0 + sum_j raw_{j+1} x_ij) + floor."""
+    raw = np.asarray(raw, F32)
+    if mode == 2:
+        r = raw
+    elif mode == 3:
+        r = raw[np.asarray(groups)]
+    else:
+        X = np.asarray(X, F32)
+        r = np.full(X.shape[0], raw[0], F32)
+        for j in range(X.shape[1]):
+            r = (r + raw[j + 1] * X[:, j]).astype(F32)
+    return np.array([_softplus(v) for v in r], F32) + F32(floor)
+
+
+def learned_noise_grad(mode: int, raw, rowdot, floor: float, reg: float, target: float,
+                       groups=None, X=None) -> np.ndarray:
+    """Gradient of the objective with respect to the raw noise state
+    (jit_training.mojo:110-228): per point g_i = rowdot_i / n plus, with
+    reg > 0, reg log(noise / target) / (noise * count) (count n per point,
+    the group count per group), through the softplus; mode 4 chains g_i to
+    the intercept and the weights and adds reg w_p / max(d, 1)."""
+    raw = np.asarray(raw, np.float64)
+    rowdot = np.asarray(rowdot, np.float64)
+    n = rowdot.shape[0]
+    target = max(float(target), float(floor))
+
+    def regg(noise, count):
+        return reg * np.log(noise / target) / (noise * count) if reg > 0 else 0.0 * noise
+
+    def sp(x):
+        return np.logaddexp(0.0, x)
+
+    def dsp(x):
+        return 1.0 / (1.0 + np.exp(-x))
+
+    if mode == 2:
+        noise = sp(raw) + floor
+        return (rowdot / n + regg(noise, n)) * dsp(raw)
+    if mode == 3:
+        groups = np.asarray(groups)
+        G = raw.shape[0]
+        s = np.bincount(groups, weights=rowdot / n, minlength=G)
+        noise = sp(raw) + floor
+        return (s + regg(noise, G)) * dsp(raw)
+    X = np.asarray(X, np.float64)
+    r = raw[0] + X @ raw[1:]
+    noise = sp(r) + floor
+    gr = (rowdot / n + regg(noise, n)) * dsp(r)
+    g = np.concatenate([[gr.sum()], X.T @ gr])
+    if reg > 0:
+        g[1:] += reg * raw[1:] / max(X.shape[1], 1)
+    return g
 
 
 # ---------------------------------------------------------------- training
@@ -340,12 +401,30 @@ def _clip(g, m=100.0):
 
 def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_iterations=50,
           learning_rate=0.01, num_probes=10, max_cg=100, cg_tol=1e-2, precond_rank=0,
-          max_tridiag=30, rebuild_threshold=0.5, init_mean=None, noise_vec=None):
+          max_tridiag=30, rebuild_threshold=0.5, init_mean=None, noise_vec=None,
+          learned=None):
     """Adam over raw (inverse-softplus) hyperparameters and the constant mean,
     with preconditioner rebuilds, NaN recovery and best-NLL restore.  With a
     fixed noise vector the noise is not learned (jit_training.mojo:524, 717,
-    947: operator noise 0 + the vector, noise slot frozen, reported noise 0)."""
-    fixed = noise_vec is not None
+    947: operator noise 0 + the vector, noise slot frozen, reported noise 0).
+
+    ``learned``: dict(mode=2|3|4, floor, reg, groups / X) for the learned
+    per-point noise modes (jit_training.mojo:352-960): the vector is rebuilt
+    from its raw state every iteration, the preconditioner rebuilt every
+    iteration, the raw state updated by its own Adam after the kernel step."""
+    fixed = noise_vec is not None and learned is None
+    if learned is not None:
+        lmode, lfloor, lreg = learned["mode"], float(learned["floor"]), float(learned["reg"])
+        lgroups, lX = learned.get("groups"), learned.get("X")
+        S = {2: len(X), 3: int(np.max(lgroups)) + 1 if lgroups is not None else 0,
+             4: (np.asarray(X).shape[1] + 1)}[lmode]
+        r0 = _inv_softplus(max(F32(init_noise) - F32(lfloor), F32(1e-8)))
+        lraw = np.full(S, r0 if lmode != 4 else 0.0, F32)
+        lraw[0] = r0
+        lm = np.zeros(S, F32)
+        lv = np.zeros(S, F32)
+        lbest = (lraw.copy(), lm.copy(), lv.copy())
+        noise_vec = learned_noise_vector(lmode, lraw, lfloor, lgroups, lX).astype(np.float64)
     X = np.asarray(X, np.float64)
     y = np.asarray(y, np.float64)
     n = X.shape[0]
@@ -366,7 +445,7 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             return None
         K = ok.kernel_matrix(kind, X, X, params, ard)
         L, _ = pivoted_cholesky(K, precond_rank)
-        return Precond(L, np.asarray(noise_vec, np.float64) if fixed else noise)
+        return Precond(L, np.asarray(noise_vec, np.float64) if noise_vec is not None else noise)
 
     P = build(np.asarray(init_params, np.float64), init_noise)
     last_params, last_noise = np.asarray(init_params, F32).copy(), F32(init_noise)
@@ -375,11 +454,15 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
     for it in range(max_iterations):
         params = np.array([_softplus(r) for r in raw[:Pn]], F32)
         noise = F32(0.0) if fixed else _softplus(raw[Pn])
+        if learned is not None:
+            noise_vec = learned_noise_vector(lmode, lraw, lfloor, lgroups, lX).astype(np.float64)
         if it > 0:
             rel = np.abs(params - last_params) / np.maximum(np.abs(last_params), 1e-8)
             rel = float(rel.max())
             if not fixed:
                 rel = max(rel, abs(noise - last_noise) / max(abs(last_noise), 1e-8))
+            if learned is not None:
+                rel = rebuild_threshold + 1.0
             if rel > rebuild_threshold:
                 P = build(params, noise)
                 last_params, last_noise = params.copy(), noise
@@ -400,11 +483,17 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             params = np.array([_softplus(r) for r in raw[:Pn]], F32)
             noise = _softplus(raw[Pn])
             last_params, last_noise = params.copy(), noise
+            if learned is not None:
+                lraw, lm, lv = (a.copy() for a in lbest)
+                noise_vec = learned_noise_vector(lmode, lraw, lfloor, lgroups,
+                                                 lX).astype(np.float64)
             P = build(params, noise)
             continue
         if nll < best["nll"]:
             best.update(nll=nll, raw=raw.copy(), mean=raw_mean, m=m.copy(), v=v.copy(), mm=mm,
                         vm=vm, t=t, alpha=res["alpha"].copy())
+            if learned is not None:
+                lbest = (lraw.copy(), lm.copy(), lv.copy())
         g = res["grads"].astype(F32)
         if fixed:
             g[Pn] = F32(0.0)
@@ -418,6 +507,13 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
         for q in range(Pn + 1):
             nr = raw[q] - lr * (m[q] / bc1) / (np.sqrt(v[q] / bc2) + F32(1e-8))
             raw[q] = F32(min(max(nr, -20.0), 20.0))
+        if learned is not None:
+            lg = learned_noise_grad(lmode, lraw, res["rowdot"], lfloor, lreg, init_noise,
+                                    lgroups, lX).astype(F32)
+            lg[~np.isfinite(lg) | (np.abs(lg) > 1e6)] = 0.0
+            lm = (F32(0.9) * lm + F32(0.1) * lg).astype(F32)
+            lv = (F32(0.999) * lv + F32(0.001) * lg * lg).astype(F32)
+            lraw = (lraw - lr * (lm / bc1) / (np.sqrt(lv / bc2) + F32(1e-8))).astype(F32)
         mg = _clip(-np.sum(res["alpha"]) / n)
         mm = F32(0.9) * mm + F32(0.1) * mg
         vm = F32(0.999) * vm + F32(0.001) * mg * mg
@@ -426,7 +522,12 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             raw_mean = F32(init_mean)
         nll_hist.append(nll)
     params = np.array([_softplus(r) for r in best["raw"][:Pn]], F32)
-    return {"params": params, "noise": 0.0 if fixed else float(_softplus(best["raw"][Pn])),
+    extra = {}
+    if learned is not None:
+        extra["learned_noise"] = learned_noise_vector(lmode, lbest[0], lfloor, lgroups, lX)
+        extra["noise_raw"] = lbest[0].copy()
+    return {**extra, "params": params,
+            "noise": 0.0 if fixed else float(_softplus(best["raw"][Pn])),
             "mean": float(best["mean"]), "final_nll": float(best["nll"]),
             "alpha": best["alpha"], "nll_history": np.array(nll_hist),
             "cg_iterations_history": np.array(cg_hist)}

@@ -181,5 +181,5 @@ def test_grouped_and_callable_fixed_noise():
     np.testing.assert_allclose(v2, l2 + fn(Xs), rtol=1e-6)
     with pytest.raises(ValueError):
         SingleOutputGP(Matern52()).fit(X, y, observation_noise=gnoise[groups])  # learn_noise
-    with pytest.raises(NotImplementedError):
-        SingleOutputGP(Matern52()).fit(X, y, noise_model="learned_vector")
+    with pytest.raises(ValueError):
+        SingleOutputGP(Matern52()).fit(X, y, noise_model="learned_vector", learn_noise=False)
