@@ -237,6 +237,29 @@ MGP_API int mgp_train(void* handle, const float* y, const float* init_params,
                       const mgp_train_opts_t* opts, mgp_progress_cb cb,
                       void* user, mgp_train_result_t* out);
 
+/* Mixed continuous x categorical training of a kernel-tree provider whose
+ * spec has categorical leaves (code 6): split Adam as in train_mixed
+ * (jit_engine_bindings.mojo:1241-1460, jit_mixed.mojo:428-909): continuous
+ * parameters, noise and mean from BBMM, categorical raw parameters
+ * (cat_kinds[ncat] per categorical leaf in tree order: 0 GD, 1 CR, 2 EHH,
+ * 3 HH, 4 FE; ncat_params raw values in that order) from
+ * -0.5 alpha^T dK alpha + (0.5/S) sum_s (K^-1 z_s)^T dK zn_s.  Writes the
+ * best raw categorical parameters to cat_raw_out[ncat_params] and leaves the
+ * provider at the best state. */
+MGP_API int mgp_train_mixed(void* handle, const float* y, const float* init_params,
+                            int nparams, float init_noise, const int* cat_kinds, int ncat,
+                            const float* init_cat_raw, int ncat_params,
+                            const mgp_train_opts_t* opts, mgp_progress_cb cb, void* user,
+                            mgp_train_result_t* out, float* cat_raw_out);
+/* Categorical correlation tables of a tree provider from raw parameters
+ * (same layout as mgp_train_mixed; replaces the mixed prediction's
+ * categorical_prediction_params + update_correlation_matrices,
+ * mojogp/kernel.py:132-174). */
+MGP_API int mgp_set_categorical_params(void* handle, const int* cat_kinds, int ncat,
+                                       const float* raw, int nraw);
+/* Raw correlation tables (tree.table_size entries, leaf p0 offsets). */
+MGP_API int mgp_set_categorical_tables(void* handle, const float* tables, int size);
+
 /* One BBMM evaluation at the provider's current hyperparameters: NLL per
  * sample, y^T K^-1 y, log|K| (SLQ) and gradients[nparams + 1] (kernel
  * params, then noise) of the reference's bbmm_with_precond

@@ -254,6 +254,87 @@ class Engine:
             out["learned_noise_function_params"] = fnp[:res.noise_fn_len].copy()
         return out
 
+    # ------------------------------------------------------------ mixed
+    _CAT_KIND = {"gd": 0, "cr": 1, "ehh": 2, "hh": 3, "fe": 4}
+
+    def train_mixed(self, *args) -> dict[str, Any]:
+        """train_mixed (jit_engine_bindings.mojo:1241-1460): args = info, y,
+        continuous params, noise, C [n, ncat] int32, cat_specs
+        ({"levels", "kernel_type"} per categorical leaf in tree order), raw
+        categorical params, then max_iterations, learning_rate, num_probes,
+        max_cg_iter, cg_tol, precond_rank, verbose, method, precond_method,
+        enable_early_stopping, early_stop_patience, early_stop_tol, callback,
+        progress_interval.  The binding's loop defaults hold: cosine rate,
+        mean from 0, 30 Lanczos steps, rebuild threshold 0.5.  The provider
+        reads each leaf's levels from its input column (C must match it)."""
+        if len(args) < 7 or len(args) > 21:
+            raise ValueError("train_mixed() expects between 7 and 21 positional arguments")
+        info, y, params, init_noise, Cmat, specs, cat_init = args[:7]
+        prov = _provider(info)
+        Cmat = np.asarray(Cmat)
+        if Cmat.ndim != 2 or Cmat.shape[0] != prov.n or Cmat.shape[1] != len(specs):
+            raise ValueError("cat_data must have shape (n, number of categorical leaves)")
+        o = _lib.TrainOpts()
+        o.max_iterations = int(args[7]) if len(args) > 7 else 100
+        o.learning_rate = float(args[8]) if len(args) > 8 else 0.01
+        o.num_probes = int(args[9]) if len(args) > 9 else 10
+        o.max_cg_iter = int(args[10]) if len(args) > 10 else 100
+        o.cg_tol = float(args[11]) if len(args) > 11 else 1e-2
+        o.precond_rank = int(args[12]) if len(args) > 12 else 10
+        o.verbose = int(bool(args[13])) if len(args) > 13 else 0
+        method = int(args[14]) if len(args) > 14 else 0
+        o.precond_method = int(args[15]) if len(args) > 15 else 0
+        o.enable_early_stopping = int(bool(args[16])) if len(args) > 16 else 0
+        o.early_stop_patience = int(args[17]) if len(args) > 17 else 10
+        o.early_stop_tol = float(args[18]) if len(args) > 18 else 1e-4
+        callback = args[19] if len(args) > 19 else None
+        o.progress_interval = int(args[20]) if len(args) > 20 else 1
+        o.use_cosine_lr, o.use_preconditioner, o.max_tridiag_iter = 1, 1, 30
+        o.precond_rebuild_threshold, o.init_mean, o.learn_noise = 0.5, 0.0, 1
+        o.noise_floor, o.noise_regularization = 1e-6, 0.0
+        if o.max_iterations <= 0:
+            raise ValueError("max_iterations must be > 0")
+        kinds = np.array([self._CAT_KIND[str(s["kernel_type"]).lower()] for s in specs],
+                         np.int32)
+        cat_init = _lib.f32(cat_init).ravel()
+        y = _lib.f32(y).ravel()
+        params = _lib.f32(params).ravel()
+        P, T = prov.nparams, o.max_iterations
+        out_params = np.zeros(P, np.float32)
+        nll_h = np.zeros(T, np.float32)
+        times = np.zeros(T, np.float64)
+        cg_h = np.zeros(T, np.int32)
+        cat_out = np.zeros(max(cat_init.size, 1), np.float32)
+        res = _lib.TrainResult()
+        res.params = _lib.fptr(out_params)
+        res.nll_history = _lib.fptr(nll_h)
+        res.iter_times_ms = _lib.dptr(times)
+        res.cg_iterations_history = cg_h.ctypes.data_as(_lib.c_int_p)
+        cfun, _keep = _progress_bridge(callback)
+        _lib.call("mgp_train_mixed", prov.handle, _lib.fptr(y), _lib.fptr(params), P,
+                  float(init_noise), kinds.ctypes.data_as(C.POINTER(C.c_int)), int(kinds.size),
+                  _lib.fptr(cat_init), int(cat_init.size), C.byref(o), cfun, None, C.byref(res),
+                  _lib.fptr(cat_out))
+        prov.cat_kinds, prov.cat_raw = kinds, cat_out[:cat_init.size].copy()
+        hl = res.history_len
+        return {
+            "status": "trained", "num_cat_vars": int(kinds.size),
+            "total_cat_params": int(cat_init.size), "num_cont_params": P,
+            "nll": float(res.final_nll), "noise": float(res.noise), "mean": float(res.mean),
+            "iterations": int(res.iterations), "converged": bool(res.converged),
+            "training_route": "materialized" if method == 1 else "matrix_free",
+            "materialization_mode": method, "precond_method": int(o.precond_method),
+            "precond_rank": int(o.precond_rank),
+            "enable_early_stopping": bool(o.enable_early_stopping),
+            "early_stop_patience": int(o.early_stop_patience),
+            "early_stop_tol": float(o.early_stop_tol),
+            "params": [float(v) for v in out_params],
+            "cat_params": cat_out[:cat_init.size].copy(),
+            "iter_times_ms": [float(v) for v in times[:hl]],
+            "nll_history": [float(v) for v in nll_h[:hl]],
+            "cg_iterations_history": [int(v) for v in cg_h[:res.cg_history_len]],
+        }
+
     # ------------------------------------------------------------ predict
     def predict(self, *args) -> dict[str, Any]:
         if len(args) < 7 or len(args) > 16:
@@ -744,7 +825,7 @@ def load_engine() -> Engine:
     return _ENGINE
 
 
-def load_kernel_module(kind, ard: bool, dim: int) -> KernelModule:
+def load_kernel_module(kind, ard: bool, dim: int, default_dims=None) -> KernelModule:
     """Counterpart of mojogp.loader.load_kernel_module_engine (loader.py:331-429).
 
     ``kind``: a kind code / name, or a (resolved) KernelNode; nodes other than a
@@ -754,5 +835,5 @@ def load_kernel_module(kind, ard: bool, dim: int) -> KernelModule:
     if isinstance(kind, KernelNode):
         if kind.is_native_leaf():
             return KernelModule(kind.native_kind(), kind.ard_dim is not None, dim)
-        return KernelModule(None, False, dim, tree_spec=kind.to_tree_spec(dim))
+        return KernelModule(None, False, dim, tree_spec=kind.to_tree_spec(dim, default_dims))
     return KernelModule(kind, ard, dim)

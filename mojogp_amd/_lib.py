@@ -158,6 +158,9 @@ _SIGNATURES = {
     "mgp_init_provider_tree": (C.c_int, [C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int64,
                                          c_float_p, c_float_p, C.c_int, C.c_float, c_void_pp]),
     "mgp_destroy_provider": (C.c_int, [C.c_void_p]),
+    "mgp_set_categorical_tables": (C.c_int, [C.c_void_p, c_float_p, C.c_int]),
+    "mgp_set_categorical_params": (C.c_int, [C.c_void_p, C.POINTER(C.c_int), C.c_int,
+                                             c_float_p, C.c_int]),
     "mgp_set_learned_noise": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int), C.c_int]),
     "mgp_materialize": (C.c_int, [C.c_void_p]),
     "mgp_update_params": (C.c_int, [C.c_void_p, c_float_p, C.c_int]),
@@ -184,6 +187,10 @@ _SIGNATURES = {
     "mgp_train": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int, C.c_float,
                             C.POINTER(TrainOpts), PROGRESS_CB, C.c_void_p,
                             C.POINTER(TrainResult)]),
+    "mgp_train_mixed": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int, C.c_float,
+                                  C.POINTER(C.c_int), C.c_int, c_float_p, C.c_int,
+                                  C.POINTER(TrainOpts), PROGRESS_CB, C.c_void_p,
+                                  C.POINTER(TrainResult), c_float_p]),
     "mgp_predict": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int64,
                               C.POINTER(PredictOpts), c_float_p, c_float_p, c_float_p,
                               c_float_p, c_float_p, c_float_p, C.POINTER(PredictInfo)]),

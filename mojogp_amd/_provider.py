@@ -110,6 +110,14 @@ class NativeProvider:
         _lib.call("mgp_set_noise_vector", self.handle, _lib.fptr(v))
         self.noise_vec = v.copy()
 
+    def set_categorical_params(self, kinds, raw) -> None:
+        """Correlation tables of the categorical leaves (tree order) from raw
+        parameters (kinds: 0 GD, 1 CR, 2 EHH, 3 HH, 4 FE)."""
+        k = np.ascontiguousarray(np.asarray(kinds, dtype=np.int32).ravel())
+        r = _lib.f32(raw).ravel()
+        _lib.call("mgp_set_categorical_params", self.handle, k.ctypes.data_as(C.POINTER(C.c_int)),
+                  int(k.size), _lib.fptr(r), int(r.size))
+
     def set_learned_noise(self, mode: int, group_ids=None, num_groups=None) -> None:
         """Learned per-point noise for training (modes 2 per point, 3 per group,
         4 linear in the inputs; 0 clears).  The current noise vector is the

@@ -5,6 +5,7 @@
 #include <cstring>
 
 #include "engine.h"
+#include "mixed.h"
 #include "mojogp_amd.h"
 
 using namespace mgp;
@@ -162,6 +163,67 @@ int mgp_train(void* handle, const float* y, const float* init_params, int nparam
     out->has_learned_noise = r.learned_noise.empty() ? 0 : 1;
     copy_out(out->learned_noise, r.learned_noise);
     out->noise_fn_len = copy_out(out->noise_fn_params, r.noise_fn_params);
+  });
+}
+
+int mgp_set_categorical_params(void* handle, const int* cat_kinds, int ncat, const float* raw,
+                               int nraw) {
+  return guarded([&] {
+    Provider* pv = as_provider(handle);
+    MGP_REQUIRE(ncat >= 0 && (ncat == 0 || cat_kinds), "null categorical kinds");
+    set_categorical_raw(*pv, std::vector<int>(cat_kinds, cat_kinds + ncat), raw, nraw);
+  });
+}
+
+int mgp_train_mixed(void* handle, const float* y, const float* init_params, int nparams,
+                    float init_noise, const int* cat_kinds, int ncat, const float* init_cat_raw,
+                    int ncat_params, const mgp_train_opts_t* opts, mgp_progress_cb cb,
+                    void* user, mgp_train_result_t* out, float* cat_raw_out) {
+  return guarded([&] {
+    Provider* pv = as_provider(handle);
+    MGP_REQUIRE(y && init_params && out && cat_kinds && init_cat_raw, "null argument");
+    MGP_REQUIRE(nparams == pv->nparams, "wrong number of initial parameters");
+    TrainOptions o = to_options(opts);
+    std::function<void(const ProgressEvent&)> progress;
+    if (cb) {
+      progress = [cb, user](const ProgressEvent& e) {
+        mgp_progress_t p;
+        p.phase = e.phase;
+        p.current = e.current;
+        p.total = e.total;
+        p.nll = e.nll;
+        p.best_nll = e.best_nll;
+        p.cg_iter = e.cg_iter;
+        p.iter_ms = e.iter_ms;
+        p.noise = e.noise;
+        p.mean = e.mean;
+        p.precond_rank = e.precond_rank;
+        p.precond_rebuild_count = e.precond_rebuild_count;
+        p.converged = e.converged ? 1 : 0;
+        cb(&p, user);
+      };
+    }
+    MixedTrainResult r = train_mixed(*pv, y, std::vector<float>(init_params, init_params + nparams),
+                                     init_noise, std::vector<int>(cat_kinds, cat_kinds + ncat),
+                                     std::vector<float>(init_cat_raw, init_cat_raw + ncat_params),
+                                     o, progress);
+    copy_out(out->params, r.base.params);
+    out->final_nll = r.base.final_nll;
+    out->noise = r.base.noise;
+    out->mean = r.base.mean;
+    out->iterations = r.base.iterations;
+    out->converged = r.base.converged ? 1 : 0;
+    out->history_len = copy_out(out->nll_history, r.base.nll_history);
+    copy_out(out->iter_times_ms, r.base.iter_times_ms);
+    out->cg_history_len = copy_out(out->cg_iterations_history, r.base.cg_iterations_history);
+    out->rank_history_len = 0;
+    out->rebuild_steps_len = 0;
+    out->precond_build_count = r.base.precond_build_count;
+    out->precond_build_total_ms = 0.0;
+    out->has_alpha = 0;
+    out->has_learned_noise = 0;
+    out->noise_fn_len = 0;
+    copy_out(cat_raw_out, r.cat_raw);
   });
 }
 

@@ -130,6 +130,11 @@ int mgp_init_provider_tree(const int* spec, int spec_len, int d, int64_t n, cons
     pv->ard = false;
     pv->is_tree = true;
     pv->tree = t;
+    pv->cat_tables.assign((size_t)t.table_size, 0.0f);  // identity tables until set
+    for (int l = 0; l < t.nleaves; ++l)
+      if (t.leaf[l].kind == KIND_CAT)
+        for (int a = 0; a < t.leaf[l].ard; ++a)
+          pv->cat_tables[(size_t)t.leaf[l].p0 + (size_t)a * t.leaf[l].ard + a] = 1.0f;
     *out_handle = finish_provider(pv, d, n, X, params, nparams, noise);
   });
 }
@@ -262,6 +267,20 @@ int mgp_cross_matvec(void* h, const float* Xs, int64_t m, const float* V,
     pv->cross(pv->test, dv, ncols, dout);
     MGP_HIP_CHECK(hipMemcpyAsync(out, dout, to * sizeof(float), hipMemcpyDeviceToHost, pv->st));
     MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+int mgp_set_categorical_tables(void* h, const float* tables, int size) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(pv->is_tree, "categorical tables belong to kernel-tree providers");
+    MGP_REQUIRE(size == pv->tree.table_size,
+                "expected " + std::to_string(pv->tree.table_size) + " table entries");
+    MGP_REQUIRE(tables != nullptr || size == 0, "null tables");
+    for (int e = 0; e < size; ++e)
+      MGP_REQUIRE(std::isfinite(tables[e]), "categorical tables must be finite");
+    pv->cat_tables.assign(tables, tables + size);
+    pv->refresh_coords();
   });
 }
 

@@ -15,6 +15,12 @@
 //   RBF / Matern     [ls | ls_0..ls_{q-1}], os
 //   RQ               [ls | ls_0..ls_{q-1}], alpha, os
 //   periodic         [ls | ls_0..ls_{q-1}], period, os
+//   categorical      no parameters: the leaf value is R[l_i][l_j] of an L x L
+//                    correlation table (L in the leaf's ard field) stored at
+//                    table offset p0 after the nparams parameters; the leaf's
+//                    one dimension holds the level index as a float
+//                    (the reference's mixed kernels,
+//                    codegen_engine/expressions.py:493-516, cat_k symbols).
 // Nodes are listed children first; the last node is the root.
 #pragma once
 
@@ -27,10 +33,14 @@ constexpr int kTreeMaxNodes = 16;
 constexpr int kTreeMaxDims = 64;    // sum over leaves of their dimension counts
 constexpr int kTreeMaxParams = 48;
 constexpr int kTreeMaxInputDim = 32;
+constexpr int kTreeMaxLevels = 32;     // categorical levels per leaf
+constexpr int kTreeMaxTable = 1024;    // correlation-table entries over all leaves
+constexpr int kTreeMaxCatRow = 64;     // sum over categorical leaves of their levels
 
 // Leaf families beyond the radial kinds of mgp_common.h.
 constexpr int KIND_RQ = 4;
 constexpr int KIND_PERIODIC = 5;
+constexpr int KIND_CAT = 6;
 // Provider kind reported for composite kernel trees.
 constexpr int KIND_TREE = -1;
 
@@ -47,6 +57,8 @@ struct TreeNode {
 
 struct KernelTree {
   int d = 0, nparams = 0, nleaves = 0, nnodes = 0;
+  int table_size = 0;  // categorical table entries after the parameters
+  int ncat = 0;        // categorical leaves
   TreeLeaf leaf[kTreeMaxLeaves];
   TreeNode node[kTreeMaxNodes];
   int dims[kTreeMaxDims];
@@ -69,11 +81,25 @@ struct LeafEval {
   float h;   // radial / RQ: dk/dl_q = h dx_q^2 / l_q^3; periodic: k (see below)
 };
 
+// Level index of a categorical coordinate, clamped into [0, L).
+__device__ __forceinline__ int tree_level(float x, int L) {
+  const int v = (int)x;
+  return v < 0 ? 0 : (v >= L ? L - 1 : v);
+}
+
 __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
                                                    const float* __restrict__ p,
                                                    const float* xi, const float* xj) {
   const TreeLeaf& lf = t.leaf[l];
   LeafEval e;
+  if (lf.kind == KIND_CAT) {
+    const int dq = t.dims[lf.dim_off];
+    const int L = lf.ard;
+    e.k = p[t.nparams + lf.p0 + tree_level(xi[dq], L) * L + tree_level(xj[dq], L)];
+    e.r2 = 0.0f;
+    e.h = 0.0f;
+    return e;
+  }
   if (lf.kind == KIND_PERIODIC) {
     const float period = p[lf.p0 + (lf.ard ? lf.ndim : 1)];
     const float os = p[lf.p0 + (lf.ard ? lf.ndim : 1) + 1];
@@ -183,6 +209,7 @@ __device__ __forceinline__ void tree_grad_accumulate(const KernelTree& t,
       const int l = nd.a;
       const TreeLeaf& lf = t.leaf[l];
       const LeafEval& e = le[l];
+      if (lf.kind == KIND_CAT) continue;  // tables are learned outside this pass
       const int nls = lf.ard ? lf.ndim : 1;
       if (lf.kind == KIND_PERIODIC) {
         const float period = p[lf.p0 + nls];
@@ -222,6 +249,32 @@ __device__ __forceinline__ void tree_grad_accumulate(const KernelTree& t,
         ios += 1;
       }
       g[ios] += a * e.k / p[ios];
+    }
+  }
+}
+
+// Adjoint w dK/dv_l of every leaf value v_l at one pair (leaf_adj[nleaves]).
+__device__ __forceinline__ void tree_leaf_adjoints(const KernelTree& t,
+                                                   const float* __restrict__ p,
+                                                   const float* xi, const float* xj, float w,
+                                                   float* leaf_adj) {
+  float val[kTreeMaxNodes], adj[kTreeMaxNodes];
+  tree_value(t, p, xi, xj, nullptr, val);
+  for (int i = 0; i < t.nnodes; ++i) adj[i] = 0.0f;
+  adj[t.nnodes - 1] = w;
+  for (int i = t.nnodes - 1; i >= 0; --i) {
+    const TreeNode& nd = t.node[i];
+    const float a = adj[i];
+    if (nd.code == TN_ADD) {
+      adj[nd.a] += a;
+      adj[nd.b] += a;
+    } else if (nd.code == TN_MUL) {
+      adj[nd.a] += a * val[nd.b];
+      adj[nd.b] += a * val[nd.a];
+    } else if (nd.code == TN_SCALE) {
+      adj[nd.a] += a * p[nd.b];
+    } else {
+      leaf_adj[nd.a] = a;
     }
   }
 }

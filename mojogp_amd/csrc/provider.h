@@ -40,6 +40,9 @@ struct Provider {
   bool is_tree = false;
   KernelTree tree;
   DevBuf<float> tparams;
+  // Categorical correlation tables of the tree's categorical leaves
+  // (tree.table_size entries, placed after the parameters in tparams).
+  std::vector<float> cat_tables;
 
   hipStream_t st = nullptr;
   DevBuf<float> X;             // raw training inputs [n][d]

@@ -13,9 +13,13 @@ void Provider::refresh_coords() {
     for (int q = 0; q < nparams; ++q)
       MGP_REQUIRE(std::isfinite(params[q]) && params[q] > 0.f,
                   "kernel tree parameters must be finite and > 0");
-    tparams.ensure((size_t)nparams);
+    tparams.ensure((size_t)nparams + (size_t)tree.table_size);
     MGP_HIP_CHECK(hipMemcpyAsync(tparams.ptr, params.data(), (size_t)nparams * sizeof(float),
                                  hipMemcpyHostToDevice, st));
+    if (tree.table_size > 0)
+      MGP_HIP_CHECK(hipMemcpyAsync(tparams.ptr + nparams, cat_tables.data(),
+                                   (size_t)tree.table_size * sizeof(float),
+                                   hipMemcpyHostToDevice, st));
     pack(X.ptr, n, train);
     if (materialized) fill_dense();
     MGP_HIP_CHECK(hipStreamSynchronize(st));  // params may change after return

@@ -139,6 +139,77 @@ __global__ __launch_bounds__(256) void k_tree_grad_trace(
   }
 }
 
+// part[(y*gx + x)*table_size + e] = sum over the block's pairs (a, b) of
+// w_ab dK_ab/dv_l at table entry e = p0_l + level_a * L + level_b of every
+// categorical leaf l, with w_ab = sum_c Lf[c][a] Rf[c][b].
+__global__ __launch_bounds__(256) void k_tree_cat_grad(
+    const float* __restrict__ X, int64_t n, KernelTree t, const float* __restrict__ p,
+    const float* __restrict__ Lf, const float* __restrict__ Rf, int ncols, int c0,
+    double* __restrict__ part) {
+  __shared__ float xb[64][kTreeMaxInputDim];
+  __shared__ float rb[64][kGradCols];
+  __shared__ float tab[kTreeMaxTable];
+  const int d = t.d;
+  const int cn = min(kGradCols, ncols - c0);
+  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = a < n;
+  for (int e = threadIdx.x; e < t.table_size; e += blockDim.x) tab[e] = 0.0f;
+  float xa[kTreeMaxInputDim], la[kGradCols];
+  for (int k = 0; k < d; ++k) xa[k] = live ? X[a * d + k] : 0.0f;
+  for (int c = 0; c < kGradCols; ++c) la[c] = (live && c < cn) ? Lf[(int64_t)(c0 + c) * n + a] : 0.0f;
+  float acc[kTreeMaxCatRow];
+  for (int q = 0; q < kTreeMaxCatRow; ++q) acc[q] = 0.0f;
+  const int64_t tiles = (n + 63) / 64;
+  const int64_t tps = (tiles + gridDim.y - 1) / gridDim.y;
+  const int64_t jb = min(n, (int64_t)blockIdx.y * tps * 64);
+  const int64_t je = min(n, jb + tps * 64);
+  for (int64_t b0 = jb; b0 < je; b0 += 64) {
+    __syncthreads();
+    for (int q = threadIdx.x; q < 64 * kTreeMaxInputDim; q += blockDim.x) {
+      const int bb = q / kTreeMaxInputDim, k = q - bb * kTreeMaxInputDim;
+      const int64_t b = b0 + bb;
+      xb[bb][k] = (b < je && k < d) ? X[b * d + k] : 0.0f;
+    }
+    for (int q = threadIdx.x; q < 64 * kGradCols; q += blockDim.x) {
+      const int bb = q / kGradCols, c = q - bb * kGradCols;
+      const int64_t b = b0 + bb;
+      rb[bb][c] = (b < je && c < cn) ? Rf[(int64_t)(c0 + c) * n + b] : 0.0f;
+    }
+    __syncthreads();
+    const int cnt = (int)min((int64_t)64, je - b0);
+    if (live) {
+      for (int bb = 0; bb < cnt; ++bb) {
+        float w = 0.0f;
+        for (int c = 0; c < kGradCols; ++c) w = fmaf(la[c], rb[bb][c], w);
+        float ladj[kTreeMaxLeaves];
+        tree_leaf_adjoints(t, p, xa, xb[bb], w, ladj);
+        int off = 0;
+        for (int l = 0; l < t.nleaves; ++l) {
+          const TreeLeaf& lf = t.leaf[l];
+          if (lf.kind != KIND_CAT) continue;
+          acc[off + tree_level(xb[bb][t.dims[lf.dim_off]], lf.ard)] += ladj[l];
+          off += lf.ard;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (live) {
+    int off = 0;
+    for (int l = 0; l < t.nleaves; ++l) {
+      const TreeLeaf& lf = t.leaf[l];
+      if (lf.kind != KIND_CAT) continue;
+      const int L = lf.ard;
+      const int row = lf.p0 + tree_level(xa[t.dims[lf.dim_off]], L) * L;
+      for (int lb = 0; lb < L; ++lb) atomicAdd(&tab[row + lb], acc[off + lb]);
+      off += L;
+    }
+  }
+  __syncthreads();
+  double* dst = part + ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * t.table_size;
+  for (int e = threadIdx.x; e < t.table_size; e += blockDim.x) dst[e] = (double)tab[e];
+}
+
 }  // namespace
 
 KernelTree parse_kernel_tree(const int* spec, int len) {
@@ -157,7 +228,7 @@ KernelTree parse_kernel_tree(const int* spec, int len) {
   require(t.nparams >= 1 && t.nparams <= kTreeMaxParams, "kernel tree has too many parameters");
   require(t.nleaves >= 1 && t.nleaves <= kTreeMaxLeaves, "kernel tree needs 1..8 leaves");
   require(t.nnodes >= 1 && t.nnodes <= kTreeMaxNodes, "kernel tree needs 1..16 nodes");
-  int doff = 0;
+  int doff = 0, cat_levels = 0;
   for (int l = 0; l < t.nleaves; ++l) {
     TreeLeaf& lf = t.leaf[l];
     lf.kind = next();
@@ -165,18 +236,30 @@ KernelTree parse_kernel_tree(const int* spec, int len) {
     lf.ndim = next();
     lf.p0 = next();
     lf.dim_off = doff;
-    require(lf.kind >= KIND_RBF && lf.kind <= KIND_PERIODIC, "unknown kernel tree leaf kind");
+    require(lf.kind >= KIND_RBF && lf.kind <= KIND_CAT, "unknown kernel tree leaf kind");
     require(lf.ndim >= 1 && doff + lf.ndim <= kTreeMaxDims, "kernel tree leaf dimensions");
     for (int q = 0; q < lf.ndim; ++q) {
       const int dq = next();
       require(dq >= 0 && dq < t.d, "kernel tree leaf dimension out of range");
       t.dims[doff++] = dq;
     }
+    if (lf.kind == KIND_CAT) {
+      require(lf.ndim == 1, "a categorical leaf reads one input column");
+      require(lf.ard >= 2 && lf.ard <= kTreeMaxLevels, "categorical leaves need 2..32 levels");
+      require(lf.p0 >= 0 && lf.p0 + lf.ard * lf.ard <= kTreeMaxTable,
+              "categorical tables exceed 1024 entries");
+      t.table_size = std::max(t.table_size, lf.p0 + lf.ard * lf.ard);
+      t.ncat += 1;
+      cat_levels += lf.ard;
+      continue;
+    }
     const int nls = lf.ard ? lf.ndim : 1;
     const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1 : 0;
     require(lf.p0 >= 0 && lf.p0 + nls + extra + 1 <= t.nparams,
             "kernel tree leaf parameters out of range");
   }
+  require(cat_levels <= kTreeMaxCatRow, "categorical leaves exceed 64 levels in total");
+  int leaf_uses[kTreeMaxLeaves] = {0};
   for (int i = 0; i < t.nnodes; ++i) {
     TreeNode& nd = t.node[i];
     nd.code = next();
@@ -185,6 +268,7 @@ KernelTree parse_kernel_tree(const int* spec, int len) {
     switch (nd.code) {
       case TN_LEAF:
         require(nd.a >= 0 && nd.a < t.nleaves, "kernel tree leaf node index");
+        require(++leaf_uses[nd.a] == 1, "a kernel tree leaf appears in more than one node");
         break;
       case TN_ADD:
       case TN_MUL:
@@ -199,6 +283,8 @@ KernelTree parse_kernel_tree(const int* spec, int len) {
     }
   }
   require(pos == len, "kernel tree spec has trailing entries");
+  for (int l = 0; l < t.nleaves; ++l)
+    require(leaf_uses[l] == 1, "every kernel tree leaf needs one leaf node");
   return t;
 }
 
@@ -206,7 +292,9 @@ double tree_diag(const KernelTree& t, const float* params) {
   std::vector<double> v((size_t)t.nnodes);
   for (int i = 0; i < t.nnodes; ++i) {
     const TreeNode& nd = t.node[i];
-    if (nd.code == TN_LEAF) {
+    if (nd.code == TN_LEAF && t.leaf[nd.a].kind == KIND_CAT) {
+      v[i] = 1.0;  // every correlation table has a unit diagonal
+    } else if (nd.code == TN_LEAF) {
       const TreeLeaf& lf = t.leaf[nd.a];
       const int nls = lf.ard ? lf.ndim : 1;
       const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1 : 0;
@@ -242,6 +330,31 @@ void tree_fill(const KernelTree& t, const float* p_dev, const float* Xr, int64_t
   hipLaunchKernelGGL(k_tree_fill, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, Xr,
                      r0, rows, Xc, n, t, p_dev, out);
   MGP_HIP_CHECK(hipGetLastError());
+}
+
+void tree_cat_grad_tables(const KernelTree& t, const float* p_dev, const float* X, int64_t n,
+                          const float* Lf, const float* Rf, int ncols, double* G_host,
+                          hipStream_t st) {
+  const int S = t.table_size;
+  for (int e = 0; e < S; ++e) G_host[e] = 0.0;
+  if (S == 0) return;
+  const int64_t rows = ceil_div(n, 256);
+  const int splits = (int)std::max<int64_t>(
+      1, std::min<int64_t>(ceil_div(2048, rows), ceil_div(n, 1024)));
+  const int64_t nblk = rows * splits;
+  DevBuf<double> part;
+  part.ensure((size_t)nblk * S);
+  std::vector<double> hp((size_t)nblk * S);
+  for (int c0 = 0; c0 < ncols; c0 += kGradCols) {
+    hipLaunchKernelGGL(k_tree_cat_grad, dim3((unsigned)rows, (unsigned)splits), dim3(256), 0, st,
+                       X, n, t, p_dev, Lf, Rf, ncols, c0, part.ptr);
+    MGP_HIP_CHECK(hipGetLastError());
+    MGP_HIP_CHECK(hipMemcpyAsync(hp.data(), part.ptr, hp.size() * sizeof(double),
+                                 hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    for (int64_t b = 0; b < nblk; ++b)
+      for (int e = 0; e < S; ++e) G_host[e] += hp[(size_t)b * S + e];
+  }
 }
 
 void tree_grad_traces(const KernelTree& t, const float* p_dev, const float* X, int64_t n,

@@ -23,7 +23,7 @@ from typing import Any, Optional, Tuple, Union
 import numpy as np
 
 from . import _engine
-from .kernel import KernelNode, KernelType, make_ard_kernel
+from .kernel import KernelNode, KernelType, cat_default_raw_param, make_ard_kernel
 
 _MODEL_SCHEMA_VERSION = 1
 _DEFAULT_PREDICT_LANCZOS_RANK = 100
@@ -116,6 +116,14 @@ class TrainingResult:
 
 
 @dataclass
+class MixedTrainingResult(TrainingResult):
+    """TrainingResult of a mixed continuous x categorical model: ``params``
+    in the public layout (categorical slots at their defaults), ``cat_params``
+    the trained raw categorical parameters (gp.py:2405-2418)."""
+    cat_params: Optional[np.ndarray] = None
+
+
+@dataclass
 class PredictionResult:
     mean: np.ndarray
     variance: np.ndarray
@@ -126,14 +134,25 @@ class PredictionResult:
 # Provider noise modes of the learned per-sample models (fn_ptr_module.py:297-327).
 _LEARNED_NOISE_MODES = {"learned_vector": 2, "learned_grouped": 3, "learned_input_dependent": 4}
 
-def _check_served(kernel: KernelNode, dim: int) -> None:
+
+def _cat_kernel_summary(specs, cat_dims):
+    """The reference's cat_kernel config value: one name when every
+    categorical leaf uses the same family, else a column -> name map."""
+    if not specs:
+        return "ehh"
+    names = [sp["kernel_type"] for sp in specs]
+    if len(set(names)) == 1:
+        return names[0]
+    return {str(col): nm for col, nm in zip(cat_dims, names)}
+
+def _check_served(kernel: KernelNode, dim: int, default_dims=None) -> None:
     """Raise NotImplementedError for kernels the gfx950 engine does not serve
     (single RBF / Matern leaves run on the tile path, other stationary trees
-    on the kernel-tree products)."""
+    and mixed categorical trees on the kernel-tree products)."""
     if kernel.is_native_leaf():
         kernel.native_kind()
     else:
-        kernel.to_tree_spec(dim)
+        kernel.to_tree_spec(dim, default_dims)
 
 class SingleOutputGP:
     """Exact Gaussian process regression on one MI355X.
@@ -192,6 +211,11 @@ class SingleOutputGP:
         self._noise_group_values: Optional[np.ndarray] = None
         self._observation_noise_fn = None
         self._noise_function_params: Optional[np.ndarray] = None
+        # mixed continuous x categorical models
+        self.cat_dims: dict = {}
+        self._cat_specs: list = []
+        self._cont_cols: Optional[list] = None
+        self._cat_params_raw: Optional[np.ndarray] = None
 
     # ------------------------------------------------------------ properties
     @property
@@ -224,8 +248,41 @@ class SingleOutputGP:
     # ------------------------------------------------------------ lifecycle
     def _ensure_compiled(self) -> None:
         if self._kernel_module is None or self._engine is None:
-            self._kernel_module = _engine.load_kernel_module(self.kernel, False, self.dim)
+            cont = self._cont_cols if self.kernel.has_categorical() else None
+            self._kernel_module = _engine.load_kernel_module(self.kernel, False, self.dim,
+                                                             default_dims=cont)
             self._engine = _engine.load_engine()
+
+    def _resolve_mixed(self, X) -> None:
+        """Categorical columns, levels and continuous columns of a mixed kernel
+        (analyze_kernel_tree, kernel.py:1118-1166, gp.py:1176-1206); levels
+        must be integer codes in [0, L)."""
+        leaves = self._kernel_pre_ard.categorical_leaves()
+        self.cat_dims, self._cat_specs = {}, []
+        for lf in leaves:
+            col = int(lf.active_dims[0])
+            if col in self.cat_dims:
+                raise ValueError(f"input column {col} has more than one categorical kernel")
+            self.cat_dims[col] = int(lf.levels)
+            self._cat_specs.append({"levels": int(lf.levels),
+                                    "kernel_type": lf.kernel_type.name.lower()})
+        for col, L in self.cat_dims.items():
+            if col >= X.shape[1]:
+                raise ValueError(f"categorical column {col} out of range")
+            v = X[:, col]
+            if np.any(v != np.round(v)) or np.any(v < 0) or np.any(v >= L):
+                raise ValueError(f"column {col} must hold integer levels in [0, {L})")
+        self._cont_cols = [c for c in range(X.shape[1]) if c not in self.cat_dims]
+        if not self._cont_cols:
+            raise ValueError("Pure categorical kernels (all dimensions categorical, no "
+                             "continuous) are not supported")
+
+    def _set_categorical_tables(self, info) -> None:
+        raw = getattr(self, "_cat_params_raw", None)
+        if raw is None or not self.kernel.has_categorical():
+            return
+        kinds = [_engine.Engine._CAT_KIND[s["kernel_type"]] for s in self._cat_specs]
+        _engine._provider(info).set_categorical_params(kinds, raw)
 
     def _destroy_prediction_cache(self) -> None:
         if self._prediction_cache_handle and self._engine is not None:
@@ -269,6 +326,8 @@ class SingleOutputGP:
                                                  float(noise), observation_noise=obs,
                                                  noise_mode=mode, noise_group_train=groups,
                                                  num_noise_groups=ngroups)
+        if not training:
+            self._set_categorical_tables(info)
         if (method or self._training_method) == "materialized":
             self._kernel_module.materialize(info)
         return info
@@ -370,8 +429,16 @@ class SingleOutputGP:
         self.dim = X.shape[1]
         self._noise_floor = float(noise_floor)
         self._noise_regularization = float(noise_regularization)
-        self.kernel = make_ard_kernel(self._kernel_pre_ard, self.dim) if self.ard else self._kernel_pre_ard
-        _check_served(self.kernel, self.dim)  # rejects kernels outside the engine
+        mixed = self._kernel_pre_ard.has_categorical()
+        self._cat_params_raw = None
+        if mixed:
+            self._resolve_mixed(X)
+            if noise_mode != "scalar":
+                raise NotImplementedError("mixed categorical models train with scalar noise")
+        cont_dim = len(self._cont_cols) if mixed else self.dim
+        self.kernel = (make_ard_kernel(self._kernel_pre_ard, cont_dim) if self.ard
+                       else self._kernel_pre_ard)
+        _check_served(self.kernel, self.dim, self._cont_cols if mixed else None)
         self._kernel_module = None
         self._engine = None
 
@@ -433,6 +500,11 @@ class SingleOutputGP:
                                      precond_rebuild_threshold=resolved_threshold,
                                      precond=resolved_precond)
         init_mean = self._init_mean if self._init_mean is not None else float(np.mean(y))
+        if mixed:
+            return self._fit_mixed(X, y, initial_params, initial_noise, max_iterations,
+                                   learning_rate, resolved, enable_early_stopping,
+                                   early_stop_patience, early_stop_tol, _verbose, cg, progress,
+                                   progress_interval)
         result = self._fit_engine(X, y, initial_params, initial_noise, max_iterations,
                                   learning_rate, resolved, enable_early_stopping, _verbose, cg,
                                   use_cosine_lr, init_mean, use_preconditioner,
@@ -442,6 +514,56 @@ class SingleOutputGP:
             self.prepare_prediction_cache(variance_method="love",
                                           max_root_decomposition_size=prediction_cache_rank)
         return result
+
+    def _fit_mixed(self, X, y, initial_params, initial_noise, max_iterations, learning_rate,
+                   route, enable_early_stopping, early_stop_patience, early_stop_tol, verbose,
+                   cg, progress, progress_interval) -> MixedTrainingResult:
+        """gp.py:2281-2440: continuous kernel on the tree provider, categorical
+        tables from default raw parameters, split-Adam training."""
+        engine_params = self.kernel.to_engine_params(np.asarray(initial_params, np.float32))
+        self._destroy_provider_info()
+        self._provider_info = self._build_provider_info(X, engine_params, initial_noise, route,
+                                                        training=True)
+        self._provider_state_current = True
+        leaves = self.kernel.categorical_leaves()
+        cat_init = np.concatenate([
+            [cat_default_raw_param(lf.kernel_type, i, lf.levels) for i in range(lf.num_params())]
+            for lf in leaves]).astype(np.float32)
+        Cm = np.stack([X[:, int(lf.active_dims[0])] for lf in leaves], 1).astype(np.int32)
+        args = [self._provider_info, y.astype(np.float32), engine_params, float(initial_noise),
+                Cm, self._cat_specs, cat_init, max_iterations, float(learning_rate),
+                int(cg["num_probes"]), int(cg["max_cg_iter"]), float(cg["cg_tol"]),
+                int(cg["precond_rank"]), bool(verbose), 1 if route == "materialized" else 0,
+                int(cg["precond_method"]), bool(enable_early_stopping), int(early_stop_patience),
+                float(early_stop_tol)]
+        if callable(progress):
+            args.extend([progress, int(progress_interval)])
+        result = self._engine.train_mixed(*args)
+        self._is_trained = True
+        self._provider_state_current = False
+        self._invalidate_prediction_caches()
+        self._cat_params_raw = np.asarray(result["cat_params"], np.float32)
+        self._fitted_mean = self._engine_predict_mean = float(result["mean"])
+        nll_h = np.array(result["nll_history"], np.float32)
+        times = np.array(result["iter_times_ms"], np.float64)
+        cg_h = np.array(result["cg_iterations_history"], np.int32)
+        self._training_result = MixedTrainingResult(
+            params=self.kernel.from_engine_params(np.array(result["params"], np.float32)),
+            noise=float(result["noise"]), mean=float(result["mean"]), nll=float(result["nll"]),
+            iterations=int(result["iterations"]), converged=bool(result["converged"]),
+            lanczos_root=None, lanczos_rank=int(cg["max_tridiag_iter"]), nll_history=nll_h,
+            cg_iterations_history=cg_h, iter_times_ms=times, cat_params=self._cat_params_raw)
+        self._backend_train_info = {
+            "training_route": result["training_route"], "is_mixed": True,
+            "materialization_mode": int(result["materialization_mode"]),
+            "precond_method": int(result["precond_method"]),
+            "precond_rank": int(result["precond_rank"]), "noise_mode": "scalar",
+            "num_cat_vars": int(result["num_cat_vars"]),
+            "total_cat_params": int(result["total_cat_params"]),
+            "cat_dims": dict(self.cat_dims),
+            "cg_iterations_history": cg_h.tolist(), "iter_times_ms": times.tolist(),
+        }
+        return self._training_result
 
     def _resolve_noise_model(self, X, noise_model, observation_noise, observation_noise_fn,
                              noise_function, learn_noise, noise_floor, initial_noise,
@@ -952,9 +1074,11 @@ class SingleOutputGP:
         cfg = {
             "schema_version": _MODEL_SCHEMA_VERSION, "mojogp_version": __version__,
             "wrapper": "SingleOutputGP", "dim": int(self.dim), "ard": bool(self.ard),
-            "verbose": bool(self.verbose), "cat_dims": {}, "cat_kernel": "ehh",
+            "verbose": bool(self.verbose),
+            "cat_dims": {str(k): int(v) for k, v in self.cat_dims.items()},
+            "cat_kernel": _cat_kernel_summary(self._cat_specs, self.cat_dims),
             "kernel_mojo_type": self.kernel.to_mojo_type(),
-            "kernel_tree": self._original_kernel.to_dict(), "is_mixed": False,
+            "kernel_tree": self._original_kernel.to_dict(), "is_mixed": bool(self.cat_dims),
             "training_method": self._training_method,
             "engine_mean": self._engine_predict_mean,
             "backend_train_info": self._backend_train_info,
@@ -970,7 +1094,9 @@ class SingleOutputGP:
             "has_observation_noise_fn": self._observation_noise_fn is not None,
             "has_noise_group_train": self._noise_group_train is not None,
             "has_group_noise": self._noise_group_values is not None,
-            "result_type": "TrainingResult", "noise": float(tr.noise), "mean": float(tr.mean),
+            "result_type": ("MixedTrainingResult" if isinstance(tr, MixedTrainingResult)
+                            else "TrainingResult"),
+            "noise": float(tr.noise), "mean": float(tr.mean),
             "nll": float(tr.nll), "iterations": int(tr.iterations),
             "converged": bool(tr.converged), "lanczos_rank": int(tr.lanczos_rank),
         }
@@ -985,6 +1111,8 @@ class SingleOutputGP:
             arrays["noise_function_params"] = self._noise_function_params
         if self._noise_group_values is not None:
             arrays["group_noise"] = self._noise_group_values
+        if self._cat_params_raw is not None:
+            arrays["cat_params"] = self._cat_params_raw
         np.savez(path + "_arrays.npz", **arrays)
 
     @classmethod
@@ -1002,9 +1130,9 @@ class SingleOutputGP:
         if int(cfg.get("schema_version", 0)) != _MODEL_SCHEMA_VERSION:
             raise ValueError(f"Unsupported SingleOutputGP schema_version="
                              f"{cfg.get('schema_version')}; expected {_MODEL_SCHEMA_VERSION}.")
-        if cfg.get("is_mixed") or cfg.get("result_type", "TrainingResult") != "TrainingResult":
-            raise NotImplementedError("mixed continuous/categorical models are outside the "
-                                      "gfx950 engine")
+        if cfg.get("result_type", "TrainingResult") not in ("TrainingResult",
+                                                            "MixedTrainingResult"):
+            raise ValueError(f"unknown result_type {cfg.get('result_type')!r}")
         mode = cfg.get("noise_mode", "scalar")
         if mode not in ("scalar", "fixed_vector", "fixed_input_dependent", "fixed_grouped",
                         *_LEARNED_NOISE_MODES):
@@ -1020,7 +1148,12 @@ class SingleOutputGP:
         gp._X_train = np.ascontiguousarray(arr["X_train"], np.float32)
         gp._y_train = np.ascontiguousarray(arr["y_train"], np.float32)
         gp.dim = int(gp._X_train.shape[1])
-        gp.kernel = make_ard_kernel(gp._kernel_pre_ard, gp.dim) if gp.ard else gp._kernel_pre_ard
+        if gp._kernel_pre_ard.has_categorical():
+            gp._resolve_mixed(gp._X_train)
+            gp._cat_params_raw = np.ascontiguousarray(arr["cat_params"], np.float32)
+        cont_dim = len(gp._cont_cols) if gp.cat_dims else gp.dim
+        gp.kernel = (make_ard_kernel(gp._kernel_pre_ard, cont_dim) if gp.ard
+                     else gp._kernel_pre_ard)
         gp._training_method = cfg.get("training_method") or "matrix_free"
         gp._backend_train_info = cfg.get("backend_train_info") or {}
         gp._cached_love_method = cfg.get("cached_love_method")
@@ -1042,6 +1175,10 @@ class SingleOutputGP:
             mean=float(cfg.get("mean", 0.0)), nll=float(cfg["nll"]),
             iterations=int(cfg["iterations"]), converged=bool(cfg["converged"]),
             lanczos_root=None, lanczos_rank=int(cfg["lanczos_rank"]))
+        if gp._cat_params_raw is not None:
+            tr0 = gp._training_result
+            gp._training_result = MixedTrainingResult(**{**tr0.__dict__,
+                                                         "cat_params": gp._cat_params_raw})
         engine_mean = cfg.get("engine_mean")
         gp._engine_predict_mean = float(engine_mean if engine_mean is not None
                                         else gp._training_result.mean)

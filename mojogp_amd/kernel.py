@@ -37,6 +37,45 @@ class KernelType(Enum):
     LINEAR = "LinearComposable"
     RQ = "RQComposable"
     POLYNOMIAL = "PolynomialComposable"
+    GD = "GDCategorical"
+    CR = "CRCategorical"
+    EHH = "EHHCategorical"
+    HH = "HHCategorical"
+    FE = "FECategorical"
+
+
+# Categorical families (kernel.py:63-69 parameter counts; native kind codes of
+# the mixed training entry point: 0 GD, 1 CR, 2 EHH, 3 HH, 4 FE).
+CATEGORICAL_KINDS = {KernelType.GD: 0, KernelType.CR: 1, KernelType.EHH: 2, KernelType.HH: 3,
+                     KernelType.FE: 4}
+_CAT_PARAM_COUNTS = {
+    KernelType.GD: lambda L: 1,
+    KernelType.CR: lambda L: L,
+    KernelType.EHH: lambda L: L * (L - 1) // 2,
+    KernelType.HH: lambda L: L * (L - 1) // 2,
+    KernelType.FE: lambda L: L * (L + 1) // 2,
+}
+
+
+def _inv_softplus(x: float) -> float:
+    return float(np.log(np.expm1(x)))
+
+
+def _inv_sigmoid(x: float) -> float:
+    return float(np.log(x / (1.0 - x)))
+
+
+def cat_default_raw_param(kernel_type: KernelType, param_index: int, L: int) -> float:
+    """Default raw categorical parameter (kernel.py:84-101)."""
+    if kernel_type == KernelType.GD:
+        return _inv_softplus(0.5)
+    if kernel_type == KernelType.CR:
+        return _inv_softplus(0.3)
+    if kernel_type in (KernelType.EHH, KernelType.HH):
+        return _inv_sigmoid(0.25)
+    if kernel_type == KernelType.FE:
+        return _inv_sigmoid(0.25) if param_index < L * (L - 1) // 2 else _inv_softplus(0.3)
+    return 0.0
 
 
 # Families the native kernels implement (value = native kind code).
@@ -44,6 +83,7 @@ NATIVE_KINDS = {KernelType.RBF: 0, KernelType.MATERN52: 1, KernelType.MATERN12: 
                 KernelType.MATERN32: 3}
 # Leaf codes of the kernel-tree spec (radial kinds keep their codes).
 TREE_LEAF_CODES = {**NATIVE_KINDS, KernelType.RQ: 4, KernelType.PERIODIC: 5}
+_CAT_LEAF_CODE = 6
 _TN_LEAF, _TN_ADD, _TN_MUL, _TN_SCALE = 0, 1, 2, 3
 
 
@@ -58,6 +98,7 @@ class KernelNode:
     initial_values: Optional[Dict[str, float]] = None
     ard: bool = False
     active_dims: Optional[tuple] = None
+    levels: Optional[int] = None  # categorical leaves
 
     # ---------------------------------------------------------- composition
     def __add__(self, other: "KernelNode") -> "KernelNode":
@@ -99,14 +140,39 @@ class KernelNode:
     def is_native_leaf(self) -> bool:
         return self.kernel_type in NATIVE_KINDS and self.operator is None and self.active_dims is None
 
+    def is_categorical(self) -> bool:
+        return self.kernel_type in CATEGORICAL_KINDS
+
+    def has_categorical(self) -> bool:
+        if self.kernel_type is not None:
+            return self.is_categorical()
+        return bool((self.left and self.left.has_categorical())
+                    or (self.right and self.right.has_categorical()))
+
+    def categorical_leaves(self) -> List["KernelNode"]:
+        """Categorical leaves in tree order."""
+        if self.kernel_type is not None:
+            return [self] if self.is_categorical() else []
+        out = self.left.categorical_leaves() if self.left else []
+        return out + (self.right.categorical_leaves() if self.right else [])
+
+    def engine_num_params(self) -> int:
+        """Continuous parameters only (categorical leaves train separately,
+        kernel.py:462-480)."""
+        if self.kernel_type is not None:
+            return 0 if self.is_categorical() else self.num_params()
+        if self.operator == "scale":
+            return self.left.engine_num_params() + 1
+        return self.left.engine_num_params() + self.right.engine_num_params()
+
     def is_tree_servable(self) -> bool:
         """Every leaf is one of the stationary families the tree products serve."""
         if self.kernel_type is not None:
-            return self.kernel_type in TREE_LEAF_CODES
+            return self.kernel_type in TREE_LEAF_CODES or self.is_categorical()
         return bool(self.left.is_tree_servable()
                     and (self.operator == "scale" or self.right.is_tree_servable()))
 
-    def to_tree_spec(self, dim: int) -> List[int]:
+    def to_tree_spec(self, dim: int, default_dims=None) -> List[int]:
         """Flat integer spec of the native kernel-tree products.
 
         Layout: [d, nparams, nleaves, nnodes, per leaf (tree order): code, ard,
@@ -120,12 +186,21 @@ class KernelNode:
                 "Matern32, Matern52, RQ, Periodic under sum / product / scale)")
         leaves: List[List[int]] = []
         nodes: List[List[int]] = []
+        table = [0]
 
         def walk(node: "KernelNode", dims: tuple, offset: int):
             dims = node.active_dims if node.active_dims is not None else dims
             for x in dims:
                 if not 0 <= x < dim:
                     raise ValueError(f"active_dims index {x} out of range for {dim}-dimensional input")
+            if node.is_categorical():
+                if node.active_dims is None or len(node.active_dims) != 1 or not node.levels:
+                    raise ValueError("categorical kernels need levels and one active dim")
+                L = int(node.levels)
+                leaves.append([_CAT_LEAF_CODE, L, 1, table[0], int(node.active_dims[0])])
+                table[0] += L * L
+                nodes.append([_TN_LEAF, len(leaves) - 1, 0])
+                return len(nodes) - 1, offset
             if node.kernel_type is not None:
                 ard = node.ard_dim is not None
                 if ard and node.ard_dim != len(dims):
@@ -141,12 +216,16 @@ class KernelNode:
                 nodes.append([_TN_ADD if node.operator == "sum" else _TN_MUL, a, b])
                 return len(nodes) - 1, end
             if node.operator == "scale":
+                if node.left.has_categorical():
+                    raise ValueError("Cannot apply scale to a kernel tree containing categorical "
+                                     "nodes (kernel.py:1118-1128)")
                 a, mid = walk(node.left, dims, offset)
                 nodes.append([_TN_SCALE, a, mid])
                 return len(nodes) - 1, mid + 1
             raise ValueError(f"Unknown operator: {node.operator}")
 
-        _, nparams = walk(self, tuple(range(dim)), 0)
+        start = tuple(range(dim)) if default_dims is None else tuple(default_dims)
+        _, nparams = walk(self, start, 0)
         if (len(leaves) > 8 or len(nodes) > 16 or nparams > 48 or dim > 32
                 or sum(lf[2] for lf in leaves) > 64):
             raise NotImplementedError("kernel trees are served up to 8 leaves, 16 nodes, "
@@ -168,6 +247,10 @@ class KernelNode:
         return NATIVE_KINDS[self.kernel_type]
 
     def num_params(self) -> int:
+        if self.is_categorical():
+            if self.levels is None:
+                raise ValueError(f"Categorical kernel {self.kernel_type.name} requires levels")
+            return _CAT_PARAM_COUNTS[self.kernel_type](self.levels)
         if self.kernel_type is not None:
             if self.ard_dim is not None:
                 if self.kernel_type in (KernelType.PERIODIC, KernelType.RQ):
@@ -189,6 +272,12 @@ class KernelNode:
             base = self.kernel_type.name.lower()
             if prefix:
                 base = f"{prefix}_{base}"
+            if self.is_categorical():
+                col = (f"_col{self.active_dims[0]}"
+                       if self.active_dims is not None and len(self.active_dims) == 1 else "")
+                k = self.num_params()
+                return [f"{base}{col}_theta"] if k == 1 else [f"{base}{col}_theta_{i}"
+                                                               for i in range(k)]
             if self.ard_dim is not None:
                 names = [f"{base}_ls_{d}" for d in range(self.ard_dim)]
                 if self.kernel_type == KernelType.PERIODIC:
@@ -224,6 +313,11 @@ class KernelNode:
         return values
 
     def _fill_initial(self, values: np.ndarray, offset: int) -> int:
+        if self.is_categorical():
+            n = self.num_params()
+            for i in range(n):
+                values[offset + i] = cat_default_raw_param(self.kernel_type, i, self.levels or 2)
+            return offset + n
         if self.kernel_type is not None:
             n = self.num_params()
             if self.initial_values:
@@ -244,17 +338,32 @@ class KernelNode:
             return mid + 1
         return offset
 
+    def _public_slots(self) -> List[bool]:
+        """Per public parameter: True when it is an engine (continuous) one."""
+        if self.kernel_type is not None:
+            return [not self.is_categorical()] * self.num_params()
+        if self.operator == "scale":
+            return self.left._public_slots() + [True]
+        return self.left._public_slots() + self.right._public_slots()
+
     def to_engine_params(self, public_params) -> np.ndarray:
+        """Public layout -> engine layout: the continuous parameters in tree
+        order, categorical slots dropped (kernel.py:494-568)."""
         p = np.asarray(public_params, dtype=np.float32)
         if p.shape != (self.num_params(),):
             raise ValueError(f"public_params must have shape ({self.num_params()},), got {p.shape}")
-        return p.copy()
+        return p[np.array(self._public_slots(), dtype=bool)].copy()
 
     def from_engine_params(self, engine_params) -> np.ndarray:
+        """Engine layout -> public layout; categorical slots keep their
+        default initial values (kernel.py:511-526)."""
         p = np.asarray(engine_params, dtype=np.float32)
-        if p.shape != (self.num_params(),):
-            raise ValueError(f"engine_params must have shape ({self.num_params()},), got {p.shape}")
-        return p.copy()
+        if p.shape != (self.engine_num_params(),):
+            raise ValueError(f"engine_params must have shape ({self.engine_num_params()},), "
+                             f"got {p.shape}")
+        out = self.get_initial_params()
+        out[np.array(self._public_slots(), dtype=bool)] = p
+        return out
 
     # ---------------------------------------------------------- serialisation
     # Type names written into saved model configs ("kernel_mojo_type"); the
@@ -301,6 +410,8 @@ class KernelNode:
             d["ard"] = True
         if self.active_dims is not None:
             d["active_dims"] = list(self.active_dims)
+        if self.levels is not None:
+            d["levels"] = int(self.levels)
         return d
 
     @staticmethod
@@ -315,6 +426,7 @@ class KernelNode:
             initial_values=d.get("initial_values"),
             ard=d.get("ard", False),
             active_dims=tuple(d["active_dims"]) if "active_dims" in d else None,
+            levels=d.get("levels"),
         )
 
     # ---------------------------------------------------------- evaluation
@@ -390,6 +502,9 @@ def make_ard_kernel(kernel: KernelNode, dim: int) -> KernelNode:
 
     A leaf gets one lengthscale per dimension it sees: its own active_dims,
     else those of its nearest ancestor with active_dims, else ``dim``."""
+    if kernel.is_categorical():
+        return KernelNode(kernel_type=kernel.kernel_type, levels=kernel.levels,
+                          active_dims=kernel.active_dims)
     if kernel.active_dims is not None:
         dim = len(kernel.active_dims)
     if kernel.kernel_type is not None:
@@ -451,3 +566,36 @@ def Polynomial(degree: float = 3.0, offset: float = 1.0, outputscale: float = 1.
                ard: bool = False, active_dims: Optional[List[int]] = None) -> KernelNode:
     return _leaf(KernelType.POLYNOMIAL, ard, active_dims, degree=degree, offset=offset,
                  outputscale=outputscale)
+
+
+def _cat_leaf(kt: KernelType, levels: int, active_dims) -> KernelNode:
+    if active_dims is None or len(active_dims) != 1:
+        raise ValueError("categorical kernels take exactly one active dimension")
+    if int(levels) < 2:
+        raise ValueError("categorical kernels need at least 2 levels")
+    return KernelNode(kernel_type=kt, levels=int(levels), active_dims=tuple(active_dims))
+
+
+def GD(levels: int, active_dims: Optional[List[int]] = None) -> KernelNode:
+    """Gower-distance categorical kernel: R_ij = exp(-theta) off the diagonal."""
+    return _cat_leaf(KernelType.GD, levels, active_dims)
+
+
+def CR(levels: int, active_dims: Optional[List[int]] = None) -> KernelNode:
+    """Continuous-relaxation kernel: R_ij = exp(-(theta_i + theta_j))."""
+    return _cat_leaf(KernelType.CR, levels, active_dims)
+
+
+def EHH(levels: int, active_dims: Optional[List[int]] = None) -> KernelNode:
+    """Exponential homoscedastic hypersphere kernel."""
+    return _cat_leaf(KernelType.EHH, levels, active_dims)
+
+
+def HH(levels: int, active_dims: Optional[List[int]] = None) -> KernelNode:
+    """Homoscedastic hypersphere kernel: R = C C^T."""
+    return _cat_leaf(KernelType.HH, levels, active_dims)
+
+
+def FE(levels: int, active_dims: Optional[List[int]] = None) -> KernelNode:
+    """Fully exponential kernel (hypersphere angles plus per-level terms)."""
+    return _cat_leaf(KernelType.FE, levels, active_dims)

@@ -303,7 +303,7 @@ def bbmm_step(kind: int, ard: bool, X, y_c, params, noise: float, P: Precond | N
     rowdot = -0.5 * alpha * alpha + (0.5 / max(T, 1)) * np.sum(U * W, axis=1)
     return {"nll": nll, "inv_quad": inv_quad, "logdet": logdet, "grads": np.array(grads),
             "alpha": alpha, "x": x, "cg_iterations": iters, "converged": conv,
-            "rowdot": rowdot}
+            "rowdot": rowdot, "U": U, "Zn": Zn}
 
 
 # ---------------------------------------------------------------- learned noise
@@ -673,3 +673,135 @@ def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=
         iters.append(it)
     return var, rank, iters
 
+
+
+# ---------------------------------------------------------------- mixed training
+def train_mixed(node: dict, X, y, init_params, init_noise: float, cat_specs, init_cat_raw, *,
+                default_dims=None, max_iterations=20, learning_rate=0.01, num_probes=10,
+                max_cg=100, cg_tol=1e-2, precond_rank=10, max_tridiag=30,
+                rebuild_threshold=0.5, use_cosine_lr=True, init_mean=0.0):
+    """Split-Adam training of a mixed continuous x categorical tree
+    (kernels/jit/jit_mixed.mojo:428-909, binding defaults of
+    jit_engine_bindings.mojo:1241-1460: cosine rate, mean from 0, 30 Lanczos
+    steps, rebuild threshold 0.5, preconditioner on).
+
+    Continuous parameters, noise and mean step as in ``train`` (without the
+    NaN restore); categorical raw parameters (cat_specs: (kind, L) per leaf,
+    oracle.categorical codes) get dNLL/dtheta_k = -0.5 alpha^T dK_k alpha +
+    (0.5/S) sum_s (K^-1 z_s)^T dK_k zn_s with the unit-norm probes zn_s, not
+    divided by n, clipped, chained through their transforms and stepped by
+    their own Adam (raw clamp +-20)."""
+    from . import categorical as oc
+    X = np.asarray(X, np.float64)
+    y = np.asarray(y, np.float64)
+    n = X.shape[0]
+    Pn = len(init_params)
+    sizes = [oc.num_params(k, L) for k, L in cat_specs]
+    offs = np.cumsum([0] + sizes)
+
+    def tables(rc):
+        return [oc.correlation(k, L, oc.constrain(k, L, rc[offs[i]:offs[i + 1]]))
+                for i, (k, L) in enumerate(cat_specs)]
+
+    raw = np.array([_inv_softplus(v) for v in init_params] + [_inv_softplus(init_noise)], F32)
+    rcat = np.asarray(init_cat_raw, F32).copy()
+    raw_mean = F32(init_mean)
+    m = np.zeros(Pn + 1, F32)
+    v = np.zeros(Pn + 1, F32)
+    mc = np.zeros(rcat.size, F32)
+    vc = np.zeros(rcat.size, F32)
+    mm = vm = F32(0)
+    t = tc = 0
+    best = dict(nll=np.inf, raw=raw.copy(), cat=rcat.copy(), mean=raw_mean)
+    lr = F32(learning_rate)
+
+    def tree(rc):
+        return ok.TreeKernel(node, X.shape[1], tables(rc), default_dims)
+
+    def build(T, params, noise):
+        if precond_rank <= 0:
+            return None
+        L, _ = pivoted_cholesky(T.matrix(X, X, params), precond_rank)
+        return Precond(L, noise)
+
+    T0 = tree(rcat)
+    P = build(T0, np.asarray(init_params, np.float64), init_noise)
+    last_params, last_noise = np.asarray(init_params, F32).copy(), F32(init_noise)
+    x_prev = None
+    nll_hist = []
+    for it in range(max_iterations):
+        params = np.array([_softplus(r) for r in raw[:Pn]], F32)
+        noise = _softplus(raw[Pn])
+        T = tree(rcat)
+        if it > 0:
+            rel = float((np.abs(params - last_params)
+                         / np.maximum(np.abs(last_params), 1e-8)).max())
+            rel = max(rel, abs(noise - last_noise) / max(abs(last_noise), 1e-8))
+            if rel > rebuild_threshold:
+                P = build(T, params.astype(np.float64), float(noise))
+                last_params, last_noise = params.copy(), noise
+        y_c = (y.astype(F32) - raw_mean).astype(np.float64)
+        warm = None
+        if it > 0 and x_prev is not None:
+            warm = x_prev.copy()
+            warm[:, 1:] = 0.0
+        res = bbmm_step(T, False, X, y_c, params.astype(np.float64), float(noise), P,
+                        num_probes, max_cg, max_tridiag, cg_tol, it, warm)
+        x_prev = res["x"]
+        nll = res["nll"]
+        if np.isnan(nll):
+            lr = lr * F32(0.5)
+            continue
+        if nll < best["nll"]:
+            best.update(nll=nll, raw=raw.copy(), cat=rcat.copy(), mean=raw_mean)
+        lr_eff = lr
+        if use_cosine_lr:
+            lr_min = learning_rate / 20.0
+            lr_eff = F32(lr_min + 0.5 * (learning_rate - lr_min)
+                         * (1.0 + np.cos(np.pi * it / max(max_iterations, 1))))
+        g = res["grads"].astype(F32)
+        for q in range(Pn + 1):
+            gr = _clip(g[q]) * _softplus_deriv(raw[q])
+            m[q] = F32(0.9) * m[q] + F32(0.1) * gr
+            v[q] = F32(0.999) * v[q] + F32(0.001) * gr * gr
+        t += 1
+        bc1 = F32(1) - F32(0.9) ** t
+        bc2 = F32(1) - F32(0.999) ** t
+        for q in range(Pn + 1):
+            nr = raw[q] - lr_eff * (m[q] / bc1) / (np.sqrt(v[q] / bc2) + F32(1e-8))
+            raw[q] = F32(min(max(nr, -20.0), 20.0))
+        mg = _clip(-np.sum(res["alpha"]) / n)
+        mm = F32(0.9) * mm + F32(0.1) * mg
+        vm = F32(0.999) * vm + F32(0.001) * mg * mg
+        raw_mean = F32(raw_mean - lr_eff * (mm / bc1) / (np.sqrt(vm / bc2) + F32(1e-8)))
+        if np.isnan(raw_mean) or abs(raw_mean) > 1000:
+            raw_mean = F32(init_mean)
+        # categorical step
+        D, lv = T.cat_leaf_derivatives(X, X, params.astype(np.float64))
+        alpha, U, Zn = res["alpha"], res["U"], res["Zn"]
+        gc = np.zeros(rcat.size, F32)
+        for i, (kind, L) in enumerate(cat_specs):
+            th = oc.constrain(kind, L, rcat[offs[i]:offs[i + 1]])
+            dR = oc.correlation_gradients(kind, L, th)
+            li, lj = lv[i]
+            for k in range(sizes[i]):
+                dK = D[i] * dR[k][li[:, None], lj[None, :]]
+                val = -0.5 * alpha @ dK @ alpha
+                if num_probes > 0:
+                    val += 0.5 / num_probes * np.sum(U * (dK @ Zn))
+                gc[offs[i] + k] = _clip(val)
+        chain = np.concatenate([oc.chain_derivative(k, L, rcat[offs[i]:offs[i + 1]])
+                                for i, (k, L) in enumerate(cat_specs)]).astype(F32)
+        tc += 1
+        cb1 = F32(1) - F32(0.9) ** tc
+        cb2 = F32(1) - F32(0.999) ** tc
+        gr = (gc * chain).astype(F32)
+        mc = (F32(0.9) * mc + F32(0.1) * gr).astype(F32)
+        vc = (F32(0.999) * vc + F32(0.001) * gr * gr).astype(F32)
+        rcat = np.clip(rcat - lr_eff * (mc / cb1) / (np.sqrt(vc / cb2) + F32(1e-8)),
+                       -20.0, 20.0).astype(F32)
+        nll_hist.append(nll)
+    return {"params": np.array([_softplus(r) for r in best["raw"][:Pn]], F32),
+            "noise": float(_softplus(best["raw"][Pn])), "mean": float(best["mean"]),
+            "final_nll": float(best["nll"]), "cat_raw": best["cat"].copy(),
+            "nll_history": np.array(nll_hist)}

@@ -176,16 +176,28 @@ PERIODIC_LEAF = "PERIODIC"
 _RADIAL_NAMES = {"RBF": RBF, "MATERN52": MATERN52, "MATERN12": MATERN12, "MATERN32": MATERN32}
 
 
+CAT_LEAVES = ("GD", "CR", "EHH", "HH", "FE")
+
+
 class TreeKernel:
     """A kernel tree given as nested dicts (``kernel_type`` or ``operator``,
-    ``left`` / ``right``, ``ard_dim``, ``active_dims``) over ``dim`` inputs."""
+    ``left`` / ``right``, ``ard_dim``, ``active_dims``, ``levels``) over ``dim``
+    inputs.  Categorical leaves (mixed kernels, codegen_engine/expressions.py:
+    493-516) take no tree parameters: their value is R[l_i, l_j] of the table
+    in ``cat_tables`` (one L x L matrix per categorical leaf, tree order), the
+    level index read from the leaf's input column.  Continuous leaves without
+    active_dims see ``default_dims`` (default: all inputs)."""
 
-    def __init__(self, node: dict, dim: int):
+    def __init__(self, node: dict, dim: int, cat_tables=None, default_dims=None):
         self.node = node
         self.dim = dim
+        self.cat_tables = [np.asarray(t, np.float64) for t in (cat_tables or [])]
+        self.default_dims = list(range(dim)) if default_dims is None else list(default_dims)
         self.nparams = self._count(node)
 
     def _count(self, nd) -> int:
+        if nd.get("kernel_type") in CAT_LEAVES:
+            return 0
         if "kernel_type" in nd:
             extra = 1 if nd["kernel_type"] in (RQ_LEAF, PERIODIC_LEAF) else 0
             return (nd.get("ard_dim") or 1) + extra + 1
@@ -210,22 +222,69 @@ class TreeKernel:
         p = np.asarray(params, dtype=np.float64)
         if p.shape != (self.nparams,):
             raise ValueError(f"tree expects {self.nparams} parameters, got {p.shape}")
-        K, G, _ = self._node(self.node, X1, X2, p, 0, grads)
+        self._cat_i = 0
+        self._cat_d = []
+        K, G, _ = self._node(self.node, X1[:, self.default_dims], X2[:, self.default_dims], p, 0,
+                             grads, X1, X2)
         return K, G
 
-    def _node(self, nd, X1, X2, p, off, grads):
+    def cat_leaf_derivatives(self, X1, X2, params):
+        """dK/dv_l per pair for every categorical leaf l (tree order), each
+        (n1, n2), with the levels (l_i, l_j) of the leaf's column."""
+        X1 = np.atleast_2d(np.asarray(X1, dtype=np.float64))
+        X2 = np.atleast_2d(np.asarray(X2, dtype=np.float64))
+        self._cat_i = 0
+        self._cat_d = []
+        _, _, _, D = self._nodeD(self.node, X1[:, self.default_dims], X2[:, self.default_dims],
+                                 np.asarray(params, np.float64), 0, X1, X2)
+        return [D[k] for k in sorted(D)], self._cat_d
+
+    def _nodeD(self, nd, X1, X2, p, off, F1, F2):
+        """(K, None, next_offset, {cat leaf index: dK/dv})."""
+        if nd.get("kernel_type") in CAT_LEAVES:
+            k = self._cat_i
+            self._cat_i += 1
+            col = int(nd["active_dims"][0])
+            li, lj = F1[:, col].astype(int), F2[:, col].astype(int)
+            self._cat_d.append((li, lj))
+            K = self.cat_tables[k][li[:, None], lj[None, :]]
+            return K, None, off, {k: np.ones_like(K)}
         if nd.get("active_dims") is not None:
             cols = list(nd["active_dims"])
-            X1, X2 = X1[:, cols], X2[:, cols]
+            X1, X2 = F1[:, cols], F2[:, cols]
+        if "kernel_type" in nd:
+            n = self._count(nd)
+            K, _ = _tree_leaf(nd, X1, X2, p[off:off + n], False)
+            return K, None, off + n, {}
+        A, _, mid, DA = self._nodeD(nd["left"], X1, X2, p, off, F1, F2)
+        if nd["operator"] == "scale":
+            c = p[mid]
+            return c * A, None, mid + 1, {k: c * v for k, v in DA.items()}
+        B, _, end, DB = self._nodeD(nd["right"], X1, X2, p, mid, F1, F2)
+        if nd["operator"] == "sum":
+            return A + B, None, end, {**DA, **DB}
+        return (A * B, None, end, {**{k: v * B for k, v in DA.items()},
+                                   **{k: A * v for k, v in DB.items()}})
+
+    def _node(self, nd, X1, X2, p, off, grads, F1=None, F2=None):
+        if nd.get("kernel_type") in CAT_LEAVES:
+            k = self._cat_i
+            self._cat_i += 1
+            col = int(nd["active_dims"][0])
+            li, lj = F1[:, col].astype(int), F2[:, col].astype(int)
+            return self.cat_tables[k][li[:, None], lj[None, :]], ([] if grads else None), off
+        if nd.get("active_dims") is not None:
+            cols = list(nd["active_dims"])
+            X1, X2 = F1[:, cols], F2[:, cols]
         if "kernel_type" in nd:
             n = self._count(nd)
             K, G = _tree_leaf(nd, X1, X2, p[off:off + n], grads)
             return K, G, off + n
-        A, GA, mid = self._node(nd["left"], X1, X2, p, off, grads)
+        A, GA, mid = self._node(nd["left"], X1, X2, p, off, grads, F1, F2)
         if nd["operator"] == "scale":
             c = p[mid]
             return c * A, ([c * g for g in GA] + [A] if grads else None), mid + 1
-        B, GB, end = self._node(nd["right"], X1, X2, p, mid, grads)
+        B, GB, end = self._node(nd["right"], X1, X2, p, mid, grads, F1, F2)
         if nd["operator"] == "sum":
             return A + B, (GA + GB if grads else None), end
         return A * B, ([g * B for g in GA] + [A * g for g in GB] if grads else None), end
