@@ -317,6 +317,14 @@ int mgp_set_noise_vector(void* h, const float* noise_vec) {
 int mgp_extract_diagonal(void* h, float* out) {
   return guarded([&] {
     Provider* pv = as_provider(h);
+    if (pv->nonstationary()) {
+      DevBuf<float> d;
+      pv->diag_values(pv->train, pv->n, d.ensure((size_t)pv->n));
+      MGP_HIP_CHECK(hipMemcpyAsync(out, d.ptr, (size_t)pv->n * sizeof(float),
+                                   hipMemcpyDeviceToHost, pv->st));
+      MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+      return;
+    }
     const float os = pv->kdiag();
     for (int64_t i = 0; i < pv->n; ++i) out[i] = os;
   });
@@ -325,7 +333,19 @@ int mgp_extract_diagonal(void* h, float* out) {
 int mgp_extract_diagonal_test(void* h, const float* Xs, int64_t m, float* out) {
   return guarded([&] {
     Provider* pv = as_provider(h);
-    (void)Xs;
+    if (pv->nonstationary()) {
+      MGP_REQUIRE(Xs != nullptr && m >= 1, "non-stationary diagonals need test points");
+      float* dx = pv->Xs.ensure((size_t)m * pv->d);
+      MGP_HIP_CHECK(hipMemcpyAsync(dx, Xs, (size_t)m * pv->d * sizeof(float),
+                                   hipMemcpyHostToDevice, pv->st));
+      pv->pack(dx, m, pv->test);
+      DevBuf<float> d;
+      pv->diag_values(pv->test, m, d.ensure((size_t)m));
+      MGP_HIP_CHECK(hipMemcpyAsync(out, d.ptr, (size_t)m * sizeof(float), hipMemcpyDeviceToHost,
+                                   pv->st));
+      MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+      return;
+    }
     const float os = pv->kdiag();
     for (int64_t i = 0; i < m; ++i) out[i] = os;
   });

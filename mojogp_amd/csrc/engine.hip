@@ -1139,9 +1139,9 @@ void lanczos_inv_root(Provider& pv, int r, PredictState& ps) {
 
 namespace {
 __global__ void k_exact_var(const double* __restrict__ dots, int C, float diag,
-                            float* __restrict__ var) {
+                            const float* __restrict__ dvec, float* __restrict__ var) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c < C) var[c] = fmaxf(diag - (float)dots[c], 1e-10f);
+  if (c < C) var[c] = fmaxf((dvec ? dvec[c] : diag) - (float)dots[c], 1e-10f);
 }
 }  // namespace
 
@@ -1172,6 +1172,8 @@ void exact_variance(Provider& pv, int64_t m, const ExactVarianceOptions& o, floa
   DevBuf<double> part, dots;
   CGWork w;
   const float os = pv.kdiag();
+  DevBuf<float> dself;  // per-test-point k(x*, x*) of non-stationary trees
+  if (pv.nonstationary()) pv.diag_values(pv.test, m, dself.ensure((size_t)m));
   for (int64_t s0 = 0; s0 < m; s0 += block) {
     const int C = (int)std::min<int64_t>(block, m - s0);
     const size_t nc = (size_t)n * C;
@@ -1195,7 +1197,7 @@ void exact_variance(Provider& pv, int64_t m, const ExactVarianceOptions& o, floa
     coldot_partial(kc, w.x.ptr, n, C, nb, pt, st);
     coldot_finalize(pt, nb, C, dd, st);
     hipLaunchKernelGGL(k_exact_var, dim3((unsigned)ceil_div(C, 256)), dim3(256), 0, st, dd, C,
-                       os, var_dev + s0);
+                       os, pv.nonstationary() ? dself.ptr + s0 : nullptr, var_dev + s0);
     MGP_HIP_CHECK(hipGetLastError());
   }
   MGP_HIP_CHECK(hipStreamSynchronize(st));
@@ -1225,7 +1227,10 @@ void predict_from_state(Provider& pv, const PredictState& ps, const float* Xs_ho
     Vs.ensure((size_t)ps.rank * m);
     var.ensure(m);
     pv.cross(pv.test, ps.root.ptr, ps.rank, Vs.ptr);
-    love_variance(Vs.ptr, m, ps.rank, pv.kdiag(), var.ptr, st);
+    DevBuf<float> dv;
+    if (pv.nonstationary()) pv.diag_values(pv.test, m, dv.ensure((size_t)m));
+    love_variance(Vs.ptr, m, ps.rank, pv.kdiag(), var.ptr, st,
+                  pv.nonstationary() ? dv.ptr : nullptr);
     MGP_HIP_CHECK(hipMemcpyAsync(var_out, var.ptr, m * sizeof(float), hipMemcpyDeviceToHost, st));
     MGP_HIP_CHECK(hipStreamSynchronize(st));
     t.variance_s = secs_since(t1);

@@ -15,6 +15,13 @@
 //   RBF / Matern     [ls | ls_0..ls_{q-1}], os
 //   RQ               [ls | ls_0..ls_{q-1}], alpha, os
 //   periodic         [ls | ls_0..ls_{q-1}], period, os
+//   linear           [variance | var_0..var_{q-1}], os:
+//                    os * var * x.x'  |  os * sum_q var_q x_q x'_q
+//   polynomial       [variance | var_0..var_{q-1}], degree, offset, os:
+//                    os * (var * x.x' + offset)^D (ARD: sum_q var_q x_q x'_q),
+//                    D the leaf's fixed integer degree (deg field); the
+//                    degree parameter slot is carried but not read
+//                    (expressions.py:57-71, 327-421)
 //   categorical      no parameters: the leaf value is R[l_i][l_j] of an L x L
 //                    correlation table (L in the leaf's ard field) stored at
 //                    table offset p0 after the nparams parameters; the leaf's
@@ -41,6 +48,8 @@ constexpr int kTreeMaxCatRow = 64;     // sum over categorical leaves of their l
 constexpr int KIND_RQ = 4;
 constexpr int KIND_PERIODIC = 5;
 constexpr int KIND_CAT = 6;
+constexpr int KIND_LINEAR = 7;
+constexpr int KIND_POLY = 8;
 // Provider kind reported for composite kernel trees.
 constexpr int KIND_TREE = -1;
 
@@ -48,6 +57,7 @@ enum TreeCode : int { TN_LEAF = 0, TN_ADD = 1, TN_MUL = 2, TN_SCALE = 3 };
 
 struct TreeLeaf {
   int kind, ard, ndim, dim_off, p0;
+  int deg;  // polynomial degree (KIND_POLY)
 };
 // LEAF: a = leaf index; ADD / MUL: a, b = child nodes; SCALE: a = child node,
 // b = index of the scale factor in the parameter vector.
@@ -59,6 +69,7 @@ struct KernelTree {
   int d = 0, nparams = 0, nleaves = 0, nnodes = 0;
   int table_size = 0;  // categorical table entries after the parameters
   int ncat = 0;        // categorical leaves
+  int nonstationary = 0;  // linear / polynomial leaves: k(x, x) varies with x
   TreeLeaf leaf[kTreeMaxLeaves];
   TreeNode node[kTreeMaxNodes];
   int dims[kTreeMaxDims];
@@ -98,6 +109,32 @@ __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
     e.k = p[t.nparams + lf.p0 + tree_level(xi[dq], L) * L + tree_level(xj[dq], L)];
     e.r2 = 0.0f;
     e.h = 0.0f;
+    return e;
+  }
+  if (lf.kind == KIND_LINEAR || lf.kind == KIND_POLY) {
+    // r2 holds the (weighted) dot product, h the derivative factor
+    float dot = 0.0f;
+    for (int q = 0; q < lf.ndim; ++q) {
+      const int dq = t.dims[lf.dim_off + q];
+      const float xx = xi[dq] * xj[dq];
+      dot = lf.ard ? fmaf(p[lf.p0 + q], xx, dot) : dot + xx;
+    }
+    const int nls = lf.ard ? lf.ndim : 1;
+    if (!lf.ard) dot *= p[lf.p0];
+    e.r2 = dot;
+    if (lf.kind == KIND_LINEAR) {
+      const float os = p[lf.p0 + nls];
+      e.k = os * dot;
+      e.h = os;
+      return e;
+    }
+    const float offset = p[lf.p0 + nls + 1];
+    const float os = p[lf.p0 + nls + 2];
+    const float B = dot + offset;
+    float bp = 1.0f;  // B^(D-1)
+    for (int k = 1; k < lf.deg; ++k) bp *= B;
+    e.k = os * bp * B;
+    e.h = os * (float)lf.deg * bp;  // dk/dB
     return e;
   }
   if (lf.kind == KIND_PERIODIC) {
@@ -211,6 +248,22 @@ __device__ __forceinline__ void tree_grad_accumulate(const KernelTree& t,
       const LeafEval& e = le[l];
       if (lf.kind == KIND_CAT) continue;  // tables are learned outside this pass
       const int nls = lf.ard ? lf.ndim : 1;
+      if (lf.kind == KIND_LINEAR || lf.kind == KIND_POLY) {
+        // dk/dvar: h x.x' (iso) or h x_q x'_q (ARD); h = os (linear) or
+        // os D B^(D-1) (polynomial); dk/doffset = h; dk/dos = k / os
+        if (lf.ard) {
+          for (int q = 0; q < lf.ndim; ++q) {
+            const int dq = t.dims[lf.dim_off + q];
+            g[lf.p0 + q] += a * e.h * xi[dq] * xj[dq];
+          }
+        } else {
+          g[lf.p0] += a * e.h * e.r2 / p[lf.p0];
+        }
+        const int ios = lf.p0 + nls + (lf.kind == KIND_POLY ? 2 : 0);
+        if (lf.kind == KIND_POLY) g[lf.p0 + nls + 1] += a * e.h;
+        g[ios] += a * e.k / p[ios];
+        continue;
+      }
       if (lf.kind == KIND_PERIODIC) {
         const float period = p[lf.p0 + nls];
         const int ios = lf.p0 + nls + 1;

@@ -64,7 +64,16 @@ struct Provider {
   float outputscale() const { return params[nparams - 1]; }
   // k(x, x) (every supported kernel is stationary): the outputscale for a
   // single leaf, the tree evaluated at zero distance for composite kernels.
-  float kdiag() const { return is_tree ? (float)tree_diag(tree, params.data()) : outputscale(); }
+  float kdiag() const {
+    if (!is_tree) return outputscale();
+    // non-stationary trees: the last parameter, as the reference's
+    // get_diagonal_value hint (fn_ptr_module.py:948-961); per-point
+    // diagonals come from diag_values
+    return tree.nonstationary ? params.back() : (float)tree_diag(tree, params.data());
+  }
+  bool nonstationary() const { return is_tree && tree.nonstationary; }
+  // out[i] = k(x_i, x_i) for m device points of a packed set (device out).
+  void diag_values(const PackedPoints& pts, int64_t m, float* out);
   float lengthscale(int k) const { return ard ? params[k] : params[0]; }
 
   // Recompute the coordinate map from params and repack the training points.

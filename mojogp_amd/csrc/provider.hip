@@ -105,6 +105,16 @@ void Provider::load_noise_vector(const float* host) {
 
 void Provider::fill_dense() { fill_block(train, 0, n, K.ptr); }
 
+void Provider::diag_values(const PackedPoints& pts, int64_t m, float* out) {
+  if (is_tree) {
+    tree_self_values(tree, tparams.ptr, pts.z.ptr, m, out, st);
+    return;
+  }
+  std::vector<float> h((size_t)std::max<int64_t>(m, 1), kdiag());
+  MGP_HIP_CHECK(hipMemcpyAsync(out, h.data(), (size_t)m * sizeof(float), hipMemcpyHostToDevice, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+}
+
 void Provider::fill_block(const PackedPoints& rows, int64_t r0, int64_t nrows, float* out) {
   if (is_tree) {
     tree_fill(tree, tparams.ptr, rows.z.ptr, r0, nrows, train.z.ptr, n, out, st);

@@ -140,8 +140,9 @@ void multi_axpy(const float* Q, int nvec, const double* coef, float* w, int64_t 
 // S[c*n + i] = sum_k Q[k*n + i] * T[k*r + c]  (n x r times r x r)
 void gemm_nr_rr(const float* Q, const float* T, int64_t n, int r, float* S,
                 hipStream_t st);
-// var[j] = max(diag - sum_k V[k*m + j]^2, 1e-10)  (jit_prediction.mojo:211-233)
+// var[j] = max(diag_j - sum_k V[k*m + j]^2, 1e-10) with diag_j = diag_vec[j]
+// (device, optional) or diag (jit_prediction.mojo:211-233)
 void love_variance(const float* V, int64_t m, int r, float diag, float* var,
-                   hipStream_t st);
+                   hipStream_t st, const float* diag_vec = nullptr);
 
 }  // namespace mgp

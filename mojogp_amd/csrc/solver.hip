@@ -798,8 +798,8 @@ __global__ void k_gemm_nr_rr(const float* __restrict__ Q, const float* __restric
     if (c < cn) S[(int64_t)(c0 + c) * n + i] = acc[c];
 }
 
-__global__ void k_love_variance(const float* __restrict__ V, int64_t m, int r, float diag,
-                                float* __restrict__ var) {
+__global__ void k_love_variance(const float* __restrict__ V, int64_t m, int r, float diag0,
+                                const float* __restrict__ dvec, float* __restrict__ var) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= m) return;
   float s = 0.0f;
@@ -807,6 +807,7 @@ __global__ void k_love_variance(const float* __restrict__ V, int64_t m, int r, f
     const float v = V[(int64_t)k * m + j];
     s = fmaf(v, v, s);
   }
+  const float diag = dvec ? dvec[j] : diag0;
   var[j] = fmaxf(diag - s, 1e-10f);
 }
 
@@ -924,6 +925,7 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
   fill(L, (int64_t)rank * n, 0.0f, st);
   const float os = pv.kdiag();
   hipLaunchKernelGGL(k_pc_init, grid1(n), dim3(kBlock), 0, st, diag.ptr, mask.ptr, n, os);
+  if (pv.nonstationary()) pv.diag_values(pv.train, n, diag.ptr);  // extract_diagonal
   hipLaunchKernelGGL(k_pc_argmax_part, dim3(nb), dim3(kBlock), 0, st, diag.ptr, mask.ptr,
                      n, nb, pvv.ptr, piv.ptr, pa.ptr);
   MGP_HIP_CHECK(hipGetLastError());
@@ -1148,8 +1150,10 @@ void gemm_nr_rr(const float* Q, const float* T, int64_t n, int r, float* S, hipS
   MGP_HIP_CHECK(hipGetLastError());
 }
 
-void love_variance(const float* V, int64_t m, int r, float diag, float* var, hipStream_t st) {
-  hipLaunchKernelGGL(k_love_variance, grid1(m), dim3(kBlock), 0, st, V, m, r, diag, var);
+void love_variance(const float* V, int64_t m, int r, float diag, float* var, hipStream_t st,
+                   const float* diag_vec) {
+  hipLaunchKernelGGL(k_love_variance, grid1(m), dim3(kBlock), 0, st, V, m, r, diag, diag_vec,
+                     var);
   MGP_HIP_CHECK(hipGetLastError());
 }
 

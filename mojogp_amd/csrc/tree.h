@@ -10,6 +10,9 @@ namespace mgp {
 void tree_matvec(const KernelTree& t, const float* p_dev, const float* Xr, int64_t m,
                  const float* Xc, int64_t n, const float* V, int ncols, float noise,
                  bool square, float* out, hipStream_t st);
+// out[i] = K(X_i, X_i) for device points X [m][d].
+void tree_self_values(const KernelTree& t, const float* p_dev, const float* X, int64_t m,
+                      float* out, hipStream_t st);
 // out[c*n + i] = K(Xr[r0 + c], Xc[i]) for c < rows.
 void tree_fill(const KernelTree& t, const float* p_dev, const float* Xr, int64_t r0,
                int64_t rows, const float* Xc, int64_t n, float* out, hipStream_t st);

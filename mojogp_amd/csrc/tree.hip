@@ -64,6 +64,16 @@ __global__ __launch_bounds__(256) void k_tree_matvec(
   }
 }
 
+// out[i] = K(x_i, x_i)
+__global__ void k_tree_self(const float* __restrict__ X, int64_t m, KernelTree t,
+                            const float* __restrict__ p, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  float x[kTreeMaxInputDim];
+  for (int k = 0; k < t.d; ++k) x[k] = X[i * t.d + k];
+  out[i] = tree_value(t, p, x, x);
+}
+
 // out[c*n + i] = K(rows[r0 + c], cols[i])
 __global__ void k_tree_fill(const float* __restrict__ Xr, int64_t r0, int64_t rows,
                             const float* __restrict__ Xc, int64_t n, KernelTree t,
@@ -236,7 +246,12 @@ KernelTree parse_kernel_tree(const int* spec, int len) {
     lf.ndim = next();
     lf.p0 = next();
     lf.dim_off = doff;
-    require(lf.kind >= KIND_RBF && lf.kind <= KIND_CAT, "unknown kernel tree leaf kind");
+    lf.deg = 0;
+    if (lf.kind == KIND_POLY) {
+      lf.deg = next();
+      require(lf.deg >= 1 && lf.deg <= 16, "polynomial degree must be an integer in [1, 16]");
+    }
+    require(lf.kind >= KIND_RBF && lf.kind <= KIND_POLY, "unknown kernel tree leaf kind");
     require(lf.ndim >= 1 && doff + lf.ndim <= kTreeMaxDims, "kernel tree leaf dimensions");
     for (int q = 0; q < lf.ndim; ++q) {
       const int dq = next();
@@ -254,9 +269,12 @@ KernelTree parse_kernel_tree(const int* spec, int len) {
       continue;
     }
     const int nls = lf.ard ? lf.ndim : 1;
-    const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1 : 0;
+    const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1
+                      : lf.kind == KIND_POLY                           ? 2
+                                                                       : 0;
     require(lf.p0 >= 0 && lf.p0 + nls + extra + 1 <= t.nparams,
             "kernel tree leaf parameters out of range");
+    if (lf.kind == KIND_LINEAR || lf.kind == KIND_POLY) t.nonstationary = 1;
   }
   require(cat_levels <= kTreeMaxCatRow, "categorical leaves exceed 64 levels in total");
   int leaf_uses[kTreeMaxLeaves] = {0};
@@ -297,8 +315,12 @@ double tree_diag(const KernelTree& t, const float* params) {
     } else if (nd.code == TN_LEAF) {
       const TreeLeaf& lf = t.leaf[nd.a];
       const int nls = lf.ard ? lf.ndim : 1;
-      const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1 : 0;
-      v[i] = (double)params[lf.p0 + nls + extra];  // every leaf is os at zero distance
+      const int extra = (lf.kind == KIND_RQ || lf.kind == KIND_PERIODIC) ? 1
+                        : lf.kind == KIND_POLY                           ? 2
+                                                                         : 0;
+      // os of a stationary leaf at zero distance (linear / polynomial trees
+      // take per-point diagonals, tree_self_values)
+      v[i] = (double)params[lf.p0 + nls + extra];
     } else if (nd.code == TN_ADD) {
       v[i] = v[(size_t)nd.a] + v[(size_t)nd.b];
     } else if (nd.code == TN_MUL) {
@@ -321,6 +343,14 @@ void tree_matvec(const KernelTree& t, const float* p_dev, const float* Xr, int64
                        noise, square ? 1 : 0, out + (int64_t)c0 * m);
     MGP_HIP_CHECK(hipGetLastError());
   }
+}
+
+void tree_self_values(const KernelTree& t, const float* p_dev, const float* X, int64_t m,
+                      float* out, hipStream_t st) {
+  if (m <= 0) return;
+  hipLaunchKernelGGL(k_tree_self, dim3((unsigned)ceil_div(m, 256)), dim3(256), 0, st, X, m, t,
+                     p_dev, out);
+  MGP_HIP_CHECK(hipGetLastError());
 }
 
 void tree_fill(const KernelTree& t, const float* p_dev, const float* Xr, int64_t r0,

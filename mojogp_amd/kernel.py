@@ -82,7 +82,8 @@ def cat_default_raw_param(kernel_type: KernelType, param_index: int, L: int) -> 
 NATIVE_KINDS = {KernelType.RBF: 0, KernelType.MATERN52: 1, KernelType.MATERN12: 2,
                 KernelType.MATERN32: 3}
 # Leaf codes of the kernel-tree spec (radial kinds keep their codes).
-TREE_LEAF_CODES = {**NATIVE_KINDS, KernelType.RQ: 4, KernelType.PERIODIC: 5}
+TREE_LEAF_CODES = {**NATIVE_KINDS, KernelType.RQ: 4, KernelType.PERIODIC: 5,
+                   KernelType.LINEAR: 7, KernelType.POLYNOMIAL: 8}
 _CAT_LEAF_CODE = 6
 _TN_LEAF, _TN_ADD, _TN_MUL, _TN_SCALE = 0, 1, 2, 3
 
@@ -156,11 +157,25 @@ class KernelNode:
         out = self.left.categorical_leaves() if self.left else []
         return out + (self.right.categorical_leaves() if self.right else [])
 
+    def structural_degree(self) -> int:
+        """Fixed integer degree of a polynomial leaf (expressions.py:57-71)."""
+        deg = float((self.initial_values or {}).get("degree", 2.0))
+        d = int(round(deg))
+        if abs(deg - d) > 1e-5 or d < 1:
+            raise ValueError("Polynomial kernel degree must be a fixed positive integer, "
+                             f"got {deg:.6g}.")
+        return d
+
     def engine_num_params(self) -> int:
-        """Continuous parameters only (categorical leaves train separately,
-        kernel.py:462-480)."""
+        """Continuous parameters only (categorical leaves train separately);
+        an isotropic polynomial carries a hidden variance slot
+        (kernel.py:462-480)."""
         if self.kernel_type is not None:
-            return 0 if self.is_categorical() else self.num_params()
+            if self.is_categorical():
+                return 0
+            if self.kernel_type == KernelType.POLYNOMIAL and self.ard_dim is None:
+                return 4
+            return self.num_params()
         if self.operator == "scale":
             return self.left.engine_num_params() + 1
         return self.left.engine_num_params() + self.right.engine_num_params()
@@ -206,10 +221,11 @@ class KernelNode:
                 if ard and node.ard_dim != len(dims):
                     raise ValueError(f"ARD leaf {node!r} has {node.ard_dim} lengthscales for "
                                      f"{len(dims)} active dimensions")
-                leaves.append([TREE_LEAF_CODES[node.kernel_type], int(ard), len(dims), offset,
-                               *dims])
+                code = TREE_LEAF_CODES[node.kernel_type]
+                extra = [node.structural_degree()] if code == 8 else []
+                leaves.append([code, int(ard), len(dims), offset, *extra, *dims])
                 nodes.append([_TN_LEAF, len(leaves) - 1, 0])
-                return len(nodes) - 1, offset + node.num_params()
+                return len(nodes) - 1, offset + node.engine_num_params()
             if node.operator in ("sum", "product"):
                 a, mid = walk(node.left, dims, offset)
                 b, end = walk(node.right, dims, mid)
@@ -227,7 +243,7 @@ class KernelNode:
         start = tuple(range(dim)) if default_dims is None else tuple(default_dims)
         _, nparams = walk(self, start, 0)
         if (len(leaves) > 8 or len(nodes) > 16 or nparams > 48 or dim > 32
-                or sum(lf[2] for lf in leaves) > 64):
+                or sum(lf[2] for lf in leaves if lf[0] != _CAT_LEAF_CODE) > 64):
             raise NotImplementedError("kernel trees are served up to 8 leaves, 16 nodes, "
                                       "48 parameters, 32 input dimensions and 64 leaf "
                                       "dimensions in total")
@@ -338,32 +354,69 @@ class KernelNode:
             return mid + 1
         return offset
 
-    def _public_slots(self) -> List[bool]:
-        """Per public parameter: True when it is an engine (continuous) one."""
-        if self.kernel_type is not None:
-            return [not self.is_categorical()] * self.num_params()
-        if self.operator == "scale":
-            return self.left._public_slots() + [True]
-        return self.left._public_slots() + self.right._public_slots()
-
     def to_engine_params(self, public_params) -> np.ndarray:
-        """Public layout -> engine layout: the continuous parameters in tree
-        order, categorical slots dropped (kernel.py:494-568)."""
+        """Public layout -> engine layout (kernel.py:494-568): continuous
+        parameters in tree order, categorical slots dropped, an isotropic
+        polynomial's [degree, offset, os] as [1, degree, offset, os]."""
         p = np.asarray(public_params, dtype=np.float32)
         if p.shape != (self.num_params(),):
             raise ValueError(f"public_params must have shape ({self.num_params()},), got {p.shape}")
-        return p[np.array(self._public_slots(), dtype=bool)].copy()
+        out: List[float] = []
+        self._fill_engine(p, 0, out)
+        return np.asarray(out, dtype=np.float32)
+
+    def _fill_engine(self, p, off: int, out: list) -> int:
+        if self.kernel_type is not None:
+            n = self.num_params()
+            if self.is_categorical():
+                return off + n
+            if self.kernel_type == KernelType.POLYNOMIAL and self.ard_dim is None:
+                out.extend([1.0, *p[off:off + 3]])
+            else:
+                out.extend(p[off:off + n])
+            return off + n
+        mid = self.left._fill_engine(p, off, out)
+        if self.operator == "scale":
+            out.append(p[mid])
+            return mid + 1
+        return self.right._fill_engine(p, mid, out)
 
     def from_engine_params(self, engine_params) -> np.ndarray:
-        """Engine layout -> public layout; categorical slots keep their
-        default initial values (kernel.py:511-526)."""
+        """Engine layout -> public layout (kernel.py:511-606): categorical
+        slots keep their defaults, a polynomial reports its structural degree
+        (the hidden variance slot is dropped)."""
         p = np.asarray(engine_params, dtype=np.float32)
         if p.shape != (self.engine_num_params(),):
             raise ValueError(f"engine_params must have shape ({self.engine_num_params()},), "
                              f"got {p.shape}")
         out = self.get_initial_params()
-        out[np.array(self._public_slots(), dtype=bool)] = p
+        self._strip_engine(p, 0, out, 0)
         return out
+
+    def _strip_engine(self, p, eoff: int, out, poff: int):
+        if self.kernel_type is not None:
+            n = self.num_params()
+            if self.is_categorical():
+                return eoff, poff + n
+            if self.kernel_type == KernelType.POLYNOMIAL and self.ard_dim is None:
+                out[poff] = float(self.structural_degree())
+                out[poff + 1:poff + 3] = p[eoff + 2:eoff + 4]
+                return eoff + 4, poff + 3
+            out[poff:poff + n] = p[eoff:eoff + n]
+            return eoff + n, poff + n
+        e, q = self.left._strip_engine(p, eoff, out, poff)
+        if self.operator == "scale":
+            out[q] = p[e]
+            return e + 1, q + 1
+        return self.right._strip_engine(p, e, out, q)
+
+    def _public_slots(self) -> List[bool]:
+        """Per public parameter: False for categorical slots."""
+        if self.kernel_type is not None:
+            return [not self.is_categorical()] * self.num_params()
+        if self.operator == "scale":
+            return self.left._public_slots() + [True]
+        return self.left._public_slots() + self.right._public_slots()
 
     # ---------------------------------------------------------- serialisation
     # Type names written into saved model configs ("kernel_mojo_type"); the
@@ -469,8 +522,15 @@ class KernelNode:
 
 def _leaf_matrix(node: KernelNode, X, X2, p) -> np.ndarray:
     kt = node.kernel_type
-    if kt in (KernelType.LINEAR, KernelType.POLYNOMIAL):
-        raise NotImplementedError("evaluate() covers the stationary leaves")
+    if kt == KernelType.LINEAR:  # kernel.py:822-826
+        nls = node.ard_dim if node.ard_dim is not None else 1
+        var = p[:nls]
+        return p[nls] * ((X * var) @ X2.T if nls > 1 else var[0] * (X @ X2.T))
+    if kt == KernelType.POLYNOMIAL:  # kernel.py:828-844 (public [degree, offset, os])
+        if node.ard_dim is not None:
+            raise NotImplementedError("ARD polynomial evaluation is not supported")
+        deg = node.structural_degree()
+        return p[2] * np.power(X @ X2.T + p[1], deg)
     q = X.shape[1]
     nls = node.ard_dim if node.ard_dim is not None else 1
     if node.ard_dim is not None and node.ard_dim != q:

@@ -39,10 +39,15 @@ F32 = np.float32
 
 
 # ---------------------------------------------------------------- RNG
-def _kdiag(kind, params) -> float:
-    """k(x, x) of a stationary kernel: the outputscale, or a tree at zero distance."""
+def _kdiag(kind, params, Xs=None):
+    """k(x, x): the outputscale of a single kernel; for trees k(x*_j, x*_j) per
+    test point (linear / polynomial leaves make it vary with x)."""
     if isinstance(kind, ok.TreeKernel):
-        return kind.diag(params)
+        if Xs is None:
+            return kind.diag(params)
+        Xs = np.atleast_2d(np.asarray(Xs, np.float64))
+        return np.array([kind.matrix(Xs[j:j + 1], Xs[j:j + 1], params)[0, 0]
+                         for j in range(Xs.shape[0])])
     return float(np.asarray(params)[-1])
 
 
@@ -626,7 +631,7 @@ def predict(kind: int, ard: bool, X, y, Xs, params, noise: float, mean: float, *
     mu = Ks @ alpha + mean
     S = lanczos_inv_root(A, lanczos_rank)
     V = Ks @ S
-    var = np.maximum(_kdiag(kind, params) - np.sum(V * V, axis=1), 1e-10)
+    var = np.maximum(_kdiag(kind, params, Xs) - np.sum(V * V, axis=1), 1e-10)
     return mu, var, alpha
 
 
@@ -647,7 +652,11 @@ def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=
     K = ok.kernel_matrix(kind, X, X, params, ard)
     vec = noise_vec is not None
     A = K + (np.diag(np.asarray(noise_vec, np.float64)) if vec else noise * np.eye(n))
-    os_ = _kdiag(kind, params)
+    prior = _kdiag(kind, params, Xs) * np.ones(m)
+    # pivot error-ratio hint: k(x, x) of a stationary kernel, the last
+    # parameter for trees with linear / polynomial leaves (get_diagonal_value)
+    os_ = (float(np.asarray(params)[-1])
+           if isinstance(kind, ok.TreeKernel) and kind.nonstationary else _kdiag(kind, params))
     if block_cols > 0:
         block = min(block_cols, m)
     elif materialized:
@@ -669,7 +678,7 @@ def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=
         norms = np.where(norms > 0, norms, 1.0)
         x, it, _, _, _ = batched_cg(A, Kc / norms, P, max_cg, 0, tol)
         sol = x * norms
-        var[s0:s0 + block] = np.maximum(os_ - np.sum(Kc * sol, axis=0), 1e-10)
+        var[s0:s0 + block] = np.maximum(prior[s0:s0 + block] - np.sum(Kc * sol, axis=0), 1e-10)
         iters.append(it)
     return var, rank, iters
 

@@ -198,12 +198,25 @@ class TreeKernel:
     def _count(self, nd) -> int:
         if nd.get("kernel_type") in CAT_LEAVES:
             return 0
+        if nd.get("kernel_type") == "LINEAR":
+            return (nd.get("ard_dim") or 1) + 1
+        if nd.get("kernel_type") == "POLYNOMIAL":
+            return 4 if nd.get("ard_dim") is None else nd["ard_dim"] + 3
         if "kernel_type" in nd:
             extra = 1 if nd["kernel_type"] in (RQ_LEAF, PERIODIC_LEAF) else 0
             return (nd.get("ard_dim") or 1) + extra + 1
         if nd["operator"] == "scale":
             return self._count(nd["left"]) + 1
         return self._count(nd["left"]) + self._count(nd["right"])
+
+    @property
+    def nonstationary(self) -> bool:
+        """True when a linear or polynomial leaf makes k(x, x) vary with x."""
+        def walk(nd):
+            if "kernel_type" in nd:
+                return nd["kernel_type"] in ("LINEAR", "POLYNOMIAL")
+            return walk(nd["left"]) or ("right" in nd and walk(nd["right"]))
+        return walk(self.node)
 
     def matrix(self, X1, X2, params) -> np.ndarray:
         return self._walk(X1, X2, params, False)[0]
@@ -297,6 +310,29 @@ def _tree_leaf(nd, X1, X2, p, grads):
     if ard and nd["ard_dim"] != q:
         raise ValueError("ARD leaf lengthscale count differs from its dimension count")
     nls = q if ard else 1
+    if kt in ("LINEAR", "POLYNOMIAL"):
+        # engine layout (kernel.py:462-568, expressions.py:327-421): linear
+        # [variance | var_q], os; polynomial [variance | var_q], degree,
+        # offset, os with the structural integer degree in the forward
+        prod = X1[:, None, :] * X2[None, :, :]
+        var = p[:nls]
+        dot = (prod * var).sum(-1) if ard else var[0] * prod.sum(-1)
+        if kt == "LINEAR":
+            os = p[nls]
+            k = os * dot
+            if not grads:
+                return k, None
+            G = ([os * prod[:, :, j] for j in range(q)] if ard else [os * prod.sum(-1)])
+            return k, G + [dot]
+        D = int(round(float((nd.get("initial_values") or {}).get("degree", 2.0))))
+        off, os = p[nls + 1], p[nls + 2]
+        B = dot + off
+        k = os * B**D
+        if not grads:
+            return k, None
+        h = os * D * B ** (D - 1)
+        G = ([h * prod[:, :, j] for j in range(q)] if ard else [h * prod.sum(-1)])
+        return k, G + [np.zeros_like(k), h, B**D]
     ls = p[:nls] if ard else np.full(q, p[0])
     diff = X1[:, None, :] - X2[None, :, :]
     if kt == PERIODIC_LEAF:

@@ -11,7 +11,8 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from mojogp_amd import RBF, RQ, Matern12, Matern32, Matern52, Periodic, make_ard_kernel
+from mojogp_amd import (RBF, RQ, Linear, Matern12, Matern32, Matern52, Periodic, Polynomial,
+                        make_ard_kernel)
 from mojogp_amd import _lib
 from mojogp_amd._provider import NativeProvider
 from oracle import engine as oe
@@ -148,3 +149,99 @@ def test_tree_fit_predict_save_load(tmp_path):
     m2, s2 = gp2.predict(Xs, return_std=True, cg_tolerance=1e-6)
     np.testing.assert_allclose(m2, mean_t, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(s2, std_t, rtol=1e-5, atol=1e-6)
+
+
+NONSTAT = {
+    "linear*rbf+poly2": (lambda: Linear() * RBF()
+                         + Polynomial(degree=2), 3),
+    "linear_ard+rbf": (lambda: make_ard_kernel(Linear(ard=True) + RBF(), 3), 3),
+    "poly3_ard+m52": (lambda: make_ard_kernel(Polynomial(degree=3, ard=True)
+                                              + Matern52(), 2), 2),
+}
+
+
+@pytest.mark.parametrize("name", list(NONSTAT))
+def test_nonstationary_tree_products_and_bbmm(name):
+    """Linear / polynomial leaves: products, per-point diagonals (pivoted
+    Cholesky start, extract_diagonal), and one preconditioned BBMM."""
+    mk, d = NONSTAT[name]
+    node = mk()
+    rng = np.random.default_rng(21)
+    n = 500
+    X = rng.uniform(-1.5, 1.5, size=(n, d)).astype(np.float32)
+    T = ok.TreeKernel(node.to_dict(), d)
+    params = rng.uniform(0.5, 1.2, T.nparams).astype(np.float32)
+    V = rng.normal(size=(3, n)).astype(np.float32)
+    y = (np.sin(X).sum(1) + 0.1 * rng.normal(size=n)).astype(np.float32)
+    print(f"non-stationary tree {name}", flush=True)
+    p = NativeProvider(None, False, X, params, 0.2, tree_spec=node.to_tree_spec(d))
+    g = np.zeros(params.size + 1, np.float32)
+    nll, iq, ld, ci, pl = C.c_float(), C.c_float(), C.c_float(), C.c_int(), C.c_float()
+    L = np.zeros((20, n), np.float32)
+    rk, lpd = C.c_int(), C.c_float()
+    diag = np.zeros(n, np.float32)
+    try:
+        fwd = p.forward_matvec(V)
+        _lib.call("mgp_extract_diagonal", p.handle, _lib.fptr(diag))
+        _lib.call("mgp_pivoted_cholesky", p.handle, 20, 0, 0.0, 0.01, 42, _lib.fptr(L),
+                  C.byref(rk), C.byref(lpd))
+        _lib.call("mgp_bbmm_eval", p.handle, _lib.fptr(y), 0.0, 10, 100, 30, 1e-2, 2, 20,
+                  C.byref(nll), C.byref(iq), C.byref(ld), _lib.fptr(g), C.byref(ci), C.byref(pl),
+                  None)
+    finally:
+        p.close()
+    K = T.matrix(X, X, params)
+    assert _rel(fwd, ok.forward_matvec(T, X, V, params, 0.2, False)) <= 1e-5
+    np.testing.assert_allclose(diag, np.diag(K), rtol=1e-5, atol=1e-6)
+    Lr, kr = oe.pivoted_cholesky(K, 20)
+    assert rk.value == kr
+    assert np.abs(L[:kr].T - Lr).max() <= 1e-4 * np.abs(Lr).max()
+    r = oe.bbmm_step(T, False, X, y.astype(np.float64), params.astype(np.float64), 0.2,
+                     oe.Precond(Lr, 0.2), 10, 100, 30, 1e-2, 2)
+    print(f"  nll {nll.value:.7f} vs {r['nll']:.7f}; grads {_rel(g, r['grads']):.2e}", flush=True)
+    assert nll.value == pytest.approx(r["nll"], rel=1e-4)
+    assert _rel(g, r["grads"]) <= 1e-3
+
+
+def test_nonstationary_fit_predict():
+    """Linear x RBF + polynomial fit on the restatement's trajectory; LOVE and
+    exact variances with per-test-point prior diagonals."""
+    from mojogp_amd import SingleOutputGP
+    rng = np.random.default_rng(8)
+    n = 300
+    X = rng.uniform(-2, 2, size=(n, 2)).astype(np.float32)
+    y = (0.8 * X[:, 0] + np.sin(2 * X[:, 1]) + 0.1 * rng.normal(size=n)).astype(np.float32)
+    kernel = Linear() * RBF() + Polynomial(degree=2)
+    gp = SingleOutputGP(kernel)
+    tr = gp.fit(X, y, max_iterations=8, method="matrix_free", learning_rate=0.02)
+    T = ok.TreeKernel(gp.kernel.to_dict(), 2)
+    init = gp.kernel.to_engine_params(gp.kernel.get_initial_params())
+    ref = oe.train(T, False, X, y, init, 0.1, max_iterations=8, learning_rate=0.02,
+                   num_probes=10, max_cg=100, cg_tol=1e-2, precond_rank=0, max_tridiag=30)
+    eng_trained = ref["params"]
+    print(f"nonstationary fit: noise {tr.noise} vs {ref['noise']}", flush=True)
+    assert tr.noise == pytest.approx(ref["noise"], rel=1e-3)
+    # public params report the structural degree; compare the engine slots the
+    # public layout keeps (kernel.py:570-606)
+    pub_ref = gp.kernel.from_engine_params(eng_trained)
+    assert _rel(tr.params, pub_ref) <= 1e-3
+    Xs = rng.uniform(-2.5, 2.5, size=(40, 2)).astype(np.float32)
+    mean_t, std_t = gp.predict(Xs, return_std=True, cg_tolerance=1e-6)
+    pe = gp.kernel.to_engine_params(tr.params).astype(np.float64)
+    mu, var, _ = oe.predict(T, False, X, y, Xs, pe, tr.noise, tr.mean, max_cg=300, tol=1e-6,
+                            lanczos_rank=100)
+    # var = k(x*, x*) - |V|^2 cancels: polynomial priors reach ~100 here
+    # against posterior variances ~0.05, so fp32 rounding of the prior term
+    # alone is ~2e-7 * prior / var relative; the bar scales with that factor.
+    prior = oe._kdiag(T, pe, Xs)
+    cancel = float(np.max(prior / var))
+    bar = max(1e-4, 2e-7 * cancel)
+    print(f"  predict mean {_rel(mean_t, mu):.2e} std {_rel(std_t, np.sqrt(var)):.2e} "
+          f"(prior / variance up to {cancel:.0f}, bar {bar:.1e})", flush=True)
+    assert _rel(mean_t, mu) <= 1e-4
+    assert _rel(std_t, np.sqrt(var)) <= bar
+    _, var_e = gp.predict(Xs, return_var=True, variance_method="exact", cg_tolerance=1e-6,
+                          max_cg_iterations=1000)
+    ve, _, _ = oe.exact_variance(T, False, X, Xs, pe, tr.noise, max_cg=1000, tol=1e-6)
+    print(f"  exact std {_rel(np.sqrt(var_e), np.sqrt(ve)):.2e}", flush=True)
+    assert _rel(np.sqrt(var_e), np.sqrt(ve)) <= bar

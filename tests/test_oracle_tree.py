@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 from sklearn.gaussian_process import kernels as sk
 
-from mojogp_amd import RBF, RQ, Matern12, Matern32, Matern52, Periodic, make_ard_kernel
+from mojogp_amd import (RBF, RQ, Linear, Matern12, Matern32, Matern52, Periodic, Polynomial,
+                        make_ard_kernel)
 from mojogp_amd.kernel import KernelNode
 from oracle import kernels as ok
 
@@ -174,9 +175,8 @@ def test_tree_spec_layout():
 
 
 def test_tree_spec_rejects_unserved():
-    from mojogp_amd import Linear
-    with pytest.raises(NotImplementedError):
-        (RBF() + Linear()).to_tree_spec(2)
+    with pytest.raises(ValueError):    # non-integer polynomial degree
+        Polynomial(degree=2.5).to_tree_spec(2)
     with pytest.raises(ValueError):
         RBF(active_dims=[3]).to_tree_spec(2)
     with pytest.raises(NotImplementedError):
@@ -184,3 +184,44 @@ def test_tree_spec_rejects_unserved():
         for _ in range(8):
             node = node + RBF()
         node.to_tree_spec(2)
+
+
+def test_linear_and_polynomial_leaves_match_sklearn():
+    """Linear os*var*x.x' and polynomial os*(var*x.x' + offset)^D against
+    scikit-learn's DotProduct (sigma_0 = 0, resp. sqrt(offset)) and its
+    Exponentiation; the engine's polynomial layout carries a hidden variance
+    and an unread degree slot (kernel.py:462-606)."""
+    X, Y = _rng_X(12, 14, 3), _rng_X(13, 9, 3)
+    K = _tree(Linear(), 3).matrix(X, Y, [0.7, 1.3])
+    np.testing.assert_allclose(K, 1.3 * 0.7 * sk.DotProduct(sigma_0=0.0)(X, Y), rtol=1e-12)
+    T = _tree(Polynomial(degree=3), 3)
+    assert T.nparams == 4
+    K = T.matrix(X, Y, [1.0, 2.7, 0.5, 1.2])   # degree slot 2.7 is not read
+    ref = 1.2 * sk.Exponentiation(sk.DotProduct(sigma_0=np.sqrt(0.5)), 3)(X, Y)
+    np.testing.assert_allclose(K, ref, rtol=1e-12)
+    node = Polynomial(degree=2) * RBF()
+    p_pub = np.array([2.0, 0.4, 1.1, 0.9, 1.3])
+    np.testing.assert_allclose(node.evaluate(X, Y, p_pub),
+                               _tree(node, 3).matrix(X, Y, node.to_engine_params(p_pub)),
+                               rtol=2e-6)
+
+
+@pytest.mark.parametrize("mk", [
+    lambda: Linear() * RBF() + Polynomial(degree=2),
+    lambda: make_ard_kernel(Linear(ard=True), 3),
+    lambda: make_ard_kernel(Polynomial(degree=3, ard=True), 3),
+])
+def test_nonstationary_gradients_match_finite_differences(mk):
+    node = mk()
+    T = _tree(node, 3)
+    rng = np.random.default_rng(14)
+    X, Y = rng.uniform(-1, 1, (10, 3)), rng.uniform(-1, 1, (8, 3))
+    p = rng.uniform(0.6, 1.4, T.nparams)
+    G = T.gradients(X, Y, p)
+    for q in range(T.nparams):
+        h = 1e-6 * p[q]
+        pp, pm = p.copy(), p.copy()
+        pp[q] += h
+        pm[q] -= h
+        fd = (T.matrix(X, Y, pp) - T.matrix(X, Y, pm)) / (2 * h)
+        np.testing.assert_allclose(G[q], fd, rtol=2e-6, atol=1e-8)
