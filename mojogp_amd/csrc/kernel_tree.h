@@ -194,6 +194,97 @@ __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
   return e;
 }
 
+// Leaf values of one row against kTreeChunk columns (rows of xc with stride
+// w): the leaf's fields and parameters are read once for the whole chunk.
+constexpr int kTreeChunk = 4;
+
+__device__ __forceinline__ void tree_leaf_chunk(const KernelTree& t, int l,
+                                                const float* __restrict__ p, const float* xi,
+                                                const float* xc, int w, float* out) {
+  const TreeLeaf lf = t.leaf[l];
+  if (lf.kind == KIND_CAT || lf.kind == KIND_LINEAR || lf.kind == KIND_POLY) {
+    for (int c = 0; c < kTreeChunk; ++c) out[c] = tree_leaf_eval(t, l, p, xi, xc + c * w).k;
+    return;
+  }
+  const int nls = lf.ard ? lf.ndim : 1;
+  if (lf.kind == KIND_PERIODIC) {
+    const float ip = kTreePi / p[lf.p0 + nls];
+    const float os = p[lf.p0 + nls + 1];
+    float s[kTreeChunk];
+    for (int c = 0; c < kTreeChunk; ++c) s[c] = 0.0f;
+    for (int q = 0; q < lf.ndim; ++q) {
+      const int dq = t.dims[lf.dim_off + q];
+      const float il = 1.0f / p[lf.p0 + (lf.ard ? q : 0)];
+      const float a = xi[dq];
+      for (int c = 0; c < kTreeChunk; ++c) {
+        const float sn = sinf((a - xc[c * w + dq]) * ip);
+        s[c] = fmaf(sn * sn, il, s[c]);
+      }
+    }
+    for (int c = 0; c < kTreeChunk; ++c) out[c] = os * __expf(fmaxf(-2.0f * s[c], -20.0f));
+    return;
+  }
+  float r2[kTreeChunk];
+  for (int c = 0; c < kTreeChunk; ++c) r2[c] = 0.0f;
+  for (int q = 0; q < lf.ndim; ++q) {
+    const int dq = t.dims[lf.dim_off + q];
+    const float inv = 1.0f / p[lf.p0 + (lf.ard ? q : 0)];
+    const float a = xi[dq];
+    for (int c = 0; c < kTreeChunk; ++c) {
+      const float u = (a - xc[c * w + dq]) * inv;
+      r2[c] = fmaf(u, u, r2[c]);
+    }
+  }
+  if (lf.kind == KIND_RQ) {
+    const float alpha = p[lf.p0 + nls], os = p[lf.p0 + nls + 1];
+    const float ia = 0.5f / alpha;
+    // B^-alpha = 2^(-alpha log2 B), B >= 1
+    for (int c = 0; c < kTreeChunk; ++c)
+      out[c] = os * exp2f(-alpha * __log2f(fmaf(r2[c], ia, 1.0f)));
+    return;
+  }
+  const float os = p[lf.p0 + nls];
+  if (lf.kind == KIND_RBF) {
+    for (int c = 0; c < kTreeChunk; ++c) out[c] = os * __expf(fmaxf(-0.5f * r2[c], -20.0f));
+    return;
+  }
+  for (int c = 0; c < kTreeChunk; ++c) {
+    const float r = sqrtf(fmaxf(r2[c] + 1e-20f, 1e-20f));
+    if (lf.kind == KIND_MATERN12) {
+      out[c] = os * __expf(fmaxf(-r, -20.0f));
+    } else if (lf.kind == KIND_MATERN32) {
+      const float s3 = 1.7320508075688772f * r;
+      out[c] = os * (1.0f + s3) * __expf(fmaxf(-s3, -20.0f));
+    } else {
+      const float s5 = 2.2360679774997897f * r;
+      out[c] = os * (1.0f + s5 + (5.0f / 3.0f) * r2[c]) * __expf(fmaxf(-s5, -20.0f));
+    }
+  }
+}
+
+// Tree values of one row against kTreeChunk columns.
+__device__ __forceinline__ void tree_value_chunk(const KernelTree& t, const float* __restrict__ p,
+                                                 const float* xi, const float* xc, int w,
+                                                 float* out) {
+  float v[kTreeMaxNodes][kTreeChunk];
+  for (int i = 0; i < t.nnodes; ++i) {
+    const TreeNode nd = t.node[i];
+    float x[kTreeChunk];
+    if (nd.code == TN_LEAF) {
+      tree_leaf_chunk(t, nd.a, p, xi, xc, w, x);
+    } else if (nd.code == TN_ADD) {
+      for (int c = 0; c < kTreeChunk; ++c) x[c] = v[nd.a][c] + v[nd.b][c];
+    } else if (nd.code == TN_MUL) {
+      for (int c = 0; c < kTreeChunk; ++c) x[c] = v[nd.a][c] * v[nd.b][c];
+    } else {
+      const float s = p[nd.b];
+      for (int c = 0; c < kTreeChunk; ++c) x[c] = s * v[nd.a][c];
+    }
+    for (int c = 0; c < kTreeChunk; ++c) v[i][c] = x[c];
+  }
+  for (int c = 0; c < kTreeChunk; ++c) out[c] = v[t.nnodes - 1][c];
+}
+
 // Tree value for one pair; node values (and leaf evaluations) optionally kept.
 __device__ __forceinline__ float tree_value(const KernelTree& t, const float* __restrict__ p,
                                             const float* xi, const float* xj,

@@ -16,6 +16,7 @@ namespace {
 constexpr int kTile = 128;      // column points per LDS tile
 constexpr int kMaxCols = 16;    // right-hand sides per pass
 constexpr int kGradCols = 16;   // gradient-trace factor columns per pass
+static_assert(kTreeChunk == 4 && kTile % kTreeChunk == 0, "float4 chunk reads");
 
 void require(bool ok, const std::string& msg) {
   if (!ok) throw Error(ST_INVALID, msg);
@@ -27,31 +28,40 @@ __global__ __launch_bounds__(256) void k_tree_matvec(
     const float* __restrict__ Xr, int64_t m, const float* __restrict__ Xc, int64_t n,
     KernelTree t, const float* __restrict__ p, const float* __restrict__ V, int ncols,
     float noise, int add_noise, float* __restrict__ out) {
-  extern __shared__ float sm[];  // [kTile][d + ncols]
+  // LDS: column coordinates [kTile][d], then right-hand sides transposed
+  // [ncols][kTile] so one 16-byte read serves a chunk of four columns
+  extern __shared__ float sm[];
   const int d = t.d;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int w = d + ncols;
+  float* vt = sm + kTile * d;
   float xi[kTreeMaxInputDim];
   for (int k = 0; k < d; ++k) xi[k] = (i < m) ? Xr[i * d + k] : 0.0f;
   double acc[kMaxCols];
   for (int c = 0; c < kMaxCols; ++c) acc[c] = 0.0;
   for (int64_t j0 = 0; j0 < n; j0 += kTile) {
     __syncthreads();
-    for (int q = threadIdx.x; q < kTile * w; q += blockDim.x) {
-      const int jj = q / w, k = q - jj * w;
+    for (int q = threadIdx.x; q < kTile * d; q += blockDim.x) {
+      const int64_t j = j0 + q / d;
+      sm[q] = j < n ? Xc[j0 * d + q] : 0.0f;
+    }
+    for (int q = threadIdx.x; q < kTile * ncols; q += blockDim.x) {
+      const int c = q / kTile, jj = q - c * kTile;
       const int64_t j = j0 + jj;
-      float val = 0.0f;
-      if (j < n) val = (k < d) ? Xc[j * d + k] : V[(int64_t)(k - d) * n + j];
-      sm[q] = val;
+      vt[q] = j < n ? V[(int64_t)c * n + j] : 0.0f;
     }
     __syncthreads();
+    // columns past n are zero in LDS (coordinates and right-hand sides), so
+    // whole chunks can run: their values multiply zeros
     const int cnt = (int)min((int64_t)kTile, n - j0);
     float part[kMaxCols];
     for (int c = 0; c < kMaxCols; ++c) part[c] = 0.0f;
-    for (int jj = 0; jj < cnt; ++jj) {
-      const float* row = sm + jj * w;
-      const float kv = tree_value(t, p, xi, row);
-      for (int c = 0; c < ncols; ++c) part[c] = fmaf(kv, row[d + c], part[c]);
+    for (int jj = 0; jj < cnt; jj += kTreeChunk) {
+      float kv[kTreeChunk];
+      tree_value_chunk(t, p, xi, sm + jj * d, d, kv);
+      for (int c = 0; c < ncols; ++c) {
+        const float4 vv = *reinterpret_cast<const float4*>(vt + c * kTile + jj);
+        part[c] = fmaf(kv[0], vv.x, fmaf(kv[1], vv.y, fmaf(kv[2], vv.z, fmaf(kv[3], vv.w, part[c]))));
+      }
     }
     for (int c = 0; c < ncols; ++c) acc[c] += (double)part[c];
   }
