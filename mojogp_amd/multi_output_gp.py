@@ -840,7 +840,14 @@ class MultiOutputGP:
             kernel = _KERNEL_STRINGS[kernel.lower()]()
         if not isinstance(kernel, KernelNode):
             raise ValueError(f"kernel must be a string or KernelNode, got {type(kernel)}")
-        kernel.native_kind()  # raises for unsupported trees
+        if not kernel.is_native_leaf():
+            # composite trees run on the kernel-tree products; categorical
+            # leaves are single-output only
+            if (kernel.has_categorical() or not kernel.is_tree_servable()
+                    or kernel.num_params() != kernel.engine_num_params()):
+                raise NotImplementedError(f"kernel {kernel!r} is outside the gfx950 ICM engine "
+                                          "(categorical and isotropic polynomial leaves are "
+                                          "single-output only)")
         self._is_composite = True
         self.kernel = kernel
         self._original_kernel = kernel
@@ -919,8 +926,7 @@ class MultiOutputGP:
 
     def _ensure_compiled(self, dim: int) -> None:
         self._engine = _engine.load_engine()
-        self._kernel_module = _engine.load_kernel_module(self._compiled_kernel.native_kind(),
-                                                         self.ard, dim)
+        self._kernel_module = _engine.load_kernel_module(self._compiled_kernel, False, dim)
         self._dim = dim
 
     def _build_provider_info(self, X, params, noise) -> dict:
@@ -1055,6 +1061,11 @@ class MultiOutputGP:
                                  else KernelNode.from_dict(self._original_kernel.to_dict()))
         self.kernel = self._compiled_kernel
         num_params = self._compiled_kernel.num_params()
+        if not self._compiled_kernel.is_native_leaf() and (
+                initial_lengthscales is not None or initial_lengthscale != 1.0
+                or initial_outputscale != 1.0):
+            raise ValueError("initial_lengthscale(s) / initial_outputscale apply to single "
+                             "RBF / Matern kernels; pass initial_params for kernel trees")
         if initial_lengthscales is not None and len(initial_lengthscales) != num_params - 1:
             raise ValueError(f"initial_lengthscales must have shape ({num_params - 1},), got "
                              f"({len(initial_lengthscales)},)")
@@ -1287,6 +1298,9 @@ class MultiOutputGP:
         mean = np.asarray(self._fitted_mean if self._fitted_mean is not None
                           else r.mean_per_task, np.float32)
         y_c = (self._Y_train - mean[None, :]).astype(np.float32)
+        if not self._compiled_kernel.is_native_leaf():
+            raise NotImplementedError("pathwise samples need an RBF / Matern kernel (random "
+                                      "Fourier features); composite trees have none")
         fmap = build_pathwise_feature_map(self._compiled_kernel.native_kind(), params,
                                           input_dim=d, n_features=n_rff_features, rng=rng,
                                           ard=self.ard)

@@ -354,3 +354,44 @@ def test_multi_output_gp_surface(tmp_path):
                  group_noise=np.array([[0.01, 0.02, 0.03], [0.02, 0.02, 0.02]], np.float32))
     assert gpg.backend_train_info["noise_mode"] == "fixed_per_sample_task"
     assert gpg.precond_rank == 0 and np.all(np.isfinite(rg.nll_history))
+
+
+def test_icm_with_kernel_tree():
+    """ICM over a composite kernel (RBF[0] x Matern-5/2[1] + RQ): four Adam
+    steps against the restatement with the tree as its kernel, then the
+    MultiOutputGP surface (fit, LOVE and exact prediction) on the same tree."""
+    from mojogp_amd import RQ, Matern52, MultiOutputGP, RBF
+    n, d, T = 120, 2, 2
+    rng = np.random.default_rng(77)
+    X = rng.uniform(0, 1, size=(n, d)).astype(np.float32)
+    Y = np.stack([np.sin(5 * X[:, 0]), np.sin(5 * X[:, 0] + 0.6) * X[:, 1]]) \
+        + 0.05 * rng.normal(size=(T, n))
+    Yb = np.ascontiguousarray(Y.reshape(-1), dtype=np.float32)
+    node = RBF(active_dims=[0]) * Matern52(active_dims=[1]) + RQ()
+    tree = ok.TreeKernel(node.to_dict(), d)
+    init = np.array([0.5, 1.0, 0.7, 1.0, 0.6, 1.5, 0.5], np.float32)
+    noise0 = np.full(T, 0.1, np.float32)
+    mean0 = Y.mean(axis=1).astype(np.float32)
+    iters = 4
+    print("icm train with kernel tree", flush=True)
+    o = _lib.ICMTrainOpts(iters, 0.05, -1, 6, 300, 1e-4, 5, 0, 0.5, 30, 15, 1e-4, 0, 1)
+    prov = NativeProvider(None, False, X, init, 0.0, tree_spec=node.to_tree_spec(d))
+    try:
+        got = _train_native(prov, Yb, T, init, noise0, 1.0, mean0, o, None)
+    finally:
+        prov.close()
+    ref = oi.train(tree, False, X, Yb, init, noise0, 1.0, mean0, fixed=None, max_iterations=iters,
+                   learning_rate=0.05, num_probes=6, max_cg=300, max_tridiag=30, cg_tol=1e-4,
+                   precond_rank=5)
+    print(f"  nll {got['nll_history']} vs {ref['nll_history']}", flush=True)
+    np.testing.assert_allclose(got["nll_history"], ref["nll_history"], rtol=0, atol=1e-4)
+    assert _rel(got["params"], ref["params"]) <= 1e-3
+    assert _rel(got["B"], ref["B"]) <= 1e-3
+    gp = MultiOutputGP(node)
+    gp.fit(X, Y.T.astype(np.float32), max_iterations=10, initial_params=init)
+    Xs = rng.uniform(0, 1, size=(15, d)).astype(np.float32)
+    for vm in ("love", "exact"):
+        mean, var = gp.predict(Xs, return_var=True, variance_method=vm)
+        assert np.all(np.isfinite(mean)) and np.all(np.asarray(var) > 0)
+    with pytest.raises(NotImplementedError):
+        gp.sample_posterior(Xs, n_samples=2, method="pathwise")
