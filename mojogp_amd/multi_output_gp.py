@@ -127,7 +127,11 @@ class MultiOutputLMCGP:
                 k = _KERNEL_STRINGS[k.lower()]()
             if not isinstance(k, KernelNode):
                 raise ValueError("All kernels must be KernelNode objects or valid kernel strings.")
-            k.native_kind()  # raises for unsupported trees
+            if not k.is_native_leaf() and (k.has_categorical() or not k.is_tree_servable()
+                                           or k.num_params() != k.engine_num_params()):
+                raise NotImplementedError(f"latent kernel {k!r} is outside the gfx950 LMC "
+                                          "engine (categorical and isotropic polynomial "
+                                          "leaves are single-output only)")
             conv.append(k)
         if not conv:
             raise ValueError("MultiOutputLMCGP needs at least one latent kernel")
@@ -203,8 +207,7 @@ class MultiOutputLMCGP:
 
     def _build_providers(self, X: np.ndarray, params_per_latent, method: str) -> list:
         d = X.shape[1]
-        self._modules = [_engine.load_kernel_module(k.native_kind(), self.ard, d)
-                         for k in self.kernels]
+        self._modules = [_engine.load_kernel_module(k, False, d) for k in self.kernels]
         infos = []
         for mod, p in zip(self._modules, params_per_latent):
             info = mod.init_provider(X, np.asarray(p, np.float32), 0.0)
@@ -332,7 +335,8 @@ class MultiOutputLMCGP:
             num_latents=R, num_tasks=T,
             noise_per_task=np.asarray(raw["noise_per_task"], np.float32),
             lengthscales=ls, outputscales=os_, params_per_latent=[p.tolist() for p in params],
-            kernel_types=np.asarray([k.native_kind() for k in self.kernels], np.int32),
+            kernel_types=np.asarray([k.native_kind() if k.is_native_leaf() else -1
+                                     for k in self.kernels], np.int32),
             A_matrices=A, L_factors=np.asarray(raw["L_factors"], np.float32), B=B,
             Q=Q.astype(np.float32), Lambda=lam.astype(np.float32),
             alpha=np.asarray(raw["alpha"], np.float32), use_ard=self.ard,
@@ -554,6 +558,9 @@ class MultiOutputLMCGP:
         noise = np.asarray(r.noise_per_task, np.float32)
         mean = np.asarray(self._fitted_mean, np.float32)
         fmaps, mix = [], []
+        if not all(k.is_native_leaf() for k in self.kernels):
+            raise NotImplementedError("pathwise samples need RBF / Matern latents (random "
+                                      "Fourier features); composite trees have none")
         for s in range(R):
             fmaps.append(build_pathwise_feature_map(
                 self.kernels[s].native_kind(), r.params_per_latent[s], input_dim=d,

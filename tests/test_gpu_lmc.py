@@ -402,3 +402,49 @@ def test_multi_output_lmcgp_surface(tmp_path):
     gp2 = MultiOutputLMCGP.load(str(tmp_path / "lmc"))
     np.testing.assert_allclose(gp2.predict(Xs, variance_method="mean_only").mean, mean,
                                rtol=1e-6, atol=1e-6)
+
+
+def test_lmc_train_with_tree_latent():
+    """LMC with a composite latent (RBF[0] + Matern-5/2[1]) beside a plain
+    RBF latent: four joint Adam steps against the restatement with the tree
+    as that latent's kernel."""
+    from mojogp_amd import Matern52, RBF
+    n, d, T, iters = 90, 2, 2, 4
+    rng = np.random.default_rng(55)
+    X = rng.uniform(0, 1, size=(n, d)).astype(np.float32)
+    Y = np.stack([np.sin(5 * X[:, 0]), np.cos(3 * X[:, 1])]) + 0.05 * rng.normal(size=(T, n))
+    Yb = np.ascontiguousarray(Y.reshape(-1), dtype=np.float32)
+    node = RBF(active_dims=[0]) + Matern52(active_dims=[1])
+    tree = ok.TreeKernel(node.to_dict(), d)
+    init = [np.array([0.5, 1.0], np.float32), np.array([0.6, 0.8, 0.7, 0.9], np.float32)]
+    noise0 = np.full(T, 0.1, np.float32)
+    mean0 = Y.mean(axis=1).astype(np.float32)
+    print("lmc train with a tree latent", flush=True)
+    provs = [NativeProvider(ok.RBF, False, X, init[0], 0.0),
+             NativeProvider(None, False, X, init[1], 0.0, tree_spec=node.to_tree_spec(d))]
+    o = _lib.LMCTrainOpts(iters, 0.05, 6, 200, 1e-3, 5, 0, 0.5, 30, 1e-4, 15)
+    P = 6
+    out_p = np.zeros(P, np.float32)
+    outA, outL = np.zeros((2, T, T), np.float32), np.zeros((2, T, T), np.float32)
+    vd, nz, mn = np.zeros((2, T), np.float32), np.zeros(T, np.float32), np.zeros(T, np.float32)
+    alpha = np.zeros(n * T, np.float32)
+    hist, times = np.zeros(iters, np.float32), np.zeros(iters, np.float64)
+    res = _lib.LMCTrainResult()
+    res.params, res.A, res.L, res.var_diag = (_lib.fptr(out_p), _lib.fptr(outA),
+                                              _lib.fptr(outL), _lib.fptr(vd))
+    res.noise, res.mean, res.alpha = _lib.fptr(nz), _lib.fptr(mn), _lib.fptr(alpha)
+    res.nll_history, res.iter_times_ms = _lib.fptr(hist), _lib.dptr(times)
+    mask = np.ones(P, np.int32)
+    try:
+        _lib.call("mgp_lmc_train", _lib.handles(provs), 2, T, _lib.fptr(Yb),
+                  _lib.fptr(np.concatenate(init)), mask.ctypes.data_as(_lib.c_int_p),
+                  _lib.fptr(noise0), None, _lib.fptr(mean0), C.byref(o), C.byref(res))
+    finally:
+        _close(provs)
+    ref = ol.train([ok.RBF, tree], [False, False], X, Yb, init, noise0, mean0,
+                   max_iterations=iters, learning_rate=0.05, num_probes=6, max_cg=200,
+                   max_tridiag=30, cg_tol=1e-3, precond_rank=5)
+    print(f"  nll {hist[:res.history_len]} vs {ref['nll_history']}", flush=True)
+    np.testing.assert_allclose(hist, ref["nll_history"], rtol=0, atol=1e-4)
+    assert _rel(out_p, np.concatenate(ref["params"])) <= 1e-3
+    assert _rel(nz, ref["noise"]) <= 1e-3
