@@ -55,14 +55,20 @@ MGP_API int mgp_init_provider(int kind, int ard, int d, int64_t n,
                               const float* X, const float* params, int nparams,
                               float noise, void** out_handle);
 /* Provider for a composite kernel tree: sums, products and scales of RBF,
- * Matern-1/2, 3/2, 5/2, RQ and periodic leaves, each leaf on a subset of the
- * input dimensions.  spec[spec_len] = [d, nparams, nleaves, nnodes,
+ * Matern-1/2, 3/2, 5/2, RQ, periodic, linear, polynomial and categorical
+ * leaves, each leaf on a subset of the input dimensions.
+ * spec[spec_len] = [d, nparams, nleaves, nnodes,
  *   per leaf (tree order): code (0 RBF, 1 M52, 2 M12, 3 M32, 4 RQ,
- *   5 periodic), ard, ndim, p0, dims[ndim],
+ *   5 periodic, 6 categorical, 7 linear, 8 polynomial), ard, ndim, p0,
+ *   [degree: polynomial leaves only], dims[ndim],
  *   per node (children first, root last): code (0 leaf: a = leaf index;
  *   1 sum / 2 product: a, b = child nodes; 3 scale: a = child node,
  *   b = index of the scale factor in params), a, b].
- * Leaf parameters start at p0: [ls | ls_0..ls_{q-1}], (alpha | period), os.
+ * Leaf parameters start at p0: [ls | ls_0..ls_{q-1}], (alpha | period), os;
+ * linear [var | var_0..], os; polynomial [var | var_0..], degree, offset, os.
+ * Categorical leaves: ard = number of levels L, ndim = 1 (the column holding
+ * the level code), p0 = offset of their L x L table after the parameters
+ * (mgp_set_categorical_tables / mgp_set_categorical_params).
  * At most 8 leaves, 16 nodes, 48 parameters, d <= 32, 64 leaf dimensions.
  * Replaces init_provider of a generated composite module (the kernel
  * expression tree of codegen_engine/expressions.py:474-648 compiled per
