@@ -196,7 +196,7 @@ __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
 
 // Leaf values of one row against kTreeChunk columns (rows of xc with stride
 // w): the leaf's fields and parameters are read once for the whole chunk.
-constexpr int kTreeChunk = 4;
+constexpr int kTreeChunk = 8;
 
 __device__ __forceinline__ void tree_leaf_chunk(const KernelTree& t, int l,
                                                 const float* __restrict__ p, const float* xi,

@@ -16,7 +16,7 @@ namespace {
 constexpr int kTile = 128;      // column points per LDS tile
 constexpr int kMaxCols = 16;    // right-hand sides per pass
 constexpr int kGradCols = 16;   // gradient-trace factor columns per pass
-static_assert(kTreeChunk == 4 && kTile % kTreeChunk == 0, "float4 chunk reads");
+static_assert(kTreeChunk % 4 == 0 && kTile % kTreeChunk == 0, "float4 chunk reads");
 
 void require(bool ok, const std::string& msg) {
   if (!ok) throw Error(ST_INVALID, msg);
@@ -59,8 +59,12 @@ __global__ __launch_bounds__(256) void k_tree_matvec(
       float kv[kTreeChunk];
       tree_value_chunk(t, p, xi, sm + jj * d, d, kv);
       for (int c = 0; c < ncols; ++c) {
-        const float4 vv = *reinterpret_cast<const float4*>(vt + c * kTile + jj);
-        part[c] = fmaf(kv[0], vv.x, fmaf(kv[1], vv.y, fmaf(kv[2], vv.z, fmaf(kv[3], vv.w, part[c]))));
+        float s = part[c];
+        for (int h = 0; h < kTreeChunk; h += 4) {
+          const float4 vv = *reinterpret_cast<const float4*>(vt + c * kTile + jj + h);
+          s = fmaf(kv[h], vv.x, fmaf(kv[h + 1], vv.y, fmaf(kv[h + 2], vv.z, fmaf(kv[h + 3], vv.w, s))));
+        }
+        part[c] = s;
       }
     }
     for (int c = 0; c < ncols; ++c) acc[c] += (double)part[c];
