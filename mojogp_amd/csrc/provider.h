@@ -43,6 +43,7 @@ struct Provider {
   // Categorical correlation tables of the tree's categorical leaves
   // (tree.table_size entries, placed after the parameters in tparams).
   std::vector<float> cat_tables;
+  DevBuf<float> tree_ws;  // column-split partial products of the tree matvec
 
   hipStream_t st = nullptr;
   DevBuf<float> X;             // raw training inputs [n][d]

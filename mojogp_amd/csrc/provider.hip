@@ -201,7 +201,7 @@ void Provider::forward_scalar(const float* V, int ncols, float* out) {
   }
   if (is_tree) {
     tree_matvec(tree, tparams.ptr, train.z.ptr, n, train.z.ptr, n, V, ncols, noise, true, out,
-                st);
+                tree_ws, st);
     return;
   }
   if (!gram_form_ok(kind, train, train)) {
@@ -236,7 +236,7 @@ void Provider::cross(const PackedPoints& rows, const float* V, int ncols,
                      float* out) {
   if (is_tree) {
     tree_matvec(tree, tparams.ptr, rows.z.ptr, rows.n, train.z.ptr, n, V, ncols, 0.f, false,
-                out, st);
+                out, tree_ws, st);
     return;
   }
   MatvecArgs a;

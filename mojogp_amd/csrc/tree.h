@@ -9,7 +9,7 @@ namespace mgp {
 // device row-major points Xr [m][d], Xc [n][d] and column-major V [ncols][n].
 void tree_matvec(const KernelTree& t, const float* p_dev, const float* Xr, int64_t m,
                  const float* Xc, int64_t n, const float* V, int ncols, float noise,
-                 bool square, float* out, hipStream_t st);
+                 bool square, float* out, DevBuf<float>& work, hipStream_t st);
 // out[i] = K(X_i, X_i) for device points X [m][d].
 void tree_self_values(const KernelTree& t, const float* p_dev, const float* X, int64_t m,
                       float* out, hipStream_t st);

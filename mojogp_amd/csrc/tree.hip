@@ -27,7 +27,7 @@ void require(bool ok, const std::string& msg) {
 __global__ __launch_bounds__(256) void k_tree_matvec(
     const float* __restrict__ Xr, int64_t m, const float* __restrict__ Xc, int64_t n,
     KernelTree t, const float* __restrict__ p, const float* __restrict__ V, int ncols,
-    float noise, int add_noise, float* __restrict__ out) {
+    float* __restrict__ part) {
   // LDS: column coordinates [kTile][d], then right-hand sides transposed
   // [ncols][kTile] so one 16-byte read serves a chunk of four columns
   extern __shared__ float sm[];
@@ -38,7 +38,12 @@ __global__ __launch_bounds__(256) void k_tree_matvec(
   for (int k = 0; k < d; ++k) xi[k] = (i < m) ? Xr[i * d + k] : 0.0f;
   double acc[kMaxCols];
   for (int c = 0; c < kMaxCols; ++c) acc[c] = 0.0;
-  for (int64_t j0 = 0; j0 < n; j0 += kTile) {
+  // column range of this split (whole tiles)
+  const int64_t tiles = (n + kTile - 1) / kTile;
+  const int64_t tps = (tiles + gridDim.y - 1) / gridDim.y;
+  const int64_t jbeg = (int64_t)blockIdx.y * tps * kTile;
+  const int64_t jend = min(n, jbeg + tps * kTile);
+  for (int64_t j0 = jbeg; j0 < jend; j0 += kTile) {
     __syncthreads();
     for (int q = threadIdx.x; q < kTile * d; q += blockDim.x) {
       const int64_t j = j0 + q / d;
@@ -70,12 +75,22 @@ __global__ __launch_bounds__(256) void k_tree_matvec(
     for (int c = 0; c < ncols; ++c) acc[c] += (double)part[c];
   }
   if (i < m) {
-    for (int c = 0; c < ncols; ++c) {
-      float o = (float)acc[c];
-      if (add_noise) o = fmaf(noise, V[(int64_t)c * m + i], o);
-      out[(int64_t)c * m + i] = o;
-    }
+    float* dst = part + (int64_t)blockIdx.y * ncols * m;
+    for (int c = 0; c < ncols; ++c) dst[(int64_t)c * m + i] = (float)acc[c];
   }
+}
+
+// out[c][i] = sum_y part[y][c][i] (+ noise V[c][i]), splits summed in order.
+__global__ void k_tree_reduce(const float* __restrict__ part, int splits, int64_t m, int ncols,
+                              const float* __restrict__ V, float noise, int add_noise,
+                              float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= m * ncols) return;
+  double s = 0.0;
+  for (int y = 0; y < splits; ++y) s += (double)part[(int64_t)y * ncols * m + idx];
+  float o = (float)s;
+  if (add_noise) o = fmaf(noise, V[idx], o);
+  out[idx] = o;
 }
 
 // out[i] = K(x_i, x_i)
@@ -348,13 +363,24 @@ double tree_diag(const KernelTree& t, const float* params) {
 
 void tree_matvec(const KernelTree& t, const float* p_dev, const float* Xr, int64_t m,
                  const float* Xc, int64_t n, const float* V, int ncols, float noise,
-                 bool square, float* out, hipStream_t st) {
+                 bool square, float* out, DevBuf<float>& work, hipStream_t st) {
+  if (m <= 0) return;
+  // Column splits so that the launch covers the chip (>= ~2048 blocks of
+  // 256 rows), at least one 128-column tile per split.
+  const int64_t rows = ceil_div(m, 256);
+  const int64_t tiles = ceil_div(std::max<int64_t>(n, 1), kTile);
+  const int splits = (int)std::max<int64_t>(
+      1, std::min<int64_t>(ceil_div(2048, rows), tiles));
   for (int c0 = 0; c0 < ncols; c0 += kMaxCols) {
     const int nc = std::min(kMaxCols, ncols - c0);
+    float* part = work.ensure((size_t)splits * nc * m);
     const size_t shm = (size_t)kTile * (t.d + nc) * sizeof(float);
-    hipLaunchKernelGGL(k_tree_matvec, dim3((unsigned)ceil_div(std::max<int64_t>(m, 1), 256)),
-                       dim3(256), shm, st, Xr, m, Xc, n, t, p_dev, V + (int64_t)c0 * n, nc,
-                       noise, square ? 1 : 0, out + (int64_t)c0 * m);
+    hipLaunchKernelGGL(k_tree_matvec, dim3((unsigned)rows, (unsigned)splits), dim3(256), shm, st,
+                       Xr, m, Xc, n, t, p_dev, V + (int64_t)c0 * n, nc, part);
+    MGP_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(k_tree_reduce, dim3((unsigned)ceil_div(m * nc, 256)), dim3(256), 0, st,
+                       part, splits, m, nc, V + (int64_t)c0 * n, noise, square ? 1 : 0,
+                       out + (int64_t)c0 * m);
     MGP_HIP_CHECK(hipGetLastError());
   }
 }
