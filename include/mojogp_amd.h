@@ -182,6 +182,11 @@ typedef struct mgp_train_opts {
   float noise_floor;
   float noise_regularization;
   int progress_interval;
+  /* Forced-failure switch for tests of the NaN recovery (no counterpart in
+   * the reference's arguments): bit i set treats the evaluated NLL of
+   * iteration i (i < 64) as NaN, which runs the recovery path of
+   * jit_training.mojo:605-685.  0 in normal use. */
+  unsigned long long nan_inject_mask;
 } mgp_train_opts_t;
 
 /* Progress event (the reference's event dict, jit_progress.mojo:22-65). */

@@ -158,7 +158,10 @@ class Engine:
     """Engine module: training and prediction entry points."""
 
     # ------------------------------------------------------------ train
-    def train(self, *args) -> dict[str, Any]:
+    def train(self, *args, nan_inject_mask: int = 0) -> dict[str, Any]:
+        """train_python (jit_engine_bindings.mojo:123-432).  ``nan_inject_mask``
+        (keyword only, tests): bit i treats the NLL of iteration i as NaN so
+        the recovery path runs."""
         if len(args) < 17 or len(args) > 25:
             raise ValueError("train() expects between 17 and 25 positional arguments")
         info, y, params, init_noise = args[0], args[1], args[2], float(args[3])
@@ -185,6 +188,7 @@ class Engine:
         o.noise_regularization = float(args[22]) if len(args) > 22 else 0.01
         callback = args[23] if len(args) > 23 else None
         o.progress_interval = int(args[24]) if len(args) > 24 else 1
+        o.nan_inject_mask = int(nan_inject_mask)
         if o.max_iterations <= 0:
             raise ValueError("max_iterations must be > 0")
 

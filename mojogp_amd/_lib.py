@@ -36,6 +36,7 @@ class TrainOpts(C.Structure):
         ("enable_early_stopping", C.c_int), ("early_stop_patience", C.c_int),
         ("early_stop_tol", C.c_float), ("learn_noise", C.c_int), ("noise_floor", C.c_float),
         ("noise_regularization", C.c_float), ("progress_interval", C.c_int),
+        ("nan_inject_mask", C.c_ulonglong),
     ]
 
 

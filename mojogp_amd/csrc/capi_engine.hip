@@ -3,6 +3,8 @@
 // include/mojogp_amd.h.
 #include <chrono>
 #include <cstring>
+#include <mutex>
+#include <set>
 
 #include "engine.h"
 #include "mixed.h"
@@ -24,6 +26,21 @@ struct PredictionCache {
   int variance_method = 0;
   ExactVarianceOptions exact;
 };
+
+// Live prediction-cache handles.  The reference passes the raw pointer as an
+// int (jit_engine_bindings.mojo:111-121); here every handle is checked
+// against this set, so a destroyed or foreign handle is an error, not a
+// use-after-free.
+std::mutex g_cache_mu;
+std::set<PredictionCache*> g_caches;
+
+PredictionCache* live_cache(void* h) {
+  std::lock_guard<std::mutex> lk(g_cache_mu);
+  auto* c = static_cast<PredictionCache*>(h);
+  MGP_REQUIRE(h != nullptr && g_caches.count(c) != 0,
+              "unknown or destroyed prediction cache handle");
+  return c;
+}
 
 ExactVarianceOptions exact_options(const mgp_predict_opts_t& o) {
   ExactVarianceOptions e;
@@ -66,6 +83,7 @@ TrainOptions to_options(const mgp_train_opts_t* o) {
   t.noise_floor = o->noise_floor;
   t.noise_regularization = o->noise_regularization;
   t.progress_interval = o->progress_interval;
+  t.nan_inject_mask = o->nan_inject_mask;
   return t;
 }
 
@@ -337,6 +355,10 @@ int mgp_prepare_prediction_cache(void* handle, const float* y, const mgp_predict
       delete c;
       throw;
     }
+    {
+      std::lock_guard<std::mutex> lk(g_cache_mu);
+      g_caches.insert(c);
+    }
     *cache_out = c;
   });
 }
@@ -346,8 +368,7 @@ int mgp_predict_with_cache(void* handle, void* cache, const float* Xs, int64_t m
                            mgp_predict_info_t* info) {
   return guarded([&] {
     Provider* pv = as_provider(handle);
-    MGP_REQUIRE(cache != nullptr, "null prediction cache");
-    auto* c = static_cast<PredictionCache*>(cache);
+    auto* c = live_cache(cache);
     MGP_REQUIRE(c->owner == pv, "prediction cache belongs to another provider");
     MGP_REQUIRE(variance_method != 1 || c->state.rank > 0,
                 "cache holds no LOVE root; prepare it with variance_method=1");
@@ -369,7 +390,14 @@ int mgp_predict_with_cache(void* handle, void* cache, const float* Xs, int64_t m
 }
 
 int mgp_destroy_prediction_cache(void* cache) {
-  return guarded([&] { delete static_cast<PredictionCache*>(cache); });
+  return guarded([&] {
+    auto* c = live_cache(cache);
+    {
+      std::lock_guard<std::mutex> lk(g_cache_mu);
+      g_caches.erase(c);
+    }
+    delete c;
+  });
 }
 
 }  // extern "C"

@@ -120,6 +120,7 @@ struct TrainOptions {
   float noise_floor = 1e-6f;
   float noise_regularization = 0.01f;
   int progress_interval = 1;
+  uint64_t nan_inject_mask = 0;  // tests: bit i forces the NLL of iteration i to NaN
 };
 
 struct ProgressEvent {

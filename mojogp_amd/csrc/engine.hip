@@ -5,6 +5,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <limits>
 
 #include "host_numerics.h"
 
@@ -832,7 +833,8 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
     sub_scalar(yc.ptr, y.ptr, raw_mean, n, st);
     BBMMResult r = bbmm_step(pv, Pc, o.use_preconditioner, yc.ptr, o.num_probes, o.max_cg_iter,
                              o.max_tridiag_iter, o.cg_tol, it, it > 0, work);
-    const float nll = r.nll;
+    const bool forced_nan = it < 64 && ((o.nan_inject_mask >> it) & 1ull);
+    const float nll = forced_nan ? std::numeric_limits<float>::quiet_NaN() : r.nll;
     res.cg_iterations_history.push_back(r.cg_iterations);
 
     if (nll != nll) {

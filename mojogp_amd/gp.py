@@ -191,6 +191,7 @@ class SingleOutputGP:
         self._training_method: Optional[str] = None
         self._kernel_module: Optional[_engine.KernelModule] = None
         self._engine: Optional[_engine.Engine] = None
+        self._module_signature: Optional[tuple] = None
         self._provider_info: Optional[dict] = None
         self._provider_state_current = False
         self._cached_alpha: Optional[np.ndarray] = None
@@ -245,13 +246,28 @@ class SingleOutputGP:
     def _is_single_kernel_type(self, kt: KernelType) -> bool:
         return self.kernel.operator is None and self.kernel.kernel_type == kt
 
+    def _has_periodic_kernel(self) -> bool:
+        """Any periodic leaf in the tree (gp.py:702-716)."""
+        def walk(node) -> bool:
+            if node is None or not isinstance(node, KernelNode):
+                return False
+            if node.kernel_type == KernelType.PERIODIC:
+                return True
+            return walk(node.left) or walk(node.right)
+        return walk(self.kernel)
+
     # ------------------------------------------------------------ lifecycle
+    def _current_module_signature(self) -> tuple:
+        cont = self._cont_cols if self.kernel.has_categorical() else None
+        return (repr(self.kernel.to_dict()), self.dim, None if cont is None else tuple(cont))
+
     def _ensure_compiled(self) -> None:
         if self._kernel_module is None or self._engine is None:
             cont = self._cont_cols if self.kernel.has_categorical() else None
             self._kernel_module = _engine.load_kernel_module(self.kernel, False, self.dim,
                                                              default_dims=cont)
             self._engine = _engine.load_engine()
+            self._module_signature = self._current_module_signature()
 
     def _resolve_mixed(self, X) -> None:
         """Categorical columns, levels and continuous columns of a mixed kernel
@@ -296,8 +312,9 @@ class SingleOutputGP:
 
     def _destroy_provider_info(self) -> None:
         self._destroy_prediction_cache()
-        if self._provider_info is not None and self._kernel_module is not None:
-            self._kernel_module.destroy_provider(self._provider_info)
+        destroy = getattr(self._kernel_module, "destroy_provider", None)
+        if self._provider_info is not None and destroy is not None:
+            destroy(self._provider_info)
         self._provider_info = None
         self._provider_state_current = False
 
@@ -321,11 +338,16 @@ class SingleOutputGP:
             if mode == 3:
                 groups = self._noise_group_train
                 ngroups = int(self._noise_group_values.size)
-        info = self._kernel_module.init_provider(np.ascontiguousarray(X, dtype=np.float32),
-                                                 np.ascontiguousarray(engine_params, np.float32),
-                                                 float(noise), observation_noise=obs,
-                                                 noise_mode=mode, noise_group_train=groups,
-                                                 num_noise_groups=ngroups)
+        # Positional, optional tail only when present (gp.py:470-482).
+        provider_args = [np.ascontiguousarray(X, dtype=np.float32),
+                         np.ascontiguousarray(engine_params, np.float32), float(noise)]
+        if obs is not None:
+            provider_args.append(obs)
+            if mode is not None:
+                provider_args.append(int(mode))
+                if groups is not None:
+                    provider_args.extend([groups, int(ngroups or 0)])
+        info = self._kernel_module.init_provider(*provider_args)
         if not training:
             self._set_categorical_tables(info)
         if (method or self._training_method) == "materialized":
@@ -439,8 +461,13 @@ class SingleOutputGP:
         self.kernel = (make_ard_kernel(self._kernel_pre_ard, cont_dim) if self.ard
                        else self._kernel_pre_ard)
         _check_served(self.kernel, self.dim, self._cont_cols if mixed else None)
-        self._kernel_module = None
-        self._engine = None
+        if (self._module_signature is not None
+                and self._module_signature != self._current_module_signature()):
+            # Another kernel layout or input dimension: reload the modules
+            # (modules set by a caller before the first fit are kept, as the
+            # reference's engine-plumbing tests inject them).
+            self._kernel_module = None
+            self._engine = None
 
         default_initial_params = initial_params is None
         if default_initial_params:
@@ -450,6 +477,9 @@ class SingleOutputGP:
             if initial_params.shape[0] != self.num_params:
                 raise ValueError(f"initial_params has {initial_params.shape[0]} values, "
                                  f"expected {self.num_params}")
+        # Noise floor for periodic kernels (gp.py:1331-1333).
+        if self._has_periodic_kernel() and initial_noise < 0.05:
+            initial_noise = max(initial_noise, 0.05)
         _verbose = verbose if verbose is not None else self.verbose
 
         method = normalize_fit_method(method, allow_auto=True)

@@ -404,19 +404,76 @@ def _clip(g, m=100.0):
     return F32(min(max(g, -m), m))
 
 
+def cosine_lr(lr_max, iteration: int, total: int):
+    """Cosine annealing from lr_max to lr_max/20 (training_utils.mojo:23-40)."""
+    lr_max = F32(lr_max)
+    lr_min = lr_max / F32(20.0)
+    frac = F32(iteration) / F32(max(total, 1))
+    return F32(lr_min + F32(0.5) * (lr_max - lr_min) * (F32(1.0) + F32(np.cos(F32(np.pi) * frac))))
+
+
+def adam_update(raw, m, v, t: int, grads, lr, chain=None):
+    """One Adam step on raw (unconstrained) parameters, in fp32
+    (training_utils.mojo:214-316): the gradient in constrained space is
+    clipped to [-100, 100] (NaN / |g| > 1e30 -> 0), taken through the
+    softplus chain rule (or the given d(constrained)/d(raw)), moments with
+    beta = (0.9, 0.999), bias correction at step t + 1, eps 1e-8, and the
+    new raw value clamped to [-20, 20].  Returns (raw, m, v, t + 1)."""
+    raw = np.array(raw, F32)
+    m = np.array(m, F32)
+    v = np.array(v, F32)
+    for q in range(len(raw)):
+        d = _softplus_deriv(raw[q]) if chain is None else F32(chain[q])
+        gr = _clip(grads[q]) * d
+        m[q] = F32(0.9) * m[q] + F32(0.1) * gr
+        v[q] = F32(0.999) * v[q] + F32(0.001) * gr * gr
+    t += 1
+    bc1 = F32(1) - F32(0.9) ** t
+    bc2 = F32(1) - F32(0.999) ** t
+    for q in range(len(raw)):
+        nr = raw[q] - F32(lr) * (m[q] / bc1) / (np.sqrt(v[q] / bc2) + F32(1e-8))
+        raw[q] = F32(min(max(nr, -20.0), 20.0))
+    return raw, m, v, t
+
+
+def adam_mean_update(raw_mean, mm, vm, t: int, grad, lr):
+    """Adam step of the constant mean (jit_training.mojo:858-875): clipped
+    gradient, no chain rule, bias correction with the kernel step's t (already
+    incremented), no clamp.  Returns (raw_mean, mm, vm)."""
+    mg = _clip(grad)
+    mm = F32(0.9) * F32(mm) + F32(0.1) * mg
+    vm = F32(0.999) * F32(vm) + F32(0.001) * mg * mg
+    bc1 = F32(1) - F32(0.9) ** t
+    bc2 = F32(1) - F32(0.999) ** t
+    return F32(raw_mean - F32(lr) * (mm / bc1) / (np.sqrt(vm / bc2) + F32(1e-8))), mm, vm
+
+
 def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_iterations=50,
           learning_rate=0.01, num_probes=10, max_cg=100, cg_tol=1e-2, precond_rank=0,
           max_tridiag=30, rebuild_threshold=0.5, init_mean=None, noise_vec=None,
-          learned=None):
+          learned=None, use_cosine_lr=False, enable_early_stopping=False,
+          early_stop_patience=10, early_stop_tol=1e-4, nan_iterations=(), evaluate=None):
     """Adam over raw (inverse-softplus) hyperparameters and the constant mean,
-    with preconditioner rebuilds, NaN recovery and best-NLL restore.  With a
-    fixed noise vector the noise is not learned (jit_training.mojo:524, 717,
-    947: operator noise 0 + the vector, noise slot frozen, reported noise 0).
+    with preconditioner rebuilds, NaN recovery and best-NLL restore
+    (jit_training.mojo:274-1008).  With a fixed noise vector the noise is not
+    learned (jit_training.mojo:524, 717, 947: operator noise 0 + the vector,
+    noise slot frozen, reported noise 0).
 
     ``learned``: dict(mode=2|3|4, floor, reg, groups / X) for the learned
     per-point noise modes (jit_training.mojo:352-960): the vector is rebuilt
     from its raw state every iteration, the preconditioner rebuilt every
-    iteration, the raw state updated by its own Adam after the kernel step."""
+    iteration, the raw state updated by its own Adam after the kernel step.
+
+    ``use_cosine_lr``: the step uses cosine_lr(learning_rate, it, max_iterations)
+    (computed from the initial rate, so NaN halving does not change it;
+    jit_training.mojo:697-699).  ``enable_early_stopping``: stop once the NLL
+    has not improved on the best-so-far by more than early_stop_tol for
+    early_stop_patience iterations (jit_training.mojo:884-905; converged).
+
+    Test hooks: ``nan_iterations`` replaces the evaluated NLL of those
+    iterations by NaN (the engine's forced-failure switch), and ``evaluate``
+    replaces the BBMM evaluation: evaluate(it, params, noise, y_c, P, warm)
+    returns a dict with nll, grads [P + 1], alpha [n], x, cg_iterations."""
     fixed = noise_vec is not None and learned is None
     if learned is not None:
         lmode, lfloor, lreg = learned["mode"], float(learned["floor"]), float(learned["reg"])
@@ -444,19 +501,30 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
     best = dict(nll=np.inf, raw=raw.copy(), mean=raw_mean, m=m.copy(), v=v.copy(), mm=mm, vm=vm, t=t,
                 alpha=None)
     lr = F32(learning_rate)
+    nan_iterations = set(int(i) for i in nan_iterations)
+
+    scripted = evaluate is not None  # a scripted objective needs no preconditioner
 
     def build(params, noise):
-        if precond_rank <= 0:
+        if precond_rank <= 0 or scripted:
             return None
         K = ok.kernel_matrix(kind, X, X, params, ard)
         L, _ = pivoted_cholesky(K, precond_rank)
         return Precond(L, np.asarray(noise_vec, np.float64) if noise_vec is not None else noise)
 
+    if evaluate is None:
+        def evaluate(it, params, noise, y_c, P, warm):
+            return bbmm_step(kind, ard, X, y_c, params.astype(np.float64), float(noise), P,
+                             num_probes, max_cg, max_tridiag, cg_tol, it, warm,
+                             noise_vec=noise_vec)
+
     P = build(np.asarray(init_params, np.float64), init_noise)
     last_params, last_noise = np.asarray(init_params, F32).copy(), F32(init_noise)
     x_prev = None
-    nll_hist, cg_hist = [], []
+    nll_hist, cg_hist, lr_hist, rebuild_steps = [], [], [], []
+    best_es, no_improve, converged, iterations = F32(1e30), 0, False, 0
     for it in range(max_iterations):
+        iterations = it + 1
         params = np.array([_softplus(r) for r in raw[:Pn]], F32)
         noise = F32(0.0) if fixed else _softplus(raw[Pn])
         if learned is not None:
@@ -470,62 +538,64 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
                 rel = rebuild_threshold + 1.0
             if rel > rebuild_threshold:
                 P = build(params, noise)
+                rebuild_steps.append(it)
                 last_params, last_noise = params.copy(), noise
         y_c = (y.astype(F32) - raw_mean).astype(np.float64)
         warm = None
         if it > 0 and x_prev is not None:
             warm = x_prev.copy()
             warm[:, 1:] = 0.0
-        res = bbmm_step(kind, ard, X, y_c, params.astype(np.float64), float(noise), P, num_probes,
-                        max_cg, max_tridiag, cg_tol, it, warm, noise_vec=noise_vec)
-        x_prev = res["x"]
-        nll = res["nll"]
+        res = evaluate(it, params, noise, y_c, P, warm)
+        x_prev = res.get("x")
+        nll = F32(np.nan) if it in nan_iterations else res["nll"]
         cg_hist.append(res["cg_iterations"])
         if np.isnan(nll):
             lr = lr * F32(0.5)
             raw, raw_mean = best["raw"].copy(), best["mean"]
             m, v, mm, vm, t = best["m"].copy(), best["v"].copy(), best["mm"], best["vm"], best["t"]
             params = np.array([_softplus(r) for r in raw[:Pn]], F32)
-            noise = _softplus(raw[Pn])
+            noise = F32(0.0) if fixed else _softplus(raw[Pn])
             last_params, last_noise = params.copy(), noise
             if learned is not None:
                 lraw, lm, lv = (a.copy() for a in lbest)
                 noise_vec = learned_noise_vector(lmode, lraw, lfloor, lgroups,
                                                  lX).astype(np.float64)
             P = build(params, noise)
+            rebuild_steps.append(it)
             continue
         if nll < best["nll"]:
             best.update(nll=nll, raw=raw.copy(), mean=raw_mean, m=m.copy(), v=v.copy(), mm=mm,
-                        vm=vm, t=t, alpha=res["alpha"].copy())
+                        vm=vm, t=t, alpha=np.asarray(res["alpha"]).copy())
             if learned is not None:
                 lbest = (lraw.copy(), lm.copy(), lv.copy())
-        g = res["grads"].astype(F32)
+        lr_eff = cosine_lr(learning_rate, it, max_iterations) if use_cosine_lr else lr
+        lr_hist.append(float(lr_eff))
+        g = np.asarray(res["grads"], F32).copy()
         if fixed:
             g[Pn] = F32(0.0)
-        for q in range(Pn + 1):
-            gr = _clip(g[q]) * _softplus_deriv(raw[q])
-            m[q] = F32(0.9) * m[q] + F32(0.1) * gr
-            v[q] = F32(0.999) * v[q] + F32(0.001) * gr * gr
-        t += 1
-        bc1 = F32(1) - F32(0.9) ** t
-        bc2 = F32(1) - F32(0.999) ** t
-        for q in range(Pn + 1):
-            nr = raw[q] - lr * (m[q] / bc1) / (np.sqrt(v[q] / bc2) + F32(1e-8))
-            raw[q] = F32(min(max(nr, -20.0), 20.0))
+        raw, m, v, t = adam_update(raw, m, v, t, g, lr_eff)
         if learned is not None:
+            bc1 = F32(1) - F32(0.9) ** t
+            bc2 = F32(1) - F32(0.999) ** t
             lg = learned_noise_grad(lmode, lraw, res["rowdot"], lfloor, lreg, init_noise,
                                     lgroups, lX).astype(F32)
             lg[~np.isfinite(lg) | (np.abs(lg) > 1e6)] = 0.0
             lm = (F32(0.9) * lm + F32(0.1) * lg).astype(F32)
             lv = (F32(0.999) * lv + F32(0.001) * lg * lg).astype(F32)
-            lraw = (lraw - lr * (lm / bc1) / (np.sqrt(lv / bc2) + F32(1e-8))).astype(F32)
-        mg = _clip(-np.sum(res["alpha"]) / n)
-        mm = F32(0.9) * mm + F32(0.1) * mg
-        vm = F32(0.999) * vm + F32(0.001) * mg * mg
-        raw_mean = F32(raw_mean - lr * (mm / bc1) / (np.sqrt(vm / bc2) + F32(1e-8)))
+            lraw = (lraw - lr_eff * (lm / bc1) / (np.sqrt(lv / bc2) + F32(1e-8))).astype(F32)
+        raw_mean, mm, vm = adam_mean_update(raw_mean, mm, vm, t,
+                                            -np.sum(res["alpha"]) / n, lr_eff)
         if np.isnan(raw_mean) or abs(raw_mean) > 1000:
             raw_mean = F32(init_mean)
         nll_hist.append(nll)
+        if enable_early_stopping:
+            if nll < best_es - F32(early_stop_tol):
+                best_es, no_improve = F32(nll), 0
+            else:
+                no_improve += 1
+                if no_improve >= early_stop_patience:
+                    converged = True
+                    break
     params = np.array([_softplus(r) for r in best["raw"][:Pn]], F32)
     extra = {}
     if learned is not None:
@@ -535,7 +605,9 @@ def train(kind: int, ard: bool, X, y, init_params, init_noise: float, *, max_ite
             "noise": 0.0 if fixed else float(_softplus(best["raw"][Pn])),
             "mean": float(best["mean"]), "final_nll": float(best["nll"]),
             "alpha": best["alpha"], "nll_history": np.array(nll_hist),
-            "cg_iterations_history": np.array(cg_hist)}
+            "cg_iterations_history": np.array(cg_hist), "iterations": iterations,
+            "converged": converged, "lr_history": np.array(lr_hist),
+            "precond_rebuild_steps": rebuild_steps}
 
 
 # ---------------------------------------------------------------- prediction
