@@ -123,6 +123,20 @@ MGP_API int mgp_forward_matvec(void* handle, const float* V, int ncols,
 /* Same with device-resident V/out (no PCIe copies). */
 MGP_API int mgp_forward_matvec_device(void* handle, const float* V_device,
                                       int ncols, float* out_device);
+/* Same as mgp_forward_matvec_device, allocating nothing: no hipMalloc, no
+ * hipFree, no allocating library call.  No counterpart in the reference; it
+ * is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Its work buffers (packed
+ * right-hand sides, column maxima, split partial sums) live in one fixed
+ * 64 MiB device array per GPU, held until the process ends; split partials
+ * that do not fit reduce the split count.  A call whose packed right-hand
+ * sides alone exceed the array (about 4 n min(ncols, 64) bytes: n up to ~1M at
+ * 16 columns, ~260k at 64) fails with MGP_ERR_INVALID.  Serves the single-kernel
+ * matrix-free route only (not kernel trees or materialized providers).  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ * threads, other providers' streams) race. */
+MGP_API int mgp_forward_matvec_device_noalloc(void* handle, const float* V_device,
+                                              int ncols, float* out_device);
 /* (K + noise I) V from per-dimension differences (no Gram form, no MFMA):
  * an independent device cross-check of mgp_forward_matvec.  No reference
  * counterpart; kept for parity tests. */

@@ -174,6 +174,8 @@ _SIGNATURES = {
     "mgp_forward_matvec": (C.c_int, [C.c_void_p, c_float_p, C.c_int, c_float_p]),
     "mgp_forward_matvec_device": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int,
                                             C.c_void_p]),
+    "mgp_forward_matvec_device_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int,
+                                                    C.c_void_p]),
     "mgp_direct_matvec": (C.c_int, [C.c_void_p, c_float_p, C.c_int, c_float_p]),
     "mgp_cross_matvec": (C.c_int, [C.c_void_p, c_float_p, C.c_int64, c_float_p,
                                    C.c_int, c_float_p]),

@@ -3,6 +3,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "mojogp_amd.h"
@@ -25,6 +26,53 @@ __global__ void k_calibration_copy(const float4* __restrict__ a,
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
     b[i] = a[i];
+}
+
+// Work buffers of the allocation-free forward matvec
+// (mgp_forward_matvec_device_noalloc): one fixed array per GPU, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel (on the
+// host the name is only a stand-in); it uses the device address that
+// hipGetSymbolAddress returns for the current device, kept per device below.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+struct ScratchSlot {
+  uint8_t* ptr = nullptr;
+  hipError_t err = hipSuccess;
+  bool tried = false;
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kMaxScratchDevices];
+
+// Resolves this device's scratch address once, with `dev` current (called at
+// provider set-up).  A failure is recorded, not raised: it only disables the
+// allocation-free entry point, which reports it.
+static void setup_scratch(int dev) {
+  if (dev < 0 || dev >= kMaxScratchDevices) return;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  ScratchSlot& s = g_scratch[dev];
+  if (s.tried) return;
+  s.tried = true;
+  void* p = nullptr;
+  s.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (s.err == hipSuccess && p != nullptr) {
+    s.ptr = static_cast<uint8_t*>(p);
+  } else {
+    if (s.err == hipSuccess) s.err = hipErrorInvalidSymbol;
+    (void)hipGetLastError();
+  }
+}
+
+static uint8_t* scratch_of(int dev) {
+  MGP_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  const ScratchSlot& s = g_scratch[dev];
+  MGP_REQUIRE(s.tried, "scratch of this device was never set up");
+  if (s.ptr == nullptr)
+    throw Error(ST_HIP, std::string("scratch unavailable on this device: hipGetSymbolAddress: ") +
+                            hipGetErrorString(s.err));
+  return s.ptr;
 }
 
 }  // namespace mgp
@@ -68,6 +116,8 @@ Provider* finish_provider(Provider* pv, int d, int64_t n, const float* X, const 
     for (int64_t i = 0; i < n; ++i)
       for (int k = 0; k < d; ++k) pv->center[k] += (double)X[i * d + k];
     for (int k = 0; k < d; ++k) pv->center[k] /= (double)n;
+    MGP_HIP_CHECK(hipGetDevice(&pv->device));
+    setup_scratch(pv->device);
     MGP_HIP_CHECK(hipStreamCreateWithFlags(&pv->st, hipStreamNonBlocking));
     pv->X.ensure((size_t)n * d);
     MGP_HIP_CHECK(hipMemcpyAsync(pv->X.ptr, X, (size_t)n * d * sizeof(float),
@@ -224,6 +274,30 @@ int mgp_forward_matvec_device(void* h, const float* V_dev, int ncols,
     MGP_REQUIRE(ncols >= 1, "ncols must be >= 1");
     MGP_REQUIRE(V_dev && out_dev, "null device array");
     pv->forward(V_dev, ncols, out_dev);
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
+int mgp_forward_matvec_device_noalloc(void* h, const float* V_dev, int ncols, float* out_dev) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(ncols >= 1, "ncols must be >= 1");
+    MGP_REQUIRE(V_dev && out_dev, "null device array");
+    MGP_REQUIRE(!pv->is_tree, "the allocation-free matvec does not serve kernel trees");
+    MGP_REQUIRE(!pv->materialized, "the allocation-free matvec does not serve the materialized "
+                                   "route");
+    MatvecWorkspace w;  // fixed-arena mode: its own buffers stay unallocated
+    w.arena = scratch_of(pv->device);
+    w.arena_bytes = kNoAllocScratchBytes;
+    if (pv->fused_route()) {
+      const size_t need = fused_matvec_min_arena(pv->train, ncols);
+      MGP_REQUIRE(need <= kNoAllocScratchBytes,
+                  "n = " + std::to_string(pv->n) + " with " + std::to_string(ncols) +
+                      " columns needs " + std::to_string(need) +
+                      " bytes of scratch; the allocation-free matvec holds at most " +
+                      std::to_string(kNoAllocScratchBytes) + " (64 MiB)");
+    }
+    pv->forward(V_dev, ncols, out_dev, &w);
     MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
   });
 }

@@ -104,6 +104,12 @@ struct MatvecWorkspace {
   DevBuf<uint32_t> colmax;       // per-column max |V| (fp16 scaling of the product)
   DevBuf<uint32_t> colmax_part;  // [64][chunks] row-chunk maxima
   DevBuf<float> partial;  // split-K partial sums
+  // Fixed-arena mode (allocation-free callers): when arena is set, every work
+  // buffer above is carved from [arena, arena + arena_bytes) instead of being
+  // grown with hipMalloc; the split count is capped so the partial sums fit,
+  // and a request that cannot fit even unsplit raises ST_INVALID.
+  uint8_t* arena = nullptr;
+  size_t arena_bytes = 0;
   // Optional HIP-event timing of the tile kernel alone (bench hook).
   bool time_tile = false;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -114,6 +120,11 @@ struct MatvecWorkspace {
 void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,
                   MatvecWorkspace& ws, hipStream_t st, int force_splits = 0);
+
+// Bytes of work buffers one fused_matvec call with ncols right-hand sides
+// over cols needs at the least (no split partials): the arena size below which
+// the fixed-arena mode rejects the call.
+size_t fused_matvec_min_arena(const PackedPoints& cols, int ncols);
 
 // Reference-form product evaluated per pair from per-dimension differences of
 // the scaled coordinates (no Gram form, no MFMA).  Used as an independent

@@ -789,6 +789,42 @@ void pack_points(const float* X_dev, int64_t n, const Coords& co,
   std::memcpy(&pp.max_norm, &bits, sizeof(bits));
 }
 
+namespace {
+
+// Work-buffer source of one fused_matvec column chunk: the workspace's growable
+// buffers, or 256-byte aligned slices of its fixed arena (reset per chunk; the
+// chunks run in stream order, so a later chunk may reuse an earlier one's bytes).
+struct ChunkBuffers {
+  MatvecWorkspace& ws;
+  size_t off = 0;
+  explicit ChunkBuffers(MatvecWorkspace& w) : ws(w) {}
+  size_t left() const { return ws.arena_bytes - off; }
+  template <class T>
+  T* take(DevBuf<T>& buf, size_t count) {
+    if (ws.arena == nullptr) return buf.ensure(count);
+    const size_t bytes = round_up((int64_t)std::max<size_t>(count, 1) * sizeof(T), 256);
+    MGP_REQUIRE(bytes <= left(), "fused matvec work buffers exceed the fixed scratch arena");
+    T* p = reinterpret_cast<T*>(ws.arena + off);
+    off += bytes;
+    return p;
+  }
+};
+
+size_t rhs_pack_bytes(int64_t col_tiles, int ncg) {
+  if (ncg == 0) return (size_t)round_up(col_tiles * 16 * 4, 256);
+  return (size_t)round_up((int64_t)ncg * (col_tiles / 2) * 64 * 32, 256);
+}
+
+}  // namespace
+
+size_t fused_matvec_min_arena(const PackedPoints& cols, int ncols) {
+  const int nc = std::min(ncols, 64);
+  const int ncg = nc == 1 ? 0 : (nc <= 16 ? 1 : (nc <= 32 ? 2 : 4));
+  size_t b = rhs_pack_bytes(cols.ntiles, ncg);
+  if (ncg > 0) b += 256 + (size_t)round_up(64 * 64 * 4, 256);
+  return b;
+}
+
 void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,
                   MatvecWorkspace& ws, hipStream_t st, int force_splits) {
@@ -817,23 +853,24 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
 
     // Pack right-hand sides.
     const int64_t col_pairs = col_tiles / 2;
+    ChunkBuffers buf(ws);
     float* vp;
     uint32_t* colmax = nullptr;
     if (ncg == 0) {
       const int64_t npad = col_tiles * 16;
-      vp = ws.vpack.ensure((size_t)npad);
+      vp = buf.take(ws.vpack, (size_t)npad);
       hipLaunchKernelGGL(k_pad_vec, dim3((unsigned)ceil_div(npad, 256)), dim3(256),
                          0, st, Vc, a.n, npad, vp);
     } else {
-      colmax = ws.colmax.ensure(64);
+      colmax = buf.take(ws.colmax, 64);
       const int chunks = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(a.n, 1), 4096), 64);
-      uint32_t* cpart = ws.colmax_part.ensure((size_t)64 * chunks);
+      uint32_t* cpart = buf.take(ws.colmax_part, (size_t)64 * chunks);
       hipLaunchKernelGGL(k_col_absmax_part, dim3((unsigned)chunks, (unsigned)nc), dim3(256), 0,
                          st, Vc, a.n, cpart);
       hipLaunchKernelGGL(k_col_absmax_final, dim3(1), dim3(64), 0, st, cpart, chunks, nc,
                          colmax);
       const int64_t total = (int64_t)ncg * col_pairs * 64;  // 8-half vectors per part
-      vp = ws.vpack.ensure((size_t)total * 2 * 4);
+      vp = buf.take(ws.vpack, (size_t)total * 2 * 4);
       hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256),
                          0, st, Vc, a.n, nc, ncg, col_pairs, colmax,
                          reinterpret_cast<h8*>(vp));
@@ -852,12 +889,18 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
              splits < 64)
         splits *= 2;
     }
+    if (ws.arena != nullptr && splits > 1) {
+      // Fixed arena: as many splits as the remaining bytes hold partials for.
+      const size_t per_split = (size_t)round_up((int64_t)cpad * mpad * 4, 256);
+      const int64_t fit = (int64_t)(buf.left() / per_split);
+      while (splits > 1 && splits > fit) splits /= 2;
+    }
     const int64_t pairs_per_split = ceil_div(col_pairs, splits);
     splits = ceil_div(col_pairs, pairs_per_split);
 
     float* partial = nullptr;
     if (splits > 1 || mixing)
-      partial = ws.partial.ensure((size_t)splits * cpad * mpad);
+      partial = buf.take(ws.partial, (size_t)splits * cpad * mpad);
 
     MGP_REQUIRE(a.kind != KIND_MATERN12, "Matern-1/2 has no Gram-form tile path");
     TileFn fn = a.kind == KIND_RBF        ? pick_tile<KIND_RBF>(kb, ncg)

@@ -46,6 +46,7 @@ struct Provider {
   DevBuf<float> tree_ws;  // column-split partial products of the tree matvec
 
   hipStream_t st = nullptr;
+  int device = 0;              // HIP device current when the provider was created
   DevBuf<float> X;             // raw training inputs [n][d]
   Coords co;
   PackedPoints train;
@@ -99,8 +100,11 @@ struct Provider {
 
   // (K + noise I) V (or (K + diag(noise_vec)) V) for device arrays V, out
   // ([ncols][n] column-major).
-  void forward(const float* V, int ncols, float* out);
-  void forward_scalar(const float* V, int ncols, float* out);  // without the noise vector
+  // wsp: work buffers of the fused tile route (default: the provider's own,
+  // grown on demand; a fixed-arena workspace keeps the call allocation-free).
+  void forward(const float* V, int ncols, float* out, MatvecWorkspace* wsp = nullptr);
+  void forward_scalar(const float* V, int ncols, float* out,  // without the noise vector
+                      MatvecWorkspace* wsp = nullptr);
   // True when forward() runs the fused tile kernel (not materialized, Gram form
   // accurate for the packed training set).
   bool fused_route() const;

@@ -165,8 +165,8 @@ void Provider::pack(const float* X_dev, int64_t m, PackedPoints& pp) {
   pack_points(X_dev, m, co, pp, st);
 }
 
-void Provider::forward(const float* V, int ncols, float* out) {
-  forward_scalar(V, ncols, out);
+void Provider::forward(const float* V, int ncols, float* out, MatvecWorkspace* wsp) {
+  forward_scalar(V, ncols, out, wsp);
   if (has_noise_vec) {
     const int64_t total = n * (int64_t)ncols;
     hipLaunchKernelGGL(k_add_diag_vec, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
@@ -175,7 +175,7 @@ void Provider::forward(const float* V, int ncols, float* out) {
   }
 }
 
-void Provider::forward_scalar(const float* V, int ncols, float* out) {
+void Provider::forward_scalar(const float* V, int ncols, float* out, MatvecWorkspace* wsp) {
   const float noise = scalar_noise();
   MatvecArgs a;
   a.kind = kind;
@@ -208,7 +208,7 @@ void Provider::forward_scalar(const float* V, int ncols, float* out) {
     direct_matvec(a, train, train, d, V, out, st);
     return;
   }
-  fused_matvec(a, train, train, V, out, ws, st);
+  fused_matvec(a, train, train, V, out, wsp ? *wsp : ws, st);
 }
 
 bool Provider::fused_route() const {
