@@ -1013,6 +1013,7 @@ class SingleOutputGP:
             "prediction_love_root_time_s": float(res.get("love_root_time_s", 0.0)),
             "alpha_cache_used": bool(res.get("alpha_cache_used", False)),
             "love_root_cache_used": bool(res.get("love_root_cache_used", False)),
+            "alpha_cg_iterations": int(res.get("alpha_cg_iterations", 0)),
         }
         self._backend_predict_info.update(
             {k: v for k, v in res.items() if k.startswith("exact_")})
