@@ -13,24 +13,27 @@ struct Coords {
   DevBuf<float> coef;  // [2*d]: center[d] then scale[d]
 };
 
-// Points laid out as v_mfma_f32_16x16x32_bf16 operands.
+// Points laid out as v_mfma_f32_16x16x32_f16 operands.
 //   A-side (columns j): aug = [z_0..z_{d-1}, |z|^2, 1]
 //   B-side (rows i):    aug = [-2 z_0..-2 z_{d-1}, 1, |z|^2]
-// Every fp32 aug value is split exactly into three bf16 parts
-// (x = hi + mid + lo, 8 significant bits each).  The dot product of the two
-// augmented vectors is then the sum of six part-products per dimension,
-//   hi.hi + hi.mid + mid.hi + hi.lo + lo.hi + mid.mid
-// (the dropped mid.lo, lo.mid, lo.lo terms are below 2^-23 relative), which
-// yields |z_i - z_j|^2 at fp32 accuracy on the bf16 matrix cores.
+// Every fp32 aug value x is split into two fp16 parts, hi = RNE16(x) and
+// lo = RNE16(x - hi) (x - hi is exact in fp32).  The dot product of the two
+// augmented vectors is then the sum of three part-products per dimension,
+//   hi.hi + hi.lo + lo.hi,
+// with the dropped lo.lo term and the rounding of lo below 3 * 2^-24 |a b| per
+// slot (subnormal lo parts of values under 2^-3 add at most 2^-25 absolute),
+// which yields |z_i - z_j|^2 at fp32 accuracy on the fp16 matrix cores.  The
+// aug values stay inside fp16's range wherever the Gram form is used (|z|^2 up
+// to the norm bounds below, all under 65504).
 // Slot k (0 <= k < 32*kb) of a point holds product p = k / D, dimension
-// t = k % D (D = d + 2), zero for k >= 6 D; lane (li + 16 g) of MFMA m carries
+// t = k % D (D = d + 2), zero for k >= 3 D; lane (li + 16 g) of MFMA m carries
 // slots 32 m + 8 g + e, e = 0..7:
-//   pack[tile][m][lane][e] (bf16), lane = point%16 + 16 g
+//   pack[tile][m][lane][e] (fp16), lane = point%16 + 16 g
 struct PackedPoints {
   int64_t n = 0;       // real points
   int64_t ntiles = 0;  // 16-point tiles (zero padded)
-  int kb = 0;          // K=32 bf16 MFMAs per 16x16 distance tile
-  DevBuf<uint32_t> A, B;  // two bf16 per dword
+  int kb = 0;          // K=32 fp16 MFMAs per 16x16 distance tile
+  DevBuf<uint32_t> A, B;  // two fp16 per dword
   DevBuf<float> z;     // scaled coordinates, row-major [n][d] (direct path)
   float max_norm = 0.f;      // max_i |z_i|^2 (Gram-form error scale)
   DevBuf<uint32_t> max_norm_dev;
@@ -58,8 +61,8 @@ inline bool gram_form_ok(int kind, const PackedPoints& rows, const PackedPoints&
   return rows.kb > 0 && rows.max_norm + cols.max_norm <= bound;
 }
 
-// Number of K=32 MFMAs for input dimension d: ceil(6 (d + 2) / 32).
-inline int split_mfma_count(int d) { return (6 * (d + 2) + 31) / 32; }
+// Number of K=32 MFMAs for input dimension d: ceil(3 (d + 2) / 32).
+inline int split_mfma_count(int d) { return (3 * (d + 2) + 31) / 32; }
 
 // Multiplier applied to (x - center)/lengthscale so that the squared distance
 // of the scaled points feeds exp2 directly:
@@ -147,7 +150,7 @@ void gradient_matvec(int kind, bool ard, const PackedPoints& pts, int d, float o
                      const float* pscale_dev, const float* V_dev, int ncols, float* out_dev,
                      hipStream_t st);
 
-// Maximum input dimension served by the MFMA tile path (six K=32 MFMAs).
+// Maximum input dimension served by the MFMA tile path (three K=32 MFMAs).
 constexpr int kMaxMfmaDim = 30;
 
 }  // namespace mgp

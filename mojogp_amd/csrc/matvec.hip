@@ -8,11 +8,10 @@
 //
 // Design (not a translation): the product out = K V is evaluated like an
 // attention block.  Per 16x16 tile of (row i, column j) pairs:
-//   1. S^T = A_j . B_i   (v_mfma_f32_16x16x32_bf16 over the three-way bf16
+//   1. S^T = A_j . B_i   (v_mfma_f32_16x16x32_f16 over the two-term fp16
 //      split of the augmented coordinates, see PackedPoints) yields the scaled
 //      squared distance |z_i - z_j|^2 at fp32 accuracy (Gram form, norms in two
-//      extra dimensions); 4 MFMAs at d = 16 instead of 5 fp32 K=4 MFMAs of
-//      twice the cycle count each;
+//      extra dimensions); 2 MFMAs at d = 16;
 //   2. the kernel value is formed in registers (RBF: med3 + exp2;
 //      Matern-5/2: sqrt, min, exp2, two FMAs, one multiply);
 //   3. O^T += V^T . P^T  (four more 16x16x4 MFMAs per 16 right-hand sides).
@@ -27,13 +26,15 @@
 namespace mgp {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void g_void;
 
 namespace {
 
 constexpr int kWaves = 4;           // waves per workgroup
+constexpr int kStageSteps = 2;      // column-tile pairs per LDS stage of the tile kernel
 constexpr int kFlushTiles = 16;     // j tiles between fp64 flushes
 constexpr float kM52A = 0.69314718055994530942f;                     // ln 2
 constexpr float kM52B = 0.69314718055994530942f * 0.69314718055994530942f / 3.0f;
@@ -85,24 +86,20 @@ __global__ void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
   if (i < n) p[i] = v;
 }
 
-// Exact three-way bf16 split of an fp32 value by truncation: x = hi + mid + lo
-// with each remainder exact in fp32.  Returns the requested part's bits.
-__device__ __forceinline__ uint16_t bf16_part(float x, int part) {
-  const uint32_t b0 = __float_as_uint(x) & 0xFFFF0000u;
-  if (part == 0) return (uint16_t)(b0 >> 16);
-  const float r1 = x - __uint_as_float(b0);
-  const uint32_t b1 = __float_as_uint(r1) & 0xFFFF0000u;
-  if (part == 1) return (uint16_t)(b1 >> 16);
-  const float r2 = r1 - __uint_as_float(b1);
-  return (uint16_t)(__float_as_uint(r2) >> 16);
+// Two-term fp16 split of an fp32 value: hi = RNE16(x), lo = RNE16(x - hi).
+// Returns the requested part's bits.
+__device__ __forceinline__ uint16_t f16_part(float x, int part) {
+  const _Float16 hi = (_Float16)x;
+  const _Float16 v = part == 0 ? hi : (_Float16)(x - (float)hi);
+  return __builtin_bit_cast(uint16_t, v);
 }
 
 // Part-product table: slot product p multiplies A part kPartA[p] with B part
-// kPartB[p] (hi=0, mid=1, lo=2).
-__constant__ int kPartA[6] = {0, 0, 1, 0, 2, 1};
-__constant__ int kPartB[6] = {0, 1, 0, 2, 0, 1};
+// kPartB[p] (hi = 0, lo = 1).
+__constant__ int kPartA[3] = {0, 0, 1};
+__constant__ int kPartB[3] = {0, 1, 0};
 
-// One thread per (padded) point: scaled coordinates, norm, and the 32*kb bf16
+// One thread per (padded) point: scaled coordinates, norm, and the 32*kb fp16
 // slots of both operand sides.
 __global__ void k_pack_points(const float* __restrict__ X, int64_t n, int d,
                               const float* __restrict__ coef, int kb,
@@ -132,7 +129,7 @@ __global__ void k_pack_points(const float* __restrict__ X, int64_t n, int d,
   const int D = d + 2;
   for (int k = 0; k < 32 * kb; ++k) {
     uint16_t a = 0, b = 0;
-    if (k < 6 * D) {
+    if (k < 3 * D) {
       const int p = k / D, t = k - p * D;
       float av, bv;
       if (t < d) {
@@ -146,8 +143,8 @@ __global__ void k_pack_points(const float* __restrict__ X, int64_t n, int d,
         av = 1.0f;
         bv = nrm;
       }
-      a = bf16_part(av, kPartA[p]);
-      b = bf16_part(bv, kPartB[p]);
+      a = f16_part(av, kPartA[p]);
+      b = f16_part(bv, kPartB[p]);
     }
     const int m = k >> 5, g = (k >> 3) & 3, e = k & 7;
     const int64_t off = ((tile * kb + m) * 64 + li + 16 * g) * 8 + e;
@@ -298,20 +295,29 @@ __device__ __forceinline__ void split_pair(float f0, float g0, float f1, float g
 // ---------------------------------------------------------------------------
 template <int KIND, int KB, int NCG, int R>
 __global__ __launch_bounds__(256) void k_fused_tile(
-    const bf8* __restrict__ Bi, int64_t row_tiles, const bf8* __restrict__ Aj,
+    const h8* __restrict__ Bi, int64_t row_tiles, const h8* __restrict__ Aj,
     const void* __restrict__ Vp, int64_t col_pairs, int64_t pairs_per_split,
     int64_t diag_shift, int64_t m, int ncols, float os, float noise,
     const uint32_t* __restrict__ colmax, const float* __restrict__ Vin,
     float* __restrict__ out, float* __restrict__ partial, int64_t mpad, int cpad) {
   static_assert(R % 2 == 0, "row tiles per wave must be even (pair alignment)");
   static_assert(KIND != KIND_MATERN12, "Matern-1/2 is evaluated from coordinate differences");
+  // LDS stages: kStageSteps column-tile pairs each, as 1-KB blocks (64 lanes x
+  // 16 B, the MFMA operand layout): per step 2 KB blocks of A (tiles 2u, 2u+1),
+  // then per right-hand-side group 2 blocks of V (hi, lo) after all A blocks.
+  constexpr int kA = 2 * KB;
+  constexpr int kV = NCG > 0 ? 2 * NCG : 0;
+  constexpr int kBlocks = kStageSteps * (kA + kV);
+  __shared__ h8 lds[2][kBlocks][64];
+
   const int lane = threadIdx.x & 63;
-  // Wave index made wave-uniform (SGPR) so the j-loop bounds stay scalar.
+  // Wave index made wave-uniform (SGPR) so loop bounds and LDS bases stay scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t tile0 = ((int64_t)blockIdx.x * kWaves + wave) * R;
-  if (tile0 >= row_tiles) return;  // whole wave idle (no barriers used)
+  // Waves without rows still fill LDS stages and meet every barrier.
+  const bool active = tile0 < row_tiles;
 
-  bf8 bi[R][KB];
+  h8 bi[R][KB];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t it = tile0 + r;
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(256) void k_fused_tile(
         bi[r][kb] = Bi[(it * KB + kb) * 64 + lane];
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) bi[r][kb][e] = (__bf16)0.0f;
+        for (int e = 0; e < 8; ++e) bi[r][kb][e] = (_Float16)0.0f;
       }
     }
   }
@@ -351,37 +357,82 @@ __global__ __launch_bounds__(256) void k_fused_tile(
   const h8* V16 = reinterpret_cast<const h8*>(Vp);
   const float* V32 = reinterpret_cast<const float*>(Vp);
 
-  // One pair of j tiles against the wave's R row tiles.  MASK restores the
-  // exact zero self-distance on diagonal tiles (Gram-form cancellation guard).
-  auto step = [&](int64_t u, auto mask_tag) __attribute__((always_inline)) {
+  // Stage fill: steps [u0, u0 + ns) of A and V into lds[st] by LDS DMA, the
+  // blocks dealt round-robin to the four waves.  Both ranges are contiguous in
+  // global memory (A blocks 2 u0 KB .., V blocks (g col_pairs + u0) 2 ..).
+  auto fill = [&](int st, int64_t u0, int ns) __attribute__((always_inline)) {
+    const int na = ns * kA;
+    for (int b = wave; b < na; b += kWaves)
+      __builtin_amdgcn_global_load_lds(
+          (const g_void*)(Aj + (2 * u0 * KB + b) * 64 + lane), (lds_void*)&lds[st][b][0], 16, 0,
+          0);
+    if constexpr (NCG > 0) {
+      const int nv = 2 * ns;
+      for (int b = wave; b < NCG * nv; b += kWaves) {
+        const int g = b / nv, k = b - g * nv;
+        __builtin_amdgcn_global_load_lds(
+            (const g_void*)(V16 + (((int64_t)g * col_pairs + u0) * 2 + k) * 64 + lane),
+            (lds_void*)&lds[st][kStageSteps * kA + g * 2 * kStageSteps + k][0], 16, 0, 0);
+      }
+    }
+  };
+
+  // One pair of j tiles (step k of stage st) against the wave's R row tiles.
+  // MASK restores the exact zero self-distance on diagonal tiles (Gram-form
+  // cancellation guard).
+  auto step = [&](int st, int k, int64_t u, auto mask_tag) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int64_t jt0 = 2 * u;
-    bf8 a0[KB], a1[KB];
+    h8 a0[KB], a1[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      a0[kb] = Aj[(jt0 * KB + kb) * 64 + lane];
-      a1[kb] = Aj[((jt0 + 1) * KB + kb) * 64 + lane];
+      a0[kb] = lds[st][k * kA + kb][lane];
+      a1[kb] = lds[st][k * kA + KB + kb][lane];
     }
     h8 vh[G], vl[G];
     f4 v0, v1;
     if constexpr (NCG > 0) {
 #pragma unroll
       for (int g = 0; g < NCG; ++g) {
-        const int64_t base = ((int64_t)g * col_pairs + u) * 2;
-        vh[g] = V16[base * 64 + lane];
-        vl[g] = V16[(base + 1) * 64 + lane];
+        vh[g] = lds[st][kStageSteps * kA + g * 2 * kStageSteps + 2 * k][lane];
+        vl[g] = lds[st][kStageSteps * kA + g * 2 * kStageSteps + 2 * k + 1][lane];
       }
     } else {
       v0 = *reinterpret_cast<const f4*>(V32 + 16 * jt0 + lj);
       v1 = *reinterpret_cast<const f4*>(V32 + 16 * jt0 + 16 + lj);
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    // Software pipeline over the wave's row tiles: stage r issues the
+    // distance MFMAs of row r + 1 and the product MFMAs of row r - 1 while
+    // the VALU forms row r's kernel values, so the matrix cores and the VALU
+    // work side by side within the wave.
+    auto dist = [&](int r, f4& s0, f4& s1) __attribute__((always_inline)) {
+      s0 = f4{0.f, 0.f, 0.f, 0.f};
+      s1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[kb], bi[r][kb], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[kb], bi[r][kb], s1, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[kb], bi[r][kb], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[kb], bi[r][kb], s1, 0, 0, 0);
+      }
+    };
+    auto product = [&](int r, const h8& ph, const h8& pl) __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) {
+        f4 a = acc[r][g];
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[g], ph, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl[g], ph, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[g], pl, a, 0, 0, 0);
+        acc[r][g] = a;
+      }
+    };
+    f4 S0[2], S1[2];
+    h8 PH[2], PL[2];
+    dist(0, S0[0], S1[0]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      f4 s0 = S0[r & 1], s1 = S1[r & 1];
+      if (r + 1 < R) dist(r + 1, S0[(r + 1) & 1], S1[(r + 1) & 1]);
+      if constexpr (NCG > 0) {
+        if (r > 0) product(r - 1, PH[(r - 1) & 1], PL[(r - 1) & 1]);
       }
       if constexpr (MASK) {
         const int64_t dt = tile0 + r + diag_shift;
@@ -404,16 +455,8 @@ __global__ __launch_bounds__(256) void k_fused_tile(
         split_pair<KIND != KIND_MATERN52 && KIND != KIND_MATERN32>(f0[2], g0[2], f0[3], g0[3], hB, lB);
         split_pair<KIND != KIND_MATERN52 && KIND != KIND_MATERN32>(f1[0], g1[0], f1[1], g1[1], hC, lC);
         split_pair<KIND != KIND_MATERN52 && KIND != KIND_MATERN32>(f1[2], g1[2], f1[3], g1[3], hD, lD);
-        const h8 ph = {hA[0], hA[1], hB[0], hB[1], hC[0], hC[1], hD[0], hD[1]};
-        const h8 pl = {lA[0], lA[1], lB[0], lB[1], lC[0], lC[1], lD[0], lD[1]};
-#pragma unroll
-        for (int g = 0; g < NCG; ++g) {
-          f4 a = acc[r][g];
-          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[g], ph, a, 0, 0, 0);
-          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl[g], ph, a, 0, 0, 0);
-          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[g], pl, a, 0, 0, 0);
-          acc[r][g] = a;
-        }
+        PH[r & 1] = h8{hA[0], hA[1], hB[0], hB[1], hC[0], hC[1], hD[0], hD[1]};
+        PL[r & 1] = h8{lA[0], lA[1], lB[0], lB[1], lC[0], lC[1], lD[0], lD[1]};
       } else {
         float a = acc1[r];
 #pragma unroll
@@ -424,6 +467,15 @@ __global__ __launch_bounds__(256) void k_fused_tile(
         acc1[r] = a;
       }
     }
+    if constexpr (NCG > 0) product(R - 1, PH[(R - 1) & 1], PL[(R - 1) & 1]);
+#ifdef MGP_TILE_SCHED
+    // Interleave: one MFMA, then VALU, through the step.
+#pragma unroll
+    for (int i = 0; i < R * (2 * KB + 3 * NCG); ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, MGP_TILE_SCHED, 0);
+    }
+#endif
   };
   auto flush = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -441,23 +493,42 @@ __global__ __launch_bounds__(256) void k_fused_tile(
       }
     }
   };
-  // Plain pairs in chunks of kFlushTiles tiles (no branch in the hot loop),
-  // then the diagonal pairs with the mask.
-  constexpr int kFlushPairs = kFlushTiles / 2;
-  auto run = [&](int64_t a, int64_t b) __attribute__((always_inline)) {
-    for (int64_t c0 = a; c0 < b; c0 += kFlushPairs) {
-      const int64_t e = min(b, c0 + kFlushPairs);
-      for (int64_t u = c0; u < e; ++u) step(u, std::false_type{});
-      flush();
-    }
-  };
 
+  // Walk the split's pairs stage by stage: while stage c is consumed, stage
+  // c + 1 streams into the other buffer.  The barrier at the top of each
+  // stage makes stage c visible to all waves and frees the buffer of c - 1.
   const int64_t u_begin = (int64_t)blockIdx.y * pairs_per_split;
   const int64_t u_end = min(col_pairs, u_begin + pairs_per_split);
   const int64_t dlo = (tile0 + diag_shift) / 2, dhi = dlo + R / 2;
-  run(u_begin, min(u_end, dlo));
-  run(max(u_begin, dhi), u_end);
-  for (int64_t u = max(u_begin, dlo); u < min(u_end, dhi); ++u) step(u, std::true_type{});
+  const int64_t nstages = (u_end - u_begin + kStageSteps - 1) / kStageSteps;
+  fill(0, u_begin, (int)min((int64_t)kStageSteps, u_end - u_begin));
+  int since_flush = 0;
+  for (int64_t c = 0; c < nstages; ++c) {
+    const int st = (int)(c & 1);
+    const int64_t u0 = u_begin + c * kStageSteps;
+    const int ns = (int)min((int64_t)kStageSteps, u_end - u0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (c + 1 < nstages) {
+      const int64_t u1 = u0 + kStageSteps;
+      fill(st ^ 1, u1, (int)min((int64_t)kStageSteps, u_end - u1));
+    }
+    if (active) {
+      for (int k = 0; k < ns; ++k) {
+        const int64_t u = u0 + k;
+        if (u >= dlo && u < dhi)
+          step(st, k, u, std::true_type{});
+        else
+          step(st, k, u, std::false_type{});
+      }
+      since_flush += ns;
+      if (since_flush >= kFlushTiles / 2) {
+        flush();
+        since_flush = 0;
+      }
+    }
+  }
+  if (!active) return;
   flush();
 
   // Epilogue: undo the fp16 scaling exactly (powers of two).
@@ -728,13 +799,13 @@ __global__ __launch_bounds__(256) void k_grad_matvec(
 // ---------------------------------------------------------------------------
 // Dispatch tables
 // ---------------------------------------------------------------------------
-using TileFn = void (*)(const bf8*, int64_t, const bf8*, const void*, int64_t,
+using TileFn = void (*)(const h8*, int64_t, const h8*, const void*, int64_t,
                         int64_t, int64_t, int64_t, int, float, float,
                         const uint32_t*, const float*, float*, float*, int64_t, int);
 
 // Row tiles per wave: 4, or 2 where the register budget needs it (more than 16
-// right-hand sides, or more than four distance MFMAs per tile).
-constexpr int rows_per_wave_tiles(int kb, int ncg) { return (ncg >= 2 || kb > 4) ? 2 : 4; }
+// right-hand sides).
+constexpr int rows_per_wave_tiles(int, int ncg) { return ncg >= 2 ? 2 : 4; }
 
 template <int KIND, int NCG>
 TileFn pick_kb(int kb) {
@@ -742,9 +813,6 @@ TileFn pick_kb(int kb) {
     case 1: return k_fused_tile<KIND, 1, NCG, rows_per_wave_tiles(1, NCG)>;
     case 2: return k_fused_tile<KIND, 2, NCG, rows_per_wave_tiles(2, NCG)>;
     case 3: return k_fused_tile<KIND, 3, NCG, rows_per_wave_tiles(3, NCG)>;
-    case 4: return k_fused_tile<KIND, 4, NCG, rows_per_wave_tiles(4, NCG)>;
-    case 5: return k_fused_tile<KIND, 5, NCG, rows_per_wave_tiles(5, NCG)>;
-    case 6: return k_fused_tile<KIND, 6, NCG, rows_per_wave_tiles(6, NCG)>;
   }
   return nullptr;
 }
@@ -829,7 +897,7 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,
                   MatvecWorkspace& ws, hipStream_t st, int force_splits) {
   MGP_REQUIRE(a.ncols >= 1, "ncols must be >= 1");
-  MGP_REQUIRE(rows.kb == cols.kb && rows.kb >= 1 && rows.kb <= 6,
+  MGP_REQUIRE(rows.kb == cols.kb && rows.kb >= 1 && rows.kb <= 3,
               "MFMA tile path supports input dimension <= 30");
   const int kb = rows.kb;
   const int64_t row_tiles = rows.ntiles, col_tiles = cols.ntiles;
@@ -910,8 +978,8 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
     const int64_t diag_shift = a.square ? 0 : (int64_t)1 << 40;
     if (ws.time_tile) MGP_HIP_CHECK(hipEventRecord(ws.ev0, st));
     hipLaunchKernelGGL(fn, dim3((unsigned)row_blocks, (unsigned)splits), dim3(256), 0,
-                       st, reinterpret_cast<const bf8*>(rows.B.ptr), row_tiles,
-                       reinterpret_cast<const bf8*>(cols.A.ptr), (const void*)vp, col_pairs,
+                       st, reinterpret_cast<const h8*>(rows.B.ptr), row_tiles,
+                       reinterpret_cast<const h8*>(cols.A.ptr), (const void*)vp, col_pairs,
                        pairs_per_split, diag_shift, a.m, nc, a.outputscale, a.noise,
                        colmax, Vin, outc, partial, mpad, cpad);
     MGP_HIP_CHECK(hipGetLastError());

