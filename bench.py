@@ -9,9 +9,13 @@ Work model (per (row, column) pair): F = 2d + 2t + c_k flops (c_k = 9 for
 Matern-5/2, 5 for RBF) plus n_tr transcendentals (2 for Matern-5/2).
 value = N^2 F / (host wall time per step); roofline.achieved uses the HIP-event
 duration of the fused tile kernel measured on the provider's stream.  The
-arithmetic is fp32-accurate (distances from an exact three-way bf16 split, the
-K.V product from a two-term fp16 split), so the roofline peak is MI355X's fp32
-dense matrix peak.
+arithmetic is fp32-accurate (distances from an exact two-term fp16 split on
+the fp16 matrix cores, the K.V product from a two-term fp16 split), so the
+kernel is bound by the mix of VALU (two transcendentals and 5.5 other
+instructions per pair value) and 16-bit MFMA issue, not by any single
+published peak: roofline.peak is the pipe model, the cycles per 16x16 tile
+that the per-instruction costs measured live by mgp_pipe_probe give for the
+kernel's instruction mix, expressed in the same algorithmic TFLOP/s.
 
 The cpu_baseline leg times the C restatement of the reference matvec
 (oracle/cpu_ref, OpenMP) on a bounded sample of rows of the same workload.
@@ -31,26 +35,45 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-PEAK_FP32_TFLOPS = 157.3       # MI355X dense fp32 (MFMA / packed VALU)
-PEAK_TRANS_PER_S = 9.83e12     # assumed quarter-rate transcendentals (256 CU x 2.4 GHz x 16)
+PEAK_FP16_MFMA_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak (published)
 
 N, D, T = 250_000, 16, 16
 C_K = 9                        # Matern-5/2 epilogue flops per pair
 N_TR = 2                       # sqrt + exp per pair
 FLOPS_PER_PAIR = 2 * D + 2 * T + C_K
-# HBM bytes per launch of the tile kernel at this workload: FETCH_SIZE x 2.000 +
-# WRITE_SIZE x 1.000 (copy-kernel calibration), profiles/fused_tile_c3_matvec.md.
-TILE_TRAFFIC_BYTES = 3.610e9
+# HBM bytes per launch of the tile kernel at this workload (rocprofv3 FETCH_SIZE
+# x 2.000 + WRITE_SIZE x 1.000, copy-kernel calibration; profiles/
+# fused_tile_c3_matvec.md).
+TILE_TRAFFIC_BYTES = 1.995e9
 
-# Instruction-cost model of the tile kernel, cycles per 16x16 tile of pairs on
-# one SIMD at 2.4 GHz, with per-instruction costs measured on MI355X (16-bit
-# K=32 MFMA 16 cycles, VALU 4, transcendental 8) and MFMA / VALU issue taken as
-# serialized (co-execution covers ~30% of MFMA time in the profile):
-#   MFMA: kb distance MFMAs + 1.5 fp16 product MFMAs (t = 16), kb = ceil(6(d+2)/32)
-#   VALU: 4 pairs per lane x (2 transcendentals x 8 + 5.5 other ops x 4)
-KB = -(-6 * (D + 2) // 32)
-MODEL_CYCLES_PER_TILE = (KB + 1.5) * 16 + 4 * (2 * 8 + 5.5 * 4)
-SIMDS, CLOCK_HZ = 1024, 2.4e9
+# Instruction mix of the tile kernel k_fused_tile<Matern52, KB, NCG=1, R=4> per
+# 16x16 tile (gfx950 ISA of this build): 4 pair values per lane, each with 2
+# transcendentals (v_sqrt, v_exp) and 5.5 other VALU instructions (v_min, two
+# FMAs, the product f*g, half a v_cvt_pk_f16_f32, one v_fma_mix); KB distance
+# MFMAs plus 1.5 product MFMAs (v_mfma_f32_16x16x32_f16).
+KB = -(-3 * (D + 2) // 32)
+MFMA_PER_TILE = KB + 1.5
+VALUES_PER_LANE = 4
+TRANS_PER_VALUE, VALU_PER_VALUE = 2, 5.5
+ROW_TILES, COL_TILES = -(-N // 16), 2 * -(-N // 32)
+
+
+def _pipe_model(probe):
+    """Cycles per 16x16 tile and the kernel time they imply: VALU cycles plus
+    the MFMA's measured cost inside a VALU stream (the two pipes overlap only
+    partly on gfx950: out[4] of mgp_pipe_probe)."""
+    ghz, c_tr, c_valu, c_mfma, c_mfma_mixed = probe[:5]
+    cycles = (VALUES_PER_LANE * (TRANS_PER_VALUE * c_tr + VALU_PER_VALUE * c_valu)
+              + MFMA_PER_TILE * c_mfma_mixed)
+    return cycles, ghz
+
+
+def _probe():
+    import ctypes
+    from mojogp_amd import _lib
+    out = (ctypes.c_double * 6)()
+    _lib.call("mgp_pipe_probe", out, 6)
+    return [float(v) for v in out]
 
 
 def _make_inputs():
@@ -83,6 +106,32 @@ def _mbcg_iteration_ms(X, params, noise, iterations: int = 20):
     finally:
         prov.close()
     return loop_ms.value / max(ci.value, 1), time.perf_counter() - t0
+
+
+def _c3_fit_predict_seconds():
+    """Config 3 end to end: Matern-5/2 ARD, N=250k, d=16, 50 Adam steps, 15
+    probes, rank-200 preconditioner (matrix-free), then mean + LOVE std at
+    10 000 test points (the generator of tests/test_gpu_configs_at_size.py)."""
+    from mojogp_amd import Matern52, SingleOutputGP
+    rng = np.random.default_rng(0)
+    X = rng.normal(size=(N, D)).astype(np.float32)
+    W = rng.normal(size=(1024, D)) / 2.0
+    b = rng.uniform(0, 2 * np.pi, size=1024)
+    w = rng.normal(size=1024)
+    y = (np.sqrt(2.0 / 1024) * np.cos(X @ W.T + b) @ w
+         + 0.05 * rng.normal(size=N)).astype(np.float32)
+    Xs = rng.normal(size=(10_000, D)).astype(np.float32)
+    gp = SingleOutputGP(Matern52(ard=True))
+    t0 = time.perf_counter()
+    tr = gp.fit(X, y, method="matrix_free", max_iterations=50, num_probes=15,
+                cg_tolerance=1e-2, preconditioner_rank=200)
+    fit_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    gp.predict(Xs, return_std=True, variance_method="love")
+    pred_s = time.perf_counter() - t0
+    info = gp.backend_train_info or {}
+    return fit_s, pred_s, {"final_nll": tr.nll,
+                           "cg_iterations_total": info.get("cg_iterations_total")}
 
 
 def _fit_c2_seconds():
@@ -287,8 +336,12 @@ def main(argv=None) -> int:
     ms_per_step = float(np.mean(times_ms))
     value = pairs * FLOPS_PER_PAIR / (ms_per_step * 1e-3) / 1e12
     achieved = pairs * FLOPS_PER_PAIR / (tile_ms * 1e-3) / 1e12
-    t_roof_ms = pairs * (FLOPS_PER_PAIR / (PEAK_FP32_TFLOPS * 1e12) + N_TR / PEAK_TRANS_PER_S) * 1e3
-    t_model_ms = (N / 16) ** 2 / SIMDS * MODEL_CYCLES_PER_TILE / CLOCK_HZ * 1e3
+    probe = _probe()
+    cycles, ghz = _pipe_model(probe)
+    simds = 4 * int(probe[5])
+    t_model_ms = ROW_TILES * COL_TILES / simds * cycles / (ghz * 1e9) * 1e3
+    peak = pairs * FLOPS_PER_PAIR / (t_model_ms * 1e-3) / 1e12
+    mfma_tflops = ROW_TILES * COL_TILES * MFMA_PER_TILE * 16384 / (tile_ms * 1e-3) / 1e12
 
     result = {
         "metric": "fused K.V matvec TFLOP/s (N=250k, d=16, t=16, Matern-5/2 ARD)",
@@ -309,20 +362,32 @@ def main(argv=None) -> int:
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 3),
-            "peak": PEAK_FP32_TFLOPS,
+            "peak": round(peak, 3),
             "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+            "frac": round(t_model_ms / tile_ms, 4),
             "traffic": TILE_TRAFFIC_BYTES,
+            "peak_kind": "pipe model: VALU + 16-bit MFMA cycles per 16x16 tile from "
+                         "per-instruction costs measured live (mgp_pipe_probe)",
+            "model_ms": round(t_model_ms, 3),
+            "cycles_per_tile": round(cycles, 2),
+            "instruction_cycles": {"clock_ghz": round(probe[0], 3),
+                                   "v_exp_f32": round(probe[1], 2),
+                                   "v_fma_f32": round(probe[2], 2),
+                                   "mfma_f16_k32": round(probe[3], 2),
+                                   "mfma_f16_k32_in_valu_stream": round(probe[4], 2)},
+            "fp16_mfma_tflops": round(mfma_tflops, 2),
+            "fp16_mfma_peak": PEAK_FP16_MFMA_TFLOPS,
         },
+        "fp32_equivalent_tflops": round(achieved, 3),
         "tile_kernel_ms": round(tile_ms, 4),
-        "issue_slot_roofline_ms": round(t_roof_ms, 3),
-        "issue_slot_roofline_frac": round(t_roof_ms / tile_ms, 4),
-        "issue_model_ms": round(t_model_ms, 3),
-        "issue_model_frac": round(t_model_ms / tile_ms, 4),
     }
     if not args.no_extras:
         it_ms, _ = _mbcg_iteration_ms(X, params, noise)
         result["mbcg_iter_ms"] = round(it_ms, 3)
+        c3_fit, c3_pred, c3_info = _c3_fit_predict_seconds()
+        result["fit_seconds_c3"] = round(c3_fit, 3)
+        result["predict_love_seconds_c3"] = round(c3_pred, 3)
+        result["fit_c3_info"] = c3_info
         fit_s, fit_info = _fit_c2_seconds()
         result["fit_seconds"] = round(fit_s, 3)
         result["fit_config"] = ("config 2: RBF-ARD N=50000 d=8, 30 Adam steps, 15 probes, "

@@ -633,6 +633,14 @@ MGP_API int mgp_rff_prior_values(const float* X, int64_t n, int d,
  * counterpart. */
 MGP_API int mgp_calibration_copy(int64_t bytes, int repeats, double* ms_avg);
 
+/* Pipe-throughput probe for the tile kernel's instruction-cost model: out[0]
+ * shader clock (GHz), then cycles per wave-instruction per SIMD of out[1]
+ * v_exp_f32, out[2] v_fma_f32, out[3] v_mfma_f32_16x16x32_f16, out[4] the same
+ * MFMA interleaved with VALU work of the same waves (4 MFMA + 16 FMA per
+ * iteration, FMA cycles subtracted), out[5] the compute-unit count.
+ * nout >= 6.  Measurement hook; no reference counterpart. */
+MGP_API int mgp_pipe_probe(double* out, int nout);
+
 #ifdef __cplusplus
 }
 #endif

@@ -187,6 +187,7 @@ _SIGNATURES = {
                                              C.c_int, C.c_int, c_double_p, c_double_p,
                                              c_float_p]),
     "mgp_calibration_copy": (C.c_int, [C.c_int64, C.c_int, c_double_p]),
+    "mgp_pipe_probe": (C.c_int, [c_double_p, C.c_int]),
     "mgp_train": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int, C.c_float,
                             C.POINTER(TrainOpts), PROGRESS_CB, C.c_void_p,
                             C.POINTER(TrainResult)]),
