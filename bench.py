@@ -85,27 +85,39 @@ def _make_inputs():
     return X, V, params, 0.1
 
 
-def _mbcg_iteration_ms(X, params, noise, iterations: int = 20):
-    """One mBCG iteration at config 3: (K + sigma^2 I) P over t=16 columns with a
-    rank-200 greedy pivoted-Cholesky preconditioner, Woodbury apply, fused
-    dots/updates.  Returns (ms per iteration, wall seconds of the eval)."""
+def _mbcg_iteration_ms(X, params, noise, iterations: int = 20, kind=None, ard=True, rank=200):
+    """One mBCG iteration over t=16 columns (y plus 15 probes) with a rank-`rank`
+    greedy pivoted-Cholesky preconditioner and its Woodbury apply (config 3 by
+    default: Matern-5/2 ARD, rank 200).  Returns (ms per iteration, wall
+    seconds of the eval)."""
     import ctypes
     from mojogp_amd import _lib
     from mojogp_amd._provider import NativeProvider, KIND_MATERN52
+    n = X.shape[0]
     rng = np.random.default_rng(1)
-    y = rng.normal(size=N).astype(np.float32)
-    prov = NativeProvider(KIND_MATERN52, True, X, params, noise)
+    y = rng.normal(size=n).astype(np.float32)
+    prov = NativeProvider(KIND_MATERN52 if kind is None else kind, ard, X, params, noise)
     g = np.zeros(params.size + 1, np.float32)
     nll, iq, ld, pl = (ctypes.c_float() for _ in range(4))
     ci, loop_ms = ctypes.c_int(), ctypes.c_double()
     t0 = time.perf_counter()
     try:
         _lib.call("mgp_bbmm_eval", prov.handle, _lib.fptr(y), 0.0, T - 1, iterations,
-                  iterations, 0.0, 0, 200, ctypes.byref(nll), ctypes.byref(iq), ctypes.byref(ld),
-                  _lib.fptr(g), ctypes.byref(ci), ctypes.byref(pl), ctypes.byref(loop_ms))
+                  iterations, 0.0, 0, rank, ctypes.byref(nll), ctypes.byref(iq),
+                  ctypes.byref(ld), _lib.fptr(g), ctypes.byref(ci), ctypes.byref(pl),
+                  ctypes.byref(loop_ms))
     finally:
         prov.close()
     return loop_ms.value / max(ci.value, 1), time.perf_counter() - t0
+
+
+def _mbcg_iteration_ms_c2(iterations: int = 20):
+    """One mBCG iteration at config 2: RBF ARD, N=50k, d=8, rank 100."""
+    from mojogp_amd._provider import KIND_RBF
+    rng = np.random.default_rng(0)
+    X = rng.uniform(size=(50_000, 8)).astype(np.float32)
+    params = np.concatenate([np.full(8, 0.5), [1.0]]).astype(np.float32)
+    return _mbcg_iteration_ms(X, params, 0.01, iterations, kind=KIND_RBF, rank=100)[0]
 
 
 def _c3_fit_predict_seconds():
@@ -300,6 +312,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the mBCG-iteration and fit() measurements")
+    ap.add_argument("--mbcg-only", action="store_true",
+                    help="only time one mBCG iteration at configs 3 and 2 (profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel of BYTES (HBM counter calibration)")
     args = ap.parse_args(argv)
@@ -312,6 +326,13 @@ def main(argv=None) -> int:
         gbs = 2 * args.calibrate_copy / (ms.value * 1e-3) / 1e9
         print(json.dumps({"calibration_copy_bytes": args.calibrate_copy,
                           "ms": ms.value, "GB/s": gbs}), flush=True)
+        return 0
+
+    if args.mbcg_only:
+        X, _, params, noise = _make_inputs()
+        c3, _ = _mbcg_iteration_ms(X, params, noise)
+        print(json.dumps({"mbcg_iter_ms_c3": round(c3, 4),
+                          "mbcg_iter_ms_c2": round(_mbcg_iteration_ms_c2(), 4)}), flush=True)
         return 0
 
     if args.gpus != 1:
@@ -384,6 +405,7 @@ def main(argv=None) -> int:
     if not args.no_extras:
         it_ms, _ = _mbcg_iteration_ms(X, params, noise)
         result["mbcg_iter_ms"] = round(it_ms, 3)
+        result["mbcg_iter_ms_c2"] = round(_mbcg_iteration_ms_c2(), 3)
         c3_fit, c3_pred, c3_info = _c3_fit_predict_seconds()
         result["fit_seconds_c3"] = round(c3_fit, 3)
         result["predict_love_seconds_c3"] = round(c3_pred, 3)

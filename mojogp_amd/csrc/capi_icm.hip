@@ -187,7 +187,7 @@ int mgp_kron_precond(void* provider, int T, float outputscale, const float* B,
       dr.ensure(N * C);
       dz.ensure(N * C);
       MGP_HIP_CHECK(hipMemcpyAsync(dr.ptr, rhs, N * C * sizeof(float), hipMemcpyHostToDevice, m.st));
-      Pk.apply(dr.ptr, C, dz.ptr, nullptr, m.st);
+      Pk.apply(dr.ptr, C, dz.ptr, nullptr, 0, m.st);
       MGP_HIP_CHECK(hipMemcpyAsync(solved, dz.ptr, N * C * sizeof(float), hipMemcpyDeviceToHost,
                                    m.st));
     }

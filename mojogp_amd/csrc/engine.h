@@ -43,7 +43,7 @@ struct CGWork {
   DevBuf<float> x, r, z, p, Ap;  // [C][n]
   DevBuf<float> scal;            // rz_old | alpha | beta   (3*C)
   DevBuf<float> hist_a, hist_b;  // [max_tridiag][C]
-  DevBuf<double> part_a, part_b; // [C][nb]
+  DevBuf<double> part_a, part_b, part_c;  // [C][nb]: pAp, r.z, r.r partials
   DevBuf<float> resn;            // [1]
   DevBuf<int> done;
   CGScalars scalars(int ncols);
@@ -60,12 +60,14 @@ struct CGResult {
 // A symmetric positive definite operator on device vectors of length n for
 // mBCG: matvec(V, C, out) = A V for C columns ([C][n]); precond (optional)
 // writes z = P^{-1} r for C columns plus the fixed-chunk partials of the
-// column dots r.z into rz_part[C * reduction_chunks(n)].
+// column dots r.z over the nb chunks the CG passes (cg_chunks(n)).
 struct CGOperator {
   int64_t n = 0;
   hipStream_t st = nullptr;
   std::function<void(const float*, int, float*)> matvec;
-  std::function<void(const float*, int, float*, double*)> precond;
+  // precond(r, ncols, z, rz_part, nb): z = P^-1 r and, when rz_part is set,
+  // the partials rz_part[c*nb + b] of r . z over nb row chunks.
+  std::function<void(const float*, int, float*, double*, int)> precond;
 };
 
 // Solves A X = rhs for `ncols` columns (device rhs [C][n]) by the reference's

@@ -29,18 +29,20 @@ __global__ void k_recip_sqrt(const float* __restrict__ d, int64_t n, float* __re
   dsqrt[i] = sqrtf(d[i]);
 }
 
+// One wave per column (grid = ncols, 64 threads); fixed-order fp64 sum.
 __global__ void k_part_to_float(const double* __restrict__ part, int nb, int ncols,
                                 float* __restrict__ out) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= ncols) return;
+  const int c = blockIdx.x, lane = threadIdx.x;
   double s = 0.0;
-  for (int b = 0; b < nb; ++b) s += part[(int64_t)c * nb + b];
-  out[c] = (float)s;
+  for (int b = lane; b < nb; b += 64) s += part[(int64_t)c * nb + b];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) out[c] = (float)s;
 }
 
 void part_to_float(const double* part, int nb, int ncols, float* out, hipStream_t st) {
-  hipLaunchKernelGGL(k_part_to_float, dim3((unsigned)ceil_div(ncols, 256)), dim3(256), 0, st,
-                     part, nb, ncols, out);
+  hipLaunchKernelGGL(k_part_to_float, dim3((unsigned)std::max(ncols, 1)), dim3(64), 0, st, part,
+                     nb, ncols, out);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -352,8 +354,7 @@ CGResult batched_cg(Provider& pv, Precond* P, const float* rhs, int C, int max_i
   op.st = pv.st;
   op.matvec = [&pv](const float* V, int ncols, float* out) { pv.forward(V, ncols, out); };
   if (P && P->rank > 0) {
-    const int nb = reduction_chunks(pv.n);
-    op.precond = [&pv, P, nb](const float* r, int ncols, float* z, double* rz_part) {
+    op.precond = [&pv, P](const float* r, int ncols, float* z, double* rz_part, int nb) {
       woodbury_apply(P->L.ptr, pv.n, P->rank, P->Minv.ptr, P->noise, r, ncols, z, P->work, r,
                      nb, rz_part, pv.st, P->dinv_ptr());
     };
@@ -365,7 +366,7 @@ CGResult batched_cg(const CGOperator& op, const float* rhs, int C, int max_iter,
                     int max_tridiag, float tol, CGWork& w, bool warm_start) {
   const int64_t n = op.n;
   hipStream_t st = op.st;
-  const int nb = reduction_chunks(n);
+  const int nb = cg_chunks(n);
   const bool pre = (bool)op.precond;
   const size_t nc = (size_t)n * C;
   float* x = w.x.ptr;  // caller ensured capacity (warm start keeps contents)
@@ -379,6 +380,7 @@ CGResult batched_cg(const CGOperator& op, const float* rhs, int C, int max_iter,
   w.hist_b.ensure((size_t)mt * C);
   double* pa = w.part_a.ensure((size_t)C * nb);
   double* pb = w.part_b.ensure((size_t)C * nb);
+  double* prr = w.part_c.ensure((size_t)C * nb);
   w.resn.ensure(1);
   w.done.ensure(1);
   CGScalars s = w.scalars(C);
@@ -392,7 +394,7 @@ CGResult batched_cg(const CGOperator& op, const float* rhs, int C, int max_iter,
     copy(r, rhs, nc, st);
   }
   if (pre) {
-    op.precond(r, C, z, pb);
+    op.precond(r, C, z, pb, nb);
   } else {
     coldot_partial(r, r, n, C, nb, pb, st);
   }
@@ -407,18 +409,17 @@ CGResult batched_cg(const CGOperator& op, const float* rhs, int C, int max_iter,
     res.iterations = iter + 1;
     op.matvec(p, C, Ap);
     coldot_partial(p, Ap, n, C, nb, pa, st);
-    cg_alpha(pa, nb, C, s, st);
-    cg_update(x, r, p, Ap, n, C, nb, s, pa, st);  // pa <- r.r partials
+    cg_update(x, r, p, Ap, n, C, nb, pa, s, prr, st);  // alpha from pAp; r.r partials
     if (pre) {
-      op.precond(r, C, z, pb);
+      op.precond(r, C, z, pb, nb);
       cg_beta(pb, nb, C, s, iter, max_tridiag, st);
     } else {
-      cg_beta(pa, nb, C, s, iter, max_tridiag, st);
+      cg_beta(prr, nb, C, s, iter, max_tridiag, st);
     }
     cg_pupdate(p, z, n, C, s, st);
     if (iter < max_tridiag) tridiag_size = iter + 1;
     if (iter >= 10 && (((iter + 1) % 10) == 0 || iter == max_iter - 1)) {
-      cg_mean_resnorm(pa, nb, C, w.resn.ptr, st);
+      cg_mean_resnorm(prr, nb, C, w.resn.ptr, st);
       float mean_res = 0.f;
       MGP_HIP_CHECK(hipMemcpyAsync(&mean_res, w.resn.ptr, sizeof(float),
                                    hipMemcpyDeviceToHost, st));
@@ -555,7 +556,7 @@ BBMMResult bbmm_step(Provider& pv, Precond& P, bool use_precond, const float* y_
     scale_columns(rf + n, facs.ptr + C + 1, n, T, false, st);
     if (pre)
       woodbury_apply(P.L.ptr, n, P.rank, P.Minv.ptr, P.noise, rf + n, T, rf + n, P.work,
-                     nullptr, reduction_chunks(n), nullptr, st, P.dinv_ptr());
+                     nullptr, 0, nullptr, st, P.dinv_ptr());
   }
   const int np = pv.nparams;
   std::vector<double> g(np, 0.0);

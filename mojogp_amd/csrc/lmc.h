@@ -76,7 +76,8 @@ struct LMCPrecond {
   void build(LMCModel& m, int precond_rank, const PivotOptions& po);
   // z = P^{-1} r for C task-blocked columns; rz_part gets the column-dot
   // partials of r.z (fixed chunking of n*T).
-  void apply(const float* r, int C, float* z, double* rz_part, hipStream_t st);
+  // z = P^-1 r; with rz_part, the partials rz_part[c*nb + b] of r . z.
+  void apply(const float* r, int C, float* z, double* rz_part, int nb, hipStream_t st);
   // N(0, P) probes: D^{1/2} eps + U w (counter-hash Gaussians, seeds
   // seed + 1000000 and seed).
   virtual void sample(float* out, int C, uint64_t seed, hipStream_t st);

@@ -398,7 +398,8 @@ static void lmc_u_times(LMCPrecond& P, const float* z, int C, float* res, hipStr
   MGP_HIP_CHECK(hipGetLastError());
 }
 
-void LMCPrecond::apply(const float* r, int C, float* z, double* rz_part, hipStream_t st) {
+void LMCPrecond::apply(const float* r, int C, float* z, double* rz_part, int nb,
+                       hipStream_t st) {
   const int64_t nT = n * T, total = nT * C;
   // 1. w = D^-1 r
   float* wv = w.ensure((size_t)total);
@@ -422,7 +423,7 @@ void LMCPrecond::apply(const float* r, int C, float* z, double* rz_part, hipStre
   // 5. z = w - D^-1 res
   hipLaunchKernelGGL(k_woodbury_lmc, g1(total), dim3(256), 0, st, z, wv, rs_, dinv.ptr, n, T, C);
   MGP_HIP_CHECK(hipGetLastError());
-  if (rz_part) coldot_partial(r, z, nT, C, reduction_chunks(nT), rz_part, st);
+  if (rz_part) coldot_partial(r, z, nT, C, nb, rz_part, st);
 }
 
 void LMCPrecond::sample(float* out, int C, uint64_t seed, hipStream_t st) {
@@ -596,8 +597,8 @@ LMCEval lmc_bbmm(LMCModel& m, LMCPrecond* P, const float* y_c, int num_probes, i
   op.st = st;
   op.matvec = [&m](const float* V, int ncols, float* out) { m.forward(V, ncols, out); };
   if (pre)
-    op.precond = [P, st](const float* r, int ncols, float* z, double* rzp) {
-      P->apply(r, ncols, z, rzp, st);
+    op.precond = [P, st](const float* r, int ncols, float* z, double* rzp, int nb) {
+      P->apply(r, ncols, z, rzp, nb, st);
     };
   const bool warm = recycle && iteration > 0 && w.has_x && w.cg.x.count >= nC;
   if (!warm) w.cg.x.ensure(nC);
@@ -656,7 +657,7 @@ LMCEval lmc_bbmm(LMCModel& m, LMCPrecond* P, const float* y_c, int num_probes, i
   if (Pn > 0) {
     copy(rf + N, probes, nP, st);
     scale_columns(rf + N, facs + C + 1, N, Pn, false, st);
-    if (pre) P->apply(rf + N, Pn, rf + N, nullptr, st);
+    if (pre) P->apply(rf + N, Pn, rf + N, nullptr, 0, st);
   }
   // Kernel-parameter gradients per latent: tr((A_s (x) dK_s) Rf Lf^T) =
   // sum over (column, task) of Lf_{c,t}^T dK_s (A_s Rf_c)_t.

@@ -176,18 +176,28 @@ __device__ __forceinline__ int col_shift(uint32_t maxbits) {
 
 // part[c*chunks + b] = max |V[c*n + j]| over the contiguous row chunk b, as
 // float bits (non-negative floats order as unsigned integers).  grid =
-// (chunks, ncols); no atomics, so no same-address serialisation.
+// (chunks, ncols); no atomics, so no same-address serialisation.  Chunks are
+// a multiple of 4 rows; vec4 (n a multiple of 4) reads 16 bytes per lane.
 __global__ __launch_bounds__(256) void k_col_absmax_part(const float* __restrict__ V, int64_t n,
-                                                         uint32_t* __restrict__ part) {
+                                                         int vec4, uint32_t* __restrict__ part) {
   __shared__ uint32_t wm[4];
   const int c = blockIdx.y;
   const int chunks = gridDim.x;
-  const int64_t len = (n + chunks - 1) / chunks;
-  const int64_t j0 = (int64_t)blockIdx.x * len, j1 = min(n, j0 + len);
+  const int64_t len = (((n + chunks - 1) / chunks) + 3) & ~(int64_t)3;
+  const int64_t j0 = min(n, (int64_t)blockIdx.x * len), j1 = min(n, j0 + len);
   const float* col = V + (int64_t)c * n;
   uint32_t mx = 0;
-  for (int64_t j = j0 + threadIdx.x; j < j1; j += blockDim.x)
-    mx = max(mx, __float_as_uint(fabsf(col[j])));
+  if (vec4) {
+#pragma unroll 4
+    for (int64_t j = j0 + 4 * threadIdx.x; j < j1; j += 4 * blockDim.x) {
+      const f4 x = *reinterpret_cast<const f4*>(col + j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx = max(mx, __float_as_uint(fabsf(x[e])));
+    }
+  } else {
+    for (int64_t j = j0 + threadIdx.x; j < j1; j += blockDim.x)
+      mx = max(mx, __float_as_uint(fabsf(col[j])));
+  }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
   if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = mx;
@@ -196,14 +206,14 @@ __global__ __launch_bounds__(256) void k_col_absmax_part(const float* __restrict
     part[(int64_t)c * chunks + blockIdx.x] = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
 }
 
-// colmax[c] = max_b part[c*chunks + b] for c < ncols (one thread per column).
-__global__ void k_col_absmax_final(const uint32_t* __restrict__ part, int chunks, int ncols,
+// colmax[c] = max_b part[c*chunks + b] (chunks <= 64): one wave per column.
+__global__ void k_col_absmax_final(const uint32_t* __restrict__ part, int chunks,
                                    uint32_t* __restrict__ colmax) {
-  const int c = threadIdx.x;
-  if (c >= ncols) return;
-  uint32_t mx = 0;
-  for (int b = 0; b < chunks; ++b) mx = max(mx, part[(int64_t)c * chunks + b]);
-  colmax[c] = mx;
+  const int c = blockIdx.x, lane = threadIdx.x;
+  uint32_t mx = lane < chunks ? part[(int64_t)c * chunks + lane] : 0u;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  if (lane == 0) colmax[c] = mx;
 }
 
 // Vp[((g*upairs + u)*2 + part)*64 + lane] (8 fp16): element e holds
@@ -211,7 +221,7 @@ __global__ void k_col_absmax_final(const uint32_t* __restrict__ part, int chunks
 // part 1 = lo.  One thread per (g, u, lane).
 __global__ void k_pack_rhs16(const float* __restrict__ V, int64_t n, int ncols,
                              int ncg, int64_t upairs, const uint32_t* __restrict__ colmax,
-                             h8* __restrict__ P) {
+                             int vec4, h8* __restrict__ P) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)ncg * upairs * 64) return;
   const int lane = (int)(idx & 63);
@@ -220,10 +230,28 @@ __global__ void k_pack_rhs16(const float* __restrict__ V, int64_t n, int ncols,
   const int c = 16 * g + (lane & 15);
   h8 hi, lo;
   const int shift = c < ncols ? col_shift(colmax[c]) : 0;
+  // rows j0 .. j0 + 3 (e < 4) and j0 + 16 .. j0 + 19 (e >= 4)
+  const int64_t j0 = 32 * u + 4 * (lane >> 4);
+  float x[8];
+  if (vec4) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t j = j0 + 16 * h;
+      const f4 q = (c < ncols && j < n) ? *reinterpret_cast<const f4*>(V + (int64_t)c * n + j)
+                                        : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * h + e] = q[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t j = j0 + 16 * (e >> 2) + (e & 3);
+      x[e] = (c < ncols && j < n) ? V[(int64_t)c * n + j] : 0.0f;
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int64_t j = 16 * (2 * u + (e >> 2)) + 4 * (lane >> 4) + (e & 3);
-    const float v = (c < ncols && j < n) ? ldexpf(V[(int64_t)c * n + j], shift) : 0.0f;
+    const float v = ldexpf(x[e], shift);
     hi[e] = (_Float16)v;
     lo[e] = (_Float16)(v - (float)hi[e]);
   }
@@ -591,6 +619,47 @@ __global__ void k_reduce_splits(const float* __restrict__ partial, int splits,
   out[idx] = o;
 }
 
+// k_reduce_splits for four consecutive rows per thread (m and mpad multiples
+// of 4): idx4 indexes quads of out; the splits are loaded four at a time and
+// added in split order, as above.
+__global__ void k_reduce_splits4(const float* __restrict__ partial, int splits, int cpad,
+                                 int64_t mpad, int64_t m, int ncols, float os, float noise,
+                                 int add_noise, const float* __restrict__ Vin,
+                                 float* __restrict__ out) {
+  const int64_t q4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q4 >= (int64_t)ncols * (m / 4)) return;
+  const int64_t idx = 4 * q4;
+  const int c = (int)(idx / m);
+  const int64_t i = idx - (int64_t)c * m;
+  const float* pc = partial + (int64_t)c * mpad + i;
+  const int64_t sstride = (int64_t)cpad * mpad;
+  double tot[4] = {0.0, 0.0, 0.0, 0.0};
+  int s = 0;
+  for (; s + 4 <= splits; s += 4) {
+    f4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const f4*>(pc + (s + q) * sstride);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tot[e] += v[q][e];
+  }
+  for (; s < splits; ++s) {
+    const f4 v = *reinterpret_cast<const f4*>(pc + s * sstride);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tot[e] += v[e];
+  }
+  f4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = os * (float)tot[e];
+  if (add_noise) {
+    const f4 vin = *reinterpret_cast<const f4*>(Vin + idx);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = fmaf(noise, vin[e], o[e]);
+  }
+  *reinterpret_cast<f4*>(out + idx) = o;
+}
+
 // Task-mixing reduction: one thread per (column block cc, row i) sums the split
 // partials of the block's T columns once, then writes the T mixed outputs
 // out[(cc*T + t)*m + i] (+)= sum_t' mix[t*T + t'] (os sum_s partial + noise V).
@@ -933,14 +1002,15 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
       colmax = buf.take(ws.colmax, 64);
       const int chunks = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(a.n, 1), 4096), 64);
       uint32_t* cpart = buf.take(ws.colmax_part, (size_t)64 * chunks);
+      const int vec4 = (a.n % 4 == 0 && reinterpret_cast<uintptr_t>(Vc) % 16 == 0) ? 1 : 0;
       hipLaunchKernelGGL(k_col_absmax_part, dim3((unsigned)chunks, (unsigned)nc), dim3(256), 0,
-                         st, Vc, a.n, cpart);
-      hipLaunchKernelGGL(k_col_absmax_final, dim3(1), dim3(64), 0, st, cpart, chunks, nc,
+                         st, Vc, a.n, vec4, cpart);
+      hipLaunchKernelGGL(k_col_absmax_final, dim3((unsigned)nc), dim3(64), 0, st, cpart, chunks,
                          colmax);
       const int64_t total = (int64_t)ncg * col_pairs * 64;  // 8-half vectors per part
       vp = buf.take(ws.vpack, (size_t)total * 2 * 4);
       hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256),
-                         0, st, Vc, a.n, nc, ncg, col_pairs, colmax,
+                         0, st, Vc, a.n, nc, ncg, col_pairs, colmax, vec4,
                          reinterpret_cast<h8*>(vp));
     }
     MGP_HIP_CHECK(hipGetLastError());
@@ -1000,9 +1070,18 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
       MGP_HIP_CHECK(hipGetLastError());
     } else if (splits > 1) {
       const int64_t tot = (int64_t)nc * a.m;
-      hipLaunchKernelGGL(k_reduce_splits, dim3((unsigned)ceil_div(tot, 256)), dim3(256),
-                         0, st, partial, (int)splits, cpad, mpad, a.m, nc,
-                         a.outputscale, a.noise, a.square ? 1 : 0, Vin, outc);
+      const bool q4 = a.m % 4 == 0 && mpad % 4 == 0 &&
+                      reinterpret_cast<uintptr_t>(outc) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(partial) % 16 == 0 &&
+                      (Vin == nullptr || reinterpret_cast<uintptr_t>(Vin) % 16 == 0);
+      if (q4)
+        hipLaunchKernelGGL(k_reduce_splits4, dim3((unsigned)ceil_div(tot / 4, 256)), dim3(256),
+                           0, st, partial, (int)splits, cpad, mpad, a.m, nc, a.outputscale,
+                           a.noise, a.square ? 1 : 0, Vin, outc);
+      else
+        hipLaunchKernelGGL(k_reduce_splits, dim3((unsigned)ceil_div(tot, 256)), dim3(256),
+                           0, st, partial, (int)splits, cpad, mpad, a.m, nc,
+                           a.outputscale, a.noise, a.square ? 1 : 0, Vin, outc);
       MGP_HIP_CHECK(hipGetLastError());
     }
   }

@@ -9,6 +9,9 @@ namespace mgp {
 
 // Number of row chunks per column used by the two-stage reductions.
 int reduction_chunks(int64_t n);
+// Row chunks of the batched CG's dot partials (~256 rows each, <= 2048): the
+// CG vector kernels and the Woodbury apply run one workgroup per chunk.
+int cg_chunks(int64_t n);
 
 // part[c*nb + b] = sum_{i in chunk b} a[c*n+i] * b[c*n+i]   (fp64)
 void coldot_partial(const float* a, const float* b, int64_t n, int ncols, int nb,
@@ -27,12 +30,12 @@ struct CGScalars {
   int* done;       // [1] device stop flag (single-rhs solves)
 };
 
-// alpha = safe(rz_old / pAp)   (reference: cg_solver.mojo:181-209)
-void cg_alpha(const double* pap_part, int nb, int ncols, CGScalars s, hipStream_t st);
-// x += alpha p, r -= alpha Ap with the reference skip rules
+// alpha = safe(rz_old / pAp) from the pAp partials (cg_solver.mojo:181-209),
+// stored in s.alpha; x += alpha p, r -= alpha Ap with the reference skip rules
 // (cg_solver.mojo:138-179); writes rr partials (r.r) for every column.
 void cg_update(float* x, float* r, const float* p, const float* Ap, int64_t n,
-               int ncols, int nb, CGScalars s, double* rr_part, hipStream_t st);
+               int ncols, int nb, const double* pap_part, CGScalars s, double* rr_part,
+               hipStream_t st);
 // beta = safe(rz_new / rz_old), rz_old = rz_new (cg_solver.mojo:211-255);
 // stores alpha/beta into the history slot `iter` when iter < max_tridiag.
 void cg_beta(const double* rz_part, int nb, int ncols, CGScalars s, int iter,
@@ -99,7 +102,8 @@ void cross_ltl(const float* La, int ka, const float* Lb, int kb, int64_t n, doub
 
 // out = (v - L u)/noise with u = Minv (L^T v) for ncols columns (Woodbury,
 // pivoted_cholesky.mojo:1646-1771).  Optionally writes dot partials of
-// dotv . out (for r.z).  out may alias v.
+// dotv . out (for r.z) over nb row chunks, dot_part[c*nb + b].  out and dotv
+// may alias v.
 struct WoodburyWork {
   DevBuf<float> wpart;   // [nbw][C][k] row-chunk partials of L^T v
   DevBuf<float> wsum;    // [C][k]

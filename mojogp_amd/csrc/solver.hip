@@ -4,6 +4,8 @@
 #include "solver.h"
 
 #include <algorithm>
+#include <cstdint>
+#include <initializer_list>
 #include <cmath>
 #include <vector>
 
@@ -12,6 +14,7 @@ namespace mgp {
 namespace {
 
 constexpr int kBlock = 256;
+typedef float f4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ double block_sum_d(double v, double* sm) {
 #pragma unroll
@@ -33,22 +36,6 @@ inline dim3 grid1(int64_t count) {
 }
 
 // ------------------------------------------------------------- reductions
-__global__ void k_coldot_part(const float* __restrict__ a, const float* __restrict__ b,
-                              int64_t n, int nb, double* __restrict__ part) {
-  __shared__ double sm[4];
-  const int c = blockIdx.y;
-  const int64_t chunk = (n + nb - 1) / nb;
-  const int64_t i0 = (int64_t)blockIdx.x * chunk;
-  const int64_t i1 = min(n, i0 + chunk);
-  const float* ac = a + (int64_t)c * n;
-  const float* bc = b + (int64_t)c * n;
-  double acc = 0.0;
-  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x)
-    acc += (double)ac[i] * (double)bc[i];
-  const double t = block_sum_d(acc, sm);
-  if (threadIdx.x == 0) part[(int64_t)c * nb + blockIdx.x] = t;
-}
-
 __global__ void k_coldot_final(const double* __restrict__ part, int nb, int ncols,
                                double* __restrict__ out) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -64,52 +51,156 @@ __device__ __forceinline__ float part_sum_f(const double* part, int c, int nb) {
   return (float)s;
 }
 
-// ------------------------------------------------------------- CG scalars
-__global__ void k_cg_alpha(const double* __restrict__ pap_part, int nb, int ncols,
-                           CGScalars s) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= ncols) return;
-  const float pap = part_sum_f(pap_part, c, nb);
-  const float rz = s.rz_old[c];
-  float a;
-  if (is_nan(rz) || is_nan(pap) || pap < 1e-10f) a = 0.0f;
-  else a = rz / pap;
-  s.alpha[c] = a;
+// Fixed-order fp64 sum of part[c*nb + b] over b by one wave: lane l sums
+// b = l, l + 64, ... in order, then a butterfly of shuffles (every lane adds
+// the same two operands at each level, so all lanes hold the same total).
+__device__ __forceinline__ double wave_part_sum(const double* part, int c, int nb) {
+  const int lane = threadIdx.x & 63;
+  const double* pc = part + (int64_t)c * nb;
+  double s = 0.0;
+  int b = lane;
+  // eight independent loads in flight, added in the same order as one by one
+  for (; b + 7 * 64 < nb; b += 8 * 64) {
+    double t[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) t[q] = pc[b + 64 * q];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s += t[q];
+  }
+  for (; b < nb; b += 64) s += pc[b];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  return s;
 }
 
-__global__ void k_cg_update(float* __restrict__ x, float* __restrict__ r,
-                            const float* __restrict__ p, const float* __restrict__ Ap,
-                            int64_t n, int nb, CGScalars s, double* __restrict__ rr_part) {
-  __shared__ double sm[4];
-  const int c = blockIdx.y;
+// ------------------------------------------------------------- CG scalars
+// One wave per (chunk b = blockIdx.x, column c = blockIdx.y); 4 consecutive
+// elements per lane per step when vec4 (n and the chunk length multiples of
+// 4, so quads never straddle a chunk or column boundary).
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// part[c*nb + b] = sum_{i in chunk b} a[c][i] b[c][i] (fp64)
+__global__ __launch_bounds__(64) void k_coldot_w(const float* __restrict__ a,
+                                                 const float* __restrict__ bv, int64_t n, int nb,
+                                                 int vec4, double* __restrict__ part) {
+  const int c = blockIdx.y, lane = threadIdx.x;
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  const float* ac = a + (int64_t)c * n;
+  const float* bc = bv + (int64_t)c * n;
+  double acc = 0.0;
+  if (vec4) {
+    for (int64_t i = i0 + 4 * lane; i < i1; i += 256) {
+      const f4v x = *reinterpret_cast<const f4v*>(ac + i), y = *reinterpret_cast<const f4v*>(bc + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc += (double)x[e] * (double)y[e];
+    }
+  } else {
+    for (int64_t i = i0 + lane; i < i1; i += 64) acc += (double)ac[i] * (double)bc[i];
+  }
+  acc = wave_sum_d(acc);
+  if (lane == 0) part[(int64_t)c * nb + blockIdx.x] = acc;
+}
+
+// alpha_c = safe(rz_old / sum of pAp partials) (cg_solver.mojo:181-209): one
+// wave per column (grid = ncols, 64 threads).
+__global__ void k_cg_alpha(const double* __restrict__ pap_part, int nb, CGScalars s) {
+  const int c = blockIdx.x;
+  const float pap = (float)wave_part_sum(pap_part, c, nb);
+  if (threadIdx.x != 0) return;
+  const float rz = s.rz_old[c];
+  s.alpha[c] = (is_nan(rz) || is_nan(pap) || pap < 1e-10f) ? 0.0f : rz / pap;
+}
+
+// x += alpha p, r -= alpha Ap with the reference skip rules
+// (cg_solver.mojo:138-179) and rr partials of the updated r.
+__global__ __launch_bounds__(64) void k_cg_update_w(float* __restrict__ x, float* __restrict__ r,
+                                                    const float* __restrict__ p,
+                                                    const float* __restrict__ Ap, int64_t n,
+                                                    int nb, int vec4, CGScalars s,
+                                                    double* __restrict__ rr_part) {
+  const int c = blockIdx.y, lane = threadIdx.x;
   const float a = s.alpha[c];
   const bool active = !(a == 0.0f || is_nan(a));
   const int64_t chunk = (n + nb - 1) / nb;
-  const int64_t i0 = (int64_t)blockIdx.x * chunk;
-  const int64_t i1 = min(n, i0 + chunk);
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   const int64_t off = (int64_t)c * n;
   double acc = 0.0;
-  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
-    float ri = r[off + i];
-    if (active) {
-      const float pi = p[off + i], api = Ap[off + i];
-      if (!is_nan(pi) && !is_nan(api)) {
-        x[off + i] += a * pi;
-        ri -= a * api;
+  auto one = [&](float& xi, float& ri, float pi, float api) __attribute__((always_inline)) {
+    if (active && !is_nan(pi) && !is_nan(api)) {
+      xi += a * pi;
+      ri -= a * api;
+    }
+    acc += (double)ri * (double)ri;
+  };
+  if (vec4) {
+    for (int64_t i = i0 + 4 * lane; i < i1; i += 256) {
+      f4v xv = *reinterpret_cast<const f4v*>(x + off + i);
+      f4v rv = *reinterpret_cast<const f4v*>(r + off + i);
+      const f4v pv = *reinterpret_cast<const f4v*>(p + off + i);
+      const f4v av = *reinterpret_cast<const f4v*>(Ap + off + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float xi = xv[e], ri = rv[e];
+        one(xi, ri, pv[e], av[e]);
+        xv[e] = xi;
+        rv[e] = ri;
+      }
+      if (active) {
+        *reinterpret_cast<f4v*>(x + off + i) = xv;
+        *reinterpret_cast<f4v*>(r + off + i) = rv;
+      }
+    }
+  } else {
+    for (int64_t i = i0 + lane; i < i1; i += 64) {
+      float xi = x[off + i], ri = r[off + i];
+      one(xi, ri, p[off + i], Ap[off + i]);
+      if (active) {
+        x[off + i] = xi;
         r[off + i] = ri;
       }
     }
-    acc += (double)ri * (double)ri;
   }
-  const double t = block_sum_d(acc, sm);
-  if (threadIdx.x == 0) rr_part[(int64_t)c * nb + blockIdx.x] = t;
+  acc = wave_sum_d(acc);
+  if (lane == 0) rr_part[(int64_t)c * nb + blockIdx.x] = acc;
 }
 
+// p = z + beta p (cg_solver.mojo:108-136)
+__global__ __launch_bounds__(64) void k_cg_pupdate_w(float* __restrict__ p,
+                                                     const float* __restrict__ z, int64_t n,
+                                                     int nb, int vec4, CGScalars s) {
+  const int c = blockIdx.y, lane = threadIdx.x;
+  const float b = s.beta[c];
+  const bool plain = (b == 0.0f || is_nan(b));
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  const int64_t off = (int64_t)c * n;
+  auto one = [&](float po, float zi) __attribute__((always_inline)) -> float {
+    return (plain || is_nan(po)) ? zi : zi + b * po;
+  };
+  if (vec4) {
+    for (int64_t i = i0 + 4 * lane; i < i1; i += 256) {
+      f4v pv = *reinterpret_cast<const f4v*>(p + off + i);
+      const f4v zv = *reinterpret_cast<const f4v*>(z + off + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[e] = one(pv[e], zv[e]);
+      *reinterpret_cast<f4v*>(p + off + i) = pv;
+    }
+  } else {
+    for (int64_t i = i0 + lane; i < i1; i += 64) p[off + i] = one(p[off + i], z[off + i]);
+  }
+}
+
+// One wave per column (grid = ncols, 64 threads).
 __global__ void k_cg_beta(const double* __restrict__ rz_part, int nb, int ncols,
                           CGScalars s, int iter, int max_tridiag) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= ncols) return;
-  const float rz_new = part_sum_f(rz_part, c, nb);
+  const int c = blockIdx.x;
+  const float rz_new = (float)wave_part_sum(rz_part, c, nb);
+  if (threadIdx.x != 0) return;
   const float rz_old = s.rz_old[c];
   float beta = 0.0f;
   if (!is_nan(rz_old) && !is_nan(rz_new) && rz_old >= 1e-20f) {
@@ -124,26 +215,12 @@ __global__ void k_cg_beta(const double* __restrict__ rz_part, int nb, int ncols,
   }
 }
 
-__global__ void k_cg_pupdate(float* __restrict__ p, const float* __restrict__ z,
-                             int64_t n, int ncols, CGScalars s) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= n * ncols) return;
-  const int c = (int)(idx / n);
-  const float b = s.beta[c];
-  if (b == 0.0f || is_nan(b)) {
-    p[idx] = z[idx];
-  } else {
-    const float po = p[idx];
-    p[idx] = is_nan(po) ? z[idx] : z[idx] + b * po;
-  }
-}
-
+// One wave (grid = 1, 64 threads): mean over columns of sqrt(sum of partials).
 __global__ void k_mean_resnorm(const double* __restrict__ rr_part, int nb, int ncols,
                                float* __restrict__ out) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
   float sum = 0.0f;
-  for (int c = 0; c < ncols; ++c) sum += sqrtf(part_sum_f(rr_part, c, nb));
-  out[0] = ncols > 0 ? sum / (float)ncols : 0.0f;
+  for (int c = 0; c < ncols; ++c) sum += sqrtf((float)wave_part_sum(rr_part, c, nb));
+  if (threadIdx.x == 0) out[0] = ncols > 0 ? sum / (float)ncols : 0.0f;
 }
 
 // ------------------------------------------------------------- vectors
@@ -484,22 +561,6 @@ __global__ void k_cross_final(const double* __restrict__ part, int64_t count, in
   M[idx] = s;
 }
 
-// out[c*k + kk] = sum over chunks b of wpart[(b*ncols + c)*k + kk]: one wave
-// per output, lanes stride the chunks, fp64 sum in a fixed order (lane
-// partials, then the shuffle tree), fp32 result.
-__global__ __launch_bounds__(256) void k_lt_reduce(const float* __restrict__ wpart, int nb, int k,
-                                                   int ncols, float* __restrict__ out) {
-  const int64_t o = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
-  const int64_t total = (int64_t)k * ncols;
-  if (o >= total) return;  // uniform per wave
-  double s = 0.0;
-  for (int b = lane; b < nb; b += 64) s += (double)wpart[(int64_t)b * total + o];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-  if (lane == 0) out[o] = (float)s;
-}
-
 // w-part[(b*ncols + c)*k + kk] = sum_{i in chunk b} L[kk][i] v[c][i]; block =
 // 16 kk x 16 c, grid = (chunks, kk tiles, column tiles).
 // rs (optional): per-row scale of v (diag(rs) v).
@@ -531,51 +592,458 @@ __global__ void k_lt_part(const float* __restrict__ L, int64_t n, int k,
   if (kk < k && c < ncols) wpart[((int64_t)blockIdx.x * ncols + c) * k + kk] = acc;
 }
 
-// u[c*k + kk] = sum_q Minv[kk*k + q] * w[q][c],  w = sum over chunks.
-__global__ void k_small_solve(const float* __restrict__ w, int k, const float* __restrict__ Minv,
-                              float* __restrict__ u) {
-  extern __shared__ float ws[];  // [k]
-  const int c = blockIdx.x;
-  for (int kk = threadIdx.x; kk < k; kk += blockDim.x) ws[kk] = w[(int64_t)c * k + kk];
-  __syncthreads();
-  for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
-    float s = 0.0f;
-    for (int q = 0; q < k; ++q) s = fmaf(Minv[(int64_t)kk * k + q], ws[q], s);
-    u[(int64_t)c * k + kk] = s;
+// wpart[(b*ncols + c)*k + kk] = sum_{i in chunk b} L[kk][i] v[c][i] (rs[i] v
+// when rs is given) on the fp32 matrix cores, v_mfma_f32_16x16x4_f32 with
+// A = L tile [16 kk x 4 rows], B = v tile [4 rows x 16 c], D[kk][c].  Lane l
+// supplies rows 4 (l/16) .. + 3 of a 16-row group, element e to MFMA e (the
+// same rows on both sides).  Wave w takes kk tiles w, w + 4, .. (<= 4 tiles,
+// k <= 256); each pass loads U groups of 16 rows (all tiles, all columns)
+// before their MFMAs so the loads overlap, double-buffered across passes.
+// Every load is unconditional, with no branch between a load and its use, so
+// the compiler's memory wait counts stay exact and both stages stay in flight:
+// a row past the chunk, an L row past k or a column past ncols is clamped to a
+// valid address and its value replaced by zero.  VEC4: n and the chunk are
+// multiples of 4, so a quad of rows is all in or all out of the chunk.  RS:
+// rs is given.
+template <int NCT, int U, bool VEC4, bool RS>
+__global__ __launch_bounds__(256) void k_ltv_mfma(const float* __restrict__ L, int64_t n, int k,
+                                                  const float* __restrict__ v, int ncols,
+                                                  int64_t chunk, float* __restrict__ wpart,
+                                                  const float* __restrict__ rs) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lm = lane & 15, lq = lane >> 4;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  const int ktiles = (k + 15) / 16;
+  int nt = 0;
+  while (nt < 4 && wave + 4 * nt < ktiles) ++nt;
+  const int64_t safe_row = VEC4 ? n - 4 : n - 1;
+  const f4v zero = f4v{0.f, 0.f, 0.f, 0.f};
+  // rows r0 .. r0 + 3 of one matrix row, zero outside the chunk
+  auto quad = [&](const float* base, int64_t r0) __attribute__((always_inline)) -> f4v {
+    if constexpr (VEC4) {
+      const bool ok = r0 < i1;
+      const f4v x = *reinterpret_cast<const f4v*>(base + (ok ? r0 : safe_row));
+      return ok ? x : zero;
+    } else {
+      f4v x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool ok = r0 + e < i1;
+        const float y = base[ok ? r0 + e : safe_row];
+        x[e] = ok ? y : 0.0f;
+      }
+      return x;
+    }
+  };
+  f4v acc[4][NCT];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) acc[t][ct] = f4v{0.f, 0.f, 0.f, 0.f};
+  // U groups of 16 rows starting at row i (zeros past the chunk end)
+  auto load = [&](int64_t i, f4v (&a)[U][4], f4v (&b)[U][NCT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r0 = i + 16 * u + 4 * lq;
+      f4v sv = zero;
+      if constexpr (RS) sv = quad(rs, r0);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const int c = ct * 16 + lm;
+        f4v x = quad(v + (int64_t)(c < ncols ? c : ncols - 1) * n, r0);
+        if constexpr (RS) x *= sv;
+        b[u][ct] = c < ncols ? x : zero;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int kk = (wave + 4 * t) * 16 + lm;
+        const f4v x = quad(L + (int64_t)(kk < k ? kk : k - 1) * n, r0);
+        a[u][t] = kk < k ? x : zero;
+      }
+    }
+  };
+  auto mma = [&](const f4v (&a)[U][4], const f4v (&b)[U][NCT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (t >= nt) break;  // uniform per wave
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[t][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][t][e], b[u][ct][e], acc[t][ct],
+                                                             0, 0, 0);
+      }
+  };
+  // Two register stages: the loads of one stage are in flight while the other
+  // stage's MFMAs run.
+  f4v a0[U][4], b0[U][NCT], a1[U][4], b1[U][NCT];
+  load(i0, a0, b0);
+  for (int64_t i = i0; i < i1; i += 32 * U) {
+    load(i + 16 * U, a1, b1);
+    mma(a0, b0);
+    load(i + 32 * U, a0, b0);
+    mma(a1, b1);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (t >= nt) break;
+    const int kt = wave + 4 * t;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int kk = kt * 16 + 4 * lq + q, c = ct * 16 + lm;
+        if (kk < k && c < ncols) wpart[((int64_t)blockIdx.x * ncols + c) * k + kk] = acc[t][ct][q];
+      }
   }
 }
 
-// out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * inv_noise (or * dinv[i]);
-// one thread per row, grid = (row blocks, column tiles of 16).
-__global__ __launch_bounds__(256) void k_woodbury_final(
-    const float* __restrict__ L, int64_t n, int k, const float* __restrict__ u,
-    int ncols, float inv_noise, const float* v, float* out, const float* __restrict__ dinv) {
-  extern __shared__ float us[];  // [16][k]
-  const int c0 = blockIdx.y * 16;
-  const int cn = min(16, ncols - c0);
-  for (int t = threadIdx.x; t < 16 * k; t += blockDim.x) {
-    const int c = t / k, kk = t - c * k;
-    us[t] = c < cn ? u[(int64_t)(c0 + c) * k + kk] : 0.0f;
-  }
-  __syncthreads();
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float z[16];
+// k_ltv_mfma for ncols <= 16 and k <= 256 with the chunk's rows and kk tiles
+// split over the waves: wave w takes the 64-row groups g0 = i0 + 64 (w & 1),
+// + 128, .. and the kk tiles t = (w >> 1) + 2 j, streaming the tiles over each
+// group (16 L rows x 64 rows per stage, double buffered; the waves of a block
+// read 512-byte runs of each L row) with the group's v values in registers.
+// MFMA roles as in k_ltv_mfma (A = L, B = v, D[kk][c]).  The two row halves
+// of a tile set are added through LDS (w & 1 = 0 plus w & 1 = 1), and waves 0
+// and 2 write the chunk's partial.  v rows past the chunk are zero; other
+// out-of-range loads use clamped addresses and only feed D entries that are
+// not written.
+template <bool VEC4, bool RS>
+__global__ __launch_bounds__(256) void k_ltv_c16(const float* __restrict__ L, int64_t n, int k,
+                                                 const float* __restrict__ v, int ncols,
+                                                 int64_t chunk, float* __restrict__ wpart,
+                                                 const float* __restrict__ rs) {
+  __shared__ f4v red[2][8][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rh = wave & 1, th = wave >> 1;
+  const int lm = lane & 15, lq = lane >> 4;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  const int ktiles = (k + 15) / 16;
+  const int64_t safe = VEC4 ? n - 4 : n - 1;
+  const f4v zero = f4v{0.f, 0.f, 0.f, 0.f};
+  auto quad = [&](const float* base, int64_t r0) __attribute__((always_inline)) -> f4v {
+    if constexpr (VEC4) {
+      return *reinterpret_cast<const f4v*>(base + (r0 < n ? r0 : safe));
+    } else {
+      f4v x;
 #pragma unroll
-  for (int c = 0; c < 16; ++c) z[c] = 0.0f;
-  for (int kk = 0; kk < k; ++kk) {
-    const float l = L[(int64_t)kk * n + i];
+      for (int e = 0; e < 4; ++e) x[e] = base[r0 + e < n ? r0 + e : safe];
+      return x;
+    }
+  };
+  f4v acc[8];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) z[c] = fmaf(l, us[c * k + kk], z[c]);
-  }
-  const float sc = dinv ? dinv[i] : inv_noise;
+  for (int j = 0; j < 8; ++j) acc[j] = zero;
+  const float* vc = v + (int64_t)(lm < ncols ? lm : ncols - 1) * n;
+  for (int64_t g0 = i0 + 64 * rh; g0 < i1; g0 += 128) {
+    f4v b[4];
 #pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    if (c < cn) {
-      const int64_t off = (int64_t)(c0 + c) * n + i;
-      out[off] = sc * (v[off] - z[c]);
+    for (int u = 0; u < 4; ++u) {
+      const int64_t r0 = g0 + 16 * u + 4 * lq;
+      f4v x = quad(vc, r0);
+      if constexpr (RS) x *= quad(rs, r0);
+      if constexpr (VEC4) {
+        b[u] = r0 < i1 ? x : zero;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b[u][e] = r0 + e < i1 ? x[e] : 0.0f;
+      }
+    }
+    // tile t = th + 2 j
+    auto load = [&](int j, f4v (&a)[4]) __attribute__((always_inline)) {
+      const float* lr = L + (int64_t)min(16 * (th + 2 * j) + lm, k - 1) * n;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = quad(lr, g0 + 16 * u + 4 * lq);
+    };
+    auto mma = [&](f4v& d, const f4v (&a)[4]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][e], b[u][e], d, 0, 0, 0);
+    };
+    f4v a0[4], a1[4];
+    load(0, a0);
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      if (th + 2 * j >= ktiles) break;  // uniform
+      load(j + 1, a1);
+      mma(acc[j], a0);
+      if (th + 2 * (j + 1) >= ktiles) break;
+      load(j + 2, a0);
+      mma(acc[j + 1], a1);
     }
   }
+  if (rh == 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (th + 2 * j < ktiles) red[th][j][lane] = acc[j];
+  }
+  __syncthreads();
+  if (rh == 1 || lm >= ncols) return;
+  float* wp = wpart + ((int64_t)blockIdx.x * ncols + lm) * k;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int t = th + 2 * j;
+    if (t >= ktiles) break;
+    const f4v tot = acc[j] + red[th][j][lane];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int kk = 16 * t + 4 * lq + q;
+      if (kk < k) wp[kk] = tot[q];
+    }
+  }
+}
+
+// out[o] = sum_b wpart[b*total + o] (fp64, fixed order) for o < total: block =
+// 16 consecutive outputs x 16 stripes of chunks (b = s, s + 16, ..); each
+// thread keeps 8 loads in flight and adds them in order, then the stripes are
+// added in order.
+__global__ __launch_bounds__(256) void k_part_reduce(const float* __restrict__ wpart, int nb,
+                                                     int64_t total, float* __restrict__ out) {
+  __shared__ double sm[16][16];
+  const int j = threadIdx.x & 15, sidx = threadIdx.x >> 4;
+  const int64_t o = (int64_t)blockIdx.x * 16 + j;
+  double acc = 0.0;
+  if (o < total) {
+    int b = sidx;
+    for (; b + 7 * 16 < nb; b += 8 * 16) {
+      float t[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) t[q] = wpart[(int64_t)(b + 16 * q) * total + o];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc += (double)t[q];
+    }
+    for (; b < nb; b += 16) acc += (double)wpart[(int64_t)b * total + o];
+  }
+  sm[sidx][j] = acc;
+  __syncthreads();
+  if (sidx == 0 && o < total) {
+    double t = sm[0][j];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) t += sm[q][j];
+    out[o] = (float)t;
+  }
+}
+
+// u = Minv w per column, written transposed by 16-column tiles:
+// ut[((c/16)*k + kk)*16 + c%16] = sum_q Minv[kk*k + q] w[c*k + q] (zero for
+// padding columns).  One wave per output, lanes stride q (coalesced row of
+// Minv), fixed-order shuffle sum.
+__global__ __launch_bounds__(256) void k_small_solve_t(const float* __restrict__ w, int k,
+                                                       int ncols, const float* __restrict__ Minv,
+                                                       float* __restrict__ ut) {
+  const int64_t o = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int cpad = ((ncols + 15) / 16) * 16;
+  if (o >= (int64_t)k * cpad) return;  // uniform per wave
+  const int c = (int)(o / k), kk = (int)(o - (int64_t)c * k);
+  float s = 0.0f;
+  if (c < ncols)
+    for (int q = lane; q < k; q += 64) s = fmaf(Minv[(int64_t)kk * k + q], w[(int64_t)c * k + q], s);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) ut[((int64_t)(c / 16) * k + kk) * 16 + (c & 15)] = s;
+}
+
+// out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * (DINV ? dinv[i] : inv_noise)
+// for the 16 columns of tile blockIdx.y, one thread per row of chunk
+// blockIdx.x (rows i0 + tid, i0 + tid + 256, ..): L read once, coalesced; u is
+// the same for every row, read from ut (k_small_solve_t layout) with scalar
+// loads.  DOT: dpart[c*nb + b] = sum over the chunk of dotv[c][i] out[c][i]
+// (fp64, fixed order: each thread's rows in order, then the wave's shuffle
+// tree, then the four waves).  v, dotv and out may alias: each element is read
+// and written by one thread.  All loads are unconditional (indices clamped
+// into range), so the compiler's memory wait counts stay exact: the row's v
+// and dotv values and the next 16 rows of L are in flight during the FMAs.
+template <bool DINV, bool DOT>
+__global__ __launch_bounds__(256) void k_woodbury_rows(
+    const float* __restrict__ L, int64_t n, int k, const float* __restrict__ ut, int ncols,
+    float inv_noise, const float* v, float* out, const float* __restrict__ dinv,
+    const float* dotv, int nb, double* __restrict__ dpart) {
+  __shared__ double wsum[4][16];
+  const int c0 = blockIdx.y * 16;
+  const int cn = min(16, ncols - c0);
+  const float* __restrict__ ub = ut + (int64_t)blockIdx.y * k * 16;
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  double dacc[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) dacc[c] = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    float vin[16], din[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int64_t off = (int64_t)(c0 + (c < cn ? c : cn - 1)) * n + i;
+      vin[c] = v[off];
+      if constexpr (DOT) din[c] = dotv[off];
+    }
+    const float sc = DINV ? dinv[i] : inv_noise;
+    float z[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) z[c] = 0.0f;
+    // groups of 16 L rows; the next group's loads (rows clamped to k - 1) are
+    // issued before this group's FMAs
+    const int kmain = k & ~15;
+    float lc[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) lc[q] = L[(int64_t)min(q, k - 1) * n + i];
+    for (int kg = 0; kg < kmain; kg += 16) {
+      float ln[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) ln[q] = L[(int64_t)min(kg + 16 + q, k - 1) * n + i];
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+#pragma unroll
+        for (int c = 0; c < 16; ++c) z[c] = fmaf(lc[q], ub[(kg + q) * 16 + c], z[c]);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) lc[q] = ln[q];
+    }
+    // rows kmain .. k - 1 are in lc
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if (kmain + q >= k) break;  // uniform
+#pragma unroll
+      for (int c = 0; c < 16; ++c) z[c] = fmaf(lc[q], ub[(kmain + q) * 16 + c], z[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      if (c < cn) {
+        const float zz = sc * (vin[c] - z[c]);
+        out[(int64_t)(c0 + c) * n + i] = zz;
+        if constexpr (DOT) dacc[c] += (double)din[c] * (double)zz;
+      }
+    }
+  }
+  if constexpr (!DOT) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    double t = dacc[c];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+    if (lane == 0) wsum[wave][c] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < cn)
+    dpart[(int64_t)(c0 + threadIdx.x) * nb + blockIdx.x] =
+        ((wsum[0][threadIdx.x] + wsum[1][threadIdx.x]) + wsum[2][threadIdx.x]) +
+        wsum[3][threadIdx.x];
+}
+
+// k_woodbury_rows on the fp32 matrix cores (k <= kWoodMfmaMaxK).  Block =
+// chunk blockIdx.x x the 16 columns of tile blockIdx.y; wave w takes the
+// 64-row groups g0 = i0 + 64 w, + 256, ..  Per group, v_mfma_f32_16x16x4_f32
+// tile t (0..3) maps MFMA row m to row g0 + 4 m + t and the MFMA k index to
+// L row kk: lane l supplies A = L[kk0 + l/16][g0 + 4 (l%16) + t] (one 16-byte
+// load per L row per lane covers the four tiles, 256 contiguous bytes per L
+// row) and B = u[c0 + l%16][kk0 + l/16] from the u tile staged in LDS (zero
+// past k).  D row 4 (l/16) + q of tile t is row g0 + 16 (l/16) + 4 q + t of
+// column c0 + l%16, so each lane writes four runs of four rows.  dpart: each
+// lane's rows in order, the four lanes of a column by a shuffle butterfly,
+// then the waves in order.  Loads are unconditional (addresses clamped into
+// range; the D rows they feed are not stored), so wait counts stay exact.
+constexpr int kWoodMfmaMaxK = 256;
+template <bool VEC4, bool DINV, bool DOT>
+__global__ __launch_bounds__(256) void k_woodbury_mfma(
+    const float* __restrict__ L, int64_t n, int k, const float* __restrict__ ut, int ncols,
+    float inv_noise, const float* v, float* out, const float* __restrict__ dinv,
+    const float* dotv, int nb, double* __restrict__ dpart) {
+  __shared__ float sB[kWoodMfmaMaxK * 16];
+  __shared__ double wsum[4][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lm = lane & 15, lq = lane >> 4;
+  const int c0 = blockIdx.y * 16, cn = min(16, ncols - c0);
+  const int kpad = (k + 31) & ~31;
+  {
+    const float* __restrict__ ub = ut + (int64_t)blockIdx.y * k * 16;
+    for (int j = threadIdx.x; j < kpad * 16; j += 256) sB[j] = j < k * 16 ? ub[j] : 0.0f;
+  }
+  __syncthreads();
+  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
+  const int64_t safe = VEC4 ? n - 4 : n - 1;
+  const f4v zero = f4v{0.f, 0.f, 0.f, 0.f};
+  // rows r .. r + 3 of a matrix row (values past n come from a clamped address)
+  auto quad = [&](const float* base, int64_t r) __attribute__((always_inline)) -> f4v {
+    if constexpr (VEC4) {
+      return *reinterpret_cast<const f4v*>(base + (r < n ? r : safe));
+    } else {
+      f4v x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = base[r + e < n ? r + e : safe];
+      return x;
+    }
+  };
+  const int cc = c0 + (lm < cn ? lm : cn - 1);
+  double dacc = 0.0;
+  for (int64_t g0 = i0 + 64 * wave; g0 < i1; g0 += 256) {
+    const int64_t ra = g0 + 4 * lm;
+    f4v acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = zero;
+    // a batch = 16 L rows kb .. kb + 15: lane rows kb + 4 j + lq, j = 0..3
+    auto load = [&](int kb, f4v (&a)[4]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[j] = quad(L + (int64_t)min(kb + 4 * j + lq, k - 1) * n, ra);
+    };
+    auto mma = [&](int kb, const f4v (&a)[4]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b = sB[(kb + 4 * j + lq) * 16 + lm];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][t], b, acc[t], 0, 0, 0);
+      }
+    };
+    f4v a0[4], a1[4];
+    load(0, a0);
+    for (int kb = 0; kb < kpad; kb += 32) {
+      load(kb + 16, a1);
+      mma(kb, a0);
+      load(kb + 32, a0);
+      mma(kb + 16, a1);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t r = g0 + 16 * lq + 4 * q;
+      const f4v vq = quad(v + (int64_t)cc * n, r);
+      f4v dq = zero, sq = f4v{inv_noise, inv_noise, inv_noise, inv_noise};
+      if constexpr (DOT) dq = quad(dotv + (int64_t)cc * n, r);
+      if constexpr (DINV) sq = quad(dinv, r);
+      f4v zz;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) zz[t] = sq[t] * (vq[t] - acc[t][q]);
+      if (lm < cn) {
+        float* o = out + (int64_t)cc * n;
+        if (VEC4 && r + 3 < i1) {
+          *reinterpret_cast<f4v*>(o + r) = zz;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (r + t < i1) o[r + t] = zz[t];
+        }
+      }
+      if constexpr (DOT) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (r + t < i1) dacc += (double)dq[t] * (double)zz[t];
+      }
+    }
+  }
+  if constexpr (!DOT) return;
+  dacc += __shfl_xor(dacc, 16);
+  dacc += __shfl_xor(dacc, 32);
+  if (lq == 0) wsum[wave][lm] = dacc;
+  __syncthreads();
+  if (threadIdx.x < cn)
+    dpart[(int64_t)(c0 + threadIdx.x) * nb + blockIdx.x] =
+        ((wsum[0][threadIdx.x] + wsum[1][threadIdx.x]) + wsum[2][threadIdx.x]) +
+        wsum[3][threadIdx.x];
 }
 
 // grid = (row blocks, column tiles of 16)
@@ -819,9 +1287,23 @@ int reduction_chunks(int64_t n) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(256, ceil_div(n, 2048)));
 }
 
+int cg_chunks(int64_t n) {
+  return (int)std::max<int64_t>(1, std::min<int64_t>(2048, ceil_div(n, 256)));
+}
+
+// 16-byte vector access is safe when the arrays are 16-byte aligned and every
+// column and chunk starts on a multiple of 4 elements.
+static int vec4_ok(int64_t n, int nb, std::initializer_list<const void*> ptrs) {
+  if (n % 4 != 0 || ceil_div(n, nb) % 4 != 0) return 0;
+  for (const void* q : ptrs)
+    if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return 0;
+  return 1;
+}
+
 void coldot_partial(const float* a, const float* b, int64_t n, int ncols, int nb,
                     double* part, hipStream_t st) {
-  hipLaunchKernelGGL(k_coldot_part, dim3(nb, ncols), dim3(kBlock), 0, st, a, b, n, nb, part);
+  hipLaunchKernelGGL(k_coldot_w, dim3(nb, ncols), dim3(64), 0, st, a, b, n, nb,
+                     vec4_ok(n, nb, {a, b}), part);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -830,28 +1312,26 @@ void coldot_finalize(const double* part, int nb, int ncols, double* out, hipStre
   MGP_HIP_CHECK(hipGetLastError());
 }
 
-void cg_alpha(const double* pap_part, int nb, int ncols, CGScalars s, hipStream_t st) {
-  hipLaunchKernelGGL(k_cg_alpha, grid1(ncols), dim3(kBlock), 0, st, pap_part, nb, ncols, s);
-  MGP_HIP_CHECK(hipGetLastError());
-}
-
 void cg_update(float* x, float* r, const float* p, const float* Ap, int64_t n, int ncols,
-               int nb, CGScalars s, double* rr_part, hipStream_t st) {
-  hipLaunchKernelGGL(k_cg_update, dim3(nb, ncols), dim3(kBlock), 0, st, x, r, p, Ap, n, nb,
-                     s, rr_part);
+               int nb, const double* pap_part, CGScalars s, double* rr_part, hipStream_t st) {
+  hipLaunchKernelGGL(k_cg_alpha, dim3(ncols), dim3(64), 0, st, pap_part, nb, s);
+  hipLaunchKernelGGL(k_cg_update_w, dim3(nb, ncols), dim3(64), 0, st, x, r, p, Ap, n, nb,
+                     vec4_ok(n, nb, {x, r, p, Ap}), s, rr_part);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
 void cg_beta(const double* rz_part, int nb, int ncols, CGScalars s, int iter,
              int max_tridiag, hipStream_t st) {
-  hipLaunchKernelGGL(k_cg_beta, grid1(ncols), dim3(kBlock), 0, st, rz_part, nb, ncols, s,
-                     iter, max_tridiag);
+  hipLaunchKernelGGL(k_cg_beta, dim3(ncols), dim3(64), 0, st, rz_part, nb, ncols, s, iter,
+                     max_tridiag);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
 void cg_pupdate(float* p, const float* z, int64_t n, int ncols, CGScalars s,
                 hipStream_t st) {
-  hipLaunchKernelGGL(k_cg_pupdate, grid1(n * ncols), dim3(kBlock), 0, st, p, z, n, ncols, s);
+  const int nb = cg_chunks(n);
+  hipLaunchKernelGGL(k_cg_pupdate_w, dim3(nb, ncols), dim3(64), 0, st, p, z, n, nb,
+                     vec4_ok(n, nb, {p, z}), s);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -1055,24 +1535,90 @@ static void launch_lt_part(const float* L, int64_t n, int k, const float* v, int
   hipLaunchKernelGGL(k_lt_part, grid, dim3(256), 0, st, L, n, k, v, ncols, nbw, wpart, rs);
 }
 
+// fp32-MFMA L^T v partials over row chunks of a multiple of 16 rows (ncols <= 64,
+// k <= 256); returns the chunk count, 0 when the shape is not served.
+static int launch_ltv_mfma(const float* L, int64_t n, int k, const float* v, int ncols,
+                           WoodburyWork& w, float** wpart_out, hipStream_t st, const float* rs) {
+  const int nct = (ncols + 15) / 16;
+  if (nct > 4 || k > 256) return 0;
+  const int64_t chunk = round_up(ceil_div(n, cg_chunks(n)), 16);
+  const int nbw = (int)ceil_div(n, chunk);
+  float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
+  const bool vec4 = n % 4 == 0 && chunk % 4 == 0 && reinterpret_cast<uintptr_t>(L) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                    (rs == nullptr || reinterpret_cast<uintptr_t>(rs) % 16 == 0);
+  const dim3 grid((unsigned)nbw), block(256);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, block, 0, st, L, n, k, v, ncols, chunk, wpart, rs);
+  };
+#define MGP_LTV(NCT, U)                                                          \
+  (vec4 ? (rs ? go(k_ltv_mfma<NCT, U, true, true>) : go(k_ltv_mfma<NCT, U, true, false>)) \
+        : (rs ? go(k_ltv_mfma<NCT, U, false, true>) : go(k_ltv_mfma<NCT, U, false, false>)))
+  switch (nct) {
+    case 1:
+      if (vec4)
+        rs ? go(k_ltv_c16<true, true>) : go(k_ltv_c16<true, false>);
+      else
+        rs ? go(k_ltv_c16<false, true>) : go(k_ltv_c16<false, false>);
+      break;
+    case 2: MGP_LTV(2, 1); break;
+    case 3: MGP_LTV(3, 1); break;
+    default: MGP_LTV(4, 1); break;
+  }
+#undef MGP_LTV
+  MGP_HIP_CHECK(hipGetLastError());
+  *wpart_out = wpart;
+  return nbw;
+}
+
+// L^T v for ncols columns into wsum [ncols][k] (fp32 result of fp64 partial sums).
+static void ltv(const float* L, int64_t n, int k, const float* v, int ncols, float* wsum,
+                WoodburyWork& w, hipStream_t st, const float* rs) {
+  float* wpart = nullptr;
+  int nbw = launch_ltv_mfma(L, n, k, v, ncols, w, &wpart, st, rs);
+  if (nbw == 0) {
+    nbw = lt_chunks(n);
+    wpart = w.wpart.ensure((size_t)nbw * k * ncols);
+    launch_lt_part(L, n, k, v, ncols, nbw, wpart, st, rs);
+  }
+  const int64_t total = (int64_t)k * ncols;
+  hipLaunchKernelGGL(k_part_reduce, dim3((unsigned)ceil_div(total, 16)), dim3(256), 0, st, wpart,
+                     nbw, total, wsum);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
 void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float noise,
                     const float* v, int ncols, float* out, WoodburyWork& w,
                     const float* dotv, int nb, double* dot_part, hipStream_t st,
                     const float* dinv) {
-  const int nbw = lt_chunks(n);
-  float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
   float* wsum = w.wsum.ensure((size_t)ncols * k);
-  float* u = w.u.ensure((size_t)ncols * k);
-  launch_lt_part(L, n, k, v, ncols, nbw, wpart, st, dinv);
-  hipLaunchKernelGGL(k_lt_reduce, dim3((unsigned)ceil_div((int64_t)k * ncols * 64, 256)),
-                     dim3(256), 0, st, wpart, nbw, k, ncols, wsum);
-  hipLaunchKernelGGL(k_small_solve, dim3(ncols), dim3(256), (size_t)k * sizeof(float), st,
-                     wsum, k, Minv, u);
-  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256), (unsigned)ceil_div(ncols, 16));
-  hipLaunchKernelGGL(k_woodbury_final, grid, dim3(256), (size_t)16 * k * sizeof(float), st, L,
-                     n, k, u, ncols, 1.0f / noise, v, out, dinv);
+  const int cpad = (int)round_up(ncols, 16);
+  float* ut = w.u.ensure((size_t)cpad * k);
+  ltv(L, n, k, v, ncols, wsum, w, st, dinv);
+  hipLaunchKernelGGL(k_small_solve_t, dim3((unsigned)ceil_div((int64_t)k * cpad * 64, 256)),
+                     dim3(256), 0, st, wsum, k, ncols, Minv, ut);
+  const int nbf = nb > 0 ? nb : cg_chunks(n);
+  const dim3 grid((unsigned)nbf, (unsigned)ceil_div(ncols, 16));
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, L, n, k, ut, ncols, 1.0f / noise, v, out,
+                       dinv, dotv, nbf, dot_part);
+  };
+  if (k <= kWoodMfmaMaxK) {
+    const bool vec4 = vec4_ok(n, nbf, {L, v, out, dinv, dotv});
+#define MGP_WOOD(V4)                                                                  \
+  (dinv ? (dot_part ? go(k_woodbury_mfma<V4, true, true>) : go(k_woodbury_mfma<V4, true, false>)) \
+        : (dot_part ? go(k_woodbury_mfma<V4, false, true>) : go(k_woodbury_mfma<V4, false, false>)))
+    if (vec4)
+      MGP_WOOD(true);
+    else
+      MGP_WOOD(false);
+#undef MGP_WOOD
+  } else if (dinv) {
+    dot_part ? go(k_woodbury_rows<true, true>) : go(k_woodbury_rows<true, false>);
+  } else {
+    dot_part ? go(k_woodbury_rows<false, true>) : go(k_woodbury_rows<false, false>);
+  }
   MGP_HIP_CHECK(hipGetLastError());
-  if (dot_part) coldot_partial(dotv, out, n, ncols, nb, dot_part, st);
 }
 
 void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const float* zn,
@@ -1174,12 +1720,7 @@ void cross_ltl(const float* La, int ka, const float* Lb, int kb, int64_t n, doub
 void lt_matmul(const float* L, int64_t n, int k, const float* V, int ncols, float* out,
                WoodburyWork& w, hipStream_t st) {
   if (k <= 0 || ncols <= 0) return;
-  const int nbw = lt_chunks(n);
-  float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
-  launch_lt_part(L, n, k, V, ncols, nbw, wpart, st);
-  hipLaunchKernelGGL(k_lt_reduce, dim3((unsigned)ceil_div((int64_t)k * ncols * 64, 256)),
-                     dim3(256), 0, st, wpart, nbw, k, ncols, out);
-  MGP_HIP_CHECK(hipGetLastError());
+  ltv(L, n, k, V, ncols, out, w, st, nullptr);
 }
 
 void l_matmul(const float* L, int64_t n, int k, const float* Z, int ncols, float* out,
