@@ -40,19 +40,22 @@ struct PackedPoints {
 };
 
 // Upper bound on max|z_i|^2 + max|z_j|^2 for the Gram-form tile path.  Its
-// distance error is ~2^-23 (|z_i|^2 + |z_j|^2), so the product error grows with
-// the data spread in lengthscales; beyond these bounds (measured product error
-// about 1e-5 at the bound) the products are evaluated from per-dimension
-// differences (direct_matvec) instead.  RBF is more sensitive (dk/ds = -ln2 k
-// against ~-0.08 near 0 for Matern-5/2, and a 14x smaller coordinate scale).
-// Matern-3/2 has dk/ds three times Matern-5/2's at s = 0 and a smaller
-// coordinate scale, hence a 4x tighter bound.  Matern-1/2 is never evaluated
-// in Gram form: k = 2^-sqrt(s) has an unbounded slope in s at s = 0, so the
-// absolute distance error e of near-coincident pairs becomes a kernel error
-// of ~ln2 sqrt(e) instead of ~e.
-constexpr float kGramMaxNormSumRBF = 4096.0f;
-constexpr float kGramMaxNormSumM52 = 32768.0f;
-constexpr float kGramMaxNormSumM32 = 8192.0f;
+// distance error is ~2^-23 (|z_i|^2 + |z_j|^2) from the fp32 accumulation of
+// the norm terms, so the product error grows with the norms of the pairs that
+// carry weight.  The worst case is data whose every point sits near the
+// largest norm (an annulus of radius many lengthscales, near-coincident pairs
+// everywhere): measured there on gfx950, the normwise relative product error
+// is 5.3e-6 (RBF) at a sum of 128, 4.3e-6 (Matern-3/2) at 512 and 7.6e-6
+// (Matern-5/2) at 2048, and crosses 1e-5 at the next power of two (the error
+// steps with the binade of the norms).  Beyond these bounds the products are
+// evaluated from per-dimension differences (direct_matvec) instead.  RBF is the
+// most sensitive: dk/ds = -ln2 k against at most -0.08 os for Matern-5/2.
+// Matern-1/2 is never evaluated in Gram form: k = 2^-sqrt(s) has an unbounded
+// slope in s at s = 0, so the absolute distance error e of near-coincident
+// pairs becomes a kernel error of ~ln2 sqrt(e) instead of ~e.
+constexpr float kGramMaxNormSumRBF = 128.0f;
+constexpr float kGramMaxNormSumM52 = 2048.0f;
+constexpr float kGramMaxNormSumM32 = 512.0f;
 inline bool gram_form_ok(int kind, const PackedPoints& rows, const PackedPoints& cols) {
   if (kind == KIND_MATERN12) return false;
   const float bound = kind == KIND_RBF       ? kGramMaxNormSumRBF

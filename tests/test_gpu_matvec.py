@@ -4,6 +4,8 @@ Bar (north star): norm-wise relative error <= 1e-5 per right-hand side,
 against oracle/kernels.py which restates the reference arithmetic
 (codegen_engine/expressions.py + passes/numerical_stability.py)."""
 
+import math
+
 import numpy as np
 import pytest
 
@@ -127,6 +129,61 @@ def test_spread_far_beyond_lengthscale(kind):
           f"cross relerr {_relerr(gotx, refx):.3e}", flush=True)
     assert _relerr(got, ref) <= TOL
     assert _relerr(gotx, refx) <= TOL
+
+
+# Gram-form bound on max|z_rows|^2 + max|z_cols|^2 per kernel and the base-2
+# coordinate scale (z = (x - mean) * scale / lengthscale).
+_GRAM_BOUND = {ok.RBF: (128.0, 0.84932180028801904272),
+               ok.MATERN32: (512.0, 2.49882111064734320000),
+               ok.MATERN52: (2048.0, 3.22596433305849393025)}
+
+
+@pytest.mark.parametrize("kind", [ok.RBF, ok.MATERN32, ok.MATERN52])
+@pytest.mark.parametrize("side", [0.95, 1.05])
+def test_gram_routing_boundary(kind, side):
+    """Points on an annulus whose outer radius puts max|z|^2 + max|z|^2 at
+    side^2 x the kernel's Gram-form bound (X symmetric, so the centre is 0).
+    Just below the bound the tile kernel runs (its output is not bit-equal to
+    the difference path); just above, the product is the difference path's
+    bit for bit.  Both sides, and the cross product from test points on the
+    same annulus, stay within the product bar of the float64 oracle, with
+    near-coincident pairs at the largest norms."""
+    bound, scale = _GRAM_BOUND[kind]
+    ls, n2, m, t = 0.1, 1500, 200, 16
+    r_out = side * math.sqrt(bound / 2.0) * ls / scale
+    rng = np.random.default_rng(17 + int(100 * side) + kind)
+
+    def annulus(k):
+        rad = np.sqrt(rng.uniform((0.7 * r_out) ** 2, r_out ** 2, size=k))
+        ang = rng.uniform(0, 2 * np.pi, size=k)
+        return np.stack([rad * np.cos(ang), rad * np.sin(ang)], 1)
+
+    P = annulus(n2)
+    P[0] = [r_out, 0.0]
+    X = np.concatenate([P, -P]).astype(np.float32)
+    Xs = annulus(m).astype(np.float32)
+    n = X.shape[0]
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = np.array([ls, 1.3], dtype=np.float32)
+    print(f"gram boundary kind={kind} side={side} r_out={r_out:.4f}", flush=True)
+    p = NativeProvider(kind, False, X, params, 0.05)
+    try:
+        got = p.forward_matvec(V)
+        direct = p.direct_matvec(V)
+        gotx = p.cross_matvec(Xs, V)
+    finally:
+        p.close()
+    ref = ok.forward_matvec(kind, X, V, params, 0.05, False)
+    refx = ok.cross_matvec(kind, Xs, X, V, params, False)
+    e, ex = _relerr(got, ref), _relerr(gotx, refx)
+    print(f"  forward relerr {e:.3e} cross relerr {ex:.3e} "
+          f"bit-equal to difference path {np.array_equal(got, direct)}", flush=True)
+    if side < 1.0:
+        assert not np.array_equal(got, direct)
+    else:
+        assert np.array_equal(got, direct)
+    assert e <= TOL
+    assert ex <= TOL
 
 
 @pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, False, 4, 3000, 16),
