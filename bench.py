@@ -162,6 +162,58 @@ def _fit_c2_seconds():
     return dt, {"final_nll": tr.nll, "cg_iterations_total": info.get("cg_iterations_total")}
 
 
+def _c4_materialized():
+    """Config 4: RBF (isotropic) N=40k d=4 on the materialized route (dense K as a
+    two-term fp16 split, 6.4 GB), default fit, exact variance at 4096 test
+    points (the generator of tests/test_gpu_configs_at_size.py), and the dense
+    product alone at 16 and 4096 right-hand sides (wall time per call, column
+    maxima + packing + MFMA product + reduction, inputs resident on the device)."""
+    from mojogp_amd import RBF, SingleOutputGP
+    from mojogp_amd._provider import NativeProvider, KIND_RBF
+    rng = np.random.default_rng(0)
+    n, d, m = 40_000, 4, 4096
+    X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
+    y = (np.prod(np.cos(X), axis=1) + 0.05 * rng.normal(size=n)).astype(np.float32)
+    Xs = rng.uniform(-2, 2, size=(m, d)).astype(np.float32)
+    gp = SingleOutputGP(RBF())
+    t0 = time.perf_counter()
+    tr = gp.fit(X, y, method="materialized")
+    fit_s = time.perf_counter() - t0
+    info = gp.backend_train_info or {}
+    t0 = time.perf_counter()
+    gp.predict(Xs, return_var=True, variance_method="exact")
+    ev_s = time.perf_counter() - t0
+    einfo = gp.backend_predict_info or {}
+    params = np.asarray(gp.kernel.to_engine_params(np.asarray(tr.params, np.float32)),
+                        np.float32)
+    prov = NativeProvider(KIND_RBF, False, X, params, float(tr.noise))
+    try:
+        prov.materialize()
+        npad = -(-n // 256) * 256
+        kbytes = 4.0 * npad * npad
+        t16, _, _ = prov.benchmark_forward(rng.normal(size=(16, n)).astype(np.float32), 10, 2)
+        ms16 = float(np.median(t16))
+        tw, _, _ = prov.benchmark_forward(rng.normal(size=(m, n)).astype(np.float32), 3, 1)
+        msw = float(np.median(tw))
+    finally:
+        prov.close()
+    flops_w = 2.0 * n * n * m
+    return {
+        "workload": "config 4: RBF N=40000 d=4, materialized route, default fit, exact "
+                    "variance at 4096 test points",
+        "fit_seconds": round(fit_s, 3),
+        "fit_iterations": len(tr.nll_history),
+        "cg_iterations_total": info.get("cg_iterations_total"),
+        "exact_variance_seconds": round(ev_s, 3),
+        "exact_cg_total_iterations": einfo.get("exact_cg_total_iterations"),
+        "dense_matvec_ms_16": round(ms16, 4),
+        "dense_matvec_GBps_16": round(kbytes / (ms16 * 1e-3) / 1e9, 1),
+        "dense_matvec_ms_4096": round(msw, 3),
+        "dense_matvec_fp32_equiv_tflops_4096": round(flops_w / (msw * 1e-3) / 1e12, 2),
+        "dense_matvec_fp16_mfma_tflops_4096": round(3 * flops_w / (msw * 1e-3) / 1e12, 2),
+    }
+
+
 C5_N, C5_D, C5_T, C5_PROBES = 20_000, 6, 4, 15
 C5_C = C5_PROBES + 1                   # columns per task block (t = 16)
 
@@ -415,6 +467,7 @@ def main(argv=None) -> int:
         result["fit_config"] = ("config 2: RBF-ARD N=50000 d=8, 30 Adam steps, 15 probes, "
                                 "rank-100 greedy preconditioner")
         result["fit_info"] = fit_info
+        result["materialized_c4"] = _c4_materialized()
         c5, c5_inputs = _lmc_c5(repeats=10, warmup=2)
         result["lmc_c5"] = c5
     if not args.no_cpu_baseline:

@@ -44,8 +44,7 @@ HIP_FLAGS = [
 ]
 
 
-# rocBLAS serves the plain fp32 GEMM of the materialized route (dense K times
-# the right-hand sides).
+# rocBLAS serves the fp64 feature GEMM of the pathwise prior samples.
 LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 
 

@@ -196,7 +196,6 @@ int mgp_destroy_provider(void* h) {
     if (pv->ws.ev0) (void)hipEventDestroy(pv->ws.ev0);
     if (pv->ws.ev1) (void)hipEventDestroy(pv->ws.ev1);
     hipStream_t st = pv->st;
-    pv->release_blas();
     delete pv;  // frees device buffers
     if (st) (void)hipStreamDestroy(st);
   });

@@ -1,0 +1,48 @@
+// Dense kernel matrix of the materialized route and its products on the fp16
+// matrix cores.
+//
+// Reference counterpart: the dense K of the reference's materialized mode and
+// its matmul (_do_materialize / impl_forward_matvec with a stored K,
+// mojogp/codegen_engine/emit/fn_ptr_module.py:363-420) and the exact-variance
+// block products (kernels/jit/jit_prediction.mojo:438-587).
+//
+// Storage: K is held as a scaled two-term fp16 split.  Every entry is scaled
+// by 2^shift (max |K| in [2^14, 2^15), so the reference's e^-20 kernel floor
+// stays a normal fp16 number) and split into hi = RNE16(x), lo = RNE16(x - hi);
+// row i keeps groups of 8 consecutive columns as {hi[8], lo[8]} (32 bytes), so
+// the storage is 4 bytes per entry like fp32 and one 32-byte load per lane is
+// a v_mfma_f32_16x16x32_f16 operand of either part.  Rows and columns are
+// padded with zeros to npad = round_up(n, 256).
+#pragma once
+
+#include "mgp_common.h"
+
+namespace mgp {
+
+struct DenseK {
+  int64_t n = 0, npad = 0;
+  int shift = 0;              // stored value = K * 2^shift (split)
+  DevBuf<uint32_t> data;      // [npad][npad / 8] groups of 16 fp16 (8 dwords)
+  int64_t groups_per_row() const { return npad / 8; }
+};
+
+// Work buffers of dense_forward, grown on demand.
+struct DenseWorkspace {
+  DevBuf<uint32_t> vpack;           // packed right-hand sides [cpad][npad / 8] groups
+  DevBuf<uint32_t> colmax, colmax_part;
+  DevBuf<float> part;               // [splits][cpad][npad]
+};
+
+// Allocate K for n points (npad^2 entries, padding zeroed) with the scale of
+// entries of magnitude up to kmax (> 0).
+void dense_alloc(DenseK& K, int64_t n, float kmax, hipStream_t st);
+// Pack rows [r0, r0 + nrows) of K given in fp32 with row stride n.
+void dense_pack_rows(const float* rows, int64_t r0, int64_t nrows, DenseK& K, hipStream_t st);
+// out = K V + noise V for V, out device [ncols][n]: products on the fp16 matrix
+// cores (Kh Vh + Kh Vl + Kl Vh, each right-hand side split after scaling its
+// column to max |V| in [2^14, 2^15)), fp32 accumulation over split ranges of
+// columns of K, the split partials added in fixed order in fp64.
+void dense_forward(const DenseK& K, const float* V, int ncols, float noise, float* out,
+                   DenseWorkspace& w, hipStream_t st);
+
+}  // namespace mgp

@@ -7,6 +7,7 @@
 
 #include <vector>
 
+#include "dense.h"
 #include "matvec.h"
 #include "tree.h"
 
@@ -57,11 +58,11 @@ struct Provider {
   PackedPoints test;
   DevBuf<float> Xs;
 
-  // Dense K (materialized route), row-major [n][n] (symmetric, so also
-  // column-major), refilled on every parameter update.
+  // Dense K (materialized route) as a scaled two-term fp16 split (dense.h),
+  // refilled on every parameter update.
   bool materialized = false;
-  DevBuf<float> K;
-  void* blas = nullptr;  // rocblas_handle bound to `st` (materialized route)
+  DenseK dense;
+  DenseWorkspace dense_ws;
 
   float outputscale() const { return params[nparams - 1]; }
   // k(x, x) (every supported kernel is stationary): the outputscale for a
@@ -86,9 +87,10 @@ struct Provider {
   // Allocate and fill the dense K (materialized route, _do_materialize).
   void materialize();
   void fill_dense();
-  void release_blas();
-  // Rebind the provider (and its rocBLAS handle) to another stream.
-  void set_stream(hipStream_t s);
+  // max_i k(x_i, x_i): bounds every |K_ij| of a positive semi-definite kernel.
+  float kdiag_max();
+  // Rebind the provider to another stream.
+  void set_stream(hipStream_t s) { st = s; }
 
   // Host [n] noise variances (all finite and > 0), or nullptr to clear.
   void set_noise_vector(const float* host);

@@ -1,7 +1,6 @@
 // Provider state management and the matvec entry points it serves.
 #include "provider.h"
 
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cmath>
@@ -57,20 +56,6 @@ void Provider::gradient(const float* V, int ncols, float* out) {
 }
 
 namespace {
-#define MGP_BLAS_CHECK(expr)                                                        \
-  do {                                                                              \
-    const rocblas_status s_ = (expr);                                               \
-    if (s_ != rocblas_status_success)                                               \
-      throw Error(ST_HIP, std::string("rocBLAS error in " #expr ": ") +             \
-                              rocblas_status_to_string(s_));                        \
-  } while (0)
-
-__global__ void k_scaled_copy(float* __restrict__ y, const float* __restrict__ x, float a,
-                              int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = a * x[i];
-}
-
 // out[c][i] += dvec[i] * V[c][i]
 __global__ void k_add_diag_vec(float* __restrict__ out, const float* __restrict__ V,
                                const float* __restrict__ dvec, int64_t n, int ncols) {
@@ -103,7 +88,32 @@ void Provider::load_noise_vector(const float* host) {
   has_noise_vec = true;
 }
 
-void Provider::fill_dense() { fill_block(train, 0, n, K.ptr); }
+float Provider::kdiag_max() {
+  if (!is_tree) return outputscale();
+  float* d = io_c.ensure((size_t)n);
+  diag_values(train, n, d);
+  std::vector<float> h((size_t)n);
+  MGP_HIP_CHECK(hipMemcpyAsync(h.data(), d, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
+  float mx = 0.f;
+  for (float v : h) mx = std::max(mx, std::fabs(v));
+  return mx;
+}
+
+void Provider::fill_dense() {
+  float kmax = kdiag_max();
+  MGP_REQUIRE(std::isfinite(kmax), "kernel diagonal is not finite");
+  if (!(kmax > 0.f)) kmax = 1.f;  // K = 0: any scale
+  dense_alloc(dense, n, kmax, st);
+  // fp32 rows in blocks of <= 32M entries, each packed into the split storage
+  const int64_t rows = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t)1 << 25) / n));
+  float* tmp = io_c.ensure((size_t)rows * n);
+  for (int64_t r0 = 0; r0 < n; r0 += rows) {
+    const int64_t nr = std::min(rows, n - r0);
+    fill_block(train, r0, nr, tmp);
+    dense_pack_rows(tmp, r0, nr, dense, st);
+  }
+}
 
 void Provider::diag_values(const PackedPoints& pts, int64_t m, float* out) {
   if (is_tree) {
@@ -125,29 +135,12 @@ void Provider::fill_block(const PackedPoints& rows, int64_t r0, int64_t nrows, f
 
 void Provider::materialize() {
   if (!materialized) {
-    const double bytes = (double)n * (double)n * sizeof(float);
+    const double bytes = (double)round_up(n, 256) * (double)round_up(n, 256) * sizeof(float);
     MGP_REQUIRE(bytes <= 200e9, "dense K of this size does not fit the device");
-    K.ensure((size_t)n * (size_t)n);
-    if (!blas) {
-      rocblas_handle h = nullptr;
-      MGP_BLAS_CHECK(rocblas_create_handle(&h));
-      blas = h;
-      MGP_BLAS_CHECK(rocblas_set_stream(h, st));
-    }
     materialized = true;
   }
   fill_dense();
   MGP_HIP_CHECK(hipStreamSynchronize(st));
-}
-
-void Provider::set_stream(hipStream_t s) {
-  st = s;
-  if (blas) MGP_BLAS_CHECK(rocblas_set_stream(static_cast<rocblas_handle>(blas), s));
-}
-
-void Provider::release_blas() {
-  if (blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(blas));
-  blas = nullptr;
 }
 
 void Provider::pack(const float* X_dev, int64_t m, PackedPoints& pp) {
@@ -186,17 +179,7 @@ void Provider::forward_scalar(const float* V, int ncols, float* out, MatvecWorks
   a.n = n;
   a.ncols = ncols;
   if (materialized) {
-    // out = noise V, then out += K V (rocBLAS sgemm, fp32; K symmetric so its
-    // row-major storage is the column-major operand).
-    const int64_t total = n * (int64_t)ncols;
-    hipLaunchKernelGGL(k_scaled_copy, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
-                       out, V, noise, total);
-    MGP_HIP_CHECK(hipGetLastError());
-    const float one = 1.0f;
-    MGP_BLAS_CHECK(rocblas_sgemm(static_cast<rocblas_handle>(blas), rocblas_operation_none,
-                                 rocblas_operation_none, (rocblas_int)n, ncols, (rocblas_int)n,
-                                 &one, K.ptr, (rocblas_int)n, V, (rocblas_int)n, &one, out,
-                                 (rocblas_int)n));
+    dense_forward(dense, V, ncols, noise, out, dense_ws, st);
     return;
   }
   if (is_tree) {

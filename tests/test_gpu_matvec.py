@@ -188,10 +188,12 @@ def test_gram_routing_boundary(kind, side):
 
 @pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, False, 4, 3000, 16),
                                             (ok.MATERN52, True, 3, 2048, 1),
-                                            (ok.RBF, True, 2, 1500, 40)])
+                                            (ok.RBF, True, 2, 1500, 40),
+                                            (ok.MATERN32, False, 5, 1001, 130)])
 def test_materialized_route_parity(kind, ard, d, n, t):
-    """Dense K filled on the device, products by fp32 GEMM (+ noise V); refilled
-    after a parameter update."""
+    """Dense K filled on the device and stored as a two-term fp16 split, products
+    on the fp16 matrix cores (+ noise V): the 16-, 64- and 128-column block
+    shapes, n not a multiple of 8; refilled after a parameter update."""
     rng = np.random.default_rng(40 + d + t)
     X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
     V = rng.normal(size=(t, n)).astype(np.float32)
