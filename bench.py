@@ -206,6 +206,7 @@ def _c4_materialized():
         "cg_iterations_total": info.get("cg_iterations_total"),
         "exact_variance_seconds": round(ev_s, 3),
         "exact_cg_total_iterations": einfo.get("exact_cg_total_iterations"),
+        "lengthscale": float(params[0]),
         "dense_matvec_ms_16": round(ms16, 4),
         "dense_matvec_GBps_16": round(kbytes / (ms16 * 1e-3) / 1e9, 1),
         "dense_matvec_ms_4096": round(msw, 3),
@@ -332,6 +333,140 @@ def _cpu_baseline_c5(X, V1, target_s: float):
     }
 
 
+def _c1_data():
+    """Config 1: X = linspace(-3, 3, 2000), y = sin(2x) + 0.05 N(0, 1) (seed 0);
+    test points linspace(-4, 4, 128)."""
+    rng = np.random.default_rng(0)
+    X = np.linspace(-3, 3, 2000, dtype=np.float32)[:, None]
+    y = (np.sin(2 * X[:, 0]) + 0.05 * rng.normal(size=2000)).astype(np.float32)
+    Xs = np.linspace(-4, 4, 128, dtype=np.float32)[:, None]
+    return X, y, Xs
+
+
+def _c1_gpu_seconds():
+    """Config 1 on the GPU: 50-step matrix-free fit + LOVE predict at 128 points."""
+    from mojogp_amd import RBF, SingleOutputGP
+    X, y, Xs = _c1_data()
+    gp = SingleOutputGP(RBF())
+    t0 = time.perf_counter()
+    gp.fit(X, y, max_iterations=50, method="matrix_free")
+    gp.predict(Xs, return_std=True, variance_method="love")
+    return time.perf_counter() - t0
+
+
+def _row_sample_seconds(run, total_rows: int, target_s: float, probe: int = 64):
+    """Seconds of run(rows) for all total_rows, extrapolated linearly from a
+    timed prefix sized to about target_s.  Returns (seconds, rows timed)."""
+    t0 = time.perf_counter()
+    run(probe)
+    dt = max(time.perf_counter() - t0, 1e-4)
+    rows = int(min(total_rows, max(probe, target_s / dt * probe)))
+    t0 = time.perf_counter()
+    run(rows)
+    dt = time.perf_counter() - t0
+    return dt * total_rows / rows, rows
+
+
+def _cpu_legs(gpu: dict, target_s: float) -> dict:
+    """CPU timings of configs 1-4 on this host (the oracle restatements: the
+    numpy training loop, the fp32 reference-order C product, numpy fp32 dense
+    algebra), each beside the GPU figure of the same work.  Config 1 runs in
+    full; the others time a prefix of rows of their products and extrapolate."""
+    from oracle import cpu_ref
+    from oracle import engine as oe
+    from oracle import kernels as ok
+    threads = cpu_ref.num_threads()
+    legs = {}
+    # config 1: the whole fit + predict
+    X, y, Xs = _c1_data()
+    t0 = time.perf_counter()
+    ref = oe.train(ok.RBF, False, X, y, [1.0, 1.0], 0.1, max_iterations=50, num_probes=10,
+                   max_cg=100, cg_tol=1e-2, precond_rank=0, max_tridiag=30)
+    oe.predict(ok.RBF, False, X, y, Xs, np.asarray(ref["params"], np.float64), ref["noise"],
+               ref["mean"], max_cg=300, tol=1e-3, lanczos_rank=100)
+    c1 = time.perf_counter() - t0
+    legs["c1"] = {"cpu_seconds": round(c1, 3), "gpu_seconds": gpu.get("c1"),
+                  "work": "50-step fit + LOVE predict at 128 points, measured in full",
+                  "kind": "port (numpy restatement of the training loop)"}
+    # config 2: one 16-column product per CG iteration, times the GPU fit's CG count
+    rng = np.random.default_rng(0)
+    X2 = rng.uniform(size=(50_000, 8)).astype(np.float32)
+    p2 = np.concatenate([np.full(8, 0.5), [1.0]]).astype(np.float32)
+    V2 = rng.normal(size=(16, 50_000)).astype(np.float32)
+    mv2, rows2 = _row_sample_seconds(
+        lambda r: cpu_ref.forward_matvec_rows(0, True, X2, p2, 0.01, V2, 0, r), 50_000,
+        target_s / 4)
+    cg2 = gpu.get("c2_cg_iterations") or 0
+    legs["c2"] = {"cpu_seconds_per_product": round(mv2, 3),
+                  "cpu_fit_seconds_extrapolated": round(mv2 * cg2, 1) if cg2 else None,
+                  "gpu_fit_seconds": gpu.get("c2_fit"),
+                  "work": f"(K + s^2 I) V, 16 columns, rows [0,{rows2}) timed; fit = product x "
+                          f"the GPU fit's {cg2} CG iterations (vector work and gradients "
+                          f"not counted: a lower bound)",
+                  "kind": "port (fp32 reference-order C restatement)"}
+    # config 3: one mBCG iteration = product (row sample) + Woodbury apply (numpy)
+    X3, _, p3, noise3 = _make_inputs()
+    V3 = np.random.default_rng(1).normal(size=(16, N)).astype(np.float32)
+    mv3, rows3 = _row_sample_seconds(
+        lambda r: cpu_ref.forward_matvec_rows(1, True, X3, p3, noise3, V3, 0, r), N,
+        target_s / 4)
+    L = np.random.default_rng(2).normal(size=(200, N)).astype(np.float32)
+    Minv = np.eye(200, dtype=np.float32)
+    t0 = time.perf_counter()
+    w = L @ V3.T
+    z = (V3 - (L.T @ (Minv @ w)).T) / np.float32(noise3)
+    wb3 = time.perf_counter() - t0
+    legs["c3"] = {"cpu_ms_per_mbcg_iteration": round((mv3 + wb3) * 1e3, 1),
+                  "gpu_ms_per_mbcg_iteration": gpu.get("c3_mbcg_ms"),
+                  "work": f"product rows [0,{rows3}) timed and extrapolated, plus the rank-200 "
+                          f"Woodbury apply in numpy fp32 ({wb3 * 1e3:.0f} ms); the gradient "
+                          f"pass has no CPU restatement at this size",
+                  "kind": "port (C restatement + numpy)"}
+    del L, z, w
+    # config 4: dense K fill and one 16-column product (row samples), and the
+    # 4096-column exact-variance product
+    rng4 = np.random.default_rng(0)
+    n4 = 40_000
+    X4 = rng4.uniform(-2, 2, size=(n4, 4)).astype(np.float32)
+    ls, os_ = np.float32(gpu.get("c4_lengthscale") or 1.0), np.float32(1.0)
+    blk = {}
+
+    def fill(r):
+        d2 = np.zeros((r, n4), np.float32)
+        for k in range(X4.shape[1]):
+            d2 += ((X4[:r, k, None] - X4[None, :, k]) / ls) ** 2
+        blk["K"] = os_ * np.exp(np.maximum(np.float32(-0.5) * d2, np.float32(-20.0)))
+    fill_s, rows4 = _row_sample_seconds(fill, n4, target_s / 8, probe=16)
+    Kb = blk["K"]
+    V16 = rng4.normal(size=(n4, 16)).astype(np.float32)
+    t0 = time.perf_counter()
+    Kb @ V16
+    p16 = (time.perf_counter() - t0) * n4 / Kb.shape[0]
+    Vw = rng4.normal(size=(n4, 512)).astype(np.float32)
+    t0 = time.perf_counter()
+    Kb @ Vw
+    pw = (time.perf_counter() - t0) * n4 / Kb.shape[0] * (4096 / 512)
+    cg4 = gpu.get("c4_cg_iterations") or 0
+    legs["c4"] = {"cpu_fill_seconds": round(fill_s, 2),
+                  "cpu_ms_per_product_16": round(p16 * 1e3, 1),
+                  "gpu_ms_per_product_16": gpu.get("c4_ms_16"),
+                  "cpu_seconds_per_product_4096": round(pw, 2),
+                  "gpu_seconds_per_product_4096": gpu.get("c4_s_4096"),
+                  "cpu_fit_seconds_extrapolated": round(p16 * cg4 + 100 * fill_s, 1) if cg4 else None,
+                  "gpu_fit_seconds": gpu.get("c4_fit"),
+                  "cpu_exact_variance_seconds_extrapolated": round(50 * pw, 1),
+                  "gpu_exact_variance_seconds": gpu.get("c4_exact"),
+                  "work": f"K rows [0,{rows4}) filled (numpy fp32, per-dimension differences) "
+                          f"and multiplied by 16 and 512 columns (numpy fp32 GEMM), all "
+                          f"extrapolated to N=40000 (and 4096 columns); fit = 100 fills + one "
+                          f"16-column product per GPU CG iteration ({cg4}); exact variance = "
+                          f"50 products of 4096 columns",
+                  "kind": "port (numpy fp32)"}
+    for leg in legs.values():
+        leg["threads"] = threads
+    return legs
+
+
 def _cpu_baseline(X, V, params, noise, target_s: float):
     from oracle import cpu_ref
     threads = cpu_ref.num_threads()
@@ -362,6 +497,9 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--c4-only", action="store_true",
+                    help="only the config-4 materialized leg (fit, exact variance, dense "
+                         "products)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the mBCG-iteration and fit() measurements")
     ap.add_argument("--mbcg-only", action="store_true",
@@ -380,6 +518,9 @@ def main(argv=None) -> int:
                           "ms": ms.value, "GB/s": gbs}), flush=True)
         return 0
 
+    if args.c4_only:
+        print(json.dumps(_c4_materialized()), flush=True)
+        return 0
     if args.mbcg_only:
         X, _, params, noise = _make_inputs()
         c3, _ = _mbcg_iteration_ms(X, params, noise)
@@ -468,12 +609,24 @@ def main(argv=None) -> int:
                                 "rank-100 greedy preconditioner")
         result["fit_info"] = fit_info
         result["materialized_c4"] = _c4_materialized()
+        result["fit_predict_seconds_c1"] = round(_c1_gpu_seconds(), 3)
         c5, c5_inputs = _lmc_c5(repeats=10, warmup=2)
         result["lmc_c5"] = c5
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = _cpu_baseline(X, V, params, noise, args.cpu_seconds)
         if not args.no_extras:
             result["lmc_c5"]["cpu_baseline"] = _cpu_baseline_c5(*c5_inputs, args.cpu_seconds / 2)
+            c4 = result["materialized_c4"]
+            gpu = {"c1": result["fit_predict_seconds_c1"],
+                   "c2_fit": result["fit_seconds"],
+                   "c2_cg_iterations": (result.get("fit_info") or {}).get("cg_iterations_total"),
+                   "c3_mbcg_ms": result["mbcg_iter_ms"],
+                   "c4_ms_16": c4["dense_matvec_ms_16"],
+                   "c4_s_4096": round(c4["dense_matvec_ms_4096"] / 1e3, 4),
+                   "c4_fit": c4["fit_seconds"], "c4_exact": c4["exact_variance_seconds"],
+                   "c4_cg_iterations": c4["cg_iterations_total"],
+                   "c4_lengthscale": c4.get("lengthscale")}
+            result["cpu_baseline"]["legs"] = _cpu_legs(gpu, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
 
