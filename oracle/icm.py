@@ -186,9 +186,14 @@ def train(kind: int, ard: bool, X, Y_blocked, init_params, init_noise, init_os, 
           trainable=None, fixed=None, max_iterations=100, learning_rate=0.05, task_rank=-1,
           num_probes=10, max_cg=200, max_tridiag=30, cg_tol=1e-2, precond_rank=15,
           precond_method=0, rebuild_threshold=0.5, early_stop_patience=15,
-          early_stop_tol=1e-4, use_cosine_lr=False):
+          early_stop_tol=1e-4, use_cosine_lr=False, evaluate=None):
     """train_multi_output_jit restated (jit_multi_output.mojo:130-817), fp32
-    host scalars; the preconditioner keeps the parameters of its last build."""
+    host scalars; the preconditioner keeps the parameters of its last build.
+
+    Test hook: ``evaluate(it, params, os, B, noise, y_c)`` replaces the BBMM
+    evaluation and returns a dict with ``nll``, ``kernel_grads``,
+    ``noise_grads``, ``G_A`` ([1][T][T], dNLL/dA for A = os B),
+    ``grad_outputscale``, ``alpha`` (T*n) and ``cg_iterations``."""
     sp, isp = oe._softplus, oe._inv_softplus
     X = np.asarray(X, np.float64)
     n = X.shape[0]
@@ -208,7 +213,7 @@ def train(kind: int, ard: bool, X, Y_blocked, init_params, init_noise, init_os, 
     madam = np.zeros(total, F32)
     vadam = np.zeros(total, F32)
     b1, b2, eps = F32(0.9), F32(0.999), F32(1e-8)
-    use_pre = precond_rank > 0 and not fixed_vec
+    use_pre = precond_rank > 0 and not fixed_vec and evaluate is None
     sig = lambda x: F32(1.0) / (F32(1.0) + F32(np.exp(-F32(x))))  # noqa: E731
 
     def constrained(raw):
@@ -257,8 +262,12 @@ def train(kind: int, ard: bool, X, Y_blocked, init_params, init_noise, init_os, 
             rebuilds += 1
         yc = (Y - raw_mean[:, None]).reshape(-1)
         op_noise = np.zeros(T) if fixed_vec else noise
-        ev = bbmm(kind, ard, X, cur_p, os_, B, op_noise, yc, fixed=fixed, num_probes=num_probes,
-                  max_cg=max_cg, max_tridiag=max_tridiag, tol=cg_tol, iteration=it, P=P)
+        if evaluate is not None:
+            ev = evaluate(it, cur_p, os_, B, op_noise, yc)
+        else:
+            ev = bbmm(kind, ard, X, cur_p, os_, B, op_noise, yc, fixed=fixed,
+                      num_probes=num_probes, max_cg=max_cg, max_tridiag=max_tridiag, tol=cg_tol,
+                      iteration=it, P=P)
         ok_cg = ev["cg_iterations"] < max_cg
         if not ok_cg and use_pre:
             P = build(cur_p, os_, B, noise)

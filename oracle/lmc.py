@@ -199,12 +199,17 @@ def _a_from_l(L, vd):
 def train(kinds, ards, X, Y_blocked, init_params, init_noise, init_mean, *, trainable=None,
           fixed=None, max_iterations=100, learning_rate=0.05, num_probes=10, max_cg=200,
           max_tridiag=30, cg_tol=1.0, precond_rank=15, precond_method=0,
-          rebuild_threshold=0.5, early_stop_tol=1e-4, early_stop_patience=15):
+          rebuild_threshold=0.5, early_stop_tol=1e-4, early_stop_patience=15, evaluate=None):
     """train_lmc_jit restated (jit_lmc.mojo:699-1529): Adam over raw (inverse
     softplus) kernel parameters and noise, L_s (diagonal through softplus,
     strictly lower part unconstrained), var_diag (softplus) and the per-task
     mean, gradient clip 10, NaN recovery, best-NLL tracking and smoothed-NLL
-    early stopping.  Float32 host scalars as the reference."""
+    early stopping.  Float32 host scalars as the reference.
+
+    Test hook: ``evaluate(it, params, A, noise, y_c)`` replaces the BBMM
+    evaluation and returns a dict with ``nll``, ``kernel_grads`` (latents'
+    parameters concatenated), ``noise_grads``, ``G_A`` ([R][T][T], dNLL/dA_s)
+    and ``alpha`` (T*n; the mean step is -sum(alpha_t)/(n T))."""
     sp, isp, dsp = oe._softplus, oe._inv_softplus, oe._softplus_deriv
     X = np.asarray(X, np.float64)
     n = X.shape[0]
@@ -286,9 +291,12 @@ def train(kinds, ards, X, Y_blocked, init_params, init_noise, init_mean, *, trai
             last_rb = np.concatenate(params)
             last_rb_noise = noise.copy()
             P_state = (A.copy(), noise.copy(), [p.copy() for p in params])
-        ev = _bbmm_with_frozen_precond(kinds, ards, X, params, A, noise, yc, fixed, num_probes,
-                                       max_cg, max_tridiag, cg_tol, it, precond_rank,
-                                       precond_method, P_state)
+        if evaluate is not None:
+            ev = evaluate(it, params, A, noise, yc)
+        else:
+            ev = _bbmm_with_frozen_precond(kinds, ards, X, params, A, noise, yc, fixed,
+                                           num_probes, max_cg, max_tridiag, cg_tol, it,
+                                           precond_rank, precond_method, P_state)
         nll = F32(ev["nll"])
         hist.append(float(nll))
         if np.isnan(nll):

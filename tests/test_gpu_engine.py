@@ -233,9 +233,11 @@ def test_fit_then_predict_matches_oracle():
                    max_cg=100, cg_tol=1e-2, precond_rank=0, max_tridiag=30)
     print(f"params {tr.params} vs {ref['params']}; noise {tr.noise} vs {ref['noise']}; "
           f"mean {tr.mean} vs {ref['mean']}; nll {tr.nll} vs {ref['final_nll']}", flush=True)
-    assert _rel(tr.params, ref["params"]) <= 1e-3
-    assert tr.noise == pytest.approx(ref["noise"], rel=1e-3)
-    assert tr.nll == pytest.approx(ref["final_nll"], rel=1e-3)
+    # the fp32 CG floor of the parameters after the Adam steps is ~2e-4
+    # (test_oracle_training.py::test_c1_fp32_rounding_floor); NLL at the bar
+    assert _rel(tr.params, ref["params"]) <= 5e-4
+    assert tr.noise == pytest.approx(ref["noise"], rel=1e-4)
+    assert tr.nll == pytest.approx(ref["final_nll"], rel=1e-4)
     mu, var, _ = oe.predict(ok.RBF, False, X, y, Xs, tr.params.astype(np.float64), tr.noise,
                             tr.mean, max_cg=300, tol=1e-3, lanczos_rank=100)
     print(f"predict mean relerr {_rel(mean, mu):.2e} std relerr {_rel(std, np.sqrt(var)):.2e}",
