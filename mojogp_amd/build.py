@@ -55,9 +55,34 @@ def _hipcc() -> str:
     return path
 
 
-def _compile_one(src: Path) -> Path:
-    obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, "-I", str(CSRC), "-I", str(REPO_DIR / "include"),
+# Host-side sanitizers for the checking build (device code is compiled exactly
+# as in the product library; every -fsanitize applies to the host pass only).
+ASAN_DIR = LIB_DIR / "asan"
+ASAN_LIB_PATH = ASAN_DIR / "libmojogp_amd.so"
+HOST_SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize=function",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+]
+
+# Runtimes preloaded into a process that loads the sanitized library: the
+# system GCC libasan / libubsan (same ASan v8 interface).  The ROCm clang ASan
+# runtime is not used: it also intercepts the HSA memory-pool allocator for
+# device-side ASan, which fails without XNACK, so device allocations abort.
+_SANITIZER_RUNTIMES = [Path("/usr/lib/x86_64-linux-gnu/libasan.so.6"),
+                       Path("/usr/lib/x86_64-linux-gnu/libubsan.so.1")]
+
+
+def sanitizer_runtimes() -> list[Path] | None:
+    """Libraries to preload (in order) for the sanitized build, or None."""
+    return _SANITIZER_RUNTIMES if all(p.exists() for p in _SANITIZER_RUNTIMES) else None
+
+
+def _compile_one(src: Path, obj_dir: Path = OBJ_DIR, extra=()) -> Path:
+    obj = obj_dir / (src.stem + ".o")
+    cmd = [_hipcc(), *HIP_FLAGS, *extra, "-I", str(CSRC), "-I", str(REPO_DIR / "include"),
            "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -65,25 +90,32 @@ def _compile_one(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile all HIP sources and link the shared library. Returns its path."""
-    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+def build(verbose: bool = False, jobs: int | None = None, sanitized: bool = False) -> Path:
+    """Compile all HIP sources and link the shared library. Returns its path.
+
+    sanitized: the checking build instead, host code under AddressSanitizer
+    and UndefinedBehaviorSanitizer (``mojogp_amd/lib/asan``); a process that
+    loads it preloads sanitizer_runtimes()."""
+    obj_dir = (ASAN_DIR / "obj") if sanitized else OBJ_DIR
+    lib_path = ASAN_LIB_PATH if sanitized else LIB_PATH
+    extra = HOST_SANITIZE_FLAGS if sanitized else ()
+    obj_dir.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = jobs or min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile_one, sources))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile_one(src, obj_dir, extra), sources))
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs), *LINK_LIBS]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH} from {len(sources)} sources")
-    return LIB_PATH
+        print(f"built {lib_path} from {len(sources)} sources")
+    return lib_path
 
 
 if __name__ == "__main__":

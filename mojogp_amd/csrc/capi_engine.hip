@@ -14,10 +14,7 @@ using namespace mgp;
 
 namespace {
 
-Provider* as_provider(void* h) {
-  MGP_REQUIRE(h != nullptr, "null provider handle");
-  return static_cast<Provider*>(h);
-}
+Provider* as_provider(void* h) { return checked_provider(h); }
 
 struct PredictionCache {
   Provider* owner = nullptr;

@@ -11,10 +11,7 @@ using namespace mgp;
 
 namespace {
 
-Provider* provider_of(void* h) {
-  if (h == nullptr) throw Error(ST_INVALID, "null provider handle");
-  return static_cast<Provider*>(h);
-}
+Provider* provider_of(void* h) { return checked_provider(h); }
 
 template <class T>
 int copy_to(T* dst, const std::vector<T>& src) {

@@ -17,7 +17,7 @@ void init_model(LMCModel& m, void* const* providers, int R, int T) {
   m.T = T;
   for (int s = 0; s < R; ++s) {
     if (providers[s] == nullptr) throw Error(ST_INVALID, "null latent provider");
-    m.prov.push_back(static_cast<Provider*>(providers[s]));
+    m.prov.push_back(checked_provider(providers[s]));
   }
   m.n = m.prov[0]->n;
   for (Provider* p : m.prov)

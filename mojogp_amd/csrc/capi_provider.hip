@@ -15,10 +15,7 @@ namespace mgp {
 thread_local std::string g_last_error;
 void set_last_error(const std::string& msg) { g_last_error = msg; }
 
-static Provider* as_provider(void* h) {
-  MGP_REQUIRE(h != nullptr, "null provider handle");
-  return static_cast<Provider*>(h);
-}
+static Provider* as_provider(void* h) { return checked_provider(h); }
 
 // Plain streaming copy used to calibrate HBM byte counters.
 __global__ void k_calibration_copy(const float4* __restrict__ a,
@@ -129,6 +126,7 @@ Provider* finish_provider(Provider* pv, int d, int64_t n, const float* X, const 
     delete pv;
     throw;
   }
+  register_provider(pv);
   return pv;
 }
 }  // namespace
@@ -192,6 +190,7 @@ int mgp_init_provider_tree(const int* spec, int spec_len, int d, int64_t n, cons
 int mgp_destroy_provider(void* h) {
   return guarded([&] {
     Provider* pv = as_provider(h);
+    unregister_provider(pv);
     if (pv->st) (void)hipStreamSynchronize(pv->st);
     if (pv->ws.ev0) (void)hipEventDestroy(pv->ws.ev0);
     if (pv->ws.ev1) (void)hipEventDestroy(pv->ws.ev1);

@@ -126,4 +126,12 @@ struct Provider {
   void fill_block(const PackedPoints& rows, int64_t r0, int64_t nrows, float* out);
 };
 
+// Live provider handles.  Every C entry point turns a handle into a Provider
+// through checked_provider(), which rejects null, unknown and destroyed handles
+// without dereferencing them; creation registers a provider, destruction
+// unregisters it first.
+Provider* checked_provider(void* h);
+void register_provider(Provider* p);
+void unregister_provider(Provider* p);
+
 }  // namespace mgp

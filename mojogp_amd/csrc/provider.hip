@@ -3,6 +3,8 @@
 
 
 #include <algorithm>
+#include <mutex>
+#include <set>
 #include <cmath>
 
 namespace mgp {
@@ -235,6 +237,29 @@ void Provider::cross(const PackedPoints& rows, const float* V, int ncols,
     return;
   }
   fused_matvec(a, rows, train, V, out, ws, st);
+}
+
+namespace {
+std::mutex g_provider_mu;
+std::set<Provider*> g_providers;
+}  // namespace
+
+Provider* checked_provider(void* h) {
+  auto* p = static_cast<Provider*>(h);
+  std::lock_guard<std::mutex> lk(g_provider_mu);
+  MGP_REQUIRE(h != nullptr, "null provider handle");
+  MGP_REQUIRE(g_providers.count(p) != 0, "unknown or destroyed provider handle");
+  return p;
+}
+
+void register_provider(Provider* p) {
+  std::lock_guard<std::mutex> lk(g_provider_mu);
+  g_providers.insert(p);
+}
+
+void unregister_provider(Provider* p) {
+  std::lock_guard<std::mutex> lk(g_provider_mu);
+  g_providers.erase(p);
 }
 
 }  // namespace mgp
