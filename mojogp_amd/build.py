@@ -44,8 +44,9 @@ HIP_FLAGS = [
 ]
 
 
-# rocBLAS serves the fp64 feature GEMM of the pathwise prior samples.
-LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+# rocBLAS serves the fp64 feature GEMM of the pathwise prior samples; hiprtc
+# compiles the per-tree product kernels (tree_jit.hip) at run time.
+LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def _hipcc() -> str:

@@ -84,6 +84,12 @@ double tree_diag(const KernelTree& t, const float* params);
 
 #if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
 constexpr float kTreePi = 3.14159265358979323846f;
+// Every evaluator of a tree (the run-time compiled products of tree_jit.hip,
+// the chunk and pair evaluators below for fills, pivots and gradients) uses
+// the same arithmetic: exp as __expf, RQ's B^-alpha as exp2(-alpha log2 B),
+// the periodic sine as __sinf (v_sin_f32; absolute error ~2^-21 for arguments
+// within 256 revolutions), so the operator, the dense K and the gradients
+// agree to rounding.
 
 // Leaf value and the pair quantities its gradient needs.
 struct LeafEval {
@@ -143,12 +149,12 @@ __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
     float s = 0.0f;
     for (int q = 0; q < lf.ndim; ++q) {
       const int dq = t.dims[lf.dim_off + q];
-      const float sn = sinf(kTreePi * (xi[dq] - xj[dq]) / period);
+      const float sn = __sinf(kTreePi * (xi[dq] - xj[dq]) / period);
       s += lf.ard ? sn * sn / p[lf.p0 + q] : sn * sn;
     }
     if (!lf.ard) s /= p[lf.p0];
     e.r2 = s;
-    e.k = os * expf(fmaxf(-2.0f * s, -20.0f));
+    e.k = os * __expf(fmaxf(-2.0f * s, -20.0f));
     e.h = e.k;
     return e;
   }
@@ -164,30 +170,30 @@ __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
     const float alpha = p[lf.p0 + nls];
     const float os = p[lf.p0 + nls + 1];
     const float B = 1.0f + r2 / (2.0f * alpha);
-    const float Bm = powf(B, -alpha);
+    const float Bm = exp2f(-alpha * __log2f(B));
     e.k = os * Bm;
     e.h = os * Bm / B;
     return e;
   }
   const float os = p[lf.p0 + nls];
   if (lf.kind == KIND_RBF) {
-    e.k = os * expf(fmaxf(-0.5f * r2, -20.0f));
+    e.k = os * __expf(fmaxf(-0.5f * r2, -20.0f));
     e.h = e.k;
     return e;
   }
   const float r = sqrtf(fmaxf(r2 + 1e-20f, 1e-20f));
   if (lf.kind == KIND_MATERN12) {
-    const float ex = expf(fmaxf(-r, -20.0f));
+    const float ex = __expf(fmaxf(-r, -20.0f));
     e.k = os * ex;
     e.h = os * ex / r;
   } else if (lf.kind == KIND_MATERN32) {
     const float s3 = 1.7320508075688772f * r;
-    const float ex = expf(fmaxf(-s3, -20.0f));
+    const float ex = __expf(fmaxf(-s3, -20.0f));
     e.k = os * (1.0f + s3) * ex;
     e.h = 3.0f * os * ex;
   } else {  // Matern-5/2
     const float s5 = 2.2360679774997897f * r;
-    const float ex = expf(fmaxf(-s5, -20.0f));
+    const float ex = __expf(fmaxf(-s5, -20.0f));
     e.k = os * (1.0f + s5 + (5.0f / 3.0f) * r * r) * ex;
     e.h = (5.0f / 3.0f) * os * (1.0f + s5) * ex;
   }
@@ -217,7 +223,7 @@ __device__ __forceinline__ void tree_leaf_chunk(const KernelTree& t, int l,
       const float il = 1.0f / p[lf.p0 + (lf.ard ? q : 0)];
       const float a = xi[dq];
       for (int c = 0; c < kTreeChunk; ++c) {
-        const float sn = sinf((a - xc[c * w + dq]) * ip);
+        const float sn = __sinf((a - xc[c * w + dq]) * ip);
         s[c] = fmaf(sn * sn, il, s[c]);
       }
     }
@@ -364,7 +370,7 @@ __device__ __forceinline__ void tree_grad_accumulate(const KernelTree& t,
           const int dq = t.dims[lf.dim_off + q];
           const float dx = xi[dq] - xj[dq];
           const float ang = kTreePi * dx / period;
-          const float sn = sinf(ang), cs = cosf(ang);
+          const float sn = __sinf(ang), cs = __cosf(ang);
           const float lq = p[lf.p0 + (lf.ard ? q : 0)];
           if (lf.ard) g[lf.p0 + q] += a * e.k * 2.0f * sn * sn / (lq * lq);
           dperiod += sn * cs * dx / lq;

@@ -3,6 +3,7 @@
 // the Gram-form tile path serves single radial leaves).  Tree semantics and
 // reference citations are in kernel_tree.h.
 #include "tree.h"
+#include "tree_jit.h"
 
 #include <algorithm>
 #include <cmath>
@@ -20,64 +21,6 @@ static_assert(kTreeChunk % 4 == 0 && kTile % kTreeChunk == 0, "float4 chunk read
 
 void require(bool ok, const std::string& msg) {
   if (!ok) throw Error(ST_INVALID, msg);
-}
-
-// out[c][i] = sum_j K(r_i, c_j) V[c][j] (+ noise V[c][i] when square); one
-// thread per row, column points and right-hand sides staged in LDS.
-__global__ __launch_bounds__(256) void k_tree_matvec(
-    const float* __restrict__ Xr, int64_t m, const float* __restrict__ Xc, int64_t n,
-    KernelTree t, const float* __restrict__ p, const float* __restrict__ V, int ncols,
-    float* __restrict__ part) {
-  // LDS: column coordinates [kTile][d], then right-hand sides transposed
-  // [ncols][kTile] so one 16-byte read serves a chunk of four columns
-  extern __shared__ float sm[];
-  const int d = t.d;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  float* vt = sm + kTile * d;
-  float xi[kTreeMaxInputDim];
-  for (int k = 0; k < d; ++k) xi[k] = (i < m) ? Xr[i * d + k] : 0.0f;
-  double acc[kMaxCols];
-  for (int c = 0; c < kMaxCols; ++c) acc[c] = 0.0;
-  // column range of this split (whole tiles)
-  const int64_t tiles = (n + kTile - 1) / kTile;
-  const int64_t tps = (tiles + gridDim.y - 1) / gridDim.y;
-  const int64_t jbeg = (int64_t)blockIdx.y * tps * kTile;
-  const int64_t jend = min(n, jbeg + tps * kTile);
-  for (int64_t j0 = jbeg; j0 < jend; j0 += kTile) {
-    __syncthreads();
-    for (int q = threadIdx.x; q < kTile * d; q += blockDim.x) {
-      const int64_t j = j0 + q / d;
-      sm[q] = j < n ? Xc[j0 * d + q] : 0.0f;
-    }
-    for (int q = threadIdx.x; q < kTile * ncols; q += blockDim.x) {
-      const int c = q / kTile, jj = q - c * kTile;
-      const int64_t j = j0 + jj;
-      vt[q] = j < n ? V[(int64_t)c * n + j] : 0.0f;
-    }
-    __syncthreads();
-    // columns past n are zero in LDS (coordinates and right-hand sides), so
-    // whole chunks can run: their values multiply zeros
-    const int cnt = (int)min((int64_t)kTile, n - j0);
-    float part[kMaxCols];
-    for (int c = 0; c < kMaxCols; ++c) part[c] = 0.0f;
-    for (int jj = 0; jj < cnt; jj += kTreeChunk) {
-      float kv[kTreeChunk];
-      tree_value_chunk(t, p, xi, sm + jj * d, d, kv);
-      for (int c = 0; c < ncols; ++c) {
-        float s = part[c];
-        for (int h = 0; h < kTreeChunk; h += 4) {
-          const float4 vv = *reinterpret_cast<const float4*>(vt + c * kTile + jj + h);
-          s = fmaf(kv[h], vv.x, fmaf(kv[h + 1], vv.y, fmaf(kv[h + 2], vv.z, fmaf(kv[h + 3], vv.w, s))));
-        }
-        part[c] = s;
-      }
-    }
-    for (int c = 0; c < ncols; ++c) acc[c] += (double)part[c];
-  }
-  if (i < m) {
-    float* dst = part + (int64_t)blockIdx.y * ncols * m;
-    for (int c = 0; c < ncols; ++c) dst[(int64_t)c * m + i] = (float)acc[c];
-  }
 }
 
 // out[c][i] = sum_y part[y][c][i] (+ noise V[c][i]), splits summed in order.
@@ -374,10 +317,18 @@ void tree_matvec(const KernelTree& t, const float* p_dev, const float* Xr, int64
   for (int c0 = 0; c0 < ncols; c0 += kMaxCols) {
     const int nc = std::min(kMaxCols, ncols - c0);
     float* part = work.ensure((size_t)splits * nc * m);
-    const size_t shm = (size_t)kTile * (t.d + nc) * sizeof(float);
-    hipLaunchKernelGGL(k_tree_matvec, dim3((unsigned)rows, (unsigned)splits), dim3(256), shm, st,
-                       Xr, m, Xc, n, t, p_dev, V + (int64_t)c0 * n, nc, part);
-    MGP_HIP_CHECK(hipGetLastError());
+    // the tree's straight-line kernel (tree_jit.hip)
+    const TreeJitKernel jk = tree_jit_kernel(t, nc);
+    const int64_t rblocks = ceil_div(m, jk.rows_per_block);
+    {
+      const float* vc = V + (int64_t)c0 * n;
+      long long mm = m, nn = n;
+      int ncc = nc;
+      void* args[] = {(void*)&Xr, &mm, (void*)&Xc, &nn, (void*)&p_dev, (void*)&vc, &ncc,
+                      (void*)&part};
+      MGP_HIP_CHECK(hipModuleLaunchKernel(jk.fn, (unsigned)rblocks, (unsigned)splits, 1, 256, 1, 1,
+                                          (unsigned)jk.lds_bytes, st, args, nullptr));
+    }
     hipLaunchKernelGGL(k_tree_reduce, dim3((unsigned)ceil_div(m * nc, 256)), dim3(256), 0, st,
                        part, splits, m, nc, V + (int64_t)c0 * n, noise, square ? 1 : 0,
                        out + (int64_t)c0 * m);

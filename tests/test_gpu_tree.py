@@ -65,10 +65,15 @@ def test_tree_products_match_oracle(name):
     ref = ok.forward_matvec(T, X, V, params, 0.2, False)
     refc = ok.cross_matvec(T, Xs, X, V, params, False)
     print(f"  forward {_rel(fwd, ref):.2e} cross {_rel(cr, refc):.2e} "
-          f"materialized {_rel(mat, ref):.2e}", flush=True)
+          f"materialized {_rel(mat, ref):.2e} matrix-free vs materialized "
+          f"{_rel(fwd, mat):.2e}", flush=True)
     assert _rel(fwd, ref) <= 1e-5
     assert _rel(cr, refc) <= 1e-5
     assert _rel(mat, ref) <= 1e-5
+    # the compiled product and the dense fill evaluate the same arithmetic
+    # (data spread over 3-6 lengthscales): they differ by the product
+    # rounding only (fp32 / fp16-split MFMA sums)
+    assert _rel(fwd, mat) <= 5e-6
 
 
 @pytest.mark.parametrize("name", ["rbf+m52", "rq_ard+per[1]"])
