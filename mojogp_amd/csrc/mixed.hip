@@ -355,7 +355,7 @@ MixedTrainResult train_mixed(Provider& pv, const float* y_host,
                            dim3(256), 0, st, rf + n, work.probes.ptr, (int64_t)o.num_probes * n);
       MGP_HIP_CHECK(hipGetLastError());
       tree_cat_grad_tables(pv.tree, pv.tparams.ptr, pv.train.z.ptr, n, work.lf.ptr, rf, C,
-                           G.data(), st);
+                           G.data(), pv.tree_gws, st);
       std::vector<float> gc((size_t)KC), chain_f((size_t)KC);
       for (const auto& c : cl) {
         th.resize((size_t)c.nparam);

@@ -45,6 +45,9 @@ struct Provider {
   // (tree.table_size entries, placed after the parameters in tparams).
   std::vector<float> cat_tables;
   DevBuf<float> tree_ws;  // column-split partial products of the tree matvec
+  // block partials of the tree gradient / table traces (scratch, so usable
+  // through a const provider)
+  mutable DevBuf<double> tree_gws;
 
   hipStream_t st = nullptr;
   int device = 0;              // HIP device current when the provider was created

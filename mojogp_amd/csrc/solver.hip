@@ -1632,7 +1632,8 @@ void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const fl
 void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int ncols,
                      double* g_host, hipStream_t st) {
   if (pv.is_tree) {
-    tree_grad_traces(pv.tree, pv.tparams.ptr, pv.train.z.ptr, pv.n, Lf, Rf, ncols, g_host, st);
+    tree_grad_traces(pv.tree, pv.tparams.ptr, pv.train.z.ptr, pv.n, Lf, Rf, ncols, g_host,
+                     pv.tree_gws, st);
     return;
   }
   const int d = pv.d;

@@ -18,12 +18,13 @@ void tree_fill(const KernelTree& t, const float* p_dev, const float* Xr, int64_t
                int64_t rows, const float* Xc, int64_t n, float* out, hipStream_t st);
 // G[e] = sum_{a,b} dK_ab/dR_l[level_a][level_b] sum_c Lf[c][a] Rf[c][b] for every
 // categorical table entry e (fp64, host, G[table_size]).
+// work: device partials (grown on demand, owned by the caller).
 void tree_cat_grad_tables(const KernelTree& t, const float* p_dev, const float* X, int64_t n,
                           const float* Lf, const float* Rf, int ncols, double* G_host,
-                          hipStream_t st);
+                          DevBuf<double>& work, hipStream_t st);
 // g[q] = sum_{a,b} dK_ab/dtheta_q sum_c Lf[c][a] Rf[c][b] (fp64, host).
 void tree_grad_traces(const KernelTree& t, const float* p_dev, const float* X, int64_t n,
                       const float* Lf, const float* Rf, int ncols, double* g_host,
-                      hipStream_t st);
+                      DevBuf<double>& work, hipStream_t st);
 
 }  // namespace mgp

@@ -353,53 +353,63 @@ void tree_fill(const KernelTree& t, const float* p_dev, const float* Xr, int64_t
   MGP_HIP_CHECK(hipGetLastError());
 }
 
+namespace {
+// acc[q] (+)= sum_b part[b * Q + q] for q < Q: one wave per q, lane l sums
+// b = l, l + 64, .. in order, then a butterfly of shuffles (fixed order).
+__global__ void k_tree_part_sum(const double* __restrict__ part, int64_t nblk, int Q,
+                                int accumulate, double* __restrict__ acc) {
+  const int q = blockIdx.x, lane = threadIdx.x;
+  double s = 0.0;
+  for (int64_t b = lane; b < nblk; b += 64) s += part[b * Q + q];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) acc[q] = accumulate ? acc[q] + s : s;
+}
+
+int64_t grad_splits(int64_t n) {
+  const int64_t rows = ceil_div(n, 256);
+  return std::max<int64_t>(1, std::min<int64_t>(ceil_div(2048, rows), ceil_div(n, 1024)));
+}
+}  // namespace
+
 void tree_cat_grad_tables(const KernelTree& t, const float* p_dev, const float* X, int64_t n,
                           const float* Lf, const float* Rf, int ncols, double* G_host,
-                          hipStream_t st) {
+                          DevBuf<double>& work, hipStream_t st) {
   const int S = t.table_size;
   for (int e = 0; e < S; ++e) G_host[e] = 0.0;
   if (S == 0) return;
-  const int64_t rows = ceil_div(n, 256);
-  const int splits = (int)std::max<int64_t>(
-      1, std::min<int64_t>(ceil_div(2048, rows), ceil_div(n, 1024)));
-  const int64_t nblk = rows * splits;
-  DevBuf<double> part;
-  part.ensure((size_t)nblk * S);
-  std::vector<double> hp((size_t)nblk * S);
+  const int64_t rows = ceil_div(n, 256), splits = grad_splits(n), nblk = rows * splits;
+  double* part = work.ensure((size_t)nblk * S + S);
+  double* acc = part + (size_t)nblk * S;
   for (int c0 = 0; c0 < ncols; c0 += kGradCols) {
     hipLaunchKernelGGL(k_tree_cat_grad, dim3((unsigned)rows, (unsigned)splits), dim3(256), 0, st,
-                       X, n, t, p_dev, Lf, Rf, ncols, c0, part.ptr);
+                       X, n, t, p_dev, Lf, Rf, ncols, c0, part);
+    hipLaunchKernelGGL(k_tree_part_sum, dim3((unsigned)S), dim3(64), 0, st, part, nblk, S,
+                       c0 > 0 ? 1 : 0, acc);
     MGP_HIP_CHECK(hipGetLastError());
-    MGP_HIP_CHECK(hipMemcpyAsync(hp.data(), part.ptr, hp.size() * sizeof(double),
-                                 hipMemcpyDeviceToHost, st));
-    MGP_HIP_CHECK(hipStreamSynchronize(st));
-    for (int64_t b = 0; b < nblk; ++b)
-      for (int e = 0; e < S; ++e) G_host[e] += hp[(size_t)b * S + e];
   }
+  MGP_HIP_CHECK(hipMemcpyAsync(G_host, acc, (size_t)S * sizeof(double), hipMemcpyDeviceToHost,
+                               st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
 }
 
 void tree_grad_traces(const KernelTree& t, const float* p_dev, const float* X, int64_t n,
                       const float* Lf, const float* Rf, int ncols, double* g_host,
-                      hipStream_t st) {
+                      DevBuf<double>& work, hipStream_t st) {
   const int P = t.nparams;
-  const int64_t rows = ceil_div(n, 256);
-  const int splits = (int)std::max<int64_t>(
-      1, std::min<int64_t>(ceil_div(2048, rows), ceil_div(n, 1024)));
-  const int64_t nblk = rows * splits;
-  DevBuf<double> part;
-  part.ensure((size_t)nblk * P);
-  std::vector<double> acc((size_t)P, 0.0), hp((size_t)nblk * P);
+  const int64_t rows = ceil_div(n, 256), splits = grad_splits(n), nblk = rows * splits;
+  double* part = work.ensure((size_t)nblk * P + P);
+  double* acc = part + (size_t)nblk * P;
   for (int c0 = 0; c0 < ncols; c0 += kGradCols) {
     hipLaunchKernelGGL(k_tree_grad_trace, dim3((unsigned)rows, (unsigned)splits), dim3(256), 0,
-                       st, X, n, t, p_dev, Lf, Rf, ncols, c0, part.ptr);
+                       st, X, n, t, p_dev, Lf, Rf, ncols, c0, part);
+    hipLaunchKernelGGL(k_tree_part_sum, dim3((unsigned)P), dim3(64), 0, st, part, nblk, P,
+                       c0 > 0 ? 1 : 0, acc);
     MGP_HIP_CHECK(hipGetLastError());
-    MGP_HIP_CHECK(hipMemcpyAsync(hp.data(), part.ptr, hp.size() * sizeof(double),
-                                 hipMemcpyDeviceToHost, st));
-    MGP_HIP_CHECK(hipStreamSynchronize(st));
-    for (int64_t b = 0; b < nblk; ++b)
-      for (int q = 0; q < P; ++q) acc[(size_t)q] += hp[(size_t)b * P + q];
   }
-  for (int q = 0; q < P; ++q) g_host[q] = acc[(size_t)q];
+  MGP_HIP_CHECK(hipMemcpyAsync(g_host, acc, (size_t)P * sizeof(double), hipMemcpyDeviceToHost,
+                               st));
+  MGP_HIP_CHECK(hipStreamSynchronize(st));
 }
 
 }  // namespace mgp

@@ -695,7 +695,8 @@ class MultiOutputLMCGP:
         return gp
 
     def __repr__(self) -> str:
-        kinds = ", ".join(k.kernel_type.name.lower() for k in self._original_kernels)
+        kinds = ", ".join(k.kernel_type.name.lower() if k.kernel_type is not None else repr(k)
+                          for k in self._original_kernels)
         return (f"MultiOutputLMCGP(kernels=[{kinds}], num_latents={self.num_latents}, "
                 f"trained={self._is_trained})")
 

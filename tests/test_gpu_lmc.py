@@ -448,3 +448,33 @@ def test_lmc_train_with_tree_latent():
     np.testing.assert_allclose(hist, ref["nll_history"], rtol=0, atol=1e-4)
     assert _rel(out_p, np.concatenate(ref["params"])) <= 1e-3
     assert _rel(nz, ref["noise"]) <= 1e-3
+
+
+def test_lmc_tree_latent_python_path(tmp_path):
+    """MultiOutputLMCGP with a composite latent through the Python surface: fit
+    (matrix-free), mean / LOVE predict, the model file (kernel_types -1 for
+    the tree latent, its tree in the config) and predictions after reload."""
+    from mojogp_amd import Matern52, MultiOutputLMCGP, RBF
+    rng = np.random.default_rng(61)
+    n, d, T = 300, 2, 2
+    X = rng.uniform(0, 1, size=(n, d)).astype(np.float32)
+    Y = np.stack([np.sin(5 * X[:, 0]), np.cos(3 * X[:, 1])], 1) + 0.05 * rng.normal(size=(n, T))
+    Y = Y.astype(np.float32)
+    Xs = rng.uniform(0, 1, size=(40, d)).astype(np.float32)
+    print("lmc python path with a tree latent", flush=True)
+    gp = MultiOutputLMCGP([RBF(), RBF(active_dims=[0]) + Matern52(active_dims=[1])])
+    tr = gp.fit(X, Y, max_iterations=6, method="matrix_free")
+    assert np.all(np.isfinite(tr.nll_history))
+    assert list(tr.kernel_types) == [0, -1]
+    mean, var = gp.predict(Xs, return_var=True)
+    assert mean.shape == (40, T) and np.all(np.isfinite(mean)) and np.all(var > 0)
+    assert "MultiOutputLMCGP" in repr(gp)
+    path = str(tmp_path / "lmc_tree")
+    gp.save(path)
+    g2 = MultiOutputLMCGP.load(path)
+    assert g2.kernels[1].kernel_type is None  # the tree comes back from the config
+    mean2, var2 = g2.predict(Xs, return_var=True)
+    print(f"  reload: mean {np.max(np.abs(mean2 - mean)):.2e} var "
+          f"{np.max(np.abs(var2 - var)):.2e}", flush=True)
+    np.testing.assert_allclose(mean2, mean, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(var2, var, rtol=1e-5, atol=1e-7)
