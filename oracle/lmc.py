@@ -188,7 +188,8 @@ def bbmm(kinds, ards, X, params_list, A, noise, y_c, *, fixed=None, num_probes=1
         ng[t] = 0.5 * v / N
     return {"nll": nll, "inv_quad": inv_quad, "logdet": logdet, "kernel_grads": np.array(kgrads),
             "G_A": G_A, "noise_grads": ng, "alpha": alpha, "cg_iterations": iters,
-            "precond_logdet": P.logdet if P is not None else 0.0, "x": x}
+            "precond_logdet": P.logdet if P is not None else 0.0, "x": x,
+            "U": U, "Zn": Zn}
 
 
 # ---------------------------------------------------------------- training
@@ -374,6 +375,255 @@ def train(kinds, ards, X, Y_blocked, init_params, init_noise, init_mean, *, trai
     return {"params": out_params, "noise": np.array([sp(v) for v in bnoise], F32),
             "mean": bmean, "A": A, "L": L, "var_diag": vdiag, "alpha": best_alpha,
             "nll_history": np.array(hist), "final_nll": float(best_nll) if best_nll < 1e29 else 0.0,
+            "iterations": iterations, "converged": converged}
+
+
+def cat_gradients(tree_s, X, params_s, A_s, cat_specs, raw_cat, ev, clip=10.0):
+    """Categorical raw-parameter gradients of one mixed latent
+    (jit_lmc_mixed.mojo:1259-1327): for each constrained parameter theta_k of a
+    categorical leaf, dK = A_s (x) (dK_s/dR o dR/dtheta_k) and
+        g_k = clip((-0.5 alpha^T dK alpha + (0.5/P) sum_j u_j^T dK zn_j) / N)
+    with the probe solutions u_j (scaled by their probe norms) and the
+    unit-norm probes zn_j of the evaluation, times the transform's chain
+    derivative.  Returns the raw gradients (float32, concatenated over the
+    leaves)."""
+    from . import categorical as oc
+    D, lv = tree_s.cat_leaf_derivatives(X, X, np.asarray(params_s, np.float64))
+    alpha, U, Zn = ev["alpha"], ev["U"], ev["Zn"]
+    N = alpha.shape[0]
+    Pn = U.shape[1]
+    A_s = np.asarray(A_s, np.float64)
+    out = []
+    off = 0
+    for i, (kind, L) in enumerate(cat_specs):
+        K = oc.num_params(kind, L)
+        rc = np.asarray(raw_cat[off:off + K], F32)
+        th = oc.constrain(kind, L, rc)
+        dR = oc.correlation_gradients(kind, L, th)
+        chain = oc.chain_derivative(kind, L, rc)
+        li, lj = lv[i]
+        for k in range(K):
+            dK = np.kron(A_s, D[i] * dR[k][li[:, None], lj[None, :]])
+            val = -0.5 * alpha @ dK @ alpha
+            if Pn > 0:
+                val += 0.5 / Pn * np.sum(U * (dK @ Zn))
+            g = F32(val / N)
+            g = F32(clip) if g > clip else (F32(-clip) if g < -clip else g)
+            out.append(F32(g * F32(chain[k])))
+        off += K
+    return np.array(out, F32)
+
+
+def train_mixed(nodes, X, Y_blocked, init_params, init_noise, init_mean, cat_specs,
+                init_cat_raw, *, max_iterations=100, learning_rate=0.05, num_probes=10,
+                max_cg=200, max_tridiag=30, cg_tol=1.0, precond_rank=15, precond_method=0,
+                rebuild_threshold=0.5, early_stop_tol=1e-4, early_stop_patience=15,
+                evaluate=None):
+    """train_lmc_mixed_jit restated (jit_lmc_mixed.mojo:684-1557): the LMC
+    parametrisation and Adam of ``train`` plus per-latent categorical raw
+    parameters with their own Adam moments (same step count), and this
+    loop's own rules: NaN ends the run, the best-NLL evaluation is the only
+    snapshot, after iteration 20 every evaluation not below the best NLL
+    (the improving one included, whose counter was just reset) counts toward
+    the patience, and the preconditioner rebuild also watches the constrained
+    categorical parameters.  nodes: per latent a radial kind code or a kernel
+    tree dict; cat_specs[s]: (categorical kind, levels) of latent s's
+    categorical leaves in tree order (empty for others); init_cat_raw[s]:
+    their raw parameters.  Float32 host scalars as the reference.
+
+    Test hook: ``evaluate(it, trees, params, A, noise, y_c, cat_raw)``
+    replaces the BBMM evaluation (dict as ``bbmm`` returns, with ``cat_grads``
+    per latent replacing the categorical gradient computation; cat_raw: the
+    current raw categorical parameters per latent)."""
+    from . import categorical as oc
+    sp, isp, dsp = oe._softplus, oe._inv_softplus, oe._softplus_deriv
+    X = np.asarray(X, np.float64)
+    n, d = X.shape
+    T = len(init_noise)
+    R = len(nodes)
+    Y = np.asarray(Y_blocked, F32).reshape(T, n)
+    raw = [np.array([isp(v) for v in p], F32) for p in init_params]
+    rcat = [np.asarray(c, F32).copy() for c in init_cat_raw]
+    raw_noise = np.array([isp(v) for v in init_noise], F32)
+    raw_mean = np.asarray(init_mean, F32).copy()
+    init_diag = F32(np.sqrt(F32(1.0) / F32(R)))
+    Lall = np.zeros((R, T, T), F32)
+    raw_Ld = np.zeros((R, T), F32)
+    for s in range(R):
+        for i in range(T):
+            for j in range(i):
+                Lall[s, i, j] = F32(0.01) * F32(s + 1) / F32(R)
+            Lall[s, i, i] = init_diag
+            raw_Ld[s, i] = isp(init_diag)
+    raw_vd = np.full((R, T), isp(F32(0.1)), F32)
+    nkp = sum(len(p) for p in init_params)
+    total = nkp + T + R * T * T + R * T + T
+    madam, vadam = np.zeros(total, F32), np.zeros(total, F32)
+    mcat = [np.zeros(len(c), F32) for c in rcat]
+    vcat = [np.zeros(len(c), F32) for c in rcat]
+    b1, b2, eps, lr = F32(0.9), F32(0.999), F32(1e-8), F32(learning_rate)
+    t_step = 0
+
+    def clip(g):
+        g = F32(g)
+        return F32(10.0) if g > 10 else (F32(-10.0) if g < -10 else g)
+
+    def adam(mm, vv, idx, g):
+        m = b1 * mm[idx] + (F32(1) - b1) * F32(g)
+        v = b2 * vv[idx] + (F32(1) - b2) * F32(g) * F32(g)
+        mm[idx], vv[idx] = m, v
+        mh = m / (F32(1) - F32(b1 ** t_step))
+        vh = v / (F32(1) - F32(b2 ** t_step))
+        return F32(-lr * mh / (np.sqrt(vh) + eps))
+
+    def constrained_cat(s):
+        out, off = [], 0
+        for kind, L in cat_specs[s]:
+            K = oc.num_params(kind, L)
+            out.append(oc.constrain(kind, L, rcat[s][off:off + K]))
+            off += K
+        return np.concatenate(out).astype(F32) if out else np.zeros(0, F32)
+
+    def trees():
+        out = []
+        for s in range(R):
+            if isinstance(nodes[s], dict):
+                tabs, off = [], 0
+                for kind, L in cat_specs[s]:
+                    K = oc.num_params(kind, L)
+                    tabs.append(oc.correlation(kind, L, oc.constrain(kind, L,
+                                                                  rcat[s][off:off + K])))
+                    off += K
+                out.append(ok.TreeKernel(nodes[s], d, tabs or None))
+            else:
+                out.append(nodes[s])
+        return out
+
+    def a_all():
+        A = np.zeros((R, T, T), F32)
+        for s in range(R):
+            vd = np.array([sp(v) for v in raw_vd[s]], F32)
+            for i in range(T):
+                Lall[s, i, i] = sp(raw_Ld[s, i])
+            A[s] = _a_from_l(Lall[s].astype(np.float64), vd).astype(F32)
+            try:
+                np.linalg.cholesky(A[s].astype(np.float64))
+            except np.linalg.LinAlgError:
+                A[s] += F32(1e-4) * np.eye(T, dtype=F32)
+        return A
+
+    ards = [False] * R
+    last_p = [np.asarray(p, F32).copy() for p in init_params]
+    last_cat = [constrained_cat(s) for s in range(R)]
+    last_A = a_all()
+    last_noise = np.asarray(init_noise, F32).copy()
+
+    def build(tr, params, A, noise):
+        if precond_rank <= 0 or evaluate is not None:
+            return None
+        return Precond(latent_kernels(tr, ards, X, params), A,
+                       precond_noise(noise, None, n), precond_rank, precond_method)
+
+    P = build(trees(), last_p, last_A, last_noise)
+    snap = lambda: ([r.copy() for r in raw], [c.copy() for c in rcat], raw_noise.copy(),  # noqa: E731
+                    raw_mean.copy(), Lall.copy(), raw_Ld.copy(), raw_vd.copy())
+    best = snap()
+    best_nll = F32(1e30)
+    best_alpha = np.zeros(n * T)
+    patience, converged, iterations = 0, False, 0
+    hist = []
+    for it in range(max_iterations):
+        iterations = it + 1
+        t_step += 1
+        params = [np.array([sp(v) for v in r], F32) for r in raw]
+        tr = trees()
+        noise = np.array([sp(v) for v in raw_noise], F32)
+        yc = (Y - raw_mean[:, None]).reshape(-1)
+        A = a_all()
+        rel = lambda a, b: float(np.max(np.abs(np.asarray(b, F32) - np.asarray(a, F32))  # noqa: E731
+                                        / (np.abs(np.asarray(a, F32)) + F32(1e-8)))) if len(a) else 0.0
+        rebuild = (max(rel(last_p[s], params[s]) for s in range(R)) > rebuild_threshold
+                   or max(rel(last_cat[s], constrained_cat(s)) for s in range(R)) > rebuild_threshold
+                   or rel(last_A.ravel(), A.ravel()) > rebuild_threshold
+                   or rel(last_noise, noise) > rebuild_threshold)
+        if rebuild:
+            P = build(tr, params, A, noise)
+            last_p = [p.copy() for p in params]
+            last_cat = [constrained_cat(s) for s in range(R)]
+            last_A, last_noise = A.copy(), noise.copy()
+        if evaluate is not None:
+            ev = evaluate(it, tr, params, A, noise, yc, [c.copy() for c in rcat])
+        else:
+            ev = bbmm(tr, ards, X, params, A, noise, yc, num_probes=num_probes, max_cg=max_cg,
+                      max_tridiag=max_tridiag, tol=cg_tol, iteration=it, P=P)
+        nll = F32(ev["nll"])
+        hist.append(float(nll))
+        if np.isnan(nll):
+            break
+        if nll < best_nll:
+            best_nll = nll
+            patience = 0
+            best = snap()
+            best_alpha = np.asarray(ev["alpha"]).copy()
+        for s in range(R):  # categorical parameters
+            if len(rcat[s]) == 0:
+                continue
+            g = (ev["cat_grads"][s] if "cat_grads" in ev
+                 else cat_gradients(tr[s], X, params[s], A[s], cat_specs[s], rcat[s], ev))
+            for k in range(len(rcat[s])):
+                rcat[s][k] += adam(mcat[s], vcat[s], k, g[k])
+        ai = 0
+        off = 0
+        for s in range(R):
+            for p in range(len(raw[s])):
+                g = clip(ev["kernel_grads"][off + p]) * dsp(raw[s][p])
+                raw[s][p] += adam(madam, vadam, ai, g)
+                ai += 1
+            off += len(raw[s])
+        for t in range(T):
+            raw_noise[t] += adam(madam, vadam, ai, clip(ev["noise_grads"][t]) * dsp(raw_noise[t]))
+            ai += 1
+        G = np.asarray(ev["G_A"], F32)
+        for s in range(R):
+            for i in range(T):
+                for j in range(i + 1):
+                    g = F32(0.0)
+                    for b in range(T):
+                        g += G[s, i, b] * Lall[s, b, j]
+                    g = clip(F32(2.0) * g)
+                    if i == j:
+                        raw_Ld[s, i] += adam(madam, vadam, ai, g * dsp(raw_Ld[s, i]))
+                    else:
+                        Lall[s, i, j] += adam(madam, vadam, ai, g)
+                    ai += 1
+                ai += T - 1 - i
+        for s in range(R):
+            for i in range(T):
+                raw_vd[s, i] += adam(madam, vadam, ai, clip(G[s, i, i]) * dsp(raw_vd[s, i]))
+                ai += 1
+        al = np.asarray(ev["alpha"]).reshape(T, n)
+        for t in range(T):
+            g = clip(F32(-np.sum(al[t].astype(F32), dtype=F32)) / F32(n * T))
+            raw_mean[t] += adam(madam, vadam, ai, g)
+            ai += 1
+        if nll >= best_nll and it > 20 and early_stop_tol > 0:
+            patience += 1
+            if patience >= early_stop_patience:
+                converged = True
+                break
+    braw, bcat, bnoise, bmean, bL, bLd, bvd = best
+    L = bL.copy()
+    vdiag = np.zeros((R, T), F32)
+    A = np.zeros((R, T, T), F32)
+    for s in range(R):
+        for i in range(T):
+            L[s, i, i] = sp(bLd[s, i])
+            vdiag[s, i] = sp(bvd[s, i])
+        A[s] = _a_from_l(L[s].astype(np.float64), vdiag[s]).astype(F32)
+    return {"params": [np.array([sp(v) for v in r], F32) for r in braw], "cat_raw": bcat,
+            "noise": np.array([sp(v) for v in bnoise], F32), "mean": bmean, "A": A, "L": L,
+            "var_diag": vdiag, "alpha": best_alpha, "nll_history": np.array(hist),
+            "final_nll": float(best_nll) if best_nll < 1e29 else 0.0,
             "iterations": iterations, "converged": converged}
 
 
