@@ -437,6 +437,31 @@ MGP_API int mgp_lmc_train(void* const* providers, int R, int T,
                           const mgp_lmc_train_opts_t* opts,
                           mgp_lmc_train_result_t* out);
 
+/* Mixed continuous x categorical LMC: mgp_lmc_train plus the raw correlation
+ * parameters of the categorical leaves of each kernel-tree latent, trained by
+ * their own Adam moments on (-0.5 alpha^T dK alpha + (0.5/P) sum_j
+ * u_j^T dK zn_j) / (nT) with dK = A_s (x) dK_s (every parameter trained, no
+ * masks).  cat_counts[R]: categorical leaves per latent; cat_kinds: their
+ * kinds (0 GD, 1 CR, 2 EHH, 3 HH, 4 FE) in tree order, concatenated over the
+ * latents; init_cat_raw[ncat_params]: their raw parameters in the same order.
+ * Outputs (either may be NULL): cat_raw_out[ncat_params] the best raw values,
+ * cat_params_out[ncat_params] their constrained values (the reference's
+ * cat_params_per_latent).  The loop stops at the first NaN NLL, keeps the
+ * best-NLL state only, counts after iteration 20 every evaluation not below
+ * the best toward the patience, and rebuilds the preconditioner when a kernel
+ * parameter, a constrained categorical parameter, an entry of A_s or a task
+ * noise moved by more than the threshold.  Replaces train_lmc_mixed()
+ * (train_lmc_mixed_python, jit_engine_lmc_bindings.mojo:54-360 ->
+ * train_lmc_mixed_jit, kernels/jit/jit_lmc_mixed.mojo:684-1557). */
+MGP_API int mgp_lmc_train_mixed(void* const* providers, int R, int T,
+                                const float* y_blocked, const float* init_params,
+                                const float* init_noise, const float* fixed_noise,
+                                const float* init_mean, const int* cat_counts,
+                                const int* cat_kinds, const float* init_cat_raw,
+                                int ncat_params, const mgp_lmc_train_opts_t* opts,
+                                mgp_lmc_train_result_t* out, float* cat_raw_out,
+                                float* cat_params_out);
+
 /* One BBMM evaluation of the LMC marginal likelihood at fixed A / noise /
  * kernel parameters (y_c: task-blocked, mean removed): NLL per joint entry,
  * y^T K^-1 y, log|K|, kernel gradients [sum_s P_s], dNLL/dA [R][T][T],

@@ -214,6 +214,10 @@ _SIGNATURES = {
     "mgp_lmc_train": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p, c_int_p,
                                 c_float_p, c_float_p, c_float_p, C.POINTER(LMCTrainOpts),
                                 C.POINTER(LMCTrainResult)]),
+    "mgp_lmc_train_mixed": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p,
+                                      c_float_p, c_float_p, c_float_p, c_int_p, c_int_p,
+                                      c_float_p, C.c_int, C.POINTER(LMCTrainOpts),
+                                      C.POINTER(LMCTrainResult), c_float_p, c_float_p]),
     "mgp_lmc_bbmm_eval": (C.c_int, [c_void_pp, C.c_int, C.c_int, c_float_p, c_float_p,
                                     c_float_p, c_float_p, C.c_int, C.c_int, C.c_int, C.c_float,
                                     C.c_int, C.c_int, C.c_int, c_float_p, c_float_p, c_float_p,

@@ -5,6 +5,7 @@
 #include <string>
 
 #include "lmc.h"
+#include "mixed.h"
 #include "mojogp_amd.h"
 
 using namespace mgp;
@@ -37,6 +38,51 @@ void set_mixing(LMCModel& m, const float* A, const float* noise) {
   for (int t = 0; t < m.T; ++t)
     if (!std::isfinite(m.noise[t]) || m.noise[t] < 0.0f)
       throw Error(ST_INVALID, "task noise must be finite and >= 0");
+}
+
+LMCTrainOptions train_options(const mgp_lmc_train_opts_t* opts) {
+  LMCTrainOptions o;
+  o.max_iterations = opts->max_iterations;
+  o.learning_rate = opts->learning_rate;
+  o.num_probes = opts->num_probes;
+  o.max_cg_iter = opts->max_cg_iter;
+  o.max_tridiag_iter = opts->max_tridiag_iter;
+  o.cg_tol = opts->cg_tol;
+  o.precond_rank = opts->precond_rank;
+  o.precond_method = opts->precond_method;
+  o.precond_rebuild_threshold = opts->precond_rebuild_threshold;
+  o.early_stop_tol = opts->early_stop_tol;
+  o.early_stop_patience = opts->early_stop_patience;
+  return o;
+}
+
+void put_result(const LMCTrainResult& r, const mgp_lmc_train_opts_t* opts,
+                mgp_lmc_train_result_t* out) {
+  auto put = [](float* dst, const std::vector<float>& v) {
+    if (dst && !v.empty()) std::memcpy(dst, v.data(), v.size() * sizeof(float));
+  };
+  if (out->params) {
+    size_t q = 0;
+    for (const auto& ps : r.params)
+      for (float v : ps) out->params[q++] = v;
+  }
+  put(out->A, r.A);
+  put(out->L, r.L);
+  put(out->var_diag, r.var_diag);
+  put(out->noise, r.noise);
+  put(out->mean, r.mean);
+  put(out->alpha, r.alpha);
+  const int hl = (int)std::min<size_t>(r.nll_history.size(), (size_t)opts->max_iterations);
+  if (out->nll_history)
+    for (int i = 0; i < hl; ++i) out->nll_history[i] = r.nll_history[i];
+  if (out->iter_times_ms)
+    for (int i = 0; i < (int)std::min<size_t>(r.iter_times_ms.size(), (size_t)opts->max_iterations); ++i)
+      out->iter_times_ms[i] = r.iter_times_ms[i];
+  out->history_len = hl;
+  out->final_nll = r.final_nll;
+  out->iterations = r.iterations;
+  out->converged = r.converged ? 1 : 0;
+  out->precond_rebuild_count = r.precond_rebuild_count;
 }
 
 }  // namespace
@@ -84,45 +130,69 @@ int mgp_lmc_train(void* const* providers, int R, int T, const float* y_blocked,
       for (int q = 0; q < P; ++q) tm[s].push_back(trainable[off + q] ? 1 : 0);
       off += P;
     }
-    LMCTrainOptions o;
-    o.max_iterations = opts->max_iterations;
-    o.learning_rate = opts->learning_rate;
-    o.num_probes = opts->num_probes;
-    o.max_cg_iter = opts->max_cg_iter;
-    o.max_tridiag_iter = opts->max_tridiag_iter;
-    o.cg_tol = opts->cg_tol;
-    o.precond_rank = opts->precond_rank;
-    o.precond_method = opts->precond_method;
-    o.precond_rebuild_threshold = opts->precond_rebuild_threshold;
-    o.early_stop_tol = opts->early_stop_tol;
-    o.early_stop_patience = opts->early_stop_patience;
+    const LMCTrainOptions o = train_options(opts);
     std::vector<float> noise(init_noise, init_noise + T), mean(init_mean, init_mean + T);
     LMCTrainResult r = lmc_train(m, y_blocked, ip, tm, noise, mean, o);
-    auto put = [](float* dst, const std::vector<float>& v) {
-      if (dst && !v.empty()) std::memcpy(dst, v.data(), v.size() * sizeof(float));
-    };
-    if (out->params) {
-      size_t q = 0;
-      for (const auto& ps : r.params)
-        for (float v : ps) out->params[q++] = v;
+    put_result(r, opts, out);
+  });
+}
+
+int mgp_lmc_train_mixed(void* const* providers, int R, int T, const float* y_blocked,
+                        const float* init_params, const float* init_noise,
+                        const float* fixed_noise, const float* init_mean, const int* cat_counts,
+                        const int* cat_kinds, const float* init_cat_raw, int ncat_params,
+                        const mgp_lmc_train_opts_t* opts, mgp_lmc_train_result_t* out,
+                        float* cat_raw_out, float* cat_params_out) {
+  return guarded([&] {
+    LMCModel m;
+    init_model(m, providers, R, T);
+    set_fixed(m, fixed_noise);
+    if (!y_blocked || !init_params || !init_noise || !init_mean || !cat_counts || !opts || !out)
+      throw Error(ST_INVALID, "null argument");
+    if (ncat_params < 0 || (ncat_params > 0 && !init_cat_raw))
+      throw Error(ST_INVALID, "init_cat_raw must hold ncat_params values");
+    std::vector<std::vector<float>> ip(R), craw(R);
+    std::vector<std::vector<int>> ck(R);
+    std::vector<std::vector<CatLeafRef>> leaves(R);
+    int off = 0, koff = 0, roff = 0;
+    for (int s = 0; s < R; ++s) {
+      Provider& pv = *m.prov[s];
+      ip[s].assign(init_params + off, init_params + off + pv.nparams);
+      off += pv.nparams;
+      const int cc = cat_counts[s];
+      if (cc < 0) throw Error(ST_INVALID, "cat_counts must be >= 0");
+      if (cc == 0) continue;
+      if (!cat_kinds) throw Error(ST_INVALID, "cat_kinds is required with categorical leaves");
+      if (!pv.is_tree) throw Error(ST_INVALID, "categorical leaves need a kernel-tree latent");
+      ck[s].assign(cat_kinds + koff, cat_kinds + koff + cc);
+      koff += cc;
+      leaves[s] = cat_leaves(pv, ck[s]);
+      int K = 0;
+      for (const auto& c : leaves[s]) K += c.nparam;
+      if (roff + K > ncat_params)
+        throw Error(ST_INVALID, "ncat_params is smaller than the categorical leaves need");
+      craw[s].assign(init_cat_raw + roff, init_cat_raw + roff + K);
+      roff += K;
     }
-    put(out->A, r.A);
-    put(out->L, r.L);
-    put(out->var_diag, r.var_diag);
-    put(out->noise, r.noise);
-    put(out->mean, r.mean);
-    put(out->alpha, r.alpha);
-    const int hl = (int)std::min<size_t>(r.nll_history.size(), (size_t)opts->max_iterations);
-    if (out->nll_history)
-      for (int i = 0; i < hl; ++i) out->nll_history[i] = r.nll_history[i];
-    if (out->iter_times_ms)
-      for (int i = 0; i < (int)std::min<size_t>(r.iter_times_ms.size(), (size_t)opts->max_iterations); ++i)
-        out->iter_times_ms[i] = r.iter_times_ms[i];
-    out->history_len = hl;
-    out->final_nll = r.final_nll;
-    out->iterations = r.iterations;
-    out->converged = r.converged ? 1 : 0;
-    out->precond_rebuild_count = r.precond_rebuild_count;
+    if (roff != ncat_params)
+      throw Error(ST_INVALID, "ncat_params must equal the categorical leaves' parameter count (" +
+                                  std::to_string(roff) + ")");
+    const LMCTrainOptions o = train_options(opts);
+    std::vector<float> noise(init_noise, init_noise + T), mean(init_mean, init_mean + T);
+    LMCMixedResult r = lmc_train_mixed(m, y_blocked, ip, ck, craw, noise, mean, o);
+    put_result(r, opts, out);
+    int q = 0;
+    std::vector<double> th;
+    for (int s = 0; s < R; ++s)
+      for (const auto& c : leaves[s]) {
+        th.resize((size_t)c.nparam);
+        cat_constrain(c.kind, c.L, r.cat_raw[s].data() + c.param_off, c.nparam, th.data(),
+                      nullptr);
+        for (int k = 0; k < c.nparam; ++k, ++q) {
+          if (cat_raw_out) cat_raw_out[q] = r.cat_raw[s][(size_t)(c.param_off + k)];
+          if (cat_params_out) cat_params_out[q] = (float)th[(size_t)k];
+        }
+      }
   });
 }
 

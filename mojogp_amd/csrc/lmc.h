@@ -161,6 +161,29 @@ LMCTrainResult lmc_train(LMCModel& m, const float* y_blocked_host,
                          const std::vector<float>& init_noise,
                          const std::vector<float>& init_mean, const LMCTrainOptions& o);
 
+// Mixed continuous x categorical LMC (train_lmc_mixed_jit,
+// kernels/jit/jit_lmc_mixed.mojo:684-1557): the parametrisation and Adam of
+// lmc_train plus, for every latent whose kernel tree has categorical leaves,
+// their raw correlation parameters (cat_kinds[s]: one kind per categorical
+// leaf in tree order; init_cat_raw[s]: their raw parameters, concatenated)
+// with Adam moments of their own and the shared step count.  The loop's own
+// rules: a NaN NLL ends the run; the best-NLL evaluation is the only snapshot;
+// after iteration 20 every evaluation not below the best NLL counts toward
+// the patience (the improving one included); the preconditioner is rebuilt
+// when a kernel parameter, a constrained categorical parameter, an entry of
+// A_s or a task noise moved by more than the threshold since the last build.
+// Every parameter is trained (no masks).
+struct LMCMixedResult : LMCTrainResult {
+  std::vector<std::vector<float>> cat_raw;  // best raw categorical parameters per latent
+};
+
+LMCMixedResult lmc_train_mixed(LMCModel& m, const float* y_blocked_host,
+                               const std::vector<std::vector<float>>& init_params,
+                               const std::vector<std::vector<int>>& cat_kinds,
+                               const std::vector<std::vector<float>>& init_cat_raw,
+                               const std::vector<float>& init_noise,
+                               const std::vector<float>& init_mean, const LMCTrainOptions& o);
+
 // out[c][t][i] = sum_s sum_t' A_s[t][t'] (K_s(X*, X) alpha_{c,t'})[i] for C
 // task-blocked columns alpha [C][T][n] (test inputs already packed into every
 // latent provider's `test`); out is a device array [C][T][mtest].

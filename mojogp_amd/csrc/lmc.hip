@@ -7,6 +7,8 @@
 #include <cmath>
 
 #include "host_numerics.h"
+#include "mixed.h"
+#include "tree.h"
 
 namespace mgp {
 
@@ -999,6 +1001,317 @@ LMCTrainResult lmc_train(LMCModel& m, const float* y_blocked_host,
     pv.params = res.params[s];
     pv.noise = 0.0f;
     pv.refresh_coords();
+  }
+  m.A = res.A;
+  m.noise = res.noise;
+  m.upload();
+  return res;
+}
+
+// ------------------------------------------------------------------ mixed training
+LMCMixedResult lmc_train_mixed(LMCModel& m, const float* y_blocked_host,
+                               const std::vector<std::vector<float>>& init_params,
+                               const std::vector<std::vector<int>>& cat_kinds,
+                               const std::vector<std::vector<float>>& init_cat_raw,
+                               const std::vector<float>& init_noise,
+                               const std::vector<float>& init_mean, const LMCTrainOptions& o) {
+  const int R = m.R, T = m.T, TT = T * T;
+  const int64_t n = m.n, nT = n * T;
+  check((int)init_params.size() == R && (int)cat_kinds.size() == R &&
+            (int)init_cat_raw.size() == R,
+        "per-latent arrays mismatch");
+  check((int)init_noise.size() == T && (int)init_mean.size() == T, "per-task arrays mismatch");
+  check(o.max_iterations >= 1, "max_iterations must be >= 1");
+  check(o.num_probes >= 0, "num_probes must be >= 0");
+  hipStream_t st = m.st;
+  LMCStreamGuard guard(m);
+
+  std::vector<int> np(R);
+  int total_kp = 0;
+  std::vector<std::vector<float>> raw(R), rcat(init_cat_raw);
+  std::vector<std::vector<CatLeafRef>> cl(R);
+  for (int s = 0; s < R; ++s) {
+    Provider& pv = *m.prov[s];
+    np[s] = (int)init_params[s].size();
+    check(np[s] == pv.nparams, "initial params length does not match the provider");
+    total_kp += np[s];
+    for (float v : init_params[s]) raw[s].push_back(inv_softplus(v));
+    if (cat_kinds[s].empty()) {
+      check(rcat[s].empty(), "categorical parameters given for a latent without categorical kinds");
+      check(!pv.is_tree || pv.tree.ncat == 0,
+            "a latent with categorical leaves needs one categorical kind per leaf");
+      continue;
+    }
+    check(pv.is_tree, "categorical parameters need a kernel-tree latent");
+    cl[s] = cat_leaves(pv, cat_kinds[s]);
+    size_t K = 0;
+    for (const auto& c : cl[s]) K += (size_t)c.nparam;
+    check(rcat[s].size() == K, "categorical parameter count does not match the leaves");
+    for (float v : rcat[s]) check(std::isfinite(v), "categorical parameters must be finite");
+  }
+  std::vector<float> raw_noise(T), raw_mean(init_mean);
+  for (int t = 0; t < T; ++t) raw_noise[t] = inv_softplus(init_noise[t]);
+
+  // L_s, var_diag and A_s as lmc_train (jit_lmc_mixed.mojo:850-900).
+  const float init_diag = std::sqrt(1.0f / (float)R);
+  std::vector<float> Lall((size_t)R * TT, 0.0f), raw_Ld((size_t)R * T), raw_vd((size_t)R * T);
+  for (int s = 0; s < R; ++s)
+    for (int i = 0; i < T; ++i) {
+      for (int j = 0; j < T; ++j)
+        Lall[(size_t)s * TT + i * T + j] =
+            i == j ? init_diag : (j < i ? 0.01f * (float)(s + 1) / (float)R : 0.0f);
+      raw_Ld[(size_t)s * T + i] = inv_softplus(init_diag);
+    }
+  std::fill(raw_vd.begin(), raw_vd.end(), inv_softplus(0.1f));
+  auto set_A = [&]() {
+    m.A.assign((size_t)R * TT, 0.0f);
+    std::vector<float> vd(T), cs((size_t)TT);
+    for (int s = 0; s < R; ++s) {
+      for (int i = 0; i < T; ++i) {
+        vd[i] = softplus(raw_vd[(size_t)s * T + i]);
+        Lall[(size_t)s * TT + i * T + i] = softplus(raw_Ld[(size_t)s * T + i]);
+      }
+      a_from_l(&Lall[(size_t)s * TT], vd.data(), T, &m.A[(size_t)s * TT]);
+      if (!chol_t(&m.A[(size_t)s * TT], T, cs.data()))
+        for (int i = 0; i < T; ++i) m.A[(size_t)s * TT + i * T + i] += 1e-4f;
+    }
+  };
+  auto constrained_cat = [&](int s) {
+    std::vector<float> out;
+    std::vector<double> th;
+    for (const auto& c : cl[s]) {
+      th.resize((size_t)c.nparam);
+      cat_constrain(c.kind, c.L, rcat[s].data() + c.param_off, c.nparam, th.data(), nullptr);
+      for (double v : th) out.push_back((float)v);
+    }
+    return out;
+  };
+
+  // Adam: one moment array for the continuous parameters in the reference's
+  // order, one per latent for the categorical ones, a shared step count.
+  const int total_adam = total_kp + T + R * TT + R * T + T;
+  std::vector<float> madam(total_adam, 0.0f), vadam(total_adam, 0.0f);
+  std::vector<std::vector<float>> mcat(R), vcat(R);
+  for (int s = 0; s < R; ++s) {
+    mcat[s].assign(rcat[s].size(), 0.0f);
+    vcat[s].assign(rcat[s].size(), 0.0f);
+  }
+  const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f, clipv = 10.0f;
+  int t_step = 0;
+  auto adam = [&](float* mm, float* vv, int idx, float g) {
+    const float a = b1 * mm[idx] + (1.0f - b1) * g;
+    const float b = b2 * vv[idx] + (1.0f - b2) * g * g;
+    mm[idx] = a;
+    vv[idx] = b;
+    const float mh = a / (1.0f - pow_float32(b1, t_step));
+    const float vh = b / (1.0f - pow_float32(b2, t_step));
+    return -o.learning_rate * mh / (std::sqrt(vh) + eps);
+  };
+  auto clip = [&](float g) { return g > clipv ? clipv : (g < -clipv ? -clipv : g); };
+
+  std::vector<float> y_orig(y_blocked_host, y_blocked_host + nT), yh((size_t)nT);
+  DevBuf<float> ydev, rfc, rfcm;
+  ydev.ensure(nT);
+
+  LMCMixedResult res;
+  LMCWork work;
+  LMCPrecond Pc;
+  const bool use_pre = o.precond_rank > 0;
+  const PivotOptions po = training_pivot_options(o.precond_method);
+
+  // State of the last preconditioner build (jit_lmc_mixed.mojo:950-972).
+  std::vector<float> last_kp, last_noise(init_noise), last_A;
+  for (int s = 0; s < R; ++s) last_kp.insert(last_kp.end(), init_params[s].begin(), init_params[s].end());
+  std::vector<std::vector<float>> last_cat(R);
+  for (int s = 0; s < R; ++s) last_cat[s] = constrained_cat(s);
+  set_A();
+  last_A = m.A;
+
+  float best_nll = 1e30f;
+  auto best_raw = raw, best_cat = rcat;
+  auto best_noise = raw_noise, best_mean = raw_mean;
+  auto best_L = Lall, best_Ld = raw_Ld, best_vd = raw_vd;
+  std::vector<float> best_alpha((size_t)nT, 0.0f);
+  int patience = 0;
+
+  for (int it = 0; it < o.max_iterations; ++it) {
+    res.iterations = it + 1;
+    ++t_step;
+    const auto t0 = Clock::now();
+    for (int s = 0; s < R; ++s) {
+      Provider& pv = *m.prov[s];
+      for (int p = 0; p < np[s]; ++p) pv.params[p] = softplus(raw[s][p]);
+      pv.noise = 0.0f;
+      if (cl[s].empty()) pv.refresh_coords();
+      else set_categorical_raw(pv, cat_kinds[s], rcat[s].data(), (int)rcat[s].size());
+    }
+    std::vector<float> cur_noise(T);
+    for (int t = 0; t < T; ++t) cur_noise[t] = softplus(raw_noise[t]);
+    for (int t = 0; t < T; ++t)
+      for (int64_t i = 0; i < n; ++i) yh[(size_t)t * n + i] = y_orig[(size_t)t * n + i] - raw_mean[t];
+    MGP_HIP_CHECK(hipMemcpyAsync(ydev.ptr, yh.data(), nT * sizeof(float), hipMemcpyHostToDevice, st));
+    set_A();
+    m.noise = cur_noise;
+    m.upload();
+
+    // Rebuild when anything the preconditioner holds moved by more than the
+    // threshold, relative to its last build (jit_lmc_mixed.mojo:1060-1108).
+    float max_rel = 0.0f;
+    auto watch = [&](float cur, float prev) {
+      max_rel = std::max(max_rel, std::fabs(cur - prev) / (std::fabs(prev) + 1e-8f));
+    };
+    {
+      int q = 0;
+      for (int s = 0; s < R; ++s)
+        for (int p = 0; p < np[s]; ++p) watch(softplus(raw[s][p]), last_kp[q++]);
+    }
+    std::vector<std::vector<float>> cur_cat(R);
+    for (int s = 0; s < R; ++s) {
+      cur_cat[s] = constrained_cat(s);
+      for (size_t k = 0; k < cur_cat[s].size(); ++k) watch(cur_cat[s][k], last_cat[s][k]);
+    }
+    for (size_t i = 0; i < m.A.size(); ++i) watch(m.A[i], last_A[i]);
+    for (int t = 0; t < T; ++t) watch(cur_noise[t], last_noise[t]);
+    const bool moved = max_rel > o.precond_rebuild_threshold;
+    if (it == 0 || moved) {
+      // iteration 0 builds from the initial state, as the reference does
+      // before its loop
+      if (moved) ++res.precond_rebuild_count;
+      if (use_pre) Pc.build(m, o.precond_rank, po);
+      int q = 0;
+      for (int s = 0; s < R; ++s)
+        for (int p = 0; p < np[s]; ++p) last_kp[q++] = softplus(raw[s][p]);
+      last_cat = cur_cat;
+      last_A = m.A;
+      last_noise = cur_noise;
+    }
+
+    LMCEval ev = lmc_bbmm(m, use_pre ? &Pc : nullptr, ydev.ptr, o.num_probes, o.max_cg_iter,
+                          o.max_tridiag_iter, o.cg_tol, it, it > 0 && !moved, work);
+    const float nll = ev.nll;
+    res.nll_history.push_back(nll);
+    if (std::isnan(nll)) {  // jit_lmc_mixed.mojo:1191-1215: the run ends
+      res.iter_times_ms.push_back(std::chrono::duration<double, std::milli>(Clock::now() - t0).count());
+      break;
+    }
+    if (nll < best_nll) {
+      best_nll = nll;
+      patience = 0;
+      best_raw = raw;
+      best_cat = rcat;
+      best_noise = raw_noise;
+      best_mean = raw_mean;
+      best_L = Lall;
+      best_Ld = raw_Ld;
+      best_vd = raw_vd;
+      best_alpha = ev.alpha;
+    }
+
+    // Categorical gradients (jit_lmc_mixed.mojo:1259-1327): for dK = A_s (x)
+    // dK_s/dtheta_k, (-0.5 alpha^T dK alpha + (0.5/P) sum_j u_j^T dK zn_j) / N
+    // with u_j the probe solutions at the raw probe scale and zn_j the
+    // unit-norm probes.  The evaluation's left factors are
+    // Lf = [-alpha/2 | (0.5/P) u_j]; with Rf = [alpha | zn_j] mixed by A_s
+    // one tree pass over the C*T columns gives the per-entry sums G.
+    const int C = 1 + o.num_probes;
+    bool have_rf = false;
+    for (int s = 0; s < R; ++s) {
+      if (cl[s].empty()) continue;
+      Provider& pv = *m.prov[s];
+      if (!have_rf) {
+        float* rf = rfc.ensure((size_t)nT * C);
+        copy(rf, work.sol.ptr, nT, st);
+        if (o.num_probes > 0) copy(rf + nT, work.probes.ptr, nT * o.num_probes, st);
+        have_rf = true;
+      }
+      float* rfm = rfcm.ensure((size_t)nT * C);
+      hipLaunchKernelGGL(k_lmc_mix, g1(nT * C), dim3(256), 0, st, rfm, rfc.ptr,
+                         m.A_dev.ptr + (size_t)s * TT, n, T, C, 0);
+      MGP_HIP_CHECK(hipGetLastError());
+      std::vector<double> G((size_t)pv.tree.table_size, 0.0);
+      tree_cat_grad_tables(pv.tree, pv.tparams.ptr, pv.train.z.ptr, n, work.lf.ptr, rfm, C * T,
+                           G.data(), pv.tree_gws, st);
+      std::vector<float> g(rcat[s].size());
+      cat_raw_gradients(cl[s], rcat[s].data(), G, 1.0 / (double)nT, clipv, g.data());
+      for (size_t k = 0; k < g.size(); ++k)
+        rcat[s][k] += adam(mcat[s].data(), vcat[s].data(), (int)k, g[k]);
+    }
+
+    // Continuous parameters (jit_lmc_mixed.mojo:1329-1372).
+    int ai = 0;
+    {
+      int off = 0;
+      for (int s = 0; s < R; ++s) {
+        for (int p = 0; p < np[s]; ++p, ++ai)
+          raw[s][p] += adam(madam.data(), vadam.data(), ai,
+                            clip(ev.kernel_grads[off + p]) * sigmoid(raw[s][p]));
+        off += np[s];
+      }
+    }
+    for (int t = 0; t < T; ++t, ++ai)
+      raw_noise[t] += adam(madam.data(), vadam.data(), ai,
+                           clip(ev.noise_grads[t]) * sigmoid(raw_noise[t]));
+    for (int s = 0; s < R; ++s)
+      for (int i = 0; i < T; ++i) {
+        for (int j = 0; j <= i; ++j, ++ai) {
+          float g = 0.0f;
+          for (int b = 0; b < T; ++b)
+            g += ev.G_A[(size_t)s * TT + i * T + b] * Lall[(size_t)s * TT + b * T + j];
+          g = clip(2.0f * g);
+          if (i == j)
+            raw_Ld[(size_t)s * T + i] +=
+                adam(madam.data(), vadam.data(), ai, g * sigmoid(raw_Ld[(size_t)s * T + i]));
+          else
+            Lall[(size_t)s * TT + i * T + j] += adam(madam.data(), vadam.data(), ai, g);
+        }
+        ai += T - 1 - i;
+      }
+    for (int s = 0; s < R; ++s)
+      for (int i = 0; i < T; ++i, ++ai)
+        raw_vd[(size_t)s * T + i] +=
+            adam(madam.data(), vadam.data(), ai,
+                 clip(ev.G_A[(size_t)s * TT + i * T + i]) * sigmoid(raw_vd[(size_t)s * T + i]));
+    for (int t = 0; t < T; ++t, ++ai) {
+      float g = 0.0f;
+      for (int64_t i = 0; i < n; ++i) g -= ev.alpha[(size_t)t * n + i];
+      raw_mean[t] += adam(madam.data(), vadam.data(), ai, clip(g / (float)nT));
+    }
+    res.iter_times_ms.push_back(std::chrono::duration<double, std::milli>(Clock::now() - t0).count());
+    // Patience (jit_lmc_mixed.mojo:1375-1380): after iteration 20 every
+    // evaluation not below the best counts, the one that just set it included.
+    if (nll >= best_nll && it > 20 && o.early_stop_tol > 0.0f && ++patience >= o.early_stop_patience) {
+      res.converged = true;
+      break;
+    }
+  }
+
+  // Best state, constrained (jit_lmc_mixed.mojo:1440-1500); the providers keep
+  // it (noise 0) with their tables at the best categorical parameters.
+  res.params.resize(R);
+  for (int s = 0; s < R; ++s)
+    for (int p = 0; p < np[s]; ++p) res.params[s].push_back(softplus(best_raw[s][p]));
+  res.cat_raw = best_cat;
+  res.noise.resize(T);
+  for (int t = 0; t < T; ++t) res.noise[t] = softplus(best_noise[t]);
+  res.mean = best_mean;
+  res.L = best_L;
+  res.var_diag.resize((size_t)R * T);
+  res.A.assign((size_t)R * TT, 0.0f);
+  for (int s = 0; s < R; ++s) {
+    for (int i = 0; i < T; ++i) {
+      res.L[(size_t)s * TT + i * T + i] = softplus(best_Ld[(size_t)s * T + i]);
+      res.var_diag[(size_t)s * T + i] = softplus(best_vd[(size_t)s * T + i]);
+    }
+    a_from_l(&res.L[(size_t)s * TT], &res.var_diag[(size_t)s * T], T, &res.A[(size_t)s * TT]);
+  }
+  res.alpha = best_alpha;
+  res.final_nll = best_nll < 1e29f ? best_nll : 0.0f;
+  for (int s = 0; s < R; ++s) {
+    Provider& pv = *m.prov[s];
+    pv.params = res.params[s];
+    pv.noise = 0.0f;
+    if (cl[s].empty()) pv.refresh_coords();
+    else set_categorical_raw(pv, cat_kinds[s], best_cat[s].data(), (int)best_cat[s].size());
   }
   m.A = res.A;
   m.noise = res.noise;

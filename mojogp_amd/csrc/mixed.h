@@ -23,6 +23,17 @@ void cat_correlation(int kind, int L, const double* theta, double* R, std::vecto
 void set_categorical_raw(Provider& pv, const std::vector<int>& kinds, const float* raw,
                          int nraw);
 
+// A categorical leaf of a tree provider: kind, levels, table offset (after the
+// tree parameters), offset and count of its raw parameters.
+struct CatLeafRef {
+  int kind, L, table_off, param_off, nparam;
+};
+std::vector<CatLeafRef> cat_leaves(const Provider& pv, const std::vector<int>& kinds);
+// Raw-parameter gradients from per-entry table sums G[table_size]:
+// out[k] = clip(scale sum_e dR_k[e] G[e]) * d(theta_k)/d(raw_k), clip at +-clipv.
+void cat_raw_gradients(const std::vector<CatLeafRef>& cl, const float* rcat,
+                       const std::vector<double>& G, double scale, float clipv, float* out);
+
 struct MixedTrainResult {
   TrainResult base;            // continuous params, noise, mean, histories
   std::vector<float> cat_raw;  // best raw categorical parameters

@@ -151,11 +151,6 @@ void cat_correlation(int kind, int L, const double* th, double* R,
     }
 }
 
-namespace {
-struct CatLeafRef {
-  int kind, L, table_off, param_off, nparam;
-};
-
 std::vector<CatLeafRef> cat_leaves(const Provider& pv, const std::vector<int>& kinds) {
   std::vector<CatLeafRef> out;
   int po = 0, i = 0;
@@ -172,6 +167,27 @@ std::vector<CatLeafRef> cat_leaves(const Provider& pv, const std::vector<int>& k
   return out;
 }
 
+void cat_raw_gradients(const std::vector<CatLeafRef>& cl, const float* rcat,
+                       const std::vector<double>& G, double scale, float clipv, float* out) {
+  std::vector<double> th, chain, R, dR;
+  for (const CatLeafRef& c : cl) {
+    th.resize((size_t)c.nparam);
+    chain.resize((size_t)c.nparam);
+    R.resize((size_t)c.L * c.L);
+    cat_constrain(c.kind, c.L, rcat + c.param_off, c.nparam, th.data(), chain.data());
+    cat_correlation(c.kind, c.L, th.data(), R.data(), &dR);
+    const size_t LL = (size_t)c.L * c.L;
+    for (int k = 0; k < c.nparam; ++k) {
+      double s = 0.0;
+      for (size_t e = 0; e < LL; ++e) s += dR[(size_t)k * LL + e] * G[(size_t)c.table_off + e];
+      float g = (float)(s * scale);
+      g = g > clipv ? clipv : (g < -clipv ? -clipv : g);
+      out[c.param_off + k] = g * (float)chain[(size_t)k];
+    }
+  }
+}
+
+namespace {
 void write_tables(Provider& pv, const std::vector<CatLeafRef>& cl, const std::vector<float>& raw) {
   std::vector<double> th, R;
   for (const CatLeafRef& c : cl) {

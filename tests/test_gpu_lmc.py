@@ -478,3 +478,89 @@ def test_lmc_tree_latent_python_path(tmp_path):
           f"{np.max(np.abs(var2 - var)):.2e}", flush=True)
     np.testing.assert_allclose(mean2, mean, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(var2, var, rtol=1e-5, atol=1e-7)
+
+
+def _mixed_native(provs, Yb, init, noise0, mean0, counts, kinds, raw0, iters, rank):
+    T = noise0.size
+    R = len(provs)
+    P = sum(p.size for p in init)
+    n = Yb.size // T
+    o = _lib.LMCTrainOpts(iters, 0.05, 6, 200, 1e-3, rank, 0, 0.5, 30, 1e-4, 15)
+    out = {"params": np.zeros(P, np.float32), "A": np.zeros((R, T, T), np.float32),
+           "L": np.zeros((R, T, T), np.float32), "var_diag": np.zeros((R, T), np.float32),
+           "noise": np.zeros(T, np.float32), "mean": np.zeros(T, np.float32),
+           "alpha": np.zeros(n * T, np.float32), "hist": np.zeros(iters, np.float32),
+           "times": np.zeros(iters, np.float64), "cat_raw": np.zeros(raw0.size, np.float32),
+           "cat_params": np.zeros(raw0.size, np.float32)}
+    res = _lib.LMCTrainResult()
+    res.params, res.A, res.L = _lib.fptr(out["params"]), _lib.fptr(out["A"]), _lib.fptr(out["L"])
+    res.var_diag, res.noise = _lib.fptr(out["var_diag"]), _lib.fptr(out["noise"])
+    res.mean, res.alpha = _lib.fptr(out["mean"]), _lib.fptr(out["alpha"])
+    res.nll_history, res.iter_times_ms = _lib.fptr(out["hist"]), _lib.dptr(out["times"])
+    counts = np.asarray(counts, np.int32)
+    kinds = np.asarray(kinds, np.int32)
+    _lib.call("mgp_lmc_train_mixed", _lib.handles(provs), R, T, _lib.fptr(Yb),
+              _lib.fptr(np.concatenate(init)), _lib.fptr(noise0), None, _lib.fptr(mean0),
+              counts.ctypes.data_as(_lib.c_int_p), kinds.ctypes.data_as(_lib.c_int_p),
+              _lib.fptr(raw0), int(raw0.size), C.byref(o), C.byref(res),
+              _lib.fptr(out["cat_raw"]), _lib.fptr(out["cat_params"]))
+    out["history_len"], out["iterations"] = res.history_len, res.iterations
+    return out
+
+
+@pytest.mark.parametrize("case,rank", [("ehh", 0), ("ehh", 5), ("gd_cr", 5)])
+def test_lmc_train_mixed_matches_oracle(case, rank):
+    """Mixed continuous x categorical LMC (train_lmc_mixed_jit): a plain RBF
+    latent beside a kernel-tree latent with categorical leaves on column 1;
+    four joint Adam steps of the kernel parameters, L_s, var_diag, task
+    noise and mean and the categorical raw parameters against the CPU
+    restatement on the same probes.  gd_cr: two categorical leaves (GD, CR)
+    in one tree."""
+    from mojogp_amd import CR, EHH, GD, Matern52, RBF
+    from oracle import categorical as oc
+    n, T, L, iters = 90, 2, 3, 4
+    rng = np.random.default_rng(71)
+    X = np.c_[rng.uniform(0, 1, n), rng.integers(0, L, n)].astype(np.float32)
+    Y = np.stack([np.sin(4 * X[:, 0]) + 0.3 * X[:, 1], np.cos(3 * X[:, 0]) - 0.2 * X[:, 1]])
+    Y = (Y + 0.05 * rng.normal(size=(T, n))).astype(np.float32)
+    Yb = np.ascontiguousarray(Y.reshape(-1))
+    if case == "ehh":
+        node = RBF(active_dims=[0]) * EHH(L, active_dims=[1])
+        specs = [(oc.EHH, L)]
+        init1 = np.array([0.6, 0.9], np.float32)
+    else:
+        node = (RBF(active_dims=[0]) * GD(L, active_dims=[1])
+                + Matern52(active_dims=[0]) * CR(L, active_dims=[1]))
+        specs = [(oc.GD, L), (oc.CR, L)]
+        init1 = np.array([0.6, 0.9, 0.4, 0.7], np.float32)
+    raw1 = np.concatenate([oc.default_raw(k, lv) + 0.2 for k, lv in specs]).astype(np.float32)
+    init = [np.array([0.5, 1.0], np.float32), init1]
+    noise0 = np.full(T, 0.1, np.float32)
+    mean0 = Y.mean(axis=1).astype(np.float32)
+    print(f"lmc mixed train case={case} rank={rank}", flush=True)
+    provs = [NativeProvider(ok.RBF, False, X, init[0], 0.0),
+             NativeProvider(None, False, X, init[1], 0.0, tree_spec=node.to_tree_spec(2))]
+    try:
+        got = _mixed_native(provs, Yb, init, noise0, mean0, [0, len(specs)],
+                            [k for k, _ in specs], raw1, iters, rank)
+    finally:
+        _close(provs)
+    ref = ol.train_mixed([ok.RBF, node.to_dict()], X, Yb, init, noise0, mean0,
+                         [[], specs], [np.zeros(0, np.float32), raw1], max_iterations=iters,
+                         learning_rate=0.05, num_probes=6, max_cg=200, max_tridiag=30,
+                         cg_tol=1e-3, precond_rank=rank)
+    print(f"  nll {got['hist'][:got['history_len']]} vs {ref['nll_history']}", flush=True)
+    print(f"  cat raw {got['cat_raw']} vs {ref['cat_raw'][1]}", flush=True)
+    assert got["history_len"] == iters and got["iterations"] == iters
+    np.testing.assert_allclose(got["hist"], ref["nll_history"], rtol=0, atol=1e-4)
+    assert _rel(got["params"], np.concatenate(ref["params"])) <= 1e-3
+    assert _rel(got["A"], ref["A"]) <= 1e-3
+    assert _rel(got["noise"], ref["noise"]) <= 1e-3
+    assert _rel(got["mean"], ref["mean"]) <= 1e-3
+    # the categorical steps: raw values moved by ~iters * lr; compare the moves
+    np.testing.assert_allclose(got["cat_raw"] - raw1, ref["cat_raw"][1] - raw1, rtol=0,
+                               atol=2e-3 * 0.05 * iters)
+    want_c = np.concatenate([oc.constrain(k, lv, got["cat_raw"][o:o + oc.num_params(k, lv)])
+                             for (k, lv), o in zip(specs, np.cumsum(
+                                 [0] + [oc.num_params(k, lv) for k, lv in specs])[:-1])])
+    np.testing.assert_allclose(got["cat_params"], want_c, rtol=1e-6, atol=1e-7)
