@@ -562,6 +562,135 @@ class Engine:
             "iter_times_ms": [float(v) for v in times[:hl]],
         }
 
+    def train_lmc_mixed(self, *args) -> dict[str, Any]:
+        """train_lmc_mixed(provider_infos, init_params_per_latent, Y [n, T], num_tasks,
+        latent_C_trains, latent_cat_specs, cat_init_params_per_latent, max_iters, lr,
+        verbose, num_probes, max_cg_iter, cg_tol, precond_rank, precond_method,
+        precond_rebuild_threshold, max_tridiag_iter, init_noise [T], fixed_noise [n, T],
+        has_fixed_noise, init_mean [T], method_int [, progress_callback,
+        progress_interval]) (train_lmc_mixed_python, jit_engine_lmc_bindings.mojo:54-360).
+
+        latent_cat_specs[s]: one {"levels", "kernel_type"} dict per categorical
+        leaf of latent s in tree order; latent_C_trains[s]: their integer
+        level columns [n, len(specs)] (the tree provider reads the levels from
+        its input columns, so these must match them); cat_init: their raw
+        parameters.  Returns the reference's dict (``cat_params_per_latent``
+        constrained) plus ``cat_raw_per_latent``."""
+        if len(args) < 22 or len(args) > 24:
+            raise ValueError("train_lmc_mixed() expects 22 to 24 positional arguments")
+        infos = list(args[0])
+        provs = [_provider(i) for i in infos]
+        R = len(provs)
+        Y = _lib.f32(args[2])
+        T = int(args[3])
+        if Y.ndim != 2 or Y.shape[1] != T:
+            raise ValueError("Y must have shape (n, num_tasks)")
+        n = Y.shape[0]
+        if int(args[21]) == 2:
+            raise ValueError("method int 2 is not a public MojoGP training route")
+        Cs, specs, cat0 = list(args[4]), list(args[5]), list(args[6])
+        if not (len(args[1]) == len(Cs) == len(specs) == len(cat0) == R):
+            raise ValueError("train_lmc_mixed() needs one entry per latent in every "
+                             "per-latent list")
+        init_params, counts, kinds, raws = [], [], [], []
+        for s, prov in enumerate(provs):
+            p = _lib.f32(args[1][s]).ravel()
+            if p.shape[0] != prov.nparams:
+                raise ValueError("train_lmc_mixed() initial params length does not match "
+                                 "provider gradient params")
+            init_params.append(p)
+            Cm = np.asarray(Cs[s])
+            if Cm.ndim != 2 or Cm.shape != (n, len(specs[s])):
+                raise ValueError(f"latent {s}: C_train must have shape (n, number of "
+                                 "categorical leaves)")
+            counts.append(len(specs[s]))
+            kinds.extend(self._CAT_KIND[str(sp["kernel_type"]).lower()] for sp in specs[s])
+            raws.append(_lib.f32(cat0[s]).ravel())
+        o = _lib.LMCTrainOpts()
+        o.max_iterations = int(args[7])
+        o.learning_rate = float(args[8])
+        o.num_probes = int(args[10])
+        o.max_cg_iter = int(args[11])
+        o.cg_tol = float(args[12])
+        o.precond_rank = int(args[13])
+        o.precond_method = int(args[14])
+        o.precond_rebuild_threshold = float(args[15])
+        o.max_tridiag_iter = int(args[16])
+        o.early_stop_tol = 1e-4
+        o.early_stop_patience = 15
+        if o.max_iterations <= 0:
+            raise ValueError("max_iterations must be > 0")
+        noise0 = _lib.f32(args[17]).ravel()
+        fixed = None
+        if bool(args[19]):
+            fn = _lib.f32(args[18])
+            if fn.shape != (n, T):
+                raise ValueError("train_lmc_mixed() fixed observation noise must have shape [n, T]")
+            fixed = np.ascontiguousarray(fn.T)
+        mean0 = _lib.f32(args[20]).ravel()
+        y_blocked = np.ascontiguousarray(Y.T)
+        flat_p = np.concatenate(init_params).astype(np.float32)
+        flat_raw = (np.concatenate(raws) if raws else np.zeros(0)).astype(np.float32)
+        cnt = np.asarray(counts, np.int32)
+        knd = np.asarray(kinds if kinds else [0], np.int32)
+        it_max = o.max_iterations
+        out_params = np.zeros_like(flat_p)
+        A = np.zeros((R, T, T), np.float32)
+        L = np.zeros((R, T, T), np.float32)
+        vd = np.zeros((R, T), np.float32)
+        noise = np.zeros(T, np.float32)
+        mean = np.zeros(T, np.float32)
+        alpha = np.zeros(n * T, np.float32)
+        hist = np.zeros(it_max, np.float32)
+        times = np.zeros(it_max, np.float64)
+        raw_out = np.zeros(max(flat_raw.size, 1), np.float32)
+        con_out = np.zeros(max(flat_raw.size, 1), np.float32)
+        res = _lib.LMCTrainResult()
+        res.params, res.A, res.L = _lib.fptr(out_params), _lib.fptr(A), _lib.fptr(L)
+        res.var_diag, res.noise, res.mean = _lib.fptr(vd), _lib.fptr(noise), _lib.fptr(mean)
+        res.alpha, res.nll_history = _lib.fptr(alpha), _lib.fptr(hist)
+        res.iter_times_ms = _lib.dptr(times)
+        _lib.call("mgp_lmc_train_mixed", _lib.handles(provs), R, T, _lib.fptr(y_blocked),
+                  _lib.fptr(flat_p), _lib.fptr(noise0), _lib.ofptr(fixed), _lib.fptr(mean0),
+                  cnt.ctypes.data_as(_lib.c_int_p), knd.ctypes.data_as(_lib.c_int_p),
+                  _lib.fptr(flat_raw if flat_raw.size else raw_out), int(flat_raw.size),
+                  C.byref(o), C.byref(res), _lib.fptr(raw_out), _lib.fptr(con_out))
+        hl = int(res.history_len)
+        per_latent, cat_con, cat_raw = [], [], []
+        off = roff = koff = 0
+        for s, prov in enumerate(provs):
+            per_latent.append([float(v) for v in out_params[off:off + prov.nparams]])
+            prov.params = out_params[off:off + prov.nparams].copy()
+            prov.noise = 0.0
+            off += prov.nparams
+            k = raws[s].size
+            cat_con.append([float(v) for v in con_out[roff:roff + k]])
+            cat_raw.append(raw_out[roff:roff + k].copy())
+            if counts[s]:
+                prov.cat_kinds = knd[koff:koff + counts[s]].copy()
+                prov.cat_raw = cat_raw[-1]
+            roff += k
+            koff += counts[s]
+        mode = int(args[21])
+        return {
+            "status": "trained", "model_type": "lmc_mixed", "num_latents": R, "num_tasks": T,
+            "n": n, "final_nll": float(res.final_nll), "iterations": int(res.iterations),
+            "converged": bool(res.converged), "max_tridiag_iter": o.max_tridiag_iter,
+            "precond_rebuild_threshold": o.precond_rebuild_threshold,
+            "precond_rebuild_count": int(res.precond_rebuild_count),
+            "precond_rank": o.precond_rank, "precond_method": o.precond_method,
+            "uses_fixed_observation_noise": fixed is not None,
+            "training_route": "materialized" if mode == 1 else "matrix_free",
+            "materialization_mode": mode,
+            "params_per_latent": per_latent, "cat_params_per_latent": cat_con,
+            "cat_raw_per_latent": cat_raw,
+            "noise_per_task": [float(v) for v in noise],
+            "mean_per_task": [float(v) for v in mean],
+            "A_matrices": A, "L_factors": L, "var_diag": vd, "alpha": alpha,
+            "nll_history": [float(v) for v in hist[:hl]],
+            "iter_times_ms": [float(v) for v in times[:hl]],
+        }
+
     def predict_lmc(self, *args) -> dict[str, Any]:
         """predict_lmc(provider_infos, alpha [n*T], A [R, T, T], X_test [m, d],
         params_per_latent, mean_per_task [T], n_train, num_tasks

@@ -78,6 +78,23 @@ def cat_default_raw_param(kernel_type: KernelType, param_index: int, L: int) -> 
     return 0.0
 
 
+def cat_raw_from_constrained(kernel_type: KernelType, L: int, theta) -> np.ndarray:
+    """Raw parameters of one categorical leaf from its constrained values: the
+    inverse of the transforms of categorical_prediction_params
+    (kernel.py:132-174): softplus for GD / CR and the FE diagonal, pi *
+    sigmoid for the EHH / HH angles and the first L(L-1)/2 FE entries.  Angles
+    are kept inside (0, pi) by 1e-7 of a half-turn."""
+    th = np.asarray(theta, np.float64).ravel()
+    n_angles = {KernelType.EHH: len(th), KernelType.HH: len(th),
+                KernelType.FE: L * (L - 1) // 2}.get(kernel_type, 0)
+    out = np.empty_like(th)
+    u = np.clip(th[:n_angles] / np.pi, 1e-7, 1.0 - 1e-7)
+    out[:n_angles] = np.log(u / (1.0 - u))
+    v = np.maximum(th[n_angles:], 1e-30)
+    out[n_angles:] = np.where(v > 20.0, v, np.log(np.expm1(np.minimum(v, 20.0))))
+    return out.astype(np.float32)
+
+
 # Families the native kernels implement (value = native kind code).
 NATIVE_KINDS = {KernelType.RBF: 0, KernelType.MATERN52: 1, KernelType.MATERN12: 2,
                 KernelType.MATERN32: 3}

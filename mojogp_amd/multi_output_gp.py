@@ -7,19 +7,25 @@ save / load 6638-7013.  Same argument names and defaults; the model is
 
     K_full = sum_s A_s (x) K_s + diag(noise_t) (+ fixed observation noise),
 
-one RBF / Matern-5/2 latent kernel per s (isotropic or ARD) over shared inputs.
-Training, prediction, exact variance and the pathwise correction run in
+one latent kernel per s over shared inputs: an RBF / Matern leaf (isotropic or
+ARD), a composite kernel tree, or a mixed continuous x categorical tree whose
+categorical leaves read integer levels from their input columns
+(_fit_mixed_composite, multi_output_gp.py:5144-5405; its categorical
+correlation parameters train beside the continuous ones).  Training,
+prediction, exact variance and the pathwise correction run in
 libmojogp_amd.so; the RFF prior draws use the caller's NumPy Generator exactly
 as the reference and are evaluated on the device.
 
-Scope: continuous inputs, RBF / Matern-5/2 latents.  Categorical / mixed
-latents, composite kernel trees and heteroskedastic noise models raise
-``NotImplementedError``.
+Outside the engine (``NotImplementedError``): isotropic polynomial leaves,
+heteroskedastic noise models, fixed observation noise with mixed latents (as
+the reference) and pathwise samples of composite latents (no random Fourier
+features).
 """
 
 from __future__ import annotations
 
 import json
+import warnings
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Any, Optional, Union
@@ -28,7 +34,8 @@ import numpy as np
 
 from . import _engine
 from .gp import normalize_fit_method
-from .kernel import KernelNode, Matern12, Matern32, Matern52, RBF, make_ard_kernel
+from .kernel import (KernelNode, Matern12, Matern32, Matern52, RBF, cat_raw_from_constrained,
+                     make_ard_kernel)
 from .pathwise_prior import (build_feature_weights, build_pathwise_feature_map,
                              sample_prior_values)
 
@@ -71,6 +78,47 @@ class LMCTrainingResult:
     var_diag: Optional[np.ndarray] = None
     iter_times_ms: Optional[np.ndarray] = None
     fixed_observation_noise: Optional[np.ndarray] = None
+    cat_params_per_latent: Optional[list] = None       # constrained, per latent
+    cat_param_names_per_latent: Optional[list] = None
+
+
+def _leaves(node: KernelNode) -> list:
+    if node.kernel_type is not None:
+        return [node]
+    out = _leaves(node.left) if node.left is not None else []
+    return out + (_leaves(node.right) if node.right is not None else [])
+
+
+def _mixed_layout(kernel: KernelNode, X: np.ndarray, latent: int):
+    """Categorical layout of one mixed latent (_configure_latent_kernels_for_fit,
+    multi_output_gp.py:4136-4218): the leaves' {"levels", "kernel_type"} specs
+    in tree order, their input columns, the continuous columns (the default
+    dimensions of the latent's continuous leaves) and the categorical parameter
+    names.  Columns must hold integer levels in [0, L)."""
+    leaves = kernel.categorical_leaves()
+    if all(lf.is_categorical() for lf in _leaves(kernel)):
+        raise ValueError("Pure categorical latent kernels are not supported for "
+                         f"MultiOutputLMCGP. Latent kernel {latent} contains no continuous "
+                         "dimensions.")
+    specs, cols, names = [], [], []
+    for lf in leaves:
+        col = int(lf.active_dims[0])
+        if col >= X.shape[1]:
+            raise ValueError(f"latent {latent}: categorical column {col} out of range")
+        v = X[:, col]
+        L = int(lf.levels)
+        if np.any(v != np.round(v)) or np.any(v < 0) or np.any(v >= L):
+            raise ValueError(f"latent {latent}: column {col} must hold integer levels in "
+                             f"[0, {L})")
+        specs.append({"levels": L, "kernel_type": lf.kernel_type.name.lower()})
+        cols.append(col)
+        names.extend(lf.get_param_names())
+    cont = [c for c in range(X.shape[1]) if c not in set(cols)]
+    if not cont:
+        raise ValueError("Pure categorical latent kernels are not supported for "
+                         f"MultiOutputLMCGP. Latent kernel {latent} has no continuous "
+                         "dimensions.")
+    return specs, cols, cont, names
 
 
 def _resolve_precond(rank: int, method: str, use_preconditioner: Optional[bool]):
@@ -127,11 +175,12 @@ class MultiOutputLMCGP:
                 k = _KERNEL_STRINGS[k.lower()]()
             if not isinstance(k, KernelNode):
                 raise ValueError("All kernels must be KernelNode objects or valid kernel strings.")
-            if not k.is_native_leaf() and (k.has_categorical() or not k.is_tree_servable()
-                                           or k.num_params() != k.engine_num_params()):
+            ncat = sum(lf.num_params() for lf in k.categorical_leaves())
+            if not k.is_native_leaf() and (not k.is_tree_servable()
+                                           or k.num_params() - ncat != k.engine_num_params()):
                 raise NotImplementedError(f"latent kernel {k!r} is outside the gfx950 LMC "
-                                          "engine (categorical and isotropic polynomial "
-                                          "leaves are single-output only)")
+                                          "engine (isotropic polynomial leaves are "
+                                          "single-output only)")
             conv.append(k)
         if not conv:
             raise ValueError("MultiOutputLMCGP needs at least one latent kernel")
@@ -162,6 +211,17 @@ class MultiOutputLMCGP:
         self._backend_predict_info: Optional[dict] = None
         self._backend_sample_info: Optional[dict] = None
         self._fixed_observation_noise: Optional[np.ndarray] = None
+        # per latent: continuous columns of a mixed latent (None otherwise),
+        # categorical specs and raw categorical parameters
+        self._latent_cont_cols: list = [None] * len(conv)
+        self._latent_cat_specs: list = [[] for _ in conv]
+        self._latent_cat_raw: list = [np.zeros(0, np.float32) for _ in conv]
+        self._latent_cat_cols: list = [[] for _ in conv]
+        self._latent_cat_names: list = [[] for _ in conv]
+
+    @property
+    def has_mixed_latents(self) -> bool:
+        return any(k.has_categorical() for k in self._original_kernels)
 
     # ------------------------------------------------------------ properties
     @property
@@ -207,10 +267,15 @@ class MultiOutputLMCGP:
 
     def _build_providers(self, X: np.ndarray, params_per_latent, method: str) -> list:
         d = X.shape[1]
-        self._modules = [_engine.load_kernel_module(k, False, d) for k in self.kernels]
+        self._modules = [_engine.load_kernel_module(k, False, d, default_dims=cc)
+                         for k, cc in zip(self.kernels, self._latent_cont_cols)]
         infos = []
-        for mod, p in zip(self._modules, params_per_latent):
+        for s, (mod, p) in enumerate(zip(self._modules, params_per_latent)):
             info = mod.init_provider(X, np.asarray(p, np.float32), 0.0)
+            if self._latent_cat_specs[s]:
+                kinds = [_engine.Engine._CAT_KIND[c["kernel_type"]]
+                         for c in self._latent_cat_specs[s]]
+                _engine._provider(info).set_categorical_params(kinds, self._latent_cat_raw[s])
             if method == "materialized":
                 mod.materialize(info)
             infos.append(info)
@@ -221,6 +286,40 @@ class MultiOutputLMCGP:
             params = [np.asarray(p, np.float32) for p in self._result.params_per_latent]
             self._provider_infos = self._build_providers(self._X_train, params, self.method)
         return self._provider_infos
+
+    def _resolve_latents(self, X: np.ndarray) -> None:
+        """Per-latent categorical layout for the training inputs X and the
+        kernels as trained (ARD over the continuous columns of a mixed latent)."""
+        d = X.shape[1]
+        self._latent_cont_cols, self._latent_cat_specs = [], []
+        self._latent_cat_names, self._latent_cat_cols = [], []
+        kernels = []
+        for s, k in enumerate(self._original_kernels):
+            if k.has_categorical():
+                specs, cols, cont, names = _mixed_layout(k, X, s)
+                kernels.append(make_ard_kernel(k, len(cont)) if self.ard
+                               else KernelNode.from_dict(k.to_dict()))
+            else:
+                specs, cols, cont, names = [], [], None, []
+                kernels.append(make_ard_kernel(k, d) if self.ard
+                               else KernelNode.from_dict(k.to_dict()))
+            self._latent_cont_cols.append(cont)
+            self._latent_cat_specs.append(specs)
+            self._latent_cat_cols.append(cols)
+            self._latent_cat_names.append(names)
+        self.kernels = kernels
+
+    def _latent_init(self, s: int) -> np.ndarray:
+        """Initial parameters of latent s in its fit layout: the public layout
+        for a continuous latent, the continuous (engine) parameters of a mixed
+        one, whose categorical parameters train separately."""
+        k = self.kernels[s]
+        p = k.get_initial_params().astype(np.float32)
+        return k.to_engine_params(p) if self._latent_cat_specs[s] else p
+
+    def _latent_count(self, s: int) -> int:
+        k = self.kernels[s]
+        return k.engine_num_params() if self._latent_cat_specs[s] else k.num_params()
 
     # ------------------------------------------------------------ fit
     def fit(self, X, Y, max_iterations: int = 100, learning_rate: float = 0.05,
@@ -278,10 +377,14 @@ class MultiOutputLMCGP:
                 raise ValueError("all initial_noise_per_task entries must be > 0")
         else:
             noise0 = np.full(T, initial_noise, np.float32)
+        mixed = self.has_mixed_latents
+        if mixed and fixed_observation_noise is not None:
+            raise NotImplementedError(
+                "fixed_observation_noise for mixed MultiOutputLMCGP is not yet supported; use "
+                "continuous LMC or omit fixed observation noise.")
         self.method = method
-        self.kernels = [make_ard_kernel(k, d) if self.ard else KernelNode.from_dict(k.to_dict())
-                        for k in self._original_kernels]
-        counts = [k.num_params() for k in self.kernels]
+        self._resolve_latents(X)
+        counts = [self._latent_count(s) for s in range(R)]
         if initial_params is not None and initial_lengthscales is not None:
             raise ValueError("Provide either initial_params or initial_lengthscales for "
                              "MultiOutputLMCGP.fit(), not both.")
@@ -291,7 +394,7 @@ class MultiOutputLMCGP:
                 raise ValueError(f"init_params must have shape ({sum(counts)},) "
                                  "[flat concat of per-latent params]")
         else:
-            flat = np.concatenate([k.get_initial_params() for k in self.kernels]).astype(np.float32)
+            flat = np.concatenate([self._latent_init(s) for s in range(R)]).astype(np.float32)
             if initial_lengthscales is not None:
                 flat = self._params_from_lengthscales(np.asarray(initial_lengthscales, np.float32))
         if self._init_mean is None:
@@ -301,30 +404,56 @@ class MultiOutputLMCGP:
         else:
             mean0 = np.asarray(self._init_mean, np.float32)
         per_latent, off = [], 0
-        for c, k in zip(counts, self.kernels):
-            per_latent.append(k.to_engine_params(flat[off:off + c]))
+        for s, (c, k) in enumerate(zip(counts, self.kernels)):
+            sl = flat[off:off + c]
+            per_latent.append(sl.copy() if self._latent_cat_specs[s] else k.to_engine_params(sl))
             off += c
         self._destroy_providers()
         self._engine = _engine.load_engine()
+        from .kernel import cat_default_raw_param
+        cat0 = [np.asarray([cat_default_raw_param(lf.kernel_type, i, lf.levels)
+                            for lf in k.categorical_leaves() for i in range(lf.num_params())],
+                           np.float32) for k in self.kernels]
+        self._latent_cat_raw = cat0
         infos = self._build_providers(X, per_latent, method)
         masks = [np.ones(c, bool) for c in counts]
+        fixed_arg = (fixed_observation_noise if fixed_observation_noise is not None
+                     else np.zeros((n, T), np.float32))
         try:
-            raw = self._engine.train_lmc(
-                infos, per_latent, masks, Y, T, int(max_iterations), float(learning_rate),
-                bool(verbose), self.num_probes, self.max_cg_iter, float(self.cg_tol),
-                self.precond_rank, self.precond_method, float(self.precond_rebuild_threshold),
-                self.max_tridiag_iter, noise0,
-                fixed_observation_noise if fixed_observation_noise is not None
-                else np.zeros((n, T), np.float32),
-                fixed_observation_noise is not None, mean0)
+            if mixed:
+                if early_stop_patience != 15 or early_stop_tol != 1e-4:
+                    warnings.warn("early_stop_patience and early_stop_tol are not used: the "
+                                  "engine handles convergence internally via max_iterations.",
+                                  UserWarning, stacklevel=2)
+                Cs = [np.ascontiguousarray(X[:, cols], np.int32).reshape(n, len(cols))
+                      for cols in self._latent_cat_cols]
+                raw = self._engine.train_lmc_mixed(
+                    infos, per_latent, Y, T, Cs, self._latent_cat_specs, cat0,
+                    int(max_iterations), float(learning_rate), bool(verbose), self.num_probes,
+                    self.max_cg_iter, float(self.cg_tol), self.precond_rank,
+                    self.precond_method, float(self.precond_rebuild_threshold),
+                    self.max_tridiag_iter, noise0, fixed_arg, False, mean0,
+                    1 if method == "materialized" else 0)
+            else:
+                raw = self._engine.train_lmc(
+                    infos, per_latent, masks, Y, T, int(max_iterations), float(learning_rate),
+                    bool(verbose), self.num_probes, self.max_cg_iter, float(self.cg_tol),
+                    self.precond_rank, self.precond_method,
+                    float(self.precond_rebuild_threshold), self.max_tridiag_iter, noise0,
+                    fixed_arg, fixed_observation_noise is not None, mean0)
         except Exception:
             for mod, info in zip(self._modules, infos):
                 mod.destroy_provider(info)
             raise
         self._provider_infos = infos
-        params = [k.from_engine_params(np.asarray(p, np.float32))
+        if mixed:
+            self._latent_cat_raw = [np.asarray(r, np.float32) for r in raw["cat_raw_per_latent"]]
+        params = [np.asarray(p, np.float32) if self._latent_cat_specs[s]
+                  else k.from_engine_params(np.asarray(p, np.float32))
+                  for s, (k, p) in enumerate(zip(self.kernels, raw["params_per_latent"]))]
+        public = [k.from_engine_params(np.asarray(p, np.float32))
                   for k, p in zip(self.kernels, raw["params_per_latent"])]
-        ls, os_, lpd = _summarize(self.kernels, params, self.ard)
+        ls, os_, lpd = _summarize(self.kernels, public, self.ard)
         A = np.asarray(raw["A_matrices"], np.float32)
         B = A.sum(axis=0).astype(np.float32)
         lam, Q = np.linalg.eigh(B.astype(np.float64))
@@ -343,7 +472,10 @@ class MultiOutputLMCGP:
             lengthscales_per_dim=lpd, mean_per_task=np.asarray(raw["mean_per_task"], np.float32),
             var_diag=np.asarray(raw["var_diag"], np.float32),
             iter_times_ms=np.asarray(raw["iter_times_ms"], np.float64),
-            fixed_observation_noise=fixed_observation_noise)
+            fixed_observation_noise=fixed_observation_noise,
+            cat_params_per_latent=([np.asarray(c, np.float32) for c in
+                                    raw["cat_params_per_latent"]] if mixed else None),
+            cat_param_names_per_latent=(self._latent_cat_names if mixed else None))
         self._X_train, self._Y_train = X, Y
         self._fixed_observation_noise = fixed_observation_noise
         self._raw_result = raw
@@ -378,10 +510,10 @@ class MultiOutputLMCGP:
             raise ValueError(f"initial_lengthscales has shape {values.shape}, incompatible "
                              f"with per-latent lengthscale counts {counts}")
         out = []
-        for k, ix, v in zip(self.kernels, idx, per):
+        for s, (k, ix, v) in enumerate(zip(self.kernels, idx, per)):
             p = k.get_initial_params().copy()
             p[ix] = v
-            out.append(p)
+            out.append(k.to_engine_params(p) if self._latent_cat_specs[s] else p)
         return np.concatenate(out).astype(np.float32)
 
     # ------------------------------------------------------------ predict
@@ -613,7 +745,8 @@ class MultiOutputLMCGP:
         tr = self._result
         cfg = {"schema_version": _MODEL_SCHEMA_VERSION, "mojogp_version": __version__,
                "wrapper": "MultiOutputLMCGP", "is_composite": True,
-               "has_mixed_latents": False, "ard": self.ard, "method": self.method,
+               "has_mixed_latents": self.has_mixed_latents, "ard": self.ard,
+               "method": self.method,
                "num_probes": self.num_probes, "max_cg_iter": self.max_cg_iter,
                "cg_tol": self.cg_tol, "use_preconditioner": self.use_preconditioner,
                "precond_rank": self.precond_rank, "precond": self.precond,
@@ -636,6 +769,9 @@ class MultiOutputLMCGP:
                   "fixed_observation_noise": self._fixed_observation_noise}
         for s, p in enumerate(tr.params_per_latent):
             arrays[f"params_latent_{s}"] = np.asarray(p, np.float32)
+            if tr.cat_params_per_latent is not None:
+                arrays[f"cat_params_latent_{s}"] = np.asarray(
+                    tr.cat_params_per_latent[s], np.float32)
         np.savez(path + "_arrays.npz", **{k: v for k, v in arrays.items() if v is not None})
 
     @classmethod
@@ -648,9 +784,6 @@ class MultiOutputLMCGP:
             raise ValueError("saved model is not a MultiOutputLMCGP")
         if int(cfg.get("schema_version", 0)) != _MODEL_SCHEMA_VERSION:
             raise ValueError("unsupported model schema version")
-        if cfg.get("has_mixed_latents"):
-            raise NotImplementedError("mixed continuous/categorical LMC latents are outside "
-                                      "the gfx950 engine")
         arr = np.load(path + "_arrays.npz", allow_pickle=False)
         missing = [k for k in ("X_train", "Y_train", "noise_per_task", "A_matrices",
                                "nll_history") if k not in arr]
@@ -667,13 +800,36 @@ class MultiOutputLMCGP:
         gp.method = cfg.get("method", "materialized")
         gp._X_train = np.ascontiguousarray(arr["X_train"], np.float32)
         gp._Y_train = np.ascontiguousarray(arr["Y_train"], np.float32)
-        d = gp._X_train.shape[1]
-        gp.kernels = [make_ard_kernel(k, d) if gp.ard else k for k in gp._original_kernels]
+        gp._resolve_latents(gp._X_train)
+        R = int(cfg["num_latents"])
+        mixed = bool(cfg.get("has_mixed_latents"))
+        if mixed:
+            # the file holds the constrained categorical parameters (as the
+            # reference writes them); the tables come from their raw values
+            miss = [f"cat_params_latent_{s}" for s in range(R)
+                    if gp._latent_cat_specs[s] and f"cat_params_latent_{s}" not in arr]
+            if miss:
+                raise ValueError("MultiOutputLMCGP artifact is missing required arrays: "
+                                 + ", ".join(miss))
+            gp._latent_cat_raw = []
+            for s in range(R):
+                raw, off = [], 0
+                theta = (np.asarray(arr[f"cat_params_latent_{s}"], np.float32)
+                         if gp._latent_cat_specs[s] else np.zeros(0, np.float32))
+                for lf in gp.kernels[s].categorical_leaves():
+                    k = lf.num_params()
+                    raw.append(cat_raw_from_constrained(lf.kernel_type, int(lf.levels),
+                                                        theta[off:off + k]))
+                    off += k
+                if off != theta.size:
+                    raise ValueError(f"cat_params_latent_{s} has {theta.size} values, the "
+                                     f"latent's categorical leaves need {off}")
+                gp._latent_cat_raw.append(np.concatenate(raw).astype(np.float32) if raw
+                                          else np.zeros(0, np.float32))
         get = lambda k: arr[k] if k in arr else None  # noqa: E731
         fixed = get("fixed_observation_noise")
         gp._fixed_observation_noise = (np.ascontiguousarray(fixed, np.float32)
                                        if fixed is not None else None)
-        R = int(cfg["num_latents"])
         gp._result = LMCTrainingResult(
             final_nll=float(cfg["final_nll"]), nll_history=arr["nll_history"],
             iterations=int(cfg["iterations"]), converged=bool(cfg["converged"]),
@@ -686,7 +842,11 @@ class MultiOutputLMCGP:
             alpha=get("alpha"), use_ard=bool(cfg.get("use_ard", False)),
             lengthscales_per_dim=get("lengthscales_per_dim"),
             mean_per_task=get("mean_per_task"), var_diag=get("var_diag"),
-            iter_times_ms=get("iter_times_ms"), fixed_observation_noise=gp._fixed_observation_noise)
+            iter_times_ms=get("iter_times_ms"), fixed_observation_noise=gp._fixed_observation_noise,
+            cat_params_per_latent=([np.asarray(arr[f"cat_params_latent_{s}"], np.float32)
+                                    if gp._latent_cat_specs[s] else np.zeros(0, np.float32)
+                                    for s in range(R)] if mixed else None),
+            cat_param_names_per_latent=(gp._latent_cat_names if mixed else None))
         fm = get("fitted_mean")
         gp._fitted_mean = fm if fm is not None else gp._result.mean_per_task
         gp._backend_train_info = {"training_route": gp.method}

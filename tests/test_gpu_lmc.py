@@ -564,3 +564,60 @@ def test_lmc_train_mixed_matches_oracle(case, rank):
                              for (k, lv), o in zip(specs, np.cumsum(
                                  [0] + [oc.num_params(k, lv) for k, lv in specs])[:-1])])
     np.testing.assert_allclose(got["cat_params"], want_c, rtol=1e-6, atol=1e-7)
+
+
+def test_lmc_mixed_python_path(tmp_path):
+    """MultiOutputLMCGP with a mixed latent (Matern-5/2 on the continuous
+    column x EHH on the categorical column 1) beside a plain RBF latent: fit,
+    the constrained categorical parameters in the result, the predictive mean
+    against the dense posterior at the trained state (CPU restatement; the
+    Matern leaf's default dimensions are the continuous columns), the model
+    file (constrained parameters, as the reference writes them) and
+    predictions after reload; fixed observation noise is refused for mixed
+    latents, as in the reference."""
+    from mojogp_amd import EHH, Matern52, MultiOutputLMCGP, RBF
+    from oracle import categorical as oc
+    rng = np.random.default_rng(83)
+    n, T, L = 240, 2, 3
+    X = np.c_[rng.uniform(0, 1, n), rng.integers(0, L, n)].astype(np.float32)
+    Y = np.stack([np.sin(4 * X[:, 0]) + 0.4 * X[:, 1], np.cos(3 * X[:, 0]) - 0.3 * X[:, 1]], 1)
+    Y = (Y + 0.05 * rng.normal(size=(n, T))).astype(np.float32)
+    Xs = np.c_[rng.uniform(0, 1, 30), rng.integers(0, L, 30)].astype(np.float32)
+    print("lmc python path with a mixed latent", flush=True)
+    gp = MultiOutputLMCGP([RBF(), Matern52() * EHH(L, active_dims=[1])], cg_tolerance=1e-5,
+                          max_cg_iterations=600, preconditioner_rank=10)
+    with pytest.raises(NotImplementedError, match="fixed_observation_noise"):
+        gp.fit(X, Y, max_iterations=2, fixed_observation_noise=np.full((n, T), 0.01, np.float32))
+    tr = gp.fit(X, Y, max_iterations=8, method="matrix_free")
+    assert np.all(np.isfinite(tr.nll_history)) and tr.iterations == 8
+    theta = np.asarray(tr.cat_params_per_latent[1])
+    assert theta.shape == (3,) and np.all((theta > 0) & (theta < np.pi))
+    assert len(tr.cat_param_names_per_latent[1]) == 3
+    mean = gp.predict(Xs, variance_method="mean_only").mean
+    # dense posterior mean at the trained parameters
+    node = (Matern52(active_dims=[0]) * EHH(L, active_dims=[1])).to_dict()
+    tree = ok.TreeKernel(node, 2, [oc.correlation(oc.EHH, L, theta.astype(np.float64))])
+    p0 = np.asarray(tr.params_per_latent[0], np.float64)
+    p1 = np.asarray(tr.params_per_latent[1], np.float64)
+    Ks = [ok.kernel_matrix(ok.RBF, X, X, p0, False), tree.matrix(X, X, p1)]
+    Kx = [ok.kernel_matrix(ok.RBF, Xs, X, p0, False), tree.matrix(Xs, X, p1)]
+    Kf = ol.dense_operator(Ks, tr.A_matrices, tr.noise_per_task)
+    yc = (Y - np.asarray(tr.mean_per_task)[None, :]).T.reshape(-1)
+    al = np.linalg.solve(Kf, yc).reshape(T, n)
+    want = sum((Kx[s] @ al.T) @ np.asarray(tr.A_matrices[s], np.float64).T for s in range(2))
+    want = want + np.asarray(tr.mean_per_task)[None, :]
+    err = np.max(np.abs(mean - want)) / np.max(np.abs(want))
+    print(f"  mean vs dense posterior: {err:.2e}", flush=True)
+    assert err <= 2e-3
+    m1, v1 = gp.predict(Xs, return_var=True)
+    assert np.all(np.isfinite(m1)) and np.all(v1 > 0)
+    path = str(tmp_path / "lmc_mixed")
+    gp.save(path)
+    arr = np.load(path + "_arrays.npz")
+    np.testing.assert_array_equal(arr["cat_params_latent_1"], theta.astype(np.float32))
+    g2 = MultiOutputLMCGP.load(path)
+    m2, v2 = g2.predict(Xs, return_var=True)
+    print(f"  reload: mean {np.max(np.abs(m2 - m1)):.2e} var {np.max(np.abs(v2 - v1)):.2e}",
+          flush=True)
+    np.testing.assert_allclose(m2, m1, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(v2, v1, rtol=1e-3, atol=1e-6)

@@ -155,3 +155,22 @@ def test_train_mixed_patience_counts_improving_steps_after_20():
     obj = _Scripted(X.shape[0], Y.shape[0], nll_seq=np.linspace(5.0, 1.0, 30))
     res, _ = _train(obj, X, Y, 30, early_stop_tol=0.0, early_stop_patience=3)
     assert not res["converged"] and res["iterations"] == 30
+
+
+@pytest.mark.parametrize("kind", [oc.GD, oc.CR, oc.EHH, oc.HH, oc.FE])
+def test_cat_raw_from_constrained_inverts_the_transform(kind):
+    """Models store constrained categorical parameters (the reference's
+    cat_params_latent_s); loading recovers the raw values through
+    kernel.cat_raw_from_constrained, the inverse of the oracle's constrain."""
+    from mojogp_amd.kernel import KernelType, cat_raw_from_constrained
+    kt = {oc.GD: KernelType.GD, oc.CR: KernelType.CR, oc.EHH: KernelType.EHH,
+          oc.HH: KernelType.HH, oc.FE: KernelType.FE}[kind]
+    L = 4
+    rng = np.random.default_rng(kind)
+    raw = (oc.default_raw(kind, L) + rng.uniform(-1.5, 1.5, oc.num_params(kind, L))).astype(F32)
+    theta = oc.constrain(kind, L, raw)
+    back = cat_raw_from_constrained(kt, L, theta.astype(F32))
+    np.testing.assert_allclose(back, raw, rtol=1e-5, atol=2e-6)
+    # the tables from the recovered values match the stored state
+    np.testing.assert_allclose(oc.correlation(kind, L, oc.constrain(kind, L, back)),
+                               oc.correlation(kind, L, theta), rtol=0, atol=2e-6)
