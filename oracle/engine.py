@@ -81,7 +81,7 @@ def _xorshift64(state: int) -> int:
 
 def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32, method: int = 0,
                      error_tol: float = 0.0, adaptive_tol: float = 0.01, seed: int = 42,
-                     noise: float = 0.0, diag_value=None):
+                     noise: float = 0.0, diag_value=None, diag_init=None):
     """Pivoted Cholesky of the kernel matrix K (no noise). Returns (L [n,k], k).
 
     Restates build_pivoted_cholesky_precond_unified
@@ -95,10 +95,14 @@ def pivoted_cholesky(K: np.ndarray, rank: int, dtype=np.float32, method: int = 0
     Runs at the reference's working precision (fp32 by default): the residual
     diagonal of far-away points rounds to exactly the outputscale, so many
     entries tie and the lowest index wins; a float64 run breaks those ties
-    differently and picks other pivots."""
+    differently and picks other pivots.
+
+    ``diag_init``: the residual diagonal the provider reports, when it is not
+    the matrix's own diagonal (the Kronecker operator of the mixed ICM)."""
     n = K.shape[0]
     Kd = np.asarray(K).astype(dtype)
-    diag = np.diag(Kd).copy()
+    diag = (np.diag(Kd).copy() if diag_init is None
+            else np.asarray(diag_init).astype(dtype).copy())
     dval = dtype(diag_value if diag_value is not None else diag.max())
     mask = np.ones(n, dtype=bool)
     L = np.zeros((n, rank), dtype=dtype)
@@ -271,6 +275,20 @@ def bbmm_step(kind: int, ard: bool, X, y_c, params, noise: float, P: Precond | N
     K = ok.kernel_matrix(kind, X, X, params, ard)
     A = K + (np.diag(np.asarray(noise_vec, np.float64)) if noise_vec is not None
              else noise * np.eye(n))
+    G = ok.kernel_gradients(kind, X, X, params, ard)
+    return bbmm_dense(A, G, y_c, P, num_probes, max_cg, max_tridiag, tol, iteration, x_warm)
+
+
+def bbmm_dense(A: np.ndarray, dAs, y_c, P: Precond | None, num_probes: int, max_cg: int,
+               max_tridiag: int, tol: float, iteration: int,
+               x_warm: np.ndarray | None = None):
+    """One BBMM evaluation (bbmm_with_precond, combined_inv_quad_logdet.mojo:
+    452-1140) of a dense operator A [N, N] with parameter derivatives dAs
+    (each [N, N]); the last gradient is the one of a unit diagonal (the noise).
+    Returns the NLL per entry, the gradients, alpha, the CG state and the
+    factors U (probe solutions at the raw probe scale), W (P^-1 of the raw
+    probes) and Zn (unit-norm probes)."""
+    n = A.shape[0]
     T = num_probes
     seed = iteration * 104729 + 42
     if P is not None:
@@ -296,9 +314,8 @@ def bbmm_step(kind: int, ard: bool, X, y_c, params, noise: float, P: Precond | N
     W = Zn * pnorm
     if P is not None:
         W = P.apply(W)
-    G = ok.kernel_gradients(kind, X, X, params, ard)
     grads = []
-    for g in G:
+    for g in dAs:
         data = alpha @ g @ alpha
         trace = np.sum(U * (g @ W)) if T > 0 else 0.0
         grads.append((-0.5 * data + 0.5 * trace / max(T, 1)) / n)
@@ -308,7 +325,7 @@ def bbmm_step(kind: int, ard: bool, X, y_c, params, noise: float, P: Precond | N
     rowdot = -0.5 * alpha * alpha + (0.5 / max(T, 1)) * np.sum(U * W, axis=1)
     return {"nll": nll, "inv_quad": inv_quad, "logdet": logdet, "grads": np.array(grads),
             "alpha": alpha, "x": x, "cg_iterations": iters, "converged": conv,
-            "rowdot": rowdot, "U": U, "Zn": Zn}
+            "rowdot": rowdot, "U": U, "W": W, "Zn": Zn}
 
 
 # ---------------------------------------------------------------- learned noise

@@ -20,6 +20,12 @@ path, used only to check the gfx950 product (never imported by it):
                     (kernels/jit/jit_engine_multi_output_bindings.mojo:329-549)
   pathwise          sample_multi_output_pathwise_python (:552-712) is the LMC
                     correction with one latent and A = B: oracle.lmc.pathwise_correction
+  kron_pivot_precond / mixed_gradients / train_mixed
+                    the mixed continuous x categorical ICM
+                    (kernels/jit/jit_multi_output_mixed.mojo:477-1148): the
+                    single-output BBMM of the full operator under a pivoted
+                    Cholesky of that operator, categorical raw parameters
+                    trained beside the ICM ones
 
 What pins each piece (tests/test_oracle_icm.py): jacobi_eigen against
 numpy.linalg.eigh and the reconstruction V diag(e) V^T; the preconditioner's
@@ -341,6 +347,248 @@ def train(kind: int, ard: bool, X, Y_blocked, init_params, init_noise, init_os, 
             "cg_iterations_history": np.array(cg_hist), "final_nll": float(best_seen),
             "iterations": iterations, "converged": converged, "precond_rebuild_count": rebuilds,
             "W": W, "raw_v": raw_v}
+
+
+# ---------------------------------------------------------------- mixed categorical
+def kron_pivot_precond(K, os: float, B, noise, rank: int, method: int = 0) -> oe.Precond:
+    """The mixed ICM's preconditioner (jit_multi_output_mixed.mojo:594-611,
+    741-755): build_pivoted_cholesky_precond_unified over the full Kronecker
+    operator (KroneckerDirectProvider, kronecker_direct_provider.mojo:182-209,
+    338-386, 511-553).  Its columns are forward products of unit vectors
+    minus the provider noise at the pivot, i.e. columns of
+    os (B (x) K) + diag(noise_s - min_t noise_t); the provider noise is the
+    smallest task noise; the residual diagonal starts at os B_ss (the provider
+    reports a base-kernel diagonal of 1) and the error normaliser is
+    max_s os B_ss.  P = L L^T + min noise I."""
+    K = np.asarray(K, np.float64)
+    n = K.shape[0]
+    B = np.asarray(B, F32).astype(np.float64)
+    noise = np.asarray(noise, F32)
+    T = noise.size
+    nmin = F32(noise.min())
+    os32 = F32(os)
+    Kf = float(os32) * np.kron(B, K) + np.diag(np.repeat((noise - nmin).astype(np.float64), n))
+    dB = (os32 * np.diag(np.asarray(B, F32))).astype(F32)
+    L, _ = oe.pivoted_cholesky(Kf, rank, method=method,
+                               error_tol=0.0 if method == 0 else 1e-3, noise=float(nmin),
+                               diag_value=float(dB.max()), diag_init=np.repeat(dB, n))
+    return oe.Precond(L, float(nmin))
+
+
+def mixed_gradients(K, os: float, ev, n: int, T: int):
+    """Task-covariance and per-task noise gradients of the mixed ICM
+    (jit_multi_output_mixed.mojo:815-885) from one evaluation of the full
+    operator: G_B[s][t] = 0.5 os (-a_s^T K a_t + (1/P) sum_j u_js^T K w_jt) / nT
+    (before the +-10 clip; u: probe solutions, w: P^-1 probes) and
+    g_noise[t] = 0.5 (-a_t^T a_t + (1/P) sum_j u_jt^T w_jt) / nT."""
+    K = np.asarray(K, np.float64)
+    a = np.asarray(ev["alpha"], np.float64).reshape(T, n)
+    U = np.asarray(ev["U"], np.float64)
+    W = np.asarray(ev["W"], np.float64)
+    P = U.shape[1]
+    GB = -(a @ K @ a.T)
+    gn = -np.sum(a * a, axis=1)
+    for j in range(P):
+        u = U[:, j].reshape(T, n)
+        w = W[:, j].reshape(T, n)
+        GB += (u @ K @ w.T) / P
+        gn += np.sum(u * w, axis=1) / P
+    return 0.5 * float(os) * GB / (n * T), 0.5 * gn / (n * T)
+
+
+def train_mixed(node: dict, X, Y_blocked, init_params, init_noise, init_os, init_mean,
+                cat_specs, init_cat_raw, *, task_rank=-1, max_iterations=100,
+                learning_rate=0.05, num_probes=10, max_cg=200, max_tridiag=30, cg_tol=1e-2,
+                precond_rank=15, precond_method=0, rebuild_threshold=0.5,
+                use_cosine_lr=False, early_stop_patience=15, early_stop_tol=1e-4,
+                evaluate=None):
+    """train_multi_output_mixed_jit restated (jit_multi_output_mixed.mojo:477-1148):
+    the ICM parametrisation (kernel parameters, outputscale, per-task noise,
+    W, raw_v, means; one Adam moment array in that order) plus the raw
+    categorical parameters of the kernel tree's categorical leaves (their own
+    moments, the same step count), on the single-output BBMM of the full
+    operator os (B (x) K) + D (oracle.engine.bbmm_dense) under
+    kron_pivot_precond.  This loop's rules: kernel, outputscale, noise and W
+    gradients are not clipped (G_B is, at +-10; the mean gradient at +-100);
+    categorical gradients are (-0.5 a^T dK a + (0.5/P) sum_j u_j^T dK zn_j)
+    times the transform's chain derivative, dK = os (B (x) dK_X), neither
+    divided by nT nor clipped; rebuild after iteration 0 when a kernel
+    parameter, a constrained categorical parameter, the outputscale, a task
+    noise or an entry of B moved by more than the threshold; no NaN handling;
+    best-NLL snapshot; early stop after early_stop_patience evaluations not
+    below the best by early_stop_tol; cosine rate optional.  Float32 host
+    scalars as the reference.
+
+    Test hook: ``evaluate(it, tree, params, os, B, noise, y_c, cat_raw)``
+    replaces the evaluation; it returns ``nll``, ``grads`` (kernel params then
+    outputscale), ``alpha``, ``G_B`` (before the clip), ``noise_grads``,
+    ``cat_grads`` and ``cg_iterations``."""
+    from . import categorical as oc
+    sp, isp = oe._softplus, oe._inv_softplus
+    X = np.asarray(X, np.float64)
+    n, d = X.shape
+    T = len(init_noise)
+    R = T if task_rank < 0 else task_rank
+    P_ = len(init_params)
+    Y = np.asarray(Y_blocked, F32).reshape(T, n)
+    raw_p = np.array([isp(F32(v)) for v in init_params], F32)
+    raw_os = isp(F32(init_os))
+    raw_noise = np.array([isp(F32(v)) for v in init_noise], F32)
+    raw_mean = np.asarray(init_mean, F32).copy()
+    rcat = np.asarray(init_cat_raw, F32).copy()
+    W = init_w(T, R)
+    raw_v = np.zeros(T, F32)
+    total = P_ + 1 + T + T * R + T + T
+    madam, vadam = np.zeros(total, F32), np.zeros(total, F32)
+    mcat, vcat = np.zeros(rcat.size, F32), np.zeros(rcat.size, F32)
+    b1, b2, eps = F32(0.9), F32(0.999), F32(1e-8)
+    sig = lambda x: F32(1.0) / (F32(1.0) + F32(np.exp(-F32(x))))  # noqa: E731
+
+    def constrained(raw):
+        return np.array([sp(F32(v)) for v in raw], F32)
+
+    def constrained_cat(rc):
+        out, off = [], 0
+        for kind, L in cat_specs:
+            k = oc.num_params(kind, L)
+            out.append(oc.constrain(kind, L, rc[off:off + k]))
+            off += k
+        return np.concatenate(out).astype(F32) if out else np.zeros(0, F32)
+
+    def tree(rc):
+        tabs, off = [], 0
+        for kind, L in cat_specs:
+            k = oc.num_params(kind, L)
+            tabs.append(oc.correlation(kind, L, oc.constrain(kind, L, rc[off:off + k])))
+            off += k
+        return ok.TreeKernel(node, d, tabs or None)
+
+    def build(params, rc, os_, B_, noise_):
+        if precond_rank <= 0 or evaluate is not None:
+            return None
+        K = tree(rc).matrix(X, X, np.asarray(params, np.float64))
+        return kron_pivot_precond(K, os_, B_, noise_, precond_rank, precond_method)
+
+    # initial preconditioner: the given kernel parameters, round-tripped
+    # outputscale and noise (:566-611)
+    os0 = sp(raw_os)
+    noise0 = constrained(raw_noise)
+    B = task_b(W, raw_v)
+    P = build(np.asarray(init_params, F32), rcat, os0, B, noise0)
+    last = (np.asarray(init_params, F32).copy(), constrained_cat(rcat), os0, noise0.copy(),
+            B.copy())
+    rebuilds = 0
+    best_nll, best_seen, patience = F32(1e30), F32(1e30), 0
+    best = (raw_p.copy(), raw_os, raw_noise.copy(), raw_mean.copy(), rcat.copy(), B.copy(),
+            np.zeros(n * T))
+    hist, cg_hist = [], []
+    converged, iterations, t_step = False, 0, 1
+    x_prev = None
+
+    def adam(mm, vv, idx, g, lr):
+        mm[idx] = b1 * mm[idx] + (F32(1) - b1) * F32(g)
+        vv[idx] = b2 * vv[idx] + (F32(1) - b2) * F32(g) * F32(g)
+        mh = mm[idx] / (F32(1) - F32(b1 ** t_step))
+        vh = vv[idx] / (F32(1) - F32(b2 ** t_step))
+        return F32(-F32(lr) * mh / (np.sqrt(vh) + eps))
+
+    rel = lambda a, b: (float(np.max(np.abs(np.asarray(b, F32) - np.asarray(a, F32))  # noqa: E731
+                                      / (np.abs(np.asarray(a, F32)) + F32(1e-8))))
+                        if np.size(a) else 0.0)
+    for it in range(max_iterations):
+        iterations = it + 1
+        params = constrained(raw_p)
+        cc = constrained_cat(rcat)
+        os_ = sp(raw_os)
+        noise = constrained(raw_noise)
+        B = task_b(W, raw_v)
+        tr = tree(rcat)
+        rebuild = False
+        if it > 0:
+            mr = max(rel(last[0], params), rel(last[1], cc), rel([last[2]], [os_]),
+                     rel(last[3], noise), rel(last[4], B))
+            rebuild = mr > rebuild_threshold
+        if rebuild:
+            P = build(params, rcat, os_, B, noise)
+            last = (params.copy(), cc.copy(), os_, noise.copy(), B.copy())
+            rebuilds += 1
+        yc = (Y - raw_mean[:, None]).reshape(-1)
+        if evaluate is not None:
+            ev = evaluate(it, tr, params, os_, B, noise, yc, rcat.copy())
+        else:
+            K = tr.matrix(X, X, params.astype(np.float64))
+            Bd = np.asarray(B, F32).astype(np.float64)
+            os32 = float(F32(os_))
+            A = os32 * np.kron(Bd, K) + np.diag(np.repeat(noise.astype(np.float64), n))
+            dAs = [os32 * np.kron(Bd, g) for g in tr.gradients(X, X, params.astype(np.float64))]
+            dAs.append(np.kron(Bd, K))
+            warm = None
+            if it > 0 and not rebuild and x_prev is not None:
+                warm = x_prev.copy()
+                warm[:, 1:] = 0.0
+            ev = oe.bbmm_dense(A, dAs, yc.astype(np.float64), P, num_probes, max_cg,
+                               max_tridiag, cg_tol, it, warm)
+            ev["grads"] = ev["grads"][:-1]  # kernel params then outputscale
+            ev["G_B"], ev["noise_grads"] = mixed_gradients(K, os_, ev, n, T)
+            if rcat.size:
+                ev["cat_grads"] = ol.cat_gradients(tr, X, params, os32 * Bd, cat_specs, rcat,
+                                                   ev, clip=None, per_entry=False)
+            x_prev = ev["x"]
+        nll = F32(ev["nll"])
+        hist.append(float(nll))
+        cg_hist.append(int(ev["cg_iterations"]))
+        if nll < best_seen:
+            best_seen = nll
+            best = (raw_p.copy(), raw_os, raw_noise.copy(), raw_mean.copy(), rcat.copy(),
+                    B.copy(), np.asarray(ev["alpha"]).copy())
+        GB = np.clip(np.asarray(ev["G_B"], F32), -10, 10).astype(F32)
+        lr = learning_rate
+        if use_cosine_lr:
+            lr = oe.cosine_lr(learning_rate, it, max_iterations)
+        if rcat.size:
+            g = np.asarray(ev["cat_grads"], F32)
+            for k in range(rcat.size):
+                rcat[k] += adam(mcat, vcat, k, g[k], lr)
+        ai = 0
+        for p in range(P_):
+            raw_p[p] += adam(madam, vadam, ai, F32(ev["grads"][p]) * sig(raw_p[p]), lr)
+            ai += 1
+        raw_os = F32(raw_os + adam(madam, vadam, ai, F32(ev["grads"][P_]) * sig(raw_os), lr))
+        ai += 1
+        for t in range(T):
+            raw_noise[t] += adam(madam, vadam, ai, F32(ev["noise_grads"][t]) * sig(raw_noise[t]),
+                                 lr)
+            ai += 1
+        for s_ in range(T):
+            for r in range(R):
+                gw = F32(0.0)
+                for t in range(T):
+                    gw = F32(gw + GB[s_, t] * W[t, r])
+                W[s_, r] += adam(madam, vadam, ai, F32(2.0) * gw, lr)
+                ai += 1
+        for t in range(T):
+            raw_v[t] += adam(madam, vadam, ai, GB[t, t] * sig(raw_v[t]), lr)
+            ai += 1
+        al = np.asarray(ev["alpha"]).reshape(T, n)
+        for t in range(T):
+            g = oe._clip(F32(-np.sum(al[t].astype(F32), dtype=F32)) / F32(n * T))
+            raw_mean[t] += adam(madam, vadam, ai, g, lr)
+            ai += 1
+        t_step += 1
+        if early_stop_tol > 0:
+            if nll < best_nll - F32(early_stop_tol):
+                best_nll, patience = nll, 0
+            else:
+                patience += 1
+                if patience >= early_stop_patience:
+                    converged = True
+                    break
+    bp, bos, bn, bm, bc, bB, balpha = best
+    return {"params": constrained(bp), "outputscale": sp(bos), "noise": constrained(bn),
+            "mean": bm, "cat_raw": bc, "B": bB, "alpha": balpha, "nll_history": np.array(hist),
+            "cg_iterations_history": np.array(cg_hist), "final_nll": float(best_seen),
+            "iterations": iterations, "converged": converged, "precond_rebuild_count": rebuilds,
+            "task_rank": R}
 
 
 # ---------------------------------------------------------------- prediction

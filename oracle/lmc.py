@@ -378,7 +378,8 @@ def train(kinds, ards, X, Y_blocked, init_params, init_noise, init_mean, *, trai
             "iterations": iterations, "converged": converged}
 
 
-def cat_gradients(tree_s, X, params_s, A_s, cat_specs, raw_cat, ev, clip=10.0):
+def cat_gradients(tree_s, X, params_s, A_s, cat_specs, raw_cat, ev, clip=10.0,
+                  per_entry=True):
     """Categorical raw-parameter gradients of one mixed latent
     (jit_lmc_mixed.mojo:1259-1327): for each constrained parameter theta_k of a
     categorical leaf, dK = A_s (x) (dK_s/dR o dR/dtheta_k) and
@@ -386,7 +387,8 @@ def cat_gradients(tree_s, X, params_s, A_s, cat_specs, raw_cat, ev, clip=10.0):
     with the probe solutions u_j (scaled by their probe norms) and the
     unit-norm probes zn_j of the evaluation, times the transform's chain
     derivative.  Returns the raw gradients (float32, concatenated over the
-    leaves)."""
+    leaves).  per_entry=False, clip=None: the mixed ICM's form (the estimator
+    neither divided by N nor clipped, jit_multi_output_mixed.mojo:911-960)."""
     from . import categorical as oc
     D, lv = tree_s.cat_leaf_derivatives(X, X, np.asarray(params_s, np.float64))
     alpha, U, Zn = ev["alpha"], ev["U"], ev["Zn"]
@@ -407,8 +409,9 @@ def cat_gradients(tree_s, X, params_s, A_s, cat_specs, raw_cat, ev, clip=10.0):
             val = -0.5 * alpha @ dK @ alpha
             if Pn > 0:
                 val += 0.5 / Pn * np.sum(U * (dK @ Zn))
-            g = F32(val / N)
-            g = F32(clip) if g > clip else (F32(-clip) if g < -clip else g)
+            g = F32(val / N) if per_entry else F32(val)
+            if clip is not None:
+                g = F32(clip) if g > clip else (F32(-clip) if g < -clip else g)
             out.append(F32(g * F32(chain[k])))
         off += K
     return np.array(out, F32)
