@@ -597,6 +597,29 @@ MGP_API int mgp_icm_train(void* provider, int T, const float* y_blocked,
                           const mgp_icm_train_opts_t* opts, mgp_progress_cb cb,
                           void* user, mgp_icm_train_result_t* out);
 
+/* Mixed continuous x categorical ICM on a kernel-tree provider with
+ * categorical leaves: mgp_icm_train's parameters (every one trained, no
+ * fixed noise) plus the raw correlation parameters of the leaves, trained by
+ * Adam moments of their own on (-0.5 a^T dK a + (0.5/P) sum_j u_j^T dK zn_j)
+ * times the transform's chain derivative with dK = os (B (x) dK_X), neither
+ * divided by nT nor clipped.  The evaluation is the single-output BBMM of the
+ * full operator os (B (x) K) + D preconditioned by a pivoted Cholesky of that
+ * operator (columns from unit-vector products, a base diagonal of 1, the
+ * smallest task noise).  cat_kinds[ncat]: the leaves' kinds (0 GD, 1 CR,
+ * 2 EHH, 3 HH, 4 FE) in tree order; init_cat_raw[ncat_params]: their raw
+ * parameters; cat_raw_out[ncat_params] (may be NULL): the best raw values.
+ * The provider ends with the best parameters and tables.  Replaces
+ * train_multi_output_mixed() (train_multi_output_mixed_python,
+ * jit_engine_multi_output_bindings.mojo:953-1200 ->
+ * train_multi_output_mixed_jit, kernels/jit/jit_multi_output_mixed.mojo:477-1148). */
+MGP_API int mgp_icm_train_mixed(void* provider, int T, const float* y_blocked,
+                                const float* init_params, const float* init_noise,
+                                float init_outputscale, const float* init_mean,
+                                const int* cat_kinds, int ncat, const float* init_cat_raw,
+                                int ncat_params, const mgp_icm_train_opts_t* opts,
+                                mgp_progress_cb cb, void* user, mgp_icm_train_result_t* out,
+                                float* cat_raw_out);
+
 /* Mean [m][T] (and variance [m][T] for variance_method 1 LOVE / 2 exact)
  * from the rotated posterior state: alpha_rot [T][n] (eigen-task s's
  * weights in row s), Q [T][T] row-major and scales[T] the eigenvectors and

@@ -239,6 +239,10 @@ _SIGNATURES = {
     "mgp_icm_train": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_float_p, c_int_p, c_float_p,
                                 C.c_float, c_float_p, c_float_p, C.POINTER(ICMTrainOpts),
                                 PROGRESS_CB, C.c_void_p, C.POINTER(ICMTrainResult)]),
+    "mgp_icm_train_mixed": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_float_p, c_float_p,
+                                      C.c_float, c_float_p, c_int_p, C.c_int, c_float_p,
+                                      C.c_int, C.POINTER(ICMTrainOpts), PROGRESS_CB,
+                                      C.c_void_p, C.POINTER(ICMTrainResult), c_float_p]),
     "mgp_icm_predict": (C.c_int, [C.c_void_p, C.c_int, c_float_p, c_float_p, c_float_p,
                                   c_float_p, C.c_int64, C.c_float, C.c_int, C.c_int, C.c_float,
                                   C.c_int, C.c_int, c_float_p, c_float_p]),

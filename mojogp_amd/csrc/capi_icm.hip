@@ -34,6 +34,64 @@ void icm_model(LMCModel& m, Provider* pv, int T, float os, const float* B, const
   if (fixed) m.fixed.assign(fixed, fixed + (size_t)m.n * T);
 }
 
+ICMTrainOptions icm_options(const mgp_icm_train_opts_t* opts) {
+  ICMTrainOptions o;
+  o.max_iterations = opts->max_iterations;
+  o.learning_rate = opts->learning_rate;
+  o.task_rank = opts->task_rank;
+  o.num_probes = opts->num_probes;
+  o.max_cg_iter = opts->max_cg_iter;
+  o.cg_tol = opts->cg_tol;
+  o.precond_rank = opts->precond_rank;
+  o.precond_method = opts->precond_method;
+  o.precond_rebuild_threshold = opts->precond_rebuild_threshold;
+  o.max_tridiag_iter = opts->max_tridiag_iter;
+  o.early_stop_patience = opts->early_stop_patience;
+  o.early_stop_tol = opts->early_stop_tol;
+  o.use_cosine_lr = opts->use_cosine_lr != 0;
+  o.progress_interval = opts->progress_interval;
+  if (o.num_probes < 0 || o.max_cg_iter < 1 || o.max_tridiag_iter < 0)
+    throw Error(ST_INVALID, "bad CG settings");
+  return o;
+}
+
+std::function<void(const ProgressEvent&)> icm_progress(mgp_progress_cb cb, void* user) {
+  if (!cb) return {};
+  return [cb, user](const ProgressEvent& e) {
+    mgp_progress_t p;
+    p.phase = e.phase;
+    p.current = e.current;
+    p.total = e.total;
+    p.nll = e.nll;
+    p.best_nll = e.best_nll;
+    p.cg_iter = e.cg_iter;
+    p.iter_ms = e.iter_ms;
+    p.noise = e.noise;
+    p.mean = e.mean;
+    p.precond_rank = e.precond_rank;
+    p.precond_rebuild_count = e.precond_rebuild_count;
+    p.converged = e.converged ? 1 : 0;
+    cb(&p, user);
+  };
+}
+
+void put_icm_result(const ICMTrainResult& r, mgp_icm_train_result_t* out) {
+  copy_to(out->params, r.params);
+  copy_to(out->noise, r.noise);
+  copy_to(out->mean, r.mean);
+  copy_to(out->B, r.B);
+  copy_to(out->alpha, r.alpha);
+  out->history_len = copy_to(out->nll_history, r.nll_history);
+  copy_to(out->cg_iterations_history, r.cg_iterations_history);
+  copy_to(out->iter_times_ms, r.iter_times_ms);
+  out->outputscale = r.outputscale;
+  out->final_nll = r.final_nll;
+  out->iterations = r.iterations;
+  out->converged = r.converged ? 1 : 0;
+  out->task_rank = r.task_rank;
+  out->precond_rebuild_count = r.precond_rebuild_count;
+}
+
 }  // namespace
 
 extern "C" {
@@ -49,42 +107,7 @@ int mgp_icm_train(void* provider, int T, const float* y_blocked, const float* in
       throw Error(ST_INVALID, "null argument");
     if (T < 1) throw Error(ST_INVALID, "num_tasks must be >= 1");
     const int P = pv->nparams;
-    ICMTrainOptions o;
-    o.max_iterations = opts->max_iterations;
-    o.learning_rate = opts->learning_rate;
-    o.task_rank = opts->task_rank;
-    o.num_probes = opts->num_probes;
-    o.max_cg_iter = opts->max_cg_iter;
-    o.cg_tol = opts->cg_tol;
-    o.precond_rank = opts->precond_rank;
-    o.precond_method = opts->precond_method;
-    o.precond_rebuild_threshold = opts->precond_rebuild_threshold;
-    o.max_tridiag_iter = opts->max_tridiag_iter;
-    o.early_stop_patience = opts->early_stop_patience;
-    o.early_stop_tol = opts->early_stop_tol;
-    o.use_cosine_lr = opts->use_cosine_lr != 0;
-    o.progress_interval = opts->progress_interval;
-    if (o.num_probes < 0 || o.max_cg_iter < 1 || o.max_tridiag_iter < 0)
-      throw Error(ST_INVALID, "bad CG settings");
-    std::function<void(const ProgressEvent&)> progress;
-    if (cb) {
-      progress = [cb, user](const ProgressEvent& e) {
-        mgp_progress_t p;
-        p.phase = e.phase;
-        p.current = e.current;
-        p.total = e.total;
-        p.nll = e.nll;
-        p.best_nll = e.best_nll;
-        p.cg_iter = e.cg_iter;
-        p.iter_ms = e.iter_ms;
-        p.noise = e.noise;
-        p.mean = e.mean;
-        p.precond_rank = e.precond_rank;
-        p.precond_rebuild_count = e.precond_rebuild_count;
-        p.converged = e.converged ? 1 : 0;
-        cb(&p, user);
-      };
-    }
+    const ICMTrainOptions o = icm_options(opts);
     std::vector<float> ip(init_params, init_params + P);
     std::vector<char> tm(P);
     for (int p = 0; p < P; ++p) tm[p] = trainable[p] != 0;
@@ -92,21 +115,34 @@ int mgp_icm_train(void* provider, int T, const float* y_blocked, const float* in
     std::vector<float> fixed;
     if (fixed_noise) fixed.assign(fixed_noise, fixed_noise + (size_t)pv->n * T);
     ICMTrainResult r = icm_train(*pv, T, y_blocked, ip, tm, noise0, init_outputscale, mean0,
-                                 fixed, o, progress);
-    copy_to(out->params, r.params);
-    copy_to(out->noise, r.noise);
-    copy_to(out->mean, r.mean);
-    copy_to(out->B, r.B);
-    copy_to(out->alpha, r.alpha);
-    out->history_len = copy_to(out->nll_history, r.nll_history);
-    copy_to(out->cg_iterations_history, r.cg_iterations_history);
-    copy_to(out->iter_times_ms, r.iter_times_ms);
-    out->outputscale = r.outputscale;
-    out->final_nll = r.final_nll;
-    out->iterations = r.iterations;
-    out->converged = r.converged ? 1 : 0;
-    out->task_rank = r.task_rank;
-    out->precond_rebuild_count = r.precond_rebuild_count;
+                                 fixed, o, icm_progress(cb, user));
+    put_icm_result(r, out);
+  });
+}
+
+int mgp_icm_train_mixed(void* provider, int T, const float* y_blocked, const float* init_params,
+                        const float* init_noise, float init_outputscale, const float* init_mean,
+                        const int* cat_kinds, int ncat, const float* init_cat_raw,
+                        int ncat_params, const mgp_icm_train_opts_t* opts, mgp_progress_cb cb,
+                        void* user, mgp_icm_train_result_t* out, float* cat_raw_out) {
+  return guarded([&] {
+    Provider* pv = provider_of(provider);
+    if (!y_blocked || !init_params || !init_noise || !init_mean || !opts || !out)
+      throw Error(ST_INVALID, "null argument");
+    if (T < 1) throw Error(ST_INVALID, "num_tasks must be >= 1");
+    if (ncat < 1 || !cat_kinds) throw Error(ST_INVALID, "cat_kinds must name every categorical leaf");
+    if (ncat_params < 0 || (ncat_params > 0 && !init_cat_raw))
+      throw Error(ST_INVALID, "init_cat_raw must hold ncat_params values");
+    const int P = pv->nparams;
+    const ICMTrainOptions o = icm_options(opts);
+    std::vector<float> ip(init_params, init_params + P);
+    std::vector<float> noise0(init_noise, init_noise + T), mean0(init_mean, init_mean + T);
+    std::vector<int> kinds(cat_kinds, cat_kinds + ncat);
+    std::vector<float> raw0(init_cat_raw, init_cat_raw + ncat_params);
+    ICMMixedResult r = icm_train_mixed(*pv, T, y_blocked, ip, noise0, init_outputscale, mean0,
+                                       kinds, raw0, o, icm_progress(cb, user));
+    put_icm_result(r, out);
+    copy_to(cat_raw_out, r.cat_raw);
   });
 }
 

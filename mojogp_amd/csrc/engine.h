@@ -38,6 +38,9 @@ struct Precond {
 // stop; rpcholesky / nystrom: error_tol 1e-3; adaptive_tol 0.01; seed 42).
 PivotOptions training_pivot_options(int method);
 void build_precond(Provider& pv, int rank, const PivotOptions& po, Precond& P);
+// Scalar-noise Woodbury pieces (Minv, log|P|) of P = L L^T + P.noise I for a
+// factor already in P.L ([k][n]).
+void precond_from_factor(Precond& P, int64_t n, int k, hipStream_t st);
 
 struct CGWork {
   DevBuf<float> x, r, z, p, Ap;  // [C][n]

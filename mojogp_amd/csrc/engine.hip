@@ -327,6 +327,12 @@ void build_precond(Provider& pv, int rank, const PivotOptions& po, Precond& P) {
     P.logdet = (float)(ld + logdet_spd(M, k));
     return;
   }
+  precond_from_factor(P, n, k, st);
+}
+
+void precond_from_factor(Precond& P, int64_t n, int k, hipStream_t st) {
+  P.rank = k;
+  P.vec = false;
   DevBuf<double> Md;
   Md.ensure((size_t)k * k);
   syrk_ltl(P.L.ptr, n, k, Md.ptr, st);

@@ -72,6 +72,34 @@ ICMTrainResult icm_train(Provider& base, int T, const float* y_blocked_host,
                          const ICMTrainOptions& o,
                          const std::function<void(const ProgressEvent&)>& progress);
 
+// Mixed continuous x categorical ICM (train_multi_output_mixed_jit,
+// kernels/jit/jit_multi_output_mixed.mojo:477-1148): base is a kernel-tree
+// provider with categorical leaves (cat_kinds: one per leaf in tree order;
+// init_cat_raw: their raw parameters).  The evaluation is the single-output
+// BBMM of the full operator os (B (x) K) + D with the single-output probe
+// streams, preconditioned by a pivoted Cholesky of that operator
+// (pivoted_cholesky_kron) with the smallest task noise; the categorical raw
+// parameters train by Adam moments of their own on
+// (-0.5 a^T dK a + (0.5/P) sum_j u_j^T dK zn_j) times the transform's chain
+// derivative, dK = os (B (x) dK_X), neither divided by nT nor clipped; the
+// kernel, outputscale, noise and W gradients are unclipped (G_B at +-10, the
+// mean gradient at +-100); no NaN handling; rebuild when a kernel
+// parameter, a constrained categorical parameter, the outputscale, a task
+// noise or an entry of B moved by more than the threshold (after iteration
+// 0); best-NLL snapshot; early stop on early_stop_patience evaluations not
+// below the best by early_stop_tol.  Every parameter is trained.
+struct ICMMixedResult : ICMTrainResult {
+  std::vector<float> cat_raw;  // best raw categorical parameters
+};
+ICMMixedResult icm_train_mixed(Provider& base, int T, const float* y_blocked_host,
+                               const std::vector<float>& init_params,
+                               const std::vector<float>& init_noise, float init_outputscale,
+                               const std::vector<float>& init_mean,
+                               const std::vector<int>& cat_kinds,
+                               const std::vector<float>& init_cat_raw,
+                               const ICMTrainOptions& o,
+                               const std::function<void(const ProgressEvent&)>& progress);
+
 // Prediction from the rotated posterior state (predict_multi_output_python,
 // jit_engine_multi_output_bindings.mojo:329-549): for each eigen-task s,
 // mean[i][t] += Q[t][s] scale_s (K(X*, X) alpha_rot[s])[i] and, when

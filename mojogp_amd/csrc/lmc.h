@@ -77,7 +77,7 @@ struct LMCPrecond {
   // z = P^{-1} r for C task-blocked columns; rz_part gets the column-dot
   // partials of r.z (fixed chunking of n*T).
   // z = P^-1 r; with rz_part, the partials rz_part[c*nb + b] of r . z.
-  void apply(const float* r, int C, float* z, double* rz_part, int nb, hipStream_t st);
+  virtual void apply(const float* r, int C, float* z, double* rz_part, int nb, hipStream_t st);
   // N(0, P) probes: D^{1/2} eps + U w (counter-hash Gaussians, seeds
   // seed + 1000000 and seed).
   virtual void sample(float* out, int C, uint64_t seed, hipStream_t st);

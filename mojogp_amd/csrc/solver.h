@@ -90,6 +90,19 @@ struct PivotOptions {
 // diagonal) back to the host once per pivot, as the reference does.
 int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
                      hipStream_t st);
+// The same builder over the full Kronecker operator os (B (x) K) + D of a
+// base provider (build_pivoted_cholesky_precond_unified over
+// KroneckerDirectProvider, kronecker_direct_provider.mojo:182-209, 338-386,
+// 511-553): N = n T entries, task-blocked; column p is the forward product of
+// the unit vector e_p minus noise_min at the pivot (os_B[:, t_p] (x) K[:, j_p]
+// plus task_noise[t_p] - noise_min at p); the residual diagonal starts at
+// os_B[s][s] (the provider reports a base diagonal of 1) and the stop rule
+// uses max_s os_B[s][s] and noise_min.  osB_dev / task_noise_dev: device
+// [T][T] and [T]; L: [rank][N].
+int pivoted_cholesky_kron(Provider& base, int T, const float* osB_dev,
+                          const std::vector<float>& osB, const float* task_noise_dev,
+                          float noise_min, int rank, const PivotOptions& o, float* L,
+                          hipStream_t st);
 
 // M = L^T L (k x k, fp64) for the first k columns.
 // M = L^T diag(wt) L when wt (device [n]) is given.

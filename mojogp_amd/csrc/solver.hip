@@ -3,6 +3,8 @@
 // result is bit-reproducible run to run.
 #include "solver.h"
 
+#include <functional>
+
 #include <algorithm>
 #include <cstdint>
 #include <initializer_list>
@@ -1384,86 +1386,62 @@ void gaussian(float* out, int64_t len, uint64_t seed, hipStream_t st) {
   MGP_HIP_CHECK(hipGetLastError());
 }
 
-int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
-                     hipStream_t st) {
-  MGP_REQUIRE(o.method >= 0 && o.method <= 2, "precond_method must be 0, 1 or 2");
-  const int64_t n = pv.n;
-  const int nb = reduction_chunks(n);
+namespace {
+// Device state of one pivoted-Cholesky build over n residual entries.
+struct PivotBufs {
+  int64_t n = 0;
+  int nb = 0;
   DevBuf<float> diag, mask, coef, pvv;
   DevBuf<int64_t> piv;
   DevBuf<double> pa;
   DevBuf<PivotDev> state;
-  diag.ensure(n);
-  mask.ensure(n);
-  coef.ensure(std::max(rank, 1));
-  pvv.ensure(nb);
-  piv.ensure(nb);
-  pa.ensure(nb);
-  state.ensure(1);
-  PivotDev init{0, rank, 0, 0.f, 0.f};
-  MGP_HIP_CHECK(hipMemcpyAsync(state.ptr, &init, sizeof(init), hipMemcpyHostToDevice, st));
-  fill(L, (int64_t)rank * n, 0.0f, st);
-  const float os = pv.kdiag();
-  hipLaunchKernelGGL(k_pc_init, grid1(n), dim3(kBlock), 0, st, diag.ptr, mask.ptr, n, os);
-  if (pv.nonstationary()) pv.diag_values(pv.train, n, diag.ptr);  // extract_diagonal
-  hipLaunchKernelGGL(k_pc_argmax_part, dim3(nb), dim3(kBlock), 0, st, diag.ptr, mask.ptr,
-                     n, nb, pvv.ptr, piv.ptr, pa.ptr);
-  MGP_HIP_CHECK(hipGetLastError());
-  auto launch_column = [&](int m) {
-    const size_t shm = (size_t)(m + pv.d) * sizeof(float);
-    const float* Z = pv.train.z.ptr;
-    const int d = pv.d;
-    const float osk = pv.outputscale();
-    if (pv.is_tree) {
-      hipLaunchKernelGGL(k_pc_column<TreeColumn>, dim3(nb), dim3(kBlock), shm, st,
-                         TreeColumn{pv.tree, pv.tparams.ptr}, Z, d, n, m, L, diag.ptr, mask.ptr,
-                         coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
-    } else if (pv.kind == KIND_RBF) {
-      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_RBF>>, dim3(nb), dim3(kBlock), shm, st,
-                         RadialColumn<KIND_RBF>{osk, d}, Z, d, n, m, L, diag.ptr, mask.ptr,
-                         coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
-    } else if (pv.kind == KIND_MATERN12) {
-      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_MATERN12>>, dim3(nb), dim3(kBlock), shm,
-                         st, RadialColumn<KIND_MATERN12>{osk, d}, Z, d, n, m, L, diag.ptr,
-                         mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
-    } else if (pv.kind == KIND_MATERN32) {
-      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_MATERN32>>, dim3(nb), dim3(kBlock), shm,
-                         st, RadialColumn<KIND_MATERN32>{osk, d}, Z, d, n, m, L, diag.ptr,
-                         mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
-    } else {
-      hipLaunchKernelGGL(k_pc_column<RadialColumn<KIND_MATERN52>>, dim3(nb), dim3(kBlock), shm,
-                         st, RadialColumn<KIND_MATERN52>{osk, d}, Z, d, n, m, L, diag.ptr,
-                         mask.ptr, coef.ptr, state.ptr, nb, pvv.ptr, piv.ptr, pa.ptr);
-    }
-    MGP_HIP_CHECK(hipGetLastError());
-  };
+  PivotBufs(int64_t n_, int rank, float* L, hipStream_t st) : n(n_), nb(reduction_chunks(n_)) {
+    diag.ensure(n);
+    mask.ensure(n);
+    coef.ensure(std::max(rank, 1));
+    pvv.ensure(nb);
+    piv.ensure(nb);
+    pa.ensure(nb);
+    state.ensure(1);
+    PivotDev init{0, rank, 0, 0.f, 0.f};
+    MGP_HIP_CHECK(hipMemcpyAsync(state.ptr, &init, sizeof(init), hipMemcpyHostToDevice, st));
+    fill(L, (int64_t)rank * n, 0.0f, st);
+  }
+};
 
+// Pivot selection and stopping (pivoted_cholesky.mojo:2195-2334) over a
+// residual diagonal already in b.diag / b.mask; launch_column(m) writes
+// column m of L and updates the residual and the argmax partials.
+// diag_value: the provider's diagonal value (stop rule normaliser); noise:
+// the provider noise (Nystrom stop rule).
+int pivot_loop(PivotBufs& b, int rank, const PivotOptions& o, float* L, float diag_value,
+               float noise, hipStream_t st, const std::function<void(int)>& launch_column) {
+  const int64_t n = b.n;
+  const int nb = b.nb;
+  hipLaunchKernelGGL(k_pc_argmax_part, dim3(nb), dim3(kBlock), 0, st, b.diag.ptr, b.mask.ptr,
+                     n, nb, b.pvv.ptr, b.piv.ptr, b.pa.ptr);
+  MGP_HIP_CHECK(hipGetLastError());
   if (o.method == 0 && !(o.error_tol > 0.f)) {
     // Greedy without a trace stop: selection stays on the device.
     for (int m = 0; m < rank; ++m) {
-      hipLaunchKernelGGL(k_pc_select, dim3(1), dim3(kBlock), 0, st, pvv.ptr, piv.ptr,
-                         pa.ptr, nb, m, state.ptr, mask.ptr, L, n, coef.ptr);
+      hipLaunchKernelGGL(k_pc_select, dim3(1), dim3(kBlock), 0, st, b.pvv.ptr, b.piv.ptr,
+                         b.pa.ptr, nb, m, b.state.ptr, b.mask.ptr, L, n, b.coef.ptr);
       launch_column(m);
     }
     PivotDev fin;
-    MGP_HIP_CHECK(hipMemcpyAsync(&fin, state.ptr, sizeof(fin), hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipMemcpyAsync(&fin, b.state.ptr, sizeof(fin), hipMemcpyDeviceToHost, st));
     MGP_HIP_CHECK(hipStreamSynchronize(st));
     return fin.stopped ? fin.rank : rank;
   }
-
-  // Host-driven selection (pivoted_cholesky.mojo:2195-2334).
-  const float diag_value = os;  // provider diagonal value k(x, x)
-  // vector-noise providers report the 1e-6 floor here (impl_get_noise,
-  // fn_ptr_module.py:673-679)
-  const float noise = pv.has_noise_vec ? 1e-6f : pv.noise;
+  // Host-driven selection.
   std::vector<char> used((size_t)n, 0);
   std::vector<float> dh;
   uint64_t rng = o.seed;
   for (int m = 0; m < rank; ++m) {
-    hipLaunchKernelGGL(k_pc_reduce, dim3(1), dim3(64), 0, st, pvv.ptr, piv.ptr, pa.ptr, nb,
-                       state.ptr);
+    hipLaunchKernelGGL(k_pc_reduce, dim3(1), dim3(64), 0, st, b.pvv.ptr, b.piv.ptr, b.pa.ptr,
+                       nb, b.state.ptr);
     PivotDev cur;
-    MGP_HIP_CHECK(hipMemcpyAsync(&cur, state.ptr, sizeof(cur), hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipMemcpyAsync(&cur, b.state.ptr, sizeof(cur), hipMemcpyDeviceToHost, st));
     MGP_HIP_CHECK(hipStreamSynchronize(st));
     int64_t pivot = cur.pivot;
     float maxval = cur.maxval;
@@ -1476,7 +1454,7 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
     }
     if (o.method != 0) {
       dh.resize((size_t)n);
-      MGP_HIP_CHECK(hipMemcpyAsync(dh.data(), diag.ptr, (size_t)n * sizeof(float),
+      MGP_HIP_CHECK(hipMemcpyAsync(dh.data(), b.diag.ptr, (size_t)n * sizeof(float),
                                    hipMemcpyDeviceToHost, st));
       MGP_HIP_CHECK(hipStreamSynchronize(st));
       float total = 0.0f;
@@ -1502,12 +1480,133 @@ int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
       }
     }
     used[(size_t)pivot] = 1;
-    hipLaunchKernelGGL(k_pc_setpivot, dim3(1), dim3(kBlock), 0, st, state.ptr, mask.ptr, L,
-                       n, m, coef.ptr, pivot, maxval);
+    hipLaunchKernelGGL(k_pc_setpivot, dim3(1), dim3(kBlock), 0, st, b.state.ptr, b.mask.ptr, L,
+                       n, m, b.coef.ptr, pivot, maxval);
     launch_column(m);
   }
   MGP_HIP_CHECK(hipStreamSynchronize(st));
   return rank;
+}
+
+// Column m of the pivoted Cholesky of os_B (x) K + diag(extra) over the
+// task-blocked index i = s n + j (s < T, j < n), extra = task_noise[t_p] -
+// noise_min at the pivot p = t_p n + j_p only: the forward product of a unit
+// vector minus the provider noise at the pivot.
+template <class Eval>
+__global__ __launch_bounds__(256) void k_pc_column_kron(
+    Eval ev, const float* __restrict__ Z, int d, int64_t n, int T,
+    const float* __restrict__ osB, const float* __restrict__ task_noise, float noise_min,
+    int m, float* __restrict__ L, float* __restrict__ diag, const float* __restrict__ mask,
+    const float* __restrict__ coef, const PivotDev* __restrict__ state, int nb, float* pv,
+    int64_t* pi, double* pa) {
+  extern __shared__ float sh[];  // coef[m], zp[d], bcol[T]
+  if (state->stopped) return;    // uniform across the grid
+  const int64_t N = n * T;
+  const int64_t p = state->pivot;
+  const int tp = (int)(p / n);
+  const int64_t jp = p - (int64_t)tp * n;
+  const float scale = 1.0f / sqrtf(fmaxf(state->maxval, 1e-10f));
+  float* scoef = sh;
+  float* zp = sh + m;
+  float* bcol = zp + d;
+  for (int j = threadIdx.x; j < m; j += blockDim.x) scoef[j] = coef[j];
+  for (int k = threadIdx.x; k < d; k += blockDim.x) zp[k] = Z[jp * d + k];
+  for (int s = threadIdx.x; s < T; s += blockDim.x) bcol[s] = osB[s * T + tp];
+  __syncthreads();
+  const float extra = task_noise[tp] - noise_min;
+  const int64_t chunk = (N + nb - 1) / nb;
+  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(N, i0 + chunk);
+  ArgmaxAcc loc{-1e30f, -1};
+  double abss = 0.0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+    const int s = (int)(i / n);
+    const int64_t j = i - (int64_t)s * n;
+    float kv = bcol[s] * ev(Z + j * d, zp);
+    if (i == p) kv += extra;
+    float sum = 0.0f;
+    for (int q = 0; q < m; ++q) sum += scoef[q] * L[(int64_t)q * N + i];
+    const float v = (kv - sum) * scale;
+    L[(int64_t)m * N + i] = v;
+    if (mask[i] > 0.5f) {
+      const float dn = diag[i] - v * v;
+      diag[i] = dn;
+      loc = amax_merge(loc, ArgmaxAcc{dn, i});
+      abss += (double)fabsf(dn);
+    }
+  }
+  block_argmax_write(loc, abss, pv, pi, pa, blockIdx.x);
+}
+
+// diag[s n + j] = os_B[s][s] (a base-kernel diagonal of 1), mask 1.
+__global__ void k_pc_init_kron(float* __restrict__ diag, float* __restrict__ mask, int64_t n,
+                               int T, const float* __restrict__ osB) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n * T) {
+    const int s = (int)(i / n);
+    diag[i] = osB[s * T + s];
+    mask[i] = 1.0f;
+  }
+}
+
+template <class F>
+void dispatch_column(Provider& pv, F&& launch) {
+  const int d = pv.d;
+  const float osk = pv.outputscale();
+  if (pv.is_tree) launch(TreeColumn{pv.tree, pv.tparams.ptr});
+  else if (pv.kind == KIND_RBF) launch(RadialColumn<KIND_RBF>{osk, d});
+  else if (pv.kind == KIND_MATERN12) launch(RadialColumn<KIND_MATERN12>{osk, d});
+  else if (pv.kind == KIND_MATERN32) launch(RadialColumn<KIND_MATERN32>{osk, d});
+  else launch(RadialColumn<KIND_MATERN52>{osk, d});
+}
+}  // namespace
+
+int pivoted_cholesky(Provider& pv, int rank, const PivotOptions& o, float* L,
+                     hipStream_t st) {
+  MGP_REQUIRE(o.method >= 0 && o.method <= 2, "precond_method must be 0, 1 or 2");
+  const int64_t n = pv.n;
+  PivotBufs b(n, rank, L, st);
+  const float os = pv.kdiag();
+  hipLaunchKernelGGL(k_pc_init, grid1(n), dim3(kBlock), 0, st, b.diag.ptr, b.mask.ptr, n, os);
+  if (pv.nonstationary()) pv.diag_values(pv.train, n, b.diag.ptr);  // extract_diagonal
+  auto launch_column = [&](int m) {
+    const size_t shm = (size_t)(m + pv.d) * sizeof(float);
+    const float* Z = pv.train.z.ptr;
+    dispatch_column(pv, [&](auto ev) {
+      hipLaunchKernelGGL(k_pc_column<decltype(ev)>, dim3(b.nb), dim3(kBlock), shm, st, ev, Z,
+                         pv.d, n, m, L, b.diag.ptr, b.mask.ptr, b.coef.ptr, b.state.ptr, b.nb,
+                         b.pvv.ptr, b.piv.ptr, b.pa.ptr);
+    });
+    MGP_HIP_CHECK(hipGetLastError());
+  };
+  // diagonal value k(x, x); vector-noise providers report the 1e-6 floor as
+  // their noise (impl_get_noise, fn_ptr_module.py:673-679)
+  return pivot_loop(b, rank, o, L, os, pv.has_noise_vec ? 1e-6f : pv.noise, st, launch_column);
+}
+
+int pivoted_cholesky_kron(Provider& base, int T, const float* osB_dev,
+                          const std::vector<float>& osB, const float* task_noise_dev,
+                          float noise_min, int rank, const PivotOptions& o, float* L,
+                          hipStream_t st) {
+  MGP_REQUIRE(o.method >= 0 && o.method <= 2, "precond_method must be 0, 1 or 2");
+  MGP_REQUIRE(T >= 1 && (int)osB.size() == T * T, "os B must be T x T");
+  const int64_t n = base.n, N = n * T;
+  PivotBufs b(N, rank, L, st);
+  hipLaunchKernelGGL(k_pc_init_kron, grid1(N), dim3(kBlock), 0, st, b.diag.ptr, b.mask.ptr, n,
+                     T, osB_dev);
+  float diag_value = 0.0f;  // max_s os B_ss (get_diagonal_value)
+  for (int s = 0; s < T; ++s) diag_value = std::max(diag_value, osB[(size_t)s * T + s]);
+  auto launch_column = [&](int m) {
+    const size_t shm = (size_t)(m + base.d + T) * sizeof(float);
+    const float* Z = base.train.z.ptr;
+    dispatch_column(base, [&](auto ev) {
+      hipLaunchKernelGGL(k_pc_column_kron<decltype(ev)>, dim3(b.nb), dim3(kBlock), shm, st, ev,
+                         Z, base.d, n, T, osB_dev, task_noise_dev, noise_min, m, L, b.diag.ptr,
+                         b.mask.ptr, b.coef.ptr, b.state.ptr, b.nb, b.pvv.ptr, b.piv.ptr,
+                         b.pa.ptr);
+    });
+    MGP_HIP_CHECK(hipGetLastError());
+  };
+  return pivot_loop(b, rank, o, L, diag_value, noise_min, st, launch_column);
 }
 
 void syrk_ltl(const float* L, int64_t n, int k, double* M_dev, hipStream_t st,

@@ -398,3 +398,76 @@ def test_icm_with_kernel_tree():
         assert np.all(np.isfinite(mean)) and np.all(np.asarray(var) > 0)
     with pytest.raises(NotImplementedError):
         gp.sample_posterior(Xs, n_samples=2, method="pathwise")
+
+
+def _train_mixed_native(prov, Yb, T, init, noise0, os0, mean0, kinds, raw0, o):
+    n = Yb.size // T
+    it = o.max_iterations
+    out_p = np.zeros(init.size, np.float32)
+    nz, mn, Bo = np.zeros(T, np.float32), np.zeros(T, np.float32), np.zeros(T * T, np.float32)
+    alpha = np.zeros(n * T, np.float32)
+    hist, cg = np.zeros(it, np.float32), np.zeros(it, np.int32)
+    times = np.zeros(it, np.float64)
+    raw_out = np.zeros(raw0.size, np.float32)
+    res = _lib.ICMTrainResult()
+    res.params, res.noise, res.mean, res.B = (_lib.fptr(out_p), _lib.fptr(nz), _lib.fptr(mn),
+                                              _lib.fptr(Bo))
+    res.alpha, res.nll_history = _lib.fptr(alpha), _lib.fptr(hist)
+    res.cg_iterations_history = cg.ctypes.data_as(_lib.c_int_p)
+    res.iter_times_ms = _lib.dptr(times)
+    k = np.asarray(kinds, np.int32)
+    _lib.call("mgp_icm_train_mixed", prov.handle, T, _lib.fptr(Yb), _lib.fptr(init),
+              _lib.fptr(noise0), float(os0), _lib.fptr(mean0), k.ctypes.data_as(_lib.c_int_p),
+              int(k.size), _lib.fptr(raw0), int(raw0.size), C.byref(o), _lib.PROGRESS_CB(), None,
+              C.byref(res), _lib.fptr(raw_out))
+    hl = res.history_len
+    return {"params": out_p, "noise": nz, "mean": mn, "B": Bo.reshape(T, T), "alpha": alpha,
+            "nll_history": hist[:hl], "cg": cg[:hl], "outputscale": res.outputscale,
+            "final_nll": res.final_nll, "iterations": res.iterations,
+            "rebuilds": res.precond_rebuild_count, "cat_raw": raw_out}
+
+
+@pytest.mark.parametrize("rank,cosine", [(0, False), (6, False), (6, True)])
+def test_icm_train_mixed_matches_oracle(rank, cosine):
+    """Mixed continuous x categorical ICM (train_multi_output_mixed_jit) on an
+    RBF[0] x EHH(3)[1] tree: five Adam steps of the kernel parameters,
+    outputscale, noise, W, raw_v, means and the categorical raw parameters
+    against the CPU restatement on the same probes, without and with the
+    pivoted Cholesky of the full Kronecker operator."""
+    from mojogp_amd import EHH, RBF
+    from oracle import categorical as oc
+    n, T, L, iters = 80, 2, 3, 5
+    rng = np.random.default_rng(5)
+    X = np.c_[rng.uniform(0, 1, n), rng.integers(0, L, n)].astype(np.float32)
+    Y = np.stack([np.sin(4 * X[:, 0]) + 0.3 * X[:, 1], np.cos(3 * X[:, 0]) - 0.2 * X[:, 1]])
+    Y = (Y + 0.05 * rng.normal(size=(T, n))).astype(np.float32)
+    Yb = np.ascontiguousarray(Y.reshape(-1))
+    node = RBF(active_dims=[0]) * EHH(L, active_dims=[1])
+    init = np.array([0.5, 1.0], np.float32)
+    noise0 = np.array([0.1, 0.08], np.float32)
+    mean0 = Y.mean(axis=1).astype(np.float32)
+    raw0 = (oc.default_raw(oc.EHH, L) + np.array([0.1, -0.1, 0.2])).astype(np.float32)
+    print(f"icm mixed train rank={rank} cosine={cosine}", flush=True)
+    o = _lib.ICMTrainOpts(iters, 0.05, -1, 6, 300, 1e-4, rank, 0, 0.5, 30, 15, 1e-4,
+                          int(cosine), 1)
+    prov = NativeProvider(None, False, X, init, 0.0, tree_spec=node.to_tree_spec(2))
+    try:
+        got = _train_mixed_native(prov, Yb, T, init, noise0, 1.0, mean0, [oc.EHH], raw0, o)
+    finally:
+        prov.close()
+    ref = oi.train_mixed(node.to_dict(), X, Yb, init, noise0, 1.0, mean0, [(oc.EHH, L)], raw0,
+                         max_iterations=iters, learning_rate=0.05, num_probes=6, max_cg=300,
+                         max_tridiag=30, cg_tol=1e-4, precond_rank=rank, use_cosine_lr=cosine)
+    print(f"  nll {got['nll_history']} vs {ref['nll_history']}", flush=True)
+    print(f"  cat raw {got['cat_raw']} vs {ref['cat_raw']}; os {got['outputscale']:.6f} vs "
+          f"{ref['outputscale']:.6f}", flush=True)
+    assert got["iterations"] == iters and len(got["nll_history"]) == iters
+    np.testing.assert_allclose(got["nll_history"], ref["nll_history"], rtol=0, atol=1e-4)
+    assert _rel(got["params"], ref["params"]) <= 1e-3
+    assert got["outputscale"] == pytest.approx(ref["outputscale"], rel=1e-3)
+    assert _rel(got["noise"], ref["noise"]) <= 1e-3
+    assert _rel(got["mean"], ref["mean"]) <= 1e-3
+    assert _rel(got["B"], ref["B"]) <= 1e-3
+    np.testing.assert_allclose(got["cat_raw"] - raw0, ref["cat_raw"] - raw0, rtol=0,
+                               atol=2e-3 * 0.05 * iters)
+    assert got["rebuilds"] == ref["precond_rebuild_count"]
