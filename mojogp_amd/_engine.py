@@ -880,6 +880,110 @@ class Engine:
             "alpha": alpha,
         }
 
+    def train_multi_output_mixed(self, *args) -> dict[str, Any]:
+        """train_multi_output_mixed(provider_info, Y [n, T], params, noise_per_task [T],
+        initial_outputscale, mean_per_task [T], num_tasks, cat_data [n, ncat],
+        cat_specs, cat_params (raw), max_iterations, learning_rate, task_rank,
+        verbose, num_probes, max_cg_iter, cg_tol, precond_rank, precond_method,
+        precond_rebuild_threshold, method_int, max_tridiag_iter,
+        early_stop_patience, early_stop_tol [, use_cosine_lr, progress_callback,
+        progress_interval]) (train_multi_output_mixed_python,
+        jit_engine_multi_output_bindings.mojo:953-1200).  The tree provider
+        reads each leaf's levels from its input column (cat_data must match
+        it); ``cat_params`` of the result are the best raw values."""
+        if len(args) < 24 or len(args) > 27:
+            raise ValueError("train_multi_output_mixed() expects 24 to 27 positional arguments")
+        info = args[0]
+        prov = _provider(info)
+        T = int(args[6])
+        Y = _lib.f32(args[1])
+        if Y.ndim != 2 or Y.shape[1] != T:
+            raise ValueError("Y must have shape (n, num_tasks)")
+        n = Y.shape[0]
+        params = _lib.f32(args[2]).ravel()
+        if params.shape[0] != prov.nparams:
+            raise ValueError("train_multi_output_mixed() initial params length does not match "
+                             "provider gradient params")
+        noise0 = _lib.f32(args[3]).ravel()
+        os0 = float(args[4])
+        mean0 = _lib.f32(args[5]).ravel()
+        Cmat = np.asarray(args[7])
+        specs = list(args[8])
+        if Cmat.ndim != 2 or Cmat.shape != (n, len(specs)):
+            raise ValueError("cat_data must have shape (n, number of categorical leaves)")
+        kinds = np.array([self._CAT_KIND[str(sp["kernel_type"]).lower()] for sp in specs],
+                         np.int32)
+        cat0 = _lib.f32(args[9]).ravel()
+        o = _lib.ICMTrainOpts()
+        o.max_iterations = int(args[10])
+        o.learning_rate = float(args[11])
+        o.task_rank = int(args[12])
+        o.num_probes = int(args[14])
+        o.max_cg_iter = int(args[15])
+        o.cg_tol = float(args[16])
+        o.precond_rank = int(args[17])
+        o.precond_method = int(args[18])
+        o.precond_rebuild_threshold = float(args[19])
+        mode = int(args[20])
+        o.max_tridiag_iter = int(args[21])
+        o.early_stop_patience = int(args[22])
+        o.early_stop_tol = float(args[23])
+        o.use_cosine_lr = int(bool(args[24])) if len(args) > 24 else 0
+        callback = args[25] if len(args) > 25 else None
+        o.progress_interval = int(args[26]) if len(args) > 26 else 1
+        if o.max_iterations <= 0:
+            raise ValueError("max_iterations must be > 0")
+        it_max = o.max_iterations
+        out_params = np.zeros(prov.nparams, np.float32)
+        noise = np.zeros(T, np.float32)
+        mean = np.zeros(T, np.float32)
+        B = np.zeros(T * T, np.float32)
+        alpha = np.zeros(n * T, np.float32)
+        hist = np.zeros(it_max, np.float32)
+        cg_hist = np.zeros(it_max, np.int32)
+        times = np.zeros(it_max, np.float64)
+        cat_out = np.zeros(max(cat0.size, 1), np.float32)
+        res = _lib.ICMTrainResult()
+        res.params, res.noise, res.mean = _lib.fptr(out_params), _lib.fptr(noise), _lib.fptr(mean)
+        res.B, res.alpha, res.nll_history = _lib.fptr(B), _lib.fptr(alpha), _lib.fptr(hist)
+        res.cg_iterations_history = cg_hist.ctypes.data_as(_lib.c_int_p)
+        res.iter_times_ms = _lib.dptr(times)
+        cfun, keep = _progress_bridge(callback, model="multi_output_icm")
+        y_blocked = np.ascontiguousarray(Y.T)
+        _lib.call("mgp_icm_train_mixed", prov.handle, T, _lib.fptr(y_blocked),
+                  _lib.fptr(params), _lib.fptr(noise0), os0, _lib.fptr(mean0),
+                  kinds.ctypes.data_as(_lib.c_int_p), int(kinds.size),
+                  _lib.fptr(cat0 if cat0.size else cat_out), int(cat0.size), C.byref(o), cfun,
+                  None, C.byref(res), _lib.fptr(cat_out))
+        del keep
+        hl = int(res.history_len)
+        prov.params = out_params.copy()
+        prov.noise = 0.0
+        prov.cat_kinds, prov.cat_raw = kinds, cat_out[:cat0.size].copy()
+        return {
+            "final_nll": float(res.final_nll), "outputscale": float(res.outputscale),
+            "iterations": int(res.iterations), "converged": bool(res.converged),
+            "num_tasks": T, "task_rank": int(res.task_rank),
+            "max_tridiag_iter": o.max_tridiag_iter,
+            "precond_rebuild_threshold": float(o.precond_rebuild_threshold),
+            "precond_rebuild_count": int(res.precond_rebuild_count),
+            "precond_rank": o.precond_rank, "precond_method": o.precond_method,
+            "early_stop_patience": o.early_stop_patience,
+            "early_stop_tol": float(o.early_stop_tol),
+            "use_cosine_lr": bool(o.use_cosine_lr),
+            "training_route": "materialized" if mode == 1 else "matrix_free",
+            "materialization_mode": mode,
+            "cg_iterations_history": [int(v) for v in cg_hist[:hl]],
+            "iter_times_ms": [float(v) for v in times[:hl]],
+            "nll_history": [float(v) for v in hist[:hl]],
+            "params": [float(v) for v in out_params],
+            "cat_params": cat_out[:cat0.size].copy(),
+            "noise_per_task": [float(v) for v in noise],
+            "mean_per_task": [float(v) for v in mean],
+            "B_flat": [float(v) for v in B],
+            "alpha": alpha,
+        }
+
     def predict_multi_output(self, *args) -> dict[str, Any]:
         """predict_multi_output(provider_info, alpha_rotated [n, T], Q [T, T],
         effective_scales [T], X_test [m, d], params, noise, variance_method

@@ -89,35 +89,36 @@ def _leaves(node: KernelNode) -> list:
     return out + (_leaves(node.right) if node.right is not None else [])
 
 
-def _mixed_layout(kernel: KernelNode, X: np.ndarray, latent: int):
+def _mixed_layout(kernel: KernelNode, X: np.ndarray, latent: Optional[int] = None):
     """Categorical layout of one mixed latent (_configure_latent_kernels_for_fit,
     multi_output_gp.py:4136-4218): the leaves' {"levels", "kernel_type"} specs
     in tree order, their input columns, the continuous columns (the default
     dimensions of the latent's continuous leaves) and the categorical parameter
-    names.  Columns must hold integer levels in [0, L)."""
+    names.  Columns must hold integer levels in [0, L).  latent: the LMC
+    latent index (None: the ICM kernel), for the messages."""
     leaves = kernel.categorical_leaves()
+    what = "kernel" if latent is None else f"latent {latent}"
+    pure = ("Pure categorical kernels (all dimensions categorical, no continuous) are not "
+            "supported" if latent is None else
+            "Pure categorical latent kernels are not supported for MultiOutputLMCGP. "
+            f"Latent kernel {latent} contains no continuous dimensions.")
     if all(lf.is_categorical() for lf in _leaves(kernel)):
-        raise ValueError("Pure categorical latent kernels are not supported for "
-                         f"MultiOutputLMCGP. Latent kernel {latent} contains no continuous "
-                         "dimensions.")
+        raise ValueError(pure)
     specs, cols, names = [], [], []
     for lf in leaves:
         col = int(lf.active_dims[0])
         if col >= X.shape[1]:
-            raise ValueError(f"latent {latent}: categorical column {col} out of range")
+            raise ValueError(f"{what}: categorical column {col} out of range")
         v = X[:, col]
         L = int(lf.levels)
         if np.any(v != np.round(v)) or np.any(v < 0) or np.any(v >= L):
-            raise ValueError(f"latent {latent}: column {col} must hold integer levels in "
-                             f"[0, {L})")
+            raise ValueError(f"{what}: column {col} must hold integer levels in [0, {L})")
         specs.append({"levels": L, "kernel_type": lf.kernel_type.name.lower()})
         cols.append(col)
         names.extend(lf.get_param_names())
     cont = [c for c in range(X.shape[1]) if c not in set(cols)]
     if not cont:
-        raise ValueError("Pure categorical latent kernels are not supported for "
-                         f"MultiOutputLMCGP. Latent kernel {latent} has no continuous "
-                         "dimensions.")
+        raise ValueError(pure)
     return specs, cols, cont, names
 
 
@@ -1009,13 +1010,14 @@ class MultiOutputGP:
         if not isinstance(kernel, KernelNode):
             raise ValueError(f"kernel must be a string or KernelNode, got {type(kernel)}")
         if not kernel.is_native_leaf():
-            # composite trees run on the kernel-tree products; categorical
-            # leaves are single-output only
-            if (kernel.has_categorical() or not kernel.is_tree_servable()
-                    or kernel.num_params() != kernel.engine_num_params()):
+            # composite and mixed continuous x categorical trees run on the
+            # kernel-tree products; the isotropic polynomial's hidden variance
+            # slot is single-output only
+            ncat = sum(lf.num_params() for lf in kernel.categorical_leaves())
+            if (not kernel.is_tree_servable()
+                    or kernel.num_params() - ncat != kernel.engine_num_params()):
                 raise NotImplementedError(f"kernel {kernel!r} is outside the gfx950 ICM engine "
-                                          "(categorical and isotropic polynomial leaves are "
-                                          "single-output only)")
+                                          "(isotropic polynomial leaves are single-output only)")
         self._is_composite = True
         self.kernel = kernel
         self._original_kernel = kernel
@@ -1050,6 +1052,16 @@ class MultiOutputGP:
         self._backend_train_info: Optional[dict] = None
         self._backend_predict_info: Optional[dict] = None
         self._backend_sample_info: Optional[dict] = None
+        # mixed continuous x categorical kernels: continuous columns, the
+        # categorical leaves' specs / columns and their raw parameters
+        self._cont_cols: Optional[list] = None
+        self._cat_specs: list = []
+        self._cat_cols: list = []
+        self._cat_params_raw: Optional[np.ndarray] = None
+
+    @property
+    def _is_mixed(self) -> bool:
+        return self._original_kernel.has_categorical()
 
     # ------------------------------------------------------------ properties
     @property
@@ -1094,16 +1106,36 @@ class MultiOutputGP:
 
     def _ensure_compiled(self, dim: int) -> None:
         self._engine = _engine.load_engine()
-        self._kernel_module = _engine.load_kernel_module(self._compiled_kernel, False, dim)
+        self._kernel_module = _engine.load_kernel_module(
+            self._compiled_kernel, False, dim,
+            default_dims=self._cont_cols if self._is_mixed else None)
         self._dim = dim
 
     def _build_provider_info(self, X, params, noise) -> dict:
         info = self._kernel_module.init_provider(np.ascontiguousarray(X, np.float32),
                                                  np.ascontiguousarray(params, np.float32),
                                                  float(noise))
+        if self._is_mixed and self._cat_params_raw is not None:
+            kinds = [_engine.Engine._CAT_KIND[c["kernel_type"]] for c in self._cat_specs]
+            _engine._provider(info).set_categorical_params(kinds, self._cat_params_raw)
         if self.method == "materialized":
             self._kernel_module.materialize(info)
         return info
+
+    def _engine_params(self, params) -> np.ndarray:
+        """Engine layout of result parameters: a mixed kernel's results are
+        already its continuous (engine) parameters."""
+        p = np.asarray(params, np.float32)
+        return p if self._is_mixed else self._compiled_kernel.to_engine_params(p)
+
+    def _continuous_param_names(self) -> list:
+        """Names of the engine-layout parameters (the public names with the
+        categorical slots dropped)."""
+        k = self._compiled_kernel
+        names = k.get_param_names()
+        idx = np.rint(k.to_engine_params(np.arange(k.num_params(), dtype=np.float32) + 0.25)
+                      - 0.25).astype(int)
+        return [names[i] for i in idx]
 
     def _ensure_provider(self) -> dict:
         r = self._result
@@ -1111,8 +1143,7 @@ class MultiOutputGP:
             if self._kernel_module is None:
                 self._ensure_compiled(self._X_train.shape[1])
             self._provider_info = self._build_provider_info(
-                self._X_train, self._compiled_kernel.to_engine_params(r.params),
-                float(np.mean(r.noise_per_task)))
+                self._X_train, self._engine_params(r.params), float(np.mean(r.noise_per_task)))
         return self._provider_info
 
     # ------------------------------------------------------------ fit
@@ -1194,6 +1225,10 @@ class MultiOutputGP:
                 raise ValueError("noise_group_train references a group id outside group_noise")
             observation_noise = gnoise_arr[groups_arr]
         obs = None
+        if observation_noise is not None and self._is_mixed:
+            raise NotImplementedError(
+                "MultiOutputGP fixed per-sample-task observation_noise currently supports "
+                "continuous kernels only; mixed heteroskedastic noise is in development")
         if observation_noise is not None:
             obs = np.ascontiguousarray(observation_noise, dtype=np.float32)
             if obs.shape != Y.shape:
@@ -1225,6 +1260,22 @@ class MultiOutputGP:
         self._observation_noise_train = obs
         self._noise_group_train = groups_arr
         self._noise_group_values = gnoise_arr
+        self._cat_params_raw = None
+        if self._is_mixed:
+            self._cat_specs, self._cat_cols, self._cont_cols, self._cat_names = _mixed_layout(
+                self._original_kernel, X)
+            cont_d = len(self._cont_cols)
+            self._compiled_kernel = (make_ard_kernel(self._original_kernel, cont_d) if self.ard
+                                     else KernelNode.from_dict(self._original_kernel.to_dict()))
+            self.kernel = self._compiled_kernel
+            if initial_lengthscales is not None or initial_lengthscale != 1.0:
+                raise ValueError("initial_lengthscale(s) apply to single RBF / Matern kernels; "
+                                 "pass initial_params for kernel trees")
+            return self._fit_mixed(X, Y, T, max_iterations, learning_rate, initial_params,
+                                   initial_noise, initial_noise_per_task, initial_outputscale,
+                                   verbose, early_stop_tol, early_stop_patience,
+                                   lr_schedule == "cosine", progress, progress_interval)
+        self._cont_cols, self._cat_specs, self._cat_cols = None, [], []
         self._compiled_kernel = (make_ard_kernel(self._original_kernel, d) if self.ard
                                  else KernelNode.from_dict(self._original_kernel.to_dict()))
         self.kernel = self._compiled_kernel
@@ -1316,6 +1367,98 @@ class MultiOutputGP:
         self._backend_sample_info = None
         return self._result
 
+    def _fit_mixed(self, X, Y, T, max_iterations, learning_rate, initial_params, initial_noise,
+                   initial_noise_per_task, initial_outputscale, verbose, early_stop_tol,
+                   early_stop_patience, use_cosine_lr, progress, progress_interval):
+        """_fit_mixed_composite (multi_output_gp.py:2036-2228): the kernel tree's
+        continuous parameters (engine layout), the ICM outputscale, per-task
+        noise and means, and the categorical leaves' raw parameters from their
+        defaults, trained by the mixed ICM loop."""
+        from .kernel import cat_default_raw_param
+        n, d = X.shape
+        k = self._compiled_kernel
+        num_params = k.engine_num_params()
+        if initial_params is None:
+            initial_params = k.to_engine_params(k.get_initial_params())
+        initial_params = np.ascontiguousarray(initial_params, dtype=np.float32)
+        if initial_params.shape != (num_params,):
+            raise ValueError(f"init_params must have shape ({num_params},), got "
+                             f"{initial_params.shape}. Kernel {k.to_mojo_type()} has "
+                             f"{num_params} continuous parameters: "
+                             f"{self._continuous_param_names()}")
+        if self._init_mean is None:
+            mean0 = np.mean(Y, axis=0).astype(np.float32)
+        elif isinstance(self._init_mean, (int, float)):
+            mean0 = np.full(T, float(self._init_mean), np.float32)
+        else:
+            mean0 = np.asarray(self._init_mean, np.float32)
+        noise0 = (np.ascontiguousarray(initial_noise_per_task, np.float32)
+                  if initial_noise_per_task is not None
+                  else np.full(T, initial_noise, np.float32))
+        cat0 = np.asarray([cat_default_raw_param(lf.kernel_type, i, lf.levels)
+                           for lf in k.categorical_leaves() for i in range(lf.num_params())],
+                          np.float32)
+        self._ensure_compiled(d)
+        self._cat_params_raw = cat0
+        info = self._build_provider_info(X, initial_params, 0.0)
+        self._provider_info = info
+        self._training_method = self.method
+        C = np.ascontiguousarray(X[:, self._cat_cols], np.int32).reshape(n, len(self._cat_cols))
+        args = [info, Y, initial_params, noise0, float(initial_outputscale), mean0, int(T), C,
+                self._cat_specs, cat0, int(max_iterations), float(learning_rate),
+                int(self.task_rank), bool(verbose), int(self.num_probes), int(self.max_cg_iter),
+                float(self.cg_tol), int(self.precond_rank), int(self.precond_method),
+                float(self.precond_rebuild_threshold),
+                1 if self.method == "materialized" else 0, int(self.max_tridiag_iter),
+                int(early_stop_patience), float(early_stop_tol), bool(use_cosine_lr)]
+        if callable(progress):
+            args.extend([progress, int(progress_interval)])
+        try:
+            raw = self._engine.train_multi_output_mixed(*args)
+        except Exception:
+            self._destroy_persistent_provider()
+            raise
+        noise_pt = np.asarray(raw["noise_per_task"], np.float32)
+        mean_pt = np.asarray(raw["mean_per_task"], np.float32)
+        params = np.asarray(raw["params"], np.float32)
+        os_ = float(raw["outputscale"])
+        self._cat_params_raw = np.asarray(raw["cat_params"], np.float32)
+        B_flat = np.asarray(raw["B_flat"], np.float32)
+        B = B_flat.reshape(T, T) if B_flat.size == T * T else np.eye(T, dtype=np.float32)
+        B_scaled = os_ * B
+        eigvals, Q = np.linalg.eigh(B_scaled)
+        Lam = np.maximum(eigvals, 1e-6).astype(np.float32)
+        alpha_blocked = np.asarray(raw["alpha"], np.float32)
+        alpha_rot = (alpha_blocked.reshape(T, n).T.astype(np.float64)
+                     @ Q.astype(np.float64)).astype(np.float32)
+        hist = np.asarray(raw["nll_history"], np.float32)
+        self._result = MultiOutputTrainingResult(
+            params=params, noise=float(np.mean(noise_pt)), noise_per_task=noise_pt,
+            final_nll=float(raw["final_nll"]), iterations=int(raw["iterations"]),
+            converged=bool(raw["converged"]), num_tasks=T, task_rank=int(raw["task_rank"]),
+            num_kernel_params=len(params), B=B_scaled.astype(np.float32),
+            Q=Q.astype(np.float32), Lambda=Lam, effective_scales=Lam,
+            W=np.zeros((T, max(int(raw["task_rank"]), 1)), np.float32),
+            raw_v=np.zeros(T, np.float32), alpha_rotated=alpha_rot, mean_per_task=mean_pt,
+            nll_history=hist if hist.size else np.array([raw["final_nll"]], np.float32),
+            param_names=self._continuous_param_names(),
+            cat_params=self._cat_params_raw if self._cat_params_raw.size else None,
+            cat_param_names=list(self._cat_names),
+            iter_times_ms=np.asarray(raw["iter_times_ms"], np.float64))
+        self._X_train, self._Y_train = X, Y
+        self._raw_result = raw
+        self._backend_train_info = {
+            k_: raw[k_] for k_ in ("training_route", "materialization_mode", "max_tridiag_iter",
+                                   "precond_rebuild_threshold", "precond_rebuild_count",
+                                   "precond_rank", "precond_method", "iter_times_ms")}
+        self._backend_train_info["use_preconditioner"] = bool(self.use_preconditioner)
+        self._backend_train_info["is_mixed"] = True
+        self._is_trained = True
+        self._fitted_mean = mean_pt.copy()
+        self._backend_predict_info = None
+        self._backend_sample_info = None
+        return self._result
+
     # ------------------------------------------------------------ predict
     def _check_test(self, X_test) -> np.ndarray:
         if not self._is_trained:
@@ -1349,7 +1492,7 @@ class MultiOutputGP:
         T = r.num_tasks
         vm = {"mean_only": 0, "love": 1, "exact": 2}[variance_method]
         info = self._ensure_provider()
-        params = self._compiled_kernel.to_engine_params(np.asarray(r.params, np.float32))
+        params = self._engine_params(r.params)
         noise = float(np.mean(r.noise_per_task))
         tol = min(float(self.cg_tol), 1e-2) if float(self.cg_tol) > 0.0 else 1e-2
         rank = self._predict_rank()
@@ -1548,6 +1691,12 @@ class MultiOutputGP:
             arrays["group_noise"] = self._noise_group_values
         if self._fitted_mean is not None:
             arrays["fitted_mean"] = self._fitted_mean
+        if self._is_mixed:
+            # the reference's mixed artifact: raw categorical parameters, the
+            # continuous and the integer categorical columns
+            arrays["cat_params"] = self._cat_params_raw
+            arrays["X_train_cont"] = np.ascontiguousarray(self._X_train[:, self._cont_cols])
+            arrays["C_train"] = np.ascontiguousarray(self._X_train[:, self._cat_cols], np.int32)
         np.savez(path + "_arrays.npz", **arrays)
 
     @classmethod
@@ -1566,9 +1715,6 @@ class MultiOutputGP:
         if cfg.get("result_type") != "MultiOutputTrainingResult":
             raise ValueError(f"Unsupported MultiOutputGP result_type={cfg.get('result_type')!r}")
         arr = np.load(path + "_arrays.npz", allow_pickle=False)
-        if "C_train" in arr or "cat_params" in arr:
-            raise NotImplementedError("mixed continuous/categorical ICM models are outside the "
-                                      "gfx950 engine")
         if kernel is None:
             kernel = (KernelNode.from_dict(cfg["kernel_tree"]) if cfg.get("kernel_tree")
                       else cfg.get("kernel", "rbf"))
@@ -1591,6 +1737,13 @@ class MultiOutputGP:
         gp._dim = cfg.get("dim")
         gp._training_method = cfg.get("training_method", gp.method)
         d = gp._X_train.shape[1]
+        if gp._is_mixed:
+            if "cat_params" not in arr:
+                raise ValueError("mixed MultiOutputGP artifact is missing cat_params")
+            (gp._cat_specs, gp._cat_cols, gp._cont_cols,
+             gp._cat_names) = _mixed_layout(gp._original_kernel, gp._X_train)
+            gp._cat_params_raw = np.ascontiguousarray(arr["cat_params"], np.float32)
+            d = len(gp._cont_cols)
         gp._compiled_kernel = (make_ard_kernel(gp._original_kernel, d) if gp.ard
                                else gp._original_kernel)
         gp.kernel = gp._compiled_kernel
@@ -1608,6 +1761,7 @@ class MultiOutputGP:
             alpha_rotated=np.asarray(arr["alpha_rotated"], np.float32),
             mean_per_task=np.asarray(arr["mean_per_task"], np.float32),
             nll_history=arr["nll_history"], param_names=list(cfg["param_names"]),
+            cat_params=gp._cat_params_raw,
             cat_param_names=list(cfg.get("cat_param_names", [])),
             iter_times_ms=get("iter_times_ms"))
         fm = get("fitted_mean")

@@ -471,3 +471,62 @@ def test_icm_train_mixed_matches_oracle(rank, cosine):
     np.testing.assert_allclose(got["cat_raw"] - raw0, ref["cat_raw"] - raw0, rtol=0,
                                atol=2e-3 * 0.05 * iters)
     assert got["rebuilds"] == ref["precond_rebuild_count"]
+
+
+def test_multi_output_gp_mixed_python_path(tmp_path):
+    """MultiOutputGP with a mixed kernel (RBF on the continuous column x EHH on
+    the categorical column 1): fit on both routes (same probes, so the NLL
+    histories agree), the raw categorical parameters and continuous parameter
+    names in the result, exact-variance prediction against the dense
+    per-eigen-task posterior of the CPU restatement (the RBF leaf's default
+    dimensions are the continuous columns), the model file (raw categorical
+    parameters, continuous and categorical columns, as the reference writes
+    them) and predictions after reload; fixed observation noise is refused for
+    mixed kernels, as in the reference."""
+    from mojogp_amd import EHH, MultiOutputGP, RBF
+    from oracle import categorical as oc
+    rng = np.random.default_rng(91)
+    n, T, L, m = 200, 2, 3, 30
+    X = np.c_[rng.uniform(0, 1, n), rng.integers(0, L, n)].astype(np.float32)
+    Y = np.stack([np.sin(4 * X[:, 0]) + 0.4 * X[:, 1], np.sin(4 * X[:, 0] + 0.5) - 0.3 * X[:, 1]],
+                 1)
+    Y = (Y + 0.05 * rng.normal(size=(n, T))).astype(np.float32)
+    Xs = np.c_[rng.uniform(0, 1, m), rng.integers(0, L, m)].astype(np.float32)
+    print("icm python path with a mixed kernel", flush=True)
+    kern = RBF() * EHH(L, active_dims=[1])
+    gp = MultiOutputGP(kern, cg_tolerance=1e-6, max_cg_iterations=1000, preconditioner_rank=8)
+    with pytest.raises(NotImplementedError, match="observation_noise"):
+        gp.fit(X, Y, max_iterations=2, observation_noise=np.full((n, T), 0.01, np.float32))
+    tr = gp.fit(X, Y, max_iterations=6, method="matrix_free")
+    g_mat = MultiOutputGP(kern, cg_tolerance=1e-6, max_cg_iterations=1000,
+                          preconditioner_rank=8)
+    tr_m = g_mat.fit(X, Y, max_iterations=6, method="materialized")
+    print(f"  nll matrix-free {tr.nll_history} materialized {tr_m.nll_history}", flush=True)
+    np.testing.assert_allclose(tr_m.nll_history, tr.nll_history, rtol=0, atol=2e-4)
+    assert np.all(np.isfinite(tr.nll_history)) and tr.iterations == 6
+    assert tr.cat_params.shape == (3,) and len(tr.cat_param_names) == 3
+    assert len(tr.param_names) == 2 and tr.params.shape == (2,)
+    mean, var = gp.predict(Xs, return_var=True, variance_method="exact")
+    theta = oc.constrain(oc.EHH, L, tr.cat_params)
+    node = (RBF(active_dims=[0]) * EHH(L, active_dims=[1])).to_dict()
+    tree = ok.TreeKernel(node, 2, [oc.correlation(oc.EHH, L, theta)])
+    mref, vref = oi.predict(tree, False, X, Xs, np.asarray(tr.params, np.float64),
+                            tr.alpha_rotated, tr.Q, tr.effective_scales, tr.noise)
+    mref = mref + tr.mean_per_task[None, :]
+    print(f"  mean relerr {_rel(mean, mref):.2e} exact std relerr "
+          f"{_rel(np.sqrt(var), np.sqrt(vref)):.2e}", flush=True)
+    assert _rel(mean, mref) <= 1e-4
+    assert _rel(np.sqrt(var), np.sqrt(vref)) <= 1e-4
+    m1, v1 = gp.predict(Xs, return_var=True)  # LOVE
+    assert np.all(np.isfinite(m1)) and np.all(v1 > 0)
+    path = str(tmp_path / "icm_mixed")
+    gp.save(path)
+    arr = np.load(path + "_arrays.npz")
+    np.testing.assert_array_equal(arr["cat_params"], tr.cat_params)
+    np.testing.assert_array_equal(arr["C_train"], X[:, 1].astype(np.int32)[:, None])
+    g2 = MultiOutputGP.load(path)
+    m2, v2 = g2.predict(Xs, return_var=True)
+    print(f"  reload: mean {np.max(np.abs(m2 - m1)):.2e} var {np.max(np.abs(v2 - v1)):.2e}",
+          flush=True)
+    np.testing.assert_allclose(m2, m1, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(v2, v1, rtol=1e-4, atol=1e-7)
