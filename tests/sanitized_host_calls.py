@@ -13,8 +13,8 @@ error-message buffer, the task-covariance initialiser, and a mutation fuzz
 of the kernel-tree spec parser (every spec must be rejected or accepted
 without a memory error).
 gpu: fit / predict through every route (matrix-free, materialized, kernel
-tree, LMC, ICM), the prediction cache, save / load and stale-handle
-rejection after destruction.
+tree, LMC, ICM, mixed categorical ICM and LMC), the prediction cache, save /
+load and stale-handle rejection after destruction.
 """
 
 from __future__ import annotations
@@ -76,6 +76,11 @@ def cpu() -> None:
     _expect_fail("mgp_forward_matvec", junk, fp(V), 1, fp(V), contains="unknown or destroyed")
     _expect_fail("mgp_materialize", junk, contains="unknown or destroyed")
     _expect_fail("mgp_destroy_prediction_cache", junk, contains="prediction cache")
+    # mixed multi-output entry points: argument checks before any device work
+    _expect_fail("mgp_lmc_train_mixed", None, 1, 1, None, None, None, None, None, None, None,
+                 None, 0, None, None, None, None, contains="need >= 1 latent")
+    _expect_fail("mgp_icm_train_mixed", junk, 2, None, None, None, 1.0, None, None, 0, None, 0,
+                 None, _lib.PROGRESS_CB(), None, None, None, contains="unknown or destroyed")
     # host task-covariance initialiser
     W = np.zeros(6, np.float32)
     assert _status("mgp_icm_task_covariance_init", 3, 2, 42, fp(W)) == 0
@@ -151,6 +156,17 @@ def gpu() -> None:
     lmc.fit(X, Y, max_iterations=5, method="matrix_free")
     assert np.all(np.isfinite(lmc.predict(Xs).mean))
     print("gpu: ICM and LMC fit + predict", flush=True)
+    from mojogp_amd import EHH
+    Xm = np.c_[X[:, :2], rng.integers(0, 3, n)].astype(np.float32)
+    mixed = RBF() * EHH(3, active_dims=[2])
+    icm_m = MultiOutputGP(mixed)
+    icm_m.fit(Xm, Y, max_iterations=4, method="matrix_free")
+    Xsm = np.c_[Xs[:, :2], rng.integers(0, 3, Xs.shape[0])].astype(np.float32)
+    assert np.all(np.isfinite(icm_m.predict(Xsm).mean))
+    lmc_m = MultiOutputLMCGP([RBF(), mixed])
+    lmc_m.fit(Xm, Y, max_iterations=4, method="materialized")
+    assert np.all(np.isfinite(lmc_m.predict(Xsm).mean))
+    print("gpu: mixed ICM and LMC fit + predict", flush=True)
     params = np.concatenate([np.ones(d), [1.0]]).astype(np.float32)
     p = NativeProvider(KIND_MATERN52, True, X, params, 0.1)
     V = rng.normal(size=(4, n)).astype(np.float32)
