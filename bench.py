@@ -15,7 +15,11 @@ kernel is bound by the mix of VALU (two transcendentals and 5.5 other
 instructions per pair value) and 16-bit MFMA issue, not by any single
 published peak: roofline.peak is the pipe model, the cycles per 16x16 tile
 that the per-instruction costs measured live by mgp_pipe_probe give for the
-kernel's instruction mix, expressed in the same algorithmic TFLOP/s.
+kernel's instruction mix, expressed in the same algorithmic TFLOP/s.  At
+config 3 the product runs on the symmetric kernel, which forms each
+off-diagonal tile once for both of its entries (half the tiles, 1.5 more
+MFMAs each); the model counts the tiles it forms, while value and achieved
+stay per N^2 pairs.
 
 The cpu_baseline leg times the C restatement of the reference matvec
 (oracle/cpu_ref, OpenMP) on a bounded sample of rows of the same workload.
@@ -58,14 +62,51 @@ TRANS_PER_VALUE, VALU_PER_VALUE = 2, 5.5
 ROW_TILES, COL_TILES = -(-N // 16), 2 * -(-N // 32)
 
 
+# Symmetric route (matvec.hip k_sym_tile / sym_route): square products with
+# 2..16 right-hand sides over >= 48 blocks of 512 points form each
+# off-diagonal 16x16 tile once and use it for both of its entries: the same
+# VALU per tile, KB distance MFMAs plus 1.5 forward and 1.5 transposed product
+# MFMAs.  The diagonal blocks are formed one-sided (both triangles).
+SYM_ROWS, SYM_MIN_BLOCKS, SYM_MAX_BYTES = 512, 48, 16e9
+SYM_MFMA_PER_TILE = KB + 3.0
+
+
+def _sym_blocks(n, ncols=T):
+    """(blocks, off-diagonal block pairs) when a square product of n points
+    runs on the symmetric kernel, else None (the library's route rule,
+    including the MGP_SYM_MATVEC switch)."""
+    env = os.environ.get("MGP_SYM_MATVEC")
+    if env is not None and env.startswith("0"):
+        return None
+    if not 2 <= ncols <= 16:
+        return None
+    nb = -(-n // SYM_ROWS)
+    if env is None and nb < SYM_MIN_BLOCKS:
+        return None
+    if nb * (nb // 2) * SYM_ROWS * 16 * 4 > SYM_MAX_BYTES:
+        return None
+    return nb, nb * (nb - 1) // 2
+
+
 def _pipe_model(probe):
-    """Cycles per 16x16 tile and the kernel time they imply: VALU cycles plus
-    the MFMA's measured cost inside a VALU stream (the two pipes overlap only
-    partly on gfx950: out[4] of mgp_pipe_probe)."""
+    """Cycles per 16x16 tile (one-sided, symmetric) and the clock: VALU
+    cycles plus the MFMA's measured cost inside a VALU stream (the two pipes
+    overlap only partly on gfx950: out[4] of mgp_pipe_probe)."""
     ghz, c_tr, c_valu, c_mfma, c_mfma_mixed = probe[:5]
-    cycles = (VALUES_PER_LANE * (TRANS_PER_VALUE * c_tr + VALU_PER_VALUE * c_valu)
-              + MFMA_PER_TILE * c_mfma_mixed)
-    return cycles, ghz
+    valu = VALUES_PER_LANE * (TRANS_PER_VALUE * c_tr + VALU_PER_VALUE * c_valu)
+    return valu + MFMA_PER_TILE * c_mfma_mixed, valu + SYM_MFMA_PER_TILE * c_mfma_mixed, ghz
+
+
+def _tile_counts():
+    """(one-sided tiles, symmetric tiles, MFMAs, kernel name) of one config-3 product."""
+    sym = _sym_blocks(N)
+    if sym is None:
+        tiles = ROW_TILES * COL_TILES
+        return tiles, 0, tiles * MFMA_PER_TILE, "k_fused_tile (one-sided)"
+    nb, off = sym
+    per_block = (SYM_ROWS // 16) ** 2
+    diag, offt = nb * per_block, off * per_block
+    return diag, offt, diag * MFMA_PER_TILE + offt * SYM_MFMA_PER_TILE, "k_sym_tile (symmetric)"
 
 
 def _probe():
@@ -551,11 +592,12 @@ def main(argv=None) -> int:
     value = pairs * FLOPS_PER_PAIR / (ms_per_step * 1e-3) / 1e12
     achieved = pairs * FLOPS_PER_PAIR / (tile_ms * 1e-3) / 1e12
     probe = _probe()
-    cycles, ghz = _pipe_model(probe)
+    cycles, sym_cycles, ghz = _pipe_model(probe)
     simds = 4 * int(probe[5])
-    t_model_ms = ROW_TILES * COL_TILES / simds * cycles / (ghz * 1e9) * 1e3
+    one_tiles, sym_tiles, mfmas, kernel = _tile_counts()
+    t_model_ms = (one_tiles * cycles + sym_tiles * sym_cycles) / simds / (ghz * 1e9) * 1e3
     peak = pairs * FLOPS_PER_PAIR / (t_model_ms * 1e-3) / 1e12
-    mfma_tflops = ROW_TILES * COL_TILES * MFMA_PER_TILE * 16384 / (tile_ms * 1e-3) / 1e12
+    mfma_tflops = mfmas * 16384 / (tile_ms * 1e-3) / 1e12
 
     result = {
         "metric": "fused K.V matvec TFLOP/s (N=250k, d=16, t=16, Matern-5/2 ARD)",
@@ -580,10 +622,15 @@ def main(argv=None) -> int:
             "unit": "TFLOP/s",
             "frac": round(t_model_ms / tile_ms, 4),
             "traffic": TILE_TRAFFIC_BYTES,
-            "peak_kind": "pipe model: VALU + 16-bit MFMA cycles per 16x16 tile from "
-                         "per-instruction costs measured live (mgp_pipe_probe)",
+            "peak_kind": "pipe model: VALU + 16-bit MFMA cycles per 16x16 tile formed "
+                         "(symmetric tiles carry 1.5 more MFMAs) from per-instruction costs "
+                         "measured live (mgp_pipe_probe)",
             "model_ms": round(t_model_ms, 3),
+            "kernel": kernel,
+            "tiles_formed": {"one_sided": one_tiles, "symmetric": sym_tiles,
+                             "all_pairs_equivalent": ROW_TILES * COL_TILES},
             "cycles_per_tile": round(cycles, 2),
+            "cycles_per_symmetric_tile": round(sym_cycles, 2),
             "instruction_cycles": {"clock_ghz": round(probe[0], 3),
                                    "v_exp_f32": round(probe[1], 2),
                                    "v_fma_f32": round(probe[2], 2),

@@ -32,6 +32,7 @@ struct Coords {
 struct PackedPoints {
   int64_t n = 0;       // real points
   int64_t ntiles = 0;  // 16-point tiles (zero padded)
+  int64_t ntiles_alloc = 0;  // tiles packed (>= ntiles, a multiple of kPackTileAlign)
   int kb = 0;          // K=32 fp16 MFMAs per 16x16 distance tile
   DevBuf<uint32_t> A, B;  // two fp16 per dword
   DevBuf<float> z;     // scaled coordinates, row-major [n][d] (direct path)
@@ -82,6 +83,10 @@ inline float kernel_scale(int kind) {
   }
 }
 
+// Packed tile counts are padded to a multiple of this (512 points) so the
+// symmetric product's 256-point blocks never read past the packing.
+constexpr int64_t kPackTileAlign = 32;
+
 // Builds packed operands (and scaled coordinates) for n points X[n][d].
 void pack_points(const float* X_dev, int64_t n, const Coords& co,
                  PackedPoints& pp, hipStream_t st);
@@ -110,6 +115,7 @@ struct MatvecWorkspace {
   DevBuf<uint32_t> colmax;       // per-column max |V| (fp16 scaling of the product)
   DevBuf<uint32_t> colmax_part;  // [64][chunks] row-chunk maxima
   DevBuf<float> partial;  // split-K partial sums
+  DevBuf<float> sym_tp;   // transposed partial sums of the symmetric product
   // Fixed-arena mode (allocation-free callers): when arena is set, every work
   // buffer above is carved from [arena, arena + arena_bytes) instead of being
   // grown with hipMalloc; the split count is capped so the partial sums fit,
@@ -123,9 +129,18 @@ struct MatvecWorkspace {
   int64_t tile_calls = 0;
 };
 
+// A square product (rows and cols the same packed points) with 2..16
+// right-hand sides runs on the symmetric kernel, which forms each
+// off-diagonal kernel value once for both of its entries, when the points fill
+// at least kSymMinBlocks 256-point blocks and its transposed partial sums
+// (n^2/8 bytes) stay within kSymMaxBytes.  The environment variable
+// MGP_SYM_MATVEC=0 turns that route off, =1 takes it for every square product
+// the kernel can serve (any n), for tests and measurements.
 void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,
                   MatvecWorkspace& ws, hipStream_t st, int force_splits = 0);
+constexpr int64_t kSymMinBlocks = 48;
+constexpr double kSymMaxBytes = 16e9;
 
 // Bytes of work buffers one fused_matvec call with ncols right-hand sides
 // over cols needs at the least (no split partials): the arena size below which

@@ -20,6 +20,7 @@
 #include "matvec.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -660,6 +661,377 @@ __global__ void k_reduce_splits4(const float* __restrict__ partial, int splits, 
   *reinterpret_cast<f4*>(out + idx) = o;
 }
 
+// ---------------------------------------------------------------------------
+// Symmetric product K(X, X) V (rows and columns the same points, 2..16
+// right-hand sides): every off-diagonal kernel value is formed once and used
+// twice, out[i] += k_ij V[j] and out[j] += k_ij V[i], which halves the
+// transcendental and VALU work that bounds the tile kernel.
+//
+// The points form nb blocks of kSymRows; row block b owns the diagonal block
+// and the off-diagonal column blocks J = (b + delta) mod nb for
+// delta = 1 .. sym_span(b, nb), so every unordered pair of blocks is formed
+// exactly once and each row block carries the same work.  Workgroup (b, s)
+// takes deltas [s dps, (s + 1) dps); its kSymWaves waves own 64 rows each.
+// Per column-tile pair a wave forms its 4 row tiles exactly as k_fused_tile
+// (distances, values, forward product into out[i]), and also:
+//   * stores each row tile's fp16 values (hi and lo, both column tiles) to a
+//     wave-private LDS scratch as 8-byte chunks (row i, columns 4s .. 4s + 3)
+//     at chunk index 16 s + (i ^ 4 s), a swizzle under which both the
+//     stores and the transposed reads below touch every bank once per 16
+//     lanes;
+//   * reads them back with ds_read_b64_tr_b16 (lane 16g + 4e + s fetches the
+//     chunk of row 4g + e, columns 4s ..; the instruction then hands lane
+//     16g + k the elements P[4g + e][k], e = 0..3): the values transposed into the B
+//     operand of O_J^T += V_I^T P, contracted over the rows of a row-tile
+//     pair with the same K permutation as the packed right-hand sides (so
+//     V_I is the packed V of the row pair, loaded once per wave);
+//   * hands its transposed sums (32 columns x 16 right-hand sides over its 64
+//     rows) to the workgroup through LDS; after the next barrier the
+//     waves' sums are added in wave order and written to
+//     tp[b][delta - 1][column][c].
+// The diagonal block is formed once without the transposed half (both of its
+// triangles), with the exact zero self-distance restored on diagonal tiles.
+// k_sym_reduce sums, per point, the forward split partials and the transposed
+// partials of every row block that formed its column block, in a fixed order.
+// ---------------------------------------------------------------------------
+constexpr int kSymR = 4;                            // row tiles per wave
+constexpr int kSymWaves = 8;                        // waves per workgroup
+constexpr int kSymRows = 16 * kSymR * kSymWaves;    // rows (and columns) per block
+constexpr int kSymPairs = kSymRows / 32;            // column-tile pairs per block
+constexpr int kSymStages = kSymPairs / kStageSteps; // LDS stages per block
+constexpr int kSymSchedValu = 6;                    // VALU instructions per MFMA slot
+static_assert(kSymRows <= 16 * kPackTileAlign, "blocks must tile the packed points");
+
+// Off-diagonal column blocks formed by row block b of nb.
+__host__ __device__ inline int64_t sym_span(int64_t b, int64_t nb) {
+  if (nb & 1) return (nb - 1) / 2;
+  return b < nb / 2 ? nb / 2 : nb / 2 - 1;
+}
+
+typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+typedef __fp16 tr4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) tr4 lds_tr4;
+
+// Scratch chunk index of (row i, column quad s) of a 16x16 tile.
+__device__ __forceinline__ int sym_chunk(int i, int s) { return 16 * s + (i ^ (4 * s)); }
+
+// ds_read_b64_tr_b16 from the chunk at p.
+__device__ __forceinline__ uint64_t tr_read(const uint64_t* p) {
+  const tr4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+      (lds_tr4*)((__attribute__((address_space(3))) char*)(p)));
+  return __builtin_bit_cast(uint64_t, v);
+}
+
+template <int KIND, int KB>
+__global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
+    const h8* __restrict__ Bi, const h8* __restrict__ Aj, const h8* __restrict__ Vp,
+    int64_t nb, int64_t dps, int64_t hmax, int ncols, const uint32_t* __restrict__ colmax,
+    float* __restrict__ fwd, float* __restrict__ tp, int64_t mpad) {
+  constexpr int R = kSymR, W = kSymWaves;
+  static_assert(R == 4, "the pipeline below is written for two row-tile pairs");
+  static_assert(W >= 4, "a stage's transposed sums are reduced by 256 threads");
+  constexpr bool UNIT_G = KIND != KIND_MATERN52 && KIND != KIND_MATERN32;
+  constexpr int kA = 2 * KB;
+  constexpr int kBlocks = kStageSteps * (kA + 2);
+  __shared__ h8 lds[2][kBlocks][64];
+  // Wave-private value scratch: [column tile][hi, lo][row tile of the pair][chunk].
+  __shared__ uint64_t tsc[W][2][2][2][64];
+  // Transposed sums per stage: [buffer][step][wave][column tile][lane].
+  __shared__ f4 tbuf[2][kStageSteps][W][2][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b = blockIdx.x;
+  const int64_t tile0 = (b * W + wave) * R;
+
+  h8 bi[R][KB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) bi[r][kb] = Bi[((tile0 + r) * KB + kb) * 64 + lane];
+  // Packed right-hand sides of the wave's two row-tile pairs (A operand of the
+  // transposed product).
+  h8 vih[R / 2], vil[R / 2];
+#pragma unroll
+  for (int w = 0; w < R / 2; ++w) {
+    const int64_t upr = tile0 / 2 + w;
+    vih[w] = Vp[(upr * 2) * 64 + lane];
+    vil[w] = Vp[(upr * 2 + 1) * 64 + lane];
+  }
+
+  f4 acc[R];
+  double accd[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    acc[r] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) accd[r][q] = 0.0;
+  }
+  const float clampv = clamp_reg();
+  float one = 1.0f;
+  asm volatile("" : "+v"(one));
+  const int li = lane & 15;
+  const int lj = 4 * (lane >> 4);
+  // Chunk this lane stores (row li, quad lane/16) and the chunk it fetches
+  // for the transposed operand (row 4 (lane/16) + (lane/4)%4, quad lane%4).
+  const int chunk_w = sym_chunk(li, lane >> 4);
+  const int chunk_r = sym_chunk(4 * (lane >> 4) + ((lane >> 2) & 3), lane & 3);
+
+  const int64_t span = sym_span(b, nb);
+  const int64_t d0 = (int64_t)blockIdx.y * dps;
+  const int64_t d1 = min(d0 + dps, span + 1);
+  const int64_t nst = d1 > d0 ? (d1 - d0) * kSymStages : 0;
+  auto stage_delta = [&](int64_t c) { return d0 + c / kSymStages; };
+  auto stage_u0 = [&](int64_t c) {
+    int64_t J = b + stage_delta(c);
+    if (J >= nb) J -= nb;
+    return J * kSymPairs + (c % kSymStages) * kStageSteps;
+  };
+
+  auto fill = [&](int st, int64_t u0) __attribute__((always_inline)) {
+    for (int bb = wave; bb < kStageSteps * kA; bb += W)
+      __builtin_amdgcn_global_load_lds((const g_void*)(Aj + (2 * u0 * KB + bb) * 64 + lane),
+                                       (lds_void*)&lds[st][bb][0], 16, 0, 0);
+    for (int bb = wave; bb < 2 * kStageSteps; bb += W)
+      __builtin_amdgcn_global_load_lds((const g_void*)(Vp + (u0 * 2 + bb) * 64 + lane),
+                                       (lds_void*)&lds[st][kStageSteps * kA + bb][0], 16, 0, 0);
+  };
+
+  // One pair of column tiles against the wave's R row tiles.  SYM adds the
+  // transposed product into tbuf[slot][k][wave]; MASK restores the exact zero
+  // self-distance on diagonal tiles.
+  auto step = [&](int st, int k, int64_t u, int slot, auto mask_tag, auto sym_tag)
+                  __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr bool SYM = decltype(sym_tag)::value;
+    const int64_t jt0 = 2 * u;
+    h8 a0[KB], a1[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      a0[kb] = lds[st][k * kA + kb][lane];
+      a1[kb] = lds[st][k * kA + KB + kb][lane];
+    }
+    const h8 vh = lds[st][kStageSteps * kA + 2 * k][lane];
+    const h8 vl = lds[st][kStageSteps * kA + 2 * k + 1][lane];
+    auto dist = [&](int r, f4& s0, f4& s1) __attribute__((always_inline)) {
+      s0 = f4{0.f, 0.f, 0.f, 0.f};
+      s1 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[kb], bi[r][kb], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[kb], bi[r][kb], s1, 0, 0, 0);
+      }
+    };
+    auto product = [&](int r, const h8& ph, const h8& pl) __attribute__((always_inline)) {
+      f4 a = acc[r];
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, a, 0, 0, 0);
+      a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, a, 0, 0, 0);
+      acc[r] = a;
+    };
+    f4 tacc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+    // Transposed operands of one row-tile pair: [column tile][hi, lo].
+    h8 TP[2][2];
+    auto tr_issue = [&]() __attribute__((always_inline)) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const u64x2 v = {tr_read(&tsc[wave][t][p][0][chunk_r]),
+                           tr_read(&tsc[wave][t][p][1][chunk_r])};
+          TP[t][p] = __builtin_bit_cast(h8, v);
+        }
+      asm volatile("" ::: "memory");
+    };
+    auto tr_product = [&](int w) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f4 a = tacc[t];
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih[w], TP[t][0], a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vil[w], TP[t][0], a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih[w], TP[t][1], a, 0, 0, 0);
+        tacc[t] = a;
+      }
+    };
+    f4 S0[2], S1[2];
+    h8 PH[2], PL[2];
+    dist(0, S0[0], S1[0]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      f4 s0 = S0[r & 1], s1 = S1[r & 1];
+      if (r + 1 < R) dist(r + 1, S0[(r + 1) & 1], S1[(r + 1) & 1]);
+      if (r > 0) product(r - 1, PH[(r - 1) & 1], PL[(r - 1) & 1]);
+      if constexpr (MASK) {
+        const int64_t dt = tile0 + r;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (jt0 == dt && li == lj + q) s0[q] = 0.0f;
+          if (jt0 + 1 == dt && li == lj + q) s1[q] = 0.0f;
+        }
+      }
+      float f0[4], g0[4], f1[4], g1[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        kval_scaled<KIND>(s0[q], clampv, one, f0[q], g0[q]);
+        kval_scaled<KIND>(s1[q], clampv, one, f1[q], g1[q]);
+      }
+      h2 hA, hB, hC, hD, lA, lB, lC, lD;
+      split_pair<UNIT_G>(f0[0], g0[0], f0[1], g0[1], hA, lA);
+      split_pair<UNIT_G>(f0[2], g0[2], f0[3], g0[3], hB, lB);
+      split_pair<UNIT_G>(f1[0], g1[0], f1[1], g1[1], hC, lC);
+      split_pair<UNIT_G>(f1[2], g1[2], f1[3], g1[3], hD, lD);
+      PH[r & 1] = h8{hA[0], hA[1], hB[0], hB[1], hC[0], hC[1], hD[0], hD[1]};
+      PL[r & 1] = h8{lA[0], lA[1], lB[0], lB[1], lC[0], lC[1], lD[0], lD[1]};
+      if constexpr (SYM) {
+        const u64x2 ph = __builtin_bit_cast(u64x2, PH[r & 1]);
+        const u64x2 pl = __builtin_bit_cast(u64x2, PL[r & 1]);
+        tsc[wave][0][0][r & 1][chunk_w] = ph[0];
+        tsc[wave][1][0][r & 1][chunk_w] = ph[1];
+        tsc[wave][0][1][r & 1][chunk_w] = pl[0];
+        tsc[wave][1][1][r & 1][chunk_w] = pl[1];
+        // Row-tile pair w = r/2 complete: fetch its transposed operands now,
+        // multiply them one row tile later (after the next tile's VALU work).
+        if (r & 1) tr_issue();
+        if (r == 2) tr_product(0);
+      }
+    }
+    product(R - 1, PH[(R - 1) & 1], PL[(R - 1) & 1]);
+    if constexpr (SYM) {
+      // Issue order: one MFMA, then kSymSchedValu VALU instructions, through
+      // the step (measured at config 3: 16.8 -> 16.1 ms against the
+      // compiler's default order, which bunches the kernel-value VALU).
+#pragma unroll
+      for (int i = 0; i < R * (2 * KB + 3) + 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kSymSchedValu, 0);
+      }
+    }
+    if constexpr (SYM) {
+      tr_product(R / 2 - 1);
+      tbuf[slot][k][wave][0][lane] = tacc[0];
+      tbuf[slot][k][wave][1][lane] = tacc[1];
+    }
+  };
+  auto flush = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) accd[r][q] += (double)acc[r][q];
+      acc[r] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // Adds the waves' transposed sums of stage c (buffer c & 1) in wave order
+  // and writes them, unscaled, to tp (threads 0..255, one f4 each).
+  auto reduce_stage = [&](int64_t c) __attribute__((always_inline)) {
+    const int slot = (int)(c & 1);
+    const int tid = threadIdx.x;
+    if (tid >= 2 * kStageSteps * 64) return;
+    const int kk = tid >> 7, t = (tid >> 6) & 1, ln = tid & 63;
+    f4 sum = tbuf[slot][kk][0][t][ln];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += tbuf[slot][kk][w][t][ln];
+    const int c0 = 4 * (ln >> 4);
+    f4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int cc = c0 + q;
+      const int shift = cc < ncols ? col_shift(colmax[cc]) : 0;
+      o[q] = ldexpf(sum[q], -(shift + kPScaleLog2));
+    }
+    const int64_t jl = 32 * ((c % kSymStages) * kStageSteps + kk) + 16 * t + (ln & 15);
+    const int64_t blk = b * hmax + stage_delta(c) - 1;
+    *reinterpret_cast<f4*>(tp + (blk * kSymRows + jl) * 16 + c0) = o;
+  };
+
+  const int64_t dlo = tile0 / 2, dhi = dlo + R / 2;
+  if (nst > 0) fill(0, stage_u0(0));
+  int since_flush = 0;
+  for (int64_t c = 0; c < nst; ++c) {
+    const int st = (int)(c & 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (c + 1 < nst) fill(st ^ 1, stage_u0(c + 1));
+    if (c > 0 && stage_delta(c - 1) > 0) reduce_stage(c - 1);
+    const int64_t u0 = stage_u0(c);
+    if (stage_delta(c) == 0) {
+      for (int k = 0; k < kStageSteps; ++k) {
+        const int64_t u = u0 + k;
+        if (u >= dlo && u < dhi)
+          step(st, k, u, st, std::true_type{}, std::false_type{});
+        else
+          step(st, k, u, st, std::false_type{}, std::false_type{});
+      }
+    } else {
+      for (int k = 0; k < kStageSteps; ++k)
+        step(st, k, u0 + k, st, std::false_type{}, std::true_type{});
+    }
+    since_flush += kStageSteps;
+    if (since_flush >= kFlushTiles / 2) {
+      flush();
+      since_flush = 0;
+    }
+  }
+  if (nst > 0 && stage_delta(nst - 1) > 0) {
+    __syncthreads();
+    reduce_stage(nst - 1);
+  }
+  flush();
+
+  // Forward partials of this split, unscaled by the fp16 factors.
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = lj + q;
+      const int64_t i = 16 * (tile0 + r) + li;
+      const int shift = c < ncols ? col_shift(colmax[c]) : 0;
+      fwd[((int64_t)blockIdx.y * 16 + c) * mpad + i] =
+          (float)ldexp(accd[r][q] + (double)acc[r][q], -(shift + kPScaleLog2));
+    }
+  }
+}
+
+// out[c*m + j] = os * (sum_s fwd[s][c][j] + sum of the transposed partials of
+// the row blocks that formed j's column block, in delta order) + noise V.
+// One thread per point, all right-hand sides (fp64 sums).
+__global__ __launch_bounds__(256) void k_sym_reduce(const float* __restrict__ fwd, int splits,
+                                                    const float* __restrict__ tp, int64_t nb,
+                                                    int64_t hmax, int64_t mpad, int64_t m,
+                                                    int ncols, float os, float noise,
+                                                    const float* __restrict__ Vin,
+                                                    float* __restrict__ out) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= m) return;
+  double tot[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) tot[c] = 0.0;
+  for (int s = 0; s < splits; ++s)
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c < ncols) tot[c] += fwd[((int64_t)s * 16 + c) * mpad + j];
+  const int64_t J = j / kSymRows, jl = j - J * kSymRows;
+  for (int64_t dl = 1; dl <= hmax; ++dl) {
+    int64_t bb = J - dl;
+    if (bb < 0) bb += nb;
+    if (dl > sym_span(bb, nb)) continue;
+    const f4* p = reinterpret_cast<const f4*>(tp + ((bb * hmax + dl - 1) * kSymRows + jl) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f4 v = p[q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tot[4 * q + e] += v[e];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    if (c < ncols) {
+      const int64_t idx = (int64_t)c * m + j;
+      out[idx] = fmaf(noise, Vin[idx], os * (float)tot[c]);
+    }
+  }
+}
+
 // Task-mixing reduction: one thread per (column block cc, row i) sums the split
 // partials of the block's T columns once, then writes the T mixed outputs
 // out[(cc*T + t)*m + i] (+)= sum_t' mix[t*T + t'] (os sum_s partial + noise V).
@@ -906,18 +1278,19 @@ void pack_points(const float* X_dev, int64_t n, const Coords& co,
   pp.n = n;
   // Even tile count: the tile kernel walks column tiles in pairs.
   pp.ntiles = 2 * ceil_div(std::max<int64_t>(n, 1), 32);
+  pp.ntiles_alloc = round_up(pp.ntiles, kPackTileAlign);
   // Beyond kMaxMfmaDim only the scaled coordinates are built (direct path).
   pp.kb = d <= kMaxMfmaDim ? split_mfma_count(d) : 0;
-  const size_t sz = (size_t)pp.ntiles * std::max(pp.kb, 1) * 64 * 4;  // dwords
+  const size_t sz = (size_t)pp.ntiles_alloc * std::max(pp.kb, 1) * 64 * 4;  // dwords
   pp.A.ensure(sz);
   pp.B.ensure(sz);
   pp.z.ensure((size_t)std::max<int64_t>(n, 1) * d);
-  const int64_t threads = pp.ntiles * 16;
+  const int64_t threads = pp.ntiles_alloc * 16;
   uint32_t* mx = pp.max_norm_dev.ensure(1);
   hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, st, mx, (int64_t)1, 0u);
   hipLaunchKernelGGL(k_pack_points, dim3((unsigned)ceil_div(threads, 256)),
                      dim3(256), 0, st, X_dev, n, d, co.coef.ptr, pp.kb,
-                     pp.ntiles, reinterpret_cast<uint16_t*>(pp.A.ptr),
+                     pp.ntiles_alloc, reinterpret_cast<uint16_t*>(pp.A.ptr),
                      reinterpret_cast<uint16_t*>(pp.B.ptr), pp.z.ptr, mx);
   MGP_HIP_CHECK(hipGetLastError());
   uint32_t bits = 0;
@@ -962,6 +1335,90 @@ size_t fused_matvec_min_arena(const PackedPoints& cols, int ncols) {
   return b;
 }
 
+namespace {
+
+// Symmetric-route choice for one column chunk of nc right-hand sides.
+bool sym_route(const MatvecArgs& a, const PackedPoints& rows, const PackedPoints& cols, int nc,
+               const MatvecWorkspace& ws) {
+  if (!a.square || a.mix != nullptr || ws.arena != nullptr || &rows != &cols) return false;
+  if (nc < 2 || nc > 16 || a.m != a.n || a.n != rows.n) return false;
+  const char* env = std::getenv("MGP_SYM_MATVEC");
+  const int mode = env == nullptr ? -1 : (env[0] == '0' ? 0 : 1);
+  if (mode == 0) return false;
+  const int64_t nb = ceil_div(std::max<int64_t>(a.n, 1), kSymRows);
+  if (nb * kSymRows > rows.ntiles_alloc * 16) return false;
+  if (mode < 0 && nb < kSymMinBlocks) return false;
+  const double tp_bytes = (double)nb * (double)(nb / 2) * kSymRows * 16 * 4;
+  return tp_bytes <= kSymMaxBytes;
+}
+
+using SymFn = void (*)(const h8*, const h8*, const h8*, int64_t, int64_t, int64_t, int,
+                       const uint32_t*, float*, float*, int64_t);
+
+template <int KIND>
+SymFn pick_sym(int kb) {
+  switch (kb) {
+    case 1: return k_sym_tile<KIND, 1>;
+    case 2: return k_sym_tile<KIND, 2>;
+    case 3: return k_sym_tile<KIND, 3>;
+  }
+  return nullptr;
+}
+
+// out = (K + noise I) V for nc <= 16 columns of V on the symmetric kernel.
+void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, int nc,
+                float* outc, MatvecWorkspace& ws, hipStream_t st) {
+  const int64_t n = a.n;
+  const int64_t nb = ceil_div(std::max<int64_t>(n, 1), kSymRows);
+  const int64_t hmax = nb / 2;
+  const int64_t pairs = nb * kSymPairs;
+  const int64_t mpad = nb * kSymRows;
+
+  uint32_t* colmax = ws.colmax.ensure(64);
+  const int chunks = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(n, 1), 4096), 64);
+  uint32_t* cpart = ws.colmax_part.ensure((size_t)64 * chunks);
+  const int vec4 = (n % 4 == 0 && reinterpret_cast<uintptr_t>(Vc) % 16 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(k_col_absmax_part, dim3((unsigned)chunks, (unsigned)nc), dim3(256), 0, st,
+                     Vc, n, vec4, cpart);
+  hipLaunchKernelGGL(k_col_absmax_final, dim3((unsigned)nc), dim3(64), 0, st, cpart, chunks,
+                     colmax);
+  const int64_t total = pairs * 64;  // 8-half vectors per part, one column group
+  float* vp = ws.vpack.ensure((size_t)total * 2 * 4);
+  hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, Vc,
+                     n, nc, 1, pairs, colmax, vec4, reinterpret_cast<h8*>(vp));
+  MGP_HIP_CHECK(hipGetLastError());
+
+  // Splits of the delta range: >= 2048 workgroups where the blocks allow.
+  int64_t splits = std::min<int64_t>(std::max<int64_t>(ceil_div(2048, nb), 1), hmax + 1);
+  const int64_t dps = ceil_div(hmax + 1, splits);
+  splits = ceil_div(hmax + 1, dps);
+  float* fwd = ws.partial.ensure((size_t)splits * 16 * mpad);
+  float* tp = ws.sym_tp.ensure((size_t)std::max<int64_t>(nb * hmax, 1) * kSymRows * 16);
+
+  SymFn fn = a.kind == KIND_RBF        ? pick_sym<KIND_RBF>(pts.kb)
+             : a.kind == KIND_MATERN32 ? pick_sym<KIND_MATERN32>(pts.kb)
+                                       : pick_sym<KIND_MATERN52>(pts.kb);
+  MGP_REQUIRE(fn != nullptr, "no symmetric tile kernel for this shape");
+  if (ws.time_tile) MGP_HIP_CHECK(hipEventRecord(ws.ev0, st));
+  hipLaunchKernelGGL(fn, dim3((unsigned)nb, (unsigned)splits), dim3(64 * kSymWaves), 0, st,
+                     reinterpret_cast<const h8*>(pts.B.ptr), reinterpret_cast<const h8*>(pts.A.ptr),
+                     reinterpret_cast<const h8*>(vp), nb, dps, hmax, nc, colmax, fwd, tp, mpad);
+  MGP_HIP_CHECK(hipGetLastError());
+  if (ws.time_tile) {
+    MGP_HIP_CHECK(hipEventRecord(ws.ev1, st));
+    MGP_HIP_CHECK(hipEventSynchronize(ws.ev1));
+    float ms = 0.f;
+    MGP_HIP_CHECK(hipEventElapsedTime(&ms, ws.ev0, ws.ev1));
+    ws.tile_ms += ms;
+    ws.tile_calls += 1;
+  }
+  hipLaunchKernelGGL(k_sym_reduce, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st, fwd,
+                     (int)splits, tp, nb, hmax, mpad, n, nc, a.outputscale, a.noise, Vc, outc);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
 void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,
                   MatvecWorkspace& ws, hipStream_t st, int force_splits) {
@@ -987,6 +1444,10 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
     const float* Vc = V_dev + (int64_t)c0 * a.n;
     float* outc = out_dev + (int64_t)c0 * a.m;
     const float* Vin = a.square ? V_dev + (int64_t)c0 * a.m : nullptr;
+    if (force_splits <= 0 && sym_route(a, rows, cols, nc, ws)) {
+      sym_matvec(a, rows, Vc, nc, outc, ws, st);
+      continue;
+    }
 
     // Pack right-hand sides.
     const int64_t col_pairs = col_tiles / 2;

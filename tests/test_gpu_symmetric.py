@@ -1,0 +1,108 @@
+"""Parity of the symmetric K(X, X) V kernel (each off-diagonal kernel value
+formed once, used for both of its entries) with the float64 oracle.
+
+MGP_SYM_MATVEC=1 routes every square product with 2..16 right-hand sides
+through it (any n), =0 keeps the one-sided tile kernel; unset, the symmetric
+route is taken from 48 blocks of 512 points on.  Bar: norm-wise relative error
+<= 1e-5 per right-hand side (the north star's matvec bar)."""
+
+import numpy as np
+import pytest
+
+from mojogp_amd._provider import NativeProvider
+from oracle import kernels as ok
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _relerr(got, ref):
+    got = np.atleast_2d(np.asarray(got, dtype=np.float64))
+    ref = np.atleast_2d(ref)
+    num = np.linalg.norm(got - ref, axis=1)
+    den = np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
+    return float(np.max(num / den))
+
+
+def _product(kind, ard, X, V, params, noise):
+    p = NativeProvider(kind, ard, X, params, noise)
+    try:
+        return p.forward_matvec(V)
+    finally:
+        p.close()
+
+
+# kind, ard, d, n, t: 1 .. 5 blocks of 512 points (odd and even), partial last
+# blocks, every K=32 MFMA count (d = 1, 8, 16, 30), 2 .. 16 right-hand sides.
+CASES = [
+    (ok.MATERN52, True, 16, 17, 2),
+    (ok.RBF, True, 8, 256, 16),
+    (ok.MATERN52, True, 16, 300, 16),
+    (ok.MATERN32, True, 4, 777, 11),
+    (ok.RBF, False, 1, 1000, 16),
+    (ok.MATERN52, True, 30, 1290, 5),
+    (ok.RBF, True, 6, 2048, 3),
+    (ok.MATERN52, False, 3, 2500, 16),
+]
+
+
+@pytest.mark.parametrize("kind,ard,d,n,t", CASES)
+def test_symmetric_forward_parity(monkeypatch, kind, ard, d, n, t):
+    rng = np.random.default_rng(4000 + 13 * d + n)
+    print(f"symmetric case kind={kind} ard={ard} d={d} n={n} t={t}", flush=True)
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    ls = rng.uniform(0.6, 1.6, size=d if ard else 1)
+    params = np.concatenate([ls, [1.3]]).astype(np.float32)
+    ref = ok.forward_matvec(kind, X, V, params, 0.05, ard)
+    monkeypatch.setenv("MGP_SYM_MATVEC", "1")
+    got = _product(kind, ard, X, V, params, 0.05)
+    assert got.shape == V.shape and np.all(np.isfinite(got))
+    err = _relerr(got, ref)
+    print(f"  relerr {err:.3e}", flush=True)
+    assert err <= TOL
+    # A second product through the same workspaces (grown buffers reused).
+    monkeypatch.setenv("MGP_SYM_MATVEC", "0")
+    one_sided = _product(kind, ard, X, V, params, 0.05)
+    assert _relerr(got, one_sided.astype(np.float64)) <= 2 * TOL
+
+
+@pytest.mark.parametrize("kind,n,t", [(ok.MATERN52, 24_577, 16), (ok.RBF, 25_000, 9)])
+def test_symmetric_auto_route_against_one_sided(monkeypatch, kind, n, t):
+    """Above the block threshold the default route is symmetric: it agrees with
+    the one-sided kernel on every entry and with the oracle on sampled rows."""
+    rng = np.random.default_rng(n)
+    d = 8
+    print(f"symmetric auto case kind={kind} n={n} t={t}", flush=True)
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = np.concatenate([rng.uniform(0.7, 1.4, size=d), [0.9]]).astype(np.float32)
+    monkeypatch.delenv("MGP_SYM_MATVEC", raising=False)
+    got = _product(kind, True, X, V, params, 0.1)
+    monkeypatch.setenv("MGP_SYM_MATVEC", "0")
+    one_sided = _product(kind, True, X, V, params, 0.1)
+    rows = np.sort(rng.choice(n, size=128, replace=False))
+    ref = ok.forward_matvec(kind, X, V, params, 0.1, True, rows=rows, block=64)
+    e_ref = _relerr(got[:, rows], ref)
+    e_one = _relerr(got, one_sided.astype(np.float64))
+    print(f"  sampled-row relerr {e_ref:.3e}, vs one-sided {e_one:.3e}", flush=True)
+    assert e_ref <= TOL
+    assert e_one <= 2 * TOL
+
+
+def test_symmetric_repeated_calls_bit_identical(monkeypatch):
+    """Fixed-order reductions: the same product twice gives the same bits."""
+    rng = np.random.default_rng(5)
+    n, d, t = 3000, 5, 16
+    X = rng.normal(size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    params = np.array([1.1] * d + [1.0], dtype=np.float32)
+    monkeypatch.setenv("MGP_SYM_MATVEC", "1")
+    p = NativeProvider(ok.MATERN52, True, X, params, 0.1)
+    try:
+        a = p.forward_matvec(V)
+        b = p.forward_matvec(V)
+    finally:
+        p.close()
+    assert np.array_equal(a, b)
