@@ -83,9 +83,9 @@ inline float kernel_scale(int kind) {
   }
 }
 
-// Packed tile counts are padded to a multiple of this (512 points) so the
-// symmetric product's 256-point blocks never read past the packing.
-constexpr int64_t kPackTileAlign = 32;
+// Packed tile counts are padded to a multiple of this (1536 points) so the
+// symmetric product's blocks (256, 512 or 768 points) never read past the packing.
+constexpr int64_t kPackTileAlign = 96;
 
 // Builds packed operands (and scaled coordinates) for n points X[n][d].
 void pack_points(const float* X_dev, int64_t n, const Coords& co,

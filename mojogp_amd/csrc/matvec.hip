@@ -684,7 +684,7 @@ __global__ void k_reduce_splits4(const float* __restrict__ partial, int splits, 
 //     16g + k the elements P[4g + e][k], e = 0..3): the values transposed into the B
 //     operand of O_J^T += V_I^T P, contracted over the rows of a row-tile
 //     pair with the same K permutation as the packed right-hand sides (so
-//     V_I is the packed V of the row pair, loaded once per wave);
+//     V_I is the packed V of the row pair, copied once per wave into LDS);
 //   * hands its transposed sums (32 columns x 16 right-hand sides over its 64
 //     rows) to the workgroup through LDS; after the next barrier the
 //     waves' sums are added in wave order and written to
@@ -698,9 +698,10 @@ constexpr int kSymR = 4;                            // row tiles per wave
 constexpr int kSymWaves = 8;                        // waves per workgroup
 constexpr int kSymRows = 16 * kSymR * kSymWaves;    // rows (and columns) per block
 constexpr int kSymPairs = kSymRows / 32;            // column-tile pairs per block
-constexpr int kSymStages = kSymPairs / kStageSteps; // LDS stages per block
+constexpr int kSymSteps = 2;                        // column-tile pairs per LDS stage
+constexpr int kSymStages = kSymPairs / kSymSteps;   // LDS stages per block
 constexpr int kSymSchedValu = 6;                    // VALU instructions per MFMA slot
-static_assert(kSymRows <= 16 * kPackTileAlign, "blocks must tile the packed points");
+static_assert((16 * kPackTileAlign) % kSymRows == 0, "blocks must tile the packed points");
 
 // Off-diagonal column blocks formed by row block b of nb.
 __host__ __device__ inline int64_t sym_span(int64_t b, int64_t nb) {
@@ -729,15 +730,16 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     float* __restrict__ fwd, float* __restrict__ tp, int64_t mpad) {
   constexpr int R = kSymR, W = kSymWaves;
   static_assert(R == 4, "the pipeline below is written for two row-tile pairs");
-  static_assert(W >= 4, "a stage's transposed sums are reduced by 256 threads");
+  static_assert(64 * W >= 256 * kSymSteps, "a stage's transposed sums are reduced by "
+                                           "256 threads per column-tile pair");
   constexpr bool UNIT_G = KIND != KIND_MATERN52 && KIND != KIND_MATERN32;
   constexpr int kA = 2 * KB;
-  constexpr int kBlocks = kStageSteps * (kA + 2);
+  constexpr int kBlocks = kSymSteps * (kA + 2);
   __shared__ h8 lds[2][kBlocks][64];
   // Wave-private value scratch: [column tile][hi, lo][row tile of the pair][chunk].
   __shared__ uint64_t tsc[W][2][2][2][64];
   // Transposed sums per stage: [buffer][step][wave][column tile][lane].
-  __shared__ f4 tbuf[2][kStageSteps][W][2][64];
+  __shared__ f4 tbuf[2][kSymSteps][W][2][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -750,13 +752,13 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) bi[r][kb] = Bi[((tile0 + r) * KB + kb) * 64 + lane];
   // Packed right-hand sides of the wave's two row-tile pairs (A operand of the
-  // transposed product).
-  h8 vih[R / 2], vil[R / 2];
+  // transposed product), kept in LDS and read where they are used.
+  __shared__ h8 vrow[W][R / 2][2][64];
 #pragma unroll
   for (int w = 0; w < R / 2; ++w) {
     const int64_t upr = tile0 / 2 + w;
-    vih[w] = Vp[(upr * 2) * 64 + lane];
-    vil[w] = Vp[(upr * 2 + 1) * 64 + lane];
+    vrow[wave][w][0][lane] = Vp[(upr * 2) * 64 + lane];
+    vrow[wave][w][1][lane] = Vp[(upr * 2 + 1) * 64 + lane];
   }
 
   f4 acc[R];
@@ -785,16 +787,33 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
   auto stage_u0 = [&](int64_t c) {
     int64_t J = b + stage_delta(c);
     if (J >= nb) J -= nb;
-    return J * kSymPairs + (c % kSymStages) * kStageSteps;
+    return J * kSymPairs + (c % kSymStages) * kSymSteps;
   };
 
-  auto fill = [&](int st, int64_t u0) __attribute__((always_inline)) {
-    for (int bb = wave; bb < kStageSteps * kA; bb += W)
-      __builtin_amdgcn_global_load_lds((const g_void*)(Aj + (2 * u0 * KB + bb) * 64 + lane),
-                                       (lds_void*)&lds[st][bb][0], 16, 0, 0);
-    for (int bb = wave; bb < 2 * kStageSteps; bb += W)
-      __builtin_amdgcn_global_load_lds((const g_void*)(Vp + (u0 * 2 + bb) * 64 + lane),
-                                       (lds_void*)&lds[st][kStageSteps * kA + bb][0], 16, 0, 0);
+  // Stage operands go through registers: the loads of stage c + 1 are issued
+  // at the top of stage c and written to the other LDS buffer at its end, so
+  // the wait for them falls after stage c's arithmetic.  (An LDS DMA fill
+  // makes the compiler wait for it before the first LDS read of stage c,
+  // since it cannot tell the two buffers apart.)
+  constexpr int kFillPerWave = (kBlocks + W - 1) / W;
+  h8 pre[kFillPerWave];
+  // Branch-free (one load per slot, blocks past the stage clamped onto its
+  // last block) so the loads stay in one basic block and no wait separates them.
+  auto fetch = [&](int64_t u0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < kFillPerWave; ++q) {
+      const int bb = min(wave + q * W, kBlocks - 1);
+      const h8* src = bb < kSymSteps * kA ? Aj + (2 * u0 * KB + bb) * 64
+                                          : Vp + (u0 * 2 + (bb - kSymSteps * kA)) * 64;
+      pre[q] = src[lane];
+    }
+  };
+  auto commit = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < kFillPerWave; ++q) {
+      const int bb = wave + q * W;
+      if (bb < kBlocks) lds[st][bb][lane] = pre[q];
+    }
   };
 
   // One pair of column tiles against the wave's R row tiles.  SYM adds the
@@ -811,8 +830,8 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
       a0[kb] = lds[st][k * kA + kb][lane];
       a1[kb] = lds[st][k * kA + KB + kb][lane];
     }
-    const h8 vh = lds[st][kStageSteps * kA + 2 * k][lane];
-    const h8 vl = lds[st][kStageSteps * kA + 2 * k + 1][lane];
+    const h8 vh = lds[st][kSymSteps * kA + 2 * k][lane];
+    const h8 vl = lds[st][kSymSteps * kA + 2 * k + 1][lane];
     auto dist = [&](int r, f4& s0, f4& s1) __attribute__((always_inline)) {
       s0 = f4{0.f, 0.f, 0.f, 0.f};
       s1 = f4{0.f, 0.f, 0.f, 0.f};
@@ -845,12 +864,13 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
       asm volatile("" ::: "memory");
     };
     auto tr_product = [&](int w) __attribute__((always_inline)) {
+      const h8 vih = vrow[wave][w][0][lane], vil = vrow[wave][w][1][lane];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         f4 a = tacc[t];
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih[w], TP[t][0], a, 0, 0, 0);
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vil[w], TP[t][0], a, 0, 0, 0);
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih[w], TP[t][1], a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih, TP[t][0], a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vil, TP[t][0], a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih, TP[t][1], a, 0, 0, 0);
         tacc[t] = a;
       }
     };
@@ -922,40 +942,49 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     }
   };
   // Adds the waves' transposed sums of stage c (buffer c & 1) in wave order
-  // and writes them, unscaled, to tp (threads 0..255, one f4 each).
-  auto reduce_stage = [&](int64_t c) __attribute__((always_inline)) {
-    const int slot = (int)(c & 1);
-    const int tid = threadIdx.x;
-    if (tid >= 2 * kStageSteps * 64) return;
-    const int kk = tid >> 7, t = (tid >> 6) & 1, ln = tid & 63;
-    f4 sum = tbuf[slot][kk][0][t][ln];
+  // and writes them, unscaled, to tp.  Thread u < kSymSteps * 256 owns two
+  // right-hand sides (2h, 2h + 1 of the lane's four) of one lane of one
+  // column tile; its column scales are fixed for the kernel.
+  constexpr int kRedUnits = kSymSteps * 256;
+  const int ru = threadIdx.x;
+  const int r_kk = ru >> 8, r_t = (ru >> 7) & 1, r_ln = (ru >> 1) & 63, r_h = ru & 1;
+  const int r_c = 4 * (r_ln >> 4) + 2 * r_h;
+  f2 r_scale = {0.f, 0.f};
+  if (ru < kRedUnits) {
 #pragma unroll
-    for (int w = 1; w < W; ++w) sum += tbuf[slot][kk][w][t][ln];
-    const int c0 = 4 * (ln >> 4);
-    f4 o;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int cc = c0 + q;
+    for (int e = 0; e < 2; ++e) {
+      const int cc = r_c + e;
       const int shift = cc < ncols ? col_shift(colmax[cc]) : 0;
-      o[q] = ldexpf(sum[q], -(shift + kPScaleLog2));
+      r_scale[e] = ldexpf(1.0f, -(shift + kPScaleLog2));
     }
-    const int64_t jl = 32 * ((c % kSymStages) * kStageSteps + kk) + 16 * t + (ln & 15);
+  }
+  auto reduce_stage = [&](int64_t c) __attribute__((always_inline)) {
+    if (ru >= kRedUnits) return;
+    const int slot = (int)(c & 1);
+    const float* src = reinterpret_cast<const float*>(&tbuf[slot][r_kk][0][r_t][r_ln]) + 2 * r_h;
+    constexpr int wstride = (int)(sizeof(tbuf[0][0][0]) / sizeof(float));
+    f2 sum = *reinterpret_cast<const f2*>(src);
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += *reinterpret_cast<const f2*>(src + w * wstride);
+    const int64_t jl = 32 * ((c % kSymStages) * kSymSteps + r_kk) + 16 * r_t + (r_ln & 15);
     const int64_t blk = b * hmax + stage_delta(c) - 1;
-    *reinterpret_cast<f4*>(tp + (blk * kSymRows + jl) * 16 + c0) = o;
+    *reinterpret_cast<f2*>(tp + (blk * kSymRows + jl) * 16 + r_c) = sum * r_scale;
   };
 
   const int64_t dlo = tile0 / 2, dhi = dlo + R / 2;
-  if (nst > 0) fill(0, stage_u0(0));
+  if (nst > 0) {
+    fetch(stage_u0(0));
+    commit(0);
+  }
   int since_flush = 0;
   for (int64_t c = 0; c < nst; ++c) {
     const int st = (int)(c & 1);
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (c + 1 < nst) fill(st ^ 1, stage_u0(c + 1));
+    if (c + 1 < nst) fetch(stage_u0(c + 1));
     if (c > 0 && stage_delta(c - 1) > 0) reduce_stage(c - 1);
     const int64_t u0 = stage_u0(c);
     if (stage_delta(c) == 0) {
-      for (int k = 0; k < kStageSteps; ++k) {
+      for (int k = 0; k < kSymSteps; ++k) {
         const int64_t u = u0 + k;
         if (u >= dlo && u < dhi)
           step(st, k, u, st, std::true_type{}, std::false_type{});
@@ -963,14 +992,15 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
           step(st, k, u, st, std::false_type{}, std::false_type{});
       }
     } else {
-      for (int k = 0; k < kStageSteps; ++k)
+      for (int k = 0; k < kSymSteps; ++k)
         step(st, k, u0 + k, st, std::false_type{}, std::true_type{});
     }
-    since_flush += kStageSteps;
+    since_flush += kSymSteps;
     if (since_flush >= kFlushTiles / 2) {
       flush();
       since_flush = 0;
     }
+    if (c + 1 < nst) commit(st ^ 1);
   }
   if (nst > 0 && stage_delta(nst - 1) > 0) {
     __syncthreads();
