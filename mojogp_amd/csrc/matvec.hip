@@ -701,6 +701,7 @@ constexpr int kSymPairs = kSymRows / 32;            // column-tile pairs per blo
 constexpr int kSymSteps = 2;                        // column-tile pairs per LDS stage
 constexpr int kSymStages = kSymPairs / kSymSteps;   // LDS stages per block
 constexpr int kSymSchedValu = 6;                    // VALU instructions per MFMA slot
+constexpr int kXcds = 8;                            // XCDs of the MI355X
 static_assert((16 * kPackTileAlign) % kSymRows == 0, "blocks must tile the packed points");
 
 // Off-diagonal column blocks formed by row block b of nb.
@@ -726,8 +727,9 @@ __device__ __forceinline__ uint64_t tr_read(const uint64_t* p) {
 template <int KIND, int KB>
 __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     const h8* __restrict__ Bi, const h8* __restrict__ Aj, const h8* __restrict__ Vp,
-    int64_t nb, int64_t dps, int64_t hmax, int ncols, const uint32_t* __restrict__ colmax,
-    float* __restrict__ fwd, float* __restrict__ tp, int64_t mpad) {
+    int64_t nb, int64_t splits, int64_t dps, int64_t hmax, int ncols,
+    const uint32_t* __restrict__ colmax, float* __restrict__ fwd, float* __restrict__ tp,
+    int64_t mpad) {
   constexpr int R = kSymR, W = kSymWaves;
   static_assert(R == 4, "the pipeline below is written for two row-tile pairs");
   static_assert(64 * W >= 256 * kSymSteps, "a stage's transposed sums are reduced by "
@@ -743,7 +745,15 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b = blockIdx.x;
+  // XCD-aware order: the hardware deals consecutive workgroups to the eight
+  // XCDs in turn; logical work item L = xcd * per + k (b fastest) gives each
+  // XCD a run of consecutive row blocks, which read the same column blocks a
+  // step apart from its L2.  Items past nb * splits leave before any barrier.
+  const int64_t per = (int64_t)gridDim.x / kXcds;
+  const int64_t L = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (L >= nb * splits) return;
+  const int64_t b = L % nb;
+  const int64_t split = L / nb;
   const int64_t tile0 = (b * W + wave) * R;
 
   h8 bi[R][KB];
@@ -780,7 +790,7 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
   const int chunk_r = sym_chunk(4 * (lane >> 4) + ((lane >> 2) & 3), lane & 3);
 
   const int64_t span = sym_span(b, nb);
-  const int64_t d0 = (int64_t)blockIdx.y * dps;
+  const int64_t d0 = split * dps;
   const int64_t d1 = min(d0 + dps, span + 1);
   const int64_t nst = d1 > d0 ? (d1 - d0) * kSymStages : 0;
   auto stage_delta = [&](int64_t c) { return d0 + c / kSymStages; };
@@ -1016,7 +1026,7 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
       const int c = lj + q;
       const int64_t i = 16 * (tile0 + r) + li;
       const int shift = c < ncols ? col_shift(colmax[c]) : 0;
-      fwd[((int64_t)blockIdx.y * 16 + c) * mpad + i] =
+      fwd[(split * 16 + c) * mpad + i] =
           (float)ldexp(accd[r][q] + (double)acc[r][q], -(shift + kPScaleLog2));
     }
   }
@@ -1382,8 +1392,8 @@ bool sym_route(const MatvecArgs& a, const PackedPoints& rows, const PackedPoints
   return tp_bytes <= kSymMaxBytes;
 }
 
-using SymFn = void (*)(const h8*, const h8*, const h8*, int64_t, int64_t, int64_t, int,
-                       const uint32_t*, float*, float*, int64_t);
+using SymFn = void (*)(const h8*, const h8*, const h8*, int64_t, int64_t, int64_t, int64_t,
+                       int, const uint32_t*, float*, float*, int64_t);
 
 template <int KIND>
 SymFn pick_sym(int kb) {
@@ -1430,9 +1440,11 @@ void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, i
                                        : pick_sym<KIND_MATERN52>(pts.kb);
   MGP_REQUIRE(fn != nullptr, "no symmetric tile kernel for this shape");
   if (ws.time_tile) MGP_HIP_CHECK(hipEventRecord(ws.ev0, st));
-  hipLaunchKernelGGL(fn, dim3((unsigned)nb, (unsigned)splits), dim3(64 * kSymWaves), 0, st,
+  const int64_t items = round_up(nb * splits, kXcds);
+  hipLaunchKernelGGL(fn, dim3((unsigned)items), dim3(64 * kSymWaves), 0, st,
                      reinterpret_cast<const h8*>(pts.B.ptr), reinterpret_cast<const h8*>(pts.A.ptr),
-                     reinterpret_cast<const h8*>(vp), nb, dps, hmax, nc, colmax, fwd, tp, mpad);
+                     reinterpret_cast<const h8*>(vp), nb, splits, dps, hmax, nc, colmax, fwd, tp,
+                     mpad);
   MGP_HIP_CHECK(hipGetLastError());
   if (ws.time_tile) {
     MGP_HIP_CHECK(hipEventRecord(ws.ev1, st));
