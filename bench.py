@@ -46,9 +46,10 @@ C_K = 9                        # Matern-5/2 epilogue flops per pair
 N_TR = 2                       # sqrt + exp per pair
 FLOPS_PER_PAIR = 2 * D + 2 * T + C_K
 # HBM bytes per launch of the tile kernel at this workload (rocprofv3 FETCH_SIZE
-# x 2.000 + WRITE_SIZE x 1.000, copy-kernel calibration; profiles/
-# fused_tile_c3_matvec.md).
-TILE_TRAFFIC_BYTES = 1.995e9
+# x 2.000 + WRITE_SIZE x 1.000, copy-kernel calibration): the symmetric kernel
+# (profiles/symmetric_tile_c3_matvec.md: 4.315 GB read, 3.990 GB of partial
+# sums written) and the one-sided kernel (profiles/fused_tile_c3_matvec.md).
+TILE_TRAFFIC_BYTES = {"symmetric": 8.305e9, "one_sided": 1.995e9}
 
 # Instruction mix of the tile kernel k_fused_tile<Matern52, KB, NCG=1, R=4> per
 # 16x16 tile (gfx950 ISA of this build): 4 pair values per lane, each with 2
@@ -621,7 +622,7 @@ def main(argv=None) -> int:
             "peak": round(peak, 3),
             "unit": "TFLOP/s",
             "frac": round(t_model_ms / tile_ms, 4),
-            "traffic": TILE_TRAFFIC_BYTES,
+            "traffic": TILE_TRAFFIC_BYTES["symmetric" if sym_tiles else "one_sided"],
             "peak_kind": "pipe model: VALU + 16-bit MFMA cycles per 16x16 tile formed "
                          "(symmetric tiles carry 1.5 more MFMAs) from per-instruction costs "
                          "measured live (mgp_pipe_probe)",
