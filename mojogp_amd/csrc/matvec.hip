@@ -732,8 +732,7 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     int64_t mpad) {
   constexpr int R = kSymR, W = kSymWaves;
   static_assert(R == 4, "the pipeline below is written for two row-tile pairs");
-  static_assert(64 * W >= 256 * kSymSteps, "a stage's transposed sums are reduced by "
-                                           "256 threads per column-tile pair");
+  static_assert(W % 2 == 0, "the stage reduction strides by a multiple of 128 threads");
   constexpr bool UNIT_G = KIND != KIND_MATERN52 && KIND != KIND_MATERN32;
   constexpr int kA = 2 * KB;
   constexpr int kBlocks = kSymSteps * (kA + 2);
@@ -952,15 +951,16 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     }
   };
   // Adds the waves' transposed sums of stage c (buffer c & 1) in wave order
-  // and writes them, unscaled, to tp.  Thread u < kSymSteps * 256 owns two
+  // and writes them, unscaled, to tp.  Unit u < kSymSteps * 256 is two
   // right-hand sides (2h, 2h + 1 of the lane's four) of one lane of one
-  // column tile; its column scales are fixed for the kernel.
+  // column tile; a thread's units share the lane half, so its column scales
+  // are fixed for the kernel.
   constexpr int kRedUnits = kSymSteps * 256;
   const int ru = threadIdx.x;
-  const int r_kk = ru >> 8, r_t = (ru >> 7) & 1, r_ln = (ru >> 1) & 63, r_h = ru & 1;
+  const int r_ln = (ru >> 1) & 63, r_h = ru & 1;
   const int r_c = 4 * (r_ln >> 4) + 2 * r_h;
   f2 r_scale = {0.f, 0.f};
-  if (ru < kRedUnits) {
+  {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int cc = r_c + e;
@@ -969,16 +969,22 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     }
   }
   auto reduce_stage = [&](int64_t c) __attribute__((always_inline)) {
-    if (ru >= kRedUnits) return;
     const int slot = (int)(c & 1);
-    const float* src = reinterpret_cast<const float*>(&tbuf[slot][r_kk][0][r_t][r_ln]) + 2 * r_h;
-    constexpr int wstride = (int)(sizeof(tbuf[0][0][0]) / sizeof(float));
-    f2 sum = *reinterpret_cast<const f2*>(src);
-#pragma unroll
-    for (int w = 1; w < W; ++w) sum += *reinterpret_cast<const f2*>(src + w * wstride);
-    const int64_t jl = 32 * ((c % kSymStages) * kSymSteps + r_kk) + 16 * r_t + (r_ln & 15);
     const int64_t blk = b * hmax + stage_delta(c) - 1;
-    *reinterpret_cast<f2*>(tp + (blk * kSymRows + jl) * 16 + r_c) = sum * r_scale;
+    constexpr int wstride = (int)(sizeof(tbuf[0][0][0]) / sizeof(float));
+    // Units ru, ru + 64 W, ...: the same lane half (64 W is a multiple of 128).
+#pragma unroll
+    for (int uu = 0; uu < kRedUnits; uu += 64 * W) {
+      const int u = uu + ru;
+      if (u >= kRedUnits) break;
+      const int kk = u >> 8, t = (u >> 7) & 1;
+      const float* src = reinterpret_cast<const float*>(&tbuf[slot][kk][0][t][r_ln]) + 2 * r_h;
+      f2 sum = *reinterpret_cast<const f2*>(src);
+#pragma unroll
+      for (int w = 1; w < W; ++w) sum += *reinterpret_cast<const f2*>(src + w * wstride);
+      const int64_t jl = 32 * ((c % kSymStages) * kSymSteps + kk) + 16 * t + (r_ln & 15);
+      *reinterpret_cast<f2*>(tp + (blk * kSymRows + jl) * 16 + r_c) = sum * r_scale;
+    }
   };
 
   const int64_t dlo = tile0 / 2, dhi = dlo + R / 2;
