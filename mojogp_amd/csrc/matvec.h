@@ -1,6 +1,8 @@
 // Fused kernel-matrix products on gfx950: declarations shared by the C ABI.
 #pragma once
 
+#include <vector>
+
 #include "mgp_common.h"
 
 namespace mgp {
@@ -170,5 +172,34 @@ void gradient_matvec(int kind, bool ard, const PackedPoints& pts, int d, float o
 
 // Maximum input dimension served by the MFMA tile path (three K=32 MFMAs).
 constexpr int kMaxMfmaDim = 30;
+
+// Work buffers of the matrix-core gradient trace (grown on demand, kept by
+// the provider).
+struct GradTraceWorkspace {
+  DevBuf<float> wa, wb;          // packed [Rf'|Lf'] / [Lf';Rf'] operands (fp16 pairs)
+  DevBuf<float> zz;              // packed [z | z^2] column operands (fp16 pairs)
+  DevBuf<uint32_t> colmax, colmax_part;  // |Lf|, |Rf| column maxima (32) and row-chunk parts
+  DevBuf<int> shifts;            // per-column exponents of Lf', Rf' and the common scale T
+  DevBuf<double> part;           // workgroup partials
+  std::vector<double> hpart;
+};
+
+// Gradient traces on the matrix cores, for the Gram-form kernels (RBF,
+// Matern-3/2, Matern-5/2; not Matern-1/2) in up to 16 dimensions over a packed
+// point set whose norms keep the Gram form accurate:
+//   acc[q] += sum_ab W_ab h_ab (z_aq - z_bq)^2   (q < d),
+//   acc[d] += sum_ab W_ab k_ab / os,
+// with W = Lf^T Rf over ncols columns ([ncols][n] device arrays), z the
+// scaled coordinates and h the kernel's lengthscale factor (RBF k/os,
+// Matern-3/2 3 e^{-u}, Matern-5/2 (5/3)(1 + u) e^{-u}), the same sums as the
+// pair-loop trace.  Only the symmetric part of W meets the symmetric h dz^2,
+// so each unordered block pair is formed once with (W + W^T).  The
+// environment variable MGP_GRAD_MFMA=0 keeps the pair-loop trace, =1 takes
+// this one for any n the route allows.
+bool grad_trace_mfma_route(int kind, const PackedPoints& pts, int d);
+void grad_trace_mfma(int kind, const PackedPoints& pts, int d, const float* Lf,
+                     const float* Rf, int ncols, double* acc, GradTraceWorkspace& ws,
+                     hipStream_t st);
+constexpr int64_t kGradMfmaMinPoints = 4096;
 
 }  // namespace mgp

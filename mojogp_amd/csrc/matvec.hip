@@ -1038,6 +1038,400 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Gradient traces on the matrix cores (Gram-form kernels).
+//
+// The pair-loop trace (solver.hip k_grad_trace) spends ~90 VALU instructions
+// per pair on per-dimension differences, the 16-column dot g_ab = sum_c
+// Lf_ca Rf_cb and the per-dimension accumulation.  Here, per 16x16 tile:
+//   * the scaled squared distance comes from the Gram-form distance MFMAs of
+//     the product kernels (KB per tile);
+//   * D = W + W^T comes from one K=32 contraction of [Rf'_b | Lf'_b] with
+//     [Lf'_a ; Rf'_a] (3 MFMAs for the two-term fp16 split).  Lf and Rf are
+//     scaled per column by powers of two (Lf' = 2^sL_c Lf_c with max |Lf'_c|
+//     in [2^13, 2^14), Rf' = 2^(T - sL_c) Rf_c) so every product carries the
+//     common factor 2^T and the largest column products sit at 2^28;
+//   * M = D h (the kernel's lengthscale factor, scaled by 2^-kGtMExp into
+//     fp16 range) is contracted with [z_b | z_b^2] on the matrix cores (3 per
+//     tile per 16 dimensions), and its row sums R_a on VALU;
+//   * every kGtFold column-tile pairs the point's terms
+//       sum_b M_ab (z_aq - z_bq)^2 = z_aq^2 R_a - 2 z_aq (M z)_aq + (M z^2)_aq
+//     are formed in fp64 (the expansion cancels; each fp32 input carries 24
+//     bits over at most 256 columns) and accumulated.
+// Since h (z_aq - z_bq)^2 and k are symmetric, only the symmetric part of W
+// contributes: row block b forms its diagonal block with weight 1/2 on D and
+// the off-diagonal blocks of the cyclic half (sym_span) with weight 1, so
+// every ordered pair is counted once.  The os term sum_ab W_ab k_ab/os is
+// accumulated from D k on VALU alongside.
+// ---------------------------------------------------------------------------
+constexpr int kGtR = 2;                              // row tiles per wave
+constexpr int kGtWaves = 8;                          // waves per workgroup
+constexpr int kGtRows = 16 * kGtR * kGtWaves;        // rows (and columns) per block
+constexpr int kGtPairs = kGtRows / 32;               // column-tile pairs per block
+constexpr int kGtSteps = 2;                          // column-tile pairs per LDS stage
+constexpr int kGtStages = kGtPairs / kGtSteps;       // LDS stages per block
+constexpr int kGtFold = 8;                           // column-tile pairs between fp64 folds
+constexpr int kGtMExp = 20;                          // M = D h 2^-kGtMExp before its split
+static_assert((16 * kPackTileAlign) % kGtRows == 0, "blocks must tile the packed points");
+
+// Column exponents of a 16-column chunk: colmax[0..15] = max |Lf_c|,
+// colmax[16..31] = max |Rf_c| (float bits).  shifts[c] = sL_c,
+// shifts[16 + c] = T - sL_c, shifts[32] = T.  One thread.
+__global__ void k_grad_shifts(const uint32_t* __restrict__ colmax, int nc,
+                              int* __restrict__ shifts) {
+  if (threadIdx.x != 0) return;
+  int eL[16], eR[16];
+  bool live[16];
+  int smax = -100000;
+  for (int c = 0; c < 16; ++c) {
+    const float ml = c < nc ? __uint_as_float(colmax[c]) : 0.0f;
+    const float mr = c < nc ? __uint_as_float(colmax[16 + c]) : 0.0f;
+    live[c] = ml > 0.0f && mr > 0.0f && ml < 3.0e38f && mr < 3.0e38f;
+    (void)frexpf(live[c] ? ml : 1.0f, &eL[c]);
+    (void)frexpf(live[c] ? mr : 1.0f, &eR[c]);
+    if (live[c]) smax = max(smax, eL[c] + eR[c]);
+  }
+  const int T = smax == -100000 ? 0 : 28 - smax;
+  for (int c = 0; c < 16; ++c) {
+    shifts[c] = live[c] ? 14 - eL[c] : 0;
+    shifts[16 + c] = live[c] ? T - (14 - eL[c]) : 0;
+  }
+  shifts[32] = T;
+}
+
+// One thread per (tile, lane) of ntiles tiles: WA (column side, A operand,
+// row m = point, K = [Rf' c0..15 | Lf' c0..15]) and WB (row side, B operand,
+// column n = point, K = [Lf' | Rf']), lane l holding K = 8 (l/16) .. + 7 of
+// point 16 tile + l%16; parts hi, lo at [(tile*2 + part)*64 + lane].
+__global__ void k_pack_grad_w(const float* __restrict__ Lf, const float* __restrict__ Rf,
+                              int64_t n, int nc, int64_t ntiles, const int* __restrict__ shifts,
+                              h8* __restrict__ WA, h8* __restrict__ WB) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= ntiles * 64) return;
+  const int lane = (int)(idx & 63);
+  const int64_t tile = idx >> 6;
+  const int64_t p = 16 * tile + (lane & 15);
+  const int k0 = 8 * (lane >> 4);
+  h8 ah, al, bh, bl;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int k = k0 + e;
+    const int c = k & 15;
+    const bool live = p < n && c < nc;
+    const float lf = live ? ldexpf(Lf[(int64_t)c * n + p], shifts[c]) : 0.0f;
+    const float rf = live ? ldexpf(Rf[(int64_t)c * n + p], shifts[16 + c]) : 0.0f;
+    const float va = k < 16 ? rf : lf;  // column side [Rf' | Lf']
+    const float vb = k < 16 ? lf : rf;  // row side [Lf' ; Rf']
+    ah[e] = (_Float16)va;
+    al[e] = (_Float16)(va - (float)ah[e]);
+    bh[e] = (_Float16)vb;
+    bl[e] = (_Float16)(vb - (float)bh[e]);
+  }
+  WA[(tile * 2) * 64 + lane] = ah;
+  WA[(tile * 2 + 1) * 64 + lane] = al;
+  WB[(tile * 2) * 64 + lane] = bh;
+  WB[(tile * 2 + 1) * 64 + lane] = bl;
+}
+
+// One thread per (pair u, group gr < 2 QG, lane): the A operand of U = [z|z^2] M
+// (row m = dimension q = 16 (gr % QG) + lane%16, squares for gr >= QG; K = the
+// pair's 32 columns in the packed right-hand-side order: element e holds point
+// 16 (2u + e/4) + 4 (lane/16) + e%4); parts hi, lo at
+// [((u*2QG + gr)*2 + part)*64 + lane].
+__global__ void k_pack_grad_zz(const float* __restrict__ Z, int64_t n, int d, int qg,
+                               int64_t pairs, h8* __restrict__ ZZ) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= pairs * 2 * qg * 64) return;
+  const int lane = (int)(idx & 63);
+  const int gr = (int)((idx >> 6) % (2 * qg));
+  const int64_t u = (idx >> 6) / (2 * qg);
+  const int q = 16 * (gr % qg) + (lane & 15);
+  const bool sq = gr >= qg;
+  h8 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t b = 32 * u + 16 * (e >> 2) + 4 * (lane >> 4) + (e & 3);
+    float v = (b < n && q < d) ? Z[b * d + q] : 0.0f;
+    if (sq) v = v * v;
+    hi[e] = (_Float16)v;
+    lo[e] = (_Float16)(v - (float)hi[e]);
+  }
+  ZZ[((u * 2 * qg + gr) * 2) * 64 + lane] = hi;
+  ZZ[((u * 2 * qg + gr) * 2 + 1) * 64 + lane] = lo;
+}
+
+// kv = k/os and h (the derivative factor of the pair-loop trace) from the
+// scaled squared distance s.
+template <int KIND>
+__device__ __forceinline__ void grad_factors(float s, float clampv, float& kv, float& h) {
+  if constexpr (KIND == KIND_RBF) {
+    kv = __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(s, 0.0f, clampv));
+    h = kv;
+  } else if constexpr (KIND == KIND_MATERN32) {
+    const float u = __builtin_amdgcn_sqrtf(fabsf(s));
+    float mn = fminf(u, clampv);
+    asm("" : "+v"(mn));
+    const float e = __builtin_amdgcn_exp2f(-mn);
+    kv = fmaf(u, kLn2, 1.0f) * e;
+    h = 3.0f * e;
+  } else {
+    const float u = __builtin_amdgcn_sqrtf(fabsf(s));
+    float mn = fminf(u, clampv);
+    asm("" : "+v"(mn));
+    const float e = __builtin_amdgcn_exp2f(-mn);
+    kv = fmaf(u, fmaf(u, kLn2 * kLn2 / 3.0f, kLn2), 1.0f) * e;
+    h = fmaf(u, (5.0f / 3.0f) * kLn2, 5.0f / 3.0f) * e;
+  }
+}
+
+// part[L][q] (q < 16 QG: sum_ab M (z_aq - z_bq)^2 at scale 2^(T - kGtMExp)),
+// part[L][16 QG] (sum_ab D k/os at scale 2^T) for work item L = (row block b,
+// delta split).
+template <int KIND, int KB, int QG>
+__global__ __launch_bounds__(64 * kGtWaves) void k_grad_sym(
+    const h8* __restrict__ Bi, const h8* __restrict__ Aj, const h8* __restrict__ WA,
+    const h8* __restrict__ WB, const h8* __restrict__ ZZ, const float* __restrict__ Z, int d,
+    int64_t n, int64_t nb, int64_t splits, int64_t dps, double* __restrict__ part) {
+  constexpr int R = kGtR, W = kGtWaves;
+  constexpr int kA = 2 * KB;   // distance operand blocks per pair
+  constexpr int kW = 4;        // W operand blocks per pair (2 tiles x hi, lo)
+  constexpr int kZ = 4 * QG;   // [z|z^2] blocks per pair (2 QG groups x hi, lo)
+  constexpr int kBlocks = kGtSteps * (kA + kW + kZ);
+  constexpr int NQ = 16 * QG;
+  __shared__ h8 lds[2][kBlocks][64];
+  __shared__ double red[W][NQ + 1];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t per = (int64_t)gridDim.x / kXcds;
+  const int64_t L = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (L >= nb * splits) return;  // whole workgroup, before any barrier
+  const int64_t b = L % nb;
+  const int64_t split = L / nb;
+  const int64_t tile0 = (b * W + wave) * R;
+  const int li = lane & 15, lg = lane >> 4, lj = 4 * lg;
+
+  h8 bi[R][KB], wb[R][2];
+  float zr[R][QG][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) bi[r][kb] = Bi[((tile0 + r) * KB + kb) * 64 + lane];
+    wb[r][0] = WB[((tile0 + r) * 2) * 64 + lane];
+    wb[r][1] = WB[((tile0 + r) * 2 + 1) * 64 + lane];
+    const int64_t a = 16 * (tile0 + r) + li;
+#pragma unroll
+    for (int g = 0; g < QG; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int q = 16 * g + lj + e;
+        zr[r][g][e] = (a < n && q < d) ? Z[a * d + q] : 0.0f;
+      }
+  }
+  f4 U[R][2 * QG];
+  float rs[R];
+  double T[QG][4];
+  float osf = 0.0f;
+  double osd = 0.0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rs[r] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 2 * QG; ++g) U[r][g] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int g = 0; g < QG; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) T[g][e] = 0.0;
+  const float clampv = clamp_reg();
+
+  const int64_t span = sym_span(b, nb);
+  const int64_t d0 = split * dps;
+  const int64_t d1 = min(d0 + dps, span + 1);
+  const int64_t nst = d1 > d0 ? (d1 - d0) * kGtStages : 0;
+  auto stage_delta = [&](int64_t c) { return d0 + c / kGtStages; };
+  auto stage_u0 = [&](int64_t c) {
+    int64_t J = b + stage_delta(c);
+    if (J >= nb) J -= nb;
+    return J * kGtPairs + (c % kGtStages) * kGtSteps;
+  };
+
+  // Stage operands through registers (see k_sym_tile): blocks [distance |
+  // W | z], each range contiguous in global memory.
+  constexpr int kFillPerWave = (kBlocks + W - 1) / W;
+  h8 pre[kFillPerWave];
+  auto fetch = [&](int64_t u0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < kFillPerWave; ++q) {
+      const int bb = min(wave + q * W, kBlocks - 1);
+      const h8* src = bb < kGtSteps * kA ? Aj + (2 * u0 * KB + bb) * 64
+                      : bb < kGtSteps * (kA + kW)
+                          ? WA + (4 * u0 + (bb - kGtSteps * kA)) * 64
+                          : ZZ + (u0 * kZ + (bb - kGtSteps * (kA + kW))) * 64;
+      pre[q] = src[lane];
+    }
+  };
+  auto commit = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < kFillPerWave; ++q) {
+      const int bb = wave + q * W;
+      if (bb < kBlocks) lds[st][bb][lane] = pre[q];
+    }
+  };
+
+  // One column-tile pair against the wave's R row tiles.  DIAG: a tile of the
+  // diagonal block (weight 1/2 on D); MASK: restore the exact zero
+  // self-distance on diagonal tiles.
+  auto step = [&](int st, int k, int64_t u, auto mask_tag, auto diag_tag)
+                  __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    constexpr float wd = DIAG ? 0.5f : 1.0f;
+    constexpr float mscale = wd * (1.0f / (float)(1 << kGtMExp));
+    const int64_t jt0 = 2 * u;
+    h8 a0[KB], a1[KB], wa[2][2], zz[2 * QG][2];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      a0[kb] = lds[st][k * kA + kb][lane];
+      a1[kb] = lds[st][k * kA + KB + kb][lane];
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) wa[t][p] = lds[st][kGtSteps * kA + k * kW + 2 * t + p][lane];
+#pragma unroll
+    for (int g = 0; g < 2 * QG; ++g)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        zz[g][p] = lds[st][kGtSteps * (kA + kW) + k * kZ + 2 * g + p][lane];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      f4 s0 = f4{0.f, 0.f, 0.f, 0.f}, s1 = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[kb], bi[r][kb], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1[kb], bi[r][kb], s1, 0, 0, 0);
+      }
+      f4 D0 = f4{0.f, 0.f, 0.f, 0.f}, D1 = f4{0.f, 0.f, 0.f, 0.f};
+      D0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[0][0], wb[r][0], D0, 0, 0, 0);
+      D1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[1][0], wb[r][0], D1, 0, 0, 0);
+      D0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[0][1], wb[r][0], D0, 0, 0, 0);
+      D1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[1][1], wb[r][0], D1, 0, 0, 0);
+      D0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[0][0], wb[r][1], D0, 0, 0, 0);
+      D1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[1][0], wb[r][1], D1, 0, 0, 0);
+      if constexpr (MASK) {
+        const int64_t dt = tile0 + r;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (jt0 == dt && li == lj + q) s0[q] = 0.0f;
+          if (jt0 + 1 == dt && li == lj + q) s1[q] = 0.0f;
+        }
+      }
+      float m0[4], m1[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float kv, h;
+        grad_factors<KIND>(s0[q], clampv, kv, h);
+        m0[q] = D0[q] * (h * mscale);
+        osf = fmaf(D0[q] * wd, kv, osf);
+        grad_factors<KIND>(s1[q], clampv, kv, h);
+        m1[q] = D1[q] * (h * mscale);
+        osf = fmaf(D1[q] * wd, kv, osf);
+        rs[r] += m0[q] + m1[q];
+      }
+      h2 hA, hB, hC, hD, lA, lB, lC, lD;
+      split_pair<true>(m0[0], 1.0f, m0[1], 1.0f, hA, lA);
+      split_pair<true>(m0[2], 1.0f, m0[3], 1.0f, hB, lB);
+      split_pair<true>(m1[0], 1.0f, m1[1], 1.0f, hC, lC);
+      split_pair<true>(m1[2], 1.0f, m1[3], 1.0f, hD, lD);
+      const h8 mh = h8{hA[0], hA[1], hB[0], hB[1], hC[0], hC[1], hD[0], hD[1]};
+      const h8 ml = h8{lA[0], lA[1], lB[0], lB[1], lC[0], lC[1], lD[0], lD[1]};
+#pragma unroll
+      for (int g = 0; g < 2 * QG; ++g) {
+        f4 a = U[r][g];
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(zz[g][0], mh, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(zz[g][1], mh, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(zz[g][0], ml, a, 0, 0, 0);
+        U[r][g] = a;
+      }
+    }
+  };
+  // Per point: z^2 R - 2 z (M z) + (M z^2) in fp64, accumulated per lane.
+  auto fold = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float rsum = rs[r];
+      rsum += __shfl_xor(rsum, 16);
+      rsum += __shfl_xor(rsum, 32);
+      const double Rd = (double)rsum;
+#pragma unroll
+      for (int g = 0; g < QG; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const double z = (double)zr[r][g][e];
+          T[g][e] += z * z * Rd - 2.0 * z * (double)U[r][g][e] + (double)U[r][QG + g][e];
+        }
+      rs[r] = 0.0f;
+#pragma unroll
+      for (int g = 0; g < 2 * QG; ++g) U[r][g] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    osd += (double)osf;
+    osf = 0.0f;
+  };
+
+  const int64_t dlo = tile0 / 2, dhi = dlo + R / 2;
+  if (nst > 0) {
+    fetch(stage_u0(0));
+    commit(0);
+  }
+  int since_fold = 0;
+  for (int64_t c = 0; c < nst; ++c) {
+    const int st = (int)(c & 1);
+    __syncthreads();
+    if (c + 1 < nst) fetch(stage_u0(c + 1));
+    const int64_t u0 = stage_u0(c);
+    if (stage_delta(c) == 0) {
+      for (int k = 0; k < kGtSteps; ++k) {
+        const int64_t u = u0 + k;
+        if (u >= dlo && u < dhi)
+          step(st, k, u, std::true_type{}, std::true_type{});
+        else
+          step(st, k, u, std::false_type{}, std::true_type{});
+      }
+    } else {
+      for (int k = 0; k < kGtSteps; ++k) step(st, k, u0 + k, std::false_type{}, std::false_type{});
+    }
+    since_fold += kGtSteps;
+    if (since_fold >= kGtFold) {
+      fold();
+      since_fold = 0;
+    }
+    if (c + 1 < nst) commit(st ^ 1);
+  }
+  fold();
+
+  // Sum over the 16 rows of each lane group, then over the waves in order.
+#pragma unroll
+  for (int g = 0; g < QG; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      double v = T[g][e];
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off);
+      if (li == 0) red[wave][16 * g + lj + e] = v;
+    }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) osd += __shfl_xor(osd, off);
+  if (lane == 0) red[wave][NQ] = osd;
+  __syncthreads();
+  if (threadIdx.x <= NQ) {
+    double tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) tot += red[w][threadIdx.x];
+    part[L * (NQ + 1) + threadIdx.x] = tot;
+  }
+}
+
 // out[c*m + j] = os * (sum_s fwd[s][c][j] + sum of the transposed partials of
 // the row blocks that formed j's column block, in delta order) + noise V.
 // One thread per point, all right-hand sides (fp64 sums).
@@ -1466,6 +1860,115 @@ void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, i
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Matrix-core gradient trace: host side.
+// ---------------------------------------------------------------------------
+bool grad_trace_mfma_route(int kind, const PackedPoints& pts, int d) {
+  const char* env = std::getenv("MGP_GRAD_MFMA");
+  const int mode = env == nullptr ? -1 : (env[0] == '0' ? 0 : 1);
+  if (mode == 0) return false;
+  // d <= 16: one 16-dimension group of [z | z^2] (two groups spill registers).
+  if (kind == KIND_MATERN12 || d < 1 || d > 16 || pts.kb < 1 || pts.kb > 3) return false;
+  if (!gram_form_ok(kind, pts, pts)) return false;
+  const int64_t nb = ceil_div(std::max<int64_t>(pts.n, 1), kGtRows);
+  if (nb * kGtRows > pts.ntiles_alloc * 16) return false;
+  return mode > 0 || pts.n >= kGradMfmaMinPoints;
+}
+
+namespace {
+
+using GradFn = void (*)(const h8*, const h8*, const h8*, const h8*, const h8*, const float*, int,
+                        int64_t, int64_t, int64_t, int64_t, double*);
+
+template <int KIND, int QG>
+GradFn pick_grad_kb(int kb) {
+  switch (kb) {
+    case 1: return k_grad_sym<KIND, 1, QG>;
+    case 2: return k_grad_sym<KIND, 2, QG>;
+    case 3: return k_grad_sym<KIND, 3, QG>;
+  }
+  return nullptr;
+}
+
+template <int KIND>
+GradFn pick_grad(int kb, int qg) {
+  return qg == 1 ? pick_grad_kb<KIND, 1>(kb) : nullptr;
+}
+
+}  // namespace
+
+void grad_trace_mfma(int kind, const PackedPoints& pts, int d, const float* Lf,
+                     const float* Rf, int ncols, double* acc, GradTraceWorkspace& ws,
+                     hipStream_t st) {
+  MGP_REQUIRE(grad_trace_mfma_route(kind, pts, d),
+              "matrix-core gradient trace does not serve this point set");
+  const int64_t n = pts.n;
+  const int64_t nb = ceil_div(std::max<int64_t>(n, 1), kGtRows);
+  const int64_t ntiles = nb * 16;
+  const int64_t pairs = nb * kGtPairs;
+  const int qg = d <= 16 ? 1 : 2;
+  const int nq = 16 * qg;
+  const int64_t hmax = nb / 2;
+  int64_t splits = std::min<int64_t>(std::max<int64_t>(ceil_div(2048, nb), 1), hmax + 1);
+  const int64_t dps = ceil_div(hmax + 1, splits);
+  splits = ceil_div(hmax + 1, dps);
+  const int64_t items = round_up(nb * splits, kXcds);
+
+  h8* ZZ = reinterpret_cast<h8*>(ws.zz.ensure((size_t)pairs * 2 * qg * 2 * 64 * 4));
+  h8* WA = reinterpret_cast<h8*>(ws.wa.ensure((size_t)ntiles * 2 * 64 * 4));
+  h8* WB = reinterpret_cast<h8*>(ws.wb.ensure((size_t)ntiles * 2 * 64 * 4));
+  uint32_t* colmax = ws.colmax.ensure(32);
+  const int chunks = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(n, 1), 4096), 64);
+  uint32_t* cpart = ws.colmax_part.ensure((size_t)64 * chunks);
+  int* shifts = ws.shifts.ensure(33);
+  double* part = ws.part.ensure((size_t)nb * splits * (nq + 1));
+  ws.hpart.resize((size_t)nb * splits * (nq + 1));
+
+  const int64_t zthreads = pairs * 2 * qg * 64;
+  hipLaunchKernelGGL(k_pack_grad_zz, dim3((unsigned)ceil_div(zthreads, 256)), dim3(256), 0, st,
+                     pts.z.ptr, n, d, qg, pairs, ZZ);
+  MGP_HIP_CHECK(hipGetLastError());
+  GradFn fn = kind == KIND_RBF        ? pick_grad<KIND_RBF>(pts.kb, qg)
+              : kind == KIND_MATERN32 ? pick_grad<KIND_MATERN32>(pts.kb, qg)
+                                      : pick_grad<KIND_MATERN52>(pts.kb, qg);
+  MGP_REQUIRE(fn != nullptr, "no gradient trace kernel for this shape");
+
+  for (int c0 = 0; c0 < ncols; c0 += 16) {
+    const int nc = std::min(16, ncols - c0);
+    const float* L = Lf + (int64_t)c0 * n;
+    const float* Rr = Rf + (int64_t)c0 * n;
+    const int vecL = (n % 4 == 0 && reinterpret_cast<uintptr_t>(L) % 16 == 0) ? 1 : 0;
+    const int vecR = (n % 4 == 0 && reinterpret_cast<uintptr_t>(Rr) % 16 == 0) ? 1 : 0;
+    hipLaunchKernelGGL(k_col_absmax_part, dim3((unsigned)chunks, (unsigned)nc), dim3(256), 0, st,
+                       L, n, vecL, cpart);
+    hipLaunchKernelGGL(k_col_absmax_final, dim3((unsigned)nc), dim3(64), 0, st, cpart, chunks,
+                       colmax);
+    hipLaunchKernelGGL(k_col_absmax_part, dim3((unsigned)chunks, (unsigned)nc), dim3(256), 0, st,
+                       Rr, n, vecR, cpart);
+    hipLaunchKernelGGL(k_col_absmax_final, dim3((unsigned)nc), dim3(64), 0, st, cpart, chunks,
+                       colmax + 16);
+    hipLaunchKernelGGL(k_grad_shifts, dim3(1), dim3(64), 0, st, colmax, nc, shifts);
+    hipLaunchKernelGGL(k_pack_grad_w, dim3((unsigned)ceil_div(ntiles * 64, 256)), dim3(256), 0,
+                       st, L, Rr, n, nc, ntiles, shifts, WA, WB);
+    MGP_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(fn, dim3((unsigned)items), dim3(64 * kGtWaves), 0, st,
+                       reinterpret_cast<const h8*>(pts.B.ptr), reinterpret_cast<const h8*>(pts.A.ptr),
+                       WA, WB, ZZ, pts.z.ptr, d, n, nb, splits, dps, part);
+    MGP_HIP_CHECK(hipGetLastError());
+    int T = 0;
+    MGP_HIP_CHECK(hipMemcpyAsync(&T, shifts + 32, sizeof(int), hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipMemcpyAsync(ws.hpart.data(), part, ws.hpart.size() * sizeof(double),
+                                 hipMemcpyDeviceToHost, st));
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    std::vector<double> sum(nq + 1, 0.0);
+    for (int64_t it = 0; it < nb * splits; ++it)
+      for (int q = 0; q <= nq; ++q) sum[q] += ws.hpart[(size_t)it * (nq + 1) + q];
+    const double sm = std::ldexp(1.0, kGtMExp - T), so = std::ldexp(1.0, -T);
+    for (int q = 0; q < d; ++q) acc[q] += sum[q] * sm;
+    acc[d] += sum[nq] * so;
+  }
+}
 
 void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,

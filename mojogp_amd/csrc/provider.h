@@ -48,6 +48,8 @@ struct Provider {
   // block partials of the tree gradient / table traces (scratch, so usable
   // through a const provider)
   mutable DevBuf<double> tree_gws;
+  // work buffers of the matrix-core gradient trace (scratch, as above)
+  mutable GradTraceWorkspace gtws;
 
   hipStream_t st = nullptr;
   int device = 0;              // HIP device current when the provider was created

@@ -1737,6 +1737,20 @@ void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int n
   }
   const int d = pv.d;
   MGP_REQUIRE(d <= 32, "gradient kernel supports d <= 32");
+  const double s = (double)kernel_scale(pv.kind);
+  const double os = (double)pv.outputscale();
+  const int nls = pv.ard ? d : 1;
+  if (grad_trace_mfma_route(pv.kind, pv.train, d)) {
+    // Matrix-core trace: per-dimension sums, then the pair-loop's layout.
+    std::vector<double> acc(d + 1, 0.0);
+    grad_trace_mfma(pv.kind, pv.train, d, Lf, Rf, ncols, acc.data(), pv.gtws, st);
+    double iso = 0.0;
+    for (int q = 0; q < d; ++q) iso += acc[q];
+    for (int q = 0; q < nls; ++q)
+      g_host[q] = os * (pv.ard ? acc[q] : iso) / (s * s * (double)pv.lengthscale(q));
+    g_host[nls] = acc[d];
+    return;
+  }
   const int dm = d <= 1 ? 1 : d <= 2 ? 2 : d <= 4 ? 4 : d <= 8 ? 8 : d <= 16 ? 16 : 32;
   const int nterms = pv.ard ? d + 1 : 2;
   const int64_t nblk = ceil_div(pv.n, 256) * grad_splits(pv.n);
@@ -1766,9 +1780,6 @@ void gradient_traces(const Provider& pv, const float* Lf, const float* Rf, int n
   }
   // Convert pair sums (scaled coordinates z = (x - c) * kernel_scale / ls) to
   // parameter derivatives: dk/dl_d = os h (dx_d)^2 / l_d^3 = os h dz_d^2 / (s^2 l_d).
-  const double s = (double)kernel_scale(pv.kind);
-  const double os = (double)pv.outputscale();
-  const int nls = pv.ard ? d : 1;
   for (int q = 0; q < nls; ++q)
     g_host[q] = os * acc[q] / (s * s * (double)pv.lengthscale(q));
   g_host[nls] = acc[nterms - 1];
