@@ -1434,40 +1434,58 @@ __global__ __launch_bounds__(64 * kGtWaves) void k_grad_sym(
 
 // out[c*m + j] = os * (sum_s fwd[s][c][j] + sum of the transposed partials of
 // the row blocks that formed j's column block, in delta order) + noise V.
-// One thread per point, all right-hand sides (fp64 sums).
+// Four threads per point, each owning four right-hand sides (16 contiguous
+// bytes of every partial row); fp64 sums in a fixed order.  The delta loop
+// loads four partials at a time unconditionally (every (block, delta) slot
+// is allocated) and keeps the formed ones by a select.
 __global__ __launch_bounds__(256) void k_sym_reduce(const float* __restrict__ fwd, int splits,
                                                     const float* __restrict__ tp, int64_t nb,
                                                     int64_t hmax, int64_t mpad, int64_t m,
                                                     int ncols, float os, float noise,
                                                     const float* __restrict__ Vin,
                                                     float* __restrict__ out) {
-  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t j = t >> 2;
+  const int c4 = (int)(t & 3);
   if (j >= m) return;
-  double tot[16];
-#pragma unroll
-  for (int c = 0; c < 16; ++c) tot[c] = 0.0;
+  double tot[4] = {0.0, 0.0, 0.0, 0.0};
   for (int s = 0; s < splits; ++s)
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-      if (c < ncols) tot[c] += fwd[((int64_t)s * 16 + c) * mpad + j];
+    for (int e = 0; e < 4; ++e) {
+      const int c = 4 * c4 + e;
+      if (c < ncols) tot[e] += fwd[((int64_t)s * 16 + c) * mpad + j];
+    }
   const int64_t J = j / kSymRows, jl = j - J * kSymRows;
-  for (int64_t dl = 1; dl <= hmax; ++dl) {
+  const float* col = tp + jl * 16 + 4 * c4;
+  auto slot = [&](int64_t dl, bool& formed) {
     int64_t bb = J - dl;
     if (bb < 0) bb += nb;
-    if (dl > sym_span(bb, nb)) continue;
-    const f4* p = reinterpret_cast<const f4*>(tp + ((bb * hmax + dl - 1) * kSymRows + jl) * 16);
+    formed = dl <= sym_span(bb, nb);
+    return *reinterpret_cast<const f4*>(col + (bb * hmax + dl - 1) * (int64_t)kSymRows * 16);
+  };
+  int64_t dl = 1;
+  for (; dl + 3 <= hmax; dl += 4) {
+    f4 v[4];
+    bool ok[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f4 v = p[q];
+    for (int q = 0; q < 4; ++q) v[q] = slot(dl + q, ok[q]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) tot[4 * q + e] += v[e];
-    }
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tot[e] += ok[q] ? (double)v[q][e] : 0.0;
+  }
+  for (; dl <= hmax; ++dl) {
+    bool ok;
+    const f4 v = slot(dl, ok);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tot[e] += ok ? (double)v[e] : 0.0;
   }
 #pragma unroll
-  for (int c = 0; c < 16; ++c) {
+  for (int e = 0; e < 4; ++e) {
+    const int c = 4 * c4 + e;
     if (c < ncols) {
       const int64_t idx = (int64_t)c * m + j;
-      out[idx] = fmaf(noise, Vin[idx], os * (float)tot[c]);
+      out[idx] = fmaf(noise, Vin[idx], os * (float)tot[e]);
     }
   }
 }
@@ -1854,7 +1872,7 @@ void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, i
     ws.tile_ms += ms;
     ws.tile_calls += 1;
   }
-  hipLaunchKernelGGL(k_sym_reduce, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st, fwd,
+  hipLaunchKernelGGL(k_sym_reduce, dim3((unsigned)ceil_div(4 * n, 256)), dim3(256), 0, st, fwd,
                      (int)splits, tp, nb, hmax, mpad, n, nc, a.outputscale, a.noise, Vc, outc);
   MGP_HIP_CHECK(hipGetLastError());
 }
