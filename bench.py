@@ -64,7 +64,7 @@ ROW_TILES, COL_TILES = -(-N // 16), 2 * -(-N // 32)
 
 
 # Symmetric route (matvec.hip k_sym_tile / sym_route): square products with
-# 2..16 right-hand sides over >= 48 blocks of 512 points form each
+# 1..16 right-hand sides over >= 48 blocks of 512 points form each
 # off-diagonal 16x16 tile once and use it for both of its entries: the same
 # VALU per tile, KB distance MFMAs plus 1.5 forward and 1.5 transposed product
 # MFMAs.  The diagonal blocks are formed one-sided (both triangles).
@@ -79,7 +79,7 @@ def _sym_blocks(n, ncols=T):
     env = os.environ.get("MGP_SYM_MATVEC")
     if env is not None and env.startswith("0"):
         return None
-    if not 2 <= ncols <= 16:
+    if not 1 <= ncols <= 16:
         return None
     nb = -(-n // SYM_ROWS)
     if env is None and nb < SYM_MIN_BLOCKS:

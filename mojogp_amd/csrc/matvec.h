@@ -131,7 +131,7 @@ struct MatvecWorkspace {
   int64_t tile_calls = 0;
 };
 
-// A square product (rows and cols the same packed points) with 2..16
+// A square product (rows and cols the same packed points) with 1..16
 // right-hand sides runs on the symmetric kernel, which forms each
 // off-diagonal kernel value once for both of its entries, when the points fill
 // at least kSymMinBlocks 256-point blocks and its transposed partial sums

@@ -662,7 +662,7 @@ __global__ void k_reduce_splits4(const float* __restrict__ partial, int splits, 
 }
 
 // ---------------------------------------------------------------------------
-// Symmetric product K(X, X) V (rows and columns the same points, 2..16
+// Symmetric product K(X, X) V (rows and columns the same points, 1..16
 // right-hand sides): every off-diagonal kernel value is formed once and used
 // twice, out[i] += k_ij V[j] and out[j] += k_ij V[i], which halves the
 // transcendental and VALU work that bounds the tile kernel.
@@ -1799,7 +1799,7 @@ namespace {
 bool sym_route(const MatvecArgs& a, const PackedPoints& rows, const PackedPoints& cols, int nc,
                const MatvecWorkspace& ws) {
   if (!a.square || a.mix != nullptr || ws.arena != nullptr || &rows != &cols) return false;
-  if (nc < 2 || nc > 16 || a.m != a.n || a.n != rows.n) return false;
+  if (nc < 1 || nc > 16 || a.m != a.n || a.n != rows.n) return false;
   const char* env = std::getenv("MGP_SYM_MATVEC");
   const int mode = env == nullptr ? -1 : (env[0] == '0' ? 0 : 1);
   if (mode == 0) return false;

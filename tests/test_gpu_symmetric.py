@@ -1,7 +1,7 @@
 """Parity of the symmetric K(X, X) V kernel (each off-diagonal kernel value
 formed once, used for both of its entries) with the float64 oracle.
 
-MGP_SYM_MATVEC=1 routes every square product with 2..16 right-hand sides
+MGP_SYM_MATVEC=1 routes every square product with 1..16 right-hand sides
 through it (any n), =0 keeps the one-sided tile kernel; unset, the symmetric
 route is taken from 48 blocks of 512 points on.  Bar: norm-wise relative error
 <= 1e-5 per right-hand side (the north star's matvec bar)."""
@@ -34,7 +34,7 @@ def _product(kind, ard, X, V, params, noise):
 
 
 # kind, ard, d, n, t: 1 .. 5 blocks of 512 points (odd and even), partial last
-# blocks, every K=32 MFMA count (d = 1, 8, 16, 30), 2 .. 16 right-hand sides.
+# blocks, every K=32 MFMA count (d = 1, 8, 16, 30), 1 .. 16 right-hand sides.
 CASES = [
     (ok.MATERN52, True, 16, 17, 2),
     (ok.RBF, True, 8, 256, 16),
@@ -43,6 +43,7 @@ CASES = [
     (ok.RBF, False, 1, 1000, 16),
     (ok.MATERN52, True, 30, 1290, 5),
     (ok.RBF, True, 6, 2048, 3),
+    (ok.MATERN52, True, 8, 1500, 1),
     (ok.MATERN52, False, 3, 2500, 16),
 ]
 
