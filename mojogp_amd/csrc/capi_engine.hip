@@ -100,6 +100,20 @@ void prepare_state(Provider& pv, const float* y, const mgp_predict_opts_t& o,
                    const float* alpha_in, const float* root_in, PredictState& ps,
                    mgp_predict_info_t* info) {
   auto t0 = Clock::now();
+  if (!alpha_in && o.variance_method == 1 && !root_in) {
+    // Both solves: side by side where the products allow it.
+    MGP_REQUIRE(y != nullptr, "training targets are required to solve for alpha");
+    MGP_REQUIRE(o.lanczos_rank >= 1, "lanczos_rank must be >= 1 for LOVE variance");
+    double a_s = 0.0, r_s = 0.0;
+    const int its = solve_alpha_and_root(pv, y, o.mean, o.max_cg_iter, o.cg_tol,
+                                         o.lanczos_rank, ps, &a_s, &r_s);
+    if (info) {
+      info->alpha_cg_iterations = its;
+      info->alpha_time_s = a_s;
+      info->love_root_time_s = r_s;
+    }
+    return;
+  }
   if (alpha_in) {
     ps.alpha.ensure(pv.n);
     MGP_HIP_CHECK(hipMemcpy(ps.alpha.ptr, alpha_in, pv.n * sizeof(float), hipMemcpyHostToDevice));

@@ -180,6 +180,12 @@ int solve_columns(const CGOperator& op, const float* B, int C, int max_iter, flo
                   float* X);
 // Lanczos inverse root S (S S^T ~ (K + noise I)^{-1}), rank r.
 void lanczos_inv_root(Provider& pv, int r, PredictState& ps);
+// solve_alpha followed by lanczos_inv_root with the same results; where the
+// provider's products are column independent the two run side by side, one
+// two-column product per iteration while both are active.  alpha_s is the
+// time until alpha is done, root_s the rest.  Returns solve_alpha's count.
+int solve_alpha_and_root(Provider& pv, const float* y_host, float mean, int max_iter, float tol,
+                         int rank, PredictState& ps, double* alpha_s, double* root_s);
 
 struct PredictTimes {
   double alpha_s = 0, love_root_s = 0, mean_s = 0, variance_s = 0, total_s = 0;

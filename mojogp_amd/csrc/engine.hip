@@ -970,48 +970,79 @@ TrainResult train(Provider& pv, const float* y_host, const std::vector<float>& i
 }
 
 // ------------------------------------------------------------------ prediction
-int solve_alpha(Provider& pv, const float* y_host, float mean, int max_iter, float tol,
-                PredictState& ps) {
-  const int64_t n = pv.n;
-  hipStream_t st = pv.st;
-  const int nb = reduction_chunks(n);
-  DevBuf<float> r, p, Ap, s;
+namespace {
+
+// Unpreconditioned single-column CG for alpha = (K + noise I)^-1 (y - mean),
+// one iteration per step() after the caller has formed Ap = A p.  p and Ap
+// may live in a caller's product buffer (shared products with the Lanczos
+// root); the stop flag is read every 4 iterations, as the reference's host
+// solver checks its residual (solve_single_rhs_deterministic_host_jit).
+struct AlphaSolve {
+  Provider& pv;
+  int64_t n;
+  hipStream_t st;
+  int nb, max_iter;
+  float tol;
+  DevBuf<float> r, pbuf, Apbuf, s;
   DevBuf<double> part;
   DevBuf<int> done;
-  float* x = ps.alpha.ensure(n);
-  r.ensure(n);
-  p.ensure(n);
-  Ap.ensure(n);
-  s.ensure(4);
-  part.ensure((size_t)2 * nb);
-  done.ensure(1);
-  MGP_HIP_CHECK(hipMemcpyAsync(r.ptr, y_host, n * sizeof(float), hipMemcpyHostToDevice, st));
-  sub_scalar(r.ptr, r.ptr, mean, n, st);
-  fill(x, n, 0.0f, st);
-  copy(p.ptr, r.ptr, n, st);
-  coldot_partial(r.ptr, r.ptr, n, 1, nb, part.ptr, st);
-  hipLaunchKernelGGL(k_a1_init, dim3(1), dim3(64), 0, st, part.ptr, nb, s.ptr, done.ptr);
+  float *x, *p, *Ap;
   int it = 0;
-  for (; it < max_iter; ++it) {
-    pv.forward(p.ptr, 1, Ap.ptr);
-    coldot_partial(p.ptr, Ap.ptr, n, 1, nb, part.ptr, st);
+  bool finished = false;
+
+  AlphaSolve(Provider& pv_, const float* y_host, float mean, int max_iter_, float tol_,
+             PredictState& ps, float* p_ext = nullptr, float* Ap_ext = nullptr)
+      : pv(pv_), n(pv_.n), st(pv_.st), nb(reduction_chunks(pv_.n)), max_iter(max_iter_),
+        tol(tol_) {
+    x = ps.alpha.ensure(n);
+    r.ensure(n);
+    p = p_ext ? p_ext : pbuf.ensure(n);
+    Ap = Ap_ext ? Ap_ext : Apbuf.ensure(n);
+    s.ensure(4);
+    part.ensure((size_t)2 * nb);
+    done.ensure(1);
+    MGP_HIP_CHECK(hipMemcpyAsync(r.ptr, y_host, n * sizeof(float), hipMemcpyHostToDevice, st));
+    sub_scalar(r.ptr, r.ptr, mean, n, st);
+    fill(x, n, 0.0f, st);
+    copy(p, r.ptr, n, st);
+    coldot_partial(r.ptr, r.ptr, n, 1, nb, part.ptr, st);
+    hipLaunchKernelGGL(k_a1_init, dim3(1), dim3(64), 0, st, part.ptr, nb, s.ptr, done.ptr);
+    finished = max_iter <= 0;
+  }
+  void step() {
+    coldot_partial(p, Ap, n, 1, nb, part.ptr, st);
     hipLaunchKernelGGL(k_a1_alpha, dim3(1), dim3(64), 0, st, part.ptr, nb, s.ptr, done.ptr);
-    hipLaunchKernelGGL(k_a1_update, dim3(nb), dim3(256), 0, st, x, r.ptr, p.ptr, Ap.ptr, n, nb,
-                       s.ptr, done.ptr, part.ptr + nb);
+    hipLaunchKernelGGL(k_a1_update, dim3(nb), dim3(256), 0, st, x, r.ptr, p, Ap, n, nb, s.ptr,
+                       done.ptr, part.ptr + nb);
     hipLaunchKernelGGL(k_a1_beta, dim3(1), dim3(64), 0, st, part.ptr + nb, nb, tol, s.ptr,
                        done.ptr);
-    hipLaunchKernelGGL(k_a1_pupdate, g1(n), dim3(256), 0, st, p.ptr, r.ptr, n, s.ptr, done.ptr);
+    hipLaunchKernelGGL(k_a1_pupdate, g1(n), dim3(256), 0, st, p, r.ptr, n, s.ptr, done.ptr);
     MGP_HIP_CHECK(hipGetLastError());
     if ((it & 3) == 3 || it == max_iter - 1) {
       int dh = 0;
       MGP_HIP_CHECK(hipMemcpyAsync(&dh, done.ptr, sizeof(int), hipMemcpyDeviceToHost, st));
       MGP_HIP_CHECK(hipStreamSynchronize(st));
-      if (dh) break;
+      if (dh) {  // iterations reported as the index of the stopping one
+        finished = true;
+        return;
+      }
     }
+    if (++it >= max_iter) finished = true;
   }
-  MGP_HIP_CHECK(hipStreamSynchronize(st));
+};
+
+}  // namespace
+
+int solve_alpha(Provider& pv, const float* y_host, float mean, int max_iter, float tol,
+                PredictState& ps) {
+  AlphaSolve a(pv, y_host, mean, max_iter, tol, ps);
+  while (!a.finished) {
+    pv.forward(a.p, 1, a.Ap);
+    a.step();
+  }
+  MGP_HIP_CHECK(hipStreamSynchronize(pv.st));
   ps.has_alpha = true;
-  return it;
+  return a.it;
 }
 
 int solve_columns(const CGOperator& op, const float* B, int C, int max_iter, float tol,
@@ -1063,87 +1094,163 @@ int solve_columns(const CGOperator& op, const float* B, int C, int max_iter, flo
   return it;
 }
 
-void lanczos_inv_root(Provider& pv, int r, PredictState& ps) {
-  const int64_t n = pv.n;
-  hipStream_t st = pv.st;
-  MGP_REQUIRE(r >= 1 && r <= 1000, "Lanczos rank must be in [1, 1000]");
-  const int nb = reduction_chunks(n);
-  DevBuf<float> Q, w;
-  DevBuf<double> part, coef;
-  Q.ensure((size_t)r * n);
-  w.ensure(n);
-  part.ensure((size_t)(r + 1) * nb + 8);
-  coef.ensure((size_t)r + 1);
-  fill(Q.ptr, (int64_t)r * n, 0.0f, st);
-  // Deterministic +-1 start vector (jit_prediction.mojo:999-1015).
-  std::vector<float> z(n);
-  float zsq = 0.0f;
-  for (int64_t i = 0; i < n; ++i) {
-    uint64_t s = 0xC0FFEE1234567890ull ^ ((uint64_t)i * 0x9E3779B97F4A7C15ull) ^
-                 ((uint64_t)r * 0xBF58476D1CE4E5B9ull);
-    s ^= s >> 12;
-    s ^= s << 25;
-    s ^= s >> 27;
-    s *= 0x2545F4914F6CDD1Dull;
-    z[i] = (s & 0x20000ull) ? 1.0f : -1.0f;
-    zsq += z[i] * z[i];
-  }
-  const float zn = std::sqrt(zsq);
-  for (int64_t i = 0; i < n; ++i) z[i] /= zn;
-  MGP_HIP_CHECK(hipMemcpyAsync(Q.ptr, z.data(), n * sizeof(float), hipMemcpyHostToDevice, st));
+namespace {
 
-  std::vector<double> alpha(r, 0.0), beta(std::max(r - 1, 0), 0.0);
-  std::vector<double> inner(r + 1);
+// Lanczos on K + noise I from the deterministic +-1 start vector
+// (compute_lanczos_inv_root_jit, jit_prediction.mojo:974-1177), one iteration
+// per step() after the caller has formed w = A v_j (w may live in a caller's
+// product buffer); finish() forms the inverse root.
+struct LanczosSolve {
+  Provider& pv;
+  int64_t n;
+  hipStream_t st;
+  int r, nb;
+  DevBuf<float> Q, wbuf;
+  DevBuf<double> part, coef;
+  float* w;
+  std::vector<double> alpha, beta, inner;
   float beta_prev = 0.0f;
-  for (int j = 0; j < r; ++j) {
-    const float* v = Q.ptr + (size_t)j * n;
-    pv.forward(v, 1, w.ptr);
-    const float aj = dot_f(v, w.ptr, n, part, st);
+  int j = 0;
+  bool finished = false;
+
+  LanczosSolve(Provider& pv_, int r_, float* w_ext = nullptr)
+      : pv(pv_), n(pv_.n), st(pv_.st), r(r_), nb(reduction_chunks(pv_.n)) {
+    MGP_REQUIRE(r >= 1 && r <= 1000, "Lanczos rank must be in [1, 1000]");
+    Q.ensure((size_t)r * n);
+    w = w_ext ? w_ext : wbuf.ensure(n);
+    part.ensure((size_t)(r + 1) * nb + 8);
+    coef.ensure((size_t)r + 1);
+    fill(Q.ptr, (int64_t)r * n, 0.0f, st);
+    // Deterministic +-1 start vector (jit_prediction.mojo:999-1015).
+    std::vector<float> z(n);
+    float zsq = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+      uint64_t s = 0xC0FFEE1234567890ull ^ ((uint64_t)i * 0x9E3779B97F4A7C15ull) ^
+                   ((uint64_t)r * 0xBF58476D1CE4E5B9ull);
+      s ^= s >> 12;
+      s ^= s << 25;
+      s ^= s >> 27;
+      s *= 0x2545F4914F6CDD1Dull;
+      z[i] = (s & 0x20000ull) ? 1.0f : -1.0f;
+      zsq += z[i] * z[i];
+    }
+    const float zn = std::sqrt(zsq);
+    for (int64_t i = 0; i < n; ++i) z[i] /= zn;
+    MGP_HIP_CHECK(hipMemcpyAsync(Q.ptr, z.data(), n * sizeof(float), hipMemcpyHostToDevice, st));
+    // The start vector's host buffer must outlive the copy.
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    alpha.assign(r, 0.0);
+    beta.assign(std::max(r - 1, 0), 0.0);
+    inner.assign(r + 1, 0.0);
+  }
+  const float* vec() const { return Q.ptr + (size_t)j * n; }
+  void step() {
+    const float* v = vec();
+    const float aj = dot_f(v, w, n, part, st);
     alpha[j] = aj;
-    hipLaunchKernelGGL(k_three_term, g1(n), dim3(256), 0, st, w.ptr, v,
+    hipLaunchKernelGGL(k_three_term, g1(n), dim3(256), 0, st, w, v,
                        j > 0 ? Q.ptr + (size_t)(j - 1) * n : nullptr, aj, beta_prev, n);
     // Full re-orthogonalisation against Q_0..Q_j, at most two passes; the
     // second pass runs only if the first saw an inner product >= 1e-5.
     for (int pass = 0; pass < 2; ++pass) {
-      multi_dot(Q.ptr, j + 1, w.ptr, n, part.ptr, nb, coef.ptr, st);
+      multi_dot(Q.ptr, j + 1, w, n, part.ptr, nb, coef.ptr, st);
       MGP_HIP_CHECK(hipMemcpyAsync(inner.data(), coef.ptr, (j + 1) * sizeof(double),
                                    hipMemcpyDeviceToHost, st));
       MGP_HIP_CHECK(hipStreamSynchronize(st));
       double mx = 0.0;
       for (int k = 0; k <= j; ++k) mx = std::max(mx, std::fabs(inner[k]));
-      multi_axpy(Q.ptr, j + 1, coef.ptr, w.ptr, n, st);
+      multi_axpy(Q.ptr, j + 1, coef.ptr, w, n, st);
       if (mx < 1e-5) break;
     }
-    const float bj = std::sqrt(dot_f(w.ptr, w.ptr, n, part, st));
+    const float bj = std::sqrt(dot_f(w, w, n, part, st));
     if (j < r - 1) beta[j] = bj;
-    if (bj < 1e-10f) break;  // remaining Q columns stay zero
-    if (j + 1 < r)
-      hipLaunchKernelGGL(k_scale_into, g1(n), dim3(256), 0, st, Q.ptr + (size_t)(j + 1) * n,
-                         w.ptr, bj, n);
-    beta_prev = bj;
-  }
-  std::vector<double> ev, V;
-  if (!tridiag_eigh(alpha, beta, ev, &V))
-    throw Error(ST_NUMERIC, "Lanczos tridiagonal eigendecomposition did not converge");
-  double max_eig = 1e-10;
-  for (double e : ev) max_eig = std::max(max_eig, e);
-  const double clamp = max_eig * 1e-6;
-  std::vector<float> Tinv((size_t)r * r);
-  for (int i = 0; i < r; ++i)
-    for (int c = 0; c < r; ++c) {
-      double s = 0.0;
-      for (int k = 0; k < r; ++k)
-        s += V[(size_t)i * r + k] * V[(size_t)c * r + k] / std::sqrt(std::max(ev[k], clamp));
-      Tinv[(size_t)i * r + c] = (float)s;
+    if (bj < 1e-10f) {  // remaining Q columns stay zero
+      finished = true;
+      return;
     }
-  DevBuf<float> Td;
-  Td.ensure(Tinv.size());
-  MGP_HIP_CHECK(hipMemcpyAsync(Td.ptr, Tinv.data(), Tinv.size() * sizeof(float),
-                               hipMemcpyHostToDevice, st));
-  ps.root.ensure((size_t)r * n);
-  gemm_nr_rr(Q.ptr, Td.ptr, n, r, ps.root.ptr, st);
-  MGP_HIP_CHECK(hipStreamSynchronize(st));
-  ps.rank = r;
+    if (j + 1 < r)
+      hipLaunchKernelGGL(k_scale_into, g1(n), dim3(256), 0, st, Q.ptr + (size_t)(j + 1) * n, w,
+                         bj, n);
+    beta_prev = bj;
+    if (++j >= r) finished = true;
+  }
+  void finish(PredictState& ps) {
+    std::vector<double> ev, V;
+    if (!tridiag_eigh(alpha, beta, ev, &V))
+      throw Error(ST_NUMERIC, "Lanczos tridiagonal eigendecomposition did not converge");
+    double max_eig = 1e-10;
+    for (double e : ev) max_eig = std::max(max_eig, e);
+    const double clamp = max_eig * 1e-6;
+    std::vector<float> Tinv((size_t)r * r);
+    for (int i = 0; i < r; ++i)
+      for (int c = 0; c < r; ++c) {
+        double s = 0.0;
+        for (int k = 0; k < r; ++k)
+          s += V[(size_t)i * r + k] * V[(size_t)c * r + k] / std::sqrt(std::max(ev[k], clamp));
+        Tinv[(size_t)i * r + c] = (float)s;
+      }
+    DevBuf<float> Td;
+    Td.ensure(Tinv.size());
+    MGP_HIP_CHECK(hipMemcpyAsync(Td.ptr, Tinv.data(), Tinv.size() * sizeof(float),
+                                 hipMemcpyHostToDevice, st));
+    ps.root.ensure((size_t)r * n);
+    gemm_nr_rr(Q.ptr, Td.ptr, n, r, ps.root.ptr, st);
+    MGP_HIP_CHECK(hipStreamSynchronize(st));
+    ps.rank = r;
+  }
+};
+
+}  // namespace
+
+void lanczos_inv_root(Provider& pv, int r, PredictState& ps) {
+  LanczosSolve l(pv, r);
+  while (!l.finished) {
+    pv.forward(l.vec(), 1, l.w);
+    l.step();
+  }
+  l.finish(ps);
+}
+
+int solve_alpha_and_root(Provider& pv, const float* y_host, float mean, int max_iter, float tol,
+                         int rank, PredictState& ps, double* alpha_s, double* root_s) {
+  const auto t0 = Clock::now();
+  if (!pv.column_independent_products()) {
+    const int its = solve_alpha(pv, y_host, mean, max_iter, tol, ps);
+    *alpha_s = secs_since(t0);
+    const auto t1 = Clock::now();
+    lanczos_inv_root(pv, rank, ps);
+    *root_s = secs_since(t1);
+    return its;
+  }
+  const int64_t n = pv.n;
+  DevBuf<float> V2, O2;  // [p | v_j] and [A p | A v_j]
+  V2.ensure((size_t)2 * n);
+  O2.ensure((size_t)2 * n);
+  AlphaSolve a(pv, y_host, mean, max_iter, tol, ps, V2.ptr, O2.ptr);
+  LanczosSolve l(pv, rank, O2.ptr + n);
+  *alpha_s = 0.0;
+  while (!a.finished || !l.finished) {
+    if (!a.finished && !l.finished) {
+      copy(V2.ptr + n, l.vec(), n, pv.st);
+      pv.forward(V2.ptr, 2, O2.ptr);
+      a.step();
+      if (a.finished) *alpha_s = secs_since(t0);
+      l.step();
+    } else if (!a.finished) {
+      pv.forward(a.p, 1, a.Ap);
+      a.step();
+      if (a.finished) *alpha_s = secs_since(t0);
+    } else {
+      pv.forward(l.vec(), 1, l.w);
+      l.step();
+    }
+  }
+  MGP_HIP_CHECK(hipStreamSynchronize(pv.st));
+  if (*alpha_s == 0.0) *alpha_s = secs_since(t0);
+  ps.has_alpha = true;
+  l.finish(ps);
+  *root_s = std::max(0.0, secs_since(t0) - *alpha_s);
+  return a.it;
 }
 
 namespace {

@@ -142,6 +142,10 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
                   const PackedPoints& cols, const float* V_dev, float* out_dev,
                   MatvecWorkspace& ws, hipStream_t st, int force_splits = 0);
 constexpr int64_t kSymMinBlocks = 48;
+// True when a square product of the packed points with ncols right-hand
+// sides (own work buffers) runs on the symmetric kernel, whose result for
+// each column does not depend on the other columns.
+bool symmetric_route_taken(const PackedPoints& pts, int ncols);
 constexpr double kSymMaxBytes = 16e9;
 
 // Bytes of work buffers one fused_matvec call with ncols right-hand sides

@@ -1810,6 +1810,19 @@ bool sym_route(const MatvecArgs& a, const PackedPoints& rows, const PackedPoints
   return tp_bytes <= kSymMaxBytes;
 }
 
+}  // namespace
+
+bool symmetric_route_taken(const PackedPoints& pts, int ncols) {
+  MatvecArgs a;
+  a.square = true;
+  a.m = a.n = pts.n;
+  a.ncols = ncols;
+  MatvecWorkspace ws;  // no fixed arena
+  return pts.kb >= 1 && sym_route(a, pts, pts, ncols, ws);
+}
+
+namespace {
+
 using SymFn = void (*)(const h8*, const h8*, const h8*, int64_t, int64_t, int64_t, int64_t,
                        int, const uint32_t*, float*, float*, int64_t);
 

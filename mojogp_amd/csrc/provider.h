@@ -115,6 +115,10 @@ struct Provider {
   // True when forward() runs the fused tile kernel (not materialized, Gram form
   // accurate for the packed training set).
   bool fused_route() const;
+  // True when forward() gives every column the same bits whether it runs
+  // alone or beside other columns (one and two columns on the symmetric
+  // kernel), so independent solvers may share products.
+  bool column_independent_products() const;
   // Fused route only: out[cc][t] (+)= sum_t' mix[t][t'] ((K + noise I) V)[cc][t'] for
   // task blocks of T columns (mix: device [T][T]), mixing folded into the
   // split-K reduction.

@@ -196,6 +196,10 @@ void Provider::forward_scalar(const float* V, int ncols, float* out, MatvecWorks
   fused_matvec(a, train, train, V, out, wsp ? *wsp : ws, st);
 }
 
+bool Provider::column_independent_products() const {
+  return fused_route() && symmetric_route_taken(train, 1) && symmetric_route_taken(train, 2);
+}
+
 bool Provider::fused_route() const {
   return !is_tree && !materialized && gram_form_ok(kind, train, train);
 }
