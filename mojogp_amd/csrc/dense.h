@@ -23,14 +23,33 @@ struct DenseK {
   int64_t n = 0, npad = 0;
   int shift = 0;              // stored value = K * 2^shift (split)
   DevBuf<uint32_t> data;      // [npad][npad / 8] groups of 16 fp16 (8 dwords)
+  bool full_valid = false;    // data holds K for the current parameters
   int64_t groups_per_row() const { return npad / 8; }
+  // Symmetric half: for nb = npad / 256 blocks of 256 points, the blocks
+  // (b, (b + delta) mod nb), delta = 0 .. sym_span(b, nb) (the diagonal block
+  // and the cyclic half of the others, each unordered pair once), each stored
+  // as [256 rows][32 groups] in the split format above, at block index
+  // dense_half_index(b, delta, nb): n^2/2 + 128 n entries instead of n^2.
+  DevBuf<uint32_t> half;
+  bool half_valid = false;
+  int64_t blocks() const { return npad / 256; }
 };
+
+// Storage position of block (b, (b + delta) mod nb) of the symmetric half.
+__host__ __device__ inline int64_t dense_half_index(int64_t b, int64_t delta, int64_t nb) {
+  if (nb & 1) return b * ((nb - 1) / 2 + 1) + delta;
+  const int64_t h = nb / 2;
+  return (b < h ? b * (h + 1) : h * (h + 1) + (b - h) * h) + delta;
+}
+inline int64_t dense_half_blocks(int64_t nb) { return nb * (nb + 1) / 2; }
 
 // Work buffers of dense_forward, grown on demand.
 struct DenseWorkspace {
   DevBuf<uint32_t> vpack;           // packed right-hand sides [cpad][npad / 8] groups
+  DevBuf<uint32_t> vpair;           // right-hand sides in row-tile-pair order (symmetric route)
   DevBuf<uint32_t> colmax, colmax_part;
   DevBuf<float> part;               // [splits][cpad][npad]
+  DevBuf<float> tpart;              // transposed partial sums of the symmetric route
 };
 
 // Allocate K for n points (npad^2 entries, padding zeroed) with the scale of
@@ -38,6 +57,17 @@ struct DenseWorkspace {
 void dense_alloc(DenseK& K, int64_t n, float kmax, hipStream_t st);
 // Pack rows [r0, r0 + nrows) of K given in fp32 with row stride n.
 void dense_pack_rows(const float* rows, int64_t r0, int64_t nrows, DenseK& K, hipStream_t st);
+// Allocate the symmetric half for n points with the scale of kmax (> 0).
+void dense_alloc_half(DenseK& K, int64_t n, float kmax);
+// Pack the symmetric half's blocks of row block b from its rows of K in fp32
+// ([nrows][n], row stride n, nrows <= 256; rows past nrows are zero).
+void dense_pack_half(const float* rows, int64_t b, int64_t nrows, DenseK& K, hipStream_t st);
+// out = K V + noise V for 1..16 columns from the symmetric half: every
+// off-diagonal block is read once and used for both of its products (the
+// transposed one through gfx950's transposing LDS read), half the bytes of
+// dense_forward.
+void dense_sym_forward(const DenseK& K, const float* V, int ncols, float noise, float* out,
+                       DenseWorkspace& w, hipStream_t st);
 // out = K V + noise V for V, out device [ncols][n]: products on the fp16 matrix
 // cores (Kh Vh + Kh Vl + Kl Vh, each right-hand side split after scaling its
 // column to max |V| in [2^14, 2^15)), fp32 accumulation over split ranges of

@@ -9,6 +9,7 @@
 // |K V| per entry, and the accumulation is fp32 per column split, as in an
 // fp32 GEMM; split partials are added in fp64.
 #include "dense.h"
+#include "sym_common.h"
 
 #include <algorithm>
 #include <cmath>
@@ -18,6 +19,7 @@ namespace mgp {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h16 __attribute__((ext_vector_type(16)));
+typedef float f2 __attribute__((ext_vector_type(2)));
 
 namespace {
 
@@ -261,6 +263,292 @@ __global__ void k_dense_reduce(const float* __restrict__ part, int splits, int c
   out[idx] = fmaf(noise, V[idx], (float)(sc * s));
 }
 
+// ---------------------------------------------------------------------------
+// Symmetric half of K and its products.
+//
+// K is symmetric, so the half keeps the diagonal blocks and the cyclic half
+// of the off-diagonal blocks of 256 points (sym_span), each unordered pair
+// once.  A product with <= 16 right-hand sides reads every stored block once:
+//   * forward, out_b += K_bJ V_J: the block rows straight from global memory
+//     as the A operand (the layout of dense_forward), V_J in the same group
+//     order as the B operand;
+//   * transposed (J != b), out_J += K_bJ^T V_b: each wave stores its two row
+//     tiles' 8-byte chunks (row, 4 columns) of both parts to a wave-private
+//     LDS scratch and reads them back with ds_read_b64_tr_b16, which yields
+//     the block transposed into the B operand of O_J^T += V_b^T K_bJ,
+//     contracted over the wave's two row tiles in the row-tile-pair order of
+//     the pair-packed V_b (A operand, loaded once per wave);
+//   * the waves' transposed sums (32 rows each) are added in wave order after
+//     the next barrier and written as the 256-row partial tp[b][delta - 1];
+//     k_dense_sym_reduce adds, per point, the forward split partials and the
+//     partials of the row blocks that formed its column block (fp64, fixed
+//     order).
+// ---------------------------------------------------------------------------
+constexpr int kDsRows = 256;                    // points per block
+constexpr int kDsGroups = kDsRows / 8;          // 8-column groups per block row
+constexpr int kDsWaves = 8;                     // waves per workgroup, 32 rows each
+constexpr int kDsSteps = kDsRows / 32;          // 32-column steps per block
+constexpr int kDsStage = 2;                     // steps per transposed hand-off
+constexpr int kDsStages = kDsSteps / kDsStage;  // hand-offs per block
+
+// One thread per (delta, row, group) of row block b's stored blocks.
+__global__ void k_dense_pack_half(const float* __restrict__ rows, int64_t nrows, int64_t n,
+                                  int64_t b, int64_t nb, int64_t span, int shift, int vec4,
+                                  h16* __restrict__ half) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (span + 1) * kDsRows * kDsGroups) return;
+  const int64_t delta = idx / (kDsRows * kDsGroups);
+  const int64_t rem = idx - delta * (kDsRows * kDsGroups);
+  const int64_t r = rem / kDsGroups, g = rem - r * kDsGroups;
+  int64_t J = b + delta;
+  if (J >= nb) J -= nb;
+  const int64_t j0 = J * kDsRows + 8 * g;
+  float x[8];
+  const float* s = rows + r * n;
+  if (r < nrows && vec4 && j0 + 8 <= n) {
+    const f4 a = *reinterpret_cast<const f4*>(s + j0);
+    const f4 c = *reinterpret_cast<const f4*>(s + j0 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = a[e];
+      x[4 + e] = c[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (r < nrows && j0 + e < n) ? s[j0 + e] : 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = ldexpf(x[e], shift);
+  half[(dense_half_index(b, delta, nb) * kDsRows + r) * kDsGroups + g] = split16(x);
+}
+
+// Right-hand sides in row-tile-pair order: Vp[(u*2 + part)*64 + lane] (8
+// fp16), element e = 2^s_c V[c = lane%16][32 u + 16 (e/4) + 4 (lane/16) + e%4],
+// part 0 = hi, 1 = lo; zero for c >= ncols or past n.
+__global__ void k_dense_pack_pair(const float* __restrict__ V, int64_t n, int ncols,
+                                  int64_t pairs, const uint32_t* __restrict__ colmax,
+                                  h8* __restrict__ Vp) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= pairs * 64) return;
+  const int lane = (int)(idx & 63);
+  const int64_t u = idx >> 6;
+  const int c = lane & 15;
+  const int sh = c < ncols ? scale_shift(__uint_as_float(colmax[c])) : 0;
+  h8 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t j = 32 * u + 16 * (e >> 2) + 4 * (lane >> 4) + (e & 3);
+    const float v = (c < ncols && j < n) ? ldexpf(V[(int64_t)c * n + j], sh) : 0.0f;
+    hi[e] = (_Float16)v;
+    lo[e] = (_Float16)(v - (float)hi[e]);
+  }
+  Vp[(u * 2) * 64 + lane] = hi;
+  Vp[(u * 2 + 1) * 64 + lane] = lo;
+}
+
+// Work item L = (row block b, delta split) of the symmetric half product.
+// fwd[(split*16 + c)*mpad + i]: forward sums of the split's blocks, unscaled;
+// tp[((b*hmax + delta - 1)*256 + column)*16 + c]: transposed block sums.
+__global__ __launch_bounds__(64 * kDsWaves) void k_dense_sym(
+    const h16* __restrict__ Kh, const h16* __restrict__ Vn, const h8* __restrict__ Vpp,
+    int64_t nb, int64_t splits, int64_t dps, int64_t hmax, int64_t gpr, int ncols, int kshift,
+    const uint32_t* __restrict__ colmax, float* __restrict__ fwd, float* __restrict__ tp,
+    int64_t mpad) {
+  constexpr int W = kDsWaves;
+  // Wave-private transposition scratch: [column tile][hi, lo][row tile][chunk].
+  __shared__ uint64_t tsc[W][2][2][2][64];
+  // Transposed sums per hand-off: [buffer][step][wave][column tile][lane].
+  __shared__ f4 tbuf[2][kDsStage][W][2][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t per = (int64_t)gridDim.x / kXcds;
+  const int64_t L = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  if (L >= nb * splits) return;  // whole workgroup, before any barrier
+  const int64_t b = L % nb;
+  const int64_t split = L / nb;
+  const int li = lane & 15, lg = lane >> 4;
+  const int row0 = 32 * wave;  // this wave's rows within the block
+  const int64_t upr = (b * kDsRows + row0) / 32;
+  const h8 vih = Vpp[(upr * 2) * 64 + lane], vil = Vpp[(upr * 2 + 1) * 64 + lane];
+  const int chunk_r = sym_read_chunk(lane);
+  const int tw = lg >> 1, q0 = 2 * (lg & 1);  // column tile and first quad of this lane's group
+
+  f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+  double accd[2][4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) accd[r][q] = 0.0;
+
+  const int64_t span = sym_span(b, nb);
+  const int64_t d0 = split * dps;
+  const int64_t d1 = min(d0 + dps, span + 1);
+  const int64_t nsteps = d1 > d0 ? (d1 - d0) * kDsSteps : 0;
+  const int64_t nst = nsteps / kDsStage;
+  auto step_delta = [&](int64_t t) { return d0 + t / kDsSteps; };
+  // Loads of step t: the wave's two row tiles of the block (lane: row
+  // 16 r + li, group 4 s + lg) and V_J (lane: column li, same group).
+  auto load = [&](int64_t t, h16 (&ka)[2], h16& va) __attribute__((always_inline)) {
+    const int64_t delta = step_delta(t);
+    const int s = (int)(t % kDsSteps);
+    int64_t J = b + delta;
+    if (J >= nb) J -= nb;
+    const h16* kp = Kh + (dense_half_index(b, delta, nb) * kDsRows + row0) * kDsGroups + 4 * s + lg;
+    ka[0] = kp[(int64_t)li * kDsGroups];
+    ka[1] = kp[(int64_t)(16 + li) * kDsGroups];
+    va = Vn[(int64_t)li * gpr + J * kDsGroups + 4 * s + lg];
+  };
+  auto flush = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) accd[r][q] += (double)acc[r][q];
+      acc[r] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  // Stage reduction (all 512 threads): unit u < kDsStage*256 is two
+  // right-hand sides (2h, 2h + 1 of the lane's four) of one lane of one
+  // column tile; a thread's units share the lane half, so its scales are fixed.
+  constexpr int kRedUnits = kDsStage * 256;
+  const int ru = threadIdx.x;
+  const int r_ln = (ru >> 1) & 63, r_h = ru & 1;
+  const int r_c = 4 * (r_ln >> 4) + 2 * r_h;
+  f2 r_scale;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int cc = r_c + e;
+    const int sh = cc < ncols ? scale_shift(__uint_as_float(colmax[cc])) : 0;
+    r_scale[e] = ldexpf(1.0f, -(kshift + sh));
+  }
+  auto reduce_stage = [&](int64_t c) __attribute__((always_inline)) {
+    const int slot = (int)(c & 1);
+    const int64_t blk = b * hmax + step_delta(c * kDsStage) - 1;
+    constexpr int wstride = (int)(sizeof(tbuf[0][0][0]) / sizeof(float));
+#pragma unroll
+    for (int uu = 0; uu < kRedUnits; uu += 64 * W) {
+      const int u = uu + ru;
+      if (u >= kRedUnits) break;
+      const int kk = u >> 8, t = (u >> 7) & 1;
+      const float* src = reinterpret_cast<const float*>(&tbuf[slot][kk][0][t][r_ln]) + 2 * r_h;
+      f2 sum = *reinterpret_cast<const f2*>(src);
+#pragma unroll
+      for (int w = 1; w < W; ++w) sum += *reinterpret_cast<const f2*>(src + w * wstride);
+      const int64_t s = (c * kDsStage) % kDsSteps + kk;
+      const int64_t jl = 32 * s + 16 * t + (r_ln & 15);
+      *reinterpret_cast<f2*>(tp + (blk * kDsRows + jl) * 16 + r_c) = sum * r_scale;
+    }
+  };
+
+  h16 ka[2], va, kn[2], vn;
+  if (nsteps > 0) load(0, ka, va);
+  for (int64_t c = 0; c < nst; ++c) {
+    __syncthreads();
+    if (c > 0 && step_delta((c - 1) * kDsStage) > 0) reduce_stage(c - 1);
+    const bool sym = step_delta(c * kDsStage) > 0;
+#pragma unroll
+    for (int k = 0; k < kDsStage; ++k) {
+      const int64_t t = c * kDsStage + k;
+      load(min(t + 1, nsteps - 1), kn, vn);  // next step (clamped: always a valid block)
+      const h8 vh = first8(va), vl = last8(va);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const h8 kh = first8(ka[r]), kl = last8(ka[r]);
+        f4 a = acc[r];
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, vh, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, vl, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, vh, a, 0, 0, 0);
+        acc[r] = a;
+      }
+      if (sym) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const u64x2 h = __builtin_bit_cast(u64x2, first8(ka[r]));
+          const u64x2 l = __builtin_bit_cast(u64x2, last8(ka[r]));
+          tsc[wave][tw][0][r][sym_chunk(li, q0)] = h[0];
+          tsc[wave][tw][0][r][sym_chunk(li, q0 + 1)] = h[1];
+          tsc[wave][tw][1][r][sym_chunk(li, q0)] = l[0];
+          tsc[wave][tw][1][r][sym_chunk(li, q0 + 1)] = l[1];
+        }
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          h8 tp2[2];
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const u64x2 v = {tr_read(&tsc[wave][tt][p][0][chunk_r]),
+                             tr_read(&tsc[wave][tt][p][1][chunk_r])};
+            tp2[p] = __builtin_bit_cast(h8, v);
+          }
+          f4 a = f4{0.f, 0.f, 0.f, 0.f};
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih, tp2[0], a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vil, tp2[0], a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih, tp2[1], a, 0, 0, 0);
+          tbuf[c & 1][k][wave][tt][lane] = a;
+        }
+        asm volatile("" ::: "memory");
+      }
+      ka[0] = kn[0];
+      ka[1] = kn[1];
+      va = vn;
+    }
+    if ((c + 1) % kDsStages == 0) flush();  // end of a block
+  }
+  if (nst > 0 && step_delta((nst - 1) * kDsStage) > 0) {
+    __syncthreads();
+    reduce_stage(nst - 1);
+  }
+  flush();
+  // Forward partials (lane: column li, rows 16 r + 4 lg + q of the wave).
+  const int sh = li < ncols ? scale_shift(__uint_as_float(colmax[li])) : 0;
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t i = b * kDsRows + row0 + 16 * r + 4 * lg + q;
+      fwd[(split * 16 + li) * mpad + i] = (float)ldexp(accd[r][q], -(kshift + sh));
+    }
+}
+
+// out[c*n + j] = sum_s fwd[s][c][j] + the transposed partials of the row
+// blocks that formed j's column block (delta order) + noise V; four threads
+// per point, four right-hand sides each, fp64 sums.
+__global__ __launch_bounds__(256) void k_dense_sym_reduce(
+    const float* __restrict__ fwd, int splits, const float* __restrict__ tp, int64_t nb,
+    int64_t hmax, int64_t mpad, int64_t n, int ncols, float noise,
+    const float* __restrict__ V, float* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t j = t >> 2;
+  const int c4 = (int)(t & 3);
+  if (j >= n) return;
+  double tot[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int s = 0; s < splits; ++s)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = 4 * c4 + e;
+      if (c < ncols) tot[e] += fwd[((int64_t)s * 16 + c) * mpad + j];
+    }
+  const int64_t J = j / kDsRows, jl = j - J * kDsRows;
+  const float* col = tp + jl * 16 + 4 * c4;
+  for (int64_t dl = 1; dl <= hmax; ++dl) {
+    int64_t bb = J - dl;
+    if (bb < 0) bb += nb;
+    const f4 v = *reinterpret_cast<const f4*>(col + (bb * hmax + dl - 1) * (int64_t)kDsRows * 16);
+    const bool formed = dl <= sym_span(bb, nb);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tot[e] += formed ? (double)v[e] : 0.0;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int c = 4 * c4 + e;
+    if (c < ncols) {
+      const int64_t idx = (int64_t)c * n + j;
+      out[idx] = fmaf(noise, V[idx], (float)tot[e]);
+    }
+  }
+}
+
 }  // namespace
 
 void dense_alloc(DenseK& K, int64_t n, float kmax, hipStream_t st) {
@@ -289,6 +577,66 @@ void dense_pack_rows(const float* rows, int64_t r0, int64_t nrows, DenseK& K, hi
   h16* dst = reinterpret_cast<h16*>(K.data.ptr) + r0 * gpr;
   hipLaunchKernelGGL(k_dense_pack, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, rows,
                      nrows, K.n, gpr, K.shift, vec4, dst);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void dense_alloc_half(DenseK& K, int64_t n, float kmax) {
+  MGP_REQUIRE(n >= 1, "dense K needs at least one point");
+  MGP_REQUIRE(std::isfinite(kmax) && kmax > 0.f, "dense K scale needs a finite maximum > 0");
+  K.n = n;
+  K.npad = round_up(n, kDsRows);
+  K.shift = scale_shift(kmax);
+  K.half.ensure((size_t)dense_half_blocks(K.blocks()) * kDsRows * kDsGroups * 8);
+}
+
+void dense_pack_half(const float* rows, int64_t b, int64_t nrows, DenseK& K, hipStream_t st) {
+  const int64_t nb = K.blocks();
+  MGP_REQUIRE(b >= 0 && b < nb && nrows >= 0 && nrows <= kDsRows, "dense K block out of range");
+  const int64_t span = sym_span(b, nb);
+  const int64_t total = (span + 1) * kDsRows * kDsGroups;
+  const int vec4 = (K.n % 4 == 0 && reinterpret_cast<uintptr_t>(rows) % 16 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(k_dense_pack_half, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                     rows, nrows, K.n, b, nb, span, K.shift, vec4,
+                     reinterpret_cast<h16*>(K.half.ptr));
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void dense_sym_forward(const DenseK& K, const float* V, int ncols, float noise, float* out,
+                       DenseWorkspace& w, hipStream_t st) {
+  MGP_REQUIRE(ncols >= 1 && ncols <= 16, "the symmetric dense product takes 1..16 columns");
+  MGP_REQUIRE(K.half_valid, "the symmetric half of K is not filled");
+  const int64_t n = K.n, npad = K.npad, gpr = K.groups_per_row(), nb = K.blocks();
+  const int64_t hmax = nb / 2;
+  const int chunks = (int)std::min<int64_t>(64, std::max<int64_t>(1, ceil_div(n, 4096)));
+  uint32_t* cpart = w.colmax_part.ensure((size_t)chunks * ncols);
+  uint32_t* colmax = w.colmax.ensure((size_t)ncols);
+  hipLaunchKernelGGL(k_dense_absmax_part, dim3((unsigned)chunks, (unsigned)ncols), dim3(256), 0,
+                     st, V, n, cpart);
+  hipLaunchKernelGGL(k_dense_absmax_final, dim3((unsigned)ncols), dim3(64), 0, st, cpart, chunks,
+                     colmax);
+  const int64_t vtot = 16 * gpr;
+  h16* vn = reinterpret_cast<h16*>(w.vpack.ensure((size_t)vtot * 8));
+  const int vec4 = (n % 4 == 0 && reinterpret_cast<uintptr_t>(V) % 16 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(k_dense_pack_rhs, dim3((unsigned)ceil_div(vtot, 256)), dim3(256), 0, st, V,
+                     n, ncols, 16, gpr, colmax, vec4, vn);
+  const int64_t pairs = npad / 32;
+  h8* vp = reinterpret_cast<h8*>(w.vpair.ensure((size_t)pairs * 2 * 64 * 4));
+  hipLaunchKernelGGL(k_dense_pack_pair, dim3((unsigned)ceil_div(pairs * 64, 256)), dim3(256), 0,
+                     st, V, n, ncols, pairs, colmax, vp);
+  MGP_HIP_CHECK(hipGetLastError());
+
+  int64_t splits = std::min<int64_t>(std::max<int64_t>(ceil_div(2048, nb), 1), hmax + 1);
+  const int64_t dps = ceil_div(hmax + 1, splits);
+  splits = ceil_div(hmax + 1, dps);
+  float* fwd = w.part.ensure((size_t)splits * 16 * npad);
+  float* tp = w.tpart.ensure((size_t)std::max<int64_t>(nb * hmax, 1) * kDsRows * 16);
+  const int64_t items = round_up(nb * splits, kXcds);
+  hipLaunchKernelGGL(k_dense_sym, dim3((unsigned)items), dim3(64 * kDsWaves), 0, st,
+                     reinterpret_cast<const h16*>(K.half.ptr), vn, vp, nb, splits, dps, hmax, gpr,
+                     ncols, K.shift, colmax, fwd, tp, npad);
+  MGP_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(k_dense_sym_reduce, dim3((unsigned)ceil_div(4 * n, 256)), dim3(256), 0, st,
+                     fwd, (int)splits, tp, nb, hmax, npad, n, ncols, noise, V, out);
   MGP_HIP_CHECK(hipGetLastError());
 }
 

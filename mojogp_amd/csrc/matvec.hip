@@ -18,6 +18,7 @@
 // K never touches HBM.  Accumulators are flushed into fp64 every 256 columns so
 // the long N-term sums keep ~1e-7 relative accuracy.
 #include "matvec.h"
+#include "sym_common.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -701,28 +702,7 @@ constexpr int kSymPairs = kSymRows / 32;            // column-tile pairs per blo
 constexpr int kSymSteps = 2;                        // column-tile pairs per LDS stage
 constexpr int kSymStages = kSymPairs / kSymSteps;   // LDS stages per block
 constexpr int kSymSchedValu = 6;                    // VALU instructions per MFMA slot
-constexpr int kXcds = 8;                            // XCDs of the MI355X
 static_assert((16 * kPackTileAlign) % kSymRows == 0, "blocks must tile the packed points");
-
-// Off-diagonal column blocks formed by row block b of nb.
-__host__ __device__ inline int64_t sym_span(int64_t b, int64_t nb) {
-  if (nb & 1) return (nb - 1) / 2;
-  return b < nb / 2 ? nb / 2 : nb / 2 - 1;
-}
-
-typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
-typedef __fp16 tr4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
-typedef __attribute__((address_space(3))) tr4 lds_tr4;
-
-// Scratch chunk index of (row i, column quad s) of a 16x16 tile.
-__device__ __forceinline__ int sym_chunk(int i, int s) { return 16 * s + (i ^ (4 * s)); }
-
-// ds_read_b64_tr_b16 from the chunk at p.
-__device__ __forceinline__ uint64_t tr_read(const uint64_t* p) {
-  const tr4 v = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-      (lds_tr4*)((__attribute__((address_space(3))) char*)(p)));
-  return __builtin_bit_cast(uint64_t, v);
-}
 
 template <int KIND, int KB>
 __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
@@ -786,7 +766,7 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
   // Chunk this lane stores (row li, quad lane/16) and the chunk it fetches
   // for the transposed operand (row 4 (lane/16) + (lane/4)%4, quad lane%4).
   const int chunk_w = sym_chunk(li, lane >> 4);
-  const int chunk_r = sym_chunk(4 * (lane >> 4) + ((lane >> 2) & 3), lane & 3);
+  const int chunk_r = sym_read_chunk(lane);
 
   const int64_t span = sym_span(b, nb);
   const int64_t d0 = split * dps;

@@ -63,8 +63,9 @@ struct Provider {
   PackedPoints test;
   DevBuf<float> Xs;
 
-  // Dense K (materialized route) as a scaled two-term fp16 split (dense.h),
-  // refilled on every parameter update.
+  // Dense K (materialized route) as a scaled two-term fp16 split (dense.h):
+  // its symmetric half refilled on every parameter update (products with up
+  // to 16 right-hand sides), the full matrix filled on demand (wider products).
   bool materialized = false;
   DenseK dense;
   DenseWorkspace dense_ws;
@@ -91,7 +92,8 @@ struct Provider {
 
   // Allocate and fill the dense K (materialized route, _do_materialize).
   void materialize();
-  void fill_dense();
+  void fill_dense();       // symmetric half of K (dense.h), after every update
+  void fill_dense_full();  // full K, when a product needs it and it is stale
   // max_i k(x_i, x_i): bounds every |K_ij| of a positive semi-definite kernel.
   float kdiag_max();
   // Rebind the provider to another stream.

@@ -3,6 +3,7 @@
 
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 #include <set>
 #include <cmath>
@@ -103,9 +104,31 @@ float Provider::kdiag_max() {
 }
 
 void Provider::fill_dense() {
+  // The symmetric half (products with <= 16 right-hand sides) after every
+  // parameter update; the full matrix on the first wider product after it.
   float kmax = kdiag_max();
   MGP_REQUIRE(std::isfinite(kmax), "kernel diagonal is not finite");
   if (!(kmax > 0.f)) kmax = 1.f;  // K = 0: any scale
+  dense_alloc_half(dense, n, kmax);
+  float* tmp = io_c.ensure((size_t)256 * n);
+  const int64_t nb = dense.blocks();
+  for (int64_t b = 0; b < nb; ++b) {
+    const int64_t r0 = b * 256, nr = std::min<int64_t>(256, n - r0);
+    if (nr > 0) fill_block(train, r0, nr, tmp);
+    dense_pack_half(tmp, b, std::max<int64_t>(nr, 0), dense, st);
+  }
+  dense.half_valid = true;
+  dense.full_valid = false;
+}
+
+void Provider::fill_dense_full() {
+  if (dense.full_valid) return;
+  const double npad = (double)round_up(n, 256);
+  MGP_REQUIRE(npad * npad * 6.0 <= 250e9,
+              "the full dense K beside its symmetric half does not fit the device");
+  float kmax = kdiag_max();
+  MGP_REQUIRE(std::isfinite(kmax), "kernel diagonal is not finite");
+  if (!(kmax > 0.f)) kmax = 1.f;
   dense_alloc(dense, n, kmax, st);
   // fp32 rows in blocks of <= 32M entries, each packed into the split storage
   const int64_t rows = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t)1 << 25) / n));
@@ -115,6 +138,7 @@ void Provider::fill_dense() {
     fill_block(train, r0, nr, tmp);
     dense_pack_rows(tmp, r0, nr, dense, st);
   }
+  dense.full_valid = true;
 }
 
 void Provider::diag_values(const PackedPoints& pts, int64_t m, float* out) {
@@ -181,7 +205,14 @@ void Provider::forward_scalar(const float* V, int ncols, float* out, MatvecWorks
   a.n = n;
   a.ncols = ncols;
   if (materialized) {
-    dense_forward(dense, V, ncols, noise, out, dense_ws, st);
+    const char* env = std::getenv("MGP_SYM_MATVEC");
+    const bool sym_off = env != nullptr && env[0] == '0';
+    if (ncols <= 16 && dense.half_valid && !sym_off) {
+      dense_sym_forward(dense, V, ncols, noise, out, dense_ws, st);
+    } else {
+      fill_dense_full();
+      dense_forward(dense, V, ncols, noise, out, dense_ws, st);
+    }
     return;
   }
   if (is_tree) {

@@ -107,3 +107,37 @@ def test_symmetric_repeated_calls_bit_identical(monkeypatch):
     finally:
         p.close()
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, False, 4, 1100, 16),
+                                            (ok.MATERN52, True, 3, 3000, 5),
+                                            (ok.RBF, True, 2, 300, 1)])
+def test_materialized_symmetric_half(monkeypatch, kind, ard, d, n, t):
+    """Materialized route, <= 16 columns: products from the symmetric half of K
+    (5, 12 and 2 blocks of 256 points) against the oracle and against the full
+    stored matrix (MGP_SYM_MATVEC=0), also after a parameter update."""
+    rng = np.random.default_rng(600 + n)
+    X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    ls = rng.uniform(0.6, 1.4, size=d if ard else 1)
+    params = np.concatenate([ls, [1.2]]).astype(np.float32)
+    params2 = np.concatenate([ls * 0.7, [0.8]]).astype(np.float32)
+    print(f"materialized symmetric case kind={kind} d={d} n={n} t={t}", flush=True)
+    monkeypatch.delenv("MGP_SYM_MATVEC", raising=False)
+    p = NativeProvider(kind, ard, X, params, 0.07)
+    try:
+        p.materialize()
+        half = p.forward_matvec(V)
+        monkeypatch.setenv("MGP_SYM_MATVEC", "0")
+        full = p.forward_matvec(V)
+        monkeypatch.delenv("MGP_SYM_MATVEC", raising=False)
+        p.update_params(params2)
+        half2 = p.forward_matvec(V)
+    finally:
+        p.close()
+    ref = ok.forward_matvec(kind, X, V, params, 0.07, ard)
+    ref2 = ok.forward_matvec(kind, X, V, params2, 0.07, ard)
+    e, e_full, e2 = _relerr(half, ref), _relerr(half, full.astype(np.float64)), _relerr(half2, ref2)
+    print(f"  relerr {e:.2e}, vs full {e_full:.2e}, after update {e2:.2e}", flush=True)
+    assert e <= TOL and e2 <= TOL
+    assert e_full <= 2 * TOL
