@@ -531,13 +531,30 @@ __global__ __launch_bounds__(256) void k_dense_sym_reduce(
     }
   const int64_t J = j / kDsRows, jl = j - J * kDsRows;
   const float* col = tp + jl * 16 + 4 * c4;
-  for (int64_t dl = 1; dl <= hmax; ++dl) {
+  // Four partials in flight at a time (every slot is allocated; the formed
+  // ones are kept by a select), in delta order.
+  auto slot = [&](int64_t dl, bool& formed) {
     int64_t bb = J - dl;
     if (bb < 0) bb += nb;
-    const f4 v = *reinterpret_cast<const f4*>(col + (bb * hmax + dl - 1) * (int64_t)kDsRows * 16);
-    const bool formed = dl <= sym_span(bb, nb);
+    formed = dl <= sym_span(bb, nb);
+    return *reinterpret_cast<const f4*>(col + (bb * hmax + dl - 1) * (int64_t)kDsRows * 16);
+  };
+  int64_t dl = 1;
+  for (; dl + 3 <= hmax; dl += 4) {
+    f4 v[4];
+    bool ok[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) tot[e] += formed ? (double)v[e] : 0.0;
+    for (int q = 0; q < 4; ++q) v[q] = slot(dl + q, ok[q]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tot[e] += ok[q] ? (double)v[q][e] : 0.0;
+  }
+  for (; dl <= hmax; ++dl) {
+    bool ok;
+    const f4 v = slot(dl, ok);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tot[e] += ok ? (double)v[e] : 0.0;
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
