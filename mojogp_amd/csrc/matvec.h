@@ -166,6 +166,12 @@ void direct_matvec(const MatvecArgs& a, const PackedPoints& rows,
 void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r0,
                 int64_t nrows, const PackedPoints& cols, int d, float* out, hipStream_t st);
 
+// The symmetric half of the dense K (dense.h layout: nb blocks of 256 points,
+// block index dense_half_index) filled directly from the packed points with
+// the arithmetic of fill_cross, each value scaled by 2^shift and split.
+void fill_dense_half(int kind, float outputscale, const PackedPoints& pts, int d, int shift,
+                     int64_t nb, uint32_t* half, hipStream_t st);
+
 // out[p][c][i] = sum_j dk(x_i, x_j)/dtheta_p V[c][j] for the P engine
 // parameters ([l | l_0..l_{d-1}, os]); pscale_dev[p] converts the per-pair sums
 // (h |dz|^2 terms, k/os terms) into derivatives: 1/(s^2 l_p) for lengthscales

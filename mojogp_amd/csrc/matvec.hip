@@ -1575,6 +1575,81 @@ __global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr
   out[idx] = os * kval<KIND>(r2);
 }
 
+// Symmetric half of the dense K (dense.h layout): one thread per (stored
+// block, row, 8-column group) evaluates os * k(z_row, z_col) for the group's
+// eight columns from per-dimension differences (the arithmetic of
+// k_fill_cross), scales by 2^shift and stores the two-term fp16 split
+// {hi[8], lo[8]}; rows and columns past n are zero.
+constexpr int kHalfRows = 256;
+template <int KIND>
+__global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, int64_t n, int d,
+                                                   float os, int shift, int64_t nb,
+                                                   int64_t nblocks, uint32_t* __restrict__ half) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  constexpr int kGroups = kHalfRows / 8;
+  if (idx >= nblocks * kHalfRows * kGroups) return;
+  const int64_t blk = idx / (kHalfRows * kGroups);
+  const int64_t rem = idx - blk * (kHalfRows * kGroups);
+  const int64_t r = rem / kGroups, g = rem - r * kGroups;
+  // block index -> (b, delta), the inverse of dense_half_index
+  int64_t b, delta;
+  if (nb & 1) {
+    const int64_t w = (nb - 1) / 2 + 1;
+    b = blk / w;
+    delta = blk - b * w;
+  } else {
+    const int64_t h = nb / 2;
+    if (blk < h * (h + 1)) {
+      b = blk / (h + 1);
+      delta = blk - b * (h + 1);
+    } else {
+      const int64_t q = blk - h * (h + 1);
+      b = h + q / h;
+      delta = q - (q / h) * h;
+    }
+  }
+  int64_t J = b + delta;
+  if (J >= nb) J -= nb;
+  const int64_t i = b * kHalfRows + r;
+  const int64_t j0 = J * kHalfRows + 8 * g;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+  if (i < n) {
+    const float* zr = Z + i * d;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t j = j0 + e;
+      if (j < n) {
+        const float* zc = Z + j * d;
+        float r2 = 0.0f;
+        for (int k = 0; k < d; ++k) {
+          const float df = zr[k] - zc[k];
+          r2 = fmaf(df, df, r2);
+        }
+        x[e] = ldexpf(os * kval<KIND>(r2), shift);
+      }
+    }
+  }
+  _Float16 hi[8], lo[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hi[e] = (_Float16)x[e];
+    lo[e] = (_Float16)(x[e] - (float)hi[e]);
+  }
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    w[e] = (uint32_t)__builtin_bit_cast(uint16_t, hi[2 * e]) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, hi[2 * e + 1]) << 16);
+    w[4 + e] = (uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e + 1]) << 16);
+  }
+  uint32_t* dst = half + ((blk * kHalfRows + r) * kGroups + g) * 8;
+  *reinterpret_cast<f4*>(dst) = __builtin_bit_cast(f4, (uint32_t __attribute__((ext_vector_type(4)))){w[0], w[1], w[2], w[3]});
+  *reinterpret_cast<f4*>(dst + 4) = __builtin_bit_cast(f4, (uint32_t __attribute__((ext_vector_type(4)))){w[4], w[5], w[6], w[7]});
+}
+
 // ---------------------------------------------------------------------------
 // Gradient products: out[p][c][i] = sum_j dk(x_i, x_j)/dtheta_p V[c][j] for the
 // engine parameters theta = [l | l_0..l_{d-1}, os] (fused_all_gradients_matvec,
@@ -2140,6 +2215,20 @@ void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r
                                     : k_fill_cross<KIND_MATERN52>;
   hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, rows.z.ptr,
                      r0, nrows, cols.z.ptr, cols.n, d, outputscale, out);
+  MGP_HIP_CHECK(hipGetLastError());
+}
+
+void fill_dense_half(int kind, float outputscale, const PackedPoints& pts, int d, int shift,
+                     int64_t nb, uint32_t* half, hipStream_t st) {
+  MGP_REQUIRE(d >= 1 && pts.n >= 1, "dense fill needs points");
+  const int64_t nblocks = nb * (nb + 1) / 2;
+  const int64_t total = nblocks * kHalfRows * (kHalfRows / 8);
+  auto fn = kind == KIND_RBF        ? k_fill_half<KIND_RBF>
+            : kind == KIND_MATERN12 ? k_fill_half<KIND_MATERN12>
+            : kind == KIND_MATERN32 ? k_fill_half<KIND_MATERN32>
+                                    : k_fill_half<KIND_MATERN52>;
+  hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, pts.z.ptr, pts.n,
+                     d, outputscale, shift, nb, nblocks, half);
   MGP_HIP_CHECK(hipGetLastError());
 }
 

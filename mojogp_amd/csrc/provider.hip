@@ -110,12 +110,17 @@ void Provider::fill_dense() {
   MGP_REQUIRE(std::isfinite(kmax), "kernel diagonal is not finite");
   if (!(kmax > 0.f)) kmax = 1.f;  // K = 0: any scale
   dense_alloc_half(dense, n, kmax);
-  float* tmp = io_c.ensure((size_t)256 * n);
   const int64_t nb = dense.blocks();
-  for (int64_t b = 0; b < nb; ++b) {
-    const int64_t r0 = b * 256, nr = std::min<int64_t>(256, n - r0);
-    if (nr > 0) fill_block(train, r0, nr, tmp);
-    dense_pack_half(tmp, b, std::max<int64_t>(nr, 0), dense, st);
+  if (!is_tree) {
+    // only the stored blocks, evaluated straight into the split storage
+    fill_dense_half(kind, outputscale(), train, d, dense.shift, nb, dense.half.ptr, st);
+  } else {
+    float* tmp = io_c.ensure((size_t)256 * n);
+    for (int64_t b = 0; b < nb; ++b) {
+      const int64_t r0 = b * 256, nr = std::min<int64_t>(256, n - r0);
+      if (nr > 0) fill_block(train, r0, nr, tmp);
+      dense_pack_half(tmp, b, std::max<int64_t>(nr, 0), dense, st);
+    }
   }
   dense.half_valid = true;
   dense.full_valid = false;
