@@ -204,12 +204,33 @@ def _fit_c2_seconds():
     return dt, {"final_nll": tr.nll, "cg_iterations_total": info.get("cg_iterations_total")}
 
 
+def _c4_product_only():
+    """The config-4 16-column dense product alone (profiling): one materialize
+    of K(X, X) (RBF, lengthscale 1.5, outputscale 1, noise 0.01, X ~ U(-2, 2)^4,
+    seed 0), then 3 warm-up and 30 timed products."""
+    from mojogp_amd._provider import NativeProvider, KIND_RBF
+    rng = np.random.default_rng(0)
+    n = 40_000
+    X = rng.uniform(-2, 2, size=(n, 4)).astype(np.float32)
+    prov = NativeProvider(KIND_RBF, False, X, np.array([1.5, 1.0], np.float32), 0.01)
+    try:
+        prov.materialize()
+        V = rng.normal(size=(16, n)).astype(np.float32)
+        t, _, _ = prov.benchmark_forward(V, 30, 3)
+    finally:
+        prov.close()
+    return {"dense_matvec_ms_16_mean": round(float(np.mean(t)), 4),
+            "dense_matvec_ms_16_min": round(float(np.min(t)), 4)}
+
+
 def _c4_materialized():
     """Config 4: RBF (isotropic) N=40k d=4 on the materialized route (dense K as a
-    two-term fp16 split, 6.4 GB), default fit, exact variance at 4096 test
-    points (the generator of tests/test_gpu_configs_at_size.py), and the dense
-    product alone at 16 and 4096 right-hand sides (wall time per call, column
-    maxima + packing + MFMA product + reduction, inputs resident on the device)."""
+    two-term fp16 split: the symmetric half, 3.25 GB, for products of <= 16
+    columns, the full 6.46 GB layout for wider ones), default fit, exact
+    variance at 4096 test points (the generator of
+    tests/test_gpu_configs_at_size.py), and the dense product alone at 16 and
+    4096 right-hand sides (wall time per call, column maxima + packing + MFMA
+    product + reduction, inputs resident on the device)."""
     from mojogp_amd import RBF, SingleOutputGP
     from mojogp_amd._provider import NativeProvider, KIND_RBF
     rng = np.random.default_rng(0)
@@ -231,8 +252,10 @@ def _c4_materialized():
     prov = NativeProvider(KIND_RBF, False, X, params, float(tr.noise))
     try:
         prov.materialize()
-        npad = -(-n // 256) * 256
-        kbytes = 4.0 * npad * npad
+        # The 16-column product reads the stored symmetric half of K: the
+        # diagonal and cyclic-half blocks of 256 points, 4 B per entry.
+        nbk = -(-n // 256)
+        kbytes = 4.0 * 256 * 256 * nbk * (nbk + 1) / 2
         t16, _, _ = prov.benchmark_forward(rng.normal(size=(16, n)).astype(np.float32), 10, 2)
         ms16 = float(np.median(t16))
         tw, _, _ = prov.benchmark_forward(rng.normal(size=(m, n)).astype(np.float32), 3, 1)
@@ -250,6 +273,7 @@ def _c4_materialized():
         "exact_cg_total_iterations": einfo.get("exact_cg_total_iterations"),
         "lengthscale": float(params[0]),
         "dense_matvec_ms_16": round(ms16, 4),
+        "dense_matvec_bytes_16": kbytes,
         "dense_matvec_GBps_16": round(kbytes / (ms16 * 1e-3) / 1e9, 1),
         "dense_matvec_ms_4096": round(msw, 3),
         "dense_matvec_fp32_equiv_tflops_4096": round(flops_w / (msw * 1e-3) / 1e12, 2),
@@ -542,6 +566,8 @@ def main(argv=None) -> int:
     ap.add_argument("--c4-only", action="store_true",
                     help="only the config-4 materialized leg (fit, exact variance, dense "
                          "products)")
+    ap.add_argument("--c4-product", action="store_true",
+                    help="only the config-4 16-column dense product (profiling)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the mBCG-iteration and fit() measurements")
     ap.add_argument("--mbcg-only", action="store_true",
@@ -562,6 +588,9 @@ def main(argv=None) -> int:
 
     if args.c4_only:
         print(json.dumps(_c4_materialized()), flush=True)
+        return 0
+    if args.c4_product:
+        print(json.dumps(_c4_product_only()), flush=True)
         return 0
     if args.mbcg_only:
         X, _, params, noise = _make_inputs()
