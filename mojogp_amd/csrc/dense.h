@@ -7,8 +7,10 @@
 // block products (kernels/jit/jit_prediction.mojo:438-587).
 //
 // Storage: K is held as a scaled two-term fp16 split.  Every entry is scaled
-// by 2^shift (max |K| in [2^14, 2^15), so the reference's e^-20 kernel floor
-// stays a normal fp16 number) and split into hi = RNE16(x), lo = RNE16(x - hi);
+// by 2^shift (max |K| in [2^14, 2^15), so the e^-20 floor of the clamped
+// kernels stays a normal fp16 number; unclamped RBF tails below that fall into
+// fp16's subnormal range with absolute error <= 2^-25 of the scaled value) and
+// split into hi = RNE16(x), lo = RNE16(x - hi);
 // row i keeps groups of 8 consecutive columns as {hi[8], lo[8]} (32 bytes), so
 // the storage is 4 bytes per entry like fp32 and one 32-byte load per lane is
 // a v_mfma_f32_16x16x32_f16 operand of either part.  Rows and columns are

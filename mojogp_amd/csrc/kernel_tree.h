@@ -5,9 +5,12 @@
 // Reference semantics (caspbian/mojogp):
 //   leaf expressions      codegen_engine/expressions.py:77-380 (RBF, Matern
 //                         1/2, 3/2, 5/2, periodic, RQ)
-//   guards                codegen_engine/passes/numerical_stability.py:29-70
-//                         (exp(max(x, -20)) for negative arguments,
-//                         sqrt(max(x, 1e-20)))
+//   guards                codegen_engine/passes/numerical_stability.py:29-85
+//                         (sqrt(max(x, 1e-20)); exp(max(x, -20)) where the
+//                         emitted exponent matches its syntactic test: the
+//                         Matern-3/2 and 5/2 leaves and ARD Matern-1/2 leaves,
+//                         not RBF, isotropic Matern-1/2 or periodic leaves;
+//                         exp2_limit in mgp_common.h)
 //   engine param layout   mojogp/kernel.py:462-640 (leaves in tree order,
 //                         a scale's factor after its subtree)
 //
@@ -154,7 +157,7 @@ __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
     }
     if (!lf.ard) s /= p[lf.p0];
     e.r2 = s;
-    e.k = os * __expf(fmaxf(-2.0f * s, -20.0f));
+    e.k = os * __expf(-2.0f * s);  // not clamped by the reference
     e.h = e.k;
     return e;
   }
@@ -177,13 +180,14 @@ __device__ __forceinline__ LeafEval tree_leaf_eval(const KernelTree& t, int l,
   }
   const float os = p[lf.p0 + nls];
   if (lf.kind == KIND_RBF) {
-    e.k = os * __expf(fmaxf(-0.5f * r2, -20.0f));
+    e.k = os * __expf(-0.5f * r2);  // not clamped by the reference
     e.h = e.k;
     return e;
   }
   const float r = sqrtf(fmaxf(r2 + 1e-20f, 1e-20f));
   if (lf.kind == KIND_MATERN12) {
-    const float ex = __expf(fmaxf(-r, -20.0f));
+    // clamped for ARD leaves only (exp2_limit in mgp_common.h)
+    const float ex = __expf(lf.ard ? fmaxf(-r, -20.0f) : -r);
     e.k = os * ex;
     e.h = os * ex / r;
   } else if (lf.kind == KIND_MATERN32) {
@@ -227,7 +231,7 @@ __device__ __forceinline__ void tree_leaf_chunk(const KernelTree& t, int l,
         s[c] = fmaf(sn * sn, il, s[c]);
       }
     }
-    for (int c = 0; c < kTreeChunk; ++c) out[c] = os * __expf(fmaxf(-2.0f * s[c], -20.0f));
+    for (int c = 0; c < kTreeChunk; ++c) out[c] = os * __expf(-2.0f * s[c]);
     return;
   }
   float r2[kTreeChunk];
@@ -251,13 +255,13 @@ __device__ __forceinline__ void tree_leaf_chunk(const KernelTree& t, int l,
   }
   const float os = p[lf.p0 + nls];
   if (lf.kind == KIND_RBF) {
-    for (int c = 0; c < kTreeChunk; ++c) out[c] = os * __expf(fmaxf(-0.5f * r2[c], -20.0f));
+    for (int c = 0; c < kTreeChunk; ++c) out[c] = os * __expf(-0.5f * r2[c]);
     return;
   }
   for (int c = 0; c < kTreeChunk; ++c) {
     const float r = sqrtf(fmaxf(r2[c] + 1e-20f, 1e-20f));
     if (lf.kind == KIND_MATERN12) {
-      out[c] = os * __expf(fmaxf(-r, -20.0f));
+      out[c] = os * __expf(lf.ard ? fmaxf(-r, -20.0f) : -r);
     } else if (lf.kind == KIND_MATERN32) {
       const float s3 = 1.7320508075688772f * r;
       out[c] = os * (1.0f + s3) * __expf(fmaxf(-s3, -20.0f));

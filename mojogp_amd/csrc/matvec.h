@@ -13,6 +13,9 @@ namespace mgp {
 struct Coords {
   int d = 0;
   DevBuf<float> coef;  // [2*d]: center[d] then scale[d]
+  // Limit on the base-2 exponent of the kernel value, exp2_limit(kind, ard)
+  // (mgp_common.h): where the reference's generated code clamps exp at -20.
+  float exp2_limit = kExp2Clamp;
 };
 
 // Points laid out as v_mfma_f32_16x16x32_f16 operands.
@@ -39,6 +42,7 @@ struct PackedPoints {
   DevBuf<uint32_t> A, B;  // two fp16 per dword
   DevBuf<float> z;     // scaled coordinates, row-major [n][d] (direct path)
   float max_norm = 0.f;      // max_i |z_i|^2 (Gram-form error scale)
+  float exp2_limit = kExp2Clamp;  // the Coords' exponent limit
   DevBuf<uint32_t> max_norm_dev;
 };
 
@@ -72,9 +76,10 @@ inline int split_mfma_count(int d) { return (3 * (d + 2) + 31) / 32; }
 
 // Multiplier applied to (x - center)/lengthscale so that the squared distance
 // of the scaled points feeds exp2 directly:
-//   RBF:       s = 0.5*log2(e)*r^2,  k = os*2^-min(s, 20 log2 e)
+//   RBF:       s = 0.5*log2(e)*r^2,  k = os*2^-s  (not clamped)
 //   Matern52:  s = 5*log2(e)^2*r^2,   u = sqrt(s) = sqrt(5) r log2(e)
-//   Matern12:  u = sqrt(s) = r log2(e),  k = os*2^-min(u, 20 log2 e)
+//   Matern12:  u = sqrt(s) = r log2(e),  k = os*2^-min(u, lim)  (lim: 20 log2 e
+//              for ARD kernels, none for isotropic ones; exp2_limit)
 //   Matern32:  u = sqrt(3) r log2(e),   k = os*(1 + u ln2)*2^-min(u, 20 log2 e)
 inline float kernel_scale(int kind) {
   switch (kind) {

@@ -49,15 +49,17 @@ __device__ __forceinline__ float clamp_reg() {
 }
 
 // Kernel value from the scaled squared distance s (see kernel_scale()).
-// clampv = kExp2Clamp (from clamp_reg() in hot loops).
+// clampv = the exponent limit exp2_limit(kind, ard) (kExp2Clamp, from
+// clamp_reg() in hot loops, for the Matern-3/2 and 5/2 kernels; the point
+// set's exp2_limit for Matern-1/2; RBF has none).
 template <int KIND>
 __device__ __forceinline__ float kval(float s, float clampv = kExp2Clamp) {
   if constexpr (KIND == KIND_RBF) {
-    // os * exp(max(-0.5 r^2, -20)) = os * 2^-clamp(s, 0, 20 log2 e)
-    const float t = __builtin_amdgcn_fmed3f(s, 0.0f, kExp2Clamp);
-    return __builtin_amdgcn_exp2f(-t);
+    // os * exp(-0.5 r^2) = os * 2^-max(s, 0) (the max only absorbs Gram-form
+    // rounding below zero; the reference does not clamp the RBF exponent)
+    return __builtin_amdgcn_exp2f(-fmaxf(s, 0.0f));
   } else if constexpr (KIND == KIND_MATERN12) {
-    // os * exp(max(-r, -20)),  u = r log2 e
+    // os * exp(-r) (isotropic) or os * exp(max(-r, -20)) (ARD),  u = r log2 e
     const float u = __builtin_amdgcn_sqrtf(fabsf(s));
     return __builtin_amdgcn_exp2f(-fminf(u, clampv));
   } else if constexpr (KIND == KIND_MATERN32) {
@@ -158,9 +160,13 @@ __global__ void k_pack_points(const float* __restrict__ X, int64_t n, int d,
 // ---------------------------------------------------------------------------
 // Right-hand sides for the fp16 product O^T += V^T P^T
 //
-// P is formed as P' = 2^kPScaleLog2 * k / os in [2^-13.9, 2^15] (the reference
-// clamp keeps k/os >= e^-20), so P' is a normal fp16 number and its two-term
-// split P' = Ph + Pl (both round-to-nearest fp16) carries 22+ significant bits.
+// P is formed as P' = 2^kPScaleLog2 * k / os <= 2^15.  Where the kernel's
+// exponent is clamped (Matern-3/2 and 5/2: k/os >= e^-20) P' >= 2^-13.9 is a
+// normal fp16 number and its two-term split P' = Ph + Pl (both
+// round-to-nearest fp16) carries 22+ significant bits.  The RBF exponent is
+// not clamped: values with P' below 2^-14 (k/os < 2^-29) lose relative
+// precision in the subnormal range, but their absolute error stays below
+// 2^-25 in P', i.e. 2^-40 os per pair.
 // Each column of V is scaled by 2^shift_c so max|V'_c| lies in [2^14, 2^15) and
 // split the same way.  Ph.Vh + Ph.Vl + Pl.Vh then reproduces P.V to ~2^-23
 // relative; the dropped Pl.Vl term is below 2^-24.  The result is unscaled
@@ -277,7 +283,8 @@ __device__ __forceinline__ void kval_scaled(float s, float clampv, float one, fl
                                             float& g) {
   constexpr float P = (float)(1 << kPScaleLog2);
   if constexpr (KIND == KIND_RBF) {
-    const float t = __builtin_amdgcn_fmed3f(s, 0.0f, clampv);
+    (void)clampv;  // the RBF exponent is not clamped
+    const float t = fmaxf(s, 0.0f);
     f = __builtin_amdgcn_exp2f((float)kPScaleLog2 - t);
     g = one;
   } else if constexpr (KIND == KIND_MATERN32) {
@@ -1145,7 +1152,8 @@ __global__ void k_pack_grad_zz(const float* __restrict__ Z, int64_t n, int d, in
 template <int KIND>
 __device__ __forceinline__ void grad_factors(float s, float clampv, float& kv, float& h) {
   if constexpr (KIND == KIND_RBF) {
-    kv = __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(s, 0.0f, clampv));
+    (void)clampv;  // the RBF exponent is not clamped
+    kv = __builtin_amdgcn_exp2f(-fmaxf(s, 0.0f));
     h = kv;
   } else if constexpr (KIND == KIND_MATERN32) {
     const float u = __builtin_amdgcn_sqrtf(fabsf(s));
@@ -1516,7 +1524,7 @@ template <int KIND>
 __global__ __launch_bounds__(256) void k_direct(
     const float* __restrict__ Zr, int64_t m, const float* __restrict__ Zc,
     int64_t n, int d, const float* __restrict__ V, int ncols, float os,
-    float noise, int add_noise, float* __restrict__ out) {
+    float noise, int add_noise, float lim, float* __restrict__ out) {
   extern __shared__ float sm[];  // [kDirectTile][d + ncols]
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int w = d + ncols;
@@ -1542,7 +1550,7 @@ __global__ __launch_bounds__(256) void k_direct(
         const float df = xi[k] - row[k];
         r2 = fmaf(df, df, r2);
       }
-      const float kv = kval<KIND>(r2);
+      const float kv = kval<KIND>(r2, lim);
       for (int c = 0; c < ncols; ++c) acc[c] += (double)(kv * row[d + c]);
     }
   }
@@ -1560,7 +1568,7 @@ __global__ __launch_bounds__(256) void k_direct(
 template <int KIND>
 __global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr, int64_t r0,
                                                     int64_t rows, const float* __restrict__ Zc,
-                                                    int64_t n, int d, float os,
+                                                    int64_t n, int d, float os, float lim,
                                                     float* __restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= rows * n) return;
@@ -1572,7 +1580,7 @@ __global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr
     const float df = zr[k] - zc[k];
     r2 = fmaf(df, df, r2);
   }
-  out[idx] = os * kval<KIND>(r2);
+  out[idx] = os * kval<KIND>(r2, lim);
 }
 
 // Symmetric half of the dense K (dense.h layout): one thread per (stored
@@ -1583,7 +1591,7 @@ __global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr
 constexpr int kHalfRows = 256;
 template <int KIND>
 __global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, int64_t n, int d,
-                                                   float os, int shift, int64_t nb,
+                                                   float os, float lim, int shift, int64_t nb,
                                                    int64_t nblocks, uint32_t* __restrict__ half) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   constexpr int kGroups = kHalfRows / 8;
@@ -1627,7 +1635,7 @@ __global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, 
           const float df = zr[k] - zc[k];
           r2 = fmaf(df, df, r2);
         }
-        x[e] = ldexpf(os * kval<KIND>(r2), shift);
+        x[e] = ldexpf(os * kval<KIND>(r2, lim), shift);
       }
     }
   }
@@ -1668,7 +1676,7 @@ constexpr int kGradMaxDim = 32;
 template <int KIND, bool ARD>
 __global__ __launch_bounds__(256) void k_grad_matvec(
     const float* __restrict__ Z, int64_t n, int d, const float* __restrict__ V, int ncols,
-    int c0, float os, const float* __restrict__ pscale, float* __restrict__ out) {
+    int c0, float os, float lim, const float* __restrict__ pscale, float* __restrict__ out) {
   extern __shared__ float sm[];  // [kGradTile][d + kGradCols]
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int w = d + kGradCols;
@@ -1708,7 +1716,7 @@ __global__ __launch_bounds__(256) void k_grad_matvec(
         dz2[k] = df * df;
         S += dz2[k];
       }
-      const float kv = kval<KIND>(S);  // k / os
+      const float kv = kval<KIND>(S, lim);  // k / os
       float h;
       if constexpr (KIND == KIND_RBF) {
         h = kv;
@@ -1789,6 +1797,7 @@ void pack_points(const float* X_dev, int64_t n, const Coords& co,
   const int d = co.d;
   MGP_REQUIRE(d >= 1, "dimension must be >= 1");
   pp.n = n;
+  pp.exp2_limit = co.exp2_limit;
   // Even tile count: the tile kernel walks column tiles in pairs.
   pp.ntiles = 2 * ceil_div(std::max<int64_t>(n, 1), 32);
   pp.ntiles_alloc = round_up(pp.ntiles, kPackTileAlign);
@@ -2199,7 +2208,7 @@ void direct_matvec(const MatvecArgs& a, const PackedPoints& rows,
                                         : k_direct<KIND_MATERN52>;
     hipLaunchKernelGGL(fn, grid, dim3(256), shm, st, rows.z.ptr, a.m, cols.z.ptr,
                        a.n, d, V_dev + (int64_t)c0 * a.n, nc, a.outputscale,
-                       a.noise, a.square ? 1 : 0, out_dev + (int64_t)c0 * a.m);
+                       a.noise, a.square ? 1 : 0, cols.exp2_limit, out_dev + (int64_t)c0 * a.m);
     MGP_HIP_CHECK(hipGetLastError());
   }
 }
@@ -2214,7 +2223,7 @@ void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r
             : kind == KIND_MATERN32 ? k_fill_cross<KIND_MATERN32>
                                     : k_fill_cross<KIND_MATERN52>;
   hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, rows.z.ptr,
-                     r0, nrows, cols.z.ptr, cols.n, d, outputscale, out);
+                     r0, nrows, cols.z.ptr, cols.n, d, outputscale, cols.exp2_limit, out);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -2228,7 +2237,7 @@ void fill_dense_half(int kind, float outputscale, const PackedPoints& pts, int d
             : kind == KIND_MATERN32 ? k_fill_half<KIND_MATERN32>
                                     : k_fill_half<KIND_MATERN52>;
   hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, pts.z.ptr, pts.n,
-                     d, outputscale, shift, nb, nblocks, half);
+                     d, outputscale, pts.exp2_limit, shift, nb, nblocks, half);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -2240,8 +2249,8 @@ void gradient_matvec(int kind, bool ard, const PackedPoints& pts, int d, float o
   const int64_t n = pts.n;
   const size_t shm = (size_t)kGradTile * (d + kGradCols) * sizeof(float);
   const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256));
-  using Fn = void (*)(const float*, int64_t, int, const float*, int, int, float, const float*,
-                      float*);
+  using Fn = void (*)(const float*, int64_t, int, const float*, int, int, float, float,
+                      const float*, float*);
   Fn fn;
   if (kind == KIND_RBF) fn = ard ? k_grad_matvec<KIND_RBF, true> : k_grad_matvec<KIND_RBF, false>;
   else if (kind == KIND_MATERN12)
@@ -2251,7 +2260,7 @@ void gradient_matvec(int kind, bool ard, const PackedPoints& pts, int d, float o
   else fn = ard ? k_grad_matvec<KIND_MATERN52, true> : k_grad_matvec<KIND_MATERN52, false>;
   for (int c0 = 0; c0 < ncols; c0 += kGradCols) {
     hipLaunchKernelGGL(fn, grid, dim3(256), shm, st, pts.z.ptr, n, d, V_dev, ncols, c0,
-                       outputscale, pscale_dev, out_dev);
+                       outputscale, pts.exp2_limit, pscale_dev, out_dev);
     MGP_HIP_CHECK(hipGetLastError());
   }
 }

@@ -25,6 +25,27 @@ constexpr float kLog2e = 1.44269504088896340736f;
 // exp(max(x, -20)) clamp of the reference's numerical-stability pass, expressed
 // in base 2: 20 * log2(e).
 constexpr float kExp2Clamp = 20.0f * 1.44269504088896340736f;
+// Exponent limit standing for "no clamp" (exp2 of anything beyond it is 0).
+constexpr float kExp2NoClamp = 3.0e38f;
+
+// Where the reference's generated code clamps a leaf's exponent.  Its
+// numerical-stability pass rewrites exp(x) as exp(max(x, -20)) only when x is
+// syntactically a negative constant, a product with a negative constant as a
+// direct operand, or c - y with c <= 0 (passes/numerical_stability.py:29-41,
+// 62-85), after products were left-nested (ir.py:183-190) and CSE ran.  The
+// emitted expressions (recorded per kind, iso/ARD and d in
+// tests/golden/ref_kernel_exprs.json) therefore clamp
+//   Matern-3/2, Matern-5/2 (iso and ARD):  exp(max(-1 * u, -20)),
+//   Matern-1/2 ARD:                         exp(max(-1 * r, -20)),
+// and leave unclamped
+//   RBF (iso: exp((-0.5 dist_sq) inv_l^2); ARD: exp(sum of per-dimension terms)),
+//   Matern-1/2 isotropic (exp((-1 r_raw) inv_l)), periodic leaves.
+// The limit on the base-2 exponent (u or s) of one leaf:
+inline float exp2_limit(int kind, bool ard) {
+  if (kind == KIND_RBF) return kExp2NoClamp;
+  if (kind == KIND_MATERN12 && !ard) return kExp2NoClamp;
+  return kExp2Clamp;
+}
 // The reference's r = sqrt(r^2 + 1e-20) floor of the Matern-1/2 distance in
 // the base-2 scaled coordinates (log2(e)^2 * 1e-20); only the gradient weight
 // 1/r needs it.

@@ -36,6 +36,7 @@ void Provider::refresh_coords() {
     coef[d + k] = base / ls;
   }
   co.d = d;
+  co.exp2_limit = exp2_limit(kind, ard);
   co.coef.ensure(coef.size());
   MGP_HIP_CHECK(hipMemcpyAsync(co.coef.ptr, coef.data(), coef.size() * sizeof(float),
                                hipMemcpyHostToDevice, st));

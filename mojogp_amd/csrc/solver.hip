@@ -414,10 +414,13 @@ __global__ void k_pc_setpivot(PivotDev* __restrict__ state, float* __restrict__ 
 
 // Pivot-column kernel values: radial kinds read scaled coordinates (z rows);
 // kernel trees read raw coordinates.
+// lim = the exponent limit exp2_limit(kind, ard) (used by Matern-1/2; the
+// RBF exponent is never clamped, the Matern-3/2 and 5/2 ones always).
 template <int KIND>
 struct RadialColumn {
   float os;
   int d;
+  float lim;
   __device__ float operator()(const float* __restrict__ zi, const float* zp) const {
     float r2 = 0.0f;
     for (int k = 0; k < d; ++k) {
@@ -425,10 +428,10 @@ struct RadialColumn {
       r2 = fmaf(df, df, r2);
     }
     if constexpr (KIND == KIND_RBF) {
-      return os * __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
+      return os * __builtin_amdgcn_exp2f(-fmaxf(r2, 0.0f));
     } else if constexpr (KIND == KIND_MATERN12) {
       const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
-      return os * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+      return os * __builtin_amdgcn_exp2f(-fminf(u, lim));
     } else if constexpr (KIND == KIND_MATERN32) {
       const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
       return os * fmaf(u, kLn2, 1.0f) * __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
@@ -1143,12 +1146,13 @@ __global__ __launch_bounds__(256) void k_grad_trace(
       }
       float kv, h;
       if constexpr (KIND == KIND_RBF) {
-        kv = __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(r2, 0.0f, kExp2Clamp));
+        kv = __builtin_amdgcn_exp2f(-fmaxf(r2, 0.0f));  // not clamped
         h = kv;
       } else if constexpr (KIND == KIND_MATERN12) {
-        // h = log2(e) k / r with the reference's floored r = sqrt(r^2 + 1e-20)
+        // h = log2(e) k / r with the reference's floored r = sqrt(r^2 + 1e-20);
+        // the exponent is clamped for ARD only (exp2_limit)
         const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
-        kv = __builtin_amdgcn_exp2f(-fminf(u, kExp2Clamp));
+        kv = __builtin_amdgcn_exp2f(ARD ? -fminf(u, kExp2Clamp) : -u);
         h = kLog2e * kv / __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f) + kM12RFloor);
       } else if constexpr (KIND == KIND_MATERN32) {
         const float u = __builtin_amdgcn_sqrtf(fmaxf(r2, 0.0f));
@@ -1553,10 +1557,10 @@ void dispatch_column(Provider& pv, F&& launch) {
   const int d = pv.d;
   const float osk = pv.outputscale();
   if (pv.is_tree) launch(TreeColumn{pv.tree, pv.tparams.ptr});
-  else if (pv.kind == KIND_RBF) launch(RadialColumn<KIND_RBF>{osk, d});
-  else if (pv.kind == KIND_MATERN12) launch(RadialColumn<KIND_MATERN12>{osk, d});
-  else if (pv.kind == KIND_MATERN32) launch(RadialColumn<KIND_MATERN32>{osk, d});
-  else launch(RadialColumn<KIND_MATERN52>{osk, d});
+  else if (pv.kind == KIND_RBF) launch(RadialColumn<KIND_RBF>{osk, d, pv.train.exp2_limit});
+  else if (pv.kind == KIND_MATERN12) launch(RadialColumn<KIND_MATERN12>{osk, d, pv.train.exp2_limit});
+  else if (pv.kind == KIND_MATERN32) launch(RadialColumn<KIND_MATERN32>{osk, d, pv.train.exp2_limit});
+  else launch(RadialColumn<KIND_MATERN52>{osk, d, pv.train.exp2_limit});
 }
 }  // namespace
 

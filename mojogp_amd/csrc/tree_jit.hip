@@ -95,8 +95,7 @@ void emit_tree(const KernelTree& t, std::string& pro, std::string& pair) {
         Q << "  { const float sn = __sinf((xi[" << dim(q) << "] - xj[" << dim(q) << "]) * " << L
           << "ip); " << L << "s = fmaf(sn * sn, " << L << "il" << (lf.ard ? q : 0) << ", " << L
           << "s); }\n";
-      Q << "  const float " << L << " = " << L << "os * __expf(fmaxf(-2.0f * " << L
-        << "s, -20.0f));\n";
+      Q << "  const float " << L << " = " << L << "os * __expf(-2.0f * " << L << "s);\n";
       continue;
     }
     Q << "  float " << L << "r2 = 0.0f;\n";
@@ -113,14 +112,17 @@ void emit_tree(const KernelTree& t, std::string& pro, std::string& pair) {
     }
     P << "  const float " << L << "os = p[" << lf.p0 + nls << "];\n";
     if (lf.kind == KIND_RBF) {
-      Q << "  const float " << L << " = " << L << "os * __expf(fmaxf(-0.5f * " << L
-        << "r2, -20.0f));\n";
+      Q << "  const float " << L << " = " << L << "os * __expf(-0.5f * " << L << "r2);\n";
       continue;
     }
     Q << "  const float " << L << "r = sqrtf(fmaxf(" << L << "r2 + 1e-20f, 1e-20f));\n";
     if (lf.kind == KIND_MATERN12) {
-      Q << "  const float " << L << " = " << L << "os * __expf(fmaxf(-" << L
-        << "r, -20.0f));\n";
+      // the -20 clamp applies to ARD Matern-1/2 leaves only (exp2_limit)
+      if (lf.ard)
+        Q << "  const float " << L << " = " << L << "os * __expf(fmaxf(-" << L
+          << "r, -20.0f));\n";
+      else
+        Q << "  const float " << L << " = " << L << "os * __expf(-" << L << "r);\n";
     } else if (lf.kind == KIND_MATERN32) {
       Q << "  const float " << L << "s3 = 1.7320508075688772f * " << L << "r;\n"
         << "  const float " << L << " = " << L << "os * (1.0f + " << L << "s3) * __expf(fmaxf(-"

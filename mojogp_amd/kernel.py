@@ -505,7 +505,10 @@ class KernelNode:
 
         Leaves follow the engine's expressions (codegen_engine/expressions.py:
         77-326): periodic divides the summed sin^2 terms by the lengthscale
-        (not its square) on raw differences, RQ uses (1 + r^2 / (2 alpha))^-alpha."""
+        (not its square) on raw differences, RQ uses (1 + r^2 / (2 alpha))^-alpha,
+        and exp is clamped at -20 where the engine's generated code clamps it
+        (Matern-3/2, Matern-5/2 and ARD Matern-1/2 leaves; not RBF, isotropic
+        Matern-1/2 or periodic leaves, passes/numerical_stability.py:62-85)."""
         X = np.atleast_2d(np.asarray(X, dtype=np.float64))
         X2 = X if X2 is None else np.atleast_2d(np.asarray(X2, dtype=np.float64))
         p = np.ones(self.num_params()) if params is None else np.asarray(params, np.float64)
@@ -558,17 +561,17 @@ def _leaf_matrix(node: KernelNode, X, X2, p) -> np.ndarray:
         period, os = p[nls], p[nls + 1]
         s2 = np.sin(np.pi * diff / period) ** 2
         S = (s2 / ls).sum(-1) if nls > 1 else s2.sum(-1) / ls[0]
-        return os * np.exp(np.maximum(-2.0 * S, -20.0))
+        return os * np.exp(-2.0 * S)
     r2 = ((diff / ls) ** 2).sum(-1)
     if kt == KernelType.RQ:
         alpha, os = p[nls], p[nls + 1]
         return os * (1.0 + r2 / (2.0 * alpha)) ** (-alpha)
     os = p[nls]
     if kt == KernelType.RBF:
-        return os * np.exp(np.maximum(-0.5 * r2, -20.0))
+        return os * np.exp(-0.5 * r2)
     r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
     if kt == KernelType.MATERN12:
-        return os * np.exp(np.maximum(-r, -20.0))
+        return os * np.exp(np.maximum(-r, -20.0) if node.ard_dim is not None else -r)
     if kt == KernelType.MATERN32:
         return os * (1 + np.sqrt(3.0) * r) * np.exp(np.maximum(-np.sqrt(3.0) * r, -20.0))
     return os * (1 + np.sqrt(5.0) * r + 5.0 / 3.0 * r2) * np.exp(np.maximum(-np.sqrt(5.0) * r, -20.0))

@@ -5,8 +5,10 @@
  * Follows caspbian/mojogp mojogp/codegen_engine/emit/gpu_kernel.py:151-260:
  * one output row i at a time, for every column j the kernel value is formed
  * from per-dimension differences (diff_d / l_d), guarded as in
- * codegen_engine/passes/numerical_stability.py:29-41 (exp(max(x,-20)),
- * sqrt(max(x,1e-20)), Matern r carrying +1e-20, expressions.py:197-240), and
+ * codegen_engine/passes/numerical_stability.py:29-41,62-85 (sqrt(max(x,1e-20)),
+ * Matern r carrying +1e-20, expressions.py:197-240; exp(max(x,-20)) for the
+ * Matern-5/2 exponent, no clamp on the RBF exponent, as the reference's
+ * generated code has them), and
  * accumulated in fp32 as acc[c] += k * v[c*n + j]; the row is written as
  * out[c*n + i] = acc[c] + noise * v[c*n + i].  Rows are spread over OpenMP
  * threads; the arithmetic per row is the reference's sequential order.
@@ -22,11 +24,7 @@
 #define MAX_COLS 64
 
 static inline float kval(int kind, float r2, float os) {
-  if (kind == 0) {
-    float a = -0.5f * r2;
-    if (a < -20.0f) a = -20.0f;
-    return os * expf(a);
-  }
+  if (kind == 0) return os * expf(-0.5f * r2);  /* RBF: not clamped */
   float x = r2 + 1e-20f;
   if (x < 1e-20f) x = 1e-20f;
   const float r = sqrtf(x);

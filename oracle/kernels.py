@@ -1,22 +1,31 @@
 """float64 restatement of the reference kernel arithmetic (test infrastructure).
 
 Reference semantics (caspbian/mojogp):
-  * RBF       k = os * exp(max(-0.5 * sum_d (diff_d / l_d)^2, -20))
+  * RBF       k = os * exp(-0.5 * sum_d (diff_d / l_d)^2)
   * Matern52  k = os * (1 + sqrt5 r + 5/3 r^2) * exp(max(-sqrt5 r, -20)),
               r = sqrt(max(sum_d (diff_d / l_d)^2 + 1e-20, 1e-20))
-  * Matern12  k = os * exp(max(-r, -20))
+  * Matern12  k = os * exp(-r) (isotropic), os * exp(max(-r, -20)) (ARD)
   * Matern32  k = os * (1 + sqrt3 r) * exp(max(-sqrt3 r, -20))
     (codegen_engine/expressions.py:77-240: forward expressions;
-     codegen_engine/passes/numerical_stability.py:29-41: exp clamp at -20 for
-     syntactically negative arguments and sqrt(max(x, 1e-20)))
+     codegen_engine/passes/numerical_stability.py:29-41,62-85: sqrt(max(x,
+     1e-20)), and exp(max(x, -20)) only where the post-pass exponent is
+     syntactically negative -- a negative constant, a product with a negative
+     constant as a direct operand, or c - y with c <= 0.  After from_sympy's
+     left-nested products (ir.py:183-190) and CSE that holds for the Matern-3/2
+     and 5/2 exponents (exp(max(-1 * u, -20))) and the ARD Matern-1/2 one, and
+     not for RBF (iso: exp((-0.5 dist_sq) inv_l^2); ARD: a sum of terms), the
+     isotropic Matern-1/2 (exp((-1 r_raw) inv_l)) or periodic leaves.)
   * isotropic kernels use a single lengthscale (params [ls, os]); ARD kernels
     use params [ls_0..ls_{d-1}, os] (kernel.py:324-365, 494-509).
   * forward product: out[c, i] = sum_j k(x_i, x_j) V[c, j] + noise V[c, i]
     (codegen_engine/emit/gpu_kernel.py:151-260).
 
-Pinned by tests/test_oracle_kernels.py: scikit-learn RBF / Matern(nu=0.5,
-1.5, 2.5) kernels (unclamped region), the clamp special cases (exact os*e^-20 tails, k(x,
-x) = os), SymPy derivatives and central finite differences of the gradients.
+Pinned by tests/test_oracle_kernels.py: the values and gradients of the
+reference's own post-pass expressions at pairs on both sides of the -20 clamp
+(tests/golden/ref_kernel_exprs.npz, written by tests/golden/gen_kernel_exprs.py
+from the reference's code generator), scikit-learn RBF / Matern(nu=0.5, 1.5,
+2.5) kernels, SymPy derivatives and central finite differences of the
+gradients.
 """
 
 from __future__ import annotations
@@ -51,16 +60,36 @@ def sq_dist(X1: np.ndarray, X2: np.ndarray, ls: np.ndarray) -> np.ndarray:
     return out
 
 
-def kernel_from_sq(kind: int, r2: np.ndarray, os: float) -> np.ndarray:
-    """Kernel value from the scaled squared distance, with the reference guards."""
+def exp_clamped(kind: int, ard: bool) -> bool:
+    """Whether the reference's generated code clamps this kernel's exponent at
+    -20 (see the module docstring; recorded per kind, iso/ARD and dimension in
+    tests/golden/ref_kernel_exprs.json)."""
     if kind == RBF:
-        return os * np.exp(np.maximum(-0.5 * r2, -20.0))
+        return False
+    if kind == MATERN12:
+        return bool(ard)
+    return True
+
+
+def _exp_guard(x: np.ndarray, clamp: bool) -> np.ndarray:
+    """exp(max(x, -20)) where the reference clamps, exp(x) where it does not."""
+    with np.errstate(under="ignore"):
+        return np.exp(np.maximum(x, -20.0) if clamp else x)
+
+
+def kernel_from_sq(kind: int, r2: np.ndarray, os: float, ard: bool = True) -> np.ndarray:
+    """Kernel value from the scaled squared distance, with the reference guards
+    (``ard`` matters for Matern-1/2 only: its exponent is clamped for ARD
+    kernels and not for isotropic ones)."""
+    clamp = exp_clamped(kind, ard)
+    if kind == RBF:
+        return os * _exp_guard(-0.5 * r2, clamp)
     r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
     if kind == MATERN12:
-        return os * np.exp(np.maximum(-r, -20.0))
+        return os * _exp_guard(-r, clamp)
     if kind == MATERN32:
-        return os * (1.0 + _SQRT3 * r) * np.exp(np.maximum(-_SQRT3 * r, -20.0))
-    return os * (1.0 + _SQRT5 * r + (5.0 / 3.0) * r * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
+        return os * (1.0 + _SQRT3 * r) * _exp_guard(-_SQRT3 * r, clamp)
+    return os * (1.0 + _SQRT5 * r + (5.0 / 3.0) * r * r) * _exp_guard(-_SQRT5 * r, clamp)
 
 
 def kernel_matrix(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
@@ -72,7 +101,7 @@ def kernel_matrix(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
     d = X1.shape[1]
     ls = _lengthscales(params, d, ard)
     os = float(np.asarray(params, dtype=np.float64)[-1])
-    return kernel_from_sq(kind, sq_dist(X1, X2, ls), os)
+    return kernel_from_sq(kind, sq_dist(X1, X2, ls), os, ard)
 
 
 def forward_matvec(kind: int, X, V, params, noise: float, ard: bool,
@@ -108,13 +137,16 @@ def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
     """dK/dtheta_p for every engine parameter p, shape (P, n1, n2), float64.
 
     The reference differentiates the unclamped forward expression with SymPy and
-    then applies the same exp clamp to the result (numerical_stability pass runs
-    on gradients too, passes/numerical_stability.py:92-112); for Matern the r
-    in d/dl cancels analytically (overrides.py:24-41).
-      RBF:      dk/dl_d = k_clamped * diff_d^2 / l_d^3
+    then applies the same exp guard to the result (numerical_stability pass runs
+    on gradients too, passes/numerical_stability.py:92-112; after CSE the
+    gradients share the forward's exp let, so they are clamped exactly where
+    the forward is); for Matern the r in d/dl cancels analytically
+    (overrides.py:24-41).
+      RBF:      dk/dl_d = k * diff_d^2 / l_d^3
       Matern52: dk/dl_d = (5/3) os (1 + sqrt5 r) exp(max(-sqrt5 r, -20)) diff_d^2 / l_d^3
       Matern32: dk/dl_d = 3 os exp(max(-sqrt3 r, -20)) diff_d^2 / l_d^3
-      Matern12: dk/dl_d = os exp(max(-r, -20)) / r diff_d^2 / l_d^3 (r floored as above)
+      Matern12: dk/dl_d = os exp(-r) / r diff_d^2 / l_d^3 (r floored as above;
+                exp(max(-r, -20)) for ARD)
       all:      dk/dos  = k / os
     Isotropic: dk/dl = sum_d of the per-dimension terms with l_d = l.
     """
@@ -128,16 +160,8 @@ def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
     os = p[-1]
     diff2 = (X1[:, None, :] - X2[None, :, :]) ** 2          # raw differences
     r2 = np.einsum("ijk,k->ij", diff2, 1.0 / ls**2)
-    k = kernel_from_sq(kind, r2, os)
-    r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
-    if kind == RBF:
-        h = k
-    elif kind == MATERN12:
-        h = os * np.exp(np.maximum(-r, -20.0)) / r
-    elif kind == MATERN32:
-        h = 3.0 * os * np.exp(np.maximum(-_SQRT3 * r, -20.0))
-    else:
-        h = (5.0 / 3.0) * os * (1.0 + _SQRT5 * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
+    k = kernel_from_sq(kind, r2, os, ard)
+    h = _grad_factor(kind, r2, os, ard, k)
     terms = diff2 / ls**3                                    # (n1, n2, d)
     if ard:
         g = [h * terms[:, :, q] for q in range(d)]
@@ -145,6 +169,19 @@ def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
         g = [h * terms.sum(axis=2)]
     g.append(k / os)
     return np.stack(g, axis=0)
+
+
+def _grad_factor(kind: int, r2: np.ndarray, os: float, ard: bool, k: np.ndarray) -> np.ndarray:
+    """h with dk/dl_q = h diff_q^2 / l_q^3 (radial kinds; see kernel_gradients)."""
+    if kind == RBF:
+        return k
+    r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
+    clamp = exp_clamped(kind, ard)
+    if kind == MATERN12:
+        return os * _exp_guard(-r, clamp) / r
+    if kind == MATERN32:
+        return 3.0 * os * _exp_guard(-_SQRT3 * r, clamp)
+    return (5.0 / 3.0) * os * (1.0 + _SQRT5 * r) * _exp_guard(-_SQRT5 * r, clamp)
 
 
 def gradient_matvec(kind: int, X, V, params, ard: bool) -> np.ndarray:
@@ -163,7 +200,7 @@ def gradient_matvec(kind: int, X, V, params, ard: bool) -> np.ndarray:
 # the parameter vector, kernel.py:528-568) with the leaf expressions of the
 # engine (codegen_engine/expressions.py:77-326):
 #   RQ        k = os (1 + r^2 / (2 alpha))^-alpha, r^2 = sum_q (dx_q / l_q)^2
-#   Periodic  k = os exp(max(-2 S, -20)), S = sum_q sin^2(pi dx_q / period) / l_q
+#   Periodic  k = os exp(-2 S), S = sum_q sin^2(pi dx_q / period) / l_q (no clamp)
 #             (isotropic: sum_q sin^2(pi dx_q / period) / l)
 # and the radial leaves as above.  Pinned by tests/test_oracle_tree.py:
 # scikit-learn RBF / Matern / RationalQuadratic / ExpSineSquared leaves,
@@ -340,7 +377,7 @@ def _tree_leaf(nd, X1, X2, p, grads):
         ang = np.pi * diff / period
         s2 = np.sin(ang) ** 2
         S = (s2 / ls).sum(-1)
-        k = os * np.exp(np.maximum(-2.0 * S, -20.0))
+        k = os * _exp_guard(-2.0 * S, False)   # periodic: never clamped
         if not grads:
             return k, None
         G = ([2.0 * k * s2[:, :, j] / ls[j] ** 2 for j in range(q)] if ard
@@ -359,16 +396,8 @@ def _tree_leaf(nd, X1, X2, p, grads):
     else:
         kind = _RADIAL_NAMES[kt]
         os = p[nls]
-        k = kernel_from_sq(kind, r2, os)
-        r = np.sqrt(np.maximum(r2 + 1e-20, 1e-20))
-        if kind == RBF:
-            h = k
-        elif kind == MATERN12:
-            h = os * np.exp(np.maximum(-r, -20.0)) / r
-        elif kind == MATERN32:
-            h = 3.0 * os * np.exp(np.maximum(-_SQRT3 * r, -20.0))
-        else:
-            h = (5.0 / 3.0) * os * (1.0 + _SQRT5 * r) * np.exp(np.maximum(-_SQRT5 * r, -20.0))
+        k = kernel_from_sq(kind, r2, os, ard)
+        h = _grad_factor(kind, r2, os, ard, k)
         extra = []
     if not grads:
         return k, None

@@ -1,6 +1,10 @@
 """Pins the float64 kernel oracle (oracle/kernels.py) against independent facts:
-scikit-learn kernels, the reference's clamp guards, SymPy derivatives and finite
-differences.  CPU only."""
+the reference's own emitted kernel expressions (where the -20 exp clamp lands,
+values and gradients on both sides of it), scikit-learn kernels, SymPy
+derivatives and finite differences.  CPU only."""
+
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -30,22 +34,106 @@ def test_matches_sklearn_in_unclamped_region(kind, ard, rng):
     np.testing.assert_allclose(K, sk, rtol=1e-10, atol=1e-13)
 
 
-def test_rbf_clamp_tail_is_exact_e_minus_20():
-    # 0.5 r^2 = 50 > 20: the reference clamps the exponent to -20.
-    X1 = np.zeros((1, 2))
-    X2 = np.array([[10.0, 0.0]])
-    K = ok.kernel_matrix(ok.RBF, X1, X2, [1.0, 2.5], False)
-    assert K[0, 0] == pytest.approx(2.5 * np.exp(-20.0), rel=1e-14)
+# ---------------------------------------------------------------------------
+# The reference's own post-pass expressions (tests/golden/gen_kernel_exprs.py
+# ran its code generator: KernelExprBuilder -> gradients -> to_ir -> optimize,
+# codegen_engine/__init__.py:176-236) and their float64 values at point pairs
+# whose exponents fall on both sides of -20.
+# ---------------------------------------------------------------------------
+GOLDEN = Path(__file__).parent / "golden"
+_LEAF = {"rbf": ok.RBF, "matern12": ok.MATERN12, "matern32": ok.MATERN32,
+         "matern52": ok.MATERN52}
 
 
-def test_matern_clamp_tail_keeps_polynomial():
-    # sqrt5 r = 30 > 20: exp clamps at -20 but the polynomial still grows.
-    r = 30.0 / np.sqrt(5.0)
-    X1 = np.zeros((1, 1))
-    X2 = np.array([[r]])
-    K = ok.kernel_matrix(ok.MATERN52, X1, X2, [1.0, 1.0], False)
-    expect = (1 + 30.0 + (5.0 / 3.0) * r * r) * np.exp(-20.0)
-    assert K[0, 0] == pytest.approx(expect, rel=1e-12)
+@pytest.fixture(scope="module")
+def exprs():
+    meta = json.loads((GOLDEN / "ref_kernel_exprs.json").read_text())
+    arrays = np.load(GOLDEN / "ref_kernel_exprs.npz")
+    return meta, arrays
+
+
+def _radial_cases(meta):
+    out = []
+    for key in sorted(meta):
+        fam, tag, _ = key.split("_") if key.count("_") == 2 else (None, None, None)
+        if fam in _LEAF:
+            out.append((key, _LEAF[fam], tag == "ard"))
+    return out
+
+
+def test_fixture_covers_every_radial_kind_iso_ard_and_dimension(exprs):
+    meta, _ = exprs
+    cases = _radial_cases(meta)
+    assert {(k, a) for _, k, a in cases} == {(k, a) for k in ok.KINDS for a in (False, True)}
+    assert {meta[key]["dim"] for key, _, _ in cases} == {1, 4, 8, 16}
+
+
+def test_clamp_placement_matches_reference_codegen(exprs):
+    """exp_clamped(kind, ard) is what the reference's stability pass emitted
+    for every radial leaf, iso and ARD, d in {1, 4, 8, 16}."""
+    meta, _ = exprs
+    for key, kind, ard in _radial_cases(meta):
+        assert meta[key]["exp_clamped"] == [ok.exp_clamped(kind, ard)], key
+    # RBF is never clamped, Matern-1/2 only for ARD: the distinction is real
+    assert meta["rbf_ard_d16"]["exp_clamped"] == [False]
+    assert meta["matern12_iso_d4"]["exp_clamped"] == [False]
+    assert meta["matern12_ard_d4"]["exp_clamped"] == [True]
+    assert meta["matern52_ard_d16"]["exp_clamped"] == [True]
+    for key in ("periodic_iso_d1", "periodic_ard_d4", "product_rbf_periodic_d2"):
+        assert not any(meta[key]["exp_clamped"]), key
+
+
+def test_radial_values_and_gradients_match_reference_expressions(exprs):
+    """Oracle K and dK/dtheta at the fixture pairs equal the reference's
+    emitted expressions in float64 -- including far pairs where a wrongly
+    placed clamp would give os e^-20 instead of the true tail."""
+    meta, A = exprs
+    far_seen = 0
+    for key, kind, ard in _radial_cases(meta):
+        p = A[f"{key}__params"]
+        X1, X2 = A[f"{key}__x1"], A[f"{key}__x2"]
+        want_k, want_g = A[f"{key}__k"], A[f"{key}__grad"]
+        K = np.array([ok.kernel_matrix(kind, X1[i:i + 1], X2[i:i + 1], p, ard)[0, 0]
+                      for i in range(X1.shape[0])])
+        np.testing.assert_allclose(K, want_k, rtol=1e-12, atol=1e-300, err_msg=key)
+        G = np.stack([ok.kernel_gradients(kind, X1[i:i + 1], X2[i:i + 1], p, ard)[:, 0, 0]
+                      for i in range(X1.shape[0])], axis=1)
+        # atol: the isotropic Matern-1/2 gradient at a coincident pair is
+        # os 1e-10 / l^2 in the reference (r floored before the 1/l scale)
+        np.testing.assert_allclose(G, want_g, rtol=1e-8, atol=1e-9, err_msg=key)
+        far_seen += int(np.sum((want_k > 0) & (want_k < p[-1] * np.exp(-20.0))))
+    assert far_seen > 50  # unclamped tails below os e^-20 are exercised
+
+
+def _tree_params(meta, key, p):
+    """Fixture parameters (the generated code's order) in the engine layout:
+    a scale node's factor moves from before its subtree to after it."""
+    names = meta[key]["param_names"]
+    if names and names[0] == "scale":
+        return np.concatenate([p[1:], p[:1]])
+    return p
+
+
+@pytest.mark.parametrize("key", [
+    "periodic_iso_d1", "periodic_iso_d4", "periodic_ard_d1", "periodic_ard_d4",
+    "rq_iso_d1", "rq_iso_d4", "rq_ard_d1", "rq_ard_d4",
+    "linear_iso_d1", "linear_iso_d4", "linear_ard_d1", "linear_ard_d4",
+    "polynomial_iso_d4", "sum_rbf_matern52_d4", "product_rbf_periodic_d2",
+    "product_matern12_matern32ard_d3", "scale_rbf_d2", "product_sum_m12ard_rbf_matern52_d4"])
+def test_tree_values_and_gradients_match_reference_expressions(exprs, key):
+    meta, A = exprs
+    tk = ok.TreeKernel(meta[key]["kernel"], meta[key]["dim"])
+    p = A[f"{key}__params"]
+    pe = _tree_params(meta, key, p)
+    X1, X2 = A[f"{key}__x1"], A[f"{key}__x2"]
+    K = np.array([tk.matrix(X1[i:i + 1], X2[i:i + 1], pe)[0, 0] for i in range(X1.shape[0])])
+    np.testing.assert_allclose(K, A[f"{key}__k"], rtol=1e-11, atol=1e-300)
+    G = np.stack([tk.gradients(X1[i:i + 1], X2[i:i + 1], pe)[:, 0, 0]
+                  for i in range(X1.shape[0])], axis=1)
+    want = A[f"{key}__grad"]
+    if meta[key]["param_names"][0] == "scale":
+        want = np.concatenate([want[1:], want[:1]])
+    np.testing.assert_allclose(G, want, rtol=1e-8, atol=1e-9)
 
 
 @pytest.mark.parametrize("kind", ok.KINDS)
