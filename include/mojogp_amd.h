@@ -158,6 +158,17 @@ MGP_API int mgp_extract_diagonal_test(void* handle, const float* Xs, int64_t m,
  * 493-541; kernels gpu_kernel.py:382-484, 878-975). */
 MGP_API int mgp_gradient_matvec(void* handle, const float* V, int ncols, float* out);
 
+/* out[p] = sum_{a,b} dK_p[a,b] sum_c Lf[c*n+a] Rf[c*n+b] for every kernel
+ * parameter p (engine layout), Lf and Rf host [ncols][n], out host [P].  The
+ * trace routine of mgp_bbmm_eval's gradient step (the matrix-core trace where
+ * its route applies, MGP_GRAD_MFMA as there, else the pair loop) on
+ * caller-given weight columns, in place of the reference's per-parameter
+ * fused_gradient_matvec + kernel_dot_*_vs_strided pair
+ * (combined_inv_quad_logdet.mojo:715-800).  Internal to the reference (no
+ * exported counterpart); exposed for at-size parity tests. */
+MGP_API int mgp_gradient_trace(void* handle, const float* Lf, const float* Rf,
+                               int ncols, double* out);
+
 /* Isolated timing of provider ops.  Replaces benchmark_provider_ops(info, rhs,
  * num_cols, op_code, repeats, warmup) (jit_engine_bindings.mojo:439-572);
  * op 0 forward matvec, 1 fused gradient products, 2 gradient products + the

@@ -183,6 +183,7 @@ _SIGNATURES = {
     "mgp_extract_diagonal_test": (C.c_int, [C.c_void_p, c_float_p, C.c_int64,
                                             c_float_p]),
     "mgp_gradient_matvec": (C.c_int, [C.c_void_p, c_float_p, C.c_int, c_float_p]),
+    "mgp_gradient_trace": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int, c_double_p]),
     "mgp_benchmark_provider_ops": (C.c_int, [C.c_void_p, c_float_p, C.c_int, C.c_int,
                                              C.c_int, C.c_int, c_double_p, c_double_p,
                                              c_float_p]),

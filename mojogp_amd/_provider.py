@@ -187,6 +187,18 @@ class NativeProvider:
                   _lib.fptr(out))
         return times, float(tile.value), out
 
+    def gradient_trace(self, Lf, Rf) -> np.ndarray:
+        """g[p] = sum_ab dK_p[a, b] sum_c Lf[c, a] Rf[c, b] (float64, [P]): the
+        BBMM gradient step's trace routine on given weight columns."""
+        L, _ = _cols(Lf, self.n)
+        R, _ = _cols(Rf, self.n)
+        if L.shape != R.shape:
+            raise ValueError("Lf and Rf must have the same shape")
+        out = np.zeros(self.nparams, dtype=np.float64)
+        _lib.call("mgp_gradient_trace", self.handle, _lib.fptr(L), _lib.fptr(R), L.shape[0],
+                  _lib.dptr(out))
+        return out
+
     def gradient_matvec(self, V) -> np.ndarray:
         """out[p, c, i] = sum_j dk_p(x_i, x_j) V[c, j] for the P engine parameters."""
         Vc, vec = _cols(V, self.n)

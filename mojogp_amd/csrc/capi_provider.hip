@@ -441,6 +441,20 @@ int mgp_gradient_matvec(void* h, const float* V, int ncols, float* out) {
   });
 }
 
+int mgp_gradient_trace(void* h, const float* Lf, const float* Rf, int ncols, double* out) {
+  return guarded([&] {
+    Provider* pv = as_provider(h);
+    MGP_REQUIRE(Lf && Rf && out && ncols >= 1, "bad arguments");
+    const size_t tot = (size_t)pv->n * ncols;
+    float* dl = pv->io_a.ensure(tot);
+    float* dr = pv->io_b.ensure(tot);
+    MGP_HIP_CHECK(hipMemcpyAsync(dl, Lf, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    MGP_HIP_CHECK(hipMemcpyAsync(dr, Rf, tot * sizeof(float), hipMemcpyHostToDevice, pv->st));
+    gradient_traces(*pv, dl, dr, ncols, out, pv->st);
+    MGP_HIP_CHECK(hipStreamSynchronize(pv->st));
+  });
+}
+
 int mgp_benchmark_provider_ops(void* h, const float* rhs, int ncols, int op,
                                int repeats, int warmup, double* times_ms,
                                double* tile_ms_avg, float* out_or_null) {

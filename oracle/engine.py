@@ -17,8 +17,10 @@ caspbian/mojogp's engine so the gfx950 product can be checked against it:
   train                 kernels/jit/jit_training.mojo:274-1008 with
                         kernels/training_utils.mojo:23-320, kernels/utils.mojo:14-90
   solve_alpha           kernels/jit/jit_prediction.mojo:681-765
-  lanczos_inv_root      kernels/jit/jit_prediction.mojo:974-1177
-  love_variance         kernels/jit/jit_prediction.mojo:211-233
+  lanczos_inv_root      kernels/jit/jit_prediction.mojo:974-1177 (float64, or
+                        fp32 as the reference runs it)
+  love_variance_fp32    kernels/jit/jit_prediction.mojo:211-233,1236-1350 in
+                        the reference's fp32 arithmetic (a rounding floor)
 
 What pins each piece (tests/test_oracle_engine.py): the RNG by moments and a
 Kolmogorov-Smirnov test; pivoted Cholesky by exact reconstruction of low-rank
@@ -670,14 +672,21 @@ def lanczos_start(n: int, r: int) -> np.ndarray:
     return z / np.linalg.norm(z)
 
 
-def lanczos_inv_root(A: np.ndarray, r: int) -> np.ndarray:
-    """S [n, r] with S S^T ~ A^{-1}: Lanczos with full re-orthogonalisation."""
+def lanczos_inv_root(A: np.ndarray, r: int, dtype=np.float64) -> np.ndarray:
+    """S [n, r] with S S^T ~ A^{-1}: Lanczos with full re-orthogonalisation.
+
+    ``dtype=np.float32`` runs the recurrence, the re-orthogonalisation and the
+    root S = Q V diag(lambda^-1/2) V^T in fp32, as the reference does
+    (jit_prediction.mojo:974-1177, 417-436); the tridiagonal eigensolve stays
+    float64 (the reference's is an fp32 QL, native_numerics.mojo:271-400), so
+    the fp32 result is if anything closer to exact than the reference's."""
     n = A.shape[0]
-    Q = np.zeros((n, r))
-    alpha = np.zeros(r)
-    beta = np.zeros(max(r - 1, 0))
+    A = np.asarray(A, dtype)
+    Q = np.zeros((n, r), dtype)
+    alpha = np.zeros(r, dtype)
+    beta = np.zeros(max(r - 1, 0), dtype)
     Q[:, 0] = lanczos_start(n, r)
-    b_prev = 0.0
+    b_prev = dtype(0.0)
     for j in range(r):
         v = Q[:, j]
         w = A @ v
@@ -699,10 +708,11 @@ def lanczos_inv_root(A: np.ndarray, r: int) -> np.ndarray:
             Q[:, j + 1] = w / b
         b_prev = b
     from scipy.linalg import eigh_tridiagonal
-    lam, V = eigh_tridiagonal(alpha, beta) if r > 1 else (alpha.copy(), np.ones((1, 1)))
+    al, be = alpha.astype(np.float64), beta.astype(np.float64)
+    lam, V = eigh_tridiagonal(al, be) if r > 1 else (al.copy(), np.ones((1, 1)))
     clamp = max(1e-10, lam.max()) * 1e-6
     lam = np.maximum(lam, clamp)
-    Tis = (V / np.sqrt(lam)) @ V.T
+    Tis = ((V / np.sqrt(lam)) @ V.T).astype(dtype)
     return Q @ Tis
 
 
@@ -722,6 +732,25 @@ def predict(kind: int, ard: bool, X, y, Xs, params, noise: float, mean: float, *
     V = Ks @ S
     var = np.maximum(_kdiag(kind, params, Xs) - np.sum(V * V, axis=1), 1e-10)
     return mu, var, alpha
+
+
+def love_variance_fp32(kind: int, ard: bool, X, Xs, params, noise: float, *,
+                       lanczos_rank=100) -> np.ndarray:
+    """LOVE variance in the reference's fp32 arithmetic and order: fp32 kernel
+    values (the exact values rounded once, more accurate than any fp32 kernel
+    evaluation), the fp32 Lanczos root above, the fp32 cross product K(X*, X) S
+    and var = k** - sum_j (K* S)_j^2 summed in fp32 with the 1e-10 floor
+    (jit_prediction.mojo:1236-1350, kernel_love_variance :211-233).  Its
+    distance from the float64 LOVE (predict) is the rounding floor any fp32
+    implementation of the method carries."""
+    X = np.asarray(X, np.float64)
+    n = X.shape[0]
+    A = (ok.kernel_matrix(kind, X, X, params, ard) + noise * np.eye(n)).astype(F32)
+    S = lanczos_inv_root(A, lanczos_rank, dtype=F32)
+    Ks = ok.kernel_matrix(kind, Xs, X, params, ard).astype(F32)
+    W = Ks @ S
+    kss = F32(_kdiag(kind, params, Xs))
+    return np.maximum(kss - np.sum(W * W, axis=1, dtype=F32), F32(1e-10))
 
 
 def exact_variance(kind: int, ard: bool, X, Xs, params, noise: float, *, max_cg=300,

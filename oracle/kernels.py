@@ -159,7 +159,7 @@ def kernel_gradients(kind: int, X1, X2, params, ard: bool) -> np.ndarray:
     ls = _lengthscales(p, d, ard)
     os = p[-1]
     diff2 = (X1[:, None, :] - X2[None, :, :]) ** 2          # raw differences
-    r2 = np.einsum("ijk,k->ij", diff2, 1.0 / ls**2)
+    r2 = diff2 @ (1.0 / ls**2)
     k = kernel_from_sq(kind, r2, os, ard)
     h = _grad_factor(kind, r2, os, ard, k)
     terms = diff2 / ls**3                                    # (n1, n2, d)
@@ -184,12 +184,27 @@ def _grad_factor(kind: int, r2: np.ndarray, os: float, ard: bool, k: np.ndarray)
     return (5.0 / 3.0) * os * (1.0 + _SQRT5 * r) * _exp_guard(-_SQRT5 * r, clamp)
 
 
-def gradient_matvec(kind: int, X, V, params, ard: bool) -> np.ndarray:
+def gradient_matvec(kind: int, X, V, params, ard: bool, rows: np.ndarray | None = None,
+                    block: int = 8) -> np.ndarray:
     """out[p, c, i] = sum_j dk_p(x_i, x_j) V[c, j] (reference fused_gradient_matvec
-    layout out[p*n*C + c*n + i], gpu_kernel.py:382-484)."""
-    G = kernel_gradients(kind, X, X, params, ard)
+    layout out[p*n*C + c*n + i], gpu_kernel.py:382-484), optionally only for
+    `rows` (shape (P, ncols, len(rows)), blocks of `block` rows so large n fits)."""
     V = np.atleast_2d(np.asarray(V, dtype=np.float64))
-    return np.einsum("pij,cj->pci", G, V)
+    if rows is None:
+        G = kernel_gradients(kind, X, X, params, ard)
+        return np.einsum("pij,cj->pci", G, V)
+    X = np.asarray(X, dtype=np.float64)
+    idx = np.asarray(rows)
+    out = None
+    for s in range(0, idx.shape[0], block):
+        r = idx[s:s + block]
+        G = kernel_gradients(kind, X[r], X, params, ard)          # (P, nr, n)
+        P_, nr = G.shape[0], G.shape[1]
+        part = (G.reshape(P_ * nr, -1) @ V.T).reshape(P_, nr, -1).transpose(0, 2, 1)
+        if out is None:
+            out = np.empty((G.shape[0], V.shape[0], idx.shape[0]), dtype=np.float64)
+        out[:, :, s:s + block] = part
+    return out
 
 
 # ---------------------------------------------------------------------------

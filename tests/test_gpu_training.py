@@ -82,14 +82,21 @@ def test_config1_fit_and_love_predict_at_size():
     var_err = float(np.max(np.abs(std.astype(np.float64) ** 2 - var))) / kss
     _log(f"  LOVE std relerr {_rel(std, np.sqrt(var)):.2e}, variance error {var_err:.2e} of "
          f"k**, mean relerr {_rel(mean, mu):.2e}")
-    # var = k** - ||K* S||^2 cancels ~5000-fold inside the data (var ~2.5e-4
-    # k**): the fp32 products' ~1e-6 relative error is ~1e-6 k** absolute in
-    # var, so the check is on the variance error relative to k**; the plain
-    # std error (dominated by those interior points) is bounded by that floor
+    # var = k** - ||K* S||^2 cancels ~5000-fold inside the data (var ~2e-4
+    # k**), so the float64 std is out of fp32's reach at 1e-4 there: LOVE in
+    # the reference's own fp32 arithmetic and order lands ~1.2e-4 from it
+    # (oracle.engine.love_variance_fp32; pinned on the CPU by
+    # test_oracle_engine.py::test_love_fp32_floor_on_config1).  The device
+    # must be at least as close to float64 as that restatement, and within
+    # 1e-5 k** on the variance itself.
+    var32 = oe.love_variance_fp32(ok.RBF, False, X, Xs, params, tr.noise, lanczos_rank=100)
+    floor = _rel(np.sqrt(var32.astype(np.float64)), np.sqrt(var))
+    std_err = _rel(std, np.sqrt(var))
+    _log(f"  LOVE std relerr {std_err:.2e} (fp32 reference-order restatement: {floor:.2e})")
     assert var_err <= 1e-5
-    assert _rel(std, np.sqrt(var)) <= 5e-4
-    # predictions of the two fits (GPU hyperparameters vs the restatement's):
-    # bounded by the same fp32 floor (restatement fp32 vs fp64: 6e-5 std)
+    assert std_err <= max(1e-4, floor)
+    # predictions of the two fits (GPU hyperparameters vs the restatement's),
+    # both evaluated in float64
     mu_r, var_r, _ = oe.predict(ok.RBF, False, X, y, Xs, np.asarray(ref["params"], np.float64),
                                 ref["noise"], ref["mean"], max_cg=300, tol=1e-8,
                                 lanczos_rank=100)
@@ -97,8 +104,8 @@ def test_config1_fit_and_love_predict_at_size():
                                 max_cg=300, tol=1e-8, lanczos_rank=100)
     _log(f"  fitted-model predictions: mean {_rel(mu_g, mu_r):.2e}, "
          f"std {_rel(np.sqrt(var_g), np.sqrt(var_r)):.2e}")
-    assert _rel(mu_g, mu_r) <= 5e-4
-    assert _rel(np.sqrt(var_g), np.sqrt(var_r)) <= 5e-4
+    assert _rel(mu_g, mu_r) <= 1e-4
+    assert _rel(np.sqrt(var_g), np.sqrt(var_r)) <= 1e-4
     # alpha CG stops at relative residual 1e-3: two correct solves (fp32 /
     # fp64) agree on the mean only to about that; at 1e-6 the bar is 1e-4
     assert _rel(mean, mu) <= 5e-3
