@@ -91,11 +91,13 @@ MGP_API int mgp_set_learned_noise(void* handle, int mode, const int* group_ids,
 /* Replaces destroy_provider(info) (fn_ptr_module.py:1183-1195). */
 MGP_API int mgp_destroy_provider(void* handle);
 
-/* Select the materialized route: allocate the dense K [n][n] (fp32, 4 n^2
- * bytes) on the device, fill it, and refill it on every parameter update;
- * forward products then run as a fp32 GEMM (rocBLAS) plus the noise term.
- * Replaces materialize(info) / _do_materialize (fn_ptr_module.py:363-384,
- * 1168-1181). */
+/* Select the materialized route: hold the dense K on the device as a scaled
+ * two-term fp16 split (4 bytes per entry, like fp32), fill its symmetric half
+ * and refill it on every parameter update (the full matrix is filled on the
+ * first product wider than 16 columns); forward products then run on the
+ * hand-written fp16 matrix-core kernels (three part products, fp32/fp64
+ * accumulation) plus the noise term.  Replaces materialize(info) /
+ * _do_materialize (fn_ptr_module.py:363-384, 1168-1181). */
 MGP_API int mgp_materialize(void* handle);
 /* Replace the impl_update_params / impl_update_noise / impl_get_noise /
  * impl_get_diagonal_value fn pointers (fn_ptr_module.py:651-703). */
@@ -111,6 +113,26 @@ MGP_API int mgp_update_noise(void* handle, float noise);
 MGP_API int mgp_set_noise_vector(void* handle, const float* noise_vec);
 MGP_API int mgp_get_noise(void* handle, float* out);
 MGP_API int mgp_get_diagonal_value(void* handle, float* out);
+
+/* The reference's non-raising provider fn pointers with their exact
+ * signatures (UpdateNoiseFn fn(Int, Float32), GetFloatFn fn(Int) -> Float32,
+ * GetIntFn fn(Int) -> Int, GetPtrFn fn(Int) -> Float32*;
+ * erased_provider.mojo:43-50; implementations impl_update_noise ..
+ * impl_get_noise_vector_ptr, impl_get_diagonal_value, fn_ptr_module.py:
+ * 666-696): their addresses are the provider dict's update_noise, get_noise,
+ * get_noise_mode, get_noise_vector_ptr and get_diagonal_value entries
+ * (fn_ptr_module.py:1120-1166), callable through ctypes as the reference's
+ * Python does (update_noise: CFUNCTYPE(None, c_ssize_t, c_float),
+ * _multi_output_backend.py:166-183).  handle = the provider_ptr value.
+ * They return no status: a failure is recorded for mgp_last_error and they
+ * return NaN / -1 / NULL (update_noise leaves the noise unchanged).
+ * get_noise_mode: 0 scalar, 1 fixed vector, 2-4 learned; get_noise_vector_ptr:
+ * the device array of per-point noise, NULL in mode 0. */
+MGP_API void mgp_fn_update_noise(intptr_t handle, float noise);
+MGP_API float mgp_fn_get_noise(intptr_t handle);
+MGP_API intptr_t mgp_fn_get_noise_mode(intptr_t handle);
+MGP_API float* mgp_fn_get_noise_vector_ptr(intptr_t handle);
+MGP_API float mgp_fn_get_diagonal_value(intptr_t handle);
 /* Shape of a provider (the n / dim / num_gradient_params / is_ard keys of the
  * reference's provider dict, fn_ptr_module.py:1120-1166). */
 MGP_API int mgp_provider_info(void* handle, int64_t* n, int* d, int* nparams,
@@ -125,16 +147,23 @@ MGP_API int mgp_forward_matvec_device(void* handle, const float* V_device,
                                       int ncols, float* out_device);
 /* Same as mgp_forward_matvec_device, allocating nothing: no hipMalloc, no
  * hipFree, no allocating library call.  No counterpart in the reference; it
- * is for callers that cannot allocate (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc).  Its work buffers (packed
- * right-hand sides, column maxima, split partial sums) live in one fixed
- * 64 MiB device array per GPU, held until the process ends; split partials
- * that do not fit reduce the split count.  A call whose packed right-hand
- * sides alone exceed the array (about 4 n min(ncols, 64) bytes: n up to ~1M at
- * 16 columns, ~260k at 64) fails with MGP_ERR_INVALID.  Serves the single-kernel
- * matrix-free route only (not kernel trees or materialized providers).  Every
- * call on a GPU shares that GPU's array: calls that overlap on one GPU (other
- * threads, other providers' streams) race. */
+ * is for callers that cannot allocate (tight serving loops, harnesses that
+ * forbid hipMalloc).  The work runs eagerly on the provider's own stream and
+ * ends in a stream synchronize, so it is not recorded into a caller's HIP
+ * graph.  Its work buffers (packed right-hand sides, column maxima, split
+ * partial sums) live in one fixed 64 MiB device array per GPU, held until the
+ * process ends; split partials that do not fit reduce the split count.  A
+ * call whose packed right-hand sides alone exceed the array (about
+ * 4 n min(ncols, 64) bytes: n up to ~1M at 16 columns, ~260k at 64) fails
+ * with MGP_ERR_INVALID.  Serves the single-kernel matrix-free route only (not
+ * kernel trees or materialized providers), always on the one-sided tile
+ * kernel: the symmetric kernel's transposed partial sums (n^2/16 bytes) do
+ * not fit a fixed array, so above the automatic symmetric threshold
+ * (n >= 24065) this call is slower than mgp_forward_matvec_device (config 3:
+ * ~22.8 ms against ~16.9 ms) and agrees with it to the product rounding, not
+ * bit for bit.  Every call on a GPU shares that GPU's array; a per-device
+ * lock, held until the call's stream has drained, makes overlapping calls
+ * (other threads, other providers) run one after another. */
 MGP_API int mgp_forward_matvec_device_noalloc(void* handle, const float* V_device,
                                               int ncols, float* out_device);
 /* (K + noise I) V from per-dimension differences (no Gram form, no MFMA):

@@ -85,13 +85,23 @@ class KernelModule:
             "has_observation_noise_vector": mode >= 1,
             "noise_group_ptr": 0,
             "num_noise_groups": 0,
+            # the non-raising fn pointers, C-callable with the reference's
+            # signatures (fn_ptr_module.py:1120-1166; the raising ones are
+            # Mojo-ABI entry points only its engine calls, so they have no
+            # counterpart here)
+            "update_noise": _lib.fn_address("mgp_fn_update_noise"),
+            "get_noise": _lib.fn_address("mgp_fn_get_noise"),
+            "get_noise_mode": _lib.fn_address("mgp_fn_get_noise_mode"),
+            "get_noise_vector_ptr": _lib.fn_address("mgp_fn_get_noise_vector_ptr"),
+            "get_diagonal_value": _lib.fn_address("mgp_fn_get_diagonal_value"),
             "_provider": prov,
         }
 
     def materialize(self, info: dict) -> bool:
-        """Select the materialized route: dense K on the device, refilled on
-        every parameter update, products by fp32 GEMM
-        (materialize / _do_materialize, fn_ptr_module.py:363-384, 1168-1181)."""
+        """Select the materialized route: dense K on the device as a scaled
+        two-term fp16 split, refilled on every parameter update, products on
+        the hand-written fp16 matrix-core kernels (materialize /
+        _do_materialize, fn_ptr_module.py:363-384, 1168-1181)."""
         _provider(info).materialize()
         info["materialization_mode"] = 1
         return True

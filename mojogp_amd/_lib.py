@@ -184,6 +184,12 @@ _SIGNATURES = {
                                             c_float_p]),
     "mgp_gradient_matvec": (C.c_int, [C.c_void_p, c_float_p, C.c_int, c_float_p]),
     "mgp_gradient_trace": (C.c_int, [C.c_void_p, c_float_p, c_float_p, C.c_int, c_double_p]),
+    # fn-pointer exports with the reference's provider signatures (no status)
+    "mgp_fn_update_noise": (None, [C.c_ssize_t, C.c_float]),
+    "mgp_fn_get_noise": (C.c_float, [C.c_ssize_t]),
+    "mgp_fn_get_noise_mode": (C.c_ssize_t, [C.c_ssize_t]),
+    "mgp_fn_get_noise_vector_ptr": (C.c_void_p, [C.c_ssize_t]),
+    "mgp_fn_get_diagonal_value": (C.c_float, [C.c_ssize_t]),
     "mgp_benchmark_provider_ops": (C.c_int, [C.c_void_p, c_float_p, C.c_int, C.c_int,
                                              C.c_int, C.c_int, c_double_p, c_double_p,
                                              c_float_p]),
@@ -296,6 +302,12 @@ def load() -> C.CDLL:
             fn.argtypes = args
         _lib = lib
         return lib
+
+
+def fn_address(name: str) -> int:
+    """Address of an exported entry point (the provider dict's fn-pointer
+    values)."""
+    return int(C.cast(getattr(load(), name), C.c_void_p).value)
 
 
 def last_error() -> str:

@@ -41,6 +41,10 @@ struct ScratchSlot {
 };
 std::mutex g_scratch_mu;
 ScratchSlot g_scratch[kMaxScratchDevices];
+// One lock per device, held by an allocation-free call from its first use of
+// the device's array until its stream has drained: calls that would share
+// the array run one after another instead of racing.
+std::mutex g_noalloc_mu[kMaxScratchDevices];
 
 // Resolves this device's scratch address once, with `dev` current (called at
 // provider set-up).  A failure is recorded, not raised: it only disables the
@@ -238,6 +242,44 @@ int mgp_get_diagonal_value(void* h, float* out) {
   return guarded([&] { *out = as_provider(h)->kdiag(); });
 }
 
+// Fn-pointer exports: the reference's non-raising provider signatures
+// (erased_provider.mojo:43-50), whose addresses go into the provider dict.
+// They cannot return a status: a failure is recorded for mgp_last_error and
+// the call returns NaN / -1 / null (update_noise leaves the noise unchanged).
+void mgp_fn_update_noise(intptr_t h, float noise) {
+  (void)mgp_update_noise(reinterpret_cast<void*>(h), noise);
+}
+
+float mgp_fn_get_noise(intptr_t h) {
+  float v = std::nanf("");
+  (void)mgp_get_noise(reinterpret_cast<void*>(h), &v);
+  return v;
+}
+
+intptr_t mgp_fn_get_noise_mode(intptr_t h) {
+  intptr_t mode = -1;
+  (void)guarded([&] {
+    const Provider* pv = as_provider(reinterpret_cast<void*>(h));
+    mode = pv->learned_noise_mode > 0 ? pv->learned_noise_mode : (pv->has_noise_vec ? 1 : 0);
+  });
+  return mode;
+}
+
+float* mgp_fn_get_noise_vector_ptr(intptr_t h) {
+  float* p = nullptr;
+  (void)guarded([&] {
+    Provider* pv = as_provider(reinterpret_cast<void*>(h));
+    p = pv->has_noise_vec ? pv->noise_vec.ptr : nullptr;
+  });
+  return p;
+}
+
+float mgp_fn_get_diagonal_value(intptr_t h) {
+  float v = std::nanf("");
+  (void)mgp_get_diagonal_value(reinterpret_cast<void*>(h), &v);
+  return v;
+}
+
 int mgp_provider_info(void* h, int64_t* n, int* d, int* nparams, int* kind,
                       int* ard) {
   return guarded([&] {
@@ -284,8 +326,10 @@ int mgp_forward_matvec_device_noalloc(void* h, const float* V_dev, int ncols, fl
     MGP_REQUIRE(!pv->is_tree, "the allocation-free matvec does not serve kernel trees");
     MGP_REQUIRE(!pv->materialized, "the allocation-free matvec does not serve the materialized "
                                    "route");
+    uint8_t* arena = scratch_of(pv->device);
+    std::lock_guard<std::mutex> lk(g_noalloc_mu[pv->device]);
     MatvecWorkspace w;  // fixed-arena mode: its own buffers stay unallocated
-    w.arena = scratch_of(pv->device);
+    w.arena = arena;
     w.arena_bytes = kNoAllocScratchBytes;
     if (pv->fused_route()) {
       const size_t need = fused_matvec_min_arena(pv->train, ncols);

@@ -139,8 +139,8 @@ struct MatvecWorkspace {
 // A square product (rows and cols the same packed points) with 1..16
 // right-hand sides runs on the symmetric kernel, which forms each
 // off-diagonal kernel value once for both of its entries, when the points fill
-// at least kSymMinBlocks 256-point blocks and its transposed partial sums
-// (n^2/8 bytes) stay within kSymMaxBytes.  The environment variable
+// at least kSymMinBlocks 512-point blocks (n >= 47 * 512 + 1 = 24065) and its
+// transposed partial sums (n^2/16 bytes) stay within kSymMaxBytes.  The environment variable
 // MGP_SYM_MATVEC=0 turns that route off, =1 takes it for every square product
 // the kernel can serve (any n), for tests and measurements.
 void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,

@@ -44,3 +44,25 @@ def test_error_path_reports_message():
     with pytest.raises(_lib.NativeCallError, match="expected 3"):
         _lib.call("mgp_init_provider", 0, 1, 2, 4, _lib.fptr(X), _lib.fptr(params), 5,
                   0.1, ctypes.byref(ctypes.c_void_p()))
+
+
+def test_fn_pointer_exports_report_on_dead_handles():
+    """The reference-signature fn pointers (the provider dict's update_noise,
+    get_noise, get_noise_mode, get_noise_vector_ptr, get_diagonal_value) take
+    the provider_ptr value and return no status: on a handle that is no live
+    provider they record the error and return their sentinels, before any
+    device work (safe without a GPU)."""
+    import math
+    upd = ctypes.CFUNCTYPE(None, ctypes.c_ssize_t, ctypes.c_float)(
+        _lib.fn_address("mgp_fn_update_noise"))
+    upd(0, 0.5)
+    assert "null provider handle" in _lib.last_error()
+    get_f = ctypes.CFUNCTYPE(ctypes.c_float, ctypes.c_ssize_t)
+    get_i = ctypes.CFUNCTYPE(ctypes.c_ssize_t, ctypes.c_ssize_t)
+    get_p = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_ssize_t)
+    bogus = 0x1000
+    assert math.isnan(get_f(_lib.fn_address("mgp_fn_get_noise"))(bogus))
+    assert "unknown or destroyed provider handle" in _lib.last_error()
+    assert math.isnan(get_f(_lib.fn_address("mgp_fn_get_diagonal_value"))(bogus))
+    assert get_i(_lib.fn_address("mgp_fn_get_noise_mode"))(bogus) == -1
+    assert get_p(_lib.fn_address("mgp_fn_get_noise_vector_ptr"))(bogus) is None

@@ -1,22 +1,33 @@
 """The allocation-free forward matvec (mgp_forward_matvec_device_noalloc)
 against the allocating one (mgp_forward_matvec_device) through the C ABI.
 
+The allocation-free call always runs the one-sided tile kernel, so it is
+compared with the allocating call on that same kernel (MGP_SYM_MATVEC=0), and
+separately with the allocating call's automatic route, which above
+n = 24065 is the symmetric kernel (a different summation, 1e-6 apart).
 Calls in a row with decreasing inputs share one fixed scratch array that keeps
 the previous call's bytes, so each call must rebuild everything it reads:
 * config 3 (N = 250k, d = 16, t = 16, Matern-5/2 ARD): its split partials do
   not all fit the 64 MiB array, so fewer splits run; the product then differs
-  from the allocating call's by summation order only (<= 1e-6 relative);
+  from the one-sided allocating call's by summation order only (<= 1e-6);
+* N = 30000, d = 8, t = 16 (above the symmetric threshold): same splits as
+  the one-sided allocating call, bit-identical output;
 * N = 20000, d = 8, t = 16: same splits, bit-identical output;
 * N = 3000, d = 5, t = 5, RBF with a fixed noise vector: bit-identical.
 An input whose packed right-hand sides exceed the array is rejected before any
-launch, and free device memory is unchanged across an allocation-free call on
-a fresh provider (whose own workspace would otherwise grow on first use).
+launch, free device memory is unchanged across an allocation-free call on a
+fresh provider (whose own workspace would otherwise grow on first use), and
+calls from two threads on two providers -- which share the device's array --
+give each its own sequential result bit for bit (a per-device lock orders
+them).
 Device buffers for inputs and outputs come from the HIP runtime the library
 itself loaded, through ctypes.
 """
 
 import ctypes as C
+import os
 import sys
+import threading
 
 import numpy as np
 import pytest
@@ -84,7 +95,24 @@ def _free_mem(hip):
     return fr.value
 
 
+def _allocating(prov, src, dst, t, sym):
+    """mgp_forward_matvec_device with the symmetric route allowed or not."""
+    old = os.environ.get("MGP_SYM_MATVEC")
+    try:
+        if sym:
+            os.environ.pop("MGP_SYM_MATVEC", None)
+        else:
+            os.environ["MGP_SYM_MATVEC"] = "0"
+        _lib.call("mgp_forward_matvec_device", prov.handle, src.ptr, t, dst.ptr)
+    finally:
+        if old is None:
+            os.environ.pop("MGP_SYM_MATVEC", None)
+        else:
+            os.environ["MGP_SYM_MATVEC"] = old
+
+
 def _case(hip, kind, n, d, t, seed, noise_vec=False, check_memory=False):
+    """(no-alloc output, one-sided allocating output, automatic-route output)."""
     rng = np.random.default_rng(seed)
     X = rng.normal(size=(n, d)).astype(np.float32)
     V = rng.normal(size=(t, n)).astype(np.float32)
@@ -104,30 +132,88 @@ def _case(hip, kind, n, d, t, seed, noise_vec=False, check_memory=False):
         _lib.call("mgp_forward_matvec_device_noalloc", prov.handle, bufs[0].ptr, t, bufs[2].ptr)
         after = _free_mem(hip)
         got = bufs[2].get((t, n))
-        _lib.call("mgp_forward_matvec_device", prov.handle, bufs[0].ptr, t, bufs[1].ptr)
+        _allocating(prov, bufs[0], bufs[1], t, sym=False)
         ref = bufs[1].get((t, n))
         grown = before - _free_mem(hip)
+        _allocating(prov, bufs[0], bufs[1], t, sym=True)
+        auto = bufs[1].get((t, n))
         if check_memory:
             _log(f"  free memory: no-alloc call {before - after} B, allocating call {grown} B")
             assert abs(before - after) < (1 << 20)
         assert np.all(np.isfinite(got))
-        return got, ref
+        return got, ref, auto
     finally:
         for b in bufs:
             b.free()
         prov.close()
 
 
+def _colrel(a, b):
+    return float(np.max(np.linalg.norm(a - b, axis=1) / np.linalg.norm(b, axis=1)))
+
+
 def test_noalloc_matches_allocating_entry_point():
     hip = _hip()
-    got, ref = _case(hip, KIND_MATERN52, 250_000, 16, 16, 0, check_memory=True)
-    rel = np.linalg.norm(got - ref, axis=1) / np.linalg.norm(ref, axis=1)
-    _log(f"  config 3: max column relerr {rel.max():.2e}")
-    assert rel.max() <= 1e-6
-    got, ref = _case(hip, KIND_MATERN52, 20_000, 8, 16, 1)
+    got, ref, auto = _case(hip, KIND_MATERN52, 250_000, 16, 16, 0, check_memory=True)
+    _log(f"  config 3: vs one-sided {_colrel(got, ref):.2e}, vs symmetric {_colrel(got, auto):.2e}")
+    assert _colrel(got, ref) <= 1e-6       # fewer splits: summation order only
+    assert _colrel(got, auto) <= 5e-6      # the symmetric kernel's own summation
+    got, ref, auto = _case(hip, KIND_MATERN52, 30_000, 8, 16, 4)
+    _log(f"  n=30000: vs symmetric {_colrel(got, auto):.2e}")
     np.testing.assert_array_equal(got, ref)
-    got, ref = _case(hip, KIND_RBF, 3000, 5, 5, 2, noise_vec=True)
+    assert _colrel(got, auto) <= 5e-6
+    got, ref, _ = _case(hip, KIND_MATERN52, 20_000, 8, 16, 1)
     np.testing.assert_array_equal(got, ref)
+    got, ref, _ = _case(hip, KIND_RBF, 3000, 5, 5, 2, noise_vec=True)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_noalloc_calls_from_two_threads_are_ordered():
+    """Two providers on one GPU share its scratch array; calls from two threads
+    (ctypes releases the GIL during the call) must each reproduce their own
+    sequential result bit for bit."""
+    hip = _hip()
+    rng = np.random.default_rng(9)
+    jobs = []
+    for n, d, t, kind in ((20_000, 8, 16, KIND_MATERN52), (12_000, 4, 8, KIND_RBF)):
+        X = rng.normal(size=(n, d)).astype(np.float32)
+        V = rng.normal(size=(t, n)).astype(np.float32)
+        params = np.concatenate([rng.uniform(0.7, 1.4, size=d), [1.1]]).astype(np.float32)
+        prov = NativeProvider(kind, True, X, params, 0.1)
+        src, dst = _Dev(hip, 4 * n * t), _Dev(hip, 4 * n * t)
+        src.put(V)
+        jobs.append((prov, src, dst, t, n))
+    try:
+        seq = []
+        for prov, src, dst, t, n in jobs:
+            _lib.call("mgp_forward_matvec_device_noalloc", prov.handle, src.ptr, t, dst.ptr)
+            seq.append(dst.get((t, n)))
+        _log("no-alloc threads: two providers, 6 calls each")
+        errors = []
+
+        def run(k):
+            prov, src, dst, t, n = jobs[k]
+            try:
+                for _ in range(6):
+                    _lib.call("mgp_forward_matvec_device_noalloc", prov.handle, src.ptr, t,
+                              dst.ptr)
+                    if not np.array_equal(dst.get((t, n)), seq[k]):
+                        errors.append(f"provider {k}: output differs from its sequential call")
+            except Exception as exc:  # reported after the join
+                errors.append(f"provider {k}: {exc}")
+
+        threads = [threading.Thread(target=run, args=(k,)) for k in range(2)]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join(timeout=120)
+        assert not any(th.is_alive() for th in threads)
+        assert not errors, errors
+    finally:
+        for prov, src, dst, _, _ in jobs:
+            src.free()
+            dst.free()
+            prov.close()
 
 
 def test_noalloc_rejects_inputs_beyond_the_scratch():
