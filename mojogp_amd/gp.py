@@ -201,6 +201,7 @@ class SingleOutputGP:
         self._fitted_mean: Optional[float] = None
         self._backend_train_info: Optional[dict] = None
         self._backend_predict_info: Optional[dict] = None
+        self._backend_sample_info: Optional[dict] = None
         self._prediction_cache_handle: Optional[int] = None
         self._prediction_cache_signature: Optional[tuple] = None
         self._prediction_cache_info: Optional[dict] = None
@@ -242,6 +243,19 @@ class SingleOutputGP:
     @property
     def backend_predict_info(self) -> Optional[dict]:
         return self._backend_predict_info
+
+    @property
+    def nll_history(self) -> Optional[np.ndarray]:
+        """NLL per training iteration (gp.py:759-764)."""
+        if self._training_result is None:
+            return None
+        return self._training_result.nll_history
+
+    @property
+    def backend_sample_info(self) -> Optional[dict]:
+        """Sampling-route metadata of the most recent sample_posterior call
+        (gp.py:776-779)."""
+        return self._backend_sample_info
 
     def _is_single_kernel_type(self, kt: KernelType) -> bool:
         return self.kernel.operator is None and self.kernel.kernel_type == kt
@@ -1038,6 +1052,161 @@ class SingleOutputGP:
         """p(f_test | y_train)."""
         kwargs.pop("target", None)
         return self.predict(X, target="latent", **kwargs)
+
+    # ------------------------------------------------------------ scoring
+    def score(self, X_test, y_test) -> float:
+        """R^2 of the predictive mean on test data (gp.py:3059-3070)."""
+        if not self._is_trained:
+            raise RuntimeError("Model must be trained before scoring")
+        X_test = np.asarray(X_test, dtype=np.float32)
+        y_test = np.asarray(y_test, dtype=np.float32)
+        mean, _ = self.predict(X_test, return_std=True)
+        ss_res = np.sum((y_test - mean) ** 2)
+        ss_tot = np.sum((y_test - np.mean(y_test)) ** 2)
+        if ss_tot == 0:
+            return 0.0
+        return float(1.0 - ss_res / ss_tot)
+
+    def get_learned_params(self) -> dict:
+        """Learned parameters by name, plus noise (and the learned noise state
+        of noise modes 2-4) and mean (gp.py:3072-3099)."""
+        if not self._is_trained:
+            raise RuntimeError("Model must be trained before getting params")
+        tr = self._training_result
+        params = {}
+        for i, name in enumerate(self.kernel.get_param_names()):
+            if i < len(tr.params):
+                params[name] = float(tr.params[i])
+        params["noise"] = float(tr.noise)
+        obs = self._observation_noise_train
+        if self._noise_mode == "learned_vector" and obs is not None:
+            params["observation_noise_train"] = np.asarray(obs, dtype=np.float32).copy()
+        if self._noise_mode == "learned_grouped" and self._noise_group_values is not None:
+            params["group_noise"] = np.asarray(self._noise_group_values, dtype=np.float32).copy()
+        if self._noise_mode == "learned_input_dependent" and self._noise_function_params is not None:
+            params["noise_function"] = "linear"
+            params["noise_function_params"] = np.asarray(self._noise_function_params,
+                                                         dtype=np.float32).copy()
+            if obs is not None:
+                params["observation_noise_train"] = np.asarray(obs, dtype=np.float32).copy()
+        params["mean"] = float(tr.mean)
+        return params
+
+    def log_marginal_likelihood(self) -> float:
+        """Log marginal likelihood at the learned hyperparameters: -NLL of the
+        training result (gp.py:3642-3646)."""
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained first.")
+        return -float(self._training_result.nll)
+
+    # ------------------------------------------------------------ sampling
+    def sample_posterior(self, X_test, n_samples: int = 1, method: str = "diagonal",
+                         n_rff_features: int = 1024,
+                         rng: Optional[np.random.Generator] = None) -> np.ndarray:
+        """Posterior samples [n_samples, m] (gp.py:3101-3196).
+
+        'diagonal': independent draws mean + std z from the predictive std.
+        'pathwise': Matheron's rule -- an RFF prior draw (device features,
+        pathwise_prior.py) corrected by the engine's solve against the residual
+        y - mu - (f_prior(X) + sqrt(noise) eps) (gp.py:3266-3433), for single
+        RBF / Matern kernels."""
+        if not self._is_trained:
+            raise RuntimeError("GP must be trained before sampling.")
+        if method not in ("diagonal", "pathwise"):
+            raise ValueError(f"method must be 'diagonal' or 'pathwise', got '{method}'")
+        if rng is None:
+            rng = np.random.default_rng()
+        training_route = (self._backend_train_info or {}).get(
+            "training_route", self._training_method or "matrix_free")
+        if method == "pathwise":
+            samples = self._sample_posterior_pathwise(X_test, int(n_samples),
+                                                      int(n_rff_features), rng)
+            self._backend_sample_info = {
+                "requested_method": method,
+                "actual_sampling_method": "pathwise",
+                "actual_sampling_route": "provider_pathwise",
+                "backend_sampling_used": True,
+                "backend_correction_used": True,
+                "backend_correction_route": "predict",
+                "training_route": training_route,
+                "prior_sampler_family": "shared_feature_map",
+                "n_rff_features": int(n_rff_features),
+            }
+            return samples
+        pred = self.predict(X_test)
+        z = rng.standard_normal((int(n_samples), len(pred.mean)))
+        samples = pred.mean[np.newaxis, :] + pred.std[np.newaxis, :] * z
+        self._backend_sample_info = {
+            "requested_method": method,
+            "actual_sampling_method": "diagonal",
+            "actual_sampling_route": "diagonal_from_predictive_std",
+            "backend_sampling_used": True,
+            "backend_correction_used": False,
+            "training_route": training_route,
+        }
+        return samples.astype(np.float32)
+
+    _PATHWISE_TEST_CHUNK = 512   # test points per correction call (gp.py:84)
+
+    def _sample_posterior_pathwise(self, X_test, n_samples: int, n_rff_features: int,
+                                   rng: np.random.Generator) -> np.ndarray:
+        """Per sample: weights w ~ N(0, I_F); prior at the training points plus
+        sqrt(noise) eps; residual r = (y - mu) - that; per test chunk the
+        engine's mean-only prediction against r (max_cg 100, tol 1e-2,
+        rank-10 preconditioner, as the reference passes) gives K* (K + s^2 I)^-1 r,
+        and the sample is mu + f_prior(X*) + that correction.  The Generator
+        is drawn in the reference's order (features, then per sample weights
+        and the noise vector), so a seeded run draws the same prior."""
+        from .pathwise_prior import (build_feature_weights, build_pathwise_feature_map,
+                                     sample_prior_values)
+        kt = self.kernel.kernel_type if self.kernel.operator is None else None
+        if kt not in (KernelType.RBF, KernelType.MATERN12, KernelType.MATERN32,
+                      KernelType.MATERN52) or self.kernel.active_dims is not None \
+                or self._cat_specs:
+            raise NotImplementedError(
+                "pathwise sampling is served for single RBF / Matern kernels; use "
+                "method='diagonal' for kernel trees and mixed kernels")
+        X_test = np.ascontiguousarray(X_test, dtype=np.float32)
+        if X_test.ndim != 2 or X_test.shape[1] != self.dim:
+            raise ValueError(f"X_test must have shape (m, {self.dim})")
+        tr = self._training_result
+        noise = float(tr.noise)
+        mean_val = float(tr.mean)
+        y_centered = self._y_train.astype(np.float32) - np.float32(mean_val)
+        public = np.ascontiguousarray(tr.params, dtype=np.float32)
+        params = self.kernel.to_engine_params(public)
+        kind = {KernelType.RBF: 0, KernelType.MATERN52: 1, KernelType.MATERN12: 2,
+                KernelType.MATERN32: 3}[kt]
+        fmap = build_pathwise_feature_map(kind, public, input_dim=self.dim,
+                                          n_features=n_rff_features, rng=rng,
+                                          ard=self.kernel.ard_dim is not None)
+        n, m = self._X_train.shape[0], X_test.shape[0]
+        samples = np.empty((n_samples, m), dtype=np.float32)
+        noise_scale = np.float32(np.sqrt(max(noise, 0.0)))
+        rank = _prediction_lanczos_rank(getattr(tr, "lanczos_rank", 0), self._training_method,
+                                        self.ard)
+        info = self._provider_for_prediction(params, noise)
+        chunk = min(self._PATHWISE_TEST_CHUNK, max(m, 1))
+        for s_i in range(n_samples):
+            w = build_feature_weights(fmap, 1, rng)
+            prior_train = sample_prior_values(fmap, self._X_train, w)[0]
+            obs_prior = prior_train + noise_scale * rng.standard_normal(n).astype(np.float32)
+            residual = np.ascontiguousarray(y_centered - obs_prior, dtype=np.float32)
+            alpha = None
+            for start in range(0, m, chunk):
+                Xc = np.ascontiguousarray(X_test[start:start + chunk])
+                prior_chunk = sample_prior_values(fmap, Xc, w)[0]
+                args = [info, residual, Xc, params, noise, 0.0, 0, 100, 1e-2, 10, rank,
+                        bool(self._provider_state_current), 0]
+                if alpha is not None:     # one solve per sample, reused by every chunk
+                    args.append(alpha)
+                res = self._engine.predict(*args)
+                self._provider_state_current = True
+                if alpha is None and res.get("cached_alpha") is not None:
+                    alpha = np.ascontiguousarray(res["cached_alpha"], dtype=np.float32)
+                correction = np.asarray(res["mean"], dtype=np.float32)
+                samples[s_i, start:start + chunk] = np.float32(mean_val) + prior_chunk + correction
+        return samples
 
     # ------------------------------------------------------------ cache
     def _cache_signature(self, prediction_method, variance_method, sc, params, noise, mean):

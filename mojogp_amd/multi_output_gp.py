@@ -593,6 +593,31 @@ class MultiOutputLMCGP:
             mean=mean, variance=variance,
             std=np.sqrt(variance) if variance is not None else None)
 
+    def predict_latent(self, X_test, return_var: bool = False, return_std: bool = False,
+                       variance_method: str = "love", **kwargs):
+        """p(f_test | y_train) of every task (multi_output_gp.py:5558-5577)."""
+        return self.predict(X_test, return_var=return_var, return_std=return_std,
+                            variance_method=variance_method, **kwargs)
+
+    def predict_observed(self, X_test, observation_noise=None, noise_group_test=None,
+                         return_var: bool = False, return_std: bool = False,
+                         variance_method: str = "love", **kwargs):
+        """p(y_test | y_train) with explicit test-point noise variances [m, T];
+        training noise is never reused for new points
+        (multi_output_gp.py:5579-5609)."""
+        latent = self.predict(X_test, variance_method=variance_method, **kwargs)
+        noise = _resolve_observed_noise(latent.mean.shape[0], latent.mean.shape[1],
+                                        observation_noise, noise_group_test, None)
+        var = std = None
+        if latent.variance is not None:
+            var = np.ascontiguousarray(latent.variance + noise, dtype=np.float32)
+            std = np.sqrt(var)
+        if return_var:
+            return latent.mean, var
+        if return_std:
+            return latent.mean, std
+        return MultiOutputPredictionResult(mean=latent.mean, variance=var, std=std)
+
     def exact_variance(self, X_test, *, max_cg_iter: Optional[int] = None,
                        cg_tol: Optional[float] = None, block_points: int = 0) -> np.ndarray:
         """Exact joint posterior variance [m, T] with the task noise

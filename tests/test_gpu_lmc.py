@@ -389,6 +389,17 @@ def test_multi_output_lmcgp_surface(tmp_path):
     mean_e, var_e = gp.predict(Xs, return_var=True, variance_method="exact")
     assert mean.shape == (25, T) and np.all(std > 0) and np.all(var_e > 0)
     np.testing.assert_allclose(mean, mean_e, rtol=1e-5, atol=1e-6)
+    # latent / observed prediction (multi_output_gp.py:5558-5609)
+    m_l, v_l = gp.predict_latent(Xs, return_var=True, variance_method="exact")
+    np.testing.assert_array_equal(m_l, mean_e)
+    np.testing.assert_array_equal(v_l, var_e)
+    obs = np.full((25, T), 0.03, np.float32)
+    m_o, v_o = gp.predict_observed(Xs, observation_noise=obs, return_var=True,
+                                   variance_method="exact")
+    np.testing.assert_array_equal(m_o, mean_e)
+    np.testing.assert_allclose(v_o, var_e + 0.03, rtol=1e-6)
+    with pytest.raises(ValueError, match="observation_noise must have shape"):
+        gp.predict_observed(Xs, observation_noise=obs[:, :1], variance_method="exact")
     s1 = gp.sample_posterior(Xs, n_samples=64, method="pathwise", rng=np.random.default_rng(5))
     s2 = gp.sample_posterior(Xs, n_samples=64, method="pathwise", rng=np.random.default_rng(5))
     assert s1.shape == (64, 25, T)
