@@ -368,6 +368,18 @@ def _lmc_c5(repeats: int, warmup: int):
     }, (X, V[:1])
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (first /proc/cpuinfo "model name" line)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _cpu_baseline_c5(X, V1, target_s: float):
     """Reference-order fp32 C restatement of the config-5 structured product on
     a bounded sample of rows: both latents' (K_s V) rows for the 64 columns
@@ -393,6 +405,7 @@ def _cpu_baseline_c5(X, V1, target_s: float):
         "value": rows * C5_N * _c5_flops_per_pair() / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "cpu_model": _cpu_model(),
         "kind": "port",
         "sample": f"rows [0,{rows}) of both latents' products (64 columns each) of the "
                   f"config-5 structured matvec; {dt:.1f} s on {threads} threads",
@@ -549,6 +562,7 @@ def _cpu_baseline(X, V, params, noise, target_s: float):
         "value": flops / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "cpu_model": _cpu_model(),
         "kind": "port",
         "sample": f"rows [0,{rows}) of the config-3 matvec ({rows}x{N} pairs, t={T}); "
                   f"{dt:.1f} s on {threads} threads",

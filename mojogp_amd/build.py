@@ -44,9 +44,9 @@ HIP_FLAGS = [
 ]
 
 
-# rocBLAS serves the fp64 feature GEMM of the pathwise prior samples; hiprtc
-# compiles the per-tree product kernels (tree_jit.hip) at run time.
-LINK_LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"]
+# hiprtc compiles the per-tree product kernels (tree_jit.hip) at run time; no
+# vendor math library is linked.
+LINK_LIBS = ["-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def _hipcc() -> str:
