@@ -20,6 +20,8 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h16 __attribute__((ext_vector_type(16)));
 typedef float f2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void g_void;
 
 namespace {
 
@@ -52,15 +54,18 @@ __device__ __forceinline__ h8 last8(const h16& v) {
   return __builtin_shufflevector(v, v, 8, 9, 10, 11, 12, 13, 14, 15);
 }
 
-__global__ void k_zero_u32(uint32_t* __restrict__ p, int64_t count) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < count) p[i] = 0u;
+// Fragment layout of the full K and of the packed right-hand sides (dense.h):
+// the h8 index of row (or right-hand side) i, columns 8 g .. 8 g + 7, part p.
+__host__ __device__ inline int64_t frag_index(int64_t i, int64_t g, int64_t nks, int p) {
+  const int64_t lane = (i & 15) + 16 * (g & 3);
+  return (((i >> 4) * nks + (g >> 2)) * 2 + p) * 64 + lane;
 }
 
-// dst[r * gpr + g] = split of 2^shift src[r * n + 8 g + e], e = 0..7 (zero
-// past n), for r < nrows, g < gpr.  vec4: n a multiple of 4 (16-byte rows).
-__global__ void k_dense_pack(const float* __restrict__ src, int64_t nrows, int64_t n,
-                             int64_t gpr, int shift, int vec4, h16* __restrict__ dst) {
+// Rows [r0, r0 + nrows) of 2^shift src (row stride n, zero past column n) into
+// the fragment layout; one thread per (row, 8-column group).  vec4: n a
+// multiple of 4 (16-byte rows).
+__global__ void k_dense_pack(const float* __restrict__ src, int64_t r0, int64_t nrows, int64_t n,
+                             int64_t gpr, int shift, int vec4, h8* __restrict__ dst) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= nrows * gpr) return;
   const int64_t r = idx / gpr, g = idx - r * gpr;
@@ -81,7 +86,22 @@ __global__ void k_dense_pack(const float* __restrict__ src, int64_t nrows, int64
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = ldexpf(x[e], shift);
-  dst[idx] = split16(x);
+  const h16 v = split16(x);
+  const int64_t nks = gpr / 4;
+  dst[frag_index(r0 + r, g, nks, 0)] = first8(v);
+  dst[frag_index(r0 + r, g, nks, 1)] = last8(v);
+}
+
+// Zero rows [r0, r1) of the fragment layout (padding rows).
+__global__ void k_dense_zero_rows(int64_t r0, int64_t r1, int64_t gpr, h8* __restrict__ dst) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (r1 - r0) * gpr) return;
+  const int64_t r = r0 + idx / gpr, g = idx % gpr;
+  h8 z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z[e] = (_Float16)0.0f;
+  dst[frag_index(r, g, gpr / 4, 0)] = z;
+  dst[frag_index(r, g, gpr / 4, 1)] = z;
 }
 
 // part[c * chunks + b] = max |V[c][i]| over row chunk b (float bits; grid =
@@ -114,11 +134,46 @@ __global__ void k_dense_absmax_final(const uint32_t* __restrict__ part, int chun
   if (lane == 0) colmax[c] = mx;
 }
 
-// Vp[c * gpr + g] = split of 2^s_c V[c][8 g + e] (zero for c >= ncols or past
-// n), s_c from the column maximum.
+// Right-hand sides in group order for the symmetric route: Vn[c * gpr + g] =
+// split of 2^s_c V[c][8 g + e] (zero for c >= ncols or past n).
+__global__ void k_dense_pack_rhs_groups(const float* __restrict__ V, int64_t n, int ncols,
+                                        int cpad, int64_t gpr,
+                                        const uint32_t* __restrict__ colmax, int vec4,
+                                        h16* __restrict__ Vn) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)cpad * gpr) return;
+  const int c = (int)(idx / gpr);
+  const int64_t g = idx - (int64_t)c * gpr, j0 = 8 * g;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+  if (c < ncols) {
+    const float* src = V + (int64_t)c * n;
+    if (vec4 && j0 + 8 <= n) {
+      const f4 a = *reinterpret_cast<const f4*>(src + j0);
+      const f4 b = *reinterpret_cast<const f4*>(src + j0 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = a[e];
+        x[4 + e] = b[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = j0 + e < n ? src[j0 + e] : 0.0f;
+    }
+    const int sh = scale_shift(__uint_as_float(colmax[c]));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = ldexpf(x[e], sh);
+  }
+  Vn[idx] = split16(x);
+}
+
+// Right-hand sides in the fragment layout: column c, group g holds the split
+// of 2^s_c V[c][8 g + e] (zero for c >= ncols or past n), s_c from the column
+// maximum.
 __global__ void k_dense_pack_rhs(const float* __restrict__ V, int64_t n, int ncols, int cpad,
                                  int64_t gpr, const uint32_t* __restrict__ colmax, int vec4,
-                                 h16* __restrict__ Vp) {
+                                 h8* __restrict__ Vp) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)cpad * gpr) return;
   const int c = (int)(idx / gpr);
@@ -145,23 +200,25 @@ __global__ void k_dense_pack_rhs(const float* __restrict__ V, int64_t n, int nco
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = ldexpf(x[e], sh);
   }
-  Vp[idx] = split16(x);
+  const h16 v = split16(x);
+  Vp[frag_index(c, g, gpr / 4, 0)] = first8(v);
+  Vp[frag_index(c, g, gpr / 4, 1)] = last8(v);
 }
 
-// D = K V over the column groups [g0, g1) of split blockIdx.z (4 groups = 32
-// columns of K per step).  Wave (wr, wc) of the block computes R row tiles x
-// NCT column tiles of 16: rows i0 + 16 r + m, right-hand sides c0 + 16 ct + n.
-// v_mfma_f32_16x16x32_f16 operands come straight from global memory in MFMA
-// layout: lane l holds K[i0 + 16 r + l%16][8 (g + l/16) .. + 7] (A, both
-// parts in one 32-byte load) and V[c0 + 16 ct + l%16][same columns] (B).  Each
-// tile accumulates Kh.Vh + Kh.Vl + Kl.Vh.  The loads of the next step are
-// issued before this step's MFMAs (two register stages; the address of the
-// prefetch is clamped into the split so no load is conditional).  DIRECT
-// (one split): out[c][i] = 2^-(kshift + s_c) D + noise V[c][i] for i < n,
-// c < ncols; otherwise part[(z cpad + c) npad + i] = D.
+// D = K V over the 32-column steps [s0, s1) of split blockIdx.z (narrow
+// products).  Wave (wr, wc) of the block computes R row tiles x NCT column
+// tiles of 16: rows i0 + 16 r + m, right-hand sides c0 + 16 ct + n.
+// v_mfma_f32_16x16x32_f16 operands come straight from global memory: the
+// fragment layout stores each 16 x 32 operand lane-ordered (hi 1 KB, lo 1 KB),
+// so lane l loads 16 contiguous bytes per part.  Each tile accumulates
+// Kh.Vh + Kh.Vl + Kl.Vh.  The loads of the next step are issued before this
+// step's MFMAs (two register stages; the address of the prefetch is clamped
+// into the split so no load is conditional).  DIRECT (one split):
+// out[c][i] = 2^-(kshift + s_c) D + noise V[c][i] for i < n, c < ncols;
+// otherwise part[(z cpad + c) npad + i] = D.
 template <int R, int NCT, int WR, bool DIRECT>
 __global__ __launch_bounds__(256) void k_dense_mm(
-    const h16* __restrict__ Kp, int64_t gpr, const h16* __restrict__ Vp, int64_t gsplit,
+    const h8* __restrict__ Kp, int64_t nks, const h8* __restrict__ Vp, int64_t ssplit,
     int64_t npad, int cpad, float* __restrict__ part, int64_t n, int ncols, int kshift,
     const uint32_t* __restrict__ colmax, float noise, const float* __restrict__ V,
     float* __restrict__ out) {
@@ -171,47 +228,60 @@ __global__ __launch_bounds__(256) void k_dense_mm(
   const int lm = lane & 15, lq = lane >> 4;
   const int64_t i0 = ((int64_t)blockIdx.x * WR + wr) * (R * 16);
   const int c0 = (blockIdx.y * WC + wc) * (NCT * 16);
-  const int64_t g0 = (int64_t)blockIdx.z * gsplit, g1 = min(gpr, g0 + gsplit);
-  const h16* ka[R];
+  const int64_t s0 = (int64_t)blockIdx.z * ssplit, s1 = min(nks, s0 + ssplit);
+  // fragment (tile t, step s, part p) at ((t nks + s) 2 + p) 64 + lane
+  const h8* ka[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) ka[r] = Kp + (i0 + 16 * r + lm) * gpr + lq;
-  const h16* vb[NCT];
+  for (int r = 0; r < R; ++r) ka[r] = Kp + ((i0 / 16 + r) * nks) * 128 + lane;
+  const h8* vb[NCT];
 #pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) vb[ct] = Vp + (int64_t)(c0 + 16 * ct + lm) * gpr + lq;
+  for (int ct = 0; ct < NCT; ++ct) vb[ct] = Vp + ((int64_t)(c0 / 16 + ct) * nks) * 128 + lane;
   f4 acc[R][NCT];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) acc[r][ct] = f4{0.f, 0.f, 0.f, 0.f};
-  auto load = [&](int64_t g, h16 (&a)[R], h16 (&b)[NCT]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) a[r] = ka[r][g];
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) b[ct] = vb[ct][g];
-  };
-  auto mma = [&](const h16 (&a)[R], const h16 (&b)[NCT]) __attribute__((always_inline)) {
+  auto load = [&](int64_t s, h8 (&ah)[R], h8 (&al)[R], h8 (&bh)[NCT], h8 (&bl)[NCT])
+      __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const h8 ah = first8(a[r]), al = last8(a[r]);  // hi, lo parts
+      ah[r] = ka[r][s * 128];
+      al[r] = ka[r][s * 128 + 64];
+    }
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        const h8 bh = first8(b[ct]), bl = last8(b[ct]);
-        acc[r][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[r][ct], 0, 0, 0);
-        acc[r][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc[r][ct], 0, 0, 0);
-        acc[r][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc[r][ct], 0, 0, 0);
-      }
+    for (int ct = 0; ct < NCT; ++ct) {
+      bh[ct] = vb[ct][s * 128];
+      bl[ct] = vb[ct][s * 128 + 64];
     }
   };
-  if (g0 < g1) {
-    const int64_t glast = g1 - 4;  // (g1 - g0) is a multiple of 4
-    h16 a0[R], b0[NCT], a1[R], b1[NCT];
-    load(g0, a0, b0);
-    for (int64_t g = g0; g < g1; g += 8) {
-      load(min(g + 4, glast), a1, b1);
-      mma(a0, b0);
-      if (g + 4 >= g1) break;
-      load(min(g + 8, glast), a0, b0);
-      mma(a1, b1);
+  auto mma = [&](const h8 (&ah)[R], const h8 (&al)[R], const h8 (&bh)[NCT],
+                 const h8 (&bl)[NCT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc[r][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[r], bh[ct], acc[r][ct], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc[r][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[r], bl[ct], acc[r][ct], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+        acc[r][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[r], bh[ct], acc[r][ct], 0, 0, 0);
+  };
+  if (s0 < s1) {
+    const int64_t slast = s1 - 1;
+    h8 a0h[R], a0l[R], b0h[NCT], b0l[NCT], a1h[R], a1l[R], b1h[NCT], b1l[NCT];
+    load(s0, a0h, a0l, b0h, b0l);
+    for (int64_t s = s0; s < s1; s += 2) {
+      load(min(s + 1, slast), a1h, a1l, b1h, b1l);
+      mma(a0h, a0l, b0h, b0l);
+      if (s + 1 >= s1) break;
+      load(min(s + 2, slast), a0h, a0l, b0h, b0l);
+      mma(a1h, a1l, b1h, b1l);
     }
   }
 #pragma unroll
@@ -233,6 +303,127 @@ __global__ __launch_bounds__(256) void k_dense_mm(
       } else {
         *reinterpret_cast<f4*>(part + ((int64_t)blockIdx.z * cpad + c) * npad + i) = acc[r][ct];
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wide products (ncols > 128, the exact-variance blocks): D = K V for a
+// 128-row x 256-column workgroup tile of 8 waves (2 x 4; each wave 4 x 4
+// tiles of 16 x 16).  Per 32-column step the workgroup's 8 K fragments and 16
+// V fragments (2 KB each, lane-ordered in global memory) are brought into LDS
+// by the global-to-LDS DMA, 6 blocks of 1 KB per wave, into one of three
+// stage buffers (48 KB each), two steps ahead of the MFMAs, so every operand
+// byte crosses L2 once per workgroup instead of once per wave.  Workgroups are
+// ordered for the XCDs: XCD x takes the row blocks x, x + 8, ... and walks
+// them in groups of 8 row blocks x 4 column blocks, so the 32 workgroups an
+// XCD runs at a time share their K rows and V columns in its L2.  The
+// epilogue is the narrow kernel's DIRECT one (one split).
+// ---------------------------------------------------------------------------
+constexpr int kWideWaves = 8;
+constexpr int kWideRowTiles = 8;    // 128 rows per workgroup
+constexpr int kWideColTiles = 16;   // 256 right-hand sides per workgroup
+constexpr int kWideStages = 3;
+constexpr int kWideBlocks = 2 * (kWideRowTiles + kWideColTiles);  // 1-KB blocks per stage
+constexpr int kWideGroupRows = 8, kWideGroupCols = 4;
+
+__global__ __launch_bounds__(64 * kWideWaves) void k_dense_mm_wide(
+    const h8* __restrict__ Kp, int64_t nks, const h8* __restrict__ Vp, int64_t rblocks,
+    int64_t cblocks, int gcols, int64_t n, int ncols, int kshift,
+    const uint32_t* __restrict__ colmax, float noise, const float* __restrict__ V,
+    float* __restrict__ out) {
+  __shared__ h8 lds[kWideStages][kWideBlocks][64];
+  // workgroup -> (row block, column block), XCD-grouped (see above)
+  const int64_t L = blockIdx.x;
+  const int64_t x = L % kXcds, j = L / kXcds;
+  const int64_t rbx = (rblocks - x + kXcds - 1) / kXcds;   // row blocks of XCD x
+  if (j >= rbx * cblocks) return;                          // whole workgroup: no barrier yet
+  const int64_t per_group = (int64_t)kWideGroupRows * cblocks;
+  const int64_t g_r = j / per_group, rem = j - g_r * per_group;
+  const int64_t ga = min((int64_t)kWideGroupRows, rbx - g_r * kWideGroupRows);
+  const int64_t g_c = rem / (ga * gcols), inner = rem - g_c * (ga * gcols);
+  const int64_t rr = g_r * kWideGroupRows + inner / gcols;
+  const int64_t rb = x + kXcds * rr;
+  const int64_t cb = g_c * gcols + inner % gcols;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wr = wave & 1, wc = wave >> 1;        // 2 row x 4 column waves
+  const int64_t rt0 = rb * kWideRowTiles, ct0 = cb * kWideColTiles;
+  // LDS block b of a stage: b < 16: K fragment (row tile b / 2, part b % 2);
+  // b >= 16: V fragment (column tile (b - 16) / 2, part b % 2).
+  auto fill = [&](int st, int64_t s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < kWideBlocks / kWideWaves; ++k) {
+      const int b = wave + kWideWaves * k;
+      const h8* src = b < 2 * kWideRowTiles
+                          ? Kp + (((rt0 + (b >> 1)) * nks + s) * 2 + (b & 1)) * 64
+                          : Vp + (((ct0 + ((b - 2 * kWideRowTiles) >> 1)) * nks + s) * 2 +
+                                  (b & 1)) * 64;
+      __builtin_amdgcn_global_load_lds((const g_void*)(src + lane), (lds_void*)&lds[st][b][0],
+                                       16, 0, 0);
+    }
+  };
+  f4 acc[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[r][c] = f4{0.f, 0.f, 0.f, 0.f};
+  fill(0, 0);
+  if (nks > 1) fill(1, 1);
+  for (int64_t s = 0; s < nks; ++s) {
+    const int st = (int)(s % kWideStages);
+    // this wave's blocks of step s have landed (those of s + 1 may be in
+    // flight); the barrier makes every wave's blocks of step s visible and
+    // frees the buffer of step s - 1 for step s + 2
+    if (s + 1 < nks)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (kWideBlocks / kWideWaves));  // vmcnt <= 6
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);                              // vmcnt = 0
+    __syncthreads();
+    if (s + 2 < nks) fill((int)((s + 2) % kWideStages), s + 2);
+    h8 ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ah[r] = lds[st][2 * (4 * wr + r)][lane];
+      al[r] = lds[st][2 * (4 * wr + r) + 1][lane];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      bh[c] = lds[st][2 * kWideRowTiles + 2 * (4 * wc + c)][lane];
+      bl[c] = lds[st][2 * kWideRowTiles + 2 * (4 * wc + c) + 1][lane];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[r], bh[c], acc[r][c], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[r], bl[c], acc[r][c], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[r], bh[c], acc[r][c], 0, 0, 0);
+  }
+  const int lm = lane & 15, lq = lane >> 4;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int64_t col = (ct0 + 4 * wc + c) * 16 + lm;
+    if (col >= ncols) continue;
+    const double sc = ldexp(1.0, -(kshift + scale_shift(__uint_as_float(colmax[col]))));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t i = (rt0 + 4 * wr + r) * 16 + 4 * lq;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (i + q < n) {
+          const int64_t o = col * n + i + q;
+          out[o] = fmaf(noise, V[o], (float)(sc * (double)acc[r][c][q]));
+        }
     }
   }
 }
@@ -577,10 +768,10 @@ void dense_alloc(DenseK& K, int64_t n, float kmax, hipStream_t st) {
   const int64_t gpr = K.groups_per_row();
   K.data.ensure((size_t)K.npad * (size_t)gpr * 8);
   // padding rows [n, npad); padding columns are written by the row packing
-  const int64_t pad = (K.npad - n) * gpr * 8;
+  const int64_t pad = (K.npad - n) * gpr;
   if (pad > 0) {
-    hipLaunchKernelGGL(k_zero_u32, dim3((unsigned)ceil_div(pad, 256)), dim3(256), 0, st,
-                       K.data.ptr + (size_t)n * gpr * 8, pad);
+    hipLaunchKernelGGL(k_dense_zero_rows, dim3((unsigned)ceil_div(pad, 256)), dim3(256), 0, st,
+                       n, K.npad, gpr, reinterpret_cast<h8*>(K.data.ptr));
     MGP_HIP_CHECK(hipGetLastError());
   }
 }
@@ -591,9 +782,8 @@ void dense_pack_rows(const float* rows, int64_t r0, int64_t nrows, DenseK& K, hi
   const int64_t gpr = K.groups_per_row();
   const int64_t total = nrows * gpr;
   const int vec4 = (K.n % 4 == 0 && reinterpret_cast<uintptr_t>(rows) % 16 == 0) ? 1 : 0;
-  h16* dst = reinterpret_cast<h16*>(K.data.ptr) + r0 * gpr;
   hipLaunchKernelGGL(k_dense_pack, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, rows,
-                     nrows, K.n, gpr, K.shift, vec4, dst);
+                     r0, nrows, K.n, gpr, K.shift, vec4, reinterpret_cast<h8*>(K.data.ptr));
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -634,8 +824,8 @@ void dense_sym_forward(const DenseK& K, const float* V, int ncols, float noise, 
   const int64_t vtot = 16 * gpr;
   h16* vn = reinterpret_cast<h16*>(w.vpack.ensure((size_t)vtot * 8));
   const int vec4 = (n % 4 == 0 && reinterpret_cast<uintptr_t>(V) % 16 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(k_dense_pack_rhs, dim3((unsigned)ceil_div(vtot, 256)), dim3(256), 0, st, V,
-                     n, ncols, 16, gpr, colmax, vec4, vn);
+  hipLaunchKernelGGL(k_dense_pack_rhs_groups, dim3((unsigned)ceil_div(vtot, 256)), dim3(256), 0,
+                     st, V, n, ncols, 16, gpr, colmax, vec4, vn);
   const int64_t pairs = npad / 32;
   h8* vp = reinterpret_cast<h8*>(w.vpair.ensure((size_t)pairs * 2 * 64 * 4));
   hipLaunchKernelGGL(k_dense_pack_pair, dim3((unsigned)ceil_div(pairs * 64, 256)), dim3(256), 0,
@@ -660,7 +850,8 @@ void dense_sym_forward(const DenseK& K, const float* V, int ncols, float noise, 
 void dense_forward(const DenseK& K, const float* V, int ncols, float noise, float* out,
                    DenseWorkspace& w, hipStream_t st) {
   MGP_REQUIRE(ncols >= 1, "ncols must be >= 1");
-  const int64_t n = K.n, npad = K.npad, gpr = K.groups_per_row();
+  const int64_t n = K.n, npad = K.npad, gpr = K.groups_per_row(), nks = gpr / 4;
+  const bool wide = ncols > 128;
   // block shape: rows x right-hand sides per workgroup
   int R = 4, NCT, WR;
   if (ncols <= 16) { NCT = 1; WR = 4; }
@@ -668,9 +859,11 @@ void dense_forward(const DenseK& K, const float* V, int ncols, float noise, floa
   else if (ncols <= 64) { NCT = 4; WR = 4; }
   else { NCT = 4; WR = 2; }
   const int WC = 4 / WR;
-  const int64_t brows = (int64_t)WR * R * 16, bcols = (int64_t)WC * NCT * 16;
+  const int64_t brows = (int64_t)WR * R * 16;
+  const int64_t bcols = wide ? 16 * kWideColTiles : (int64_t)WC * NCT * 16;
   const int cpad = (int)round_up(ncols, bcols);
-  const int64_t rblocks = npad / brows, cblocks = cpad / bcols;
+  const int64_t rblocks = wide ? npad / (16 * kWideRowTiles) : npad / brows;
+  const int64_t cblocks = cpad / bcols;
 
   // column maxima and packed right-hand sides
   const int chunks = (int)std::min<int64_t>(64, std::max<int64_t>(1, ceil_div(n, 4096)));
@@ -681,24 +874,34 @@ void dense_forward(const DenseK& K, const float* V, int ncols, float noise, floa
   hipLaunchKernelGGL(k_dense_absmax_final, dim3((unsigned)ncols), dim3(64), 0, st, cpart, chunks,
                      colmax);
   const int64_t vtot = (int64_t)cpad * gpr;
-  h16* vp = reinterpret_cast<h16*>(w.vpack.ensure((size_t)vtot * 8));
+  h8* vp = reinterpret_cast<h8*>(w.vpack.ensure((size_t)vtot * 8));
   const int vec4 = (n % 4 == 0 && reinterpret_cast<uintptr_t>(V) % 16 == 0) ? 1 : 0;
   hipLaunchKernelGGL(k_dense_pack_rhs, dim3((unsigned)ceil_div(vtot, 256)), dim3(256), 0, st, V,
                      n, ncols, cpad, gpr, colmax, vec4, vp);
   MGP_HIP_CHECK(hipGetLastError());
+  const h8* kp = reinterpret_cast<const h8*>(K.data.ptr);
 
-  // splits of the K columns: >= 2048 workgroups while every split keeps >= 32
-  // groups (256 columns of K)
+  if (wide) {
+    const int gcols = cblocks % kWideGroupCols == 0 ? kWideGroupCols : (cblocks % 2 == 0 ? 2 : 1);
+    const int64_t per_xcd = ceil_div(rblocks, kXcds) * cblocks;
+    hipLaunchKernelGGL(k_dense_mm_wide, dim3((unsigned)(per_xcd * kXcds)),
+                       dim3(64 * kWideWaves), 0, st, kp, nks, vp, rblocks, cblocks, gcols, n,
+                       ncols, K.shift, colmax, noise, V, out);
+    MGP_HIP_CHECK(hipGetLastError());
+    return;
+  }
+
+  // splits of the K columns: >= 2048 workgroups while every split keeps >= 8
+  // steps (256 columns of K)
   int64_t splits = 1;
-  while (rblocks * cblocks * splits < 2048 && gpr / (splits * 2) >= 32 && splits < 64) splits *= 2;
-  const int64_t gsplit = round_up(ceil_div(gpr, splits), 4);
-  splits = ceil_div(gpr, gsplit);
+  while (rblocks * cblocks * splits < 2048 && nks / (splits * 2) >= 8 && splits < 64) splits *= 2;
+  const int64_t ssplit = ceil_div(nks, splits);
+  splits = ceil_div(nks, ssplit);
   float* part = nullptr;
   if (splits > 1) part = w.part.ensure((size_t)splits * cpad * npad);
-  const h16* kp = reinterpret_cast<const h16*>(K.data.ptr);
   const dim3 grid((unsigned)rblocks, (unsigned)cblocks, (unsigned)splits);
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, kp, gpr, vp, gsplit, npad, cpad, part, n,
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, kp, nks, vp, ssplit, npad, cpad, part, n,
                        ncols, K.shift, colmax, noise, V, out);
   };
 #define MGP_DENSE(NCT_, WR_)                                                          \
