@@ -223,6 +223,50 @@ def _c4_product_only():
             "dense_matvec_ms_16_min": round(float(np.min(t)), 4)}
 
 
+def _c4_wide_product_only():
+    """The config-4 4096-column dense product alone (profiling): one
+    materialize (as _c4_product_only), the full K filled by a warm-up
+    product, then 3 timed products of 4096 columns (the exact-variance
+    block)."""
+    from mojogp_amd._provider import NativeProvider, KIND_RBF
+    rng = np.random.default_rng(0)
+    n = 40_000
+    X = rng.uniform(-2, 2, size=(n, 4)).astype(np.float32)
+    prov = NativeProvider(KIND_RBF, False, X, np.array([1.5, 1.0], np.float32), 0.01)
+    try:
+        prov.materialize()
+        V = rng.normal(size=(4096, n)).astype(np.float32)
+        t, _, _ = prov.benchmark_forward(V, 3, 1)
+    finally:
+        prov.close()
+    return {"dense_matvec_ms_4096_mean": round(float(np.mean(t)), 3),
+            "dense_matvec_ms_4096_min": round(float(np.min(t)), 3)}
+
+
+def _c3_gradient_trace_only():
+    """The config-3 gradient trace alone (profiling): the matrix-core trace
+    sum_ab dK_p[a,b] (Lf Rf^T)_ab over N = 250k, d = 16, Matern-5/2 ARD with
+    16 weight columns (the BBMM gradient step's shape: alpha and 15 probe
+    solves), 1 warm-up and 5 timed calls through mgp_gradient_trace."""
+    from mojogp_amd._provider import NativeProvider, KIND_MATERN52
+    X, _, params, noise = _make_inputs()
+    rng = np.random.default_rng(1)
+    L = rng.normal(size=(T, N)).astype(np.float32)
+    R = rng.normal(size=(T, N)).astype(np.float32)
+    prov = NativeProvider(KIND_MATERN52, True, X, params, noise)
+    try:
+        prov.gradient_trace(L, R)
+        t = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            prov.gradient_trace(L, R)
+            t.append((time.perf_counter() - t0) * 1e3)
+    finally:
+        prov.close()
+    return {"gradient_trace_ms_mean": round(float(np.mean(t)), 3),
+            "gradient_trace_ms_min": round(float(np.min(t)), 3)}
+
+
 def _c4_materialized():
     """Config 4: RBF (isotropic) N=40k d=4 on the materialized route (dense K as a
     two-term fp16 split: the symmetric half, 3.25 GB, for products of <= 16
@@ -582,6 +626,10 @@ def main(argv=None) -> int:
                          "products)")
     ap.add_argument("--c4-product", action="store_true",
                     help="only the config-4 16-column dense product (profiling)")
+    ap.add_argument("--c4-wide", action="store_true",
+                    help="only the config-4 4096-column dense product (profiling)")
+    ap.add_argument("--c3-grad", action="store_true",
+                    help="only the config-3 gradient trace, 16 columns (profiling)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the mBCG-iteration and fit() measurements")
     ap.add_argument("--mbcg-only", action="store_true",
@@ -605,6 +653,12 @@ def main(argv=None) -> int:
         return 0
     if args.c4_product:
         print(json.dumps(_c4_product_only()), flush=True)
+        return 0
+    if args.c4_wide:
+        print(json.dumps(_c4_wide_product_only()), flush=True)
+        return 0
+    if args.c3_grad:
+        print(json.dumps(_c3_gradient_trace_only()), flush=True)
         return 0
     if args.mbcg_only:
         X, _, params, noise = _make_inputs()
