@@ -271,8 +271,9 @@ float dot_f(const float* a, const float* b, int64_t n, DevBuf<double>& part, hip
 CGScalars CGWork::scalars(int ncols) {
   CGScalars s;
   s.rz_old = scal.ptr;
-  s.alpha = scal.ptr + ncols;
-  s.beta = scal.ptr + 2 * ncols;
+  s.rz_next = scal.ptr + ncols;
+  s.alpha = scal.ptr + 2 * ncols;
+  s.beta = scal.ptr + 3 * ncols;
   s.hist_alpha = hist_a.ptr;
   s.hist_beta = hist_b.ptr;
   s.done = done.ptr;
@@ -380,7 +381,7 @@ CGResult batched_cg(const CGOperator& op, const float* rhs, int C, int max_iter,
   float* z = pre ? w.z.ensure(nc) : r;
   float* p = w.p.ensure(nc);
   float* Ap = w.Ap.ensure(nc);
-  w.scal.ensure((size_t)3 * C);
+  w.scal.ensure((size_t)4 * C);
   const int mt = std::max(max_tridiag, 1);
   w.hist_a.ensure((size_t)mt * C);
   w.hist_b.ensure((size_t)mt * C);
@@ -416,13 +417,10 @@ CGResult batched_cg(const CGOperator& op, const float* rhs, int C, int max_iter,
     op.matvec(p, C, Ap);
     coldot_partial(p, Ap, n, C, nb, pa, st);
     cg_update(x, r, p, Ap, n, C, nb, pa, s, prr, st);  // alpha from pAp; r.r partials
-    if (pre) {
-      op.precond(r, C, z, pb, nb);
-      cg_beta(pb, nb, C, s, iter, max_tridiag, st);
-    } else {
-      cg_beta(prr, nb, C, s, iter, max_tridiag, st);
-    }
-    cg_pupdate(p, z, n, C, s, st);
+    if (pre) op.precond(r, C, z, pb, nb);
+    // beta from the r.z partials (r.r without a preconditioner), p update
+    cg_pupdate(p, z, n, C, nb, pre ? pb : prr, s, iter, max_tridiag, st);
+    std::swap(s.rz_old, s.rz_next);
     if (iter < max_tridiag) tridiag_size = iter + 1;
     if (iter >= 10 && (((iter + 1) % 10) == 0 || iter == max_iter - 1)) {
       cg_mean_resnorm(prr, nb, C, w.resn.ptr, st);

@@ -22,7 +22,8 @@ void coldot_finalize(const double* part, int nb, int ncols, double* out, hipStre
 // ---------------------------------------------------------------- batched CG
 // Per-column scalars live in one device block (CGScalars).
 struct CGScalars {
-  float* rz_old;   // [C]
+  float* rz_old;   // [C] r.z of the current iteration
+  float* rz_next;  // [C] r.z of the next one (the caller swaps the two)
   float* alpha;    // [C]
   float* beta;     // [C]
   float* hist_alpha;  // [max_tridiag][C]
@@ -36,13 +37,12 @@ struct CGScalars {
 void cg_update(float* x, float* r, const float* p, const float* Ap, int64_t n,
                int ncols, int nb, const double* pap_part, CGScalars s, double* rr_part,
                hipStream_t st);
-// beta = safe(rz_new / rz_old), rz_old = rz_new (cg_solver.mojo:211-255);
-// stores alpha/beta into the history slot `iter` when iter < max_tridiag.
-void cg_beta(const double* rz_part, int nb, int ncols, CGScalars s, int iter,
-             int max_tridiag, hipStream_t st);
-// p = z + beta p (cg_solver.mojo:108-136)
-void cg_pupdate(float* p, const float* z, int64_t n, int ncols, CGScalars s,
-                hipStream_t st);
+// beta = safe(rz_new / rz_old) from the rz partials, s.rz_next = rz_new
+// (cg_solver.mojo:211-255), alpha / beta into the history slot `iter` when
+// iter < max_tridiag, then p = z + beta p (cg_solver.mojo:108-136).  The
+// caller swaps s.rz_old and s.rz_next before the next iteration.
+void cg_pupdate(float* p, const float* z, int64_t n, int ncols, int nb, const double* rz_part,
+                CGScalars s, int iter, int max_tridiag, hipStream_t st);
 // mean_c sqrt(rr_c) into *out (cg_solver.mojo:446-543)
 void cg_mean_resnorm(const double* rr_part, int nb, int ncols, float* out,
                      hipStream_t st);

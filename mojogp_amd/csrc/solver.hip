@@ -108,82 +108,107 @@ __global__ __launch_bounds__(64) void k_coldot_w(const float* __restrict__ a,
   if (lane == 0) part[(int64_t)c * nb + blockIdx.x] = acc;
 }
 
-// alpha_c = safe(rz_old / sum of pAp partials) (cg_solver.mojo:181-209): one
-// wave per column (grid = ncols, 64 threads).
-__global__ void k_cg_alpha(const double* __restrict__ pap_part, int nb, CGScalars s) {
-  const int c = blockIdx.x;
-  const float pap = (float)wave_part_sum(pap_part, c, nb);
-  if (threadIdx.x != 0) return;
-  const float rz = s.rz_old[c];
-  s.alpha[c] = (is_nan(rz) || is_nan(pap) || pap < 1e-10f) ? 0.0f : rz / pap;
-}
-
-// x += alpha p, r -= alpha Ap with the reference skip rules
-// (cg_solver.mojo:138-179) and rr partials of the updated r.
+// alpha_c = safe(rz_old_c / sum of the pAp partials) (cg_solver.mojo:181-209),
+// then x += alpha p, r -= alpha Ap with the reference skip rules
+// (cg_solver.mojo:138-179) and rr partials of the updated r.  One wave per
+// (group of G consecutive chunks, column c): each wave forms alpha itself
+// with the fixed-order wave sum of the partials (every wave obtains the same
+// value), the first wave of the column stores it; chunk partials are summed
+// per chunk exactly as one wave per chunk would.
 __global__ __launch_bounds__(64) void k_cg_update_w(float* __restrict__ x, float* __restrict__ r,
                                                     const float* __restrict__ p,
                                                     const float* __restrict__ Ap, int64_t n,
-                                                    int nb, int vec4, CGScalars s,
-                                                    double* __restrict__ rr_part) {
+                                                    int nb, int G, int vec4,
+                                                    const double* __restrict__ pap_part,
+                                                    CGScalars s, double* __restrict__ rr_part) {
   const int c = blockIdx.y, lane = threadIdx.x;
-  const float a = s.alpha[c];
+  const float pap = (float)wave_part_sum(pap_part, c, nb);
+  const float rz = s.rz_old[c];
+  const float a = (is_nan(rz) || is_nan(pap) || pap < 1e-10f) ? 0.0f : rz / pap;
+  if (blockIdx.x == 0 && lane == 0) s.alpha[c] = a;
   const bool active = !(a == 0.0f || is_nan(a));
   const int64_t chunk = (n + nb - 1) / nb;
-  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   const int64_t off = (int64_t)c * n;
-  double acc = 0.0;
-  auto one = [&](float& xi, float& ri, float pi, float api) __attribute__((always_inline)) {
-    if (active && !is_nan(pi) && !is_nan(api)) {
-      xi += a * pi;
-      ri -= a * api;
-    }
-    acc += (double)ri * (double)ri;
-  };
-  if (vec4) {
-    for (int64_t i = i0 + 4 * lane; i < i1; i += 256) {
-      f4v xv = *reinterpret_cast<const f4v*>(x + off + i);
-      f4v rv = *reinterpret_cast<const f4v*>(r + off + i);
-      const f4v pv = *reinterpret_cast<const f4v*>(p + off + i);
-      const f4v av = *reinterpret_cast<const f4v*>(Ap + off + i);
+  const int b0 = blockIdx.x * G, b1 = min(nb, b0 + G);
+  for (int bb = b0; bb < b1; ++bb) {
+    const int64_t i0 = (int64_t)bb * chunk, i1 = min(n, i0 + chunk);
+    double acc = 0.0;
+    auto one = [&](float& xi, float& ri, float pi, float api) __attribute__((always_inline)) {
+      if (active && !is_nan(pi) && !is_nan(api)) {
+        xi += a * pi;
+        ri -= a * api;
+      }
+      acc += (double)ri * (double)ri;
+    };
+    if (vec4) {
+      for (int64_t i = i0 + 4 * lane; i < i1; i += 256) {
+        f4v xv = *reinterpret_cast<const f4v*>(x + off + i);
+        f4v rv = *reinterpret_cast<const f4v*>(r + off + i);
+        const f4v pv = *reinterpret_cast<const f4v*>(p + off + i);
+        const f4v av = *reinterpret_cast<const f4v*>(Ap + off + i);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float xi = xv[e], ri = rv[e];
-        one(xi, ri, pv[e], av[e]);
-        xv[e] = xi;
-        rv[e] = ri;
+        for (int e = 0; e < 4; ++e) {
+          float xi = xv[e], ri = rv[e];
+          one(xi, ri, pv[e], av[e]);
+          xv[e] = xi;
+          rv[e] = ri;
+        }
+        if (active) {
+          *reinterpret_cast<f4v*>(x + off + i) = xv;
+          *reinterpret_cast<f4v*>(r + off + i) = rv;
+        }
       }
-      if (active) {
-        *reinterpret_cast<f4v*>(x + off + i) = xv;
-        *reinterpret_cast<f4v*>(r + off + i) = rv;
+    } else {
+      for (int64_t i = i0 + lane; i < i1; i += 64) {
+        float xi = x[off + i], ri = r[off + i];
+        one(xi, ri, p[off + i], Ap[off + i]);
+        if (active) {
+          x[off + i] = xi;
+          r[off + i] = ri;
+        }
       }
     }
-  } else {
-    for (int64_t i = i0 + lane; i < i1; i += 64) {
-      float xi = x[off + i], ri = r[off + i];
-      one(xi, ri, p[off + i], Ap[off + i]);
-      if (active) {
-        x[off + i] = xi;
-        r[off + i] = ri;
-      }
-    }
+    acc = wave_sum_d(acc);
+    if (lane == 0) rr_part[(int64_t)c * nb + bb] = acc;
   }
-  acc = wave_sum_d(acc);
-  if (lane == 0) rr_part[(int64_t)c * nb + blockIdx.x] = acc;
 }
 
-// p = z + beta p (cg_solver.mojo:108-136)
+// beta_c = safe(rz_new_c / rz_old_c) from the rz partials, rz_next_c = rz_new_c
+// (cg_solver.mojo:211-255; rz_old and rz_next are distinct arrays, swapped
+// by the caller between iterations, so no wave reads a value another wave
+// of this launch writes), the alpha / beta history slot `iter` when
+// iter < max_tridiag, then p = z + beta p (cg_solver.mojo:108-136).  One wave
+// per (group of G consecutive chunks, column c), beta formed by every wave
+// with the same fixed-order sum and stored by the column's first wave.
 __global__ __launch_bounds__(64) void k_cg_pupdate_w(float* __restrict__ p,
                                                      const float* __restrict__ z, int64_t n,
-                                                     int nb, int vec4, CGScalars s) {
+                                                     int nb, int G, int vec4,
+                                                     const double* __restrict__ rz_part,
+                                                     int ncols, CGScalars s, int iter,
+                                                     int max_tridiag) {
   const int c = blockIdx.y, lane = threadIdx.x;
-  const float b = s.beta[c];
+  const float rz_new = (float)wave_part_sum(rz_part, c, nb);
+  const float rz_old = s.rz_old[c];
+  float b = 0.0f;
+  if (!is_nan(rz_old) && !is_nan(rz_new) && rz_old >= 1e-20f) {
+    b = rz_new / (rz_old + 1e-20f);
+    if (b < 0.0f || is_nan(b)) b = 0.0f;
+  }
+  if (blockIdx.x == 0 && lane == 0) {
+    s.beta[c] = b;
+    s.rz_next[c] = is_nan(rz_new) ? 0.0f : rz_new;
+    if (iter < max_tridiag) {
+      s.hist_alpha[(int64_t)iter * ncols + c] = s.alpha[c];
+      s.hist_beta[(int64_t)iter * ncols + c] = b;
+    }
+  }
   const bool plain = (b == 0.0f || is_nan(b));
   const int64_t chunk = (n + nb - 1) / nb;
-  const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   const int64_t off = (int64_t)c * n;
   auto one = [&](float po, float zi) __attribute__((always_inline)) -> float {
     return (plain || is_nan(po)) ? zi : zi + b * po;
   };
+  const int64_t i0 = (int64_t)blockIdx.x * G * chunk, i1 = min(n, i0 + G * chunk);
   if (vec4) {
     for (int64_t i = i0 + 4 * lane; i < i1; i += 256) {
       f4v pv = *reinterpret_cast<const f4v*>(p + off + i);
@@ -194,26 +219,6 @@ __global__ __launch_bounds__(64) void k_cg_pupdate_w(float* __restrict__ p,
     }
   } else {
     for (int64_t i = i0 + lane; i < i1; i += 64) p[off + i] = one(p[off + i], z[off + i]);
-  }
-}
-
-// One wave per column (grid = ncols, 64 threads).
-__global__ void k_cg_beta(const double* __restrict__ rz_part, int nb, int ncols,
-                          CGScalars s, int iter, int max_tridiag) {
-  const int c = blockIdx.x;
-  const float rz_new = (float)wave_part_sum(rz_part, c, nb);
-  if (threadIdx.x != 0) return;
-  const float rz_old = s.rz_old[c];
-  float beta = 0.0f;
-  if (!is_nan(rz_old) && !is_nan(rz_new) && rz_old >= 1e-20f) {
-    beta = rz_new / (rz_old + 1e-20f);
-    if (beta < 0.0f || is_nan(beta)) beta = 0.0f;
-  }
-  s.beta[c] = beta;
-  s.rz_old[c] = is_nan(rz_new) ? 0.0f : rz_new;
-  if (iter < max_tridiag) {
-    s.hist_alpha[(int64_t)iter * ncols + c] = s.alpha[c];
-    s.hist_beta[(int64_t)iter * ncols + c] = beta;
   }
 }
 
@@ -1318,26 +1323,26 @@ void coldot_finalize(const double* part, int nb, int ncols, double* out, hipStre
   MGP_HIP_CHECK(hipGetLastError());
 }
 
+// Chunks per wave of the CG vector kernels: about 2048 waves in all, so the
+// per-wave reduction of a column's scalar partials stays small next to the
+// vector traffic.
+static int cg_group(int nb, int ncols) {
+  return std::max(1, (nb * ncols) / 2048);
+}
+
 void cg_update(float* x, float* r, const float* p, const float* Ap, int64_t n, int ncols,
                int nb, const double* pap_part, CGScalars s, double* rr_part, hipStream_t st) {
-  hipLaunchKernelGGL(k_cg_alpha, dim3(ncols), dim3(64), 0, st, pap_part, nb, s);
-  hipLaunchKernelGGL(k_cg_update_w, dim3(nb, ncols), dim3(64), 0, st, x, r, p, Ap, n, nb,
-                     vec4_ok(n, nb, {x, r, p, Ap}), s, rr_part);
+  const int G = cg_group(nb, ncols);
+  hipLaunchKernelGGL(k_cg_update_w, dim3((unsigned)ceil_div(nb, G), ncols), dim3(64), 0, st, x, r,
+                     p, Ap, n, nb, G, vec4_ok(n, nb, {x, r, p, Ap}), pap_part, s, rr_part);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
-void cg_beta(const double* rz_part, int nb, int ncols, CGScalars s, int iter,
-             int max_tridiag, hipStream_t st) {
-  hipLaunchKernelGGL(k_cg_beta, dim3(ncols), dim3(64), 0, st, rz_part, nb, ncols, s, iter,
-                     max_tridiag);
-  MGP_HIP_CHECK(hipGetLastError());
-}
-
-void cg_pupdate(float* p, const float* z, int64_t n, int ncols, CGScalars s,
-                hipStream_t st) {
-  const int nb = cg_chunks(n);
-  hipLaunchKernelGGL(k_cg_pupdate_w, dim3(nb, ncols), dim3(64), 0, st, p, z, n, nb,
-                     vec4_ok(n, nb, {p, z}), s);
+void cg_pupdate(float* p, const float* z, int64_t n, int ncols, int nb, const double* rz_part,
+                CGScalars s, int iter, int max_tridiag, hipStream_t st) {
+  const int G = cg_group(nb, ncols);
+  hipLaunchKernelGGL(k_cg_pupdate_w, dim3((unsigned)ceil_div(nb, G), ncols), dim3(64), 0, st, p,
+                     z, n, nb, G, vec4_ok(n, nb, {p, z}), rz_part, ncols, s, iter, max_tridiag);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
