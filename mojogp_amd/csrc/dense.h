@@ -10,11 +10,12 @@
 // by 2^shift (max |K| in [2^14, 2^15), so the e^-20 floor of the clamped
 // kernels stays a normal fp16 number; unclamped RBF tails below that fall into
 // fp16's subnormal range with absolute error <= 2^-25 of the scaled value) and
-// split into hi = RNE16(x), lo = RNE16(x - hi);
-// row i keeps groups of 8 consecutive columns as {hi[8], lo[8]} (32 bytes), so
-// the storage is 4 bytes per entry like fp32 and one 32-byte load per lane is
-// a v_mfma_f32_16x16x32_f16 operand of either part.  Rows and columns are
-// padded with zeros to npad = round_up(n, 256).
+// split into hi = RNE16(x), lo = RNE16(x - hi), 4 bytes per entry like fp32.
+// Both layouts store 8 consecutive columns of one row and one part as a
+// 16-byte unit, lane-ordered so that 64 consecutive units are one 1 KB
+// v_mfma_f32_16x16x32_f16 operand (16 rows x 32 columns) and one load per
+// lane fetches it.  Rows and columns are padded with zeros to
+// npad = round_up(n, 256).
 #pragma once
 
 #include "mgp_common.h"
@@ -24,14 +25,14 @@ namespace mgp {
 struct DenseK {
   int64_t n = 0, npad = 0;
   int shift = 0;              // stored value = K * 2^shift (split)
-  DevBuf<uint32_t> data;      // [npad][npad / 8] groups of 16 fp16 (8 dwords)
+  DevBuf<uint32_t> data;      // full K, fragment order (frag_index in dense.hip)
   bool full_valid = false;    // data holds K for the current parameters
   int64_t groups_per_row() const { return npad / 8; }
   // Symmetric half: for nb = npad / 256 blocks of 256 points, the blocks
   // (b, (b + delta) mod nb), delta = 0 .. sym_span(b, nb) (the diagonal block
-  // and the cyclic half of the others, each unordered pair once), each stored
-  // as [256 rows][32 groups] in the split format above, at block index
-  // dense_half_index(b, delta, nb): n^2/2 + 128 n entries instead of n^2.
+  // and the cyclic half of the others, each unordered pair once), each 256 KB
+  // of the split format above in fragment order (half_frag_index), at block
+  // index dense_half_index(b, delta, nb): n^2/2 + 128 n entries instead of n^2.
   DevBuf<uint32_t> half;
   bool half_valid = false;
   int64_t blocks() const { return npad / 256; }
@@ -45,11 +46,24 @@ __host__ __device__ inline int64_t dense_half_index(int64_t b, int64_t delta, in
 }
 inline int64_t dense_half_blocks(int64_t nb) { return nb * (nb + 1) / 2; }
 
+// Fragment order of a stored block: the 8-fp16 unit (h8 index) holding part p
+// (0 hi, 1 lo) of row r (0..255), columns 8 g .. 8 g + 7 (g = 0..31) of
+// stored block hb.  Per 32-column step s = g / 4 and 32-row slice w = r / 32,
+// the two 16-row tiles' hi and lo parts are four consecutive 1 KB
+// v_mfma_f32_16x16x32_f16 A operands (lane = r % 16 + 16 (g % 4)), so a
+// wave's loads of one step are 4 KB contiguous and a workgroup of 8 such
+// waves streams each step's 32 KB in one run.
+__host__ __device__ inline int64_t half_frag_index(int64_t hb, int r, int g, int p) {
+  const int lane = (r & 15) + 16 * (g & 3);
+  return ((((hb * 8 + (g >> 2)) * 8 + (r >> 5)) * 2 + ((r >> 4) & 1)) * 2 + p) * 64 + lane;
+}
+
 // Work buffers of dense_forward, grown on demand.
 struct DenseWorkspace {
   DevBuf<uint32_t> vpack;           // packed right-hand sides [cpad][npad / 8] groups
   DevBuf<uint32_t> vpair;           // right-hand sides in row-tile-pair order (symmetric route)
   DevBuf<uint32_t> colmax, colmax_part;
+  DevBuf<uint32_t> shifts;          // output exponents of the symmetric route [16]
   DevBuf<float> part;               // [splits][cpad][npad]
   DevBuf<float> tpart;              // transposed partial sums of the symmetric route
 };

@@ -134,40 +134,6 @@ __global__ void k_dense_absmax_final(const uint32_t* __restrict__ part, int chun
   if (lane == 0) colmax[c] = mx;
 }
 
-// Right-hand sides in group order for the symmetric route: Vn[c * gpr + g] =
-// split of 2^s_c V[c][8 g + e] (zero for c >= ncols or past n).
-__global__ void k_dense_pack_rhs_groups(const float* __restrict__ V, int64_t n, int ncols,
-                                        int cpad, int64_t gpr,
-                                        const uint32_t* __restrict__ colmax, int vec4,
-                                        h16* __restrict__ Vn) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)cpad * gpr) return;
-  const int c = (int)(idx / gpr);
-  const int64_t g = idx - (int64_t)c * gpr, j0 = 8 * g;
-  float x[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-  if (c < ncols) {
-    const float* src = V + (int64_t)c * n;
-    if (vec4 && j0 + 8 <= n) {
-      const f4 a = *reinterpret_cast<const f4*>(src + j0);
-      const f4 b = *reinterpret_cast<const f4*>(src + j0 + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[e] = a[e];
-        x[4 + e] = b[e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = j0 + e < n ? src[j0 + e] : 0.0f;
-    }
-    const int sh = scale_shift(__uint_as_float(colmax[c]));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = ldexpf(x[e], sh);
-  }
-  Vn[idx] = split16(x);
-}
-
 // Right-hand sides in the fragment layout: column c, group g holds the split
 // of 2^s_c V[c][8 g + e] (zero for c >= ncols or past n), s_c from the column
 // maximum.
@@ -459,38 +425,41 @@ __global__ void k_dense_reduce(const float* __restrict__ part, int splits, int c
 //
 // K is symmetric, so the half keeps the diagonal blocks and the cyclic half
 // of the off-diagonal blocks of 256 points (sym_span), each unordered pair
-// once.  A product with <= 16 right-hand sides reads every stored block once:
-//   * forward, out_b += K_bJ V_J: the block rows straight from global memory
-//     as the A operand (the layout of dense_forward), V_J in the same group
-//     order as the B operand;
-//   * transposed (J != b), out_J += K_bJ^T V_b: each wave stores its two row
-//     tiles' 8-byte chunks (row, 4 columns) of both parts to a wave-private
+// once, in fragment order.  A product with <= 16 right-hand sides reads every
+// stored block once, each wave one 32-column slice of it:
+//   * forward, out_b += K_bJ V_J: the block's fragments straight from global
+//     memory as the A operand, V_J's fragment as the B operand;
+//   * transposed (J != b), out_J += K_bJ^T V_b: the wave stores each row
+//     pair's 8-byte chunks (row, 4 columns) of both parts to a wave-private
 //     LDS scratch and reads them back with ds_read_b64_tr_b16, which yields
-//     the block transposed into the B operand of O_J^T += V_b^T K_bJ,
-//     contracted over the wave's two row tiles in the row-tile-pair order of
-//     the pair-packed V_b (A operand, loaded once per wave);
-//   * the waves' transposed sums (32 rows each) are added in wave order after
-//     the next barrier and written as the 256-row partial tp[b][delta - 1];
-//     k_dense_sym_reduce adds, per point, the forward split partials and the
+//     the slice transposed into the B operand of O_J^T += V_b^T K_bJ,
+//     contracted over the pair's rows in the row-tile-pair order of the
+//     pair-packed V_b (A operand, loaded once per wave) and accumulated over
+//     the block's 8 row pairs, so the slice's 256-row partial tp[b][delta - 1]
+//     is complete in the wave;
+//   * k_dense_sym_reduce adds, per point, the forward split partials and the
 //     partials of the row blocks that formed its column block (fp64, fixed
 //     order).
 // ---------------------------------------------------------------------------
 constexpr int kDsRows = 256;                    // points per block
 constexpr int kDsGroups = kDsRows / 8;          // 8-column groups per block row
-constexpr int kDsWaves = 8;                     // waves per workgroup, 32 rows each
+constexpr int kDsWaves = 8;                     // waves per workgroup, one column step each
 constexpr int kDsSteps = kDsRows / 32;          // 32-column steps per block
-constexpr int kDsStage = 2;                     // steps per transposed hand-off
-constexpr int kDsStages = kDsSteps / kDsStage;  // hand-offs per block
+constexpr int kDsRing = 4;                      // register sets of sub-step operands
+constexpr int kDsDepth = 3;                     // sub-steps loaded ahead
 
-// One thread per (delta, row, group) of row block b's stored blocks.
+// One thread per (delta, row, group) of row block b's stored blocks, in
+// fragment order (consecutive threads write consecutive 16-byte units).
 __global__ void k_dense_pack_half(const float* __restrict__ rows, int64_t nrows, int64_t n,
                                   int64_t b, int64_t nb, int64_t span, int shift, int vec4,
-                                  h16* __restrict__ half) {
+                                  h8* __restrict__ half) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (span + 1) * kDsRows * kDsGroups) return;
   const int64_t delta = idx / (kDsRows * kDsGroups);
-  const int64_t rem = idx - delta * (kDsRows * kDsGroups);
-  const int64_t r = rem / kDsGroups, g = rem - r * kDsGroups;
+  const int u = (int)(idx - delta * (kDsRows * kDsGroups));
+  const int lane = u & 63;
+  const int r = 32 * ((u >> 7) & 7) + 16 * ((u >> 6) & 1) + (lane & 15);
+  const int g = 4 * (u >> 10) + (lane >> 4);
   int64_t J = b + delta;
   if (J >= nb) J -= nb;
   const int64_t j0 = J * kDsRows + 8 * g;
@@ -510,16 +479,23 @@ __global__ void k_dense_pack_half(const float* __restrict__ rows, int64_t nrows,
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) x[e] = ldexpf(x[e], shift);
-  half[(dense_half_index(b, delta, nb) * kDsRows + r) * kDsGroups + g] = split16(x);
+  const h16 v = split16(x);
+  const int64_t hb = dense_half_index(b, delta, nb);
+  half[half_frag_index(hb, r, g, 0)] = first8(v);
+  half[half_frag_index(hb, r, g, 1)] = last8(v);
 }
 
 // Right-hand sides in row-tile-pair order: Vp[(u*2 + part)*64 + lane] (8
 // fp16), element e = 2^s_c V[c = lane%16][32 u + 16 (e/4) + 4 (lane/16) + e%4],
-// part 0 = hi, 1 = lo; zero for c >= ncols or past n.
+// part 0 = hi, 1 = lo; zero for c >= ncols or past n.  Threads 0..15 also
+// write the output exponents shifts[c] = kshift + s_c (s_c = 0 for
+// c >= ncols), so the product reads them without a branch.
 __global__ void k_dense_pack_pair(const float* __restrict__ V, int64_t n, int ncols,
                                   int64_t pairs, const uint32_t* __restrict__ colmax,
-                                  h8* __restrict__ Vp) {
+                                  int kshift, int* __restrict__ shifts, h8* __restrict__ Vp) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < 16)
+    shifts[idx] = kshift + ((int)idx < ncols ? scale_shift(__uint_as_float(colmax[idx])) : 0);
   if (idx >= pairs * 64) return;
   const int lane = (int)(idx & 63);
   const int64_t u = idx >> 6;
@@ -538,125 +514,124 @@ __global__ void k_dense_pack_pair(const float* __restrict__ V, int64_t n, int nc
 }
 
 // Work item L = (row block b, delta split) of the symmetric half product.
+// Kf: the half in fragment order (half_frag_index); Vf: the right-hand sides
+// in the fragment layout of k_dense_pack_rhs (16 columns, one tile), so the
+// B operand of 32-column step S of the points is Vf[(2 S + p) 64 + lane];
+// Vpp: the right-hand sides in row-tile-pair order and shifts the output
+// exponents (k_dense_pack_pair).
+// Wave w owns the 32-column step w of every block of the item and streams
+// its column slice (8 row pairs of 4 KB, one contiguous 32 KB run) forming
+//   forward     acc[tile] += K[tile rows, step w] V_J[step w]  (16 row tiles)
+//   transposed  tacc[tt]  += V_b[pair rows]^T K[pair rows, step w]
+// so the transposed sums of the block's 32 columns complete inside the wave
+// over all 256 rows and go straight to tp, and only the forward sums, which
+// accumulate over the item's blocks, are added across the 8 waves, once.
 // fwd[(split*16 + c)*mpad + i]: forward sums of the split's blocks, unscaled;
 // tp[((b*hmax + delta - 1)*256 + column)*16 + c]: transposed block sums.
 __global__ __launch_bounds__(64 * kDsWaves) void k_dense_sym(
-    const h16* __restrict__ Kh, const h16* __restrict__ Vn, const h8* __restrict__ Vpp,
-    int64_t nb, int64_t splits, int64_t dps, int64_t hmax, int64_t gpr, int ncols, int kshift,
-    const uint32_t* __restrict__ colmax, float* __restrict__ fwd, float* __restrict__ tp,
-    int64_t mpad) {
+    const h8* __restrict__ Kf, const h8* __restrict__ Vf, const h8* __restrict__ Vpp,
+    int64_t nb, int64_t splits, int64_t dps, int64_t hmax, const int* __restrict__ shifts,
+    float* __restrict__ fwd, float* __restrict__ tp, int64_t mpad) {
   constexpr int W = kDsWaves;
+  static_assert(W == kDsSteps, "one wave per 32-column step of a block");
   // Wave-private transposition scratch: [column tile][hi, lo][row tile][chunk].
   __shared__ uint64_t tsc[W][2][2][2][64];
-  // Transposed sums per hand-off: [buffer][step][wave][column tile][lane].
-  __shared__ f4 tbuf[2][kDsStage][W][2][64];
+  // Forward sums of 8 row tiles per wave, for the cross-wave addition.
+  __shared__ f4 red[W][8][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t per = (int64_t)gridDim.x / kXcds;
-  const int64_t L = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  // Items in launch order (the XCDs are dealt workgroups in turn): the short
+  // last split's items are spread over all XCDs instead of loading one.
+  const int64_t L = blockIdx.x;
   if (L >= nb * splits) return;  // whole workgroup, before any barrier
   const int64_t b = L % nb;
   const int64_t split = L / nb;
   const int li = lane & 15, lg = lane >> 4;
-  const int row0 = 32 * wave;  // this wave's rows within the block
-  const int64_t upr = (b * kDsRows + row0) / 32;
-  const h8 vih = Vpp[(upr * 2) * 64 + lane], vil = Vpp[(upr * 2 + 1) * 64 + lane];
   const int chunk_r = sym_read_chunk(lane);
   const int tw = lg >> 1, q0 = 2 * (lg & 1);  // column tile and first quad of this lane's group
 
-  f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-  double accd[2][4];
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) accd[r][q] = 0.0;
-
   const int64_t span = sym_span(b, nb);
   const int64_t d0 = split * dps;
-  const int64_t d1 = min(d0 + dps, span + 1);
-  const int64_t nsteps = d1 > d0 ? (d1 - d0) * kDsSteps : 0;
-  const int64_t nst = nsteps / kDsStage;
-  auto step_delta = [&](int64_t t) { return d0 + t / kDsSteps; };
-  // Loads of step t: the wave's two row tiles of the block (lane: row
-  // 16 r + li, group 4 s + lg) and V_J (lane: column li, same group).
-  auto load = [&](int64_t t, h16 (&ka)[2], h16& va) __attribute__((always_inline)) {
-    const int64_t delta = step_delta(t);
-    const int s = (int)(t % kDsSteps);
-    int64_t J = b + delta;
+  const int64_t nblk = max(min(d0 + dps, span + 1) - d0, (int64_t)0);
+  const int64_t nsub = nblk * kDsSteps;  // (block, row pair) sub-steps of the item
+  // Sub-step t: the wave's step of row pair t % 8 of block d0 + t / 8, both
+  // row tiles, hi and lo (lane: row 16 r + li, group 4 w + lg).  The half is
+  // read once per product, so its loads are non-temporal: they do not
+  // displace the partial sums and operands held in the caches.
+  auto load = [&](int64_t t, h8 (&kh)[2], h8 (&kl)[2]) __attribute__((always_inline)) {
+    const int64_t delta = d0 + t / kDsSteps;
+    const int rp = (int)(t % kDsSteps);
+    const h8* kp =
+        Kf + half_frag_index(dense_half_index(b, delta, nb), 32 * rp, 4 * wave, 0) + lane;
+    kh[0] = __builtin_nontemporal_load(kp);
+    kl[0] = __builtin_nontemporal_load(kp + 64);
+    kh[1] = __builtin_nontemporal_load(kp + 128);
+    kl[1] = __builtin_nontemporal_load(kp + 192);
+  };
+
+  // V_J of block bi (column step w), loaded one block ahead: a load issued at
+  // the block start and consumed at once would also wait for the previous
+  // block's tp stores, which the memory counter orders before it.
+  auto load_v = [&](int64_t bi, h8& vh, h8& vl) __attribute__((always_inline)) {
+    int64_t J = b + d0 + bi;
     if (J >= nb) J -= nb;
-    const h16* kp = Kh + (dense_half_index(b, delta, nb) * kDsRows + row0) * kDsGroups + 4 * s + lg;
-    ka[0] = kp[(int64_t)li * kDsGroups];
-    ka[1] = kp[(int64_t)(16 + li) * kDsGroups];
-    va = Vn[(int64_t)li * gpr + J * kDsGroups + 4 * s + lg];
+    const h8* vp = Vf + (J * kDsSteps + wave) * 128 + lane;
+    vh = vp[0];
+    vl = vp[64];
   };
-  auto flush = [&]() __attribute__((always_inline)) {
+  // Loads run kDsDepth sub-steps ahead in a ring of kDsRing register sets;
+  // a block's 8 sub-steps are unrolled, so every set is addressed statically
+  // (no register copies, which would wait for loads still in flight).  The
+  // item's first loads go out oldest-first in the order they are consumed,
+  // so no wait inside the loop covers more than the operand it needs.
+  constexpr int R = kDsRing, D = kDsDepth;
+  static_assert(kDsSteps % R == 0 && D < R, "the ring must tile a block's sub-steps");
+  h8 bkh[R][2], bkl[R][2];
+  h8 vh, vl, nvh, nvl;
+  if (nblk > 0) load_v(0, vh, vl);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+  for (int k = 0; k < D; ++k)
+    if (nsub > 0) load(min((int64_t)k, nsub - 1), bkh[k], bkl[k]);
+  // V_b in row-tile-pair order: the A operand of the transposed products.
+  h8 vbh[kDsSteps], vbl[kDsSteps];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) accd[r][q] += (double)acc[r][q];
-      acc[r] = f4{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-
-  // Stage reduction (all 512 threads): unit u < kDsStage*256 is two
-  // right-hand sides (2h, 2h + 1 of the lane's four) of one lane of one
-  // column tile; a thread's units share the lane half, so its scales are fixed.
-  constexpr int kRedUnits = kDsStage * 256;
-  const int ru = threadIdx.x;
-  const int r_ln = (ru >> 1) & 63, r_h = ru & 1;
-  const int r_c = 4 * (r_ln >> 4) + 2 * r_h;
-  f2 r_scale;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int cc = r_c + e;
-    const int sh = cc < ncols ? scale_shift(__uint_as_float(colmax[cc])) : 0;
-    r_scale[e] = ldexpf(1.0f, -(kshift + sh));
+  for (int rp = 0; rp < kDsSteps; ++rp) {
+    const int64_t u = b * kDsSteps + rp;
+    vbh[rp] = Vpp[(u * 2) * 64 + lane];
+    vbl[rp] = Vpp[(u * 2 + 1) * 64 + lane];
   }
-  auto reduce_stage = [&](int64_t c) __attribute__((always_inline)) {
-    const int slot = (int)(c & 1);
-    const int64_t blk = b * hmax + step_delta(c * kDsStage) - 1;
-    constexpr int wstride = (int)(sizeof(tbuf[0][0][0]) / sizeof(float));
-#pragma unroll
-    for (int uu = 0; uu < kRedUnits; uu += 64 * W) {
-      const int u = uu + ru;
-      if (u >= kRedUnits) break;
-      const int kk = u >> 8, t = (u >> 7) & 1;
-      const float* src = reinterpret_cast<const float*>(&tbuf[slot][kk][0][t][r_ln]) + 2 * r_h;
-      f2 sum = *reinterpret_cast<const f2*>(src);
-#pragma unroll
-      for (int w = 1; w < W; ++w) sum += *reinterpret_cast<const f2*>(src + w * wstride);
-      const int64_t s = (c * kDsStage) % kDsSteps + kk;
-      const int64_t jl = 32 * s + 16 * t + (r_ln & 15);
-      *reinterpret_cast<f2*>(tp + (blk * kDsRows + jl) * 16 + r_c) = sum * r_scale;
-    }
-  };
+  // Output exponents: the lane's transposed right-hand sides 4 lg + q and its
+  // forward right-hand side li.
+  const int4 tsh = *reinterpret_cast<const int4*>(shifts + 4 * lg);
+  const int fsh = shifts[li];
 
-  h16 ka[2], va, kn[2], vn;
-  if (nsteps > 0) load(0, ka, va);
-  for (int64_t c = 0; c < nst; ++c) {
-    __syncthreads();
-    if (c > 0 && step_delta((c - 1) * kDsStage) > 0) reduce_stage(c - 1);
-    const bool sym = step_delta(c * kDsStage) > 0;
+  f4 acc[2 * kDsSteps];
 #pragma unroll
-    for (int k = 0; k < kDsStage; ++k) {
-      const int64_t t = c * kDsStage + k;
-      load(min(t + 1, nsteps - 1), kn, vn);  // next step (clamped: always a valid block)
-      const h8 vh = first8(va), vl = last8(va);
+  for (int u = 0; u < 2 * kDsSteps; ++u) acc[u] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t bi = 0; bi < nblk; ++bi) {
+    const int64_t delta = d0 + bi;
+    const bool sym = delta > 0;
+    f4 tacc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int k = 0; k < kDsSteps; ++k) {
+      const int64_t t = bi * kDsSteps + k;
+      const int cur = k % R, nxt = (k + D) % R;
+      load(min(t + D, nsub - 1), bkh[nxt], bkl[nxt]);  // clamped: always a valid block
+      if (k == 0) load_v(min(bi + 1, nblk - 1), nvh, nvl);
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const h8 kh = first8(ka[r]), kl = last8(ka[r]);
-        f4 a = acc[r];
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, vh, a, 0, 0, 0);
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, vl, a, 0, 0, 0);
-        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, vh, a, 0, 0, 0);
-        acc[r] = a;
+        f4 a = acc[2 * k + r];
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(bkh[cur][r], vh, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(bkh[cur][r], vl, a, 0, 0, 0);
+        a = __builtin_amdgcn_mfma_f32_16x16x32_f16(bkl[cur][r], vh, a, 0, 0, 0);
+        acc[2 * k + r] = a;
       }
       if (sym) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-          const u64x2 h = __builtin_bit_cast(u64x2, first8(ka[r]));
-          const u64x2 l = __builtin_bit_cast(u64x2, last8(ka[r]));
+          const u64x2 h = __builtin_bit_cast(u64x2, bkh[cur][r]);
+          const u64x2 l = __builtin_bit_cast(u64x2, bkl[cur][r]);
           tsc[wave][tw][0][r][sym_chunk(li, q0)] = h[0];
           tsc[wave][tw][0][r][sym_chunk(li, q0 + 1)] = h[1];
           tsc[wave][tw][1][r][sym_chunk(li, q0)] = l[0];
@@ -672,34 +647,50 @@ __global__ __launch_bounds__(64 * kDsWaves) void k_dense_sym(
                              tr_read(&tsc[wave][tt][p][1][chunk_r])};
             tp2[p] = __builtin_bit_cast(h8, v);
           }
-          f4 a = f4{0.f, 0.f, 0.f, 0.f};
-          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih, tp2[0], a, 0, 0, 0);
-          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vil, tp2[0], a, 0, 0, 0);
-          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vih, tp2[1], a, 0, 0, 0);
-          tbuf[c & 1][k][wave][tt][lane] = a;
+          f4 a = tacc[tt];
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbh[k], tp2[0], a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbl[k], tp2[0], a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_f16(vbh[k], tp2[1], a, 0, 0, 0);
+          tacc[tt] = a;
         }
         asm volatile("" ::: "memory");
       }
-      ka[0] = kn[0];
-      ka[1] = kn[1];
-      va = vn;
     }
-    if ((c + 1) % kDsStages == 0) flush();  // end of a block
+    if (sym) {
+      // lane: right-hand sides 4 lg + q of column 32 w + 16 tt + li of block J
+      const int64_t blk = b * hmax + delta - 1;
+      const f4 tscale = {ldexpf(1.0f, -tsh.x), ldexpf(1.0f, -tsh.y), ldexpf(1.0f, -tsh.z),
+                         ldexpf(1.0f, -tsh.w)};
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        *reinterpret_cast<f4*>(tp + (blk * kDsRows + 32 * wave + 16 * tt + li) * 16 + 4 * lg) =
+            tacc[tt] * tscale;
+    }
+    vh = nvh;
+    vl = nvl;
   }
-  if (nst > 0 && step_delta((nst - 1) * kDsStage) > 0) {
+  // Forward sums: the 8 waves' fp32 sums of each row tile added in wave order
+  // in fp64, 8 row tiles per round (thread: tile wave, lane = column li, rows
+  // 4 lg + q of the tile).
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
     __syncthreads();
-    reduce_stage(nst - 1);
-  }
-  flush();
-  // Forward partials (lane: column li, rows 16 r + 4 lg + q of the wave).
-  const int sh = li < ncols ? scale_shift(__uint_as_float(colmax[li])) : 0;
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+    for (int u = 0; u < 8; ++u) red[wave][u][lane] = acc[8 * h + u];
+    __syncthreads();
+    double sum[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t i = b * kDsRows + row0 + 16 * r + 4 * lg + q;
-      fwd[(split * 16 + li) * mpad + i] = (float)ldexp(accd[r][q], -(kshift + sh));
+    for (int w = 0; w < W; ++w) {
+      const f4 v = red[w][wave][lane];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum[q] += (double)v[q];
     }
+    f4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = (float)ldexp(sum[q], -fsh);
+    const int tile = 8 * h + wave;
+    *reinterpret_cast<f4*>(fwd + (split * 16 + li) * mpad + b * kDsRows + 16 * tile + 4 * lg) = o;
+  }
 }
 
 // out[c*n + j] = sum_s fwd[s][c][j] + the transposed partials of the row
@@ -804,7 +795,7 @@ void dense_pack_half(const float* rows, int64_t b, int64_t nrows, DenseK& K, hip
   const int vec4 = (K.n % 4 == 0 && reinterpret_cast<uintptr_t>(rows) % 16 == 0) ? 1 : 0;
   hipLaunchKernelGGL(k_dense_pack_half, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
                      rows, nrows, K.n, b, nb, span, K.shift, vec4,
-                     reinterpret_cast<h16*>(K.half.ptr));
+                     reinterpret_cast<h8*>(K.half.ptr));
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -822,14 +813,15 @@ void dense_sym_forward(const DenseK& K, const float* V, int ncols, float noise, 
   hipLaunchKernelGGL(k_dense_absmax_final, dim3((unsigned)ncols), dim3(64), 0, st, cpart, chunks,
                      colmax);
   const int64_t vtot = 16 * gpr;
-  h16* vn = reinterpret_cast<h16*>(w.vpack.ensure((size_t)vtot * 8));
+  h8* vf = reinterpret_cast<h8*>(w.vpack.ensure((size_t)vtot * 8));
   const int vec4 = (n % 4 == 0 && reinterpret_cast<uintptr_t>(V) % 16 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(k_dense_pack_rhs_groups, dim3((unsigned)ceil_div(vtot, 256)), dim3(256), 0,
-                     st, V, n, ncols, 16, gpr, colmax, vec4, vn);
+  hipLaunchKernelGGL(k_dense_pack_rhs, dim3((unsigned)ceil_div(vtot, 256)), dim3(256), 0, st, V,
+                     n, ncols, 16, gpr, colmax, vec4, vf);
   const int64_t pairs = npad / 32;
   h8* vp = reinterpret_cast<h8*>(w.vpair.ensure((size_t)pairs * 2 * 64 * 4));
+  int* shifts = reinterpret_cast<int*>(w.shifts.ensure(16));
   hipLaunchKernelGGL(k_dense_pack_pair, dim3((unsigned)ceil_div(pairs * 64, 256)), dim3(256), 0,
-                     st, V, n, ncols, pairs, colmax, vp);
+                     st, V, n, ncols, pairs, colmax, K.shift, shifts, vp);
   MGP_HIP_CHECK(hipGetLastError());
 
   int64_t splits = std::min<int64_t>(std::max<int64_t>(ceil_div(2048, nb), 1), hmax + 1);
@@ -837,10 +829,10 @@ void dense_sym_forward(const DenseK& K, const float* V, int ncols, float noise, 
   splits = ceil_div(hmax + 1, dps);
   float* fwd = w.part.ensure((size_t)splits * 16 * npad);
   float* tp = w.tpart.ensure((size_t)std::max<int64_t>(nb * hmax, 1) * kDsRows * 16);
-  const int64_t items = round_up(nb * splits, kXcds);
+  const int64_t items = nb * splits;
   hipLaunchKernelGGL(k_dense_sym, dim3((unsigned)items), dim3(64 * kDsWaves), 0, st,
-                     reinterpret_cast<const h16*>(K.half.ptr), vn, vp, nb, splits, dps, hmax, gpr,
-                     ncols, K.shift, colmax, fwd, tp, npad);
+                     reinterpret_cast<const h8*>(K.half.ptr), vf, vp, nb, splits, dps, hmax,
+                     shifts, fwd, tp, npad);
   MGP_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(k_dense_sym_reduce, dim3((unsigned)ceil_div(4 * n, 256)), dim3(256), 0, st,
                      fwd, (int)splits, tp, nb, hmax, npad, n, ncols, noise, V, out);

@@ -17,6 +17,7 @@
 //   3. O^T += V^T . P^T  (four more 16x16x4 MFMAs per 16 right-hand sides).
 // K never touches HBM.  Accumulators are flushed into fp64 every 256 columns so
 // the long N-term sums keep ~1e-7 relative accuracy.
+#include "dense.h"
 #include "matvec.h"
 #include "sym_common.h"
 
@@ -1586,8 +1587,9 @@ __global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr
 // Symmetric half of the dense K (dense.h layout): one thread per (stored
 // block, row, 8-column group) evaluates os * k(z_row, z_col) for the group's
 // eight columns from per-dimension differences (the arithmetic of
-// k_fill_cross), scales by 2^shift and stores the two-term fp16 split
-// {hi[8], lo[8]}; rows and columns past n are zero.
+// k_fill_cross), scales by 2^shift and stores the two-term fp16 split, hi and
+// lo as two 16-byte units in fragment order (half_frag_index; consecutive
+// threads write consecutive units); rows and columns past n are zero.
 constexpr int kHalfRows = 256;
 template <int KIND>
 __global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, int64_t n, int d,
@@ -1597,8 +1599,10 @@ __global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, 
   constexpr int kGroups = kHalfRows / 8;
   if (idx >= nblocks * kHalfRows * kGroups) return;
   const int64_t blk = idx / (kHalfRows * kGroups);
-  const int64_t rem = idx - blk * (kHalfRows * kGroups);
-  const int64_t r = rem / kGroups, g = rem - r * kGroups;
+  const int u = (int)(idx - blk * (kHalfRows * kGroups));
+  const int lane = u & 63;
+  const int r = 32 * ((u >> 7) & 7) + 16 * ((u >> 6) & 1) + (lane & 15);
+  const int g = 4 * (u >> 10) + (lane >> 4);
   // block index -> (b, delta), the inverse of dense_half_index
   int64_t b, delta;
   if (nb & 1) {
@@ -1653,9 +1657,9 @@ __global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, 
     w[4 + e] = (uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e]) |
                ((uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e + 1]) << 16);
   }
-  uint32_t* dst = half + ((blk * kHalfRows + r) * kGroups + g) * 8;
-  *reinterpret_cast<f4*>(dst) = __builtin_bit_cast(f4, (uint32_t __attribute__((ext_vector_type(4)))){w[0], w[1], w[2], w[3]});
-  *reinterpret_cast<f4*>(dst + 4) = __builtin_bit_cast(f4, (uint32_t __attribute__((ext_vector_type(4)))){w[4], w[5], w[6], w[7]});
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  *reinterpret_cast<u4*>(half + half_frag_index(blk, r, g, 0) * 4) = u4{w[0], w[1], w[2], w[3]};
+  *reinterpret_cast<u4*>(half + half_frag_index(blk, r, g, 1) * 4) = u4{w[4], w[5], w[6], w[7]};
 }
 
 // ---------------------------------------------------------------------------
