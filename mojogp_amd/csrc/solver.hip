@@ -712,24 +712,24 @@ __global__ __launch_bounds__(256) void k_ltv_mfma(const float* __restrict__ L, i
 }
 
 // k_ltv_mfma for ncols <= 16 and k <= 256 with the chunk's rows and kk tiles
-// split over the waves: wave w takes the 64-row groups g0 = i0 + 64 (w & 1),
-// + 128, .. and the kk tiles t = (w >> 1) + 2 j, streaming the tiles over each
+// split over 16 waves: wave w takes the 64-row groups g0 = i0 + 64 (w & 3),
+// + 256, .. and the kk tiles t = (w >> 2) + 4 j, streaming the tiles over each
 // group (16 L rows x 64 rows per stage, double buffered; the waves of a block
-// read 512-byte runs of each L row) with the group's v values in registers.
-// MFMA roles as in k_ltv_mfma (A = L, B = v, D[kk][c]).  The two row halves
-// of a tile set are added through LDS (w & 1 = 0 plus w & 1 = 1), and waves 0
-// and 2 write the chunk's partial.  v rows past the chunk are zero; other
-// out-of-range loads use clamped addresses and only feed D entries that are
-// not written.
+// read 1 KB runs of each L row) with the group's v values in registers.
+// MFMA roles as in k_ltv_mfma (A = L, B = v, D[kk][c]).  The four row
+// quarters of a tile set are added through LDS in quarter order, and the
+// waves of quarter 0 write the chunk's partial.  v rows past the chunk are
+// zero; other out-of-range loads use clamped addresses and only feed D
+// entries that are not written.
+constexpr int kLtvWaves = 16;
 template <bool VEC4, bool RS>
-__global__ __launch_bounds__(256) void k_ltv_c16(const float* __restrict__ L, int64_t n, int k,
-                                                 const float* __restrict__ v, int ncols,
-                                                 int64_t chunk, float* __restrict__ wpart,
-                                                 const float* __restrict__ rs) {
-  __shared__ f4v red[2][8][64];
+__global__ __launch_bounds__(64 * kLtvWaves) void k_ltv_c16(
+    const float* __restrict__ L, int64_t n, int k, const float* __restrict__ v, int ncols,
+    int64_t chunk, float* __restrict__ wpart, const float* __restrict__ rs) {
+  __shared__ f4v red[3][4][4][64];  // quarters 1..3: [quarter - 1][tile set][j][lane]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rh = wave & 1, th = wave >> 1;
+  const int rh = wave & 3, th = wave >> 2;
   const int lm = lane & 15, lq = lane >> 4;
   const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   const int ktiles = (k + 15) / 16;
@@ -745,11 +745,11 @@ __global__ __launch_bounds__(256) void k_ltv_c16(const float* __restrict__ L, in
       return x;
     }
   };
-  f4v acc[8];
+  f4v acc[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = zero;
+  for (int j = 0; j < 4; ++j) acc[j] = zero;
   const float* vc = v + (int64_t)(lm < ncols ? lm : ncols - 1) * n;
-  for (int64_t g0 = i0 + 64 * rh; g0 < i1; g0 += 128) {
+  for (int64_t g0 = i0 + 64 * rh; g0 < i1; g0 += 256) {
     f4v b[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -763,9 +763,9 @@ __global__ __launch_bounds__(256) void k_ltv_c16(const float* __restrict__ L, in
         for (int e = 0; e < 4; ++e) b[u][e] = r0 + e < i1 ? x[e] : 0.0f;
       }
     }
-    // tile t = th + 2 j
+    // tile t = th + 4 j
     auto load = [&](int j, f4v (&a)[4]) __attribute__((always_inline)) {
-      const float* lr = L + (int64_t)min(16 * (th + 2 * j) + lm, k - 1) * n;
+      const float* lr = L + (int64_t)min(16 * (th + 4 * j) + lm, k - 1) * n;
 #pragma unroll
       for (int u = 0; u < 4; ++u) a[u] = quad(lr, g0 + 16 * u + 4 * lq);
     };
@@ -779,28 +779,28 @@ __global__ __launch_bounds__(256) void k_ltv_c16(const float* __restrict__ L, in
     f4v a0[4], a1[4];
     load(0, a0);
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      if (th + 2 * j >= ktiles) break;  // uniform
+    for (int j = 0; j < 4; j += 2) {
+      if (th + 4 * j >= ktiles) break;  // uniform
       load(j + 1, a1);
       mma(acc[j], a0);
-      if (th + 2 * (j + 1) >= ktiles) break;
+      if (th + 4 * (j + 1) >= ktiles) break;
       load(j + 2, a0);
       mma(acc[j + 1], a1);
     }
   }
-  if (rh == 1) {
+  if (rh > 0) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (th + 2 * j < ktiles) red[th][j][lane] = acc[j];
+    for (int j = 0; j < 4; ++j)
+      if (th + 4 * j < ktiles) red[rh - 1][th][j][lane] = acc[j];
   }
   __syncthreads();
-  if (rh == 1 || lm >= ncols) return;
+  if (rh > 0 || lm >= ncols) return;
   float* wp = wpart + ((int64_t)blockIdx.x * ncols + lm) * k;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int t = th + 2 * j;
+  for (int j = 0; j < 4; ++j) {
+    const int t = th + 4 * j;
     if (t >= ktiles) break;
-    const f4v tot = acc[j] + red[th][j][lane];
+    const f4v tot = ((acc[j] + red[0][th][j][lane]) + red[1][th][j][lane]) + red[2][th][j][lane];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int kk = 16 * t + 4 * lq + q;
@@ -858,6 +858,59 @@ __global__ __launch_bounds__(256) void k_small_solve_t(const float* __restrict__
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
   if (lane == 0) ut[((int64_t)(c / 16) * k + kk) * 16 + (c & 15)] = s;
+}
+
+// k_part_reduce followed by k_small_solve_t in one launch, for the Woodbury
+// apply: block c (of cpad) adds column c's chunk partials w[c][kk] =
+// sum_b wpart[(b ncols + c) k + kk] in the order of k_part_reduce (16
+// stripes of chunks b = s, s + 16, .., each in order, then the stripes in
+// order, rounded to fp32) into LDS, then forms ut[((c/16) k + kk) 16 + c%16]
+// = sum_q Minv[kk k + q] w[c][q] as k_small_solve_t does (one wave per
+// output, lanes stride q, fixed shuffle tree); zero for padding columns.
+constexpr int kPartSolveMaxK = 256;
+__global__ __launch_bounds__(1024) void k_part_solve_t(const float* __restrict__ wpart, int nb,
+                                                       int k, int ncols,
+                                                       const float* __restrict__ Minv,
+                                                       float* __restrict__ ut) {
+  __shared__ double sm[16][64];
+  __shared__ float wc[kPartSolveMaxK];
+  const int c = blockIdx.x;
+  const int kl = threadIdx.x & 63, sidx = threadIdx.x >> 6;
+  const int64_t total = (int64_t)k * ncols;
+  for (int kk0 = 0; kk0 < k; kk0 += 64) {
+    const int kk = kk0 + kl;
+    double acc = 0.0;
+    if (c < ncols && kk < k) {
+      const int64_t o = (int64_t)c * k + kk;
+      int b = sidx;
+      for (; b + 7 * 16 < nb; b += 8 * 16) {
+        float t[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) t[q] = wpart[(int64_t)(b + 16 * q) * total + o];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc += (double)t[q];
+      }
+      for (; b < nb; b += 16) acc += (double)wpart[(int64_t)b * total + o];
+    }
+    sm[sidx][kl] = acc;
+    __syncthreads();
+    if (sidx == 0 && kk < k) {
+      double t = sm[0][kl];
+#pragma unroll
+      for (int q = 1; q < 16; ++q) t += sm[q][kl];
+      wc[kk] = (float)t;
+    }
+    __syncthreads();
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int kk = wave; kk < k; kk += 16) {
+    float s = 0.0f;
+    if (c < ncols)
+      for (int q = lane; q < k; q += 64) s = fmaf(Minv[(int64_t)kk * k + q], wc[q], s);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) ut[((int64_t)(c / 16) * k + kk) * 16 + (c & 15)] = s;
+  }
 }
 
 // out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * (DINV ? dinv[i] : inv_noise)
@@ -946,32 +999,42 @@ __global__ __launch_bounds__(256) void k_woodbury_rows(
 }
 
 // k_woodbury_rows on the fp32 matrix cores (k <= kWoodMfmaMaxK).  Block =
-// chunk blockIdx.x x the 16 columns of tile blockIdx.y; wave w takes the
-// 64-row groups g0 = i0 + 64 w, + 256, ..  Per group, v_mfma_f32_16x16x4_f32
-// tile t (0..3) maps MFMA row m to row g0 + 4 m + t and the MFMA k index to
-// L row kk: lane l supplies A = L[kk0 + l/16][g0 + 4 (l%16) + t] (one 16-byte
-// load per L row per lane covers the four tiles, 256 contiguous bytes per L
-// row) and B = u[c0 + l%16][kk0 + l/16] from the u tile staged in LDS (zero
-// past k).  D row 4 (l/16) + q of tile t is row g0 + 16 (l/16) + 4 q + t of
-// column c0 + l%16, so each lane writes four runs of four rows.  dpart: each
-// lane's rows in order, the four lanes of a column by a shuffle butterfly,
-// then the waves in order.  Loads are unconditional (addresses clamped into
+// chunk blockIdx.x x the 16 columns of tile blockIdx.y, 16 waves: wave w
+// takes the 64-row groups g0 = i0 + 64 (w & 3), + 256, .. and the quarter
+// w >> 2 of the L rows (kq rows each, a multiple of 32), so four times as
+// many loads are in flight as with one wave per row group.  Per group,
+// v_mfma_f32_16x16x4_f32 tile t (0..3) maps MFMA row m to row g0 + 4 m + t
+// and the MFMA k index to L row kk: lane l supplies A = L[kk0 + l/16][g0 +
+// 4 (l%16) + t] (one 16-byte load per L row per lane covers the four tiles,
+// 256 contiguous bytes per L row) and B = u[c0 + l%16][kk0 + l/16] from the u
+// tile staged in LDS (zero past k).  The quarters' tiles are added through
+// LDS in quarter order by the waves of quarter 0, which finish the group: D
+// row 4 (l/16) + q of tile t is row g0 + 16 (l/16) + 4 q + t of column
+// c0 + l%16, so each lane writes four runs of four rows.  dpart: each lane's
+// rows in order, the four lanes of a column by a shuffle butterfly, then the
+// row groups in order.  Loads are unconditional (addresses clamped into
 // range; the D rows they feed are not stored), so wait counts stay exact.
 constexpr int kWoodMfmaMaxK = 256;
+constexpr int kWoodWaves = 16;
 template <bool VEC4, bool DINV, bool DOT>
-__global__ __launch_bounds__(256) void k_woodbury_mfma(
+__global__ __launch_bounds__(64 * kWoodWaves) void k_woodbury_mfma(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ ut, int ncols,
     float inv_noise, const float* v, float* out, const float* __restrict__ dinv,
     const float* dotv, int nb, double* __restrict__ dpart) {
   __shared__ float sB[kWoodMfmaMaxK * 16];
+  __shared__ f4v red[3][4][4][64];  // quarters 1..3: [quarter - 1][row group][tile][lane]
   __shared__ double wsum[4][16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = wave & 3, kh = wave >> 2;
   const int lm = lane & 15, lq = lane >> 4;
   const int c0 = blockIdx.y * 16, cn = min(16, ncols - c0);
   const int kpad = (k + 31) & ~31;
+  const int kq = (((kpad + 3) / 4) + 31) & ~31;
+  const int kb0 = min(kpad, kh * kq), kb1 = min(kpad, kb0 + kq);
   {
     const float* __restrict__ ub = ut + (int64_t)blockIdx.y * k * 16;
-    for (int j = threadIdx.x; j < kpad * 16; j += 256) sB[j] = j < k * 16 ? ub[j] : 0.0f;
+    for (int j = threadIdx.x; j < kpad * 16; j += 64 * kWoodWaves) sB[j] = j < k * 16 ? ub[j] : 0.0f;
   }
   __syncthreads();
   const int64_t chunk = (n + nb - 1) / nb;
@@ -991,7 +1054,11 @@ __global__ __launch_bounds__(256) void k_woodbury_mfma(
   };
   const int cc = c0 + (lm < cn ? lm : cn - 1);
   double dacc = 0.0;
-  for (int64_t g0 = i0 + 64 * wave; g0 < i1; g0 += 256) {
+  // every wave makes the same number of passes (the barriers below); rows
+  // past the chunk only feed D rows that are not stored
+  const int64_t passes = (i1 - i0 + 255) / 256;
+  for (int64_t pass = 0; pass < passes; ++pass) {
+    const int64_t g0 = i0 + 256 * pass + 64 * rg;
     const int64_t ra = g0 + 4 * lm;
     f4v acc[4];
 #pragma unroll
@@ -1010,45 +1077,60 @@ __global__ __launch_bounds__(256) void k_woodbury_mfma(
           acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][t], b, acc[t], 0, 0, 0);
       }
     };
-    f4v a0[4], a1[4];
-    load(0, a0);
-    for (int kb = 0; kb < kpad; kb += 32) {
-      load(kb + 16, a1);
-      mma(kb, a0);
-      load(kb + 32, a0);
-      mma(kb + 16, a1);
+    if (kb0 < kb1) {
+      f4v a0[4], a1[4];
+      load(kb0, a0);
+      for (int kb = kb0; kb < kb1; kb += 32) {
+        load(kb + 16, a1);
+        mma(kb, a0);
+        load(kb + 32, a0);
+        mma(kb + 16, a1);
+      }
     }
+    if (kh > 0) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t r = g0 + 16 * lq + 4 * q;
-      const f4v vq = quad(v + (int64_t)cc * n, r);
-      f4v dq = zero, sq = f4v{inv_noise, inv_noise, inv_noise, inv_noise};
-      if constexpr (DOT) dq = quad(dotv + (int64_t)cc * n, r);
-      if constexpr (DINV) sq = quad(dinv, r);
-      f4v zz;
+      for (int t = 0; t < 4; ++t) red[kh - 1][rg][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (kh == 0) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) zz[t] = sq[t] * (vq[t] - acc[t][q]);
-      if (lm < cn) {
-        float* o = out + (int64_t)cc * n;
-        if (VEC4 && r + 3 < i1) {
-          *reinterpret_cast<f4v*>(o + r) = zz;
-        } else {
+      for (int t = 0; t < 4; ++t) acc[t] = ((acc[t] + red[0][rg][t][lane]) + red[1][rg][t][lane]) +
+                                           red[2][rg][t][lane];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t r = g0 + 16 * lq + 4 * q;
+        const f4v vq = quad(v + (int64_t)cc * n, r);
+        f4v dq = zero, sq = f4v{inv_noise, inv_noise, inv_noise, inv_noise};
+        if constexpr (DOT) dq = quad(dotv + (int64_t)cc * n, r);
+        if constexpr (DINV) sq = quad(dinv, r);
+        f4v zz;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) zz[t] = sq[t] * (vq[t] - acc[t][q]);
+        if (lm < cn) {
+          float* o = out + (int64_t)cc * n;
+          if (VEC4 && r + 3 < i1) {
+            *reinterpret_cast<f4v*>(o + r) = zz;
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (r + t < i1) o[r + t] = zz[t];
+          }
+        }
+        if constexpr (DOT) {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
-            if (r + t < i1) o[r + t] = zz[t];
+            if (r + t < i1) dacc += (double)dq[t] * (double)zz[t];
         }
       }
-      if constexpr (DOT) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          if (r + t < i1) dacc += (double)dq[t] * (double)zz[t];
-      }
     }
+    __syncthreads();  // red is rewritten by the next pass
   }
   if constexpr (!DOT) return;
-  dacc += __shfl_xor(dacc, 16);
-  dacc += __shfl_xor(dacc, 32);
-  if (lq == 0) wsum[wave][lm] = dacc;
+  if (kh == 0) {
+    dacc += __shfl_xor(dacc, 16);
+    dacc += __shfl_xor(dacc, 32);
+    if (lq == 0) wsum[rg][lm] = dacc;
+  }
   __syncthreads();
   if (threadIdx.x < cn)
     dpart[(int64_t)(c0 + threadIdx.x) * nb + blockIdx.x] =
@@ -1659,15 +1741,19 @@ static int launch_ltv_mfma(const float* L, int64_t n, int k, const float* v, int
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, block, 0, st, L, n, k, v, ncols, chunk, wpart, rs);
   };
+  auto go16 = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kLtvWaves), 0, st, L, n, k, v, ncols, chunk, wpart,
+                       rs);
+  };
 #define MGP_LTV(NCT, U)                                                          \
   (vec4 ? (rs ? go(k_ltv_mfma<NCT, U, true, true>) : go(k_ltv_mfma<NCT, U, true, false>)) \
         : (rs ? go(k_ltv_mfma<NCT, U, false, true>) : go(k_ltv_mfma<NCT, U, false, false>)))
   switch (nct) {
     case 1:
       if (vec4)
-        rs ? go(k_ltv_c16<true, true>) : go(k_ltv_c16<true, false>);
+        rs ? go16(k_ltv_c16<true, true>) : go16(k_ltv_c16<true, false>);
       else
-        rs ? go(k_ltv_c16<false, true>) : go(k_ltv_c16<false, false>);
+        rs ? go16(k_ltv_c16<false, true>) : go16(k_ltv_c16<false, false>);
       break;
     case 2: MGP_LTV(2, 1); break;
     case 3: MGP_LTV(3, 1); break;
@@ -1699,23 +1785,42 @@ void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float n
                     const float* v, int ncols, float* out, WoodburyWork& w,
                     const float* dotv, int nb, double* dot_part, hipStream_t st,
                     const float* dinv) {
-  float* wsum = w.wsum.ensure((size_t)ncols * k);
   const int cpad = (int)round_up(ncols, 16);
   float* ut = w.u.ensure((size_t)cpad * k);
-  ltv(L, n, k, v, ncols, wsum, w, st, dinv);
-  hipLaunchKernelGGL(k_small_solve_t, dim3((unsigned)ceil_div((int64_t)k * cpad * 64, 256)),
-                     dim3(256), 0, st, wsum, k, ncols, Minv, ut);
+  if (k <= kPartSolveMaxK) {
+    // chunk partials of L^T v, then their sum and the small solve in one launch
+    float* wpart = nullptr;
+    int nbw = launch_ltv_mfma(L, n, k, v, ncols, w, &wpart, st, dinv);
+    if (nbw == 0) {
+      nbw = lt_chunks(n);
+      wpart = w.wpart.ensure((size_t)nbw * k * ncols);
+      launch_lt_part(L, n, k, v, ncols, nbw, wpart, st, dinv);
+    }
+    hipLaunchKernelGGL(k_part_solve_t, dim3((unsigned)cpad), dim3(1024), 0, st, wpart, nbw, k,
+                       ncols, Minv, ut);
+  } else {
+    float* wsum = w.wsum.ensure((size_t)ncols * k);
+    ltv(L, n, k, v, ncols, wsum, w, st, dinv);
+    hipLaunchKernelGGL(k_small_solve_t, dim3((unsigned)ceil_div((int64_t)k * cpad * 64, 256)),
+                       dim3(256), 0, st, wsum, k, ncols, Minv, ut);
+  }
   const int nbf = nb > 0 ? nb : cg_chunks(n);
   const dim3 grid((unsigned)nbf, (unsigned)ceil_div(ncols, 16));
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, L, n, k, ut, ncols, 1.0f / noise, v, out,
                        dinv, dotv, nbf, dot_part);
   };
+  auto go_mfma = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(64 * kWoodWaves), 0, st, L, n, k, ut, ncols,
+                       1.0f / noise, v, out, dinv, dotv, nbf, dot_part);
+  };
   if (k <= kWoodMfmaMaxK) {
     const bool vec4 = vec4_ok(n, nbf, {L, v, out, dinv, dotv});
 #define MGP_WOOD(V4)                                                                  \
-  (dinv ? (dot_part ? go(k_woodbury_mfma<V4, true, true>) : go(k_woodbury_mfma<V4, true, false>)) \
-        : (dot_part ? go(k_woodbury_mfma<V4, false, true>) : go(k_woodbury_mfma<V4, false, false>)))
+  (dinv ? (dot_part ? go_mfma(k_woodbury_mfma<V4, true, true>)                          \
+                    : go_mfma(k_woodbury_mfma<V4, true, false>))                        \
+        : (dot_part ? go_mfma(k_woodbury_mfma<V4, false, true>)                         \
+                    : go_mfma(k_woodbury_mfma<V4, false, false>)))
     if (vec4)
       MGP_WOOD(true);
     else
