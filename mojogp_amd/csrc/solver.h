@@ -12,6 +12,12 @@ int reduction_chunks(int64_t n);
 // Row chunks of the batched CG's dot partials (~256 rows each, <= 2048): the
 // CG vector kernels and the Woodbury apply run one workgroup per chunk.
 int cg_chunks(int64_t n);
+// Rows per chunk of those kernels: ceil(n / nb) rounded up to a multiple of 4,
+// so 16-byte vector accesses never straddle a chunk (trailing chunks may be
+// empty and then contribute zero partials).
+__host__ __device__ inline int64_t cg_chunk_rows(int64_t n, int64_t nb) {
+  return (((n + nb - 1) / nb) + 3) & ~(int64_t)3;
+}
 
 // part[c*nb + b] = sum_{i in chunk b} a[c*n+i] * b[c*n+i]   (fp64)
 void coldot_partial(const float* a, const float* b, int64_t n, int ncols, int nb,

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(64) void k_coldot_w(const float* __restrict__ a,
                                                  const float* __restrict__ bv, int64_t n, int nb,
                                                  int vec4, double* __restrict__ part) {
   const int c = blockIdx.y, lane = threadIdx.x;
-  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t chunk = cg_chunk_rows(n, nb);
   const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   const float* ac = a + (int64_t)c * n;
   const float* bc = bv + (int64_t)c * n;
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(64) void k_cg_update_w(float* __restrict__ x, float
   const float a = (is_nan(rz) || is_nan(pap) || pap < 1e-10f) ? 0.0f : rz / pap;
   if (blockIdx.x == 0 && lane == 0) s.alpha[c] = a;
   const bool active = !(a == 0.0f || is_nan(a));
-  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t chunk = cg_chunk_rows(n, nb);
   const int64_t off = (int64_t)c * n;
   const int b0 = blockIdx.x * G, b1 = min(nb, b0 + G);
   for (int bb = b0; bb < b1; ++bb) {
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(64) void k_cg_pupdate_w(float* __restrict__ p,
     }
   }
   const bool plain = (b == 0.0f || is_nan(b));
-  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t chunk = cg_chunk_rows(n, nb);
   const int64_t off = (int64_t)c * n;
   auto one = [&](float po, float zi) __attribute__((always_inline)) -> float {
     return (plain || is_nan(po)) ? zi : zi + b * po;
@@ -861,56 +861,66 @@ __global__ __launch_bounds__(256) void k_small_solve_t(const float* __restrict__
 }
 
 // k_part_reduce followed by k_small_solve_t in one launch, for the Woodbury
-// apply: block c (of cpad) adds column c's chunk partials w[c][kk] =
-// sum_b wpart[(b ncols + c) k + kk] in the order of k_part_reduce (16
-// stripes of chunks b = s, s + 16, .., each in order, then the stripes in
-// order, rounded to fp32) into LDS, then forms ut[((c/16) k + kk) 16 + c%16]
-// = sum_q Minv[kk k + q] w[c][q] as k_small_solve_t does (one wave per
-// output, lanes stride q, fixed shuffle tree); zero for padding columns.
+// apply.  Block (c, g) of (cpad, ceil(k / 16)): first column c's chunk
+// partials w[c][kk] = sum_b wpart[(b ncols + c) k + kk] for every kk, added in
+// the order of k_part_reduce (16 stripes of chunks b = s, s + 16, .., each in
+// order, then the stripes in order, rounded to fp32) into LDS; then wave w
+// forms ut[((c/16) k + kk) 16 + c%16] = sum_q Minv[kk k + q] w[c][q] for
+// kk = 16 g + w as k_small_solve_t does (lanes stride q, fixed shuffle tree);
+// zero for padding columns.
 constexpr int kPartSolveMaxK = 256;
 __global__ __launch_bounds__(1024) void k_part_solve_t(const float* __restrict__ wpart, int nb,
                                                        int k, int ncols,
                                                        const float* __restrict__ Minv,
                                                        float* __restrict__ ut) {
-  __shared__ double sm[16][64];
+  __shared__ double sm[16][kPartSolveMaxK];
   __shared__ float wc[kPartSolveMaxK];
   const int c = blockIdx.x;
   const int kl = threadIdx.x & 63, sidx = threadIdx.x >> 6;
   const int64_t total = (int64_t)k * ncols;
-  for (int kk0 = 0; kk0 < k; kk0 += 64) {
-    const int kk = kk0 + kl;
-    double acc = 0.0;
-    if (c < ncols && kk < k) {
-      const int64_t o = (int64_t)c * k + kk;
-      int b = sidx;
-      for (; b + 7 * 16 < nb; b += 8 * 16) {
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  if (c < ncols) {
+    const float* wc0 = wpart + (int64_t)c * k + kl;
+    int b = sidx;
+    for (; b + 7 * 16 < nb; b += 8 * 16) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (kl + 64 * u >= k) break;
         float t[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) t[q] = wpart[(int64_t)(b + 16 * q) * total + o];
+        for (int q = 0; q < 8; ++q) t[q] = wc0[(int64_t)(b + 16 * q) * total + 64 * u];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc += (double)t[q];
+        for (int q = 0; q < 8; ++q) acc[u] += (double)t[q];
       }
-      for (; b < nb; b += 16) acc += (double)wpart[(int64_t)b * total + o];
     }
-    sm[sidx][kl] = acc;
-    __syncthreads();
-    if (sidx == 0 && kk < k) {
-      double t = sm[0][kl];
+    for (; b < nb; b += 16)
 #pragma unroll
-      for (int q = 1; q < 16; ++q) t += sm[q][kl];
+      for (int u = 0; u < 4; ++u)
+        if (kl + 64 * u < k) acc[u] += (double)wc0[(int64_t)b * total + 64 * u];
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (kl + 64 * u < k) sm[sidx][kl + 64 * u] = acc[u];
+  __syncthreads();
+  if (sidx < 4) {
+    const int kk = kl + 64 * sidx;
+    if (kk < k) {
+      double t = sm[0][kk];
+#pragma unroll
+      for (int q = 1; q < 16; ++q) t += sm[q][kk];
       wc[kk] = (float)t;
     }
-    __syncthreads();
   }
+  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int kk = wave; kk < k; kk += 16) {
-    float s = 0.0f;
-    if (c < ncols)
-      for (int q = lane; q < k; q += 64) s = fmaf(Minv[(int64_t)kk * k + q], wc[q], s);
+  const int kk = 16 * blockIdx.y + wave;
+  if (kk >= k) return;
+  float s = 0.0f;
+  if (c < ncols)
+    for (int q = lane; q < k; q += 64) s = fmaf(Minv[(int64_t)kk * k + q], wc[q], s);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    if (lane == 0) ut[((int64_t)(c / 16) * k + kk) * 16 + (c & 15)] = s;
-  }
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) ut[((int64_t)(c / 16) * k + kk) * 16 + (c & 15)] = s;
 }
 
 // out[c][i] = (v[c][i] - sum_kk L[kk][i] u[c][kk]) * (DINV ? dinv[i] : inv_noise)
@@ -1037,7 +1047,7 @@ __global__ __launch_bounds__(64 * kWoodWaves) void k_woodbury_mfma(
     for (int j = threadIdx.x; j < kpad * 16; j += 64 * kWoodWaves) sB[j] = j < k * 16 ? ub[j] : 0.0f;
   }
   __syncthreads();
-  const int64_t chunk = (n + nb - 1) / nb;
+  const int64_t chunk = cg_chunk_rows(n, nb);
   const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   const int64_t safe = VEC4 ? n - 4 : n - 1;
   const f4v zero = f4v{0.f, 0.f, 0.f, 0.f};
@@ -1056,7 +1066,7 @@ __global__ __launch_bounds__(64 * kWoodWaves) void k_woodbury_mfma(
   double dacc = 0.0;
   // every wave makes the same number of passes (the barriers below); rows
   // past the chunk only feed D rows that are not stored
-  const int64_t passes = (i1 - i0 + 255) / 256;
+  const int64_t passes = i1 > i0 ? (i1 - i0 + 255) / 256 : 0;
   for (int64_t pass = 0; pass < passes; ++pass) {
     const int64_t g0 = i0 + 256 * pass + 64 * rg;
     const int64_t ra = g0 + 4 * lm;
@@ -1385,9 +1395,9 @@ int cg_chunks(int64_t n) {
 }
 
 // 16-byte vector access is safe when the arrays are 16-byte aligned and every
-// column and chunk starts on a multiple of 4 elements.
+// column and chunk (cg_chunk_rows) starts on a multiple of 4 elements.
 static int vec4_ok(int64_t n, int nb, std::initializer_list<const void*> ptrs) {
-  if (n % 4 != 0 || ceil_div(n, nb) % 4 != 0) return 0;
+  if (n % 4 != 0 || cg_chunk_rows(n, nb) % 4 != 0) return 0;
   for (const void* q : ptrs)
     if (reinterpret_cast<uintptr_t>(q) % 16 != 0) return 0;
   return 1;
@@ -1796,8 +1806,8 @@ void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float n
       wpart = w.wpart.ensure((size_t)nbw * k * ncols);
       launch_lt_part(L, n, k, v, ncols, nbw, wpart, st, dinv);
     }
-    hipLaunchKernelGGL(k_part_solve_t, dim3((unsigned)cpad), dim3(1024), 0, st, wpart, nbw, k,
-                       ncols, Minv, ut);
+    hipLaunchKernelGGL(k_part_solve_t, dim3((unsigned)cpad, (unsigned)ceil_div(k, 16)),
+                       dim3(1024), 0, st, wpart, nbw, k, ncols, Minv, ut);
   } else {
     float* wsum = w.wsum.ensure((size_t)ncols * k);
     ltv(L, n, k, v, ncols, wsum, w, st, dinv);
