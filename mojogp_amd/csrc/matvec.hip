@@ -1662,6 +1662,91 @@ __global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, 
   *reinterpret_cast<u4*>(half + half_frag_index(blk, r, g, 1) * 4) = u4{w[4], w[5], w[6], w[7]};
 }
 
+// k_fill_half with one workgroup per stored block: the block's 256 row points
+// and 256 column points are staged in LDS dimension-major ([k][256], zero past
+// n), so a thread's eight columns and its row cost LDS reads instead of
+// 9 d scalar global loads; thread t forms the units t, t + 256, .. of the
+// block in fragment order (the same arithmetic, so the same values, as
+// k_fill_half).  d <= kFillLdsMaxD.
+constexpr int kFillLdsMaxD = 32;
+template <int KIND>
+__global__ __launch_bounds__(256) void k_fill_half_lds(const float* __restrict__ Z, int64_t n,
+                                                       int d, float os, float lim, int shift,
+                                                       int64_t nb, uint32_t* __restrict__ half) {
+  extern __shared__ float zs[];  // [2][d][256]: rows, then columns
+  constexpr int kGroups = kHalfRows / 8;
+  const int64_t blk = blockIdx.x;
+  // block index -> (b, delta), the inverse of dense_half_index (uniform)
+  int64_t b, delta;
+  if (nb & 1) {
+    const int64_t w = (nb - 1) / 2 + 1;
+    b = blk / w;
+    delta = blk - b * w;
+  } else {
+    const int64_t h = nb / 2;
+    if (blk < h * (h + 1)) {
+      b = blk / (h + 1);
+      delta = blk - b * (h + 1);
+    } else {
+      const int64_t q = blk - h * (h + 1);
+      b = h + q / h;
+      delta = q - (q / h) * h;
+    }
+  }
+  int64_t J = b + delta;
+  if (J >= nb) J -= nb;
+  for (int t = threadIdx.x; t < 2 * kHalfRows * d; t += 256) {
+    const int side = t / (kHalfRows * d);
+    const int rem = t - side * (kHalfRows * d);
+    const int p = rem / d, k = rem - p * d;
+    const int64_t pt = (side ? J : b) * kHalfRows + p;
+    zs[(side * d + k) * kHalfRows + p] = pt < n ? Z[pt * d + k] : 0.0f;
+  }
+  __syncthreads();
+  const float* zr_s = zs;
+  const float* zc_s = zs + d * kHalfRows;
+  const int64_t row0 = b * kHalfRows, col0 = J * kHalfRows;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  for (int u = threadIdx.x; u < kHalfRows * kGroups; u += 256) {
+    const int lane = u & 63;
+    const int r = 32 * ((u >> 7) & 7) + 16 * ((u >> 6) & 1) + (lane & 15);
+    const int g = 4 * (u >> 10) + (lane >> 4);
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+    if (row0 + r < n) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = 8 * g + e;
+        if (col0 + c < n) {
+          float r2 = 0.0f;
+          for (int k = 0; k < d; ++k) {
+            const float df = zr_s[k * kHalfRows + r] - zc_s[k * kHalfRows + c];
+            r2 = fmaf(df, df, r2);
+          }
+          x[e] = ldexpf(os * kval<KIND>(r2, lim), shift);
+        }
+      }
+    }
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      hi[e] = (_Float16)x[e];
+      lo[e] = (_Float16)(x[e] - (float)hi[e]);
+    }
+    uint32_t w[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w[e] = (uint32_t)__builtin_bit_cast(uint16_t, hi[2 * e]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, hi[2 * e + 1]) << 16);
+      w[4 + e] = (uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e]) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e + 1]) << 16);
+    }
+    *reinterpret_cast<u4*>(half + half_frag_index(blk, r, g, 0) * 4) = u4{w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<u4*>(half + half_frag_index(blk, r, g, 1) * 4) = u4{w[4], w[5], w[6], w[7]};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Gradient products: out[p][c][i] = sum_j dk(x_i, x_j)/dtheta_p V[c][j] for the
 // engine parameters theta = [l | l_0..l_{d-1}, os] (fused_all_gradients_matvec,
@@ -2235,6 +2320,17 @@ void fill_dense_half(int kind, float outputscale, const PackedPoints& pts, int d
                      int64_t nb, uint32_t* half, hipStream_t st) {
   MGP_REQUIRE(d >= 1 && pts.n >= 1, "dense fill needs points");
   const int64_t nblocks = nb * (nb + 1) / 2;
+  if (d <= kFillLdsMaxD) {
+    auto fn = kind == KIND_RBF        ? k_fill_half_lds<KIND_RBF>
+              : kind == KIND_MATERN12 ? k_fill_half_lds<KIND_MATERN12>
+              : kind == KIND_MATERN32 ? k_fill_half_lds<KIND_MATERN32>
+                                      : k_fill_half_lds<KIND_MATERN52>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256),
+                       (size_t)2 * d * kHalfRows * sizeof(float), st, pts.z.ptr, pts.n, d,
+                       outputscale, pts.exp2_limit, shift, nb, half);
+    MGP_HIP_CHECK(hipGetLastError());
+    return;
+  }
   const int64_t total = nblocks * kHalfRows * (kHalfRows / 8);
   auto fn = kind == KIND_RBF        ? k_fill_half<KIND_RBF>
             : kind == KIND_MATERN12 ? k_fill_half<KIND_MATERN12>
