@@ -971,7 +971,10 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
 #pragma unroll
       for (int w = 1; w < W; ++w) sum += *reinterpret_cast<const f2*>(src + w * wstride);
       const int64_t jl = 32 * ((c % kSymStages) * kSymSteps + kk) + 16 * t + (r_ln & 15);
-      *reinterpret_cast<f2*>(tp + (blk * kSymRows + jl) * 16 + r_c) = sum * r_scale;
+      // read once, by k_sym_reduce after this kernel: non-temporal, so the
+      // partials do not displace the column operands the XCDs share in L2
+      __builtin_nontemporal_store(sum * r_scale,
+                                  reinterpret_cast<f2*>(tp + (blk * kSymRows + jl) * 16 + r_c));
     }
   };
 
@@ -1446,20 +1449,22 @@ __global__ __launch_bounds__(256) void k_sym_reduce(const float* __restrict__ fw
     }
   const int64_t J = j / kSymRows, jl = j - J * kSymRows;
   const float* col = tp + jl * 16 + 4 * c4;
+  // The partials are read once: non-temporal loads, eight in flight.
   auto slot = [&](int64_t dl, bool& formed) {
     int64_t bb = J - dl;
     if (bb < 0) bb += nb;
     formed = dl <= sym_span(bb, nb);
-    return *reinterpret_cast<const f4*>(col + (bb * hmax + dl - 1) * (int64_t)kSymRows * 16);
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const f4*>(col + (bb * hmax + dl - 1) * (int64_t)kSymRows * 16));
   };
   int64_t dl = 1;
-  for (; dl + 3 <= hmax; dl += 4) {
-    f4 v[4];
-    bool ok[4];
+  for (; dl + 7 <= hmax; dl += 8) {
+    f4 v[8];
+    bool ok[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = slot(dl + q, ok[q]);
+    for (int q = 0; q < 8; ++q) v[q] = slot(dl + q, ok[q]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < 8; ++q)
 #pragma unroll
       for (int e = 0; e < 4; ++e) tot[e] += ok[q] ? (double)v[q][e] : 0.0;
   }
