@@ -712,24 +712,25 @@ __global__ __launch_bounds__(256) void k_ltv_mfma(const float* __restrict__ L, i
 }
 
 // k_ltv_mfma for ncols <= 16 and k <= 256 with the chunk's rows and kk tiles
-// split over 16 waves: wave w takes the 64-row groups g0 = i0 + 64 (w & 3),
-// + 256, .. and the kk tiles t = (w >> 2) + 4 j, streaming the tiles over each
-// group (16 L rows x 64 rows per stage, double buffered; the waves of a block
-// read 1 KB runs of each L row) with the group's v values in registers.
-// MFMA roles as in k_ltv_mfma (A = L, B = v, D[kk][c]).  The four row
-// quarters of a tile set are added through LDS in quarter order, and the
-// waves of quarter 0 write the chunk's partial.  v rows past the chunk are
+// split over RG x TS waves: wave w takes the 64-row groups g0 = i0 +
+// 64 (w % RG), + 64 RG, .. and the kk tiles t = w / RG + TS j, streaming the
+// tiles over each group (16 L rows x 64 rows per stage, double buffered; the
+// waves of a block read 64 RG-row runs of each L row) with the group's v
+// values in registers.  MFMA roles as in k_ltv_mfma (A = L, B = v, D[kk][c]).
+// The RG row groups of a tile set are added through LDS in group order, and
+// the waves of group 0 write the chunk's partial.  v rows past the chunk are
 // zero; other out-of-range loads use clamped addresses and only feed D
-// entries that are not written.
-constexpr int kLtvWaves = 16;
-template <bool VEC4, bool RS>
-__global__ __launch_bounds__(64 * kLtvWaves) void k_ltv_c16(
+// entries that are not written.  RG = TS = 2 (4 waves) when there are enough
+// chunks to fill the GPU, RG = TS = 4 (16 waves) for small n.
+template <bool VEC4, bool RS, int RG, int TS>
+__global__ __launch_bounds__(64 * RG * TS) void k_ltv_c16(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ v, int ncols,
     int64_t chunk, float* __restrict__ wpart, const float* __restrict__ rs) {
-  __shared__ f4v red[3][4][4][64];  // quarters 1..3: [quarter - 1][tile set][j][lane]
+  constexpr int NJ = 16 / TS;  // tiles per wave (k <= 256)
+  __shared__ f4v red[RG - 1][TS][NJ][64];  // groups 1..RG-1: [group - 1][tile set][j][lane]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rh = wave & 3, th = wave >> 2;
+  const int rh = wave % RG, th = wave / RG;
   const int lm = lane & 15, lq = lane >> 4;
   const int64_t i0 = (int64_t)blockIdx.x * chunk, i1 = min(n, i0 + chunk);
   const int ktiles = (k + 15) / 16;
@@ -745,11 +746,11 @@ __global__ __launch_bounds__(64 * kLtvWaves) void k_ltv_c16(
       return x;
     }
   };
-  f4v acc[4];
+  f4v acc[NJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = zero;
+  for (int j = 0; j < NJ; ++j) acc[j] = zero;
   const float* vc = v + (int64_t)(lm < ncols ? lm : ncols - 1) * n;
-  for (int64_t g0 = i0 + 64 * rh; g0 < i1; g0 += 256) {
+  for (int64_t g0 = i0 + 64 * rh; g0 < i1; g0 += 64 * RG) {
     f4v b[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -763,9 +764,9 @@ __global__ __launch_bounds__(64 * kLtvWaves) void k_ltv_c16(
         for (int e = 0; e < 4; ++e) b[u][e] = r0 + e < i1 ? x[e] : 0.0f;
       }
     }
-    // tile t = th + 4 j
+    // tile t = th + TS j
     auto load = [&](int j, f4v (&a)[4]) __attribute__((always_inline)) {
-      const float* lr = L + (int64_t)min(16 * (th + 4 * j) + lm, k - 1) * n;
+      const float* lr = L + (int64_t)min(16 * (th + TS * j) + lm, k - 1) * n;
 #pragma unroll
       for (int u = 0; u < 4; ++u) a[u] = quad(lr, g0 + 16 * u + 4 * lq);
     };
@@ -779,28 +780,30 @@ __global__ __launch_bounds__(64 * kLtvWaves) void k_ltv_c16(
     f4v a0[4], a1[4];
     load(0, a0);
 #pragma unroll
-    for (int j = 0; j < 4; j += 2) {
-      if (th + 4 * j >= ktiles) break;  // uniform
+    for (int j = 0; j < NJ; j += 2) {
+      if (th + TS * j >= ktiles) break;  // uniform
       load(j + 1, a1);
       mma(acc[j], a0);
-      if (th + 4 * (j + 1) >= ktiles) break;
+      if (th + TS * (j + 1) >= ktiles) break;
       load(j + 2, a0);
       mma(acc[j + 1], a1);
     }
   }
   if (rh > 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (th + 4 * j < ktiles) red[rh - 1][th][j][lane] = acc[j];
+    for (int j = 0; j < NJ; ++j)
+      if (th + TS * j < ktiles) red[rh - 1][th][j][lane] = acc[j];
   }
   __syncthreads();
   if (rh > 0 || lm >= ncols) return;
   float* wp = wpart + ((int64_t)blockIdx.x * ncols + lm) * k;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = th + 4 * j;
+  for (int j = 0; j < NJ; ++j) {
+    const int t = th + TS * j;
     if (t >= ktiles) break;
-    const f4v tot = ((acc[j] + red[0][th][j][lane]) + red[1][th][j][lane]) + red[2][th][j][lane];
+    f4v tot = acc[j];
+#pragma unroll
+    for (int g = 0; g < RG - 1; ++g) tot += red[g][th][j][lane];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int kk = 16 * t + 4 * lq + q;
@@ -1009,30 +1012,30 @@ __global__ __launch_bounds__(256) void k_woodbury_rows(
 }
 
 // k_woodbury_rows on the fp32 matrix cores (k <= kWoodMfmaMaxK).  Block =
-// chunk blockIdx.x x the 16 columns of tile blockIdx.y, 16 waves: wave w
-// takes the 64-row groups g0 = i0 + 64 (w & 3), + 256, .. and the quarter
-// w >> 2 of the L rows (kq rows each, a multiple of 32), so four times as
-// many loads are in flight as with one wave per row group.  Per group,
+// chunk blockIdx.x x the 16 columns of tile blockIdx.y, 4 KS waves: wave w
+// takes the 64-row groups g0 = i0 + 64 (w & 3), + 256, .. and the part w >> 2
+// of KS parts of the L rows (kq rows each, a multiple of 32); KS = 4 for
+// small n, where the chunks do not fill the GPU (four times as many loads in
+// flight), KS = 1 (no split, no exchange) otherwise.  Per group,
 // v_mfma_f32_16x16x4_f32 tile t (0..3) maps MFMA row m to row g0 + 4 m + t
 // and the MFMA k index to L row kk: lane l supplies A = L[kk0 + l/16][g0 +
 // 4 (l%16) + t] (one 16-byte load per L row per lane covers the four tiles,
 // 256 contiguous bytes per L row) and B = u[c0 + l%16][kk0 + l/16] from the u
-// tile staged in LDS (zero past k).  The quarters' tiles are added through
-// LDS in quarter order by the waves of quarter 0, which finish the group: D
+// tile staged in LDS (zero past k).  The parts' tiles are added through
+// LDS in part order by the waves of part 0, which finish the group: D
 // row 4 (l/16) + q of tile t is row g0 + 16 (l/16) + 4 q + t of column
 // c0 + l%16, so each lane writes four runs of four rows.  dpart: each lane's
 // rows in order, the four lanes of a column by a shuffle butterfly, then the
 // row groups in order.  Loads are unconditional (addresses clamped into
 // range; the D rows they feed are not stored), so wait counts stay exact.
 constexpr int kWoodMfmaMaxK = 256;
-constexpr int kWoodWaves = 16;
-template <bool VEC4, bool DINV, bool DOT>
-__global__ __launch_bounds__(64 * kWoodWaves) void k_woodbury_mfma(
+template <bool VEC4, bool DINV, bool DOT, int KS>
+__global__ __launch_bounds__(256 * KS) void k_woodbury_mfma(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ ut, int ncols,
     float inv_noise, const float* v, float* out, const float* __restrict__ dinv,
     const float* dotv, int nb, double* __restrict__ dpart) {
   __shared__ float sB[kWoodMfmaMaxK * 16];
-  __shared__ f4v red[3][4][4][64];  // quarters 1..3: [quarter - 1][row group][tile][lane]
+  __shared__ f4v red[KS > 1 ? KS - 1 : 1][4][4][64];  // parts 1..KS-1: [part - 1][group][tile][lane]
   __shared__ double wsum[4][16];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1040,11 +1043,11 @@ __global__ __launch_bounds__(64 * kWoodWaves) void k_woodbury_mfma(
   const int lm = lane & 15, lq = lane >> 4;
   const int c0 = blockIdx.y * 16, cn = min(16, ncols - c0);
   const int kpad = (k + 31) & ~31;
-  const int kq = (((kpad + 3) / 4) + 31) & ~31;
+  const int kq = (((kpad + KS - 1) / KS) + 31) & ~31;
   const int kb0 = min(kpad, kh * kq), kb1 = min(kpad, kb0 + kq);
   {
     const float* __restrict__ ub = ut + (int64_t)blockIdx.y * k * 16;
-    for (int j = threadIdx.x; j < kpad * 16; j += 64 * kWoodWaves) sB[j] = j < k * 16 ? ub[j] : 0.0f;
+    for (int j = threadIdx.x; j < kpad * 16; j += 256 * KS) sB[j] = j < k * 16 ? ub[j] : 0.0f;
   }
   __syncthreads();
   const int64_t chunk = cg_chunk_rows(n, nb);
@@ -1097,15 +1100,20 @@ __global__ __launch_bounds__(64 * kWoodWaves) void k_woodbury_mfma(
         mma(kb + 16, a1);
       }
     }
-    if (kh > 0) {
+    if constexpr (KS > 1) {
+      if (kh > 0) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) red[kh - 1][rg][t][lane] = acc[t];
+        for (int t = 0; t < 4; ++t) red[kh - 1][rg][t][lane] = acc[t];
+      }
+      __syncthreads();
+      if (kh == 0) {
+#pragma unroll
+        for (int g = 0; g < KS - 1; ++g)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[t] += red[g][rg][t][lane];
+      }
     }
-    __syncthreads();
     if (kh == 0) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = ((acc[t] + red[0][rg][t][lane]) + red[1][rg][t][lane]) +
-                                           red[2][rg][t][lane];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t r = g0 + 16 * lq + 4 * q;
@@ -1133,7 +1141,7 @@ __global__ __launch_bounds__(64 * kWoodWaves) void k_woodbury_mfma(
         }
       }
     }
-    __syncthreads();  // red is rewritten by the next pass
+    if constexpr (KS > 1) __syncthreads();  // red is rewritten by the next pass
   }
   if constexpr (!DOT) return;
   if (kh == 0) {
@@ -1393,6 +1401,14 @@ int reduction_chunks(int64_t n) {
 int cg_chunks(int64_t n) {
   return (int)std::max<int64_t>(1, std::min<int64_t>(2048, ceil_div(n, 256)));
 }
+
+// Below this many chunks (two per CU) the L-streaming kernels of the Woodbury
+// apply run 16 waves per chunk instead of 4 (measured: n = 40k-50k faster,
+// n = 250k slower with 16).
+constexpr int kFewChunks = 512;
+// The merged chunk-sum and small solve re-adds a column's chunks x k partials
+// in every block; above this much work two launches are cheaper.
+constexpr int64_t kPartSolveMaxWork = 32768;
 
 // 16-byte vector access is safe when the arrays are 16-byte aligned and every
 // column and chunk (cg_chunk_rows) starts on a multiple of 4 elements.
@@ -1752,18 +1768,26 @@ static int launch_ltv_mfma(const float* L, int64_t n, int k, const float* v, int
     hipLaunchKernelGGL(kern, grid, block, 0, st, L, n, k, v, ncols, chunk, wpart, rs);
   };
   auto go16 = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, dim3(64 * kLtvWaves), 0, st, L, n, k, v, ncols, chunk, wpart,
-                       rs);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * 16), 0, st, L, n, k, v, ncols, chunk, wpart, rs);
   };
+  // 16 waves per chunk while the chunks do not fill the GPU, 4 otherwise
+  const bool wide = nbw < kFewChunks;
 #define MGP_LTV(NCT, U)                                                          \
   (vec4 ? (rs ? go(k_ltv_mfma<NCT, U, true, true>) : go(k_ltv_mfma<NCT, U, true, false>)) \
         : (rs ? go(k_ltv_mfma<NCT, U, false, true>) : go(k_ltv_mfma<NCT, U, false, false>)))
   switch (nct) {
     case 1:
-      if (vec4)
-        rs ? go16(k_ltv_c16<true, true>) : go16(k_ltv_c16<true, false>);
-      else
-        rs ? go16(k_ltv_c16<false, true>) : go16(k_ltv_c16<false, false>);
+      if (wide) {
+        if (vec4)
+          rs ? go16(k_ltv_c16<true, true, 4, 4>) : go16(k_ltv_c16<true, false, 4, 4>);
+        else
+          rs ? go16(k_ltv_c16<false, true, 4, 4>) : go16(k_ltv_c16<false, false, 4, 4>);
+      } else {
+        if (vec4)
+          rs ? go(k_ltv_c16<true, true, 2, 2>) : go(k_ltv_c16<true, false, 2, 2>);
+        else
+          rs ? go(k_ltv_c16<false, true, 2, 2>) : go(k_ltv_c16<false, false, 2, 2>);
+      }
       break;
     case 2: MGP_LTV(2, 1); break;
     case 3: MGP_LTV(3, 1); break;
@@ -1797,7 +1821,7 @@ void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float n
                     const float* dinv) {
   const int cpad = (int)round_up(ncols, 16);
   float* ut = w.u.ensure((size_t)cpad * k);
-  if (k <= kPartSolveMaxK) {
+  if (k <= kPartSolveMaxK && (int64_t)cg_chunks(n) * k <= kPartSolveMaxWork) {
     // chunk partials of L^T v, then their sum and the small solve in one launch
     float* wpart = nullptr;
     int nbw = launch_ltv_mfma(L, n, k, v, ncols, w, &wpart, st, dinv);
@@ -1820,22 +1844,25 @@ void woodbury_apply(const float* L, int64_t n, int k, const float* Minv, float n
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, L, n, k, ut, ncols, 1.0f / noise, v, out,
                        dinv, dotv, nbf, dot_part);
   };
+  const bool wide = nbf < kFewChunks;  // 16 waves per chunk for small n
   auto go_mfma = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, dim3(64 * kWoodWaves), 0, st, L, n, k, ut, ncols,
+    hipLaunchKernelGGL(kern, grid, dim3(wide ? 1024 : 256), 0, st, L, n, k, ut, ncols,
                        1.0f / noise, v, out, dinv, dotv, nbf, dot_part);
   };
   if (k <= kWoodMfmaMaxK) {
     const bool vec4 = vec4_ok(n, nbf, {L, v, out, dinv, dotv});
-#define MGP_WOOD(V4)                                                                  \
-  (dinv ? (dot_part ? go_mfma(k_woodbury_mfma<V4, true, true>)                          \
-                    : go_mfma(k_woodbury_mfma<V4, true, false>))                        \
-        : (dot_part ? go_mfma(k_woodbury_mfma<V4, false, true>)                         \
-                    : go_mfma(k_woodbury_mfma<V4, false, false>)))
+#define MGP_WOOD_KS(V4, KS)                                                           \
+  (dinv ? (dot_part ? go_mfma(k_woodbury_mfma<V4, true, true, KS>)                      \
+                    : go_mfma(k_woodbury_mfma<V4, true, false, KS>))                    \
+        : (dot_part ? go_mfma(k_woodbury_mfma<V4, false, true, KS>)                     \
+                    : go_mfma(k_woodbury_mfma<V4, false, false, KS>)))
+#define MGP_WOOD(V4) (wide ? MGP_WOOD_KS(V4, 4) : MGP_WOOD_KS(V4, 1))
     if (vec4)
       MGP_WOOD(true);
     else
       MGP_WOOD(false);
 #undef MGP_WOOD
+#undef MGP_WOOD_KS
   } else if (dinv) {
     dot_part ? go(k_woodbury_rows<true, true>) : go(k_woodbury_rows<true, false>);
   } else {
