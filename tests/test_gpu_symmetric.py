@@ -111,11 +111,12 @@ def test_symmetric_repeated_calls_bit_identical(monkeypatch):
 
 @pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, False, 4, 1100, 16),
                                             (ok.MATERN52, True, 3, 3000, 5),
-                                            (ok.RBF, True, 2, 300, 1)])
+                                            (ok.RBF, True, 2, 300, 1),
+                                            (ok.MATERN32, False, 2, 200, 3)])
 def test_materialized_symmetric_half(monkeypatch, kind, ard, d, n, t):
     """Materialized route, <= 16 columns: products from the symmetric half of K
-    (5, 12 and 2 blocks of 256 points) against the oracle and against the full
-    stored matrix (MGP_SYM_MATVEC=0), also after a parameter update."""
+    (5, 12, 2 and 1 blocks of 256 points) against the oracle and against the
+    full stored matrix (MGP_SYM_MATVEC=0), also after a parameter update."""
     rng = np.random.default_rng(600 + n)
     X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
     V = rng.normal(size=(t, n)).astype(np.float32)
@@ -141,3 +142,37 @@ def test_materialized_symmetric_half(monkeypatch, kind, ard, d, n, t):
     print(f"  relerr {e:.2e}, vs full {e_full:.2e}, after update {e2:.2e}", flush=True)
     assert e <= TOL and e2 <= TOL
     assert e_full <= 2 * TOL
+
+
+@pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, True, 4, 17800, 16),
+                                            (ok.MATERN52, False, 3, 20000, 7)])
+def test_materialized_symmetric_multi_block_items(monkeypatch, kind, ard, d, n, t):
+    """Sizes where a work item of the symmetric product covers several stored
+    blocks (70 blocks, even: 18 splits of 2 offsets; 79 blocks, odd: 20 splits
+    of 2), so the operand prefetch crosses blocks and some items are empty:
+    every row against the full stored matrix (MGP_SYM_MATVEC=0), 128 sampled
+    rows against the float64 oracle."""
+    rng = np.random.default_rng(700 + n)
+    X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
+    V = rng.normal(size=(t, n)).astype(np.float32)
+    V[0] *= 1e-3                                      # columns of different scales
+    ls = rng.uniform(0.6, 1.4, size=d if ard else 1)
+    params = np.concatenate([ls, [1.1]]).astype(np.float32)
+    rows = np.sort(rng.choice(n, size=128, replace=False))
+    print(f"materialized symmetric multi-block case kind={kind} d={d} n={n} t={t}", flush=True)
+    monkeypatch.delenv("MGP_SYM_MATVEC", raising=False)
+    p = NativeProvider(kind, ard, X, params, 0.05)
+    try:
+        p.materialize()
+        half = p.forward_matvec(V)
+        monkeypatch.setenv("MGP_SYM_MATVEC", "0")
+        full = p.forward_matvec(V)
+        monkeypatch.delenv("MGP_SYM_MATVEC", raising=False)
+    finally:
+        p.close()
+    ref = ok.forward_matvec(kind, X, V, params, 0.05, ard, rows=rows)
+    e_full = _relerr(half, full.astype(np.float64))
+    e = _relerr(half[:, rows], ref)
+    print(f"  vs full {e_full:.2e}, sampled rows vs oracle {e:.2e}", flush=True)
+    assert np.all(np.isfinite(half))
+    assert e <= TOL and e_full <= 2 * TOL
