@@ -64,6 +64,7 @@ struct DenseWorkspace {
   DevBuf<uint32_t> vpair;           // right-hand sides in row-tile-pair order (symmetric route)
   DevBuf<uint32_t> colmax, colmax_part;
   DevBuf<uint32_t> shifts;          // output exponents of the symmetric route [16]
+  DevBuf<uint32_t> colmax_sym;      // column maxima of the symmetric route, zero between products
   DevBuf<float> part;               // [splits][cpad][npad]
   DevBuf<float> tpart;              // transposed partial sums of the symmetric route
 };

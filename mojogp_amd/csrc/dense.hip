@@ -485,40 +485,103 @@ __global__ void k_dense_pack_half(const float* __restrict__ rows, int64_t nrows,
   half[half_frag_index(hb, r, g, 1)] = last8(v);
 }
 
-// Right-hand sides in row-tile-pair order: Vp[(u*2 + part)*64 + lane] (8
-// fp16), element e = 2^s_c V[c = lane%16][32 u + 16 (e/4) + 4 (lane/16) + e%4],
-// part 0 = hi, 1 = lo; zero for c >= ncols or past n.  Threads 0..15 also
-// write the output exponents shifts[c] = kshift + s_c (s_c = 0 for
-// c >= ncols), so the product reads them without a branch.
-__global__ void k_dense_pack_pair(const float* __restrict__ V, int64_t n, int ncols,
-                                  int64_t pairs, const uint32_t* __restrict__ colmax,
-                                  int kshift, int* __restrict__ shifts, h8* __restrict__ Vp) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx < 16)
-    shifts[idx] = kshift + ((int)idx < ncols ? scale_shift(__uint_as_float(colmax[idx])) : 0);
-  if (idx >= pairs * 64) return;
-  const int lane = (int)(idx & 63);
-  const int64_t u = idx >> 6;
-  const int c = lane & 15;
-  const int sh = c < ncols ? scale_shift(__uint_as_float(colmax[c])) : 0;
-  h8 hi, lo;
+// Column maxima of |V| for the symmetric route in one launch: block
+// (chunk, c) folds the max of its rows' |V| bits into cm[c] with an unsigned
+// atomicMax, which is order independent, so cm[c] equals the two-launch
+// k_dense_absmax_part / _final result bit for bit.  cm holds zeros on entry:
+// k_dense_sym_reduce clears it for the next product.
+__global__ __launch_bounds__(256) void k_dense_colmax_atomic(const float* __restrict__ V,
+                                                            int64_t n, uint32_t* __restrict__ cm) {
+  __shared__ uint32_t wm[4];
+  const int c = blockIdx.y, chunks = gridDim.x;
+  const int64_t len = (n + chunks - 1) / chunks;
+  const int64_t i0 = (int64_t)blockIdx.x * len, i1 = min(n, i0 + len);
+  const float* col = V + (int64_t)c * n;
+  uint32_t mx = 0;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x)
+    mx = max(mx, __float_as_uint(fabsf(col[i])));
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int64_t j = 32 * u + 16 * (e >> 2) + 4 * (lane >> 4) + (e & 3);
-    const float v = (c < ncols && j < n) ? ldexpf(V[(int64_t)c * n + j], sh) : 0.0f;
+  for (int o = 32; o >= 1; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
+  if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicMax(cm + c, max(max(wm[0], wm[1]), max(wm[2], wm[3])));
+}
+
+// Both right-hand-side layouts of the symmetric route in one launch, one
+// thread per (column c < 16, 32-point unit u): the fragment layout of
+// k_dense_pack_rhs (Vf, 16 columns) and the row-tile-pair layout (Vpp[(2 u +
+// part) 64 + c + 16 lg] holds points 32 u + 16 (e/4) + 4 lg + e%4), with the
+// scaling and split of k_dense_pack_rhs, plus the output exponents
+// shifts[c] = kshift + s_c.  Zero for c >= ncols or past n.
+__global__ __launch_bounds__(256) void k_dense_pack_sym(
+    const float* __restrict__ V, int64_t n, int ncols, int64_t units,
+    const uint32_t* __restrict__ cm, int kshift, int vec4, int* __restrict__ shifts,
+    h8* __restrict__ Vf, h8* __restrict__ Vpp) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= units * 16) return;
+  const int c = (int)(idx & 15);
+  const int64_t u = idx >> 4;
+  const int sh = c < ncols ? scale_shift(__uint_as_float(cm[c])) : 0;
+  if (u == 0) shifts[c] = kshift + sh;
+  float x[32];
+  const int64_t j0 = 32 * u;
+  const float* src = V + (int64_t)(c < ncols ? c : 0) * n + j0;
+  if (c < ncols && vec4 && j0 + 32 <= n) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const f4 a = *reinterpret_cast<const f4*>(src + 4 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * q + e] = a[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) x[e] = (c < ncols && j0 + e < n) ? src[e] : 0.0f;
+  }
+  _Float16 hi[32], lo[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const float v = ldexpf(x[e], sh);
     hi[e] = (_Float16)v;
     lo[e] = (_Float16)(v - (float)hi[e]);
   }
-  Vp[(u * 2) * 64 + lane] = hi;
-  Vp[(u * 2 + 1) * 64 + lane] = lo;
+  // fragment layout: group g = 4 u + k holds points 8 g .. 8 g + 7
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    h8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] = hi[8 * k + e];
+      b[e] = lo[8 * k + e];
+    }
+    Vf[(u * 2) * 64 + c + 16 * k] = a;
+    Vf[(u * 2 + 1) * 64 + c + 16 * k] = b;
+  }
+  // pair layout: lane c + 16 lg holds points 32 u + 16 (e / 4) + 4 lg + e % 4
+#pragma unroll
+  for (int lg = 0; lg < 4; ++lg) {
+    h8 a, b;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int p = 16 * (e >> 2) + 4 * lg + (e & 3);
+      a[e] = hi[p];
+      b[e] = lo[p];
+    }
+    Vpp[(u * 2) * 64 + c + 16 * lg] = a;
+    Vpp[(u * 2 + 1) * 64 + c + 16 * lg] = b;
+  }
+}
+
+__global__ void k_dense_clear16(uint32_t* __restrict__ p) {
+  if (threadIdx.x < 16) p[threadIdx.x] = 0u;
 }
 
 // Work item L = (row block b, delta split) of the symmetric half product.
 // Kf: the half in fragment order (half_frag_index); Vf: the right-hand sides
 // in the fragment layout of k_dense_pack_rhs (16 columns, one tile), so the
 // B operand of 32-column step S of the points is Vf[(2 S + p) 64 + lane];
-// Vpp: the right-hand sides in row-tile-pair order and shifts the output
-// exponents (k_dense_pack_pair).
+// Vpp: the right-hand sides in row-tile-pair order (element e of lane
+// c + 16 lg of unit u is point 32 u + 16 (e/4) + 4 lg + e%4) and shifts the
+// output exponents (both from k_dense_pack_sym).
 // Wave w owns the 32-column step w of every block of the item and streams
 // its column slice (8 row pairs of 4 KB, one contiguous 32 KB run) forming
 //   forward     acc[tile] += K[tile rows, step w] V_J[step w]  (16 row tiles)
@@ -699,8 +762,9 @@ __global__ __launch_bounds__(64 * kDsWaves) void k_dense_sym(
 __global__ __launch_bounds__(256) void k_dense_sym_reduce(
     const float* __restrict__ fwd, int splits, const float* __restrict__ tp, int64_t nb,
     int64_t hmax, int64_t mpad, int64_t n, int ncols, float noise,
-    const float* __restrict__ V, float* __restrict__ out) {
+    const float* __restrict__ V, float* __restrict__ out, uint32_t* __restrict__ cm) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < 16) cm[t] = 0u;  // the column maxima of the next product start from zero
   const int64_t j = t >> 2;
   const int c4 = (int)(t & 3);
   if (j >= n) return;
@@ -805,37 +869,35 @@ void dense_sym_forward(const DenseK& K, const float* V, int ncols, float noise, 
   MGP_REQUIRE(K.half_valid, "the symmetric half of K is not filled");
   const int64_t n = K.n, npad = K.npad, gpr = K.groups_per_row(), nb = K.blocks();
   const int64_t hmax = nb / 2;
-  const int chunks = (int)std::min<int64_t>(64, std::max<int64_t>(1, ceil_div(n, 4096)));
-  uint32_t* cpart = w.colmax_part.ensure((size_t)chunks * ncols);
-  uint32_t* colmax = w.colmax.ensure((size_t)ncols);
-  hipLaunchKernelGGL(k_dense_absmax_part, dim3((unsigned)chunks, (unsigned)ncols), dim3(256), 0,
-                     st, V, n, cpart);
-  hipLaunchKernelGGL(k_dense_absmax_final, dim3((unsigned)ncols), dim3(64), 0, st, cpart, chunks,
-                     colmax);
-  const int64_t vtot = 16 * gpr;
-  h8* vf = reinterpret_cast<h8*>(w.vpack.ensure((size_t)vtot * 8));
-  const int vec4 = (n % 4 == 0 && reinterpret_cast<uintptr_t>(V) % 16 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(k_dense_pack_rhs, dim3((unsigned)ceil_div(vtot, 256)), dim3(256), 0, st, V,
-                     n, ncols, 16, gpr, colmax, vec4, vf);
-  const int64_t pairs = npad / 32;
-  h8* vp = reinterpret_cast<h8*>(w.vpair.ensure((size_t)pairs * 2 * 64 * 4));
-  int* shifts = reinterpret_cast<int*>(w.shifts.ensure(16));
-  hipLaunchKernelGGL(k_dense_pack_pair, dim3((unsigned)ceil_div(pairs * 64, 256)), dim3(256), 0,
-                     st, V, n, ncols, pairs, colmax, K.shift, shifts, vp);
-  MGP_HIP_CHECK(hipGetLastError());
-
   int64_t splits = std::min<int64_t>(std::max<int64_t>(ceil_div(2048, nb), 1), hmax + 1);
   const int64_t dps = ceil_div(hmax + 1, splits);
   splits = ceil_div(hmax + 1, dps);
+  // every buffer first: nothing may fail between the column maxima (which
+  // accumulate into cm) and the reduction that clears cm again
+  const bool fresh = w.colmax_sym.count < 16;
+  uint32_t* cm = w.colmax_sym.ensure(16);
+  const int64_t vtot = 16 * gpr;
+  h8* vf = reinterpret_cast<h8*>(w.vpack.ensure((size_t)vtot * 8));
+  const int64_t units = npad / 32;
+  h8* vp = reinterpret_cast<h8*>(w.vpair.ensure((size_t)units * 2 * 64 * 4));
+  int* shifts = reinterpret_cast<int*>(w.shifts.ensure(16));
   float* fwd = w.part.ensure((size_t)splits * 16 * npad);
   float* tp = w.tpart.ensure((size_t)std::max<int64_t>(nb * hmax, 1) * kDsRows * 16);
+  if (fresh) hipLaunchKernelGGL(k_dense_clear16, dim3(1), dim3(64), 0, st, cm);
+  const int chunks = (int)std::min<int64_t>(64, std::max<int64_t>(1, ceil_div(n, 4096)));
+  hipLaunchKernelGGL(k_dense_colmax_atomic, dim3((unsigned)chunks, (unsigned)ncols), dim3(256), 0,
+                     st, V, n, cm);
+  const int vec4 = (n % 4 == 0 && reinterpret_cast<uintptr_t>(V) % 16 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(k_dense_pack_sym, dim3((unsigned)ceil_div(units * 16, 256)), dim3(256), 0,
+                     st, V, n, ncols, units, cm, K.shift, vec4, shifts, vf, vp);
+  MGP_HIP_CHECK(hipGetLastError());
   const int64_t items = nb * splits;
   hipLaunchKernelGGL(k_dense_sym, dim3((unsigned)items), dim3(64 * kDsWaves), 0, st,
                      reinterpret_cast<const h8*>(K.half.ptr), vf, vp, nb, splits, dps, hmax,
                      shifts, fwd, tp, npad);
   MGP_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(k_dense_sym_reduce, dim3((unsigned)ceil_div(4 * n, 256)), dim3(256), 0, st,
-                     fwd, (int)splits, tp, nb, hmax, npad, n, ncols, noise, V, out);
+                     fwd, (int)splits, tp, nb, hmax, npad, n, ncols, noise, V, out, cm);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
