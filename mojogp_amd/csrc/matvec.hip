@@ -1589,90 +1589,16 @@ __global__ __launch_bounds__(256) void k_fill_cross(const float* __restrict__ Zr
   out[idx] = os * kval<KIND>(r2, lim);
 }
 
-// Symmetric half of the dense K (dense.h layout): one thread per (stored
-// block, row, 8-column group) evaluates os * k(z_row, z_col) for the group's
-// eight columns from per-dimension differences (the arithmetic of
-// k_fill_cross), scales by 2^shift and stores the two-term fp16 split, hi and
-// lo as two 16-byte units in fragment order (half_frag_index; consecutive
-// threads write consecutive units); rows and columns past n are zero.
+// Symmetric half of the dense K (dense.h layout), one workgroup per stored
+// block: the block's 256 row points and 256 column points are staged in LDS
+// dimension-major ([k][256], zero past n); thread t forms the units t,
+// t + 256, .. of the block in fragment order: os * k(z_row, z_col) for one
+// row and eight columns from per-dimension differences (the arithmetic of
+// k_fill_cross), scaled by 2^shift and stored as the two-term fp16 split, hi
+// and lo as two 16-byte units (consecutive threads write consecutive units);
+// rows and columns past n are zero.  d <= kFillLdsMaxD (the provider's
+// dimension limit).
 constexpr int kHalfRows = 256;
-template <int KIND>
-__global__ __launch_bounds__(256) void k_fill_half(const float* __restrict__ Z, int64_t n, int d,
-                                                   float os, float lim, int shift, int64_t nb,
-                                                   int64_t nblocks, uint32_t* __restrict__ half) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  constexpr int kGroups = kHalfRows / 8;
-  if (idx >= nblocks * kHalfRows * kGroups) return;
-  const int64_t blk = idx / (kHalfRows * kGroups);
-  const int u = (int)(idx - blk * (kHalfRows * kGroups));
-  const int lane = u & 63;
-  const int r = 32 * ((u >> 7) & 7) + 16 * ((u >> 6) & 1) + (lane & 15);
-  const int g = 4 * (u >> 10) + (lane >> 4);
-  // block index -> (b, delta), the inverse of dense_half_index
-  int64_t b, delta;
-  if (nb & 1) {
-    const int64_t w = (nb - 1) / 2 + 1;
-    b = blk / w;
-    delta = blk - b * w;
-  } else {
-    const int64_t h = nb / 2;
-    if (blk < h * (h + 1)) {
-      b = blk / (h + 1);
-      delta = blk - b * (h + 1);
-    } else {
-      const int64_t q = blk - h * (h + 1);
-      b = h + q / h;
-      delta = q - (q / h) * h;
-    }
-  }
-  int64_t J = b + delta;
-  if (J >= nb) J -= nb;
-  const int64_t i = b * kHalfRows + r;
-  const int64_t j0 = J * kHalfRows + 8 * g;
-  float x[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-  if (i < n) {
-    const float* zr = Z + i * d;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int64_t j = j0 + e;
-      if (j < n) {
-        const float* zc = Z + j * d;
-        float r2 = 0.0f;
-        for (int k = 0; k < d; ++k) {
-          const float df = zr[k] - zc[k];
-          r2 = fmaf(df, df, r2);
-        }
-        x[e] = ldexpf(os * kval<KIND>(r2, lim), shift);
-      }
-    }
-  }
-  _Float16 hi[8], lo[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    hi[e] = (_Float16)x[e];
-    lo[e] = (_Float16)(x[e] - (float)hi[e]);
-  }
-  uint32_t w[8];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    w[e] = (uint32_t)__builtin_bit_cast(uint16_t, hi[2 * e]) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, hi[2 * e + 1]) << 16);
-    w[4 + e] = (uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e]) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, lo[2 * e + 1]) << 16);
-  }
-  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-  *reinterpret_cast<u4*>(half + half_frag_index(blk, r, g, 0) * 4) = u4{w[0], w[1], w[2], w[3]};
-  *reinterpret_cast<u4*>(half + half_frag_index(blk, r, g, 1) * 4) = u4{w[4], w[5], w[6], w[7]};
-}
-
-// k_fill_half with one workgroup per stored block: the block's 256 row points
-// and 256 column points are staged in LDS dimension-major ([k][256], zero past
-// n), so a thread's eight columns and its row cost LDS reads instead of
-// 9 d scalar global loads; thread t forms the units t, t + 256, .. of the
-// block in fragment order (the same arithmetic, so the same values, as
-// k_fill_half).  d <= kFillLdsMaxD.
 constexpr int kFillLdsMaxD = 32;
 template <int KIND>
 __global__ __launch_bounds__(256) void k_fill_half_lds(const float* __restrict__ Z, int64_t n,
@@ -2324,25 +2250,15 @@ void fill_cross(int kind, float outputscale, const PackedPoints& rows, int64_t r
 void fill_dense_half(int kind, float outputscale, const PackedPoints& pts, int d, int shift,
                      int64_t nb, uint32_t* half, hipStream_t st) {
   MGP_REQUIRE(d >= 1 && pts.n >= 1, "dense fill needs points");
+  MGP_REQUIRE(d <= kFillLdsMaxD, "dense fill supports input dimension <= 32");
   const int64_t nblocks = nb * (nb + 1) / 2;
-  if (d <= kFillLdsMaxD) {
-    auto fn = kind == KIND_RBF        ? k_fill_half_lds<KIND_RBF>
-              : kind == KIND_MATERN12 ? k_fill_half_lds<KIND_MATERN12>
-              : kind == KIND_MATERN32 ? k_fill_half_lds<KIND_MATERN32>
-                                      : k_fill_half_lds<KIND_MATERN52>;
-    hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256),
-                       (size_t)2 * d * kHalfRows * sizeof(float), st, pts.z.ptr, pts.n, d,
-                       outputscale, pts.exp2_limit, shift, nb, half);
-    MGP_HIP_CHECK(hipGetLastError());
-    return;
-  }
-  const int64_t total = nblocks * kHalfRows * (kHalfRows / 8);
-  auto fn = kind == KIND_RBF        ? k_fill_half<KIND_RBF>
-            : kind == KIND_MATERN12 ? k_fill_half<KIND_MATERN12>
-            : kind == KIND_MATERN32 ? k_fill_half<KIND_MATERN32>
-                                    : k_fill_half<KIND_MATERN52>;
-  hipLaunchKernelGGL(fn, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, pts.z.ptr, pts.n,
-                     d, outputscale, pts.exp2_limit, shift, nb, nblocks, half);
+  auto fn = kind == KIND_RBF        ? k_fill_half_lds<KIND_RBF>
+            : kind == KIND_MATERN12 ? k_fill_half_lds<KIND_MATERN12>
+            : kind == KIND_MATERN32 ? k_fill_half_lds<KIND_MATERN32>
+                                    : k_fill_half_lds<KIND_MATERN52>;
+  hipLaunchKernelGGL(fn, dim3((unsigned)nblocks), dim3(256),
+                     (size_t)2 * d * kHalfRows * sizeof(float), st, pts.z.ptr, pts.n, d,
+                     outputscale, pts.exp2_limit, shift, nb, half);
   MGP_HIP_CHECK(hipGetLastError());
 }
 

@@ -112,11 +112,16 @@ def test_symmetric_repeated_calls_bit_identical(monkeypatch):
 @pytest.mark.parametrize("kind,ard,d,n,t", [(ok.RBF, False, 4, 1100, 16),
                                             (ok.MATERN52, True, 3, 3000, 5),
                                             (ok.RBF, True, 2, 300, 1),
-                                            (ok.MATERN32, False, 2, 200, 3)])
+                                            (ok.MATERN32, False, 2, 200, 3),
+                                            (ok.MATERN52, False, 32, 2000, 16),
+                                            (ok.RBF, True, 7, 2001, 4)])
 def test_materialized_symmetric_half(monkeypatch, kind, ard, d, n, t):
     """Materialized route, <= 16 columns: products from the symmetric half of K
-    (5, 12, 2 and 1 blocks of 256 points) against the oracle and against the
-    full stored matrix (MGP_SYM_MATVEC=0), also after a parameter update."""
+    (5, 12, 2, 1 and 8 blocks of 256 points) against the oracle and against
+    the full stored matrix (MGP_SYM_MATVEC=0), also after a parameter update.
+    d = 32 is the largest input dimension the provider takes (the fill stages
+    its points in LDS); n = 2001 packs the right-hand sides without 16-byte
+    loads."""
     rng = np.random.default_rng(600 + n)
     X = rng.uniform(-2, 2, size=(n, d)).astype(np.float32)
     V = rng.normal(size=(t, n)).astype(np.float32)
