@@ -636,6 +636,9 @@ def main(argv=None) -> int:
                     help="skip the mBCG-iteration and fit() measurements")
     ap.add_argument("--mbcg-only", action="store_true",
                     help="only time one mBCG iteration at configs 3 and 2 (profiling)")
+    ap.add_argument("--c5-only", action="store_true",
+                    help="only the config-5 LMC leg (structured product, mBCG iteration, "
+                         "fit, pathwise samples)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel of BYTES (HBM counter calibration)")
     args = ap.parse_args(argv)
@@ -661,6 +664,10 @@ def main(argv=None) -> int:
         return 0
     if args.c3_grad:
         print(json.dumps(_c3_gradient_trace_only()), flush=True)
+        return 0
+    if args.c5_only:
+        c5, _ = _lmc_c5(repeats=10, warmup=2)
+        print(json.dumps(c5), flush=True)
         return 0
     if args.mbcg_only:
         X, _, params, noise = _make_inputs()
