@@ -942,8 +942,13 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
   // and writes them, unscaled, to tp.  Unit u < kSymSteps * 256 is two
   // right-hand sides (2h, 2h + 1 of the lane's four) of one lane of one
   // column tile; a thread's units share the lane half, so its column scales
-  // are fixed for the kernel.
+  // are fixed for the kernel.  Only the first W / 2 waves reduce: they are
+  // the older wave of each SIMD, which the issue arbiter favours, and they
+  // reach the stage barrier ~1000 cycles before their SIMD partner, so the
+  // reduction fills that wait while the younger waves go straight on to the
+  // next stage's arithmetic.
   constexpr int kRedUnits = kSymSteps * 256;
+  constexpr int kRedThreads = 64 * (W / 2);
   const int ru = threadIdx.x;
   const int r_ln = (ru >> 1) & 63, r_h = ru & 1;
   const int r_c = 4 * (r_ln >> 4) + 2 * r_h;
@@ -960,9 +965,11 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     const int slot = (int)(c & 1);
     const int64_t blk = b * hmax + stage_delta(c) - 1;
     constexpr int wstride = (int)(sizeof(tbuf[0][0][0]) / sizeof(float));
-    // Units ru, ru + 64 W, ...: the same lane half (64 W is a multiple of 128).
+    if (wave >= W / 2) return;
+    // Units ru, ru + kRedThreads, ...: the same lane half (kRedThreads is a
+    // multiple of 128).
 #pragma unroll
-    for (int uu = 0; uu < kRedUnits; uu += 64 * W) {
+    for (int uu = 0; uu < kRedUnits; uu += kRedThreads) {
       const int u = uu + ru;
       if (u >= kRedUnits) break;
       const int kk = u >> 8, t = (u >> 7) & 1;
@@ -990,8 +997,19 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     if (c + 1 < nst) fetch(stage_u0(c + 1));
     if (c > 0 && stage_delta(c - 1) > 0) reduce_stage(c - 1);
     const int64_t u0 = stage_u0(c);
+    // Wave priority per step: the younger wave of each SIMD leads the first
+    // step, the older one the second.  Under the arbiter's default (oldest
+    // first) the older wave finished its stage ~3000 cycles before its
+    // partner, which then ran alone at single-wave speed until the barrier.
+    auto lead = [&](int k) __attribute__((always_inline)) {
+      if ((wave < W / 2) == (k == 0))
+        __builtin_amdgcn_s_setprio(0);
+      else
+        __builtin_amdgcn_s_setprio(1);
+    };
     if (stage_delta(c) == 0) {
       for (int k = 0; k < kSymSteps; ++k) {
+        lead(k);
         const int64_t u = u0 + k;
         if (u >= dlo && u < dhi)
           step(st, k, u, st, std::true_type{}, std::false_type{});
@@ -999,8 +1017,10 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
           step(st, k, u, st, std::false_type{}, std::false_type{});
       }
     } else {
-      for (int k = 0; k < kSymSteps; ++k)
+      for (int k = 0; k < kSymSteps; ++k) {
+        lead(k);
         step(st, k, u0 + k, st, std::false_type{}, std::true_type{});
+      }
     }
     since_flush += kSymSteps;
     if (since_flush >= kFlushTiles / 2) {
