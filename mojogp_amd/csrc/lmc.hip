@@ -227,13 +227,16 @@ void LMCModel::latent_forward(int s, const float* V, int cols, float* out) {
 
 void LMCModel::forward(const float* V, int C, float* out) {
   const int64_t total = n * T * (int64_t)C;
+  // The latents share X and V: the first fused product packs V and the
+  // others reuse its packing (all latent providers run on one stream).
+  PackedRhs packed;
   for (int s = 0; s < R; ++s) {
     Provider& pv = *prov[s];
     if (pv.fused_route() && T <= 16) {
       // A_s mixing folded into the latent product's split-K reduction
       const float saved = pv.noise;
       pv.noise = 0.0f;
-      pv.forward_mixed(V, T * C, A_dev.ptr + s * T * T, T, s > 0, out);
+      pv.forward_mixed(V, T * C, A_dev.ptr + s * T * T, T, s > 0, out, &packed);
       pv.noise = saved;
       continue;
     }

@@ -98,6 +98,17 @@ constexpr int64_t kPackTileAlign = 96;
 void pack_points(const float* X_dev, int64_t n, const Coords& co,
                  PackedPoints& pp, hipStream_t st);
 
+// Right-hand sides packed for the tile kernels by one product, for reuse by
+// the next product of the same columns V over the same column points (the
+// latents of an LMC product share V and X).
+struct PackedRhs {
+  const float* src = nullptr;  // V the packing was made from
+  int64_t col_tiles = -1;      // column tiles of the points it was packed for
+  int ncols = 0;
+  const void* vp = nullptr;    // packed fp16 parts
+  const uint32_t* colmax = nullptr;
+};
+
 struct MatvecArgs {
   int kind = KIND_RBF;
   float outputscale = 1.f;
@@ -113,6 +124,13 @@ struct MatvecArgs {
   const float* mix = nullptr;
   int mix_T = 0;
   bool mix_accumulate = false;
+  // Optional packing reuse for a one-chunk product (ncols <= 64) on the
+  // one-sided tile kernel without a fixed arena: when *reuse describes V at
+  // these column points its packing is used, otherwise this product packs V
+  // and records its buffers in *reuse.  The recorded buffers live in this
+  // product's workspace and stay valid until that workspace's next product on
+  // the same stream.
+  PackedRhs* reuse = nullptr;
 };
 
 // out[c*m + i] = os * sum_j k(r_i, c_j) V[c*n + j]  (+ noise*V[c*m+i] if square)

@@ -2135,30 +2135,47 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
       continue;
     }
 
-    // Pack right-hand sides.
+    // Pack right-hand sides (or take the packing a previous product of the
+    // same V made over the same column points).
     const int64_t col_pairs = col_tiles / 2;
     ChunkBuffers buf(ws);
-    float* vp;
-    uint32_t* colmax = nullptr;
-    if (ncg == 0) {
+    const void* vp;
+    const uint32_t* colmax = nullptr;
+    PackedRhs* share = (a.reuse != nullptr && a.ncols <= chunk && ncg > 0 && ws.arena == nullptr)
+                           ? a.reuse : nullptr;
+    if (share != nullptr && share->vp != nullptr && share->src == Vc &&
+        share->col_tiles == col_tiles && share->ncols == nc) {
+      vp = share->vp;
+      colmax = share->colmax;
+    } else if (ncg == 0) {
       const int64_t npad = col_tiles * 16;
-      vp = buf.take(ws.vpack, (size_t)npad);
+      float* padded = buf.take(ws.vpack, (size_t)npad);
       hipLaunchKernelGGL(k_pad_vec, dim3((unsigned)ceil_div(npad, 256)), dim3(256),
-                         0, st, Vc, a.n, npad, vp);
+                         0, st, Vc, a.n, npad, padded);
+      vp = padded;
     } else {
-      colmax = buf.take(ws.colmax, 64);
+      uint32_t* cm = buf.take(ws.colmax, 64);
       const int chunks = (int)std::min<int64_t>(ceil_div(std::max<int64_t>(a.n, 1), 4096), 64);
       uint32_t* cpart = buf.take(ws.colmax_part, (size_t)64 * chunks);
       const int vec4 = (a.n % 4 == 0 && reinterpret_cast<uintptr_t>(Vc) % 16 == 0) ? 1 : 0;
       hipLaunchKernelGGL(k_col_absmax_part, dim3((unsigned)chunks, (unsigned)nc), dim3(256), 0,
                          st, Vc, a.n, vec4, cpart);
       hipLaunchKernelGGL(k_col_absmax_final, dim3((unsigned)nc), dim3(64), 0, st, cpart, chunks,
-                         colmax);
+                         cm);
       const int64_t total = (int64_t)ncg * col_pairs * 64;  // 8-half vectors per part
-      vp = buf.take(ws.vpack, (size_t)total * 2 * 4);
+      float* packed = buf.take(ws.vpack, (size_t)total * 2 * 4);
       hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256),
-                         0, st, Vc, a.n, nc, ncg, col_pairs, colmax, vec4,
-                         reinterpret_cast<h8*>(vp));
+                         0, st, Vc, a.n, nc, ncg, col_pairs, cm, vec4,
+                         reinterpret_cast<h8*>(packed));
+      vp = packed;
+      colmax = cm;
+      if (share != nullptr) {
+        share->src = Vc;
+        share->col_tiles = col_tiles;
+        share->ncols = nc;
+        share->vp = packed;
+        share->colmax = cm;
+      }
     }
     MGP_HIP_CHECK(hipGetLastError());
 

@@ -125,7 +125,7 @@ struct Provider {
   // task blocks of T columns (mix: device [T][T]), mixing folded into the
   // split-K reduction.
   void forward_mixed(const float* V, int ncols, const float* mix, int T, bool accumulate,
-                     float* out);
+                     float* out, PackedRhs* reuse = nullptr);
   // out[p][c][i] = sum_j dk_p(x_i, x_j) V[c][j] for all P parameters (device
   // arrays; out is [P][ncols][n]).
   DevBuf<float> gscale;  // per-parameter scale of the gradient sums

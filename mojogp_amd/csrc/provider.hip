@@ -242,7 +242,7 @@ bool Provider::fused_route() const {
 }
 
 void Provider::forward_mixed(const float* V, int ncols, const float* mix, int T, bool accumulate,
-                             float* out) {
+                             float* out, PackedRhs* reuse) {
   MGP_REQUIRE(fused_route(), "forward_mixed needs the fused tile route");
   MatvecArgs a;
   a.kind = kind;
@@ -255,6 +255,7 @@ void Provider::forward_mixed(const float* V, int ncols, const float* mix, int T,
   a.mix = mix;
   a.mix_T = T;
   a.mix_accumulate = accumulate;
+  a.reuse = reuse;
   fused_matvec(a, train, train, V, out, ws, st);
 }
 
