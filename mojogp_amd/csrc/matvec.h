@@ -141,8 +141,6 @@ struct MatvecWorkspace {
   DevBuf<uint32_t> colmax_part;  // [64][chunks] row-chunk maxima
   DevBuf<float> partial;  // split-K partial sums
   DevBuf<float> sym_tp;   // transposed partial sums of the symmetric product
-  DevBuf<uint32_t> pts32_a, pts32_b;  // points in the 32x32x16 operand layout
-  DevBuf<float> rhs32_f, rhs32_t;     // right-hand-side stacks of the 32x32 kernel
   // Fixed-arena mode (allocation-free callers): when arena is set, every work
   // buffer above is carved from [arena, arena + arena_bytes) instead of being
   // grown with hipMalloc; the split count is capped so the partial sums fit,

@@ -1057,369 +1057,6 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
 }
 
 // ---------------------------------------------------------------------------
-// Symmetric product on the 32x32x16 matrix cores (v_mfma_f32_32x32x16_f16).
-//
-// Same blocks, work items, partial layouts and reduction as k_sym_tile; the
-// larger MFMA shape hides about twice as well in the VALU stream of the
-// kernel values.  Operand layouts of v_mfma_f32_32x32x16_f16 (pinned on the
-// GPU): A[m][k] and B[k][n] sit at lane (m or n) + 32 (k / 8), element k % 8;
-// D[m][n] at lane n + 32 ((m / 4) % 2), element 4 (m / 8) + m % 4.
-// A wave owns two 32-row tiles of the block; a step is one 32-column tile:
-//   * distances D[j][i] (A = column points, B = row points; the Gram-form
-//     slots in 16-slot chunks, lane p + 32 h holding slots 16 m + 8 h + e of
-//     point p): lane l holds i = l % 32 and j = 8 (e / 4) + 4 (l / 32) + e % 4;
-//   * elements 8c .. 8c + 7 of the values are the B operand (K = j of chunk
-//     c) of the forward product out_I += [Vh; Vl]_J^T P, whose A operand is
-//     packed with the same j order, j(c, h, e) = 16 c + 8 (e / 4) + 4 h + e % 4,
-//     hi parts of the right-hand sides in rows 0..15 and lo parts in 16..31:
-//     one accumulator carries both, summed when flushed;
-//   * the values go to a wave-private LDS scratch as 8-byte (row i, 4
-//     columns) chunks at row i, quad jq ^ ((i / 4) % 8) and come back through
-//     ds_read_b64_tr_b16 as the B operand (K = rows i, natural order) of
-//     out_J^T += [Vh; Vl]_I^T P^T: lane 16 g + 4 e + s fetches the chunk of
-//     row 16 c + 8 (g / 2) + 4 rho + e, quad 4 (g % 2) + s, and receives
-//     P[16 c + 8 (g / 2) + 4 rho + e'][16 (g % 2) + lane % 16], e' = 0..3.
-// ---------------------------------------------------------------------------
-constexpr int kS32Waves = 8;                             // 64 rows each
-constexpr int kS32Steps = 2;                             // 32-column tiles per stage
-constexpr int kS32Stages = kSymRows / (32 * kS32Steps);  // stages per block
-constexpr int kS32SchedValu = 8;                         // VALU instructions per MFMA slot
-static_assert(kS32Waves * 64 == kSymRows, "a workgroup covers one block");
-
-typedef float f16v __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ int s32_quad(int i, int jq) { return 8 * i + (jq ^ ((i >> 2) & 7)); }
-
-template <int KIND, int KC>
-__global__ __launch_bounds__(64 * kS32Waves) void k_sym_tile32(
-    const h8* __restrict__ Bi, const h8* __restrict__ Aj, const h8* __restrict__ Vf,
-    const h8* __restrict__ Vt, int64_t nb, int64_t splits, int64_t dps, int64_t hmax, int ncols,
-    const uint32_t* __restrict__ colmax, float* __restrict__ fwd, float* __restrict__ tp,
-    int64_t mpad) {
-  constexpr int W = kS32Waves;
-  constexpr bool UNIT_G = KIND != KIND_MATERN52 && KIND != KIND_MATERN32;
-  constexpr int kBlk = KC + 2;  // 1 KB operand blocks per step: distance chunks, V stack
-  constexpr int kBlocks = kS32Steps * kBlk;
-  __shared__ h8 lds[2][kBlocks][64];
-  __shared__ uint64_t tsc[W][2][32 * 8];       // [wave][hi, lo][swizzled (row, quad)]
-  __shared__ f4 tbuf[2][kS32Steps][W][2][64];  // [buffer][step][wave][a][lane]
-  __shared__ h8 vrow[W][2][2][64];             // [wave][row tile][chunk][lane]
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t per = (int64_t)gridDim.x / kXcds;
-  const int64_t L = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
-  if (L >= nb * splits) return;
-  const int64_t b = L % nb;
-  const int64_t split = L / nb;
-  const int64_t rt0 = (b * kSymRows + 64 * wave) / 32;  // first 32-row tile of the wave
-  const int li = lane & 31, lh = lane >> 5;
-
-  h8 bi[2][KC];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) bi[rt][kc] = Bi[((rt0 + rt) * KC + kc) * 64 + lane];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) vrow[wave][rt][c][lane] = Vt[((rt0 + rt) * 2 + c) * 64 + lane];
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // as in k_sym_tile
-
-  f16v acc[2];
-  double accd[2][8];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[rt][e] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) accd[rt][e] = 0.0;
-  }
-  const float clampv = clamp_reg();
-  float one = 1.0f;
-  asm volatile("" : "+v"(one));
-  // Scratch quads this lane writes (row li, quad 2 q + lh) and fetches.
-  int wq[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) wq[q] = s32_quad(li, 2 * q + lh);
-  int rq[2][2];  // [chunk c][rho]
-#pragma unroll
-  for (int c = 0; c < 2; ++c)
-#pragma unroll
-    for (int rho = 0; rho < 2; ++rho)
-      rq[c][rho] = s32_quad(16 * c + 8 * lh + 4 * rho + ((lane >> 2) & 3),
-                            4 * ((lane >> 4) & 1) + (lane & 3));
-
-  const int64_t span = sym_span(b, nb);
-  const int64_t d0 = split * dps;
-  const int64_t d1 = min(d0 + dps, span + 1);
-  const int64_t nst = d1 > d0 ? (d1 - d0) * kS32Stages : 0;
-  auto stage_delta = [&](int64_t c) { return d0 + c / kS32Stages; };
-  auto stage_t0 = [&](int64_t c) {  // first 32-column tile of stage c
-    int64_t J = b + stage_delta(c);
-    if (J >= nb) J -= nb;
-    return J * (kSymRows / 32) + (c % kS32Stages) * kS32Steps;
-  };
-
-  constexpr int kFillPerWave = (kBlocks + W - 1) / W;
-  h8 pre[kFillPerWave];
-  auto fetch = [&](int64_t t0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int q = 0; q < kFillPerWave; ++q) {
-      const int bb = min(wave + q * W, kBlocks - 1);
-      const int k = bb / kBlk, r = bb - k * kBlk;
-      const h8* src = r < KC ? Aj + ((t0 + k) * KC + r) * 64 : Vf + ((t0 + k) * 2 + (r - KC)) * 64;
-      pre[q] = src[lane];
-    }
-  };
-  auto commit = [&](int st) __attribute__((always_inline)) {
-#pragma unroll
-    for (int q = 0; q < kFillPerWave; ++q) {
-      const int bb = wave + q * W;
-      if (bb < kBlocks) lds[st][bb][lane] = pre[q];
-    }
-  };
-
-  auto step = [&](int st, int k, int64_t jt, int slot, auto mask_tag, auto sym_tag)
-                  __attribute__((always_inline)) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    constexpr bool SYM = decltype(sym_tag)::value;
-    h8 a[KC];
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) a[kc] = lds[st][k * kBlk + kc][lane];
-    const h8 vf0 = lds[st][k * kBlk + KC][lane];
-    const h8 vf1 = lds[st][k * kBlk + KC + 1][lane];
-    f16v D[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) D[rt][e] = 0.f;
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
-        D[rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kc], bi[rt][kc], D[rt], 0, 0, 0);
-    }
-    f16v tacc;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) tacc[e] = 0.f;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      f16v s = D[rt];
-      if constexpr (MASK) {
-        if (jt == rt0 + rt) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            if (8 * (e >> 2) + 4 * lh + (e & 3) == li) s[e] = 0.0f;
-        }
-      }
-      float f[16], g[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) kval_scaled<KIND>(s[e], clampv, one, f[e], g[e]);
-      h8 PH[2], PL[2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          h2 hi, lo;
-          const int e = 8 * c + 2 * q;
-          split_pair<UNIT_G>(f[e], g[e], f[e + 1], g[e + 1], hi, lo);
-          PH[c][2 * q] = hi[0];
-          PH[c][2 * q + 1] = hi[1];
-          PL[c][2 * q] = lo[0];
-          PL[c][2 * q + 1] = lo[1];
-        }
-      f16v x = acc[rt];
-      x = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf0, PH[0], x, 0, 0, 0);
-      x = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf0, PL[0], x, 0, 0, 0);
-      x = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf1, PH[1], x, 0, 0, 0);
-      x = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf1, PL[1], x, 0, 0, 0);
-      acc[rt] = x;
-      if constexpr (SYM) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const u64x2 ph = __builtin_bit_cast(u64x2, PH[c]);
-          const u64x2 pl = __builtin_bit_cast(u64x2, PL[c]);
-          tsc[wave][0][wq[2 * c]] = ph[0];
-          tsc[wave][0][wq[2 * c + 1]] = ph[1];
-          tsc[wave][1][wq[2 * c]] = pl[0];
-          tsc[wave][1][wq[2 * c + 1]] = pl[1];
-        }
-        h8 TP[2][2];
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            const u64x2 v = {tr_read(&tsc[wave][p][rq[c][0]]), tr_read(&tsc[wave][p][rq[c][1]])};
-            TP[c][p] = __builtin_bit_cast(h8, v);
-          }
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const h8 vi = vrow[wave][rt][c][lane];
-          tacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(vi, TP[c][0], tacc, 0, 0, 0);
-          tacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(vi, TP[c][1], tacc, 0, 0, 0);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * KC + 8 + (SYM ? 8 : 0); ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, kS32SchedValu, 0);
-    }
-    if constexpr (SYM) {
-      // hi + lo right-hand-side rows: rhs 8 a + 4 lh + r at elements 4 a + r, + 8
-#pragma unroll
-      for (int a2 = 0; a2 < 2; ++a2) {
-        f4 t;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) t[r] = tacc[4 * a2 + r] + tacc[4 * a2 + r + 8];
-        tbuf[slot][k][wave][a2][lane] = t;
-      }
-    }
-  };
-  auto flush = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) accd[rt][e] += (double)(acc[rt][e] + acc[rt][e + 8]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[rt][e] = 0.f;
-    }
-  };
-  // Stage reduction by the older wave of each SIMD (see k_sym_tile): thread u
-  // < 256 adds lane u % 64, rhs group a = (u / 64) % 2 of step u / 128 over
-  // the 8 waves and writes rhs 8 a + 4 (lane / 32) .. + 3 of column
-  // 32 (stage step) + lane % 32.
-  const int ru = threadIdx.x;
-  const int r_ln = ru & 63, r_a = (ru >> 6) & 1, r_k = (ru >> 7) & 1;
-  const int r_c = 8 * r_a + 4 * (r_ln >> 5);
-  f4 r_scale = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int cc = r_c + e;
-    const int shift = cc < ncols ? col_shift(colmax[cc]) : 0;
-    r_scale[e] = ldexpf(1.0f, -(shift + kPScaleLog2));
-  }
-  auto reduce_stage = [&](int64_t c) __attribute__((always_inline)) {
-    if (wave >= W / 2) return;
-    const int slot = (int)(c & 1);
-    const int64_t blk = b * hmax + stage_delta(c) - 1;
-    f4 sum = tbuf[slot][r_k][0][r_a][r_ln];
-#pragma unroll
-    for (int w = 1; w < W; ++w) sum += tbuf[slot][r_k][w][r_a][r_ln];
-    const int64_t jl = 32 * ((c % kS32Stages) * kS32Steps + r_k) + (r_ln & 31);
-    __builtin_nontemporal_store(sum * r_scale,
-                                reinterpret_cast<f4*>(tp + (blk * kSymRows + jl) * 16 + r_c));
-  };
-
-  if (nst > 0) {
-    fetch(stage_t0(0));
-    commit(0);
-  }
-  int since_flush = 0;
-  for (int64_t c = 0; c < nst; ++c) {
-    const int st = (int)(c & 1);
-    __syncthreads();
-    if (c + 1 < nst) fetch(stage_t0(c + 1));
-    if (c > 0 && stage_delta(c - 1) > 0) reduce_stage(c - 1);
-    const int64_t t0 = stage_t0(c);
-    auto lead = [&](int k) __attribute__((always_inline)) {
-      if ((wave < W / 2) == (k == 0))
-        __builtin_amdgcn_s_setprio(0);
-      else
-        __builtin_amdgcn_s_setprio(1);
-    };
-    if (stage_delta(c) == 0) {
-      for (int k = 0; k < kS32Steps; ++k) {
-        lead(k);
-        const int64_t jt = t0 + k;
-        if (jt == rt0 || jt == rt0 + 1)
-          step(st, k, jt, st, std::true_type{}, std::false_type{});
-        else
-          step(st, k, jt, st, std::false_type{}, std::false_type{});
-      }
-    } else {
-      for (int k = 0; k < kS32Steps; ++k) {
-        lead(k);
-        step(st, k, t0 + k, st, std::false_type{}, std::true_type{});
-      }
-    }
-    since_flush += kS32Steps;
-    if (since_flush >= kFlushTiles / 2) {
-      flush();
-      since_flush = 0;
-    }
-    if (c + 1 < nst) commit(st ^ 1);
-  }
-  if (nst > 0 && stage_delta(nst - 1) > 0) {
-    __syncthreads();
-    reduce_stage(nst - 1);
-  }
-  flush();
-
-  // Forward partials of this split, unscaled by the fp16 factors: rhs
-  // 8 (e / 4) + 4 lh + e % 4 of row 32 (rt0 + rt) + li.
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int c = 8 * (e >> 2) + 4 * lh + (e & 3);
-      const int64_t i = 32 * (rt0 + rt) + li;
-      const int shift = c < ncols ? col_shift(colmax[c]) : 0;
-      fwd[(split * 16 + c) * mpad + i] = (float)ldexp(accd[rt][e], -(shift + kPScaleLog2));
-    }
-  }
-}
-
-// 32x32 operand layout of the Gram-form slots from the 16x16 one: h8 (T, m, L)
-// of the 32-point tile T, chunk m (slots 16 m + 8 h + 0..7, h = L / 32) for
-// point 32 T + L % 32.  One thread per h8; kb = K=32 chunks of the 16x16 layout.
-__global__ void k_pack_points32(const h8* __restrict__ A16, const h8* __restrict__ B16, int kb,
-                                int64_t tiles32, h8* __restrict__ A32, h8* __restrict__ B32) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int KC = 2 * kb;
-  if (idx >= tiles32 * KC * 64) return;
-  const int L = (int)(idx & 63);
-  const int m = (int)((idx >> 6) % KC);
-  const int64_t T = (idx >> 6) / KC;
-  const int p = L & 31, h = L >> 5;
-  const int64_t t = 2 * T + (p >> 4);
-  const int q = 2 * m + h;  // 8-slot group
-  const int64_t src = (t * kb + (q >> 2)) * 64 + (p & 15) + 16 * (q & 3);
-  A32[idx] = A16[src];
-  B32[idx] = B16[src];
-}
-
-// Right-hand-side stacks of k_sym_tile32, per 32-point tile T and chunk c:
-// lane l = m + 32 h, element e holds part (m / 16) (0 = hi, 1 = lo) of
-// V'[m % 16] at row 16 c + 8 h + e (Vt) and at 16 c + 8 (e / 4) + 4 h + e % 4 (Vf).
-__global__ void k_pack_rhs32(const float* __restrict__ V, int64_t n, int ncols, int64_t tiles32,
-                             const uint32_t* __restrict__ colmax, h8* __restrict__ Vf,
-                             h8* __restrict__ Vt) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= tiles32 * 2 * 64) return;
-  const int l = (int)(idx & 63);
-  const int c = (int)((idx >> 6) & 1);
-  const int64_t T = idx >> 7;
-  const int m = l & 31, h = l >> 5;
-  const int col = m & 15, part = m >> 4;
-  const int shift = col < ncols ? col_shift(colmax[col]) : 0;
-  h8 xf, xt;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int64_t jt = 32 * T + 16 * c + 8 * h + e;
-    const int64_t jf = 32 * T + 16 * c + 8 * (e >> 2) + 4 * h + (e & 3);
-    const float vt = (col < ncols && jt < n) ? ldexpf(V[(int64_t)col * n + jt], shift) : 0.0f;
-    const float vf = (col < ncols && jf < n) ? ldexpf(V[(int64_t)col * n + jf], shift) : 0.0f;
-    const _Float16 ht = (_Float16)vt, hf = (_Float16)vf;
-    xt[e] = part == 0 ? ht : (_Float16)(vt - (float)ht);
-    xf[e] = part == 0 ? hf : (_Float16)(vf - (float)hf);
-  }
-  Vf[idx] = xf;
-  Vt[idx] = xt;
-}
-
-// ---------------------------------------------------------------------------
 // Gradient traces on the matrix cores (Gram-form kernels).
 //
 // The pair-loop trace (solver.hip k_grad_trace) spends ~90 VALU instructions
@@ -1610,6 +1247,7 @@ __global__ __launch_bounds__(64 * kGtWaves) void k_grad_sym(
         zr[r][g][e] = (a < n && q < d) ? Z[a * d + q] : 0.0f;
       }
   }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // row operands before the loop (see k_sym_tile)
   f4 U[R][2 * QG];
   float rs[R];
   double T[QG][4];
@@ -2310,23 +1948,6 @@ SymFn pick_sym(int kb) {
   return nullptr;
 }
 
-using Sym32Fn = void (*)(const h8*, const h8*, const h8*, const h8*, int64_t, int64_t, int64_t,
-                         int64_t, int, const uint32_t*, float*, float*, int64_t);
-
-template <int KIND>
-Sym32Fn pick_sym32(int kb) {
-  switch (kb) {
-    case 1: return k_sym_tile32<KIND, 2>;
-    case 2: return k_sym_tile32<KIND, 4>;
-  }
-  return nullptr;
-}
-
-bool sym32_route(const PackedPoints& pts) {
-  const char* env = std::getenv("MGP_SYM_TILE32");
-  return env != nullptr && env[0] == '1' && pts.kb >= 1 && pts.kb <= 2;
-}
-
 // out = (K + noise I) V for nc <= 16 columns of V on the symmetric kernel.
 void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, int nc,
                 float* outc, MatvecWorkspace& ws, hipStream_t st) {
@@ -2344,29 +1965,10 @@ void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, i
                      Vc, n, vec4, cpart);
   hipLaunchKernelGGL(k_col_absmax_final, dim3((unsigned)nc), dim3(64), 0, st, cpart, chunks,
                      colmax);
-  const bool t32 = sym32_route(pts);
-  const int64_t tiles32 = nb * (kSymRows / 32);
-  float* vp = nullptr;
-  h8 *a32 = nullptr, *b32 = nullptr, *vf32 = nullptr, *vt32 = nullptr;
-  if (t32) {
-    const int KC = 2 * pts.kb;
-    const size_t pts_h8 = (size_t)tiles32 * KC * 64;
-    a32 = reinterpret_cast<h8*>(ws.pts32_a.ensure(pts_h8 * 4));
-    b32 = reinterpret_cast<h8*>(ws.pts32_b.ensure(pts_h8 * 4));
-    hipLaunchKernelGGL(k_pack_points32, dim3((unsigned)ceil_div((int64_t)pts_h8, 256)), dim3(256),
-                       0, st, reinterpret_cast<const h8*>(pts.A.ptr),
-                       reinterpret_cast<const h8*>(pts.B.ptr), pts.kb, tiles32, a32, b32);
-    const size_t rhs_h8 = (size_t)tiles32 * 2 * 64;
-    vf32 = reinterpret_cast<h8*>(ws.rhs32_f.ensure(rhs_h8 * 4));
-    vt32 = reinterpret_cast<h8*>(ws.rhs32_t.ensure(rhs_h8 * 4));
-    hipLaunchKernelGGL(k_pack_rhs32, dim3((unsigned)ceil_div((int64_t)rhs_h8, 256)), dim3(256), 0,
-                       st, Vc, n, nc, tiles32, colmax, vf32, vt32);
-  } else {
-    const int64_t total = pairs * 64;  // 8-half vectors per part, one column group
-    vp = ws.vpack.ensure((size_t)total * 2 * 4);
-    hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, Vc,
-                       n, nc, 1, pairs, colmax, vec4, reinterpret_cast<h8*>(vp));
-  }
+  const int64_t total = pairs * 64;  // 8-half vectors per part, one column group
+  float* vp = ws.vpack.ensure((size_t)total * 2 * 4);
+  hipLaunchKernelGGL(k_pack_rhs16, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st, Vc,
+                     n, nc, 1, pairs, colmax, vec4, reinterpret_cast<h8*>(vp));
   MGP_HIP_CHECK(hipGetLastError());
 
   // Splits of the delta range: >= 2048 workgroups where the blocks allow.
@@ -2376,25 +1978,16 @@ void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, i
   float* fwd = ws.partial.ensure((size_t)splits * 16 * mpad);
   float* tp = ws.sym_tp.ensure((size_t)std::max<int64_t>(nb * hmax, 1) * kSymRows * 16);
 
+  SymFn fn = a.kind == KIND_RBF        ? pick_sym<KIND_RBF>(pts.kb)
+             : a.kind == KIND_MATERN32 ? pick_sym<KIND_MATERN32>(pts.kb)
+                                       : pick_sym<KIND_MATERN52>(pts.kb);
+  MGP_REQUIRE(fn != nullptr, "no symmetric tile kernel for this shape");
   if (ws.time_tile) MGP_HIP_CHECK(hipEventRecord(ws.ev0, st));
   const int64_t items = round_up(nb * splits, kXcds);
-  if (t32) {
-    Sym32Fn fn = a.kind == KIND_RBF        ? pick_sym32<KIND_RBF>(pts.kb)
-                 : a.kind == KIND_MATERN32 ? pick_sym32<KIND_MATERN32>(pts.kb)
-                                           : pick_sym32<KIND_MATERN52>(pts.kb);
-    MGP_REQUIRE(fn != nullptr, "no 32x32 symmetric tile kernel for this shape");
-    hipLaunchKernelGGL(fn, dim3((unsigned)items), dim3(64 * kS32Waves), 0, st, b32, a32, vf32,
-                       vt32, nb, splits, dps, hmax, nc, colmax, fwd, tp, mpad);
-  } else {
-    SymFn fn = a.kind == KIND_RBF        ? pick_sym<KIND_RBF>(pts.kb)
-               : a.kind == KIND_MATERN32 ? pick_sym<KIND_MATERN32>(pts.kb)
-                                         : pick_sym<KIND_MATERN52>(pts.kb);
-    MGP_REQUIRE(fn != nullptr, "no symmetric tile kernel for this shape");
-    hipLaunchKernelGGL(fn, dim3((unsigned)items), dim3(64 * kSymWaves), 0, st,
-                       reinterpret_cast<const h8*>(pts.B.ptr),
-                       reinterpret_cast<const h8*>(pts.A.ptr), reinterpret_cast<const h8*>(vp), nb,
-                       splits, dps, hmax, nc, colmax, fwd, tp, mpad);
-  }
+  hipLaunchKernelGGL(fn, dim3((unsigned)items), dim3(64 * kSymWaves), 0, st,
+                     reinterpret_cast<const h8*>(pts.B.ptr), reinterpret_cast<const h8*>(pts.A.ptr),
+                     reinterpret_cast<const h8*>(vp), nb, splits, dps, hmax, nc, colmax, fwd, tp,
+                     mpad);
   MGP_HIP_CHECK(hipGetLastError());
   if (ws.time_tile) {
     MGP_HIP_CHECK(hipEventRecord(ws.ev1, st));
