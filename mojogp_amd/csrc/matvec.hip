@@ -372,6 +372,7 @@ __global__ __launch_bounds__(256) void k_fused_tile(
       }
     }
   }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // row operands before the loop (see k_sym_tile)
 
   constexpr int G = NCG > 0 ? NCG : 1;
   f4 acc[R][G];
