@@ -414,6 +414,30 @@ def _lmc_c5(repeats: int, warmup: int):
     }, (X, V[:1])
 
 
+def _c5_product_only(repeats: int = 30, warmup: int = 3):
+    """The config-5 structured product alone (profiling): K_full V over 16
+    task-blocked columns through mgp_lmc_benchmark_forward, inputs resident,
+    `warmup` untimed and `repeats` timed calls."""
+    from mojogp_amd import _lib
+    from mojogp_amd._provider import KIND_MATERN52, KIND_RBF, NativeProvider
+    X, _, _, Wm = _c5_data()
+    A = np.stack([np.outer(Wm[:, s], Wm[:, s]) + 0.1 * np.eye(C5_T)
+                  for s in range(2)]).astype(np.float32)
+    noise = np.full(C5_T, 0.0025, np.float32)
+    provs = [NativeProvider(KIND_RBF, False, X, np.array([0.2, 1.0], np.float32), 0.0),
+             NativeProvider(KIND_MATERN52, False, X, np.array([0.7, 1.0], np.float32), 0.0)]
+    V = np.random.default_rng(2).standard_normal((C5_C, C5_T * C5_N)).astype(np.float32)
+    times = np.zeros(repeats, np.float64)
+    try:
+        _lib.call("mgp_lmc_benchmark_forward", _lib.handles(provs), 2, C5_T, _lib.fptr(A),
+                  _lib.fptr(noise), _lib.fptr(V), C5_C, repeats, warmup, _lib.dptr(times), None)
+    finally:
+        for p in provs:
+            p.close()
+    return {"structured_matvec_ms_median": round(float(np.median(times)), 4),
+            "structured_matvec_ms_min": round(float(np.min(times)), 4)}
+
+
 def _cpu_model() -> str:
     """The host CPU's model name (first /proc/cpuinfo "model name" line)."""
     try:
@@ -639,6 +663,8 @@ def main(argv=None) -> int:
     ap.add_argument("--c5-only", action="store_true",
                     help="only the config-5 LMC leg (structured product, mBCG iteration, "
                          "fit, pathwise samples)")
+    ap.add_argument("--c5-product", action="store_true",
+                    help="only the config-5 structured product (30 timed calls; profiling)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run the plain copy kernel of BYTES (HBM counter calibration)")
     args = ap.parse_args(argv)
@@ -664,6 +690,9 @@ def main(argv=None) -> int:
         return 0
     if args.c3_grad:
         print(json.dumps(_c3_gradient_trace_only()), flush=True)
+        return 0
+    if args.c5_product:
+        print(json.dumps(_c5_product_only()), flush=True)
         return 0
     if args.c5_only:
         c5, _ = _lmc_c5(repeats=10, warmup=2)
