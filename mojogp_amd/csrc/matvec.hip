@@ -1199,7 +1199,8 @@ template <int KIND>
 __device__ __forceinline__ void grad_factors(float s, float clampv, float& kv, float& h) {
   if constexpr (KIND == KIND_RBF) {
     (void)clampv;  // the RBF exponent is not clamped
-    kv = __builtin_amdgcn_exp2f(-fmaxf(s, 0.0f));
+    // med3 rather than fmaxf on the MFMA result (see kval_scaled)
+    kv = __builtin_amdgcn_exp2f(-__builtin_amdgcn_fmed3f(s, 0.0f, 3.0e38f));
     h = kv;
   } else if constexpr (KIND == KIND_MATERN32) {
     const float u = __builtin_amdgcn_sqrtf(fabsf(s));
