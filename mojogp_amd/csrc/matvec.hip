@@ -279,29 +279,20 @@ __global__ void k_pad_vec(const float* __restrict__ V, int64_t n, int64_t npad,
   if (j < npad) P[j] = j < n ? V[j] : 0.0f;
 }
 
-// Value the distance MFMAs of the tile kernels accumulate from: the RBF
-// exponent 2^(kPScaleLog2 - s) needs s - kPScaleLog2, so its accumulators
-// start there (and an exact self-distance is restored to it); the Matern
-// kinds take s itself.
-template <int KIND>
-constexpr float dist_bias() {
-  return KIND == KIND_RBF ? -(float)kPScaleLog2 : 0.0f;
-}
-
-// 2^kPScaleLog2 * k / os from the scaled squared distance (s + dist_bias),
-// returned as a product f * g (Matern-5/2: polynomial times exponential; RBF:
-// g = 1) so the fp16 split can round the exact product (see split_pair).
+// 2^kPScaleLog2 * k / os from the scaled squared distance s, returned as a
+// product f * g (Matern-5/2: polynomial times exponential; RBF: g = 1) so the
+// fp16 split can round the exact product (see split_pair).
 template <int KIND>
 __device__ __forceinline__ void kval_scaled(float s, float clampv, float one, float& f,
                                             float& g) {
   constexpr float P = (float)(1 << kPScaleLog2);
   if constexpr (KIND == KIND_RBF) {
     (void)clampv;  // the RBF exponent is not clamped
-    // s = d - kPScaleLog2: 2^(kPScaleLog2 - max(d, 0)) = 2^-max(s, -kPScaleLog2).
-    // v_med3_f32 takes the MFMA result as it is; fmaxf would first
-    // canonicalize it (IEEE mode), one more VALU instruction per value.
-    const float t = __builtin_amdgcn_fmed3f(s, dist_bias<KIND>(), 3.0e38f);
-    f = __builtin_amdgcn_exp2f(-t);
+    // max(s, 0) as v_med3_f32, which takes the MFMA result as it is; fmaxf
+    // would first canonicalize it (IEEE mode), one more VALU instruction per
+    // value.  Same value for every finite s.
+    const float t = __builtin_amdgcn_fmed3f(s, 0.0f, 3.0e38f);
+    f = __builtin_amdgcn_exp2f((float)kPScaleLog2 - t);
     g = one;
   } else if constexpr (KIND == KIND_MATERN32) {
     const float u = __builtin_amdgcn_sqrtf(fabsf(s));
@@ -460,9 +451,8 @@ __global__ __launch_bounds__(256) void k_fused_tile(
     // the VALU forms row r's kernel values, so the matrix cores and the VALU
     // work side by side within the wave.
     auto dist = [&](int r, f4& s0, f4& s1) __attribute__((always_inline)) {
-      constexpr float z = dist_bias<KIND>();
-      s0 = f4{z, z, z, z};
-      s1 = f4{z, z, z, z};
+      s0 = f4{0.f, 0.f, 0.f, 0.f};
+      s1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[kb], bi[r][kb], s0, 0, 0, 0);
@@ -493,8 +483,8 @@ __global__ __launch_bounds__(256) void k_fused_tile(
         const int64_t dt = tile0 + r + diag_shift;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (jt0 == dt && li == lj + q) s0[q] = dist_bias<KIND>();
-          if (jt0 + 1 == dt && li == lj + q) s1[q] = dist_bias<KIND>();
+          if (jt0 == dt && li == lj + q) s0[q] = 0.0f;
+          if (jt0 + 1 == dt && li == lj + q) s1[q] = 0.0f;
         }
       }
       float f0[4], g0[4], f1[4], g1[4];
@@ -851,9 +841,8 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     const h8 vh = lds[st][kSymSteps * kA + 2 * k][lane];
     const h8 vl = lds[st][kSymSteps * kA + 2 * k + 1][lane];
     auto dist = [&](int r, f4& s0, f4& s1) __attribute__((always_inline)) {
-      constexpr float z = dist_bias<KIND>();
-      s0 = f4{z, z, z, z};
-      s1 = f4{z, z, z, z};
+      s0 = f4{0.f, 0.f, 0.f, 0.f};
+      s1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0[kb], bi[r][kb], s0, 0, 0, 0);
@@ -905,8 +894,8 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
         const int64_t dt = tile0 + r;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (jt0 == dt && li == lj + q) s0[q] = dist_bias<KIND>();
-          if (jt0 + 1 == dt && li == lj + q) s1[q] = dist_bias<KIND>();
+          if (jt0 == dt && li == lj + q) s0[q] = 0.0f;
+          if (jt0 + 1 == dt && li == lj + q) s1[q] = 0.0f;
         }
       }
       float f0[4], g0[4], f1[4], g1[4];
