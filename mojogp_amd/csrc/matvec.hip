@@ -559,12 +559,21 @@ __global__ __launch_bounds__(256) void k_fused_tile(
       fill(st ^ 1, u1, (int)min((int64_t)kStageSteps, u_end - u1));
     }
     if (active) {
-      for (int k = 0; k < ns; ++k) {
+      auto one = [&](int k) __attribute__((always_inline)) {
         const int64_t u = u0 + k;
         if (u >= dlo && u < dhi)
           step(st, k, u, std::true_type{});
         else
           step(st, k, u, std::false_type{});
+      };
+      // Full stages unrolled: as a loop, the steps' accumulators were copied
+      // back to the loop-carried registers at every step (16 v_mov_b64 with
+      // 64 right-hand sides); config-5 product 0.61 -> 0.59 ms.
+      if (ns == kStageSteps) {
+#pragma unroll
+        for (int k = 0; k < kStageSteps; ++k) one(k);
+      } else {
+        for (int k = 0; k < ns; ++k) one(k);
       }
       since_flush += ns;
       if (since_flush >= kFlushTiles / 2) {
