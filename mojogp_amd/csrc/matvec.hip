@@ -1037,6 +1037,10 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
           step(st, k, u, st, std::false_type{}, std::false_type{});
       }
     } else {
+      // Unrolled: no accumulator copies at a step back-edge (15.88 -> 15.72
+      // ms at config 3, measured once the loop head no longer waited for the
+      // next stage's operand loads; before that it measured slower).
+#pragma unroll
       for (int k = 0; k < kSymSteps; ++k) {
         lead(k);
         step(st, k, u0 + k, st, std::false_type{}, std::true_type{});
