@@ -725,7 +725,7 @@ constexpr int kSymRows = 16 * kSymR * kSymWaves;    // rows (and columns) per bl
 constexpr int kSymPairs = kSymRows / 32;            // column-tile pairs per block
 constexpr int kSymSteps = 2;                        // column-tile pairs per LDS stage
 constexpr int kSymStages = kSymPairs / kSymSteps;   // LDS stages per block
-constexpr int kSymSchedValu = 6;                    // VALU instructions per MFMA slot
+constexpr int kSymSchedValu = 8;                    // VALU instructions per MFMA slot
 static_assert((16 * kPackTileAlign) % kSymRows == 0, "blocks must tile the packed points");
 
 template <int KIND, int KB>
@@ -937,7 +937,8 @@ __global__ __launch_bounds__(64 * kSymWaves) void k_sym_tile(
     if constexpr (SYM) {
       // Issue order: one MFMA, then kSymSchedValu VALU instructions, through
       // the step (measured at config 3: 16.8 -> 16.1 ms against the
-      // compiler's default order, which bunches the kernel-value VALU).
+      // compiler's default order, which bunches the kernel-value VALU; with
+      // the unrolled stage loop 8 beats 7, 6 and 10 by 1-4%).
 #pragma unroll
       for (int i = 0; i < R * (2 * KB + 3) + 12; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
