@@ -24,6 +24,10 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
+#include <mutex>
+#include <queue>
+#include <unordered_map>
 #include <vector>
 
 namespace mgp {
@@ -1979,6 +1983,70 @@ SymFn pick_sym(int kb) {
   return nullptr;
 }
 
+// Delta splits of the symmetric product.  The kernel runs one workgroup per
+// CU; item L of the grid goes to XCD L / per (launch order deals workgroups
+// to the XCDs in turn), and each XCD's CUs take its items in order as they
+// free up.  A partly filled last round of items leaves CUs idle for up to
+// one item, so the split count is chosen by simulating that dispatch: items
+// cost 8 stages per delta (kSymStages) plus about one stage of set-up (both
+// fitted to measured launches at nb = 489: 5, 9, 12 and 35 splits gave 3.81
+// to 3.87 us per simulated stage), and more splits cost their forward
+// partials' extra read in k_sym_reduce (priced at 2 us per stage, a short
+// stage, so the choice leans towards fewer splits).  Cached per block count
+// and device.
+int64_t sym_splits(int64_t nb, SymFn fn) {
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, int64_t> cache;
+  int dev = 0;
+  MGP_HIP_CHECK(hipGetDevice(&dev));
+  const uint64_t key = (uint64_t)nb * 1024 + (uint64_t)dev;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int cus = 0, per_cu = 0;
+  MGP_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  MGP_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      &per_cu, reinterpret_cast<const void*>(fn), 64 * kSymWaves, 0));
+  const int slots = std::max(1, cus * std::max(per_cu, 1) / kXcds);
+  const int64_t hmax = nb / 2;
+  constexpr double kStageUs = 2.0, kReduceBytesPerUs = 6.0e6;
+  int64_t best_s = 1, last_dps = -1;
+  double best = 0.0;
+  for (int64_t s0 = 1; s0 <= std::min<int64_t>(hmax + 1, 64); ++s0) {
+    const int64_t dps = ceil_div(hmax + 1, s0);
+    if (dps == last_dps) continue;
+    last_dps = dps;
+    const int64_t splits = ceil_div(hmax + 1, dps);
+    const int64_t items = nb * splits;
+    const int64_t per = round_up(items, (int64_t)kXcds) / kXcds;
+    double make = 0.0;
+    for (int x = 0; x < kXcds; ++x) {
+      std::priority_queue<double, std::vector<double>, std::greater<double>> cu;
+      for (int i = 0; i < slots; ++i) cu.push(0.0);
+      for (int64_t k = 0; k < per; ++k) {
+        const int64_t L = x * per + k;
+        if (L >= items) break;
+        const int64_t b = L % nb, d0 = (L / nb) * dps;
+        const int64_t d1 = std::min(d0 + dps, sym_span(b, nb) + 1);
+        const double cost = (double)std::max<int64_t>(d1 - d0, 0) * kSymStages + 1.0;
+        const double t = cu.top();
+        cu.pop();
+        cu.push(t + cost);
+      }
+      while (cu.size() > 1) cu.pop();
+      make = std::max(make, cu.top());
+    }
+    const double fwd_bytes = (double)splits * (double)nb * kSymRows * 16 * 4;
+    const double total = make + fwd_bytes / kReduceBytesPerUs / kStageUs;
+    if (s0 == 1 || total < best - 1e-9) {
+      best = total;
+      best_s = splits;
+    }
+  }
+  cache.emplace(key, best_s);
+  return best_s;
+}
+
 // out = (K + noise I) V for nc <= 16 columns of V on the symmetric kernel.
 void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, int nc,
                 float* outc, MatvecWorkspace& ws, hipStream_t st) {
@@ -2002,17 +2070,16 @@ void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, i
                      n, nc, 1, pairs, colmax, vec4, reinterpret_cast<h8*>(vp));
   MGP_HIP_CHECK(hipGetLastError());
 
-  // Splits of the delta range: >= 2048 workgroups where the blocks allow.
-  int64_t splits = std::min<int64_t>(std::max<int64_t>(ceil_div(2048, nb), 1), hmax + 1);
+  SymFn fn = a.kind == KIND_RBF        ? pick_sym<KIND_RBF>(pts.kb)
+             : a.kind == KIND_MATERN32 ? pick_sym<KIND_MATERN32>(pts.kb)
+                                       : pick_sym<KIND_MATERN52>(pts.kb);
+  MGP_REQUIRE(fn != nullptr, "no symmetric tile kernel for this shape");
+  int64_t splits = sym_splits(nb, fn);
   const int64_t dps = ceil_div(hmax + 1, splits);
   splits = ceil_div(hmax + 1, dps);
   float* fwd = ws.partial.ensure((size_t)splits * 16 * mpad);
   float* tp = ws.sym_tp.ensure((size_t)std::max<int64_t>(nb * hmax, 1) * kSymRows * 16);
 
-  SymFn fn = a.kind == KIND_RBF        ? pick_sym<KIND_RBF>(pts.kb)
-             : a.kind == KIND_MATERN32 ? pick_sym<KIND_MATERN32>(pts.kb)
-                                       : pick_sym<KIND_MATERN52>(pts.kb);
-  MGP_REQUIRE(fn != nullptr, "no symmetric tile kernel for this shape");
   if (ws.time_tile) MGP_HIP_CHECK(hipEventRecord(ws.ev0, st));
   const int64_t items = round_up(nb * splits, kXcds);
   hipLaunchKernelGGL(fn, dim3((unsigned)items), dim3(64 * kSymWaves), 0, st,
