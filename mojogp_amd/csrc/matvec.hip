@@ -27,6 +27,7 @@
 #include <functional>
 #include <mutex>
 #include <queue>
+#include <string>
 #include <unordered_map>
 #include <vector>
 
@@ -1983,30 +1984,30 @@ SymFn pick_sym(int kb) {
   return nullptr;
 }
 
-// Delta splits of the symmetric product.  The kernel runs one workgroup per
-// CU; item L of the grid goes to XCD L / per (launch order deals workgroups
-// to the XCDs in turn), and each XCD's CUs take its items in order as they
-// free up.  A partly filled last round of items leaves CUs idle for up to
-// one item, so the split count is chosen by simulating that dispatch: items
-// cost 8 stages per delta (kSymStages) plus about one stage of set-up (both
-// fitted to measured launches at nb = 489: 5, 9, 12 and 35 splits gave 3.81
-// to 3.87 us per simulated stage), and more splits cost their forward
-// partials' extra read in k_sym_reduce (priced at 2 us per stage, a short
-// stage, so the choice leans towards fewer splits).  Cached per block count
-// and device.
-int64_t sym_splits(int64_t nb, SymFn fn) {
+// Delta splits of the symmetric kernels (k_sym_tile, k_grad_sym).  They run
+// one workgroup per CU; item L of the grid goes to XCD L / per (launch order
+// deals workgroups to the XCDs in turn), and each XCD's CUs take its items in
+// order as they free up.  A partly filled last round of items leaves CUs idle
+// for up to one item, so the split count is chosen by simulating that
+// dispatch: an item costs `stages` per delta plus about one stage of set-up
+// (fitted to measured k_sym_tile launches at nb = 489: 5, 9, 12 and 35
+// splits gave 3.81 to 3.87 us per simulated stage), and each split's partial
+// sums (`split_bytes`) cost their extra read in the reduction (priced at 2 us
+// per stage, a short stage, so the choice leans towards fewer splits).
+// Cached per kernel, block count and device.
+int64_t delta_splits(int64_t nb, int stages, const void* fn, int threads, double split_bytes) {
   static std::mutex mu;
-  static std::unordered_map<uint64_t, int64_t> cache;
+  static std::unordered_map<std::string, int64_t> cache;
   int dev = 0;
   MGP_HIP_CHECK(hipGetDevice(&dev));
-  const uint64_t key = (uint64_t)nb * 1024 + (uint64_t)dev;
+  const std::string key = std::to_string(reinterpret_cast<uintptr_t>(fn)) + ":" +
+                          std::to_string(nb) + ":" + std::to_string(dev);
   std::lock_guard<std::mutex> lock(mu);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int cus = 0, per_cu = 0;
   MGP_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-  MGP_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      &per_cu, reinterpret_cast<const void*>(fn), 64 * kSymWaves, 0));
+  MGP_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0));
   const int slots = std::max(1, cus * std::max(per_cu, 1) / kXcds);
   const int64_t hmax = nb / 2;
   constexpr double kStageUs = 2.0, kReduceBytesPerUs = 6.0e6;
@@ -2028,7 +2029,7 @@ int64_t sym_splits(int64_t nb, SymFn fn) {
         if (L >= items) break;
         const int64_t b = L % nb, d0 = (L / nb) * dps;
         const int64_t d1 = std::min(d0 + dps, sym_span(b, nb) + 1);
-        const double cost = (double)std::max<int64_t>(d1 - d0, 0) * kSymStages + 1.0;
+        const double cost = (double)std::max<int64_t>(d1 - d0, 0) * stages + 1.0;
         const double t = cu.top();
         cu.pop();
         cu.push(t + cost);
@@ -2036,8 +2037,7 @@ int64_t sym_splits(int64_t nb, SymFn fn) {
       while (cu.size() > 1) cu.pop();
       make = std::max(make, cu.top());
     }
-    const double fwd_bytes = (double)splits * (double)nb * kSymRows * 16 * 4;
-    const double total = make + fwd_bytes / kReduceBytesPerUs / kStageUs;
+    const double total = make + (double)splits * split_bytes / kReduceBytesPerUs / kStageUs;
     if (s0 == 1 || total < best - 1e-9) {
       best = total;
       best_s = splits;
@@ -2074,7 +2074,8 @@ void sym_matvec(const MatvecArgs& a, const PackedPoints& pts, const float* Vc, i
              : a.kind == KIND_MATERN32 ? pick_sym<KIND_MATERN32>(pts.kb)
                                        : pick_sym<KIND_MATERN52>(pts.kb);
   MGP_REQUIRE(fn != nullptr, "no symmetric tile kernel for this shape");
-  int64_t splits = sym_splits(nb, fn);
+  int64_t splits = delta_splits(nb, kSymStages, reinterpret_cast<const void*>(fn),
+                                64 * kSymWaves, (double)nb * kSymRows * 16 * 4);
   const int64_t dps = ceil_div(hmax + 1, splits);
   splits = ceil_div(hmax + 1, dps);
   float* fwd = ws.partial.ensure((size_t)splits * 16 * mpad);
@@ -2151,7 +2152,14 @@ void grad_trace_mfma(int kind, const PackedPoints& pts, int d, const float* Lf,
   const int qg = d <= 16 ? 1 : 2;
   const int nq = 16 * qg;
   const int64_t hmax = nb / 2;
-  int64_t splits = std::min<int64_t>(std::max<int64_t>(ceil_div(2048, nb), 1), hmax + 1);
+  GradFn fn = kind == KIND_RBF        ? pick_grad<KIND_RBF>(pts.kb, qg)
+              : kind == KIND_MATERN32 ? pick_grad<KIND_MATERN32>(pts.kb, qg)
+                                      : pick_grad<KIND_MATERN52>(pts.kb, qg);
+  MGP_REQUIRE(fn != nullptr, "no gradient trace kernel for this shape");
+  // Each split's per-item partials travel to the host over PCIe (~25 GB/s,
+  // 240x slower than the HBM read the split model prices).
+  int64_t splits = delta_splits(nb, kGtStages, reinterpret_cast<const void*>(fn), 64 * kGtWaves,
+                                240.0 * (double)nb * (nq + 1) * sizeof(double));
   const int64_t dps = ceil_div(hmax + 1, splits);
   splits = ceil_div(hmax + 1, dps);
   const int64_t items = round_up(nb * splits, kXcds);
@@ -2170,10 +2178,6 @@ void grad_trace_mfma(int kind, const PackedPoints& pts, int d, const float* Lf,
   hipLaunchKernelGGL(k_pack_grad_zz, dim3((unsigned)ceil_div(zthreads, 256)), dim3(256), 0, st,
                      pts.z.ptr, n, d, qg, pairs, ZZ);
   MGP_HIP_CHECK(hipGetLastError());
-  GradFn fn = kind == KIND_RBF        ? pick_grad<KIND_RBF>(pts.kb, qg)
-              : kind == KIND_MATERN32 ? pick_grad<KIND_MATERN32>(pts.kb, qg)
-                                      : pick_grad<KIND_MATERN52>(pts.kb, qg);
-  MGP_REQUIRE(fn != nullptr, "no gradient trace kernel for this shape");
 
   for (int c0 = 0; c0 < ncols; c0 += 16) {
     const int nc = std::min(16, ncols - c0);
