@@ -48,10 +48,10 @@ N_TR = 2                       # sqrt + exp per pair
 FLOPS_PER_PAIR = 2 * D + 2 * T + C_K
 # HBM bytes per launch of the tile kernel at this workload (rocprofv3 FETCH_SIZE
 # x 2.000 + WRITE_SIZE x 1.000, copy-kernel calibration): the symmetric kernel
-# (profiles/symmetric_tile_c3_matvec.md: 0.897 GB read, 4.119 GB written, most
+# (profiles/symmetric_tile_c3_matvec.md: 1.610 GB read, 4.316 GB written, most
 # of it the transposed partial sums) and the one-sided kernel
 # (profiles/fused_tile_c3_matvec.md).
-TILE_TRAFFIC_BYTES = {"symmetric": 5.016e9, "one_sided": 1.995e9}
+TILE_TRAFFIC_BYTES = {"symmetric": 5.926e9, "one_sided": 1.995e9}
 
 # Instruction mix of the tile kernel k_fused_tile<Matern52, KB, NCG=1, R=4> per
 # 16x16 tile (gfx950 ISA of this build): 4 pair values per lane, each with 2
