@@ -1583,6 +1583,60 @@ __global__ void k_reduce_mix(const float* __restrict__ partial, int splits, int 
   }
 }
 
+// k_reduce_mix over four consecutive rows per thread with 16-byte loads and
+// stores (m and mpad multiples of 4, 16-byte aligned arrays); the same sums
+// in the same order per row.
+__global__ void k_reduce_mix4(const float* __restrict__ partial, int splits, int cpad,
+                              int64_t mpad, int64_t m, int nblocks, int T, float os, float noise,
+                              int add_noise, const float* __restrict__ Vin,
+                              const float* __restrict__ mix, int accumulate,
+                              float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t m4 = m / 4;
+  if (idx >= (int64_t)nblocks * m4) return;
+  const int cc = (int)(idx / m4);
+  const int64_t i = 4 * (idx - (int64_t)cc * m4);
+  f4 v[kMaxMixT];
+#pragma unroll
+  for (int tp = 0; tp < kMaxMixT; ++tp) {
+    if (tp < T) {
+      const int c = cc * T + tp;
+      double tot[4] = {0.0, 0.0, 0.0, 0.0};
+      for (int sp = 0; sp < splits; ++sp) {
+        const f4 q = *reinterpret_cast<const f4*>(partial + ((int64_t)sp * cpad + c) * mpad + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tot[e] += (double)q[e];
+      }
+      f4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = os * (float)tot[e];
+      if (add_noise) {
+        const f4 x = *reinterpret_cast<const f4*>(Vin + (int64_t)c * m + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = fmaf(noise, x[e], o[e]);
+      }
+      v[tp] = o;
+    }
+  }
+  for (int t = 0; t < T; ++t) {
+    f4 o = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tp = 0; tp < kMaxMixT; ++tp)
+      if (tp < T) {
+        const float w = mix[t * T + tp];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = fmaf(w, v[tp][e], o[e]);
+      }
+    f4* dst = reinterpret_cast<f4*>(out + (int64_t)(cc * T + t) * m + i);
+    if (accumulate) {
+      const f4 prev = *dst;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] += prev[e];
+    }
+    *dst = o;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Direct (per-dimension difference) product: one thread per row, LDS tiles of
 // column points.  Arithmetic follows the reference order: r^2 = sum_d diff^2.
@@ -2338,9 +2392,19 @@ void fused_matvec(const MatvecArgs& a, const PackedPoints& rows,
     if (mixing) {
       const int nblk = nc / a.mix_T;
       const int64_t tot = (int64_t)nblk * a.m;
-      hipLaunchKernelGGL(k_reduce_mix, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st,
-                         partial, (int)splits, cpad, mpad, a.m, nblk, a.mix_T, a.outputscale,
-                         a.noise, a.square ? 1 : 0, Vin, a.mix, a.mix_accumulate ? 1 : 0, outc);
+      const bool q4 = a.m % 4 == 0 && mpad % 4 == 0 &&
+                      reinterpret_cast<uintptr_t>(outc) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(partial) % 16 == 0 &&
+                      (Vin == nullptr || reinterpret_cast<uintptr_t>(Vin) % 16 == 0);
+      if (q4)
+        hipLaunchKernelGGL(k_reduce_mix4, dim3((unsigned)ceil_div(tot / 4, 256)), dim3(256), 0,
+                           st, partial, (int)splits, cpad, mpad, a.m, nblk, a.mix_T,
+                           a.outputscale, a.noise, a.square ? 1 : 0, Vin, a.mix,
+                           a.mix_accumulate ? 1 : 0, outc);
+      else
+        hipLaunchKernelGGL(k_reduce_mix, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st,
+                           partial, (int)splits, cpad, mpad, a.m, nblk, a.mix_T, a.outputscale,
+                           a.noise, a.square ? 1 : 0, Vin, a.mix, a.mix_accumulate ? 1 : 0, outc);
       MGP_HIP_CHECK(hipGetLastError());
     } else if (splits > 1) {
       const int64_t tot = (int64_t)nc * a.m;
