@@ -550,44 +550,82 @@ __global__ __launch_bounds__(256) void k_fused_tile(
   const int64_t u_begin = (int64_t)blockIdx.y * pairs_per_split;
   const int64_t u_end = min(col_pairs, u_begin + pairs_per_split);
   const int64_t dlo = (tile0 + diag_shift) / 2, dhi = dlo + R / 2;
-  const int64_t nstages = (u_end - u_begin + kStageSteps - 1) / kStageSteps;
-  fill(0, u_begin, (int)min((int64_t)kStageSteps, u_end - u_begin));
-  int since_flush = 0;
-  for (int64_t c = 0; c < nstages; ++c) {
-    const int st = (int)(c & 1);
-    const int64_t u0 = u_begin + c * kStageSteps;
-    const int ns = (int)min((int64_t)kStageSteps, u_end - u0);
+  const int64_t npairs = max((int64_t)0, u_end - u_begin);
+  const int64_t nfull = npairs / kStageSteps;  // full stages; a last partial one follows
+  const int64_t nstages = (npairs + kStageSteps - 1) / kStageSteps;
+  fill(0, u_begin, (int)min((int64_t)kStageSteps, npairs));
+  auto stage_top = [&](int64_t c) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (c + 1 < nstages) {
-      const int64_t u1 = u0 + kStageSteps;
-      fill(st ^ 1, u1, (int)min((int64_t)kStageSteps, u_end - u1));
+      const int64_t u1 = u_begin + (c + 1) * kStageSteps;
+      fill((int)((c + 1) & 1), u1, (int)min((int64_t)kStageSteps, u_end - u1));
     }
-    if (active) {
-      auto one = [&](int k) __attribute__((always_inline)) {
-        const int64_t u = u0 + k;
-        if (u >= dlo && u < dhi)
-          step(st, k, u, std::true_type{});
-        else
-          step(st, k, u, std::false_type{});
-      };
-      // Full stages unrolled: as a loop, the steps' accumulators were copied
-      // back to the loop-carried registers at every step (16 v_mov_b64 with
-      // 64 right-hand sides); config-5 product 0.61 -> 0.59 ms.
-      if (ns == kStageSteps) {
-#pragma unroll
-        for (int k = 0; k < kStageSteps; ++k) one(k);
-      } else {
-        for (int k = 0; k < ns; ++k) one(k);
-      }
-      since_flush += ns;
-      if (since_flush >= kFlushTiles / 2) {
-        flush();
-        since_flush = 0;
-      }
-    }
+  };
+  if (!active) {
+    for (int64_t c = 0; c < nstages; ++c) stage_top(c);
+    return;
   }
-  if (!active) return;
+  // The stage loops below hold no branch that merges accumulator values: the
+  // full stages without a diagonal pair of this wave run as straight code,
+  // the fp64 flush (every kFlushStages full stages, 256 columns) closes a
+  // group of them, and the stages holding a diagonal pair and the last
+  // partial stage are peeled off.  As one loop with those branches inside,
+  // every stage copied the accumulators (48 v_mov_b64 with 64 right-hand
+  // sides).  Flush points and summation order are those of a per-stage
+  // column count.
+  constexpr int kFlushStages = kFlushTiles / (2 * kStageSteps);
+  auto plain_stage = [&](int64_t c) __attribute__((always_inline)) {
+    const int st = (int)(c & 1);
+    const int64_t u0 = u_begin + c * kStageSteps;
+#pragma unroll
+    for (int k = 0; k < kStageSteps; ++k) step(st, k, u0 + k, std::false_type{});
+  };
+  auto checked_stage = [&](int64_t c, int ns) __attribute__((always_inline)) {
+    const int st = (int)(c & 1);
+    const int64_t u0 = u_begin + c * kStageSteps;
+    auto one = [&](int k) __attribute__((always_inline)) {
+      const int64_t u = u0 + k;
+      if (u >= dlo && u < dhi)
+        step(st, k, u, std::true_type{});
+      else
+        step(st, k, u, std::false_type{});
+    };
+    if (ns == kStageSteps) {
+#pragma unroll
+      for (int k = 0; k < kStageSteps; ++k) one(k);
+    } else {
+      for (int k = 0; k < ns; ++k) one(k);
+    }
+  };
+  auto run_plain = [&](int64_t c0, int64_t c1) __attribute__((always_inline)) {
+    for (int64_t g = c0; g < c1;) {
+      const int64_t ge = min(c1, (g / kFlushStages + 1) * kFlushStages);
+      for (int64_t c = g; c < ge; ++c) {
+        stage_top(c);
+        plain_stage(c);
+      }
+      if (ge % kFlushStages == 0) flush();
+      g = ge;
+    }
+  };
+  // Full stages [cd0, cd1) hold the wave's diagonal pairs [dlo, dhi).
+  int64_t cd0 = 0, cd1 = 0;
+  if (dlo < u_end && dhi > u_begin) {
+    cd0 = min(nfull, (max(dlo, u_begin) - u_begin) / kStageSteps);
+    cd1 = min(nfull, (min(dhi, u_end) - 1 - u_begin) / kStageSteps + 1);
+  }
+  run_plain(0, cd0);
+  for (int64_t c = cd0; c < cd1; ++c) {
+    stage_top(c);
+    checked_stage(c, kStageSteps);
+    if (c % kFlushStages == kFlushStages - 1) flush();
+  }
+  run_plain(cd1, nfull);
+  if (nstages > nfull) {
+    stage_top(nfull);
+    checked_stage(nfull, (int)(npairs - nfull * kStageSteps));
+  }
   flush();
 
   // Epilogue: undo the fp16 scaling exactly (powers of two).
