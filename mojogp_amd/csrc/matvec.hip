@@ -1640,7 +1640,19 @@ __global__ void k_reduce_mix4(const float* __restrict__ partial, int splits, int
     if (tp < T) {
       const int c = cc * T + tp;
       double tot[4] = {0.0, 0.0, 0.0, 0.0};
-      for (int sp = 0; sp < splits; ++sp) {
+      // Four split partials in flight per step (same summation order).
+      int sp = 0;
+      for (; sp + 4 <= splits; sp += 4) {
+        f4 q[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          q[k] = *reinterpret_cast<const f4*>(partial + ((int64_t)(sp + k) * cpad + c) * mpad + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tot[e] += (double)q[k][e];
+      }
+      for (; sp < splits; ++sp) {
         const f4 q = *reinterpret_cast<const f4*>(partial + ((int64_t)sp * cpad + c) * mpad + i);
 #pragma unroll
         for (int e = 0; e < 4; ++e) tot[e] += (double)q[e];
