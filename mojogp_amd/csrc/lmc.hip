@@ -85,18 +85,24 @@ __global__ void k_ut_mix(const float* __restrict__ Y, const float* __restrict__ 
 }
 
 // z[c][a] = sum_b Minv[a][b] y[c][b] in fp64 (M can be conditioned like
-// n / noise, so its inverse is neither stored nor applied in fp32); one block
-// per column, z rounded to fp32 for the U z products.
-__global__ void k_small_gemv(const double* __restrict__ Minv, const double* __restrict__ y,
-                             int K, float* __restrict__ z) {
+// n / noise, so its inverse is neither stored nor applied in fp32), rounded
+// to fp32 for the U z products.  Grid (column, group of 4 outputs): one wave
+// per output a, its lanes over b, a fixed-order shuffle sum.  (One thread per
+// output walking its row alone took 14 us per call at K = 120.)
+__global__ __launch_bounds__(256) void k_small_gemv(const double* __restrict__ Minv,
+                                                   const double* __restrict__ y, int K,
+                                                   float* __restrict__ z) {
   const int c = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int a = (int)blockIdx.y * 4 + (int)(threadIdx.x >> 6);
+  if (a >= K) return;
   const double* yc = y + (int64_t)c * K;
-  for (int a = threadIdx.x; a < K; a += blockDim.x) {
-    double s = 0.0;
-    const double* row = Minv + (int64_t)a * K;
-    for (int b = 0; b < K; ++b) s = fma(row[b], yc[b], s);
-    z[(int64_t)c * K + a] = (float)s;
-  }
+  const double* row = Minv + (int64_t)a * K;
+  double s = 0.0;
+  for (int b = lane; b < K; b += 64) s = fma(row[b], yc[b], s);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) z[(int64_t)c * K + a] = (float)s;
 }
 
 // Z[(c*T + j)*r + k] = z[c][off + j*r + k]
@@ -421,7 +427,8 @@ void LMCPrecond::apply(const float* r, int C, float* z, double* rz_part, int nb,
   }
   // 3. z' = M^-1 y
   float* zk_ = zk.ensure((size_t)C * K);
-  hipLaunchKernelGGL(k_small_gemv, dim3(C), dim3(256), 0, st, Minv.ptr, yk_, K, zk_);
+  hipLaunchKernelGGL(k_small_gemv, dim3(C, (unsigned)ceil_div(K, 4)), dim3(256), 0, st,
+                     Minv.ptr, yk_, K, zk_);
   // 4. res = U z'
   float* rs_ = res.ensure((size_t)total);
   lmc_u_times(*this, zk_, C, rs_, st);
