@@ -1757,7 +1757,11 @@ static int launch_ltv_mfma(const float* L, int64_t n, int k, const float* v, int
                            WoodburyWork& w, float** wpart_out, hipStream_t st, const float* rs) {
   const int nct = (ncols + 15) / 16;
   if (nct > 4 || k > 256) return 0;
-  const int64_t chunk = round_up(ceil_div(n, cg_chunks(n)), 16);
+  int64_t chunk = round_up(ceil_div(n, cg_chunks(n)), 16);
+  // k_ltv_mfma gives wave w the L tiles w, w + 4, ...: with k <= 16 only wave
+  // 0 of a block has work, so quarter the chunks and run four times as many
+  // blocks (LMC latents, 64 columns at N = 20000: 12.5 us per call before).
+  if (nct >= 2 && k <= 16) chunk = round_up(ceil_div(chunk, 4), 16);
   const int nbw = (int)ceil_div(n, chunk);
   float* wpart = w.wpart.ensure((size_t)nbw * k * ncols);
   const bool vec4 = n % 4 == 0 && chunk % 4 == 0 && reinterpret_cast<uintptr_t>(L) % 16 == 0 &&
