@@ -105,16 +105,6 @@ __global__ __launch_bounds__(256) void k_small_gemv(const double* __restrict__ M
   if (lane == 0) z[(int64_t)c * K + a] = (float)s;
 }
 
-// Z[(c*T + j)*r + k] = z[c][off + j*r + k]
-__global__ void k_gather_z(const float* __restrict__ z, int T, int r, int C, int K, int off,
-                           float* __restrict__ Z) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)C * T * r) return;
-  const int c = (int)(idx / ((int64_t)T * r));
-  const int rem = (int)(idx - (int64_t)c * T * r);
-  Z[idx] = z[(int64_t)c * K + off + rem];
-}
-
 // w[c][t*r + k] = raw[(t*C + c)*r + k]: the Kronecker preconditioner's rank
 // draws in its probe-major-per-task order, regrouped per probe
 __global__ void k_kron_zrank(const float* __restrict__ raw, int T, int r, int C,
@@ -395,11 +385,9 @@ static void lmc_u_times(LMCPrecond& P, const float* z, int C, float* res, hipStr
   for (int s = 0; s < P.R; ++s) {
     const int r = P.rank[s];
     if (r == 0) continue;
-    float* Z = P.Z.ensure((size_t)C * P.T * r);
-    hipLaunchKernelGGL(k_gather_z, g1((int64_t)C * P.T * r), dim3(256), 0, st, z, P.T, r, C,
-                       P.K, P.off[s], Z);
     float* ol = P.out_l.ensure((size_t)total);
-    l_matmul(P.L[s]->ptr, P.n, r, Z, C * P.T, ol, st);
+    // Z[(c T + j) r + k] = z[c K + off + j r + k], read in place
+    l_matmul_gather(P.L[s]->ptr, P.n, r, z, P.T, P.K, P.off[s], C * P.T, ol, st);
     hipLaunchKernelGGL(k_lmc_mix, g1(total), dim3(256), 0, st, res, ol,
                        (cs ? cs : P.Cs_dev.ptr) + (size_t)s * P.T * P.T, P.n, P.T, C,
                        first ? 0 : 1);

@@ -146,6 +146,11 @@ void lt_matmul(const float* L, int64_t n, int k, const float* V, int ncols, floa
 // out[c][i] = sum_kk L[kk][i] Z[c][kk] for ncols columns.
 void l_matmul(const float* L, int64_t n, int k, const float* Z, int ncols, float* out,
               hipStream_t st);
+// The same with column c = b gT + j of Z read in place from a blocked vector:
+// Z[c][kk] = z[b gK + goff + j k + kk] (the LMC preconditioner's per-latent
+// slice of each probe's coefficients, without a gathered copy).
+void l_matmul_gather(const float* L, int64_t n, int k, const float* z, int gT, int gK, int goff,
+                     int ncols, float* out, hipStream_t st);
 
 // ---------------------------------------------------------------- gradients
 // g[p] = sum_{a,b} dK_p[a,b] * sum_c Lf[c*n+a] Rf[c*n+b]  for every kernel

@@ -1161,13 +1161,17 @@ __global__ __launch_bounds__(256 * KS) void k_woodbury_mfma(
 __global__ __launch_bounds__(256) void k_low_rank_sample(
     const float* __restrict__ L, int64_t n, int k, const float* __restrict__ zr,
     const float* __restrict__ zn, float s, int ncols, float* __restrict__ out,
-    const float* __restrict__ ds) {
+    const float* __restrict__ ds, int gT, int gK, int goff) {
   extern __shared__ float zs[];  // [16][k]
   const int c0 = blockIdx.y * 16;
   const int cn = min(16, ncols - c0);
   for (int t = threadIdx.x; t < 16 * k; t += blockDim.x) {
     const int c = t / k, kk = t - c * k;
-    zs[t] = c < cn ? zr[(int64_t)(c0 + c) * k + kk] : 0.0f;
+    const int cc = c0 + c;
+    // column cc of zr, or read in place from a blocked vector (gT > 0)
+    const int64_t src = gT > 0 ? (int64_t)(cc / gT) * gK + goff + (int64_t)(cc % gT) * k + kk
+                               : (int64_t)cc * k + kk;
+    zs[t] = c < cn ? zr[src] : 0.0f;
   }
   __syncthreads();
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1879,7 +1883,7 @@ void low_rank_sample(const float* L, int64_t n, int k, const float* zr, const fl
                      float s, int ncols, float* out, hipStream_t st, const float* ds) {
   const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256), (unsigned)ceil_div(ncols, 16));
   hipLaunchKernelGGL(k_low_rank_sample, grid, dim3(256), (size_t)16 * k * sizeof(float), st, L,
-                     n, k, zr, zn, s, ncols, out, ds);
+                     n, k, zr, zn, s, ncols, out, ds, 0, 0, 0);
   MGP_HIP_CHECK(hipGetLastError());
 }
 
@@ -1997,6 +2001,20 @@ void l_matmul(const float* L, int64_t n, int k, const float* Z, int ncols, float
     return;
   }
   low_rank_sample(L, n, k, Z, nullptr, 0.0f, ncols, out, st);
+}
+
+void l_matmul_gather(const float* L, int64_t n, int k, const float* z, int gT, int gK, int goff,
+                     int ncols, float* out, hipStream_t st) {
+  if (ncols <= 0) return;
+  if (k <= 0) {
+    fill(out, n * (int64_t)ncols, 0.0f, st);
+    return;
+  }
+  MGP_REQUIRE(gT > 0 && ncols % gT == 0, "gathered columns come in blocks of gT");
+  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(n, 1), 256), (unsigned)ceil_div(ncols, 16));
+  hipLaunchKernelGGL(k_low_rank_sample, grid, dim3(256), (size_t)16 * k * sizeof(float), st, L,
+                     n, k, z, nullptr, 0.0f, ncols, out, nullptr, gT, gK, goff);
+  MGP_HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace mgp
